@@ -1,0 +1,177 @@
+// args.h — kernel argument blocks shared by the gfx950 code object and the
+// host runtime. Every kernel in kernels.hsaco takes exactly one of these by
+// value, so hipModuleLaunchKernel passes one pointer and the layout is
+// fixed in one place. Plain C types only.
+#pragma once
+#include <stdint.h>
+
+// Weight formats (ggml type ids, the reference's Quant.GG_*).
+#define CJ_F32 0
+#define CJ_F16 1
+#define CJ_Q4_0 2
+#define CJ_Q8_0 8
+#define CJ_Q4_K 12
+#define CJ_Q6_K 14
+#define CJ_MXFP4 39
+
+// GEMV prologue: where the activation comes from.
+#define CJ_PRO_PACKED 0     // an int8 pack already in HBM (320-byte blocks)
+#define CJ_PRO_PACK 1       // f32 x in HBM, packed into LDS here
+#define CJ_PRO_NORM_PACK 2  // f32 x in HBM, RMSNorm'd then packed into LDS
+#define CJ_PRO_F32 3        // f32 x in HBM, used as f32 (Q4_0, MXFP4)
+#define CJ_PRO_NORM_F32 4   // f32 x in HBM, RMSNorm'd, used as f32
+
+// GEMV epilogue: what happens to each output row.
+#define CJ_EPI_STORE 0      // y[row] = v
+#define CJ_EPI_ACCUM 1      // y[row] += v (residual rides the store)
+#define CJ_EPI_QKV_ROPE 2   // q|k rows in GGUF pair order: RoPE, q out, K/V fp16 append
+#define CJ_EPI_GLU 3        // gate/up rows interleaved: silu(g)·u, then the pack of the result
+#define CJ_EPI_ARGMAX 4     // logits out + first-occurrence argmax into the token history
+
+// Device-resident decode state the per-token graph reads and advances.
+typedef struct {
+    int32_t pos;          // position of the token being decoded
+    int32_t fixed_until;  // tokens[p] for p < fixed_until are given (prompt), not predicted
+    int32_t pad[2];
+} cj_step_state;
+
+typedef struct {
+    // tensors
+    const uint8_t *w;       // prepared weight rows
+    const float *x;         // f32 activation (PRO_PACK / NORM_PACK / F32)
+    const uint8_t *xp;      // packed activation (PRO_PACKED)
+    const float *nw;        // norm weight (NORM_*)
+    float *y;               // output rows (STORE / ACCUM / ARGMAX logits)
+    // epilogue extras
+    float *q_out;           // QKV: rotated q (HF order)
+    uint16_t *kc, *vc;      // QKV: fp16 K/V planes (page-blocked, head-major)
+    const int32_t *pgtab;   // QKV: KV page table
+    const float *rope_cs;   // QKV: [ctx][half] (cos, sin) pairs
+    float *act;             // GLU: silu(g)·u out (f32)
+    uint8_t *act_pack;      // GLU: packed result for the down projection
+    int32_t *counters;      // GLU: per-256-block arrival counters; ARGMAX: one counter
+    float *part_v;          // ARGMAX: per-workgroup best value
+    int32_t *part_i;        // ARGMAX: per-workgroup best index
+    int32_t *tokens;        // ARGMAX: token history, tokens[pos+1] written past the prompt
+    int32_t *preds;         // ARGMAX: preds[pos+1] = the argmax at every step
+    cj_step_state *state;   // device step state (pos); null: use `pos`
+    // shapes
+    int64_t rows, cols;     // weight rows (outputs) and columns (inputs)
+    int64_t row_bytes;      // prepared bytes per row
+    int64_t y_off;          // output row offset (reference yOff)
+    int32_t type;           // CJ_Q4_K ...
+    int32_t pro, epi;
+    int32_t per32;          // activation pack at one scale per 32 (Q8_0 consumers)
+    int32_t rows_per_wg;    // output rows per workgroup
+    float eps;
+    int32_t norm_form;      // 0: w, 1: (1 + w)
+    int32_t n_q, n_kv, head_dim;   // QKV layout (rows: q heads, k heads, v heads)
+    int32_t pg_base;        // QKV: page-table base of the sequence
+    int32_t pos;            // host position when state is null
+    int32_t act_n;          // GLU: real width of the activation (ffn)
+    int32_t act_per32;      // GLU: the down projection reads a per-32 pack
+    int32_t glu_form;       // GLU: 0 exp form, 1 rational-tanh form
+    int32_t batch;          // columns of activation (Cols variants), 1 at decode
+    int64_t x_stride;       // floats between activation vectors (batch / expert k)
+    int64_t xp_stride;      // bytes between packed activation vectors
+    int64_t y_stride;       // floats between output vectors (y, act) per batch / expert k
+    // MoE indirection: workgroups cover n_sel copies of the rows; copy k reads
+    // weight w + sel[k]·expert_bytes, activation x + k·x_stride, writes at k·y_stride
+    const int32_t *sel;
+    int64_t expert_bytes;
+    int32_t n_sel;
+    int32_t pad2;
+} cj_gemv_args;
+
+typedef struct {
+    float *hs; const float *y; const float *w; int64_t n; int32_t n_used; int32_t pad;
+} cj_combine_args;
+
+typedef struct {
+    uint8_t *out;           // packed blocks
+    const float *x;         // input rows
+    const float *w;         // norm weight (norm variants)
+    float *xout;            // normed f32 out (may be null)
+    int64_t n, npad;        // real and padded widths
+    int64_t rows;           // rows (each n wide in x, npad/256*320 bytes in out)
+    float eps;
+    int32_t form, per32, do_norm;
+} cj_pack_args;
+
+typedef struct {
+    float *out; const float *g, *u;
+    uint8_t *packed;        // optional pack of the result
+    int64_t n, npad;
+    int32_t form;           // 0 exp, 1 rational tanh
+    int32_t per32;
+} cj_glu_args;
+
+typedef struct { float *a; const float *b; int64_t n; } cj_add_args;
+
+typedef struct {
+    float *q, *k; const float *v;
+    uint16_t *kc, *vc;
+    const float *qw, *kw;    // optional per-head norm weights (norm != 0)
+    const float *rope_cs;    // [ctx][half] (cos, sin)
+    const int32_t *pgtab;
+    const cj_step_state *state;
+    int32_t n_q, n_kv, head_dim, norm, form, pg_base, pos;
+    float eps;
+} cj_qkprep_args;
+
+typedef struct {
+    float *part;             // [n_q][splits][hd + 2] partials
+    float *out;              // merged f32 output (null: partials only)
+    const float *q;
+    const uint16_t *kc, *vc;
+    const int32_t *pgtab;
+    const cj_step_state *state;
+    int32_t *counters;       // per kv head arrival counters (merge in the last)
+    int32_t n_q, n_kv, head_dim, splits, pg_base;
+    int32_t count, from;     // host values when state is null
+    int32_t window;          // >0: attend the last `window` positions only
+    float scale;
+} cj_attn_args;
+
+typedef struct {
+    float *out; uint8_t *packed; const float *part;
+    int32_t n_q, head_dim, splits, per32;
+} cj_merge_args;
+
+typedef struct {
+    float *out; const uint8_t *table; const int32_t *tokens; const cj_step_state *state;
+    int32_t type; int64_t hidden; int64_t row_bytes; int32_t token;
+} cj_embed_args;
+
+typedef struct {
+    int32_t *tok; const float *v; float *pv; int32_t *pi; int32_t *counter;
+    int64_t n; int32_t row;
+} cj_argmax_args;
+
+typedef struct {
+    float *out; const uint8_t *raw;
+    int64_t elems;           // rows · cols elements decoded
+    int64_t row_bytes, cols;
+    int32_t type;
+    int32_t prepared;        // 1: the gemv row layout, 0: GGUF file blocks
+} cj_dequant_args;
+
+typedef struct {
+    uint8_t *dst; const uint8_t *src; int64_t rows, cols, src_row_bytes, dst_row_bytes; int32_t type; int32_t pad;
+} cj_prepare_args;
+
+typedef struct {
+    const float *logits; int32_t *sel; float *w; int32_t n_experts, n_used, norm_topk, rows;
+} cj_route_args;
+
+typedef struct {
+    // one MoE expert stage: rows of expert sel[k] for each k < n_used
+    const uint8_t *w;        // stacked experts [E][rows][row_bytes]
+    const float *x;          // f32 input (gate/up: the normed hidden; down: per-k activations)
+    float *y;                // gate/up: act out [n_used][rows]; down: accumulate into y[rows]
+    const int32_t *sel; const float *wts;
+    int64_t rows, cols, row_bytes, expert_bytes;
+    int32_t n_used, stage;   // stage 0: gate|up + silu·u, 1: down + weighted combine
+    int32_t type;
+    int32_t pad;
+} cj_moe_args;

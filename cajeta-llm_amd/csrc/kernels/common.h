@@ -1,0 +1,165 @@
+// common.h — device helpers for the gfx950 kernels (wave64, CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include "args.h"
+
+#define DEV __device__ __forceinline__
+
+// fp16 bits <-> f32 through the hardware converts (exact / round-to-nearest-even).
+DEV float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu))); }
+DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// Exact integer exchange inside a quad of lanes (DPP quad_perm).
+DEV int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+DEV int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+
+template <int W>
+DEV float group_sum(float v) {
+#pragma unroll
+    for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+template <int W>
+DEV int group_sum_i(int v) {
+#pragma unroll
+    for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+template <int W>
+DEV float group_max(float v) {
+#pragma unroll
+    for (int m = W / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+// Round half away from zero, the reference's Math.round on pack values.
+DEV int round_away(float v) { return (int)roundf(v); }
+
+// E8M0 half-scale 2^(e-128) with the e<2 denormal patterns (Quant.mxfp4Scale).
+DEV float mxfp4_scale(uint32_t e) { return __uint_as_float(e < 2 ? (0x00200000u << e) : ((e - 1) << 23)); }
+// E2M1 code as the reference's integer table {0,1,2,3,4,6,8,12} with the sign
+// bit: an integer first, so code 8 is +0, not -0 (Quant.mxfp4Code).
+DEV float mxfp4_val(uint32_t nib) {
+    const int m = (int)(nib & 7);
+    int v = m < 5 ? m : (m == 5 ? 6 : (m == 6 ? 8 : 12));
+    if (nib & 8) v = -v;
+    return (float)v;
+}
+
+// Zero the pad bytes [292, 320) of a per-256 pack block, so a pack's bytes
+// are fully determined (thread t < 7 writes one word).
+DEV void pack_zero_pad(uint8_t *blk, int t) {
+    if (t < 7) *(uint32_t *)(blk + 292 + 4 * t) = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Activation staging into LDS: the 320-byte block layout of the reference's
+// Quant.q8kPackPad / q8kPack32Pad ([0,256) q, [256,288) 8 int32 sums of 32,
+// [288,320) the f32 scale(s)). 256 threads; thread t owns element t of every
+// 256-wide block, so a block's amax is one workgroup reduction.
+//
+// The RMSNorm follows the reference CPU row form's order exactly: thread t
+// accumulates x[t + 256k]^2 in k order, then the 256 partials fold with
+// strides 128, 64, ..., 1 — the same adds, so the same bits.
+// ---------------------------------------------------------------------------
+
+#define STAGE_CHUNK 16     // 256-wide blocks held in registers at a time
+
+// RMSNorm scale of x[0..n): thread t sums x[t + 256k]^2 in k order, the 256
+// partials fold 128, 64, ..., 1 (lanes of wave 0 for the last six), then
+// 1/sqrt(ss/n + eps). `red` is 256 floats of LDS.
+DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
+    const int t = threadIdx.x;
+    float p = 0.0f;
+    for (int64_t e = t; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
+    red[t] = p;
+    __syncthreads();
+    if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
+    __syncthreads();
+    if (t < 64) {
+        float s = __fadd_rn(red[t], red[t + 64]);
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) s = __fadd_rn(s, __shfl_down(s, m));
+        if (t == 0) red[0] = s;
+    }
+    __syncthreads();
+    const float ss = red[0];
+    __syncthreads();
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+}
+
+// The staged value of element e: x[e], or x[e]·scale·w[e] under the norm.
+DEV float stage_value(const float *x, int64_t n, int64_t e, bool norm, float scale, const float *w, int form) {
+    if (e >= n) return 0.0f;
+    const float xv = x[e];
+    if (!norm) return xv;
+    const float wi = form == 1 ? __fadd_rn(1.0f, w[e]) : w[e];
+    return __fmul_rn(__fmul_rn(xv, scale), wi);
+}
+
+// Quantize the staged values of nblk blocks into LDS 320-byte blocks at sx,
+// STAGE_CHUNK blocks at a time (thread t = element t of each block).
+DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form,
+                    int per32, uint8_t *sx, float *bmax, float *xout) {
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    for (int k0 = 0; k0 < nblk; k0 += STAGE_CHUNK) {
+        float v[STAGE_CHUNK];
+#pragma unroll
+        for (int k = 0; k < STAGE_CHUNK; k++) {
+            const int64_t e = (int64_t)(k0 + k) * 256 + t;
+            v[k] = (k0 + k < nblk) ? stage_value(x, n, e, norm, scale, w, form) : 0.0f;
+            if (xout && k0 + k < nblk && e < n) xout[e] = v[k];
+        }
+#pragma unroll
+        for (int k = 0; k < STAGE_CHUNK; k++) {
+            if (k0 + k >= nblk) break;
+            const float a = fabsf(v[k]);
+            if (per32) {
+                const float m = group_max<32>(a);
+                if ((lane & 31) == 0) bmax[k * 8 + (t >> 5)] = m;
+            } else {
+                const float m = group_max<64>(a);
+                if (lane == 0) bmax[k * 8 + wv] = m;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < STAGE_CHUNK; k++) {
+            if (k0 + k >= nblk) break;
+            const float am = per32 ? bmax[k * 8 + (t >> 5)]
+                                   : fmaxf(fmaxf(bmax[k * 8 + 0], bmax[k * 8 + 1]), fmaxf(bmax[k * 8 + 2], bmax[k * 8 + 3]));
+            const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+            const int q = round_away(__fmul_rn(v[k], inv));
+            uint8_t *blk = sx + (k0 + k) * 320;
+            blk[t] = (uint8_t)(int8_t)q;
+            const int s = group_sum_i<32>(q);
+            if ((lane & 31) == 0) *(int32_t *)(blk + 256 + 4 * (t >> 5)) = s;
+            if (per32) {
+                if ((lane & 31) == 0) *(float *)(blk + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
+            } else {
+                if (t == 0) *(float *)(blk + 288) = __fdiv_rn(am, 127.0f);
+                pack_zero_pad(blk, t);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The staged values as f32 into LDS (formats that read f32 activations).
+DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form, float *xf) {
+    for (int64_t e = threadIdx.x; e < (int64_t)nblk * 256; e += 256) xf[e] = stage_value(x, n, e, norm, scale, w, form);
+    __syncthreads();
+}
+
+// Copy an already-packed activation (nblk blocks of 320 bytes) into LDS.
+DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx) {
+    const int t = threadIdx.x;
+    int n16 = nblk * 20;
+    for (int i = t; i < n16; i += 256) ((uint4 *)sx)[i] = ((const uint4 *)xp)[i];
+    __syncthreads();
+}
+
+DEV int32_t step_pos(const cj_step_state *st, int32_t pos) { return st ? st->pos : pos; }

@@ -1,0 +1,535 @@
+// gemv.hip — quantised mat-vec family for gfx950 (wave64).
+//
+// One body serves every decode projection: a prologue stages the activation
+// in LDS (copied pack, pack of f32, or RMSNorm + pack), a per-format core
+// streams the weight rows with 128-bit loads and integer dot4s, and an
+// epilogue stores, accumulates into the residual, applies RoPE + the fp16
+// K/V append, applies SiLU·up + the pack of the result, or takes the greedy
+// argmax. Lanes split a row into LPR-lane groups; each (wave, group) owns a
+// contiguous run of rows, two at a time, so paired rows (RoPE pairs, gate/up
+// pairs) meet in one lane.
+//
+// Prepared row layouts (HBM, 16-byte aligned rows):
+//   Q4_K : the GGUF blocks as they are: {f16 d, f16 dmin, 12 B scales, 128 B qs}
+//   Q6_K : [ql nb·128][qh nb·64][scales nb·16][d nb·2, padded to 16]
+//   Q8_0 : [qs nb·32][d nb·2, padded to 16]
+//   Q4_0 : [qs nb·16][d nb·2, padded to 16]
+//   MXFP4: [qs nb·16][e nb, padded to 16]
+#include "common.h"
+
+#define LDS_SCRATCH 3072   // red[256] + bmax[512] floats
+
+// ------------------------------------------------------------------ cores
+
+// Q4_K × q8_K: per (block, 64-element chunk) unit, the two sub-blocks' int
+// dots scaled by their 6-bit scales, the mins term from the pack's sums;
+// the quad of lanes sharing a block sums exactly, then
+// term = d·xs·sumi − dmin·xs·dmins (the reference block term).
+template <int NR, int LPR>
+DEV void core_q4k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int slot, float (&acc)[NR]) {
+    const int units = nb * 4;
+    for (int u = slot; u < units; u += LPR) {
+        const int b = u >> 2, j = u & 3;
+        uint4 hd[NR], q0[NR], q1[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint8_t *blk = wr[r] + (int64_t)b * 144;
+            hd[r] = *(const uint4 *)blk;
+            q0[r] = *(const uint4 *)(blk + 16 + 32 * j);
+            q1[r] = *(const uint4 *)(blk + 32 + 32 * j);
+        }
+        const uint8_t *ax = sx + b * 320 + 64 * j;
+        const uint4 a0 = *(const uint4 *)(ax), a1 = *(const uint4 *)(ax + 16);
+        const uint4 a2 = *(const uint4 *)(ax + 32), a3 = *(const uint4 *)(ax + 48);
+        const int2 bs = *(const int2 *)(sx + b * 320 + 256 + 8 * j);
+        const float xs = *(const float *)(sx + b * 320 + 288);
+        const int hi = j >= 2;
+        const int t0 = (2 * j) & 3;
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint32_t M = 0x0F0F0F0Fu;
+            int dlo = 0, dhi = 0;
+            dlo = sdot4(q0[r].x & M, a0.x, dlo); dlo = sdot4(q0[r].y & M, a0.y, dlo);
+            dlo = sdot4(q0[r].z & M, a0.z, dlo); dlo = sdot4(q0[r].w & M, a0.w, dlo);
+            dlo = sdot4(q1[r].x & M, a1.x, dlo); dlo = sdot4(q1[r].y & M, a1.y, dlo);
+            dlo = sdot4(q1[r].z & M, a1.z, dlo); dlo = sdot4(q1[r].w & M, a1.w, dlo);
+            dhi = sdot4((q0[r].x >> 4) & M, a2.x, dhi); dhi = sdot4((q0[r].y >> 4) & M, a2.y, dhi);
+            dhi = sdot4((q0[r].z >> 4) & M, a2.z, dhi); dhi = sdot4((q0[r].w >> 4) & M, a2.w, dhi);
+            dhi = sdot4((q1[r].x >> 4) & M, a3.x, dhi); dhi = sdot4((q1[r].y >> 4) & M, a3.y, dhi);
+            dhi = sdot4((q1[r].z >> 4) & M, a3.z, dhi); dhi = sdot4((q1[r].w >> 4) & M, a3.w, dhi);
+            // 6-bit scales/mins of sub-blocks 2j, 2j+1 (the headK4 unpacking)
+            const uint32_t sy = hd[r].y, sz = hd[r].z, sw = hd[r].w;
+            int sc0, mn0, sc1, mn1;
+            {
+                uint32_t A0 = (sy >> (8 * t0)) & 255, B0 = (sz >> (8 * t0)) & 255, C0 = (sw >> (8 * t0)) & 255;
+                uint32_t A1 = (sy >> (8 * t0 + 8)) & 255, B1 = (sz >> (8 * t0 + 8)) & 255, C1 = (sw >> (8 * t0 + 8)) & 255;
+                if (hi) {
+                    sc0 = (C0 & 15) | ((A0 >> 2) & 48); mn0 = (C0 >> 4) | ((B0 >> 2) & 48);
+                    sc1 = (C1 & 15) | ((A1 >> 2) & 48); mn1 = (C1 >> 4) | ((B1 >> 2) & 48);
+                } else {
+                    sc0 = A0 & 63; mn0 = B0 & 63; sc1 = A1 & 63; mn1 = B1 & 63;
+                }
+            }
+            int sumi = dlo * sc0 + dhi * sc1;
+            int dmins = mn0 * bs.x + mn1 * bs.y;
+            sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
+            dmins += quad_xor1(dmins); dmins += quad_xor2(dmins);
+            const float d = h2f(hd[r].x), dmin = h2f(hd[r].x >> 16);
+            float term = __fsub_rn(__fmul_rn(__fmul_rn(d, xs), (float)sumi), __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
+            acc[r] += (j == 0) ? term : 0.0f;
+        }
+    }
+}
+
+// Q6_K × q8_K: unit = (block, 64 elements): half g, lane half hl; four
+// 16-element scale groups; the 6-bit values 0..63 dot the int8 activation and
+// 32·Σa comes off per group (Σa once per unit, shared by the rows).
+template <int NR, int LPR>
+DEV void core_q6k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int slot, float (&acc)[NR]) {
+    const int units = nb * 4;
+    for (int u = slot; u < units; u += LPR) {
+        const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
+        uint4 qa[NR], qb[NR], qh[NR];
+        uint2 sc[NR];
+        uint32_t dh[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint8_t *row = wr[r];
+            qa[r] = *(const uint4 *)(row + (int64_t)b * 128 + 64 * g + 16 * hl);
+            qb[r] = *(const uint4 *)(row + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
+            qh[r] = *(const uint4 *)(row + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
+            sc[r] = *(const uint2 *)(row + (int64_t)nb * 192 + (int64_t)b * 16 + 8 * g);
+            dh[r] = *(const uint16_t *)(row + (int64_t)nb * 208 + 2 * b);
+        }
+        const uint8_t *ab = sx + b * 320 + 128 * g + 16 * hl;
+        uint4 a[4];
+        int S[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            a[k] = *(const uint4 *)(ab + 32 * k);
+            int s = 0;
+            s = sdot4(0x01010101u, a[k].x, s); s = sdot4(0x01010101u, a[k].y, s);
+            s = sdot4(0x01010101u, a[k].z, s); s = sdot4(0x01010101u, a[k].w, s);
+            S[k] = s;
+        }
+        const float xs = *(const float *)(sx + b * 320 + 288);
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            int sumi = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint4 ql = (k & 1) ? qb[r] : qa[r];
+                const int sh = (k >> 1) * 4;
+                const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
+                uint32_t vx = ((ql.x >> sh) & M) | (((qh[r].x >> (2 * k)) & H) << 4);
+                uint32_t vy = ((ql.y >> sh) & M) | (((qh[r].y >> (2 * k)) & H) << 4);
+                uint32_t vz = ((ql.z >> sh) & M) | (((qh[r].z >> (2 * k)) & H) << 4);
+                uint32_t vw = ((ql.w >> sh) & M) | (((qh[r].w >> (2 * k)) & H) << 4);
+                int dt = 0;
+                dt = sdot4(vx, a[k].x, dt); dt = sdot4(vy, a[k].y, dt);
+                dt = sdot4(vz, a[k].z, dt); dt = sdot4(vw, a[k].w, dt);
+                const int byte_i = 2 * k + hl;
+                const uint32_t word = byte_i < 4 ? sc[r].x : sc[r].y;
+                const int scv = (int)(int8_t)((word >> (8 * (byte_i & 3))) & 255);
+                sumi += scv * (dt - 32 * S[k]);
+            }
+            sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
+            const float d = h2f(dh[r]);
+            float term = __fmul_rn(__fmul_rn(d, xs), (float)sumi);
+            acc[r] += (j == 0) ? term : 0.0f;
+        }
+    }
+}
+
+// Q8_0 × per-32 int8: one 32-element block a lane; (d·xs)·isum per block.
+template <int NR, int LPR>
+DEV void core_q80(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb32, int slot, float (&acc)[NR]) {
+    for (int u = slot; u < nb32; u += LPR) {
+        uint4 w0[NR], w1[NR];
+        uint32_t dh[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            w0[r] = *(const uint4 *)(wr[r] + (int64_t)u * 32);
+            w1[r] = *(const uint4 *)(wr[r] + (int64_t)u * 32 + 16);
+            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * u);
+        }
+        const uint8_t *ab = sx + (u >> 3) * 320;
+        const uint4 a0 = *(const uint4 *)(ab + 32 * (u & 7)), a1 = *(const uint4 *)(ab + 32 * (u & 7) + 16);
+        const float xs = *(const float *)(ab + 288 + 4 * (u & 7));
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            int s = 0;
+            s = sdot4(w0[r].x, a0.x, s); s = sdot4(w0[r].y, a0.y, s);
+            s = sdot4(w0[r].z, a0.z, s); s = sdot4(w0[r].w, a0.w, s);
+            s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
+            s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
+            acc[r] += __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
+        }
+    }
+}
+
+// Q4_0 × f32: d·Σ (q − 8)·x per 32-element block.
+template <int NR, int LPR>
+DEV void core_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
+    for (int u = slot; u < nb32; u += LPR) {
+        uint4 w[NR];
+        uint32_t dh[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            w[r] = *(const uint4 *)(wr[r] + (int64_t)u * 16);
+            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 16 + 2 * u);
+        }
+        float xv[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
+            xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+        }
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint32_t ws[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+            float dot = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++) {
+                const int q = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
+                dot = __fadd_rn(dot, __fmul_rn((float)((q & 15) - 8), xv[jj]));
+                dot = __fadd_rn(dot, __fmul_rn((float)((q >> 4) - 8), xv[jj + 16]));
+            }
+            acc[r] += __fmul_rn(h2f(dh[r]), dot);
+        }
+    }
+}
+
+
+// MXFP4 × f32: code(nib)·2^(e−128)·x in element order per block.
+template <int NR, int LPR>
+DEV void core_mxfp4(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
+    for (int u = slot; u < nb32; u += LPR) {
+        uint4 w[NR];
+        uint32_t eb[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            w[r] = *(const uint4 *)(wr[r] + (int64_t)u * 16);
+            eb[r] = wr[r][(int64_t)nb32 * 16 + u];
+        }
+        float xv[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
+            xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+        }
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint32_t ws[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+            const float d = mxfp4_scale(eb[r]);
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; k++) {
+                const int jj = k & 15;
+                const uint32_t byv = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
+                const uint32_t nib = k < 16 ? (byv & 15) : (byv >> 4);
+                a = __fadd_rn(a, __fmul_rn(__fmul_rn(mxfp4_val(nib), d), xv[k]));
+            }
+            acc[r] += a;
+        }
+    }
+}
+
+// f32 weights × f32 (the MoE router): four columns a unit.
+template <int NR, int LPR>
+DEV void core_f32(const uint8_t *const (&wr)[NR], const float *xf, int n4, int slot, float (&acc)[NR]) {
+    for (int u = slot; u < n4; u += LPR) {
+        const float4 x = *(const float4 *)(xf + 4 * u);
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const float4 w = *(const float4 *)(wr[r] + (int64_t)u * 16);
+            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.x, x.x));
+            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.y, x.y));
+            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.z, x.z));
+            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.w, x.w));
+        }
+    }
+}
+
+// ------------------------------------------------------------- epilogues
+
+DEV int64_t kv_index(const int32_t *pgtab, int pg_base, int pos, int nkv, int kvh, int hd) {
+    const int page = pgtab[pg_base + (pos >> 6)];
+    return (((int64_t)page * nkv + kvh) * 64 + (pos & 63)) * hd;
+}
+
+DEV float silu_exp(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, __expf(0.0f - x))); }
+
+// The CPU backend's rational-tanh SiLU (Eigen's float tanh approximation).
+DEV float silu_tanh_mul(float x, float u) {
+    const float tlo = -7.90531110763549805f;
+    float xa = fmaxf(x, -16.0f);
+    float xb = __fsub_rn(-16.0f, xa);
+    float xc = __fsub_rn(-16.0f, fmaxf(xb, -32.0f));
+    float t0 = __fmul_rn(0.5f, __fmaf_rn(__fmul_rn(0.0f, xc), __fmul_rn(xc, xc), xc));
+    float ta = fmaxf(t0, tlo);
+    float tb = __fsub_rn(tlo, ta);
+    float t = __fsub_rn(tlo, fmaxf(tb, -15.8106222152709961f));
+    float t2 = __fmul_rn(t, t);
+    float p = __fmaf_rn(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
+    p = __fmaf_rn(p, t2, -8.60467152213735e-11f);
+    p = __fmaf_rn(p, t2, 5.12229709037114e-08f);
+    p = __fmaf_rn(p, t2, 1.48572235717979e-05f);
+    p = __fmaf_rn(p, t2, 6.37261928875436e-04f);
+    p = __fmul_rn(__fmaf_rn(p, t2, 4.89352455891786e-03f), t);
+    float q = __fmaf_rn(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
+    q = __fmaf_rn(q, t2, 2.26843463243900e-03f);
+    q = __fmaf_rn(q, t2, 4.89352518554385e-03f);
+    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, xa), __fadd_rn(1.0f, __fdiv_rn(p, q))), u);
+}
+
+// Pack one 256-wide block of an f32 vector (values past n are zero) from
+// HBM into the 320-byte layout, by the whole workgroup.
+DEV void pack_block_global(const float *x, int64_t n, int64_t blk, int per32, uint8_t *out, float *bmax) {
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t e = blk * 256 + t;
+    float v = e < n ? x[e] : 0.0f;
+    float a = fabsf(v);
+    if (per32) {
+        float m = group_max<32>(a);
+        if ((lane & 31) == 0) bmax[t >> 5] = m;
+    } else {
+        float m = group_max<64>(a);
+        if (lane == 0) bmax[t >> 6] = m;
+    }
+    __syncthreads();
+    float am = per32 ? bmax[t >> 5] : fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
+    float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    int q = round_away(__fmul_rn(v, inv));
+    uint8_t *ob = out + blk * 320;
+    ob[t] = (uint8_t)(int8_t)q;
+    int s = group_sum_i<32>(q);
+    if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
+    if (per32) {
+        if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
+    } else {
+        if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
+        pack_zero_pad(ob, t);
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ body
+
+template <int FMT, int LPR>
+DEV void gemv_body(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *red = (float *)smem;
+    float *bmax = red + 256;
+    uint8_t *sx = smem + LDS_SCRATCH;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int64_t cols = a.cols;
+    const bool f32act = (FMT == CJ_Q4_0 || FMT == CJ_MXFP4 || FMT == CJ_F32);
+    const int nblk = (int)((cols + 255) / 256);
+
+    // MoE indirection: copy k of the rows reads expert sel[k]
+    int64_t wg = blockIdx.x;
+    int kidx = 0;
+    if (a.sel) {
+        const int64_t wpk = (a.rows + a.rows_per_wg - 1) / a.rows_per_wg;
+        kidx = (int)(wg / wpk);
+        wg = wg % wpk;
+    }
+    const uint8_t *W = a.w + (a.sel ? (int64_t)a.sel[kidx] * a.expert_bytes : 0);
+    const float *X = a.x ? a.x + kidx * a.x_stride : nullptr;
+    float *Y = a.y ? a.y + kidx * a.y_stride : nullptr;
+    float *ACT = a.act ? a.act + kidx * a.y_stride : nullptr;
+
+    // ---- prologue: the activation into LDS
+    if (a.pro == CJ_PRO_PACKED) {
+        stage_copy(a.xp + kidx * a.xp_stride, nblk, sx);
+    } else {
+        const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
+        const float scale = norm ? stage_norm_scale(X, cols, a.eps, red) : 1.0f;
+        if (f32act) stage_f32(X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx);
+        else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, bmax, nullptr);
+    }
+
+    // ---- rows
+    constexpr int G = 64 / LPR;
+    const int group = lane / LPR, slot = lane % LPR;
+    const int rpg = a.rows_per_wg / (4 * G);              // rows per (wave, group), even
+    const int64_t run0 = wg * a.rows_per_wg + (int64_t)(wave * G + group) * rpg;
+    const int nb = (int)(cols / 256);
+    const int nb32 = (int)(cols / 32);
+    const int pos = (a.epi == CJ_EPI_QKV_ROPE || a.epi == CJ_EPI_ARGMAX) ? step_pos(a.state, a.pos) : 0;
+
+    float best_v = 0.0f;
+    int best_i = -1;
+
+    for (int i = 0; i < rpg; i += 2) {
+        const int64_t r0 = run0 + i, r1 = r0 + 1;
+        const uint8_t *wr[2];
+        wr[0] = W + (r0 < a.rows ? r0 : a.rows - 1) * a.row_bytes;
+        wr[1] = W + (r1 < a.rows ? r1 : a.rows - 1) * a.row_bytes;
+        float acc[2] = {0.0f, 0.0f};
+        if (FMT == CJ_Q4_K) core_q4k<2, LPR>(wr, sx, nb, slot, acc);
+        else if (FMT == CJ_Q6_K) core_q6k<2, LPR>(wr, sx, nb, slot, acc);
+        else if (FMT == CJ_Q8_0) core_q80<2, LPR>(wr, sx, nb32, slot, acc);
+        else if (FMT == CJ_Q4_0) core_q40<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
+        else if (FMT == CJ_MXFP4) core_mxfp4<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
+        else core_f32<2, LPR>(wr, (const float *)sx, (int)(cols / 4), slot, acc);
+        float v0 = group_sum<LPR>(acc[0]);
+        float v1 = group_sum<LPR>(acc[1]);
+        if (slot != 0) continue;
+
+        switch (a.epi) {
+        case CJ_EPI_STORE:
+            if (r0 < a.rows) Y[a.y_off + r0] = v0;
+            if (r1 < a.rows) Y[a.y_off + r1] = v1;
+            break;
+        case CJ_EPI_ACCUM:
+            if (r0 < a.rows) Y[a.y_off + r0] = __fadd_rn(Y[a.y_off + r0], v0);
+            if (r1 < a.rows) Y[a.y_off + r1] = __fadd_rn(Y[a.y_off + r1], v1);
+            break;
+        case CJ_EPI_QKV_ROPE: {
+            if (r0 >= a.rows) break;
+            const int hd = a.head_dim, half = hd >> 1;
+            const int64_t qrows = (int64_t)a.n_q * hd, krows = (int64_t)a.n_kv * hd;
+            if (r0 < qrows + krows) {
+                // GGUF pair order: row h·hd + 2b + a holds HF dim a·half + b
+                const int64_t rr = r0 < qrows ? r0 : r0 - qrows;
+                const int h = (int)(rr / hd), bb = (int)(rr % hd) >> 1;
+                const float2 cs = *(const float2 *)(a.rope_cs + 2 * ((int64_t)pos * half + bb));
+                const float ra = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
+                const float rb = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
+                if (r0 < qrows) {
+                    a.q_out[(int64_t)h * hd + bb] = ra;
+                    a.q_out[(int64_t)h * hd + half + bb] = rb;
+                } else {
+                    const int64_t ki = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+                    a.kc[ki + bb] = f2h(ra);
+                    a.kc[ki + half + bb] = f2h(rb);
+                }
+            } else {
+                const int64_t rr = r0 - qrows - krows;
+                const int h = (int)(rr / hd), d = (int)(rr % hd);
+                const int64_t vi = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+                a.vc[vi + d] = f2h(v0);
+                a.vc[vi + d + 1] = f2h(v1);
+            }
+        } break;
+        case CJ_EPI_GLU: {
+            if (r0 >= a.rows) break;
+            const int64_t ai = r0 >> 1;
+            ACT[ai] = a.glu_form ? silu_tanh_mul(v0, v1) : __fmul_rn(silu_exp(v0), v1);
+        } break;
+        case CJ_EPI_ARGMAX: {
+            if (r0 < a.rows) {
+                a.y[r0] = v0;
+                if (best_i < 0 || v0 > best_v) { best_v = v0; best_i = (int)r0; }
+            }
+            if (r1 < a.rows) {
+                a.y[r1] = v1;
+                if (best_i < 0 || v1 > best_v) { best_v = v1; best_i = (int)r1; }
+            }
+        } break;
+        }
+    }
+
+    if (a.epi == CJ_EPI_GLU && a.act_pack) {
+        // The last workgroup to finish a 256-wide block of the activation
+        // packs it for the down projection.
+        __shared__ int last_blocks[4];
+        __shared__ int n_last;
+        __threadfence();
+        __syncthreads();
+        const int64_t a0 = (wg * a.rows_per_wg) >> 1;
+        int64_t a1 = a0 + (a.rows_per_wg >> 1);
+        if (a1 > (a.rows >> 1)) a1 = a.rows >> 1;
+        if (t == 0) {
+            n_last = 0;
+            for (int64_t blk = a0 / 256; blk * 256 < a1; blk++) {
+                const int64_t lo = blk * 256 > a0 ? blk * 256 : a0;
+                const int64_t hi = (blk + 1) * 256 < a1 ? (blk + 1) * 256 : a1;
+                const int64_t real = ((blk + 1) * 256 < a.act_n ? (blk + 1) * 256 : a.act_n) - blk * 256;
+                const int mine = (int)(hi - lo);
+                const int old = atomicAdd(&a.counters[blk], mine);
+                if (old + mine == real) last_blocks[n_last++] = (int)blk;
+            }
+        }
+        __syncthreads();
+        const int nl = n_last;
+        if (nl > 0) {
+            __threadfence();
+            for (int k = 0; k < nl; k++) {
+                const int blk = last_blocks[k];
+                pack_block_global(a.act, a.act_n, blk, a.act_per32, a.act_pack, bmax);
+                if (t == 0) a.counters[blk] = 0;
+            }
+        }
+    } else if (a.epi == CJ_EPI_ARGMAX) {
+        // first occurrence across the workgroup, then the last workgroup
+        // reduces every workgroup's partial and advances the step
+        __shared__ float bv[256];
+        __shared__ int bi[256];
+        __shared__ int ticket;
+        bv[t] = best_v;
+        bi[t] = best_i;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (t < s) {
+                float ov = bv[t + s]; int oi = bi[t + s];
+                float mv = bv[t]; int mi = bi[t];
+                bool take = mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)));
+                if (take) { bv[t] = ov; bi[t] = oi; }
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            a.part_v[blockIdx.x] = bv[0];
+            a.part_i[blockIdx.x] = bi[0];
+            __threadfence();
+            ticket = atomicAdd(a.counters, 1);
+        }
+        __syncthreads();
+        if (ticket != (int)gridDim.x - 1) return;
+        __threadfence();
+        float gb = 0.0f; int gi = -1;
+        for (int g = t; g < (int)gridDim.x; g += 256) {
+            float x = __builtin_nontemporal_load(&a.part_v[g]);
+            int xi = __builtin_nontemporal_load(&a.part_i[g]);
+            if (xi >= 0 && (gi < 0 || x > gb || (x == gb && xi < gi))) { gb = x; gi = xi; }
+        }
+        bv[t] = gb; bi[t] = gi;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (t < s) {
+                float ov = bv[t + s]; int oi = bi[t + s];
+                float mv = bv[t]; int mi = bi[t];
+                bool take = mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)));
+                if (take) { bv[t] = ov; bi[t] = oi; }
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            a.counters[0] = 0;
+            if (a.preds) a.preds[pos + 1] = bi[0];
+            if (a.tokens && (!a.state || pos + 1 >= a.state->fixed_until)) a.tokens[pos + 1] = bi[0];
+            if (a.state) a.state->pos = pos + 1;
+        }
+    }
+}
+
+#define GEMV_KERNEL(NAME, FMT, LPR)                                                    \
+    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) {            \
+        gemv_body<FMT, LPR>(a);                                                         \
+    }
+
+#define GEMV_FAMILY(PFX, FMT)               \
+    GEMV_KERNEL(PFX##_l64, FMT, 64)         \
+    GEMV_KERNEL(PFX##_l32, FMT, 32)         \
+    GEMV_KERNEL(PFX##_l16, FMT, 16)         \
+    GEMV_KERNEL(PFX##_l8, FMT, 8)
+
+GEMV_FAMILY(cj_gemv_q4k, CJ_Q4_K)
+GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K)
+GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0)
+GEMV_FAMILY(cj_gemv_q40, CJ_Q4_0)
+GEMV_FAMILY(cj_gemv_mxfp4, CJ_MXFP4)
+GEMV_FAMILY(cj_gemv_f32, CJ_F32)

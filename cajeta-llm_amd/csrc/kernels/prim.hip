@@ -1,0 +1,343 @@
+// prim.hip — the small decode primitives for gfx950: activation packs
+// (with and without the RMSNorm), SwiGLU (+ pack), residual add, embedding
+// row decode, first-occurrence argmax, block dequant and the load-time
+// re-layout of weight rows.
+#include "common.h"
+
+// ---------------------------------------------------------------- packs
+
+// One workgroup per row: optional RMSNorm, optional f32 out, then the pack
+// (Prim.rmsnormPackDevice / QuantKernel.q8kPackRowsLaunchNoSync contracts).
+extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
+    __shared__ float red[256];
+    __shared__ float bmax[STAGE_CHUNK * 8];
+    extern __shared__ __align__(16) uint8_t sx[];
+    const int64_t row = blockIdx.x;
+    const float *x = a.x + row * a.n;
+    const int nblk = (int)(a.npad / 256);
+    const float scale = a.do_norm ? stage_norm_scale(x, a.n, a.eps, red) : 1.0f;
+    float *xo = a.xout ? a.xout + row * a.n : nullptr;
+    if (!a.out) {
+        for (int64_t e = threadIdx.x; e < a.n; e += 256) xo[e] = stage_value(x, a.n, e, a.do_norm, scale, a.w, a.form);
+        return;
+    }
+    stage_pack(x, a.n, nblk, a.do_norm, scale, a.w, a.form, a.per32, sx, bmax, xo);
+    uint8_t *o = a.out + row * (int64_t)nblk * 320;
+    for (int i = threadIdx.x; i < nblk * 20; i += 256) ((uint4 *)o)[i] = ((const uint4 *)sx)[i];
+}
+
+// ------------------------------------------------------------------ glu
+
+DEV float silu_exp_p(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, __expf(0.0f - x))); }
+DEV float silu_tanh_mul_p(float x, float u);
+
+// One workgroup per 256-wide block: out = act(g)·u, then (optionally) that
+// block's pack — the block is local, so no other workgroup is waited on.
+extern "C" __global__ void __launch_bounds__(256) cj_glu(cj_glu_args a) {
+    __shared__ float bmax[8];
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t e = (int64_t)blockIdx.x * 256 + t;
+    float v = 0.0f;
+    if (e < a.n) {
+        const float g = a.g[e], u = a.u[e];
+        v = a.form ? silu_tanh_mul_p(g, u) : __fmul_rn(silu_exp_p(g), u);
+        a.out[e] = v;
+    }
+    if (!a.packed) return;
+    float am;
+    const float av = fabsf(v);
+    if (a.per32) {
+        float m = group_max<32>(av);
+        if ((lane & 31) == 0) bmax[t >> 5] = m;
+        __syncthreads();
+        am = bmax[t >> 5];
+    } else {
+        float m = group_max<64>(av);
+        if (lane == 0) bmax[t >> 6] = m;
+        __syncthreads();
+        am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
+    }
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    const int q = round_away(__fmul_rn(v, inv));
+    uint8_t *ob = a.packed + (int64_t)blockIdx.x * 320;
+    ob[t] = (uint8_t)(int8_t)q;
+    const int s = group_sum_i<32>(q);
+    if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
+    if (a.per32) {
+        if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
+    } else {
+        if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
+        pack_zero_pad(ob, t);
+    }
+}
+
+DEV float silu_tanh_mul_p(float x, float u) {
+    const float tlo = -7.90531110763549805f;
+    float xa = fmaxf(x, -16.0f);
+    float xb = __fsub_rn(-16.0f, xa);
+    float xc = __fsub_rn(-16.0f, fmaxf(xb, -32.0f));
+    float t0 = __fmul_rn(0.5f, __fmaf_rn(__fmul_rn(0.0f, xc), __fmul_rn(xc, xc), xc));
+    float ta = fmaxf(t0, tlo);
+    float tb = __fsub_rn(tlo, ta);
+    float t = __fsub_rn(tlo, fmaxf(tb, -15.8106222152709961f));
+    float t2 = __fmul_rn(t, t);
+    float p = __fmaf_rn(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
+    p = __fmaf_rn(p, t2, -8.60467152213735e-11f);
+    p = __fmaf_rn(p, t2, 5.12229709037114e-08f);
+    p = __fmaf_rn(p, t2, 1.48572235717979e-05f);
+    p = __fmaf_rn(p, t2, 6.37261928875436e-04f);
+    p = __fmul_rn(__fmaf_rn(p, t2, 4.89352455891786e-03f), t);
+    float q = __fmaf_rn(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
+    q = __fmaf_rn(q, t2, 2.26843463243900e-03f);
+    q = __fmaf_rn(q, t2, 4.89352518554385e-03f);
+    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, xa), __fadd_rn(1.0f, __fdiv_rn(p, q))), u);
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_add(cj_add_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < a.n) a.a[i] = __fadd_rn(a.a[i], a.b[i]);
+}
+
+// --------------------------------------------------------- block decode
+
+
+// Element e of a FILE-layout row (GGUF blocks), the reference block bodies
+// (Quant.q80Block / q40Block / q4kBlock / q6kBlock / mxfp4Block).
+DEV float decode_file(int type, const uint8_t *row, int64_t e) {
+    switch (type) {
+    case CJ_F32: return ((const float *)row)[e];
+    case CJ_F16: return h2f(((const uint16_t *)row)[e]);
+    case CJ_Q8_0: {
+        const uint8_t *b = row + (e >> 5) * 34;
+        return __fmul_rn(h2f(*(const uint16_t *)b), (float)(int8_t)b[2 + (e & 31)]);
+    }
+    case CJ_Q4_0: {
+        const uint8_t *b = row + (e >> 5) * 18;
+        const int j = e & 31;
+        const int q = b[2 + (j & 15)];
+        const int v = j < 16 ? (q & 15) - 8 : (q >> 4) - 8;
+        return __fmul_rn(h2f(*(const uint16_t *)b), (float)v);
+    }
+    case CJ_MXFP4: {
+        const uint8_t *b = row + (e >> 5) * 17;
+        const int j = e & 31;
+        const int byv = b[1 + (j & 15)];
+        return __fmul_rn(mxfp4_val(j < 16 ? (byv & 15) : (byv >> 4)), mxfp4_scale(b[0]));
+    }
+    case CJ_Q4_K: {
+        const uint8_t *b = row + (e >> 8) * 144;
+        const int el = e & 255, g = el / 64, r = el % 64, s = r / 32, l = r % 32, sb = el / 32;
+        const int q = (b[16 + 32 * g + l] >> (4 * s)) & 15;
+        const uint8_t *sc = b + 4;
+        int scv, mnv;
+        if (sb < 4) { scv = sc[sb] & 63; mnv = sc[sb + 4] & 63; }
+        else { scv = (sc[sb + 4] & 15) | ((sc[sb - 4] >> 2) & 48); mnv = (sc[sb + 4] >> 4) | ((sc[sb] >> 2) & 48); }
+        const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)scv), (float)q), __fmul_rn(dmin, (float)mnv));
+    }
+    case CJ_Q6_K: {
+        const uint8_t *b = row + (e >> 8) * 210;
+        const int el = e & 255, g = el / 128, r = el % 128, sl = r / 64, l64 = r % 64, sh = r / 32, l32 = r % 32;
+        const int ql = (b[64 * g + l64] >> (4 * sl)) & 15;
+        const int qh = (b[128 + 32 * g + l32] >> (2 * sh)) & 3;
+        const int q = (ql | (qh << 4)) - 32;
+        return __fmul_rn(__fmul_rn(h2f(*(const uint16_t *)(b + 208)), (float)(int8_t)b[192 + el / 16]), (float)q);
+    }
+    }
+    return 0.0f;
+}
+
+// Element e of a PREPARED row (the gemv layouts), for the layout's own check.
+DEV float decode_prepared(int type, const uint8_t *row, int64_t cols, int64_t e) {
+    const int64_t nb = cols / 256, nb32 = cols / 32;
+    switch (type) {
+    case CJ_Q8_0: {
+        const int64_t b = e >> 5;
+        return __fmul_rn(h2f(*(const uint16_t *)(row + nb32 * 32 + 2 * b)), (float)(int8_t)row[b * 32 + (e & 31)]);
+    }
+    case CJ_Q4_0: {
+        const int64_t b = e >> 5;
+        const int j = e & 31;
+        const int q = row[b * 16 + (j & 15)];
+        const int v = j < 16 ? (q & 15) - 8 : (q >> 4) - 8;
+        return __fmul_rn(h2f(*(const uint16_t *)(row + nb32 * 16 + 2 * b)), (float)v);
+    }
+    case CJ_MXFP4: {
+        const int64_t b = e >> 5;
+        const int j = e & 31;
+        const int byv = row[b * 16 + (j & 15)];
+        return __fmul_rn(mxfp4_val(j < 16 ? (byv & 15) : (byv >> 4)), mxfp4_scale(row[nb32 * 16 + b]));
+    }
+    case CJ_Q6_K: {
+        const int64_t b = e >> 8;
+        const int el = e & 255, g = el / 128, r = el % 128, sl = r / 64, l64 = r % 64, sh = r / 32, l32 = r % 32;
+        const int ql = (row[b * 128 + 64 * g + l64] >> (4 * sl)) & 15;
+        const int qh = (row[nb * 128 + b * 64 + 32 * g + l32] >> (2 * sh)) & 3;
+        const int q = (ql | (qh << 4)) - 32;
+        const float d = h2f(*(const uint16_t *)(row + nb * 208 + 2 * b));
+        return __fmul_rn(__fmul_rn(d, (float)(int8_t)row[nb * 192 + b * 16 + el / 16]), (float)q);
+    }
+    default: return decode_file(type, row, e);
+    }
+}
+
+// Dequantize rows (Quant.dequantize): grid-stride over elements, from the
+// file layout or the prepared layout.
+extern "C" __global__ void __launch_bounds__(256) cj_dequant(cj_dequant_args a) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.elems; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / a.cols, c = i % a.cols;
+        const uint8_t *row = a.raw + r * a.row_bytes;
+        a.out[i] = a.prepared ? decode_prepared(a.type, row, a.cols, c) : decode_file(a.type, row, c);
+    }
+}
+
+// Load-time re-layout of FILE rows into the prepared gemv layout: one thread
+// per block. `src` rows are the GGUF bytes, `dst` rows the prepared ones.
+
+extern "C" __global__ void __launch_bounds__(256) cj_prepare(cj_prepare_args a) {
+    const int64_t bpr = a.type == CJ_Q6_K ? a.cols / 256 : a.cols / 32;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.rows * bpr) return;
+    const int64_t r = i / bpr, b = i % bpr;
+    const uint8_t *s = a.src + r * a.src_row_bytes;
+    uint8_t *d = a.dst + r * a.dst_row_bytes;
+    switch (a.type) {
+    case CJ_Q6_K: {
+        const uint8_t *blk = s + b * 210;
+        for (int k = 0; k < 128; k++) d[b * 128 + k] = blk[k];
+        for (int k = 0; k < 64; k++) d[bpr * 128 + b * 64 + k] = blk[128 + k];
+        for (int k = 0; k < 16; k++) d[bpr * 192 + b * 16 + k] = blk[192 + k];
+        d[bpr * 208 + 2 * b] = blk[208];
+        d[bpr * 208 + 2 * b + 1] = blk[209];
+    } break;
+    case CJ_Q8_0: {
+        const uint8_t *blk = s + b * 34;
+        for (int k = 0; k < 32; k++) d[b * 32 + k] = blk[2 + k];
+        d[bpr * 32 + 2 * b] = blk[0];
+        d[bpr * 32 + 2 * b + 1] = blk[1];
+    } break;
+    case CJ_Q4_0: {
+        const uint8_t *blk = s + b * 18;
+        for (int k = 0; k < 16; k++) d[b * 16 + k] = blk[2 + k];
+        d[bpr * 16 + 2 * b] = blk[0];
+        d[bpr * 16 + 2 * b + 1] = blk[1];
+    } break;
+    case CJ_MXFP4: {
+        const uint8_t *blk = s + b * 17;
+        for (int k = 0; k < 16; k++) d[b * 16 + k] = blk[1 + k];
+        d[bpr * 16 + b] = blk[0];
+    } break;
+    }
+}
+
+// ------------------------------------------------------------ embedding
+
+// The token's row of the table decoded to f32 (EmbedKernel.embedRow*):
+// the token comes from the device token history at the step position.
+extern "C" __global__ void __launch_bounds__(256) cj_embed(cj_embed_args a) {
+    const int token = a.tokens ? a.tokens[step_pos(a.state, a.token)] : a.token;
+    const uint8_t *row = a.table + (int64_t)token * a.row_bytes;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.hidden; e += (int64_t)gridDim.x * 256)
+        a.out[e] = decode_file(a.type, row, e);
+}
+
+// --------------------------------------------------------------- argmax
+
+// QuantKernel.argmaxRowKernel's contract: the smallest index of the largest
+// value; 1024 elements a workgroup, the last workgroup reduces the partials.
+extern "C" __global__ void __launch_bounds__(256) cj_argmax(cj_argmax_args a) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    __shared__ int ticket;
+    const int t = threadIdx.x;
+    const int64_t end0 = ((int64_t)blockIdx.x + 1) * 1024;
+    const int64_t end = end0 < a.n ? end0 : a.n;
+    float best = 0.0f; int besti = -1;
+    for (int64_t i = (int64_t)blockIdx.x * 1024 + t; i < end; i += 256) {
+        const float x = a.v[i];
+        if (besti < 0 || x > best) { best = x; besti = (int)i; }
+    }
+    bv[t] = best; bi[t] = besti;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s) {
+            float ov = bv[t + s]; int oi = bi[t + s]; float mv = bv[t]; int mi = bi[t];
+            if (mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)))) { bv[t] = ov; bi[t] = oi; }
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        a.pv[blockIdx.x] = bv[0];
+        a.pi[blockIdx.x] = bi[0];
+        __threadfence();
+        ticket = atomicAdd(a.counter, 1);
+    }
+    __syncthreads();
+    if (ticket != (int)gridDim.x - 1) return;
+    __threadfence();
+    float gb = 0.0f; int gi = -1;
+    for (int g = t; g < (int)gridDim.x; g += 256) {
+        const float x = a.pv[g]; const int xi = a.pi[g];
+        if (xi >= 0 && (gi < 0 || x > gb || (x == gb && xi < gi))) { gb = x; gi = xi; }
+    }
+    bv[t] = gb; bi[t] = gi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s) {
+            float ov = bv[t + s]; int oi = bi[t + s]; float mv = bv[t]; int mi = bi[t];
+            if (mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)))) { bv[t] = ov; bi[t] = oi; }
+        }
+        __syncthreads();
+    }
+    if (t == 0) { a.counter[0] = 0; a.tok[a.row] = bi[0]; }
+}
+
+// ------------------------------------------------------------------ misc
+
+// Word fill with zero: the graph-safe clear (no memset node in a graph).
+typedef struct { uint32_t *p; int64_t words; } cj_zero_args;
+extern "C" __global__ void __launch_bounds__(256) cj_zero(cj_zero_args a) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.words; i += (int64_t)gridDim.x * 256) a.p[i] = 0u;
+}
+
+// MoeFfn.routeFromLogits per row: softmax over the experts, top-k by
+// probability with strict > (ties keep the lower index), then the optional
+// renormalisation by the sum clamped at 2^-14. One workgroup per row.
+extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
+    __shared__ float pr[256];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float *lg = a.logits + (int64_t)row * a.n_experts;
+    if (t == 0) {
+        float mx = lg[0];
+        for (int e = 1; e < a.n_experts; e++) if (lg[e] > mx) mx = lg[e];
+        float sum = 0.0f;
+        for (int e = 0; e < a.n_experts; e++) { const float p = expf(lg[e] - mx); pr[e] = p; sum = __fadd_rn(sum, p); }
+        for (int e = 0; e < a.n_experts; e++) pr[e] = __fdiv_rn(pr[e], sum);
+        float w[16];
+        int s[16];
+        for (int k = 0; k < a.n_used; k++) {
+            int best = -1; float bp = 0.0f;
+            for (int e = 0; e < a.n_experts; e++)
+                if (pr[e] >= 0.0f && (best < 0 || pr[e] > bp)) { best = e; bp = pr[e]; }
+            if (best < 0) best = 0;   // non-finite logits; the host checks the weights
+            s[k] = best; w[k] = bp; pr[best] = -1.0f;
+        }
+        if (a.norm_topk) {
+            float ws = 0.0f;
+            for (int k = 0; k < a.n_used; k++) ws = __fadd_rn(ws, w[k]);
+            if (ws < 0.00006103515625f) ws = 0.00006103515625f;
+            for (int k = 0; k < a.n_used; k++) w[k] = __fdiv_rn(w[k], ws);
+        }
+        for (int k = 0; k < a.n_used; k++) { a.sel[row * a.n_used + k] = s[k]; a.w[row * a.n_used + k] = w[k]; }
+    }
+}
+
+// MoE combine (MoeFfn.forwardRow, model/MoeFfn.cajeta:1849-1913): the
+// selected experts' rows weighted and summed in k order, then onto hs.
+extern "C" __global__ void __launch_bounds__(256) cj_moe_combine(cj_combine_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.n) return;
+    float acc = 0.0f;
+    for (int k = 0; k < a.n_used; k++) acc = __fadd_rn(acc, __fmul_rn(a.w[k], a.y[k * a.n + i]));
+    a.hs[i] = __fadd_rn(a.hs[i], acc);
+}

@@ -1,0 +1,696 @@
+// engine.cpp — the decode engine behind the LlmEngine surface: a GGUF model
+// loaded into prepared, fused device weights, paged fp16 K/V, and the whole
+// per-token decode step (embedding → layers → norm → head → argmax) captured
+// once per sequence slot into a hipGraph and replayed per token. Position and
+// token history live on the device, so step N+1 is enqueued without waiting
+// for step N (the reference's queueStep/awaitStep pipelining,
+// model/CausalLM.cajeta:1208-1256, taken to its end: the host reads tokens
+// only to check stops).
+//
+// Per dense layer the step is five launches:
+//   1. q|k|v GEMV, RMSNorm + pack in the prologue, RoPE + fp16 K/V append
+//      in the epilogue (residentLayer steps 1-3, CausalLM.cajeta:3636-3694)
+//   2. split-K flash decode, the last split merging (steps 4-5)
+//   3. o GEMV, pack prologue, residual-accumulate epilogue (step 6)
+//   4. gate|up GEMV, RMSNorm + pack prologue, SiLU·up + pack epilogue (7-9)
+//   5. down GEMV, residual-accumulate epilogue (step 10)
+// MoE layers (gpt-oss shape) replace 4-5 with router GEMV, top-k, indirected
+// expert gate|up, indirected expert down and the weighted combine.
+#include "gguf.h"
+#include "rt.h"
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <algorithm>
+#include <deque>
+#include <memory>
+#include <set>
+#include <vector>
+
+namespace cj {
+
+namespace {
+
+struct DevW {            // a prepared device weight
+    void *p = nullptr;
+    int type = 0;
+    int64_t rows = 0, cols = 0, row_bytes = 0;
+};
+
+struct Layer {
+    DevW qkv, o, gu, down;           // dense
+    DevW router, gu_exps, down_exps; // MoE
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    int window = 0;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+struct Seq {
+    int32_t *tokens = nullptr;   // device token history (inputs)
+    int32_t *preds = nullptr;    // device argmax per position
+    cj_step_state *state = nullptr;
+    int pg_base = 0;
+    hipGraphExec_t graph = nullptr;
+    int pos = 0;                 // host mirror
+    int fixed_until = 0;
+};
+
+struct Request {
+    int id = 0;
+    std::vector<int32_t> prompt, out;
+    int max_new = 0;
+    bool done = false;
+    int reason = 0;
+};
+
+}  // namespace
+
+struct Engine {
+    Gguf file;
+    int n_layers = 0, hidden = 0, n_heads = 0, n_kv = 0, head_dim = 0, ffn = 0, vocab = 0, ctx = 0, max_seqs = 1;
+    int n_experts = 0, n_used = 0, expert_ffn = 0, norm_topk = 1;
+    float eps = 1e-5f, theta = 10000.0f, scale = 1.0f;
+    int wtype = 0, head_type = 0, embd_type = 0;
+    int64_t embd_row_bytes = 0;
+    void *embd = nullptr;
+    float *out_norm = nullptr;
+    DevW head;
+    std::vector<Layer> layers;
+    int pages_per_seq = 0, splits = 1;
+    int32_t *pgtab = nullptr;
+    float *rope = nullptr;
+    // scratch
+    float *hs = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *part = nullptr;
+    uint8_t *act_pack = nullptr;
+    int32_t *glu_counters = nullptr, *argmax_counter = nullptr, *attn_counters = nullptr;
+    float *part_v = nullptr;
+    int32_t *part_i = nullptr;
+    float *moe_logits = nullptr, *moe_w = nullptr, *moe_y = nullptr;
+    int32_t *moe_sel = nullptr;
+    std::vector<Seq> seqs;
+    std::set<int> eog;
+    std::deque<int> queue;
+    std::vector<Request> reqs;
+    float last_step_us = 0.0f;
+    std::vector<void *> owned;
+
+    void *alloc(size_t n) {
+        void *p = dev_alloc(n);
+        if (p) owned.push_back(p);
+        return p;
+    }
+    ~Engine() {
+        for (auto &s : seqs)
+            if (s.graph) (void)hipGraphExecDestroy(s.graph);
+        (void)hipStreamSynchronize(stream());
+        for (void *p : owned) dev_free(p);
+    }
+    int load(const std::string &path, int ctx_, int max_seqs_);
+    int upload_weight(const std::string &name, DevW &w, int expect_rows, int64_t expect_cols);
+    int fuse_rows(const std::vector<std::string> &names, DevW &w, bool interleave, int64_t rows_each, int64_t experts);
+    int capture(int s);
+    int enqueue_step(int s);
+    int prefill(int s, const int32_t *toks, int n);
+    int decode(int s, int steps, int32_t *out);
+    int reset(int s);
+    int run_request(Request &r, int max_steps);
+};
+
+namespace {
+
+std::string lname(int l, const char *t) { return "blk." + std::to_string(l) + "." + t; }
+
+}  // namespace
+
+int Engine::upload_weight(const std::string &name, DevW &w, int expect_rows, int64_t expect_cols) {
+    const GgufTensor *t = file.tensor(name);
+    if (!t) return fail(CJ_ERR_IO, "model: tensor %s is missing", name.c_str());
+    if (t->cols() != expect_cols || (expect_rows > 0 && t->rows() != expect_rows))
+        return fail(CJ_ERR_IO, "model: tensor %s is %lldx%lld, expected %lldx%lld", name.c_str(), (long long)t->rows(),
+                    (long long)t->cols(), (long long)expect_rows, (long long)expect_cols);
+    w.type = t->type; w.rows = t->rows(); w.cols = t->cols();
+    if (t->type == CJ_F32) {
+        w.row_bytes = w.cols * 4;
+        w.p = alloc((size_t)t->bytes);
+        if (!w.p) return fail(CJ_ERR_HIP, "model: out of device memory at %s", name.c_str());
+        CJ_HIP(hipMemcpy(w.p, t->data, (size_t)t->bytes, hipMemcpyHostToDevice));
+        return CJ_OK;
+    }
+    w.row_bytes = prepared_row_bytes(t->type, t->cols());
+    if (w.row_bytes <= 0 || !gemv_supported(t->type, t->cols()))
+        return fail(CJ_ERR_IO, "model: %s has type %d x %lld columns, not served", name.c_str(), t->type, (long long)t->cols());
+    w.p = alloc((size_t)(w.row_bytes * w.rows));
+    void *stage = dev_alloc((size_t)t->bytes);
+    if (!w.p || !stage) { dev_free(stage); return fail(CJ_ERR_HIP, "model: out of device memory at %s", name.c_str()); }
+    hipError_t e = hipMemcpy(stage, t->data, (size_t)t->bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { dev_free(stage); return fail(CJ_ERR_HIP, "upload %s: %s", name.c_str(), hipGetErrorString(e)); }
+    int rc = cj_prepare_weight((int64_t)(uintptr_t)w.p, (int64_t)(uintptr_t)stage, t->type, w.rows, w.cols);
+    (void)hipStreamSynchronize(stream());
+    dev_free(stage);
+    return rc;
+}
+
+// Concatenate (or row-interleave) prepared weights into one fused weight.
+// With `experts` > 0 each tensor is [experts][rows_each] and the fusion is
+// per expert.
+int Engine::fuse_rows(const std::vector<std::string> &names, DevW &w, bool interleave, int64_t rows_each, int64_t experts) {
+    std::vector<DevW> parts(names.size());
+    for (size_t i = 0; i < names.size(); i++) {
+        int rc = upload_weight(names[i], parts[i], -1, hidden);
+        if (rc) return rc;
+        if (i && (parts[i].type != parts[0].type))
+            return fail(CJ_ERR_IO, "model: %s and %s differ in type; the fused route needs one", names[0].c_str(), names[i].c_str());
+    }
+    const int64_t rb = parts[0].row_bytes;
+    int64_t total = 0;
+    for (auto &p : parts) total += p.rows;
+    w.type = parts[0].type; w.cols = parts[0].cols; w.row_bytes = rb; w.rows = total;
+    w.p = alloc((size_t)(total * rb));
+    if (!w.p) return fail(CJ_ERR_HIP, "model: out of device memory fusing %s", names[0].c_str());
+    const int64_t E = experts > 0 ? experts : 1;
+    if (!interleave) {
+        int64_t off = 0;
+        for (auto &p : parts) {
+            CJ_HIP(hipMemcpyAsync((char *)w.p + off * rb, p.p, (size_t)(p.rows * rb), hipMemcpyDeviceToDevice, stream()));
+            off += p.rows;
+        }
+    } else {
+        // row 2i = part0 row i, row 2i+1 = part1 row i (per expert)
+        const int64_t per = rows_each;
+        for (int64_t e = 0; e < E; e++)
+            for (size_t k = 0; k < parts.size(); k++) {
+                char *dst = (char *)w.p + (e * per * parts.size() + k) * rb;
+                const char *src = (const char *)parts[k].p + e * per * rb;
+                CJ_HIP(hipMemcpy2DAsync(dst, (size_t)(parts.size() * rb), src, (size_t)rb, (size_t)rb, (size_t)per,
+                                        hipMemcpyDeviceToDevice, stream()));
+            }
+    }
+    CJ_HIP(hipStreamSynchronize(stream()));
+    for (auto &p : parts) {
+        auto it = std::find(owned.begin(), owned.end(), p.p);
+        if (it != owned.end()) owned.erase(it);
+        dev_free(p.p);
+    }
+    return CJ_OK;
+}
+
+int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
+    std::string err;
+    if (!file.open(path, err)) return fail(CJ_ERR_IO, "model: %s", err.c_str());
+    const std::string arch = file.get_str("general.architecture", "");
+    if (arch != "llama") return fail(CJ_ERR_IO, "model: architecture '%s' is not served (llama)", arch.c_str());
+    const std::string kp = arch + ".";
+    hidden = (int)file.get_int(kp + "embedding_length", -1);
+    ffn = (int)file.get_int(kp + "feed_forward_length", -1);
+    n_layers = (int)file.get_int(kp + "block_count", -1);
+    n_heads = (int)file.get_int(kp + "attention.head_count", -1);
+    if (hidden <= 0 || ffn <= 0 || n_layers <= 0 || n_heads <= 0)
+        return fail(CJ_ERR_IO, "gguf config: missing a required %s* hyperparameter", kp.c_str());
+    n_kv = (int)file.get_int(kp + "attention.head_count_kv", n_heads);
+    head_dim = (int)file.get_int(kp + "attention.key_length", file.get_int(kp + "rope.dimension_count", hidden / n_heads));
+    eps = (float)file.get_float(kp + "attention.layer_norm_rms_epsilon", 1e-5);
+    theta = (float)file.get_float(kp + "rope.freq_base", 10000.0);
+    n_experts = (int)file.get_int(kp + "expert_count", 0);
+    n_used = (int)file.get_int(kp + "expert_used_count", 0);
+    expert_ffn = (int)file.get_int(kp + "expert_feed_forward_length", ffn);
+    norm_topk = (int)file.get_int(kp + "expert_weights_norm", 1);
+    const int swa = (int)file.get_int(kp + "attention.sliding_window", 0);
+    const GgufTensor *te = file.tensor("token_embd.weight");
+    if (!te) return fail(CJ_ERR_IO, "model: token_embd.weight is missing");
+    vocab = (int)file.get_int(kp + "vocab_size", te->rows());
+    if (file.has("tokenizer.ggml.eos_token_id")) eog.insert((int)file.get_int("tokenizer.ggml.eos_token_id", -1));
+    scale = 1.0f / sqrtf((float)head_dim);
+    ctx = ctx_ > 0 ? ctx_ : (int)file.get_int(kp + "context_length", 4096);
+    max_seqs = max_seqs_ > 0 ? max_seqs_ : 1;
+    if (head_dim != 64 && head_dim != 128) return fail(CJ_ERR_IO, "model: head_dim %d is not served (64, 128)", head_dim);
+    const int grp = n_heads / n_kv;
+    if (n_heads % n_kv || (grp != 1 && grp != 2 && grp != 4 && grp != 8))
+        return fail(CJ_ERR_IO, "model: GQA %d/%d is not served", n_heads, n_kv);
+
+    // embedding: GGUF layout, decoded per row on device
+    embd_type = te->type;
+    embd_row_bytes = ggml_row_bytes(te->type, te->cols());
+    if (embd_row_bytes <= 0 || te->cols() != hidden || te->rows() != vocab)
+        return fail(CJ_ERR_IO, "model: token_embd.weight shape/type not served");
+    embd = alloc((size_t)te->bytes);
+    if (!embd) return fail(CJ_ERR_HIP, "model: out of device memory (embedding)");
+    CJ_HIP(hipMemcpy(embd, te->data, (size_t)te->bytes, hipMemcpyHostToDevice));
+
+    auto upload_f32 = [&](const std::string &name, int64_t n, float **dst) -> int {
+        const GgufTensor *t = file.tensor(name);
+        if (!t || t->type != CJ_F32 || t->cols() * t->rows() != n) return fail(CJ_ERR_IO, "model: %s missing or not f32[%lld]", name.c_str(), (long long)n);
+        *dst = (float *)alloc((size_t)n * 4);
+        if (!*dst) return fail(CJ_ERR_HIP, "model: out of device memory at %s", name.c_str());
+        CJ_HIP(hipMemcpy(*dst, t->data, (size_t)n * 4, hipMemcpyHostToDevice));
+        return CJ_OK;
+    };
+
+    layers.resize(n_layers);
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim;
+    pages_per_seq = (ctx + 63) / 64;
+    const int64_t plane = (int64_t)pages_per_seq * max_seqs * n_kv * 64 * head_dim * 2;
+    int rc;
+    for (int l = 0; l < n_layers; l++) {
+        Layer &L = layers[l];
+        if ((rc = upload_f32(lname(l, "attn_norm.weight"), hidden, &L.attn_norm))) return rc;
+        if ((rc = upload_f32(lname(l, "ffn_norm.weight"), hidden, &L.ffn_norm))) return rc;
+        if ((rc = fuse_rows({lname(l, "attn_q.weight"), lname(l, "attn_k.weight"), lname(l, "attn_v.weight")}, L.qkv, false, 0, 0))) return rc;
+        if (L.qkv.rows != qd + 2 * kvd) return fail(CJ_ERR_IO, "model: layer %d q|k|v rows %lld", l, (long long)L.qkv.rows);
+        if ((rc = upload_weight(lname(l, "attn_output.weight"), L.o, hidden, qd))) return rc;
+        if (n_experts > 0) {
+            if ((rc = upload_weight(lname(l, "ffn_gate_inp.weight"), L.router, n_experts, hidden))) return rc;
+            if ((rc = fuse_rows({lname(l, "ffn_gate_exps.weight"), lname(l, "ffn_up_exps.weight")}, L.gu_exps, true, expert_ffn, n_experts))) return rc;
+            if ((rc = upload_weight(lname(l, "ffn_down_exps.weight"), L.down_exps, (int)((int64_t)n_experts * hidden), expert_ffn))) return rc;
+            if (L.down_exps.type != CJ_MXFP4 && L.down_exps.type != CJ_Q4_0 && L.down_exps.type != CJ_Q8_0)
+                return fail(CJ_ERR_IO, "model: expert type %d not served", L.down_exps.type);
+        } else {
+            if ((rc = fuse_rows({lname(l, "ffn_gate.weight"), lname(l, "ffn_up.weight")}, L.gu, true, ffn, 0))) return rc;
+            if ((rc = upload_weight(lname(l, "ffn_down.weight"), L.down, hidden, ffn))) return rc;
+        }
+        L.window = (swa > 0 && (l % 2) == 0) ? swa : 0;
+        L.kc = (uint16_t *)alloc((size_t)plane);
+        L.vc = (uint16_t *)alloc((size_t)plane);
+        if (!L.kc || !L.vc) return fail(CJ_ERR_HIP, "model: out of device memory for the K/V planes");
+    }
+    if ((rc = upload_f32("output_norm.weight", hidden, &out_norm))) return rc;
+    const std::string head_name = file.tensor("output.weight") ? "output.weight" : "token_embd.weight";
+    if ((rc = upload_weight(head_name, head, vocab, hidden))) return rc;
+    wtype = layers[0].qkv.type;
+    head_type = head.type;
+    if (is_f32_act(wtype)) return fail(CJ_ERR_IO, "model: attention weights of type %d are not served", wtype);
+
+    // K/V page table: sequence s owns pages [s·pages_per_seq, (s+1)·pages_per_seq)
+    std::vector<int32_t> tab((size_t)pages_per_seq * max_seqs);
+    for (size_t i = 0; i < tab.size(); i++) tab[i] = (int32_t)i;
+    pgtab = (int32_t *)alloc(tab.size() * 4);
+    rope = (float *)alloc((size_t)ctx * head_dim * 4);
+    if (!pgtab || !rope) return fail(CJ_ERR_HIP, "model: out of device memory");
+    CJ_HIP(hipMemcpy(pgtab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+    if ((rc = cj_rope_table((int64_t)(uintptr_t)rope, head_dim, theta, ctx))) return rc;
+
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    splits = std::max(1, std::min(64, (cus + n_kv - 1) / n_kv));
+    const int64_t fmax = std::max<int64_t>(ffn, (int64_t)expert_ffn * std::max(1, n_used));
+    const int64_t fpad = (std::max<int64_t>(ffn, expert_ffn) + 255) / 256 * 256;
+    hs = (float *)alloc((size_t)hidden * 4);
+    q = (float *)alloc((size_t)qd * 4);
+    attn = (float *)alloc((size_t)qd * 4);
+    act = (float *)alloc((size_t)fmax * 4 + 1024);
+    act_pack = (uint8_t *)alloc((size_t)fpad / 256 * 320);
+    logits = (float *)alloc((size_t)vocab * 4);
+    part = (float *)alloc((size_t)n_heads * splits * (head_dim + 2) * 4);
+    glu_counters = (int32_t *)alloc((size_t)fpad / 256 * 4 + 64);
+    argmax_counter = (int32_t *)alloc(64);
+    attn_counters = (int32_t *)alloc((size_t)n_kv * 4 + 64);
+    const int64_t max_wg = (vocab + 3) / 4 + 64;
+    part_v = (float *)alloc((size_t)max_wg * 4);
+    part_i = (int32_t *)alloc((size_t)max_wg * 4);
+    moe_logits = (float *)alloc((size_t)std::max(1, n_experts) * 4 + 64);
+    moe_w = (float *)alloc(64 * 4);
+    moe_sel = (int32_t *)alloc(64 * 4);
+    moe_y = (float *)alloc((size_t)hidden * std::max(1, n_used) * 4);
+    if (!hs || !q || !attn || !act || !act_pack || !logits || !part || !glu_counters || !argmax_counter ||
+        !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y)
+        return fail(CJ_ERR_HIP, "model: out of device memory (scratch)");
+    CJ_HIP(hipMemset(glu_counters, 0, (size_t)fpad / 256 * 4 + 64));
+    CJ_HIP(hipMemset(argmax_counter, 0, 64));
+    CJ_HIP(hipMemset(attn_counters, 0, (size_t)n_kv * 4 + 64));
+
+    seqs.resize(max_seqs);
+    for (int s = 0; s < max_seqs; s++) {
+        Seq &S = seqs[s];
+        S.tokens = (int32_t *)alloc((size_t)(ctx + 2) * 4);
+        S.preds = (int32_t *)alloc((size_t)(ctx + 2) * 4);
+        S.state = (cj_step_state *)alloc(sizeof(cj_step_state));
+        if (!S.tokens || !S.preds || !S.state) return fail(CJ_ERR_HIP, "model: out of device memory (sequence slots)");
+        S.pg_base = s * pages_per_seq;
+        CJ_HIP(hipMemset(S.tokens, 0, (size_t)(ctx + 2) * 4));
+        CJ_HIP(hipMemset(S.preds, 0, (size_t)(ctx + 2) * 4));
+        CJ_HIP(hipMemset(S.state, 0, sizeof(cj_step_state)));
+    }
+    CJ_HIP(hipDeviceSynchronize());
+    return CJ_OK;
+}
+
+// One decode step of sequence s on the stream (captured once into a graph).
+int Engine::enqueue_step(int s) {
+    Seq &S = seqs[s];
+    int rc;
+    {
+        cj_embed_args a{};
+        a.out = hs; a.table = (const uint8_t *)embd; a.tokens = S.tokens; a.state = S.state;
+        a.type = embd_type; a.hidden = hidden; a.row_bytes = embd_row_bytes;
+        if ((rc = launch("cj_embed", (uint32_t)((hidden + 255) / 256), 256, 0, a))) return rc;
+    }
+    const int grp = n_heads / n_kv;
+    const bool per32 = wtype == CJ_Q8_0;
+    char attn_kernel[64];
+    snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_decode_h%d_g%d", head_dim, grp);
+    for (int l = 0; l < n_layers; l++) {
+        Layer &L = layers[l];
+        {   // 1. q|k|v with norm+pack prologue, RoPE + K/V append epilogue
+            cj_gemv_args a{};
+            a.w = (const uint8_t *)L.qkv.p; a.x = hs; a.nw = L.attn_norm; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
+            a.pgtab = pgtab; a.rope_cs = rope; a.state = S.state; a.rows = L.qkv.rows; a.cols = hidden;
+            a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_QKV_ROPE;
+            a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
+            a.batch = 1;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+        }
+        {   // 2. attention
+            cj_attn_args a{};
+            a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
+            a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.splits = splits;
+            a.pg_base = S.pg_base; a.window = L.window; a.scale = scale;
+            if ((rc = launch(attn_kernel, (uint32_t)(n_kv * splits), 256, 0, a))) return rc;
+        }
+        {   // 3. o projection, residual into hs
+            cj_gemv_args a{};
+            a.w = (const uint8_t *)L.o.p; a.x = attn; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
+            a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
+            a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+        }
+        if (n_experts == 0) {
+            {   // 4. gate|up with norm+pack prologue, SiLU·up + pack epilogue
+                cj_gemv_args a{};
+                a.w = (const uint8_t *)L.gu.p; a.x = hs; a.nw = L.ffn_norm; a.act = act; a.act_pack = act_pack;
+                a.counters = glu_counters; a.rows = L.gu.rows; a.cols = hidden; a.row_bytes = L.gu.row_bytes;
+                a.type = L.gu.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
+                a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
+                a.batch = 1;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 4)))) return rc;
+            }
+            {   // 5. down, residual into hs
+                cj_gemv_args a{};
+                a.w = (const uint8_t *)L.down.p; a.xp = act_pack; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
+                a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_ACCUM;
+                a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+            }
+        } else {
+            {   // router logits from the normed hidden (f32 weights)
+                cj_gemv_args a{};
+                a.w = (const uint8_t *)L.router.p; a.x = hs; a.nw = L.ffn_norm; a.y = moe_logits; a.rows = n_experts;
+                a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_NORM_F32;
+                a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
+                if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 2)))) return rc;
+            }
+            {
+                cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1};
+                if ((rc = launch("cj_moe_route", 1, 64, 0, a))) return rc;
+            }
+            {   // the selected experts' gate|up, SiLU·up into act[k]
+                cj_gemv_args a{};
+                a.w = (const uint8_t *)L.gu_exps.p; a.x = hs; a.nw = L.ffn_norm; a.act = act; a.rows = 2 * (int64_t)expert_ffn;
+                a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
+                a.pro = is_f32_act(a.type) ? CJ_PRO_NORM_F32 : CJ_PRO_NORM_PACK; a.epi = CJ_EPI_GLU; a.eps = eps;
+                a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
+                a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
+                a.y_stride = expert_ffn;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+            }
+            {   // the selected experts' down into moe_y[k]
+                cj_gemv_args a{};
+                a.w = (const uint8_t *)L.down_exps.p; a.x = act; a.y = moe_y; a.rows = hidden; a.cols = expert_ffn;
+                a.row_bytes = L.down_exps.row_bytes; a.type = L.down_exps.type;
+                a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
+                a.batch = 1; a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes;
+                a.x_stride = expert_ffn; a.y_stride = hidden;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+            }
+            {   // hs += Σ_k w_k · y_k in k order
+                cj_combine_args a{hs, moe_y, moe_w, hidden, n_used};
+                if ((rc = launch("cj_moe_combine", (uint32_t)((hidden + 255) / 256), 256, 0, a))) return rc;
+            }
+        }
+    }
+    {   // final norm + head + greedy argmax; advances the step
+        cj_gemv_args a{};
+        a.w = (const uint8_t *)head.p; a.x = hs; a.nw = out_norm; a.y = logits; a.counters = argmax_counter;
+        a.part_v = part_v; a.part_i = part_i; a.tokens = S.tokens; a.preds = S.preds; a.state = S.state;
+        a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
+        a.pro = is_f32_act(head.type) ? CJ_PRO_NORM_F32 : CJ_PRO_NORM_PACK; a.epi = CJ_EPI_ARGMAX;
+        a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 2);
+        if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
+        if ((rc = run_gemv(a, p))) return rc;
+    }
+    return CJ_OK;
+}
+
+int Engine::capture(int s) {
+    Seq &S = seqs[s];
+    if (S.graph) return CJ_OK;
+    CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(s);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(stream(), &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return fail(CJ_ERR_HIP, "capture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&S.graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { S.graph = nullptr; return fail(CJ_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e)); }
+    return CJ_OK;
+}
+
+int Engine::reset(int s) {
+    if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+    Seq &S = seqs[s];
+    cj_step_state st{};
+    CJ_HIP(hipMemcpyAsync(S.state, &st, sizeof st, hipMemcpyHostToDevice, stream()));
+    CJ_HIP(hipStreamSynchronize(stream()));
+    S.pos = 0;
+    S.fixed_until = 0;
+    return CJ_OK;
+}
+
+int Engine::prefill(int s, const int32_t *toks, int n) {
+    if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+    Seq &S = seqs[s];
+    if (n <= 0) return fail(CJ_ERR_ARG, "prefill of %d tokens", n);
+    if (S.pos + n > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + n, ctx);
+    for (int i = 0; i < n; i++)
+        if (toks[i] < 0 || toks[i] >= vocab) return fail(CJ_ERR_ARG, "token %d outside the vocabulary", toks[i]);
+    int rc;
+    if ((rc = capture(s))) return rc;
+    CJ_HIP(hipMemcpyAsync(S.tokens + S.pos, toks, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
+    cj_step_state st{};
+    st.pos = S.pos;
+    st.fixed_until = S.pos + n;
+    CJ_HIP(hipMemcpyAsync(S.state, &st, sizeof st, hipMemcpyHostToDevice, stream()));
+    for (int i = 0; i < n; i++) CJ_HIP(hipGraphLaunch(S.graph, stream()));
+    CJ_HIP(hipStreamSynchronize(stream()));
+    S.pos += n;
+    S.fixed_until = S.pos;
+    return CJ_OK;
+}
+
+int Engine::decode(int s, int steps, int32_t *out) {
+    if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+    Seq &S = seqs[s];
+    if (S.pos == 0) return fail(CJ_ERR_STATE, "decode before prefill");
+    if (steps <= 0) return CJ_OK;
+    if (S.pos + steps > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + steps, ctx);
+    int rc;
+    if ((rc = capture(s))) return rc;
+    hipEvent_t e0, e1;
+    CJ_HIP(hipEventCreate(&e0));
+    CJ_HIP(hipEventCreate(&e1));
+    CJ_HIP(hipEventRecord(e0, stream()));
+    for (int i = 0; i < steps; i++) CJ_HIP(hipGraphLaunch(S.graph, stream()));
+    CJ_HIP(hipEventRecord(e1, stream()));
+    CJ_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    CJ_HIP(hipEventElapsedTime(&ms, e0, e1));
+    last_step_us = ms * 1000.0f / (float)steps;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (out) CJ_HIP(hipMemcpy(out, S.tokens + S.pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost));
+    S.pos += steps;
+    return CJ_OK;
+}
+
+// One request to completion on slot 0: the prompt teacher-forced, then
+// greedy steps in groups, stopping at an end-of-generation id or max_new
+// (Scheduler.stepPipelined, sched/Scheduler.cajeta:640-676).
+int Engine::run_request(Request &r, int max_steps) {
+    int rc;
+    if ((rc = reset(0))) return rc;
+    if ((rc = prefill(0, r.prompt.data(), (int)r.prompt.size()))) return rc;
+    Seq &S = seqs[0];
+    int32_t first = 0;
+    CJ_HIP(hipMemcpy(&first, S.tokens + S.pos, 4, hipMemcpyDeviceToHost));
+    r.out.push_back(first);
+    if (eog.count(first)) { r.done = true; r.reason = 1; return CJ_OK; }
+    int budget = max_steps > 0 ? max_steps : (1 << 30);
+    while ((int)r.out.size() < r.max_new && budget > 0) {
+        int want = std::min(8, std::min(r.max_new - (int)r.out.size(), budget));
+        if (S.pos + want > ctx) { r.done = true; r.reason = 0; return CJ_OK; }
+        std::vector<int32_t> got((size_t)want);
+        if ((rc = decode(0, want, got.data()))) return rc;
+        budget -= want;
+        for (int32_t t : got) {
+            r.out.push_back(t);
+            if (eog.count(t)) { r.done = true; r.reason = 1; return CJ_OK; }
+        }
+    }
+    if ((int)r.out.size() >= r.max_new) { r.done = true; r.reason = 0; }
+    return CJ_OK;
+}
+
+}  // namespace cj
+
+using cj::Engine;
+
+namespace {
+Engine *eng_of(int64_t h) { return (Engine *)(uintptr_t)h; }
+}
+
+extern "C" {
+
+int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs) {
+    if (!cj::ready()) return cj::fail(CJ_ERR_STATE, "cj_init has not run"), 0;
+    if (!path) return cj::fail(CJ_ERR_ARG, "cj_engine_load: null path"), 0;
+    auto *e = new Engine();
+    int rc = e->load((const char *)path, ctx, max_seqs);
+    if (rc) { std::string m = cj::last_error(); delete e; cj::fail(rc, "%s", m.c_str()); return 0; }
+    return (int64_t)(uintptr_t)e;
+}
+
+int32_t cj_engine_close(int64_t h) {
+    delete eng_of(h);
+    return CJ_OK;
+}
+
+int32_t cj_engine_config(int64_t h, int64_t *out, int32_t n) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    int64_t v[] = {e->n_layers, e->hidden, e->n_heads, e->n_kv, e->head_dim, e->ffn, e->vocab, e->ctx,
+                   e->n_experts, e->n_used, e->wtype, e->head_type, e->expert_ffn, e->splits};
+    for (int i = 0; i < n && i < (int)(sizeof v / sizeof v[0]); i++) out[i] = v[i];
+    return CJ_OK;
+}
+
+int32_t cj_engine_submit(int64_t h, const int32_t *prompt, int32_t n, int32_t max_new) {
+    Engine *e = eng_of(h);
+    if (!e || !prompt || n <= 0 || max_new <= 0) return cj::fail(CJ_ERR_ARG, "cj_engine_submit: bad arguments");
+    cj::Request r;
+    r.id = (int)e->reqs.size() + 1;
+    r.prompt.assign(prompt, prompt + n);
+    r.max_new = max_new;
+    e->reqs.push_back(r);
+    e->queue.push_back(r.id);
+    return r.id;
+}
+
+int32_t cj_engine_step_once(int64_t h) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    while (!e->queue.empty()) {
+        cj::Request &r = e->reqs[(size_t)e->queue.front() - 1];
+        e->queue.pop_front();
+        if (r.done) continue;
+        int rc = e->run_request(r, 0);
+        if (rc) return rc;
+        return 1;
+    }
+    return 0;
+}
+
+int32_t cj_engine_run_all(int64_t h, int32_t max_steps) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    while (!e->queue.empty()) {
+        cj::Request &r = e->reqs[(size_t)e->queue.front() - 1];
+        e->queue.pop_front();
+        if (r.done) continue;
+        int rc = e->run_request(r, max_steps);
+        if (rc) return rc;
+    }
+    return CJ_OK;
+}
+
+int32_t cj_engine_request(int64_t h, int32_t id, int32_t *tokens, int32_t cap, int32_t *done, int32_t *reason) {
+    Engine *e = eng_of(h);
+    if (!e || id <= 0 || id > (int)e->reqs.size()) return cj::fail(CJ_ERR_ARG, "cj_engine_request: unknown id %d", id);
+    cj::Request &r = e->reqs[(size_t)id - 1];
+    for (int i = 0; i < cap && i < (int)r.out.size(); i++) tokens[i] = r.out[(size_t)i];
+    if (done) *done = r.done ? 1 : 0;
+    if (reason) *reason = r.reason;
+    return (int32_t)r.out.size();
+}
+
+int32_t cj_engine_cancel(int64_t h, int32_t id) {
+    Engine *e = eng_of(h);
+    if (!e || id <= 0 || id > (int)e->reqs.size()) return cj::fail(CJ_ERR_ARG, "cj_engine_cancel: unknown id %d", id);
+    cj::Request &r = e->reqs[(size_t)id - 1];
+    if (r.done) return 0;
+    r.done = true;
+    r.reason = 2;
+    return 1;
+}
+
+int32_t cj_engine_set_eog(int64_t h, const int32_t *ids, int32_t n) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    e->eog.clear();
+    for (int i = 0; i < n; i++) e->eog.insert(ids[i]);
+    return CJ_OK;
+}
+
+int32_t cj_engine_reset(int64_t h, int32_t seq) {
+    Engine *e = eng_of(h);
+    return e ? e->reset(seq) : cj::fail(CJ_ERR_STATE, "null engine");
+}
+int32_t cj_engine_prefill(int64_t h, int32_t seq, const int32_t *tokens, int32_t n) {
+    Engine *e = eng_of(h);
+    return e ? e->prefill(seq, tokens, n) : cj::fail(CJ_ERR_STATE, "null engine");
+}
+int32_t cj_engine_decode(int64_t h, int32_t seq, int32_t steps, int32_t *out) {
+    Engine *e = eng_of(h);
+    return e ? e->decode(seq, steps, out) : cj::fail(CJ_ERR_STATE, "null engine");
+}
+int32_t cj_engine_logits(int64_t h, int32_t seq, float *out, int64_t n) {
+    Engine *e = eng_of(h);
+    if (!e || n > e->vocab) return cj::fail(CJ_ERR_ARG, "cj_engine_logits: n %lld", (long long)n);
+    (void)seq;
+    CJ_HIP(hipStreamSynchronize(cj::stream()));
+    CJ_HIP(hipMemcpy(out, e->logits, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return CJ_OK;
+}
+int32_t cj_engine_preds(int64_t h, int32_t seq, int32_t *out, int32_t n) {
+    Engine *e = eng_of(h);
+    if (!e || seq < 0 || seq >= (int)e->seqs.size() || n > e->ctx) return cj::fail(CJ_ERR_ARG, "cj_engine_preds");
+    CJ_HIP(hipStreamSynchronize(cj::stream()));
+    CJ_HIP(hipMemcpy(out, e->seqs[seq].preds + 1, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return CJ_OK;
+}
+int32_t cj_engine_trace(int64_t h, int32_t what, float *out, int64_t n) {
+    Engine *e = eng_of(h);
+    if (!e || !out) return cj::fail(CJ_ERR_ARG, "cj_engine_trace: bad arguments");
+    const int64_t qd = (int64_t)e->n_heads * e->head_dim;
+    const float *src = nullptr;
+    int64_t cap = 0;
+    switch (what) {
+    case 0: src = e->hs; cap = e->hidden; break;
+    case 1: src = e->q; cap = qd; break;
+    case 2: src = e->attn; cap = qd; break;
+    case 3: src = e->act; cap = e->ffn; break;
+    case 4: src = e->logits; cap = e->vocab; break;
+    case 5: src = (const float *)e->act_pack; cap = ((int64_t)e->ffn + 255) / 256 * 80; break;
+    default: return cj::fail(CJ_ERR_ARG, "cj_engine_trace: unknown tap %d", what);
+    }
+    if (n > cap) return cj::fail(CJ_ERR_ARG, "cj_engine_trace: %lld > %lld", (long long)n, (long long)cap);
+    CJ_HIP(hipStreamSynchronize(cj::stream()));
+    CJ_HIP(hipMemcpy(out, src, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return CJ_OK;
+}
+
+float cj_engine_last_step_us(int64_t h) {
+    Engine *e = eng_of(h);
+    return e ? e->last_step_us : -1.0f;
+}
+
+}  // extern "C"

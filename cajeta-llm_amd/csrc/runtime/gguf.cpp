@@ -1,0 +1,246 @@
+// gguf.cpp — GGUF reader/writer and the in-process image registry.
+#include "gguf.h"
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <cstring>
+#include <mutex>
+
+namespace cj {
+
+namespace {
+std::mutex g_img_mu;
+std::map<std::string, std::pair<std::unique_ptr<uint8_t[]>, size_t>> g_images;
+
+struct Rd {
+    const uint8_t *p;
+    size_t n, at = 0;
+    bool ok = true;
+    template <class T> T get() {
+        T v{};
+        if (at + sizeof(T) > n) { ok = false; return v; }
+        memcpy(&v, p + at, sizeof(T));
+        at += sizeof(T);
+        return v;
+    }
+    std::string str() {
+        uint64_t len = get<uint64_t>();
+        if (!ok || at + len > n) { ok = false; return {}; }
+        std::string s((const char *)p + at, (size_t)len);
+        at += (size_t)len;
+        return s;
+    }
+};
+
+bool read_value(Rd &r, int type, GgufValue &v) {
+    v.type = type;
+    switch (type) {
+    case 0: v.i = r.get<uint8_t>(); break;
+    case 1: v.i = r.get<int8_t>(); break;
+    case 2: v.i = r.get<uint16_t>(); break;
+    case 3: v.i = r.get<int16_t>(); break;
+    case 4: v.i = r.get<uint32_t>(); break;
+    case 5: v.i = r.get<int32_t>(); break;
+    case 6: v.f = r.get<float>(); v.i = (int64_t)v.f; break;
+    case 7: v.i = r.get<uint8_t>(); break;
+    case 8: v.s = r.str(); break;
+    case 10: v.i = (int64_t)r.get<uint64_t>(); break;
+    case 11: v.i = r.get<int64_t>(); break;
+    case 12: v.f = r.get<double>(); v.i = (int64_t)v.f; break;
+    case 9: {
+        int et = (int)r.get<uint32_t>();
+        uint64_t cnt = r.get<uint64_t>();
+        for (uint64_t k = 0; k < cnt && r.ok; k++) {
+            GgufValue e;
+            if (!read_value(r, et, e)) return false;
+            if (et == 6 || et == 12) v.af.push_back(e.f);
+            else if (et != 8) v.ai.push_back(e.i);
+        }
+    } break;
+    default: return false;
+    }
+    if (type == 6 || type == 12) {} else if (type != 8 && type != 9) v.f = (double)v.i;
+    return r.ok;
+}
+}  // namespace
+
+int ggml_block_elems(int t) {
+    switch (t) { case 0: case 1: return 1; case 2: case 8: case 39: return 32; case 12: case 14: return 256; default: return -1; }
+}
+int ggml_block_bytes(int t) {
+    switch (t) { case 0: return 4; case 1: return 2; case 2: return 18; case 8: return 34; case 12: return 144; case 14: return 210; case 39: return 17; default: return -1; }
+}
+int64_t ggml_row_bytes(int type, int64_t cols) {
+    int be = ggml_block_elems(type), bb = ggml_block_bytes(type);
+    if (be < 0 || cols % be) return -1;
+    return cols / be * bb;
+}
+
+Gguf::~Gguf() {
+    if (map_) munmap(map_, map_size_);
+}
+
+bool Gguf::open(const std::string &path, std::string &err) {
+    if (path.rfind("mem:", 0) == 0) {
+        const uint8_t *p; size_t n;
+        if (!image_get(path.substr(4), &p, &n)) { err = "no in-process image " + path; return false; }
+        return parse(p, n, err);
+    }
+    int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) { err = "cannot open " + path; return false; }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 24) { ::close(fd); err = "cannot stat " + path; return false; }
+    map_size_ = (size_t)st.st_size;
+    map_ = mmap(nullptr, map_size_, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (map_ == MAP_FAILED) { map_ = nullptr; err = "mmap failed for " + path; return false; }
+    return parse((const uint8_t *)map_, map_size_, err);
+}
+
+bool Gguf::parse(const uint8_t *p, size_t n, std::string &err) {
+    Rd r{p, n};
+    if (r.get<uint32_t>() != 0x46554747u) { err = "not a GGUF file (magic)"; return false; }
+    uint32_t ver = r.get<uint32_t>();
+    if (ver != 2 && ver != 3) { err = "GGUF version " + std::to_string(ver) + " is not 2 or 3"; return false; }
+    uint64_t nt = r.get<uint64_t>(), nkv = r.get<uint64_t>();
+    for (uint64_t i = 0; i < nkv && r.ok; i++) {
+        std::string k = r.str();
+        int ty = (int)r.get<uint32_t>();
+        GgufValue v;
+        if (!read_value(r, ty, v)) { err = "bad metadata value for " + k; return false; }
+        kv_[k] = std::move(v);
+    }
+    for (uint64_t i = 0; i < nt && r.ok; i++) {
+        GgufTensor t;
+        t.name = r.str();
+        uint32_t nd = r.get<uint32_t>();
+        if (nd > 4) { err = "tensor " + t.name + " has " + std::to_string(nd) + " dims"; return false; }
+        for (uint32_t d = 0; d < nd; d++) t.dims.push_back((int64_t)r.get<uint64_t>());
+        t.type = (int)r.get<uint32_t>();
+        t.offset = r.get<uint64_t>();
+        tensors_.push_back(std::move(t));
+    }
+    if (!r.ok) { err = "truncated GGUF header"; return false; }
+    // alignment: io/GgufFile.cajeta:773-777
+    uint64_t align = (uint64_t)get_int("general.alignment", 32);
+    if (align == 0) align = 32;
+    uint64_t data = (r.at + align - 1) / align * align;
+    for (size_t i = 0; i < tensors_.size(); i++) {
+        GgufTensor &t = tensors_[i];
+        int64_t rb = ggml_row_bytes(t.type, t.cols());
+        if (rb < 0) { err = "tensor " + t.name + ": type " + std::to_string(t.type) + " is not served"; return false; }
+        t.bytes = rb * t.rows();
+        if (data + t.offset + (uint64_t)t.bytes > n) { err = "tensor " + t.name + " runs past the end of the file"; return false; }
+        t.data = p + data + t.offset;
+        index_[t.name] = i;
+    }
+    return true;
+}
+
+const GgufTensor *Gguf::tensor(const std::string &name) const {
+    auto it = index_.find(name);
+    return it == index_.end() ? nullptr : &tensors_[it->second];
+}
+const GgufValue *Gguf::get(const std::string &key) const {
+    auto it = kv_.find(key);
+    return it == kv_.end() ? nullptr : &it->second;
+}
+int64_t Gguf::get_int(const std::string &key, int64_t dflt) const {
+    const GgufValue *v = get(key);
+    return v ? v->i : dflt;
+}
+double Gguf::get_float(const std::string &key, double dflt) const {
+    const GgufValue *v = get(key);
+    return v ? v->f : dflt;
+}
+std::string Gguf::get_str(const std::string &key, const std::string &dflt) const {
+    const GgufValue *v = get(key);
+    return v && v->type == 8 ? v->s : dflt;
+}
+
+// ---------------------------------------------------------------- writer
+
+namespace {
+void put_bytes(std::vector<uint8_t> &o, const void *p, size_t n) {
+    const uint8_t *b = (const uint8_t *)p;
+    o.insert(o.end(), b, b + n);
+}
+template <class T> void put(std::vector<uint8_t> &o, T v) { put_bytes(o, &v, sizeof v); }
+void put_str(std::vector<uint8_t> &o, const std::string &s) {
+    put<uint64_t>(o, s.size());
+    put_bytes(o, s.data(), s.size());
+}
+}  // namespace
+
+void GgufWriter::kv_u32(const std::string &k, uint32_t v) { put_str(meta_, k); put<uint32_t>(meta_, 4); put(meta_, v); n_kv_++; }
+void GgufWriter::kv_i32(const std::string &k, int32_t v) { put_str(meta_, k); put<uint32_t>(meta_, 5); put(meta_, v); n_kv_++; }
+void GgufWriter::kv_f32(const std::string &k, float v) { put_str(meta_, k); put<uint32_t>(meta_, 6); put(meta_, v); n_kv_++; }
+void GgufWriter::kv_bool(const std::string &k, bool v) { put_str(meta_, k); put<uint32_t>(meta_, 7); put<uint8_t>(meta_, v ? 1 : 0); n_kv_++; }
+void GgufWriter::kv_str(const std::string &k, const std::string &v) { put_str(meta_, k); put<uint32_t>(meta_, 8); put_str(meta_, v); n_kv_++; }
+
+void GgufWriter::tensor(const std::string &name, int type, std::vector<int64_t> dims) {
+    T t{name, type, std::move(dims), 0, 0};
+    int64_t rows = 1;
+    for (size_t i = 1; i < t.dims.size(); i++) rows *= t.dims[i];
+    t.bytes = ggml_row_bytes(type, t.dims[0]) * rows;
+    ts_.push_back(std::move(t));
+}
+
+size_t GgufWriter::layout(std::vector<size_t> &offsets) {
+    size_t hdr = 4 + 4 + 8 + 8 + meta_.size();
+    for (auto &t : ts_) hdr += 8 + t.name.size() + 4 + 8 * t.dims.size() + 4 + 8;
+    const size_t align = 32;
+    header_size_ = (hdr + align - 1) / align * align;
+    uint64_t off = 0;
+    offsets.clear();
+    for (auto &t : ts_) {
+        t.off = off;
+        offsets.push_back(header_size_ + off);
+        off += ((uint64_t)t.bytes + align - 1) / align * align;
+    }
+    return header_size_ + off;
+}
+
+void GgufWriter::write_header(uint8_t *out) const {
+    std::vector<uint8_t> h;
+    put<uint32_t>(h, 0x46554747u);
+    put<uint32_t>(h, 3);
+    put<uint64_t>(h, ts_.size());
+    put<uint64_t>(h, n_kv_);
+    put_bytes(h, meta_.data(), meta_.size());
+    for (auto &t : ts_) {
+        put_str(h, t.name);
+        put<uint32_t>(h, (uint32_t)t.dims.size());
+        for (int64_t d : t.dims) put<uint64_t>(h, (uint64_t)d);
+        put<uint32_t>(h, (uint32_t)t.type);
+        put<uint64_t>(h, t.off);
+    }
+    h.resize(header_size_, 0);
+    memcpy(out, h.data(), h.size());
+}
+
+// ---------------------------------------------------------------- images
+
+uint8_t *image_create(const std::string &name, size_t bytes) {
+    std::unique_ptr<uint8_t[]> p(new (std::nothrow) uint8_t[bytes]);
+    if (!p) return nullptr;
+    uint8_t *raw = p.get();
+    std::lock_guard<std::mutex> lk(g_img_mu);
+    g_images[name] = {std::move(p), bytes};
+    return raw;
+}
+bool image_get(const std::string &name, const uint8_t **p, size_t *n) {
+    std::lock_guard<std::mutex> lk(g_img_mu);
+    auto it = g_images.find(name);
+    if (it == g_images.end()) return false;
+    *p = it->second.first.get();
+    *n = it->second.second;
+    return true;
+}
+bool image_free(const std::string &name) {
+    std::lock_guard<std::mutex> lk(g_img_mu);
+    return g_images.erase(name) != 0;
+}
+
+}  // namespace cj

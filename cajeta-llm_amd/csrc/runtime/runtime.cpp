@@ -1,0 +1,587 @@
+// runtime.cpp — the C-ABI runtime: device + stream, the kernels.hsaco
+// module and its registry, the device-buffer table behind every extent
+// check, graphs and events, and the launch seam (one validated launch per
+// reference *LaunchNoSync wrapper).
+#include "rt.h"
+#include <dlfcn.h>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace cj {
+
+namespace {
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    std::map<uintptr_t, size_t> allocs;
+    std::mutex mu;
+    int cus = 0;
+    int64_t hbm = 0;
+    int64_t lds = 0;
+};
+Ctx g;
+thread_local std::string g_err;
+
+// The reference's kernel names (KernelCap.nameOf, model/KernelCap.cajeta:100-140
+// and the launch sites) answered by the kernels of this code object.
+const std::unordered_map<std::string, std::string> &name_map() {
+    static const std::unordered_map<std::string, std::string> m = {
+        {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_l64"},
+        {"q6kQ8WaveMatVecKernel", "cj_gemv_q6k_l64"},
+        {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
+        {"q40F32WaveMatVecKernel", "cj_gemv_q40_l64"},
+        {"mxfp4MatVecKernel", "cj_gemv_mxfp4_l64"},
+        {"q8kPackKernel", "cj_pack"},
+        {"q8kPack32Kernel", "cj_pack"},
+        {"rmsnormPackRowF32", "cj_pack"},
+        {"rmsnormRowF32", "cj_pack"},
+        {"gluPackF32", "cj_glu"},
+        {"gluF32", "cj_glu"},
+        {"addF32", "cj_add"},
+        {"qkPrepKernel", "cj_qkprep"},
+        {"attnFlashDecodeGqa1Kernel", "cj_attn_decode_h128_g1"},
+        {"attnFlashDecodeGqa4Kernel", "cj_attn_decode_h128_g4"},
+        {"attnFlashDecodeGqa8Kernel", "cj_attn_decode_h128_g8"},
+        {"attnScoreKernel", "cj_attn_decode_h64_g4"},
+        {"attnCombineKernel", "cj_attn_decode_h64_g4"},
+        {"attnReducePackQ8Kernel", "cj_attn_merge"},
+        {"argmaxRowKernel", "cj_argmax"},
+        {"embedRowQ4kKernel", "cj_embed"},
+        {"embedRowQ6kKernel", "cj_embed"},
+        {"embedRowQ80Kernel", "cj_embed"},
+        {"gatherRowsF32Kernel", "cj_embed"},
+        {"routerTopKKernel", "cj_moe_route"},
+        {"q4kQ8IdGateUpGluKernel", "cj_gemv_mxfp4_l64"},
+        {"q4kQ8IdDownCombineKernel", "cj_gemv_mxfp4_l64"},
+    };
+    return m;
+}
+
+std::string module_path() {
+    if (const char *e = getenv("CJ_KERNELS_HSACO")) return e;
+    Dl_info info;
+    if (dladdr((void *)&cj_init, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t s = p.rfind('/');
+        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) + "/kernels.hsaco";
+    }
+    return "kernels.hsaco";
+}
+}  // namespace
+
+int fail(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+const char *last_error() { return g_err.c_str(); }
+bool ready() { return g.module != nullptr; }
+hipStream_t stream() { return g.stream; }
+int device_cus() { return g.cus; }
+
+bool in_buffer(const void *p, int64_t bytes) {
+    if (bytes < 0) return false;
+    std::lock_guard<std::mutex> lk(g.mu);
+    uintptr_t a = (uintptr_t)p;
+    auto it = g.allocs.upper_bound(a);
+    if (it == g.allocs.begin()) return false;
+    --it;
+    return a >= it->first && a + (uintptr_t)bytes <= it->first + it->second;
+}
+void *dptr(int64_t h) { return (void *)(uintptr_t)h; }
+
+void *dev_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g.mu);
+    g.allocs[(uintptr_t)p] = bytes ? bytes : 16;
+    return p;
+}
+void dev_free(void *p) {
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lk(g.mu);
+        g.allocs.erase((uintptr_t)p);
+    }
+    (void)hipFree(p);
+}
+
+bool has_kernel(const char *name) { return g.fns.count(name) != 0; }
+
+int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
+    auto it = g.fns.find(name);
+    if (it == g.fns.end()) return fail(CJ_ERR_NOKERNEL, "kernel %s is not in kernels.hsaco", name);
+    if (grid == 0) return CJ_OK;
+    size_t sz = size;
+    void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void *>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                   HIP_LAUNCH_PARAM_END};
+    hipError_t e = hipModuleLaunchKernel(it->second, grid, 1, 1, block, 1, 1, lds, g.stream, nullptr, cfg);
+    if (e != hipSuccess) return fail(CJ_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e));
+    return CJ_OK;
+}
+
+// ------------------------------------------------------------------ GEMV
+
+bool is_f32_act(int type) { return type == CJ_Q4_0 || type == CJ_MXFP4 || type == CJ_F32; }
+
+int64_t prepared_row_bytes(int type, int64_t cols) {
+    auto pad16 = [](int64_t v) { return (v + 15) / 16 * 16; };
+    switch (type) {
+    case CJ_Q4_K: return cols % 256 ? -1 : cols / 256 * 144;
+    case CJ_Q6_K: return cols % 256 ? -1 : cols / 256 * 208 + pad16(cols / 256 * 2);
+    case CJ_Q8_0: return cols % 32 ? -1 : cols / 32 * 32 + pad16(cols / 32 * 2);
+    case CJ_Q4_0: return cols % 32 ? -1 : cols / 32 * 16 + pad16(cols / 32 * 2);
+    case CJ_MXFP4: return cols % 32 ? -1 : cols / 32 * 16 + pad16(cols / 32);
+    case CJ_F32: return cols % 4 ? -1 : cols * 4;
+    default: return -1;
+    }
+}
+
+bool gemv_supported(int type, int64_t cols) {
+    return prepared_row_bytes(type, cols) > 0 && cols <= 16384 * (is_f32_act(type) ? 1 : 4);
+}
+
+GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
+    GemvPlan p;
+    const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
+                      : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
+    const int64_t units = (type == CJ_Q4_K || type == CJ_Q6_K) ? cols / 256 * 4 : type == CJ_F32 ? cols / 4 : cols / 32;
+    const int lpr = units >= 64 ? 64 : units >= 32 ? 32 : units >= 16 ? 16 : 8;
+    const int groups = 64 / lpr;
+    int rpg = rows_per_group > 0 ? rows_per_group : 2;
+    if (rpg & 1) rpg++;
+    p.rows_per_wg = 4 * groups * rpg;
+    p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
+    p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
+    p.per_copy = p.grid;
+    const int64_t nblk = (cols + 255) / 256;
+    p.lds = 3072 + (uint32_t)(is_f32_act(type) ? nblk * 256 * 4 : nblk * 320);
+    return p;
+}
+
+int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
+    cj_gemv_args a = a0;
+    a.rows_per_wg = p.rows_per_wg;
+    const uint32_t grid = a.sel ? p.per_copy * (uint32_t)a.n_sel : p.grid;
+    return launch(p.kernel.c_str(), grid, 256, p.lds, a);
+}
+
+}  // namespace cj
+
+using namespace cj;
+
+// ======================================================================= C-ABI
+
+extern "C" {
+
+int32_t cj_init(int32_t device) {
+    if (ready()) return g.device == device ? CJ_OK : fail(CJ_ERR_STATE, "already initialised on device %d", g.device);
+    CJ_HIP(hipSetDevice(device));
+    hipDeviceProp_t pr;
+    CJ_HIP(hipGetDeviceProperties(&pr, device));
+    g.cus = pr.multiProcessorCount;
+    g.hbm = (int64_t)pr.totalGlobalMem;
+    g.lds = (int64_t)pr.maxSharedMemoryPerMultiProcessor;
+    std::string path = module_path();
+    hipError_t e = hipModuleLoad(&g.module, path.c_str());
+    if (e != hipSuccess) {
+        g.module = nullptr;
+        return fail(CJ_ERR_NOKERNEL, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    static const char *kernels[] = {
+        "cj_gemv_q4k_l64", "cj_gemv_q4k_l32", "cj_gemv_q4k_l16", "cj_gemv_q4k_l8",
+        "cj_gemv_q6k_l64", "cj_gemv_q6k_l32", "cj_gemv_q6k_l16", "cj_gemv_q6k_l8",
+        "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
+        "cj_gemv_q40_l64", "cj_gemv_q40_l32", "cj_gemv_q40_l16", "cj_gemv_q40_l8",
+        "cj_gemv_mxfp4_l64", "cj_gemv_mxfp4_l32", "cj_gemv_mxfp4_l16", "cj_gemv_mxfp4_l8",
+        "cj_gemv_f32_l64", "cj_gemv_f32_l32", "cj_gemv_f32_l16", "cj_gemv_f32_l8", "cj_moe_combine",
+        "cj_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
+        "cj_attn_decode_h128_g1", "cj_attn_decode_h128_g2", "cj_attn_decode_h128_g4", "cj_attn_decode_h128_g8",
+        "cj_attn_decode_h64_g1", "cj_attn_decode_h64_g2", "cj_attn_decode_h64_g4", "cj_attn_decode_h64_g8",
+        "cj_attn_merge", "cj_qkprep", "cj_zero", "cj_moe_route",
+    };
+    for (const char *k : kernels) {
+        hipFunction_t f;
+        if (hipModuleGetFunction(&f, g.module, k) == hipSuccess) g.fns[k] = f;
+    }
+    CJ_HIP(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+    g.device = device;
+    return CJ_OK;
+}
+
+int32_t cj_shutdown(void) {
+    if (!ready()) return CJ_OK;
+    (void)hipStreamSynchronize(g.stream);
+    std::vector<uintptr_t> ps;
+    {
+        std::lock_guard<std::mutex> lk(g.mu);
+        for (auto &kv : g.allocs) ps.push_back(kv.first);
+        g.allocs.clear();
+    }
+    for (auto p : ps) (void)hipFree((void *)p);
+    (void)hipStreamDestroy(g.stream);
+    (void)hipModuleUnload(g.module);
+    g.module = nullptr;
+    g.fns.clear();
+    g.device = -1;
+    return CJ_OK;
+}
+
+int32_t cj_last_error(int8_t *buf, int32_t cap) {
+    if (!buf || cap <= 0) return CJ_ERR_ARG;
+    snprintf((char *)buf, (size_t)cap, "%s", g_err.c_str());
+    return CJ_OK;
+}
+
+int32_t cj_kernel_available(const int8_t *name) {
+    if (!name || !ready()) return 0;
+    std::string n((const char *)name);
+    auto it = name_map().find(n);
+    if (it != name_map().end()) n = it->second;
+    return g.fns.count(n) ? 1 : 0;
+}
+
+int32_t cj_device_info(int64_t *out, int32_t n) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
+    int64_t v[3] = {g.cus, g.hbm, g.lds};
+    for (int i = 0; i < n && i < 3; i++) out[i] = v[i];
+    return CJ_OK;
+}
+
+// ------------------------------------------------------------- buffers
+
+int64_t cj_buf_alloc(int64_t bytes) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run"), 0;
+    if (bytes <= 0) return fail(CJ_ERR_ARG, "cj_buf_alloc: %lld bytes", (long long)bytes), 0;
+    void *p = dev_alloc((size_t)bytes);
+    if (!p) return fail(CJ_ERR_HIP, "hipMalloc(%lld) failed", (long long)bytes), 0;
+    return (int64_t)(uintptr_t)p;
+}
+
+int32_t cj_buf_free(int64_t buf) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    auto it = g.allocs.find((uintptr_t)buf);
+    if (it == g.allocs.end()) return fail(CJ_ERR_STATE, "cj_buf_free: unknown handle");
+    g.allocs.erase(it);
+    (void)hipFree((void *)(uintptr_t)buf);
+    return CJ_OK;
+}
+
+int64_t cj_buf_size(int64_t buf) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    auto it = g.allocs.find((uintptr_t)buf);
+    return it == g.allocs.end() ? 0 : (int64_t)it->second;
+}
+
+int32_t cj_buf_upload(int64_t buf, int64_t off, const int8_t *src, int64_t bytes) {
+    if (!in_buffer(dptr(buf + off), bytes)) return fail(CJ_ERR_ARG, "cj_buf_upload: extent outside the buffer");
+    CJ_HIP(hipMemcpyAsync(dptr(buf + off), src, (size_t)bytes, hipMemcpyHostToDevice, g.stream));
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    return CJ_OK;
+}
+
+int32_t cj_buf_download(int64_t buf, int64_t off, int8_t *dst, int64_t bytes) {
+    if (!in_buffer(dptr(buf + off), bytes)) return fail(CJ_ERR_ARG, "cj_buf_download: extent outside the buffer");
+    CJ_HIP(hipMemcpyAsync(dst, dptr(buf + off), (size_t)bytes, hipMemcpyDeviceToHost, g.stream));
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    return CJ_OK;
+}
+
+int32_t cj_buf_zero(int64_t buf) {
+    int64_t n = cj_buf_size(buf);
+    if (n <= 0) return fail(CJ_ERR_ARG, "cj_buf_zero: unknown handle");
+    struct { uint32_t *p; int64_t words; } a = {(uint32_t *)dptr(buf), (n + 3) / 4};
+    uint32_t grid = (uint32_t)std::min<int64_t>((a.words + 255) / 256, 65535);
+    return launch("cj_zero", grid, 256, 0, a);
+}
+
+// -------------------------------------------------------- stream / graph
+
+int32_t cj_stream_sync(void) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    return CJ_OK;
+}
+
+int32_t cj_graph_begin(void) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
+    CJ_HIP(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+    return CJ_OK;
+}
+
+int64_t cj_graph_end(void) {
+    hipGraph_t gr = nullptr;
+    hipError_t e = hipStreamEndCapture(g.stream, &gr);
+    if (e != hipSuccess) return fail(CJ_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e)), 0;
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(gr);
+    if (e != hipSuccess) return fail(CJ_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e)), 0;
+    return (int64_t)(uintptr_t)ex;
+}
+
+int32_t cj_graph_launch(int64_t graph) {
+    if (!graph) return fail(CJ_ERR_ARG, "cj_graph_launch: null graph");
+    CJ_HIP(hipGraphLaunch((hipGraphExec_t)(uintptr_t)graph, g.stream));
+    return CJ_OK;
+}
+
+int32_t cj_graph_free(int64_t graph) {
+    if (graph) CJ_HIP(hipGraphExecDestroy((hipGraphExec_t)(uintptr_t)graph));
+    return CJ_OK;
+}
+
+int64_t cj_event_record(void) {
+    hipEvent_t ev;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return fail(CJ_ERR_HIP, "hipEventCreate"), 0;
+    if (hipEventRecord(ev, g.stream) != hipSuccess) return fail(CJ_ERR_HIP, "hipEventRecord"), 0;
+    return (int64_t)(uintptr_t)ev;
+}
+int32_t cj_event_wait(int64_t ev) {
+    CJ_HIP(hipEventSynchronize((hipEvent_t)(uintptr_t)ev));
+    return CJ_OK;
+}
+int32_t cj_event_free(int64_t ev) {
+    CJ_HIP(hipEventDestroy((hipEvent_t)(uintptr_t)ev));
+    return CJ_OK;
+}
+
+// --------------------------------------------------------- launch seam
+
+int32_t cj_q8k_pack(int64_t out, int64_t x, int64_t rows, int64_t n, int64_t npad, int32_t per32) {
+    if (rows <= 0 || n <= 0 || npad < n || npad % 256) return fail(CJ_ERR_ARG, "cj_q8k_pack: rows %lld n %lld npad %lld", (long long)rows, (long long)n, (long long)npad);
+    if (npad / 256 > 64) return fail(CJ_ERR_ARG, "cj_q8k_pack: %lld columns exceed the 16384 staged", (long long)npad);
+    if (!in_buffer(dptr(x), rows * n * 4) || !in_buffer(dptr(out), rows * npad / 256 * 320))
+        return fail(CJ_ERR_ARG, "cj_q8k_pack: buffers smaller than %lld rows", (long long)rows);
+    cj_pack_args a{};
+    a.out = (uint8_t *)dptr(out); a.x = (const float *)dptr(x); a.n = n; a.npad = npad; a.rows = rows; a.per32 = per32;
+    return launch("cj_pack", (uint32_t)rows, 256, (uint32_t)(npad / 256 * 320), a);
+}
+
+int32_t cj_rmsnorm_pack(int64_t out, int64_t packed, int64_t x, int64_t w, int64_t dim, float eps, int32_t form, int32_t per32) {
+    if (dim <= 0 || (!out && !packed)) return fail(CJ_ERR_ARG, "cj_rmsnorm_pack: dim %lld", (long long)dim);
+    const int64_t npad = (dim + 255) / 256 * 256;
+    if (npad / 256 > 64) return fail(CJ_ERR_ARG, "cj_rmsnorm_pack: %lld columns exceed the 16384 staged", (long long)dim);
+    if (!in_buffer(dptr(x), dim * 4) || !in_buffer(dptr(w), dim * 4) || (out && !in_buffer(dptr(out), dim * 4)) ||
+        (packed && !in_buffer(dptr(packed), npad / 256 * 320)))
+        return fail(CJ_ERR_ARG, "cj_rmsnorm_pack: a buffer is smaller than dim %lld needs", (long long)dim);
+    cj_pack_args a{};
+    a.out = (uint8_t *)dptr(packed); a.x = (const float *)dptr(x); a.w = (const float *)dptr(w);
+    a.xout = (float *)dptr(out); a.n = dim; a.npad = npad; a.rows = 1; a.eps = eps; a.form = form; a.per32 = per32; a.do_norm = 1;
+    return launch("cj_pack", 1, 256, (uint32_t)(npad / 256 * 320), a);
+}
+
+int64_t cj_prepared_row_bytes(int32_t type, int64_t cols) { return prepared_row_bytes(type, cols); }
+
+int32_t cj_prepare_weight(int64_t dst, int64_t src, int32_t type, int64_t rows, int64_t cols) {
+    const int64_t prb = prepared_row_bytes(type, cols);
+    if (prb <= 0 || rows <= 0) return fail(CJ_ERR_ARG, "cj_prepare_weight: type %d cols %lld", type, (long long)cols);
+    const int64_t be = (type == CJ_Q4_K || type == CJ_Q6_K) ? 256 : 32;
+    const int64_t bb = type == CJ_Q4_K ? 144 : type == CJ_Q6_K ? 210 : type == CJ_Q8_0 ? 34 : type == CJ_Q4_0 ? 18 : 17;
+    const int64_t srb = cols / be * bb;
+    if (!in_buffer(dptr(src), rows * srb) || !in_buffer(dptr(dst), rows * prb))
+        return fail(CJ_ERR_ARG, "cj_prepare_weight: buffers smaller than %lld rows", (long long)rows);
+    if (type == CJ_Q4_K) {
+        CJ_HIP(hipMemcpyAsync(dptr(dst), dptr(src), (size_t)(rows * srb), hipMemcpyDeviceToDevice, g.stream));
+        return CJ_OK;
+    }
+    cj_prepare_args a{};
+    a.dst = (uint8_t *)dptr(dst); a.src = (const uint8_t *)dptr(src); a.rows = rows; a.cols = cols;
+    a.src_row_bytes = srb; a.dst_row_bytes = prb; a.type = type;
+    const int64_t items = rows * (cols / be);
+    return launch("cj_prepare", (uint32_t)((items + 255) / 256), 256, 0, a);
+}
+
+int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows, int64_t cols, int64_t y_off, int32_t accum) {
+    const int64_t prb = prepared_row_bytes(type, cols);
+    if (prb <= 0 || rows <= 0 || !gemv_supported(type, cols))
+        return fail(CJ_ERR_ARG, "cj_matvec: type %d with %lld columns is not served", type, (long long)cols);
+    const int64_t nblk = (cols + 255) / 256;
+    const bool f32 = is_f32_act(type);
+    if (!in_buffer(dptr(w), rows * prb)) return fail(CJ_ERR_ARG, "cj_matvec: weight smaller than %lld prepared rows", (long long)rows);
+    if (!in_buffer(dptr(act), f32 ? cols * 4 : nblk * 320)) return fail(CJ_ERR_ARG, "cj_matvec: activation smaller than its %s form", f32 ? "f32" : "packed");
+    if (y_off < 0 || !in_buffer(dptr(y + 4 * y_off), rows * 4)) return fail(CJ_ERR_ARG, "cj_matvec: output smaller than y_off + rows");
+    cj_gemv_args a{};
+    a.w = (const uint8_t *)dptr(w);
+    if (f32) { a.x = (const float *)dptr(act); a.pro = CJ_PRO_F32; }
+    else { a.xp = (const uint8_t *)dptr(act); a.pro = CJ_PRO_PACKED; }
+    a.y = (float *)dptr(y); a.y_off = y_off; a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type;
+    a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = type == CJ_Q8_0; a.batch = 1;
+    return run_gemv(a, plan_gemv(type, rows, cols, 2));
+}
+
+int32_t cj_glu(int64_t out, int64_t packed, int64_t gb, int64_t ub, int64_t n, int32_t form, int32_t per32) {
+    const int64_t npad = (n + 255) / 256 * 256;
+    if (n <= 0 || !in_buffer(dptr(out), n * 4) || !in_buffer(dptr(gb), n * 4) || !in_buffer(dptr(ub), n * 4) ||
+        (packed && !in_buffer(dptr(packed), npad / 256 * 320)))
+        return fail(CJ_ERR_ARG, "cj_glu: buffers smaller than n %lld", (long long)n);
+    cj_glu_args a{};
+    a.out = (float *)dptr(out); a.g = (const float *)dptr(gb); a.u = (const float *)dptr(ub);
+    a.packed = (uint8_t *)dptr(packed); a.n = n; a.npad = npad; a.form = form; a.per32 = per32;
+    return launch("cj_glu", (uint32_t)(npad / 256), 256, 0, a);
+}
+
+int32_t cj_add(int64_t ab, int64_t bb, int64_t n) {
+    if (n <= 0 || !in_buffer(dptr(ab), n * 4) || !in_buffer(dptr(bb), n * 4)) return fail(CJ_ERR_ARG, "cj_add: n %lld", (long long)n);
+    cj_add_args a{(float *)dptr(ab), (const float *)dptr(bb), n};
+    return launch("cj_add", (uint32_t)((n + 255) / 256), 256, 0, a);
+}
+
+int32_t cj_rope_table(int64_t out, int32_t head_dim, float theta, int32_t ctx) {
+    const int half = head_dim / 2;
+    if (head_dim <= 0 || head_dim % 2 || ctx <= 0 || !in_buffer(dptr(out), (int64_t)ctx * half * 8))
+        return fail(CJ_ERR_ARG, "cj_rope_table: head_dim %d ctx %d", head_dim, ctx);
+    std::vector<float> inv(half), tab((size_t)ctx * half * 2);
+    for (int d = 0; d < half; d++) inv[d] = powf(theta, (0.0f - (float)(2 * d)) / (float)head_dim);
+    for (int p = 0; p < ctx; p++)
+        for (int d = 0; d < half; d++) {
+            const float ang = (float)p * inv[d];
+            tab[((size_t)p * half + d) * 2] = cosf(ang);
+            tab[((size_t)p * half + d) * 2 + 1] = sinf(ang);
+        }
+    return cj_buf_upload(out, 0, (const int8_t *)tab.data(), (int64_t)tab.size() * 4);
+}
+
+int32_t cj_qk_prep(int64_t q, int64_t k, int64_t v, int64_t kcache, int64_t vcache, int64_t qw, int64_t kw,
+                   int64_t rope, int64_t pgtab, int32_t pg_base, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                   int32_t norm, float eps, int32_t form, int32_t pos) {
+    if (n_q <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 256 || pos < 0)
+        return fail(CJ_ERR_ARG, "cj_qk_prep: heads %d/%d hd %d pos %d", n_q, n_kv, head_dim, pos);
+    const int64_t page = pos / 64;
+    if (!in_buffer(dptr(q), (int64_t)n_q * head_dim * 4) || !in_buffer(dptr(k), (int64_t)n_kv * head_dim * 4) ||
+        !in_buffer(dptr(v), (int64_t)n_kv * head_dim * 4) || !in_buffer(dptr(pgtab + 4 * (pg_base + page)), 4) ||
+        !in_buffer(dptr(rope), ((int64_t)pos + 1) * head_dim * 4) ||
+        (norm && (!in_buffer(dptr(qw), head_dim * 4) || !in_buffer(dptr(kw), head_dim * 4))))
+        return fail(CJ_ERR_ARG, "cj_qk_prep: a buffer is smaller than the shapes need");
+    int32_t pg = 0;
+    CJ_HIP(hipMemcpyAsync(&pg, dptr(pgtab + 4 * (pg_base + page)), 4, hipMemcpyDeviceToHost, g.stream));
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    const int64_t need = (((int64_t)pg + 1) * n_kv * 64) * head_dim * 2;
+    if (pg < 0 || !in_buffer(dptr(kcache), need) || !in_buffer(dptr(vcache), need))
+        return fail(CJ_ERR_CAPACITY, "cj_qk_prep: page %d outside the K/V planes", pg);
+    cj_qkprep_args a{};
+    a.q = (float *)dptr(q); a.k = (float *)dptr(k); a.v = (const float *)dptr(v);
+    a.kc = (uint16_t *)dptr(kcache); a.vc = (uint16_t *)dptr(vcache); a.qw = (const float *)dptr(qw); a.kw = (const float *)dptr(kw);
+    a.rope_cs = (const float *)dptr(rope); a.pgtab = (const int32_t *)dptr(pgtab);
+    a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim; a.norm = norm; a.form = form; a.pg_base = pg_base; a.pos = pos; a.eps = eps;
+    return launch("cj_qkprep", (uint32_t)(n_q + n_kv), 64, 0, a);
+}
+
+int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t vcache, int64_t pgtab, int32_t pg_base,
+                  int64_t counters, int32_t n_q, int32_t n_kv, int32_t head_dim, int32_t count, int32_t from,
+                  int32_t splits, float scale) {
+    if (n_kv <= 0 || n_q % n_kv || (head_dim != 64 && head_dim != 128) || count <= 0 || from < 0 || splits <= 0 || splits > 256)
+        return fail(CJ_ERR_ARG, "cj_attend: heads %d/%d hd %d count %d splits %d", n_q, n_kv, head_dim, count, splits);
+    const int grp = n_q / n_kv;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return fail(CJ_ERR_ARG, "cj_attend: GQA group %d not served", grp);
+    const int64_t pages = ((int64_t)from + count + 63) / 64;
+    if (!in_buffer(dptr(pgtab + 4 * pg_base), pages * 4) || !in_buffer(dptr(q), (int64_t)n_q * head_dim * 4) ||
+        !in_buffer(dptr(part), (int64_t)n_q * splits * (head_dim + 2) * 4) ||
+        (out && (!in_buffer(dptr(out), (int64_t)n_q * head_dim * 4) || !in_buffer(dptr(counters), (int64_t)n_kv * 4))))
+        return fail(CJ_ERR_ARG, "cj_attend: a buffer is smaller than the shapes need");
+    std::vector<int32_t> tab((size_t)pages);
+    CJ_HIP(hipMemcpyAsync(tab.data(), dptr(pgtab + 4 * pg_base), (size_t)pages * 4, hipMemcpyDeviceToHost, g.stream));
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    int32_t maxpg = 0;
+    for (int32_t p : tab) {
+        if (p < 0) return fail(CJ_ERR_ARG, "cj_attend: negative page in the table");
+        maxpg = std::max(maxpg, p);
+    }
+    const int64_t need = (((int64_t)maxpg + 1) * n_kv * 64) * head_dim * 2;
+    if (!in_buffer(dptr(kcache), need) || !in_buffer(dptr(vcache), need))
+        return fail(CJ_ERR_ARG, "cj_attend: page %d outside the K/V planes", maxpg);
+    cj_attn_args a{};
+    a.part = (float *)dptr(part); a.out = (float *)dptr(out); a.q = (const float *)dptr(q);
+    a.kc = (const uint16_t *)dptr(kcache); a.vc = (const uint16_t *)dptr(vcache); a.pgtab = (const int32_t *)dptr(pgtab);
+    a.counters = (int32_t *)dptr(counters); a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim; a.splits = splits;
+    a.pg_base = pg_base; a.count = count; a.from = from; a.window = 0; a.scale = scale;
+    char name[64];
+    snprintf(name, sizeof name, "cj_attn_decode_h%d_g%d", head_dim, grp);
+    return launch(name, (uint32_t)(n_kv * splits), 256, 0, a);
+}
+
+int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, int32_t head_dim, int32_t splits, int32_t per32) {
+    const int64_t n = (int64_t)n_q * head_dim, npad = (n + 255) / 256 * 256;
+    if (n <= 0 || splits <= 0 || !in_buffer(dptr(part), (int64_t)n_q * splits * (head_dim + 2) * 4) ||
+        (out && !in_buffer(dptr(out), n * 4)) || (packed && !in_buffer(dptr(packed), npad / 256 * 320)) || (!out && !packed))
+        return fail(CJ_ERR_ARG, "cj_attn_merge: buffers smaller than the shapes need");
+    cj_merge_args a{(float *)dptr(out), (uint8_t *)dptr(packed), (const float *)dptr(part), n_q, head_dim, splits, per32};
+    return launch("cj_attn_merge", (uint32_t)(npad / 256), 256, 0, a);
+}
+
+int32_t cj_embed_row(int64_t out, int64_t table, int32_t type, int64_t hidden, int32_t token) {
+    const int64_t be = (type == CJ_Q4_K || type == CJ_Q6_K) ? 256 : (type == CJ_F32 || type == CJ_F16) ? 1 : 32;
+    const int64_t bb = type == CJ_F32 ? 4 : type == CJ_F16 ? 2 : type == CJ_Q4_K ? 144 : type == CJ_Q6_K ? 210
+                     : type == CJ_Q8_0 ? 34 : type == CJ_Q4_0 ? 18 : type == CJ_MXFP4 ? 17 : -1;
+    if (bb < 0 || hidden % be || token < 0) return fail(CJ_ERR_ARG, "cj_embed_row: type %d hidden %lld", type, (long long)hidden);
+    const int64_t rb = hidden / be * bb;
+    if (!in_buffer(dptr(table + ((int64_t)token) * rb), rb) || !in_buffer(dptr(out), hidden * 4))
+        return fail(CJ_ERR_ARG, "cj_embed_row: token %d outside the table", token);
+    cj_embed_args a{};
+    a.out = (float *)dptr(out); a.table = (const uint8_t *)dptr(table); a.type = type; a.hidden = hidden; a.row_bytes = rb; a.token = token;
+    return launch("cj_embed", (uint32_t)((hidden + 255) / 256), 256, 0, a);
+}
+
+int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n) {
+    if (n <= 0 || row < 0 || !in_buffer(dptr(tok + 4 * row), 4) || !in_buffer(dptr(v), n * 4))
+        return fail(CJ_ERR_ARG, "cj_argmax_row: n %lld row %d", (long long)n, row);
+    static void *scratch = nullptr;
+    static int64_t scratch_groups = 0;
+    const int64_t groups = (n + 1023) / 1024;
+    if (groups > scratch_groups) {
+        CJ_HIP(hipStreamSynchronize(g.stream));
+        dev_free(scratch);
+        scratch = dev_alloc((size_t)(groups * 8 + 64));
+        if (!scratch) return fail(CJ_ERR_HIP, "cj_argmax_row: scratch allocation");
+        CJ_HIP(hipMemsetAsync(scratch, 0, (size_t)(groups * 8 + 64), g.stream));
+        scratch_groups = groups;
+    }
+    cj_argmax_args a{};
+    a.tok = (int32_t *)dptr(tok); a.v = (const float *)dptr(v); a.pv = (float *)scratch;
+    a.pi = (int32_t *)((char *)scratch + scratch_groups * 4); a.counter = (int32_t *)((char *)scratch + scratch_groups * 8);
+    a.n = n; a.row = row;
+    return launch("cj_argmax", (uint32_t)groups, 256, 0, a);
+}
+
+int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t cols, int32_t prepared) {
+    int64_t rb;
+    if (prepared) rb = prepared_row_bytes(type, cols);
+    else {
+        const int64_t be = (type == CJ_Q4_K || type == CJ_Q6_K) ? 256 : (type == CJ_F32 || type == CJ_F16) ? 1 : 32;
+        const int64_t bb = type == CJ_F32 ? 4 : type == CJ_F16 ? 2 : type == CJ_Q4_K ? 144 : type == CJ_Q6_K ? 210
+                         : type == CJ_Q8_0 ? 34 : type == CJ_Q4_0 ? 18 : type == CJ_MXFP4 ? 17 : -1;
+        rb = (bb < 0 || cols % be) ? -1 : cols / be * bb;
+    }
+    if (rb <= 0 || rows <= 0) return fail(CJ_ERR_ARG, "cj_dequant: type %d cols %lld", type, (long long)cols);
+    if (!in_buffer(dptr(raw), rows * rb) || !in_buffer(dptr(out), rows * cols * 4))
+        return fail(CJ_ERR_ARG, "cj_dequant: buffers smaller than %lld rows", (long long)rows);
+    cj_dequant_args a{};
+    a.out = (float *)dptr(out); a.raw = (const uint8_t *)dptr(raw); a.elems = rows * cols; a.row_bytes = rb; a.cols = cols;
+    a.type = type; a.prepared = prepared;
+    const int64_t grid = std::min<int64_t>((a.elems + 255) / 256, 16384);
+    return launch("cj_dequant", (uint32_t)grid, 256, 0, a);
+}
+
+int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts, int32_t n_used, int32_t norm_topk) {
+    if (rows <= 0 || n_experts <= 0 || n_experts > 256 || n_used <= 0 || n_used > n_experts || n_used > 16 ||
+        !in_buffer(dptr(logits), (int64_t)rows * n_experts * 4) || !in_buffer(dptr(sel), (int64_t)rows * n_used * 4) ||
+        !in_buffer(dptr(weights), (int64_t)rows * n_used * 4))
+        return fail(CJ_ERR_ARG, "cj_moe_route: rows %d experts %d used %d", rows, n_experts, n_used);
+    cj_route_args a{(const float *)dptr(logits), (int32_t *)dptr(sel), (float *)dptr(weights), n_experts, n_used, norm_topk, rows};
+    return launch("cj_moe_route", (uint32_t)rows, 64, 0, a);
+}
+
+}  // extern "C"

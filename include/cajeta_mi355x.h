@@ -1,0 +1,221 @@
+/*
+ * cajeta_mi355x.h — the C-ABI of the MI355X (gfx950) decode backend for
+ * cajeta-llm.
+ *
+ * Every entry point takes only int32/int64/float scalars, opaque int64
+ * handles and pointers to primitive arrays, so Cajeta's @Native (which
+ * marshals no structs or callbacks, README.md:8-10) can bind each one
+ * directly. Every call returns an int32 status (CJ_OK = 0, negative on
+ * error) or a handle (> 0, or 0 on error); cj_last_error copies the message.
+ * A refused launch enqueues nothing and returns an error: nothing is ever
+ * skipped silently.
+ *
+ * Launches are "NoSync": they enqueue on the library's single in-order HIP
+ * stream (the reference's QuantKernel.stream(), io/QuantKernel.cajeta:60-80)
+ * and return. Device buffers are handles from cj_buf_alloc; every launch
+ * checks that the extents it will touch fit inside the buffers it is given.
+ *
+ * Citations (file:line) are into jklappenbach/cajeta-llm,
+ * src/main/cajeta/dev/cajeta/llm/ unless stated otherwise.
+ */
+#ifndef CAJETA_MI355X_H
+#define CAJETA_MI355X_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CJ_OK 0
+#define CJ_ERR_ARG (-1)       /* an argument or extent check failed */
+#define CJ_ERR_HIP (-2)       /* the HIP runtime reported an error */
+#define CJ_ERR_NOKERNEL (-3)  /* the kernel is not in the loaded code object */
+#define CJ_ERR_STATE (-4)     /* not initialised, or a stale handle */
+#define CJ_ERR_CAPACITY (-5)  /* KV pages or context exhausted (DeviceKv.prep, model/DeviceKv.cajeta:409-412) */
+#define CJ_ERR_IO (-6)        /* a model file could not be read or parsed */
+
+/* Weight formats: ggml type ids (io/Quant.cajeta GG_*). */
+#define CJ_TYPE_F32 0
+#define CJ_TYPE_F16 1
+#define CJ_TYPE_Q4_0 2
+#define CJ_TYPE_Q8_0 8
+#define CJ_TYPE_Q4_K 12
+#define CJ_TYPE_Q6_K 14
+#define CJ_TYPE_MXFP4 39
+
+/* ------------------------------------------------------------- runtime */
+
+/* Select the device, create the stream, load kernels.hsaco with
+ * hipModuleLoad. Replaces Device.force(backend) (LlmEngine.cajeta:168-170). */
+int32_t cj_init(int32_t device);
+int32_t cj_shutdown(void);
+/* Copy the last error message (NUL-terminated, truncated to cap). */
+int32_t cj_last_error(int8_t *buf, int32_t cap);
+/* 1 when `name` (NUL-terminated) is a kernel this backend registered, else 0:
+ * the registry behind KernelCap.usable (model/KernelCap.cajeta:228-300),
+ * answered under the reference's kernel names (q4kQ8WaveMatVecKernel, ...). */
+int32_t cj_kernel_available(const int8_t *name);
+/* out[0] = compute units, out[1] = HBM bytes, out[2] = LDS bytes per CU. */
+int32_t cj_device_info(int64_t *out, int32_t n);
+
+/* ------------------------------------------------------------- buffers */
+
+/* KernelBuffer<T> (the cajeta.xpu runtime): device memory by handle. */
+int64_t cj_buf_alloc(int64_t bytes);
+int32_t cj_buf_free(int64_t buf);
+int64_t cj_buf_size(int64_t buf);
+int32_t cj_buf_upload(int64_t buf, int64_t off, const int8_t *src, int64_t bytes);
+int32_t cj_buf_download(int64_t buf, int64_t off, int8_t *dst, int64_t bytes);
+/* Zero a buffer with a fill kernel (safe inside a captured graph). */
+int32_t cj_buf_zero(int64_t buf);
+
+/* ------------------------------------------------------ stream / graph */
+
+int32_t cj_stream_sync(void);
+/* Capture the launches enqueued between begin and end into a hipGraph: the
+ * deferred per-token replay of KernelStream (io/QuantKernel.cajeta:69-77). */
+int32_t cj_graph_begin(void);
+int64_t cj_graph_end(void);
+int32_t cj_graph_launch(int64_t graph);
+int32_t cj_graph_free(int64_t graph);
+/* Event.recordOn / Event.waitHost (model/CausalLM.cajeta:1245-1256). */
+int64_t cj_event_record(void);
+int32_t cj_event_wait(int64_t ev);
+int32_t cj_event_free(int64_t ev);
+
+/* ------------------------------------------------------- launch seam */
+
+/* q8_K activation pack of `rows` rows of n floats into 320-byte blocks, the
+ * rows padded to npad (a multiple of 256); per32 = one scale per 32 values.
+ * Replaces QuantKernel.q8kPackLaunchNoSync / q8kPackRowsLaunchNoSync
+ * (io/QuantKernel.cajeta:42783-42800) and the q8kPack32 form (:42876-42888). */
+int32_t cj_q8k_pack(int64_t out, int64_t x, int64_t rows, int64_t n, int64_t npad, int32_t per32);
+
+/* RMSNorm (+ the pack of the result when packed != 0). out may be 0 when
+ * only the pack is wanted. Replaces Prim.rmsnormPackDevice
+ * (model/Prim.cajeta:1392-1406), rmsnormPack32RowsDevice (:1428-1438) and
+ * rmsnormDevice (:1440). form 0: x·s·w, 1: x·s·(1+w). */
+int32_t cj_rmsnorm_pack(int64_t out, int64_t packed, int64_t x, int64_t w, int64_t dim,
+                        float eps, int32_t form, int32_t per32);
+
+/* Byte size of one prepared row of `type` with `cols` columns, and the
+ * load-time re-layout of GGUF rows into it (Quant.splitInto,
+ * io/Quant.cajeta:184-251, re-designed for 128-bit loads). */
+int64_t cj_prepared_row_bytes(int32_t type, int64_t cols);
+int32_t cj_prepare_weight(int64_t dst, int64_t src, int32_t type, int64_t rows, int64_t cols);
+
+/* y[y_off + r] (+)= Σ_c W[r][c]·x[c] over a PREPARED weight. For Q4_K/Q6_K
+ * `act` is a per-256 q8_K pack, for Q8_0 a per-32 pack, for Q4_0/MXFP4 f32.
+ * Replaces the route dispatch Linear.launchOne (model/Linear.cajeta:6569-6761)
+ * over q4kQ8WaveMatVecLaunchNoSync (io/QuantKernel.cajeta:33558),
+ * q6kQ8WaveMatVecKernel (:36273), q80Q8WaveMatVecKernel (:42509),
+ * q40F32WaveMatVecKernel and mxfp4MatVecKernel (:43202); accum = 1 is
+ * matvecStagedAccum's residual store (model/Linear.cajeta:5776). */
+int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows, int64_t cols,
+                  int64_t y_off, int32_t accum);
+
+/* out = act(g)·u (act 0: SiLU exp form, 1: the CPU backend's rational-tanh
+ * form), plus its pack when packed != 0. Replaces Prim.gluPackDevice
+ * (model/Prim.cajeta:1775-1785), gluPack32Device (:1789-1800), gluDevice. */
+int32_t cj_glu(int64_t out, int64_t packed, int64_t g, int64_t u, int64_t n, int32_t form, int32_t per32);
+
+/* a += b (Prim.addDevice, model/Prim.cajeta:1629). */
+int32_t cj_add(int64_t a, int64_t b, int64_t n);
+
+/* Per-position (cos, sin) table for split-half RoPE: rope[p][d] =
+ * (cos(p·inv[d]), sin(p·inv[d])) with inv[d] = theta^(-2d/hd)
+ * (Prim.invFreq, model/Prim.cajeta:1866-1909). Writes ctx·hd floats. */
+int32_t cj_rope_table(int64_t out, int32_t head_dim, float theta, int32_t ctx);
+
+/* QK-norm (norm != 0) + RoPE + fp16 K/V append at position pos through the
+ * page table. q [n_q·hd], k/v [n_kv·hd] f32 in HF (split-half) order.
+ * Replaces AttnKernel.qkPrepLaunchNoSync (model/AttnKernel.cajeta:208-231). */
+int32_t cj_qk_prep(int64_t q, int64_t k, int64_t v, int64_t kcache, int64_t vcache, int64_t qw, int64_t kw,
+                   int64_t rope, int64_t pgtab, int32_t pg_base, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                   int32_t norm, float eps, int32_t form, int32_t pos);
+
+/* Split-K decode attention over positions [from, from+count): partials
+ * [n_q][splits][hd+2] into `part`; when out != 0 the last split of each kv
+ * head merges into out [n_q·hd]. Replaces
+ * AttnKernel.attendDecodePartialsLaunchNoSync (model/AttnKernel.cajeta:5090-5135)
+ * and, with out, attendDecodeLaunchNoSync (:6900-6970). counters: n_kv int32
+ * words left zeroed by the launch. */
+int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t vcache, int64_t pgtab,
+                  int32_t pg_base, int64_t counters, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                  int32_t count, int32_t from, int32_t splits, float scale);
+
+/* Merge split partials into f32 out and/or their pack. Replaces
+ * attnReducePackQ8Kernel (model/AttnKernel.cajeta:5165-5259). */
+int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, int32_t head_dim,
+                      int32_t splits, int32_t per32);
+
+/* out[0..hidden) = decoded row `token` of a GGUF-layout table. Replaces
+ * EmbedKernel.embedRowLaunchNoSync (model/EmbedKernel.cajeta:69-265). */
+int32_t cj_embed_row(int64_t out, int64_t table, int32_t type, int64_t hidden, int32_t token);
+
+/* tok[row] = first-occurrence argmax of v[0..n) (argmaxRowLaunchNoSync,
+ * io/QuantKernel.cajeta:41520-41527). */
+int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n);
+
+/* Dequantize rows·cols elements of a weight, GGUF layout (prepared = 0) or
+ * the prepared layout (1). Quant.dequantize (io/Quant.cajeta:693-734). */
+int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t cols, int32_t prepared);
+
+/* MoE router selection over `rows` rows of n_experts logits: softmax,
+ * top-k by probability (ties to the lower index), optional renormalisation.
+ * MoeFfn.routeFromLogits (model/MoeFfn.cajeta:908-960). */
+int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts,
+                     int32_t n_used, int32_t norm_topk);
+
+/* ------------------------------------------------------------ engine */
+
+/* The LlmEngine surface (LlmEngine.cajeta:165-546) over a GGUF model:
+ * path "mem:<name>" loads an image made by cj_synth_gguf. ctx is the KV
+ * capacity per sequence, max_seqs the sequence slots. */
+int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs);
+int32_t cj_engine_close(int64_t eng);
+/* n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab, ctx, n_experts, n_used, weight type, head type */
+int32_t cj_engine_config(int64_t eng, int64_t *out, int32_t n);
+/* LlmEngine.submitTokens (:477): a greedy request; returns the request id. */
+int32_t cj_engine_submit(int64_t eng, const int32_t *prompt, int32_t n, int32_t max_new);
+/* LlmEngine.runAll (:500) / stepOnce (:504): drive requests (bounded). */
+int32_t cj_engine_run_all(int64_t eng, int32_t max_steps);
+int32_t cj_engine_step_once(int64_t eng);
+/* Request state: writes up to cap generated ids; *done = 1 when finished,
+ * *reason 0 length, 1 EOG, 2 cancelled. Returns the generated count. */
+int32_t cj_engine_request(int64_t eng, int32_t id, int32_t *tokens, int32_t cap, int32_t *done, int32_t *reason);
+int32_t cj_engine_cancel(int64_t eng, int32_t id);
+int32_t cj_engine_set_eog(int64_t eng, const int32_t *ids, int32_t n);
+
+/* CausalLM seam: teacher-forced or free greedy decode of one sequence slot.
+ * prefill feeds tokens[0..n) at positions pos0.. (the graph-captured decode
+ * step, one per position); decode runs `steps` greedy steps from the state
+ * prefill left and writes the generated ids. logits: the last step's row. */
+int32_t cj_engine_reset(int64_t eng, int32_t seq);
+int32_t cj_engine_prefill(int64_t eng, int32_t seq, const int32_t *tokens, int32_t n);
+int32_t cj_engine_decode(int64_t eng, int32_t seq, int32_t steps, int32_t *out_tokens);
+int32_t cj_engine_logits(int64_t eng, int32_t seq, float *out, int64_t n);
+/* Predicted (argmax) ids at positions 1..n of the slot's history. */
+int32_t cj_engine_preds(int64_t eng, int32_t seq, int32_t *out, int32_t n);
+/* Average device time per decode step over the last cj_engine_decode call (µs). */
+float cj_engine_last_step_us(int64_t eng);
+/* Debug taps of the last step (CausalLM.sniffBuf, model/CausalLM.cajeta:2260-2360):
+ * what 0 = residual hs [hidden], 1 = rotated q [n_heads·hd], 2 = attention
+ * output [n_heads·hd], 3 = SiLU·up activation [ffn], 4 = logits [vocab] —
+ * each as the last layer left it. */
+int32_t cj_engine_trace(int64_t eng, int32_t what, float *out, int64_t n);
+
+/* -------------------------------------------------- synthetic models */
+
+/* Write a seeded random-init GGUF (v3, llama metadata, q/k rows in GGUF's
+ * rope order) for `spec` — "c1" ... "c5" or "key=value;..." — to `path`, or
+ * to an in-process image when path is "mem:<name>". */
+int32_t cj_synth_gguf(const int8_t *spec, const int8_t *path, int64_t seed);
+/* Host address and size of an in-process image (for checkers). */
+int32_t cj_image_info(const int8_t *name, int64_t *addr, int64_t *size);
+int32_t cj_image_free(const int8_t *name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,849 @@
+/*
+ * oracle.c — CPU restatement of cajeta-llm's CPU-backend decode arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -ffp-contract=off so
+ * every `a + b * c` below rounds twice, as written. Each function names the
+ * reference file:line it restates; `L/` = src/main/cajeta/dev/cajeta/llm/.
+ */
+#include "oracle.h"
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <stdio.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline float bits_f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline int32_t rd_i32(const uint8_t *p) { int32_t v; memcpy(&v, p, 4); return v; }
+static inline uint16_t rd_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline void wr_i32(uint8_t *p, int32_t v) { memcpy(p, &v, 4); }
+
+int or_model_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ---------------------------------------------------------------- formats */
+
+int or_block_bytes(int t) {
+    switch (t) {
+    case OR_F32: return 4; case OR_F16: return 2; case OR_Q4_0: return 18; case OR_Q8_0: return 34;
+    case OR_Q4_K: return 144; case OR_Q6_K: return 210; case OR_MXFP4: return 17; default: return -1;
+    }
+}
+int or_block_elems(int t) {
+    switch (t) {
+    case OR_F32: case OR_F16: return 1; case OR_Q4_0: case OR_Q8_0: case OR_MXFP4: return 32;
+    case OR_Q4_K: case OR_Q6_K: return 256; default: return -1;
+    }
+}
+
+/* IEEE half -> float, exact (GgufFile.halfBitsToF32, L/io/GgufFile.cajeta:1055). */
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+    uint32_t e = (h >> 10) & 31, m = h & 1023;
+    if (e == 31) return bits_f(sign | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        if (m == 0) return bits_f(sign);
+        float v = (float)m * (1.0f / 16777216.0f); /* m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    return bits_f(sign | ((e + 112) << 23) | (m << 13));
+}
+
+/* float -> half, round to nearest even (Quant.f32ToHalfBits, L/io/Quant.cajeta:838-859,
+ * which is ggml's fp32_to_fp16; restated here as plain mantissa rounding). */
+uint16_t or_f32_to_f16(float f) {
+    uint32_t x = f_bits(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return sign | 0x7e00;          /* NaN */
+    if (ax >= 0x477ff000u) return sign | 0x7c00;         /* rounds past 65504 -> inf */
+    if (ax < 0x38800000u) {                              /* below 2^-14: half subnormal */
+        uint32_t e = ax >> 23;
+        if (e < 102) return sign;                        /* < 2^-25: rounds to zero */
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t sh = 126 - e;                           /* value*2^24 = m >> sh */
+        uint32_t q = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return sign | (uint16_t)q;
+    }
+    uint32_t r = ax + 0xfffu + ((ax >> 13) & 1u);
+    return sign | (uint16_t)((r >> 13) - (112u << 10));
+}
+
+/* Q4_K / Q5_K header scales (Quant.headK4, L/io/Quant.cajeta:2044-2080). */
+static void head_k4(const uint8_t *b, float *d, float *dmin, int sc[8], int mn[8]) {
+    *d = or_f16_to_f32(rd_u16(b));
+    *dmin = or_f16_to_f32(rd_u16(b + 2));
+    const uint8_t *s = b + 4;
+    for (int j = 0; j < 4; j++) { sc[j] = s[j] & 63; mn[j] = s[4 + j] & 63; }
+    for (int j = 0; j < 4; j++) {
+        sc[4 + j] = (s[8 + j] & 15) | ((s[j] >> 2) & 48);
+        mn[4 + j] = (s[8 + j] >> 4) | ((s[4 + j] >> 2) & 48);
+    }
+}
+
+/* E2M1 code value (Quant.mxfp4Code, L/io/Quant.cajeta:1106-1120). */
+static int mxfp4_code(int nib) {
+    static const int mag[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+    int v = mag[nib & 7];
+    return (nib & 8) ? -v : v;
+}
+/* E8M0 half-scale 2^(e-128) incl. the e<2 denormals (Quant.mxfp4Scale, :1124-1131). */
+static float mxfp4_scale(int e) {
+    uint32_t b = e < 2 ? (0x00200000u << e) : ((uint32_t)(e - 1) << 23);
+    return bits_f(b);
+}
+
+/* Quant.dequantize (L/io/Quant.cajeta:693-734) and the block bodies it calls:
+ * q80Block :752, q40Block :1186-1196, q4kBlock :2084-2104, q6kBlock :2135-2154,
+ * mxfp4Block :1133-1144. */
+int or_dequant(int type, const uint8_t *raw, int64_t nb, float *out) {
+    int bb = or_block_bytes(type), be = or_block_elems(type);
+    if (bb < 0) return -1;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *r = raw + b * bb;
+        float *o = out + b * be;
+        switch (type) {
+        case OR_F32: memcpy(o, r, 4); break;
+        case OR_F16: o[0] = or_f16_to_f32(rd_u16(r)); break;
+        case OR_Q8_0: {
+            float d = or_f16_to_f32(rd_u16(r));
+            for (int j = 0; j < 32; j++) o[j] = d * (float)(int8_t)r[2 + j];
+        } break;
+        case OR_Q4_0: {
+            float d = or_f16_to_f32(rd_u16(r));
+            for (int j = 0; j < 16; j++) {
+                int q = r[2 + j];
+                o[j] = d * (float)((q & 15) - 8);
+                o[j + 16] = d * (float)((q >> 4) - 8);
+            }
+        } break;
+        case OR_Q4_K: {
+            float d, dmin; int sc[8], mn[8];
+            head_k4(r, &d, &dmin, sc, mn);
+            for (int e = 0; e < 256; e++) {
+                int g = e / 64, rr = e % 64, s = rr / 32, l = rr % 32;
+                int q = (r[16 + 32 * g + l] >> (4 * s)) & 15;
+                int sb = e / 32;
+                o[e] = d * (float)sc[sb] * (float)q - dmin * (float)mn[sb];
+            }
+        } break;
+        case OR_Q6_K: {
+            float d = or_f16_to_f32(rd_u16(r + 208));
+            for (int e = 0; e < 256; e++) {
+                int g = e / 128, rr = e % 128, sl = rr / 64, l64 = rr % 64;
+                int ql = (r[64 * g + l64] >> (4 * sl)) & 15;
+                int sh = rr / 32, l32 = rr % 32;
+                int qh = (r[128 + 32 * g + l32] >> (2 * sh)) & 3;
+                int q = (ql | (qh << 4)) - 32;
+                int scb = (int8_t)r[192 + e / 16];
+                o[e] = d * (float)scb * (float)q;
+            }
+        } break;
+        case OR_MXFP4: {
+            float d = mxfp4_scale(r[0]);
+            for (int j = 0; j < 16; j++) {
+                int b8 = r[1 + j];
+                o[j] = (float)mxfp4_code(b8 & 15) * d;
+                o[j + 16] = (float)mxfp4_code((b8 >> 4) & 15) * d;
+            }
+        } break;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ packs */
+
+/* Math.round as the pack kernels use it: half away from zero (the CPU row
+ * form's trunc + 2·frac trick, L/model/Prim.cajeta:1190-1240, is the same map). */
+static inline int round_away(float v) { return (int)roundf(v); }
+
+/* Quant.q8kPackPad (L/io/Quant.cajeta:3232-3276): per 256 values one scale
+ * amax/127, q = round(v·127/amax), eight int32 sums of 32, scale bits at 288. */
+void or_q8k_pack(const float *x, int64_t n, int64_t npad, uint8_t *out) {
+    int64_t blocks = npad / 256;
+    for (int64_t b = 0; b < blocks; b++) {
+        uint8_t *ob = out + b * 320;
+        int64_t e0 = b * 256;
+        float amax = 0.0f;
+        for (int i = 0; i < 256; i++) {
+            float v = e0 + i < n ? x[e0 + i] : 0.0f;
+            float av = v < 0.0f ? 0.0f - v : v;
+            if (av > amax) amax = av;
+        }
+        float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        memset(ob, 0, 320);
+        for (int sb = 0; sb < 8; sb++) {
+            int s = 0;
+            for (int k = 0; k < 32; k++) {
+                int64_t e = e0 + sb * 32 + k;
+                float v = e < n ? x[e] : 0.0f;
+                int q = round_away(v * inv);
+                ob[sb * 32 + k] = (uint8_t)(int8_t)q;
+                s += q;
+            }
+            wr_i32(ob + 256 + sb * 4, s);
+        }
+        wr_i32(ob + 288, (int32_t)f_bits(amax / 127.0f));
+    }
+}
+
+/* Quant.q8kPack32Pad (L/io/Quant.cajeta:3285-3321) in the form the device
+ * pack uses (QuantKernel.q8kPack32BlockSerial, L/io/QuantKernel.cajeta:42841-42872):
+ * each 32 values quantize against their own amax; scale j at 288+4j. */
+void or_q8k_pack32(const float *x, int64_t n, int64_t npad, uint8_t *out) {
+    int64_t blocks = npad / 256;
+    for (int64_t b = 0; b < blocks; b++) {
+        uint8_t *ob = out + b * 320;
+        memset(ob, 0, 320);
+        for (int sb = 0; sb < 8; sb++) {
+            int64_t e0 = b * 256 + sb * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                float v = e0 + i < n ? x[e0 + i] : 0.0f;
+                float av = v < 0.0f ? 0.0f - v : v;
+                if (av > amax) amax = av;
+            }
+            float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+            int s = 0;
+            for (int k = 0; k < 32; k++) {
+                float v = e0 + k < n ? x[e0 + k] * inv : 0.0f;
+                int q = round_away(v);
+                ob[sb * 32 + k] = (uint8_t)(int8_t)q;
+                s += q;
+            }
+            wr_i32(ob + 256 + sb * 4, s);
+            wr_i32(ob + 288 + sb * 4, (int32_t)f_bits(amax / 127.0f));
+        }
+    }
+}
+
+/* ---------------------------------------------------------------- GEMVs */
+
+/* Quant.q4kMatVecIntoQ8 (L/io/Quant.cajeta:3374-3445) on the packed form:
+ * per block an exact integer sumi and dmins, then
+ * acc = (acc + d·xs·sumi) − dmin·xs·dmins in block order. */
+static void mv_q4k(const uint8_t *w, int64_t rows, int64_t cols, const uint8_t *xp, float *y) {
+    int64_t bpr = cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t b = 0; b < bpr; b++) {
+            const uint8_t *r = w + (i * bpr + b) * 144;
+            const uint8_t *xb = xp + b * 320;
+            float d, dmin; int sc[8], mn[8];
+            head_k4(r, &d, &dmin, sc, mn);
+            int32_t sumi = 0;
+            for (int g = 0; g < 4; g++) {
+                int32_t lo = 0, hi = 0;
+                for (int l = 0; l < 32; l++) {
+                    int q = r[16 + 32 * g + l];
+                    lo += (q & 15) * (int8_t)xb[64 * g + l];
+                    hi += ((q >> 4) & 15) * (int8_t)xb[64 * g + 32 + l];
+                }
+                sumi += lo * sc[2 * g] + hi * sc[2 * g + 1];
+            }
+            int32_t dmins = 0;
+            for (int sb = 0; sb < 8; sb++) dmins += mn[sb] * rd_i32(xb + 256 + 4 * sb);
+            float xs = bits_f((uint32_t)rd_i32(xb + 288));
+            acc = acc + d * xs * (float)sumi - dmin * xs * (float)dmins;
+        }
+        y[i] = acc;
+    }
+}
+
+/* Quant.q6kMatVecIntoQ8 (L/io/Quant.cajeta:3448-3486): per block
+ * sumi = Σ_sb scale_sb·dot_sb (int), acc = acc + d·xs·sumi. */
+static void mv_q6k(const uint8_t *w, int64_t rows, int64_t cols, const uint8_t *xp, float *y) {
+    int64_t bpr = cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t b = 0; b < bpr; b++) {
+            const uint8_t *r = w + (i * bpr + b) * 210;
+            const uint8_t *xb = xp + b * 320;
+            float d = or_f16_to_f32(rd_u16(r + 208));
+            int32_t sumi = 0;
+            for (int sb = 0; sb < 16; sb++) {
+                int n = sb / 8, k = (sb % 8) / 2, h = sb % 2;
+                int32_t dot = 0;
+                for (int t = 0; t < 16; t++) {
+                    int l = 16 * h + t;
+                    int qlb = r[64 * n + 32 * (k % 2) + l];
+                    int lo4 = k < 2 ? (qlb & 15) : (qlb >> 4);
+                    int qhb = r[128 + 32 * n + l];
+                    int q = (lo4 | (((qhb >> (2 * k)) & 3) << 4)) - 32;
+                    dot += q * (int8_t)xb[128 * n + 32 * k + l];
+                }
+                sumi += (int8_t)r[192 + sb] * dot;
+            }
+            float xs = bits_f((uint32_t)rd_i32(xb + 288));
+            acc = acc + d * xs * (float)sumi;
+        }
+        y[i] = acc;
+    }
+}
+
+/* Quant.q80MatVecIntoQ8Sub with spb = 8 (L/io/Quant.cajeta:3079-3110): per 32
+ * columns an exact integer dot times (d_j · xs_j), summed per 256 into fs,
+ * then acc += fs. Blocks past `cols` (a row padded to whole 256s by
+ * Quant.q80Interleave8Pad) hold zeros and are skipped. */
+static void mv_q80(const uint8_t *w, int64_t rows, int64_t cols, const uint8_t *xp, float *y) {
+    int64_t nbk = cols / 32, sbpr = (cols + 255) / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t b = 0; b < sbpr; b++) {
+            const uint8_t *xb = xp + b * 320;
+            float fs = 0.0f;
+            for (int j = 0; j < 8; j++) {
+                int64_t blk = b * 8 + j;
+                if (blk >= nbk) break;
+                const uint8_t *r = w + (i * nbk + blk) * 34;
+                int32_t isum = 0;
+                for (int k = 0; k < 32; k++) isum += (int8_t)r[2 + k] * (int8_t)xb[32 * j + k];
+                float xs = bits_f((uint32_t)rd_i32(xb + 288 + 4 * j));
+                fs = fs + (or_f16_to_f32(rd_u16(r)) * xs) * (float)isum;
+            }
+            acc = acc + fs;
+        }
+        y[i] = acc;
+    }
+}
+
+/* Quant.q40MatVecIntoAt (L/io/Quant.cajeta:1516-1545): f32 activations. */
+static void mv_q40(const uint8_t *w, int64_t rows, int64_t cols, const float *x, float *y) {
+    int64_t bpr = cols / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t b = 0; b < bpr; b++) {
+            const uint8_t *r = w + (i * bpr + b) * 18;
+            float dv = or_f16_to_f32(rd_u16(r));
+            float dot = 0.0f;
+            const float *xb = x + b * 32;
+            for (int j = 0; j < 16; j++) {
+                int q = r[2 + j];
+                dot = dot + (float)((q & 15) - 8) * xb[j];
+                dot = dot + (float)((q >> 4) - 8) * xb[j + 16];
+            }
+            acc = acc + dv * dot;
+        }
+        y[i] = acc;
+    }
+}
+
+/* Quant.mxfp4MatVecIntoScalar (L/io/Quant.cajeta:1146-1182): f32 activations,
+ * elements in natural order, acc = acc + code·d·x. */
+static void mv_mxfp4(const uint8_t *w, int64_t rows, int64_t cols, const float *x, float *y) {
+    int64_t bpr = cols / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t b = 0; b < bpr; b++) {
+            const uint8_t *r = w + (i * bpr + b) * 17;
+            float d = mxfp4_scale(r[0]);
+            const float *xb = x + b * 32;
+            for (int k = 0; k < 32; k++) {
+                int byv = r[1 + (k & 15)];
+                int nib = k < 16 ? (byv & 15) : ((byv >> 4) & 15);
+                acc = acc + (float)mxfp4_code(nib) * d * xb[k];
+            }
+        }
+        y[i] = acc;
+    }
+}
+
+/* F32 weights (the MoE router): plain row dot in column order. */
+static void mv_f32(const float *w, int64_t rows, int64_t cols, const float *x, float *y) {
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < cols; c++) acc = acc + w[i * cols + c] * x[c];
+        y[i] = acc;
+    }
+}
+
+int or_matvec(int type, const uint8_t *w, int64_t rows, int64_t cols,
+              const uint8_t *xp, const float *xf, float *y) {
+    switch (type) {
+    case OR_Q4_K: mv_q4k(w, rows, cols, xp, y); return 0;
+    case OR_Q6_K: mv_q6k(w, rows, cols, xp, y); return 0;
+    case OR_Q8_0: mv_q80(w, rows, cols, xp, y); return 0;
+    case OR_Q4_0: mv_q40(w, rows, cols, xf, y); return 0;
+    case OR_MXFP4: mv_mxfp4(w, rows, cols, xf, y); return 0;
+    case OR_F32: mv_f32((const float *)w, rows, cols, xf, y); return 0;
+    default: return -1;
+    }
+}
+
+/* ------------------------------------------------------------ primitives */
+
+/* RMSNorm. A row of whole 256s takes the CPU row form
+ * (Prim.rmsnormPackRowCpuKernel, L/model/Prim.cajeta:977-1071): 256 lane
+ * partials accumulated in column order, folded 128,64,...,1. Other widths
+ * take the host floor (Prim.rmsnormRowHost, :120-151). form 1 = (1 + w). */
+void or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out) {
+    float ss = 0.0f;
+    if (n % 256 == 0) {
+        float p[256];
+        for (int j = 0; j < 256; j++) p[j] = 0.0f;
+        for (int64_t k = 0; k < n / 256; k++)
+            for (int j = 0; j < 256; j++) { float a = x[k * 256 + j]; p[j] = p[j] + a * a; }
+        for (int s = 128; s > 0; s >>= 1)
+            for (int j = 0; j < s; j++) p[j] = p[j] + p[j + s];
+        ss = p[0];
+    } else {
+        for (int64_t i = 0; i < n; i++) ss = ss + x[i] * x[i];
+    }
+    float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int64_t i = 0; i < n; i++) {
+        float wi = form == 1 ? 1.0f + w[i] : w[i];
+        out[i] = x[i] * scale * wi;
+    }
+}
+
+/* SwiGLU, exp form (Prim.gluF32/gluOne, L/model/Prim.cajeta:160-196):
+ * silu(g) = g / (1 + exp(-g)). */
+void or_glu_exp(const float *g, const float *u, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; i++) {
+        float x = g[i];
+        float a = x / (1.0f + expf(0.0f - x));
+        out[i] = a * u[i];
+    }
+}
+
+/* SwiGLU, the CPU backend's vector form (Prim.gluCpuKernel,
+ * L/model/Prim.cajeta:214-273): silu = 0.5·x·(1 + tanh(x/2)) with tanh as
+ * Eigen's published 13/6 rational approximation on an argument clamped to
+ * ±7.90531110763549805; 16-wide chunks inside work blocks of 4096, the
+ * remainder of a block in the exp form. */
+static float glu_tanh_one(float x, float u) {
+    const float tlo = -7.90531110763549805f;
+    float xa = x > -16.0f ? x : -16.0f;
+    float xb = -16.0f - xa;
+    float xc = -16.0f - (xb > -32.0f ? xb : -32.0f);
+    float t0 = 0.5f * fmaf(0.0f * xc, xc * xc, xc);
+    float ta = t0 > tlo ? t0 : tlo;
+    float tb = tlo - ta;
+    float t = tlo - (tb > -15.8106222152709961f ? tb : -15.8106222152709961f);
+    float t2 = t * t;
+    float p = fmaf(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
+    p = fmaf(p, t2, -8.60467152213735e-11f);
+    p = fmaf(p, t2, 5.12229709037114e-08f);
+    p = fmaf(p, t2, 1.48572235717979e-05f);
+    p = fmaf(p, t2, 6.37261928875436e-04f);
+    p = fmaf(p, t2, 4.89352455891786e-03f) * t;
+    float q = fmaf(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
+    q = fmaf(q, t2, 2.26843463243900e-03f);
+    q = fmaf(q, t2, 4.89352518554385e-03f);
+    return 0.5f * xa * (1.0f + p / q) * u;
+}
+void or_glu_tanh(const float *g, const float *u, int64_t n, float *out) {
+    for (int64_t b0 = 0; b0 < n; b0 += 4096) {
+        int64_t hi = b0 + 4096 < n ? b0 + 4096 : n, i = b0;
+        for (; i + 16 <= hi; i++) out[i] = glu_tanh_one(g[i], u[i]);
+        for (; i < hi; i++) { float x = g[i]; out[i] = x / (1.0f + expf(0.0f - x)) * u[i]; }
+    }
+}
+
+/* Prim.invFreq, plain rope (L/model/Prim.cajeta:1866-1909): θ^(−2d/hd). */
+void or_inv_freq(int hd, float theta, float *inv) {
+    for (int d = 0; d < hd / 2; d++) inv[d] = powf(theta, (0.0f - (float)(2 * d)) / (float)hd);
+}
+
+/* Split-half RoPE (Prim.ropeRowHost, L/model/Prim.cajeta:1917-1940 and
+ * qkPrepKernel, L/model/AttnKernel.cajeta:175-196): pair (d, d+hd/2). */
+void or_rope(float *t, int nheads, int hd, int pos, const float *inv) {
+    int half = hd / 2;
+    for (int h = 0; h < nheads; h++) {
+        float *b = t + (int64_t)h * hd;
+        for (int d = 0; d < half; d++) {
+            float ang = (float)pos * inv[d];
+            float c = cosf(ang), s = sinf(ang);
+            float a = b[d], bb = b[d + half];
+            b[d] = a * c - bb * s;
+            b[d + half] = a * s + bb * c;
+        }
+    }
+}
+
+/* First-occurrence argmax (HostOps.argmaxRow, L/model/HostOps.cajeta:106-121). */
+int or_argmax(const float *v, int64_t n) {
+    int best = 0; float bv = v[0];
+    for (int64_t i = 1; i < n; i++) if (v[i] > bv) { bv = v[i]; best = (int)i; }
+    return best;
+}
+
+/* MoeFfn.routeFromLogits (L/model/MoeFfn.cajeta:908-960): full softmax over
+ * the experts, top-k by probability (strict >, ties keep the lower index),
+ * optional renormalisation by the clamped sum. Returns -1 on NaN logits. */
+int or_moe_route(const float *lb, int ne, int k, int norm, int32_t *sel, float *w) {
+    float probs[512];
+    if (ne > 512) return -2;
+    float mx = lb[0];
+    for (int e = 1; e < ne; e++) if (lb[e] > mx) mx = lb[e];
+    float sum = 0.0f;
+    for (int e = 0; e < ne; e++) { float p = expf(lb[e] - mx); probs[e] = p; sum = sum + p; }
+    for (int e = 0; e < ne; e++) probs[e] = probs[e] / sum;
+    for (int j = 0; j < k; j++) {
+        int best = -1; float bp = 0.0f;
+        for (int e = 0; e < ne; e++)
+            if (probs[e] >= 0.0f && (best < 0 || probs[e] > bp)) { best = e; bp = probs[e]; }
+        if (best < 0) return -1;
+        sel[j] = best; w[j] = bp; probs[best] = -1.0f;
+    }
+    if (norm) {
+        float ws = 0.0f;
+        for (int j = 0; j < k; j++) ws = ws + w[j];
+        if (ws < 0.00006103515625f) ws = 0.00006103515625f;
+        for (int j = 0; j < k; j++) w[j] = w[j] / ws;
+    }
+    return 0;
+}
+
+/* Checkpoint.unpermuteRows (L/io/Checkpoint.cajeta:236-274): GGUF row
+ * (h·hd + 2b + a) holds HF row (h·hd + a·half + b). */
+void or_unpermute_rows(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t rb, int nh) {
+    int64_t hd = rows / nh, half = hd / 2;
+    for (int h = 0; h < nh; h++)
+        for (int a = 0; a < 2; a++)
+            for (int64_t b = 0; b < half; b++)
+                memcpy(dst + (h * hd + a * half + b) * rb, src + (h * hd + 2 * b + a) * rb, (size_t)rb);
+}
+
+/* ------------------------------------------------------------- attention */
+
+static inline float kv_at(const void *plane, int f32, int64_t i) {
+    return f32 ? ((const float *)plane)[i] : or_f16_to_f32(((const uint16_t *)plane)[i]);
+}
+
+/* AttnKernel.cpuDecodeSplits (L/model/AttnKernel.cajeta:4879-4889). */
+int or_cpu_decode_splits(int count, int rows, int nkv, int workers) {
+    int w = workers < 1 ? 1 : workers, rk = rows * nkv < 1 ? 1 : rows * nkv;
+    int s = (2 * w + rk - 1) / rk;
+    if (s > 64) s = 64;
+    if (s > count) s = count;
+    if (s < 1) s = 1;
+    return s;
+}
+
+/* AttnKernel.cpuDecodeHead (L/model/AttnKernel.cajeta:4216-4285): one query
+ * head's online softmax over positions [t0, t1); 16-lane score partials,
+ * folded pairwise; one exp per key. Writes acc[hd], m, l. */
+static void decode_head(const float *q, const void *kp, const void *vp, int f32, int64_t kvdim,
+                        int64_t koff, int hd, int t0, int t1, float scale, float *part) {
+    float acc[256];
+    for (int d = 0; d < hd; d++) acc[d] = 0.0f;
+    float m = -3.0e38f, l = 0.0f;
+    for (int t = t0; t < t1; t++) {
+        int64_t ko = (int64_t)t * kvdim + koff;
+        float dl[16];
+        for (int j = 0; j < 16; j++) dl[j] = 0.0f;
+        for (int v = 0; v < hd / 16; v++)
+            for (int j = 0; j < 16; j++) {
+                float pr = q[16 * v + j] * kv_at(kp, f32, ko + 16 * v + j);
+                dl[j] = v == 0 ? pr : dl[j] + pr;
+            }
+        float sc = ((((dl[0] + dl[1]) + (dl[2] + dl[3])) + ((dl[4] + dl[5]) + (dl[6] + dl[7])))
+                    + (((dl[8] + dl[9]) + (dl[10] + dl[11])) + ((dl[12] + dl[13]) + (dl[14] + dl[15])))) * scale;
+        if (sc > m) {
+            float c = expf(m - sc);
+            for (int d = 0; d < hd; d++) acc[d] = acc[d] * c;
+            l = l * c;
+            m = sc;
+        }
+        float p = expf(sc - m);
+        l = l + p;
+        for (int d = 0; d < hd; d++) acc[d] = acc[d] + kv_at(vp, f32, ko + d) * p;
+    }
+    for (int d = 0; d < hd; d++) part[d] = acc[d];
+    part[hd] = m;
+    part[hd + 1] = l;
+}
+
+void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, int nkv, int hd,
+               int count, int splits, float scale, int mode, float *out) {
+    int64_t kvdim = (int64_t)nkv * hd;
+    int group = nh / nkv;
+    if (mode == 0) {
+        /* attnDecodeCpuGqaKernel (:4289-4314) + reducePackBlockCpu (:5268-5400):
+         * splits of ceil(count/splits) positions; merge in four interleaved
+         * sub-sums (sp ≡ sub mod 4) added in sub order, then ·(1/Σ w·l). */
+        int stride = hd + 2;
+        float *part = (float *)malloc(sizeof(float) * (size_t)nh * splits * stride);
+        int chunk = (count + splits - 1) / splits;
+#pragma omp parallel for collapse(2) schedule(static)
+        for (int kvh = 0; kvh < nkv; kvh++)
+            for (int sp = 0; sp < splits; sp++) {
+                int t0 = sp * chunk, t1 = t0 + chunk;
+                if (t1 > count) t1 = count;
+                if (t0 > count) t0 = count;
+                for (int h = 0; h < group; h++) {
+                    int hh = kvh * group + h;
+                    decode_head(q + (int64_t)hh * hd, kp, vp, f32, kvdim, (int64_t)kvh * hd, hd, t0, t1,
+                                scale, part + ((int64_t)hh * splits + sp) * stride);
+                }
+            }
+        for (int h = 0; h < nh; h++) {
+            const float *pb0 = part + (int64_t)h * splits * stride;
+            float gm = -3.0e38f;
+            for (int s = 0; s < splits; s++) if (pb0[s * stride + hd] > gm) gm = pb0[s * stride + hd];
+            float tacc[256], gt = 0.0f;
+            for (int sub = 0; sub < 4; sub++) {
+                float a[256], gl = 0.0f;
+                for (int d = 0; d < hd; d++) a[d] = 0.0f;
+                for (int sp = sub; sp < splits; sp += 4) {
+                    const float *pb = pb0 + sp * stride;
+                    float ls = pb[hd + 1];
+                    if (ls > 0.0f) {
+                        float wt = expf(pb[hd] - gm);
+                        gl = gl + wt * ls;
+                        for (int d = 0; d < hd; d++) a[d] = a[d] + pb[d] * wt;
+                    }
+                }
+                if (sub == 0) { for (int d = 0; d < hd; d++) tacc[d] = a[d]; gt = gl; }
+                else { for (int d = 0; d < hd; d++) tacc[d] = tacc[d] + a[d]; gt = gt + gl; }
+            }
+            float rs = 1.0f / gt;
+            for (int d = 0; d < hd; d++) out[(int64_t)h * hd + d] = tacc[d] * rs;
+        }
+        free(part);
+    } else {
+        /* attnScoreKernel (:397-425) + attnCombineKernel (:441-515): scores
+         * q·k·scale, softmax with max and exp sums, then Σ_t p_t·v_t in
+         * ascending t, scaled once by 1/Σp. */
+        float *sc = (float *)malloc(sizeof(float) * (size_t)count);
+        for (int h = 0; h < nh; h++) {
+            int kvh = h / group;
+            const float *qh = q + (int64_t)h * hd;
+            for (int t = 0; t < count; t++) {
+                float s = 0.0f;
+                for (int d = 0; d < hd; d++) s = s + qh[d] * kv_at(kp, f32, (int64_t)t * kvdim + kvh * hd + d);
+                sc[t] = s * scale;
+            }
+            float mx = -3.0e38f;
+            for (int t = 0; t < count; t++) if (sc[t] > mx) mx = sc[t];
+            float sum = 0.0f;
+            for (int t = 0; t < count; t++) { float e = expf(sc[t] - mx); sc[t] = e; sum = sum + e; }
+            float rs = 1.0f / sum;
+            for (int d = 0; d < hd; d++) {
+                float acc = 0.0f;
+                for (int t = 0; t < count; t++)
+                    acc = acc + sc[t] * kv_at(vp, f32, (int64_t)t * kvdim + kvh * hd + d);
+                out[(int64_t)h * hd + d] = acc * rs;
+            }
+        }
+        free(sc);
+    }
+}
+
+/* ------------------------------------------------------------------ model */
+
+typedef struct { int type; const uint8_t *data; int64_t rows, cols; } or_tensor;
+typedef struct {
+    or_tensor attn_norm, q, k, v, o, ffn_norm, gate, up, down;
+    or_tensor router, gate_exps, up_exps, down_exps;
+} or_layer;
+
+struct or_model {
+    or_config c;
+    or_tensor embd, out_norm, head;
+    or_layer *L;
+    void **kc, **vc;             /* per-layer K/V planes [ctx][n_kv*hd] */
+    float *inv;
+    /* scratch */
+    float *hs, *xn, *q, *k, *v, *ao, *y, *g, *u, *logits, *eo, *acc;
+    uint8_t *pk;
+};
+
+or_model *or_model_new(const or_config *cfg) {
+    or_model *m = (or_model *)calloc(1, sizeof(or_model));
+    m->c = *cfg;
+    int nl = cfg->n_layers;
+    m->L = (or_layer *)calloc((size_t)nl, sizeof(or_layer));
+    m->kc = (void **)calloc((size_t)nl, sizeof(void *));
+    m->vc = (void **)calloc((size_t)nl, sizeof(void *));
+    size_t es = cfg->kv_f32 ? 4 : 2;
+    size_t plane = (size_t)cfg->ctx * cfg->n_kv * cfg->head_dim * es;
+    for (int l = 0; l < nl; l++) { m->kc[l] = calloc(1, plane); m->vc[l] = calloc(1, plane); }
+    m->inv = (float *)malloc(sizeof(float) * (size_t)cfg->head_dim / 2);
+    or_inv_freq(cfg->head_dim, cfg->theta, m->inv);
+    int64_t h = cfg->hidden, qd = (int64_t)cfg->n_heads * cfg->head_dim, kvd = (int64_t)cfg->n_kv * cfg->head_dim;
+    int64_t f = cfg->ffn > cfg->expert_ffn ? cfg->ffn : cfg->expert_ffn;
+    int64_t wmax = h > qd ? h : qd; if (f > wmax) wmax = f;
+    m->hs = calloc((size_t)h, 4); m->xn = calloc((size_t)wmax, 4); m->q = calloc((size_t)qd, 4);
+    m->k = calloc((size_t)kvd, 4); m->v = calloc((size_t)kvd, 4); m->ao = calloc((size_t)qd, 4);
+    m->y = calloc((size_t)wmax, 4); m->g = calloc((size_t)f + 256, 4); m->u = calloc((size_t)f + 256, 4);
+    m->logits = calloc((size_t)cfg->vocab, 4); m->eo = calloc((size_t)h, 4); m->acc = calloc((size_t)h, 4);
+    m->pk = calloc((size_t)((wmax + 255) / 256) * 320, 1);
+    return m;
+}
+
+void or_model_free(or_model *m) {
+    if (!m) return;
+    for (int l = 0; l < m->c.n_layers; l++) { free(m->kc[l]); free(m->vc[l]); }
+    free(m->kc); free(m->vc); free(m->L); free(m->inv);
+    free(m->hs); free(m->xn); free(m->q); free(m->k); free(m->v); free(m->ao); free(m->y);
+    free(m->g); free(m->u); free(m->logits); free(m->eo); free(m->acc); free(m->pk);
+    free(m);
+}
+
+void or_model_reset(or_model *m) {
+    size_t es = m->c.kv_f32 ? 4 : 2;
+    size_t plane = (size_t)m->c.ctx * m->c.n_kv * m->c.head_dim * es;
+    for (int l = 0; l < m->c.n_layers; l++) { memset(m->kc[l], 0, plane); memset(m->vc[l], 0, plane); }
+}
+
+int64_t or_model_trace(or_model *m, int what, float *out, int64_t n) {
+    const or_config *c = &m->c;
+    const float *src; int64_t cap;
+    switch (what) {
+    case 0: src = m->hs; cap = c->hidden; break;
+    case 1: src = m->q; cap = (int64_t)c->n_heads * c->head_dim; break;
+    case 2: src = m->ao; cap = (int64_t)c->n_heads * c->head_dim; break;
+    case 3: src = m->g; cap = c->ffn; break;
+    case 4: src = m->logits; cap = c->vocab; break;
+    default: return -1;
+    }
+    if (n > cap) n = cap;
+    memcpy(out, src, sizeof(float) * (size_t)n);
+    return n;
+}
+
+int or_model_bind(or_model *m, const char *name, int type, const void *data, int64_t rows, int64_t cols) {
+    or_tensor t = {type, (const uint8_t *)data, rows, cols};
+    if (!strcmp(name, "token_embd.weight")) { m->embd = t; return 0; }
+    if (!strcmp(name, "output_norm.weight")) { m->out_norm = t; return 0; }
+    if (!strcmp(name, "output.weight")) { m->head = t; return 0; }
+    int l; char rest[96];
+    if (sscanf(name, "blk.%d.%95s", &l, rest) != 2 || l < 0 || l >= m->c.n_layers) return -1;
+    or_layer *L = &m->L[l];
+    if (!strcmp(rest, "attn_norm.weight")) L->attn_norm = t;
+    else if (!strcmp(rest, "attn_q.weight")) L->q = t;
+    else if (!strcmp(rest, "attn_k.weight")) L->k = t;
+    else if (!strcmp(rest, "attn_v.weight")) L->v = t;
+    else if (!strcmp(rest, "attn_output.weight")) L->o = t;
+    else if (!strcmp(rest, "ffn_norm.weight")) L->ffn_norm = t;
+    else if (!strcmp(rest, "ffn_gate.weight")) L->gate = t;
+    else if (!strcmp(rest, "ffn_up.weight")) L->up = t;
+    else if (!strcmp(rest, "ffn_down.weight")) L->down = t;
+    else if (!strcmp(rest, "ffn_gate_inp.weight")) L->router = t;
+    else if (!strcmp(rest, "ffn_gate_exps.weight")) L->gate_exps = t;
+    else if (!strcmp(rest, "ffn_up_exps.weight")) L->up_exps = t;
+    else if (!strcmp(rest, "ffn_down_exps.weight")) L->down_exps = t;
+    else return -1;
+    return 0;
+}
+
+/* Which pack a weight reads on the CPU backend (Linear.act32Here,
+ * L/model/Linear.cajeta:1189-1192): Q8_0 per 32, K-quants per 256. */
+static int act32(int type) { return type == OR_Q8_0; }
+
+/* Stage x (n values) as the activation `type` reads, then y = W·x. */
+static void linear(or_model *m, const or_tensor *w, const float *x, float *y) {
+    int64_t npad = (w->cols + 255) / 256 * 256;
+    if (w->type == OR_Q4_0 || w->type == OR_MXFP4 || w->type == OR_F32) {
+        or_matvec(w->type, w->data, w->rows, w->cols, NULL, x, y);
+        return;
+    }
+    if (act32(w->type)) or_q8k_pack32(x, w->cols, npad, m->pk);
+    else or_q8k_pack(x, w->cols, npad, m->pk);
+    or_matvec(w->type, w->data, w->rows, w->cols, m->pk, NULL, y);
+}
+
+static void embed_row(or_model *m, int token, float *out) {
+    const or_tensor *e = &m->embd;
+    int64_t h = m->c.hidden;
+    int be = or_block_elems(e->type), bb = or_block_bytes(e->type);
+    int64_t row_bytes = h / be * bb;
+    or_dequant(e->type, e->data + (int64_t)token * row_bytes, h / be, out);
+}
+
+/* One MoE FFN row (MoeFfn.forwardRow, L/model/MoeFfn.cajeta:1849-1913):
+ * router logits, route, Σ_k w_k · down(silu(gate x) · up x). Expert tensors
+ * are stacked [E][rows][cols] in one buffer each. */
+static void moe_ffn(or_model *m, or_layer *L, const float *xn, float *out) {
+    int ne = m->c.n_experts, nu = m->c.n_used;
+    int64_t h = m->c.hidden, ef = m->c.expert_ffn;
+    float lg[512]; int32_t sel[64]; float w[64];
+    or_matvec(L->router.type, L->router.data, ne, h, NULL, xn, lg);
+    or_moe_route(lg, ne, nu, m->c.norm_topk, sel, w);
+    for (int64_t j = 0; j < h; j++) m->acc[j] = 0.0f;
+    for (int k = 0; k < nu; k++) {
+        int e = sel[k];
+        int64_t gb = ef * h / or_block_elems(L->gate_exps.type) * or_block_bytes(L->gate_exps.type);
+        int64_t db = h * ef / or_block_elems(L->down_exps.type) * or_block_bytes(L->down_exps.type);
+        or_tensor gt = {L->gate_exps.type, L->gate_exps.data + e * gb, ef, h};
+        or_tensor ut = {L->up_exps.type, L->up_exps.data + e * gb, ef, h};
+        or_tensor dt = {L->down_exps.type, L->down_exps.data + e * db, h, ef};
+        linear(m, &gt, xn, m->g);
+        linear(m, &ut, xn, m->u);
+        or_glu_exp(m->g, m->u, ef, m->g);
+        linear(m, &dt, m->g, m->eo);
+        for (int64_t j = 0; j < h; j++) m->acc[j] = m->acc[j] + w[k] * m->eo[j];
+    }
+    memcpy(out, m->acc, sizeof(float) * (size_t)h);
+}
+
+/* One decode token through every layer and the tail, in the order
+ * CausalLM.residentLayer takes (L/model/CausalLM.cajeta:3625-3935) and the
+ * fused tail (:1614-1661). */
+int or_model_step(or_model *m, int token, int pos, float *logits) {
+    or_config *c = &m->c;
+    int64_t h = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv;
+    int64_t kvd = nkv * hd;
+    float scale = 1.0f / sqrtf((float)hd);
+    embed_row(m, token, m->hs);
+    for (int l = 0; l < c->n_layers; l++) {
+        or_layer *L = &m->L[l];
+        /* attention sublayer */
+        or_rmsnorm(m->hs, (const float *)L->attn_norm.data, h, c->eps, 0, m->xn);
+        linear(m, &L->q, m->xn, m->q);
+        linear(m, &L->k, m->xn, m->k);
+        linear(m, &L->v, m->xn, m->v);
+        or_rope(m->q, (int)nh, (int)hd, pos, m->inv);
+        or_rope(m->k, (int)nkv, (int)hd, pos, m->inv);
+        for (int64_t i = 0; i < kvd; i++) {
+            int64_t at = (int64_t)pos * kvd + i;
+            if (c->kv_f32) { ((float *)m->kc[l])[at] = m->k[i]; ((float *)m->vc[l])[at] = m->v[i]; }
+            else { ((uint16_t *)m->kc[l])[at] = or_f32_to_f16(m->k[i]); ((uint16_t *)m->vc[l])[at] = or_f32_to_f16(m->v[i]); }
+        }
+        int count = pos + 1, from = 0;
+        if (c->swa_window > 0 && (l % 2) == 0 && count > c->swa_window) { from = count - c->swa_window; count = c->swa_window; }
+        size_t es = c->kv_f32 ? 4 : 2;
+        const uint8_t *kb = (const uint8_t *)m->kc[l] + (size_t)from * kvd * es;
+        const uint8_t *vb = (const uint8_t *)m->vc[l] + (size_t)from * kvd * es;
+        int flash = hd == 128 && (nh == 4 * nkv || nh == 8 * nkv);
+        int splits = flash ? or_cpu_decode_splits(count, 1, (int)nkv, c->workers) : 1;
+        or_attend(m->q, kb, vb, c->kv_f32, (int)nh, (int)nkv, (int)hd, count, splits, scale, flash ? 0 : 1, m->ao);
+        linear(m, &L->o, m->ao, m->y);
+        for (int64_t i = 0; i < h; i++) m->hs[i] = m->hs[i] + m->y[i];
+        /* FFN sublayer */
+        or_rmsnorm(m->hs, (const float *)L->ffn_norm.data, h, c->eps, 0, m->xn);
+        if (c->n_experts > 0) {
+            moe_ffn(m, L, m->xn, m->y);
+        } else {
+            int64_t f = c->ffn;
+            linear(m, &L->gate, m->xn, m->g);
+            linear(m, &L->up, m->xn, m->u);
+            /* Prim.gluPackDevice fuses the exp form where the width is whole
+             * 256s; otherwise Prim.gluDevice takes the CPU vector form. */
+            if (f % 256 == 0) or_glu_exp(m->g, m->u, f, m->g);
+            else or_glu_tanh(m->g, m->u, f, m->g);
+            linear(m, &L->down, m->g, m->y);
+        }
+        for (int64_t i = 0; i < h; i++) m->hs[i] = m->hs[i] + m->y[i];
+    }
+    or_rmsnorm(m->hs, (const float *)m->out_norm.data, h, c->eps, 0, m->xn);
+    linear(m, &m->head, m->xn, m->logits);
+    if (logits) memcpy(logits, m->logits, sizeof(float) * (size_t)c->vocab);
+    return or_argmax(m->logits, c->vocab);
+}

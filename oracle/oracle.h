@@ -1,0 +1,99 @@
+/*
+ * oracle.h — CPU restatement of cajeta-llm's CPU-backend decode arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the MI355X
+ * backend: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product path never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it restates (paths relative
+ * to src/main/cajeta/dev/cajeta/llm/ of jklappenbach/cajeta-llm). Pinning:
+ *   - dequant (Q8_0, Q4_0, Q4_K, Q6_K, MXFP4): bit-exact against the
+ *     reference's committed golden pairs (tests/golden/kquant, mxfp4).
+ *   - q8_K / per-32 packs: closed form + round-half-away special cases.
+ *   - int8 GEMVs: brute force (exact integer dot, f64 dense product bound)
+ *     and a planted-error check.
+ *   - rmsnorm, rope, silu, attention, argmax, MoE route: closed forms with
+ *     f64 brute force on small inputs.
+ *   - transcendental ULPs (expf/cosf/sinf/powf of the Cajeta stdlib):
+ *     parity unpinned; this file uses glibc's.
+ *   - end-to-end logits of the real reference binary: parity unpinned (the
+ *     cajeta toolchain is absent); end-to-end is the restatement.
+ */
+#ifndef CJ_ORACLE_H
+#define CJ_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (GgufFile / Quant.GG_*) */
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14, OR_MXFP4 = 39 };
+
+int   or_block_bytes(int type);
+int   or_block_elems(int type);
+float or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);
+
+/* block decode of `nblocks` blocks (Quant.dequantize, io/Quant.cajeta:693-734) */
+int or_dequant(int type, const uint8_t *raw, int64_t nblocks, float *out);
+
+/* activation packs: 320-byte blocks (io/Quant.cajeta:3232-3321) */
+void or_q8k_pack(const float *x, int64_t n, int64_t npad, uint8_t *out);
+void or_q8k_pack32(const float *x, int64_t n, int64_t npad, uint8_t *out);
+
+/* one weight × one activation. Q4_K/Q6_K read a per-256 pack, Q8_0 a
+ * per-32 pack (xp); Q4_0 and MXFP4 read f32 activations (xf). */
+int or_matvec(int type, const uint8_t *w, int64_t rows, int64_t cols,
+              const uint8_t *xp, const float *xf, float *y);
+
+/* primitives */
+void  or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out);
+void  or_glu_exp(const float *g, const float *u, int64_t n, float *out);
+void  or_glu_tanh(const float *g, const float *u, int64_t n, float *out);
+void  or_inv_freq(int hd, float theta, float *inv);
+void  or_rope(float *t, int nheads, int hd, int pos, const float *inv);
+int   or_argmax(const float *v, int64_t n);
+int   or_moe_route(const float *logits, int n_experts, int n_used, int norm_topk,
+                   int32_t *sel, float *w);
+void  or_unpermute_rows(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t row_bytes, int n_head);
+
+/* decode attention over an fp16 (or f32) KV plane for ONE layer.
+ * k/v planes are position-major: [ctx][n_kv*hd]. `count` positions from 0.
+ * mode 0: split-K online softmax (AttnKernel.cpuDecodeHead + reduce),
+ * mode 1: two-pass score/softmax/combine (attnScoreKernel + attnCombineKernel). */
+void or_attend(const float *q, const void *kplane, const void *vplane, int kv_f32,
+               int n_h, int n_kv, int hd, int count, int splits, float scale,
+               int mode, float *out);
+int  or_cpu_decode_splits(int count, int rows, int n_kv, int workers);
+
+/* ---- whole-model decode (CausalLM.residentLayer order) ---- */
+typedef struct or_model or_model;
+
+typedef struct {
+    int32_t n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab, ctx;
+    float   eps, theta;
+    int32_t kv_f32;        /* 1: f32 KV (config-literal), 0: fp16 (resident path) */
+    int32_t workers;       /* CPU worker count the attention split choice uses */
+    int32_t n_experts, n_used, norm_topk, expert_ffn;
+    int32_t swa_window;    /* >0: layers with (layer % 2 == 0) attend the last swa_window positions */
+} or_config;
+
+or_model *or_model_new(const or_config *cfg);
+void      or_model_free(or_model *m);
+/* Bind a tensor by its GGUF name; the data stays owned by the caller. */
+int       or_model_bind(or_model *m, const char *name, int type, const void *data,
+                        int64_t rows, int64_t cols);
+/* One decode step: token at position pos. Writes logits (vocab) if non-null
+ * and returns the greedy argmax. */
+int       or_model_step(or_model *m, int token, int pos, float *logits);
+void      or_model_reset(or_model *m);
+/* The last step's buffers as the last layer left them: 0 hs, 1 rotated q,
+ * 2 attention output, 3 SiLU·up activation, 4 logits. Returns the length. */
+int64_t   or_model_trace(or_model *m, int what, float *out, int64_t n);
+int       or_model_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,325 @@
+"""Kernel-level parity: each launch-seam entry point of the C-ABI on the
+MI355X against the CPU oracle on the same seeded inputs. Integer/byte work
+(dequant, packs, argmax, fp16 appends, routing ids) is bit-exact; float
+reductions are held to the tolerance written in each test."""
+import struct
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def rand_blocks(O, ty, nblocks, rng):
+    """Valid random blocks of a format: random bytes with sane scales."""
+    be, bb = O.BLOCK[ty]
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    def f16(vals):
+        return np.asarray(vals, np.float16).view(np.uint8).reshape(-1, 2)
+    if ty == O.Q8_0 or ty == O.Q4_0:
+        raw[:, 0:2] = f16(rng.uniform(0.001, 0.01, nblocks))
+    elif ty == O.Q4_K:
+        raw[:, 0:2] = f16(rng.uniform(0.0005, 0.002, nblocks))
+        raw[:, 2:4] = f16(rng.uniform(0.0005, 0.002, nblocks))
+    elif ty == O.Q6_K:
+        raw[:, 208:210] = f16(rng.uniform(0.0001, 0.001, nblocks))
+    elif ty == O.MXFP4:
+        raw[:, 0] = rng.integers(118, 126, nblocks)
+    return raw.reshape(-1)
+
+
+def golden(name):
+    import os
+    here = os.path.join(os.path.dirname(__file__), "golden", "kquant")
+    return np.fromfile(os.path.join(here, name + ".bin"), np.uint8), np.fromfile(os.path.join(here, name + ".f32"), np.float32)
+
+
+FORMATS = [("q8_0", 8), ("q4_0", 2), ("q4_k", 12), ("q6_k", 14), ("mxfp4", 39)]
+
+
+@pytest.mark.parametrize("name,ty", [f for f in FORMATS if f[0] != "mxfp4"])
+def test_dequant_file_layout_matches_golden(gpu, O, name, ty):
+    say("dequant golden", name)
+    raw, ref = golden(name)
+    be, bb = O.BLOCK[ty]
+    rows, cols = 1, ref.size
+    src, out = gpu.Buffer.of(raw), gpu.Buffer(ref.size * 4)
+    gpu.native.check(gpu.native.lib().cj_dequant(out.h, src.h, ty, rows, cols, 0), "dequant")
+    got = out.download(np.float32, ref.size)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_mxfp4_matches_golden(gpu, O):
+    import os
+    b = open(os.path.join(os.path.dirname(__file__), "golden", "mxfp4", "mxfp4_ref.bin"), "rb").read()
+    _, nb = struct.unpack("<ii", b[:8])
+    raw = np.frombuffer(b[8:8 + nb * 17], np.uint8)
+    ref = np.frombuffer(b[8 + nb * 17:], np.float32)
+    src, out = gpu.Buffer.of(raw), gpu.Buffer(ref.size * 4)
+    gpu.native.check(gpu.native.lib().cj_dequant(out.h, src.h, 39, 1, ref.size, 0), "dequant")
+    assert np.array_equal(out.download(np.float32, ref.size).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("name,ty", FORMATS)
+def test_prepared_layout_dequant_is_bit_exact(gpu, O, name, ty):
+    say("prepared dequant", name)
+    rng = np.random.default_rng(ty)
+    rows, cols = 37, 2048
+    be, bb = O.BLOCK[ty]
+    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    ref = O.dequant(ty, raw)
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(ty, cols)
+    src, dst, out = gpu.Buffer.of(raw), gpu.Buffer(prb * rows), gpu.Buffer(rows * cols * 4)
+    gpu.native.check(lib.cj_prepare_weight(dst.h, src.h, ty, rows, cols), "prepare")
+    gpu.native.check(lib.cj_dequant(out.h, dst.h, ty, rows, cols, 1), "dequant prepared")
+    assert np.array_equal(out.download(np.float32, rows * cols).view(np.uint32), ref.view(np.uint32))
+    gpu.native.check(lib.cj_dequant(out.h, src.h, ty, rows, cols, 0), "dequant file")
+    assert np.array_equal(out.download(np.float32, rows * cols).view(np.uint32), ref.view(np.uint32))
+
+
+def tie_vector(rng, n):
+    """Values with exact .5 ties after the pack's scaling (amax 127 per block)."""
+    x = (rng.integers(-126, 126, n) + 0.5).astype(np.float32)
+    x[::256] = 127.0
+    return x
+
+
+@pytest.mark.parametrize("per32", [0, 1])
+@pytest.mark.parametrize("n", [256, 1408, 4096, 14336])
+def test_pack_is_bit_exact(gpu, O, per32, n):
+    say("pack", n, per32)
+    rng = np.random.default_rng(n + per32)
+    npad = (n + 255) // 256 * 256
+    for x in (rng.standard_normal(n).astype(np.float32), tie_vector(rng, n), np.zeros(n, np.float32)):
+        xb, ob = gpu.Buffer.of(x), gpu.Buffer(npad // 256 * 320)
+        gpu.native.check(gpu.native.lib().cj_q8k_pack(ob.h, xb.h, 1, n, npad, per32), "pack")
+        got = ob.download(np.uint8, npad // 256 * 320)
+        ref = O.q8k_pack(x, per32=bool(per32), npad=npad)
+        assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dim", [512, 4096, 2880])
+@pytest.mark.parametrize("per32", [0, 1])
+def test_rmsnorm_pack(gpu, O, dim, per32):
+    say("rmsnorm_pack", dim, per32)
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal(dim) * 3).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    npad = (dim + 255) // 256 * 256
+    xb, wb, ob, pb = gpu.Buffer.of(x), gpu.Buffer.of(w), gpu.Buffer(dim * 4), gpu.Buffer(npad // 256 * 320)
+    gpu.native.check(gpu.native.lib().cj_rmsnorm_pack(ob.h, pb.h, xb.h, wb.h, dim, 1e-5, 0, per32), "rmsnorm_pack")
+    got = ob.download(np.float32, dim)
+    ref = O.rmsnorm(x, w, 1e-5)
+    if dim % 256 == 0:
+        # the CPU row form's 256-lane tree: the same adds, so the same bits
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(pb.download(np.uint8, npad // 256 * 320), O.q8k_pack(ref, per32=bool(per32), npad=npad))
+    else:
+        # a width with a remainder: the host floor sums sequentially (|rel| < 1e-6)
+        assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+def matvec_case(gpu, O, ty, rows, cols, seed, accum=False):
+    rng = np.random.default_rng(seed)
+    be, bb = O.BLOCK[ty]
+    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(ty, cols)
+    src, w = gpu.Buffer.of(raw), gpu.Buffer(prb * rows)
+    gpu.native.check(lib.cj_prepare_weight(w.h, src.h, ty, rows, cols), "prepare")
+    if ty in (O.Q4_0, O.MXFP4):
+        act = gpu.Buffer.of(x)
+        ref = O.matvec(ty, raw, rows, cols, x)
+    else:
+        xp = O.q8k_pack(x, per32=(ty == O.Q8_0))
+        act = gpu.Buffer.of(xp)
+        ref = O.matvec_packed(ty, raw, rows, cols, xp)
+    y0 = rng.standard_normal(rows).astype(np.float32) if accum else np.zeros(rows, np.float32)
+    y = gpu.Buffer.of(y0)
+    gpu.native.check(lib.cj_matvec(ty, y.h, w.h, act.h, rows, cols, 0, int(accum)), "matvec")
+    got = y.download(np.float32, rows)
+    if accum:
+        ref = (y0 + ref).astype(np.float32)
+    return got, ref, raw, x
+
+
+@pytest.mark.parametrize("name,ty", FORMATS)
+@pytest.mark.parametrize("rows,cols", [(300, 512), (1024, 4096), (96, 14336)])
+def test_matvec_matches_oracle(gpu, O, name, ty, rows, cols):
+    say("matvec", name, rows, cols)
+    got, ref, raw, x = matvec_case(gpu, O, ty, rows, cols, rows + cols + ty)
+    # integer sub-block dots are exact; only the f32 sum over blocks is
+    # re-associated (tree across lanes vs the oracle's block order)
+    scale = np.abs(ref).max() + 1e-6
+    err = np.abs(got - ref).max() / scale
+    assert err < 2e-6, "%s %dx%d: rel err %.3g" % (name, rows, cols, err)
+
+
+@pytest.mark.parametrize("name,ty", [("q4_k", 12), ("q8_0", 8)])
+def test_matvec_accumulate_store(gpu, O, name, ty):
+    got, ref, _, _ = matvec_case(gpu, O, ty, 512, 4096, 7, accum=True)
+    assert np.abs(got - ref).max() < 2e-6 * (np.abs(ref).max() + 1)
+
+
+def test_matvec_refuses_short_buffers(gpu, O):
+    lib = gpu.native.lib()
+    w, act, y = gpu.Buffer(1024), gpu.Buffer(320), gpu.Buffer(16)
+    rc = lib.cj_matvec(12, y.h, w.h, act.h, 64, 256, 0, 0)
+    assert rc == -1 and "weight" in gpu.native.last_error()
+
+
+@pytest.mark.parametrize("form", [0, 1])
+@pytest.mark.parametrize("n,per32", [(14336, 0), (1408, 1), (512, 0)])
+def test_glu_pack(gpu, O, form, n, per32):
+    say("glu", n, form, per32)
+    rng = np.random.default_rng(n + form)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    npad = (n + 255) // 256 * 256
+    gb, ub, ob, pb = gpu.Buffer.of(g), gpu.Buffer.of(u), gpu.Buffer(n * 4), gpu.Buffer(npad // 256 * 320)
+    gpu.native.check(gpu.native.lib().cj_glu(ob.h, pb.h, gb.h, ub.h, n, form, per32), "glu")
+    got = ob.download(np.float32, n)
+    ref = O.glu(g, u, "tanh" if form else "exp")
+    if form:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))   # fmaf/div are exact both sides
+    else:
+        assert np.allclose(got, ref, rtol=2e-6, atol=1e-7)                  # device exp vs glibc exp
+    # the pack of the device's own values is the oracle's pack of them, bit for bit
+    assert np.array_equal(pb.download(np.uint8, npad // 256 * 320), O.q8k_pack(got, per32=bool(per32), npad=npad))
+
+
+@pytest.mark.parametrize("n", [5, 1024, 128256, 201088])
+def test_argmax_first_occurrence(gpu, O, n):
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n).astype(np.float32)
+    v[n // 3] = 9.0
+    v[(2 * n) // 3] = 9.0          # a tie later: the smaller index wins
+    vb, tb = gpu.Buffer.of(v), gpu.Buffer(16)
+    gpu.native.check(gpu.native.lib().cj_argmax_row(tb.h, 1, vb.h, n), "argmax")
+    assert int(tb.download(np.int32, 4)[1]) == O.argmax(v) == n // 3
+
+
+def to_paged(plane, n_kv, hd, pages):
+    """position-major [ctx][n_kv·hd] fp16 -> page-blocked head-major planes"""
+    ctx = plane.shape[0]
+    out = np.zeros((pages, n_kv, 64, hd), np.uint16)
+    for p in range(ctx):
+        out[p // 64, :, p % 64, :] = plane[p].reshape(n_kv, hd)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (128, 4, 1), (128, 8, 1), (64, 8, 2), (64, 64, 8), (128, 8, 8)])
+@pytest.mark.parametrize("count,splits", [(1, 4), (37, 4), (300, 32), (2049, 32)])
+def test_attend_matches_oracle(gpu, O, hd, n_q, n_kv, count, splits):
+    say("attend", hd, n_q, n_kv, count, splits)
+    rng = np.random.default_rng(count * 7 + hd + n_q)
+    pages = (count + 63) // 64 + 1
+    ctx = pages * 64
+    kf = (rng.standard_normal((ctx, n_kv * hd))).astype(np.float32)
+    vf = (rng.standard_normal((ctx, n_kv * hd))).astype(np.float32)
+    k16, v16 = kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(n_q * hd).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(hd))
+    # a shuffled page table
+    tab = rng.permutation(pages).astype(np.int32)
+    phys = np.zeros((pages * 64, n_kv * hd), np.uint16)
+    kp = np.zeros_like(phys); vp = np.zeros_like(phys)
+    for p in range(ctx):
+        row = tab[p // 64] * 64 + p % 64
+        kp[row] = k16[p]; vp[row] = v16[p]
+    kb, vb = gpu.Buffer.of(to_paged(kp, n_kv, hd, pages)), gpu.Buffer.of(to_paged(vp, n_kv, hd, pages))
+    qb, tb = gpu.Buffer.of(q), gpu.Buffer.of(tab)
+    part, out, cnt = gpu.Buffer(n_q * splits * (hd + 2) * 4), gpu.Buffer(n_q * hd * 4), gpu.Buffer(4 * n_kv)
+    cnt.zero()
+    frm = 0
+    lib = gpu.native.lib()
+    gpu.native.check(lib.cj_attend(part.h, out.h, qb.h, kb.h, vb.h, tb.h, 0, cnt.h, n_q, n_kv, hd, count, frm,
+                                   splits, float(scale)), "attend")
+    got = out.download(np.float32, n_q * hd)
+    mode = 0 if (hd == 128 and n_q in (4 * n_kv, 8 * n_kv)) else 1
+    spl = O.cpu_decode_splits(count, 1, n_kv, 16) if mode == 0 else 1
+    ref = O.attend(q, k16[:count], v16[:count], n_q, n_kv, hd, count, spl, float(scale), mode)
+    assert np.allclose(got, ref, rtol=1e-4, atol=2e-5), np.abs(got - ref).max()
+    # the merge kernel over the same partials gives the same output
+    out2 = gpu.Buffer(n_q * hd * 4)
+    gpu.native.check(lib.cj_attn_merge(out2.h, 0, part.h, n_q, hd, splits, 0), "merge")
+    assert np.allclose(out2.download(np.float32, n_q * hd), got, rtol=1e-6, atol=1e-7)
+    assert np.array_equal(cnt.download(np.int32, n_kv), np.zeros(n_kv, np.int32))
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv,theta", [(128, 32, 8, 500000.0), (64, 8, 2, 10000.0)])
+def test_qk_prep_rope_and_append(gpu, O, hd, n_q, n_kv, theta):
+    rng = np.random.default_rng(hd)
+    ctx = 256
+    pos = 131
+    q = rng.standard_normal(n_q * hd).astype(np.float32)
+    k = rng.standard_normal(n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(n_kv * hd).astype(np.float32)
+    pages = ctx // 64
+    lib = gpu.native.lib()
+    qb, kb, vb = gpu.Buffer.of(q), gpu.Buffer.of(k), gpu.Buffer.of(v)
+    kc, vc = gpu.Buffer(pages * n_kv * 64 * hd * 2), gpu.Buffer(pages * n_kv * 64 * hd * 2)
+    kc.zero(); vc.zero()
+    rope = gpu.Buffer(ctx * hd * 4)
+    gpu.native.check(lib.cj_rope_table(rope.h, hd, theta, ctx), "rope_table")
+    tab = gpu.Buffer.of(np.arange(pages, dtype=np.int32))
+    gpu.native.check(lib.cj_qk_prep(qb.h, kb.h, vb.h, kc.h, vc.h, 0, 0, rope.h, tab.h, 0, n_q, n_kv, hd, 0, 1e-5, 0, pos),
+                     "qk_prep")
+    inv = O.inv_freq(hd, theta)
+    qr, kr = O.rope(q, n_q, hd, pos, inv), O.rope(k, n_kv, hd, pos, inv)
+    assert np.array_equal(qb.download(np.float32, q.size).view(np.uint32), qr.view(np.uint32))
+    kcache = kc.download(np.uint16, pages * n_kv * 64 * hd).reshape(pages, n_kv, 64, hd)
+    vcache = vc.download(np.uint16, pages * n_kv * 64 * hd).reshape(pages, n_kv, 64, hd)
+    assert np.array_equal(kcache[pos // 64, :, pos % 64, :].reshape(-1), O.f32_to_f16_bits(kr))
+    assert np.array_equal(vcache[pos // 64, :, pos % 64, :].reshape(-1), O.f32_to_f16_bits(v))
+
+
+@pytest.mark.parametrize("ne,k", [(32, 4), (128, 8), (8, 2)])
+def test_moe_route(gpu, O, ne, k):
+    rng = np.random.default_rng(ne)
+    rows = 5
+    lg = rng.standard_normal((rows, ne)).astype(np.float32)
+    lg[2, 3] = lg[2, 5] = 7.0                     # tie: the lower index first
+    lb, sb, wb = gpu.Buffer.of(lg), gpu.Buffer(rows * k * 4), gpu.Buffer(rows * k * 4)
+    gpu.native.check(gpu.native.lib().cj_moe_route(sb.h, wb.h, lb.h, rows, ne, k, 1), "route")
+    sel = sb.download(np.int32, rows * k).reshape(rows, k)
+    w = wb.download(np.float32, rows * k).reshape(rows, k)
+    for r in range(rows):
+        rs, rw = O.moe_route(lg[r], k, True)
+        assert np.array_equal(sel[r], rs)
+        assert np.allclose(w[r], rw, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("ty", [0, 8, 12, 14])
+def test_embed_row(gpu, O, ty):
+    rng = np.random.default_rng(ty)
+    hidden, vocab = 512, 40
+    be, bb = O.BLOCK[ty]
+    if ty == 0:
+        raw = rng.standard_normal(vocab * hidden).astype(np.float32).view(np.uint8)
+    else:
+        raw = rand_blocks(O, ty, vocab * hidden // be, rng)
+    tb, ob = gpu.Buffer.of(raw), gpu.Buffer(hidden * 4)
+    gpu.native.check(gpu.native.lib().cj_embed_row(ob.h, tb.h, ty, hidden, 33), "embed")
+    rb = hidden // be * bb
+    ref = O.dequant(ty, raw[33 * rb:34 * rb])
+    assert np.array_equal(ob.download(np.float32, hidden).view(np.uint32), ref.view(np.uint32))
+
+
+def test_kernel_registry_answers_reference_names(gpu):
+    for name in ("q4kQ8WaveMatVecKernel", "q6kQ8WaveMatVecKernel", "q80Q8WaveMatVecKernel", "q8kPackKernel",
+                 "rmsnormPackRowF32", "gluPackF32", "qkPrepKernel", "attnFlashDecodeGqa4Kernel",
+                 "attnFlashDecodeGqa8Kernel", "attnReducePackQ8Kernel", "argmaxRowKernel", "embedRowQ4kKernel",
+                 "routerTopKKernel", "mxfp4MatVecKernel"):
+        assert gpu.KernelCap.usable(name), name
+    assert not gpu.KernelCap.usable("iq2xxsQ8WaveMatVecKernel")
+    gpu.KernelCap.setOverride("q4kQ8WaveMatVecKernel", False)
+    assert not gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
+    gpu.KernelCap.clearOverrides()
+    assert gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")

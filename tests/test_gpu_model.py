@@ -1,0 +1,160 @@
+"""Model-level parity: the graph-captured decode step on the MI355X against
+the CPU oracle's restatement of the reference CPU backend, on the same GGUF
+bytes. Bars: greedy token ids identical; logits within
+max-abs 1e-3 (f32 accumulation). A non-degeneracy control requires more than
+one distinct generated token (T/BackendParityTest.cajeta:158-178)."""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "gguf")
+LOGIT_TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1):
+    """Greedy-decode `prompt` + n_gen on both sides; compare every step."""
+    from oracle.gguf_reader import GgufReader, oracle_model
+    r = GgufReader(image if image is not None else path)
+    om, cfg = oracle_model(r, ctx=ctx)
+    opts = pkg.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = 1
+    eng = pkg.LlmEngine.load(opts)
+    try:
+        eng.reset()
+        eng.prefill(prompt)
+        gpu_first = int(eng.preds(len(prompt))[-1])
+        gpu_logits = [eng.logits()]
+        gpu_toks = [gpu_first]
+        for i in range(n_gen - 1):
+            gpu_toks.append(int(eng.decode(1)[0]))
+            if (i + 1) % check_every == 0:
+                gpu_logits.append(eng.logits())
+            else:
+                gpu_logits.append(None)
+        toks = list(prompt)
+        ref_toks, ref_logits = [], []
+        for p in range(len(prompt) + n_gen - 1):
+            t, lg = om.step(toks[p], p)
+            if p >= len(prompt) - 1:
+                ref_toks.append(t)
+                ref_logits.append(lg)
+                toks.append(t)
+        worst = 0.0
+        for g, o in zip(gpu_logits, ref_logits):
+            if g is not None:
+                worst = max(worst, float(np.max(np.abs(g - o))))
+        return gpu_toks, ref_toks, worst
+    finally:
+        eng.close()
+        om.close()
+
+
+@pytest.mark.parametrize("name", ["toy-routable.gguf", "toy-routable-gqa8.gguf"])
+def test_reference_toy_fixture_greedy_parity(gpu, name):
+    say("model", name)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, 256, 12).tolist()
+    g, o, err = run_pair(gpu, os.path.join(GOLD, name), None, prompt, 40, 256)
+    assert g == o, "tokens differ: gpu %s oracle %s" % (g, o)
+    assert err <= LOGIT_TOL, err
+    assert len(set(g)) > 1
+
+
+def synth(pkg, spec, name, seed):
+    pkg.synth_gguf(spec, "mem:" + name, seed)
+    return "mem:" + name, pkg.image_bytes(name)
+
+
+def test_c1_tiny_q8_0_greedy_parity(gpu):
+    """4 layers, d 512, 8/2 heads of 64, FFN 1408, V 32000,
+    Q8_0, f32 embeddings; 16-token prompt, 64 greedy tokens."""
+    say("model c1")
+    path, img = synth(gpu, "c1", "t_c1", 1234)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, 32000, 16).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 64, 128)
+    gpu.image_free("t_c1")
+    assert g == o, "tokens differ at %d" % next(i for i, (a, b) in enumerate(zip(g, o)) if a != b)
+    assert err <= LOGIT_TOL, err
+    assert len(set(g)) > 1
+
+
+def test_c3_shape_two_layers_greedy_parity(gpu):
+    """BASELINE config 3's Llama-3-8B shapes (d 4096, 32/8 heads of 128, FFN
+    14336, V 128256, Q4_K + Q6_K head, θ 500000) at two layers."""
+    say("model c3x2")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=128256;eps=1e-5;theta=500000;" \
+           "wtype=q4_k;head=q6_k;embd=q4_k;ctx=512"
+    path, img = synth(gpu, spec, "t_c3x2", 77)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, 128256, 24).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 12, 256, check_every=3)
+    gpu.image_free("t_c3x2")
+    assert g == o
+    assert err <= LOGIT_TOL, err
+
+
+def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
+    """BASELINE config 4's Q8_0 weights on the 8B shapes, at two layers."""
+    say("model c4x2")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=32000;eps=1e-5;theta=500000;" \
+           "wtype=q8_0;head=q8_0;embd=q8_0;ctx=512"
+    path, img = synth(gpu, spec, "t_c4x2", 78)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 32000, 20).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 10, 256, check_every=3)
+    gpu.image_free("t_c4x2")
+    assert g == o
+    assert err <= LOGIT_TOL, err
+
+
+def test_c5_moe_shape_two_layers_greedy_parity(gpu):
+    """BASELINE config 5's gpt-oss-20b shapes (d 2880, 64/8 heads of 64, 32
+    MXFP4 experts top-4 of FFN 2880, alternating 128-window attention) at two
+    layers and a 32000 vocabulary."""
+    say("model c5x2")
+    spec = "layers=2;hidden=2880;heads=64;kv=8;hd=64;ffn=2880;vocab=32000;eps=1e-5;theta=150000;wtype=q8_0;" \
+           "head=q8_0;embd=q8_0;experts=32;used=4;expert_ffn=2880;expert_type=mxfp4;swa=128;ctx=512"
+    path, img = synth(gpu, spec, "t_c5x2", 79)
+    rng = np.random.default_rng(6)
+    prompt = rng.integers(0, 32000, 140).tolist()          # past the 128 window
+    g, o, err = run_pair(gpu, path, img, prompt, 10, 256, check_every=3)
+    gpu.image_free("t_c5x2")
+    assert g == o
+    assert err <= LOGIT_TOL, err
+
+
+def test_engine_request_surface(gpu):
+    """submitTokens / runAll / request / cancel and an end-of-generation stop."""
+    path = os.path.join(GOLD, "toy-routable.gguf")
+    eng = gpu.LlmEngine.load(gpu.EngineOptions(path))
+    try:
+        a = eng.submitTokens([1, 2, 3, 4], maxNew=10)
+        b = eng.submitTokens([5, 6, 7], maxNew=6)
+        c = eng.submitTokens([9, 9], maxNew=4)
+        assert eng.cancel(c)
+        eng.runAll(0)
+        ra, rb, rc = eng.request(a), eng.request(b), eng.request(c)
+        assert ra.done and len(ra.tokens) == 10 and ra.finishReason == 0
+        assert rb.done and len(rb.tokens) == 6
+        assert rc.finishReason == 2 and rc.tokens == []
+        # stop at the first generated id when it is declared end-of-generation
+        stop = ra.tokens[2]
+        eng.setEog([stop])
+        d = eng.submitTokens([1, 2, 3, 4], maxNew=10)
+        eng.runAll(0)
+        rd = eng.request(d)
+        first = ra.tokens.index(stop)
+        assert rd.finishReason == 1 and rd.tokens == ra.tokens[:first + 1]
+        with pytest.raises(gpu.LlmException):
+            eng.submitTokens([1, 2], maxNew=2, params=gpu.SampleParams(temperature=0.7))
+    finally:
+        eng.close()
