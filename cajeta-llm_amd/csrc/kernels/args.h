@@ -120,16 +120,19 @@ typedef struct {
 } cj_qkprep_args;
 
 typedef struct {
-    float *part;             // [n_q][splits][hd + 2] partials
+    float *part;             // split-K: [n_q][64][hd + 2] partials; two-pass: scores [n_q][splits]
     float *out;              // merged f32 output (null: partials only)
     const float *q;
     const uint16_t *kc, *vc;
     const int32_t *pgtab;
     const cj_step_state *state;
     int32_t *counters;       // per kv head arrival counters (merge in the last)
-    int32_t n_q, n_kv, head_dim, splits, pg_base;
+    int32_t n_q, n_kv, head_dim;
+    int32_t splits;          // two-pass: the scores row stride (≥ count)
+    int32_t pg_base;
     int32_t count, from;     // host values when state is null
     int32_t window;          // >0: attend the last `window` positions only
+    int32_t workers;         // split-K: the CPU worker count the split rule uses
     float scale;
 } cj_attn_args;
 

@@ -4,225 +4,274 @@
 // page, so one kv head's 64 positions are one contiguous 64·hd·2-byte run:
 //   element (pos, kvh, d) at ((pgtab[base + pos/64]·n_kv + kvh)·64 + pos%64)·hd + d
 //
-// cj_attn_decode: split-K over the context. One workgroup of 4 waves per
-// (kv head, split); hd/16 lanes share a position (16 dims, two 128-bit loads
-// of K and of V each), 64/(hd/16) positions per step, every lane an
-// independent online softmax for its positions and all the group's query
-// heads. Lanes fold per wave, the 4 waves fold through LDS into one partial
-// (acc, m, l) per query head; the last split of a kv head to finish merges
-// every split (the reference's reduce) into f32.
+// Two forms, chosen by shape as the reference chooses (hd 128 with 4 or 8
+// query heads per kv head takes the flash split-K; anything else the
+// two-pass score/combine), each computing exactly the reference CPU
+// backend's operation order:
+//
+// cj_attn_split_*: split-K (AttnKernel.attnDecodeCpuGqaKernel +
+//   cpuDecodeHead, model/AttnKernel.cajeta:4216-4314). Splits per
+//   cpuDecodeSplits (:4879-4889) for a given worker count; one workgroup per
+//   (kv head, split slot), 16 lanes per query head; a split's positions run
+//   in order through an online softmax whose scores are 16-lane partials
+//   folded pairwise. K/V for a tile of positions is staged in LDS in a
+//   lane-major layout. The last workgroup of a kv head merges the splits as
+//   reducePackBlockCpu does (:5268-5400): four interleaved sub-sums.
+// cj_attn_scores_* + cj_attn_combine_*: attnScoreKernel (:397-425) and
+//   attnCombineKernel (:441-515): 32-lane strided dot + butterfly, then 128
+//   lanes for max, exp and sum (stride-halving tree) and the ascending-t sum
+//   of p·v per output dimension.
 #include "common.h"
+
+#define ATTN_MAX_SPLITS 64
+#define ATTN_TILE 32
 
 DEV int64_t kv_at(const int32_t *pgtab, int pg_base, int pos, int nkv, int kvh, int hd) {
     const int page = pgtab[pg_base + (pos >> 6)];
     return (((int64_t)page * nkv + kvh) * 64 + (pos & 63)) * hd;
 }
 
-DEV void h8_to_f(const uint4 v, float *f) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) { f[2 * i] = h2f(w[i]); f[2 * i + 1] = h2f(w[i] >> 16); }
+// AttnKernel.cpuDecodeSplits: two work items a worker over the kv heads,
+// within [1, min(64, count)].
+DEV int decode_splits(int count, int nkv, int workers) {
+    const int w = workers < 1 ? 1 : workers, rk = nkv < 1 ? 1 : nkv;
+    int s = (2 * w + rk - 1) / rk;
+    if (s > 64) s = 64;
+    if (s > count) s = count;
+    if (s < 1) s = 1;
+    return s;
+}
+
+DEV void attn_window(const cj_attn_args &a, int &count, int &from) {
+    if (a.state) { count = a.state->pos + 1; from = 0; } else { count = a.count; from = a.from; }
+    if (a.window > 0 && count > a.window) { from += count - a.window; count = a.window; }
 }
 
 template <int HD, int G>
-DEV void attn_body(const cj_attn_args &a) {
-    constexpr int LP = HD / 16;       // lanes per position
-    constexpr int P = 64 / LP;        // positions per wave step
-    constexpr int U = 2;              // steps in flight
-    constexpr int PIECE = P * U;      // positions a wave takes at a time
-    __shared__ float wm[4][G], wl[4][G];
-    __shared__ float wacc[4][G][HD];
+DEV void split_body(const cj_attn_args &a) {
+    constexpr int VPL = HD / 16;                     // dims per lane: l, l+16, ...
+    __shared__ uint16_t ks[ATTN_TILE][16][VPL], vs[ATTN_TILE][16][VPL];
     __shared__ int ticket;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int kvh = blockIdx.x / a.splits, sp = blockIdx.x % a.splits;
-    const int p = lane / LP, j = lane % LP;
+    const int tid = threadIdx.x, nthr = G * 16;
+    const int h = tid >> 4, l = tid & 15;
+    const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
     int count, from;
-    if (a.state) { count = a.state->pos + 1; from = 0; } else { count = a.count; from = a.from; }
-    if (a.window > 0 && count > a.window) { from += count - a.window; count = a.window; }
-    int chunk = (count + a.splits - 1) / a.splits;
-    chunk = (chunk + PIECE - 1) / PIECE * PIECE;
-    const int t0 = sp * chunk;
-    const int t1 = t0 + chunk < count ? t0 + chunk : count;
-
-    float qv[G][16];
+    attn_window(a, count, from);
+    const int splits = decode_splits(count, a.n_kv, a.workers);
+    const int qh = kvh * G + h;
+    if (sp < splits) {
+        const int chunk = (count + splits - 1) / splits;
+        int t0 = sp * chunk, t1 = t0 + chunk;
+        if (t1 > count) t1 = count;
+        if (t0 > count) t0 = count;
+        float q[VPL], acc[VPL];
 #pragma unroll
-    for (int h = 0; h < G; h++)
-#pragma unroll
-        for (int d = 0; d < 16; d++) qv[h][d] = a.q[(int64_t)(kvh * G + h) * HD + 16 * j + d];
-    float m[G], l[G], acc[G][16];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m[h] = -3.0e38f; l[h] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 16; d++) acc[h][d] = 0.0f;
-    }
-
-    for (int tb = t0 + wave * PIECE; tb < t1; tb += 4 * PIECE) {
-        uint4 kr[U][2], vr[U][2];
-        bool ok[U];
-#pragma unroll
-        for (int uu = 0; uu < U; uu++) {
-            const int t = tb + uu * P + p;
-            ok[uu] = t < t1;
-            const int tt = from + (ok[uu] ? t : t0);
-            const int64_t base = kv_at(a.pgtab, a.pg_base, tt, a.n_kv, kvh, HD) + 16 * j;
-            kr[uu][0] = *(const uint4 *)(a.kc + base);
-            kr[uu][1] = *(const uint4 *)(a.kc + base + 8);
-            vr[uu][0] = *(const uint4 *)(a.vc + base);
-            vr[uu][1] = *(const uint4 *)(a.vc + base + 8);
-        }
-#pragma unroll
-        for (int uu = 0; uu < U; uu++) {
-            float kf[16], vf[16];
-            h8_to_f(kr[uu][0], kf); h8_to_f(kr[uu][1], kf + 8);
-            h8_to_f(vr[uu][0], vf); h8_to_f(vr[uu][1], vf + 8);
-            float s[G];
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                float x = 0.0f;
-#pragma unroll
-                for (int d = 0; d < 16; d++) x = __fadd_rn(x, __fmul_rn(qv[h][d], kf[d]));
-                s[h] = group_sum<LP>(x);
+        for (int v = 0; v < VPL; v++) { q[v] = a.q[(int64_t)qh * HD + 16 * v + l]; acc[v] = 0.0f; }
+        float m = -3.0e38f, ls = 0.0f;
+        for (int tb = t0; tb < t1; tb += ATTN_TILE) {
+            const int n = t1 - tb < ATTN_TILE ? t1 - tb : ATTN_TILE;
+            __syncthreads();
+            // stage: element d of position p to [p][d % 16][d / 16]
+            for (int e = tid; e < n * HD; e += nthr) {
+                const int p = e / HD, d = e % HD;
+                const int64_t base = kv_at(a.pgtab, a.pg_base, from + tb + p, a.n_kv, kvh, HD);
+                ks[p][d & 15][d >> 4] = a.kc[base + d];
+                vs[p][d & 15][d >> 4] = a.vc[base + d];
             }
-            if (ok[uu]) {
+            __syncthreads();
+            for (int p = 0; p < n; p++) {
+                float kf[VPL], vf[VPL];
 #pragma unroll
-                for (int h = 0; h < G; h++) {
-                    const float sc = __fmul_rn(s[h], a.scale);
-                    if (sc > m[h]) {
-                        const float c = __expf(m[h] - sc);
+                for (int v = 0; v < VPL; v++) { kf[v] = h2f(ks[p][l][v]); vf[v] = h2f(vs[p][l][v]); }
+                float d = __fmul_rn(q[0], kf[0]);
 #pragma unroll
-                        for (int d = 0; d < 16; d++) acc[h][d] = __fmul_rn(acc[h][d], c);
-                        l[h] = __fmul_rn(l[h], c);
-                        m[h] = sc;
-                    }
-                    const float pr = __expf(sc - m[h]);
-                    l[h] = __fadd_rn(l[h], pr);
+                for (int v = 1; v < VPL; v++) d = __fadd_rn(d, __fmul_rn(q[v], kf[v]));
+                d = __fadd_rn(d, __shfl_xor(d, 1));
+                d = __fadd_rn(d, __shfl_xor(d, 2));
+                d = __fadd_rn(d, __shfl_xor(d, 4));
+                d = __fadd_rn(d, __shfl_xor(d, 8));
+                const float sc = __fmul_rn(d, a.scale);
+                if (sc > m) {
+                    const float c = cj_expf(m - sc);
 #pragma unroll
-                    for (int d = 0; d < 16; d++) acc[h][d] = __fadd_rn(acc[h][d], __fmul_rn(vf[d], pr));
+                    for (int v = 0; v < VPL; v++) acc[v] = __fmul_rn(acc[v], c);
+                    ls = __fmul_rn(ls, c);
+                    m = sc;
                 }
+                const float pr = cj_expf(sc - m);
+                ls = __fadd_rn(ls, pr);
+#pragma unroll
+                for (int v = 0; v < VPL; v++) acc[v] = __fadd_rn(acc[v], __fmul_rn(vf[v], pr));
             }
         }
-    }
-
-    // fold the wave's position slots (lanes with equal j), then the 4 waves
+        float *pb = a.part + ((int64_t)qh * ATTN_MAX_SPLITS + sp) * (HD + 2);
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        float M = m[h];
-#pragma unroll
-        for (int s = LP; s < 64; s <<= 1) M = fmaxf(M, __shfl_xor(M, s));
-        const float c = l[h] > 0.0f ? __expf(m[h] - M) : 0.0f;
-        float lt = __fmul_rn(l[h], c);
-#pragma unroll
-        for (int s = LP; s < 64; s <<= 1) lt = __fadd_rn(lt, __shfl_xor(lt, s));
-#pragma unroll
-        for (int d = 0; d < 16; d++) {
-            float v = __fmul_rn(acc[h][d], c);
-#pragma unroll
-            for (int s = LP; s < 64; s <<= 1) v = __fadd_rn(v, __shfl_xor(v, s));
-            acc[h][d] = v;
-        }
-        if (p == 0) {
-#pragma unroll
-            for (int d = 0; d < 16; d++) wacc[wave][h][16 * j + d] = acc[h][d];
-        }
-        if (lane == 0) { wm[wave][h] = lt > 0.0f ? M : -3.0e38f; wl[wave][h] = lt; }
-    }
-    __syncthreads();
-    for (int e = tid; e < G * HD; e += 256) {
-        const int h = e / HD, d = e % HD;
-        float M = -3.0e38f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][h]);
-        float lt = 0.0f, v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            if (wl[w][h] > 0.0f) {
-                const float c = __expf(wm[w][h] - M);
-                lt = __fadd_rn(lt, __fmul_rn(wl[w][h], c));
-                v = __fadd_rn(v, __fmul_rn(wacc[w][h][d], c));
-            }
-        }
-        float *pb = a.part + ((int64_t)(kvh * G + h) * a.splits + sp) * (HD + 2);
-        pb[d] = v;
-        if (d == 0) { pb[HD] = lt > 0.0f ? M : -3.0e38f; pb[HD + 1] = lt; }
+        for (int v = 0; v < VPL; v++) pb[16 * v + l] = acc[v];
+        if (l == 0) { pb[HD] = m; pb[HD + 1] = ls; }
     }
     if (!a.out) return;
 
-    // the last split of this kv head merges all of them
+    // the last workgroup of this kv head merges its splits
     __threadfence();
     __syncthreads();
     if (tid == 0) ticket = atomicAdd(&a.counters[kvh], 1);
     __syncthreads();
-    if (ticket != a.splits - 1) return;
+    if (ticket != ATTN_MAX_SPLITS - 1) return;
     __threadfence();
-    for (int e = tid; e < G * HD; e += 256) {
-        const int h = e / HD, d = e % HD;
-        const int qh = kvh * G + h;
-        const float *pb0 = a.part + (int64_t)qh * a.splits * (HD + 2);
+    for (int e = tid; e < G * HD; e += nthr) {
+        const int hh = e / HD, dd = e % HD;
+        const int qq = kvh * G + hh;
+        const float *pb0 = a.part + (int64_t)qq * ATTN_MAX_SPLITS * (HD + 2);
         float gm = -3.0e38f;
-        for (int s = 0; s < a.splits; s++) gm = fmaxf(gm, pb0[s * (HD + 2) + HD]);
-        float gl = 0.0f, ac = 0.0f;
-        for (int s = 0; s < a.splits; s++) {
-            const float *pb = pb0 + s * (HD + 2);
-            const float ls = pb[HD + 1];
-            if (ls > 0.0f) {
-                const float w = __expf(pb[HD] - gm);
-                gl = __fadd_rn(gl, __fmul_rn(w, ls));
-                ac = __fadd_rn(ac, __fmul_rn(pb[d], w));
-            }
+        for (int s = 0; s < splits; s++) {
+            const float mv = pb0[s * (HD + 2) + HD];
+            if (mv > gm) gm = mv;
         }
-        a.out[(int64_t)qh * HD + d] = __fmul_rn(ac, __fdiv_rn(1.0f, gl));
+        float tacc = 0.0f, gt = 0.0f;
+        for (int sub = 0; sub < 4; sub++) {
+            float gl = 0.0f, ac = 0.0f;
+            for (int s = sub; s < splits; s += 4) {
+                const float *pb = pb0 + s * (HD + 2);
+                const float lsv = pb[HD + 1];
+                if (lsv > 0.0f) {
+                    const float wt = cj_expf(pb[HD] - gm);
+                    gl = __fadd_rn(gl, __fmul_rn(wt, lsv));
+                    ac = __fadd_rn(ac, __fmul_rn(pb[dd], wt));
+                }
+            }
+            if (sub == 0) { tacc = ac; gt = gl; }
+            else { tacc = __fadd_rn(tacc, ac); gt = __fadd_rn(gt, gl); }
+        }
+        a.out[(int64_t)qq * HD + dd] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
     }
     if (tid == 0) a.counters[kvh] = 0;
 }
 
-#define ATTN_KERNEL(HD, G) \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_decode_h##HD##_g##G(cj_attn_args a) { attn_body<HD, G>(a); }
-ATTN_KERNEL(128, 1)
-ATTN_KERNEL(128, 2)
-ATTN_KERNEL(128, 4)
-ATTN_KERNEL(128, 8)
-ATTN_KERNEL(64, 1)
-ATTN_KERNEL(64, 2)
-ATTN_KERNEL(64, 4)
-ATTN_KERNEL(64, 8)
+#define SPLIT_KERNEL(HD, G) \
+    extern "C" __global__ void __launch_bounds__(G * 16) cj_attn_split_h##HD##_g##G(cj_attn_args a) { split_body<HD, G>(a); }
+SPLIT_KERNEL(128, 4)
+SPLIT_KERNEL(128, 8)
+
+// ------------------------------------------------------------ two-pass form
+
+// scores[h][t] = scale · (q_h · K[from+t]): one 32-lane group per (h, t),
+// lane i over d = i, i+32, ..., then a butterfly over the 32 lanes.
+template <int HD>
+DEV void scores_body(const cj_attn_args &a) {
+    int count, from;
+    attn_window(a, count, from);
+    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
+    const int64_t idx = (int64_t)blockIdx.x * 8 + g;
+    const int grp = a.n_q / a.n_kv;
+    const bool ok = idx < (int64_t)a.n_q * count;
+    const int h = ok ? (int)(idx / count) : 0, t = ok ? (int)(idx % count) : 0;
+    float s = 0.0f;
+    if (ok) {
+        const int64_t kb = kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, h / grp, HD);
+        for (int d = i; d < HD; d += 32) s = __fadd_rn(s, __fmul_rn(a.q[(int64_t)h * HD + d], h2f(a.kc[kb + d])));
+    }
+    s = __fadd_rn(s, __shfl_xor(s, 16, 32));
+    s = __fadd_rn(s, __shfl_xor(s, 8, 32));
+    s = __fadd_rn(s, __shfl_xor(s, 4, 32));
+    s = __fadd_rn(s, __shfl_xor(s, 2, 32));
+    s = __fadd_rn(s, __shfl_xor(s, 1, 32));
+    if (ok && i == 0) a.part[(int64_t)h * a.splits + t] = __fmul_rn(s, a.scale);
+}
+
+// softmax over scores[h][0..count) in place and out[h] = Σ_t p_t·V_t / Σ p:
+// one workgroup of 128 per query head.
+template <int HD>
+DEV void combine_body(const cj_attn_args &a) {
+    __shared__ float red[128];
+    int count, from;
+    attn_window(a, count, from);
+    const int h = blockIdx.x, l = threadIdx.x;
+    const int grp = a.n_q / a.n_kv, kvh = h / grp;
+    float *sc = a.part + (int64_t)h * a.splits;
+    float mx = -3.0e38f;
+    for (int t = l; t < count; t += 128) if (sc[t] > mx) mx = sc[t];
+    red[l] = mx;
+    __syncthreads();
+    for (int r = 64; r > 0; r >>= 1) {
+        if (l < r && red[l + r] > red[l]) red[l] = red[l + r];
+        __syncthreads();
+    }
+    const float m = red[0];
+    __syncthreads();
+    float s = 0.0f;
+    for (int t = l; t < count; t += 128) {
+        const float e = cj_expf(sc[t] - m);
+        sc[t] = e;
+        s = __fadd_rn(s, e);
+    }
+    red[l] = s;
+    __syncthreads();
+    for (int r = 64; r > 0; r >>= 1) {
+        if (l < r) red[l] = __fadd_rn(red[l], red[l + r]);
+        __syncthreads();
+    }
+    const float rs = __fdiv_rn(1.0f, red[0]);
+    for (int d = l; d < HD; d += 128) {
+        float acc = 0.0f;
+        for (int t = 0; t < count; t++) {
+            const int64_t vb = kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD);
+            acc = __fadd_rn(acc, __fmul_rn(sc[t], h2f(a.vc[vb + d])));
+        }
+        a.out[(int64_t)h * HD + d] = __fmul_rn(acc, rs);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a); }
+extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a); }
+extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a); }
 
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
-// 256 per 256 output values (the reference's attnReducePackQ8Kernel contract).
+// 256 per 256 output values (the reference's attnReducePackQ8Kernel
+// contract), the merge in reducePackBlockCpu's order.
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
     __shared__ float bmax[8];
     const int t = threadIdx.x, lane = t & 63;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
+    const int hd = a.head_dim;
     float x = 0.0f;
     if (e < n) {
-        const int h = (int)(e / a.head_dim), d = (int)(e % a.head_dim);
-        const float *pb0 = a.part + (int64_t)h * a.splits * (a.head_dim + 2);
+        const int h = (int)(e / hd), d = (int)(e % hd);
+        const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
         float gm = -3.0e38f;
-        for (int s = 0; s < a.splits; s++) gm = fmaxf(gm, pb0[s * (a.head_dim + 2) + a.head_dim]);
-        float gl = 0.0f, ac = 0.0f;
         for (int s = 0; s < a.splits; s++) {
-            const float *pb = pb0 + s * (a.head_dim + 2);
-            const float ls = pb[a.head_dim + 1];
-            if (ls > 0.0f) {
-                const float w = __expf(pb[a.head_dim] - gm);
-                gl = __fadd_rn(gl, __fmul_rn(w, ls));
-                ac = __fadd_rn(ac, __fmul_rn(pb[d], w));
-            }
+            const float mv = pb0[s * (hd + 2) + hd];
+            if (mv > gm) gm = mv;
         }
-        x = __fmul_rn(ac, __fdiv_rn(1.0f, gl));
+        float tacc = 0.0f, gt = 0.0f;
+        for (int sub = 0; sub < 4; sub++) {
+            float gl = 0.0f, ac = 0.0f;
+            for (int s = sub; s < a.splits; s += 4) {
+                const float *pb = pb0 + s * (hd + 2);
+                const float ls = pb[hd + 1];
+                if (ls > 0.0f) {
+                    const float w = cj_expf(pb[hd] - gm);
+                    gl = __fadd_rn(gl, __fmul_rn(w, ls));
+                    ac = __fadd_rn(ac, __fmul_rn(pb[d], w));
+                }
+            }
+            if (sub == 0) { tacc = ac; gt = gl; }
+            else { tacc = __fadd_rn(tacc, ac); gt = __fadd_rn(gt, gl); }
+        }
+        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
         if (a.out) a.out[e] = x;
     }
     if (!a.packed) return;
     const float av = fabsf(x);
     float am;
     if (a.per32) {
-        float mm = group_max<32>(av);
+        const float mm = group_max<32>(av);
         if ((lane & 31) == 0) bmax[t >> 5] = mm;
         __syncthreads();
         am = bmax[t >> 5];
     } else {
-        float mm = group_max<64>(av);
+        const float mm = group_max<64>(av);
         if (lane == 0) bmax[t >> 6] = mm;
         __syncthreads();
         am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
@@ -244,7 +293,6 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
 // QK-norm (optional) + split-half RoPE + fp16 K/V append, one workgroup of
 // 64 per head, q heads first (AttnKernel.qkPrepKernel's contract).
 extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
-    __shared__ float red[64];
     const int head = blockIdx.x, t = threadIdx.x;
     const bool isq = head < a.n_q;
     const int hd = a.head_dim, half = hd >> 1;
@@ -255,7 +303,7 @@ extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
         float ss = 0.0f;
         for (int i = t; i < hd; i += 64) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
         ss = group_sum<64>(ss);
-        const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), a.eps)));
+        const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), a.eps)));
         const float *w = isq ? a.qw : a.kw;
         for (int i = t; i < hd; i += 64) {
             const float wi = a.form == 1 ? __fadd_rn(1.0f, w[i]) : w[i];

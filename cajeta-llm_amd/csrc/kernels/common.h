@@ -10,6 +10,11 @@
 DEV float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu))); }
 DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
+// Correctly rounded f32 square root. (HIP's __fsqrt_rn is the hardware's
+// approximate v_sqrt_f32 unless OCML's rounded operations are enabled; the
+// llvm.sqrt expansion for gfx950 rounds to nearest even.)
+DEV float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // Exact integer exchange inside a quad of lanes (DPP quad_perm).
@@ -49,6 +54,70 @@ DEV float mxfp4_val(uint32_t nib) {
     return (float)v;
 }
 
+// exp(x) in f32 from correctly rounded steps only, so it gives the same bits
+// as the checker's restatement: n = rint(x·log2 e); r = x − n·ln2 by two fma
+// (Cody–Waite, ln2_hi with trailing zeros); e^r by the degree-7 Taylor
+// polynomial (Horner, fma); ·2^n in two exact power-of-two steps.
+DEV float cj_expf(float x) {
+    if (x != x) return x;
+    if (x < -104.0f) return 0.0f;
+    if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
+    const float n = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
+    float r = __fmaf_rn(n, -0.693145751953125f, x);
+    r = __fmaf_rn(n, -1.428606765330187045e-06f, r);
+    float p = 1.98412698412698413e-04f;
+    p = __fmaf_rn(p, r, 1.38888888888888889e-03f);
+    p = __fmaf_rn(p, r, 8.33333333333333333e-03f);
+    p = __fmaf_rn(p, r, 4.16666666666666667e-02f);
+    p = __fmaf_rn(p, r, 1.66666666666666667e-01f);
+    p = __fmaf_rn(p, r, 0.5f);
+    p = __fmaf_rn(p, r, 1.0f);
+    p = __fmaf_rn(p, r, 1.0f);
+    const int ni = (int)n, n1 = ni / 2, n2 = ni - n1;
+    return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(n1 + 127) << 23)), __uint_as_float((uint32_t)(n2 + 127) << 23));
+}
+
+// SiLU(x)·u, exp form: x / (1 + exp(−x)) · u (Prim.gluF32 / gluOne).
+DEV float silu_exp_mul(float x, float u) {
+    return __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, cj_expf(0.0f - x))), u);
+}
+
+// SiLU(x)·u, the CPU backend's vector form (Prim.gluCpuKernel): 0.5·x·(1 +
+// tanh(x/2)) with tanh as Eigen's float rational approximation on a clamped
+// argument; every step a correctly rounded op or an fma.
+DEV float silu_tanh_mul(float x, float u) {
+    const float tlo = -7.90531110763549805f;
+    float xa = fmaxf(x, -16.0f);
+    float xb = __fsub_rn(-16.0f, xa);
+    float xc = __fsub_rn(-16.0f, fmaxf(xb, -32.0f));
+    float t0 = __fmul_rn(0.5f, __fmaf_rn(__fmul_rn(0.0f, xc), __fmul_rn(xc, xc), xc));
+    float ta = fmaxf(t0, tlo);
+    float tb = __fsub_rn(tlo, ta);
+    float t = __fsub_rn(tlo, fmaxf(tb, -15.8106222152709961f));
+    float t2 = __fmul_rn(t, t);
+    float p = __fmaf_rn(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
+    p = __fmaf_rn(p, t2, -8.60467152213735e-11f);
+    p = __fmaf_rn(p, t2, 5.12229709037114e-08f);
+    p = __fmaf_rn(p, t2, 1.48572235717979e-05f);
+    p = __fmaf_rn(p, t2, 6.37261928875436e-04f);
+    p = __fmul_rn(__fmaf_rn(p, t2, 4.89352455891786e-03f), t);
+    float q = __fmaf_rn(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
+    q = __fmaf_rn(q, t2, 2.26843463243900e-03f);
+    q = __fmaf_rn(q, t2, 4.89352518554385e-03f);
+    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, xa), __fadd_rn(1.0f, __fdiv_rn(p, q))), u);
+}
+
+// Element e of silu(g)·u over a row of n in the given form. The vector form
+// (form 1) covers each 4096-wide work block in 16-wide chunks and leaves the
+// block's tail to the exp form, as gluCpuKernel does.
+DEV float glu_value(int form, int64_t e, int64_t n, float g, float u) {
+    if (!form) return silu_exp_mul(g, u);
+    const int64_t b0 = e & ~(int64_t)4095;
+    const int64_t hi = b0 + 4096 < n ? b0 + 4096 : n;
+    const int64_t vec_end = b0 + ((hi - b0) & ~(int64_t)15);
+    return e < vec_end ? silu_tanh_mul(g, u) : silu_exp_mul(g, u);
+}
+
 // Zero the pad bytes [292, 320) of a per-256 pack block, so a pack's bytes
 // are fully determined (thread t < 7 writes one word).
 DEV void pack_zero_pad(uint8_t *blk, int t) {
@@ -68,11 +137,25 @@ DEV void pack_zero_pad(uint8_t *blk, int t) {
 
 #define STAGE_CHUNK 16     // 256-wide blocks held in registers at a time
 
-// RMSNorm scale of x[0..n): thread t sums x[t + 256k]^2 in k order, the 256
-// partials fold 128, 64, ..., 1 (lanes of wave 0 for the last six), then
-// 1/sqrt(ss/n + eps). `red` is 256 floats of LDS.
+// RMSNorm scale of x[0..n): for whole 256s (the CPU row form,
+// Prim.rmsnormPackRowCpuKernel, model/Prim.cajeta:977-1071) thread t sums
+// x[t + 256k]^2 in k order and the 256 partials fold 128, 64, ..., 1 (lanes of
+// wave 0 for the last six); other widths sum in element order on one thread
+// (Prim.rmsnormRowHost, :120-151). Then 1/sqrt(ss/n + eps). `red` is 256
+// floats of LDS.
 DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     const int t = threadIdx.x;
+    if (n & 255) {
+        if (t == 0) {
+            float s = 0.0f;
+            for (int64_t e = 0; e < n; e++) s = __fadd_rn(s, __fmul_rn(x[e], x[e]));
+            red[0] = s;
+        }
+        __syncthreads();
+        const float ss = red[0];
+        __syncthreads();
+        return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+    }
     float p = 0.0f;
     for (int64_t e = t; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
@@ -88,7 +171,7 @@ DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     __syncthreads();
     const float ss = red[0];
     __syncthreads();
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+    return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
 }
 
 // The staged value of element e: x[e], or x[e]·scale·w[e] under the norm.

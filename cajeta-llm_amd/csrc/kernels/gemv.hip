@@ -1,13 +1,22 @@
 // gemv.hip — quantised mat-vec family for gfx950 (wave64).
 //
-// One body serves every decode projection: a prologue stages the activation
-// in LDS (copied pack, pack of f32, or RMSNorm + pack), a per-format core
-// streams the weight rows with 128-bit loads and integer dot4s, and an
-// epilogue stores, accumulates into the residual, applies RoPE + the fp16
-// K/V append, applies SiLU·up + the pack of the result, or takes the greedy
-// argmax. Lanes split a row into LPR-lane groups; each (wave, group) owns a
-// contiguous run of rows, two at a time, so paired rows (RoPE pairs, gate/up
-// pairs) meet in one lane.
+// One body serves every decode projection. A prologue stages the activation
+// in LDS (a copied pack, the pack of an f32 vector, or RMSNorm + pack). Then:
+//
+//   phase A  lanes stream the weight rows with 128-bit loads — lanes across a
+//            row's blocks, LPR lanes a row, two rows in flight — and compute
+//            each block's exact terms: integer dot4s for the quants, the
+//            6-bit scales and mins in integer space, the quad of lanes that
+//            shares a block summed exactly, then the block's f32 terms as the
+//            reference forms them. The terms go to LDS per (row, block).
+//   phase B  one thread per row folds its row's terms in block order — the
+//            order Quant.q4kMatVecIntoQ8 / q6kMatVecIntoQ8 / q80MatVecIntoQ8Sub
+//            add them (io/Quant.cajeta:3079-3110, :3374-3486) — and runs the
+//            epilogue: store, residual accumulate, RoPE + the fp16 K/V append,
+//            SiLU·up + the pack of the result, or the greedy argmax.
+//
+// The f32-activation formats (Q4_0, MXFP4, the f32 router) keep a lane-tree
+// sum per row (their checks are held to a tolerance).
 //
 // Prepared row layouts (HBM, 16-byte aligned rows):
 //   Q4_K : the GGUF blocks as they are: {f16 d, f16 dmin, 12 B scales, 128 B qs}
@@ -15,18 +24,28 @@
 //   Q8_0 : [qs nb·32][d nb·2, padded to 16]
 //   Q4_0 : [qs nb·16][d nb·2, padded to 16]
 //   MXFP4: [qs nb·16][e nb, padded to 16]
+//   F32  : the f32 row
 #include "common.h"
 
 #define LDS_SCRATCH 3072   // red[256] + bmax[512] floats
 
-// ------------------------------------------------------------------ cores
+// Terms each row leaves in LDS, by format.
+DEV int terms_per_row(int fmt, int64_t cols) {
+    switch (fmt) {
+    case CJ_Q4_K: return (int)(cols / 256) * 2;
+    case CJ_Q6_K: return (int)(cols / 256);
+    case CJ_Q8_0: return (int)((cols / 32 + 7) / 8);
+    default: return 1;
+    }
+}
 
-// Q4_K × q8_K: per (block, 64-element chunk) unit, the two sub-blocks' int
-// dots scaled by their 6-bit scales, the mins term from the pack's sums;
-// the quad of lanes sharing a block sums exactly, then
-// term = d·xs·sumi − dmin·xs·dmins (the reference block term).
+// ----------------------------------------------------------------- phase A
+
+// Q4_K × q8_K. Unit (block b, 64-element chunk j): the two sub-blocks' int
+// dots × their 6-bit scales and the mins × the pack's sub-block sums, summed
+// over the quad exactly; the leader writes (d·xs·sumi, dmin·xs·dmins).
 template <int NR, int LPR>
-DEV void core_q4k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int slot, float (&acc)[NR]) {
+DEV void terms_q4k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb, int slot) {
     const int units = nb * 4;
     for (int u = slot; u < units; u += LPR) {
         const int b = u >> 2, j = u & 3;
@@ -59,33 +78,33 @@ DEV void core_q4k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int
             dhi = sdot4((q1[r].z >> 4) & M, a3.z, dhi); dhi = sdot4((q1[r].w >> 4) & M, a3.w, dhi);
             // 6-bit scales/mins of sub-blocks 2j, 2j+1 (the headK4 unpacking)
             const uint32_t sy = hd[r].y, sz = hd[r].z, sw = hd[r].w;
+            const uint32_t A0 = (sy >> (8 * t0)) & 255, B0 = (sz >> (8 * t0)) & 255, C0 = (sw >> (8 * t0)) & 255;
+            const uint32_t A1 = (sy >> (8 * t0 + 8)) & 255, B1 = (sz >> (8 * t0 + 8)) & 255, C1 = (sw >> (8 * t0 + 8)) & 255;
             int sc0, mn0, sc1, mn1;
-            {
-                uint32_t A0 = (sy >> (8 * t0)) & 255, B0 = (sz >> (8 * t0)) & 255, C0 = (sw >> (8 * t0)) & 255;
-                uint32_t A1 = (sy >> (8 * t0 + 8)) & 255, B1 = (sz >> (8 * t0 + 8)) & 255, C1 = (sw >> (8 * t0 + 8)) & 255;
-                if (hi) {
-                    sc0 = (C0 & 15) | ((A0 >> 2) & 48); mn0 = (C0 >> 4) | ((B0 >> 2) & 48);
-                    sc1 = (C1 & 15) | ((A1 >> 2) & 48); mn1 = (C1 >> 4) | ((B1 >> 2) & 48);
-                } else {
-                    sc0 = A0 & 63; mn0 = B0 & 63; sc1 = A1 & 63; mn1 = B1 & 63;
-                }
+            if (hi) {
+                sc0 = (C0 & 15) | ((A0 >> 2) & 48); mn0 = (C0 >> 4) | ((B0 >> 2) & 48);
+                sc1 = (C1 & 15) | ((A1 >> 2) & 48); mn1 = (C1 >> 4) | ((B1 >> 2) & 48);
+            } else {
+                sc0 = A0 & 63; mn0 = B0 & 63; sc1 = A1 & 63; mn1 = B1 & 63;
             }
             int sumi = dlo * sc0 + dhi * sc1;
             int dmins = mn0 * bs.x + mn1 * bs.y;
             sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
             dmins += quad_xor1(dmins); dmins += quad_xor2(dmins);
-            const float d = h2f(hd[r].x), dmin = h2f(hd[r].x >> 16);
-            float term = __fsub_rn(__fmul_rn(__fmul_rn(d, xs), (float)sumi), __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
-            acc[r] += (j == 0) ? term : 0.0f;
+            if (j == 0) {
+                const float d = h2f(hd[r].x), dmin = h2f(hd[r].x >> 16);
+                *(float2 *)(tr[r] + 2 * b) = make_float2(__fmul_rn(__fmul_rn(d, xs), (float)sumi),
+                                                         __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
+            }
         }
     }
 }
 
-// Q6_K × q8_K: unit = (block, 64 elements): half g, lane half hl; four
-// 16-element scale groups; the 6-bit values 0..63 dot the int8 activation and
-// 32·Σa comes off per group (Σa once per unit, shared by the rows).
+// Q6_K × q8_K. Unit (block b, 64 elements): half g, lane half hl; four
+// 16-element scale groups; the 6-bit values 0..63 dot the int8 activation
+// and 32·Σa comes off per group. The leader writes d·xs·sumi.
 template <int NR, int LPR>
-DEV void core_q6k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int slot, float (&acc)[NR]) {
+DEV void terms_q6k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb, int slot) {
     const int units = nb * 4;
     for (int u = slot; u < units; u += LPR) {
         const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
@@ -121,10 +140,10 @@ DEV void core_q6k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int
                 const uint4 ql = (k & 1) ? qb[r] : qa[r];
                 const int sh = (k >> 1) * 4;
                 const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
-                uint32_t vx = ((ql.x >> sh) & M) | (((qh[r].x >> (2 * k)) & H) << 4);
-                uint32_t vy = ((ql.y >> sh) & M) | (((qh[r].y >> (2 * k)) & H) << 4);
-                uint32_t vz = ((ql.z >> sh) & M) | (((qh[r].z >> (2 * k)) & H) << 4);
-                uint32_t vw = ((ql.w >> sh) & M) | (((qh[r].w >> (2 * k)) & H) << 4);
+                const uint32_t vx = ((ql.x >> sh) & M) | (((qh[r].x >> (2 * k)) & H) << 4);
+                const uint32_t vy = ((ql.y >> sh) & M) | (((qh[r].y >> (2 * k)) & H) << 4);
+                const uint32_t vz = ((ql.z >> sh) & M) | (((qh[r].z >> (2 * k)) & H) << 4);
+                const uint32_t vw = ((ql.w >> sh) & M) | (((qh[r].w >> (2 * k)) & H) << 4);
                 int dt = 0;
                 dt = sdot4(vx, a[k].x, dt); dt = sdot4(vy, a[k].y, dt);
                 dt = sdot4(vz, a[k].z, dt); dt = sdot4(vw, a[k].w, dt);
@@ -134,28 +153,35 @@ DEV void core_q6k(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb, int
                 sumi += scv * (dt - 32 * S[k]);
             }
             sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
-            const float d = h2f(dh[r]);
-            float term = __fmul_rn(__fmul_rn(d, xs), (float)sumi);
-            acc[r] += (j == 0) ? term : 0.0f;
+            if (j == 0) tr[r][b] = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)sumi);
         }
     }
 }
 
-// Q8_0 × per-32 int8: one 32-element block a lane; (d·xs)·isum per block.
+// Q8_0 × per-32 int8. One 32-element block a lane, term (d·xs)·isum; the 8
+// lanes of a 256-wide group then sum their terms in block order (the
+// reference's fs) and the group's first lane writes it.
 template <int NR, int LPR>
-DEV void core_q80(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb32, int slot, float (&acc)[NR]) {
-    for (int u = slot; u < nb32; u += LPR) {
+DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
+    const int lane = threadIdx.x & 63;
+    const int base = lane & ~7;
+    const int iters = (nb32 + LPR - 1) / LPR;
+    for (int it = 0; it < iters; it++) {
+        const int u = slot + it * LPR;
+        const bool ok = u < nb32;
+        const int uu = ok ? u : nb32 - 1;
         uint4 w0[NR], w1[NR];
         uint32_t dh[NR];
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            w0[r] = *(const uint4 *)(wr[r] + (int64_t)u * 32);
-            w1[r] = *(const uint4 *)(wr[r] + (int64_t)u * 32 + 16);
-            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * u);
+            w0[r] = *(const uint4 *)(wr[r] + (int64_t)uu * 32);
+            w1[r] = *(const uint4 *)(wr[r] + (int64_t)uu * 32 + 16);
+            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
         }
-        const uint8_t *ab = sx + (u >> 3) * 320;
-        const uint4 a0 = *(const uint4 *)(ab + 32 * (u & 7)), a1 = *(const uint4 *)(ab + 32 * (u & 7) + 16);
-        const float xs = *(const float *)(ab + 288 + 4 * (u & 7));
+        const uint8_t *ab = sx + (uu >> 3) * 320;
+        const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
+        const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
+        const int left = nb32 - (u & ~7);          // real blocks in this group of 8
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             int s = 0;
@@ -163,14 +189,21 @@ DEV void core_q80(const uint8_t *const (&wr)[NR], const uint8_t *sx, int nb32, i
             s = sdot4(w0[r].z, a0.z, s); s = sdot4(w0[r].w, a0.w, s);
             s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
             s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
-            acc[r] += __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
+            const float t = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
+            float fs = __shfl(t, base);
+#pragma unroll
+            for (int k = 1; k < 8; k++) {
+                const float o = __shfl(t, base + k);
+                if (k < left) fs = __fadd_rn(fs, o);
+            }
+            if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
     }
 }
 
-// Q4_0 × f32: d·Σ (q − 8)·x per 32-element block.
+// Q4_0 × f32: d·Σ (q − 8)·x per block, lane partials (tree across lanes).
 template <int NR, int LPR>
-DEV void core_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
+DEV void acc_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
     for (int u = slot; u < nb32; u += LPR) {
         uint4 w[NR];
         uint32_t dh[NR];
@@ -182,7 +215,7 @@ DEV void core_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int
         float xv[32];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
+            const float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
             xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
         }
 #pragma unroll
@@ -195,15 +228,14 @@ DEV void core_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int
                 dot = __fadd_rn(dot, __fmul_rn((float)((q & 15) - 8), xv[jj]));
                 dot = __fadd_rn(dot, __fmul_rn((float)((q >> 4) - 8), xv[jj + 16]));
             }
-            acc[r] += __fmul_rn(h2f(dh[r]), dot);
+            acc[r] = __fadd_rn(acc[r], __fmul_rn(h2f(dh[r]), dot));
         }
     }
 }
 
-
-// MXFP4 × f32: code(nib)·2^(e−128)·x in element order per block.
+// MXFP4 × f32: code(nib)·2^(e−128)·x per element, lane partials.
 template <int NR, int LPR>
-DEV void core_mxfp4(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
+DEV void acc_mxfp4(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
     for (int u = slot; u < nb32; u += LPR) {
         uint4 w[NR];
         uint32_t eb[NR];
@@ -215,29 +247,27 @@ DEV void core_mxfp4(const uint8_t *const (&wr)[NR], const float *xf, int nb32, i
         float xv[32];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
+            const float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
             xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
         }
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             const uint32_t ws[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
             const float d = mxfp4_scale(eb[r]);
-            float a = 0.0f;
 #pragma unroll
             for (int k = 0; k < 32; k++) {
                 const int jj = k & 15;
                 const uint32_t byv = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
                 const uint32_t nib = k < 16 ? (byv & 15) : (byv >> 4);
-                a = __fadd_rn(a, __fmul_rn(__fmul_rn(mxfp4_val(nib), d), xv[k]));
+                acc[r] = __fadd_rn(acc[r], __fmul_rn(__fmul_rn(mxfp4_val(nib), d), xv[k]));
             }
-            acc[r] += a;
         }
     }
 }
 
-// f32 weights × f32 (the MoE router): four columns a unit.
+// f32 weights × f32 (the MoE router): four columns a unit, lane partials.
 template <int NR, int LPR>
-DEV void core_f32(const uint8_t *const (&wr)[NR], const float *xf, int n4, int slot, float (&acc)[NR]) {
+DEV void acc_f32(const uint8_t *const (&wr)[NR], const float *xf, int n4, int slot, float (&acc)[NR]) {
     for (int u = slot; u < n4; u += LPR) {
         const float4 x = *(const float4 *)(xf + 4 * u);
 #pragma unroll
@@ -258,52 +288,27 @@ DEV int64_t kv_index(const int32_t *pgtab, int pg_base, int pos, int nkv, int kv
     return (((int64_t)page * nkv + kvh) * 64 + (pos & 63)) * hd;
 }
 
-DEV float silu_exp(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, __expf(0.0f - x))); }
-
-// The CPU backend's rational-tanh SiLU (Eigen's float tanh approximation).
-DEV float silu_tanh_mul(float x, float u) {
-    const float tlo = -7.90531110763549805f;
-    float xa = fmaxf(x, -16.0f);
-    float xb = __fsub_rn(-16.0f, xa);
-    float xc = __fsub_rn(-16.0f, fmaxf(xb, -32.0f));
-    float t0 = __fmul_rn(0.5f, __fmaf_rn(__fmul_rn(0.0f, xc), __fmul_rn(xc, xc), xc));
-    float ta = fmaxf(t0, tlo);
-    float tb = __fsub_rn(tlo, ta);
-    float t = __fsub_rn(tlo, fmaxf(tb, -15.8106222152709961f));
-    float t2 = __fmul_rn(t, t);
-    float p = __fmaf_rn(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
-    p = __fmaf_rn(p, t2, -8.60467152213735e-11f);
-    p = __fmaf_rn(p, t2, 5.12229709037114e-08f);
-    p = __fmaf_rn(p, t2, 1.48572235717979e-05f);
-    p = __fmaf_rn(p, t2, 6.37261928875436e-04f);
-    p = __fmul_rn(__fmaf_rn(p, t2, 4.89352455891786e-03f), t);
-    float q = __fmaf_rn(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
-    q = __fmaf_rn(q, t2, 2.26843463243900e-03f);
-    q = __fmaf_rn(q, t2, 4.89352518554385e-03f);
-    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, xa), __fadd_rn(1.0f, __fdiv_rn(p, q))), u);
-}
-
 // Pack one 256-wide block of an f32 vector (values past n are zero) from
 // HBM into the 320-byte layout, by the whole workgroup.
 DEV void pack_block_global(const float *x, int64_t n, int64_t blk, int per32, uint8_t *out, float *bmax) {
     const int t = threadIdx.x, lane = t & 63;
     const int64_t e = blk * 256 + t;
-    float v = e < n ? x[e] : 0.0f;
-    float a = fabsf(v);
+    const float v = e < n ? x[e] : 0.0f;
+    const float a = fabsf(v);
     if (per32) {
-        float m = group_max<32>(a);
+        const float m = group_max<32>(a);
         if ((lane & 31) == 0) bmax[t >> 5] = m;
     } else {
-        float m = group_max<64>(a);
+        const float m = group_max<64>(a);
         if (lane == 0) bmax[t >> 6] = m;
     }
     __syncthreads();
-    float am = per32 ? bmax[t >> 5] : fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
-    float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
-    int q = round_away(__fmul_rn(v, inv));
+    const float am = per32 ? bmax[t >> 5] : fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    const int q = round_away(__fmul_rn(v, inv));
     uint8_t *ob = out + blk * 320;
     ob[t] = (uint8_t)(int8_t)q;
-    int s = group_sum_i<32>(q);
+    const int s = group_sum_i<32>(q);
     if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
     if (per32) {
         if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
@@ -312,6 +317,10 @@ DEV void pack_block_global(const float *x, int64_t n, int64_t blk, int per32, ui
         pack_zero_pad(ob, t);
     }
     __syncthreads();
+}
+
+DEV bool argmax_take(float ov, int oi, float mv, int mi) {
+    return mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)));
 }
 
 // ------------------------------------------------------------------ body
@@ -324,14 +333,18 @@ DEV void gemv_body(const cj_gemv_args &a) {
     uint8_t *sx = smem + LDS_SCRATCH;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int64_t cols = a.cols;
-    const bool f32act = (FMT == CJ_Q4_0 || FMT == CJ_MXFP4 || FMT == CJ_F32);
+    constexpr bool f32act = (FMT == CJ_Q4_0 || FMT == CJ_MXFP4 || FMT == CJ_F32);
     const int nblk = (int)((cols + 255) / 256);
+    const int act_bytes = f32act ? nblk * 1024 : nblk * 320;
+    float *terms = (float *)(sx + act_bytes);
+    const int TB = terms_per_row(FMT, cols);
+    const int R = a.rows_per_wg;
 
     // MoE indirection: copy k of the rows reads expert sel[k]
     int64_t wg = blockIdx.x;
     int kidx = 0;
     if (a.sel) {
-        const int64_t wpk = (a.rows + a.rows_per_wg - 1) / a.rows_per_wg;
+        const int64_t wpk = (a.rows + R - 1) / R;
         kidx = (int)(wg / wpk);
         wg = wg % wpk;
     }
@@ -339,6 +352,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
     const float *X = a.x ? a.x + kidx * a.x_stride : nullptr;
     float *Y = a.y ? a.y + kidx * a.y_stride : nullptr;
     float *ACT = a.act ? a.act + kidx * a.y_stride : nullptr;
+    const int64_t row0 = wg * R;
 
     // ---- prologue: the activation into LDS
     if (a.pro == CJ_PRO_PACKED) {
@@ -350,86 +364,91 @@ DEV void gemv_body(const cj_gemv_args &a) {
         else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, bmax, nullptr);
     }
 
-    // ---- rows
-    constexpr int G = 64 / LPR;
-    const int group = lane / LPR, slot = lane % LPR;
-    const int rpg = a.rows_per_wg / (4 * G);              // rows per (wave, group), even
-    const int64_t run0 = wg * a.rows_per_wg + (int64_t)(wave * G + group) * rpg;
-    const int nb = (int)(cols / 256);
-    const int nb32 = (int)(cols / 32);
+    // ---- phase A: block terms of the workgroup's R rows
+    {
+        constexpr int G = 64 / LPR;
+        const int group = lane / LPR, slot = lane % LPR;
+        const int lanes_groups = 4 * G;                      // row slots across the workgroup
+        const int nb = (int)(cols / 256), nb32 = (int)(cols / 32);
+        for (int i = 0; i < R; i += 2 * lanes_groups) {
+            const int rl0 = i + 2 * (wave * G + group), rl1 = rl0 + 1;
+            const int64_t r0 = row0 + rl0, r1 = row0 + rl1;
+            const uint8_t *wr[2];
+            wr[0] = W + (r0 < a.rows ? r0 : a.rows - 1) * a.row_bytes;
+            wr[1] = W + (r1 < a.rows ? r1 : a.rows - 1) * a.row_bytes;
+            float *tr[2] = {terms + (rl0 < R ? rl0 : 0) * TB, terms + (rl1 < R ? rl1 : 0) * TB};
+            if (rl0 >= R) continue;     // uniform per LPR group
+            if (FMT == CJ_Q4_K) terms_q4k<2, LPR>(wr, tr, sx, nb, slot);
+            else if (FMT == CJ_Q6_K) terms_q6k<2, LPR>(wr, tr, sx, nb, slot);
+            else if (FMT == CJ_Q8_0) terms_q80<2, LPR>(wr, tr, sx, nb32, slot);
+            else {
+                float acc[2] = {0.0f, 0.0f};
+                if (FMT == CJ_Q4_0) acc_q40<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
+                else if (FMT == CJ_MXFP4) acc_mxfp4<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
+                else acc_f32<2, LPR>(wr, (const float *)sx, (int)(cols / 4), slot, acc);
+                const float v0 = group_sum<LPR>(acc[0]), v1 = group_sum<LPR>(acc[1]);
+                if (slot == 0) { tr[0][0] = v0; tr[1][0] = v1; }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- phase B: thread t folds row t's terms in block order
+    const int64_t r = row0 + t;
+    const bool live = t < R && r < a.rows;
+    float v = 0.0f;
+    if (t < R) {
+        const float *tp = terms + t * TB;
+        if (FMT == CJ_Q4_K) {
+            for (int b = 0; b < TB; b += 2) v = __fsub_rn(__fadd_rn(v, tp[b]), tp[b + 1]);
+        } else if (FMT == CJ_Q6_K || FMT == CJ_Q8_0) {
+            for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
+        } else {
+            v = tp[0];
+        }
+    }
+    const float vp = __shfl_xor(v, 1);      // the paired row (RoPE pair, gate/up pair)
     const int pos = (a.epi == CJ_EPI_QKV_ROPE || a.epi == CJ_EPI_ARGMAX) ? step_pos(a.state, a.pos) : 0;
 
-    float best_v = 0.0f;
-    int best_i = -1;
-
-    for (int i = 0; i < rpg; i += 2) {
-        const int64_t r0 = run0 + i, r1 = r0 + 1;
-        const uint8_t *wr[2];
-        wr[0] = W + (r0 < a.rows ? r0 : a.rows - 1) * a.row_bytes;
-        wr[1] = W + (r1 < a.rows ? r1 : a.rows - 1) * a.row_bytes;
-        float acc[2] = {0.0f, 0.0f};
-        if (FMT == CJ_Q4_K) core_q4k<2, LPR>(wr, sx, nb, slot, acc);
-        else if (FMT == CJ_Q6_K) core_q6k<2, LPR>(wr, sx, nb, slot, acc);
-        else if (FMT == CJ_Q8_0) core_q80<2, LPR>(wr, sx, nb32, slot, acc);
-        else if (FMT == CJ_Q4_0) core_q40<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
-        else if (FMT == CJ_MXFP4) core_mxfp4<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
-        else core_f32<2, LPR>(wr, (const float *)sx, (int)(cols / 4), slot, acc);
-        float v0 = group_sum<LPR>(acc[0]);
-        float v1 = group_sum<LPR>(acc[1]);
-        if (slot != 0) continue;
-
-        switch (a.epi) {
-        case CJ_EPI_STORE:
-            if (r0 < a.rows) Y[a.y_off + r0] = v0;
-            if (r1 < a.rows) Y[a.y_off + r1] = v1;
-            break;
-        case CJ_EPI_ACCUM:
-            if (r0 < a.rows) Y[a.y_off + r0] = __fadd_rn(Y[a.y_off + r0], v0);
-            if (r1 < a.rows) Y[a.y_off + r1] = __fadd_rn(Y[a.y_off + r1], v1);
-            break;
-        case CJ_EPI_QKV_ROPE: {
-            if (r0 >= a.rows) break;
-            const int hd = a.head_dim, half = hd >> 1;
-            const int64_t qrows = (int64_t)a.n_q * hd, krows = (int64_t)a.n_kv * hd;
-            if (r0 < qrows + krows) {
-                // GGUF pair order: row h·hd + 2b + a holds HF dim a·half + b
-                const int64_t rr = r0 < qrows ? r0 : r0 - qrows;
-                const int h = (int)(rr / hd), bb = (int)(rr % hd) >> 1;
-                const float2 cs = *(const float2 *)(a.rope_cs + 2 * ((int64_t)pos * half + bb));
-                const float ra = __fsub_rn(__fmul_rn(v0, cs.x), __fmul_rn(v1, cs.y));
-                const float rb = __fadd_rn(__fmul_rn(v0, cs.y), __fmul_rn(v1, cs.x));
-                if (r0 < qrows) {
-                    a.q_out[(int64_t)h * hd + bb] = ra;
-                    a.q_out[(int64_t)h * hd + half + bb] = rb;
-                } else {
-                    const int64_t ki = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
-                    a.kc[ki + bb] = f2h(ra);
-                    a.kc[ki + half + bb] = f2h(rb);
-                }
+    switch (a.epi) {
+    case CJ_EPI_STORE:
+        if (live) Y[a.y_off + r] = v;
+        break;
+    case CJ_EPI_ACCUM:
+        if (live) Y[a.y_off + r] = __fadd_rn(Y[a.y_off + r], v);
+        break;
+    case CJ_EPI_QKV_ROPE: {
+        if (!live || (t & 1)) break;
+        const int hd = a.head_dim, half = hd >> 1;
+        const int64_t qrows = (int64_t)a.n_q * hd, krows = (int64_t)a.n_kv * hd;
+        if (r < qrows + krows) {
+            // GGUF pair order: row h·hd + 2b + a holds HF dim a·half + b
+            const int64_t rr = r < qrows ? r : r - qrows;
+            const int h = (int)(rr / hd), bb = (int)(rr % hd) >> 1;
+            const float2 cs = *(const float2 *)(a.rope_cs + 2 * ((int64_t)pos * half + bb));
+            const float ra = __fsub_rn(__fmul_rn(v, cs.x), __fmul_rn(vp, cs.y));
+            const float rb = __fadd_rn(__fmul_rn(v, cs.y), __fmul_rn(vp, cs.x));
+            if (r < qrows) {
+                a.q_out[(int64_t)h * hd + bb] = ra;
+                a.q_out[(int64_t)h * hd + half + bb] = rb;
             } else {
-                const int64_t rr = r0 - qrows - krows;
-                const int h = (int)(rr / hd), d = (int)(rr % hd);
-                const int64_t vi = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
-                a.vc[vi + d] = f2h(v0);
-                a.vc[vi + d + 1] = f2h(v1);
+                const int64_t ki = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+                a.kc[ki + bb] = f2h(ra);
+                a.kc[ki + half + bb] = f2h(rb);
             }
-        } break;
-        case CJ_EPI_GLU: {
-            if (r0 >= a.rows) break;
-            const int64_t ai = r0 >> 1;
-            ACT[ai] = a.glu_form ? silu_tanh_mul(v0, v1) : __fmul_rn(silu_exp(v0), v1);
-        } break;
-        case CJ_EPI_ARGMAX: {
-            if (r0 < a.rows) {
-                a.y[r0] = v0;
-                if (best_i < 0 || v0 > best_v) { best_v = v0; best_i = (int)r0; }
-            }
-            if (r1 < a.rows) {
-                a.y[r1] = v1;
-                if (best_i < 0 || v1 > best_v) { best_v = v1; best_i = (int)r1; }
-            }
-        } break;
+        } else {
+            const int64_t rr = r - qrows - krows;
+            const int h = (int)(rr / hd), d = (int)(rr % hd);
+            const int64_t vi = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+            a.vc[vi + d] = f2h(v);
+            a.vc[vi + d + 1] = f2h(vp);
         }
+    } break;
+    case CJ_EPI_GLU:
+        if (live && !(t & 1)) ACT[r >> 1] = glu_value(a.glu_form, r >> 1, a.act_n, v, vp);
+        break;
+    default:
+        break;
     }
 
     if (a.epi == CJ_EPI_GLU && a.act_pack) {
@@ -439,8 +458,8 @@ DEV void gemv_body(const cj_gemv_args &a) {
         __shared__ int n_last;
         __threadfence();
         __syncthreads();
-        const int64_t a0 = (wg * a.rows_per_wg) >> 1;
-        int64_t a1 = a0 + (a.rows_per_wg >> 1);
+        const int64_t a0 = row0 >> 1;
+        int64_t a1 = a0 + (R >> 1);
         if (a1 > (a.rows >> 1)) a1 = a.rows >> 1;
         if (t == 0) {
             n_last = 0;
@@ -459,7 +478,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
             __threadfence();
             for (int k = 0; k < nl; k++) {
                 const int blk = last_blocks[k];
-                pack_block_global(a.act, a.act_n, blk, a.act_per32, a.act_pack, bmax);
+                pack_block_global(ACT, a.act_n, blk, a.act_per32, a.act_pack, bmax);
                 if (t == 0) a.counters[blk] = 0;
             }
         }
@@ -469,16 +488,12 @@ DEV void gemv_body(const cj_gemv_args &a) {
         __shared__ float bv[256];
         __shared__ int bi[256];
         __shared__ int ticket;
-        bv[t] = best_v;
-        bi[t] = best_i;
+        if (live) Y[r] = v;
+        bv[t] = v;
+        bi[t] = live ? (int)r : -1;
         __syncthreads();
         for (int s = 128; s > 0; s >>= 1) {
-            if (t < s) {
-                float ov = bv[t + s]; int oi = bi[t + s];
-                float mv = bv[t]; int mi = bi[t];
-                bool take = mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)));
-                if (take) { bv[t] = ov; bi[t] = oi; }
-            }
+            if (t < s && argmax_take(bv[t + s], bi[t + s], bv[t], bi[t])) { bv[t] = bv[t + s]; bi[t] = bi[t + s]; }
             __syncthreads();
         }
         if (t == 0) {
@@ -490,21 +505,18 @@ DEV void gemv_body(const cj_gemv_args &a) {
         __syncthreads();
         if (ticket != (int)gridDim.x - 1) return;
         __threadfence();
-        float gb = 0.0f; int gi = -1;
-        for (int g = t; g < (int)gridDim.x; g += 256) {
-            float x = __builtin_nontemporal_load(&a.part_v[g]);
-            int xi = __builtin_nontemporal_load(&a.part_i[g]);
-            if (xi >= 0 && (gi < 0 || x > gb || (x == gb && xi < gi))) { gb = x; gi = xi; }
+        float gb = 0.0f;
+        int gi = -1;
+        for (int gg = t; gg < (int)gridDim.x; gg += 256) {
+            const float x = a.part_v[gg];
+            const int xi = a.part_i[gg];
+            if (argmax_take(x, xi, gb, gi)) { gb = x; gi = xi; }
         }
-        bv[t] = gb; bi[t] = gi;
+        bv[t] = gb;
+        bi[t] = gi;
         __syncthreads();
         for (int s = 128; s > 0; s >>= 1) {
-            if (t < s) {
-                float ov = bv[t + s]; int oi = bi[t + s];
-                float mv = bv[t]; int mi = bi[t];
-                bool take = mi < 0 || (oi >= 0 && (ov > mv || (ov == mv && oi < mi)));
-                if (take) { bv[t] = ov; bi[t] = oi; }
-            }
+            if (t < s && argmax_take(bv[t + s], bi[t + s], bv[t], bi[t])) { bv[t] = bv[t + s]; bi[t] = bi[t + s]; }
             __syncthreads();
         }
         if (t == 0) {

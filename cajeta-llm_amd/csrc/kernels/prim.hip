@@ -28,9 +28,6 @@ extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
 
 // ------------------------------------------------------------------ glu
 
-DEV float silu_exp_p(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, __expf(0.0f - x))); }
-DEV float silu_tanh_mul_p(float x, float u);
-
 // One workgroup per 256-wide block: out = act(g)·u, then (optionally) that
 // block's pack — the block is local, so no other workgroup is waited on.
 extern "C" __global__ void __launch_bounds__(256) cj_glu(cj_glu_args a) {
@@ -39,8 +36,7 @@ extern "C" __global__ void __launch_bounds__(256) cj_glu(cj_glu_args a) {
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     float v = 0.0f;
     if (e < a.n) {
-        const float g = a.g[e], u = a.u[e];
-        v = a.form ? silu_tanh_mul_p(g, u) : __fmul_rn(silu_exp_p(g), u);
+        v = glu_value(a.form, e, a.n, a.g[e], a.u[e]);
         a.out[e] = v;
     }
     if (!a.packed) return;
@@ -69,28 +65,6 @@ extern "C" __global__ void __launch_bounds__(256) cj_glu(cj_glu_args a) {
         if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
         pack_zero_pad(ob, t);
     }
-}
-
-DEV float silu_tanh_mul_p(float x, float u) {
-    const float tlo = -7.90531110763549805f;
-    float xa = fmaxf(x, -16.0f);
-    float xb = __fsub_rn(-16.0f, xa);
-    float xc = __fsub_rn(-16.0f, fmaxf(xb, -32.0f));
-    float t0 = __fmul_rn(0.5f, __fmaf_rn(__fmul_rn(0.0f, xc), __fmul_rn(xc, xc), xc));
-    float ta = fmaxf(t0, tlo);
-    float tb = __fsub_rn(tlo, ta);
-    float t = __fsub_rn(tlo, fmaxf(tb, -15.8106222152709961f));
-    float t2 = __fmul_rn(t, t);
-    float p = __fmaf_rn(-2.76076847742355e-16f, t2, 2.00018790482477e-13f);
-    p = __fmaf_rn(p, t2, -8.60467152213735e-11f);
-    p = __fmaf_rn(p, t2, 5.12229709037114e-08f);
-    p = __fmaf_rn(p, t2, 1.48572235717979e-05f);
-    p = __fmaf_rn(p, t2, 6.37261928875436e-04f);
-    p = __fmul_rn(__fmaf_rn(p, t2, 4.89352455891786e-03f), t);
-    float q = __fmaf_rn(1.19825839466702e-06f, t2, 1.18534705686654e-04f);
-    q = __fmaf_rn(q, t2, 2.26843463243900e-03f);
-    q = __fmaf_rn(q, t2, 4.89352518554385e-03f);
-    return __fmul_rn(__fmul_rn(__fmul_rn(0.5f, xa), __fadd_rn(1.0f, __fdiv_rn(p, q))), u);
 }
 
 extern "C" __global__ void __launch_bounds__(256) cj_add(cj_add_args a) {
@@ -311,7 +285,7 @@ extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
         float mx = lg[0];
         for (int e = 1; e < a.n_experts; e++) if (lg[e] > mx) mx = lg[e];
         float sum = 0.0f;
-        for (int e = 0; e < a.n_experts; e++) { const float p = expf(lg[e] - mx); pr[e] = p; sum = __fadd_rn(sum, p); }
+        for (int e = 0; e < a.n_experts; e++) { const float p = cj_expf(lg[e] - mx); pr[e] = p; sum = __fadd_rn(sum, p); }
         for (int e = 0; e < a.n_experts; e++) pr[e] = __fdiv_rn(pr[e], sum);
         float w[16];
         int s[16];

@@ -76,7 +76,7 @@ struct Engine {
     float *out_norm = nullptr;
     DevW head;
     std::vector<Layer> layers;
-    int pages_per_seq = 0, splits = 1;
+    int pages_per_seq = 0, workers = 512;
     int32_t *pgtab = nullptr;
     float *rope = nullptr;
     // scratch
@@ -288,8 +288,6 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     CJ_HIP(hipMemcpy(pgtab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
     if ((rc = cj_rope_table((int64_t)(uintptr_t)rope, head_dim, theta, ctx))) return rc;
 
-    const int cus = device_cus() > 0 ? device_cus() : 256;
-    splits = std::max(1, std::min(64, (cus + n_kv - 1) / n_kv));
     const int64_t fmax = std::max<int64_t>(ffn, (int64_t)expert_ffn * std::max(1, n_used));
     const int64_t fpad = (std::max<int64_t>(ffn, expert_ffn) + 255) / 256 * 256;
     hs = (float *)alloc((size_t)hidden * 4);
@@ -298,7 +296,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     act = (float *)alloc((size_t)fmax * 4 + 1024);
     act_pack = (uint8_t *)alloc((size_t)fpad / 256 * 320);
     logits = (float *)alloc((size_t)vocab * 4);
-    part = (float *)alloc((size_t)n_heads * splits * (head_dim + 2) * 4);
+    // split-K partials [n_heads][64][hd + 2], or two-pass scores [n_heads][ctx]
+    part = (float *)alloc((size_t)n_heads * std::max<int64_t>(64 * (head_dim + 2), ctx) * 4);
     glu_counters = (int32_t *)alloc((size_t)fpad / 256 * 4 + 64);
     argmax_counter = (int32_t *)alloc(64);
     attn_counters = (int32_t *)alloc((size_t)n_kv * 4 + 64);
@@ -344,8 +343,13 @@ int Engine::enqueue_step(int s) {
     }
     const int grp = n_heads / n_kv;
     const bool per32 = wtype == CJ_Q8_0;
-    char attn_kernel[64];
-    snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_decode_h%d_g%d", head_dim, grp);
+    // the reference's choice of form: split-K for hd 128 with 4 or 8 query
+    // heads a kv head, else the two-pass score/combine
+    const bool split = head_dim == 128 && (grp == 4 || grp == 8);
+    char attn_kernel[64], combine_kernel[64];
+    if (split) snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_split_h128_g%d", grp);
+    else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
+    snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
         {   // 1. q|k|v with norm+pack prologue, RoPE + K/V append epilogue
@@ -360,9 +364,17 @@ int Engine::enqueue_step(int s) {
         {   // 2. attention
             cj_attn_args a{};
             a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
-            a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.splits = splits;
+            a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
             a.pg_base = S.pg_base; a.window = L.window; a.scale = scale;
-            if ((rc = launch(attn_kernel, (uint32_t)(n_kv * splits), 256, 0, a))) return rc;
+            if (split) {
+                if ((rc = launch(attn_kernel, (uint32_t)(n_kv * 64), (uint32_t)(grp * 16), 0, a))) return rc;
+            } else {
+                // the grid covers the longest window; the kernel idles past count
+                a.splits = ctx;
+                const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
+                if ((rc = launch(attn_kernel, (uint32_t)(((int64_t)n_heads * span + 7) / 8), 256, 0, a))) return rc;
+                if ((rc = launch(combine_kernel, (uint32_t)n_heads, 128, 0, a))) return rc;
+            }
         }
         {   // 3. o projection, residual into hs
             cj_gemv_args a{};
@@ -568,7 +580,7 @@ int32_t cj_engine_config(int64_t h, int64_t *out, int32_t n) {
     Engine *e = eng_of(h);
     if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
     int64_t v[] = {e->n_layers, e->hidden, e->n_heads, e->n_kv, e->head_dim, e->ffn, e->vocab, e->ctx,
-                   e->n_experts, e->n_used, e->wtype, e->head_type, e->expert_ffn, e->splits};
+                   e->n_experts, e->n_used, e->wtype, e->head_type, e->expert_ffn, e->workers};
     for (int i = 0; i < n && i < (int)(sizeof v / sizeof v[0]); i++) out[i] = v[i];
     return CJ_OK;
 }

@@ -47,11 +47,11 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"gluF32", "cj_glu"},
         {"addF32", "cj_add"},
         {"qkPrepKernel", "cj_qkprep"},
-        {"attnFlashDecodeGqa1Kernel", "cj_attn_decode_h128_g1"},
-        {"attnFlashDecodeGqa4Kernel", "cj_attn_decode_h128_g4"},
-        {"attnFlashDecodeGqa8Kernel", "cj_attn_decode_h128_g8"},
-        {"attnScoreKernel", "cj_attn_decode_h64_g4"},
-        {"attnCombineKernel", "cj_attn_decode_h64_g4"},
+        {"attnFlashDecodeGqa4Kernel", "cj_attn_split_h128_g4"},
+        {"attnFlashDecodeGqa8Kernel", "cj_attn_split_h128_g8"},
+        {"attnDecodeCpuGqaKernel", "cj_attn_split_h128_g4"},
+        {"attnScoreKernel", "cj_attn_scores_h64"},
+        {"attnCombineKernel", "cj_attn_combine_h64"},
         {"attnReducePackQ8Kernel", "cj_attn_merge"},
         {"argmaxRowKernel", "cj_argmax"},
         {"embedRowQ4kKernel", "cj_embed"},
@@ -163,12 +163,17 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
     const int groups = 64 / lpr;
     int rpg = rows_per_group > 0 ? rows_per_group : 2;
     if (rpg & 1) rpg++;
+    // one thread per row folds the row's block terms: at most 256 rows
+    while (4 * groups * rpg > 256 && rpg > 2) rpg -= 2;
     p.rows_per_wg = 4 * groups * rpg;
     p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
     p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
     p.per_copy = p.grid;
     const int64_t nblk = (cols + 255) / 256;
-    p.lds = 3072 + (uint32_t)(is_f32_act(type) ? nblk * 256 * 4 : nblk * 320);
+    // LDS: scratch, the staged activation, then R rows of block terms
+    const int64_t terms = type == CJ_Q4_K ? cols / 256 * 2 : type == CJ_Q6_K ? cols / 256
+                        : type == CJ_Q8_0 ? (cols / 32 + 7) / 8 : 1;
+    p.lds = 3072 + (uint32_t)(is_f32_act(type) ? nblk * 256 * 4 : nblk * 320) + (uint32_t)(p.rows_per_wg * terms * 4);
     return p;
 }
 
@@ -209,8 +214,8 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_mxfp4_l64", "cj_gemv_mxfp4_l32", "cj_gemv_mxfp4_l16", "cj_gemv_mxfp4_l8",
         "cj_gemv_f32_l64", "cj_gemv_f32_l32", "cj_gemv_f32_l16", "cj_gemv_f32_l8", "cj_moe_combine",
         "cj_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
-        "cj_attn_decode_h128_g1", "cj_attn_decode_h128_g2", "cj_attn_decode_h128_g4", "cj_attn_decode_h128_g8",
-        "cj_attn_decode_h64_g1", "cj_attn_decode_h64_g2", "cj_attn_decode_h64_g4", "cj_attn_decode_h64_g8",
+        "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
+        "cj_attn_combine_h64", "cj_attn_combine_h128",
         "cj_attn_merge", "cj_qkprep", "cj_zero", "cj_moe_route",
     };
     for (const char *k : kernels) {
@@ -482,15 +487,17 @@ int32_t cj_qk_prep(int64_t q, int64_t k, int64_t v, int64_t kcache, int64_t vcac
 
 int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t vcache, int64_t pgtab, int32_t pg_base,
                   int64_t counters, int32_t n_q, int32_t n_kv, int32_t head_dim, int32_t count, int32_t from,
-                  int32_t splits, float scale) {
-    if (n_kv <= 0 || n_q % n_kv || (head_dim != 64 && head_dim != 128) || count <= 0 || from < 0 || splits <= 0 || splits > 256)
-        return fail(CJ_ERR_ARG, "cj_attend: heads %d/%d hd %d count %d splits %d", n_q, n_kv, head_dim, count, splits);
+                  int32_t workers, float scale) {
+    if (n_kv <= 0 || n_q <= 0 || n_q % n_kv || (head_dim != 64 && head_dim != 128) || count <= 0 || from < 0 || workers <= 0)
+        return fail(CJ_ERR_ARG, "cj_attend: heads %d/%d hd %d count %d workers %d", n_q, n_kv, head_dim, count, workers);
     const int grp = n_q / n_kv;
-    if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return fail(CJ_ERR_ARG, "cj_attend: GQA group %d not served", grp);
+    const bool split = head_dim == 128 && (grp == 4 || grp == 8);
     const int64_t pages = ((int64_t)from + count + 63) / 64;
+    const int64_t part_bytes = split ? (int64_t)n_q * 64 * (head_dim + 2) * 4 : (int64_t)n_q * count * 4;
     if (!in_buffer(dptr(pgtab + 4 * pg_base), pages * 4) || !in_buffer(dptr(q), (int64_t)n_q * head_dim * 4) ||
-        !in_buffer(dptr(part), (int64_t)n_q * splits * (head_dim + 2) * 4) ||
-        (out && (!in_buffer(dptr(out), (int64_t)n_q * head_dim * 4) || !in_buffer(dptr(counters), (int64_t)n_kv * 4))))
+        !in_buffer(dptr(part), part_bytes) || (!split && !out) ||
+        (out && !in_buffer(dptr(out), (int64_t)n_q * head_dim * 4)) ||
+        (split && out && !in_buffer(dptr(counters), (int64_t)n_kv * 4)))
         return fail(CJ_ERR_ARG, "cj_attend: a buffer is smaller than the shapes need");
     std::vector<int32_t> tab((size_t)pages);
     CJ_HIP(hipMemcpyAsync(tab.data(), dptr(pgtab + 4 * pg_base), (size_t)pages * 4, hipMemcpyDeviceToHost, g.stream));
@@ -506,16 +513,28 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     cj_attn_args a{};
     a.part = (float *)dptr(part); a.out = (float *)dptr(out); a.q = (const float *)dptr(q);
     a.kc = (const uint16_t *)dptr(kcache); a.vc = (const uint16_t *)dptr(vcache); a.pgtab = (const int32_t *)dptr(pgtab);
-    a.counters = (int32_t *)dptr(counters); a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim; a.splits = splits;
-    a.pg_base = pg_base; a.count = count; a.from = from; a.window = 0; a.scale = scale;
+    a.counters = (int32_t *)dptr(counters); a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim;
+    a.pg_base = pg_base; a.count = count; a.from = from; a.window = 0; a.workers = workers; a.scale = scale;
     char name[64];
-    snprintf(name, sizeof name, "cj_attn_decode_h%d_g%d", head_dim, grp);
-    return launch(name, (uint32_t)(n_kv * splits), 256, 0, a);
+    if (split) {
+        snprintf(name, sizeof name, "cj_attn_split_h128_g%d", grp);
+        return launch(name, (uint32_t)(n_kv * 64), (uint32_t)(grp * 16), 0, a);
+    }
+    a.splits = count;   // the scores row stride
+    snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
+    if (int32_t rc = launch(name, (uint32_t)(((int64_t)n_q * count + 7) / 8), 256, 0, a)) return rc;
+    snprintf(name, sizeof name, "cj_attn_combine_h%d", head_dim);
+    return launch(name, (uint32_t)n_q, 128, 0, a);
+}
+
+int32_t cj_decode_splits(int32_t count, int32_t n_kv, int32_t workers) {
+    const int w = workers < 1 ? 1 : workers, rk = n_kv < 1 ? 1 : n_kv;
+    return std::max(1, std::min({64, count, (2 * w + rk - 1) / rk}));
 }
 
 int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, int32_t head_dim, int32_t splits, int32_t per32) {
     const int64_t n = (int64_t)n_q * head_dim, npad = (n + 255) / 256 * 256;
-    if (n <= 0 || splits <= 0 || !in_buffer(dptr(part), (int64_t)n_q * splits * (head_dim + 2) * 4) ||
+    if (n <= 0 || splits <= 0 || splits > 64 || !in_buffer(dptr(part), (int64_t)n_q * 64 * (head_dim + 2) * 4) ||
         (out && !in_buffer(dptr(out), n * 4)) || (packed && !in_buffer(dptr(packed), npad / 256 * 320)) || (!out && !packed))
         return fail(CJ_ERR_ARG, "cj_attn_merge: buffers smaller than the shapes need");
     cj_merge_args a{(float *)dptr(out), (uint8_t *)dptr(packed), (const float *)dptr(part), n_q, head_dim, splits, per32};

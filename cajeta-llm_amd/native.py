@@ -46,6 +46,7 @@ SIGNATURES = {
     "cj_rope_table": (I32, [I64, I32, F32, I32]),
     "cj_qk_prep": (I32, [I64, I64, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32, I32, F32, I32, I32]),
     "cj_attend": (I32, [I64, I64, I64, I64, I64, I64, I32, I64, I32, I32, I32, I32, I32, I32, F32]),
+    "cj_decode_splits": (I32, [I32, I32, I32]),
     "cj_attn_merge": (I32, [I64, I64, I64, I32, I32, I32, I32]),
     "cj_embed_row": (I32, [I64, I64, I32, I64, I32]),
     "cj_argmax_row": (I32, [I64, I32, I64, I64]),

@@ -134,17 +134,32 @@ int32_t cj_qk_prep(int64_t q, int64_t k, int64_t v, int64_t kcache, int64_t vcac
                    int64_t rope, int64_t pgtab, int32_t pg_base, int32_t n_q, int32_t n_kv, int32_t head_dim,
                    int32_t norm, float eps, int32_t form, int32_t pos);
 
-/* Split-K decode attention over positions [from, from+count): partials
- * [n_q][splits][hd+2] into `part`; when out != 0 the last split of each kv
- * head merges into out [n_q·hd]. Replaces
- * AttnKernel.attendDecodePartialsLaunchNoSync (model/AttnKernel.cajeta:5090-5135)
- * and, with out, attendDecodeLaunchNoSync (:6900-6970). counters: n_kv int32
- * words left zeroed by the launch. */
+/* Decode attention of n_q query heads over positions [from, from+count) of
+ * the paged fp16 K/V, in the form the reference picks by shape:
+ *  - head_dim 128 with 4 or 8 query heads per kv head: split-K into
+ *    cj_decode_splits(count, n_kv, workers) splits, partials
+ *    [n_q][64][hd+2] (acc, max, sum) into `part`; when out != 0 the last
+ *    split of each kv head merges into out [n_q·hd] (counters: n_kv int32
+ *    words, zero before the call and left zero after). Replaces
+ *    AttnKernel.attnDecodeCpuGqaKernel / cpuDecodeHead
+ *    (model/AttnKernel.cajeta:4216-4314) behind
+ *    attendDecodePartialsLaunchNoSync (:5090-5135) and, with out,
+ *    attendDecodeLaunchNoSync (:6900-6970).
+ *  - otherwise: scores [n_q][count] into `part`, then softmax and the
+ *    weighted sum into out (required). Replaces attnScoreKernel +
+ *    attnCombineKernel (:397-515).
+ * `workers` is the CPU backend's worker count the split rule uses. */
 int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t vcache, int64_t pgtab,
                   int32_t pg_base, int64_t counters, int32_t n_q, int32_t n_kv, int32_t head_dim,
-                  int32_t count, int32_t from, int32_t splits, float scale);
+                  int32_t count, int32_t from, int32_t workers, float scale);
 
-/* Merge split partials into f32 out and/or their pack. Replaces
+/* Splits of a split-K decode attend: two work items a worker over the kv
+ * heads, within [1, min(64, count)]. Replaces AttnKernel.cpuDecodeSplits
+ * (model/AttnKernel.cajeta:4879-4889). */
+int32_t cj_decode_splits(int32_t count, int32_t n_kv, int32_t workers);
+
+/* Merge the first `splits` split partials ([n_q][64][hd+2] as cj_attend
+ * writes them) into f32 out and/or their pack. Replaces
  * attnReducePackQ8Kernel (model/AttnKernel.cajeta:5165-5259). */
 int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, int32_t head_dim,
                       int32_t splits, int32_t per32);

@@ -71,7 +71,7 @@ class GgufReader:
         raise ValueError("unknown GGUF value type %d" % ty)
 
 
-def model_config(r, workers=16, kv_f32=False, ctx=None):
+def model_config(r, workers=512, kv_f32=False, ctx=None):
     """The oracle's config from GGUF metadata (model/ModelConfig.cajeta:172-320)."""
     m = r.meta
     arch = m["general.architecture"]

@@ -410,12 +410,38 @@ void or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, 
     }
 }
 
+/* exp(x) in f32, written out so that the kernels compute the same bits:
+ * n = rint(x·log2 e); r = x − n·ln2 (Cody–Waite, two fma steps, ln2_hi with
+ * trailing zeros); e^r by the degree-7 Taylor polynomial in Horner form with
+ * fma (|r| ≤ ln2/2, truncation < 4e-9 relative); then ·2^n in two exact
+ * power-of-two steps. Every step is an IEEE-754 correctly rounded operation,
+ * so any conforming implementation gives these bits. The reference's
+ * Cajeta stdlib Math.exp is not available; ULP parity with it is unpinned. */
+float or_expf(float x) {
+    if (x != x) return x;
+    if (x < -104.0f) return 0.0f;
+    if (x > 88.72283935546875f) return INFINITY;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.428606765330187045e-06f, r);
+    float p = 1.98412698412698413e-04f;
+    p = fmaf(p, r, 1.38888888888888889e-03f);
+    p = fmaf(p, r, 8.33333333333333333e-03f);
+    p = fmaf(p, r, 4.16666666666666667e-02f);
+    p = fmaf(p, r, 1.66666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n, n1 = ni / 2, n2 = ni - n1;
+    return p * bits_f((uint32_t)(n1 + 127) << 23) * bits_f((uint32_t)(n2 + 127) << 23);
+}
+
 /* SwiGLU, exp form (Prim.gluF32/gluOne, L/model/Prim.cajeta:160-196):
  * silu(g) = g / (1 + exp(-g)). */
 void or_glu_exp(const float *g, const float *u, int64_t n, float *out) {
     for (int64_t i = 0; i < n; i++) {
         float x = g[i];
-        float a = x / (1.0f + expf(0.0f - x));
+        float a = x / (1.0f + or_expf(0.0f - x));
         out[i] = a * u[i];
     }
 }
@@ -449,8 +475,9 @@ static float glu_tanh_one(float x, float u) {
 void or_glu_tanh(const float *g, const float *u, int64_t n, float *out) {
     for (int64_t b0 = 0; b0 < n; b0 += 4096) {
         int64_t hi = b0 + 4096 < n ? b0 + 4096 : n, i = b0;
-        for (; i + 16 <= hi; i++) out[i] = glu_tanh_one(g[i], u[i]);
-        for (; i < hi; i++) { float x = g[i]; out[i] = x / (1.0f + expf(0.0f - x)) * u[i]; }
+        for (; i + 16 <= hi; i += 16)
+            for (int j = 0; j < 16; j++) out[i + j] = glu_tanh_one(g[i + j], u[i + j]);
+        for (; i < hi; i++) { float x = g[i]; out[i] = x / (1.0f + or_expf(0.0f - x)) * u[i]; }
     }
 }
 
@@ -491,7 +518,7 @@ int or_moe_route(const float *lb, int ne, int k, int norm, int32_t *sel, float *
     float mx = lb[0];
     for (int e = 1; e < ne; e++) if (lb[e] > mx) mx = lb[e];
     float sum = 0.0f;
-    for (int e = 0; e < ne; e++) { float p = expf(lb[e] - mx); probs[e] = p; sum = sum + p; }
+    for (int e = 0; e < ne; e++) { float p = or_expf(lb[e] - mx); probs[e] = p; sum = sum + p; }
     for (int e = 0; e < ne; e++) probs[e] = probs[e] / sum;
     for (int j = 0; j < k; j++) {
         int best = -1; float bp = 0.0f;
@@ -555,12 +582,12 @@ static void decode_head(const float *q, const void *kp, const void *vp, int f32,
         float sc = ((((dl[0] + dl[1]) + (dl[2] + dl[3])) + ((dl[4] + dl[5]) + (dl[6] + dl[7])))
                     + (((dl[8] + dl[9]) + (dl[10] + dl[11])) + ((dl[12] + dl[13]) + (dl[14] + dl[15])))) * scale;
         if (sc > m) {
-            float c = expf(m - sc);
+            float c = or_expf(m - sc);
             for (int d = 0; d < hd; d++) acc[d] = acc[d] * c;
             l = l * c;
             m = sc;
         }
-        float p = expf(sc - m);
+        float p = or_expf(sc - m);
         l = l + p;
         for (int d = 0; d < hd; d++) acc[d] = acc[d] + kv_at(vp, f32, ko + d) * p;
     }
@@ -604,7 +631,7 @@ void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, 
                     const float *pb = pb0 + sp * stride;
                     float ls = pb[hd + 1];
                     if (ls > 0.0f) {
-                        float wt = expf(pb[hd] - gm);
+                        float wt = or_expf(pb[hd] - gm);
                         gl = gl + wt * ls;
                         for (int d = 0; d < hd; d++) a[d] = a[d] + pb[d] * wt;
                     }
@@ -617,22 +644,43 @@ void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, 
         }
         free(part);
     } else {
-        /* attnScoreKernel (:397-425) + attnCombineKernel (:441-515): scores
-         * q·k·scale, softmax with max and exp sums, then Σ_t p_t·v_t in
-         * ascending t, scaled once by 1/Σp. */
+        /* attnScoreKernel (:397-425): lane i of 32 sums q[d]·k[d] over
+         * d = i, i+32, ... in order; the 32 lane sums fold as a butterfly
+         * (lane distance 16, 8, 4, 2, 1 — the wave reduction, whose order the
+         * reference's stdlib leaves open); × scale.
+         * attnCombineKernel (:441-515): 128 lanes, lane l over t = l, l+128, ...:
+         * max (exact in any order), exp(s − max) and its lane sums, the lane
+         * sums folded with strides 64, ..., 1; then Σ_t p_t·v_t in ascending t,
+         * scaled once by 1/Σp. */
         float *sc = (float *)malloc(sizeof(float) * (size_t)count);
         for (int h = 0; h < nh; h++) {
             int kvh = h / group;
             const float *qh = q + (int64_t)h * hd;
             for (int t = 0; t < count; t++) {
-                float s = 0.0f;
-                for (int d = 0; d < hd; d++) s = s + qh[d] * kv_at(kp, f32, (int64_t)t * kvdim + kvh * hd + d);
-                sc[t] = s * scale;
+                float ls[32];
+                for (int i = 0; i < 32; i++) {
+                    float s = 0.0f;
+                    for (int d = i; d < hd; d += 32) s = s + qh[d] * kv_at(kp, f32, (int64_t)t * kvdim + kvh * hd + d);
+                    ls[i] = s;
+                }
+                for (int m = 16; m > 0; m >>= 1) {
+                    float nx[32];
+                    for (int i = 0; i < 32; i++) nx[i] = ls[i] + ls[i ^ m];
+                    memcpy(ls, nx, sizeof nx);
+                }
+                sc[t] = ls[0] * scale;
             }
             float mx = -3.0e38f;
             for (int t = 0; t < count; t++) if (sc[t] > mx) mx = sc[t];
-            float sum = 0.0f;
-            for (int t = 0; t < count; t++) { float e = expf(sc[t] - mx); sc[t] = e; sum = sum + e; }
+            float red[128];
+            for (int l = 0; l < 128; l++) {
+                float s = 0.0f;
+                for (int t = l; t < count; t += 128) { float e = or_expf(sc[t] - mx); sc[t] = e; s = s + e; }
+                red[l] = s;
+            }
+            for (int r = 64; r > 0; r >>= 1)
+                for (int l = 0; l < r; l++) red[l] = red[l] + red[l + r];
+            float sum = red[0];
             float rs = 1.0f / sum;
             for (int d = 0; d < hd; d++) {
                 float acc = 0.0f;

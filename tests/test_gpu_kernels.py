@@ -39,6 +39,7 @@ def golden(name):
 
 
 FORMATS = [("q8_0", 8), ("q4_0", 2), ("q4_k", 12), ("q6_k", 14), ("mxfp4", 39)]
+EXACT = (8, 12, 14)      # int8-activation formats: the fold over blocks is the reference's
 
 
 @pytest.mark.parametrize("name,ty", [f for f in FORMATS if f[0] != "mxfp4"])
@@ -106,22 +107,25 @@ def test_pack_is_bit_exact(gpu, O, per32, n):
 @pytest.mark.parametrize("dim", [512, 4096, 2880])
 @pytest.mark.parametrize("per32", [0, 1])
 def test_rmsnorm_pack(gpu, O, dim, per32):
+    """Whole 256s: the CPU row form's 256-lane tree; other widths: the host
+    floor's element-order sum. The kernel makes the same adds and a correctly
+    rounded sqrt and divide, so the same bits, over many rows (a 1-ulp error
+    in the scale shows on a fraction of rows only)."""
     say("rmsnorm_pack", dim, per32)
-    rng = np.random.default_rng(dim)
-    x = (rng.standard_normal(dim) * 3).astype(np.float32)
-    w = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    rng = np.random.default_rng(dim + per32)
     npad = (dim + 255) // 256 * 256
-    xb, wb, ob, pb = gpu.Buffer.of(x), gpu.Buffer.of(w), gpu.Buffer(dim * 4), gpu.Buffer(npad // 256 * 320)
-    gpu.native.check(gpu.native.lib().cj_rmsnorm_pack(ob.h, pb.h, xb.h, wb.h, dim, 1e-5, 0, per32), "rmsnorm_pack")
-    got = ob.download(np.float32, dim)
-    ref = O.rmsnorm(x, w, 1e-5)
-    if dim % 256 == 0:
-        # the CPU row form's 256-lane tree: the same adds, so the same bits
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    wb, ob, pb = gpu.Buffer.of(w), gpu.Buffer(dim * 4), gpu.Buffer(npad // 256 * 320)
+    lib = gpu.native.lib()
+    for row in range(48):
+        x = (rng.standard_normal(dim) * rng.uniform(0.05, 8)).astype(np.float32)
+        xb = gpu.Buffer.of(x)
+        gpu.native.check(lib.cj_rmsnorm_pack(ob.h, pb.h, xb.h, wb.h, dim, 1e-5, 0, per32), "rmsnorm_pack")
+        got = ob.download(np.float32, dim)
+        ref = O.rmsnorm(x, w, 1e-5)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "row %d" % row
         assert np.array_equal(pb.download(np.uint8, npad // 256 * 320), O.q8k_pack(ref, per32=bool(per32), npad=npad))
-    else:
-        # a width with a remainder: the host floor sums sequentially (|rel| < 1e-6)
-        assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+        xb.free()
 
 
 def matvec_case(gpu, O, ty, rows, cols, seed, accum=False):
@@ -154,8 +158,14 @@ def matvec_case(gpu, O, ty, rows, cols, seed, accum=False):
 def test_matvec_matches_oracle(gpu, O, name, ty, rows, cols):
     say("matvec", name, rows, cols)
     got, ref, raw, x = matvec_case(gpu, O, ty, rows, cols, rows + cols + ty)
-    # integer sub-block dots are exact; only the f32 sum over blocks is
-    # re-associated (tree across lanes vs the oracle's block order)
+    if ty in EXACT:
+        # integer sub-block dots, then the f32 fold over blocks in the
+        # reference's block order: the same bits
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+            "%s %dx%d: %d rows differ" % (name, rows, cols, int((got != ref).sum()))
+        return
+    # f32-activation formats sum lanes as a tree (the reference sums each row
+    # in element order): within float rounding of the row's magnitude
     scale = np.abs(ref).max() + 1e-6
     err = np.abs(got - ref).max() / scale
     assert err < 2e-6, "%s %dx%d: rel err %.3g" % (name, rows, cols, err)
@@ -164,7 +174,7 @@ def test_matvec_matches_oracle(gpu, O, name, ty, rows, cols):
 @pytest.mark.parametrize("name,ty", [("q4_k", 12), ("q8_0", 8)])
 def test_matvec_accumulate_store(gpu, O, name, ty):
     got, ref, _, _ = matvec_case(gpu, O, ty, 512, 4096, 7, accum=True)
-    assert np.abs(got - ref).max() < 2e-6 * (np.abs(ref).max() + 1)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 def test_matvec_refuses_short_buffers(gpu, O):
@@ -186,10 +196,9 @@ def test_glu_pack(gpu, O, form, n, per32):
     gpu.native.check(gpu.native.lib().cj_glu(ob.h, pb.h, gb.h, ub.h, n, form, per32), "glu")
     got = ob.download(np.float32, n)
     ref = O.glu(g, u, "tanh" if form else "exp")
-    if form:
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))   # fmaf/div are exact both sides
-    else:
-        assert np.allclose(got, ref, rtol=2e-6, atol=1e-7)                  # device exp vs glibc exp
+    # the rational tanh is fma/div (correctly rounded both sides); the exp
+    # form runs the same written-out expf on both sides: the same bits
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     # the pack of the device's own values is the oracle's pack of them, bit for bit
     assert np.array_equal(pb.download(np.uint8, npad // 256 * 320), O.q8k_pack(got, per32=bool(per32), npad=npad))
 
@@ -215,11 +224,11 @@ def to_paged(plane, n_kv, hd, pages):
 
 
 @pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (128, 4, 1), (128, 8, 1), (64, 8, 2), (64, 64, 8), (128, 8, 8)])
-@pytest.mark.parametrize("count,splits", [(1, 4), (37, 4), (300, 32), (2049, 32)])
-def test_attend_matches_oracle(gpu, O, hd, n_q, n_kv, count, splits):
-    say("attend", hd, n_q, n_kv, count, splits)
+@pytest.mark.parametrize("count,frm,workers", [(1, 0, 512), (37, 0, 16), (300, 5, 16), (2049, 0, 512), (130, 70, 3)])
+def test_attend_matches_oracle(gpu, O, hd, n_q, n_kv, count, frm, workers):
+    say("attend", hd, n_q, n_kv, count, frm, workers)
     rng = np.random.default_rng(count * 7 + hd + n_q)
-    pages = (count + 63) // 64 + 1
+    pages = (frm + count + 63) // 64 + 1
     ctx = pages * 64
     kf = (rng.standard_normal((ctx, n_kv * hd))).astype(np.float32)
     vf = (rng.standard_normal((ctx, n_kv * hd))).astype(np.float32)
@@ -228,29 +237,32 @@ def test_attend_matches_oracle(gpu, O, hd, n_q, n_kv, count, splits):
     scale = np.float32(1.0 / np.sqrt(hd))
     # a shuffled page table
     tab = rng.permutation(pages).astype(np.int32)
-    phys = np.zeros((pages * 64, n_kv * hd), np.uint16)
-    kp = np.zeros_like(phys); vp = np.zeros_like(phys)
+    kp = np.zeros((pages * 64, n_kv * hd), np.uint16); vp = np.zeros_like(kp)
     for p in range(ctx):
         row = tab[p // 64] * 64 + p % 64
         kp[row] = k16[p]; vp[row] = v16[p]
     kb, vb = gpu.Buffer.of(to_paged(kp, n_kv, hd, pages)), gpu.Buffer.of(to_paged(vp, n_kv, hd, pages))
     qb, tb = gpu.Buffer.of(q), gpu.Buffer.of(tab)
-    part, out, cnt = gpu.Buffer(n_q * splits * (hd + 2) * 4), gpu.Buffer(n_q * hd * 4), gpu.Buffer(4 * n_kv)
+    part = gpu.Buffer(n_q * max(64 * (hd + 2), count) * 4)
+    out, cnt = gpu.Buffer(n_q * hd * 4), gpu.Buffer(4 * n_kv)
     cnt.zero()
-    frm = 0
     lib = gpu.native.lib()
     gpu.native.check(lib.cj_attend(part.h, out.h, qb.h, kb.h, vb.h, tb.h, 0, cnt.h, n_q, n_kv, hd, count, frm,
-                                   splits, float(scale)), "attend")
+                                   workers, float(scale)), "attend")
     got = out.download(np.float32, n_q * hd)
-    mode = 0 if (hd == 128 and n_q in (4 * n_kv, 8 * n_kv)) else 1
-    spl = O.cpu_decode_splits(count, 1, n_kv, 16) if mode == 0 else 1
-    ref = O.attend(q, k16[:count], v16[:count], n_q, n_kv, hd, count, spl, float(scale), mode)
-    assert np.allclose(got, ref, rtol=1e-4, atol=2e-5), np.abs(got - ref).max()
-    # the merge kernel over the same partials gives the same output
-    out2 = gpu.Buffer(n_q * hd * 4)
-    gpu.native.check(lib.cj_attn_merge(out2.h, 0, part.h, n_q, hd, splits, 0), "merge")
-    assert np.allclose(out2.download(np.float32, n_q * hd), got, rtol=1e-6, atol=1e-7)
-    assert np.array_equal(cnt.download(np.int32, n_kv), np.zeros(n_kv, np.int32))
+    split = hd == 128 and n_q in (4 * n_kv, 8 * n_kv)
+    spl = O.cpu_decode_splits(count, 1, n_kv, workers) if split else 1
+    assert lib.cj_decode_splits(count, n_kv, workers) == O.cpu_decode_splits(count, 1, n_kv, workers)
+    ref = O.attend(q, k16[frm:frm + count], v16[frm:frm + count], n_q, n_kv, hd, count, spl, float(scale),
+                   0 if split else 1)
+    # the reference CPU backend's operation order on both sides: the same bits
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), np.abs(got - ref).max()
+    if split:
+        # the merge kernel over the same partials gives the same output
+        out2 = gpu.Buffer(n_q * hd * 4)
+        gpu.native.check(lib.cj_attn_merge(out2.h, 0, part.h, n_q, hd, spl, 0), "merge")
+        assert np.array_equal(out2.download(np.float32, n_q * hd).view(np.uint32), got.view(np.uint32))
+        assert np.array_equal(cnt.download(np.int32, n_kv), np.zeros(n_kv, np.int32))
 
 
 @pytest.mark.parametrize("hd,n_q,n_kv,theta", [(128, 32, 8, 500000.0), (64, 8, 2, 10000.0)])

@@ -47,10 +47,13 @@ def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1):
                 ref_toks.append(t)
                 ref_logits.append(lg)
                 toks.append(t)
-        worst = 0.0
+        worst, same = 0.0, True
         for g, o in zip(gpu_logits, ref_logits):
             if g is not None:
                 worst = max(worst, float(np.max(np.abs(g - o))))
+                same = same and np.array_equal(g.view(np.uint32), o.view(np.uint32))
+        say("  logits max-abs %.3g, bit-identical %s" % (worst, same))
+        run_pair.bit_identical = same
         return gpu_toks, ref_toks, worst
     finally:
         eng.close()
@@ -85,6 +88,9 @@ def test_c1_tiny_q8_0_greedy_parity(gpu):
     assert g == o, "tokens differ at %d" % next(i for i, (a, b) in enumerate(zip(g, o)) if a != b)
     assert err <= LOGIT_TOL, err
     assert len(set(g)) > 1
+    # Q8_0 throughout and the two-pass attention: the same operations in the
+    # same order as the restatement, so the logits are the same bits
+    assert run_pair.bit_identical
 
 
 def test_c3_shape_two_layers_greedy_parity(gpu):
@@ -100,6 +106,7 @@ def test_c3_shape_two_layers_greedy_parity(gpu):
     gpu.image_free("t_c3x2")
     assert g == o
     assert err <= LOGIT_TOL, err
+    assert run_pair.bit_identical
 
 
 def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
@@ -114,6 +121,7 @@ def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
     gpu.image_free("t_c4x2")
     assert g == o
     assert err <= LOGIT_TOL, err
+    assert run_pair.bit_identical
 
 
 def test_c5_moe_shape_two_layers_greedy_parity(gpu):
