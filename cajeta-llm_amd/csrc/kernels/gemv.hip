@@ -15,8 +15,8 @@
 //            epilogue: store, residual accumulate, RoPE + the fp16 K/V append,
 //            SiLU·up + the pack of the result, or the greedy argmax.
 //
-// The f32-activation formats (Q4_0, MXFP4, the f32 router) keep a lane-tree
-// sum per row (their checks are held to a tolerance).
+// The f32-activation formats (Q4_0, MXFP4, the f32 router) are summed by one
+// thread a row in the reference's element order.
 //
 // Prepared row layouts (HBM, 16-byte aligned rows):
 //   Q4_K : the GGUF blocks as they are: {f16 d, f16 dmin, 12 B scales, 128 B qs}
@@ -201,84 +201,55 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
     }
 }
 
-// Q4_0 × f32: d·Σ (q − 8)·x per block, lane partials (tree across lanes).
-template <int NR, int LPR>
-DEV void acc_q40(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
-    for (int u = slot; u < nb32; u += LPR) {
-        uint4 w[NR];
-        uint32_t dh[NR];
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            w[r] = *(const uint4 *)(wr[r] + (int64_t)u * 16);
-            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 16 + 2 * u);
+// f32-activation formats: one thread a row, the row summed in the
+// reference's element order, x from LDS.
+//   Q4_0  : Quant.q40MatVecIntoAt (io/Quant.cajeta:1516-1545): per block, dot over the
+//           16 byte pairs (low nibble then high), then acc + d·dot.
+//   MXFP4 : Quant.mxfp4MatVecIntoScalar (io/Quant.cajeta:1146-1182):
+//           acc + code·d·x element by element.
+//   F32   : the router's plain row dot in column order.
+template <int FMT>
+DEV float seq_row(const uint8_t *wr, const float *xs, int64_t cols, const float *lut) {
+    float acc = 0.0f;
+    if (FMT == CJ_F32) {
+        const float4 *w4 = (const float4 *)wr;
+        for (int64_t u = 0; u < cols / 4; u++) {
+            const float4 w = w4[u];
+            const float4 x = *(const float4 *)(xs + 4 * u);
+            acc = __fadd_rn(acc, __fmul_rn(w.x, x.x));
+            acc = __fadd_rn(acc, __fmul_rn(w.y, x.y));
+            acc = __fadd_rn(acc, __fmul_rn(w.z, x.z));
+            acc = __fadd_rn(acc, __fmul_rn(w.w, x.w));
         }
-        float xv[32];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
-            xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
-        }
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const uint32_t ws[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+        return acc;
+    }
+    const int nb32 = (int)(cols / 32);
+    for (int u = 0; u < nb32; u++) {
+        const uint4 q = *(const uint4 *)(wr + (int64_t)u * 16);
+        const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
+        const float *xb = xs + u * 32;
+        if (FMT == CJ_Q4_0) {
+            const float dv = h2f(*(const uint16_t *)(wr + (int64_t)nb32 * 16 + 2 * u));
             float dot = 0.0f;
 #pragma unroll
             for (int jj = 0; jj < 16; jj++) {
-                const int q = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
-                dot = __fadd_rn(dot, __fmul_rn((float)((q & 15) - 8), xv[jj]));
-                dot = __fadd_rn(dot, __fmul_rn((float)((q >> 4) - 8), xv[jj + 16]));
+                const int b = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
+                dot = __fadd_rn(dot, __fmul_rn((float)((b & 15) - 8), xb[jj]));
+                dot = __fadd_rn(dot, __fmul_rn((float)((b >> 4) - 8), xb[jj + 16]));
             }
-            acc[r] = __fadd_rn(acc[r], __fmul_rn(h2f(dh[r]), dot));
-        }
-    }
-}
-
-// MXFP4 × f32: code(nib)·2^(e−128)·x per element, lane partials.
-template <int NR, int LPR>
-DEV void acc_mxfp4(const uint8_t *const (&wr)[NR], const float *xf, int nb32, int slot, float (&acc)[NR]) {
-    for (int u = slot; u < nb32; u += LPR) {
-        uint4 w[NR];
-        uint32_t eb[NR];
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            w[r] = *(const uint4 *)(wr[r] + (int64_t)u * 16);
-            eb[r] = wr[r][(int64_t)nb32 * 16 + u];
-        }
-        float xv[32];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = *(const float4 *)(xf + u * 32 + 4 * i);
-            xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
-        }
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const uint32_t ws[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
-            const float d = mxfp4_scale(eb[r]);
+            acc = __fadd_rn(acc, __fmul_rn(dv, dot));
+        } else {
+            const float d = mxfp4_scale(wr[(int64_t)nb32 * 16 + u]);
 #pragma unroll
             for (int k = 0; k < 32; k++) {
                 const int jj = k & 15;
-                const uint32_t byv = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
-                const uint32_t nib = k < 16 ? (byv & 15) : (byv >> 4);
-                acc[r] = __fadd_rn(acc[r], __fmul_rn(__fmul_rn(mxfp4_val(nib), d), xv[k]));
+                const uint32_t b = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
+                const uint32_t nib = k < 16 ? (b & 15) : (b >> 4);
+                acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(lut[nib], d), xb[k]));
             }
         }
     }
-}
-
-// f32 weights × f32 (the MoE router): four columns a unit, lane partials.
-template <int NR, int LPR>
-DEV void acc_f32(const uint8_t *const (&wr)[NR], const float *xf, int n4, int slot, float (&acc)[NR]) {
-    for (int u = slot; u < n4; u += LPR) {
-        const float4 x = *(const float4 *)(xf + 4 * u);
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const float4 w = *(const float4 *)(wr[r] + (int64_t)u * 16);
-            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.x, x.x));
-            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.y, x.y));
-            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.z, x.z));
-            acc[r] = __fadd_rn(acc[r], __fmul_rn(w.w, x.w));
-        }
-    }
+    return acc;
 }
 
 // ------------------------------------------------------------- epilogues
@@ -364,6 +335,16 @@ DEV void gemv_body(const cj_gemv_args &a) {
         else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, bmax, nullptr);
     }
 
+    float v = 0.0f;
+    const int64_t r = row0 + t;
+    const bool live = t < R && r < a.rows;
+    if constexpr (f32act) {
+        // ---- one thread a row, in element order
+        __shared__ float lut[16];
+        if (t < 16) lut[t] = mxfp4_val(t);
+        __syncthreads();
+        if (live) v = seq_row<FMT>(W + r * a.row_bytes, (const float *)sx, cols, lut);
+    } else {
     // ---- phase A: block terms of the workgroup's R rows
     {
         constexpr int G = 64 / LPR;
@@ -380,32 +361,20 @@ DEV void gemv_body(const cj_gemv_args &a) {
             if (rl0 >= R) continue;     // uniform per LPR group
             if (FMT == CJ_Q4_K) terms_q4k<2, LPR>(wr, tr, sx, nb, slot);
             else if (FMT == CJ_Q6_K) terms_q6k<2, LPR>(wr, tr, sx, nb, slot);
-            else if (FMT == CJ_Q8_0) terms_q80<2, LPR>(wr, tr, sx, nb32, slot);
-            else {
-                float acc[2] = {0.0f, 0.0f};
-                if (FMT == CJ_Q4_0) acc_q40<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
-                else if (FMT == CJ_MXFP4) acc_mxfp4<2, LPR>(wr, (const float *)sx, nb32, slot, acc);
-                else acc_f32<2, LPR>(wr, (const float *)sx, (int)(cols / 4), slot, acc);
-                const float v0 = group_sum<LPR>(acc[0]), v1 = group_sum<LPR>(acc[1]);
-                if (slot == 0) { tr[0][0] = v0; tr[1][0] = v1; }
-            }
+            else terms_q80<2, LPR>(wr, tr, sx, nb32, slot);
         }
     }
     __syncthreads();
 
     // ---- phase B: thread t folds row t's terms in block order
-    const int64_t r = row0 + t;
-    const bool live = t < R && r < a.rows;
-    float v = 0.0f;
     if (t < R) {
         const float *tp = terms + t * TB;
         if (FMT == CJ_Q4_K) {
             for (int b = 0; b < TB; b += 2) v = __fsub_rn(__fadd_rn(v, tp[b]), tp[b + 1]);
-        } else if (FMT == CJ_Q6_K || FMT == CJ_Q8_0) {
-            for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
         } else {
-            v = tp[0];
+            for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
         }
+    }
     }
     const float vp = __shfl_xor(v, 1);      // the paired row (RoPE pair, gate/up pair)
     const int pos = (a.epi == CJ_EPI_QKV_ROPE || a.epi == CJ_EPI_ARGMAX) ? step_pos(a.state, a.pos) : 0;
@@ -542,6 +511,6 @@ DEV void gemv_body(const cj_gemv_args &a) {
 GEMV_FAMILY(cj_gemv_q4k, CJ_Q4_K)
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0)
-GEMV_FAMILY(cj_gemv_q40, CJ_Q4_0)
-GEMV_FAMILY(cj_gemv_mxfp4, CJ_MXFP4)
-GEMV_FAMILY(cj_gemv_f32, CJ_F32)
+GEMV_KERNEL(cj_gemv_q40, CJ_Q4_0, 64)
+GEMV_KERNEL(cj_gemv_mxfp4, CJ_MXFP4, 64)
+GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64)

@@ -37,8 +37,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_l64"},
         {"q6kQ8WaveMatVecKernel", "cj_gemv_q6k_l64"},
         {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
-        {"q40F32WaveMatVecKernel", "cj_gemv_q40_l64"},
-        {"mxfp4MatVecKernel", "cj_gemv_mxfp4_l64"},
+        {"q40F32WaveMatVecKernel", "cj_gemv_q40"},
+        {"mxfp4MatVecKernel", "cj_gemv_mxfp4"},
         {"q8kPackKernel", "cj_pack"},
         {"q8kPack32Kernel", "cj_pack"},
         {"rmsnormPackRowF32", "cj_pack"},
@@ -59,8 +59,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"embedRowQ80Kernel", "cj_embed"},
         {"gatherRowsF32Kernel", "cj_embed"},
         {"routerTopKKernel", "cj_moe_route"},
-        {"q4kQ8IdGateUpGluKernel", "cj_gemv_mxfp4_l64"},
-        {"q4kQ8IdDownCombineKernel", "cj_gemv_mxfp4_l64"},
+        {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_l64"},
+        {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_l64"},
     };
     return m;
 }
@@ -151,7 +151,8 @@ int64_t prepared_row_bytes(int type, int64_t cols) {
 }
 
 bool gemv_supported(int type, int64_t cols) {
-    return prepared_row_bytes(type, cols) > 0 && cols <= 16384 * (is_f32_act(type) ? 1 : 4);
+    // the staged activation and the per-row terms stay within 64 KB of LDS
+    return prepared_row_bytes(type, cols) > 0 && cols <= (is_f32_act(type) ? 15360 : 16384);
 }
 
 GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
@@ -167,6 +168,15 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
     while (4 * groups * rpg > 256 && rpg > 2) rpg -= 2;
     p.rows_per_wg = 4 * groups * rpg;
     p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
+    if (is_f32_act(type)) {
+        // one thread a row, summed in element order
+        p.kernel = fam;
+        p.rows_per_wg = 256;
+        p.grid = (uint32_t)((rows + 255) / 256);
+        p.per_copy = p.grid;
+        p.lds = 3072 + (uint32_t)((cols + 255) / 256 * 1024);
+        return p;
+    }
     p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
     p.per_copy = p.grid;
     const int64_t nblk = (cols + 255) / 256;
@@ -180,6 +190,7 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
 int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
     cj_gemv_args a = a0;
     a.rows_per_wg = p.rows_per_wg;
+    if (p.lds > 65536) return fail(CJ_ERR_ARG, "gemv %s: %u bytes of LDS exceed 64 KB", p.kernel.c_str(), p.lds);
     const uint32_t grid = a.sel ? p.per_copy * (uint32_t)a.n_sel : p.grid;
     return launch(p.kernel.c_str(), grid, 256, p.lds, a);
 }
@@ -210,9 +221,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q4k_l64", "cj_gemv_q4k_l32", "cj_gemv_q4k_l16", "cj_gemv_q4k_l8",
         "cj_gemv_q6k_l64", "cj_gemv_q6k_l32", "cj_gemv_q6k_l16", "cj_gemv_q6k_l8",
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
-        "cj_gemv_q40_l64", "cj_gemv_q40_l32", "cj_gemv_q40_l16", "cj_gemv_q40_l8",
-        "cj_gemv_mxfp4_l64", "cj_gemv_mxfp4_l32", "cj_gemv_mxfp4_l16", "cj_gemv_mxfp4_l8",
-        "cj_gemv_f32_l64", "cj_gemv_f32_l32", "cj_gemv_f32_l16", "cj_gemv_f32_l8", "cj_moe_combine",
+        "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_moe_combine",
         "cj_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",

@@ -138,6 +138,7 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
     gpu.image_free("t_c5x2")
     assert g == o
     assert err <= LOGIT_TOL, err
+    assert run_pair.bit_identical
 
 
 def test_engine_request_surface(gpu):
