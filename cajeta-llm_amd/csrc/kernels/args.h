@@ -138,8 +138,16 @@ typedef struct {
 
 typedef struct {
     float *out; uint8_t *packed; const float *part;
+    const cj_step_state *state;  // non-null: splits follow the device position
     int32_t n_q, head_dim, splits, per32;
+    int32_t n_kv, workers, window, pad;
 } cj_merge_args;
+
+typedef struct {
+    // the step's greedy pick from per-workgroup (value, index) partials
+    const float *pv; const int32_t *pi; int32_t n, pos;
+    int32_t *tokens, *preds; cj_step_state *state;
+} cj_pick_args;
 
 typedef struct {
     float *out; const uint8_t *table; const int32_t *tokens; const cj_step_state *state;

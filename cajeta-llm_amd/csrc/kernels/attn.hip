@@ -71,12 +71,36 @@ DEV void split_body(const cj_attn_args &a) {
         for (int tb = t0; tb < t1; tb += ATTN_TILE) {
             const int n = t1 - tb < ATTN_TILE ? t1 - tb : ATTN_TILE;
             __syncthreads();
-            // stage: element d of position p to [p][d % 16][d / 16]
-            for (int e = tid; e < n * HD; e += nthr) {
-                const int p = e / HD, d = e % HD;
-                const int64_t base = kv_at(a.pgtab, a.pg_base, from + tb + p, a.n_kv, kvh, HD);
-                ks[p][d & 15][d >> 4] = a.kc[base + d];
-                vs[p][d & 15][d >> 4] = a.vc[base + d];
+            // stage: 16-byte chunks (8 dims) of each position's K and V row,
+            // all loads issued before the scatter of element d of position p
+            // to [p][d % 16][d / 16]
+            {
+                constexpr int CPP = HD / 8;                      // chunks a position
+                constexpr int CH = ATTN_TILE * CPP / (G * 16);   // chunks a thread
+                uint4 kq[CH], vq[CH];
+#pragma unroll
+                for (int c = 0; c < CH; c++) {
+                    const int e = tid + c * nthr, p = e / CPP, j = e % CPP;
+                    if (p < n) {
+                        const int64_t base = kv_at(a.pgtab, a.pg_base, from + tb + p, a.n_kv, kvh, HD) + 8 * j;
+                        kq[c] = *(const uint4 *)(a.kc + base);
+                        vq[c] = *(const uint4 *)(a.vc + base);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CH; c++) {
+                    const int e = tid + c * nthr, p = e / CPP, j = e % CPP;
+                    if (p < n) {
+                        const uint32_t kw[4] = {kq[c].x, kq[c].y, kq[c].z, kq[c].w};
+                        const uint32_t vw[4] = {vq[c].x, vq[c].y, vq[c].z, vq[c].w};
+#pragma unroll
+                        for (int i = 0; i < 8; i++) {
+                            const int d = 8 * j + i;
+                            ks[p][d & 15][d >> 4] = (uint16_t)(kw[i >> 1] >> (16 * (i & 1)));
+                            vs[p][d & 15][d >> 4] = (uint16_t)(vw[i >> 1] >> (16 * (i & 1)));
+                        }
+                    }
+                }
             }
             __syncthreads();
             for (int p = 0; p < n; p++) {
@@ -228,41 +252,74 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_a
 
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
 // 256 per 256 output values (the reference's attnReducePackQ8Kernel
-// contract), the merge in reducePackBlockCpu's order.
+// contract), the merge in reducePackBlockCpu's order: the global max, then
+// four interleaved sub-sums (splits s ≡ 0, 1, 2, 3 mod 4, each ascending) of
+// w_s·l_s and of w_s·acc_s[d], w_s = exp(m_s − max), added in sub order;
+// out = acc · (1 / l). The (head, split) weights are computed once in LDS.
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
-    __shared__ float bmax[8];
-    const int t = threadIdx.x, lane = t & 63;
+    __shared__ float wts[4][ATTN_MAX_SPLITS];     // per head of the block, per split (0: skipped)
+    __shared__ int use[4][ATTN_MAX_SPLITS];
+    __shared__ float gsum[4];
+    const int t = threadIdx.x;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
+    int splits = a.splits;
+    if (a.state) {
+        int count = a.state->pos + 1;
+        if (a.window > 0 && count > a.window) count = a.window;
+        splits = decode_splits(count, a.n_kv, a.workers);
+    }
+    const int h0 = (int)((int64_t)blockIdx.x * 256 / hd);     // first head of the block
+    const int nh = 256 / hd < 1 ? 1 : 256 / hd;                 // heads a block (hd 64 or 128)
+    // per (head, split): the weight, from the head's max over its splits
+    {
+        const int hh = t / ATTN_MAX_SPLITS, sp = t % ATTN_MAX_SPLITS;
+        if (hh < nh && h0 + hh < a.n_q) {
+            const float *pb0 = a.part + (int64_t)(h0 + hh) * ATTN_MAX_SPLITS * (hd + 2);
+            float gm = -3.0e38f;
+            for (int s2 = 0; s2 < splits; s2++) {
+                const float mv = pb0[s2 * (hd + 2) + hd];
+                if (mv > gm) gm = mv;
+            }
+            const bool on = sp < splits && pb0[sp * (hd + 2) + hd + 1] > 0.0f;
+            use[hh][sp] = on;
+            wts[hh][sp] = on ? cj_expf(pb0[sp * (hd + 2) + hd] - gm) : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (t < nh && h0 + t < a.n_q) {
+        const float *pb0 = a.part + (int64_t)(h0 + t) * ATTN_MAX_SPLITS * (hd + 2);
+        float gt = 0.0f;
+        for (int sub = 0; sub < 4; sub++) {
+            float gl = 0.0f;
+            for (int s2 = sub; s2 < splits; s2 += 4)
+                if (use[t][s2]) gl = __fadd_rn(gl, __fmul_rn(wts[t][s2], pb0[s2 * (hd + 2) + hd + 1]));
+            gt = sub == 0 ? gl : __fadd_rn(gt, gl);
+        }
+        gsum[t] = gt;
+    }
+    __syncthreads();
     float x = 0.0f;
     if (e < n) {
-        const int h = (int)(e / hd), d = (int)(e % hd);
-        const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
-        float gm = -3.0e38f;
-        for (int s = 0; s < a.splits; s++) {
-            const float mv = pb0[s * (hd + 2) + hd];
-            if (mv > gm) gm = mv;
-        }
-        float tacc = 0.0f, gt = 0.0f;
-        for (int sub = 0; sub < 4; sub++) {
-            float gl = 0.0f, ac = 0.0f;
-            for (int s = sub; s < a.splits; s += 4) {
-                const float *pb = pb0 + s * (hd + 2);
-                const float ls = pb[hd + 1];
-                if (ls > 0.0f) {
-                    const float w = cj_expf(pb[hd] - gm);
-                    gl = __fadd_rn(gl, __fmul_rn(w, ls));
-                    ac = __fadd_rn(ac, __fmul_rn(pb[d], w));
-                }
+        const int h = (int)(e / hd), d = (int)(e % hd), hh = h - h0;
+        const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2) + d;
+        float ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < splits; s0 += 4) {
+#pragma unroll
+            for (int sub = 0; sub < 4; sub++) {
+                const int s2 = s0 + sub;
+                if (s2 < splits && use[hh][s2]) ac[sub] = __fadd_rn(ac[sub], __fmul_rn(pb0[s2 * (hd + 2)], wts[hh][s2]));
             }
-            if (sub == 0) { tacc = ac; gt = gl; }
-            else { tacc = __fadd_rn(tacc, ac); gt = __fadd_rn(gt, gl); }
         }
-        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
+        const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
+        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gsum[hh]));
         if (a.out) a.out[e] = x;
     }
     if (!a.packed) return;
+    // the block's pack: 256 values, one a thread
+    __shared__ float bmax[8];
+    const int lane = t & 63;
     const float av = fabsf(x);
     float am;
     if (a.per32) {

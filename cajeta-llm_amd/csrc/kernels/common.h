@@ -183,52 +183,65 @@ DEV float stage_value(const float *x, int64_t n, int64_t e, bool norm, float sca
     return __fmul_rn(__fmul_rn(xv, scale), wi);
 }
 
-// Quantize the staged values of nblk blocks into LDS 320-byte blocks at sx,
-// STAGE_CHUNK blocks at a time (thread t = element t of each block).
+// Quantize the staged values of nblk blocks into LDS 320-byte blocks at sx.
+// Thread t owns 16 consecutive values of each 4096-wide round (block t/16,
+// values 16·(t%16)..+15), so a 32-group is two neighbouring lanes and a
+// 256-block sixteen: the block maximum, the int8 codes and the 32-sums are
+// lane-local plus xor shuffles, with no barrier until the end. The codes
+// are the reference's q8kPack ones: q = round-half-away(v · (127/amax)).
 DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form,
-                    int per32, uint8_t *sx, float *bmax, float *xout) {
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    for (int k0 = 0; k0 < nblk; k0 += STAGE_CHUNK) {
-        float v[STAGE_CHUNK];
+                    int per32, uint8_t *sx, float *xout) {
+    const int t = threadIdx.x;
+    const int64_t total = (int64_t)nblk * 256;
+    for (int64_t e0 = 16 * t; e0 < total; e0 += 4096) {
+        float v[16];
+        if (e0 + 16 <= n && !norm) {
 #pragma unroll
-        for (int k = 0; k < STAGE_CHUNK; k++) {
-            const int64_t e = (int64_t)(k0 + k) * 256 + t;
-            v[k] = (k0 + k < nblk) ? stage_value(x, n, e, norm, scale, w, form) : 0.0f;
-            if (xout && k0 + k < nblk && e < n) xout[e] = v[k];
-        }
-#pragma unroll
-        for (int k = 0; k < STAGE_CHUNK; k++) {
-            if (k0 + k >= nblk) break;
-            const float a = fabsf(v[k]);
-            if (per32) {
-                const float m = group_max<32>(a);
-                if ((lane & 31) == 0) bmax[k * 8 + (t >> 5)] = m;
-            } else {
-                const float m = group_max<64>(a);
-                if (lane == 0) bmax[k * 8 + wv] = m;
+            for (int k = 0; k < 4; k++) {
+                const float4 f = *(const float4 *)(x + e0 + 4 * k);
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
             }
-        }
-        __syncthreads();
+        } else {
 #pragma unroll
-        for (int k = 0; k < STAGE_CHUNK; k++) {
-            if (k0 + k >= nblk) break;
-            const float am = per32 ? bmax[k * 8 + (t >> 5)]
-                                   : fmaxf(fmaxf(bmax[k * 8 + 0], bmax[k * 8 + 1]), fmaxf(bmax[k * 8 + 2], bmax[k * 8 + 3]));
-            const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+            for (int k = 0; k < 16; k++) v[k] = stage_value(x, n, e0 + k, norm, scale, w, form);
+        }
+        if (xout) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) if (e0 + k < n) xout[e0 + k] = v[k];
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) am = fmaxf(am, fabsf(v[k]));
+        am = fmaxf(am, __shfl_xor(am, 1));
+        if (!per32) {
+            am = fmaxf(am, __shfl_xor(am, 2));
+            am = fmaxf(am, __shfl_xor(am, 4));
+            am = fmaxf(am, __shfl_xor(am, 8));
+        }
+        const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+        uint32_t wd[4] = {0u, 0u, 0u, 0u};
+        int sum = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
             const int q = round_away(__fmul_rn(v[k], inv));
-            uint8_t *blk = sx + (k0 + k) * 320;
-            blk[t] = (uint8_t)(int8_t)q;
-            const int s = group_sum_i<32>(q);
-            if ((lane & 31) == 0) *(int32_t *)(blk + 256 + 4 * (t >> 5)) = s;
-            if (per32) {
-                if ((lane & 31) == 0) *(float *)(blk + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
-            } else {
-                if (t == 0) *(float *)(blk + 288) = __fdiv_rn(am, 127.0f);
-                pack_zero_pad(blk, t);
-            }
+            sum += q;
+            wd[k >> 2] |= ((uint32_t)q & 255u) << (8 * (k & 3));
         }
-        __syncthreads();
+        sum += __shfl_xor(sum, 1);
+        const int64_t blk = e0 >> 8;
+        const int in = (int)(e0 & 255);           // offset inside the block
+        uint8_t *b = sx + blk * 320;
+        *(uint4 *)(b + in) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        const int g = in >> 5, j = (in >> 4) & 15;   // 32-group, lane of the block
+        if (!(j & 1)) *(int32_t *)(b + 256 + 4 * g) = sum;
+        if (per32) {
+            if (!(j & 1)) *(float *)(b + 288 + 4 * g) = __fdiv_rn(am, 127.0f);
+        } else {
+            if (j == 0) *(float *)(b + 288) = __fdiv_rn(am, 127.0f);
+            else if (j < 8) *(uint32_t *)(b + 288 + 4 * j) = 0u;   // pad bytes 292..319
+        }
     }
+    __syncthreads();
 }
 
 // The staged values as f32 into LDS (formats that read f32 activations).

@@ -332,7 +332,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
         const float scale = norm ? stage_norm_scale(X, cols, a.eps, red) : 1.0f;
         if (f32act) stage_f32(X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx);
-        else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, bmax, nullptr);
+        else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr);
     }
 
     float v = 0.0f;
@@ -345,23 +345,27 @@ DEV void gemv_body(const cj_gemv_args &a) {
         __syncthreads();
         if (live) v = seq_row<FMT>(W + r * a.row_bytes, (const float *)sx, cols, lut);
     } else {
-    // ---- phase A: block terms of the workgroup's R rows
+    // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
     {
         constexpr int G = 64 / LPR;
+        constexpr int NR = FMT == CJ_Q6_K ? 2 : 4;
         const int group = lane / LPR, slot = lane % LPR;
-        const int lanes_groups = 4 * G;                      // row slots across the workgroup
+        const int lanes_groups = 4 * G;                      // row groups across the workgroup
         const int nb = (int)(cols / 256), nb32 = (int)(cols / 32);
-        for (int i = 0; i < R; i += 2 * lanes_groups) {
-            const int rl0 = i + 2 * (wave * G + group), rl1 = rl0 + 1;
-            const int64_t r0 = row0 + rl0, r1 = row0 + rl1;
-            const uint8_t *wr[2];
-            wr[0] = W + (r0 < a.rows ? r0 : a.rows - 1) * a.row_bytes;
-            wr[1] = W + (r1 < a.rows ? r1 : a.rows - 1) * a.row_bytes;
-            float *tr[2] = {terms + (rl0 < R ? rl0 : 0) * TB, terms + (rl1 < R ? rl1 : 0) * TB};
+        for (int i = 0; i < R; i += NR * lanes_groups) {
+            const int rl0 = i + NR * (wave * G + group);
             if (rl0 >= R) continue;     // uniform per LPR group
-            if (FMT == CJ_Q4_K) terms_q4k<2, LPR>(wr, tr, sx, nb, slot);
-            else if (FMT == CJ_Q6_K) terms_q6k<2, LPR>(wr, tr, sx, nb, slot);
-            else terms_q80<2, LPR>(wr, tr, sx, nb32, slot);
+            const uint8_t *wr[NR];
+            float *tr[NR];
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                const int64_t rk = row0 + rl0 + k;
+                wr[k] = W + (rk < a.rows ? rk : a.rows - 1) * a.row_bytes;
+                tr[k] = terms + (rl0 + k) * TB;
+            }
+            if (FMT == CJ_Q4_K) terms_q4k<NR, LPR>(wr, tr, sx, nb, slot);
+            else if (FMT == CJ_Q6_K) terms_q6k<NR, LPR>(wr, tr, sx, nb, slot);
+            else terms_q80<NR, LPR>(wr, tr, sx, nb32, slot);
         }
     }
     __syncthreads();
@@ -468,6 +472,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
         if (t == 0) {
             a.part_v[blockIdx.x] = bv[0];
             a.part_i[blockIdx.x] = bi[0];
+        }
+        if (!a.counters) return;      // the pick runs as its own launch
+        if (t == 0) {
             __threadfence();
             ticket = atomicAdd(a.counters, 1);
         }

@@ -10,7 +10,6 @@
 // (Prim.rmsnormPackDevice / QuantKernel.q8kPackRowsLaunchNoSync contracts).
 extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
     __shared__ float red[256];
-    __shared__ float bmax[STAGE_CHUNK * 8];
     extern __shared__ __align__(16) uint8_t sx[];
     const int64_t row = blockIdx.x;
     const float *x = a.x + row * a.n;
@@ -21,7 +20,7 @@ extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
         for (int64_t e = threadIdx.x; e < a.n; e += 256) xo[e] = stage_value(x, a.n, e, a.do_norm, scale, a.w, a.form);
         return;
     }
-    stage_pack(x, a.n, nblk, a.do_norm, scale, a.w, a.form, a.per32, sx, bmax, xo);
+    stage_pack(x, a.n, nblk, a.do_norm, scale, a.w, a.form, a.per32, sx, xo);
     uint8_t *o = a.out + row * (int64_t)nblk * 320;
     for (int i = threadIdx.x; i < nblk * 20; i += 256) ((uint4 *)o)[i] = ((const uint4 *)sx)[i];
 }
@@ -219,6 +218,35 @@ extern "C" __global__ void __launch_bounds__(256) cj_embed(cj_embed_args a) {
 
 // QuantKernel.argmaxRowKernel's contract: the smallest index of the largest
 // value; 1024 elements a workgroup, the last workgroup reduces the partials.
+// The step's greedy pick: first-occurrence argmax over per-workgroup
+// (value, index) partials (HostOps.argmaxRow's order), written as
+// preds[pos+1] and, past the prompt, tokens[pos+1]; advances the position.
+extern "C" __global__ void __launch_bounds__(256) cj_argmax_pick(cj_pick_args a) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int t = threadIdx.x;
+    float gb = 0.0f;
+    int gi = -1;
+    for (int g = t; g < a.n; g += 256) {
+        const float x = a.pv[g];
+        const int xi = a.pi[g];
+        if (argmax_take(x, xi, gb, gi)) { gb = x; gi = xi; }
+    }
+    bv[t] = gb;
+    bi[t] = gi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s && argmax_take(bv[t + s], bi[t + s], bv[t], bi[t])) { bv[t] = bv[t + s]; bi[t] = bi[t + s]; }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const int pos = a.state ? a.state->pos : a.pos;
+        if (a.preds) a.preds[pos + 1] = bi[0];
+        if (a.tokens && (!a.state || pos + 1 >= a.state->fixed_until)) a.tokens[pos + 1] = bi[0];
+        if (a.state) a.state->pos = pos + 1;
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256) cj_argmax(cj_argmax_args a) {
     __shared__ float bv[256];
     __shared__ int bi[256];

@@ -63,6 +63,12 @@ struct Request {
     int reason = 0;
 };
 
+// The launches of one decode step, by kind (the timing seam addresses one).
+enum Kind {
+    K_EMBED = 0, K_QKV = 1, K_ATTN = 2, K_O = 3, K_GATE_UP = 4, K_DOWN = 5,
+    K_ROUTER = 6, K_ROUTE = 7, K_EXP_GATE_UP = 8, K_EXP_DOWN = 9, K_COMBINE = 10, K_HEAD = 11
+};
+
 }  // namespace
 
 struct Engine {
@@ -81,7 +87,7 @@ struct Engine {
     float *rope = nullptr;
     // scratch
     float *hs = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *part = nullptr;
-    uint8_t *act_pack = nullptr;
+    uint8_t *act_pack = nullptr, *attn_pack = nullptr;
     int32_t *glu_counters = nullptr, *argmax_counter = nullptr, *attn_counters = nullptr;
     float *part_v = nullptr;
     int32_t *part_i = nullptr;
@@ -93,6 +99,12 @@ struct Engine {
     std::vector<Request> reqs;
     float last_step_us = 0.0f;
     std::vector<void *> owned;
+    int only = -1;             // enqueue only this kind, of layer 0 (-1: the whole step)
+    bool graphs = true;        // replay the captured step (false: enqueue its launches each token)
+    int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
+    int64_t embd_row_file_bytes = 0;
+
+    bool want(int kind, int l) const { return only < 0 || (only == kind && l == 0); }
 
     void *alloc(size_t n) {
         void *p = dev_alloc(n);
@@ -104,16 +116,21 @@ struct Engine {
             if (s.graph) (void)hipGraphExecDestroy(s.graph);
         (void)hipStreamSynchronize(stream());
         for (void *p : owned) dev_free(p);
+        if (pinned) (void)hipHostFree(pinned);
     }
     int load(const std::string &path, int ctx_, int max_seqs_);
     int upload_weight(const std::string &name, DevW &w, int expect_rows, int64_t expect_cols);
     int fuse_rows(const std::vector<std::string> &names, DevW &w, bool interleave, int64_t rows_each, int64_t experts);
     int capture(int s);
     int enqueue_step(int s);
+    int run_step(int s);
     int prefill(int s, const int32_t *toks, int n);
     int decode(int s, int steps, int32_t *out);
     int reset(int s);
     int run_request(Request &r, int max_steps);
+    int64_t kind_bytes(int kind, int count) const;
+    int64_t step_bytes(int count) const;
+    int time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel);
 };
 
 namespace {
@@ -230,6 +247,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     // embedding: GGUF layout, decoded per row on device
     embd_type = te->type;
     embd_row_bytes = ggml_row_bytes(te->type, te->cols());
+    embd_row_file_bytes = embd_row_bytes;
     if (embd_row_bytes <= 0 || te->cols() != hidden || te->rows() != vocab)
         return fail(CJ_ERR_IO, "model: token_embd.weight shape/type not served");
     embd = alloc((size_t)te->bytes);
@@ -295,6 +313,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     attn = (float *)alloc((size_t)qd * 4);
     act = (float *)alloc((size_t)fmax * 4 + 1024);
     act_pack = (uint8_t *)alloc((size_t)fpad / 256 * 320);
+    attn_pack = (uint8_t *)alloc((size_t)(qd + 255) / 256 * 320);
     logits = (float *)alloc((size_t)vocab * 4);
     // split-K partials [n_heads][64][hd + 2], or two-pass scores [n_heads][ctx]
     part = (float *)alloc((size_t)n_heads * std::max<int64_t>(64 * (head_dim + 2), ctx) * 4);
@@ -308,13 +327,15 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     moe_w = (float *)alloc(64 * 4);
     moe_sel = (int32_t *)alloc(64 * 4);
     moe_y = (float *)alloc((size_t)hidden * std::max(1, n_used) * 4);
-    if (!hs || !q || !attn || !act || !act_pack || !logits || !part || !glu_counters || !argmax_counter ||
+    if (!hs || !q || !attn || !act || !act_pack || !attn_pack || !logits || !part || !glu_counters || !argmax_counter ||
         !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y)
         return fail(CJ_ERR_HIP, "model: out of device memory (scratch)");
     CJ_HIP(hipMemset(glu_counters, 0, (size_t)fpad / 256 * 4 + 64));
     CJ_HIP(hipMemset(argmax_counter, 0, 64));
     CJ_HIP(hipMemset(attn_counters, 0, (size_t)n_kv * 4 + 64));
 
+    if (hipHostMalloc((void **)&pinned, (size_t)(ctx + 2) * 4 + sizeof(cj_step_state) + 64, 0) != hipSuccess)
+        return fail(CJ_ERR_HIP, "model: pinned staging buffer");
     seqs.resize(max_seqs);
     for (int s = 0; s < max_seqs; s++) {
         Seq &S = seqs[s];
@@ -335,7 +356,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
 int Engine::enqueue_step(int s) {
     Seq &S = seqs[s];
     int rc;
-    {
+    if (want(K_EMBED, 0)) {
         cj_embed_args a{};
         a.out = hs; a.table = (const uint8_t *)embd; a.tokens = S.tokens; a.state = S.state;
         a.type = embd_type; a.hidden = hidden; a.row_bytes = embd_row_bytes;
@@ -346,28 +367,36 @@ int Engine::enqueue_step(int s) {
     // the reference's choice of form: split-K for hd 128 with 4 or 8 query
     // heads a kv head, else the two-pass score/combine
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
+    const int64_t qd_ = (int64_t)n_heads * head_dim;
     char attn_kernel[64], combine_kernel[64];
     if (split) snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_split_h128_g%d", grp);
     else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
     snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
-        {   // 1. q|k|v with norm+pack prologue, RoPE + K/V append epilogue
+        if (want(K_QKV, l)) {   // 1. q|k|v with norm+pack prologue, RoPE + K/V append epilogue
             cj_gemv_args a{};
             a.w = (const uint8_t *)L.qkv.p; a.x = hs; a.nw = L.attn_norm; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
             a.pgtab = pgtab; a.rope_cs = rope; a.state = S.state; a.rows = L.qkv.rows; a.cols = hidden;
             a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_QKV_ROPE;
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
             a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
         }
-        {   // 2. attention
+        if (want(K_ATTN, l)) {   // 2. attention
             cj_attn_args a{};
             a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
             a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
             a.pg_base = S.pg_base; a.window = L.window; a.scale = scale;
             if (split) {
+                // partials, then the merge + the pack the o projection reads
+                a.out = nullptr;
                 if ((rc = launch(attn_kernel, (uint32_t)(n_kv * 64), (uint32_t)(grp * 16), 0, a))) return rc;
+                cj_merge_args m{};
+                m.out = attn; m.packed = attn_pack; m.part = part; m.state = S.state; m.n_q = n_heads;
+                m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0; m.n_kv = n_kv; m.workers = workers;
+                m.window = L.window;
+                if ((rc = launch("cj_attn_merge", (uint32_t)((qd_ + 255) / 256), 256, 0, m))) return rc;
             } else {
                 // the grid covers the longest window; the kernel idles past count
                 a.splits = ctx;
@@ -376,43 +405,43 @@ int Engine::enqueue_step(int s) {
                 if ((rc = launch(combine_kernel, (uint32_t)n_heads, 128, 0, a))) return rc;
             }
         }
-        {   // 3. o projection, residual into hs
+        if (want(K_O, l)) {   // 3. o projection, residual into hs
             cj_gemv_args a{};
-            a.w = (const uint8_t *)L.o.p; a.x = attn; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
-            a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
+            a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
+            a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split ? CJ_PRO_PACKED : CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
         }
         if (n_experts == 0) {
-            {   // 4. gate|up with norm+pack prologue, SiLU·up + pack epilogue
+            if (want(K_GATE_UP, l)) {   // 4. gate|up with norm+pack prologue, SiLU·up + pack epilogue
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.gu.p; a.x = hs; a.nw = L.ffn_norm; a.act = act; a.act_pack = act_pack;
-                a.counters = glu_counters; a.rows = L.gu.rows; a.cols = hidden; a.row_bytes = L.gu.row_bytes;
+                a.w = (const uint8_t *)L.gu.p; a.x = hs; a.nw = L.ffn_norm; a.act = act;
+                a.rows = L.gu.rows; a.cols = hidden; a.row_bytes = L.gu.row_bytes;
                 a.type = L.gu.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
                 a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
                 a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 4)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
             }
-            {   // 5. down, residual into hs
+            if (want(K_DOWN, l)) {   // 5. down, residual into hs
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.down.p; a.xp = act_pack; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
-                a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_ACCUM;
+                a.w = (const uint8_t *)L.down.p; a.x = act; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
+                a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
                 a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
             }
         } else {
-            {   // router logits from the normed hidden (f32 weights)
+            if (want(K_ROUTER, l)) {   // router logits from the normed hidden (f32 weights)
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.router.p; a.x = hs; a.nw = L.ffn_norm; a.y = moe_logits; a.rows = n_experts;
                 a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_NORM_F32;
                 a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 2)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0)))) return rc;
             }
-            {
+            if (want(K_ROUTE, l)) {
                 cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1};
                 if ((rc = launch("cj_moe_route", 1, 64, 0, a))) return rc;
             }
-            {   // the selected experts' gate|up, SiLU·up into act[k]
+            if (want(K_EXP_GATE_UP, l)) {   // the selected experts' gate|up, SiLU·up into act[k]
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.gu_exps.p; a.x = hs; a.nw = L.ffn_norm; a.act = act; a.rows = 2 * (int64_t)expert_ffn;
                 a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
@@ -420,33 +449,40 @@ int Engine::enqueue_step(int s) {
                 a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
                 a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
                 a.y_stride = expert_ffn;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
             }
-            {   // the selected experts' down into moe_y[k]
+            if (want(K_EXP_DOWN, l)) {   // the selected experts' down into moe_y[k]
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.down_exps.p; a.x = act; a.y = moe_y; a.rows = hidden; a.cols = expert_ffn;
                 a.row_bytes = L.down_exps.row_bytes; a.type = L.down_exps.type;
                 a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
                 a.batch = 1; a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes;
                 a.x_stride = expert_ffn; a.y_stride = hidden;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 2)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
             }
-            {   // hs += Σ_k w_k · y_k in k order
+            if (want(K_COMBINE, l)) {   // hs += Σ_k w_k · y_k in k order
                 cj_combine_args a{hs, moe_y, moe_w, hidden, n_used};
                 if ((rc = launch("cj_moe_combine", (uint32_t)((hidden + 255) / 256), 256, 0, a))) return rc;
             }
         }
     }
-    {   // final norm + head + greedy argmax; advances the step
+    if (want(K_HEAD, 0)) {   // final norm + head + greedy argmax; advances the step
         cj_gemv_args a{};
-        a.w = (const uint8_t *)head.p; a.x = hs; a.nw = out_norm; a.y = logits; a.counters = argmax_counter;
+        a.w = (const uint8_t *)head.p; a.x = hs; a.nw = out_norm; a.y = logits;
         a.part_v = part_v; a.part_i = part_i; a.tokens = S.tokens; a.preds = S.preds; a.state = S.state;
+        if (only == K_HEAD) { a.state = nullptr; a.pos = S.pos; }   // timed alone: leave the step where it is
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_NORM_F32 : CJ_PRO_NORM_PACK; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 2);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
+        if (only < 0) {
+            cj_pick_args k{};
+            k.pv = part_v; k.pi = part_i; k.n = (int32_t)p.grid; k.tokens = S.tokens; k.preds = S.preds;
+            k.state = S.state;
+            if ((rc = launch("cj_argmax_pick", 1, 256, 0, k))) return rc;
+        }
     }
     return CJ_OK;
 }
@@ -467,12 +503,19 @@ int Engine::capture(int s) {
     return CJ_OK;
 }
 
+// One decode step of slot s on the stream: the graph, or its launches.
+int Engine::run_step(int s) {
+    if (!graphs) return enqueue_step(s);
+    CJ_HIP(hipGraphLaunch(seqs[s].graph, stream()));
+    return CJ_OK;
+}
+
 int Engine::reset(int s) {
     if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
     Seq &S = seqs[s];
     cj_step_state st{};
-    CJ_HIP(hipMemcpyAsync(S.state, &st, sizeof st, hipMemcpyHostToDevice, stream()));
     CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipMemcpy(S.state, &st, sizeof st, hipMemcpyHostToDevice));
     S.pos = 0;
     S.fixed_until = 0;
     return CJ_OK;
@@ -486,13 +529,22 @@ int Engine::prefill(int s, const int32_t *toks, int n) {
     for (int i = 0; i < n; i++)
         if (toks[i] < 0 || toks[i] >= vocab) return fail(CJ_ERR_ARG, "token %d outside the vocabulary", toks[i]);
     int rc;
-    if ((rc = capture(s))) return rc;
-    CJ_HIP(hipMemcpyAsync(S.tokens + S.pos, toks, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
-    cj_step_state st{};
-    st.pos = S.pos;
-    st.fixed_until = S.pos + n;
-    CJ_HIP(hipMemcpyAsync(S.state, &st, sizeof st, hipMemcpyHostToDevice, stream()));
-    for (int i = 0; i < n; i++) CJ_HIP(hipGraphLaunch(S.graph, stream()));
+    if (graphs && (rc = capture(s))) return rc;
+    // through pinned staging: the copies are ordered on the stream and the
+    // staging is not reused before the synchronize below
+    memcpy(pinned, toks, (size_t)n * 4);
+    cj_step_state *st = (cj_step_state *)(pinned + ctx + 2);
+    *st = cj_step_state{};
+    st->pos = S.pos;
+    st->fixed_until = S.pos + n;
+    CJ_HIP(hipMemcpyAsync(S.tokens + S.pos, pinned, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
+    CJ_HIP(hipMemcpyAsync(S.state, st, sizeof *st, hipMemcpyHostToDevice, stream()));
+    for (int i = 0; i < n; i++) {
+        if ((rc = run_step(s))) return rc;
+        // bound the work in flight on long prompts (tools that track every
+        // dispatch hold a record per queued kernel)
+        if ((i & 15) == 15) CJ_HIP(hipStreamSynchronize(stream()));
+    }
     CJ_HIP(hipStreamSynchronize(stream()));
     S.pos += n;
     S.fixed_until = S.pos;
@@ -506,12 +558,17 @@ int Engine::decode(int s, int steps, int32_t *out) {
     if (steps <= 0) return CJ_OK;
     if (S.pos + steps > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + steps, ctx);
     int rc;
-    if ((rc = capture(s))) return rc;
+    if (graphs && (rc = capture(s))) return rc;
     hipEvent_t e0, e1;
     CJ_HIP(hipEventCreate(&e0));
     CJ_HIP(hipEventCreate(&e1));
     CJ_HIP(hipEventRecord(e0, stream()));
-    for (int i = 0; i < steps; i++) CJ_HIP(hipGraphLaunch(S.graph, stream()));
+    for (int i = 0; i < steps; i++) {
+        if ((rc = run_step(s))) return rc;
+        // at most 32 steps in flight (a few thousand dispatches): profilers
+        // that track every queued kernel fail beyond ~8k
+        if ((i & 31) == 31 && i + 1 < steps) CJ_HIP(hipStreamSynchronize(stream()));
+    }
     CJ_HIP(hipEventRecord(e1, stream()));
     CJ_HIP(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -522,6 +579,83 @@ int Engine::decode(int s, int steps, int32_t *out) {
     if (out) CJ_HIP(hipMemcpy(out, S.tokens + S.pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost));
     S.pos += steps;
     return CJ_OK;
+}
+
+// Algorithmic HBM bytes of one launch of `kind` (layer 0 shapes) with
+// `count` attended positions: weights at their GGUF file size, the K/V read
+// and written, and the activation vectors read and written once.
+int64_t Engine::kind_bytes(int kind, int count) const {
+    const Layer &L = layers[0];
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim, h = hidden;
+    auto wb = [](const DevW &w) { return w.rows * ggml_row_bytes(w.type, w.cols); };
+    const int64_t fpad = ((int64_t)ffn + 255) / 256 * 256;
+    switch (kind) {
+    case K_EMBED: return embd_row_file_bytes + h * 4;
+    case K_QKV: return wb(L.qkv) + h * 8 + qd * 4 + 2 * kvd * 2;
+    case K_ATTN: return (int64_t)count * kvd * 2 * 2 + qd * 8;
+    case K_O: return wb(L.o) + qd * 4 + h * 8;
+    case K_GATE_UP: return wb(L.gu) + h * 8 + (int64_t)ffn * 4 + fpad / 256 * 320;
+    case K_DOWN: return wb(L.down) + fpad / 256 * 320 + h * 8;
+    case K_ROUTER: return wb(L.router) + h * 8 + (int64_t)n_experts * 4;
+    case K_ROUTE: return (int64_t)n_experts * 4 + (int64_t)n_used * 8;
+    case K_EXP_GATE_UP:
+        return n_used * (2 * (int64_t)expert_ffn * ggml_row_bytes(L.gu_exps.type, h)) + h * 8 + (int64_t)n_used * expert_ffn * 4;
+    case K_EXP_DOWN:
+        return n_used * (h * ggml_row_bytes(L.down_exps.type, expert_ffn)) + (int64_t)n_used * (expert_ffn + h) * 4;
+    case K_COMBINE: return (int64_t)n_used * h * 4 + h * 8;
+    case K_HEAD: return wb(head) + h * 8 + (int64_t)vocab * 4;
+    default: return 0;
+    }
+}
+
+// Algorithmic HBM bytes of one whole decode step attending `count` positions.
+int64_t Engine::step_bytes(int count) const {
+    int64_t b = kind_bytes(K_EMBED, count) + kind_bytes(K_HEAD, count);
+    for (int l = 0; l < n_layers; l++) {
+        const int c = layers[l].window > 0 ? std::min(count, layers[l].window) : count;
+        b += kind_bytes(K_QKV, c) + kind_bytes(K_ATTN, c) + kind_bytes(K_O, c);
+        if (n_experts == 0) b += kind_bytes(K_GATE_UP, c) + kind_bytes(K_DOWN, c);
+        else
+            for (int k : {K_ROUTER, K_ROUTE, K_EXP_GATE_UP, K_EXP_DOWN, K_COMBINE}) b += kind_bytes(k, c);
+    }
+    return b;
+}
+
+// Time `reps` back-to-back eager launches of one kind (layer 0) of sequence
+// s's step at its current position, on the engine's stream, between two HIP
+// events. The step state is left as it was.
+int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel) {
+    if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+    if (kind < K_EMBED || kind > K_HEAD || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
+    const bool moe_kind = kind >= K_ROUTER && kind <= K_COMBINE, dense_kind = kind == K_GATE_UP || kind == K_DOWN;
+    if ((n_experts == 0 && moe_kind) || (n_experts > 0 && dense_kind))
+        return fail(CJ_ERR_ARG, "time: kind %d is not part of this model's step", kind);
+    Seq &S = seqs[s];
+    if (S.pos == 0) return fail(CJ_ERR_STATE, "time: prefill first");
+    cj_step_state saved{};
+    CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipMemcpy(&saved, S.state, sizeof saved, hipMemcpyDeviceToHost));
+    only = kind;
+    int rc = enqueue_step(s);                     // one untimed launch
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+        rc = fail(CJ_ERR_HIP, "time: event create");
+    if (!rc) {
+        kernel = last_launch();
+        (void)hipEventRecord(e0, stream());
+        for (int i = 0; i < reps && !rc; i++) rc = enqueue_step(s);
+        (void)hipEventRecord(e1, stream());
+        (void)hipEventSynchronize(e1);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        *avg_us = ms * 1000.0f / (float)reps;
+    }
+    only = -1;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipMemcpy(S.state, &saved, sizeof saved, hipMemcpyHostToDevice));
+    return rc;
 }
 
 // One request to completion on slot 0: the prompt teacher-forced, then
@@ -703,6 +837,37 @@ int32_t cj_engine_trace(int64_t h, int32_t what, float *out, int64_t n) {
 float cj_engine_last_step_us(int64_t h) {
     Engine *e = eng_of(h);
     return e ? e->last_step_us : -1.0f;
+}
+
+int32_t cj_engine_time_kernel(int64_t h, int32_t seq, int32_t kind, int32_t reps, float *avg_us, int64_t *bytes,
+                              int8_t *name, int32_t name_cap) {
+    Engine *e = eng_of(h);
+    if (!e || !avg_us || !bytes) return cj::fail(CJ_ERR_ARG, "cj_engine_time_kernel: bad arguments");
+    std::string k;
+    int rc = e->time_kind(seq, kind, reps, avg_us, k);
+    if (rc) return rc;
+    const int pos = e->seqs[seq].pos;
+    const int w = e->layers.empty() ? 0 : e->layers[0].window;
+    *bytes = e->kind_bytes(kind, w > 0 ? std::min(pos + 1, w) : pos + 1);
+    if (name && name_cap > 0) {
+        const size_t n = std::min<size_t>(k.size(), (size_t)name_cap - 1);
+        memcpy(name, k.data(), n);
+        name[n] = 0;
+    }
+    return CJ_OK;
+}
+
+int32_t cj_engine_set_graphs(int64_t h, int32_t on) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    e->graphs = on != 0;
+    return CJ_OK;
+}
+
+int64_t cj_engine_step_bytes(int64_t h, int32_t count) {
+    Engine *e = eng_of(h);
+    if (!e || count <= 0) return cj::fail(CJ_ERR_ARG, "cj_engine_step_bytes: bad arguments");
+    return e->step_bytes(count);
 }
 
 }  // extern "C"

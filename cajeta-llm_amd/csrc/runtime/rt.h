@@ -11,6 +11,7 @@ namespace cj {
 
 int fail(int code, const char *fmt, ...);
 const char *last_error();
+const char *last_launch();   // the name of the last kernel launched on this thread
 
 bool ready();
 hipStream_t stream();
@@ -39,7 +40,9 @@ struct GemvPlan {
 int64_t prepared_row_bytes(int type, int64_t cols);
 bool is_f32_act(int type);
 bool gemv_supported(int type, int64_t cols);
-GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group);
+// Kernel, rows per workgroup (`target` rounded to what one pass of the
+// workgroup covers, at most 256; 0 = one pass), grid and LDS of a GEMV.
+GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target);
 int run_gemv(const cj_gemv_args &a, const GemvPlan &p);
 
 // Device memory owned by the runtime itself (not through the handle table's

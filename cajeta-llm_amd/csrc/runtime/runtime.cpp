@@ -29,6 +29,7 @@ struct Ctx {
 };
 Ctx g;
 thread_local std::string g_err;
+thread_local std::string g_last_launch;
 
 // The reference's kernel names (KernelCap.nameOf, model/KernelCap.cajeta:100-140
 // and the launch sites) answered by the kernels of this code object.
@@ -87,6 +88,7 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 const char *last_error() { return g_err.c_str(); }
+const char *last_launch() { return g_last_launch.c_str(); }
 bool ready() { return g.module != nullptr; }
 hipStream_t stream() { return g.stream; }
 int device_cus() { return g.cus; }
@@ -125,11 +127,12 @@ int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, co
     auto it = g.fns.find(name);
     if (it == g.fns.end()) return fail(CJ_ERR_NOKERNEL, "kernel %s is not in kernels.hsaco", name);
     if (grid == 0) return CJ_OK;
-    size_t sz = size;
-    void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void *>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
-                   HIP_LAUNCH_PARAM_END};
-    hipError_t e = hipModuleLaunchKernel(it->second, grid, 1, 1, block, 1, 1, lds, g.stream, nullptr, cfg);
+    (void)size;
+    // every kernel takes one argument, the struct: kernelParams[0] points at it
+    void *params[] = {const_cast<void *>(args)};
+    hipError_t e = hipModuleLaunchKernel(it->second, grid, 1, 1, block, 1, 1, lds, g.stream, params, nullptr);
     if (e != hipSuccess) return fail(CJ_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e));
+    g_last_launch = name;
     return CJ_OK;
 }
 
@@ -155,19 +158,10 @@ bool gemv_supported(int type, int64_t cols) {
     return prepared_row_bytes(type, cols) > 0 && cols <= (is_f32_act(type) ? 15360 : 16384);
 }
 
-GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
+GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target) {
     GemvPlan p;
     const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
                       : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
-    const int64_t units = (type == CJ_Q4_K || type == CJ_Q6_K) ? cols / 256 * 4 : type == CJ_F32 ? cols / 4 : cols / 32;
-    const int lpr = units >= 64 ? 64 : units >= 32 ? 32 : units >= 16 ? 16 : 8;
-    const int groups = 64 / lpr;
-    int rpg = rows_per_group > 0 ? rows_per_group : 2;
-    if (rpg & 1) rpg++;
-    // one thread per row folds the row's block terms: at most 256 rows
-    while (4 * groups * rpg > 256 && rpg > 2) rpg -= 2;
-    p.rows_per_wg = 4 * groups * rpg;
-    p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
     if (is_f32_act(type)) {
         // one thread a row, summed in element order
         p.kernel = fam;
@@ -177,13 +171,23 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int rows_per_group) {
         p.lds = 3072 + (uint32_t)((cols + 255) / 256 * 1024);
         return p;
     }
-    p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
+    // lanes a row: enough to cover a row's units (64-element chunks, or
+    // 32-element blocks for Q8_0) in one sweep where the row allows
+    const int64_t units = (type == CJ_Q4_K || type == CJ_Q6_K) ? cols / 256 * 4 : cols / 32;
+    const int lpr = units >= 64 ? 64 : units >= 32 ? 32 : units >= 16 ? 16 : 8;
+    const int groups = 64 / lpr;
+    const int nr = type == CJ_Q6_K ? 2 : 4;            // rows in flight per lane group
+    const int pass = 4 * groups * nr;                  // rows one pass of the workgroup covers
+    int R = target > pass ? target / pass * pass : pass;
+    while (R > 256) R -= pass;                         // one phase-B thread a row
+    if (R < pass) R = pass;
+    p.rows_per_wg = R;
+    p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
+    p.grid = (uint32_t)((rows + R - 1) / R);
     p.per_copy = p.grid;
-    const int64_t nblk = (cols + 255) / 256;
-    // LDS: scratch, the staged activation, then R rows of block terms
-    const int64_t terms = type == CJ_Q4_K ? cols / 256 * 2 : type == CJ_Q6_K ? cols / 256
-                        : type == CJ_Q8_0 ? (cols / 32 + 7) / 8 : 1;
-    p.lds = 3072 + (uint32_t)(is_f32_act(type) ? nblk * 256 * 4 : nblk * 320) + (uint32_t)(p.rows_per_wg * terms * 4);
+    // LDS: scratch, the staged pack, then R rows of block terms
+    const int64_t terms = type == CJ_Q4_K ? cols / 256 * 2 : type == CJ_Q6_K ? cols / 256 : (cols / 32 + 7) / 8;
+    p.lds = 3072 + (uint32_t)((cols + 255) / 256 * 320) + (uint32_t)(R * terms * 4);
     return p;
 }
 
@@ -225,7 +229,7 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
-        "cj_attn_merge", "cj_qkprep", "cj_zero", "cj_moe_route",
+        "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
     };
     for (const char *k : kernels) {
         hipFunction_t f;
@@ -434,7 +438,7 @@ int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows,
     else { a.xp = (const uint8_t *)dptr(act); a.pro = CJ_PRO_PACKED; }
     a.y = (float *)dptr(y); a.y_off = y_off; a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type;
     a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = type == CJ_Q8_0; a.batch = 1;
-    return run_gemv(a, plan_gemv(type, rows, cols, 2));
+    return run_gemv(a, plan_gemv(type, rows, cols, 32));
 }
 
 int32_t cj_glu(int64_t out, int64_t packed, int64_t gb, int64_t ub, int64_t n, int32_t form, int32_t per32) {
@@ -546,7 +550,9 @@ int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, in
     if (n <= 0 || splits <= 0 || splits > 64 || !in_buffer(dptr(part), (int64_t)n_q * 64 * (head_dim + 2) * 4) ||
         (out && !in_buffer(dptr(out), n * 4)) || (packed && !in_buffer(dptr(packed), npad / 256 * 320)) || (!out && !packed))
         return fail(CJ_ERR_ARG, "cj_attn_merge: buffers smaller than the shapes need");
-    cj_merge_args a{(float *)dptr(out), (uint8_t *)dptr(packed), (const float *)dptr(part), n_q, head_dim, splits, per32};
+    cj_merge_args a{};
+    a.out = (float *)dptr(out); a.packed = (uint8_t *)dptr(packed); a.part = (const float *)dptr(part);
+    a.n_q = n_q; a.head_dim = head_dim; a.splits = splits; a.per32 = per32;
     return launch("cj_attn_merge", (uint32_t)(npad / 256), 256, 0, a);
 }
 

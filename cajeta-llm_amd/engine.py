@@ -24,6 +24,7 @@ class EngineOptions:
         self.maxSeqs = 4
         self.device = ""
         self.cpuThreads = 0
+        self.graphs = True       # replay the captured decode step (False: eager launches)
 
 
 class SampleParams:
@@ -89,7 +90,7 @@ class LlmEngine:
         cfg = (ctypes.c_int64 * 14)()
         check(lib().cj_engine_config(h, cfg, 14), "cj_engine_config")
         keys = ("numLayers", "hiddenSize", "numHeads", "numKvHeads", "headDim", "intermediateSize", "vocabSize",
-                "ctx", "expertCount", "expertUsedCount", "weightType", "headType", "expertFfn", "splits")
+                "ctx", "expertCount", "expertUsedCount", "weightType", "headType", "expertFfn", "attnWorkers")
         self.config = dict(zip(keys, [int(v) for v in cfg]))
         self._eog = []
 
@@ -106,6 +107,8 @@ class LlmEngine:
         native.init(dev)
         h = lib().cj_engine_load(opts.model.encode(), int(opts.ctx), int(opts.maxSeqs))
         handle(h, "LlmEngine.load(%s)" % opts.model)
+        if not getattr(opts, "graphs", True):
+            check(lib().cj_engine_set_graphs(h, 0), "cj_engine_set_graphs")
         return LlmEngine(h, opts)
 
     # -- the LlmEngine surface
@@ -189,6 +192,23 @@ class LlmEngine:
 
     def lastStepMicros(self):
         return float(lib().cj_engine_last_step_us(self.h))
+
+    def timeKernel(self, kind, reps=100, seq=0):
+        """Mean µs of `reps` eager launches of one launch kind of the step
+        (layer 0), its algorithmic HBM bytes and its kernel name."""
+        us = np.zeros(1, np.float32)
+        nb = np.zeros(1, np.int64)
+        name = np.zeros(128, np.int8)
+        check(lib().cj_engine_time_kernel(self.h, seq, int(kind), int(reps), ptr(us), ptr(nb), ptr(name), 128),
+              "time kernel")
+        return float(us[0]), int(nb[0]), bytes(name.view(np.uint8)).split(b"\0")[0].decode()
+
+    def stepBytes(self, count):
+        """Algorithmic HBM bytes of one decode step attending `count` positions."""
+        v = int(lib().cj_engine_step_bytes(self.h, int(count)))
+        if v < 0:
+            check(v, "step bytes")
+        return v
 
     def __del__(self):
         try:

@@ -219,6 +219,25 @@ float cj_engine_last_step_us(int64_t eng);
  * output [n_heads·hd], 3 = SiLU·up activation [ffn], 4 = logits [vocab] —
  * each as the last layer left it. */
 int32_t cj_engine_trace(int64_t eng, int32_t what, float *out, int64_t n);
+/* Measurement seam, no counterpart in the reference's decode API (its
+ * benches time whole steps from the host): `reps` back-to-back
+ * launches of one launch kind of the slot's step, layer 0, at its current
+ * position, timed between HIP events on the engine's stream; the step state
+ * is left unchanged. kind: 0 embed, 1 q|k|v, 2 attention, 3 o, 4 gate|up,
+ * 5 down, 6 router, 7 top-k, 8 expert gate|up, 9 expert down, 10 combine,
+ * 11 head + argmax. Writes the mean µs, the launch's algorithmic HBM bytes
+ * and the kernel's name (the last one for a two-launch kind). */
+int32_t cj_engine_time_kernel(int64_t eng, int32_t seq, int32_t kind, int32_t reps, float *avg_us, int64_t *bytes,
+                              int8_t *name, int32_t name_cap);
+/* Replay the captured step graph (on != 0, the default) or enqueue the
+ * step's launches each token. The kernels and their arguments are the same;
+ * the eager form is for tools that cannot follow graph launches. No
+ * counterpart in the reference (its host loop launches each kernel). */
+int32_t cj_engine_set_graphs(int64_t eng, int32_t on);
+/* Algorithmic HBM bytes of one whole decode step attending `count`
+ * positions: weights at their GGUF size, K/V read and appended, activation
+ * vectors once. */
+int64_t cj_engine_step_bytes(int64_t eng, int32_t count);
 
 /* -------------------------------------------------- synthetic models */
 

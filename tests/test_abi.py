@@ -32,7 +32,7 @@ def test_code_object_holds_the_registered_kernels(pkg):
     table = src[src.index("static const char *kernels[]"):]
     table = table[:table.index("};")]
     registered = re.findall(r'"(cj_[a-z0-9_]+)"', table)
-    assert len(registered) > 40
+    assert len(registered) >= 30
     missing = [k for k in registered if k not in syms]
     assert not missing, missing
 
