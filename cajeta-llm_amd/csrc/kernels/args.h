@@ -134,6 +134,8 @@ typedef struct {
     int32_t window;          // >0: attend the last `window` positions only
     int32_t workers;         // split-K: the CPU worker count the split rule uses
     float scale;
+    int32_t pg_n;            // pages the sequence owns from pg_base (bounds the table prefetch)
+    int32_t pad;
 } cj_attn_args;
 
 typedef struct {

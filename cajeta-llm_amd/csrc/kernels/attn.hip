@@ -12,11 +12,11 @@
 // cj_attn_split_*: split-K (AttnKernel.attnDecodeCpuGqaKernel +
 //   cpuDecodeHead, model/AttnKernel.cajeta:4216-4314). Splits per
 //   cpuDecodeSplits (:4879-4889) for a given worker count; one workgroup per
-//   (kv head, split slot), 16 lanes per query head; a split's positions run
-//   in order through an online softmax whose scores are 16-lane partials
-//   folded pairwise. K/V for a tile of positions is staged in LDS in a
-//   lane-major layout. The last workgroup of a kv head merges the splits as
-//   reducePackBlockCpu does (:5268-5400): four interleaved sub-sums.
+//   (kv head, split slot); a split's positions run in order through an
+//   online softmax whose scores are the reference's 16 lane partials folded
+//   pairwise. cj_attn_merge (or, with an output, the last workgroup of a kv
+//   head) merges the splits as reducePackBlockCpu does (:5268-5400): four
+//   interleaved sub-sums.
 // cj_attn_scores_* + cj_attn_combine_*: attnScoreKernel (:397-425) and
 //   attnCombineKernel (:441-515): 32-lane strided dot + butterfly, then 128
 //   lanes for max, exp and sum (stride-halving tree) and the ascending-t sum
@@ -47,115 +47,184 @@ DEV void attn_window(const cj_attn_args &a, int &count, int &from) {
     if (a.window > 0 && count > a.window) { from += count - a.window; count = a.window; }
 }
 
+// One workgroup of 256 per (kv head, split slot). A split's positions go
+// through LDS a tile at a time; per tile:
+//   scores   thread (head, position): the reference's 16 lane partials
+//            (lane l: Σ_v q[l+16v]·k[l+16v], v ascending) folded as the
+//            xor-butterfly folds them — a fixed pairwise tree — so one thread
+//            makes the same adds with no cross-lane traffic;
+//   max      thread (head): the running max in position order, noting where
+//            it rises (the reference rescales there);
+//   exps     thread (head, position): the rescale factor exp(m_prev − s) and
+//            the weight exp(s − m), all independent;
+//   update   thread (head, dim): acc·c on a rise, then acc + v·p, in position
+//            order; thread (head) does the same for the sum.
 template <int HD, int G>
 DEV void split_body(const cj_attn_args &a) {
-    constexpr int VPL = HD / 16;                     // dims per lane: l, l+16, ...
-    __shared__ uint16_t ks[ATTN_TILE][16][VPL], vs[ATTN_TILE][16][VPL];
-    __shared__ int ticket;
-    const int tid = threadIdx.x, nthr = G * 16;
-    const int h = tid >> 4, l = tid & 15;
+    constexpr int TP = 64;                           // positions a tile
+    constexpr int CK = 16;                           // positions a register chunk
+    constexpr int PGMAX = 256;                       // page-table entries prefetched
+    __shared__ __align__(16) uint16_t ks[TP][HD];
+    __shared__ __align__(16) uint16_t vs[TP][HD];
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ __align__(16) float sc[G][TP], cf[G][TP], pr[G][TP], mb[G][TP], ma[G][TP];
+    __shared__ int up[G][TP];
+    __shared__ int pgs[PGMAX];
+    __shared__ float mrun[G], lrun[G];
+    const int t = threadIdx.x;
     const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
+    // q, the page table and the step state load together
+    for (int e = t; e < G * HD; e += 256) qs[e / HD][e % HD] = a.q[(int64_t)(kvh * G) * HD + e];
+    if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[a.pg_base + t] : 0;
     int count, from;
     attn_window(a, count, from);
     const int splits = decode_splits(count, a.n_kv, a.workers);
-    const int qh = kvh * G + h;
     if (sp < splits) {
         const int chunk = (count + splits - 1) / splits;
         int t0 = sp * chunk, t1 = t0 + chunk;
         if (t1 > count) t1 = count;
         if (t0 > count) t0 = count;
-        float q[VPL], acc[VPL];
+        if (t < G) { mrun[t] = -3.0e38f; lrun[t] = 0.0f; }
+        constexpr int PAIRS = G * HD / 256;          // (head, dim) pairs a thread
+        float acc[PAIRS];
 #pragma unroll
-        for (int v = 0; v < VPL; v++) { q[v] = a.q[(int64_t)qh * HD + 16 * v + l]; acc[v] = 0.0f; }
-        float m = -3.0e38f, ls = 0.0f;
-        for (int tb = t0; tb < t1; tb += ATTN_TILE) {
-            const int n = t1 - tb < ATTN_TILE ? t1 - tb : ATTN_TILE;
+        for (int k = 0; k < PAIRS; k++) acc[k] = 0.0f;
+        for (int tb = t0; tb < t1; tb += TP) {
+            const int n = t1 - tb < TP ? t1 - tb : TP;
             __syncthreads();
-            // stage: 16-byte chunks (8 dims) of each position's K and V row,
-            // all loads issued before the scatter of element d of position p
-            // to [p][d % 16][d / 16]
-            {
-                constexpr int CPP = HD / 8;                      // chunks a position
-                constexpr int CH = ATTN_TILE * CPP / (G * 16);   // chunks a thread
-                uint4 kq[CH], vq[CH];
+            // stage the tile's K and V rows (16-byte chunks, natural layout)
+            constexpr int CPP = HD / 8;
+            for (int c = t; c < n * CPP; c += 256) {
+                const int p = c / CPP, j = c % CPP;
+                const int pos = from + tb + p, pi = pos >> 6;
+                const int page = pi < PGMAX ? pgs[pi] : a.pgtab[a.pg_base + pi];
+                const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;
+                *(uint4 *)&ks[p][8 * j] = *(const uint4 *)(a.kc + base);
+                *(uint4 *)&vs[p][8 * j] = *(const uint4 *)(a.vc + base);
+            }
+            __syncthreads();
+            // scores: thread (head, position)
+            for (int hp = t; hp < G * TP; hp += 256) {
+                const int h = hp / TP, p = hp % TP;
+                if (p < n) {
+                    float part[16];
 #pragma unroll
-                for (int c = 0; c < CH; c++) {
-                    const int e = tid + c * nthr, p = e / CPP, j = e % CPP;
-                    if (p < n) {
-                        const int64_t base = kv_at(a.pgtab, a.pg_base, from + tb + p, a.n_kv, kvh, HD) + 8 * j;
-                        kq[c] = *(const uint4 *)(a.kc + base);
-                        vq[c] = *(const uint4 *)(a.vc + base);
-                    }
+                    for (int l = 0; l < 16; l++) part[l] = __fmul_rn(qs[h][l], h2f(ks[p][l]));
+#pragma unroll
+                    for (int v = 1; v < HD / 16; v++)
+#pragma unroll
+                        for (int l = 0; l < 16; l++)
+                            part[l] = __fadd_rn(part[l], __fmul_rn(qs[h][l + 16 * v], h2f(ks[p][l + 16 * v])));
+#pragma unroll
+                    for (int w = 1; w < 16; w <<= 1)
+#pragma unroll
+                        for (int l = 0; l < 16; l += 2 * w) part[l] = __fadd_rn(part[l], part[l + w]);
+                    sc[h][p] = __fmul_rn(part[0], a.scale);
                 }
+            }
+            __syncthreads();
+            // running max, in position order (scores read a chunk ahead)
+            if (t < G) {
+                float m = mrun[t];
+                for (int p0 = 0; p0 < n; p0 += CK) {
+                    float sv[CK];
 #pragma unroll
-                for (int c = 0; c < CH; c++) {
-                    const int e = tid + c * nthr, p = e / CPP, j = e % CPP;
-                    if (p < n) {
-                        const uint32_t kw[4] = {kq[c].x, kq[c].y, kq[c].z, kq[c].w};
-                        const uint32_t vw[4] = {vq[c].x, vq[c].y, vq[c].z, vq[c].w};
+                    for (int p = 0; p < CK; p += 4) {
+                        const float4 f = *(const float4 *)&sc[t][p0 + p];
+                        sv[p] = f.x; sv[p + 1] = f.y; sv[p + 2] = f.z; sv[p + 3] = f.w;
+                    }
 #pragma unroll
-                        for (int i = 0; i < 8; i++) {
-                            const int d = 8 * j + i;
-                            ks[p][d & 15][d >> 4] = (uint16_t)(kw[i >> 1] >> (16 * (i & 1)));
-                            vs[p][d & 15][d >> 4] = (uint16_t)(vw[i >> 1] >> (16 * (i & 1)));
+                    for (int p = 0; p < CK; p++) {
+                        if (p0 + p < n) {
+                            mb[t][p0 + p] = m;
+                            up[t][p0 + p] = sv[p] > m;
+                            if (sv[p] > m) m = sv[p];
+                            ma[t][p0 + p] = m;
                         }
                     }
                 }
+                mrun[t] = m;
             }
             __syncthreads();
-            for (int p = 0; p < n; p++) {
-                float kf[VPL], vf[VPL];
-#pragma unroll
-                for (int v = 0; v < VPL; v++) { kf[v] = h2f(ks[p][l][v]); vf[v] = h2f(vs[p][l][v]); }
-                float d = __fmul_rn(q[0], kf[0]);
-#pragma unroll
-                for (int v = 1; v < VPL; v++) d = __fadd_rn(d, __fmul_rn(q[v], kf[v]));
-                d = __fadd_rn(d, __shfl_xor(d, 1));
-                d = __fadd_rn(d, __shfl_xor(d, 2));
-                d = __fadd_rn(d, __shfl_xor(d, 4));
-                d = __fadd_rn(d, __shfl_xor(d, 8));
-                const float sc = __fmul_rn(d, a.scale);
-                if (sc > m) {
-                    const float c = cj_expf(m - sc);
-#pragma unroll
-                    for (int v = 0; v < VPL; v++) acc[v] = __fmul_rn(acc[v], c);
-                    ls = __fmul_rn(ls, c);
-                    m = sc;
+            // rescale factors (exactly 1 where the max holds: x·1 = x) and weights
+            for (int hp = t; hp < G * TP; hp += 256) {
+                const int h = hp / TP, p = hp % TP;
+                if (p < n) {
+                    cf[h][p] = up[h][p] ? cj_expf(mb[h][p] - sc[h][p]) : 1.0f;
+                    pr[h][p] = cj_expf(sc[h][p] - ma[h][p]);
                 }
-                const float pr = cj_expf(sc - m);
-                ls = __fadd_rn(ls, pr);
+            }
+            __syncthreads();
+            // the recurrences, in position order, operands a chunk ahead
 #pragma unroll
-                for (int v = 0; v < VPL; v++) acc[v] = __fadd_rn(acc[v], __fmul_rn(vf[v], pr));
+            for (int k = 0; k < PAIRS; k++) {
+                const int e = t + 256 * k, h = e / HD, d = e % HD;
+                float x = acc[k];
+                for (int p0 = 0; p0 < n; p0 += CK) {
+                    float cv[CK], pv[CK], vv[CK];
+#pragma unroll
+                    for (int p = 0; p < CK; p += 4) {
+                        const float4 c4 = *(const float4 *)&cf[h][p0 + p], p4 = *(const float4 *)&pr[h][p0 + p];
+                        cv[p] = c4.x; cv[p + 1] = c4.y; cv[p + 2] = c4.z; cv[p + 3] = c4.w;
+                        pv[p] = p4.x; pv[p + 1] = p4.y; pv[p + 2] = p4.z; pv[p + 3] = p4.w;
+                    }
+#pragma unroll
+                    for (int p = 0; p < CK; p++) vv[p] = h2f(vs[p0 + p][d]);
+#pragma unroll
+                    for (int p = 0; p < CK; p++) {
+                        if (p0 + p < n) {
+                            x = __fmul_rn(x, cv[p]);
+                            x = __fadd_rn(x, __fmul_rn(vv[p], pv[p]));
+                        }
+                    }
+                }
+                acc[k] = x;
+            }
+            if (t < G) {
+                float ls = lrun[t];
+                for (int p = 0; p < n; p++) {
+                    ls = __fmul_rn(ls, cf[t][p]);
+                    ls = __fadd_rn(ls, pr[t][p]);
+                }
+                lrun[t] = ls;
             }
         }
-        float *pb = a.part + ((int64_t)qh * ATTN_MAX_SPLITS + sp) * (HD + 2);
+        __syncthreads();
 #pragma unroll
-        for (int v = 0; v < VPL; v++) pb[16 * v + l] = acc[v];
-        if (l == 0) { pb[HD] = m; pb[HD + 1] = ls; }
+        for (int k = 0; k < PAIRS; k++) {
+            const int e = t + 256 * k, h = e / HD, d = e % HD;
+            a.part[((int64_t)(kvh * G + h) * ATTN_MAX_SPLITS + sp) * (HD + 2) + d] = acc[k];
+        }
+        if (t < G) {
+            float *pb = a.part + ((int64_t)(kvh * G + t) * ATTN_MAX_SPLITS + sp) * (HD + 2);
+            pb[HD] = mrun[t];
+            pb[HD + 1] = lrun[t];
+        }
     }
     if (!a.out) return;
 
     // the last workgroup of this kv head merges its splits
+    __shared__ int ticket;
     __threadfence();
     __syncthreads();
-    if (tid == 0) ticket = atomicAdd(&a.counters[kvh], 1);
+    if (t == 0) ticket = atomicAdd(&a.counters[kvh], 1);
     __syncthreads();
     if (ticket != ATTN_MAX_SPLITS - 1) return;
     __threadfence();
-    for (int e = tid; e < G * HD; e += nthr) {
+    for (int e = t; e < G * HD; e += 256) {
         const int hh = e / HD, dd = e % HD;
         const int qq = kvh * G + hh;
         const float *pb0 = a.part + (int64_t)qq * ATTN_MAX_SPLITS * (HD + 2);
         float gm = -3.0e38f;
-        for (int s = 0; s < splits; s++) {
-            const float mv = pb0[s * (HD + 2) + HD];
+        for (int s2 = 0; s2 < splits; s2++) {
+            const float mv = pb0[s2 * (HD + 2) + HD];
             if (mv > gm) gm = mv;
         }
         float tacc = 0.0f, gt = 0.0f;
         for (int sub = 0; sub < 4; sub++) {
             float gl = 0.0f, ac = 0.0f;
-            for (int s = sub; s < splits; s += 4) {
-                const float *pb = pb0 + s * (HD + 2);
+            for (int s2 = sub; s2 < splits; s2 += 4) {
+                const float *pb = pb0 + s2 * (HD + 2);
                 const float lsv = pb[HD + 1];
                 if (lsv > 0.0f) {
                     const float wt = cj_expf(pb[HD] - gm);
@@ -168,11 +237,11 @@ DEV void split_body(const cj_attn_args &a) {
         }
         a.out[(int64_t)qq * HD + dd] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
     }
-    if (tid == 0) a.counters[kvh] = 0;
+    if (t == 0) a.counters[kvh] = 0;
 }
 
 #define SPLIT_KERNEL(HD, G) \
-    extern "C" __global__ void __launch_bounds__(G * 16) cj_attn_split_h##HD##_g##G(cj_attn_args a) { split_body<HD, G>(a); }
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h##HD##_g##G(cj_attn_args a) { split_body<HD, G>(a); }
 SPLIT_KERNEL(128, 4)
 SPLIT_KERNEL(128, 8)
 
@@ -255,65 +324,64 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_a
 // contract), the merge in reducePackBlockCpu's order: the global max, then
 // four interleaved sub-sums (splits s ≡ 0, 1, 2, 3 mod 4, each ascending) of
 // w_s·l_s and of w_s·acc_s[d], w_s = exp(m_s − max), added in sub order;
-// out = acc · (1 / l). The (head, split) weights are computed once in LDS.
+// out = acc · (1 / l).
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
-    __shared__ float wts[4][ATTN_MAX_SPLITS];     // per head of the block, per split (0: skipped)
-    __shared__ int use[4][ATTN_MAX_SPLITS];
-    __shared__ float gsum[4];
     const int t = threadIdx.x;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
+    // thread t: output e (head h, dim d). Its 64 accumulators are loaded
+    // first; meanwhile wave w (< heads in the block) reads head h0+w's
+    // (max, sum) pairs, one split a lane, and leaves the weights in LDS.
+    __shared__ float wts[4][ATTN_MAX_SPLITS], lsum[4][ATTN_MAX_SPLITS];
+    __shared__ int use[4][ATTN_MAX_SPLITS];
+    const int h0 = (int)((int64_t)blockIdx.x * 256 / hd), nh = hd >= 256 ? 1 : 256 / hd;
+    // every slot of the partials is loaded (the buffer holds 64 a head); the
+    // step's split count only masks the arithmetic, so no load waits on it
+    float pv[ATTN_MAX_SPLITS];
+    const int h = (int)(e / hd), d = (int)(e % hd);
+    {
+        const float *pb0 = a.part + (int64_t)(e < n ? h : 0) * ATTN_MAX_SPLITS * (hd + 2) + d;
+#pragma unroll
+        for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2)];
+    }
     int splits = a.splits;
     if (a.state) {
         int count = a.state->pos + 1;
         if (a.window > 0 && count > a.window) count = a.window;
         splits = decode_splits(count, a.n_kv, a.workers);
     }
-    const int h0 = (int)((int64_t)blockIdx.x * 256 / hd);     // first head of the block
-    const int nh = 256 / hd < 1 ? 1 : 256 / hd;                 // heads a block (hd 64 or 128)
-    // per (head, split): the weight, from the head's max over its splits
     {
-        const int hh = t / ATTN_MAX_SPLITS, sp = t % ATTN_MAX_SPLITS;
-        if (hh < nh && h0 + hh < a.n_q) {
-            const float *pb0 = a.part + (int64_t)(h0 + hh) * ATTN_MAX_SPLITS * (hd + 2);
-            float gm = -3.0e38f;
-            for (int s2 = 0; s2 < splits; s2++) {
-                const float mv = pb0[s2 * (hd + 2) + hd];
-                if (mv > gm) gm = mv;
-            }
-            const bool on = sp < splits && pb0[sp * (hd + 2) + hd + 1] > 0.0f;
-            use[hh][sp] = on;
-            wts[hh][sp] = on ? cj_expf(pb0[sp * (hd + 2) + hd] - gm) : 0.0f;
+        const int w = t >> 6, sl = t & 63;
+        if (w < nh) {
+            const int hw = h0 + w < a.n_q ? h0 + w : 0;
+            const float *pb = a.part + ((int64_t)hw * ATTN_MAX_SPLITS + sl) * (hd + 2) + hd;
+            const float m0 = pb[0], l0 = pb[1];
+            const bool in = h0 + w < a.n_q && sl < splits;
+            const float mv = in ? m0 : -3.0e38f, lv = in ? l0 : 0.0f;
+            const float gm = group_max<64>(mv);
+            const bool on = in && lv > 0.0f;
+            use[w][sl] = on;
+            wts[w][sl] = on ? cj_expf(mv - gm) : 0.0f;
+            lsum[w][sl] = lv;
         }
-    }
-    __syncthreads();
-    if (t < nh && h0 + t < a.n_q) {
-        const float *pb0 = a.part + (int64_t)(h0 + t) * ATTN_MAX_SPLITS * (hd + 2);
-        float gt = 0.0f;
-        for (int sub = 0; sub < 4; sub++) {
-            float gl = 0.0f;
-            for (int s2 = sub; s2 < splits; s2 += 4)
-                if (use[t][s2]) gl = __fadd_rn(gl, __fmul_rn(wts[t][s2], pb0[s2 * (hd + 2) + hd + 1]));
-            gt = sub == 0 ? gl : __fadd_rn(gt, gl);
-        }
-        gsum[t] = gt;
     }
     __syncthreads();
     float x = 0.0f;
     if (e < n) {
-        const int h = (int)(e / hd), d = (int)(e % hd), hh = h - h0;
-        const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2) + d;
-        float ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < splits; s0 += 4) {
+        const int hh = h - h0;
+        float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int sub = 0; sub < 4; sub++) {
-                const int s2 = s0 + sub;
-                if (s2 < splits && use[hh][s2]) ac[sub] = __fadd_rn(ac[sub], __fmul_rn(pb0[s2 * (hd + 2)], wts[hh][s2]));
+        for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
+            if (s2 < splits && use[hh][s2]) {
+                const float w = wts[hh][s2];
+                gl[s2 & 3] = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lsum[hh][s2]));
+                ac[s2 & 3] = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
             }
         }
+        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
         const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
-        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gsum[hh]));
+        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
         if (a.out) a.out[e] = x;
     }
     if (!a.packed) return;

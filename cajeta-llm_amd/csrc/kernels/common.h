@@ -156,8 +156,15 @@ DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
         __syncthreads();
         return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
     }
+    // the row's values loaded at once (up to 64 a thread), then summed in order
+    float xv[64];
+    const int kn = (int)(n >> 8);
+#pragma unroll
+    for (int k = 0; k < 64; k++) xv[k] = k < kn ? x[t + 256 * k] : 0.0f;
     float p = 0.0f;
-    for (int64_t e = t; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
+#pragma unroll
+    for (int k = 0; k < 64; k++) if (k < kn) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
+    for (int64_t e = t + 256 * 64; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
     __syncthreads();
     if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);

@@ -4,7 +4,7 @@
 // in LDS (a copied pack, the pack of an f32 vector, or RMSNorm + pack). Then:
 //
 //   phase A  lanes stream the weight rows with 128-bit loads — lanes across a
-//            row's blocks, LPR lanes a row, two rows in flight — and compute
+//            row's blocks, LPR lanes a row, NR (4 or 2) rows in flight — and compute
 //            each block's exact terms: integer dot4s for the quants, the
 //            6-bit scales and mins in integer space, the quad of lanes that
 //            shares a block summed exactly, then the block's f32 terms as the
@@ -296,7 +296,7 @@ DEV bool argmax_take(float ov, int oi, float mv, int mi) {
 
 // ------------------------------------------------------------------ body
 
-template <int FMT, int LPR>
+template <int FMT, int LPR, int NR>
 DEV void gemv_body(const cj_gemv_args &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *red = (float *)smem;
@@ -348,7 +348,6 @@ DEV void gemv_body(const cj_gemv_args &a) {
     // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
     {
         constexpr int G = 64 / LPR;
-        constexpr int NR = FMT == CJ_Q6_K ? 2 : 4;
         const int group = lane / LPR, slot = lane % LPR;
         const int lanes_groups = 4 * G;                      // row groups across the workgroup
         const int nb = (int)(cols / 256), nb32 = (int)(cols / 32);
@@ -504,20 +503,30 @@ DEV void gemv_body(const cj_gemv_args &a) {
     }
 }
 
-#define GEMV_KERNEL(NAME, FMT, LPR)                                                    \
+#define GEMV_KERNEL(NAME, FMT, LPR, NR)                                                \
     extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) {            \
-        gemv_body<FMT, LPR>(a);                                                         \
+        gemv_body<FMT, LPR, NR>(a);                                                     \
     }
 
-#define GEMV_FAMILY(PFX, FMT)               \
-    GEMV_KERNEL(PFX##_l64, FMT, 64)         \
-    GEMV_KERNEL(PFX##_l32, FMT, 32)         \
-    GEMV_KERNEL(PFX##_l16, FMT, 16)         \
-    GEMV_KERNEL(PFX##_l8, FMT, 8)
+#define GEMV_FAMILY(PFX, FMT, NR)               \
+    GEMV_KERNEL(PFX##_l64, FMT, 64, NR)         \
+    GEMV_KERNEL(PFX##_l32, FMT, 32, NR)         \
+    GEMV_KERNEL(PFX##_l16, FMT, 16, NR)         \
+    GEMV_KERNEL(PFX##_l8, FMT, 8, NR)
 
-GEMV_FAMILY(cj_gemv_q4k, CJ_Q4_K)
-GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K)
-GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0)
-GEMV_KERNEL(cj_gemv_q40, CJ_Q4_0, 64)
-GEMV_KERNEL(cj_gemv_mxfp4, CJ_MXFP4, 64)
-GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64)
+// cj_gemv_<fmt>_l<LPR>[_n2]: LPR lanes a row, 4 (or 2: _n2, and Q6_K) rows
+// in flight per lane group
+#define GEMV_FAMILY_N2(PFX, FMT)                    \
+    GEMV_KERNEL(PFX##_l64_n2, FMT, 64, 2)           \
+    GEMV_KERNEL(PFX##_l32_n2, FMT, 32, 2)           \
+    GEMV_KERNEL(PFX##_l16_n2, FMT, 16, 2)           \
+    GEMV_KERNEL(PFX##_l8_n2, FMT, 8, 2)
+
+GEMV_FAMILY(cj_gemv_q4k, CJ_Q4_K, 4)
+GEMV_FAMILY_N2(cj_gemv_q4k, CJ_Q4_K)
+GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
+GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
+GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)
+GEMV_KERNEL(cj_gemv_q40, CJ_Q4_0, 64, 1)
+GEMV_KERNEL(cj_gemv_mxfp4, CJ_MXFP4, 64, 1)
+GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64, 1)

@@ -25,6 +25,50 @@ extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
     for (int i = threadIdx.x; i < nblk * 20; i += 256) ((uint4 *)o)[i] = ((const uint4 *)sx)[i];
 }
 
+// RMSNorm + pack of one row, one workgroup per 256-wide block. Every
+// workgroup forms the row's sum of squares itself in the reference order
+// (thread t: x[t + 256k], k ascending, then the 128..1 tree; or element order
+// for widths that are not whole 256s) from loads it issues at once, then
+// packs its own block: no workgroup waits on another.
+extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) {
+    __shared__ float red[256];
+    __shared__ float bmax[8];
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t blk = blockIdx.x, e = blk * 256 + t;
+    const float xe = e < a.n ? a.x[e] : 0.0f;
+    const float we = e < a.n ? a.w[e] : 0.0f;
+    const float scale = stage_norm_scale(a.x, a.n, a.eps, red);
+    const float wi = a.form == 1 ? __fadd_rn(1.0f, we) : we;
+    const float v = e < a.n ? __fmul_rn(__fmul_rn(xe, scale), wi) : 0.0f;
+    if (a.xout && e < a.n) a.xout[e] = v;
+    if (!a.out) return;
+    const float av = fabsf(v);
+    float am;
+    if (a.per32) {
+        const float mm = group_max<32>(av);
+        if ((lane & 31) == 0) bmax[t >> 5] = mm;
+        __syncthreads();
+        am = bmax[t >> 5];
+    } else {
+        const float mm = group_max<64>(av);
+        if (lane == 0) bmax[t >> 6] = mm;
+        __syncthreads();
+        am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
+    }
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    const int q = round_away(__fmul_rn(v, inv));
+    uint8_t *ob = a.out + blk * 320;
+    ob[t] = (uint8_t)(int8_t)q;
+    const int s = group_sum_i<32>(q);
+    if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
+    if (a.per32) {
+        if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
+    } else {
+        if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
+        pack_zero_pad(ob, t);
+    }
+}
+
 // ------------------------------------------------------------------ glu
 
 // One workgroup per 256-wide block: out = act(g)·u, then (optionally) that

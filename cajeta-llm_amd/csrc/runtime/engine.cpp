@@ -66,7 +66,8 @@ struct Request {
 // The launches of one decode step, by kind (the timing seam addresses one).
 enum Kind {
     K_EMBED = 0, K_QKV = 1, K_ATTN = 2, K_O = 3, K_GATE_UP = 4, K_DOWN = 5,
-    K_ROUTER = 6, K_ROUTE = 7, K_EXP_GATE_UP = 8, K_EXP_DOWN = 9, K_COMBINE = 10, K_HEAD = 11
+    K_ROUTER = 6, K_ROUTE = 7, K_EXP_GATE_UP = 8, K_EXP_DOWN = 9, K_COMBINE = 10, K_HEAD = 11,
+    K_NORM = 12   // RMSNorm + pack of the residual (before q|k|v; the FFN and head ones alike)
 };
 
 }  // namespace
@@ -87,7 +88,8 @@ struct Engine {
     float *rope = nullptr;
     // scratch
     float *hs = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *part = nullptr;
-    uint8_t *act_pack = nullptr, *attn_pack = nullptr;
+    uint8_t *act_pack = nullptr, *attn_pack = nullptr, *xpack = nullptr;
+    float *xn = nullptr;       // the normed residual as f32 (f32-activation consumers)
     int32_t *glu_counters = nullptr, *argmax_counter = nullptr, *attn_counters = nullptr;
     float *part_v = nullptr;
     int32_t *part_i = nullptr;
@@ -124,6 +126,7 @@ struct Engine {
     int capture(int s);
     int enqueue_step(int s);
     int run_step(int s);
+    int norm_pack(const float *w, int per32, bool f32_out);
     int prefill(int s, const int32_t *toks, int n);
     int decode(int s, int steps, int32_t *out);
     int reset(int s);
@@ -314,6 +317,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     act = (float *)alloc((size_t)fmax * 4 + 1024);
     act_pack = (uint8_t *)alloc((size_t)fpad / 256 * 320);
     attn_pack = (uint8_t *)alloc((size_t)(qd + 255) / 256 * 320);
+    xpack = (uint8_t *)alloc((size_t)(hidden + 255) / 256 * 320);
+    xn = (float *)alloc((size_t)hidden * 4);
     logits = (float *)alloc((size_t)vocab * 4);
     // split-K partials [n_heads][64][hd + 2], or two-pass scores [n_heads][ctx]
     part = (float *)alloc((size_t)n_heads * std::max<int64_t>(64 * (head_dim + 2), ctx) * 4);
@@ -327,7 +332,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     moe_w = (float *)alloc(64 * 4);
     moe_sel = (int32_t *)alloc(64 * 4);
     moe_y = (float *)alloc((size_t)hidden * std::max(1, n_used) * 4);
-    if (!hs || !q || !attn || !act || !act_pack || !attn_pack || !logits || !part || !glu_counters || !argmax_counter ||
+    if (!hs || !q || !attn || !act || !act_pack || !attn_pack || !xpack || !xn || !logits || !part || !glu_counters || !argmax_counter ||
         !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y)
         return fail(CJ_ERR_HIP, "model: out of device memory (scratch)");
     CJ_HIP(hipMemset(glu_counters, 0, (size_t)fpad / 256 * 4 + 64));
@@ -374,24 +379,25 @@ int Engine::enqueue_step(int s) {
     snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
-        if (want(K_QKV, l)) {   // 1. q|k|v with norm+pack prologue, RoPE + K/V append epilogue
+        if (want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false))) return rc;
+        if (want(K_QKV, l)) {   // 1. q|k|v over the pack, RoPE + K/V append epilogue
             cj_gemv_args a{};
-            a.w = (const uint8_t *)L.qkv.p; a.x = hs; a.nw = L.attn_norm; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
+            a.w = (const uint8_t *)L.qkv.p; a.xp = xpack; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
             a.pgtab = pgtab; a.rope_cs = rope; a.state = S.state; a.rows = L.qkv.rows; a.cols = hidden;
-            a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_QKV_ROPE;
+            a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_QKV_ROPE;
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
             a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
         }
         if (want(K_ATTN, l)) {   // 2. attention
             cj_attn_args a{};
             a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
             a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
-            a.pg_base = S.pg_base; a.window = L.window; a.scale = scale;
+            a.pg_base = S.pg_base; a.pg_n = pages_per_seq; a.window = L.window; a.scale = scale;
             if (split) {
                 // partials, then the merge + the pack the o projection reads
                 a.out = nullptr;
-                if ((rc = launch(attn_kernel, (uint32_t)(n_kv * 64), (uint32_t)(grp * 16), 0, a))) return rc;
+                if ((rc = launch(attn_kernel, (uint32_t)(n_kv * 64), 256, 0, a))) return rc;
                 cj_merge_args m{};
                 m.out = attn; m.packed = attn_pack; m.part = part; m.state = S.state; m.n_q = n_heads;
                 m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0; m.n_kv = n_kv; m.workers = workers;
@@ -410,30 +416,34 @@ int Engine::enqueue_step(int s) {
             a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
             a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split ? CJ_PRO_PACKED : CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
+        }
+        if (want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
+            const int ct = n_experts ? L.gu_exps.type : L.gu.type;
+            if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0))) return rc;
         }
         if (n_experts == 0) {
-            if (want(K_GATE_UP, l)) {   // 4. gate|up with norm+pack prologue, SiLU·up + pack epilogue
+            if (want(K_GATE_UP, l)) {   // 4. gate|up over the pack, SiLU·up epilogue
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.gu.p; a.x = hs; a.nw = L.ffn_norm; a.act = act;
+                a.w = (const uint8_t *)L.gu.p; a.xp = xpack; a.act = act;
                 a.rows = L.gu.rows; a.cols = hidden; a.row_bytes = L.gu.row_bytes;
-                a.type = L.gu.type; a.pro = CJ_PRO_NORM_PACK; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
+                a.type = L.gu.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
                 a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
                 a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
             }
             if (want(K_DOWN, l)) {   // 5. down, residual into hs
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.down.p; a.x = act; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
                 a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
                 a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
             }
         } else {
             if (want(K_ROUTER, l)) {   // router logits from the normed hidden (f32 weights)
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.router.p; a.x = hs; a.nw = L.ffn_norm; a.y = moe_logits; a.rows = n_experts;
-                a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_NORM_F32;
+                a.w = (const uint8_t *)L.router.p; a.x = xn; a.y = moe_logits; a.rows = n_experts;
+                a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_F32;
                 a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
                 if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0)))) return rc;
             }
@@ -443,9 +453,9 @@ int Engine::enqueue_step(int s) {
             }
             if (want(K_EXP_GATE_UP, l)) {   // the selected experts' gate|up, SiLU·up into act[k]
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.gu_exps.p; a.x = hs; a.nw = L.ffn_norm; a.act = act; a.rows = 2 * (int64_t)expert_ffn;
+                a.w = (const uint8_t *)L.gu_exps.p; a.x = xn; a.xp = xpack; a.act = act; a.rows = 2 * (int64_t)expert_ffn;
                 a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
-                a.pro = is_f32_act(a.type) ? CJ_PRO_NORM_F32 : CJ_PRO_NORM_PACK; a.epi = CJ_EPI_GLU; a.eps = eps;
+                a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.eps = eps;
                 a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
                 a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
                 a.y_stride = expert_ffn;
@@ -466,13 +476,14 @@ int Engine::enqueue_step(int s) {
             }
         }
     }
-    if (want(K_HEAD, 0)) {   // final norm + head + greedy argmax; advances the step
+    if (only < 0 && (rc = norm_pack(out_norm, head.type == CJ_Q8_0, is_f32_act(head.type)))) return rc;
+    if (want(K_HEAD, 0)) {   // head over the final norm's pack + greedy argmax; advances the step
         cj_gemv_args a{};
-        a.w = (const uint8_t *)head.p; a.x = hs; a.nw = out_norm; a.y = logits;
+        a.w = (const uint8_t *)head.p; a.x = xn; a.xp = xpack; a.y = logits;
         a.part_v = part_v; a.part_i = part_i; a.tokens = S.tokens; a.preds = S.preds; a.state = S.state;
         if (only == K_HEAD) { a.state = nullptr; a.pos = S.pos; }   // timed alone: leave the step where it is
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
-        a.pro = is_f32_act(head.type) ? CJ_PRO_NORM_F32 : CJ_PRO_NORM_PACK; a.epi = CJ_EPI_ARGMAX;
+        a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
         GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
@@ -501,6 +512,17 @@ int Engine::capture(int s) {
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) { S.graph = nullptr; return fail(CJ_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e)); }
     return CJ_OK;
+}
+
+// RMSNorm of the residual hs with weight w, once for all the workgroups of
+// the next projection: its pack into xpack and, for f32-activation
+// consumers, the normed values into xn (one workgroup; the norm is a
+// reduction over the whole row).
+int Engine::norm_pack(const float *w, int per32, bool f32_out) {
+    cj_pack_args a{};
+    a.out = xpack; a.x = hs; a.w = w; a.xout = f32_out ? xn : nullptr; a.n = hidden;
+    a.npad = ((int64_t)hidden + 255) / 256 * 256; a.rows = 1; a.eps = eps; a.form = 0; a.per32 = per32; a.do_norm = 1;
+    return launch("cj_norm_pack", (uint32_t)(a.npad / 256), 256, 0, a);
 }
 
 // One decode step of slot s on the stream: the graph, or its launches.
@@ -588,14 +610,13 @@ int64_t Engine::kind_bytes(int kind, int count) const {
     const Layer &L = layers[0];
     const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim, h = hidden;
     auto wb = [](const DevW &w) { return w.rows * ggml_row_bytes(w.type, w.cols); };
-    const int64_t fpad = ((int64_t)ffn + 255) / 256 * 256;
     switch (kind) {
     case K_EMBED: return embd_row_file_bytes + h * 4;
-    case K_QKV: return wb(L.qkv) + h * 8 + qd * 4 + 2 * kvd * 2;
-    case K_ATTN: return (int64_t)count * kvd * 2 * 2 + qd * 8;
-    case K_O: return wb(L.o) + qd * 4 + h * 8;
-    case K_GATE_UP: return wb(L.gu) + h * 8 + (int64_t)ffn * 4 + fpad / 256 * 320;
-    case K_DOWN: return wb(L.down) + fpad / 256 * 320 + h * 8;
+    case K_QKV: return wb(L.qkv) + ((h + 255) / 256) * 320 + qd * 4 + 2 * kvd * 2;
+    case K_ATTN: return (int64_t)count * kvd * 2 * 2 + qd * 8 + ((qd + 255) / 256) * 320;
+    case K_O: return wb(L.o) + ((qd + 255) / 256) * 320 + h * 8;
+    case K_GATE_UP: return wb(L.gu) + ((h + 255) / 256) * 320 + (int64_t)ffn * 4;
+    case K_DOWN: return wb(L.down) + (int64_t)ffn * 4 + h * 8;
     case K_ROUTER: return wb(L.router) + h * 8 + (int64_t)n_experts * 4;
     case K_ROUTE: return (int64_t)n_experts * 4 + (int64_t)n_used * 8;
     case K_EXP_GATE_UP:
@@ -603,17 +624,18 @@ int64_t Engine::kind_bytes(int kind, int count) const {
     case K_EXP_DOWN:
         return n_used * (h * ggml_row_bytes(L.down_exps.type, expert_ffn)) + (int64_t)n_used * (expert_ffn + h) * 4;
     case K_COMBINE: return (int64_t)n_used * h * 4 + h * 8;
-    case K_HEAD: return wb(head) + h * 8 + (int64_t)vocab * 4;
+    case K_HEAD: return wb(head) + ((h + 255) / 256) * 320 + (int64_t)vocab * 4;
+    case K_NORM: return h * 8 + ((h + 255) / 256) * 320;
     default: return 0;
     }
 }
 
 // Algorithmic HBM bytes of one whole decode step attending `count` positions.
 int64_t Engine::step_bytes(int count) const {
-    int64_t b = kind_bytes(K_EMBED, count) + kind_bytes(K_HEAD, count);
+    int64_t b = kind_bytes(K_EMBED, count) + kind_bytes(K_HEAD, count) + kind_bytes(K_NORM, count);
     for (int l = 0; l < n_layers; l++) {
         const int c = layers[l].window > 0 ? std::min(count, layers[l].window) : count;
-        b += kind_bytes(K_QKV, c) + kind_bytes(K_ATTN, c) + kind_bytes(K_O, c);
+        b += 2 * kind_bytes(K_NORM, c) + kind_bytes(K_QKV, c) + kind_bytes(K_ATTN, c) + kind_bytes(K_O, c);
         if (n_experts == 0) b += kind_bytes(K_GATE_UP, c) + kind_bytes(K_DOWN, c);
         else
             for (int k : {K_ROUTER, K_ROUTE, K_EXP_GATE_UP, K_EXP_DOWN, K_COMBINE}) b += kind_bytes(k, c);
@@ -626,7 +648,7 @@ int64_t Engine::step_bytes(int count) const {
 // events. The step state is left as it was.
 int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel) {
     if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
-    if (kind < K_EMBED || kind > K_HEAD || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
+    if (kind < K_EMBED || kind > K_NORM || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
     const bool moe_kind = kind >= K_ROUTER && kind <= K_COMBINE, dense_kind = kind == K_GATE_UP || kind == K_DOWN;
     if ((n_experts == 0 && moe_kind) || (n_experts > 0 && dense_kind))
         return fail(CJ_ERR_ARG, "time: kind %d is not part of this model's step", kind);

@@ -176,13 +176,16 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target) {
     const int64_t units = (type == CJ_Q4_K || type == CJ_Q6_K) ? cols / 256 * 4 : cols / 32;
     const int lpr = units >= 64 ? 64 : units >= 32 ? 32 : units >= 16 ? 16 : 8;
     const int groups = 64 / lpr;
-    const int nr = type == CJ_Q6_K ? 2 : 4;            // rows in flight per lane group
+    // rows in flight per lane group: 4, or 2 where the target asks for fewer
+    // rows a workgroup than a 4-row pass covers (more workgroups on short
+    // matrices); Q6_K always 2 (register budget)
+    const int nr = type == CJ_Q6_K || target < 4 * groups * 4 ? 2 : 4;
     const int pass = 4 * groups * nr;                  // rows one pass of the workgroup covers
     int R = target > pass ? target / pass * pass : pass;
     while (R > 256) R -= pass;                         // one phase-B thread a row
     if (R < pass) R = pass;
     p.rows_per_wg = R;
-    p.kernel = std::string(fam) + "_l" + std::to_string(lpr);
+    p.kernel = std::string(fam) + "_l" + std::to_string(lpr) + (nr == 2 && type != CJ_Q6_K ? "_n2" : "");
     p.grid = (uint32_t)((rows + R - 1) / R);
     p.per_copy = p.grid;
     // LDS: scratch, the staged pack, then R rows of block terms
@@ -223,10 +226,12 @@ int32_t cj_init(int32_t device) {
     }
     static const char *kernels[] = {
         "cj_gemv_q4k_l64", "cj_gemv_q4k_l32", "cj_gemv_q4k_l16", "cj_gemv_q4k_l8",
+        "cj_gemv_q4k_l64_n2", "cj_gemv_q4k_l32_n2", "cj_gemv_q4k_l16_n2", "cj_gemv_q4k_l8_n2",
         "cj_gemv_q6k_l64", "cj_gemv_q6k_l32", "cj_gemv_q6k_l16", "cj_gemv_q6k_l8",
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
+        "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
         "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_moe_combine",
-        "cj_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
+        "cj_pack", "cj_norm_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
         "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
@@ -527,11 +532,11 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     a.part = (float *)dptr(part); a.out = (float *)dptr(out); a.q = (const float *)dptr(q);
     a.kc = (const uint16_t *)dptr(kcache); a.vc = (const uint16_t *)dptr(vcache); a.pgtab = (const int32_t *)dptr(pgtab);
     a.counters = (int32_t *)dptr(counters); a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim;
-    a.pg_base = pg_base; a.count = count; a.from = from; a.window = 0; a.workers = workers; a.scale = scale;
+    a.pg_base = pg_base; a.pg_n = (int32_t)pages; a.count = count; a.from = from; a.window = 0; a.workers = workers; a.scale = scale;
     char name[64];
     if (split) {
         snprintf(name, sizeof name, "cj_attn_split_h128_g%d", grp);
-        return launch(name, (uint32_t)(n_kv * 64), (uint32_t)(grp * 16), 0, a);
+        return launch(name, (uint32_t)(n_kv * 64), 256, 0, a);
     }
     a.splits = count;   // the scores row stride
     snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
