@@ -4,7 +4,14 @@
  * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -ffp-contract=off so
  * every `a + b * c` below rounds twice, as written. Each function names the
  * reference file:line it restates; `L/` = src/main/cajeta/dev/cajeta/llm/.
+ *
+ * OR_PLANT (normally undefined) compiles one deliberate mistake into a
+ * throw-away build, so the CPU tests can show that the check pinning that
+ * function fails on it (tests/test_oracle.py, test_planted_mistakes_are_caught).
  */
+#ifndef OR_PLANT
+#define OR_PLANT 0
+#endif
 #include "oracle.h"
 #include <math.h>
 #include <stdlib.h>
@@ -84,7 +91,11 @@ static void head_k4(const uint8_t *b, float *d, float *dmin, int sc[8], int mn[8
     const uint8_t *s = b + 4;
     for (int j = 0; j < 4; j++) { sc[j] = s[j] & 63; mn[j] = s[4 + j] & 63; }
     for (int j = 0; j < 4; j++) {
+#if OR_PLANT == 4
+        sc[4 + j] = (s[8 + j] & 15) | ((s[4 + j] >> 2) & 48);   /* planted: a transposed index */
+#else
         sc[4 + j] = (s[8 + j] & 15) | ((s[j] >> 2) & 48);
+#endif
         mn[4 + j] = (s[8 + j] >> 4) | ((s[4 + j] >> 2) & 48);
     }
 }
@@ -254,7 +265,11 @@ static void mv_q4k(const uint8_t *w, int64_t rows, int64_t cols, const uint8_t *
             int32_t dmins = 0;
             for (int sb = 0; sb < 8; sb++) dmins += mn[sb] * rd_i32(xb + 256 + 4 * sb);
             float xs = bits_f((uint32_t)rd_i32(xb + 288));
+#if OR_PLANT == 1
+            acc = acc + d * xs * (float)sumi;             /* planted: the min term dropped */
+#else
             acc = acc + d * xs * (float)sumi - dmin * xs * (float)dmins;
+#endif
         }
         y[i] = acc;
     }
@@ -403,7 +418,11 @@ void or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, 
     } else {
         for (int64_t i = 0; i < n; i++) ss = ss + x[i] * x[i];
     }
+#if OR_PLANT == 5
+    float scale = 1.0f / sqrtf(ss / (float)n);     /* planted: eps dropped */
+#else
     float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#endif
     for (int64_t i = 0; i < n; i++) {
         float wi = form == 1 ? 1.0f + w[i] : w[i];
         out[i] = x[i] * scale * wi;
@@ -475,8 +494,12 @@ static float glu_tanh_one(float x, float u) {
 void or_glu_tanh(const float *g, const float *u, int64_t n, float *out) {
     for (int64_t b0 = 0; b0 < n; b0 += 4096) {
         int64_t hi = b0 + 4096 < n ? b0 + 4096 : n, i = b0;
+#if OR_PLANT == 6
+        for (; i + 16 <= hi; i++) out[i] = glu_tanh_one(g[i], u[i]);   /* planted: 16-wide chunks stepped by one */
+#else
         for (; i + 16 <= hi; i += 16)
             for (int j = 0; j < 16; j++) out[i + j] = glu_tanh_one(g[i + j], u[i + j]);
+#endif
         for (; i < hi; i++) { float x = g[i]; out[i] = x / (1.0f + or_expf(0.0f - x)) * u[i]; }
     }
 }
@@ -497,7 +520,11 @@ void or_rope(float *t, int nheads, int hd, int pos, const float *inv) {
             float c = cosf(ang), s = sinf(ang);
             float a = b[d], bb = b[d + half];
             b[d] = a * c - bb * s;
+#if OR_PLANT == 2
+            b[d + half] = a * s - bb * c;                 /* planted: a sign */
+#else
             b[d + half] = a * s + bb * c;
+#endif
         }
     }
 }
@@ -505,7 +532,11 @@ void or_rope(float *t, int nheads, int hd, int pos, const float *inv) {
 /* First-occurrence argmax (HostOps.argmaxRow, L/model/HostOps.cajeta:106-121). */
 int or_argmax(const float *v, int64_t n) {
     int best = 0; float bv = v[0];
+#if OR_PLANT == 3
+    for (int64_t i = 1; i < n; i++) if (v[i] >= bv) { bv = v[i]; best = (int)i; }   /* planted: last occurrence */
+#else
     for (int64_t i = 1; i < n; i++) if (v[i] > bv) { bv = v[i]; best = (int)i; }
+#endif
     return best;
 }
 
@@ -543,7 +574,11 @@ void or_unpermute_rows(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t r
     for (int h = 0; h < nh; h++)
         for (int a = 0; a < 2; a++)
             for (int64_t b = 0; b < half; b++)
+#if OR_PLANT == 8
+                memcpy(dst + (h * hd + a * half + b) * rb, src + (h * hd + 2 * b + (1 - a)) * rb, (size_t)rb);
+#else
                 memcpy(dst + (h * hd + a * half + b) * rb, src + (h * hd + 2 * b + a) * rb, (size_t)rb);
+#endif
 }
 
 /* ------------------------------------------------------------- attention */
@@ -583,7 +618,9 @@ static void decode_head(const float *q, const void *kp, const void *vp, int f32,
                     + (((dl[8] + dl[9]) + (dl[10] + dl[11])) + ((dl[12] + dl[13]) + (dl[14] + dl[15])))) * scale;
         if (sc > m) {
             float c = or_expf(m - sc);
-            for (int d = 0; d < hd; d++) acc[d] = acc[d] * c;
+#if OR_PLANT != 7
+            for (int d = 0; d < hd; d++) acc[d] = acc[d] * c;   /* (7 plants: the rescale dropped) */
+#endif
             l = l * c;
             m = sc;
         }

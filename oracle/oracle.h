@@ -6,18 +6,26 @@
  * leg may load it. The product path never links, loads or calls it.
  *
  * Every function cites the reference file:line it restates (paths relative
- * to src/main/cajeta/dev/cajeta/llm/ of jklappenbach/cajeta-llm). Pinning:
+ * to src/main/cajeta/dev/cajeta/llm/ of jklappenbach/cajeta-llm). Pinning
+ * (tests/test_oracle.py; each check is also shown to fail on a build with a
+ * deliberate mistake, OR_PLANT):
  *   - dequant (Q8_0, Q4_0, Q4_K, Q6_K, MXFP4): bit-exact against the
  *     reference's committed golden pairs (tests/golden/kquant, mxfp4).
+ *   - fp16 conversions: every half pattern and RNE ties against IEEE.
  *   - q8_K / per-32 packs: closed form + round-half-away special cases.
- *   - int8 GEMVs: brute force (exact integer dot, f64 dense product bound)
- *     and a planted-error check.
- *   - rmsnorm, rope, silu, attention, argmax, MoE route: closed forms with
- *     f64 brute force on small inputs.
- *   - transcendental ULPs (expf/cosf/sinf/powf of the Cajeta stdlib):
- *     parity unpinned; this file uses glibc's.
- *   - end-to-end logits of the real reference binary: parity unpinned (the
- *     cajeta toolchain is absent); end-to-end is the restatement.
+ *   - GEMVs (all formats): float64 product of the dequantised weights with
+ *     the values the pack stands for, to fp32 accumulation rounding.
+ *   - rmsnorm, rope, silu (both forms), attention (split-K and two-pass),
+ *     argmax, MoE route, split count, q/k row permutation: closed forms,
+ *     invariants and float64 brute force on small inputs; the whole decode
+ *     step against a float64 forward of the reference's toy GGUF.
+ *   - or_expf: within 2 ulp of exp over its range (a written-out exp shared
+ *     with the kernels, so both sides give the same bits).
+ *   - parity unpinned: the ULPs of the Cajeta stdlib's exp/sin/cos/pow (this
+ *     file uses or_expf and glibc's sinf/cosf/powf), the stdlib's reduction
+ *     trees beyond what the reference's own code fixes, FMA contraction by
+ *     the Cajeta compiler, and end-to-end logits of the real reference binary
+ *     (the cajeta toolchain is absent, so end-to-end is the restatement).
  */
 #ifndef CJ_ORACLE_H
 #define CJ_ORACLE_H
@@ -49,6 +57,8 @@ int or_matvec(int type, const uint8_t *w, int64_t rows, int64_t cols,
 
 /* primitives */
 void  or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out);
+/* exp(x) in f32 from correctly rounded steps (shared with the kernels). */
+float or_expf(float x);
 void  or_glu_exp(const float *g, const float *u, int64_t n, float *out);
 void  or_glu_tanh(const float *g, const float *u, int64_t n, float *out);
 void  or_inv_freq(int hd, float theta, float *inv);

@@ -32,12 +32,32 @@ class Config(ctypes.Structure):
                 ("kv_f32", "workers", "n_experts", "n_used", "norm_topk", "expert_ffn", "swa_window")]
 
 
+def load(path):
+    """A configured handle on an oracle build at `path`."""
+    L = ctypes.CDLL(path)
+    _configure(L)
+    return L
+
+
+def use(L):
+    """Route the wrappers below through library `L` (None: the default build);
+    returns the previous one. Tests use it for planted-mistake builds."""
+    global _lib
+    prev, _lib = _lib, L
+    return prev
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
+        _lib = load(LIB_PATH)
+    return _lib
+
+
+def _configure(L):
+    if True:
         P, I64, I32, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
         sig = {
             "or_block_bytes": (I32, [I32]), "or_block_elems": (I32, [I32]),
@@ -52,6 +72,7 @@ def lib():
             "or_unpermute_rows": (None, [P, P, I64, I64, I32]),
             "or_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, F, I32, P]),
             "or_cpu_decode_splits": (I32, [I32, I32, I32, I32]),
+            "or_expf": (F, [F]),
             "or_model_new": (P, [ctypes.POINTER(Config)]), "or_model_free": (None, [P]),
             "or_model_bind": (I32, [P, ctypes.c_char_p, I32, P, I64, I64]),
             "or_model_step": (I32, [P, I32, I32, P]), "or_model_reset": (None, [P]),
@@ -61,8 +82,6 @@ def lib():
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
-        _lib = L
-    return _lib
 
 
 def _p(a):
@@ -180,6 +199,11 @@ def attend(q, kplane, vplane, n_h, n_kv, hd, count, splits, scale, mode, kv_f32=
     lib().or_attend(_p(q), _p(kplane), _p(vplane), int(kv_f32), n_h, n_kv, hd, count, splits,
                     scale, mode, _p(out))
     return out
+
+
+def expf(x):
+    """The written-out f32 exp the restatement (and the kernels) use."""
+    return np.array([lib().or_expf(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
 
 
 def cpu_decode_splits(count, rows, n_kv, workers):

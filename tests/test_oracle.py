@@ -1,0 +1,460 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each restated function is checked against something other than its own
+formula: the reference's golden vectors (dequant), IEEE/numpy (fp16),
+closed forms and invariants (packs, argmax, splits, row permutation) and a
+float64 brute force (GEMVs, RMSNorm, RoPE, SiLU, attention, routing, and a
+whole toy-model forward). test_planted_mistakes_are_caught rebuilds the
+oracle with one deliberate mistake at a time (OR_PLANT) and shows the check
+for that function fails on it.
+
+Runs on the CPU (no GPU marker)."""
+import math
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+GOLD = os.path.join(HERE, "golden")
+
+
+# ------------------------------------------------------------------ helpers
+
+def rand_blocks(O, ty, nblocks, rng):
+    """Valid random blocks of a format: random bytes with sane scales."""
+    be, bb = O.BLOCK[ty]
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+
+    def f16(vals):
+        return np.asarray(vals, np.float16).view(np.uint8).reshape(-1, 2)
+    if ty in (O.Q8_0, O.Q4_0):
+        raw[:, 0:2] = f16(rng.uniform(0.001, 0.01, nblocks))
+    elif ty == O.Q4_K:
+        raw[:, 0:2] = f16(rng.uniform(0.0005, 0.002, nblocks))
+        raw[:, 2:4] = f16(rng.uniform(0.0005, 0.002, nblocks))
+    elif ty == O.Q6_K:
+        raw[:, 208:210] = f16(rng.uniform(0.0001, 0.001, nblocks))
+    elif ty == O.MXFP4:
+        raw[:, 0] = rng.integers(118, 126, nblocks)
+    return raw.reshape(-1)
+
+
+def unpack(O, xp, n, per32):
+    """The values a 320-byte pack stands for: q · scale (block layout of
+    Quant.q8kPackPad / q8kPack32Pad: 256 int8, 8 int32 sums, scale(s) at 288)."""
+    out = np.zeros(n, np.float64)
+    for b in range((n + 255) // 256):
+        blk = xp[b * 320:(b + 1) * 320]
+        q = blk[:256].view(np.int8).astype(np.float64)
+        if per32:
+            s = np.repeat(blk[288:320].view(np.float32).astype(np.float64), 32)
+        else:
+            s = np.full(256, blk[288:292].view(np.float32)[0], np.float64)
+        m = min(256, n - 256 * b)
+        out[256 * b:256 * b + m] = (q * s)[:m]
+    return out
+
+
+def golden(name):
+    d = os.path.join(GOLD, "kquant")
+    return np.fromfile(os.path.join(d, name + ".bin"), np.uint8), np.fromfile(os.path.join(d, name + ".f32"), np.float32)
+
+
+def rel_err(got, ref):
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / (np.max(np.abs(ref)) + 1e-30))
+
+
+# ------------------------------------------------- checks (also run on plants)
+
+def check_dequant_golden(O):
+    """Dequant of the reference's golden blocks (gguf-py of real Llama-3.1-8B
+    blocks, F/gguf/kquant) is bit-exact."""
+    bad = []
+    for name, ty in (("q4_k", O.Q4_K), ("q6_k", O.Q6_K), ("q8_0", O.Q8_0), ("q4_0", O.Q4_0)):
+        raw, ref = golden(name)
+        got = O.dequant(ty, raw)
+        if not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
+            bad.append(name)
+    b = open(os.path.join(GOLD, "mxfp4", "mxfp4_ref.bin"), "rb").read()
+    _, nb = struct.unpack("<ii", b[:8])
+    raw = np.frombuffer(b[8:8 + nb * 17], np.uint8)
+    ref = np.frombuffer(b[8 + nb * 17:], np.float32)
+    if not np.array_equal(O.dequant(O.MXFP4, raw).view(np.uint32), ref.view(np.uint32)):
+        bad.append("mxfp4")
+    return not bad, bad
+
+
+def check_matvec(O, ty, rows=24, cols=1024, seed=3):
+    """GEMV against a float64 product of the dequantised weights with the
+    values the activation pack stands for (the int8 formats) or with x (the
+    f32-activation formats): only fp32 accumulation rounding may differ."""
+    rng = np.random.default_rng(seed + ty)
+    be, bb = O.BLOCK[ty]
+    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    W = O.dequant(ty, raw).astype(np.float64).reshape(rows, cols)
+    if ty in (O.Q4_0, O.MXFP4):
+        got = O.matvec(ty, raw, rows, cols, x)
+        ref = W @ x.astype(np.float64)
+    else:
+        per32 = ty == O.Q8_0
+        xp = O.q8k_pack(x, per32=per32)
+        got = O.matvec_packed(ty, raw, rows, cols, xp)
+        ref = W @ unpack(O, xp, cols, per32)
+    e = rel_err(got, ref)
+    return e < 2e-6, e
+
+
+def check_rmsnorm(O):
+    bad = []
+    for n, scale in ((4096, 1.0), (2880, 1.0), (512, 3e-3)):   # the last: eps matters
+        rng = np.random.default_rng(n)
+        x = (rng.standard_normal(n) * scale).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        for form in (0, 1):
+            got = O.rmsnorm(x, w, 1e-5, form)
+            xd = x.astype(np.float64)
+            wd = w.astype(np.float64) + (1.0 if form else 0.0)
+            ref = xd / np.sqrt(np.mean(xd * xd) + 1e-5) * wd
+            e = rel_err(got, ref)
+            if e > 1e-6:
+                bad.append((n, form, e))
+    return not bad, bad
+
+
+def check_rope(O):
+    bad = []
+    for hd, theta, pos in ((128, 500000.0, 2047), (64, 10000.0, 37), (128, 10000.0, 0)):
+        rng = np.random.default_rng(hd + pos)
+        nh = 3
+        t = rng.standard_normal(nh * hd).astype(np.float32)
+        inv = O.inv_freq(hd, theta)
+        got = O.rope(t.copy(), nh, hd, pos, inv)
+        half = hd // 2
+        invd = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / hd)
+        ang = pos * invd
+        z = t.reshape(nh, hd).astype(np.float64)
+        zc = (z[:, :half] + 1j * z[:, half:]) * np.exp(1j * ang)
+        ref = np.concatenate([zc.real, zc.imag], axis=1).ravel()
+        e = rel_err(got, ref)
+        if e > 2e-5 or (pos == 0 and not np.array_equal(got, t)):
+            bad.append((hd, pos, e))
+    return not bad, bad
+
+
+def check_argmax(O):
+    v = np.array([0.5, 3.0, -1.0, 3.0, 2.0, 3.0], np.float32)
+    cases = [(v, 1), (np.zeros(7, np.float32), 0), (np.array([-5, -2, -2], np.float32), 1)]
+    bad = [(list(a), O.argmax(a), want) for a, want in cases if O.argmax(a) != want]
+    return not bad, bad
+
+
+def check_glu_structure(O):
+    """gluCpuKernel: 16-wide tanh chunks across each 4096-wide work block, the
+    block's remainder in the exp form; tanh form within 4e-6 of the exp form
+    (the reference's stated bound for its rational tanh)."""
+    rng = np.random.default_rng(5)
+    n = 4096 + 4096 + 40            # two whole blocks, then 40 (two chunks + 8)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    t = O.glu(g, u, "tanh")
+    ex = O.glu(g, u, "exp")
+    tail = slice(8192 + 32, n)
+    same_tail = np.array_equal(t[tail].view(np.uint32), ex[tail].view(np.uint32))
+    # inside whole chunks the rational form is used: it differs from exp somewhere
+    last15 = slice(4096 - 15, 4096)
+    chunk_used = not np.array_equal(t[last15].view(np.uint32), ex[last15].view(np.uint32))
+    close = float(np.max(np.abs(t - ex))) < 4e-6 * 16
+    return same_tail and chunk_used and close, (same_tail, chunk_used, close)
+
+
+def attention_ref(q, k, v, nh, nkv, hd, count, scale):
+    qd = q.reshape(nh, hd).astype(np.float64)
+    kd = k[:count].reshape(count, nkv, hd).astype(np.float64)
+    vd = v[:count].reshape(count, nkv, hd).astype(np.float64)
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        kv = h // (nh // nkv)
+        s = kd[:, kv, :] @ qd[h] * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ vd[:, kv, :]
+    return out.ravel()
+
+
+def check_attention(O):
+    bad = []
+    for nh, nkv, hd, count, mode in ((8, 2, 128, 300, 0), (32, 8, 128, 2049, 0), (8, 2, 64, 257, 1),
+                                     (64, 8, 64, 130, 1), (8, 1, 128, 1, 0)):
+        rng = np.random.default_rng(count + hd)
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        k = rng.standard_normal((count, nkv * hd)).astype(np.float16)
+        v = rng.standard_normal((count, nkv * hd)).astype(np.float16)
+        scale = float(np.float32(1.0 / math.sqrt(hd)))
+        splits = O.cpu_decode_splits(count, 1, nkv, 512) if mode == 0 else 1
+        got = O.attend(q, k.view(np.uint16), v.view(np.uint16), nh, nkv, hd, count, splits, scale, mode)
+        e = rel_err(got, attention_ref(q, k, v, nh, nkv, hd, count, scale))
+        if e > 2e-5:
+            bad.append((nh, nkv, hd, count, mode, e))
+    return not bad, bad
+
+
+def check_unpermute(O):
+    """Checkpoint.unpermuteRows undoes the GGUF llama q/k row permutation:
+    HF row (h, a, b) sits at GGUF row (h, b, a) — built here by reshape."""
+    nh, hd, rb = 4, 16, 3
+    rows = nh * hd
+    hf = np.arange(rows * rb, dtype=np.uint8).reshape(rows, rb) % 251
+    gg = hf.reshape(nh, 2, hd // 2, rb).swapaxes(1, 2).reshape(rows, rb)
+    got = O.unpermute_rows(gg.ravel(), rows, rb, nh).reshape(rows, rb)
+    return np.array_equal(got, hf), None
+
+
+# ------------------------------------------------------------------- tests
+
+def test_dequant_matches_reference_goldens(O):
+    ok, bad = check_dequant_golden(O)
+    assert ok, bad
+
+
+def test_f16_conversions_match_ieee(O):
+    h = np.arange(65536, dtype=np.uint16)
+    got = O.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(4000) * 10, rng.standard_normal(2000) * 1e-5,
+                        rng.standard_normal(1000) * 7e4,
+                        # exact ties between halves round to even
+                        (np.arange(1, 200) + 0.5).astype(np.float32) * np.float32(2.0 ** -10),
+                        [0.0, -0.0, 65504.0, 65520.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26]]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.f32_to_f16_bits(x), want)
+
+
+@pytest.mark.parametrize("per32", [False, True])
+def test_pack_closed_form(O, per32):
+    # round half away from zero at exact halves; amax 127 makes the step 1
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2], x[3], x[4] = 127.0, 2.5, -2.5, 0.5, -1.5
+    if per32:
+        x[32:64] = 127.0
+        x[33], x[34] = 3.5, -3.5
+    xp = O.q8k_pack(x, per32=per32)
+    q = xp[:256].view(np.int8)
+    assert list(q[:5]) == [127, 3, -3, 1, -2]
+    if per32:
+        assert q[33] == 4 and q[34] == -4
+    sums = xp[256:288].view(np.int32)
+    assert np.array_equal(sums, q.astype(np.int32).reshape(8, 32).sum(1))
+    if per32:
+        sc = xp[288:320].view(np.float32)
+        assert sc[0] == np.float32(1.0) and sc[1] == np.float32(1.0) and np.all(sc[2:] == 0)
+    else:
+        assert xp[288:292].view(np.float32)[0] == np.float32(1.0)
+        assert not xp[292:320].any()
+    # a zero block packs to zero with scale 0; a random block reconstructs to half a step
+    z = O.q8k_pack(np.zeros(300, np.float32), per32=per32)
+    assert not z.any()
+    rng = np.random.default_rng(9)
+    r = rng.standard_normal(700).astype(np.float32)
+    rp = O.q8k_pack(r, per32=per32)
+    step = np.max(np.abs(r)) / 127
+    assert np.max(np.abs(unpack(O, rp, 700, per32) - r)) <= step * 0.5000001
+
+
+@pytest.mark.parametrize("ty", [8, 2, 12, 14, 39])
+def test_matvec_against_float64(O, ty):
+    ok, e = check_matvec(O, ty)
+    assert ok, e
+
+
+def test_rmsnorm_against_float64(O):
+    ok, bad = check_rmsnorm(O)
+    assert ok, bad
+
+
+def test_rope_against_complex_rotation(O):
+    ok, bad = check_rope(O)
+    assert ok, bad
+
+
+def test_expf_is_faithful(O):
+    xs = np.concatenate([np.linspace(-103.9, 88.7, 20001), [0.0, -0.0, 1.0, -1.0, 1e-8]]).astype(np.float32)
+    e = O.expf(xs)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(e - ref) / ulp) <= 2.0
+    assert e[-5] == 1.0 and e[-4] == 1.0
+    assert O.expf(np.float32(-105.0))[0] == 0.0 and np.isinf(O.expf(np.float32(89.0))[0])
+
+
+def test_silu_forms(O):
+    rng = np.random.default_rng(2)
+    g = (rng.standard_normal(5000) * 5).astype(np.float32)
+    u = rng.standard_normal(5000).astype(np.float32)
+    gd = g.astype(np.float64)
+    ref = gd / (1 + np.exp(-gd)) * u
+    assert rel_err(O.glu(g, u, "exp"), ref) < 1e-6
+    ok, detail = check_glu_structure(O)
+    assert ok, detail
+
+
+def test_argmax_first_occurrence(O):
+    ok, bad = check_argmax(O)
+    assert ok, bad
+
+
+def test_attention_against_float64(O):
+    ok, bad = check_attention(O)
+    assert ok, bad
+
+
+def test_decode_splits_closed_form(O):
+    # two work items a worker over the kv heads, within [1, min(64, count)]
+    assert O.cpu_decode_splits(2049, 1, 8, 512) == 64
+    assert O.cpu_decode_splits(2049, 1, 8, 16) == 4
+    assert O.cpu_decode_splits(3, 1, 8, 512) == 3
+    assert O.cpu_decode_splits(100, 1, 8, 1) == 1
+    assert O.cpu_decode_splits(100, 2, 8, 24) == 3
+
+
+def test_moe_route_against_float64(O):
+    rng = np.random.default_rng(4)
+    for ne, k in ((32, 4), (128, 8)):
+        lg = rng.standard_normal(ne).astype(np.float32)
+        lg[5] = lg[6] = np.float32(lg.max() + 1)          # a tie: the lower index first
+        sel, w = O.moe_route(lg, k, norm=True)
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = sorted(range(ne), key=lambda i: (-p[i], i))[:k]
+        assert list(sel) == order
+        assert abs(float(np.sum(w)) - 1.0) < 1e-6
+        assert rel_err(w, p[order] / p[order].sum()) < 1e-6
+
+
+def test_unpermute_rows_inverts_the_gguf_permutation(O):
+    ok, _ = check_unpermute(O)
+    assert ok
+
+
+def test_gguf_reader_reads_the_reference_toy_fixtures():
+    from oracle.gguf_reader import GgufReader, model_config
+    for name, nkv in (("toy-routable.gguf", 1), ("toy-routable-gqa8.gguf", None)):
+        r = GgufReader(os.path.join(GOLD, "gguf", name))
+        cfg = model_config(r)
+        assert cfg["hidden"] == 512 and cfg["head_dim"] == 128 and cfg["n_layers"] == 2
+        if nkv:
+            assert cfg["n_kv"] == nkv
+        assert "token_embd.weight" in r.tensors and "blk.1.ffn_down.weight" in r.tensors
+
+
+def test_toy_model_forward_against_float64(O):
+    """The oracle's whole decode step against a float64 forward of the same
+    GGUF (weights dequantised, activations through the same int8 packs, fp16
+    K/V): the layer composition — norms, RoPE, GQA, residuals, SwiGLU, head —
+    agrees to the packs' rounding."""
+    from oracle.gguf_reader import GgufReader, oracle_model
+    r = GgufReader(os.path.join(GOLD, "gguf", "toy-routable.gguf"))
+    om, cfg = oracle_model(r, ctx=16)
+    L, H, nh, nkv, hd = cfg["n_layers"], cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"]
+    eps, theta, V = cfg["eps"], cfg["theta"], cfg["vocab"]
+
+    def t(name, unperm=0):
+        ty, dims, rows, cols, data = r.tensors[name]
+        raw = np.ascontiguousarray(data)
+        if ty == O.F32:
+            return raw.view(np.float32).astype(np.float64).reshape(rows, cols) if rows > 1 else \
+                raw.view(np.float32).astype(np.float64).ravel()
+        if unperm:
+            be, bb = O.BLOCK[ty]
+            raw = O.unpermute_rows(raw, rows, cols // be * bb, unperm)
+        return O.dequant(ty, raw).astype(np.float64).reshape(rows, cols)
+
+    def lin(name, xv, unperm=0):
+        ty = r.tensors[name][0]
+        Wm = t(name, unperm)
+        if ty in (O.Q4_0, O.MXFP4, O.F32):
+            return Wm @ xv
+        x32 = xv.astype(np.float32)
+        return Wm @ unpack(O, O.q8k_pack(x32, per32=(ty == O.Q8_0)), x32.size, ty == O.Q8_0)
+
+    def norm(xv, w):
+        return xv / np.sqrt(np.mean(xv * xv) + eps) * w
+
+    half = hd // 2
+    invd = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / hd)
+
+    def rope(v, n, pos):
+        z = v.reshape(n, hd)
+        zc = (z[:, :half] + 1j * z[:, half:]) * np.exp(1j * pos * invd)
+        return np.concatenate([zc.real, zc.imag], 1).ravel()
+
+    emb = t("token_embd.weight")
+    head = "output.weight" if "output.weight" in r.tensors else "token_embd.weight"
+    toks = [3, 141, 59, 26, 5]
+    kc = [[] for _ in range(L)]
+    vc = [[] for _ in range(L)]
+    worst = 0.0
+    for pos, tok in enumerate(toks):
+        hs = emb[tok].copy()
+        for l in range(L):
+            p = "blk.%d." % l
+            xn = norm(hs, t(p + "attn_norm.weight"))
+            q = rope(lin(p + "attn_q.weight", xn, nh), nh, pos)
+            k = rope(lin(p + "attn_k.weight", xn, nkv), nkv, pos)
+            v = lin(p + "attn_v.weight", xn)
+            kc[l].append(k.astype(np.float16).astype(np.float64))
+            vc[l].append(v.astype(np.float16).astype(np.float64))
+            K, Vv = np.array(kc[l]), np.array(vc[l])
+            ao = np.zeros(nh * hd)
+            for h in range(nh):
+                g = h // (nh // nkv)
+                s = K[:, g * hd:(g + 1) * hd] @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
+                pr = np.exp(s - s.max())
+                ao[h * hd:(h + 1) * hd] = (pr / pr.sum()) @ Vv[:, g * hd:(g + 1) * hd]
+            hs = hs + lin(p + "attn_output.weight", ao)
+            xn = norm(hs, t(p + "ffn_norm.weight"))
+            gg, uu = lin(p + "ffn_gate.weight", xn), lin(p + "ffn_up.weight", xn)
+            hs = hs + lin(p + "ffn_down.weight", gg / (1 + np.exp(-gg)) * uu)
+        ref = lin(head, norm(hs, t("output_norm.weight")))
+        _, logits = om.step(tok, pos)
+        worst = max(worst, float(np.max(np.abs(logits - ref)) / np.max(np.abs(ref))))
+    om.close()
+    print("toy forward: worst relative logit difference %.3g" % worst)
+    assert worst < 1e-4, worst
+
+
+# ------------------------------------------------------- planted mistakes
+
+PLANTS = {
+    1: ("Q4_K GEMV without the min term", lambda O: check_matvec(O, O.Q4_K)),
+    2: ("RoPE with a sign error", check_rope),
+    3: ("argmax keeps the last maximum", check_argmax),
+    4: ("Q4_K 6-bit scale from the wrong byte", check_dequant_golden),
+    5: ("RMSNorm without eps", check_rmsnorm),
+    6: ("tanh-form SiLU chunks stepped by one", check_glu_structure),
+    7: ("split-K without the rescale on a new max", check_attention),
+    8: ("q/k rows unpermuted with the halves swapped", check_unpermute),
+}
+
+
+@pytest.mark.parametrize("plant", sorted(PLANTS))
+def test_planted_mistakes_are_caught(O, tmp_path, plant):
+    what, check = PLANTS[plant]
+    so = str(tmp_path / ("liboracle_plant%d.so" % plant))
+    subprocess.check_call(["gcc", "-O2", "-std=gnu11", "-fPIC", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
+                           "-DOR_PLANT=%d" % plant, "-shared", "-o", so, os.path.join(ROOT, "oracle", "oracle.c"), "-lm"])
+    assert check(O)[0], "the check must pass on the real oracle first"
+    prev = O.use(O.load(so))
+    try:
+        ok, detail = check(O)
+    finally:
+        O.use(prev)
+    assert not ok, "planted mistake not caught: %s (%s)" % (what, detail)
