@@ -15,9 +15,14 @@ region).
 Beside the line's value it reports
   roofline      the dominant kernel (the fused gate|up Q4_K GEMV) timed with
                 HIP events over back-to-back launches on the engine's
-                stream: algorithmic bytes per launch ÷ mean launch time,
-                against 8 TB/s; `traffic` is the measured HBM bytes per
-                launch from the committed rocprofv3 counter summary;
+                stream, rotating over the 32 layers' weights (2.1 GB, past
+                the 256 MB last-level cache): algorithmic bytes per launch ÷
+                mean launch time, against 8 TB/s; `traffic` is the measured
+                HBM bytes per launch from the committed rocprofv3 counter
+                summary;
+  copy          a plain 1 GiB device copy kernel (cj_buf_copy) timed the same
+                way: the practical streaming ceiling of the part, and the
+                known-size kernel the counter summaries are calibrated with;
   step_roofline the whole step: algorithmic bytes per token (weights at their
                 GGUF size + K/V read + activation vectors) ÷ ms per step;
   cpu_baseline  the C restatement of the reference CPU backend (oracle/),
@@ -44,7 +49,8 @@ WORKLOAD = ("C3: Llama-3-8B shape (32 layers, d 4096, 32/8 heads of 128, FFN 143
             "Q4_K weights + Q6_K head, fp16 paged K/V, greedy, batch 1")
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic_gemv_q4k_gate_up_c3.txt")
 K_GATE_UP = 4
-KIND_NAMES = {0: "embed", 1: "qkv", 2: "attention", 3: "o", 4: "gate_up", 5: "down", 11: "head"}
+KIND_NAMES = {0: "embed", 1: "qkv", 2: "attention", 3: "o", 4: "gate_up", 5: "down", 11: "head", 12: "norm"}
+COPY_BYTES = 1 << 30          # the streaming-copy reference: 1 GiB read + 1 GiB written
 
 
 def log(*a):
@@ -60,6 +66,26 @@ def measured_traffic():
         return int(m.group(1)) if m else None
     except OSError:
         return None
+
+
+def copy_reference(native, reps=20):
+    """Mean time of a plain 1 GiB device-to-device copy (cj_buf_copy)."""
+    lib = native.lib()
+    src, dst = native.Buffer(COPY_BYTES), native.Buffer(COPY_BYTES)
+    try:
+        src.zero()
+        native.check(lib.cj_buf_copy(dst.h, src.h, COPY_BYTES), "copy")
+        native.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            native.check(lib.cj_buf_copy(dst.h, src.h, COPY_BYTES), "copy")
+        native.sync()
+        us = (time.perf_counter() - t0) * 1e6 / reps
+    finally:
+        src.free()
+        dst.free()
+    moved = 2 * COPY_BYTES
+    return {"kernel": "cj_copy", "avg_us": round(us, 2), "bytes": moved, "GB/s": round(moved / (us * 1e-6) / 1e9, 1)}
 
 
 def cpu_baseline(pkg, image_name, vocab, budget_s, seed):
@@ -156,7 +182,7 @@ def main():
 
     # per-kernel breakdown, the dominant one first
     kernels = {}
-    for kind in (K_GATE_UP, 1, 2, 3, 5, 11, 0):
+    for kind in (K_GATE_UP, 1, 2, 3, 5, 12, 11, 0):
         us, nbytes, name = eng.timeKernel(kind, args.kernel_reps)
         kernels[KIND_NAMES[kind]] = {"kernel": name, "avg_us": round(us, 3), "bytes": nbytes,
                                      "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -164,6 +190,9 @@ def main():
                                                            nbytes / (us * 1e-6) / 1e9))
     dom = kernels["gate_up"]
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+    copy = copy_reference(native)
+    log("  copy      cj_copy                   %9.2f us  %12d B  %7.1f GB/s" % (copy["avg_us"], copy["bytes"],
+                                                                              copy["GB/s"]))
 
     cpu = None
     if not args.no_cpu:
@@ -196,6 +225,7 @@ def main():
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(step_gbs / PEAK_HBM_GBS, 4),
                           "device_us_per_step": round(dev_us, 2)},
         "kernels": kernels,
+        "copy": copy,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

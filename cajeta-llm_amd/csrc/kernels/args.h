@@ -108,6 +108,8 @@ typedef struct {
 
 typedef struct { float *a; const float *b; int64_t n; } cj_add_args;
 
+typedef struct { void *dst; const void *src; int64_t n16; } cj_copy_args;
+
 typedef struct {
     float *q, *k; const float *v;
     uint16_t *kc, *vc;

@@ -69,6 +69,13 @@ extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) {
     }
 }
 
+// Device copy of n16 16-byte words (grid-stride, one uint4 a thread a step).
+extern "C" __global__ void __launch_bounds__(256) cj_copy(cj_copy_args a) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n16; i += stride)
+        ((uint4 *)a.dst)[i] = ((const uint4 *)a.src)[i];
+}
+
 // ------------------------------------------------------------------ glu
 
 // One workgroup per 256-wide block: out = act(g)·u, then (optionally) that

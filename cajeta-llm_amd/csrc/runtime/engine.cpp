@@ -101,12 +101,15 @@ struct Engine {
     std::vector<Request> reqs;
     float last_step_us = 0.0f;
     std::vector<void *> owned;
-    int only = -1;             // enqueue only this kind, of layer 0 (-1: the whole step)
+    int only = -1;             // enqueue only this kind, of layer only_layer (-1: the whole step)
+    int only_layer = 0;
     bool graphs = true;        // replay the captured step (false: enqueue its launches each token)
     int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
     int64_t embd_row_file_bytes = 0;
 
-    bool want(int kind, int l) const { return only < 0 || (only == kind && l == 0); }
+    bool want(int kind, int l) const {
+        return only < 0 || (only == kind && l == (kind == K_EMBED || kind == K_HEAD ? 0 : only_layer));
+    }
 
     void *alloc(size_t n) {
         void *p = dev_alloc(n);
@@ -643,9 +646,12 @@ int64_t Engine::step_bytes(int count) const {
     return b;
 }
 
-// Time `reps` back-to-back eager launches of one kind (layer 0) of sequence
-// s's step at its current position, on the engine's stream, between two HIP
-// events. The step state is left as it was.
+// Time `reps` back-to-back eager launches of one kind of sequence s's step at
+// its current position, on the engine's stream, between two HIP events. The
+// launches rotate over the layers, so each reads weights the previous few did
+// not (the model's weights are far larger than the 256 MB last-level cache:
+// the timing is of HBM, not of a cached matrix). The step state is left as
+// it was.
 int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel) {
     if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
     if (kind < K_EMBED || kind > K_NORM || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
@@ -658,6 +664,7 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
     CJ_HIP(hipStreamSynchronize(stream()));
     CJ_HIP(hipMemcpy(&saved, S.state, sizeof saved, hipMemcpyDeviceToHost));
     only = kind;
+    only_layer = 0;
     int rc = enqueue_step(s);                     // one untimed launch
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
@@ -665,7 +672,10 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
     if (!rc) {
         kernel = last_launch();
         (void)hipEventRecord(e0, stream());
-        for (int i = 0; i < reps && !rc; i++) rc = enqueue_step(s);
+        for (int i = 0; i < reps && !rc; i++) {
+            only_layer = (i + 1) % (n_layers > 0 ? n_layers : 1);
+            rc = enqueue_step(s);
+        }
         (void)hipEventRecord(e1, stream());
         (void)hipEventSynchronize(e1);
         float ms = 0.0f;
@@ -673,6 +683,7 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
         *avg_us = ms * 1000.0f / (float)reps;
     }
     only = -1;
+    only_layer = 0;
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     CJ_HIP(hipStreamSynchronize(stream()));

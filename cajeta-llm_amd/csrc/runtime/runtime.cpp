@@ -4,6 +4,7 @@
 // reference *LaunchNoSync wrapper).
 #include "rt.h"
 #include <dlfcn.h>
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -231,7 +232,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
         "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
         "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_moe_combine",
-        "cj_pack", "cj_norm_pack", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
+        "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
         "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
@@ -455,6 +456,15 @@ int32_t cj_glu(int64_t out, int64_t packed, int64_t gb, int64_t ub, int64_t n, i
     a.out = (float *)dptr(out); a.g = (const float *)dptr(gb); a.u = (const float *)dptr(ub);
     a.packed = (uint8_t *)dptr(packed); a.n = n; a.npad = npad; a.form = form; a.per32 = per32;
     return launch("cj_glu", (uint32_t)(npad / 256), 256, 0, a);
+}
+
+int32_t cj_buf_copy(int64_t dst, int64_t src, int64_t bytes) {
+    if (bytes <= 0 || bytes % 16 || (dst & 15) || (src & 15) || !in_buffer(dptr(dst), bytes) || !in_buffer(dptr(src), bytes))
+        return fail(CJ_ERR_ARG, "cj_buf_copy: %lld bytes (a multiple of 16, 16-byte aligned, inside both buffers)",
+                    (long long)bytes);
+    cj_copy_args a{dptr(dst), dptr(src), bytes / 16};
+    const int64_t wgs = std::min<int64_t>((a.n16 + 255) / 256, (int64_t)std::max(1, g.cus) * 16);
+    return launch("cj_copy", (uint32_t)wgs, 256, 0, a);
 }
 
 int32_t cj_add(int64_t ab, int64_t bb, int64_t n) {

@@ -66,6 +66,10 @@ int32_t cj_buf_free(int64_t buf);
 int64_t cj_buf_size(int64_t buf);
 int32_t cj_buf_upload(int64_t buf, int64_t off, const int8_t *src, int64_t bytes);
 int32_t cj_buf_download(int64_t buf, int64_t off, int8_t *dst, int64_t bytes);
+/* Device-to-device copy of `bytes` (a multiple of 16) with a plain
+ * streaming kernel: the device leg of a KernelBuffer copy, and the
+ * known-size kernel the HBM counter summaries are calibrated against. */
+int32_t cj_buf_copy(int64_t dst, int64_t src, int64_t bytes);
 /* Zero a buffer with a fill kernel (safe inside a captured graph). */
 int32_t cj_buf_zero(int64_t buf);
 
