@@ -193,7 +193,9 @@ int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows,
  * capacity per sequence, max_seqs the sequence slots. */
 int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs);
 int32_t cj_engine_close(int64_t eng);
-/* n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab, ctx, n_experts, n_used, weight type, head type */
+/* Up to 14 values: n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab,
+ * ctx, n_experts, n_used, weight type, head type, expert ffn, and the CPU
+ * worker count the split-K attention rule is evaluated for (512). */
 int32_t cj_engine_config(int64_t eng, int64_t *out, int32_t n);
 /* LlmEngine.submitTokens (:477): a greedy request; returns the request id. */
 int32_t cj_engine_submit(int64_t eng, const int32_t *prompt, int32_t n, int32_t max_new);
