@@ -137,7 +137,8 @@ typedef struct {
     int32_t workers;         // split-K: the CPU worker count the split rule uses
     float scale;
     int32_t pg_n;            // pages the sequence owns from pg_base (bounds the table prefetch)
-    int32_t pad;
+    int32_t per32;           // split-K with an output: pack `packed` at one scale per 32
+    uint8_t *packed;         // split-K with an output: the q8 pack of the merged output (may be null)
 } cj_attn_args;
 
 typedef struct {

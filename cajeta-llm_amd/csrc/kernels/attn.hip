@@ -47,34 +47,35 @@ DEV void attn_window(const cj_attn_args &a, int &count, int &from) {
     if (a.window > 0 && count > a.window) { from += count - a.window; count = a.window; }
 }
 
-// One workgroup of 256 per (kv head, split slot). A split's positions go
-// through LDS a tile at a time; per tile:
-//   scores   thread (head, position): the reference's 16 lane partials
-//            (lane l: Σ_v q[l+16v]·k[l+16v], v ascending) folded as the
-//            xor-butterfly folds them — a fixed pairwise tree — so one thread
-//            makes the same adds with no cross-lane traffic;
-//   max      thread (head): the running max in position order, noting where
-//            it rises (the reference rescales there);
-//   exps     thread (head, position): the rescale factor exp(m_prev − s) and
-//            the weight exp(s − m), all independent;
-//   update   thread (head, dim): acc·c on a rise, then acc + v·p, in position
-//            order; thread (head) does the same for the sum.
-template <int HD, int G>
+// One workgroup of 256 per (kv head, split slot); wave w owns query heads
+// w, w+4 of the kv head's group (one for G = 4, two for G = 8). A split's
+// positions go through LDS a tile of 64 at a time. After the staging barrier
+// every step is wave-local:
+//   scores   lane p, position p: the reference's 16 lane partials (partial j:
+//            Σ_v q[16v+j]·k[16v+j], v ascending) folded as the xor-butterfly
+//            folds them — the fixed pairwise tree — K rows read from LDS
+//            rows padded to 272 bytes (16-byte reads, no bank conflicts);
+//   max      a wave prefix-max scan: lane p learns the running max before and
+//            after its position (max is exact, so the scan order is free);
+//   exps     lane p: the rescale exp(m_before − s) where s is a new maximum
+//            (the reference rescales only there) and the weight exp(s − m);
+//   update   lane d: acc·c (only where the maximum rose) then + v·w, in
+//            position order, each position's c and w read from its lane.
+// The last workgroup of a kv head to finish merges the head's splits and
+// writes the merged output and its q8 pack.
+template <int G>
 DEV void split_body(const cj_attn_args &a) {
-    constexpr int TP = 64;                           // positions a tile
-    constexpr int CK = 16;                           // positions a register chunk
-    constexpr int PGMAX = 256;                       // page-table entries prefetched
-    __shared__ __align__(16) uint16_t ks[TP][HD];
+    constexpr int HD = 128, TP = 64, KS = HD + 8, PGMAX = 256, HW = G / 4;
+    __shared__ __align__(16) uint16_t ks[TP][KS];
     __shared__ __align__(16) uint16_t vs[TP][HD];
     __shared__ __align__(16) float qs[G][HD];
-    __shared__ __align__(16) float sc[G][TP], cf[G][TP], pr[G][TP], mb[G][TP], ma[G][TP];
-    __shared__ int up[G][TP];
     __shared__ int pgs[PGMAX];
-    __shared__ float mrun[G], lrun[G];
-    const int t = threadIdx.x;
+    __shared__ float bmax[8];
+    __shared__ int ticket;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
     // q, the page table and the step state load together
-    for (int e = t; e < G * HD; e += 256) qs[e / HD][e % HD] = a.q[(int64_t)(kvh * G) * HD + e];
+    for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(a.q + (int64_t)kvh * G * HD + e);
     if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[a.pg_base + t] : 0;
     int count, from;
     attn_window(a, count, from);
@@ -84,166 +85,161 @@ DEV void split_body(const cj_attn_args &a) {
         int t0 = sp * chunk, t1 = t0 + chunk;
         if (t1 > count) t1 = count;
         if (t0 > count) t0 = count;
-        if (t < G) { mrun[t] = -3.0e38f; lrun[t] = 0.0f; }
-        constexpr int PAIRS = G * HD / 256;          // (head, dim) pairs a thread
-        float acc[PAIRS];
+        float m[HW], l[HW], acc0[HW], acc1[HW];
 #pragma unroll
-        for (int k = 0; k < PAIRS; k++) acc[k] = 0.0f;
+        for (int hh = 0; hh < HW; hh++) { m[hh] = -3.0e38f; l[hh] = 0.0f; acc0[hh] = 0.0f; acc1[hh] = 0.0f; }
         for (int tb = t0; tb < t1; tb += TP) {
             const int n = t1 - tb < TP ? t1 - tb : TP;
-            __syncthreads();
-            // stage the tile's K and V rows (16-byte chunks, natural layout)
-            constexpr int CPP = HD / 8;
-            for (int c = t; c < n * CPP; c += 256) {
-                const int p = c / CPP, j = c % CPP;
-                const int pos = from + tb + p, pi = pos >> 6;
-                const int page = pi < PGMAX ? pgs[pi] : a.pgtab[a.pg_base + pi];
-                const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;
-                *(uint4 *)&ks[p][8 * j] = *(const uint4 *)(a.kc + base);
-                *(uint4 *)&vs[p][8 * j] = *(const uint4 *)(a.vc + base);
-            }
-            __syncthreads();
-            // scores: thread (head, position)
-            for (int hp = t; hp < G * TP; hp += 256) {
-                const int h = hp / TP, p = hp % TP;
-                if (p < n) {
-                    float part[16];
+            __syncthreads();   // the previous tile's reads are done (first tile: q and pages visible)
+            // stage the tile's K and V rows: 16-byte chunks, every load issued
+            // before the first store (rows past the tile repeat its last row)
+            {
+                uint4 kr[4], vr[4];
 #pragma unroll
-                    for (int l = 0; l < 16; l++) part[l] = __fmul_rn(qs[h][l], h2f(ks[p][l]));
+                for (int i = 0; i < 4; i++) {
+                    const int c = t + 256 * i, j = c & 15;
+                    const int p = (c >> 4) < n ? (c >> 4) : n - 1;
+                    const int pos = from + tb + p, pi = pos >> 6;
+                    const int page = pi < PGMAX ? pgs[pi] : a.pgtab[a.pg_base + pi];
+                    const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;
+                    kr[i] = *(const uint4 *)(a.kc + base);
+                    vr[i] = *(const uint4 *)(a.vc + base);
+                }
 #pragma unroll
-                    for (int v = 1; v < HD / 16; v++)
-#pragma unroll
-                        for (int l = 0; l < 16; l++)
-                            part[l] = __fadd_rn(part[l], __fmul_rn(qs[h][l + 16 * v], h2f(ks[p][l + 16 * v])));
-#pragma unroll
-                    for (int w = 1; w < 16; w <<= 1)
-#pragma unroll
-                        for (int l = 0; l < 16; l += 2 * w) part[l] = __fadd_rn(part[l], part[l + w]);
-                    sc[h][p] = __fmul_rn(part[0], a.scale);
+                for (int i = 0; i < 4; i++) {
+                    const int c = t + 256 * i;
+                    *(uint4 *)&ks[c >> 4][8 * (c & 15)] = kr[i];
+                    *(uint4 *)&vs[c >> 4][8 * (c & 15)] = vr[i];
                 }
             }
             __syncthreads();
-            // running max, in position order (scores read a chunk ahead)
-            if (t < G) {
-                float m = mrun[t];
-                for (int p0 = 0; p0 < n; p0 += CK) {
-                    float sv[CK];
+            // scores of position `lane` for this wave's heads, one head at a time
+            float s[HW];
 #pragma unroll
-                    for (int p = 0; p < CK; p += 4) {
-                        const float4 f = *(const float4 *)&sc[t][p0 + p];
-                        sv[p] = f.x; sv[p + 1] = f.y; sv[p + 2] = f.z; sv[p + 3] = f.w;
-                    }
+            for (int hh = 0; hh < HW; hh++) {
+                const float *qh = &qs[wave + 4 * hh][0];
+                float part[16];
 #pragma unroll
-                    for (int p = 0; p < CK; p++) {
-                        if (p0 + p < n) {
-                            mb[t][p0 + p] = m;
-                            up[t][p0 + p] = sv[p] > m;
-                            if (sv[p] > m) m = sv[p];
-                            ma[t][p0 + p] = m;
-                        }
-                    }
-                }
-                mrun[t] = m;
-            }
-            __syncthreads();
-            // rescale factors (exactly 1 where the max holds: x·1 = x) and weights
-            for (int hp = t; hp < G * TP; hp += 256) {
-                const int h = hp / TP, p = hp % TP;
-                if (p < n) {
-                    cf[h][p] = up[h][p] ? cj_expf(mb[h][p] - sc[h][p]) : 1.0f;
-                    pr[h][p] = cj_expf(sc[h][p] - ma[h][p]);
-                }
-            }
-            __syncthreads();
-            // the recurrences, in position order, operands a chunk ahead
+                for (int c = 0; c < 16; c++) {
+                    const uint4 kk = *(const uint4 *)&ks[lane][8 * c];
+                    const float4 qa = *(const float4 *)(qh + 8 * c), qb = *(const float4 *)(qh + 8 * c + 4);
+                    const float kf[8] = {h2f(kk.x), h2f(kk.x >> 16), h2f(kk.y), h2f(kk.y >> 16),
+                                         h2f(kk.z), h2f(kk.z >> 16), h2f(kk.w), h2f(kk.w >> 16)};
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-            for (int k = 0; k < PAIRS; k++) {
-                const int e = t + 256 * k, h = e / HD, d = e % HD;
-                float x = acc[k];
-                for (int p0 = 0; p0 < n; p0 += CK) {
-                    float cv[CK], pv[CK], vv[CK];
-#pragma unroll
-                    for (int p = 0; p < CK; p += 4) {
-                        const float4 c4 = *(const float4 *)&cf[h][p0 + p], p4 = *(const float4 *)&pr[h][p0 + p];
-                        cv[p] = c4.x; cv[p + 1] = c4.y; cv[p + 2] = c4.z; cv[p + 3] = c4.w;
-                        pv[p] = p4.x; pv[p + 1] = p4.y; pv[p + 2] = p4.z; pv[p + 3] = p4.w;
-                    }
-#pragma unroll
-                    for (int p = 0; p < CK; p++) vv[p] = h2f(vs[p0 + p][d]);
-#pragma unroll
-                    for (int p = 0; p < CK; p++) {
-                        if (p0 + p < n) {
-                            x = __fmul_rn(x, cv[p]);
-                            x = __fadd_rn(x, __fmul_rn(vv[p], pv[p]));
-                        }
+                    for (int i = 0; i < 8; i++) {
+                        const int j = 8 * (c & 1) + i;
+                        const float pr = __fmul_rn(qv[i], kf[i]);
+                        part[j] = c < 2 ? pr : __fadd_rn(part[j], pr);
                     }
                 }
-                acc[k] = x;
+#pragma unroll
+                for (int w = 1; w < 16; w <<= 1)
+#pragma unroll
+                    for (int j = 0; j < 16; j += 2 * w) part[j] = __fadd_rn(part[j], part[j + w]);
+                s[hh] = __fmul_rn(part[0], a.scale);
             }
-            if (t < G) {
-                float ls = lrun[t];
+            const bool live = lane < n;
+#pragma unroll 1
+            for (int hh = 0; hh < HW; hh++) {
+                // running max before (exc) and after (inc) each position
+                float x = live ? s[hh] : -3.0e38f;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const float y = __shfl_up(x, off);
+                    if (lane >= off) x = fmaxf(x, y);
+                }
+                const float inc = fmaxf(m[hh], x);
+                float exc = __shfl_up(inc, 1);
+                if (lane == 0) exc = m[hh];
+                const bool up = live && s[hh] > exc;
+                const float cf = up ? cj_expf(exc - s[hh]) : 1.0f;
+                const float pw = live ? cj_expf(s[hh] - inc) : 0.0f;
+                const uint64_t ups = __ballot(up);
+                m[hh] = lane_f(inc, n - 1);
+                float x0 = acc0[hh], x1 = acc1[hh], ls = l[hh];
                 for (int p = 0; p < n; p++) {
-                    ls = __fmul_rn(ls, cf[t][p]);
-                    ls = __fadd_rn(ls, pr[t][p]);
+                    const float w = lane_f(pw, p);
+                    const uint32_t vv = *(const uint32_t *)&vs[p][2 * lane];
+                    if ((ups >> p) & 1) {
+                        const float c = lane_f(cf, p);
+                        x0 = __fmul_rn(x0, c);
+                        x1 = __fmul_rn(x1, c);
+                        ls = __fmul_rn(ls, c);
+                    }
+                    ls = __fadd_rn(ls, w);
+                    x0 = __fadd_rn(x0, __fmul_rn(h2f(vv), w));
+                    x1 = __fadd_rn(x1, __fmul_rn(h2f(vv >> 16), w));
                 }
-                lrun[t] = ls;
+                acc0[hh] = x0; acc1[hh] = x1; l[hh] = ls;
             }
         }
-        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < PAIRS; k++) {
-            const int e = t + 256 * k, h = e / HD, d = e % HD;
-            a.part[((int64_t)(kvh * G + h) * ATTN_MAX_SPLITS + sp) * (HD + 2) + d] = acc[k];
-        }
-        if (t < G) {
-            float *pb = a.part + ((int64_t)(kvh * G + t) * ATTN_MAX_SPLITS + sp) * (HD + 2);
-            pb[HD] = mrun[t];
-            pb[HD + 1] = lrun[t];
+        for (int hh = 0; hh < HW; hh++) {
+            float *pb = a.part + ((int64_t)(kvh * G + wave + 4 * hh) * ATTN_MAX_SPLITS + sp) * (HD + 2);
+            *(float2 *)(pb + 2 * lane) = make_float2(acc0[hh], acc1[hh]);
+            if (lane == 0) *(float2 *)(pb + HD) = make_float2(m[hh], l[hh]);
         }
     }
-    if (!a.out) return;
+    if (!a.out && !a.packed) return;
 
     // the last workgroup of this kv head merges its splits
-    __shared__ int ticket;
     __threadfence();
     __syncthreads();
     if (t == 0) ticket = atomicAdd(&a.counters[kvh], 1);
     __syncthreads();
     if (ticket != ATTN_MAX_SPLITS - 1) return;
     __threadfence();
-    for (int e = t; e < G * HD; e += 256) {
-        const int hh = e / HD, dd = e % HD;
-        const int qq = kvh * G + hh;
+    float *ob = (float *)&vs[0][0];                  // G·HD merged values (LDS reuse)
+#pragma unroll 1
+    for (int hh = 0; hh < HW; hh++) {
+        const int qq = kvh * G + wave + 4 * hh;
         const float *pb0 = a.part + (int64_t)qq * ATTN_MAX_SPLITS * (HD + 2);
-        float gm = -3.0e38f;
-        for (int s2 = 0; s2 < splits; s2++) {
-            const float mv = pb0[s2 * (HD + 2) + HD];
-            if (mv > gm) gm = mv;
-        }
-        float tacc = 0.0f, gt = 0.0f;
-        for (int sub = 0; sub < 4; sub++) {
-            float gl = 0.0f, ac = 0.0f;
-            for (int s2 = sub; s2 < splits; s2 += 4) {
-                const float *pb = pb0 + s2 * (HD + 2);
-                const float lsv = pb[HD + 1];
-                if (lsv > 0.0f) {
-                    const float wt = cj_expf(pb[HD] - gm);
-                    gl = __fadd_rn(gl, __fmul_rn(wt, lsv));
-                    ac = __fadd_rn(ac, __fmul_rn(pb[dd], wt));
+        // lane s: split s's (max, sum); the weights of the merge
+        const float2 ml = *(const float2 *)(pb0 + lane * (HD + 2) + HD);
+        const bool in = lane < splits;
+        const float mv = in ? ml.x : -3.0e38f;
+        const float gm = group_max<64>(mv);
+        const bool on = in && ml.y > 0.0f;
+        const float wt = on ? cj_expf(mv - gm) : 0.0f;
+        const uint64_t ons = __ballot(on);
+        float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < splits; s0 += 16) {
+            float2 av[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) av[k] = *(const float2 *)(pb0 + (s0 + k) * (HD + 2) + 2 * lane);
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const int s2 = s0 + k;
+                if (s2 < splits && ((ons >> s2) & 1)) {
+                    const float w = lane_f(wt, s2), lsv = lane_f(ml.y, s2);
+                    gl[k & 3] = __fadd_rn(gl[k & 3], __fmul_rn(w, lsv));
+                    ac0[k & 3] = __fadd_rn(ac0[k & 3], __fmul_rn(av[k].x, w));
+                    ac1[k & 3] = __fadd_rn(ac1[k & 3], __fmul_rn(av[k].y, w));
                 }
             }
-            if (sub == 0) { tacc = ac; gt = gl; }
-            else { tacc = __fadd_rn(tacc, ac); gt = __fadd_rn(gt, gl); }
         }
-        a.out[(int64_t)qq * HD + dd] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
+        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
+        const float rs = __fdiv_rn(1.0f, gt);
+        const float o0 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac0[0], ac0[1]), ac0[2]), ac0[3]), rs);
+        const float o1 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac1[0], ac1[1]), ac1[2]), ac1[3]), rs);
+        if (a.out) *(float2 *)(a.out + (int64_t)qq * HD + 2 * lane) = make_float2(o0, o1);
+        *(float2 *)(ob + (wave + 4 * hh) * HD + 2 * lane) = make_float2(o0, o1);
+    }
+    if (a.packed) {
+        __syncthreads();
+        // the kv head's G·HD outputs are G·HD/256 whole pack blocks
+#pragma unroll
+        for (int b = 0; b < G * HD / 256; b++)
+            pack256(ob[256 * b + t], a.per32, a.packed + ((int64_t)kvh * (G * HD / 256) + b) * 320, bmax);
     }
     if (t == 0) a.counters[kvh] = 0;
 }
 
-#define SPLIT_KERNEL(HD, G) \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h##HD##_g##G(cj_attn_args a) { split_body<HD, G>(a); }
-SPLIT_KERNEL(128, 4)
-SPLIT_KERNEL(128, 8)
+#define SPLIT_KERNEL(G) \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G>(a); }
+SPLIT_KERNEL(4)
+SPLIT_KERNEL(8)
 
 // ------------------------------------------------------------ two-pass form
 
@@ -324,95 +320,50 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_a
 // contract), the merge in reducePackBlockCpu's order: the global max, then
 // four interleaved sub-sums (splits s ≡ 0, 1, 2, 3 mod 4, each ascending) of
 // w_s·l_s and of w_s·acc_s[d], w_s = exp(m_s − max), added in sub order;
-// out = acc · (1 / l).
+// out = acc · (1 / l). Thread t owns output e (head h, dim d) and loads its
+// 64 accumulators at once; lane s of its wave holds split s's (max, sum) and
+// weight, read by every lane in split order — no LDS, no barrier before the
+// pack.
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
-    const int t = threadIdx.x;
+    __shared__ float bmax[8];
+    const int t = threadIdx.x, lane = t & 63;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
-    // thread t: output e (head h, dim d). Its 64 accumulators are loaded
-    // first; meanwhile wave w (< heads in the block) reads head h0+w's
-    // (max, sum) pairs, one split a lane, and leaves the weights in LDS.
-    __shared__ float wts[4][ATTN_MAX_SPLITS], lsum[4][ATTN_MAX_SPLITS];
-    __shared__ int use[4][ATTN_MAX_SPLITS];
-    const int h0 = (int)((int64_t)blockIdx.x * 256 / hd), nh = hd >= 256 ? 1 : 256 / hd;
-    // every slot of the partials is loaded (the buffer holds 64 a head); the
-    // step's split count only masks the arithmetic, so no load waits on it
+    // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
+    const int64_t ew = min((int64_t)blockIdx.x * 256 + (t & ~63), n - 1);
+    const int h = (int)(ew / hd), d = (int)(min(e, n - 1) % hd);
+    const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
     float pv[ATTN_MAX_SPLITS];
-    const int h = (int)(e / hd), d = (int)(e % hd);
-    {
-        const float *pb0 = a.part + (int64_t)(e < n ? h : 0) * ATTN_MAX_SPLITS * (hd + 2) + d;
 #pragma unroll
-        for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2)];
-    }
+    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
+    const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
     int splits = a.splits;
     if (a.state) {
         int count = a.state->pos + 1;
         if (a.window > 0 && count > a.window) count = a.window;
         splits = decode_splits(count, a.n_kv, a.workers);
     }
-    {
-        const int w = t >> 6, sl = t & 63;
-        if (w < nh) {
-            const int hw = h0 + w < a.n_q ? h0 + w : 0;
-            const float *pb = a.part + ((int64_t)hw * ATTN_MAX_SPLITS + sl) * (hd + 2) + hd;
-            const float m0 = pb[0], l0 = pb[1];
-            const bool in = h0 + w < a.n_q && sl < splits;
-            const float mv = in ? m0 : -3.0e38f, lv = in ? l0 : 0.0f;
-            const float gm = group_max<64>(mv);
-            const bool on = in && lv > 0.0f;
-            use[w][sl] = on;
-            wts[w][sl] = on ? cj_expf(mv - gm) : 0.0f;
-            lsum[w][sl] = lv;
-        }
-    }
-    __syncthreads();
-    float x = 0.0f;
-    if (e < n) {
-        const int hh = h - h0;
-        float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool in = lane < splits;
+    const float mv = in ? ml.x : -3.0e38f;
+    const float gm = group_max<64>(mv);
+    const bool on = in && ml.y > 0.0f;
+    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    const uint64_t ons = __ballot(on);
+    float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
-            if (s2 < splits && use[hh][s2]) {
-                const float w = wts[hh][s2];
-                gl[s2 & 3] = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lsum[hh][s2]));
-                ac[s2 & 3] = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
-            }
+    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
+        if ((ons >> s2) & 1) {
+            const float w = lane_f(wt, s2), lsv = lane_f(ml.y, s2);
+            gl[s2 & 3] = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lsv));
+            ac[s2 & 3] = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
         }
-        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
-        const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
-        x = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
-        if (a.out) a.out[e] = x;
     }
-    if (!a.packed) return;
-    // the block's pack: 256 values, one a thread
-    __shared__ float bmax[8];
-    const int lane = t & 63;
-    const float av = fabsf(x);
-    float am;
-    if (a.per32) {
-        const float mm = group_max<32>(av);
-        if ((lane & 31) == 0) bmax[t >> 5] = mm;
-        __syncthreads();
-        am = bmax[t >> 5];
-    } else {
-        const float mm = group_max<64>(av);
-        if (lane == 0) bmax[t >> 6] = mm;
-        __syncthreads();
-        am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
-    }
-    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
-    const int q = round_away(__fmul_rn(x, inv));
-    uint8_t *ob = a.packed + (int64_t)blockIdx.x * 320;
-    ob[t] = (uint8_t)(int8_t)q;
-    const int s = group_sum_i<32>(q);
-    if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
-    if (a.per32) {
-        if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
-    } else {
-        if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
-        pack_zero_pad(ob, t);
-    }
+    const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
+    const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
+    const float x = e < n ? __fmul_rn(tacc, __fdiv_rn(1.0f, gt)) : 0.0f;
+    if (a.out && e < n) a.out[e] = x;
+    if (a.packed) pack256(x, a.per32, a.packed + (int64_t)blockIdx.x * 320, bmax);
 }
 
 // QK-norm (optional) + split-half RoPE + fp16 K/V append, one workgroup of

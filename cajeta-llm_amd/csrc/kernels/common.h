@@ -124,6 +124,51 @@ DEV void pack_zero_pad(uint8_t *blk, int t) {
     if (t < 7) *(uint32_t *)(blk + 292 + 4 * t) = 0u;
 }
 
+// One 256-wide pack block written by a whole workgroup of 256, thread t
+// holding element t: the block (or 32-group) maximum, q = round-half-away(
+// v·(127/amax)), the int32 sums of 32 and the f32 scale(s) — the layout of
+// Quant.q8kPackPad / q8kPack32Pad (io/Quant.cajeta:3232-3321). `bmax` is 8
+// floats of LDS; the function ends on a barrier, so it can be called in a
+// loop over blocks.
+DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
+    const int t = threadIdx.x, lane = t & 63;
+    const float av = fabsf(v);
+    float am;
+    if (per32) {
+        float m = av;
+#pragma unroll
+        for (int s = 16; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+        if ((lane & 31) == 0) bmax[t >> 5] = m;
+        __syncthreads();
+        am = bmax[t >> 5];
+    } else {
+        float m = av;
+#pragma unroll
+        for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+        if (lane == 0) bmax[t >> 6] = m;
+        __syncthreads();
+        am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
+    }
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    const int q = round_away(__fmul_rn(v, inv));
+    ob[t] = (uint8_t)(int8_t)q;
+    int s = q;
+#pragma unroll
+    for (int k = 16; k > 0; k >>= 1) s += __shfl_xor(s, k);
+    if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
+    if (per32) {
+        if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);
+    } else {
+        if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
+        pack_zero_pad(ob, t);
+    }
+    __syncthreads();
+}
+
+// Lane-uniform reads of another lane's value (the lane index must be the
+// same on every lane of the wave).
+DEV float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
 // ---------------------------------------------------------------------------
 // Activation staging into LDS: the 320-byte block layout of the reference's
 // Quant.q8kPackPad / q8kPack32Pad ([0,256) q, [256,288) 8 int32 sums of 32,
@@ -197,7 +242,7 @@ DEV float stage_value(const float *x, int64_t n, int64_t e, bool norm, float sca
 // lane-local plus xor shuffles, with no barrier until the end. The codes
 // are the reference's q8kPack ones: q = round-half-away(v · (127/amax)).
 DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form,
-                    int per32, uint8_t *sx, float *xout) {
+                    int per32, uint8_t *sx, float *xout, int bstride = 320) {
     const int t = threadIdx.x;
     const int64_t total = (int64_t)nblk * 256;
     for (int64_t e0 = 16 * t; e0 < total; e0 += 4096) {
@@ -237,7 +282,7 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
         sum += __shfl_xor(sum, 1);
         const int64_t blk = e0 >> 8;
         const int in = (int)(e0 & 255);           // offset inside the block
-        uint8_t *b = sx + blk * 320;
+        uint8_t *b = sx + blk * bstride;
         *(uint4 *)(b + in) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
         const int g = in >> 5, j = (in >> 4) & 15;   // 32-group, lane of the block
         if (!(j & 1)) *(int32_t *)(b + 256 + 4 * g) = sum;
@@ -257,11 +302,12 @@ DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, 
     __syncthreads();
 }
 
-// Copy an already-packed activation (nblk blocks of 320 bytes) into LDS.
-DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx) {
+// Copy an already-packed activation (nblk blocks of 320 bytes) into LDS,
+// block b at sx + b·bstride.
+DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx, int bstride = 320) {
     const int t = threadIdx.x;
     int n16 = nblk * 20;
-    for (int i = t; i < n16; i += 256) ((uint4 *)sx)[i] = ((const uint4 *)xp)[i];
+    for (int i = t; i < n16; i += 256) *(uint4 *)(sx + (i / 20) * bstride + (i % 20) * 16) = ((const uint4 *)xp)[i];
     __syncthreads();
 }
 

@@ -18,8 +18,15 @@
 // The f32-activation formats (Q4_0, MXFP4, the f32 router) are summed by one
 // thread a row in the reference's element order.
 //
+// Q4_K has its own body (gemv_q4k_body): one lane a whole 256-element block,
+// the first weight block of every lane in flight before the prologue, and
+// workgroups that sweep several passes of rows with a one-block prefetch.
+//
 // Prepared row layouts (HBM, 16-byte aligned rows):
-//   Q4_K : the GGUF blocks as they are: {f16 d, f16 dmin, 12 B scales, 128 B qs}
+//   Q4_K : [c 0..7][b 0..nb-1] 16-byte pieces of the blocks' qs (piece c of
+//          block b = qs bytes 16c..16c+15), then [b] the 16-byte block
+//          headers {f16 d, f16 dmin, 12 B scales}: lanes holding consecutive
+//          blocks load consecutive 16-byte words
 //   Q6_K : [ql nb·128][qh nb·64][scales nb·16][d nb·2, padded to 16]
 //   Q8_0 : [qs nb·32][d nb·2, padded to 16]
 //   Q4_0 : [qs nb·16][d nb·2, padded to 16]
@@ -41,63 +48,57 @@ DEV int terms_per_row(int fmt, int64_t cols) {
 
 // ----------------------------------------------------------------- phase A
 
-// Q4_K × q8_K. Unit (block b, 64-element chunk j): the two sub-blocks' int
-// dots × their 6-bit scales and the mins × the pack's sub-block sums, summed
-// over the quad exactly; the leader writes (d·xs·sumi, dmin·xs·dmins).
-template <int NR, int LPR>
-DEV void terms_q4k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb, int slot) {
-    const int units = nb * 4;
-    for (int u = slot; u < units; u += LPR) {
-        const int b = u >> 2, j = u & 3;
-        uint4 hd[NR], q0[NR], q1[NR];
+// Q4_K × q8_K, one lane a whole block. The 16 sub-block halves' int dots
+// (low nibbles: sub-block 2g, high: 2g+1 of each 64-element group g), the
+// 6-bit scales and mins (Quant.headK4) and the pack's 32-sums stay in
+// integers; the block's f32 terms are formed as Quant.q4kMatVecIntoQ8 forms
+// them (io/Quant.cajeta:3374-3445): (d·xs)·sumi and (dmin·xs)·dmins.
+#define Q4K_LDS_STRIDE 336   // pack blocks in LDS: 16 lanes on 16 blocks hit distinct banks
+struct Q4kBlock { uint4 q[8]; uint4 h; };
+
+DEV void q4k_fetch(Q4kBlock &x, const uint8_t *row, int nb, int b) {
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const uint8_t *blk = wr[r] + (int64_t)b * 144;
-            hd[r] = *(const uint4 *)blk;
-            q0[r] = *(const uint4 *)(blk + 16 + 32 * j);
-            q1[r] = *(const uint4 *)(blk + 32 + 32 * j);
-        }
-        const uint8_t *ax = sx + b * 320 + 64 * j;
-        const uint4 a0 = *(const uint4 *)(ax), a1 = *(const uint4 *)(ax + 16);
-        const uint4 a2 = *(const uint4 *)(ax + 32), a3 = *(const uint4 *)(ax + 48);
-        const int2 bs = *(const int2 *)(sx + b * 320 + 256 + 8 * j);
-        const float xs = *(const float *)(sx + b * 320 + 288);
-        const int hi = j >= 2;
-        const int t0 = (2 * j) & 3;
+    for (int c = 0; c < 8; c++) x.q[c] = *(const uint4 *)(row + ((int64_t)c * nb + b) * 16);
+    x.h = *(const uint4 *)(row + (int64_t)nb * 128 + (int64_t)b * 16);
+}
+
+DEV float2 q4k_block_terms(const Q4kBlock &x, const uint8_t *ax) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    int dot[8];
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const uint32_t M = 0x0F0F0F0Fu;
-            int dlo = 0, dhi = 0;
-            dlo = sdot4(q0[r].x & M, a0.x, dlo); dlo = sdot4(q0[r].y & M, a0.y, dlo);
-            dlo = sdot4(q0[r].z & M, a0.z, dlo); dlo = sdot4(q0[r].w & M, a0.w, dlo);
-            dlo = sdot4(q1[r].x & M, a1.x, dlo); dlo = sdot4(q1[r].y & M, a1.y, dlo);
-            dlo = sdot4(q1[r].z & M, a1.z, dlo); dlo = sdot4(q1[r].w & M, a1.w, dlo);
-            dhi = sdot4((q0[r].x >> 4) & M, a2.x, dhi); dhi = sdot4((q0[r].y >> 4) & M, a2.y, dhi);
-            dhi = sdot4((q0[r].z >> 4) & M, a2.z, dhi); dhi = sdot4((q0[r].w >> 4) & M, a2.w, dhi);
-            dhi = sdot4((q1[r].x >> 4) & M, a3.x, dhi); dhi = sdot4((q1[r].y >> 4) & M, a3.y, dhi);
-            dhi = sdot4((q1[r].z >> 4) & M, a3.z, dhi); dhi = sdot4((q1[r].w >> 4) & M, a3.w, dhi);
-            // 6-bit scales/mins of sub-blocks 2j, 2j+1 (the headK4 unpacking)
-            const uint32_t sy = hd[r].y, sz = hd[r].z, sw = hd[r].w;
-            const uint32_t A0 = (sy >> (8 * t0)) & 255, B0 = (sz >> (8 * t0)) & 255, C0 = (sw >> (8 * t0)) & 255;
-            const uint32_t A1 = (sy >> (8 * t0 + 8)) & 255, B1 = (sz >> (8 * t0 + 8)) & 255, C1 = (sw >> (8 * t0 + 8)) & 255;
-            int sc0, mn0, sc1, mn1;
-            if (hi) {
-                sc0 = (C0 & 15) | ((A0 >> 2) & 48); mn0 = (C0 >> 4) | ((B0 >> 2) & 48);
-                sc1 = (C1 & 15) | ((A1 >> 2) & 48); mn1 = (C1 >> 4) | ((B1 >> 2) & 48);
-            } else {
-                sc0 = A0 & 63; mn0 = B0 & 63; sc1 = A1 & 63; mn1 = B1 & 63;
-            }
-            int sumi = dlo * sc0 + dhi * sc1;
-            int dmins = mn0 * bs.x + mn1 * bs.y;
-            sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
-            dmins += quad_xor1(dmins); dmins += quad_xor2(dmins);
-            if (j == 0) {
-                const float d = h2f(hd[r].x), dmin = h2f(hd[r].x >> 16);
-                *(float2 *)(tr[r] + 2 * b) = make_float2(__fmul_rn(__fmul_rn(d, xs), (float)sumi),
-                                                         __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
-            }
+    for (int g = 0; g < 4; g++) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint4 q = x.q[2 * g + h];
+            const uint4 al = *(const uint4 *)(ax + 64 * g + 16 * h);
+            const uint4 ah = *(const uint4 *)(ax + 64 * g + 32 + 16 * h);
+            lo = sdot4(q.x & M, al.x, lo); lo = sdot4(q.y & M, al.y, lo);
+            lo = sdot4(q.z & M, al.z, lo); lo = sdot4(q.w & M, al.w, lo);
+            hi = sdot4((q.x >> 4) & M, ah.x, hi); hi = sdot4((q.y >> 4) & M, ah.y, hi);
+            hi = sdot4((q.z >> 4) & M, ah.z, hi); hi = sdot4((q.w >> 4) & M, ah.w, hi);
         }
+        dot[2 * g] = lo;
+        dot[2 * g + 1] = hi;
     }
+    // scales[0..3] = A, [4..7] = B, [8..11] = C: sub-block j < 4 takes the
+    // low 6 bits of A_j (scale) and B_j (min); j + 4 takes the nibbles of C_j
+    // with the top two bits of A_j (scale) and B_j (min) above them
+    const uint32_t A = x.h.y, B = x.h.z, C = x.h.w;
+    const int4 s0 = *(const int4 *)(ax + 256), s1 = *(const int4 *)(ax + 272);
+    const int bs[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    int sumi = 0, dmins = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t a8 = (A >> (8 * j)) & 255, b8 = (B >> (8 * j)) & 255, c8 = (C >> (8 * j)) & 255;
+        const int sc_lo = (int)(a8 & 63), mn_lo = (int)(b8 & 63);
+        const int sc_hi = (int)((c8 & 15) | ((a8 >> 2) & 48)), mn_hi = (int)((c8 >> 4) | ((b8 >> 2) & 48));
+        sumi += dot[j] * sc_lo + dot[j + 4] * sc_hi;
+        dmins += bs[j] * mn_lo + bs[j + 4] * mn_hi;
+    }
+    const float xs = *(const float *)(ax + 288);
+    const float d = h2f(x.h.x), dmin = h2f(x.h.x >> 16);
+    return make_float2(__fmul_rn(__fmul_rn(d, xs), (float)sumi), __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
 }
 
 // Q6_K × q8_K. Unit (block b, 64 elements): half g, lane half hl; four
@@ -296,98 +297,106 @@ DEV bool argmax_take(float ov, int oi, float mv, int mi) {
 
 // ------------------------------------------------------------------ body
 
-template <int FMT, int LPR, int NR>
-DEV void gemv_body(const cj_gemv_args &a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    float *red = (float *)smem;
-    float *bmax = red + 256;
-    uint8_t *sx = smem + LDS_SCRATCH;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int64_t cols = a.cols;
-    constexpr bool f32act = (FMT == CJ_Q4_0 || FMT == CJ_MXFP4 || FMT == CJ_F32);
-    const int nblk = (int)((cols + 255) / 256);
-    const int act_bytes = f32act ? nblk * 1024 : nblk * 320;
-    float *terms = (float *)(sx + act_bytes);
-    const int TB = terms_per_row(FMT, cols);
-    const int R = a.rows_per_wg;
+// Where a workgroup's rows come from: with MoE indirection (`sel`), copy k
+// of the rows reads expert sel[k]'s weight, activation k and output k.
+struct GemvSlice {
+    const uint8_t *W;
+    const float *X;
+    float *Y, *ACT;
+    int64_t row0;
+    int kidx;
+};
 
-    // MoE indirection: copy k of the rows reads expert sel[k]
+DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
+    GemvSlice s;
+    const int R = a.rows_per_wg;
     int64_t wg = blockIdx.x;
-    int kidx = 0;
+    s.kidx = 0;
     if (a.sel) {
         const int64_t wpk = (a.rows + R - 1) / R;
-        kidx = (int)(wg / wpk);
+        s.kidx = (int)(wg / wpk);
         wg = wg % wpk;
     }
-    const uint8_t *W = a.w + (a.sel ? (int64_t)a.sel[kidx] * a.expert_bytes : 0);
-    const float *X = a.x ? a.x + kidx * a.x_stride : nullptr;
-    float *Y = a.y ? a.y + kidx * a.y_stride : nullptr;
-    float *ACT = a.act ? a.act + kidx * a.y_stride : nullptr;
-    const int64_t row0 = wg * R;
+    s.W = a.w + (a.sel ? (int64_t)a.sel[s.kidx] * a.expert_bytes : 0);
+    s.X = a.x ? a.x + s.kidx * a.x_stride : nullptr;
+    s.Y = a.y ? a.y + s.kidx * a.y_stride : nullptr;
+    s.ACT = a.act ? a.act + s.kidx * a.y_stride : nullptr;
+    s.row0 = wg * R;
+    return s;
+}
 
-    // ---- prologue: the activation into LDS
+// The activation into LDS: a copied pack, the pack of an f32 vector, RMSNorm
+// + pack, or (f32-activation formats) the f32 values, normed or not. Ends on
+// a barrier.
+DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, uint8_t *sx, float *red, int bstride) {
+    const int64_t cols = a.cols;
+    const int nblk = (int)((cols + 255) / 256);
     if (a.pro == CJ_PRO_PACKED) {
-        stage_copy(a.xp + kidx * a.xp_stride, nblk, sx);
+        stage_copy(a.xp + sl.kidx * a.xp_stride, nblk, sx, bstride);
     } else {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
-        const float scale = norm ? stage_norm_scale(X, cols, a.eps, red) : 1.0f;
-        if (f32act) stage_f32(X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx);
-        else stage_pack(X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr);
+        const float scale = norm ? stage_norm_scale(sl.X, cols, a.eps, red) : 1.0f;
+        if (f32act) stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx);
+        else stage_pack(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr, bstride);
     }
+}
 
-    float v = 0.0f;
-    const int64_t r = row0 + t;
-    const bool live = t < R && r < a.rows;
-    if constexpr (f32act) {
-        // ---- one thread a row, in element order
-        __shared__ float lut[16];
-        if (t < 16) lut[t] = mxfp4_val(t);
-        __syncthreads();
-        if (live) v = seq_row<FMT>(W + r * a.row_bytes, (const float *)sx, cols, lut);
-    } else {
-    // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
-    {
-        constexpr int G = 64 / LPR;
-        const int group = lane / LPR, slot = lane % LPR;
-        const int lanes_groups = 4 * G;                      // row groups across the workgroup
-        const int nb = (int)(cols / 256), nb32 = (int)(cols / 32);
-        for (int i = 0; i < R; i += NR * lanes_groups) {
-            const int rl0 = i + NR * (wave * G + group);
-            if (rl0 >= R) continue;     // uniform per LPR group
-            const uint8_t *wr[NR];
-            float *tr[NR];
-#pragma unroll
-            for (int k = 0; k < NR; k++) {
-                const int64_t rk = row0 + rl0 + k;
-                wr[k] = W + (rk < a.rows ? rk : a.rows - 1) * a.row_bytes;
-                tr[k] = terms + (rl0 + k) * TB;
-            }
-            if (FMT == CJ_Q4_K) terms_q4k<NR, LPR>(wr, tr, sx, nb, slot);
-            else if (FMT == CJ_Q6_K) terms_q6k<NR, LPR>(wr, tr, sx, nb, slot);
-            else terms_q80<NR, LPR>(wr, tr, sx, nb32, slot);
-        }
-    }
-    __syncthreads();
+// Operands the epilogue reads from global memory, loaded early (after the
+// weight stream is requested) so they have arrived when the rows finish:
+// the residual of an accumulating row, and for q|k|v the RoPE (cos, sin) of
+// the row's pair and the K/V page of the step position.
+struct EpiPre {
+    float y;
+    float2 cs;
+    int page;
+    int pos;
+};
 
-    // ---- phase B: thread t folds row t's terms in block order
-    if (t < R) {
-        const float *tp = terms + t * TB;
-        if (FMT == CJ_Q4_K) {
-            for (int b = 0; b < TB; b += 2) v = __fsub_rn(__fadd_rn(v, tp[b]), tp[b + 1]);
-        } else {
-            for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
-        }
+template <int EPI>
+DEV EpiPre epi_prefetch_t(const cj_gemv_args &a, const GemvSlice &sl) {
+    EpiPre e{0.0f, make_float2(0.0f, 0.0f), 0, 0};
+    const int64_t r = min(sl.row0 + (int64_t)threadIdx.x, a.rows - 1);
+    if constexpr (EPI == CJ_EPI_ACCUM) {
+        e.y = sl.Y[a.y_off + r];
+    } else if constexpr (EPI == CJ_EPI_QKV_ROPE) {
+        e.pos = step_pos(a.state, a.pos);
+        e.page = a.pgtab[a.pg_base + (e.pos >> 6)];
+        const int hd = a.head_dim, half = hd >> 1;
+        const int bb = (int)(r % hd) >> 1;
+        e.cs = *(const float2 *)(a.rope_cs + 2 * ((int64_t)e.pos * half + bb));
     }
-    }
-    const float vp = __shfl_xor(v, 1);      // the paired row (RoPE pair, gate/up pair)
-    const int pos = (a.epi == CJ_EPI_QKV_ROPE || a.epi == CJ_EPI_ARGMAX) ? step_pos(a.state, a.pos) : 0;
+    return e;
+}
 
+// The epilogue chosen at run time (the generic body).
+DEV EpiPre epi_prefetch(const cj_gemv_args &a, const GemvSlice &sl) {
     switch (a.epi) {
+    case CJ_EPI_ACCUM: return epi_prefetch_t<CJ_EPI_ACCUM>(a, sl);
+    case CJ_EPI_QKV_ROPE: return epi_prefetch_t<CJ_EPI_QKV_ROPE>(a, sl);
+    default: return epi_prefetch_t<CJ_EPI_STORE>(a, sl);
+    }
+}
+
+// Row r's value v (thread t = r − row0; the paired row r^1 sits on thread
+// t^1) through the epilogue: store, residual accumulate, RoPE + the fp16 K/V
+// append, SiLU·up (+ the pack of the result), or the greedy argmax.
+template <int EPI>
+DEV void gemv_epilogue_t(const cj_gemv_args &a, const GemvSlice &sl, float v, float *bmax, const EpiPre &pre) {
+    const int t = threadIdx.x;
+    const int R = a.rows_per_wg;
+    const int64_t r = sl.row0 + t;
+    const bool live = t < R && r < a.rows;
+    float *Y = sl.Y, *ACT = sl.ACT;
+    const int64_t row0 = sl.row0;
+    const float vp = __shfl_xor(v, 1);      // the paired row (RoPE pair, gate/up pair)
+    const int pos = EPI == CJ_EPI_QKV_ROPE ? pre.pos : EPI == CJ_EPI_ARGMAX ? step_pos(a.state, a.pos) : 0;
+
+    switch (EPI) {
     case CJ_EPI_STORE:
         if (live) Y[a.y_off + r] = v;
         break;
     case CJ_EPI_ACCUM:
-        if (live) Y[a.y_off + r] = __fadd_rn(Y[a.y_off + r], v);
+        if (live) Y[a.y_off + r] = __fadd_rn(pre.y, v);
         break;
     case CJ_EPI_QKV_ROPE: {
         if (!live || (t & 1)) break;
@@ -397,21 +406,21 @@ DEV void gemv_body(const cj_gemv_args &a) {
             // GGUF pair order: row h·hd + 2b + a holds HF dim a·half + b
             const int64_t rr = r < qrows ? r : r - qrows;
             const int h = (int)(rr / hd), bb = (int)(rr % hd) >> 1;
-            const float2 cs = *(const float2 *)(a.rope_cs + 2 * ((int64_t)pos * half + bb));
+            const float2 cs = pre.cs;
             const float ra = __fsub_rn(__fmul_rn(v, cs.x), __fmul_rn(vp, cs.y));
             const float rb = __fadd_rn(__fmul_rn(v, cs.y), __fmul_rn(vp, cs.x));
             if (r < qrows) {
                 a.q_out[(int64_t)h * hd + bb] = ra;
                 a.q_out[(int64_t)h * hd + half + bb] = rb;
             } else {
-                const int64_t ki = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+                const int64_t ki = (((int64_t)pre.page * a.n_kv + h) * 64 + (pos & 63)) * hd;
                 a.kc[ki + bb] = f2h(ra);
                 a.kc[ki + half + bb] = f2h(rb);
             }
         } else {
             const int64_t rr = r - qrows - krows;
             const int h = (int)(rr / hd), d = (int)(rr % hd);
-            const int64_t vi = kv_index(a.pgtab, a.pg_base, pos, a.n_kv, h, hd);
+            const int64_t vi = (((int64_t)pre.page * a.n_kv + h) * 64 + (pos & 63)) * hd;
             a.vc[vi + d] = f2h(v);
             a.vc[vi + d + 1] = f2h(vp);
         }
@@ -423,7 +432,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
         break;
     }
 
-    if (a.epi == CJ_EPI_GLU && a.act_pack) {
+    if (EPI == CJ_EPI_GLU && a.act_pack) {
         // The last workgroup to finish a 256-wide block of the activation
         // packs it for the down projection.
         __shared__ int last_blocks[4];
@@ -441,7 +450,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
                 const int64_t real = ((blk + 1) * 256 < a.act_n ? (blk + 1) * 256 : a.act_n) - blk * 256;
                 const int mine = (int)(hi - lo);
                 const int old = atomicAdd(&a.counters[blk], mine);
-                if (old + mine == real) last_blocks[n_last++] = (int)blk;
+                if (old + mine == real && n_last < 4) last_blocks[n_last++] = (int)blk;
             }
         }
         __syncthreads();
@@ -454,7 +463,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
                 if (t == 0) a.counters[blk] = 0;
             }
         }
-    } else if (a.epi == CJ_EPI_ARGMAX) {
+    } else if (EPI == CJ_EPI_ARGMAX) {
         // first occurrence across the workgroup, then the last workgroup
         // reduces every workgroup's partial and advances the step
         __shared__ float bv[256];
@@ -503,6 +512,322 @@ DEV void gemv_body(const cj_gemv_args &a) {
     }
 }
 
+// The epilogue chosen at run time (the generic body).
+DEV void gemv_epilogue(const cj_gemv_args &a, const GemvSlice &sl, float v, float *bmax, const EpiPre &pre) {
+    switch (a.epi) {
+    case CJ_EPI_ACCUM: gemv_epilogue_t<CJ_EPI_ACCUM>(a, sl, v, bmax, pre); break;
+    case CJ_EPI_QKV_ROPE: gemv_epilogue_t<CJ_EPI_QKV_ROPE>(a, sl, v, bmax, pre); break;
+    case CJ_EPI_GLU: gemv_epilogue_t<CJ_EPI_GLU>(a, sl, v, bmax, pre); break;
+    case CJ_EPI_ARGMAX: gemv_epilogue_t<CJ_EPI_ARGMAX>(a, sl, v, bmax, pre); break;
+    default: gemv_epilogue_t<CJ_EPI_STORE>(a, sl, v, bmax, pre); break;
+    }
+}
+
+// Generic body (Q6_K, Q8_0 and the f32-activation formats).
+template <int FMT, int LPR, int NR>
+DEV void gemv_body(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *red = (float *)smem;
+    float *bmax = red + 256;
+    uint8_t *sx = smem + LDS_SCRATCH;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int64_t cols = a.cols;
+    constexpr bool f32act = (FMT == CJ_Q4_0 || FMT == CJ_MXFP4 || FMT == CJ_F32);
+    const int nblk = (int)((cols + 255) / 256);
+    const int act_bytes = f32act ? nblk * 1024 : nblk * 320;
+    float *terms = (float *)(sx + act_bytes);
+    const int TB = terms_per_row(FMT, cols);
+    const int R = a.rows_per_wg;
+    const GemvSlice sl = gemv_slice(a);
+    const int64_t row0 = sl.row0;
+
+    gemv_prologue(a, sl, f32act, sx, red, 320);
+    const EpiPre pre = epi_prefetch(a, sl);
+
+    float v = 0.0f;
+    const int64_t r = row0 + t;
+    const bool live = t < R && r < a.rows;
+    if constexpr (f32act) {
+        // ---- one thread a row, in element order
+        __shared__ float lut[16];
+        if (t < 16) lut[t] = mxfp4_val(t);
+        __syncthreads();
+        if (live) v = seq_row<FMT>(sl.W + r * a.row_bytes, (const float *)sx, cols, lut);
+    } else {
+    // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
+    {
+        constexpr int G = 64 / LPR;
+        const int group = lane / LPR, slot = lane % LPR;
+        const int lanes_groups = 4 * G;                      // row groups across the workgroup
+        const int nb = (int)(cols / 256), nb32 = (int)(cols / 32);
+        for (int i = 0; i < R; i += NR * lanes_groups) {
+            const int rl0 = i + NR * (wave * G + group);
+            if (rl0 >= R) continue;     // uniform per LPR group
+            const uint8_t *wr[NR];
+            float *tr[NR];
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                const int64_t rk = row0 + rl0 + k;
+                wr[k] = sl.W + (rk < a.rows ? rk : a.rows - 1) * a.row_bytes;
+                tr[k] = terms + (rl0 + k) * TB;
+            }
+            if (FMT == CJ_Q6_K) terms_q6k<NR, LPR>(wr, tr, sx, nb, slot);
+            else terms_q80<NR, LPR>(wr, tr, sx, nb32, slot);
+        }
+    }
+    __syncthreads();
+
+    // ---- phase B: thread t folds row t's terms in block order
+    if (t < R) {
+        const float *tp = terms + t * TB;
+        for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
+    }
+    }
+    gemv_epilogue(a, sl, v, bmax, pre);
+}
+
+// The Q4_K prologue in two halves, so its global loads can be issued before
+// the weight stream and its arithmetic run after: loads retire in issue
+// order, so anything the prologue loaded after the weights would wait for
+// HBM. PRO is the prologue (PACKED, PACK or NORM_PACK); RND bounds the
+// activation to RND·4096 columns. The register arrays are plain locals of
+// fixed size so they stay in registers; every load is unconditional (indices
+// clamped into range, the surplus masked where it is used) because a load
+// under a branch makes the compiler wait for every load in flight at the
+// join, the weight stream included.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));   // a native 16-byte vector
+
+template <int PRO, int RND>
+struct Q4kProDims {
+    static constexpr int NPK = PRO == CJ_PRO_PACKED ? (RND * 16 * 20 + 255) / 256 : 1;
+    static constexpr int NX = PRO == CJ_PRO_PACKED ? 1 : RND;
+    static constexpr int NW = PRO == CJ_PRO_NORM_PACK ? RND : 1;
+    static constexpr int NS = PRO == CJ_PRO_NORM_PACK ? RND * 16 : 1;
+};
+
+template <int PRO, int RND>
+DEV void q4k_pro_load(const cj_gemv_args &a, const GemvSlice &sl, float4 (&px)[Q4kProDims<PRO, RND>::NX][4],
+                      float4 (&pw)[Q4kProDims<PRO, RND>::NW][4], float (&pxs)[Q4kProDims<PRO, RND>::NS],
+                      u32x4 (&ppk)[Q4kProDims<PRO, RND>::NPK]) {
+    using D = Q4kProDims<PRO, RND>;
+    const int t = threadIdx.x;
+    const int64_t n = a.cols;
+    if constexpr (PRO == CJ_PRO_PACKED) {
+        const u32x4 *src = (const u32x4 *)(a.xp + sl.kidx * a.xp_stride);
+        const int n16 = (int)(n / 256) * 20;
+#pragma unroll
+        for (int i = 0; i < D::NPK; i++) ppk[i] = src[min(t + 256 * i, n16 - 1)];
+    } else {
+        const float *X = sl.X;
+#pragma unroll
+        for (int r = 0; r < RND; r++) {
+            const int64_t e0 = min((int64_t)(4096 * r + 16 * t), n - 16);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                px[r][j] = *(const float4 *)(X + e0 + 4 * j);
+                if constexpr (PRO == CJ_PRO_NORM_PACK) pw[r][j] = *(const float4 *)(a.nw + e0 + 4 * j);
+            }
+        }
+        if constexpr (PRO == CJ_PRO_NORM_PACK) {
+#pragma unroll
+            for (int k = 0; k < RND * 16; k++) pxs[k] = X[min((int64_t)(t + 256 * k), n - 1)];
+        }
+    }
+}
+
+// Pack one 16-value slice per thread into the LDS blocks (stage_pack's
+// arithmetic: the 32-group or block maximum over lane neighbours, codes
+// round-half-away(v·127/amax), 32-sums, scale).
+DEV void q4k_pack_slice(const float (&v)[16], int64_t e0, int per32, uint8_t *sx, int bstride) {
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) am = fmaxf(am, fabsf(v[k]));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    if (!per32) {
+        am = fmaxf(am, __shfl_xor(am, 2));
+        am = fmaxf(am, __shfl_xor(am, 4));
+        am = fmaxf(am, __shfl_xor(am, 8));
+    }
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int q = round_away(__fmul_rn(v[k], inv));
+        sum += q;
+        wd[k >> 2] |= ((uint32_t)q & 255u) << (8 * (k & 3));
+    }
+    sum += __shfl_xor(sum, 1);
+    const int64_t blk = e0 >> 8;
+    const int in = (int)(e0 & 255);
+    uint8_t *b = sx + blk * bstride;
+    *(uint4 *)(b + in) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    const int g = in >> 5, j = (in >> 4) & 15;
+    if (!(j & 1)) *(int32_t *)(b + 256 + 4 * g) = sum;
+    if (per32) {
+        if (!(j & 1)) *(float *)(b + 288 + 4 * g) = __fdiv_rn(am, 127.0f);
+    } else {
+        if (j == 0) *(float *)(b + 288) = __fdiv_rn(am, 127.0f);
+        else if (j < 8) *(uint32_t *)(b + 288 + 4 * j) = 0u;
+    }
+}
+
+template <int PRO, int RND>
+DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PRO, RND>::NX][4],
+                         const float4 (&pw)[Q4kProDims<PRO, RND>::NW][4], const float (&pxs)[Q4kProDims<PRO, RND>::NS],
+                         const u32x4 (&ppk)[Q4kProDims<PRO, RND>::NPK], uint8_t *sx, float *red) {
+    using D = Q4kProDims<PRO, RND>;
+    const int t = threadIdx.x;
+    const int64_t n = a.cols;
+    if constexpr (PRO == CJ_PRO_PACKED) {
+        // words past the pack go to a dummy slot in the (here unused) scratch
+        const int n16 = (int)(n / 256) * 20;
+#pragma unroll
+        for (int i = 0; i < D::NPK; i++) {
+            const int idx = t + 256 * i;
+            uint8_t *dst = idx < n16 ? sx + (idx / 20) * Q4K_LDS_STRIDE + (idx % 20) * 16 : (uint8_t *)red + 16 * (t & 63);
+            *(u32x4 *)dst = ppk[i];
+        }
+    } else {
+        float scale = 1.0f;
+        if constexpr (PRO == CJ_PRO_NORM_PACK) {
+            // RMSNorm scale in the CPU row form's order (Prim.rmsnormPackRowCpuKernel):
+            // thread t sums x[t + 256k]^2 over k, the partials fold 128, 64, ..., 1
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RND * 16; k++)
+                if (t + 256 * k < n) s = __fadd_rn(s, __fmul_rn(pxs[k], pxs[k]));
+            red[t] = s;
+            __syncthreads();
+            if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
+            __syncthreads();
+            if (t < 64) {
+                float v = __fadd_rn(red[t], red[t + 64]);
+#pragma unroll
+                for (int m = 32; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_down(v, m));
+                if (t == 0) red[0] = v;
+            }
+            __syncthreads();
+            scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(red[0], (float)n), a.eps)));
+        }
+#pragma unroll
+        for (int r = 0; r < RND; r++) {
+            const int64_t e0 = 4096 * r + 16 * t;
+            if (e0 < n) {
+                const float xv[16] = {px[r][0].x, px[r][0].y, px[r][0].z, px[r][0].w, px[r][1].x, px[r][1].y,
+                                      px[r][1].z, px[r][1].w, px[r][2].x, px[r][2].y, px[r][2].z, px[r][2].w,
+                                      px[r][3].x, px[r][3].y, px[r][3].z, px[r][3].w};
+                float v[16];
+                if constexpr (PRO == CJ_PRO_NORM_PACK) {
+                    const float wv[16] = {pw[r][0].x, pw[r][0].y, pw[r][0].z, pw[r][0].w, pw[r][1].x, pw[r][1].y,
+                                          pw[r][1].z, pw[r][1].w, pw[r][2].x, pw[r][2].y, pw[r][2].z, pw[r][2].w,
+                                          pw[r][3].x, pw[r][3].y, pw[r][3].z, pw[r][3].w};
+#pragma unroll
+                    for (int k = 0; k < 16; k++) {
+                        const float wi = a.norm_form == 1 ? __fadd_rn(1.0f, wv[k]) : wv[k];
+                        v[k] = __fmul_rn(__fmul_rn(xv[k], scale), wi);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) v[k] = xv[k];
+                }
+                q4k_pack_slice(v, e0, a.per32, sx, Q4K_LDS_STRIDE);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Q4_K body. Lane (wave w, lane l) owns row group l / LPR of each pass and
+// blocks b = l % LPR + LPR·k of its row. The items (pass, k) run in order
+// through a ring of four 144-byte blocks: item i computes while items
+// i+1..i+3 load. Issue order: the prologue's loads, the first four items,
+// the epilogue's operands, then the prologue's arithmetic — so the norm and
+// pack run while the weight stream is in flight. The block terms go to LDS;
+// thread t then folds row t's in block order, acc = (acc + A_b) − B_b
+// (Quant.q4kMatVecIntoQ8), and runs the epilogue.
+template <int LPR, int PRO, int RND, int EPI>
+DEV void gemv_q4k_body(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *red = (float *)smem;
+    float *bmax = red + 256;
+    uint8_t *sx = smem + LDS_SCRATCH;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nb = (int)(a.cols / 256);
+    float *terms = (float *)(sx + nb * Q4K_LDS_STRIDE);
+    const int R = a.rows_per_wg;
+    const GemvSlice sl = gemv_slice(a);
+    const int64_t row0 = sl.row0;
+
+    constexpr int RG = 64 / LPR;                 // rows a wave covers in one pass
+    const int rg = lane / LPR, li = lane % LPR;
+    const int K = (nb + LPR - 1) / LPR;          // items a pass (the last may leave lanes idle)
+    const int items = (R / (4 * RG)) * K;        // R is a multiple of 4·RG
+    auto row_of = [&](int it) { return (it / K) * (4 * RG) + wave * RG + rg; };
+    auto blk_of = [&](int it) { return li + LPR * (it % K); };
+    auto fetch = [&](Q4kBlock &x, int it) {
+        const int64_t rr = row0 + row_of(it);
+        const int b = blk_of(it);
+        q4k_fetch(x, sl.W + (rr < a.rows ? rr : a.rows - 1) * a.row_bytes, nb, b < nb ? b : nb - 1);
+    };
+    auto consume = [&](const Q4kBlock &x, int it) {
+        const int rl = row_of(it), b = blk_of(it);
+        if (b < nb) *(float2 *)(terms + ((int64_t)rl * nb + b) * 2) = q4k_block_terms(x, sx + b * Q4K_LDS_STRIDE);
+    };
+
+    // issue order: f32 prologues load before the weights; a copied pack
+    // loads after the first weight item (its words are stored to LDS as soon
+    // as they arrive, which is before that item is consumed)
+    using PD = Q4kProDims<PRO, RND>;
+    float4 px[PD::NX][4], pw[PD::NW][4];
+    float pxs[PD::NS];
+    u32x4 ppk[PD::NPK];
+    Q4kBlock ring[4];
+    if constexpr (PRO != CJ_PRO_PACKED) {
+        q4k_pro_load<PRO, RND>(a, sl, px, pw, pxs, ppk);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    fetch(ring[0], 0);
+    if constexpr (PRO == CJ_PRO_PACKED) {
+        __builtin_amdgcn_sched_barrier(0);
+        q4k_pro_load<PRO, RND>(a, sl, px, pw, pxs, ppk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 1; j < 4; j++) fetch(ring[j], min(j, items - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const EpiPre pre = epi_prefetch_t<EPI>(a, sl);
+    __builtin_amdgcn_sched_barrier(0);
+    q4k_pro_compute<PRO, RND>(a, px, pw, pxs, ppk, sx, red);
+    for (int it0 = 0; it0 < items; it0 += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int it = it0 + j;
+            if (it < items) {
+                consume(ring[j], it);
+                fetch(ring[j], min(it + 4, items - 1));
+            }
+        }
+    }
+    __syncthreads();
+
+    float v = 0.0f;
+    if (t < R) {
+        const float4 *tp = (const float4 *)(terms + (int64_t)t * nb * 2);
+        int b = 0;
+        for (; b + 1 < nb; b += 2) {
+            const float4 q = tp[b >> 1];
+            v = __fsub_rn(__fadd_rn(v, q.x), q.y);
+            v = __fsub_rn(__fadd_rn(v, q.z), q.w);
+        }
+        if (b < nb) {
+            const float2 q = *(const float2 *)(terms + ((int64_t)t * nb + b) * 2);
+            v = __fsub_rn(__fadd_rn(v, q.x), q.y);
+        }
+    }
+    gemv_epilogue_t<EPI>(a, sl, v, bmax, pre);
+}
+
 #define GEMV_KERNEL(NAME, FMT, LPR, NR)                                                \
     extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) {            \
         gemv_body<FMT, LPR, NR>(a);                                                     \
@@ -522,8 +847,33 @@ DEV void gemv_body(const cj_gemv_args &a) {
     GEMV_KERNEL(PFX##_l16_n2, FMT, 16, 2)           \
     GEMV_KERNEL(PFX##_l8_n2, FMT, 8, 2)
 
-GEMV_FAMILY(cj_gemv_q4k, CJ_Q4_K, 4)
-GEMV_FAMILY_N2(cj_gemv_q4k, CJ_Q4_K)
+// cj_gemv_q4k_<prologue><epilogue>_b<LPR>[_w]: LPR lanes a row, one lane a
+// block; prologue c (copied pack), p (pack of f32) or n (RMSNorm + pack);
+// epilogue s (store), a (accumulate), q (q|k|v RoPE + K/V), g (SiLU·up) or
+// m (argmax); activations up to 4096 columns (_w: up to 16384, no norm). The
+// prologue and epilogue are compile-time so no load waits on a branch.
+#define Q4K_KERNEL(NAME, LPR, PRO, RND, EPI) \
+    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) { gemv_q4k_body<LPR, PRO, RND, EPI>(a); }
+#define Q4K_EPIS(P, LPR, PRO)                                                    \
+    Q4K_KERNEL(cj_gemv_q4k_##P##s_b##LPR, LPR, PRO, 1, CJ_EPI_STORE)             \
+    Q4K_KERNEL(cj_gemv_q4k_##P##a_b##LPR, LPR, PRO, 1, CJ_EPI_ACCUM)             \
+    Q4K_KERNEL(cj_gemv_q4k_##P##q_b##LPR, LPR, PRO, 1, CJ_EPI_QKV_ROPE)          \
+    Q4K_KERNEL(cj_gemv_q4k_##P##g_b##LPR, LPR, PRO, 1, CJ_EPI_GLU)               \
+    Q4K_KERNEL(cj_gemv_q4k_##P##m_b##LPR, LPR, PRO, 1, CJ_EPI_ARGMAX)
+Q4K_EPIS(c, 16, CJ_PRO_PACKED)
+Q4K_EPIS(p, 16, CJ_PRO_PACK)
+Q4K_EPIS(n, 16, CJ_PRO_NORM_PACK)
+Q4K_EPIS(c, 8, CJ_PRO_PACKED)
+Q4K_EPIS(p, 8, CJ_PRO_PACK)
+Q4K_EPIS(n, 8, CJ_PRO_NORM_PACK)
+#define Q4K_EPIS_W(P, PRO)                                                       \
+    Q4K_KERNEL(cj_gemv_q4k_##P##s_b16_w, 16, PRO, 4, CJ_EPI_STORE)               \
+    Q4K_KERNEL(cj_gemv_q4k_##P##a_b16_w, 16, PRO, 4, CJ_EPI_ACCUM)               \
+    Q4K_KERNEL(cj_gemv_q4k_##P##q_b16_w, 16, PRO, 4, CJ_EPI_QKV_ROPE)            \
+    Q4K_KERNEL(cj_gemv_q4k_##P##g_b16_w, 16, PRO, 4, CJ_EPI_GLU)                 \
+    Q4K_KERNEL(cj_gemv_q4k_##P##m_b16_w, 16, PRO, 4, CJ_EPI_ARGMAX)
+Q4K_EPIS_W(c, CJ_PRO_PACKED)
+Q4K_EPIS_W(p, CJ_PRO_PACK)
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)

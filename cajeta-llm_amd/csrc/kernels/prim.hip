@@ -192,6 +192,20 @@ DEV float decode_prepared(int type, const uint8_t *row, int64_t cols, int64_t e)
         const int byv = row[b * 16 + (j & 15)];
         return __fmul_rn(mxfp4_val(j < 16 ? (byv & 15) : (byv >> 4)), mxfp4_scale(row[nb32 * 16 + b]));
     }
+    case CJ_Q4_K: {
+        // qs byte k of block b at ((k / 16)·nb + b)·16 + k % 16; the header at 128·nb + 16·b
+        const int64_t b = e >> 8;
+        const int el = e & 255, g = el / 64, r = el % 64, s = r / 32, l = r % 32, sb = el / 32;
+        const int k = 32 * g + l;
+        const int q = (row[((int64_t)(k >> 4) * nb + b) * 16 + (k & 15)] >> (4 * s)) & 15;
+        const uint8_t *hb = row + nb * 128 + b * 16;
+        const uint8_t *sc = hb + 4;
+        int scv, mnv;
+        if (sb < 4) { scv = sc[sb] & 63; mnv = sc[sb + 4] & 63; }
+        else { scv = (sc[sb + 4] & 15) | ((sc[sb - 4] >> 2) & 48); mnv = (sc[sb + 4] >> 4) | ((sc[sb] >> 2) & 48); }
+        const float d = h2f(*(const uint16_t *)hb), dmin = h2f(*(const uint16_t *)(hb + 2));
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)scv), (float)q), __fmul_rn(dmin, (float)mnv));
+    }
     case CJ_Q6_K: {
         const int64_t b = e >> 8;
         const int el = e & 255, g = el / 128, r = el % 128, sl = r / 64, l64 = r % 64, sh = r / 32, l32 = r % 32;
@@ -219,13 +233,20 @@ extern "C" __global__ void __launch_bounds__(256) cj_dequant(cj_dequant_args a) 
 // per block. `src` rows are the GGUF bytes, `dst` rows the prepared ones.
 
 extern "C" __global__ void __launch_bounds__(256) cj_prepare(cj_prepare_args a) {
-    const int64_t bpr = a.type == CJ_Q6_K ? a.cols / 256 : a.cols / 32;
+    const int64_t bpr = (a.type == CJ_Q6_K || a.type == CJ_Q4_K) ? a.cols / 256 : a.cols / 32;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.rows * bpr) return;
     const int64_t r = i / bpr, b = i % bpr;
     const uint8_t *s = a.src + r * a.src_row_bytes;
     uint8_t *d = a.dst + r * a.dst_row_bytes;
     switch (a.type) {
+    case CJ_Q4_K: {
+        // piece c of the qs to ((c·bpr) + b)·16, the 16-byte header to 128·bpr + 16·b
+        const uint8_t *blk = s + b * 144;
+        for (int c = 0; c < 8; c++)
+            for (int k = 0; k < 16; k++) d[(c * bpr + b) * 16 + k] = blk[16 + 16 * c + k];
+        for (int k = 0; k < 16; k++) d[bpr * 128 + b * 16 + k] = blk[k];
+    } break;
     case CJ_Q6_K: {
         const uint8_t *blk = s + b * 210;
         for (int k = 0; k < 128; k++) d[b * 128 + k] = blk[k];

@@ -67,7 +67,8 @@ struct Request {
 enum Kind {
     K_EMBED = 0, K_QKV = 1, K_ATTN = 2, K_O = 3, K_GATE_UP = 4, K_DOWN = 5,
     K_ROUTER = 6, K_ROUTE = 7, K_EXP_GATE_UP = 8, K_EXP_DOWN = 9, K_COMBINE = 10, K_HEAD = 11,
-    K_NORM = 12   // RMSNorm + pack of the residual (before q|k|v; the FFN and head ones alike)
+    K_NORM = 12,  // RMSNorm + pack of the residual (before q|k|v; the FFN and head ones alike)
+    K_MERGE = 13  // the split-K attention's merge + pack alone (part of K_ATTN in the step)
 };
 
 }  // namespace
@@ -375,38 +376,45 @@ int Engine::enqueue_step(int s) {
     // the reference's choice of form: split-K for hd 128 with 4 or 8 query
     // heads a kv head, else the two-pass score/combine
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
-    const int64_t qd_ = (int64_t)n_heads * head_dim;
     char attn_kernel[64], combine_kernel[64];
     if (split) snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_split_h128_g%d", grp);
     else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
     snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
-        if (want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false))) return rc;
-        if (want(K_QKV, l)) {   // 1. q|k|v over the pack, RoPE + K/V append epilogue
+        // Q4_K projections fold the RMSNorm + pack into their prologue (the
+        // weight stream is in flight while it runs); others read a pack
+        const bool qkv_norm = L.qkv.type == CJ_Q4_K && hidden <= 4096 && !getenv("CJ_TMP_NOFUSE");
+        if (!qkv_norm && want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false))) return rc;
+        if (want(K_QKV, l)) {   // 1. q|k|v over the normed residual, RoPE + K/V append epilogue
             cj_gemv_args a{};
             a.w = (const uint8_t *)L.qkv.p; a.xp = xpack; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
             a.pgtab = pgtab; a.rope_cs = rope; a.state = S.state; a.rows = L.qkv.rows; a.cols = hidden;
             a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_QKV_ROPE;
+            if (qkv_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = hs; a.nw = L.attn_norm; a.norm_form = 0; }
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
             a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
-        if (want(K_ATTN, l)) {   // 2. attention
+        if (want(K_ATTN, l) || want(K_MERGE, l)) {   // 2. attention
             cj_attn_args a{};
             a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
             a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
             a.pg_base = S.pg_base; a.pg_n = pages_per_seq; a.window = L.window; a.scale = scale;
             if (split) {
                 // partials, then the merge + the pack the o projection reads
+                // (a launch boundary orders them: a merge by the last
+                // workgroup of each kv head would need device-scope fences,
+                // which cost far more than the launch on this part)
                 a.out = nullptr;
-                if ((rc = launch(attn_kernel, (uint32_t)(n_kv * 64), 256, 0, a))) return rc;
+                if (want(K_ATTN, l) && (rc = launch(attn_kernel, (uint32_t)(n_kv * 64), 256, 0, a))) return rc;
                 cj_merge_args m{};
                 m.out = attn; m.packed = attn_pack; m.part = part; m.state = S.state; m.n_q = n_heads;
                 m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0; m.n_kv = n_kv; m.workers = workers;
                 m.window = L.window;
-                if ((rc = launch("cj_attn_merge", (uint32_t)((qd_ + 255) / 256), 256, 0, m))) return rc;
-            } else {
+                if ((rc = launch("cj_attn_merge", (uint32_t)(((int64_t)n_heads * head_dim + 255) / 256), 256, 0, m)))
+                    return rc;
+            } else if (want(K_ATTN, l)) {
                 // the grid covers the longest window; the kernel idles past count
                 a.splits = ctx;
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
@@ -419,9 +427,10 @@ int Engine::enqueue_step(int s) {
             a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
             a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split ? CJ_PRO_PACKED : CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
-            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
+            if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
-        if (want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
+        const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096 && !getenv("CJ_TMP_NOFUSE");
+        if (!gu_norm && want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
             const int ct = n_experts ? L.gu_exps.type : L.gu.type;
             if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0))) return rc;
         }
@@ -433,14 +442,15 @@ int Engine::enqueue_step(int s) {
                 a.type = L.gu.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
                 a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
                 a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16)))) return rc;
+                if (gu_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = hs; a.nw = L.ffn_norm; a.norm_form = 0; }
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16, a.pro, a.epi)))) return rc;
             }
             if (want(K_DOWN, l)) {   // 5. down, residual into hs
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.down.p; a.x = act; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
                 a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
                 a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
             }
         } else {
             if (want(K_ROUTER, l)) {   // router logits from the normed hidden (f32 weights)
@@ -448,7 +458,7 @@ int Engine::enqueue_step(int s) {
                 a.w = (const uint8_t *)L.router.p; a.x = xn; a.y = moe_logits; a.rows = n_experts;
                 a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_F32;
                 a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
-                if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
             }
             if (want(K_ROUTE, l)) {
                 cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1};
@@ -462,7 +472,7 @@ int Engine::enqueue_step(int s) {
                 a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
                 a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
                 a.y_stride = expert_ffn;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
             }
             if (want(K_EXP_DOWN, l)) {   // the selected experts' down into moe_y[k]
                 cj_gemv_args a{};
@@ -471,7 +481,7 @@ int Engine::enqueue_step(int s) {
                 a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
                 a.batch = 1; a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes;
                 a.x_stride = expert_ffn; a.y_stride = hidden;
-                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32)))) return rc;
+                if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
             }
             if (want(K_COMBINE, l)) {   // hs += Σ_k w_k · y_k in k order
                 cj_combine_args a{hs, moe_y, moe_w, hidden, n_used};
@@ -488,7 +498,7 @@ int Engine::enqueue_step(int s) {
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128, a.pro, a.epi);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
         if (only < 0) {
@@ -629,6 +639,7 @@ int64_t Engine::kind_bytes(int kind, int count) const {
     case K_COMBINE: return (int64_t)n_used * h * 4 + h * 8;
     case K_HEAD: return wb(head) + ((h + 255) / 256) * 320 + (int64_t)vocab * 4;
     case K_NORM: return h * 8 + ((h + 255) / 256) * 320;
+    case K_MERGE: return (int64_t)n_heads * 64 * (head_dim + 2) * 4 + qd * 4 + ((qd + 255) / 256) * 320;
     default: return 0;
     }
 }
@@ -638,7 +649,8 @@ int64_t Engine::step_bytes(int count) const {
     int64_t b = kind_bytes(K_EMBED, count) + kind_bytes(K_HEAD, count) + kind_bytes(K_NORM, count);
     for (int l = 0; l < n_layers; l++) {
         const int c = layers[l].window > 0 ? std::min(count, layers[l].window) : count;
-        b += 2 * kind_bytes(K_NORM, c) + kind_bytes(K_QKV, c) + kind_bytes(K_ATTN, c) + kind_bytes(K_O, c);
+        const int norms = (layers[l].qkv.type == CJ_Q4_K ? 0 : 1) + (n_experts == 0 && layers[l].gu.type == CJ_Q4_K ? 0 : 1);
+        b += norms * kind_bytes(K_NORM, c) + kind_bytes(K_QKV, c) + kind_bytes(K_ATTN, c) + kind_bytes(K_O, c);
         if (n_experts == 0) b += kind_bytes(K_GATE_UP, c) + kind_bytes(K_DOWN, c);
         else
             for (int k : {K_ROUTER, K_ROUTE, K_EXP_GATE_UP, K_EXP_DOWN, K_COMBINE}) b += kind_bytes(k, c);
@@ -654,7 +666,7 @@ int64_t Engine::step_bytes(int count) const {
 // it was.
 int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel) {
     if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
-    if (kind < K_EMBED || kind > K_NORM || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
+    if (kind < K_EMBED || kind > K_MERGE || reps <= 0) return fail(CJ_ERR_ARG, "time: kind %d reps %d", kind, reps);
     const bool moe_kind = kind >= K_ROUTER && kind <= K_COMBINE, dense_kind = kind == K_GATE_UP || kind == K_DOWN;
     if ((n_experts == 0 && moe_kind) || (n_experts > 0 && dense_kind))
         return fail(CJ_ERR_ARG, "time: kind %d is not part of this model's step", kind);
@@ -665,22 +677,48 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
     CJ_HIP(hipMemcpy(&saved, S.state, sizeof saved, hipMemcpyDeviceToHost));
     only = kind;
     only_layer = 0;
+    const uint64_t before = launch_count();
     int rc = enqueue_step(s);                     // one untimed launch
+    if (!rc && launch_count() == before) rc = fail(CJ_ERR_ARG, "time: kind %d launches nothing in this model's step", kind);
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
         rc = fail(CJ_ERR_HIP, "time: event create");
     if (!rc) {
         kernel = last_launch();
-        (void)hipEventRecord(e0, stream());
-        for (int i = 0; i < reps && !rc; i++) {
-            only_layer = (i + 1) % (n_layers > 0 ? n_layers : 1);
-            rc = enqueue_step(s);
+        // the reps as the step runs them: captured into one graph and
+        // replayed (eager launches when graphs are off, for profilers)
+        hipGraphExec_t ge = nullptr;
+        if (graphs) {
+            CJ_HIP(hipStreamSynchronize(stream()));
+            CJ_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal));
+            for (int i = 0; i < reps && !rc; i++) {
+                only_layer = (i + 1) % (n_layers > 0 ? n_layers : 1);
+                rc = enqueue_step(s);
+            }
+            hipGraph_t gr = nullptr;
+            hipError_t ce = hipStreamEndCapture(stream(), &gr);
+            if (!rc && ce != hipSuccess) rc = fail(CJ_ERR_HIP, "time: capture: %s", hipGetErrorString(ce));
+            if (!rc && hipGraphInstantiate(&ge, gr, nullptr, nullptr, 0) != hipSuccess) {
+                ge = nullptr;
+                rc = fail(CJ_ERR_HIP, "time: graph instantiate");
+            }
+            if (gr) (void)hipGraphDestroy(gr);
+            if (!rc) (void)hipGraphLaunch(ge, stream());   // warm replay
         }
-        (void)hipEventRecord(e1, stream());
-        (void)hipEventSynchronize(e1);
-        float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, e0, e1);
-        *avg_us = ms * 1000.0f / (float)reps;
+        if (!rc) {
+            (void)hipEventRecord(e0, stream());
+            if (ge) (void)hipGraphLaunch(ge, stream());
+            for (int i = 0; !ge && i < reps && !rc; i++) {
+                only_layer = (i + 1) % (n_layers > 0 ? n_layers : 1);
+                rc = enqueue_step(s);
+            }
+            (void)hipEventRecord(e1, stream());
+            (void)hipEventSynchronize(e1);
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, e0, e1);
+            *avg_us = ms * 1000.0f / (float)reps;
+        }
+        if (ge) (void)hipGraphExecDestroy(ge);
     }
     only = -1;
     only_layer = 0;

@@ -12,6 +12,7 @@ namespace cj {
 int fail(int code, const char *fmt, ...);
 const char *last_error();
 const char *last_launch();   // the name of the last kernel launched on this thread
+uint64_t launch_count();     // launches made so far
 
 bool ready();
 hipStream_t stream();
@@ -42,7 +43,7 @@ bool is_f32_act(int type);
 bool gemv_supported(int type, int64_t cols);
 // Kernel, rows per workgroup (`target` rounded to what one pass of the
 // workgroup covers, at most 256; 0 = one pass), grid and LDS of a GEMV.
-GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target);
+GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, int epi);
 int run_gemv(const cj_gemv_args &a, const GemvPlan &p);
 
 // Device memory owned by the runtime itself (not through the handle table's

@@ -31,12 +31,13 @@ struct Ctx {
 Ctx g;
 thread_local std::string g_err;
 thread_local std::string g_last_launch;
+uint64_t g_launches = 0;   // launches made (the timing seam checks a kind launched something)
 
 // The reference's kernel names (KernelCap.nameOf, model/KernelCap.cajeta:100-140
 // and the launch sites) answered by the kernels of this code object.
 const std::unordered_map<std::string, std::string> &name_map() {
     static const std::unordered_map<std::string, std::string> m = {
-        {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_l64"},
+        {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_cs_b16"},
         {"q6kQ8WaveMatVecKernel", "cj_gemv_q6k_l64"},
         {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
         {"q40F32WaveMatVecKernel", "cj_gemv_q40"},
@@ -61,8 +62,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"embedRowQ80Kernel", "cj_embed"},
         {"gatherRowsF32Kernel", "cj_embed"},
         {"routerTopKKernel", "cj_moe_route"},
-        {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_l64"},
-        {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_l64"},
+        {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_cg_b16"},
+        {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_cs_b16"},
     };
     return m;
 }
@@ -134,8 +135,11 @@ int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, co
     hipError_t e = hipModuleLaunchKernel(it->second, grid, 1, 1, block, 1, 1, lds, g.stream, params, nullptr);
     if (e != hipSuccess) return fail(CJ_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e));
     g_last_launch = name;
+    g_launches++;
     return CJ_OK;
 }
+
+uint64_t launch_count() { return g_launches; }
 
 // ------------------------------------------------------------------ GEMV
 
@@ -159,7 +163,35 @@ bool gemv_supported(int type, int64_t cols) {
     return prepared_row_bytes(type, cols) > 0 && cols <= (is_f32_act(type) ? 15360 : 16384);
 }
 
-GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target) {
+// Q4_K: LPR lanes a row (one lane a block), rows a workgroup in whole passes
+// of 4·(64 / LPR), about rows / CUs of them so one wave of workgroups covers
+// the matrix, bounded by one folding thread a row and by LDS (the staged
+// pack at 336 bytes a block + 8 bytes of terms a row and block). The kernel
+// is picked by the prologue (copied pack, f32 pack, RMSNorm + pack) and the
+// activation width (up to 4096 columns, or up to 16384 without the norm).
+GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
+    GemvPlan p;
+    const int64_t nb = cols / 256;
+    const int lpr = nb >= 16 ? 16 : 8;
+    const int64_t pass = 4 * (64 / lpr);
+    int64_t R = rows / std::max(1, g.cus) / pass * pass;
+    const int64_t fixed = 3072 + nb * 336;
+    const int64_t rmax = std::min<int64_t>((65536 - fixed) / (nb * 8), 256) / pass * pass;
+    R = std::max<int64_t>(pass, std::min(R, rmax));
+    if (const char *e = getenv("CJ_TMP_Q4K_R")) R = std::max<int64_t>(pass, std::min<int64_t>(atoi(e) / pass * pass, rmax));
+    const char pc = pro == CJ_PRO_PACKED ? 'c' : pro == CJ_PRO_PACK ? 'p' : pro == CJ_PRO_NORM_PACK ? 'n' : '?';
+    const char ec = epi == CJ_EPI_STORE ? 's' : epi == CJ_EPI_ACCUM ? 'a' : epi == CJ_EPI_QKV_ROPE ? 'q'
+                  : epi == CJ_EPI_GLU ? 'g' : epi == CJ_EPI_ARGMAX ? 'm' : '?';
+    p.kernel = std::string("cj_gemv_q4k_") + pc + ec + (lpr == 16 ? "_b16" : "_b8") + (cols > 4096 ? "_w" : "");
+    p.rows_per_wg = (int)R;
+    p.grid = (uint32_t)((rows + R - 1) / R);
+    p.per_copy = p.grid;
+    p.lds = (uint32_t)(fixed + R * nb * 8);
+    return p;
+}
+
+GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, int epi) {
+    if (type == CJ_Q4_K) return plan_gemv_q4k(rows, cols, pro, epi);
     GemvPlan p;
     const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
                       : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
@@ -226,8 +258,7 @@ int32_t cj_init(int32_t device) {
         return fail(CJ_ERR_NOKERNEL, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
     }
     static const char *kernels[] = {
-        "cj_gemv_q4k_l64", "cj_gemv_q4k_l32", "cj_gemv_q4k_l16", "cj_gemv_q4k_l8",
-        "cj_gemv_q4k_l64_n2", "cj_gemv_q4k_l32_n2", "cj_gemv_q4k_l16_n2", "cj_gemv_q4k_l8_n2",
+
         "cj_gemv_q6k_l64", "cj_gemv_q6k_l32", "cj_gemv_q6k_l16", "cj_gemv_q6k_l8",
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
         "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
@@ -241,6 +272,14 @@ int32_t cj_init(int32_t device) {
         hipFunction_t f;
         if (hipModuleGetFunction(&f, g.module, k) == hipSuccess) g.fns[k] = f;
     }
+    // the Q4_K family: prologue {c, p, n} × epilogue {s, a, q, g, m} × width
+    for (const char *pro : {"c", "p", "n"})
+        for (const char *epi : {"s", "a", "q", "g", "m"})
+            for (const char *w : {"_b16", "_b8", "_b16_w"}) {
+                const std::string k = std::string("cj_gemv_q4k_") + pro + epi + w;
+                hipFunction_t f;
+                if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+            }
     CJ_HIP(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
     g.device = device;
     return CJ_OK;
@@ -418,10 +457,6 @@ int32_t cj_prepare_weight(int64_t dst, int64_t src, int32_t type, int64_t rows, 
     const int64_t srb = cols / be * bb;
     if (!in_buffer(dptr(src), rows * srb) || !in_buffer(dptr(dst), rows * prb))
         return fail(CJ_ERR_ARG, "cj_prepare_weight: buffers smaller than %lld rows", (long long)rows);
-    if (type == CJ_Q4_K) {
-        CJ_HIP(hipMemcpyAsync(dptr(dst), dptr(src), (size_t)(rows * srb), hipMemcpyDeviceToDevice, g.stream));
-        return CJ_OK;
-    }
     cj_prepare_args a{};
     a.dst = (uint8_t *)dptr(dst); a.src = (const uint8_t *)dptr(src); a.rows = rows; a.cols = cols;
     a.src_row_bytes = srb; a.dst_row_bytes = prb; a.type = type;
@@ -444,7 +479,7 @@ int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows,
     else { a.xp = (const uint8_t *)dptr(act); a.pro = CJ_PRO_PACKED; }
     a.y = (float *)dptr(y); a.y_off = y_off; a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type;
     a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = type == CJ_Q8_0; a.batch = 1;
-    return run_gemv(a, plan_gemv(type, rows, cols, 32));
+    return run_gemv(a, plan_gemv(type, rows, cols, 32, a.pro, a.epi));
 }
 
 int32_t cj_glu(int64_t out, int64_t packed, int64_t gb, int64_t ub, int64_t n, int32_t form, int32_t per32) {
@@ -562,7 +597,7 @@ int32_t cj_decode_splits(int32_t count, int32_t n_kv, int32_t workers) {
 
 int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, int32_t head_dim, int32_t splits, int32_t per32) {
     const int64_t n = (int64_t)n_q * head_dim, npad = (n + 255) / 256 * 256;
-    if (n <= 0 || splits <= 0 || splits > 64 || !in_buffer(dptr(part), (int64_t)n_q * 64 * (head_dim + 2) * 4) ||
+    if (n <= 0 || head_dim % 64 || splits <= 0 || splits > 64 || !in_buffer(dptr(part), (int64_t)n_q * 64 * (head_dim + 2) * 4) ||
         (out && !in_buffer(dptr(out), n * 4)) || (packed && !in_buffer(dptr(packed), npad / 256 * 320)) || (!out && !packed))
         return fail(CJ_ERR_ARG, "cj_attn_merge: buffers smaller than the shapes need");
     cj_merge_args a{};
