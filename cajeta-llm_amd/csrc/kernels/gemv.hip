@@ -62,7 +62,19 @@ DEV void q4k_fetch(Q4kBlock &x, const uint8_t *row, int nb, int b) {
     x.h = *(const uint4 *)(row + (int64_t)nb * 128 + (int64_t)b * 16);
 }
 
-DEV float2 q4k_block_terms(const Q4kBlock &x, const uint8_t *ax) {
+// The activation a lane needs for one block: the 256 int8 codes, the eight
+// 32-sums and the scale of one 320-byte pack block.
+struct Q4kAct { uint4 a[16]; int4 s0, s1; float xs; };
+
+DEV void q4k_act_load(Q4kAct &v, const uint8_t *ax) {
+#pragma unroll
+    for (int k = 0; k < 16; k++) v.a[k] = *(const uint4 *)(ax + 16 * k);
+    v.s0 = *(const int4 *)(ax + 256);
+    v.s1 = *(const int4 *)(ax + 272);
+    v.xs = *(const float *)(ax + 288);
+}
+
+DEV float2 q4k_block_terms(const Q4kBlock &x, const Q4kAct &v) {
     const uint32_t M = 0x0F0F0F0Fu;
     int dot[8];
 #pragma unroll
@@ -71,8 +83,8 @@ DEV float2 q4k_block_terms(const Q4kBlock &x, const uint8_t *ax) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint4 q = x.q[2 * g + h];
-            const uint4 al = *(const uint4 *)(ax + 64 * g + 16 * h);
-            const uint4 ah = *(const uint4 *)(ax + 64 * g + 32 + 16 * h);
+            const uint4 al = v.a[4 * g + h];        // elements 64g + 16h ..
+            const uint4 ah = v.a[4 * g + 2 + h];    // elements 64g + 32 + 16h ..
             lo = sdot4(q.x & M, al.x, lo); lo = sdot4(q.y & M, al.y, lo);
             lo = sdot4(q.z & M, al.z, lo); lo = sdot4(q.w & M, al.w, lo);
             hi = sdot4((q.x >> 4) & M, ah.x, hi); hi = sdot4((q.y >> 4) & M, ah.y, hi);
@@ -83,22 +95,22 @@ DEV float2 q4k_block_terms(const Q4kBlock &x, const uint8_t *ax) {
     }
     // scales[0..3] = A, [4..7] = B, [8..11] = C: sub-block j < 4 takes the
     // low 6 bits of A_j (scale) and B_j (min); j + 4 takes the nibbles of C_j
-    // with the top two bits of A_j (scale) and B_j (min) above them
+    // with the top two bits of A_j (scale) and B_j (min) above them. Every
+    // factor fits in 24 bits (|dot| ≤ 32·15·127, |32-sum| ≤ 32·127, scales
+    // and mins ≤ 63), so the 24-bit multiplies are exact.
     const uint32_t A = x.h.y, B = x.h.z, C = x.h.w;
-    const int4 s0 = *(const int4 *)(ax + 256), s1 = *(const int4 *)(ax + 272);
-    const int bs[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int bs[8] = {v.s0.x, v.s0.y, v.s0.z, v.s0.w, v.s1.x, v.s1.y, v.s1.z, v.s1.w};
     int sumi = 0, dmins = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t a8 = (A >> (8 * j)) & 255, b8 = (B >> (8 * j)) & 255, c8 = (C >> (8 * j)) & 255;
         const int sc_lo = (int)(a8 & 63), mn_lo = (int)(b8 & 63);
         const int sc_hi = (int)((c8 & 15) | ((a8 >> 2) & 48)), mn_hi = (int)((c8 >> 4) | ((b8 >> 2) & 48));
-        sumi += dot[j] * sc_lo + dot[j + 4] * sc_hi;
-        dmins += bs[j] * mn_lo + bs[j + 4] * mn_hi;
+        sumi += __mul24(dot[j], sc_lo) + __mul24(dot[j + 4], sc_hi);
+        dmins += __mul24(bs[j], mn_lo) + __mul24(bs[j + 4], mn_hi);
     }
-    const float xs = *(const float *)(ax + 288);
     const float d = h2f(x.h.x), dmin = h2f(x.h.x >> 16);
-    return make_float2(__fmul_rn(__fmul_rn(d, xs), (float)sumi), __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
+    return make_float2(__fmul_rn(__fmul_rn(d, v.xs), (float)sumi), __fmul_rn(__fmul_rn(dmin, v.xs), (float)dmins));
 }
 
 // Q6_K × q8_K. Unit (block b, 64 elements): half g, lane half hl; four
@@ -746,7 +758,7 @@ DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PR
 // pack run while the weight stream is in flight. The block terms go to LDS;
 // thread t then folds row t's in block order, acc = (acc + A_b) − B_b
 // (Quant.q4kMatVecIntoQ8), and runs the epilogue.
-template <int LPR, int PRO, int RND, int EPI>
+template <int LPR, int PRO, int RND, int EPI, int RING>
 DEV void gemv_q4k_body(const cj_gemv_args &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *red = (float *)smem;
@@ -770,9 +782,14 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
         const int b = blk_of(it);
         q4k_fetch(x, sl.W + (rr < a.rows ? rr : a.rows - 1) * a.row_bytes, nb, b < nb ? b : nb - 1);
     };
+    // a lane whose row has no more blocks than LPR keeps the one block it
+    // owns for the whole kernel: its activation is read from LDS once
+    const bool fixed = K == 1;
+    Q4kAct act;
     auto consume = [&](const Q4kBlock &x, int it) {
         const int rl = row_of(it), b = blk_of(it);
-        if (b < nb) *(float2 *)(terms + ((int64_t)rl * nb + b) * 2) = q4k_block_terms(x, sx + b * Q4K_LDS_STRIDE);
+        if (!fixed) q4k_act_load(act, sx + min(b, nb - 1) * Q4K_LDS_STRIDE);
+        if (b < nb) *(float2 *)(terms + ((int64_t)rl * nb + b) * 2) = q4k_block_terms(x, act);
     };
 
     // issue order: f32 prologues load before the weights; a copied pack
@@ -782,7 +799,7 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
     float4 px[PD::NX][4], pw[PD::NW][4];
     float pxs[PD::NS];
     u32x4 ppk[PD::NPK];
-    Q4kBlock ring[4];
+    Q4kBlock ring[RING];
     if constexpr (PRO != CJ_PRO_PACKED) {
         q4k_pro_load<PRO, RND>(a, sl, px, pw, pxs, ppk);
         __builtin_amdgcn_sched_barrier(0);
@@ -794,18 +811,19 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 1; j < 4; j++) fetch(ring[j], min(j, items - 1));
+    for (int j = 1; j < RING; j++) fetch(ring[j], min(j, items - 1));
     __builtin_amdgcn_sched_barrier(0);
     const EpiPre pre = epi_prefetch_t<EPI>(a, sl);
     __builtin_amdgcn_sched_barrier(0);
     q4k_pro_compute<PRO, RND>(a, px, pw, pxs, ppk, sx, red);
-    for (int it0 = 0; it0 < items; it0 += 4) {
+    if (fixed) q4k_act_load(act, sx + min(li, nb - 1) * Q4K_LDS_STRIDE);
+    for (int it0 = 0; it0 < items; it0 += RING) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < RING; j++) {
             const int it = it0 + j;
             if (it < items) {
                 consume(ring[j], it);
-                fetch(ring[j], min(it + 4, items - 1));
+                if (it + RING < items) fetch(ring[j], it + RING);
             }
         }
     }
@@ -852,8 +870,11 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
 // epilogue s (store), a (accumulate), q (q|k|v RoPE + K/V), g (SiLU·up) or
 // m (argmax); activations up to 4096 columns (_w: up to 16384, no norm). The
 // prologue and epilogue are compile-time so no load waits on a branch.
+#ifndef Q4K_RING
+#define Q4K_RING 2   // weight blocks in flight per lane (deeper rings delay the first block)
+#endif
 #define Q4K_KERNEL(NAME, LPR, PRO, RND, EPI) \
-    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) { gemv_q4k_body<LPR, PRO, RND, EPI>(a); }
+    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) { gemv_q4k_body<LPR, PRO, RND, EPI, Q4K_RING>(a); }
 #define Q4K_EPIS(P, LPR, PRO)                                                    \
     Q4K_KERNEL(cj_gemv_q4k_##P##s_b##LPR, LPR, PRO, 1, CJ_EPI_STORE)             \
     Q4K_KERNEL(cj_gemv_q4k_##P##a_b##LPR, LPR, PRO, 1, CJ_EPI_ACCUM)             \

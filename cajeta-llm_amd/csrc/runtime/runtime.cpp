@@ -174,7 +174,10 @@ GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
     const int64_t nb = cols / 256;
     const int lpr = nb >= 16 ? 16 : 8;
     const int64_t pass = 4 * (64 / lpr);
-    int64_t R = rows / std::max(1, g.cus) / pass * pass;
+    // the RMSNorm prologue runs once a workgroup: round up (fewer, longer
+    // workgroups); otherwise round down (every CU busy)
+    const int64_t per_cu = rows / std::max(1, g.cus);
+    int64_t R = pro == CJ_PRO_NORM_PACK ? (per_cu + pass - 1) / pass * pass : per_cu / pass * pass;
     const int64_t fixed = 3072 + nb * 336;
     const int64_t rmax = std::min<int64_t>((65536 - fixed) / (nb * 8), 256) / pass * pass;
     R = std::max<int64_t>(pass, std::min(R, rmax));
