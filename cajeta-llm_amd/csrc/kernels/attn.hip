@@ -143,33 +143,35 @@ DEV void split_body(const cj_attn_args &a) {
 #pragma unroll 1
             for (int hh = 0; hh < HW; hh++) {
                 // running max before (exc) and after (inc) each position
-                float x = live ? s[hh] : -3.0e38f;
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const float y = __shfl_up(x, off);
-                    if (lane >= off) x = fmaxf(x, y);
-                }
-                const float inc = fmaxf(m[hh], x);
-                float exc = __shfl_up(inc, 1);
-                if (lane == 0) exc = m[hh];
+                const float inc = fmaxf(m[hh], wave_prefix_max(live ? s[hh] : -3.0e38f));
+                const float exc = wave_shr1(inc, m[hh]);
                 const bool up = live && s[hh] > exc;
                 const float cf = up ? cj_expf(exc - s[hh]) : 1.0f;
                 const float pw = live ? cj_expf(s[hh] - inc) : 0.0f;
                 const uint64_t ups = __ballot(up);
                 m[hh] = lane_f(inc, n - 1);
+                // the lane's V pair of every position of the tile first (all
+                // reads in flight at once), then the recurrence in position
+                // order with each position's weight (and rescale, where the
+                // maximum rose) read from its lane
+                uint32_t vv[TP];
+#pragma unroll
+                for (int p = 0; p < TP; p++) vv[p] = *(const uint32_t *)&vs[p][2 * lane];
                 float x0 = acc0[hh], x1 = acc1[hh], ls = l[hh];
-                for (int p = 0; p < n; p++) {
-                    const float w = lane_f(pw, p);
-                    const uint32_t vv = *(const uint32_t *)&vs[p][2 * lane];
-                    if ((ups >> p) & 1) {
-                        const float c = lane_f(cf, p);
-                        x0 = __fmul_rn(x0, c);
-                        x1 = __fmul_rn(x1, c);
-                        ls = __fmul_rn(ls, c);
+#pragma unroll
+                for (int p = 0; p < TP; p++) {
+                    if (p < n) {
+                        const float w = lane_f(pw, p);
+                        if ((ups >> p) & 1) {
+                            const float c = lane_f(cf, p);
+                            x0 = __fmul_rn(x0, c);
+                            x1 = __fmul_rn(x1, c);
+                            ls = __fmul_rn(ls, c);
+                        }
+                        ls = __fadd_rn(ls, w);
+                        x0 = __fadd_rn(x0, __fmul_rn(h2f(vv[p]), w));
+                        x1 = __fadd_rn(x1, __fmul_rn(h2f(vv[p] >> 16), w));
                     }
-                    ls = __fadd_rn(ls, w);
-                    x0 = __fadd_rn(x0, __fmul_rn(h2f(vv), w));
-                    x1 = __fadd_rn(x1, __fmul_rn(h2f(vv >> 16), w));
                 }
                 acc0[hh] = x0; acc1[hh] = x1; l[hh] = ls;
             }
@@ -326,6 +328,7 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_a
 // pack.
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
     __shared__ float bmax[8];
+    __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
     const int t = threadIdx.x, lane = t & 63;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
@@ -350,13 +353,32 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     const bool on = in && ml.y > 0.0f;
     const float wt = on ? cj_expf(mv - gm) : 0.0f;
     const uint64_t ons = __ballot(on);
+    // split weights and sums through the wave's LDS row, back as broadcast
+    // 16-byte reads, 16 splits a chunk; selects (not branches): a split that
+    // takes no part leaves the sums as they were
+    const int wave = t >> 6;
+    sw[wave][lane] = wt;
+    sl[wave][lane] = ml.y;
+    __builtin_amdgcn_wave_barrier();
     float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
-        if ((ons >> s2) & 1) {
-            const float w = lane_f(wt, s2), lsv = lane_f(ml.y, s2);
-            gl[s2 & 3] = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lsv));
-            ac[s2 & 3] = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
+    for (int s0 = 0; s0 < ATTN_MAX_SPLITS; s0 += 16) {
+        float w[16], lv[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 w4 = *(const float4 *)&sw[wave][s0 + 4 * k];
+            const float4 l4 = *(const float4 *)&sl[wave][s0 + 4 * k];
+            w[4 * k] = w4.x; w[4 * k + 1] = w4.y; w[4 * k + 2] = w4.z; w[4 * k + 3] = w4.w;
+            lv[4 * k] = l4.x; lv[4 * k + 1] = l4.y; lv[4 * k + 2] = l4.z; lv[4 * k + 3] = l4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int s2 = s0 + j;
+            const bool use = (ons >> s2) & 1;
+            const float g2 = __fadd_rn(gl[s2 & 3], __fmul_rn(w[j], lv[j]));
+            const float a2 = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w[j]));
+            gl[s2 & 3] = use ? g2 : gl[s2 & 3];
+            ac[s2 & 3] = use ? a2 : ac[s2 & 3];
         }
     }
     const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);

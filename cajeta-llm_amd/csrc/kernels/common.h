@@ -169,6 +169,33 @@ DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
 // same on every lane of the wave).
 DEV float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 
+// max(v, the value DPP control CTRL brings from another lane); lanes the
+// control gives no source keep `v` (the source falls back to `v` itself).
+template <int CTRL, int ROWS>
+DEV float dpp_max(float v) {
+    const int s = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xF, false);
+    return fmaxf(v, __int_as_float(s));
+}
+
+// Inclusive prefix maximum over the 64 lanes by DPP: row_shr 1, 2, 4, 8
+// within each row of 16, then row_bcast 15 and 31 across rows (max is exact
+// in any order, so this equals the running maximum).
+DEV float wave_prefix_max(float v) {
+    v = dpp_max<0x111, 0xF>(v);   // row_shr:1
+    v = dpp_max<0x112, 0xF>(v);   // row_shr:2
+    v = dpp_max<0x114, 0xF>(v);   // row_shr:4
+    v = dpp_max<0x118, 0xF>(v);   // row_shr:8
+    v = dpp_max<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v = dpp_max<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// The value of lane − 1 (wave_shr:1); lane 0 gets `first`.
+DEV float wave_shr1(float v, float first) {
+    const int s = __builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(v), 0x138, 0xF, 0xF, false);
+    return __int_as_float(s);
+}
+
 // ---------------------------------------------------------------------------
 // Activation staging into LDS: the 320-byte block layout of the reference's
 // Quant.q8kPackPad / q8kPack32Pad ([0,256) q, [256,288) 8 int32 sums of 32,
