@@ -384,7 +384,7 @@ int Engine::enqueue_step(int s) {
         Layer &L = layers[l];
         // Q4_K projections fold the RMSNorm + pack into their prologue (the
         // weight stream is in flight while it runs); others read a pack
-        const bool qkv_norm = L.qkv.type == CJ_Q4_K && hidden <= 4096 && !getenv("CJ_TMP_NOFUSE");
+        const bool qkv_norm = L.qkv.type == CJ_Q4_K && hidden <= 4096;
         if (!qkv_norm && want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false))) return rc;
         if (want(K_QKV, l)) {   // 1. q|k|v over the normed residual, RoPE + K/V append epilogue
             cj_gemv_args a{};
@@ -429,7 +429,7 @@ int Engine::enqueue_step(int s) {
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
-        const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096 && !getenv("CJ_TMP_NOFUSE");
+        const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096;
         if (!gu_norm && want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
             const int ct = n_experts ? L.gu_exps.type : L.gu.type;
             if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0))) return rc;

@@ -181,7 +181,6 @@ GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
     const int64_t fixed = 3072 + nb * 336;
     const int64_t rmax = std::min<int64_t>((65536 - fixed) / (nb * 8), 256) / pass * pass;
     R = std::max<int64_t>(pass, std::min(R, rmax));
-    if (const char *e = getenv("CJ_TMP_Q4K_R")) R = std::max<int64_t>(pass, std::min<int64_t>(atoi(e) / pass * pass, rmax));
     const char pc = pro == CJ_PRO_PACKED ? 'c' : pro == CJ_PRO_PACK ? 'p' : pro == CJ_PRO_NORM_PACK ? 'n' : '?';
     const char ec = epi == CJ_EPI_STORE ? 's' : epi == CJ_EPI_ACCUM ? 'a' : epi == CJ_EPI_QKV_ROPE ? 'q'
                   : epi == CJ_EPI_GLU ? 'g' : epi == CJ_EPI_ARGMAX ? 'm' : '?';
