@@ -3,3 +3,4 @@
 #include "gemv.hip"
 #include "prim.hip"
 #include "attn.hip"
+#include "gemm.hip"

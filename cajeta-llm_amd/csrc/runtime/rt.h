@@ -23,10 +23,15 @@ bool in_buffer(const void *p, int64_t bytes);
 void *dptr(int64_t h);
 
 // Launch `name` from kernels.hsaco with one argument block.
-int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size);
+int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size,
+               uint32_t grid_y = 1);
 template <class A>
 int launch(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const A &a) {
     return launch_raw(name, grid, block, lds, &a, sizeof(A));
+}
+template <class A>
+int launch2(const char *name, uint32_t grid_x, uint32_t grid_y, uint32_t block, uint32_t lds, const A &a) {
+    return launch_raw(name, grid_x, block, lds, &a, sizeof(A), grid_y);
 }
 bool has_kernel(const char *name);
 
@@ -45,6 +50,11 @@ bool gemv_supported(int type, int64_t cols);
 // workgroup covers, at most 256; 0 = one pass), grid and LDS of a GEMV.
 GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, int epi);
 int run_gemv(const cj_gemv_args &a, const GemvPlan &p);
+// The batched mat-mat on the int8 matrix cores (Q8_0, Q4_K): a.batch columns
+// of packed activations a.xp (a.xp_stride bytes apart) into a.y (a.y_stride
+// floats apart); STORE or ACCUM epilogue.
+bool gemm_supported(int type);
+int run_gemm(const cj_gemv_args &a);
 
 // Device memory owned by the runtime itself (not through the handle table's
 // public free): allocation + registration for the extent checks.

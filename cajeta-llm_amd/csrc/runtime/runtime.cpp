@@ -63,6 +63,9 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"gatherRowsF32Kernel", "cj_embed"},
         {"routerTopKKernel", "cj_moe_route"},
         {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_cg_b16"},
+        {"q4kQ8WaveMatVecColsKernel", "cj_gemm_q4k"},
+        {"q80Q8X8RowsKernel", "cj_gemm_q80"},
+        {"q4kQ8X8RowsKernel", "cj_gemm_q4k"},
         {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_cs_b16"},
     };
     return m;
@@ -124,15 +127,16 @@ void dev_free(void *p) {
 
 bool has_kernel(const char *name) { return g.fns.count(name) != 0; }
 
-int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size) {
+int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size,
+               uint32_t grid_y) {
     if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
     auto it = g.fns.find(name);
     if (it == g.fns.end()) return fail(CJ_ERR_NOKERNEL, "kernel %s is not in kernels.hsaco", name);
-    if (grid == 0) return CJ_OK;
+    if (grid == 0 || grid_y == 0) return CJ_OK;
     (void)size;
     // every kernel takes one argument, the struct: kernelParams[0] points at it
     void *params[] = {const_cast<void *>(args)};
-    hipError_t e = hipModuleLaunchKernel(it->second, grid, 1, 1, block, 1, 1, lds, g.stream, params, nullptr);
+    hipError_t e = hipModuleLaunchKernel(it->second, grid, grid_y, 1, block, 1, 1, lds, g.stream, params, nullptr);
     if (e != hipSuccess) return fail(CJ_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e));
     g_last_launch = name;
     g_launches++;
@@ -229,6 +233,18 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
     return p;
 }
 
+bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K; }
+
+// One wave a 16-row × 16-column tile; up to 4 waves a workgroup side by side
+// over the columns.
+int run_gemm(const cj_gemv_args &a) {
+    if (!gemm_supported(a.type)) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
+    if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
+    const int waves = (int)std::min<int64_t>(4, (a.batch + 15) / 16);
+    const uint32_t gx = (uint32_t)((a.rows + 15) / 16), gy = (uint32_t)((a.batch + 16 * waves - 1) / (16 * waves));
+    return launch2(a.type == CJ_Q8_0 ? "cj_gemm_q80" : "cj_gemm_q4k", gx, gy, 64 * waves, 0, a);
+}
+
 int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
     cj_gemv_args a = a0;
     a.rows_per_wg = p.rows_per_wg;
@@ -268,7 +284,7 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
-        "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
+        "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_gemm_q80", "cj_gemm_q4k",
     };
     for (const char *k : kernels) {
         hipFunction_t f;
@@ -482,6 +498,25 @@ int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows,
     a.y = (float *)dptr(y); a.y_off = y_off; a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type;
     a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = type == CJ_Q8_0; a.batch = 1;
     return run_gemv(a, plan_gemv(type, rows, cols, 32, a.pro, a.epi));
+}
+
+int32_t cj_matmul(int32_t type, int64_t y, int64_t w, int64_t xp, int64_t rows, int64_t cols, int32_t ncols,
+                  int64_t xp_stride, int64_t y_stride, int64_t y_off, int32_t accum) {
+    const int64_t prb = prepared_row_bytes(type, cols);
+    if (!gemm_supported(type) || prb <= 0 || rows <= 0 || ncols <= 0)
+        return fail(CJ_ERR_ARG, "cj_matmul: type %d with %lld columns x %d is not served", type, (long long)cols, ncols);
+    const int64_t pack_bytes = (cols + 255) / 256 * 320;
+    if (xp_stride < pack_bytes || y_stride < y_off + rows || y_off < 0)
+        return fail(CJ_ERR_ARG, "cj_matmul: strides %lld/%lld smaller than one column", (long long)xp_stride, (long long)y_stride);
+    if (!in_buffer(dptr(w), rows * prb)) return fail(CJ_ERR_ARG, "cj_matmul: weight smaller than %lld prepared rows", (long long)rows);
+    if (!in_buffer(dptr(xp), (ncols - 1) * xp_stride + pack_bytes)) return fail(CJ_ERR_ARG, "cj_matmul: activation packs too small");
+    if (!in_buffer(dptr(y), ((ncols - 1) * y_stride + y_off + rows) * 4)) return fail(CJ_ERR_ARG, "cj_matmul: output too small");
+    cj_gemv_args a{};
+    a.w = (const uint8_t *)dptr(w); a.xp = (const uint8_t *)dptr(xp); a.y = (float *)dptr(y);
+    a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type; a.batch = ncols;
+    a.xp_stride = xp_stride; a.y_stride = y_stride; a.y_off = y_off;
+    a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.pro = CJ_PRO_PACKED;
+    return run_gemm(a);
 }
 
 int32_t cj_glu(int64_t out, int64_t packed, int64_t gb, int64_t ub, int64_t n, int32_t form, int32_t per32) {

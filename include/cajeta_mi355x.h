@@ -118,6 +118,18 @@ int32_t cj_prepare_weight(int64_t dst, int64_t src, int32_t type, int64_t rows, 
 int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows, int64_t cols,
                   int64_t y_off, int32_t accum);
 
+/* Y[c][y_off + r] (+)= Σ_k W[r][k]·x_c[k] for ncols activation columns at once,
+ * on the int8 matrix cores, each column bit-for-bit what cj_matvec gives it.
+ * `xp` holds the columns' packs (per-256 for Q4_K, per-32 for Q8_0)
+ * xp_stride bytes apart; y holds the outputs y_stride floats apart. Types
+ * Q8_0 and Q4_K. Replaces the many-column kernels the reference routes
+ * batched decode and prefill rows through: Linear.matmulBatchKeep
+ * (model/Linear.cajeta:3576) over q4kQ8WaveMatVecColsKernel
+ * (io/QuantKernel.cajeta:33646), q4kQ8X8RowsKernel (:1479) and
+ * q80Q8X8RowsKernel (:10236). */
+int32_t cj_matmul(int32_t type, int64_t y, int64_t w, int64_t xp, int64_t rows, int64_t cols, int32_t ncols,
+                  int64_t xp_stride, int64_t y_stride, int64_t y_off, int32_t accum);
+
 /* out = act(g)·u (act 0: SiLU exp form, 1: the CPU backend's rational-tanh
  * form), plus its pack when packed != 0. Replaces Prim.gluPackDevice
  * (model/Prim.cajeta:1775-1785), gluPack32Device (:1789-1800), gluDevice. */

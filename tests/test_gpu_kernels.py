@@ -328,3 +328,53 @@ def test_kernel_registry_answers_reference_names(gpu):
     assert not gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
     gpu.KernelCap.clearOverrides()
     assert gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
+
+
+@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12)])
+@pytest.mark.parametrize("rows,cols,ncols", [(300, 512, 1), (1024, 4096, 4), (64, 1408, 8), (272, 4096, 17),
+                                             (96, 14336, 16), (160, 2048, 70)])
+def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
+    """The batched int8 matrix-core product: every output column is the
+    one-column product of its activation pack, bit for bit (integer sub-block
+    dots are exact; the float fold runs in the reference's block order)."""
+    if ty == O.Q4_K and cols % 256:
+        pytest.skip("Q4_K rows are whole 256-element blocks")
+    say("matmul", name, rows, cols, ncols)
+    rng = np.random.default_rng(rows * 7 + cols + ncols + ty)
+    be, bb = O.BLOCK[ty]
+    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(ty, cols)
+    src, w = gpu.Buffer.of(raw), gpu.Buffer(prb * rows)
+    gpu.native.check(lib.cj_prepare_weight(w.h, src.h, ty, rows, cols), "prepare")
+    npad = (cols + 255) // 256 * 256
+    stride = npad // 256 * 320 + 64                     # a gap between columns the kernel must skip
+    packs = np.zeros((ncols, stride), np.uint8)
+    for c in range(ncols):
+        x = (rng.standard_normal(cols) * rng.uniform(0.1, 4)).astype(np.float32)
+        packs[c, :npad // 256 * 320] = O.q8k_pack(x, per32=(ty == O.Q8_0), npad=npad)
+    ystride, yoff = rows + 5, 3
+    y0 = rng.standard_normal((ncols, ystride)).astype(np.float32)
+    xb = gpu.Buffer.of(packs.reshape(-1))
+    for accum in (0, 1):
+        yb = gpu.Buffer.of(y0.reshape(-1))
+        gpu.native.check(lib.cj_matmul(ty, yb.h, w.h, xb.h, rows, cols, ncols, stride, ystride, yoff, accum), "matmul")
+        got = yb.download(np.float32, ncols * ystride).reshape(ncols, ystride)
+        for c in range(ncols):
+            ref = O.matvec_packed(ty, raw, rows, cols, packs[c, :npad // 256 * 320])
+            if accum:
+                ref = (y0[c, yoff:yoff + rows] + ref).astype(np.float32)
+            assert np.array_equal(got[c, yoff:yoff + rows].view(np.uint32), ref.view(np.uint32)), \
+                "%s column %d accum %d: %d rows differ" % (name, c, accum, int((got[c, yoff:yoff + rows] != ref).sum()))
+            # outside the column's rows nothing is written
+            assert np.array_equal(got[c, :yoff], y0[c, :yoff]) and np.array_equal(got[c, yoff + rows:], y0[c, yoff + rows:])
+        yb.free()
+
+
+def test_matmul_refuses_short_buffers(gpu, O):
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(12, 256)
+    w, xp, y = gpu.Buffer(prb * 64), gpu.Buffer(320 * 3), gpu.Buffer(64 * 4 * 4)
+    assert lib.cj_matmul(12, y.h, w.h, xp.h, 64, 256, 4, 320, 64, 0, 0) == -1
+    assert "activation" in gpu.native.last_error()
+    assert lib.cj_matmul(6, y.h, w.h, xp.h, 64, 256, 1, 320, 64, 0, 0) == -1
