@@ -23,7 +23,7 @@ KERNEL_FLAGS = ["--offload-arch=" + ARCH, "-O3", "--genco", "-ffp-contract=off",
 HOST_FLAGS = ["--offload-arch=" + ARCH, "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wno-unused-function",
               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-pthread"]
 
-KERNEL_SOURCES = ["kernels/kernels.hip", "kernels/gemv.hip", "kernels/prim.hip", "kernels/attn.hip", "kernels/gemm.hip",
+KERNEL_SOURCES = ["kernels/kernels.hip", "kernels/gemv.hip", "kernels/prim.hip", "kernels/attn.hip", "kernels/gemm.hip", "kernels/rows.hip",
                   "kernels/common.h", "kernels/args.h"]
 RUNTIME_SOURCES = ["runtime/runtime.cpp", "runtime/engine.cpp", "runtime/gguf.cpp", "runtime/synth.cpp"]
 

@@ -139,14 +139,49 @@ typedef struct {
     int32_t pg_n;            // pages the sequence owns from pg_base (bounds the table prefetch)
     int32_t per32;           // split-K with an output: pack `packed` at one scale per 32
     uint8_t *packed;         // split-K with an output: the q8 pack of the merged output (may be null)
+    // many-row forms (rowtab non-null): row r is sequence slot rowtab[2r] at
+    // position states[slot].pos + rowtab[2r+1]; its pages from slot·pg_n
+    const int32_t *rowtab;
+    const cj_step_state *states;
+    int32_t nrows;           // rows in the batch (the split rule divides the workers over rows·n_kv)
+    int32_t spl;             // split slots a row (grid: rows · n_kv · spl)
+    int64_t q_stride;        // floats between rows of q (and of out)
+    int64_t part_stride;     // floats between rows of the partials
 } cj_attn_args;
 
 typedef struct {
     float *out; uint8_t *packed; const float *part;
     const cj_step_state *state;  // non-null: splits follow the device position
     int32_t n_q, head_dim, splits, per32;
-    int32_t n_kv, workers, window, pad;
+    int32_t n_kv, workers, window, nrows;
+    // many-row form (rowtab non-null): as cj_attn_args
+    const int32_t *rowtab;
+    const cj_step_state *states;
+    int64_t part_stride, out_stride, pack_stride;
 } cj_merge_args;
+
+// The many-row step kernels (batched decode: a row a sequence; prefill: a
+// row a position of one sequence). Row r is slot rowtab[2r] at position
+// states[slot].pos + rowtab[2r+1].
+typedef struct {
+    const int32_t *rowtab;
+    cj_step_state *states;
+    int32_t *tokens, *preds;    // per-slot histories, hist ints apart
+    int64_t hist;
+    // embedding
+    const uint8_t *table; int64_t row_bytes; int32_t type; int32_t nrows;
+    // row buffers
+    const float *in; float *out; uint8_t *packed;
+    int64_t in_stride, out_stride, pack_stride;
+    // q|k|v: RoPE, q rows out, fp16 K/V append
+    float *q_out; uint16_t *kc, *vc; const int32_t *pgtab; const float *rope_cs;
+    int32_t pg_n, n_q, n_kv, head_dim;
+    // widths: embedding / GLU width n (padded npad); GLU form and pack
+    int64_t n, npad;
+    int32_t form, per32;
+    // argmax partials: [rows][nchunks] of 1024-wide chunks
+    float *pv; int32_t *pi; int32_t nchunks; int32_t pad;
+} cj_rows_args;
 
 typedef struct {
     // the step's greedy pick from per-workgroup (value, index) partials

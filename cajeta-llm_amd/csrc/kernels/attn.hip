@@ -63,7 +63,7 @@ DEV void attn_window(const cj_attn_args &a, int &count, int &from) {
 //            position order, each position's c and w read from its lane.
 // The last workgroup of a kv head to finish merges the head's splits and
 // writes the merged output and its q8 pack.
-template <int G>
+template <int G, bool ROWS>
 DEV void split_body(const cj_attn_args &a) {
     constexpr int HD = 128, TP = 64, KS = HD + 8, PGMAX = 256, HW = G / 4;
     __shared__ __align__(16) uint16_t ks[TP][KS];
@@ -73,13 +73,33 @@ DEV void split_body(const cj_attn_args &a) {
     __shared__ float bmax[8];
     __shared__ int ticket;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
+    // the workgroup's (row,) kv head and split slot; the row's q, pages and
+    // partials (many-row form: the row's sequence and position from the row
+    // table, the split rule over all rows' kv heads)
+    int kvh, sp, count, from, pg_base = a.pg_base, rows_kv = a.n_kv;
+    const float *qrow = a.q;
+    float *part = a.part;
+    if (ROWS) {
+        const int per = a.n_kv * a.spl, r = blockIdx.x / per, rem = blockIdx.x % per;
+        kvh = rem / a.spl;
+        sp = rem % a.spl;
+        const int slot = a.rowtab[2 * r];
+        count = a.states[slot].pos + a.rowtab[2 * r + 1] + 1;
+        from = 0;
+        if (a.window > 0 && count > a.window) { from = count - a.window; count = a.window; }
+        pg_base = slot * a.pg_n;
+        rows_kv = a.nrows * a.n_kv;
+        qrow = a.q + (int64_t)r * a.q_stride;
+        part = a.part + (int64_t)r * a.part_stride;
+    } else {
+        kvh = blockIdx.x / ATTN_MAX_SPLITS;
+        sp = blockIdx.x % ATTN_MAX_SPLITS;
+        attn_window(a, count, from);
+    }
     // q, the page table and the step state load together
-    for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(a.q + (int64_t)kvh * G * HD + e);
-    if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[a.pg_base + t] : 0;
-    int count, from;
-    attn_window(a, count, from);
-    const int splits = decode_splits(count, a.n_kv, a.workers);
+    for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(qrow + (int64_t)kvh * G * HD + e);
+    if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[pg_base + t] : 0;
+    const int splits = decode_splits(count, rows_kv, a.workers);
     if (sp < splits) {
         const int chunk = (count + splits - 1) / splits;
         int t0 = sp * chunk, t1 = t0 + chunk;
@@ -88,31 +108,36 @@ DEV void split_body(const cj_attn_args &a) {
         float m[HW], l[HW], acc0[HW], acc1[HW];
 #pragma unroll
         for (int hh = 0; hh < HW; hh++) { m[hh] = -3.0e38f; l[hh] = 0.0f; acc0[hh] = 0.0f; acc1[hh] = 0.0f; }
+        // a tile's K and V rows as 16-byte chunks (rows past the split's end
+        // repeat its last row); the next tile's are requested before this
+        // tile's arithmetic, so a long split streams without a gap
+        u32x4 kr[4], vr[4];   // native vectors: stay in registers across the loop
+#define SPLIT_FETCH(TB)                                                                                   \
+    do {                                                                                                  \
+        const int n_ = t1 - (TB) < TP ? t1 - (TB) : TP;                                                   \
+        _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                  \
+            const int c = t + 256 * i, j = c & 15;                                                        \
+            const int p = (c >> 4) < n_ ? (c >> 4) : n_ - 1;                                              \
+            const int pos = from + (TB) + p, pi = pos >> 6;                                               \
+            const int page = pi < PGMAX ? pgs[pi] : a.pgtab[pg_base + pi];                                \
+            const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;         \
+            kr[i] = *(const u32x4 *)(a.kc + base);                                                        \
+            vr[i] = *(const u32x4 *)(a.vc + base);                                                        \
+        }                                                                                                 \
+    } while (0)
+        __syncthreads();   // q and pages visible
+        if (t0 < t1) SPLIT_FETCH(t0);
         for (int tb = t0; tb < t1; tb += TP) {
             const int n = t1 - tb < TP ? t1 - tb : TP;
-            __syncthreads();   // the previous tile's reads are done (first tile: q and pages visible)
-            // stage the tile's K and V rows: 16-byte chunks, every load issued
-            // before the first store (rows past the tile repeat its last row)
-            {
-                uint4 kr[4], vr[4];
+            __syncthreads();   // the previous tile's reads are done
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int c = t + 256 * i, j = c & 15;
-                    const int p = (c >> 4) < n ? (c >> 4) : n - 1;
-                    const int pos = from + tb + p, pi = pos >> 6;
-                    const int page = pi < PGMAX ? pgs[pi] : a.pgtab[a.pg_base + pi];
-                    const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;
-                    kr[i] = *(const uint4 *)(a.kc + base);
-                    vr[i] = *(const uint4 *)(a.vc + base);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int c = t + 256 * i;
-                    *(uint4 *)&ks[c >> 4][8 * (c & 15)] = kr[i];
-                    *(uint4 *)&vs[c >> 4][8 * (c & 15)] = vr[i];
-                }
+            for (int i = 0; i < 4; i++) {
+                const int c = t + 256 * i;
+                *(u32x4 *)&ks[c >> 4][8 * (c & 15)] = kr[i];
+                *(u32x4 *)&vs[c >> 4][8 * (c & 15)] = vr[i];
             }
             __syncthreads();
+            if (tb + TP < t1) SPLIT_FETCH(tb + TP);
             // scores of position `lane` for this wave's heads, one head at a time
             float s[HW];
 #pragma unroll
@@ -178,12 +203,12 @@ DEV void split_body(const cj_attn_args &a) {
         }
 #pragma unroll
         for (int hh = 0; hh < HW; hh++) {
-            float *pb = a.part + ((int64_t)(kvh * G + wave + 4 * hh) * ATTN_MAX_SPLITS + sp) * (HD + 2);
+            float *pb = part + ((int64_t)(kvh * G + wave + 4 * hh) * ATTN_MAX_SPLITS + sp) * (HD + 2);
             *(float2 *)(pb + 2 * lane) = make_float2(acc0[hh], acc1[hh]);
             if (lane == 0) *(float2 *)(pb + HD) = make_float2(m[hh], l[hh]);
         }
     }
-    if (!a.out && !a.packed) return;
+    if (ROWS || (!a.out && !a.packed)) return;
 
     // the last workgroup of this kv head merges its splits
     __threadfence();
@@ -238,8 +263,9 @@ DEV void split_body(const cj_attn_args &a) {
     if (t == 0) a.counters[kvh] = 0;
 }
 
-#define SPLIT_KERNEL(G) \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G>(a); }
+#define SPLIT_KERNEL(G)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G, false>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_rows_h128_g##G(cj_attn_args a) { split_body<G, true>(a); }
 SPLIT_KERNEL(4)
 SPLIT_KERNEL(8)
 
@@ -330,22 +356,37 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     __shared__ float bmax[8];
     __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
     const int t = threadIdx.x, lane = t & 63;
-    const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
+    // many-row form: the row and its block (a row is whole blocks of 256)
+    int64_t blk = blockIdx.x;
+    const float *part = a.part;
+    float *out = a.out;
+    uint8_t *packed = a.packed;
+    int count = 0;
+    if (a.rowtab) {
+        const int64_t per = n / 256, r = blockIdx.x / per;
+        blk = blockIdx.x % per;
+        part += r * a.part_stride;
+        if (out) out += r * a.out_stride;
+        if (packed) packed += r * a.pack_stride;
+        count = a.states[a.rowtab[2 * r]].pos + a.rowtab[2 * r + 1] + 1;
+    } else if (a.state) {
+        count = a.state->pos + 1;
+    }
+    const int64_t e = blk * 256 + t;
     // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
-    const int64_t ew = min((int64_t)blockIdx.x * 256 + (t & ~63), n - 1);
+    const int64_t ew = min(blk * 256 + (t & ~63), n - 1);
     const int h = (int)(ew / hd), d = (int)(min(e, n - 1) % hd);
-    const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
+    const float *pb0 = part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
     float pv[ATTN_MAX_SPLITS];
 #pragma unroll
     for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
     const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
     int splits = a.splits;
-    if (a.state) {
-        int count = a.state->pos + 1;
+    if (a.rowtab || a.state) {
         if (a.window > 0 && count > a.window) count = a.window;
-        splits = decode_splits(count, a.n_kv, a.workers);
+        splits = decode_splits(count, (a.rowtab ? a.nrows : 1) * a.n_kv, a.workers);
     }
     const bool in = lane < splits;
     const float mv = in ? ml.x : -3.0e38f;
@@ -384,8 +425,8 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
     const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
     const float x = e < n ? __fmul_rn(tacc, __fdiv_rn(1.0f, gt)) : 0.0f;
-    if (a.out && e < n) a.out[e] = x;
-    if (a.packed) pack256(x, a.per32, a.packed + (int64_t)blockIdx.x * 320, bmax);
+    if (out && e < n) out[e] = x;
+    if (packed) pack256(x, a.per32, packed + blk * 320, bmax);
 }
 
 // QK-norm (optional) + split-half RoPE + fp16 K/V append, one workgroup of
@@ -427,3 +468,141 @@ extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
         for (int e = t; e < hd; e += 64) a.vc[vi + e] = f2h(a.v[(int64_t)kh * hd + e]);
     }
 }
+
+// ------------------------------------------------------------ prefill form
+
+// Prefill attention over rows of one sequence at head size 128 — the CPU
+// backend's prefill attend (AttnKernel.attnPrefillCpuGqaKernel,
+// model/AttnKernel.cajeta:3916-4004): one pass per (row, query head) over
+// its positions [t0, count) in order, an online softmax with q scaled first
+// (q·scale rounded, then the dot), the running max from -1e30, a rescale
+// only where the maximum rises, out = acc·(1/l).
+//
+// Sixteen lanes own one (row, head): lane j holds q[16v+j]·scale and the
+// accumulators of dims 16v+j (v < 8) and forms the partial
+// Σ_v q[16v+j]·k[16v+j] in v order; the 16 partials fold by the fixed
+// pairwise tree in four DPP steps within the 16-lane row (quad xor 1, quad
+// xor 2, half-row mirror, row mirror: pairs, quads, halves, the whole — fp
+// addition commutes, so all 16 lanes end with the tree's bits). A workgroup
+// of 4 waves takes RB rows of one kv head, 16·NS (row, head) pairs (NS a
+// wave; a wave's four pairs share a row for G ≥ 4); each tile of TK
+// positions is staged once for all of them, as f32 in lane order
+// ([t][j][v], so a lane's 8 values are two 16-byte reads that all of a
+// wave's pairs share). The heaviest row blocks are dispatched first.
+template <int CTRL>
+DEV float dpp_rowf(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false)); }
+
+template <int G>
+DEV void prefill_body(const cj_attn_args &a) {
+    constexpr int HD = 128, TK = 32, NS = G >= 8 ? G / 4 : 1, RB = 16 * NS / G;
+    __shared__ __align__(16) float kl[TK][16][8];
+    __shared__ __align__(16) float vl[TK][16][8];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, j = lane & 15, grp = lane >> 4;
+    const int nblk = (a.nrows + RB - 1) / RB;
+    const int kvh = (int)(blockIdx.x % a.n_kv), rb = nblk - 1 - (int)(blockIdx.x / a.n_kv);
+    const int slot = a.rowtab[0];
+    const int pg_base = slot * a.pg_n, base_pos = a.states[slot].pos;
+    // the workgroup's position range: the union of its rows' ranges
+    int lo = 0x7fffffff, hi = 0;
+    for (int i = 0; i < RB; i++) {
+        const int r = rb * RB + i;
+        if (r >= a.nrows) break;
+        const int count = base_pos + a.rowtab[2 * r + 1] + 1;
+        const int t0 = a.window > 0 && count > a.window ? count - a.window : 0;
+        lo = min(lo, t0);
+        hi = max(hi, count);
+    }
+    float qv[NS][8], acc[NS][8], m[NS], l[NS];
+    int c0[NS], c1[NS], row[NS], head[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int p = 16 * s + 4 * wave + grp;
+        row[s] = rb * RB + p / G;
+        head[s] = kvh * G + p % G;
+        const int rr = min(row[s], a.nrows - 1);
+        const int count = base_pos + a.rowtab[2 * rr + 1] + 1;
+        c0[s] = a.window > 0 && count > a.window ? count - a.window : 0;
+        c1[s] = row[s] < a.nrows ? count : c0[s];
+        const float *qr = a.q + (int64_t)rr * a.q_stride + (int64_t)head[s] * HD + j;
+#pragma unroll
+        for (int v = 0; v < 8; v++) {
+            qv[s][v] = __fmul_rn(qr[16 * v], a.scale);
+            acc[s][v] = 0.0f;
+        }
+        m[s] = -1.0e30f;
+        l[s] = 0.0f;
+    }
+    for (int tb = lo; tb < hi; tb += TK) {
+        const int nt = hi - tb < TK ? hi - tb : TK;
+        __syncthreads();   // the previous tile's reads are done
+        // stage: chunk c = 8 halves (dims 8m .. 8m+7) of key c/16; dim d goes
+        // to lane d & 15, slot d >> 4
+        uint4 kr[2], vr[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = t + 256 * i, kk = c >> 4, mp = c & 15;
+            const int pos = tb + (kk < nt ? kk : nt - 1);
+            const int page = a.pgtab[pg_base + (pos >> 6)];
+            const int64_t off = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * mp;
+            kr[i] = *(const uint4 *)(a.kc + off);
+            vr[i] = *(const uint4 *)(a.vc + off);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = t + 256 * i, kk = c >> 4, mp = c & 15;
+            const int j0 = (mp & 1) * 8, v0 = mp >> 1;
+            const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w}, vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kl[kk][j0 + e][v0] = h2f(kw[e >> 1] >> (16 * (e & 1)));
+                vl[kk][j0 + e][v0] = h2f(vw[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nt; tt++) {
+            const int tp = tb + tt;
+            const float4 ka = *(const float4 *)&kl[tt][j][0], kb = *(const float4 *)&kl[tt][j][4];
+            const float4 va = *(const float4 *)&vl[tt][j][0], vb = *(const float4 *)&vl[tt][j][4];
+            const float kf[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+            const float vf[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                if (tp >= c0[s] && tp < c1[s]) {
+                    float d = __fmul_rn(qv[s][0], kf[0]);
+#pragma unroll
+                    for (int v = 1; v < 8; v++) d = __fadd_rn(d, __fmul_rn(qv[s][v], kf[v]));
+                    d = __fadd_rn(d, dpp_rowf<0xB1>(d));    // quad xor 1: the pairs
+                    d = __fadd_rn(d, dpp_rowf<0x4E>(d));    // quad xor 2: the quads
+                    d = __fadd_rn(d, dpp_rowf<0x141>(d));   // half-row mirror: the halves of 8
+                    d = __fadd_rn(d, dpp_rowf<0x140>(d));   // row mirror: the 16
+                    if (d > m[s]) {
+                        const float c = cj_expf(m[s] - d);
+#pragma unroll
+                        for (int v = 0; v < 8; v++) acc[s][v] = __fmul_rn(acc[s][v], c);
+                        l[s] = __fmul_rn(l[s], c);
+                        m[s] = d;
+                    }
+                    const float pw = cj_expf(d - m[s]);
+                    l[s] = __fadd_rn(l[s], pw);
+#pragma unroll
+                    for (int v = 0; v < 8; v++) acc[s][v] = __fadd_rn(acc[s][v], __fmul_rn(vf[v], pw));
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        if (row[s] >= a.nrows) continue;
+        const float inv = __fdiv_rn(1.0f, l[s]);
+        float *o = a.out + (int64_t)row[s] * a.q_stride + (int64_t)head[s] * HD + j;
+#pragma unroll
+        for (int v = 0; v < 8; v++) o[16 * v] = __fmul_rn(acc[s][v], inv);
+    }
+}
+
+#define PREFILL_KERNEL(G) \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_prefill_h128_g##G(cj_attn_args a) { prefill_body<G>(a); }
+PREFILL_KERNEL(1)
+PREFILL_KERNEL(2)
+PREFILL_KERNEL(4)
+PREFILL_KERNEL(8)

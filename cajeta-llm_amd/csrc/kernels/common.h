@@ -7,6 +7,8 @@
 #define DEV __device__ __forceinline__
 
 // fp16 bits <-> f32 through the hardware converts (exact / round-to-nearest-even).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));   // a native 16-byte vector
+
 DEV float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu))); }
 DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 

@@ -149,13 +149,14 @@ DEV void gemm_q4k_tile(const cj_gemv_args &a, int64_t r0, int64_t c0, float (&ac
     }
 }
 
-// Workgroup (row tile, column tile): 16 rows, and 16 columns a wave over the
-// workgroup's 1..4 waves.
+// Workgroup (column tile, row tile): 16 rows, and 16 columns a wave over the
+// workgroup's 1..4 waves. The column tiles of one row tile are adjacent in
+// dispatch order, so they run together and share the rows' weights in cache.
 template <int FMT>
 DEV void gemm_body(const cj_gemv_args &a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * 16;
-    const int64_t c0 = ((int64_t)blockIdx.y * waves + wave) * 16;
+    const int64_t r0 = (int64_t)blockIdx.y * 16;
+    const int64_t c0 = ((int64_t)blockIdx.x * waves + wave) * 16;
     if (c0 >= a.batch) return;                     // uniform per wave; no barrier follows
     float acc[4];
     if (FMT == CJ_Q8_0) gemm_q80_tile(a, r0, c0, acc);

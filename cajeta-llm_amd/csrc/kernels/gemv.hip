@@ -607,7 +607,6 @@ DEV void gemv_body(const cj_gemv_args &a) {
 // clamped into range, the surplus masked where it is used) because a load
 // under a branch makes the compiler wait for every load in flight at the
 // join, the weight stream included.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));   // a native 16-byte vector
 
 template <int PRO, int RND>
 struct Q4kProDims {

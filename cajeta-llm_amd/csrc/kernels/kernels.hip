@@ -4,3 +4,4 @@
 #include "prim.hip"
 #include "attn.hip"
 #include "gemm.hip"
+#include "rows.hip"

@@ -107,6 +107,21 @@ struct Engine {
     bool graphs = true;        // replay the captured step (false: enqueue its launches each token)
     int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
     int64_t embd_row_file_bytes = 0;
+    // the many-row path: batched decode (a row a sequence) and prefill
+    // chunks (a row a position)
+    cj_step_state *states = nullptr;           // [max_seqs]; seqs[s].state = states + s
+    int32_t *tokens_all = nullptr, *preds_all = nullptr;   // [max_seqs][ctx + 2]
+    bool rows_ok = false;      // dense, head size 128, projections served as many-row products
+    bool batch_split = false;  // batched decode attention takes the split-K rows kernel
+    int chunk = 512;           // prefill rows a chunk (CausalLM.CHUNK_MAX)
+    int rows_cap = 0;          // rows the row buffers hold
+    float *r_hs = nullptr, *r_qkv = nullptr, *r_q = nullptr, *r_attn = nullptr, *r_gu = nullptr;
+    float *r_logits = nullptr, *r_part = nullptr, *r_pv = nullptr;
+    int32_t *r_pi = nullptr, *r_tab_pf = nullptr, *r_tab_b = nullptr;
+    uint8_t *r_xp = nullptr, *r_ap = nullptr, *r_actp = nullptr;
+    int32_t *pinned_tab = nullptr;             // pinned staging of a row table
+    std::vector<int> batch_slots;              // the slots the batch graph was captured for
+    hipGraphExec_t batch_graph = nullptr;
 
     bool want(int kind, int l) const {
         return only < 0 || (only == kind && l == (kind == K_EMBED || kind == K_HEAD ? 0 : only_layer));
@@ -120,9 +135,11 @@ struct Engine {
     ~Engine() {
         for (auto &s : seqs)
             if (s.graph) (void)hipGraphExecDestroy(s.graph);
+        if (batch_graph) (void)hipGraphExecDestroy(batch_graph);
         (void)hipStreamSynchronize(stream());
         for (void *p : owned) dev_free(p);
         if (pinned) (void)hipHostFree(pinned);
+        if (pinned_tab) (void)hipHostFree(pinned_tab);
     }
     int load(const std::string &path, int ctx_, int max_seqs_);
     int upload_weight(const std::string &name, DevW &w, int expect_rows, int64_t expect_cols);
@@ -130,7 +147,15 @@ struct Engine {
     int capture(int s);
     int enqueue_step(int s);
     int run_step(int s);
-    int norm_pack(const float *w, int per32, bool f32_out);
+    int norm_pack(const float *w, int per32, bool f32_out, const float *x = nullptr);
+    // the many-row path
+    int rows_alloc(int cap);
+    int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
+    int rows_norm_pack(const float *w, int per32, int n);
+    int rows_forward(const int32_t *tab, int n, bool prefill);
+    int enqueue_batch(int n);
+    int prefill_rows(int s, const int32_t *toks, int n);
+    int decode_batch(const int32_t *slots, int n, int steps, int32_t *out);
     int prefill(int s, const int32_t *toks, int n);
     int decode(int s, int steps, int32_t *out);
     int reset(int s);
@@ -345,19 +370,65 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
 
     if (hipHostMalloc((void **)&pinned, (size_t)(ctx + 2) * 4 + sizeof(cj_step_state) + 64, 0) != hipSuccess)
         return fail(CJ_ERR_HIP, "model: pinned staging buffer");
+    // sequence slots: histories and step states side by side, so the
+    // many-row kernels reach every slot's from one base
+    const size_t hist = (size_t)(ctx + 2);
+    tokens_all = (int32_t *)alloc(hist * max_seqs * 4);
+    preds_all = (int32_t *)alloc(hist * max_seqs * 4);
+    states = (cj_step_state *)alloc(sizeof(cj_step_state) * (size_t)max_seqs);
+    if (!tokens_all || !preds_all || !states) return fail(CJ_ERR_HIP, "model: out of device memory (sequence slots)");
+    CJ_HIP(hipMemset(tokens_all, 0, hist * max_seqs * 4));
+    CJ_HIP(hipMemset(preds_all, 0, hist * max_seqs * 4));
+    CJ_HIP(hipMemset(states, 0, sizeof(cj_step_state) * (size_t)max_seqs));
     seqs.resize(max_seqs);
     for (int s = 0; s < max_seqs; s++) {
         Seq &S = seqs[s];
-        S.tokens = (int32_t *)alloc((size_t)(ctx + 2) * 4);
-        S.preds = (int32_t *)alloc((size_t)(ctx + 2) * 4);
-        S.state = (cj_step_state *)alloc(sizeof(cj_step_state));
-        if (!S.tokens || !S.preds || !S.state) return fail(CJ_ERR_HIP, "model: out of device memory (sequence slots)");
+        S.tokens = tokens_all + hist * s;
+        S.preds = preds_all + hist * s;
+        S.state = states + s;
         S.pg_base = s * pages_per_seq;
-        CJ_HIP(hipMemset(S.tokens, 0, (size_t)(ctx + 2) * 4));
-        CJ_HIP(hipMemset(S.preds, 0, (size_t)(ctx + 2) * 4));
-        CJ_HIP(hipMemset(S.state, 0, sizeof(cj_step_state)));
     }
+
+    // the many-row path: dense layers at head size 128 whose projections
+    // read int8 packs (the CPU prefill attend serves head size 128,
+    // AttnKernel.cpuAttnServes, model/AttnKernel.cajeta:4439-4447)
+    rows_ok = n_experts == 0 && head_dim == 128;
+    for (auto &L : layers)
+        for (const DevW *w : {&L.qkv, &L.o, &L.gu, &L.down})
+            if (is_f32_act(w->type)) rows_ok = false;
+    batch_split = rows_ok && (grp == 4 || grp == 8);
+    if (rows_ok && (rc = rows_alloc(std::max(chunk, max_seqs)))) return rc;
     CJ_HIP(hipDeviceSynchronize());
+    return CJ_OK;
+}
+
+// Row buffers for up to `cap` rows (prefill chunk or decode batch).
+int Engine::rows_alloc(int cap) {
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim;
+    const int64_t hb = ((int64_t)hidden + 255) / 256 * 320, qb = (qd + 255) / 256 * 320;
+    const int64_t fb = ((int64_t)ffn + 255) / 256 * 320;
+    const int64_t nch = ((int64_t)vocab + 1023) / 1024;
+    const int64_t b = std::max(1, max_seqs);
+    r_hs = (float *)alloc((size_t)(cap * (int64_t)hidden * 4));
+    r_qkv = (float *)alloc((size_t)(cap * (qd + 2 * kvd) * 4));
+    r_q = (float *)alloc((size_t)(cap * qd * 4));
+    r_attn = (float *)alloc((size_t)(cap * qd * 4));
+    r_gu = (float *)alloc((size_t)(cap * 2 * (int64_t)ffn * 4));
+    r_xp = (uint8_t *)alloc((size_t)(cap * hb));
+    r_ap = (uint8_t *)alloc((size_t)(cap * qb));
+    r_actp = (uint8_t *)alloc((size_t)(cap * fb));
+    r_logits = (float *)alloc((size_t)(b * vocab * 4));
+    r_part = (float *)alloc((size_t)(b * n_heads * 64 * (head_dim + 2) * 4));
+    r_pv = (float *)alloc((size_t)(b * nch * 4));
+    r_pi = (int32_t *)alloc((size_t)(b * nch * 4));
+    r_tab_pf = (int32_t *)alloc((size_t)cap * 8);
+    r_tab_b = (int32_t *)alloc((size_t)b * 8);
+    if (!r_hs || !r_qkv || !r_q || !r_attn || !r_gu || !r_xp || !r_ap || !r_actp || !r_logits || !r_part || !r_pv ||
+        !r_pi || !r_tab_pf || !r_tab_b)
+        return fail(CJ_ERR_HIP, "model: out of device memory (row buffers for %d rows)", cap);
+    if (hipHostMalloc((void **)&pinned_tab, (size_t)cap * 8, 0) != hipSuccess)
+        return fail(CJ_ERR_HIP, "model: pinned row-table staging");
+    rows_cap = cap;
     return CJ_OK;
 }
 
@@ -531,11 +602,255 @@ int Engine::capture(int s) {
 // the next projection: its pack into xpack and, for f32-activation
 // consumers, the normed values into xn (one workgroup; the norm is a
 // reduction over the whole row).
-int Engine::norm_pack(const float *w, int per32, bool f32_out) {
+int Engine::norm_pack(const float *w, int per32, bool f32_out, const float *x) {
     cj_pack_args a{};
-    a.out = xpack; a.x = hs; a.w = w; a.xout = f32_out ? xn : nullptr; a.n = hidden;
+    a.out = xpack; a.x = x ? x : hs; a.w = w; a.xout = f32_out ? xn : nullptr; a.n = hidden;
     a.npad = ((int64_t)hidden + 255) / 256 * 256; a.rows = 1; a.eps = eps; a.form = 0; a.per32 = per32; a.do_norm = 1;
     return launch("cj_norm_pack", (uint32_t)(a.npad / 256), 256, 0, a);
+}
+
+// ------------------------------------------------------------ many rows
+
+// y rows = W · x rows for n packed activation rows: the int8 matrix-core
+// product where the format has one, else the one-row GEMV a row (both
+// compute each row exactly as the decode step does).
+int Engine::rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n) {
+    cj_gemv_args a{};
+    a.w = (const uint8_t *)W.p; a.rows = W.rows; a.cols = W.cols; a.row_bytes = W.row_bytes; a.type = W.type;
+    a.pro = CJ_PRO_PACKED; a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = W.type == CJ_Q8_0;
+    if (gemm_supported(W.type)) {
+        a.xp = xp; a.y = y; a.batch = n; a.xp_stride = xp_stride; a.y_stride = y_stride;
+        return run_gemm(a);
+    }
+    const GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi);
+    a.batch = 1;
+    for (int r = 0; r < n; r++) {
+        a.xp = xp + r * xp_stride;
+        a.y = y + r * y_stride;
+        int rc = run_gemv(a, p);
+        if (rc) return rc;
+    }
+    return CJ_OK;
+}
+
+// RMSNorm + pack of n residual rows (the row form: one workgroup a row).
+int Engine::rows_norm_pack(const float *w, int per32, int n) {
+    cj_pack_args a{};
+    const int64_t npad = ((int64_t)hidden + 255) / 256 * 256;
+    a.out = r_xp; a.x = r_hs; a.w = w; a.n = hidden; a.npad = npad; a.rows = n; a.eps = eps; a.form = 0;
+    a.per32 = per32; a.do_norm = 1;
+    return launch("cj_pack", (uint32_t)n, 256, (uint32_t)(npad / 256 * 320), a);
+}
+
+// The layers over n rows (row table `tab` on the device): embedding, then per
+// layer the norm + pack rows, q|k|v product, RoPE + K/V append rows, the
+// attention (prefill: the prefill attend + pack; batched decode: split-K
+// rows + merge/pack), o product into the residual rows, FFN norm + pack,
+// gate|up product, SiLU·up + pack rows, down product into the residual rows
+// (CausalLM.decodeBatchRows, model/CausalLM.cajeta:4133-4360, and
+// forwardRowsBatched, :2873).
+int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
+    const int64_t qd = (int64_t)n_heads * head_dim;
+    const int64_t hb = ((int64_t)hidden + 255) / 256 * 320, qb = (qd + 255) / 256 * 320;
+    const int64_t fpad = ((int64_t)ffn + 255) / 256 * 256;
+    const int grp = n_heads / n_kv;
+    int rc;
+    cj_rows_args ra{};
+    ra.rowtab = tab; ra.states = states; ra.tokens = tokens_all; ra.preds = preds_all; ra.hist = ctx + 2;
+    {
+        cj_rows_args e = ra;
+        e.table = (const uint8_t *)embd; e.row_bytes = embd_row_bytes; e.type = embd_type; e.nrows = n;
+        e.out = r_hs; e.out_stride = hidden; e.n = hidden;
+        if ((rc = launch2("cj_rows_embed", (uint32_t)((hidden + 255) / 256), (uint32_t)n, 256, 0, e))) return rc;
+    }
+    for (int l = 0; l < n_layers; l++) {
+        Layer &L = layers[l];
+        if ((rc = rows_norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, n))) return rc;
+        if ((rc = rows_linear(L.qkv, r_xp, hb, r_qkv, L.qkv.rows, false, n))) return rc;
+        {
+            cj_rows_args q = ra;
+            q.in = r_qkv; q.in_stride = L.qkv.rows; q.q_out = r_q; q.out_stride = qd; q.kc = L.kc; q.vc = L.vc;
+            q.pgtab = pgtab; q.rope_cs = rope; q.pg_n = pages_per_seq; q.n_q = n_heads; q.n_kv = n_kv;
+            q.head_dim = head_dim; q.nrows = n;
+            if ((rc = launch("cj_rows_qkv", (uint32_t)n, 256, 0, q))) return rc;
+        }
+        cj_attn_args a{};
+        a.q = r_q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
+        a.workers = workers; a.scale = scale; a.pg_n = pages_per_seq; a.window = L.window; a.rowtab = tab;
+        a.states = states; a.nrows = n; a.q_stride = qd;
+        if (prefill) {
+            a.out = r_attn;
+            const int ns = grp >= 8 ? grp / 4 : 1, rb = 16 * ns / grp;
+            char kname[48];
+            snprintf(kname, sizeof kname, "cj_attn_prefill_h128_g%d", grp);
+            if ((rc = launch(kname, (uint32_t)(n_kv * ((n + rb - 1) / rb)), 256, 0, a))) return rc;
+            cj_pack_args p{};
+            p.out = r_ap; p.x = r_attn; p.n = qd; p.npad = (qd + 255) / 256 * 256; p.rows = n; p.per32 = L.o.type == CJ_Q8_0;
+            if ((rc = launch("cj_pack", (uint32_t)n, 256, (uint32_t)qb, p))) return rc;
+        } else {
+            // split slots a row: the rule's count over every row's kv heads
+            const int rk = n * n_kv;
+            const int spl = std::min(64, std::max(1, (2 * workers + rk - 1) / rk));
+            a.part = r_part; a.spl = spl; a.part_stride = (int64_t)n_heads * 64 * (head_dim + 2);
+            char kname[48];
+            snprintf(kname, sizeof kname, "cj_attn_split_rows_h128_g%d", grp);
+            if ((rc = launch(kname, (uint32_t)(n * n_kv * spl), 256, 0, a))) return rc;
+            cj_merge_args m{};
+            m.packed = r_ap; m.part = r_part; m.n_q = n_heads; m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0;
+            m.n_kv = n_kv; m.workers = workers; m.window = L.window; m.nrows = n; m.rowtab = tab; m.states = states;
+            m.part_stride = a.part_stride; m.pack_stride = qb;
+            if ((rc = launch("cj_attn_merge", (uint32_t)(n * (qd / 256)), 256, 0, m))) return rc;
+        }
+        if ((rc = rows_linear(L.o, r_ap, qb, r_hs, hidden, true, n))) return rc;
+        if ((rc = rows_norm_pack(L.ffn_norm, L.gu.type == CJ_Q8_0, n))) return rc;
+        if ((rc = rows_linear(L.gu, r_xp, hb, r_gu, L.gu.rows, false, n))) return rc;
+        {
+            cj_rows_args g = ra;
+            g.in = r_gu; g.in_stride = L.gu.rows; g.packed = r_actp; g.pack_stride = fpad / 256 * 320;
+            g.n = ffn; g.npad = fpad; g.form = (ffn % 256) ? 1 : 0; g.per32 = L.down.type == CJ_Q8_0; g.nrows = n;
+            if ((rc = launch2("cj_rows_glu", (uint32_t)(fpad / 256), (uint32_t)n, 256, 0, g))) return rc;
+        }
+        if ((rc = rows_linear(L.down, r_actp, fpad / 256 * 320, r_hs, hidden, true, n))) return rc;
+    }
+    return CJ_OK;
+}
+
+// One batched decode step over the n slots of the batch row table: the
+// layers, then every row's final norm, head and greedy pick (advancing each
+// slot's position).
+int Engine::enqueue_batch(int n) {
+    int rc;
+    if ((rc = rows_forward(r_tab_b, n, false))) return rc;
+    const int64_t hb = ((int64_t)hidden + 255) / 256 * 320;
+    if ((rc = rows_norm_pack(out_norm, head.type == CJ_Q8_0, n))) return rc;
+    if ((rc = rows_linear(head, r_xp, hb, r_logits, vocab, false, n))) return rc;
+    cj_rows_args k{};
+    k.rowtab = r_tab_b; k.states = states; k.tokens = tokens_all; k.preds = preds_all; k.hist = ctx + 2;
+    k.in = r_logits; k.in_stride = vocab; k.n = vocab; k.pv = r_pv; k.pi = r_pi; k.nchunks = (vocab + 1023) / 1024;
+    k.nrows = n;
+    if ((rc = launch2("cj_rows_argmax", (uint32_t)k.nchunks, (uint32_t)n, 256, 0, k))) return rc;
+    return launch("cj_rows_pick", (uint32_t)n, 256, 0, k);
+}
+
+// A prompt of n > 1 tokens as prefill chunks of up to `chunk` rows
+// (CausalLM.stepSeq, model/CausalLM.cajeta:801-883): every row of a chunk
+// through each layer, the prefill attend over the positions so far; the
+// final norm, head and greedy pick on the prompt's last row only.
+int Engine::prefill_rows(int s, const int32_t *toks, int n) {
+    Seq &S = seqs[s];
+    int rc;
+    memcpy(pinned, toks, (size_t)n * 4);
+    cj_step_state *st = (cj_step_state *)(pinned + ctx + 2);
+    *st = cj_step_state{};
+    st->pos = S.pos;
+    st->fixed_until = S.pos + n;
+    CJ_HIP(hipMemcpyAsync(S.tokens + S.pos, pinned, (size_t)n * 4, hipMemcpyHostToDevice, stream()));
+    CJ_HIP(hipMemcpyAsync(S.state, st, sizeof *st, hipMemcpyHostToDevice, stream()));
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+        const int m = std::min(chunk, n - c0);
+        CJ_HIP(hipStreamSynchronize(stream()));   // the staging is free again
+        for (int r = 0; r < m; r++) { pinned_tab[2 * r] = s; pinned_tab[2 * r + 1] = c0 + r; }
+        CJ_HIP(hipMemcpyAsync(r_tab_pf, pinned_tab, (size_t)m * 8, hipMemcpyHostToDevice, stream()));
+        if ((rc = rows_forward(r_tab_pf, m, true))) return rc;
+        if (c0 + m < n) continue;
+        // the tail on the prompt's last row
+        const int last = S.pos + n - 1;
+        if ((rc = norm_pack(out_norm, head.type == CJ_Q8_0, is_f32_act(head.type), r_hs + (int64_t)(m - 1) * hidden)))
+            return rc;
+        cj_gemv_args a{};
+        a.w = (const uint8_t *)head.p; a.x = xn; a.xp = xpack; a.y = logits;
+        a.part_v = part_v; a.part_i = part_i; a.tokens = S.tokens; a.preds = S.preds; a.state = nullptr; a.pos = last;
+        a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
+        a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
+        a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128, a.pro, a.epi);
+        if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
+        if ((rc = run_gemv(a, p))) return rc;
+        cj_pick_args k{};
+        k.pv = part_v; k.pi = part_i; k.n = (int32_t)p.grid; k.pos = last; k.tokens = S.tokens; k.preds = S.preds;
+        k.state = nullptr;
+        if ((rc = launch("cj_argmax_pick", 1, 256, 0, k))) return rc;
+    }
+    S.pos += n;
+    st->pos = S.pos;
+    st->fixed_until = S.pos;
+    CJ_HIP(hipMemcpyAsync(S.state, st, sizeof *st, hipMemcpyHostToDevice, stream()));
+    CJ_HIP(hipStreamSynchronize(stream()));
+    S.fixed_until = S.pos;
+    return CJ_OK;
+}
+
+// `steps` greedy tokens for each of n prefilled slots at once (one row a
+// slot): out[i·n + r] is slot r's token i. Shapes without the split-K
+// attention decode slot by slot (the same tokens: rows only share weights).
+int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
+    if (n <= 0 || n > max_seqs) return fail(CJ_ERR_ARG, "decode batch of %d slots (1..%d)", n, max_seqs);
+    for (int r = 0; r < n; r++) {
+        const int s = slots[r];
+        if (s < 0 || s >= max_seqs) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+        for (int q2 = 0; q2 < r; q2++)
+            if (slots[q2] == s) return fail(CJ_ERR_ARG, "slot %d twice in one batch", s);
+        if (seqs[s].pos == 0) return fail(CJ_ERR_STATE, "decode of slot %d before prefill", s);
+        if (seqs[s].pos + steps > ctx)
+            return fail(CJ_ERR_CAPACITY, "kv pool exhausted: slot %d position %d of %d", s, seqs[s].pos + steps, ctx);
+    }
+    if (steps <= 0) return CJ_OK;
+    int rc;
+    if (!batch_split || n > rows_cap) {
+        std::vector<int32_t> tmp((size_t)steps);
+        for (int r = 0; r < n; r++) {
+            if ((rc = decode(slots[r], steps, tmp.data()))) return rc;
+            if (out)
+                for (int i = 0; i < steps; i++) out[(size_t)i * n + r] = tmp[i];
+        }
+        return CJ_OK;
+    }
+    const std::vector<int> want(slots, slots + n);
+    if (want != batch_slots) {
+        if (batch_graph) { (void)hipGraphExecDestroy(batch_graph); batch_graph = nullptr; }
+        CJ_HIP(hipStreamSynchronize(stream()));
+        for (int r = 0; r < n; r++) { pinned_tab[2 * r] = slots[r]; pinned_tab[2 * r + 1] = 0; }
+        CJ_HIP(hipMemcpy(r_tab_b, pinned_tab, (size_t)n * 8, hipMemcpyHostToDevice));
+        batch_slots = want;
+    }
+    if (graphs && !batch_graph) {
+        CJ_HIP(hipStreamSynchronize(stream()));
+        CJ_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal));
+        rc = enqueue_batch(n);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(stream(), &g);
+        if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+        if (e != hipSuccess) return fail(CJ_ERR_HIP, "batch capture: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&batch_graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) { batch_graph = nullptr; return fail(CJ_ERR_HIP, "batch graph instantiate: %s", hipGetErrorString(e)); }
+    }
+    hipEvent_t e0, e1;
+    CJ_HIP(hipEventCreate(&e0));
+    CJ_HIP(hipEventCreate(&e1));
+    CJ_HIP(hipEventRecord(e0, stream()));
+    for (int i = 0; i < steps; i++) {
+        if (graphs) CJ_HIP(hipGraphLaunch(batch_graph, stream()));
+        else if ((rc = enqueue_batch(n))) return rc;
+        if ((i & 7) == 7 && i + 1 < steps) CJ_HIP(hipStreamSynchronize(stream()));
+    }
+    CJ_HIP(hipEventRecord(e1, stream()));
+    CJ_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    CJ_HIP(hipEventElapsedTime(&ms, e0, e1));
+    last_step_us = ms * 1000.0f / (float)steps;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::vector<int32_t> tmp((size_t)steps);
+    for (int r = 0; r < n; r++) {
+        Seq &S = seqs[slots[r]];
+        if (out) {
+            CJ_HIP(hipMemcpy(tmp.data(), S.tokens + S.pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost));
+            for (int i = 0; i < steps; i++) out[(size_t)i * n + r] = tmp[i];
+        }
+        S.pos += steps;
+    }
+    return CJ_OK;
 }
 
 // One decode step of slot s on the stream: the graph, or its launches.
@@ -563,6 +878,7 @@ int Engine::prefill(int s, const int32_t *toks, int n) {
     if (S.pos + n > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + n, ctx);
     for (int i = 0; i < n; i++)
         if (toks[i] < 0 || toks[i] >= vocab) return fail(CJ_ERR_ARG, "token %d outside the vocabulary", toks[i]);
+    if (n > 1 && rows_ok && chunk > 1) return prefill_rows(s, toks, n);
     int rc;
     if (graphs && (rc = capture(s))) return rc;
     // through pinned staging: the copies are ordered on the stream and the
@@ -869,6 +1185,20 @@ int32_t cj_engine_decode(int64_t h, int32_t seq, int32_t steps, int32_t *out) {
     Engine *e = eng_of(h);
     return e ? e->decode(seq, steps, out) : cj::fail(CJ_ERR_STATE, "null engine");
 }
+int32_t cj_engine_decode_batch(int64_t h, const int32_t *slots, int32_t n, int32_t steps, int32_t *out) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    if (!slots) return cj::fail(CJ_ERR_ARG, "cj_engine_decode_batch: no slots");
+    return e->decode_batch(slots, n, steps, out);
+}
+int32_t cj_engine_set_prefill_chunk(int64_t h, int32_t rows) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    if (rows < 0 || (rows > 1 && rows > e->rows_cap))
+        return cj::fail(CJ_ERR_ARG, "prefill chunk %d (0..%d)", rows, e->rows_cap);
+    e->chunk = rows;
+    return CJ_OK;
+}
 int32_t cj_engine_logits(int64_t h, int32_t seq, float *out, int64_t n) {
     Engine *e = eng_of(h);
     if (!e || n > e->vocab) return cj::fail(CJ_ERR_ARG, "cj_engine_logits: n %lld", (long long)n);
@@ -897,6 +1227,7 @@ int32_t cj_engine_trace(int64_t h, int32_t what, float *out, int64_t n) {
     case 3: src = e->act; cap = e->ffn; break;
     case 4: src = e->logits; cap = e->vocab; break;
     case 5: src = (const float *)e->act_pack; cap = ((int64_t)e->ffn + 255) / 256 * 80; break;
+    case 6: src = e->r_logits; cap = e->r_logits ? (int64_t)e->batch_slots.size() * e->vocab : 0; break;
     default: return cj::fail(CJ_ERR_ARG, "cj_engine_trace: unknown tap %d", what);
     }
     if (n > cap) return cj::fail(CJ_ERR_ARG, "cj_engine_trace: %lld > %lld", (long long)n, (long long)cap);

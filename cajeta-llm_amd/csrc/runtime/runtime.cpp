@@ -241,7 +241,8 @@ int run_gemm(const cj_gemv_args &a) {
     if (!gemm_supported(a.type)) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
     if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
     const int waves = (int)std::min<int64_t>(4, (a.batch + 15) / 16);
-    const uint32_t gx = (uint32_t)((a.rows + 15) / 16), gy = (uint32_t)((a.batch + 16 * waves - 1) / (16 * waves));
+    const uint32_t gx = (uint32_t)((a.batch + 16 * waves - 1) / (16 * waves)), gy = (uint32_t)((a.rows + 15) / 16);
+    if (gy > 65535) return fail(CJ_ERR_ARG, "gemm: %lld rows exceed the grid", (long long)a.rows);
     return launch2(a.type == CJ_Q8_0 ? "cj_gemm_q80" : "cj_gemm_q4k", gx, gy, 64 * waves, 0, a);
 }
 
@@ -285,6 +286,9 @@ int32_t cj_init(int32_t device) {
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
         "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_gemm_q80", "cj_gemm_q4k",
+        "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
+        "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8",
+        "cj_attn_prefill_h128_g1", "cj_attn_prefill_h128_g2", "cj_attn_prefill_h128_g4", "cj_attn_prefill_h128_g8",
     };
     for (const char *k : kernels) {
         hipFunction_t f;

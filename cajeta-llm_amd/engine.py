@@ -25,6 +25,7 @@ class EngineOptions:
         self.device = ""
         self.cpuThreads = 0
         self.graphs = True       # replay the captured decode step (False: eager launches)
+        self.prefillChunk = 512  # rows a prefill chunk (CausalLM.CHUNK_MAX); 0: one decode step a position
 
 
 class SampleParams:
@@ -93,6 +94,7 @@ class LlmEngine:
                 "ctx", "expertCount", "expertUsedCount", "weightType", "headType", "expertFfn", "attnWorkers")
         self.config = dict(zip(keys, [int(v) for v in cfg]))
         self._eog = []
+        self._batch_rows = 0
 
     @staticmethod
     def load(opts):
@@ -109,6 +111,9 @@ class LlmEngine:
         handle(h, "LlmEngine.load(%s)" % opts.model)
         if not getattr(opts, "graphs", True):
             check(lib().cj_engine_set_graphs(h, 0), "cj_engine_set_graphs")
+        chunk = getattr(opts, "prefillChunk", 512)
+        if chunk != 512:
+            check(lib().cj_engine_set_prefill_chunk(h, int(chunk)), "cj_engine_set_prefill_chunk")
         return LlmEngine(h, opts)
 
     # -- the LlmEngine surface
@@ -170,6 +175,23 @@ class LlmEngine:
         out = np.zeros(max(1, steps), np.int32)
         check(lib().cj_engine_decode(self.h, seq, int(steps), ptr(out)), "decode")
         return out[:steps]
+
+    def decodeBatch(self, seqs, steps):
+        """`steps` greedy tokens for each prefilled slot in `seqs` at once
+        (CausalLM.decodeBatchRows): an int32 array [steps][len(seqs)]."""
+        sl = np.ascontiguousarray(seqs, dtype=np.int32)
+        out = np.zeros((max(1, steps), sl.size), np.int32)
+        check(lib().cj_engine_decode_batch(self.h, ptr(sl), int(sl.size), int(steps), ptr(out)), "decodeBatch")
+        self._batch_rows = int(sl.size)
+        return out[:steps]
+
+    def batchLogits(self):
+        """The last batched decode step's logits, [rows][vocab]."""
+        v = self.config["vocabSize"]
+        rows = self._batch_rows
+        out = np.empty(rows * v, np.float32)
+        check(lib().cj_engine_trace(self.h, 6, ptr(out), out.size), "batchLogits")
+        return out.reshape(rows, v)
 
     def logits(self, seq=0):
         out = np.empty(self.config["vocabSize"], np.float32)

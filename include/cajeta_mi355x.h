@@ -220,13 +220,26 @@ int32_t cj_engine_request(int64_t eng, int32_t id, int32_t *tokens, int32_t cap,
 int32_t cj_engine_cancel(int64_t eng, int32_t id);
 int32_t cj_engine_set_eog(int64_t eng, const int32_t *ids, int32_t n);
 
-/* CausalLM seam: teacher-forced or free greedy decode of one sequence slot.
- * prefill feeds tokens[0..n) at positions pos0.. (the graph-captured decode
- * step, one per position); decode runs `steps` greedy steps from the state
- * prefill left and writes the generated ids. logits: the last step's row. */
+/* CausalLM seam: prefill and free greedy decode of one sequence slot.
+ * prefill feeds tokens[0..n) at positions pos0..: with n > 1 on dense
+ * head-size-128 models as prefill chunks of up to the chunk size
+ * (CausalLM.stepSeq, model/CausalLM.cajeta:801-883: every row through a
+ * layer, the prefill attend, the tail on the last row only), otherwise one
+ * graph-captured decode step a position; decode runs `steps` greedy steps
+ * from the state prefill left and writes the generated ids. logits: the
+ * last step's (or the prompt's last row's) logits. */
 int32_t cj_engine_reset(int64_t eng, int32_t seq);
 int32_t cj_engine_prefill(int64_t eng, int32_t seq, const int32_t *tokens, int32_t n);
 int32_t cj_engine_decode(int64_t eng, int32_t seq, int32_t steps, int32_t *out_tokens);
+/* Batched greedy decode: `steps` tokens for each of n prefilled slots at once,
+ * one row a slot sharing every weight read (CausalLM.decodeBatchRows,
+ * model/CausalLM.cajeta:4133-4360; the reference's batched Cols kernels,
+ * io/QuantKernel.cajeta:33646, and batch attention, model/AttnKernel.cajeta:5761,
+ * :6599). out_tokens[i·n + r] is slot r's token i. */
+int32_t cj_engine_decode_batch(int64_t eng, const int32_t *slots, int32_t n, int32_t steps, int32_t *out_tokens);
+/* Rows a prefill chunk (CausalLM.CHUNK_MAX, model/CausalLM.cajeta:52; at most
+ * the row buffers' capacity); 0 or 1: prefill as one decode step a position. */
+int32_t cj_engine_set_prefill_chunk(int64_t eng, int32_t rows);
 int32_t cj_engine_logits(int64_t eng, int32_t seq, float *out, int64_t n);
 /* Predicted (argmax) ids at positions 1..n of the slot's history. */
 int32_t cj_engine_preds(int64_t eng, int32_t seq, int32_t *out, int32_t n);
@@ -235,7 +248,8 @@ float cj_engine_last_step_us(int64_t eng);
 /* Debug taps of the last step (CausalLM.sniffBuf, model/CausalLM.cajeta:2260-2360):
  * what 0 = residual hs [hidden], 1 = rotated q [n_heads·hd], 2 = attention
  * output [n_heads·hd], 3 = SiLU·up activation [ffn], 4 = logits [vocab] —
- * each as the last layer left it. */
+ * each as the last layer left it; 5 = the down projection's activation pack
+ * (as f32 words); 6 = the last batched decode step's logits [rows][vocab]. */
 int32_t cj_engine_trace(int64_t eng, int32_t what, float *out, int64_t n);
 /* Measurement seam, no counterpart in the reference's decode API (its
  * benches time whole steps from the host): `reps` back-to-back

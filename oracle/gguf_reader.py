@@ -71,7 +71,7 @@ class GgufReader:
         raise ValueError("unknown GGUF value type %d" % ty)
 
 
-def model_config(r, workers=512, kv_f32=False, ctx=None):
+def model_config(r, workers=512, kv_f32=False, ctx=None, attn_rows=1):
     """The oracle's config from GGUF metadata (model/ModelConfig.cajeta:172-320)."""
     m = r.meta
     arch = m["general.architecture"]
@@ -92,6 +92,7 @@ def model_config(r, workers=512, kv_f32=False, ctx=None):
         norm_topk=int(m.get(kp + "expert_weights_norm", 1)),
         expert_ffn=int(m.get(kp + "expert_feed_forward_length", m[kp + "feed_forward_length"])),
         swa_window=int(m.get(kp + "attention.sliding_window", 0)),
+        attn_rows=int(attn_rows),
     )
     return cfg
 

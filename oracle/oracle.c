@@ -730,6 +730,57 @@ void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, 
     }
 }
 
+/* AttnKernel.attnPrefillCpuGqaKernel (L/model/AttnKernel.cajeta:3916-4004),
+ * the CPU backend's prefill attend at head size 128: one pass per (row,
+ * query head) over positions [t0, count) with an online softmax. Unlike the
+ * decode form, q is scaled first (q·scale, rounded, then the dot), the
+ * running max starts at -1e30, and the output is acc·(1/l). The score of a
+ * key: 16 lane partials d_j = Σ_v qs[16v+j]·k[16v+j] (v ascending, each
+ * product rounded then added) folded by the fixed pairwise tree. */
+void or_prefill_attend(const float *q, const void *kp, const void *vp, int f32, int nh, int nkv, int hd,
+                       int start, int rows, int window, float scale, float *out) {
+    int64_t kvdim = (int64_t)nkv * hd;
+    int group = nh / nkv;
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
+    for (int kvh = 0; kvh < nkv; kvh++)
+        for (int r = 0; r < rows; r++) {
+            int count = start + r + 1, t0 = 0;
+            if (window > 0 && count > window) t0 = count - window;
+            for (int h = 0; h < group; h++) {
+                int hh = kvh * group + h;
+                const float *qr = q + (int64_t)r * nh * hd + (int64_t)hh * hd;
+                float qs[128], acc[128];
+                for (int d = 0; d < hd; d++) { qs[d] = qr[d] * scale; acc[d] = 0.0f; }
+                float m = -1.0e30f, l = 0.0f;
+                for (int t = t0; t < count; t++) {
+                    int64_t ko = (int64_t)t * kvdim + (int64_t)kvh * hd;
+                    float dl[16];
+                    for (int j = 0; j < 16; j++) dl[j] = qs[j] * kv_at(kp, f32, ko + j);
+                    for (int v = 1; v < hd / 16; v++)
+                        for (int j = 0; j < 16; j++) dl[j] = dl[j] + qs[16 * v + j] * kv_at(kp, f32, ko + 16 * v + j);
+#if OR_PLANT == 9
+                    float sc = dl[0];                                  /* planted: lane 0's partial only */
+#else
+                    float sc = ((((dl[0] + dl[1]) + (dl[2] + dl[3])) + ((dl[4] + dl[5]) + (dl[6] + dl[7])))
+                                + (((dl[8] + dl[9]) + (dl[10] + dl[11])) + ((dl[12] + dl[13]) + (dl[14] + dl[15]))));
+#endif
+                    if (sc > m) {
+                        float c = or_expf(m - sc);
+                        for (int d = 0; d < hd; d++) acc[d] = acc[d] * c;
+                        l = l * c;
+                        m = sc;
+                    }
+                    float p = or_expf(sc - m);
+                    l = l + p;
+                    for (int d = 0; d < hd; d++) acc[d] = acc[d] + kv_at(vp, f32, ko + d) * p;
+                }
+                float inv = 1.0f / l;
+                float *o = out + (int64_t)r * nh * hd + (int64_t)hh * hd;
+                for (int d = 0; d < hd; d++) o[d] = acc[d] * inv;
+            }
+        }
+}
+
 /* ------------------------------------------------------------------ model */
 
 typedef struct { int type; const uint8_t *data; int64_t rows, cols; } or_tensor;
@@ -907,7 +958,7 @@ int or_model_step(or_model *m, int token, int pos, float *logits) {
         const uint8_t *kb = (const uint8_t *)m->kc[l] + (size_t)from * kvd * es;
         const uint8_t *vb = (const uint8_t *)m->vc[l] + (size_t)from * kvd * es;
         int flash = hd == 128 && (nh == 4 * nkv || nh == 8 * nkv);
-        int splits = flash ? or_cpu_decode_splits(count, 1, (int)nkv, c->workers) : 1;
+        int splits = flash ? or_cpu_decode_splits(count, c->attn_rows > 0 ? c->attn_rows : 1, (int)nkv, c->workers) : 1;
         or_attend(m->q, kb, vb, c->kv_f32, (int)nh, (int)nkv, (int)hd, count, splits, scale, flash ? 0 : 1, m->ao);
         linear(m, &L->o, m->ao, m->y);
         for (int64_t i = 0; i < h; i++) m->hs[i] = m->hs[i] + m->y[i];
@@ -927,6 +978,91 @@ int or_model_step(or_model *m, int token, int pos, float *logits) {
         }
         for (int64_t i = 0; i < h; i++) m->hs[i] = m->hs[i] + m->y[i];
     }
+    or_rmsnorm(m->hs, (const float *)m->out_norm.data, h, c->eps, 0, m->xn);
+    linear(m, &m->head, m->xn, m->logits);
+    if (logits) memcpy(logits, m->logits, sizeof(float) * (size_t)c->vocab);
+    return or_argmax(m->logits, c->vocab);
+}
+
+/* The FFN sublayer of one row in place on hs (CausalLM.residentLayer steps
+ * 7-10; the same per row in the many-row forward). */
+static void ffn_row(or_model *m, or_layer *L, float *hs) {
+    or_config *c = &m->c;
+    int64_t h = c->hidden;
+    or_rmsnorm(hs, (const float *)L->ffn_norm.data, h, c->eps, 0, m->xn);
+    if (c->n_experts > 0) {
+        moe_ffn(m, L, m->xn, m->y);
+    } else {
+        int64_t f = c->ffn;
+        linear(m, &L->gate, m->xn, m->g);
+        linear(m, &L->up, m->xn, m->u);
+        if (f % 256 == 0) or_glu_exp(m->g, m->u, f, m->g);
+        else or_glu_tanh(m->g, m->u, f, m->g);
+        linear(m, &L->down, m->g, m->y);
+    }
+    for (int64_t i = 0; i < h; i++) hs[i] = hs[i] + m->y[i];
+}
+
+/* CausalLM.stepSeq with n > 1 (L/model/CausalLM.cajeta:801-883) →
+ * forwardRowsBatched (:2873): every row through a layer before the next
+ * layer; each row's norms, projections (the many-row kernels equal the
+ * one-row kernel column by column, T/selftest/CpuInt8MatVecTest.cajeta:225-300),
+ * RoPE and K/V append as in a decode step; the attention of all rows once
+ * their K/V are appended (the prefill attend above, served at head size 128,
+ * AttnKernel.cpuAttnServes :4439-4447); the tail on the last row only
+ * (interior argmaxes are discarded, :793-799). Served like the MI355X
+ * engine serves it: dense models at head size 128 whose projections read
+ * int8 packs; anything else prefills one decode step a position. */
+int or_model_prefill(or_model *m, const int32_t *tokens, int n, int start, float *logits) {
+    or_config *c = &m->c;
+    int64_t h = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv;
+    int64_t kvd = nkv * hd, qd = nh * hd;
+    if (n <= 0) return -1;
+    int rows_form = n > 1 && hd == 128 && c->n_experts == 0;
+    for (int l = 0; rows_form && l < c->n_layers; l++) {
+        const or_tensor *ws[4] = {&m->L[l].q, &m->L[l].o, &m->L[l].gate, &m->L[l].down};
+        for (int i = 0; i < 4; i++)
+            if (ws[i]->type == OR_Q4_0 || ws[i]->type == OR_MXFP4 || ws[i]->type == OR_F32) rows_form = 0;
+    }
+    if (!rows_form) {
+        int t = -1;
+        for (int r = 0; r < n; r++) t = or_model_step(m, tokens[r], start + r, r == n - 1 ? logits : NULL);
+        return t;
+    }
+    float scale = 1.0f / sqrtf((float)hd);
+    float *HS = (float *)malloc(sizeof(float) * (size_t)(n * h));
+    float *Q = (float *)malloc(sizeof(float) * (size_t)(n * qd));
+    float *AO = (float *)malloc(sizeof(float) * (size_t)(n * qd));
+    for (int r = 0; r < n; r++) embed_row(m, tokens[r], HS + (int64_t)r * h);
+    for (int l = 0; l < c->n_layers; l++) {
+        or_layer *L = &m->L[l];
+        for (int r = 0; r < n; r++) {
+            int pos = start + r;
+            or_rmsnorm(HS + (int64_t)r * h, (const float *)L->attn_norm.data, h, c->eps, 0, m->xn);
+            linear(m, &L->q, m->xn, Q + (int64_t)r * qd);
+            linear(m, &L->k, m->xn, m->k);
+            linear(m, &L->v, m->xn, m->v);
+            or_rope(Q + (int64_t)r * qd, (int)nh, (int)hd, pos, m->inv);
+            or_rope(m->k, (int)nkv, (int)hd, pos, m->inv);
+            for (int64_t i = 0; i < kvd; i++) {
+                int64_t at = (int64_t)pos * kvd + i;
+                if (c->kv_f32) { ((float *)m->kc[l])[at] = m->k[i]; ((float *)m->vc[l])[at] = m->v[i]; }
+                else { ((uint16_t *)m->kc[l])[at] = or_f32_to_f16(m->k[i]); ((uint16_t *)m->vc[l])[at] = or_f32_to_f16(m->v[i]); }
+            }
+        }
+        int window = (c->swa_window > 0 && (l % 2) == 0) ? c->swa_window : 0;
+        or_prefill_attend(Q, m->kc[l], m->vc[l], c->kv_f32, (int)nh, (int)nkv, (int)hd, start, n, window, scale, AO);
+        for (int r = 0; r < n; r++) {
+            float *hs = HS + (int64_t)r * h;
+            linear(m, &L->o, AO + (int64_t)r * qd, m->y);
+            for (int64_t i = 0; i < h; i++) hs[i] = hs[i] + m->y[i];
+            ffn_row(m, L, hs);
+        }
+    }
+    memcpy(m->hs, HS + (int64_t)(n - 1) * h, sizeof(float) * (size_t)h);
+    memcpy(m->q, Q + (int64_t)(n - 1) * qd, sizeof(float) * (size_t)qd);
+    memcpy(m->ao, AO + (int64_t)(n - 1) * qd, sizeof(float) * (size_t)qd);
+    free(HS); free(Q); free(AO);
     or_rmsnorm(m->hs, (const float *)m->out_norm.data, h, c->eps, 0, m->xn);
     linear(m, &m->head, m->xn, m->logits);
     if (logits) memcpy(logits, m->logits, sizeof(float) * (size_t)c->vocab);

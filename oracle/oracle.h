@@ -77,6 +77,14 @@ void or_attend(const float *q, const void *kplane, const void *vplane, int kv_f3
                int mode, float *out);
 int  or_cpu_decode_splits(int count, int rows, int n_kv, int workers);
 
+/* prefill attention for `rows` consecutive query rows at positions
+ * start .. start+rows-1 of one sequence (hd 128): q rows [rows][n_h*hd], the
+ * planes position-major as above and already holding every row's K/V;
+ * window > 0 cuts each row to its last `window` positions. */
+void or_prefill_attend(const float *q, const void *kplane, const void *vplane, int kv_f32,
+                       int n_h, int n_kv, int hd, int start, int rows, int window, float scale,
+                       float *out);
+
 /* ---- whole-model decode (CausalLM.residentLayer order) ---- */
 typedef struct or_model or_model;
 
@@ -87,6 +95,7 @@ typedef struct {
     int32_t workers;       /* CPU worker count the attention split choice uses */
     int32_t n_experts, n_used, norm_topk, expert_ffn;
     int32_t swa_window;    /* >0: layers with (layer % 2 == 0) attend the last swa_window positions */
+    int32_t attn_rows;     /* rows of the decode batch the split rule divides the workers over (0: 1) */
 } or_config;
 
 or_model *or_model_new(const or_config *cfg);
@@ -98,6 +107,11 @@ int       or_model_bind(or_model *m, const char *name, int type, const void *dat
  * and returns the greedy argmax. */
 int       or_model_step(or_model *m, int token, int pos, float *logits);
 void      or_model_reset(or_model *m);
+/* A prefill chunk: tokens[0..n) at positions start .. start+n-1 through
+ * every layer as rows (head size 128: the prefill attention; otherwise one
+ * decode step a row), then the tail on the last row. Writes its logits if
+ * non-null and returns their greedy argmax. */
+int       or_model_prefill(or_model *m, const int32_t *tokens, int n, int start, float *logits);
 /* The last step's buffers as the last layer left them: 0 hs, 1 rotated q,
  * 2 attention output, 3 SiLU·up activation, 4 logits. Returns the length. */
 int64_t   or_model_trace(or_model *m, int what, float *out, int64_t n);

@@ -29,7 +29,7 @@ class Config(ctypes.Structure):
                 ("n_layers", "hidden", "n_heads", "n_kv", "head_dim", "ffn", "vocab", "ctx")] + \
                [("eps", ctypes.c_float), ("theta", ctypes.c_float)] + \
                [(n, ctypes.c_int32) for n in
-                ("kv_f32", "workers", "n_experts", "n_used", "norm_topk", "expert_ffn", "swa_window")]
+                ("kv_f32", "workers", "n_experts", "n_used", "norm_topk", "expert_ffn", "swa_window", "attn_rows")]
 
 
 def load(path):
@@ -72,6 +72,8 @@ def _configure(L):
             "or_unpermute_rows": (None, [P, P, I64, I64, I32]),
             "or_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, F, I32, P]),
             "or_cpu_decode_splits": (I32, [I32, I32, I32, I32]),
+            "or_prefill_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, I32, F, P]),
+            "or_model_prefill": (I32, [P, P, I32, I32, P]),
             "or_expf": (F, [F]),
             "or_model_new": (P, [ctypes.POINTER(Config)]), "or_model_free": (None, [P]),
             "or_model_bind": (I32, [P, ctypes.c_char_p, I32, P, I64, I64]),
@@ -206,6 +208,14 @@ def expf(x):
     return np.array([lib().or_expf(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
 
 
+def prefill_attend(q, kplane, vplane, n_h, n_kv, hd, start, rows, window, scale, kv_f32=False):
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.empty(rows * n_h * hd, np.float32)
+    lib().or_prefill_attend(_p(q), _p(np.ascontiguousarray(kplane)), _p(np.ascontiguousarray(vplane)), int(kv_f32),
+                            n_h, n_kv, hd, start, rows, window, scale, _p(out))
+    return out
+
+
 def cpu_decode_splits(count, rows, n_kv, workers):
     return lib().or_cpu_decode_splits(count, rows, n_kv, workers)
 
@@ -232,6 +242,14 @@ class Model:
         lg = np.empty(self.cfg.vocab, np.float32) if want_logits else None
         t = lib().or_model_step(self.h, token, pos, _p(lg) if want_logits else None)
         return t, lg
+
+    def prefill(self, tokens, start, want_logits=True):
+        """A prefill chunk at positions start.. (the many-row forward); the
+        greedy token and logits of its last row."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        lg = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        tok = lib().or_model_prefill(self.h, _p(t), int(t.size), int(start), _p(lg) if want_logits else None)
+        return tok, lg
 
     def reset(self):
         lib().or_model_reset(self.h)

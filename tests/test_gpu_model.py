@@ -18,14 +18,17 @@ def say(*a):
     print(*a, flush=True)
 
 
-def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1):
-    """Greedy-decode `prompt` + n_gen on both sides; compare every step."""
+def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1, chunk=512):
+    """Greedy-decode `prompt` + n_gen on both sides; compare every step. The
+    prompt goes through each side's prefill (prefill chunks on dense head-size-
+    128 models, decode steps otherwise)."""
     from oracle.gguf_reader import GgufReader, oracle_model
     r = GgufReader(image if image is not None else path)
     om, cfg = oracle_model(r, ctx=ctx)
     opts = pkg.EngineOptions(path)
     opts.ctx = ctx
     opts.maxSeqs = 1
+    opts.prefillChunk = chunk
     eng = pkg.LlmEngine.load(opts)
     try:
         eng.reset()
@@ -40,13 +43,14 @@ def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1):
             else:
                 gpu_logits.append(None)
         toks = list(prompt)
-        ref_toks, ref_logits = [], []
-        for p in range(len(prompt) + n_gen - 1):
+        t, lg = om.prefill(prompt, 0)
+        ref_toks, ref_logits = [t], [lg]
+        toks.append(t)
+        for p in range(len(prompt), len(prompt) + n_gen - 1):
             t, lg = om.step(toks[p], p)
-            if p >= len(prompt) - 1:
-                ref_toks.append(t)
-                ref_logits.append(lg)
-                toks.append(t)
+            ref_toks.append(t)
+            ref_logits.append(lg)
+            toks.append(t)
         worst, same = 0.0, True
         for g, o in zip(gpu_logits, ref_logits):
             if g is not None:
@@ -69,6 +73,70 @@ def test_reference_toy_fixture_greedy_parity(gpu, name):
     assert g == o, "tokens differ: gpu %s oracle %s" % (g, o)
     assert err <= LOGIT_TOL, err
     assert len(set(g)) > 1
+
+
+def test_prefill_chunks_are_invisible(gpu):
+    """A 45-token prompt as one chunk and as chunks of 7: chunking changes
+    nothing (every row's arithmetic is the same), both against the oracle's
+    prefill of the whole prompt."""
+    say("prefill chunks")
+    path = os.path.join(GOLD, "toy-routable.gguf")
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, 256, 45).tolist()
+    g1, o1, e1 = run_pair(gpu, path, None, prompt, 12, 256, chunk=512)
+    b1 = run_pair.bit_identical
+    g7, o7, e7 = run_pair(gpu, path, None, prompt, 12, 256, chunk=7)
+    b7 = run_pair.bit_identical
+    assert g1 == o1 and g7 == o7 and g1 == g7
+    assert b1 and b7, (e1, e7)
+
+
+def batch_case(gpu, path, image, prompts, steps, ctx):
+    """Prefill every prompt into its own slot, decode all slots together;
+    the oracle decodes each sequence alone with the batch's split rule."""
+    from oracle.gguf_reader import GgufReader, oracle_model
+    n = len(prompts)
+    opts = gpu.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = n
+    eng = gpu.LlmEngine.load(opts)
+    try:
+        first = []
+        for s, p in enumerate(prompts):
+            eng.prefill(p, seq=s)
+            first.append(int(eng.preds(len(p), seq=s)[-1]))
+        out = eng.decodeBatch(list(range(n)), steps)
+        last = eng.batchLogits()
+    finally:
+        eng.close()
+    r = GgufReader(image if image is not None else path)
+    worst, same = 0.0, True
+    for s, p in enumerate(prompts):
+        om, _ = oracle_model(r, ctx=ctx, attn_rows=n)
+        t, _ = om.prefill(p, 0)
+        toks, lg = [t], None
+        for i in range(steps):
+            t, lg = om.step(toks[-1], len(p) + i)
+            toks.append(t)
+        om.close()
+        assert first[s] == toks[0], "slot %d first token" % s
+        assert out[:, s].tolist() == toks[1:], "slot %d: gpu %s oracle %s" % (s, out[:, s].tolist(), toks[1:])
+        worst = max(worst, float(np.max(np.abs(last[s] - lg))))
+        same = same and np.array_equal(last[s].view(np.uint32), lg.view(np.uint32))
+    say("  batch of %d: last-step logits max-abs %.3g, bit-identical %s" % (n, worst, same))
+    return out, worst, same
+
+
+@pytest.mark.parametrize("n", [3, 32])
+def test_batched_decode_parity_toy_gqa8(gpu, n):
+    """Batched decode (a row a sequence, the split rule over all rows' kv
+    heads) on the reference's toy GGUF with 8 query heads a kv head."""
+    say("batch toy gqa8", n)
+    rng = np.random.default_rng(30 + n)
+    prompts = [rng.integers(0, 256, int(rng.integers(2, 60))).tolist() for _ in range(n)]
+    out, err, same = batch_case(gpu, os.path.join(GOLD, "toy-routable-gqa8.gguf"), None, prompts, 10, 256)
+    assert err <= LOGIT_TOL and same
+    assert len(set(out.ravel().tolist())) > 1
 
 
 def synth(pkg, spec, name, seed):
@@ -122,6 +190,20 @@ def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
     assert g == o
     assert err <= LOGIT_TOL, err
     assert run_pair.bit_identical
+
+
+def test_c4_shape_q8_0_batched_decode_parity(gpu):
+    """BASELINE config 4's batched decode at small scale: Q8_0 8B shapes at two
+    layers, three sequences at different positions decoded together."""
+    say("model c4x2 batch")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=32000;eps=1e-5;theta=500000;" \
+           "wtype=q8_0;head=q8_0;embd=q8_0;ctx=512"
+    path, img = synth(gpu, spec, "t_c4x2b", 81)
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, 32000, k).tolist() for k in (7, 30, 65)]
+    out, err, same = batch_case(gpu, path, img, prompts, 6, 160)
+    gpu.image_free("t_c4x2b")
+    assert err <= LOGIT_TOL and same
 
 
 def test_c5_moe_shape_two_layers_greedy_parity(gpu):

@@ -202,6 +202,44 @@ def check_attention(O):
     return not bad, bad
 
 
+def prefill_ref(q, k, v, nh, nkv, hd, start, rows, window, scale):
+    """float64 causal attention of rows at positions start.. over planes that
+    hold every row's K/V (row r sees positions [t0, start + r])."""
+    out = np.zeros((rows, nh * hd))
+    kd = k.astype(np.float64).reshape(-1, nkv, hd)
+    vd = v.astype(np.float64).reshape(-1, nkv, hd)
+    qd = q.astype(np.float64).reshape(rows, nh, hd)
+    for r in range(rows):
+        count = start + r + 1
+        t0 = count - window if window and count > window else 0
+        for h in range(nh):
+            g = h // (nh // nkv)
+            s_ = kd[t0:count, g, :] @ qd[r, h] * scale
+            p = np.exp(s_ - s_.max())
+            out[r, h * hd:(h + 1) * hd] = (p / p.sum()) @ vd[t0:count, g, :]
+    return out.ravel()
+
+
+def check_prefill_attention(O):
+    """The prefill attend (one pass a row and head, q pre-scaled) against
+    float64 causal softmax attention, over offsets, GQA groups and a window."""
+    bad = []
+    hd = 128
+    for nh, nkv, start, rows, window in ((8, 2, 0, 37, 0), (32, 8, 100, 20, 0), (4, 1, 5, 9, 6), (8, 8, 0, 3, 0),
+                                         (16, 2, 300, 64, 0)):
+        rng = np.random.default_rng(start + rows + nh)
+        count = start + rows
+        q = (rng.standard_normal(rows * nh * hd) * 2).astype(np.float32)
+        k = rng.standard_normal((count, nkv * hd)).astype(np.float16)
+        v = rng.standard_normal((count, nkv * hd)).astype(np.float16)
+        scale = float(np.float32(1.0 / math.sqrt(hd)))
+        got = O.prefill_attend(q, k.view(np.uint16), v.view(np.uint16), nh, nkv, hd, start, rows, window, scale)
+        e = rel_err(got, prefill_ref(q, k, v, nh, nkv, hd, start, rows, window, scale))
+        if e > 2e-5:
+            bad.append((nh, nkv, start, rows, window, e))
+    return not bad, bad
+
+
 def check_unpermute(O):
     """Checkpoint.unpermuteRows undoes the GGUF llama q/k row permutation:
     HF row (h, a, b) sits at GGUF row (h, b, a) — built here by reshape."""
@@ -314,6 +352,56 @@ def test_argmax_first_occurrence(O):
 def test_attention_against_float64(O):
     ok, bad = check_attention(O)
     assert ok, bad
+
+
+def test_prefill_attention_against_float64(O):
+    ok, bad = check_prefill_attention(O)
+    assert ok, bad
+
+
+def test_prefill_first_row_is_the_decode_attention(O):
+    """At one position the prefill attend is softmax over one key: the output
+    is that key's V row exactly (weight exp(0) = 1, l = 1), as the decode
+    form's is."""
+    rng = np.random.default_rng(9)
+    nh, nkv, hd = 8, 2, 128
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((1, nkv * hd)).astype(np.float16)
+    v = rng.standard_normal((1, nkv * hd)).astype(np.float16)
+    got = O.prefill_attend(q, k.view(np.uint16), v.view(np.uint16), nh, nkv, hd, 0, 1, 0, 0.088)
+    want = np.repeat(v.astype(np.float32).reshape(nkv, 1, hd), nh // nkv, axis=1).ravel()
+    assert np.array_equal(got, want)
+
+
+def test_model_prefill_matches_decode_steps(O):
+    """A prefill chunk through the many-row forward (prefill attend) against
+    the same prompt as decode steps (split-K attend), on the reference's toy
+    GGUF: the attention forms round differently, so the logits agree to the
+    packs' rounding and the greedy token is the same; the K/V the chunk
+    leaves continue decoding to the same tokens."""
+    from oracle.gguf_reader import GgufReader, oracle_model
+    r = GgufReader(os.path.join(GOLD, "gguf", "toy-routable.gguf"))
+    a, _ = oracle_model(r, ctx=64)
+    b, _ = oracle_model(r, ctx=64)
+    toks = [3, 141, 59, 26, 5, 77, 200, 13, 9]
+    ta, la = a.prefill(toks, 0)
+    for p, t in enumerate(toks):
+        tb, lb = b.step(t, p)
+    assert ta == tb
+    assert float(np.max(np.abs(la - lb)) / np.max(np.abs(lb))) < 1e-4
+    ga, gb = [ta], [tb]
+    for i in range(6):
+        ga.append(a.step(ga[-1], len(toks) + i)[0])
+        gb.append(b.step(gb[-1], len(toks) + i)[0])
+    assert ga == gb
+    # a chunk split in two: the same bits (the rows' arithmetic does not
+    # depend on the chunking)
+    c, _ = oracle_model(r, ctx=64)
+    c.prefill(toks[:4], 0)
+    tc, lc = c.prefill(toks[4:], 4)
+    assert tc == ta and np.array_equal(lc.view(np.uint32), la.view(np.uint32))
+    for m in (a, b, c):
+        m.close()
 
 
 def test_decode_splits_closed_form(O):
@@ -442,6 +530,7 @@ PLANTS = {
     6: ("tanh-form SiLU chunks stepped by one", check_glu_structure),
     7: ("split-K without the rescale on a new max", check_attention),
     8: ("q/k rows unpermuted with the halves swapped", check_unpermute),
+    9: ("prefill scores from one lane partial", check_prefill_attention),
 }
 
 
