@@ -14,15 +14,21 @@
 //   Q4_K : sumi = Σ_s sc_s·dot_s, dmins = Σ_s mn_s·bsum_s (ints);
 //          acc = (acc + (d·xs)·sumi) − (dmin·xs)·dmins per block
 //          (Quant.q4kMatVecIntoQ8, io/Quant.cajeta:3374-3445)
+// Those per-output f32 steps (four VALU operations per output and 32-block
+// for Q8_0) bound the kernel at large column counts, not the matrix cores.
 //
 // MFMA 16x16x32 int8 lane layout (checked on the part): lane l supplies A row
 // l % 16 and B column l % 16, elements k = 8·(l / 16) .. +7, and receives
-// D[4·(l / 16) + i][l % 16], i < 4. A wave owns 16 weight rows × 16 columns;
-// a workgroup puts up to 4 waves side by side over the columns.
+// D[4·(l / 16) + i][l % 16], i < 4.
 //
-// Activations are the per-column packs (320-byte blocks, per-256 scale for
-// Q4_K, per-32 scales for Q8_0) `xp_stride` bytes apart; outputs `y_stride`
-// floats apart. The weights are the GEMV's prepared rows.
+// Tiling: a workgroup of 4 waves owns 64 weight rows (16 a wave) × 16·NT
+// columns. The K dimension runs in groups of 256 elements (8 Q8_0 blocks, one
+// Q4_K block). Each group's activation packs (the 320-byte block of every
+// column of the tile, verbatim) are staged in LDS once for the 4 waves; each
+// wave streams its own 16 rows' weights straight into registers. Both are
+// requested one group ahead, so the loads of group g+1 are in flight while
+// group g computes. Column tiles of one row block are adjacent in dispatch
+// order and share the rows' weights in cache.
 #include "common.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -34,142 +40,502 @@ DEV v4i mfma_i8(long a, long b) {
 
 DEV long ld8(const uint8_t *p) { return *(const long *)p; }
 
-// Q8_0: prepared row [qs nb32·32][d nb32·2 → pad 16].
-DEV void gemm_q80_tile(const cj_gemv_args &a, int64_t r0, int64_t c0, float (&acc)[4]) {
-    const int lane = threadIdx.x & 63, q = lane >> 4, m = lane & 15;
+#define GEMM_CS 336   // LDS bytes a staged column (the 320-byte block, padded against bank conflicts)
+
+// The group's activation blocks of the tile's columns into registers (NV
+// 16-byte words a thread), then into LDS: word w of column c at c·GEMM_CS + 16w.
+template <int NT>
+struct BStage {
+    static constexpr int CT = 16 * NT, WORDS = CT * 20, NV = (WORDS + 255) / 256;
+    u32x4 v[NV];
+};
+
+template <int NT>
+DEV void b_fetch(BStage<NT> &s, const cj_gemv_args &a, int64_t c0, int64_t g) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) {
+        const int w = min(t + 256 * i, BStage<NT>::WORDS - 1);
+        const int64_t c = min(c0 + w / 20, (int64_t)a.batch - 1);
+        s.v[i] = *(const u32x4 *)(a.xp + c * a.xp_stride + g * 320 + 16 * (w % 20));
+    }
+}
+
+template <int NT>
+DEV void b_store(const BStage<NT> &s, uint8_t *lds) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) {
+        const int w = t + 256 * i;
+        if (w < BStage<NT>::WORDS) *(u32x4 *)(lds + (w / 20) * GEMM_CS + 16 * (w % 20)) = s.v[i];
+    }
+}
+
+// ------------------------------------------------------------------- Q8_0
+
+// Prepared row: [qs nb32·32][d nb32·2 → padded to 16]. A lane's weights of a
+// group: 8 bytes of each of the 8 blocks of its A row, and the 8 f16 scales
+// of each of its 4 output rows (one 16-byte word a row; the scale array is
+// padded to 16 bytes, so a short last group stays inside it).
+struct Q80A {
+    long q[8];
+    uint4 d[4];
+};
+
+DEV void q80_fetch(Q80A &A, const uint8_t *wa, const uint8_t *const (&wd)[4], int64_t g, int nj) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) A.q[j] = ld8(wa + (8 * g + min(j, nj - 1)) * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) A.d[i] = *(const uint4 *)(wd[i] + 16 * g);
+}
+
+template <int NT>
+DEV void gemm_q80(const cj_gemv_args &a, uint8_t *lds) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
+    const int64_t c0 = (int64_t)blockIdx.x * 16 * NT;
+    const int64_t r0 = (int64_t)blockIdx.y * 64 + 16 * wave;
     const int64_t nb32 = a.cols / 32, ngrp = (a.cols + 255) / 256;
-    const int64_t ra = min(r0 + m, a.rows - 1);                  // the A row this lane supplies
-    const int64_t cb = min(c0 + m, (int64_t)a.batch - 1);        // the B column this lane supplies
-    const uint8_t *wa = a.w + ra * a.row_bytes + 8 * q;
-    const uint8_t *xb = a.xp + cb * a.xp_stride + 8 * q;
-    // the lane's output rows (4q .. 4q+3) and column m
+    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + 8 * q;
     const uint8_t *wd[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
-    const uint8_t *xs_base = a.xp + min(c0 + m, (int64_t)a.batch - 1) * a.xp_stride;
+    float acc[NT][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = 0.0f;
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+    BStage<NT> bs;
+    Q80A A, An;
+    b_fetch<NT>(bs, a, c0, 0);
+    q80_fetch(A, wa, wd, 0, (int)min((int64_t)8, nb32));
     for (int64_t g = 0; g < ngrp; g++) {
         const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-        long af[8], bf[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int64_t blk = 8 * g + min(j, nj - 1);
-            af[j] = ld8(wa + blk * 32);
-            bf[j] = ld8(xb + g * 320 + 32 * min(j, nj - 1));
+        __syncthreads();   // the previous group's LDS reads are done
+        b_store<NT>(bs, lds);
+        __syncthreads();
+        if (g + 1 < ngrp) {
+            b_fetch<NT>(bs, a, c0, g + 1);
+            q80_fetch(An, wa, wd, g + 1, (int)min((int64_t)8, nb32 - 8 * (g + 1)));
         }
-        const float4 x0 = *(const float4 *)(xs_base + g * 320 + 288);
-        const float4 x1 = *(const float4 *)(xs_base + g * 320 + 304);
-        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        // the group's 8 f16 scales of each output row in one 16-byte load (the
-        // scale array is padded to 16 bytes, so a short last group stays in it)
-        uint16_t dh[4][8];
+        float dr[4][8];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint4 h = *(const uint4 *)(wd[i] + 16 * g);
-            const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+            const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
 #pragma unroll
-            for (int j = 0; j < 8; j++) dh[i][j] = (uint16_t)(hw[j >> 1] >> (16 * (j & 1)));
+            for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
         }
-        float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (j < nj) {
-                const v4i d = mfma_i8(af[j], bf[j]);
+        for (int n = 0; n < NT; n++) {
+            const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
+            const float4 x0 = *(const float4 *)(col + 288), x1 = *(const float4 *)(col + 304);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int i = 0; i < 4; i++) fs[i] = __fadd_rn(fs[i], __fmul_rn(__fmul_rn(h2f(dh[i][j]), xs[j]), (float)d[i]));
+            for (int j = 0; j < 8; j++) {
+                if (j < nj) {
+                    const v4i d = mfma_i8(A.q[j], *(const long *)(col + 32 * j + 8 * q));
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        fs[i] = __fadd_rn(fs[i], __fmul_rn(__fmul_rn(dr[i][j], xs[j]), (float)d[i]));
+                }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] = __fadd_rn(acc[i], fs[i]);
+            for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], fs[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (g + 1 < ngrp) A = An;
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int64_t c = c0 + 16 * n + m;
+        if (c >= a.batch) continue;
+        float *y = a.y + c * a.y_stride + a.y_off;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t r = r0 + 4 * q + i;
+            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
+        }
     }
 }
 
-// Q4_K: the GEMV's chunk-major prepared row — qs piece c (16 bytes) of block
-// b at (c·nb + b)·16, the 16-byte header {d, dmin, scales[12]} at 128·nb + 16·b.
-// Group g (elements 64g .. 64g+63) of a block is qs bytes 32g .. 32g+31:
-// low nibbles are sub-block 2g, high nibbles sub-block 2g+1, so one 8-byte
-// load (bytes 32g + 8q ..) feeds both sub-blocks' MFMAs.
-DEV void gemm_q4k_tile(const cj_gemv_args &a, int64_t r0, int64_t c0, float (&acc)[4]) {
-    const int lane = threadIdx.x & 63, q = lane >> 4, m = lane & 15;
+// ------------------------------------------------------------------- Q4_K
+
+// The GEMV's chunk-major prepared row: qs piece c (16 bytes) of block b at
+// (c·nb + b)·16, the 16-byte header {d, dmin, scales[12]} at 128·nb + 16·b.
+// Group g4 (elements 64·g4 .. +63) of a block is qs bytes 32·g4 .. +31: low
+// nibbles are sub-block 2·g4, high nibbles 2·g4 + 1, so one 8-byte load
+// (bytes 32·g4 + 8q ..) feeds both sub-blocks' MFMAs.
+struct Q4kA {
+    long q[4];
+    uint4 h[4];
+};
+
+DEV void q4k_fetch_a(Q4kA &A, const uint8_t *wa, const uint8_t *const (&wh)[4], int64_t nb, int64_t b, int q) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++) {
+        const int byte = 32 * g4 + 8 * q;
+        A.q[g4] = ld8(wa + ((int64_t)(byte >> 4) * nb + b) * 16 + (byte & 15));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) A.h[i] = *(const uint4 *)(wh[i] + b * 16);
+}
+
+template <int NT>
+DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
+    const int64_t c0 = (int64_t)blockIdx.x * 16 * NT;
+    const int64_t r0 = (int64_t)blockIdx.y * 64 + 16 * wave;
     const int64_t nb = a.cols / 256;
-    const int64_t ra = min(r0 + m, a.rows - 1);
-    const int64_t cb = min(c0 + m, (int64_t)a.batch - 1);
-    const uint8_t *wa = a.w + ra * a.row_bytes;
-    const uint8_t *xb = a.xp + cb * a.xp_stride;
+    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes;
     const uint8_t *wh[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wh[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb * 128;
-    const uint8_t *xo = a.xp + min(c0 + m, (int64_t)a.batch - 1) * a.xp_stride;   // the lane's output column
-    const uint32_t M = 0x0F0F0F0Fu;
+    const uint64_t M = 0x0F0F0F0F0F0F0F0Full;
+    float acc[NT][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = 0.0f;
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+    BStage<NT> bs;
+    Q4kA A, An;
+    b_fetch<NT>(bs, a, c0, 0);
+    q4k_fetch_a(A, wa, wh, nb, 0, q);
     for (int64_t b = 0; b < nb; b++) {
-        long wq[4], alo[4], ahi[4];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int byte = 32 * g + 8 * q;                           // qs byte of this lane's 8
-            wq[g] = ld8(wa + ((int64_t)(byte >> 4) * nb + b) * 16 + (byte & 15));
-            alo[g] = ld8(xb + b * 320 + 64 * g + 8 * q);
-            ahi[g] = ld8(xb + b * 320 + 64 * g + 32 + 8 * q);
+        __syncthreads();
+        b_store<NT>(bs, lds);
+        __syncthreads();
+        if (b + 1 < nb) {
+            b_fetch<NT>(bs, a, c0, b + 1);
+            q4k_fetch_a(An, wa, wh, nb, b + 1, q);
         }
-        const int4 s0 = *(const int4 *)(xo + b * 320 + 256), s1 = *(const int4 *)(xo + b * 320 + 272);
-        const float xs = *(const float *)(xo + b * 320 + 288);
-        uint4 hd[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) hd[i] = *(const uint4 *)(wh[i] + b * 16);
-        int dot[4][8];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint64_t w = (uint64_t)wq[g];
-            const long lo = (long)(w & (((uint64_t)M << 32) | M));
-            const long hi = (long)((w >> 4) & (((uint64_t)M << 32) | M));
-            const v4i dl = mfma_i8(lo, alo[g]);
-            const v4i dh = mfma_i8(hi, ahi[g]);
-#pragma unroll
-            for (int i = 0; i < 4; i++) { dot[i][2 * g] = dl[i]; dot[i][2 * g + 1] = dh[i]; }
-        }
-        const int bs[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        // the 4 rows' 6-bit scales and mins, and their block scales
+        int sc[4][8], mn[4][8];
+        float dd[4], dm[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t A = hd[i].y, B = hd[i].z, C = hd[i].w;
-            int sumi = 0, dmins = 0;
+            const uint32_t X = A.h[i].y, Y = A.h[i].z, Z = A.h[i].w;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t a8 = (A >> (8 * j)) & 255, b8 = (B >> (8 * j)) & 255, c8 = (C >> (8 * j)) & 255;
-                const int sc_lo = (int)(a8 & 63), mn_lo = (int)(b8 & 63);
-                const int sc_hi = (int)((c8 & 15) | ((a8 >> 2) & 48)), mn_hi = (int)((c8 >> 4) | ((b8 >> 2) & 48));
-                sumi += __mul24(dot[i][j], sc_lo) + __mul24(dot[i][j + 4], sc_hi);
-                dmins += __mul24(bs[j], mn_lo) + __mul24(bs[j + 4], mn_hi);
+                const uint32_t a8 = (X >> (8 * j)) & 255, b8 = (Y >> (8 * j)) & 255, c8 = (Z >> (8 * j)) & 255;
+                sc[i][j] = (int)(a8 & 63);
+                mn[i][j] = (int)(b8 & 63);
+                sc[i][j + 4] = (int)((c8 & 15) | ((a8 >> 2) & 48));
+                mn[i][j + 4] = (int)((c8 >> 4) | ((b8 >> 2) & 48));
             }
-            const float d = h2f(hd[i].x), dmin = h2f(hd[i].x >> 16);
-            acc[i] = __fsub_rn(__fadd_rn(acc[i], __fmul_rn(__fmul_rn(d, xs), (float)sumi)),
-                               __fmul_rn(__fmul_rn(dmin, xs), (float)dmins));
+            dd[i] = h2f(A.h[i].x);
+            dm[i] = h2f(A.h[i].x >> 16);
+        }
+        long lo[4], hi[4];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            const uint64_t w = (uint64_t)A.q[g4];
+            lo[g4] = (long)(w & M);
+            hi[g4] = (long)((w >> 4) & M);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
+            // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
+            int sumi[4] = {0, 0, 0, 0}, dmins[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const v4i dl = mfma_i8(lo[g4], *(const long *)(col + 64 * g4 + 8 * q));
+                const v4i dh = mfma_i8(hi[g4], *(const long *)(col + 64 * g4 + 32 + 8 * q));
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    sumi[i] += __mul24(dl[i], sc[i][2 * g4]) + __mul24(dh[i], sc[i][2 * g4 + 1]);
+            }
+            const int4 s0 = *(const int4 *)(col + 256), s1 = *(const int4 *)(col + 272);
+            const float xs = *(const float *)(col + 288);
+            const int bsum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int s2 = 0; s2 < 8; s2++) dmins[i] += __mul24(bsum[s2], mn[i][s2]);
+                acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi[i])),
+                                      __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins[i]));
+            }
+            // one column tile at a time: the products of later tiles are not
+            // hoisted (their results would all be live at once)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (b + 1 < nb) A = An;
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int64_t c = c0 + 16 * n + m;
+        if (c >= a.batch) continue;
+        float *y = a.y + c * a.y_stride + a.y_off;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t r = r0 + 4 * q + i;
+            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
         }
     }
 }
 
-// Workgroup (column tile, row tile): 16 rows, and 16 columns a wave over the
-// workgroup's 1..4 waves. The column tiles of one row tile are adjacent in
-// dispatch order, so they run together and share the rows' weights in cache.
-template <int FMT>
-DEV void gemm_body(const cj_gemv_args &a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.y * 16;
-    const int64_t c0 = ((int64_t)blockIdx.x * waves + wave) * 16;
-    if (c0 >= a.batch) return;                     // uniform per wave; no barrier follows
-    float acc[4];
-    if (FMT == CJ_Q8_0) gemm_q80_tile(a, r0, c0, acc);
-    else gemm_q4k_tile(a, r0, c0, acc);
-    const int64_t c = c0 + (lane & 15);
-    if (c >= a.batch) return;
-    float *y = a.y + c * a.y_stride + a.y_off;
+// ----------------------------------------------- few columns: split K
+
+// For a handful of columns (batched decode) the weights dominate and the
+// output tile is small, so the K dimension is shared out: a workgroup of W
+// waves owns 16 rows × 16·NT columns, wave w takes the groups g ≡ w (mod W),
+// streaming its weights and the columns' pack blocks straight into registers
+// one group ahead, and hands each group's per-output terms to wave 0, which
+// folds them into the accumulators in group order (the reference's order,
+// exactly) through LDS, W groups a round.
+//   Q8_0: the group's fs (one value an output);
+//   Q4_K: the block's (d·xs)·sumi and (dmin·xs)·dmins (two values an output).
+template <int NT, int W>
+DEV void gemm_sk_q80(const cj_gemv_args &a) {
+    __shared__ __align__(16) float hand[W][NT * 4][64];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
+    const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
+    const int64_t nb32 = a.cols / 32, ngrp = (a.cols + 255) / 256;
+    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + 8 * q;
+    const uint8_t *wd[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int64_t r = r0 + 4 * (lane >> 4) + i;
-        if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[i]) : acc[i];
+    for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
+    const uint8_t *xc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) xc[n] = a.xp + min(c0 + 16 * n + m, (int64_t)a.batch - 1) * a.xp_stride;
+    float acc[NT][4];
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+    Q80A A, An;
+    if (wave < ngrp) q80_fetch(A, wa, wd, wave, (int)min((int64_t)8, nb32 - 8 * wave));
+    const int64_t rounds = (ngrp + W - 1) / W;
+    for (int64_t rd = 0; rd < rounds; rd++) {
+        const int64_t g = rd * W + wave;
+        float fs[NT][4];
+        if (g < ngrp) {
+            const int nj = (int)min((int64_t)8, nb32 - 8 * g);
+            // this group's pack blocks (hot in cache) as the group starts; the
+            // next group's weights (from HBM) a group ahead
+            long bq[NT][8];
+            float4 bx[NT][2];
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const uint8_t *col = xc[n] + g * 320;
+#pragma unroll
+                for (int j = 0; j < 8; j++) bq[n][j] = ld8(col + 32 * j + 8 * q);
+                bx[n][0] = *(const float4 *)(col + 288);
+                bx[n][1] = *(const float4 *)(col + 304);
+            }
+            if (g + W < ngrp) q80_fetch(An, wa, wd, g + W, (int)min((int64_t)8, nb32 - 8 * (g + W)));
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const float xs[8] = {bx[n][0].x, bx[n][0].y, bx[n][0].z, bx[n][0].w,
+                                     bx[n][1].x, bx[n][1].y, bx[n][1].z, bx[n][1].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (j < nj) {
+                        const v4i d = mfma_i8(A.q[j], bq[n][j]);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const uint32_t hw = j < 2 ? A.d[i].x : j < 4 ? A.d[i].y : j < 6 ? A.d[i].z : A.d[i].w;
+                            const float dj = h2f(hw >> (16 * (j & 1)));
+                            fs[n][i] = __fadd_rn(fs[n][i], __fmul_rn(__fmul_rn(dj, xs[j]), (float)d[i]));
+                        }
+                    }
+                }
+            }
+            if (g + W < ngrp) A = An;
+        }
+        if (wave > 0 && g < ngrp) {
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) hand[wave][4 * n + i][lane] = fs[n][i];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const int live = (int)min((int64_t)W, ngrp - rd * W);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], fs[n][i]);
+            for (int w = 1; w < live; w++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], hand[w][4 * n + i][lane]);
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int64_t c = c0 + 16 * n + m;
+        if (c >= a.batch) continue;
+        float *y = a.y + c * a.y_stride + a.y_off;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t r = r0 + 4 * q + i;
+            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
+        }
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) cj_gemm_q80(cj_gemv_args a) { gemm_body<CJ_Q8_0>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_gemm_q4k(cj_gemv_args a) { gemm_body<CJ_Q4_K>(a); }
+template <int NT>
+struct Q4kB {
+    long lo[NT][4], hi[NT][4];
+    int4 s0[NT], s1[NT];
+    float xs[NT];
+};
+
+template <int NT>
+DEV void q4k_fetch_b(Q4kB<NT> &B, const cj_gemv_args &a, int64_t c0, int64_t b, int q, int m) {
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const uint8_t *col = a.xp + min(c0 + 16 * n + m, (int64_t)a.batch - 1) * a.xp_stride + b * 320;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            B.lo[n][g4] = ld8(col + 64 * g4 + 8 * q);
+            B.hi[n][g4] = ld8(col + 64 * g4 + 32 + 8 * q);
+        }
+        B.s0[n] = *(const int4 *)(col + 256);
+        B.s1[n] = *(const int4 *)(col + 272);
+        B.xs[n] = *(const float *)(col + 288);
+    }
+}
+
+template <int NT, int W>
+DEV void gemm_sk_q4k(const cj_gemv_args &a) {
+    __shared__ __align__(16) float hand[W][NT * 8][64];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
+    const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
+    const int64_t nb = a.cols / 256;
+    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes;
+    const uint8_t *wh[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) wh[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb * 128;
+    const uint64_t M = 0x0F0F0F0F0F0F0F0Full;
+    float acc[NT][4];
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+    Q4kA A, An;
+    Q4kB<NT> B, Bn;
+    if (wave < nb) {
+        q4k_fetch_a(A, wa, wh, nb, wave, q);
+        q4k_fetch_b<NT>(B, a, c0, wave, q, m);
+    }
+    const int64_t rounds = (nb + W - 1) / W;
+    for (int64_t rd = 0; rd < rounds; rd++) {
+        const int64_t b = rd * W + wave;
+        float t1[NT][4], t2[NT][4];
+        if (b < nb) {
+            if (b + W < nb) {
+                q4k_fetch_a(An, wa, wh, nb, b + W, q);
+                q4k_fetch_b<NT>(Bn, a, c0, b + W, q, m);
+            }
+            int sc[4][8], mn[4][8];
+            float dd[4], dm[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t X = A.h[i].y, Y = A.h[i].z, Z = A.h[i].w;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t a8 = (X >> (8 * j)) & 255, b8 = (Y >> (8 * j)) & 255, c8 = (Z >> (8 * j)) & 255;
+                    sc[i][j] = (int)(a8 & 63);
+                    mn[i][j] = (int)(b8 & 63);
+                    sc[i][j + 4] = (int)((c8 & 15) | ((a8 >> 2) & 48));
+                    mn[i][j + 4] = (int)((c8 >> 4) | ((b8 >> 2) & 48));
+                }
+                dd[i] = h2f(A.h[i].x);
+                dm[i] = h2f(A.h[i].x >> 16);
+            }
+            long lo[4], hi[4];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const uint64_t w = (uint64_t)A.q[g4];
+                lo[g4] = (long)(w & M);
+                hi[g4] = (long)((w >> 4) & M);
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
+                int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const v4i dl = mfma_i8(lo[g4], B.lo[n][g4]);
+                    const v4i dh = mfma_i8(hi[g4], B.hi[n][g4]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        sumi[i] += __mul24(dl[i], sc[i][2 * g4]) + __mul24(dh[i], sc[i][2 * g4 + 1]);
+                }
+                const int bsum[8] = {B.s0[n].x, B.s0[n].y, B.s0[n].z, B.s0[n].w,
+                                     B.s1[n].x, B.s1[n].y, B.s1[n].z, B.s1[n].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int dmins = 0;
+#pragma unroll
+                    for (int s2 = 0; s2 < 8; s2++) dmins += __mul24(bsum[s2], mn[i][s2]);
+                    t1[n][i] = __fmul_rn(__fmul_rn(dd[i], B.xs[n]), (float)sumi[i]);
+                    t2[n][i] = __fmul_rn(__fmul_rn(dm[i], B.xs[n]), (float)dmins);
+                }
+            }
+            if (b + W < nb) { A = An; B = Bn; }
+        }
+        if (wave > 0 && b < nb) {
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    hand[wave][8 * n + i][lane] = t1[n][i];
+                    hand[wave][8 * n + 4 + i][lane] = t2[n][i];
+                }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const int live = (int)min((int64_t)W, nb - rd * W);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], t1[n][i]), t2[n][i]);
+            for (int w = 1; w < live; w++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], hand[w][8 * n + i][lane]), hand[w][8 * n + 4 + i][lane]);
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int64_t c = c0 + 16 * n + m;
+        if (c >= a.batch) continue;
+        float *y = a.y + c * a.y_stride + a.y_off;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t r = r0 + 4 * q + i;
+            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
+        }
+    }
+}
+
+// Kernels by column-tile width: 16·NT columns a workgroup.
+#define GEMM_KERNELS(NT)                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) cj_gemm_q80_n##NT(cj_gemv_args a) { \
+        __shared__ __align__(16) uint8_t lds[16 * NT * GEMM_CS];                           \
+        gemm_q80<NT>(a, lds);                                                              \
+    }                                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) cj_gemm_q4k_n##NT(cj_gemv_args a) { \
+        __shared__ __align__(16) uint8_t lds[16 * NT * GEMM_CS];                           \
+        gemm_q4k<NT>(a, lds);                                                              \
+    }
+GEMM_KERNELS(2)
+GEMM_KERNELS(4)
+
+// Split-K kernels: 16 rows × 16·NT columns a workgroup of 8 waves (the
+// widths whose registers fit two waves a SIMD without spilling).
+extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q80_n1(cj_gemv_args a) { gemm_sk_q80<1, 8>(a); }
+extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q80_n2(cj_gemv_args a) { gemm_sk_q80<2, 8>(a); }
+extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q4k_n1(cj_gemv_args a) { gemm_sk_q4k<1, 8>(a); }

@@ -63,9 +63,9 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"gatherRowsF32Kernel", "cj_embed"},
         {"routerTopKKernel", "cj_moe_route"},
         {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_cg_b16"},
-        {"q4kQ8WaveMatVecColsKernel", "cj_gemm_q4k"},
-        {"q80Q8X8RowsKernel", "cj_gemm_q80"},
-        {"q4kQ8X8RowsKernel", "cj_gemm_q4k"},
+        {"q4kQ8WaveMatVecColsKernel", "cj_gemm_sk_q4k_n1"},
+        {"q80Q8X8RowsKernel", "cj_gemm_sk_q80_n1"},
+        {"q4kQ8X8RowsKernel", "cj_gemm_sk_q4k_n1"},
         {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_cs_b16"},
     };
     return m;
@@ -235,15 +235,32 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
 
 bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K; }
 
-// One wave a 16-row × 16-column tile; up to 4 waves a workgroup side by side
-// over the columns.
+// Two kernels, chosen by shape. The tiled kernel (4 waves a 64-row ×
+// 16·NT-column tile over LDS-staged packs) when the row blocks and column
+// tiles make at least 256 workgroups (a CU's worth each) — tall projections,
+// many columns; otherwise the split-K kernel (8 waves sharing a 16-row
+// tile's K dimension), which makes 4× more, smaller workgroups for short,
+// wide products at few columns. Measured on MI355X at 32 columns (Q8_0):
+// gate|up and head 2.1-2.3 TB/s tiled vs 1.1 split-K; q|k|v, o and down
+// 0.8-1.1 TB/s split-K vs 0.3-0.5 tiled.
 int run_gemm(const cj_gemv_args &a) {
     if (!gemm_supported(a.type)) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
     if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
-    const int waves = (int)std::min<int64_t>(4, (a.batch + 15) / 16);
-    const uint32_t gx = (uint32_t)((a.batch + 16 * waves - 1) / (16 * waves)), gy = (uint32_t)((a.rows + 15) / 16);
+    const char *fmt = a.type == CJ_Q8_0 ? "q80" : "q4k";
+    char name[32];
+    const int nt = a.batch <= 32 ? 2 : 4;
+    const int64_t tiles = ((a.rows + 63) / 64) * ((a.batch + 16 * nt - 1) / (16 * nt));
+    if (tiles < 256 && a.batch <= 64) {
+        const int sn = (a.type == CJ_Q8_0 && a.batch > 16) ? 2 : 1;
+        const uint32_t gx = (uint32_t)((a.batch + 16 * sn - 1) / (16 * sn)), gy = (uint32_t)((a.rows + 15) / 16);
+        if (gy > 65535) return fail(CJ_ERR_ARG, "gemm: %lld rows exceed the grid", (long long)a.rows);
+        snprintf(name, sizeof name, "cj_gemm_sk_%s_n%d", fmt, sn);
+        return launch2(name, gx, gy, 512, 0, a);
+    }
+    const uint32_t gx = (uint32_t)((a.batch + 16 * nt - 1) / (16 * nt)), gy = (uint32_t)((a.rows + 63) / 64);
     if (gy > 65535) return fail(CJ_ERR_ARG, "gemm: %lld rows exceed the grid", (long long)a.rows);
-    return launch2(a.type == CJ_Q8_0 ? "cj_gemm_q80" : "cj_gemm_q4k", gx, gy, 64 * waves, 0, a);
+    snprintf(name, sizeof name, "cj_gemm_%s_n%d", fmt, nt);
+    return launch2(name, gx, gy, 256, 0, a);
 }
 
 int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
@@ -285,7 +302,9 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
-        "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_gemm_q80", "cj_gemm_q4k",
+        "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
+        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q4k_n4",
+        "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
         "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8",
         "cj_attn_prefill_h128_g1", "cj_attn_prefill_h128_g2", "cj_attn_prefill_h128_g4", "cj_attn_prefill_h128_g8",

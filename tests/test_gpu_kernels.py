@@ -332,7 +332,8 @@ def test_kernel_registry_answers_reference_names(gpu):
 
 @pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12)])
 @pytest.mark.parametrize("rows,cols,ncols", [(300, 512, 1), (1024, 4096, 4), (64, 1408, 8), (272, 4096, 17),
-                                             (96, 14336, 16), (160, 2048, 70)])
+                                             (96, 14336, 16), (160, 2048, 70), (100, 1408, 80), (40, 512, 33),
+                                             (130, 768, 200)])
 def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
     """The batched int8 matrix-core product: every output column is the
     one-column product of its activation pack, bit for bit (integer sub-block
