@@ -63,7 +63,7 @@ DEV void attn_window(const cj_attn_args &a, int &count, int &from) {
 //            position order, each position's c and w read from its lane.
 // The last workgroup of a kv head to finish merges the head's splits and
 // writes the merged output and its q8 pack.
-template <int G, bool ROWS>
+template <int G>
 DEV void split_body(const cj_attn_args &a) {
     constexpr int HD = 128, TP = 64, KS = HD + 8, PGMAX = 256, HW = G / 4;
     __shared__ __align__(16) uint16_t ks[TP][KS];
@@ -73,29 +73,192 @@ DEV void split_body(const cj_attn_args &a) {
     __shared__ float bmax[8];
     __shared__ int ticket;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    // the workgroup's (row,) kv head and split slot; the row's q, pages and
-    // partials (many-row form: the row's sequence and position from the row
-    // table, the split rule over all rows' kv heads)
-    int kvh, sp, count, from, pg_base = a.pg_base, rows_kv = a.n_kv;
-    const float *qrow = a.q;
-    float *part = a.part;
-    if (ROWS) {
-        const int per = a.n_kv * a.spl, r = blockIdx.x / per, rem = blockIdx.x % per;
-        kvh = rem / a.spl;
-        sp = rem % a.spl;
-        const int slot = a.rowtab[2 * r];
-        count = a.states[slot].pos + a.rowtab[2 * r + 1] + 1;
-        from = 0;
-        if (a.window > 0 && count > a.window) { from = count - a.window; count = a.window; }
-        pg_base = slot * a.pg_n;
-        rows_kv = a.nrows * a.n_kv;
-        qrow = a.q + (int64_t)r * a.q_stride;
-        part = a.part + (int64_t)r * a.part_stride;
-    } else {
-        kvh = blockIdx.x / ATTN_MAX_SPLITS;
-        sp = blockIdx.x % ATTN_MAX_SPLITS;
-        attn_window(a, count, from);
+    const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
+    // q, the page table and the step state load together
+    for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(a.q + (int64_t)kvh * G * HD + e);
+    if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[a.pg_base + t] : 0;
+    int count, from;
+    attn_window(a, count, from);
+    const int splits = decode_splits(count, a.n_kv, a.workers);
+    if (sp < splits) {
+        const int chunk = (count + splits - 1) / splits;
+        int t0 = sp * chunk, t1 = t0 + chunk;
+        if (t1 > count) t1 = count;
+        if (t0 > count) t0 = count;
+        float m[HW], l[HW], acc0[HW], acc1[HW];
+#pragma unroll
+        for (int hh = 0; hh < HW; hh++) { m[hh] = -3.0e38f; l[hh] = 0.0f; acc0[hh] = 0.0f; acc1[hh] = 0.0f; }
+        for (int tb = t0; tb < t1; tb += TP) {
+            const int n = t1 - tb < TP ? t1 - tb : TP;
+            __syncthreads();   // the previous tile's reads are done (first tile: q and pages visible)
+            // stage the tile's K and V rows: 16-byte chunks, every load issued
+            // before the first store (rows past the tile repeat its last row)
+            {
+                uint4 kr[4], vr[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int c = t + 256 * i, j = c & 15;
+                    const int p = (c >> 4) < n ? (c >> 4) : n - 1;
+                    const int pos = from + tb + p, pi = pos >> 6;
+                    const int page = pi < PGMAX ? pgs[pi] : a.pgtab[a.pg_base + pi];
+                    const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;
+                    kr[i] = *(const uint4 *)(a.kc + base);
+                    vr[i] = *(const uint4 *)(a.vc + base);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int c = t + 256 * i;
+                    *(uint4 *)&ks[c >> 4][8 * (c & 15)] = kr[i];
+                    *(uint4 *)&vs[c >> 4][8 * (c & 15)] = vr[i];
+                }
+            }
+            __syncthreads();
+            // scores of position `lane` for this wave's heads, one head at a time
+            float s[HW];
+#pragma unroll
+            for (int hh = 0; hh < HW; hh++) {
+                const float *qh = &qs[wave + 4 * hh][0];
+                float part[16];
+#pragma unroll
+                for (int c = 0; c < 16; c++) {
+                    const uint4 kk = *(const uint4 *)&ks[lane][8 * c];
+                    const float4 qa = *(const float4 *)(qh + 8 * c), qb = *(const float4 *)(qh + 8 * c + 4);
+                    const float kf[8] = {h2f(kk.x), h2f(kk.x >> 16), h2f(kk.y), h2f(kk.y >> 16),
+                                         h2f(kk.z), h2f(kk.z >> 16), h2f(kk.w), h2f(kk.w >> 16)};
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const int j = 8 * (c & 1) + i;
+                        const float pr = __fmul_rn(qv[i], kf[i]);
+                        part[j] = c < 2 ? pr : __fadd_rn(part[j], pr);
+                    }
+                }
+#pragma unroll
+                for (int w = 1; w < 16; w <<= 1)
+#pragma unroll
+                    for (int j = 0; j < 16; j += 2 * w) part[j] = __fadd_rn(part[j], part[j + w]);
+                s[hh] = __fmul_rn(part[0], a.scale);
+            }
+            const bool live = lane < n;
+#pragma unroll 1
+            for (int hh = 0; hh < HW; hh++) {
+                // running max before (exc) and after (inc) each position
+                const float inc = fmaxf(m[hh], wave_prefix_max(live ? s[hh] : -3.0e38f));
+                const float exc = wave_shr1(inc, m[hh]);
+                const bool up = live && s[hh] > exc;
+                const float cf = up ? cj_expf(exc - s[hh]) : 1.0f;
+                const float pw = live ? cj_expf(s[hh] - inc) : 0.0f;
+                const uint64_t ups = __ballot(up);
+                m[hh] = lane_f(inc, n - 1);
+                // the lane's V pair of every position of the tile first (all
+                // reads in flight at once), then the recurrence in position
+                // order with each position's weight (and rescale, where the
+                // maximum rose) read from its lane
+                uint32_t vv[TP];
+#pragma unroll
+                for (int p = 0; p < TP; p++) vv[p] = *(const uint32_t *)&vs[p][2 * lane];
+                float x0 = acc0[hh], x1 = acc1[hh], ls = l[hh];
+#pragma unroll
+                for (int p = 0; p < TP; p++) {
+                    if (p < n) {
+                        const float w = lane_f(pw, p);
+                        if ((ups >> p) & 1) {
+                            const float c = lane_f(cf, p);
+                            x0 = __fmul_rn(x0, c);
+                            x1 = __fmul_rn(x1, c);
+                            ls = __fmul_rn(ls, c);
+                        }
+                        ls = __fadd_rn(ls, w);
+                        x0 = __fadd_rn(x0, __fmul_rn(h2f(vv[p]), w));
+                        x1 = __fadd_rn(x1, __fmul_rn(h2f(vv[p] >> 16), w));
+                    }
+                }
+                acc0[hh] = x0; acc1[hh] = x1; l[hh] = ls;
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < HW; hh++) {
+            float *pb = a.part + ((int64_t)(kvh * G + wave + 4 * hh) * ATTN_MAX_SPLITS + sp) * (HD + 2);
+            *(float2 *)(pb + 2 * lane) = make_float2(acc0[hh], acc1[hh]);
+            if (lane == 0) *(float2 *)(pb + HD) = make_float2(m[hh], l[hh]);
+        }
     }
+    if (!a.out && !a.packed) return;
+
+    // the last workgroup of this kv head merges its splits
+    __threadfence();
+    __syncthreads();
+    if (t == 0) ticket = atomicAdd(&a.counters[kvh], 1);
+    __syncthreads();
+    if (ticket != ATTN_MAX_SPLITS - 1) return;
+    __threadfence();
+    float *ob = (float *)&vs[0][0];                  // G·HD merged values (LDS reuse)
+#pragma unroll 1
+    for (int hh = 0; hh < HW; hh++) {
+        const int qq = kvh * G + wave + 4 * hh;
+        const float *pb0 = a.part + (int64_t)qq * ATTN_MAX_SPLITS * (HD + 2);
+        // lane s: split s's (max, sum); the weights of the merge
+        const float2 ml = *(const float2 *)(pb0 + lane * (HD + 2) + HD);
+        const bool in = lane < splits;
+        const float mv = in ? ml.x : -3.0e38f;
+        const float gm = group_max<64>(mv);
+        const bool on = in && ml.y > 0.0f;
+        const float wt = on ? cj_expf(mv - gm) : 0.0f;
+        const uint64_t ons = __ballot(on);
+        float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < splits; s0 += 16) {
+            float2 av[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) av[k] = *(const float2 *)(pb0 + (s0 + k) * (HD + 2) + 2 * lane);
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const int s2 = s0 + k;
+                if (s2 < splits && ((ons >> s2) & 1)) {
+                    const float w = lane_f(wt, s2), lsv = lane_f(ml.y, s2);
+                    gl[k & 3] = __fadd_rn(gl[k & 3], __fmul_rn(w, lsv));
+                    ac0[k & 3] = __fadd_rn(ac0[k & 3], __fmul_rn(av[k].x, w));
+                    ac1[k & 3] = __fadd_rn(ac1[k & 3], __fmul_rn(av[k].y, w));
+                }
+            }
+        }
+        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
+        const float rs = __fdiv_rn(1.0f, gt);
+        const float o0 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac0[0], ac0[1]), ac0[2]), ac0[3]), rs);
+        const float o1 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac1[0], ac1[1]), ac1[2]), ac1[3]), rs);
+        if (a.out) *(float2 *)(a.out + (int64_t)qq * HD + 2 * lane) = make_float2(o0, o1);
+        *(float2 *)(ob + (wave + 4 * hh) * HD + 2 * lane) = make_float2(o0, o1);
+    }
+    if (a.packed) {
+        __syncthreads();
+        // the kv head's G·HD outputs are G·HD/256 whole pack blocks
+#pragma unroll
+        for (int b = 0; b < G * HD / 256; b++)
+            pack256(ob[256 * b + t], a.per32, a.packed + ((int64_t)kvh * (G * HD / 256) + b) * 320, bmax);
+    }
+    if (t == 0) a.counters[kvh] = 0;
+}
+
+// The many-row form (batched decode): workgroup (row, kv head, split slot);
+// row r's sequence, position and q from the row table, the split rule over
+// all rows' kv heads (AttnKernel.attnDecodeCpuGqaBatchKernel,
+// model/AttnKernel.cajeta:4316-4350); a long split's next tile is requested
+// during the current one.
+template <int G>
+DEV void split_rows_body(const cj_attn_args &a) {
+    constexpr int HD = 128, TP = 64, KS = HD + 8, PGMAX = 256, HW = G / 4;
+    __shared__ __align__(16) uint16_t ks[TP][KS];
+    __shared__ __align__(16) uint16_t vs[TP][HD];
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ int pgs[PGMAX];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int per = a.n_kv * a.spl, r = blockIdx.x / per, rem = blockIdx.x % per;
+    const int kvh = rem / a.spl, sp = rem % a.spl;
+    const int slot = a.rowtab[2 * r];
+    int count = a.states[slot].pos + a.rowtab[2 * r + 1] + 1, from = 0;
+    if (a.window > 0 && count > a.window) { from = count - a.window; count = a.window; }
+    const int pg_base = slot * a.pg_n, rows_kv = a.nrows * a.n_kv;
+    const float *qrow = a.q + (int64_t)r * a.q_stride;
+    float *part = a.part + (int64_t)r * a.part_stride;
     // q, the page table and the step state load together
     for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(qrow + (int64_t)kvh * G * HD + e);
     if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[pg_base + t] : 0;
@@ -208,64 +371,13 @@ DEV void split_body(const cj_attn_args &a) {
             if (lane == 0) *(float2 *)(pb + HD) = make_float2(m[hh], l[hh]);
         }
     }
-    if (ROWS || (!a.out && !a.packed)) return;
-
-    // the last workgroup of this kv head merges its splits
-    __threadfence();
-    __syncthreads();
-    if (t == 0) ticket = atomicAdd(&a.counters[kvh], 1);
-    __syncthreads();
-    if (ticket != ATTN_MAX_SPLITS - 1) return;
-    __threadfence();
-    float *ob = (float *)&vs[0][0];                  // G·HD merged values (LDS reuse)
-#pragma unroll 1
-    for (int hh = 0; hh < HW; hh++) {
-        const int qq = kvh * G + wave + 4 * hh;
-        const float *pb0 = a.part + (int64_t)qq * ATTN_MAX_SPLITS * (HD + 2);
-        // lane s: split s's (max, sum); the weights of the merge
-        const float2 ml = *(const float2 *)(pb0 + lane * (HD + 2) + HD);
-        const bool in = lane < splits;
-        const float mv = in ? ml.x : -3.0e38f;
-        const float gm = group_max<64>(mv);
-        const bool on = in && ml.y > 0.0f;
-        const float wt = on ? cj_expf(mv - gm) : 0.0f;
-        const uint64_t ons = __ballot(on);
-        float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < splits; s0 += 16) {
-            float2 av[16];
-#pragma unroll
-            for (int k = 0; k < 16; k++) av[k] = *(const float2 *)(pb0 + (s0 + k) * (HD + 2) + 2 * lane);
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const int s2 = s0 + k;
-                if (s2 < splits && ((ons >> s2) & 1)) {
-                    const float w = lane_f(wt, s2), lsv = lane_f(ml.y, s2);
-                    gl[k & 3] = __fadd_rn(gl[k & 3], __fmul_rn(w, lsv));
-                    ac0[k & 3] = __fadd_rn(ac0[k & 3], __fmul_rn(av[k].x, w));
-                    ac1[k & 3] = __fadd_rn(ac1[k & 3], __fmul_rn(av[k].y, w));
-                }
-            }
-        }
-        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
-        const float rs = __fdiv_rn(1.0f, gt);
-        const float o0 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac0[0], ac0[1]), ac0[2]), ac0[3]), rs);
-        const float o1 = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(ac1[0], ac1[1]), ac1[2]), ac1[3]), rs);
-        if (a.out) *(float2 *)(a.out + (int64_t)qq * HD + 2 * lane) = make_float2(o0, o1);
-        *(float2 *)(ob + (wave + 4 * hh) * HD + 2 * lane) = make_float2(o0, o1);
-    }
-    if (a.packed) {
-        __syncthreads();
-        // the kv head's G·HD outputs are G·HD/256 whole pack blocks
-#pragma unroll
-        for (int b = 0; b < G * HD / 256; b++)
-            pack256(ob[256 * b + t], a.per32, a.packed + ((int64_t)kvh * (G * HD / 256) + b) * 320, bmax);
-    }
-    if (t == 0) a.counters[kvh] = 0;
 }
 
-#define SPLIT_KERNEL(G)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G, false>(a); } \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_rows_h128_g##G(cj_attn_args a) { split_body<G, true>(a); }
+#undef SPLIT_FETCH
+
+#define SPLIT_KERNEL(G)                                                                                         \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G>(a); }      \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_rows_h128_g##G(cj_attn_args a) { split_rows_body<G>(a); }
 SPLIT_KERNEL(4)
 SPLIT_KERNEL(8)
 
@@ -356,24 +468,78 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     __shared__ float bmax[8];
     __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
     const int t = threadIdx.x, lane = t & 63;
+    const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
-    // many-row form: the row and its block (a row is whole blocks of 256)
-    int64_t blk = blockIdx.x;
-    const float *part = a.part;
-    float *out = a.out;
-    uint8_t *packed = a.packed;
-    int count = 0;
-    if (a.rowtab) {
-        const int64_t per = n / 256, r = blockIdx.x / per;
-        blk = blockIdx.x % per;
-        part += r * a.part_stride;
-        if (out) out += r * a.out_stride;
-        if (packed) packed += r * a.pack_stride;
-        count = a.states[a.rowtab[2 * r]].pos + a.rowtab[2 * r + 1] + 1;
-    } else if (a.state) {
-        count = a.state->pos + 1;
+    // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
+    const int64_t ew = min((int64_t)blockIdx.x * 256 + (t & ~63), n - 1);
+    const int h = (int)(ew / hd), d = (int)(min(e, n - 1) % hd);
+    const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
+    float pv[ATTN_MAX_SPLITS];
+#pragma unroll
+    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
+    const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
+    int splits = a.splits;
+    if (a.state) {
+        int count = a.state->pos + 1;
+        if (a.window > 0 && count > a.window) count = a.window;
+        splits = decode_splits(count, a.n_kv, a.workers);
     }
+    const bool in = lane < splits;
+    const float mv = in ? ml.x : -3.0e38f;
+    const float gm = group_max<64>(mv);
+    const bool on = in && ml.y > 0.0f;
+    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    const uint64_t ons = __ballot(on);
+    // split weights and sums through the wave's LDS row, back as broadcast
+    // 16-byte reads, 16 splits a chunk; selects (not branches): a split that
+    // takes no part leaves the sums as they were
+    const int wave = t >> 6;
+    sw[wave][lane] = wt;
+    sl[wave][lane] = ml.y;
+    __builtin_amdgcn_wave_barrier();
+    float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s0 = 0; s0 < ATTN_MAX_SPLITS; s0 += 16) {
+        float w[16], lv[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 w4 = *(const float4 *)&sw[wave][s0 + 4 * k];
+            const float4 l4 = *(const float4 *)&sl[wave][s0 + 4 * k];
+            w[4 * k] = w4.x; w[4 * k + 1] = w4.y; w[4 * k + 2] = w4.z; w[4 * k + 3] = w4.w;
+            lv[4 * k] = l4.x; lv[4 * k + 1] = l4.y; lv[4 * k + 2] = l4.z; lv[4 * k + 3] = l4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int s2 = s0 + j;
+            const bool use = (ons >> s2) & 1;
+            const float g2 = __fadd_rn(gl[s2 & 3], __fmul_rn(w[j], lv[j]));
+            const float a2 = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w[j]));
+            gl[s2 & 3] = use ? g2 : gl[s2 & 3];
+            ac[s2 & 3] = use ? a2 : ac[s2 & 3];
+        }
+    }
+    const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
+    const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
+    const float x = e < n ? __fmul_rn(tacc, __fdiv_rn(1.0f, gt)) : 0.0f;
+    if (a.out && e < n) a.out[e] = x;
+    if (a.packed) pack256(x, a.per32, a.packed + (int64_t)blockIdx.x * 320, bmax);
+}
+
+// The many-row form: row r's blocks (a row is whole blocks of 256), its
+// partials and split count from the row table, its output and pack at the
+// row strides.
+extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_args a) {
+    __shared__ float bmax[8];
+    __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t n = (int64_t)a.n_q * a.head_dim;
+    const int hd = a.head_dim;
+    const int64_t per = n / 256, r = blockIdx.x / per, blk = blockIdx.x % per;
+    const float *part = a.part + r * a.part_stride;
+    float *out = a.out ? a.out + r * a.out_stride : nullptr;
+    uint8_t *packed = a.packed ? a.packed + r * a.pack_stride : nullptr;
+    int count = a.states[a.rowtab[2 * r]].pos + a.rowtab[2 * r + 1] + 1;
     const int64_t e = blk * 256 + t;
     // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
     const int64_t ew = min(blk * 256 + (t & ~63), n - 1);
@@ -383,11 +549,8 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
 #pragma unroll
     for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
     const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
-    int splits = a.splits;
-    if (a.rowtab || a.state) {
-        if (a.window > 0 && count > a.window) count = a.window;
-        splits = decode_splits(count, (a.rowtab ? a.nrows : 1) * a.n_kv, a.workers);
-    }
+    if (a.window > 0 && count > a.window) count = a.window;
+    const int splits = decode_splits(count, a.nrows * a.n_kv, a.workers);
     const bool in = lane < splits;
     const float mv = in ? ml.x : -3.0e38f;
     const float gm = group_max<64>(mv);

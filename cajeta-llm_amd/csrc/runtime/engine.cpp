@@ -699,7 +699,7 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             m.packed = r_ap; m.part = r_part; m.n_q = n_heads; m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0;
             m.n_kv = n_kv; m.workers = workers; m.window = L.window; m.nrows = n; m.rowtab = tab; m.states = states;
             m.part_stride = a.part_stride; m.pack_stride = qb;
-            if ((rc = launch("cj_attn_merge", (uint32_t)(n * (qd / 256)), 256, 0, m))) return rc;
+            if ((rc = launch("cj_attn_merge_rows", (uint32_t)(n * (qd / 256)), 256, 0, m))) return rc;
         }
         if ((rc = rows_linear(L.o, r_ap, qb, r_hs, hidden, true, n))) return rc;
         if ((rc = rows_norm_pack(L.ffn_norm, L.gu.type == CJ_Q8_0, n))) return rc;

@@ -56,6 +56,9 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"attnScoreKernel", "cj_attn_scores_h64"},
         {"attnCombineKernel", "cj_attn_combine_h64"},
         {"attnReducePackQ8Kernel", "cj_attn_merge"},
+        {"attnReducePackQ8BatchKernel", "cj_attn_merge_rows"},
+        {"attnFlashDecodeGqa4BatchKernel", "cj_attn_split_rows_h128_g4"},
+        {"attnPrefillCpuGqaKernel", "cj_attn_prefill_h128_g4"},
         {"argmaxRowKernel", "cj_argmax"},
         {"embedRowQ4kKernel", "cj_embed"},
         {"embedRowQ6kKernel", "cj_embed"},
@@ -306,7 +309,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q4k_n4",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
-        "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8",
+        "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8", "cj_attn_merge_rows",
         "cj_attn_prefill_h128_g1", "cj_attn_prefill_h128_g2", "cj_attn_prefill_h128_g4", "cj_attn_prefill_h128_g8",
     };
     for (const char *k : kernels) {
