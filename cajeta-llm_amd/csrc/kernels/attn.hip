@@ -603,8 +603,18 @@ extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
     const int pos = step_pos(a.state, a.pos);
     if (a.norm) {
         float ss = 0.0f;
-        for (int i = t; i < hd; i += 64) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
-        ss = group_sum<64>(ss);
+        if (hd == 128) {
+            // AttnKernel.cpuHeadNorm's order: thread t squares the pair
+            // (2t, 2t+1); pairs fold as a tree within each 16 (xor 1, 2, 4),
+            // two 16s make a 32 (xor 8), the four 32s add in order
+            ss = __fadd_rn(__fmul_rn(x[2 * t], x[2 * t]), __fmul_rn(x[2 * t + 1], x[2 * t + 1]));
+#pragma unroll
+            for (int m = 1; m <= 8; m <<= 1) ss = __fadd_rn(ss, __shfl_xor(ss, m));
+            ss = __fadd_rn(__fadd_rn(__fadd_rn(__shfl(ss, 0), __shfl(ss, 16)), __shfl(ss, 32)), __shfl(ss, 48));
+        } else {
+            for (int i = t; i < hd; i += 64) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
+            ss = group_sum<64>(ss);
+        }
         const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), a.eps)));
         const float *w = isq ? a.qw : a.kw;
         for (int i = t; i < hd; i += 64) {

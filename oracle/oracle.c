@@ -587,6 +587,45 @@ static inline float kv_at(const void *plane, int f32, int64_t i) {
     return f32 ? ((const float *)plane)[i] : or_f16_to_f32(((const uint16_t *)plane)[i]);
 }
 
+/* AttnKernel.cpuSq16 / cpuHeadNorm (L/model/AttnKernel.cajeta:233-268): one
+ * head's QK-norm at head size 128 — squares summed in pairs, the pairs
+ * folded as a tree within each 16, two 16s a 32, the four 32s added in
+ * order; scale = 1/sqrt(tot/128 + eps); x·scale·w (form 1: w + 1). */
+static float sq16(const float *x) {
+    float a[8];
+    for (int j = 0; j < 8; j++) a[j] = x[2 * j] * x[2 * j] + x[2 * j + 1] * x[2 * j + 1];
+    float c0 = a[0] + a[1], c1 = a[2] + a[3], c2 = a[4] + a[5], c3 = a[6] + a[7];
+    return (c0 + c1) + (c2 + c3);
+}
+
+void or_head_norm128(float *x, const float *w, float eps, int form) {
+    float w0 = sq16(x) + sq16(x + 16), w1 = sq16(x + 32) + sq16(x + 48);
+    float w2 = sq16(x + 64) + sq16(x + 80), w3 = sq16(x + 96) + sq16(x + 112);
+#if OR_PLANT == 10
+    float tot = w0 + (w1 + (w2 + w3));                  /* planted: the 32s folded from the end */
+#else
+    float tot = ((w0 + w1) + w2) + w3;
+#endif
+    float scale = 1.0f / sqrtf(tot / 128.0f + eps);
+    for (int j = 0; j < 128; j++) {
+        float wi = form == 1 ? 1.0f + w[j] : w[j];
+        x[j] = x[j] * scale * wi;
+    }
+}
+
+/* AttnKernel.qkPrepCpuKernel (:272-354) at head size 128: every q and k head
+ * normed (norm != 0), then RoPE with cos/sin of pos·inv[d] (or_rope). */
+int or_qk_prep128(float *q, float *k, const float *qw, const float *kw, const float *inv, int nh, int nkv,
+                  int norm, float eps, int form, int pos) {
+    if (norm) {
+        for (int h = 0; h < nh; h++) or_head_norm128(q + (int64_t)h * 128, qw, eps, form);
+        for (int h = 0; h < nkv; h++) or_head_norm128(k + (int64_t)h * 128, kw, eps, form);
+    }
+    or_rope(q, nh, 128, pos, inv);
+    or_rope(k, nkv, 128, pos, inv);
+    return 0;
+}
+
 /* AttnKernel.cpuDecodeSplits (L/model/AttnKernel.cajeta:4879-4889). */
 int or_cpu_decode_splits(int count, int rows, int nkv, int workers) {
     int w = workers < 1 ? 1 : workers, rk = rows * nkv < 1 ? 1 : rows * nkv;
@@ -633,6 +672,37 @@ static void decode_head(const float *q, const void *kp, const void *vp, int f32,
     part[hd + 1] = l;
 }
 
+/* reducePackBlockCpu's merge (L/model/AttnKernel.cajeta:5268-5400): per
+ * head, the splits' (acc[hd], m, l) partials [nh][splits][hd+2] merge as
+ * four interleaved sub-sums (splits s ≡ sub mod 4, ascending) of w·l and
+ * w·acc with w = exp(m − max), added in sub order, then ·(1/Σ). */
+void or_attn_merge(const float *part, int nh, int splits, int hd, float *out) {
+    int stride = hd + 2;
+    for (int h = 0; h < nh; h++) {
+        const float *pb0 = part + (int64_t)h * splits * stride;
+        float gm = -3.0e38f;
+        for (int s = 0; s < splits; s++) if (pb0[s * stride + hd] > gm) gm = pb0[s * stride + hd];
+        float tacc[256], gt = 0.0f;
+        for (int sub = 0; sub < 4; sub++) {
+            float a[256], gl = 0.0f;
+            for (int d = 0; d < hd; d++) a[d] = 0.0f;
+            for (int sp = sub; sp < splits; sp += 4) {
+                const float *pb = pb0 + sp * stride;
+                float ls = pb[hd + 1];
+                if (ls > 0.0f) {
+                    float wt = or_expf(pb[hd] - gm);
+                    gl = gl + wt * ls;
+                    for (int d = 0; d < hd; d++) a[d] = a[d] + pb[d] * wt;
+                }
+            }
+            if (sub == 0) { for (int d = 0; d < hd; d++) tacc[d] = a[d]; gt = gl; }
+            else { for (int d = 0; d < hd; d++) tacc[d] = tacc[d] + a[d]; gt = gt + gl; }
+        }
+        float rs = 1.0f / gt;
+        for (int d = 0; d < hd; d++) out[(int64_t)h * hd + d] = tacc[d] * rs;
+    }
+}
+
 void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, int nkv, int hd,
                int count, int splits, float scale, int mode, float *out) {
     int64_t kvdim = (int64_t)nkv * hd;
@@ -656,29 +726,7 @@ void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, 
                                 scale, part + ((int64_t)hh * splits + sp) * stride);
                 }
             }
-        for (int h = 0; h < nh; h++) {
-            const float *pb0 = part + (int64_t)h * splits * stride;
-            float gm = -3.0e38f;
-            for (int s = 0; s < splits; s++) if (pb0[s * stride + hd] > gm) gm = pb0[s * stride + hd];
-            float tacc[256], gt = 0.0f;
-            for (int sub = 0; sub < 4; sub++) {
-                float a[256], gl = 0.0f;
-                for (int d = 0; d < hd; d++) a[d] = 0.0f;
-                for (int sp = sub; sp < splits; sp += 4) {
-                    const float *pb = pb0 + sp * stride;
-                    float ls = pb[hd + 1];
-                    if (ls > 0.0f) {
-                        float wt = or_expf(pb[hd] - gm);
-                        gl = gl + wt * ls;
-                        for (int d = 0; d < hd; d++) a[d] = a[d] + pb[d] * wt;
-                    }
-                }
-                if (sub == 0) { for (int d = 0; d < hd; d++) tacc[d] = a[d]; gt = gl; }
-                else { for (int d = 0; d < hd; d++) tacc[d] = tacc[d] + a[d]; gt = gt + gl; }
-            }
-            float rs = 1.0f / gt;
-            for (int d = 0; d < hd; d++) out[(int64_t)h * hd + d] = tacc[d] * rs;
-        }
+        or_attn_merge(part, nh, splits, hd, out);
         free(part);
     } else {
         /* attnScoreKernel (:397-425): lane i of 32 sums q[d]·k[d] over

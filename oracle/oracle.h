@@ -76,6 +76,13 @@ void or_attend(const float *q, const void *kplane, const void *vplane, int kv_f3
                int n_h, int n_kv, int hd, int count, int splits, float scale,
                int mode, float *out);
 int  or_cpu_decode_splits(int count, int rows, int n_kv, int workers);
+/* the split-K merge alone: partials [n_h][splits][hd+2] → out [n_h·hd] */
+void or_attn_merge(const float *part, int n_h, int splits, int hd, float *out);
+/* QK-norm of one 128-wide head in place, and the CPU decode prep at hd 128
+ * (norm != 0: every head normed; then RoPE at `pos` with the given inv). */
+void or_head_norm128(float *x, const float *w, float eps, int form);
+int  or_qk_prep128(float *q, float *k, const float *qw, const float *kw, const float *inv, int n_h, int n_kv,
+                   int norm, float eps, int form, int pos);
 
 /* prefill attention for `rows` consecutive query rows at positions
  * start .. start+rows-1 of one sequence (hd 128): q rows [rows][n_h*hd], the

@@ -73,6 +73,8 @@ def _configure(L):
             "or_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, F, I32, P]),
             "or_cpu_decode_splits": (I32, [I32, I32, I32, I32]),
             "or_prefill_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, I32, F, P]),
+            "or_attn_merge": (None, [P, I32, I32, I32, P]),
+            "or_qk_prep128": (I32, [P, P, P, P, P, I32, I32, I32, F, I32, I32]),
             "or_model_prefill": (I32, [P, P, I32, I32, P]),
             "or_expf": (F, [F]),
             "or_model_new": (P, [ctypes.POINTER(Config)]), "or_model_free": (None, [P]),
@@ -214,6 +216,23 @@ def prefill_attend(q, kplane, vplane, n_h, n_kv, hd, start, rows, window, scale,
     lib().or_prefill_attend(_p(q), _p(np.ascontiguousarray(kplane)), _p(np.ascontiguousarray(vplane)), int(kv_f32),
                             n_h, n_kv, hd, start, rows, window, scale, _p(out))
     return out
+
+
+def attn_merge(part, n_h, splits, hd):
+    """Merge split partials [n_h][splits][hd+2] in the reference's order."""
+    part = np.ascontiguousarray(part, np.float32)
+    out = np.empty(n_h * hd, np.float32)
+    lib().or_attn_merge(_p(part), n_h, splits, hd, _p(out))
+    return out
+
+
+def qk_prep128(q, k, qw, kw, inv, n_h, n_kv, norm, eps, form, pos):
+    """The CPU decode prep at head size 128: QK-norm (optional) and RoPE."""
+    q = np.array(q, np.float32, copy=True)
+    k = np.array(k, np.float32, copy=True)
+    lib().or_qk_prep128(_p(q), _p(k), _p(np.ascontiguousarray(qw, np.float32)), _p(np.ascontiguousarray(kw, np.float32)),
+                        _p(np.ascontiguousarray(inv, np.float32)), n_h, n_kv, int(norm), float(eps), int(form), int(pos))
+    return q, k
 
 
 def cpu_decode_splits(count, rows, n_kv, workers):

@@ -379,3 +379,50 @@ def test_matmul_refuses_short_buffers(gpu, O):
     assert lib.cj_matmul(12, y.h, w.h, xp.h, 64, 256, 4, 320, 64, 0, 0) == -1
     assert "activation" in gpu.native.last_error()
     assert lib.cj_matmul(6, y.h, w.h, xp.h, 64, 256, 1, 320, 64, 0, 0) == -1
+
+
+def test_qk_prep_with_norm_matches_the_reference_cpu_golden(gpu, O):
+    """QK-norm + RoPE + K/V append at hd 128 against the reference CPU
+    backend's recorded q and k (QkPrepTest.run(32, 4, 128, true): position
+    11, eps 1e-6, the test's own inv-frequency fill), bit for bit; the RoPE
+    table holds f32 cos/sin of pos·inv (glibc cosf/sinf reproduce the
+    recording)."""
+    import ctypes
+    from reference_goldens import cpu_golden_rows, qkprep_fill
+    g = cpu_golden_rows()
+    n_q, n_kv, hd, pos = 32, 4, 128, 11
+    q, k, v = qkprep_fill(n_q * hd, 1), qkprep_fill(n_kv * hd, 2), qkprep_fill(n_kv * hd, 3)
+    qw, kw, inv = qkprep_fill(hd, 4), qkprep_fill(hd, 5), qkprep_fill(hd // 2, 6)
+    libm = ctypes.CDLL("libm.so.6")
+    libm.cosf.restype = libm.sinf.restype = ctypes.c_float
+    libm.cosf.argtypes = libm.sinf.argtypes = [ctypes.c_float]
+    tab = np.zeros((pos + 1, hd // 2, 2), np.float32)
+    for d in range(hd // 2):
+        ang = float(np.float32(pos) * inv[d])
+        tab[pos, d] = (libm.cosf(ang), libm.sinf(ang))
+    lib = gpu.native.lib()
+    qb, kb, vb = gpu.Buffer.of(q), gpu.Buffer.of(k), gpu.Buffer.of(v)
+    qwb, kwb, rope = gpu.Buffer.of(qw), gpu.Buffer.of(kw), gpu.Buffer.of(tab.reshape(-1))
+    kc, vc = gpu.Buffer(n_kv * 64 * hd * 2), gpu.Buffer(n_kv * 64 * hd * 2)
+    pg = gpu.Buffer.of(np.zeros(1, np.int32))
+    gpu.native.check(lib.cj_qk_prep(qb.h, kb.h, vb.h, kc.h, vc.h, qwb.h, kwb.h, rope.h, pg.h, 0, n_q, n_kv, hd, 1,
+                                    1e-6, 0, pos), "qk_prep")
+    gq, gk = qb.download(np.float32, q.size), kb.download(np.float32, k.size)
+    assert np.array_equal(gq.view(np.uint32), g[("qkPrepKernel", "h32kv4d128-q")].view(np.uint32))
+    assert np.array_equal(gk.view(np.uint32), g[("qkPrepKernel", "h32kv4d128-k")].view(np.uint32))
+    kcache = kc.download(np.uint16, n_kv * 64 * hd).reshape(n_kv, 64, hd)
+    assert np.array_equal(kcache[:, pos % 64, :].reshape(-1), O.f32_to_f16_bits(gk))
+
+
+def test_attn_merge_pack_matches_the_reference_cpu_golden(gpu, O):
+    """The split merge + per-256 q8 pack of 32 heads × 8 splits against the
+    reference CPU backend's recorded bytes (reducePackGolden), bit for bit."""
+    from reference_goldens import cpu_golden_rows, reduce_pack_partials
+    want = cpu_golden_rows()[("attnReducePackQ8Kernel", "h32s8")]
+    n_q, hd, splits = 32, 128, 8
+    part = np.zeros((n_q, 64, hd + 2), np.float32)
+    part[:, :splits, :] = reduce_pack_partials().reshape(n_q, splits, hd + 2)
+    pb, ob, packed = gpu.Buffer.of(part.reshape(-1)), gpu.Buffer(n_q * hd * 4), gpu.Buffer(n_q * hd // 256 * 320)
+    gpu.native.check(gpu.native.lib().cj_attn_merge(ob.h, packed.h, pb.h, n_q, hd, splits, 0), "merge")
+    got = packed.download(np.uint8, n_q * hd // 256 * 320).view(np.int8).astype(np.float32)
+    assert np.array_equal(got, want)

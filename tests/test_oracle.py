@@ -240,6 +240,28 @@ def check_prefill_attention(O):
     return not bad, bad
 
 
+def check_reference_cpu_goldens(O):
+    """The reference CPU backend's own recorded outputs, bit for bit: the
+    decode prep at hd 128 (QK-norm + RoPE, QkPrepTest.run(32, 4, 128, true))
+    and the split merge + per-256 pack (reducePackGolden, 32 heads × 8
+    splits)."""
+    from reference_goldens import cpu_golden_rows, qkprep_fill, reduce_pack_partials
+    g = cpu_golden_rows()
+    bad = []
+    q, k = O.qk_prep128(qkprep_fill(32 * 128, 1), qkprep_fill(4 * 128, 2), qkprep_fill(128, 4), qkprep_fill(128, 5),
+                        qkprep_fill(64, 6), 32, 4, True, 1e-6, 0, 11)
+    for name, got in (("h32kv4d128-q", q), ("h32kv4d128-k", k)):
+        want = g[("qkPrepKernel", name)]
+        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            bad.append((name, int((got != want).sum())))
+    out = O.attn_merge(reduce_pack_partials(), 32, 8, 128)
+    pk = O.q8k_pack(out, per32=False, npad=4096).view(np.int8).astype(np.float32)
+    want = g[("attnReducePackQ8Kernel", "h32s8")]
+    if not np.array_equal(pk, want):
+        bad.append(("h32s8", int((pk != want).sum())))
+    return not bad, bad
+
+
 def check_unpermute(O):
     """Checkpoint.unpermuteRows undoes the GGUF llama q/k row permutation:
     HF row (h, a, b) sits at GGUF row (h, b, a) — built here by reshape."""
@@ -404,6 +426,11 @@ def test_model_prefill_matches_decode_steps(O):
         m.close()
 
 
+def test_reference_cpu_backend_goldens(O):
+    ok, bad = check_reference_cpu_goldens(O)
+    assert ok, bad
+
+
 def test_decode_splits_closed_form(O):
     # two work items a worker over the kv heads, within [1, min(64, count)]
     assert O.cpu_decode_splits(2049, 1, 8, 512) == 64
@@ -531,6 +558,7 @@ PLANTS = {
     7: ("split-K without the rescale on a new max", check_attention),
     8: ("q/k rows unpermuted with the halves swapped", check_unpermute),
     9: ("prefill scores from one lane partial", check_prefill_attention),
+    10: ("QK-norm 32-sums folded from the end", check_reference_cpu_goldens),
 }
 
 
