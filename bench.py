@@ -210,13 +210,116 @@ def run_c4(args, pkg, native):
     print(json.dumps(line), flush=True)
 
 
+C2_METRIC = "quantised GEMV / mat-mat HBM GB/s (C2 microbench, cold weights)"
+C2_FORMATS = (("q8_0", 8, 32, 34), ("q4_0", 2, 32, 18), ("q4_k", 12, 256, 144), ("q6_k", 14, 256, 210))
+C2_SHAPES = ((4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096))
+C2_BATCHES = (1, 4, 8, 16)
+C2_POOL = 512 << 20
+
+
+def c2_blocks(ty, nblocks, rng):
+    """Random blocks of a format with sane scales (the f16 scale fields set,
+    the rest random bytes), the shape of seeded N(0, 0.02) weights."""
+    bb = {8: 34, 2: 18, 12: 144, 14: 210}[ty]
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+
+    def f16(lo, hi):
+        return rng.uniform(lo, hi, nblocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    if ty in (8, 2):
+        raw[:, 0:2] = f16(0.0005, 0.002)
+    elif ty == 12:
+        raw[:, 0:2] = f16(0.0001, 0.0005)
+        raw[:, 2:4] = f16(0.0001, 0.0005)
+    else:
+        raw[:, 208:210] = f16(0.0001, 0.0003)
+    return raw.reshape(-1)
+
+
+def run_c2(args, native):
+    """each format × shape × batch, weights rotated over a
+    pool of >= 512 MB of distinct prepared copies so the 256 MB last-level
+    cache cannot serve them; one captured graph of launches, timed whole.
+    Batch 1 is the decode GEMV; batch > 1 the int8 matrix-core product where
+    the format has one (Q8_0, Q4_K), else one GEMV a column."""
+    lib = native.lib()
+    rng = np.random.default_rng(args.seed)
+    table = []
+    for fname, ty, be, bb in C2_FORMATS:
+        for rows, cols in C2_SHAPES:
+            wbytes = rows * cols // be * bb
+            ncopy = max(2, -(-C2_POOL // wbytes))
+            prb = lib.cj_prepared_row_bytes(ty, cols)
+            raw = native.Buffer.of(c2_blocks(ty, rows * cols // be, rng))
+            pool = native.Buffer(ncopy * rows * prb)
+            for i in range(ncopy):
+                native.check(lib.cj_prepare_weight(pool.h + i * rows * prb, raw.h, ty, rows, cols), "prepare")
+            raw.free()
+            bmax = max(C2_BATCHES)
+            npad = (cols + 255) // 256 * 256
+            xs = npad // 256 * 320
+            x = rng.standard_normal((bmax, cols)).astype(np.float32)
+            xb = native.Buffer.of(x)
+            xp = native.Buffer(bmax * xs)
+            native.check(lib.cj_q8k_pack(xp.h, xb.h, bmax, cols, npad, int(ty == 8)), "pack")
+            y = native.Buffer(bmax * rows * 4)
+            f32act = ty == 2
+            for B in C2_BATCHES:
+                reps = max(ncopy, 32)
+                per = B if (B > 1 and ty in (2, 14)) else 1
+                native.check(lib.cj_graph_begin(), "graph")
+                for r in range(reps):
+                    w = pool.h + (r % ncopy) * rows * prb
+                    if B == 1 or per > 1:
+                        for c in range(B):
+                            act = (xb.h + c * cols * 4) if f32act else (xp.h + c * xs)
+                            native.check(lib.cj_matvec(ty, y.h + c * rows * 4, w, act, rows, cols, 0, 0), "matvec")
+                    else:
+                        native.check(lib.cj_matmul(ty, y.h, w, xp.h, rows, cols, B, xs, rows, 0, 0), "matmul")
+                g = native.handle(lib.cj_graph_end(), "graph")
+                native.check(lib.cj_graph_launch(g), "graph launch")
+                native.sync()
+                t0 = time.perf_counter()
+                native.check(lib.cj_graph_launch(g), "graph launch")
+                native.sync()
+                us = (time.perf_counter() - t0) * 1e6 / reps
+                lib.cj_graph_free(g)
+                nbytes = wbytes + B * cols * 4 + B * rows * 4
+                gbs = nbytes / (us * 1e-6) / 1e9
+                table.append({"format": fname, "rows": rows, "cols": cols, "batch": B, "us": round(us, 2),
+                              "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                              "kernel": "gemv" if B == 1 else ("gemv per column" if per > 1 else "int8 mfma"),
+                              "pool_copies": ncopy})
+                log("  %-5s %6d x %5d B %2d: %9.2f us  %7.1f GB/s  (%s, %d copies)" % (
+                    fname, rows, cols, B, us, gbs, table[-1]["kernel"], ncopy))
+            for b in (pool, xb, xp, y):
+                b.free()
+    head = next(t for t in table if t["format"] == "q4_k" and t["rows"] == 14336 and t["batch"] == 1)
+    line = {
+        "metric": C2_METRIC,
+        "value": head["GB/s"],
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": None, "warmup": 1, "ms_per_step": None, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded random blocks (sane f16 scales), activations N(0, 1)",
+        "config": {"workload": "C2: quantised GEMV microbench; value = Q4_K 14336x4096 at batch 1",
+                   "formats": [f[0] for f in C2_FORMATS], "shapes": C2_SHAPES, "batches": C2_BATCHES,
+                   "cold_pool_bytes": C2_POOL},
+        "roofline": {"bound": "hbm", "achieved": head["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": head["frac"], "traffic": None},
+        "table": table,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps (K)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before (W)")
-    ap.add_argument("--workload", choices=("c3", "c4"), default="c3",
-                    help="c3: the headline batch-1 Q4_K decode; c4: batched Q8_0 decode + prefill")
+    ap.add_argument("--workload", choices=("c3", "c4", "c2"), default="c3",
+                    help="c3: the headline batch-1 Q4_K decode; c4: batched Q8_0 decode + prefill; "
+                         "c2: the quantised GEMV microbench")
     ap.add_argument("--ctx", type=int, default=None, help="positions prefilled before decoding (c3 2048, c4 4096)")
     ap.add_argument("--seqs", type=int, default=32, help="c4: sequences decoded together")
     ap.add_argument("--prefill-reps", type=int, default=3, help="c4: timed 512-row prefill chunks")
@@ -240,6 +343,9 @@ def main():
     from cajeta_llm_amd import native
 
     native.init()
+    if args.workload == "c2":
+        run_c2(args, native)
+        return
     if args.workload == "c4":
         if args.ctx is None:
             args.ctx = 4096
