@@ -17,9 +17,11 @@ LIB = os.path.join(HERE, "libcajeta_mi355x.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # -ffp-contract=off: the arithmetic is written in the order it must round;
-# packed-fp32-ops off: packed f32 ops are kept out of the code object.
+# packed-fp32-ops off: packed f32 ops are kept out of the code object;
+# amdgpu-mfma-vgpr-form: matrix-core results land in ordinary VGPRs (no
+# accumulator-register reads before the f32 steps that consume them).
 KERNEL_FLAGS = ["--offload-arch=" + ARCH, "-O3", "--genco", "-ffp-contract=off", "-Wno-pass-failed",
-                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 HOST_FLAGS = ["--offload-arch=" + ARCH, "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wno-unused-function",
               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-pthread"]
 

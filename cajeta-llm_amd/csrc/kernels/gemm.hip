@@ -89,6 +89,43 @@ DEV void q80_fetch(Q80A &A, const uint8_t *wa, const uint8_t *const (&wd)[4], in
     for (int i = 0; i < 4; i++) A.d[i] = *(const uint4 *)(wd[i] + 16 * g);
 }
 
+// One K-group of a wave's 16 rows × 16·NT columns: the f32 steps of the 8
+// blocks (FULL: all 8 exist; else the first nj). Each tile's 8 operand reads
+// and 8 products issue back to back, then its f32 steps.
+template <int NT, bool FULL>
+DEV void q80_tile_group(const Q80A &A, const uint8_t *lds, int q, int m, int nj, float (&acc)[NT][4]) {
+    float dr[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
+        const float4 x0 = *(const float4 *)(col + 288), x1 = *(const float4 *)(col + 304);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        long bq[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) bq[j] = *(const long *)(col + 32 * j + 8 * q);
+        v4i d[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[j]);
+        float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (FULL || j < nj) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    fs[i] = __fadd_rn(fs[i], __fmul_rn(__fmul_rn(dr[i][j], xs[j]), (float)d[j][i]));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], fs[i]);
+    }
+}
+
 template <int NT>
 DEV void gemm_q80(const cj_gemv_args &a, uint8_t *lds) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
@@ -99,50 +136,39 @@ DEV void gemm_q80(const cj_gemv_args &a, uint8_t *lds) {
     const uint8_t *wd[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
+    // this thread's pack words of the column tile: source and LDS slot
+    const uint8_t *bsrc[BStage<NT>::NV];
+    int bdst[BStage<NT>::NV];
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) {
+        const int w = min(t + 256 * i, BStage<NT>::WORDS - 1);
+        bsrc[i] = a.xp + min(c0 + w / 20, (int64_t)a.batch - 1) * a.xp_stride + 16 * (w % 20);
+        bdst[i] = t + 256 * i < BStage<NT>::WORDS ? (w / 20) * GEMM_CS + 16 * (w % 20) : -1;
+    }
     float acc[NT][4];
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
-    BStage<NT> bs;
+    u32x4 bv[BStage<NT>::NV];
     Q80A A, An;
-    b_fetch<NT>(bs, a, c0, 0);
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)bsrc[i];
     q80_fetch(A, wa, wd, 0, (int)min((int64_t)8, nb32));
     for (int64_t g = 0; g < ngrp; g++) {
         const int nj = (int)min((int64_t)8, nb32 - 8 * g);
         __syncthreads();   // the previous group's LDS reads are done
-        b_store<NT>(bs, lds);
+#pragma unroll
+        for (int i = 0; i < BStage<NT>::NV; i++)
+            if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
         __syncthreads();
         if (g + 1 < ngrp) {
-            b_fetch<NT>(bs, a, c0, g + 1);
+#pragma unroll
+            for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + (g + 1) * 320);
             q80_fetch(An, wa, wd, g + 1, (int)min((int64_t)8, nb32 - 8 * (g + 1)));
         }
-        float dr[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
-        }
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
-            const float4 x0 = *(const float4 *)(col + 288), x1 = *(const float4 *)(col + 304);
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                if (j < nj) {
-                    const v4i d = mfma_i8(A.q[j], *(const long *)(col + 32 * j + 8 * q));
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        fs[i] = __fadd_rn(fs[i], __fmul_rn(__fmul_rn(dr[i][j], xs[j]), (float)d[i]));
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], fs[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        if (nj == 8) q80_tile_group<NT, true>(A, lds, q, m, 8, acc);
+        else q80_tile_group<NT, false>(A, lds, q, m, nj, acc);
         if (g + 1 < ngrp) A = An;
     }
 #pragma unroll
@@ -285,6 +311,47 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 // exactly) through LDS, W groups a round.
 //   Q8_0: the group's fs (one value an output);
 //   Q4_K: the block's (d·xs)·sumi and (dmin·xs)·dmins (two values an output).
+// One K-group of the split-K Q8_0 kernel: the columns' pack blocks (hot in
+// cache) and the f32 terms of the 8 blocks (FULL: all 8 exist).
+template <int NT, bool FULL>
+DEV void q80_sk_group(const Q80A &A, const uint8_t *const (&xc)[NT], int64_t g, int nj, int q, float (&fs)[NT][4]) {
+    long bq[NT][8];
+    float4 bx[NT][2];
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const uint8_t *col = xc[n] + g * 320;
+#pragma unroll
+        for (int j = 0; j < 8; j++) bq[n][j] = ld8(col + 32 * j + 8 * q);
+        bx[n][0] = *(const float4 *)(col + 288);
+        bx[n][1] = *(const float4 *)(col + 304);
+    }
+    float dr[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const float xs[8] = {bx[n][0].x, bx[n][0].y, bx[n][0].z, bx[n][0].w,
+                             bx[n][1].x, bx[n][1].y, bx[n][1].z, bx[n][1].w};
+        v4i d[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[n][j]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (FULL || j < nj) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    fs[n][i] = __fadd_rn(fs[n][i], __fmul_rn(__fmul_rn(dr[i][j], xs[j]), (float)d[j][i]));
+            }
+        }
+    }
+}
+
 template <int NT, int W>
 DEV void gemm_sk_q80(const cj_gemv_args &a) {
     __shared__ __align__(16) float hand[W][NT * 4][64];
@@ -311,38 +378,9 @@ DEV void gemm_sk_q80(const cj_gemv_args &a) {
         float fs[NT][4];
         if (g < ngrp) {
             const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-            // this group's pack blocks (hot in cache) as the group starts; the
-            // next group's weights (from HBM) a group ahead
-            long bq[NT][8];
-            float4 bx[NT][2];
-#pragma unroll
-            for (int n = 0; n < NT; n++) {
-                const uint8_t *col = xc[n] + g * 320;
-#pragma unroll
-                for (int j = 0; j < 8; j++) bq[n][j] = ld8(col + 32 * j + 8 * q);
-                bx[n][0] = *(const float4 *)(col + 288);
-                bx[n][1] = *(const float4 *)(col + 304);
-            }
             if (g + W < ngrp) q80_fetch(An, wa, wd, g + W, (int)min((int64_t)8, nb32 - 8 * (g + W)));
-#pragma unroll
-            for (int n = 0; n < NT; n++) {
-                const float xs[8] = {bx[n][0].x, bx[n][0].y, bx[n][0].z, bx[n][0].w,
-                                     bx[n][1].x, bx[n][1].y, bx[n][1].z, bx[n][1].w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (j < nj) {
-                        const v4i d = mfma_i8(A.q[j], bq[n][j]);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const uint32_t hw = j < 2 ? A.d[i].x : j < 4 ? A.d[i].y : j < 6 ? A.d[i].z : A.d[i].w;
-                            const float dj = h2f(hw >> (16 * (j & 1)));
-                            fs[n][i] = __fadd_rn(fs[n][i], __fmul_rn(__fmul_rn(dj, xs[j]), (float)d[i]));
-                        }
-                    }
-                }
-            }
+            if (nj == 8) q80_sk_group<NT, true>(A, xc, g, 8, q, fs);
+            else q80_sk_group<NT, false>(A, xc, g, nj, q, fs);
             if (g + W < ngrp) A = An;
         }
         if (wave > 0 && g < ngrp) {
