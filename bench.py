@@ -49,8 +49,8 @@ WORKLOAD = ("C3: Llama-3-8B shape (32 layers, d 4096, 32/8 heads of 128, FFN 143
             "Q4_K weights + Q6_K head, fp16 paged K/V, greedy, batch 1")
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic_gemv_q4k_gate_up_c3.txt")
 K_GATE_UP = 4
-KIND_NAMES = {0: "embed", 1: "qkv", 2: "attention", 3: "o", 4: "gate_up", 5: "down", 11: "head", 12: "norm",
-              13: "attn_merge"}
+KIND_NAMES = {0: "embed", 1: "qkv", 2: "attention", 3: "o", 4: "gate_up", 5: "down", 6: "router", 7: "route",
+              8: "expert_gate_up", 9: "expert_down", 10: "combine", 11: "head", 12: "norm", 13: "attn_merge"}
 COPY_BYTES = 1 << 30          # the streaming-copy reference: 1 GiB read + 1 GiB written
 
 
@@ -312,16 +312,100 @@ def run_c2(args, native):
     print(json.dumps(line), flush=True)
 
 
+SINGLE = {
+    # workload: (synth spec, prompt positions, timed steps, metric, workload text)
+    "c1": ("c1", 16, 64, "decode us/token, tiny Llama Q8_0 (C1), batch 1",
+           "C1: 4 layers, d 512, 8/2 heads of 64, FFN 1408, vocab 32000, Q8_0 weights, f32 embeddings; "
+           "16-token prompt, 64 greedy tokens"),
+    "c5": ("c5", 4096, 64, "decode tok/s, gpt-oss-20b-shape MXFP4 MoE, batch 1, 4096 context",
+           "C5: 24 layers, d 2880, 64/8 heads of 64, 32 MXFP4 experts top-4 of FFN 2880, alternating "
+           "128-window attention, vocab 201088; fp16 paged K/V prefilled to 4096 positions, greedy"),
+}
+
+
+def run_single(args, pkg, native, which):
+    """C1 and C5: one sequence, prompt then greedy decode through the graph-
+    replayed step, as the headline does for C3."""
+    spec, ctx, steps, metric, workload = SINGLE[which]
+    ctx = args.ctx or ctx
+    steps = steps if args.steps == 256 else args.steps
+    name = "bench_" + which
+    t = time.perf_counter()
+    pkg.synth_gguf(spec, "mem:" + name, args.seed)
+    log("synthesised %s (seed %d) in %.1f s" % (which.upper(), args.seed, time.perf_counter() - t))
+    opts = pkg.EngineOptions("mem:" + name)
+    opts.ctx = ctx + args.warmup + steps + 1
+    opts.maxSeqs = 1
+    opts.graphs = not args.eager
+    opts.cpuThreads = args.cpu_threads
+    eng = pkg.LlmEngine.load(opts)
+    vocab = eng.config["vocabSize"]
+    rng = np.random.default_rng(args.seed)
+    t = time.perf_counter()
+    eng.reset()
+    eng.prefill(rng.integers(0, vocab, ctx).tolist())
+    log("prefilled %d positions in %.1f s" % (ctx, time.perf_counter() - t))
+    eng.decode(args.warmup)
+    native.sync()
+    t0 = time.perf_counter()
+    toks = eng.decode(steps)
+    native.sync()
+    wall = time.perf_counter() - t0
+    us_tok = wall * 1e6 / steps
+    log("timed %d steps: %.1f us/token wall, %.1f us/step device; %d distinct tokens"
+        % (steps, us_tok, eng.lastStepMicros(), len(set(int(x) for x in toks))))
+    first = ctx + args.warmup
+    step_bytes = float(np.mean([eng.stepBytes(int(c)) for c in range(first + 1, first + steps + 1)]))
+    step_gbs = step_bytes / (us_tok * 1e-6) / 1e9
+    kernels = {}
+    for kind, kname in sorted(KIND_NAMES.items()):
+        try:
+            us, nbytes, kn = eng.timeKernel(kind, args.kernel_reps)
+        except pkg.LlmException as e:
+            if "launches nothing" not in str(e):
+                raise
+            continue
+        kernels[kname] = {"kernel": kn, "avg_us": round(us, 3), "bytes": nbytes,
+                          "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        log("  %-13s %-26s %9.2f us  %12d B  %7.1f GB/s" % (kname, kn, us, nbytes, nbytes / (us * 1e-6) / 1e9))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(pkg, name, vocab, args.cpu_seconds, args.seed)
+        cpu["sample"] = cpu["sample"].replace("C3", which.upper())
+        log("cpu baseline: %s" % cpu)
+    eng.close()
+    pkg.image_free(name)
+    c1 = which == "c1"
+    line = {
+        "metric": metric,
+        "value": round(us_tok, 2) if c1 else round(steps / wall, 2),
+        "unit": "us/token" if c1 else "tok/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us_tok / 1e3, 4),
+        "higher_is_better": not c1, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded random-init GGUF (N(0,0.02) weights), uniform random prompt ids",
+        "config": {"workload": workload, "batch": 1, "prefill_positions": ctx,
+                   "step": "eager launches" if args.eager else "hipGraph replay", "seed": args.seed},
+        "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS,
+                          "unit": "GB/s", "frac": round(step_gbs / PEAK_HBM_GBS, 4),
+                          "wall_us_per_step": round(us_tok, 2)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps (K)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before (W)")
-    ap.add_argument("--workload", choices=("c3", "c4", "c2"), default="c3",
+    ap.add_argument("--workload", choices=("c3", "c4", "c2", "c1", "c5"), default="c3",
                     help="c3: the headline batch-1 Q4_K decode; c4: batched Q8_0 decode + prefill; "
-                         "c2: the quantised GEMV microbench")
+                         "c2: the quantised GEMV microbench; c1: tiny Q8_0 decode; c5: MoE decode")
     ap.add_argument("--ctx", type=int, default=None, help="positions prefilled before decoding (c3 2048, c4 4096)")
     ap.add_argument("--seqs", type=int, default=32, help="c4: sequences decoded together")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="the CPU worker count the attention split rule follows (0: the engine's 512)")
     ap.add_argument("--prefill-reps", type=int, default=3, help="c4: timed 512-row prefill chunks")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--kernel-reps", type=int, default=200)
@@ -346,6 +430,9 @@ def main():
     if args.workload == "c2":
         run_c2(args, native)
         return
+    if args.workload in SINGLE:
+        run_single(args, pkg, native, args.workload)
+        return
     if args.workload == "c4":
         if args.ctx is None:
             args.ctx = 4096
@@ -364,6 +451,7 @@ def main():
     opts.ctx = total
     opts.maxSeqs = 1
     opts.graphs = not args.eager
+    opts.cpuThreads = args.cpu_threads
     t = time.perf_counter()
     eng = pkg.LlmEngine.load(opts)
     cfg = eng.config

@@ -216,22 +216,34 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
     const uint8_t *wh[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wh[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb * 128;
+    const uint8_t *bsrc[BStage<NT>::NV];
+    int bdst[BStage<NT>::NV];
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) {
+        const int w = min(t + 256 * i, BStage<NT>::WORDS - 1);
+        bsrc[i] = a.xp + min(c0 + w / 20, (int64_t)a.batch - 1) * a.xp_stride + 16 * (w % 20);
+        bdst[i] = t + 256 * i < BStage<NT>::WORDS ? (w / 20) * GEMM_CS + 16 * (w % 20) : -1;
+    }
     const uint64_t M = 0x0F0F0F0F0F0F0F0Full;
     float acc[NT][4];
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
-    BStage<NT> bs;
+    u32x4 bv[BStage<NT>::NV];
     Q4kA A, An;
-    b_fetch<NT>(bs, a, c0, 0);
+#pragma unroll
+    for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)bsrc[i];
     q4k_fetch_a(A, wa, wh, nb, 0, q);
     for (int64_t b = 0; b < nb; b++) {
         __syncthreads();
-        b_store<NT>(bs, lds);
+#pragma unroll
+        for (int i = 0; i < BStage<NT>::NV; i++)
+            if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
         __syncthreads();
         if (b + 1 < nb) {
-            b_fetch<NT>(bs, a, c0, b + 1);
+#pragma unroll
+            for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + (b + 1) * 320);
             q4k_fetch_a(An, wa, wh, nb, b + 1, q);
         }
         // the 4 rows' 6-bit scales and mins, and their block scales
@@ -261,29 +273,34 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
-            // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
-            int sumi[4] = {0, 0, 0, 0}, dmins[4] = {0, 0, 0, 0};
+            // the tile's 8 operand reads and 8 products back to back, then the
+            // exact integer sums (any order) and the f32 steps
+            long bl[4], bh[4];
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
-                const v4i dl = mfma_i8(lo[g4], *(const long *)(col + 64 * g4 + 8 * q));
-                const v4i dh = mfma_i8(hi[g4], *(const long *)(col + 64 * g4 + 32 + 8 * q));
+                bl[g4] = *(const long *)(col + 64 * g4 + 8 * q);
+                bh[g4] = *(const long *)(col + 64 * g4 + 32 + 8 * q);
+            }
+            v4i dl[4], dh[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    sumi[i] += __mul24(dl[i], sc[i][2 * g4]) + __mul24(dh[i], sc[i][2 * g4 + 1]);
+            for (int g4 = 0; g4 < 4; g4++) {
+                dl[g4] = mfma_i8(lo[g4], bl[g4]);
+                dh[g4] = mfma_i8(hi[g4], bh[g4]);
             }
             const int4 s0 = *(const int4 *)(col + 256), s1 = *(const int4 *)(col + 272);
             const float xs = *(const float *)(col + 288);
             const int bsum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
+                int sumi = 0, dmins = 0;
 #pragma unroll
-                for (int s2 = 0; s2 < 8; s2++) dmins[i] += __mul24(bsum[s2], mn[i][s2]);
-                acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi[i])),
-                                      __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins[i]));
+                for (int g4 = 0; g4 < 4; g4++)
+                    sumi += __mul24(dl[g4][i], sc[i][2 * g4]) + __mul24(dh[g4][i], sc[i][2 * g4 + 1]);
+#pragma unroll
+                for (int s2 = 0; s2 < 8; s2++) dmins += __mul24(bsum[s2], mn[i][s2]);
+                acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi)),
+                                      __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins));
             }
-            // one column tile at a time: the products of later tiles are not
-            // hoisted (their results would all be live at once)
-            __builtin_amdgcn_sched_barrier(0);
         }
         if (b + 1 < nb) A = An;
     }
@@ -498,15 +515,18 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
 #pragma unroll
             for (int n = 0; n < NT; n++) {
                 // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
-                int sumi[4] = {0, 0, 0, 0};
+                v4i dl[4], dh[4];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
-                    const v4i dl = mfma_i8(lo[g4], B.lo[n][g4]);
-                    const v4i dh = mfma_i8(hi[g4], B.hi[n][g4]);
+                    dl[g4] = mfma_i8(lo[g4], B.lo[n][g4]);
+                    dh[g4] = mfma_i8(hi[g4], B.hi[n][g4]);
+                }
+                int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        sumi[i] += __mul24(dl[i], sc[i][2 * g4]) + __mul24(dh[i], sc[i][2 * g4 + 1]);
-                }
+                        sumi[i] += __mul24(dl[g4][i], sc[i][2 * g4]) + __mul24(dh[g4][i], sc[i][2 * g4 + 1]);
                 const int bsum[8] = {B.s0[n].x, B.s0[n].y, B.s0[n].z, B.s0[n].w,
                                      B.s1[n].x, B.s1[n].y, B.s1[n].z, B.s1[n].w};
 #pragma unroll
@@ -570,7 +590,10 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
         gemm_q4k<NT>(a, lds);                                                              \
     }
 GEMM_KERNELS(2)
-GEMM_KERNELS(4)
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q80_n4(cj_gemv_args a) {
+    __shared__ __align__(16) uint8_t lds[16 * 4 * GEMM_CS];
+    gemm_q80<4>(a, lds);
+}
 
 // Split-K kernels: 16 rows × 16·NT columns a workgroup of 8 waves (the
 // widths whose registers fit two waves a SIMD without spilling).

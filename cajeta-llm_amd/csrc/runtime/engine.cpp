@@ -1191,6 +1191,19 @@ int32_t cj_engine_decode_batch(int64_t h, const int32_t *slots, int32_t n, int32
     if (!slots) return cj::fail(CJ_ERR_ARG, "cj_engine_decode_batch: no slots");
     return e->decode_batch(slots, n, steps, out);
 }
+int32_t cj_engine_set_cpu_threads(int64_t h, int32_t threads) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    if (threads < 1 || threads > 65536) return cj::fail(CJ_ERR_ARG, "cpu threads %d (1..65536)", threads);
+    if (threads == e->workers) return CJ_OK;
+    CJ_HIP(hipStreamSynchronize(cj::stream()));
+    e->workers = threads;
+    // the captured steps hold the old split rule
+    for (auto &sq : e->seqs)
+        if (sq.graph) { (void)hipGraphExecDestroy(sq.graph); sq.graph = nullptr; }
+    if (e->batch_graph) { (void)hipGraphExecDestroy(e->batch_graph); e->batch_graph = nullptr; }
+    return CJ_OK;
+}
 int32_t cj_engine_set_prefill_chunk(int64_t h, int32_t rows) {
     Engine *e = eng_of(h);
     if (!e) return cj::fail(CJ_ERR_STATE, "null engine");

@@ -251,7 +251,8 @@ int run_gemm(const cj_gemv_args &a) {
     if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
     const char *fmt = a.type == CJ_Q8_0 ? "q80" : "q4k";
     char name[32];
-    const int nt = a.batch <= 32 ? 2 : 4;
+    // Q4_K's 64-column tile needs more registers than two waves a SIMD leave
+    const int nt = (a.batch <= 32 || a.type == CJ_Q4_K) ? 2 : 4;
     const int64_t tiles = ((a.rows + 63) / 64) * ((a.batch + 16 * nt - 1) / (16 * nt));
     if (tiles < 256 && a.batch <= 64) {
         const int sn = (a.type == CJ_Q8_0 && a.batch > 16) ? 2 : 1;
@@ -306,7 +307,7 @@ int32_t cj_init(int32_t device) {
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128",
         "cj_attn_merge", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
-        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q4k_n4",
+        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
         "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8", "cj_attn_merge_rows",

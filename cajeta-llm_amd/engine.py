@@ -23,7 +23,7 @@ class EngineOptions:
         self.ctx = 4096
         self.maxSeqs = 4
         self.device = ""
-        self.cpuThreads = 0
+        self.cpuThreads = 0      # the CPU worker count the attention split rule follows (0: 512)
         self.graphs = True       # replay the captured decode step (False: eager launches)
         self.prefillChunk = 512  # rows a prefill chunk (CausalLM.CHUNK_MAX); 0: one decode step a position
 
@@ -111,6 +111,8 @@ class LlmEngine:
         handle(h, "LlmEngine.load(%s)" % opts.model)
         if not getattr(opts, "graphs", True):
             check(lib().cj_engine_set_graphs(h, 0), "cj_engine_set_graphs")
+        if getattr(opts, "cpuThreads", 0):
+            check(lib().cj_engine_set_cpu_threads(h, int(opts.cpuThreads)), "cj_engine_set_cpu_threads")
         chunk = getattr(opts, "prefillChunk", 512)
         if chunk != 512:
             check(lib().cj_engine_set_prefill_chunk(h, int(chunk)), "cj_engine_set_prefill_chunk")

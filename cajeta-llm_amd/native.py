@@ -68,6 +68,7 @@ SIGNATURES = {
     "cj_engine_decode": (I32, [I64, I32, I32, P]),
     "cj_engine_decode_batch": (I32, [I64, P, I32, I32, P]),
     "cj_engine_set_prefill_chunk": (I32, [I64, I32]),
+    "cj_engine_set_cpu_threads": (I32, [I64, I32]),
     "cj_engine_logits": (I32, [I64, I32, P, I64]),
     "cj_engine_preds": (I32, [I64, I32, P, I32]),
     "cj_engine_last_step_us": (F32, [I64]),

@@ -237,6 +237,12 @@ int32_t cj_engine_decode(int64_t eng, int32_t seq, int32_t steps, int32_t *out_t
  * io/QuantKernel.cajeta:33646, and batch attention, model/AttnKernel.cajeta:5761,
  * :6599). out_tokens[i·n + r] is slot r's token i. */
 int32_t cj_engine_decode_batch(int64_t eng, const int32_t *slots, int32_t n, int32_t steps, int32_t *out_tokens);
+/* The CPU worker count the attention's split rule divides by
+ * (EngineOptions.cpuThreads → Device.multiprocessorCount on the CPU backend,
+ * AttnKernel.cpuDecodeSplits, model/AttnKernel.cajeta:4879-4889): the split
+ * count, and with it the rounding of the merged attention, follow it exactly
+ * as the reference's CPU backend with that many workers would. Default 512. */
+int32_t cj_engine_set_cpu_threads(int64_t eng, int32_t threads);
 /* Rows a prefill chunk (CausalLM.CHUNK_MAX, model/CausalLM.cajeta:52; at most
  * the row buffers' capacity); 0 or 1: prefill as one decode step a position. */
 int32_t cj_engine_set_prefill_chunk(int64_t eng, int32_t rows);
