@@ -362,7 +362,7 @@ def run_single(args, pkg, native, which):
         try:
             us, nbytes, kn = eng.timeKernel(kind, args.kernel_reps)
         except pkg.LlmException as e:
-            if "launches nothing" not in str(e):
+            if "launches nothing" not in str(e) and "not part of" not in str(e):
                 raise
             continue
         kernels[kname] = {"kernel": kn, "avg_us": round(us, 3), "bytes": nbytes,

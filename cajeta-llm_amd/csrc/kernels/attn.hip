@@ -19,8 +19,8 @@
 //   interleaved sub-sums.
 // cj_attn_scores_* + cj_attn_combine_*: attnScoreKernel (:397-425) and
 //   attnCombineKernel (:441-515): 32-lane strided dot + butterfly, then 128
-//   lanes for max, exp and sum (stride-halving tree) and the ascending-t sum
-//   of p·v per output dimension.
+//   lanes for exp and sum (stride-halving tree) and the ascending-t sum of
+//   p·v per output dimension, its products staged through LDS.
 #include "common.h"
 
 #define ATTN_MAX_SPLITS 64
@@ -383,55 +383,125 @@ SPLIT_KERNEL(8)
 
 // ------------------------------------------------------------ two-pass form
 
-// scores[h][t] = scale · (q_h · K[from+t]): one 32-lane group per (h, t),
-// lane i over d = i, i+32, ..., then a butterfly over the 32 lanes.
+// scores[h][t] = scale · (q_h · K[from+t]) in the reference's sum order:
+// partial i (i < 32) adds q[d]·k[d] for d = i, i+32, ... from 0, then the
+// xor-butterfly's pairs (16, 8, 4, 2, 1) fold the partials — a fixed tree, so
+// one lane can form all of it. Lane = position: a workgroup takes 256
+// positions of one kv head (grid: position blocks × kv heads), loads each K
+// row once and scores it against every query head of the group (q in LDS,
+// read as broadcasts). Dynamic LDS: group × HD floats.
 template <int HD>
 DEV void scores_body(const cj_attn_args &a) {
+    extern __shared__ __align__(16) float qs[];
     int count, from;
     attn_window(a, count, from);
-    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
-    const int64_t idx = (int64_t)blockIdx.x * 8 + g;
-    const int grp = a.n_q / a.n_kv;
-    const bool ok = idx < (int64_t)a.n_q * count;
-    const int h = ok ? (int)(idx / count) : 0, t = ok ? (int)(idx % count) : 0;
-    float s = 0.0f;
-    if (ok) {
-        const int64_t kb = kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, h / grp, HD);
-        for (int d = i; d < HD; d += 32) s = __fadd_rn(s, __fmul_rn(a.q[(int64_t)h * HD + d], h2f(a.kc[kb + d])));
+    const int grp = a.n_q / a.n_kv, kvh = blockIdx.y;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x * 256 >= count) return;      // the whole workgroup idles past count
+    for (int i = threadIdx.x; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
+    __syncthreads();
+    if (t >= count) return;
+    const uint16_t *kr = a.kc + kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD);
+    float k[HD];
+#pragma unroll
+    for (int j = 0; j < HD / 8; j++) {
+        const u32x4 v = *(const u32x4 *)(kr + 8 * j);
+        k[8 * j + 0] = h2f(v.x); k[8 * j + 1] = h2f(v.x >> 16);
+        k[8 * j + 2] = h2f(v.y); k[8 * j + 3] = h2f(v.y >> 16);
+        k[8 * j + 4] = h2f(v.z); k[8 * j + 5] = h2f(v.z >> 16);
+        k[8 * j + 6] = h2f(v.w); k[8 * j + 7] = h2f(v.w >> 16);
     }
-    s = __fadd_rn(s, __shfl_xor(s, 16, 32));
-    s = __fadd_rn(s, __shfl_xor(s, 8, 32));
-    s = __fadd_rn(s, __shfl_xor(s, 4, 32));
-    s = __fadd_rn(s, __shfl_xor(s, 2, 32));
-    s = __fadd_rn(s, __shfl_xor(s, 1, 32));
-    if (ok && i == 0) a.part[(int64_t)h * a.splits + t] = __fmul_rn(s, a.scale);
+    for (int g = 0; g < grp; g++) {
+        const float *q = qs + g * HD;
+        float p[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) p[i] = 0.0f;
+#pragma unroll
+        for (int d0 = 0; d0 < HD; d0 += 32) {
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 qv = *(const float4 *)(q + d0 + i);
+                p[i] = __fadd_rn(p[i], __fmul_rn(qv.x, k[d0 + i]));
+                p[i + 1] = __fadd_rn(p[i + 1], __fmul_rn(qv.y, k[d0 + i + 1]));
+                p[i + 2] = __fadd_rn(p[i + 2], __fmul_rn(qv.z, k[d0 + i + 2]));
+                p[i + 3] = __fadd_rn(p[i + 3], __fmul_rn(qv.w, k[d0 + i + 3]));
+            }
+        }
+#pragma unroll
+        for (int m = 16; m > 0; m >>= 1) {
+#pragma unroll
+            for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
+        }
+        a.part[(int64_t)(kvh * grp + g) * a.splits + t] = __fmul_rn(p[0], a.scale);
+    }
 }
 
 // softmax over scores[h][0..count) in place and out[h] = Σ_t p_t·V_t / Σ p:
-// one workgroup of 128 per query head.
+// one workgroup of 256 per query head.
+//   max   all 256 lanes (max is exact, so any order gives the same value);
+//   sum   lanes 0..127 as the reference's 128: lane l adds e_t for t = l,
+//         l+128, ... in order (e_t written over the score), then the
+//         stride-halving tree;
+//   p·V   each output dimension's ascending-t sum is one lane's chain in the
+//         first HD/64 waves (the adders). The other waves (producers) stage
+//         the rounded products e_t·v_t[d] through LDS one tile ahead, so an
+//         adder spends 1.25 instructions a position: a 16-byte LDS read of
+//         four positions' products, then four adds. Positions past count are
+//         staged as +0, which leaves the sum's bits unchanged (the sum starts
+//         at +0 and so is never -0); their loads read position count-1.
 template <int HD>
 DEV void combine_body(const cj_attn_args &a) {
-    __shared__ float red[128];
+    constexpr int A = HD / 64;               // adder waves
+    constexpr int P = 256 - 64 * A;          // producer lanes
+    constexpr int DG = HD / 8;               // 8-dimension groups of a V row
+    constexpr int TQ = P / DG;               // 4-position groups a tile: one 4 × 8 item a producer lane
+    constexpr int T = 4 * TQ;                // positions a tile
+    constexpr int S = T + 4;                 // product row stride (floats): 16 lanes' 16-byte reads hit distinct banks
+    __shared__ float red[256];
+    __shared__ __align__(16) float prod[2][HD * S];
     int count, from;
     attn_window(a, count, from);
     const int h = blockIdx.x, l = threadIdx.x;
     const int grp = a.n_q / a.n_kv, kvh = h / grp;
     float *sc = a.part + (int64_t)h * a.splits;
+
     float mx = -3.0e38f;
-    for (int t = l; t < count; t += 128) if (sc[t] > mx) mx = sc[t];
+    {
+        int t = l;
+        for (; t + 768 < count; t += 1024) {
+            const float x0 = sc[t], x1 = sc[t + 256], x2 = sc[t + 512], x3 = sc[t + 768];
+            if (x0 > mx) mx = x0;
+            if (x1 > mx) mx = x1;
+            if (x2 > mx) mx = x2;
+            if (x3 > mx) mx = x3;
+        }
+        for (; t < count; t += 256) if (sc[t] > mx) mx = sc[t];
+    }
     red[l] = mx;
     __syncthreads();
-    for (int r = 64; r > 0; r >>= 1) {
+    for (int r = 128; r > 0; r >>= 1) {
         if (l < r && red[l + r] > red[l]) red[l] = red[l + r];
         __syncthreads();
     }
     const float m = red[0];
     __syncthreads();
     float s = 0.0f;
-    for (int t = l; t < count; t += 128) {
-        const float e = cj_expf(sc[t] - m);
-        sc[t] = e;
-        s = __fadd_rn(s, e);
+    if (l < 128) {
+        int t = l;
+        for (; t + 384 < count; t += 512) {
+            const float x0 = sc[t], x1 = sc[t + 128], x2 = sc[t + 256], x3 = sc[t + 384];
+            const float e0 = cj_expf(x0 - m), e1 = cj_expf(x1 - m), e2 = cj_expf(x2 - m), e3 = cj_expf(x3 - m);
+            sc[t] = e0; sc[t + 128] = e1; sc[t + 256] = e2; sc[t + 384] = e3;
+            s = __fadd_rn(s, e0);
+            s = __fadd_rn(s, e1);
+            s = __fadd_rn(s, e2);
+            s = __fadd_rn(s, e3);
+        }
+        for (; t < count; t += 128) {
+            const float e = cj_expf(sc[t] - m);
+            sc[t] = e;
+            s = __fadd_rn(s, e);
+        }
     }
     red[l] = s;
     __syncthreads();
@@ -440,20 +510,96 @@ DEV void combine_body(const cj_attn_args &a) {
         __syncthreads();
     }
     const float rs = __fdiv_rn(1.0f, red[0]);
-    for (int d = l; d < HD; d += 128) {
-        float acc = 0.0f;
-        for (int t = 0; t < count; t++) {
-            const int64_t vb = kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD);
-            acc = __fadd_rn(acc, __fmul_rn(sc[t], h2f(a.vc[vb + d])));
-        }
-        a.out[(int64_t)h * HD + d] = __fmul_rn(acc, rs);
+
+    const int w = l >> 6, ntiles = (count + T - 1) / T;
+    const int pl = l - 64 * A, tq = pl % TQ, dg = pl / TQ;
+    u32x4 va0, va1, va2, va3, vb0, vb1, vb2, vb3;
+    float ea[4], eb[4];
+    // a producer's item of tile i: positions i·T + 4·tq + k (k < 4), dimensions 8·dg..+7
+#define COMBINE_FETCH(I, V0, V1, V2, V3, E)                                                                    \
+    {                                                                                                           \
+        const int t0 = (I) * T + 4 * tq;                                                                        \
+        u32x4 *vv[4] = {&V0, &V1, &V2, &V3};                                                                    \
+        _Pragma("unroll") for (int k = 0; k < 4; k++) {                                                         \
+            const int t = min(t0 + k, count - 1);     /* past count: loaded, then staged as +0 */               \
+            *vv[k] = *(const u32x4 *)(a.vc + kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD) + 8 * dg);   \
+            E[k] = sc[t];                                                                                       \
+        }                                                                                                       \
     }
+#define COMBINE_STORE(B, I, V0, V1, V2, V3, E)                                                                 \
+    {                                                                                                           \
+        float *pb = prod[B] + 8 * dg * S + 4 * tq;                                                              \
+        const int t0 = (I) * T + 4 * tq;                                                                        \
+        const bool ok0 = t0 < count, ok1 = t0 + 1 < count, ok2 = t0 + 2 < count, ok3 = t0 + 3 < count;         \
+        _Pragma("unroll") for (int j = 0; j < 8; j++) {                                                         \
+            const int sh = 16 * (j & 1);                                                                        \
+            float4 o;                                                                                           \
+            o.x = ok0 ? __fmul_rn(E[0], h2f(V0[j >> 1] >> sh)) : 0.0f;                                          \
+            o.y = ok1 ? __fmul_rn(E[1], h2f(V1[j >> 1] >> sh)) : 0.0f;                                          \
+            o.z = ok2 ? __fmul_rn(E[2], h2f(V2[j >> 1] >> sh)) : 0.0f;                                          \
+            o.w = ok3 ? __fmul_rn(E[3], h2f(V3[j >> 1] >> sh)) : 0.0f;                                          \
+            *(float4 *)(pb + j * S) = o;                                                                        \
+        }                                                                                                       \
+    }
+    if (w >= A) {
+        COMBINE_FETCH(0, va0, va1, va2, va3, ea);
+        COMBINE_FETCH(1, vb0, vb1, vb2, vb3, eb);
+        COMBINE_STORE(0, 0, va0, va1, va2, va3, ea);
+        va0 = vb0; va1 = vb1; va2 = vb2; va3 = vb3;
+#pragma unroll
+        for (int k = 0; k < 4; k++) ea[k] = eb[k];
+        COMBINE_FETCH(2, vb0, vb1, vb2, vb3, eb);
+    }
+    __syncthreads();
+    // the roles run separate loops with the same barriers, so no branch sits
+    // between a producer's loads and their use
+    float acc = 0.0f;
+    if (w < A) {
+        const float *pr = prod[0] + (64 * w + (l & 63)) * S;
+        for (int i = 0; i < ntiles; i++) {
+            const float *pt = pr + (i & 1) * (HD * S);
+            const int n = min(T, count - i * T);
+            if (n == T) {
+#pragma unroll
+                for (int q = 0; q < T; q += 4) {
+                    const float4 p = *(const float4 *)(pt + q);
+                    acc = __fadd_rn(acc, p.x);
+                    acc = __fadd_rn(acc, p.y);
+                    acc = __fadd_rn(acc, p.z);
+                    acc = __fadd_rn(acc, p.w);
+                }
+            } else {
+                for (int q = 0; q < n; q += 4) {
+                    const float4 p = *(const float4 *)(pt + q);
+                    acc = __fadd_rn(acc, p.x);
+                    acc = __fadd_rn(acc, p.y);
+                    acc = __fadd_rn(acc, p.z);
+                    acc = __fadd_rn(acc, p.w);
+                }
+            }
+            __syncthreads();
+        }
+    } else {
+        // no branch in the body: the last round forms a tile past the end
+        // into the idle buffer, never read
+        for (int i = 0; i < ntiles; i++) {
+            COMBINE_STORE((i + 1) & 1, i + 1, va0, va1, va2, va3, ea);
+            va0 = vb0; va1 = vb1; va2 = vb2; va3 = vb3;
+#pragma unroll
+            for (int k = 0; k < 4; k++) ea[k] = eb[k];
+            COMBINE_FETCH(i + 3, vb0, vb1, vb2, vb3, eb);
+            __syncthreads();
+        }
+    }
+#undef COMBINE_FETCH
+#undef COMBINE_STORE
+    if (w < A) a.out[(int64_t)h * HD + 64 * w + (l & 63)] = __fmul_rn(acc, rs);
 }
 
 extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a); }
-extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a); }
-extern "C" __global__ void __launch_bounds__(128) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a); }
 
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
 // 256 per 256 output values (the reference's attnReducePackQ8Kernel

@@ -204,40 +204,31 @@ DEV float wave_shr1(float v, float first) {
 // [288,320) the f32 scale(s)). 256 threads; thread t owns element t of every
 // 256-wide block, so a block's amax is one workgroup reduction.
 //
-// The RMSNorm follows the reference CPU row form's order exactly: thread t
+// The RMSNorm follows the reference's device-decode order exactly: thread t
 // accumulates x[t + 256k]^2 in k order, then the 256 partials fold with
 // strides 128, 64, ..., 1 — the same adds, so the same bits.
 // ---------------------------------------------------------------------------
 
 #define STAGE_CHUNK 16     // 256-wide blocks held in registers at a time
 
-// RMSNorm scale of x[0..n): for whole 256s (the CPU row form,
-// Prim.rmsnormPackRowCpuKernel, model/Prim.cajeta:977-1071) thread t sums
-// x[t + 256k]^2 in k order and the 256 partials fold 128, 64, ..., 1 (lanes of
-// wave 0 for the last six); other widths sum in element order on one thread
-// (Prim.rmsnormRowHost, :120-151). Then 1/sqrt(ss/n + eps). `red` is 256
-// floats of LDS.
+// RMSNorm scale of x[0..n) in the order of the reference's device-decode
+// norms: thread t sums x[t + 256k]^2 in k order (t + 256k < n, so a width
+// that is not whole 256s leaves the last round ragged) and the 256 partials
+// fold 128, 64, ..., 1 (lanes of wave 0 for the last six). For whole 256s
+// that is the CPU row form (Prim.rmsnormPackRowCpuKernel, model/Prim.cajeta:
+// 977-1071); other widths take rmsnormRowF32 (:742-775) through
+// Prim.rmsnormDevice (:1440-1450), as the resident layer does for them
+// (CausalLM.cajeta:3643, :3819). Then 1/sqrt(ss/n + eps). `red` is 256 floats
+// of LDS.
 DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     const int t = threadIdx.x;
-    if (n & 255) {
-        if (t == 0) {
-            float s = 0.0f;
-            for (int64_t e = 0; e < n; e++) s = __fadd_rn(s, __fmul_rn(x[e], x[e]));
-            red[0] = s;
-        }
-        __syncthreads();
-        const float ss = red[0];
-        __syncthreads();
-        return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
-    }
     // the row's values loaded at once (up to 64 a thread), then summed in order
     float xv[64];
-    const int kn = (int)(n >> 8);
 #pragma unroll
-    for (int k = 0; k < 64; k++) xv[k] = k < kn ? x[t + 256 * k] : 0.0f;
+    for (int k = 0; k < 64; k++) xv[k] = t + 256 * k < n ? x[t + 256 * k] : 0.0f;
     float p = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 64; k++) if (k < kn) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
+    for (int k = 0; k < 64; k++) if (t + 256 * k < n) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
     for (int64_t e = t + 256 * 64; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
     __syncthreads();

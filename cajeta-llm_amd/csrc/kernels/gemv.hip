@@ -15,8 +15,8 @@
 //            epilogue: store, residual accumulate, RoPE + the fp16 K/V append,
 //            SiLU·up + the pack of the result, or the greedy argmax.
 //
-// The f32-activation formats (Q4_0, MXFP4, the f32 router) are summed by one
-// thread a row in the reference's element order.
+// The f32-activation formats (Q4_0, MXFP4, the f32 router) are summed in the
+// reference's element order, one adder lane a row fed products through LDS.
 //
 // Q4_K has its own body (gemv_q4k_body): one lane a whole 256-element block,
 // the first weight block of every lane in flight before the prologue, and
@@ -212,57 +212,6 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
             if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
     }
-}
-
-// f32-activation formats: one thread a row, the row summed in the
-// reference's element order, x from LDS.
-//   Q4_0  : Quant.q40MatVecIntoAt (io/Quant.cajeta:1516-1545): per block, dot over the
-//           16 byte pairs (low nibble then high), then acc + d·dot.
-//   MXFP4 : Quant.mxfp4MatVecIntoScalar (io/Quant.cajeta:1146-1182):
-//           acc + code·d·x element by element.
-//   F32   : the router's plain row dot in column order.
-template <int FMT>
-DEV float seq_row(const uint8_t *wr, const float *xs, int64_t cols, const float *lut) {
-    float acc = 0.0f;
-    if (FMT == CJ_F32) {
-        const float4 *w4 = (const float4 *)wr;
-        for (int64_t u = 0; u < cols / 4; u++) {
-            const float4 w = w4[u];
-            const float4 x = *(const float4 *)(xs + 4 * u);
-            acc = __fadd_rn(acc, __fmul_rn(w.x, x.x));
-            acc = __fadd_rn(acc, __fmul_rn(w.y, x.y));
-            acc = __fadd_rn(acc, __fmul_rn(w.z, x.z));
-            acc = __fadd_rn(acc, __fmul_rn(w.w, x.w));
-        }
-        return acc;
-    }
-    const int nb32 = (int)(cols / 32);
-    for (int u = 0; u < nb32; u++) {
-        const uint4 q = *(const uint4 *)(wr + (int64_t)u * 16);
-        const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
-        const float *xb = xs + u * 32;
-        if (FMT == CJ_Q4_0) {
-            const float dv = h2f(*(const uint16_t *)(wr + (int64_t)nb32 * 16 + 2 * u));
-            float dot = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < 16; jj++) {
-                const int b = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
-                dot = __fadd_rn(dot, __fmul_rn((float)((b & 15) - 8), xb[jj]));
-                dot = __fadd_rn(dot, __fmul_rn((float)((b >> 4) - 8), xb[jj + 16]));
-            }
-            acc = __fadd_rn(acc, __fmul_rn(dv, dot));
-        } else {
-            const float d = mxfp4_scale(wr[(int64_t)nb32 * 16 + u]);
-#pragma unroll
-            for (int k = 0; k < 32; k++) {
-                const int jj = k & 15;
-                const uint32_t b = (ws[jj >> 2] >> (8 * (jj & 3))) & 255;
-                const uint32_t nib = k < 16 ? (b & 15) : (b >> 4);
-                acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(lut[nib], d), xb[k]));
-            }
-        }
-    }
-    return acc;
 }
 
 // ------------------------------------------------------------- epilogues
@@ -535,6 +484,183 @@ DEV void gemv_epilogue(const cj_gemv_args &a, const GemvSlice &sl, float v, floa
     }
 }
 
+// f32-activation formats, summed in the reference's element order:
+//   Q4_0  : Quant.q40MatVecIntoAt (io/Quant.cajeta:1516-1545): per block, dot
+//           from 0 over the 16 byte pairs (low nibble then high), then
+//           acc + d·dot;
+//   MXFP4 : Quant.mxfp4MatVecIntoScalar (io/Quant.cajeta:1146-1182):
+//           acc + (code·d)·x element by element;
+//   F32   : the router's plain row dot in column order.
+// Each row's sum is one dependent chain, so the work splits by role. Lane r
+// of the first wave (the adder) owns row r of the workgroup's 64 and only
+// adds: its row's rounded products arrive through LDS in the order it adds
+// them, a 16-byte read of four, so the chain costs 1.25 instructions an
+// element. The other three waves (producers) form the products one tile
+// ahead: in a tile of SEQ_TB 32-element blocks, producer wave p + 1 owns
+// block p of all 64 rows (one row a lane, x a broadcast from LDS), its next
+// tile's weights already loaded into registers.
+#define SEQ_TB 3                   // blocks a tile: one a producer wave
+#define SEQ_S (32 * SEQ_TB + 4)    // product row stride (floats): 16-byte reads by 16 lanes hit distinct banks
+
+template <int FMT>
+struct SeqItem {
+    u32x4 q[FMT == CJ_F32 ? 8 : 1];
+    uint32_t s;
+};
+
+// One row block's weights: 32 f32, or the 16 code bytes and the block scale.
+template <int FMT>
+DEV SeqItem<FMT> seq_fetch(const uint8_t *wr, int nb32, int blk) {
+    SeqItem<FMT> it;
+    blk = min(blk, nb32 - 1);     // a block past the row is formed but never added
+    if constexpr (FMT == CJ_F32) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) it.q[j] = *(const u32x4 *)(wr + (int64_t)blk * 128 + 16 * j);
+        it.s = 0;
+    } else {
+        it.q[0] = *(const u32x4 *)(wr + (int64_t)blk * 16);
+        if constexpr (FMT == CJ_Q4_0) it.s = *(const uint16_t *)(wr + (int64_t)nb32 * 16 + 2 * blk);
+        else it.s = wr[(int64_t)nb32 * 16 + blk];
+    }
+    return it;
+}
+
+// The block's 32 rounded products in add order into dst (and Q4_0's d).
+template <int FMT>
+DEV void seq_products(const SeqItem<FMT> &it, const float *xb, float *dst, float *dv) {
+    if constexpr (FMT == CJ_F32) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 x = *(const float4 *)(xb + 4 * j);
+            float4 o;
+            o.x = __fmul_rn(__uint_as_float(it.q[j].x), x.x);
+            o.y = __fmul_rn(__uint_as_float(it.q[j].y), x.y);
+            o.z = __fmul_rn(__uint_as_float(it.q[j].z), x.z);
+            o.w = __fmul_rn(__uint_as_float(it.q[j].w), x.w);
+            *(float4 *)(dst + 4 * j) = o;
+        }
+    } else if constexpr (FMT == CJ_MXFP4) {
+        // element k: code byte k & 15, low nibble for k < 16, high after;
+        // |code| from the low three bits by a byte permute of {0,1,2,3,4,6,8,12},
+        // the sign from bit 3. Code 8 comes out as -0 where the reference has
+        // +0: its product is a zero either way, and a zero added to the sum
+        // (which starts at +0, so is never -0) changes no bit.
+        const float d = mxfp4_scale(it.s);
+        const uint32_t ws[4] = {it.q[0].x, it.q[0].y, it.q[0].z, it.q[0].w};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint32_t nibs = g < 4 ? (ws[g & 3] & 0x0f0f0f0fu) : ((ws[g & 3] >> 4) & 0x0f0f0f0fu);
+            const uint32_t mag = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, nibs & 0x07070707u);
+            const float4 x = *(const float4 *)(xb + 4 * g);
+            const float xv[4] = {x.x, x.y, x.z, x.w};
+            float ov[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const float c = __uint_as_float(__float_as_uint((float)((mag >> (8 * kk)) & 255u)) ^
+                                                (((nibs >> (8 * kk + 3)) & 1u) << 31));
+                ov[kk] = __fmul_rn(__fmul_rn(c, d), xv[kk]);
+            }
+            *(float4 *)(dst + 4 * g) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+        }
+    } else {
+        // products (lo_j − 8)·x[j], (hi_j − 8)·x[j + 16], j ascending
+        *dv = h2f(it.s);
+        const uint32_t ws[4] = {it.q[0].x, it.q[0].y, it.q[0].z, it.q[0].w};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint32_t word = ws[g >> 1], sh = 16 * (g & 1);
+            const float4 xl = *(const float4 *)(xb + 4 * (g >> 1)), xh = *(const float4 *)(xb + 16 + 4 * (g >> 1));
+            const uint32_t b0 = (word >> sh) & 255u, b1 = (word >> (sh + 8)) & 255u;
+            float4 o;
+            o.x = __fmul_rn((float)(int)(b0 & 15u) - 8.0f, g & 1 ? xl.z : xl.x);
+            o.y = __fmul_rn((float)(int)(b0 >> 4) - 8.0f, g & 1 ? xh.z : xh.x);
+            o.z = __fmul_rn((float)(int)(b1 & 15u) - 8.0f, g & 1 ? xl.w : xl.y);
+            o.w = __fmul_rn((float)(int)(b1 >> 4) - 8.0f, g & 1 ? xh.w : xh.y);
+            *(float4 *)(dst + 4 * g) = o;
+        }
+    }
+}
+
+// Row threadIdx.x (< 64) of the workgroup's rows summed; x staged in LDS.
+// Every thread of the workgroup must call it (it holds barriers). A producer
+// lane keeps D tiles of its weights in flight (a ring indexed at compile
+// time: the tile loop is unrolled by D).
+template <int FMT>
+DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
+    constexpr int D = FMT == CJ_F32 ? 4 : 8;
+    static_assert(D % 2 == 0, "the ring depth must be even");
+    __shared__ __align__(16) float prod[2][64 * SEQ_S];
+    __shared__ float dvs[2][64 * SEQ_TB];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int nb32 = (int)(a.cols / 32), ntiles = (nb32 + SEQ_TB - 1) / SEQ_TB;
+    const int pb = w - 1;
+    const uint8_t *wr = sl.W + min(sl.row0 + lane, a.rows - 1) * a.row_bytes;
+    float *pdst = prod[0] + lane * SEQ_S + 32 * pb, *pdv = dvs[0] + lane * SEQ_TB + pb;
+    constexpr int PBUF = 64 * SEQ_S, DBUF = 64 * SEQ_TB;
+    SeqItem<FMT> ring[D];
+    if (w > 0) {
+#pragma unroll
+        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * SEQ_TB + pb);
+        seq_products<FMT>(ring[0], xs + 32 * min(pb, nb32 - 1), pdst, pdv);
+        ring[0] = seq_fetch<FMT>(wr, nb32, D * SEQ_TB + pb);
+    }
+    __syncthreads();
+    // the roles run separate loops (the same barriers in the same number), so
+    // no branch sits between a producer's loads and their use and the loads
+    // of the ring stay in flight across tiles
+    float acc = 0.0f;
+    // both loops run a whole number of D-tile rounds: the producer's body
+    // is then free of branches (tiles past the end are formed into the idle
+    // buffer and never read)
+    const int nit = (ntiles + D - 1) / D * D;
+    if (w == 0) {
+        const float *pr0 = prod[0] + lane * SEQ_S;
+        const float *dv0 = dvs[0] + lane * SEQ_TB;
+        for (int i = 0; i < nit; i++) {
+            const float *pr = pr0 + (i & 1) * PBUF;
+            const int nb = i < ntiles ? min(SEQ_TB, nb32 - i * SEQ_TB) : 0;
+            for (int b = 0; b < nb; b++) {
+                if constexpr (FMT == CJ_Q4_0) {
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                        dot = __fadd_rn(dot, p.x);
+                        dot = __fadd_rn(dot, p.y);
+                        dot = __fadd_rn(dot, p.z);
+                        dot = __fadd_rn(dot, p.w);
+                    }
+                    acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                        acc = __fadd_rn(acc, p.x);
+                        acc = __fadd_rn(acc, p.y);
+                        acc = __fadd_rn(acc, p.z);
+                        acc = __fadd_rn(acc, p.w);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    } else {
+        for (int i0 = 0; i0 < nit; i0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                const int i = i0 + j;
+                const int r = (j + 1) % D;
+                const int blk = min((i + 1) * SEQ_TB + pb, nb32 - 1);
+                const int nbuf = (j + 1) & 1;      // D is even, so (i + 1) & 1
+                seq_products<FMT>(ring[r], xs + 32 * blk, pdst + nbuf * PBUF, pdv + nbuf * DBUF);
+                ring[r] = seq_fetch<FMT>(wr, nb32, (i + 1 + D) * SEQ_TB + pb);
+                __syncthreads();
+            }
+        }
+    }
+    return acc;
+}
+
 // Generic body (Q6_K, Q8_0 and the f32-activation formats).
 template <int FMT, int LPR, int NR>
 DEV void gemv_body(const cj_gemv_args &a) {
@@ -560,11 +686,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
     const int64_t r = row0 + t;
     const bool live = t < R && r < a.rows;
     if constexpr (f32act) {
-        // ---- one thread a row, in element order
-        __shared__ float lut[16];
-        if (t < 16) lut[t] = mxfp4_val(t);
-        __syncthreads();
-        if (live) v = seq_row<FMT>(sl.W + r * a.row_bytes, (const float *)sx, cols, lut);
+        // ---- one adder lane a row, in element order (64 rows a workgroup)
+        const float sv = seq_body<FMT>(a, sl, (const float *)sx);
+        if (live) v = sv;
     } else {
     // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
     {

@@ -27,9 +27,9 @@ extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
 
 // RMSNorm + pack of one row, one workgroup per 256-wide block. Every
 // workgroup forms the row's sum of squares itself in the reference order
-// (thread t: x[t + 256k], k ascending, then the 128..1 tree; or element order
-// for widths that are not whole 256s) from loads it issues at once, then
-// packs its own block: no workgroup waits on another.
+// (thread t: x[t + 256k], k ascending, ragged past the width, then the
+// 128..1 tree) from loads it issues at once, then packs its own block: no
+// workgroup waits on another.
 extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) {
     __shared__ float red[256];
     __shared__ float bmax[8];
@@ -376,33 +376,74 @@ extern "C" __global__ void __launch_bounds__(256) cj_zero(cj_zero_args a) {
 
 // MoeFfn.routeFromLogits per row: softmax over the experts, top-k by
 // probability with strict > (ties keep the lower index), then the optional
-// renormalisation by the sum clamped at 2^-14. One workgroup per row.
+// renormalisation by the sum clamped at 2^-14. One wave per row (up to 256
+// experts): the logits and probabilities live in LDS; the max and the sum run
+// on one lane in expert order as the reference forms them, the exps and the
+// divides a lane an expert, and each top-k pick is a wave reduction — the
+// largest valid probability, the lowest index among equals, which is the
+// first strict maximum of the reference's scan whatever order finds it.
 extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
-    __shared__ float pr[256];
-    const int row = blockIdx.x, t = threadIdx.x;
-    const float *lg = a.logits + (int64_t)row * a.n_experts;
+    __shared__ float lgs[256], pr[256];
+    __shared__ float bc[2];
+    __shared__ int sel_s[64];
+    __shared__ float w_s[64];
+    const int row = blockIdx.x, t = threadIdx.x, ne = a.n_experts;
+    const float *lg = a.logits + (int64_t)row * ne;
+    for (int e = t; e < ne; e += 64) lgs[e] = lg[e];
+    __syncthreads();
     if (t == 0) {
-        float mx = lg[0];
-        for (int e = 1; e < a.n_experts; e++) if (lg[e] > mx) mx = lg[e];
+        float mx = lgs[0];
+        for (int e = 1; e < ne; e++) if (lgs[e] > mx) mx = lgs[e];
+        bc[0] = mx;
+    }
+    __syncthreads();
+    const float mx = bc[0];
+    for (int e = t; e < ne; e += 64) pr[e] = cj_expf(lgs[e] - mx);
+    __syncthreads();
+    if (t == 0) {
         float sum = 0.0f;
-        for (int e = 0; e < a.n_experts; e++) { const float p = cj_expf(lg[e] - mx); pr[e] = p; sum = __fadd_rn(sum, p); }
-        for (int e = 0; e < a.n_experts; e++) pr[e] = __fdiv_rn(pr[e], sum);
-        float w[16];
-        int s[16];
-        for (int k = 0; k < a.n_used; k++) {
-            int best = -1; float bp = 0.0f;
-            for (int e = 0; e < a.n_experts; e++)
-                if (pr[e] >= 0.0f && (best < 0 || pr[e] > bp)) { best = e; bp = pr[e]; }
-            if (best < 0) best = 0;   // non-finite logits; the host checks the weights
-            s[k] = best; w[k] = bp; pr[best] = -1.0f;
+        for (int e = 0; e < ne; e++) sum = __fadd_rn(sum, pr[e]);
+        bc[1] = sum;
+    }
+    __syncthreads();
+    const float sum = bc[1];
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = t + 64 * j;
+        v[j] = e < ne ? __fdiv_rn(pr[e], sum) : -1.0f;   // -1: no expert (never valid)
+    }
+    for (int k = 0; k < a.n_used; k++) {
+        float bv = 0.0f;
+        int bi = -1;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (v[j] >= 0.0f && (bi < 0 || v[j] > bv)) { bv = v[j]; bi = t + 64 * j; }
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) {
+            const float ov = __shfl_xor(bv, m);
+            const int oi = __shfl_xor(bi, m);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
         }
+        if (bi < 0) { bi = 0; bv = 0.0f; }   // non-finite logits; the host checks the weights
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (t + 64 * j == bi) v[j] = -1.0f;
+        if (t == 0) { sel_s[k] = bi; w_s[k] = bv; }
+    }
+    __syncthreads();
+    if (t == 0) {
         if (a.norm_topk) {
             float ws = 0.0f;
-            for (int k = 0; k < a.n_used; k++) ws = __fadd_rn(ws, w[k]);
+            for (int k = 0; k < a.n_used; k++) ws = __fadd_rn(ws, w_s[k]);
             if (ws < 0.00006103515625f) ws = 0.00006103515625f;
-            for (int k = 0; k < a.n_used; k++) w[k] = __fdiv_rn(w[k], ws);
+            for (int k = 0; k < a.n_used; k++) w_s[k] = __fdiv_rn(w_s[k], ws);
         }
-        for (int k = 0; k < a.n_used; k++) { a.sel[row * a.n_used + k] = s[k]; a.w[row * a.n_used + k] = w[k]; }
+    }
+    __syncthreads();
+    if (t < a.n_used) {
+        a.sel[row * a.n_used + t] = sel_s[t];
+        a.w[row * a.n_used + t] = w_s[t];
     }
 }
 

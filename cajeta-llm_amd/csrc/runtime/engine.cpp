@@ -263,6 +263,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     n_used = (int)file.get_int(kp + "expert_used_count", 0);
     expert_ffn = (int)file.get_int(kp + "expert_feed_forward_length", ffn);
     norm_topk = (int)file.get_int(kp + "expert_weights_norm", 1);
+    if (n_experts < 0 || n_experts > 256 || (n_experts > 0 && (n_used <= 0 || n_used > 16 || n_used > n_experts)))
+        return fail(CJ_ERR_IO, "model: %d experts, %d used (served: up to 256, 1..16 used)", n_experts, n_used);
     const int swa = (int)file.get_int(kp + "attention.sliding_window", 0);
     const GgufTensor *te = file.tensor("token_embd.weight");
     if (!te) return fail(CJ_ERR_IO, "model: token_embd.weight is missing");
@@ -489,8 +491,10 @@ int Engine::enqueue_step(int s) {
                 // the grid covers the longest window; the kernel idles past count
                 a.splits = ctx;
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
-                if ((rc = launch(attn_kernel, (uint32_t)(((int64_t)n_heads * span + 7) / 8), 256, 0, a))) return rc;
-                if ((rc = launch(combine_kernel, (uint32_t)n_heads, 128, 0, a))) return rc;
+                if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_kv, 256,
+                                  (uint32_t)(grp * head_dim * 4), a)))
+                    return rc;
+                if ((rc = launch(combine_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
             }
         }
         if (want(K_O, l)) {   // 3. o projection, residual into hs

@@ -205,10 +205,10 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
     const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
                       : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
     if (is_f32_act(type)) {
-        // one thread a row, summed in element order
+        // 64 rows a workgroup, each summed in element order by one lane
         p.kernel = fam;
-        p.rows_per_wg = 256;
-        p.grid = (uint32_t)((rows + 255) / 256);
+        p.rows_per_wg = 64;
+        p.grid = (uint32_t)((rows + 63) / 64);
         p.per_copy = p.grid;
         p.lds = 3072 + (uint32_t)((cols + 255) / 256 * 1024);
         return p;
@@ -271,6 +271,8 @@ int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
     cj_gemv_args a = a0;
     a.rows_per_wg = p.rows_per_wg;
     if (p.lds > 65536) return fail(CJ_ERR_ARG, "gemv %s: %u bytes of LDS exceed 64 KB", p.kernel.c_str(), p.lds);
+    if (is_f32_act(a.type) && a.cols % 32)
+        return fail(CJ_ERR_ARG, "gemv %s: %lld columns are not whole 32-element blocks", p.kernel.c_str(), (long long)a.cols);
     const uint32_t grid = a.sel ? p.per_copy * (uint32_t)a.n_sel : p.grid;
     return launch(p.kernel.c_str(), grid, 256, p.lds, a);
 }
@@ -615,7 +617,8 @@ int32_t cj_qk_prep(int64_t q, int64_t k, int64_t v, int64_t kcache, int64_t vcac
 int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t vcache, int64_t pgtab, int32_t pg_base,
                   int64_t counters, int32_t n_q, int32_t n_kv, int32_t head_dim, int32_t count, int32_t from,
                   int32_t workers, float scale) {
-    if (n_kv <= 0 || n_q <= 0 || n_q % n_kv || (head_dim != 64 && head_dim != 128) || count <= 0 || from < 0 || workers <= 0)
+    if (n_kv <= 0 || n_q <= 0 || n_q % n_kv || n_q / n_kv > 64 || (head_dim != 64 && head_dim != 128) || count <= 0 ||
+        from < 0 || workers <= 0)
         return fail(CJ_ERR_ARG, "cj_attend: heads %d/%d hd %d count %d workers %d", n_q, n_kv, head_dim, count, workers);
     const int grp = n_q / n_kv;
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
@@ -649,9 +652,10 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     }
     a.splits = count;   // the scores row stride
     snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
-    if (int32_t rc = launch(name, (uint32_t)(((int64_t)n_q * count + 7) / 8), 256, 0, a)) return rc;
+    if (int32_t rc = launch2(name, (uint32_t)((count + 255) / 256), (uint32_t)n_kv, 256, (uint32_t)(grp * head_dim * 4), a))
+        return rc;
     snprintf(name, sizeof name, "cj_attn_combine_h%d", head_dim);
-    return launch(name, (uint32_t)n_q, 128, 0, a);
+    return launch(name, (uint32_t)n_q, 256, 0, a);
 }
 
 int32_t cj_decode_splits(int32_t count, int32_t n_kv, int32_t workers) {

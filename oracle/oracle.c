@@ -401,23 +401,24 @@ int or_matvec(int type, const uint8_t *w, int64_t rows, int64_t cols,
 
 /* ------------------------------------------------------------ primitives */
 
-/* RMSNorm. A row of whole 256s takes the CPU row form
- * (Prim.rmsnormPackRowCpuKernel, L/model/Prim.cajeta:977-1071): 256 lane
- * partials accumulated in column order, folded 128,64,...,1. Other widths
- * take the host floor (Prim.rmsnormRowHost, :120-151). form 1 = (1 + w). */
+/* RMSNorm in the order of the reference's device-decode norms: 256 lane
+ * partials, lane j summing x[j + 256k]^2 in k order (ragged past n), folded
+ * 128, 64, ..., 1. For whole 256s that is the CPU row form
+ * (Prim.rmsnormPackRowCpuKernel, L/model/Prim.cajeta:977-1071); other widths
+ * go to rmsnormRowF32 (:742-775) through Prim.rmsnormDevice (:1440-1450), the
+ * resident layer's fallback when the fused norm + pack declines a width
+ * (CausalLM.cajeta:3643, :3819; the final norm at :1635). The host floor's
+ * element-order sum (Prim.rmsnormRowHost, :120-151) belongs to the
+ * non-resident path and is not taken here. form 1 = (1 + w). */
 void or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out) {
     float ss = 0.0f;
-    if (n % 256 == 0) {
-        float p[256];
-        for (int j = 0; j < 256; j++) p[j] = 0.0f;
-        for (int64_t k = 0; k < n / 256; k++)
-            for (int j = 0; j < 256; j++) { float a = x[k * 256 + j]; p[j] = p[j] + a * a; }
-        for (int s = 128; s > 0; s >>= 1)
-            for (int j = 0; j < s; j++) p[j] = p[j] + p[j + s];
-        ss = p[0];
-    } else {
-        for (int64_t i = 0; i < n; i++) ss = ss + x[i] * x[i];
-    }
+    float p[256];
+    for (int j = 0; j < 256; j++) p[j] = 0.0f;
+    for (int64_t k = 0; k * 256 < n; k++)
+        for (int j = 0; j < 256 && k * 256 + j < n; j++) { float a = x[k * 256 + j]; p[j] = p[j] + a * a; }
+    for (int s = 128; s > 0; s >>= 1)
+        for (int j = 0; j < s; j++) p[j] = p[j] + p[j + s];
+    ss = p[0];
 #if OR_PLANT == 5
     float scale = 1.0f / sqrtf(ss / (float)n);     /* planted: eps dropped */
 #else

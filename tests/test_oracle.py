@@ -340,6 +340,36 @@ def test_rmsnorm_against_float64(O):
     assert ok, bad
 
 
+def test_rmsnorm_sums_in_the_device_decode_order(O):
+    """Widths that are not whole 256s (gpt-oss's 2880) take the reference's
+    rmsnormRowF32 order through Prim.rmsnormDevice (L/model/Prim.cajeta:
+    742-775, :1440-1450; the resident layer's fallback, CausalLM.cajeta:3643,
+    :3819): 256 lane partials over x[j + 256k] in k order, then the halving
+    tree. The input is chosen so that element order gives other bits, so the
+    test tells the two apart."""
+    for n in (2880, 4096, 300):
+        rng = np.random.default_rng(n + 9)
+        x = (rng.standard_normal(n) * np.exp(rng.standard_normal(n))).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        p = np.zeros(256, np.float32)
+        for k in range(0, n, 256):
+            seg = x[k:k + 256]
+            p[:seg.size] = p[:seg.size] + seg * seg
+        s = 128
+        while s:
+            p[:s] = p[:s] + p[s:2 * s]
+            s //= 2
+        lanes = p[0]
+        seq = np.float32(0)
+        for v in x:
+            seq = np.float32(seq + v * v)
+        assert lanes != seq, n          # the orders differ on this input
+        scale = np.float32(1) / np.sqrt(lanes / np.float32(n) + np.float32(1e-5))
+        want = x * scale * w
+        got = O.rmsnorm(x, w, 1e-5, 0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
+
+
 def test_rope_against_complex_rotation(O):
     ok, bad = check_rope(O)
     assert ok, bad
