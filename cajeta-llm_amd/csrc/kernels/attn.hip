@@ -398,10 +398,13 @@ DEV void scores_body(const cj_attn_args &a) {
     const int grp = a.n_q / a.n_kv, kvh = blockIdx.y;
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (blockIdx.x * 256 >= count) return;      // the whole workgroup idles past count
+    // the page entry is requested with q (the K row's address waits on it)
+    const int pos = from + min(t, count - 1);
+    const int page = a.pgtab[a.pg_base + (pos >> 6)];
     for (int i = threadIdx.x; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
     __syncthreads();
     if (t >= count) return;
-    const uint16_t *kr = a.kc + kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD);
+    const uint16_t *kr = a.kc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD;
     float k[HD];
 #pragma unroll
     for (int j = 0; j < HD / 8; j++) {
@@ -436,137 +439,113 @@ DEV void scores_body(const cj_attn_args &a) {
     }
 }
 
+#define COMBINE_PAGES 2048   // K/V pages a two-pass span covers (131072 positions)
+
+// A combine producer's item of tile I: positions I·T + 4·tq + k (k < 4),
+// dimensions 8·dg..+7 of V and the positions' weights e from `ev` (past
+// count: the last position, loaded but staged as +0).
+struct CombineItem {
+    u32x4 v[4];
+    float e[4];
+};
+
+// Pages are read from `pgs`, the sequence's page-table entries staged in LDS
+// (entry j for page from/64 + j), so no V load waits on a page-table load.
+template <int HD, int T>
+DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, int count, int from, int kvh,
+                              int dg, int tq, int I) {
+    CombineItem it;
+    const int t0 = I * T + 4 * tq;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int t = min(t0 + k, count - 1), pos = from + t;
+        const int page = pgs[(pos >> 6) - (from >> 6)];
+        it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * dg);
+        it.e[k] = ev[t];
+    }
+    return it;
+}
+
+// The item's 32 rounded products e_t·v_t[d] into the tile's rows d (row
+// stride S), four positions a 16-byte store.
+template <int T, int S>
+DEV void combine_store(float *pb, const CombineItem &it, int I, int count, int tq) {
+    const int t0 = I * T + 4 * tq;
+    const bool ok0 = t0 < count, ok1 = t0 + 1 < count, ok2 = t0 + 2 < count, ok3 = t0 + 3 < count;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int sh = 16 * (j & 1);
+        float4 o;
+        o.x = ok0 ? __fmul_rn(it.e[0], h2f(it.v[0][j >> 1] >> sh)) : 0.0f;
+        o.y = ok1 ? __fmul_rn(it.e[1], h2f(it.v[1][j >> 1] >> sh)) : 0.0f;
+        o.z = ok2 ? __fmul_rn(it.e[2], h2f(it.v[2][j >> 1] >> sh)) : 0.0f;
+        o.w = ok3 ? __fmul_rn(it.e[3], h2f(it.v[3][j >> 1] >> sh)) : 0.0f;
+        *(float4 *)(pb + j * S) = o;
+    }
+}
+
 // softmax over scores[h][0..count) in place and out[h] = Σ_t p_t·V_t / Σ p:
-// one workgroup of 256 per query head.
-//   max   all 256 lanes (max is exact, so any order gives the same value);
+// one workgroup of 256 per query head, spans of up to COMBINE_PAGES pages.
+//   max   lanes 0..127 (max is exact, so any grouping gives the same value);
 //   sum   lanes 0..127 as the reference's 128: lane l adds e_t for t = l,
-//         l+128, ... in order (e_t written over the score), then the
-//         stride-halving tree;
-//   p·V   each output dimension's ascending-t sum is one lane's chain in the
-//         first HD/64 waves (the adders). The other waves (producers) stage
-//         the rounded products e_t·v_t[d] through LDS one tile ahead, so an
-//         adder spends 1.25 instructions a position: a 16-byte LDS read of
-//         four positions' products, then four adds. Positions past count are
-//         staged as +0, which leaves the sum's bits unchanged (the sum starts
-//         at +0 and so is never -0); their loads read position count-1.
+//         l+128, ... in order (e_t kept in LDS, or past COMBINE_ES positions
+//         written over the score), then the stride-halving tree;
+//   p·V   each output dimension's ascending-t sum is one lane's chain. A
+//         span of up to 2048 16-byte V chunks (256 positions at HD 64, 128 at
+//         128) stages V whole in LDS and each chain lane forms its own
+//         products. Longer spans put the chains in the first HD/64 waves (the
+//         adders). The other waves (producers) stage
+//         the rounded products e_t·v_t[d] through LDS a tile ahead, their V
+//         rows loaded CD tiles ahead, so an adder spends 1.25 instructions a
+//         position: a 16-byte LDS read of four positions' products, then four
+//         adds. Positions past count are staged as +0, which leaves the sum's
+//         bits unchanged (the sum starts at +0 and so is never -0); their
+//         loads read position count-1.
+#define COMBINE_ES 6144   // positions whose weights stay in LDS (one 48-a-lane load round)
+
 template <int HD>
-DEV void combine_body(const cj_attn_args &a) {
-    constexpr int A = HD / 64;               // adder waves
-    constexpr int P = 256 - 64 * A;          // producer lanes
-    constexpr int DG = HD / 8;               // 8-dimension groups of a V row
-    constexpr int TQ = P / DG;               // 4-position groups a tile: one 4 × 8 item a producer lane
-    constexpr int T = 4 * TQ;                // positions a tile
-    constexpr int S = T + 4;                 // product row stride (floats): 16 lanes' 16-byte reads hit distinct banks
-    __shared__ float red[256];
-    __shared__ __align__(16) float prod[2][HD * S];
-    int count, from;
-    attn_window(a, count, from);
-    const int h = blockIdx.x, l = threadIdx.x;
-    const int grp = a.n_q / a.n_kv, kvh = h / grp;
-    float *sc = a.part + (int64_t)h * a.splits;
+struct CombineDims {
+    static constexpr int A = HD / 64;               // adder waves
+    static constexpr int P = 256 - 64 * A;          // producer lanes
+    static constexpr int DG = HD / 8;               // 8-dimension groups of a V row
+    static constexpr int TQ = P / DG;               // 4-position groups a tile: one 4 × 8 item a producer lane
+    static constexpr int T = 4 * TQ;                // positions a tile
+    static constexpr int S = T + 4;                 // product row stride (floats): 16 lanes' 16-byte reads, distinct banks
+};
 
-    float mx = -3.0e38f;
-    {
-        int t = l;
-        for (; t + 768 < count; t += 1024) {
-            const float x0 = sc[t], x1 = sc[t + 256], x2 = sc[t + 512], x3 = sc[t + 768];
-            if (x0 > mx) mx = x0;
-            if (x1 > mx) mx = x1;
-            if (x2 > mx) mx = x2;
-            if (x3 > mx) mx = x3;
-        }
-        for (; t < count; t += 256) if (sc[t] > mx) mx = sc[t];
-    }
-    red[l] = mx;
-    __syncthreads();
-    for (int r = 128; r > 0; r >>= 1) {
-        if (l < r && red[l + r] > red[l]) red[l] = red[l + r];
-        __syncthreads();
-    }
-    const float m = red[0];
-    __syncthreads();
-    float s = 0.0f;
-    if (l < 128) {
-        int t = l;
-        for (; t + 384 < count; t += 512) {
-            const float x0 = sc[t], x1 = sc[t + 128], x2 = sc[t + 256], x3 = sc[t + 384];
-            const float e0 = cj_expf(x0 - m), e1 = cj_expf(x1 - m), e2 = cj_expf(x2 - m), e3 = cj_expf(x3 - m);
-            sc[t] = e0; sc[t + 128] = e1; sc[t + 256] = e2; sc[t + 384] = e3;
-            s = __fadd_rn(s, e0);
-            s = __fadd_rn(s, e1);
-            s = __fadd_rn(s, e2);
-            s = __fadd_rn(s, e3);
-        }
-        for (; t < count; t += 128) {
-            const float e = cj_expf(sc[t] - m);
-            sc[t] = e;
-            s = __fadd_rn(s, e);
-        }
-    }
-    red[l] = s;
-    __syncthreads();
-    for (int r = 64; r > 0; r >>= 1) {
-        if (l < r) red[l] = __fadd_rn(red[l], red[l + r]);
-        __syncthreads();
-    }
-    const float rs = __fdiv_rn(1.0f, red[0]);
-
-    const int w = l >> 6, ntiles = (count + T - 1) / T;
-    const int pl = l - 64 * A, tq = pl % TQ, dg = pl / TQ;
-    u32x4 va0, va1, va2, va3, vb0, vb1, vb2, vb3;
-    float ea[4], eb[4];
-    // a producer's item of tile i: positions i·T + 4·tq + k (k < 4), dimensions 8·dg..+7
-#define COMBINE_FETCH(I, V0, V1, V2, V3, E)                                                                    \
-    {                                                                                                           \
-        const int t0 = (I) * T + 4 * tq;                                                                        \
-        u32x4 *vv[4] = {&V0, &V1, &V2, &V3};                                                                    \
-        _Pragma("unroll") for (int k = 0; k < 4; k++) {                                                         \
-            const int t = min(t0 + k, count - 1);     /* past count: loaded, then staged as +0 */               \
-            *vv[k] = *(const u32x4 *)(a.vc + kv_at(a.pgtab, a.pg_base, from + t, a.n_kv, kvh, HD) + 8 * dg);   \
-            E[k] = sc[t];                                                                                       \
-        }                                                                                                       \
-    }
-#define COMBINE_STORE(B, I, V0, V1, V2, V3, E)                                                                 \
-    {                                                                                                           \
-        float *pb = prod[B] + 8 * dg * S + 4 * tq;                                                              \
-        const int t0 = (I) * T + 4 * tq;                                                                        \
-        const bool ok0 = t0 < count, ok1 = t0 + 1 < count, ok2 = t0 + 2 < count, ok3 = t0 + 3 < count;         \
-        _Pragma("unroll") for (int j = 0; j < 8; j++) {                                                         \
-            const int sh = 16 * (j & 1);                                                                        \
-            float4 o;                                                                                           \
-            o.x = ok0 ? __fmul_rn(E[0], h2f(V0[j >> 1] >> sh)) : 0.0f;                                          \
-            o.y = ok1 ? __fmul_rn(E[1], h2f(V1[j >> 1] >> sh)) : 0.0f;                                          \
-            o.z = ok2 ? __fmul_rn(E[2], h2f(V2[j >> 1] >> sh)) : 0.0f;                                          \
-            o.w = ok3 ? __fmul_rn(E[3], h2f(V3[j >> 1] >> sh)) : 0.0f;                                          \
-            *(float4 *)(pb + j * S) = o;                                                                        \
-        }                                                                                                       \
-    }
-    if (w >= A) {
-        COMBINE_FETCH(0, va0, va1, va2, va3, ea);
-        COMBINE_FETCH(1, vb0, vb1, vb2, vb3, eb);
-        COMBINE_STORE(0, 0, va0, va1, va2, va3, ea);
-        va0 = vb0; va1 = vb1; va2 = vb2; va3 = vb3;
-#pragma unroll
-        for (int k = 0; k < 4; k++) ea[k] = eb[k];
-        COMBINE_FETCH(2, vb0, vb1, vb2, vb3, eb);
-    }
-    __syncthreads();
-    // the roles run separate loops with the same barriers, so no branch sits
-    // between a producer's loads and their use
+// p·V of the combine: returns the adder lane's sum (0 on producers). `ev` is
+// the weights e_t: in LDS or, past COMBINE_ES positions, over the scores. CD
+// (even) tiles of V are in flight per producer; both roles run a whole
+// number of CD-tile rounds.
+template <int HD, int CD>
+DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float *prod, int count, int from, int kvh) {
+    using D = CombineDims<HD>;
+    constexpr int T = D::T, S = D::S;
+    const int l = threadIdx.x, w = l >> 6, ntiles = (count + T - 1) / T;
+    const int pl = l - 64 * D::A, tq = pl % D::TQ, dg = pl / D::TQ;
+    // both loops run a whole number of CD-tile rounds, so the producer's
+    // body has no branch (tiles past the end go to the idle buffer, unread)
+    const int nit = (ntiles + CD - 1) / CD * CD;
     float acc = 0.0f;
-    if (w < A) {
-        const float *pr = prod[0] + (64 * w + (l & 63)) * S;
-        for (int i = 0; i < ntiles; i++) {
+    if (w < D::A) {
+        __syncthreads();
+        const float *pr = prod + (64 * w + (l & 63)) * S;
+        for (int i = 0; i < nit; i++) {
             const float *pt = pr + (i & 1) * (HD * S);
-            const int n = min(T, count - i * T);
+            const int n = i < ntiles ? min(T, count - i * T) : 0;
             if (n == T) {
+                // every read issued before the first add (the scheduler would
+                // otherwise keep two in flight and wait out each one's latency)
+                float4 p[T / 4];
 #pragma unroll
-                for (int q = 0; q < T; q += 4) {
-                    const float4 p = *(const float4 *)(pt + q);
-                    acc = __fadd_rn(acc, p.x);
-                    acc = __fadd_rn(acc, p.y);
-                    acc = __fadd_rn(acc, p.z);
-                    acc = __fadd_rn(acc, p.w);
+                for (int q = 0; q < T / 4; q++) p[q] = *(const float4 *)(pt + 4 * q);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < T / 4; q++) {
+                    acc = __fadd_rn(acc, p[q].x);
+                    acc = __fadd_rn(acc, p[q].y);
+                    acc = __fadd_rn(acc, p[q].z);
+                    acc = __fadd_rn(acc, p[q].w);
                 }
             } else {
                 for (int q = 0; q < n; q += 4) {
@@ -580,20 +559,161 @@ DEV void combine_body(const cj_attn_args &a) {
             __syncthreads();
         }
     } else {
-        // no branch in the body: the last round forms a tile past the end
-        // into the idle buffer, never read
-        for (int i = 0; i < ntiles; i++) {
-            COMBINE_STORE((i + 1) & 1, i + 1, va0, va1, va2, va3, ea);
-            va0 = vb0; va1 = vb1; va2 = vb2; va3 = vb3;
+        // CD tiles of V rows and weights in flight, ring slot = tile mod CD
+        CombineItem ring[CD];
 #pragma unroll
-            for (int k = 0; k < 4; k++) ea[k] = eb[k];
-            COMBINE_FETCH(i + 3, vb0, vb1, vb2, vb3, eb);
-            __syncthreads();
+        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, j);
+        float *pb = prod + 8 * dg * S + 4 * tq;
+        combine_store<T, S>(pb, ring[0], 0, count, tq);
+        ring[0] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, CD);
+        __syncthreads();
+        for (int i0 = 0; i0 < nit; i0 += CD) {
+#pragma unroll
+            for (int j = 0; j < CD; j++) {
+                const int i = i0 + j, r = (j + 1) % CD;
+                combine_store<T, S>(pb + ((j + 1) & 1) * (HD * S), ring[r], i + 1, count, tq);
+                ring[r] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, i + 1 + CD);
+                __syncthreads();
+            }
         }
     }
-#undef COMBINE_FETCH
-#undef COMBINE_STORE
-    if (w < A) a.out[(int64_t)h * HD + 64 * w + (l & 63)] = __fmul_rn(acc, rs);
+    return acc;
+}
+
+template <int HD>
+DEV void combine_body(const cj_attn_args &a) {
+    using D = CombineDims<HD>;
+    __shared__ float red[4 + 128];
+    __shared__ __align__(16) float prod[2 * HD * D::S];
+    __shared__ int pgs[COMBINE_PAGES];
+    __shared__ __align__(16) float es[COMBINE_ES];
+    int count, from;
+    attn_window(a, count, from);
+    const int h = blockIdx.x, l = threadIdx.x;
+    const int grp = a.n_q / a.n_kv, kvh = h / grp;
+    float *sc = a.part + (int64_t)h * a.splits;
+    const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
+    // the page entries and the first round of scores are requested together
+    // (one memory round trip); lane l < 128 takes positions l + 128k
+    constexpr int PK = COMBINE_ES / 128;
+    const int pg0 = l < npg ? a.pgtab[a.pg_base + (from >> 6) + l] : 0;
+    float v[PK];
+    if (l < 128) {
+#pragma unroll
+        for (int k = 0; k < PK; k++) v[k] = sc[min(l + 128 * k, count - 1)];
+    }
+    if (l < npg) pgs[l] = pg0;
+    for (int j = l + 256; j < npg; j += 256) pgs[j] = a.pgtab[a.pg_base + (from >> 6) + j];
+    float mx = -3.0e38f;
+    if (l < 128) {
+#pragma unroll
+        for (int k = 0; k < PK; k++) if (l + 128 * k < count && v[k] > mx) mx = v[k];
+        for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
+            float u[PK];
+#pragma unroll
+            for (int k = 0; k < PK; k++) u[k] = sc[min(base + l + 128 * k, count - 1)];
+#pragma unroll
+            for (int k = 0; k < PK; k++) if (base + l + 128 * k < count && u[k] > mx) mx = u[k];
+        }
+    }
+    // max is exact, so a wave reduction and then the two waves' maxima
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float y = __shfl_xor(mx, o);
+        if (y > mx) mx = y;
+    }
+    if ((l & 63) == 0) red[l >> 6] = mx;
+    __syncthreads();
+    const float m = red[1] > red[0] ? red[1] : red[0];
+    // short spans take V whole into LDS: the rows are requested here (their
+    // page entries are visible after the barrier above) while the weights
+    // form, and each adder lane then runs its chain from LDS
+    constexpr int DCH = 8;                                  // 16-byte chunks a thread
+    const bool direct = count * (HD / 8) <= 256 * DCH;
+    u32x4 vst[DCH];
+    if (direct) {
+#pragma unroll
+        for (int k = 0; k < DCH; k++) {
+            const int c = l + 256 * k, j = c % (HD / 8), pos = from + min(c / (HD / 8), count - 1);
+            const int page = pgs[(pos >> 6) - (from >> 6)];
+            vst[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j);
+        }
+    }
+    // e_t in order per lane; kept in LDS when the span fits, else written
+    // over the scores
+    const bool elds = count <= COMBINE_ES;
+    float s = 0.0f;
+    if (l < 128) {
+#pragma unroll
+        for (int k = 0; k < PK; k++) {
+            const int t = l + 128 * k;
+            if (t < count) {
+                const float e = cj_expf(v[k] - m);
+                if (elds) es[t] = e;
+                else sc[t] = e;
+                s = __fadd_rn(s, e);
+            }
+        }
+        for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
+            float u[PK];
+#pragma unroll
+            for (int k = 0; k < PK; k++) u[k] = sc[min(base + l + 128 * k, count - 1)];
+#pragma unroll
+            for (int k = 0; k < PK; k++) {
+                const int t = base + l + 128 * k;
+                if (t < count) {
+                    const float e = cj_expf(u[k] - m);
+                    sc[t] = e;
+                    s = __fadd_rn(s, e);
+                }
+            }
+        }
+    }
+    // the reference's 128-lane stride-halving tree: the 64 stride crosses
+    // waves through LDS, the strides 32..1 are wave 0's shuffles
+    __syncthreads();                 // red[0..1] read by every lane above
+    if (l < 128) red[4 + l] = s;
+    __syncthreads();
+    if (l < 64) {
+        float v2 = __fadd_rn(red[4 + l], red[4 + l + 64]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        if (l == 0) red[2] = v2;
+    }
+    __syncthreads();
+    const float rs = __fdiv_rn(1.0f, red[2]);
+    if (direct) {
+        uint16_t *vs = (uint16_t *)prod;                    // [t][HD] halves
+#pragma unroll
+        for (int k = 0; k < DCH; k++) {
+            const int c = l + 256 * k;
+            if (c < count * (HD / 8)) *(u32x4 *)(vs + 8 * c) = vst[k];
+        }
+        __syncthreads();
+        if (l < HD) {
+            float acc = 0.0f;
+            int t = 0;
+            for (; t + 4 <= count; t += 4) {
+                const float4 e4 = *(const float4 *)(es + t);
+                const float v0 = h2f(vs[t * HD + l]), v1 = h2f(vs[(t + 1) * HD + l]);
+                const float v2 = h2f(vs[(t + 2) * HD + l]), v3 = h2f(vs[(t + 3) * HD + l]);
+                acc = __fadd_rn(acc, __fmul_rn(e4.x, v0));
+                acc = __fadd_rn(acc, __fmul_rn(e4.y, v1));
+                acc = __fadd_rn(acc, __fmul_rn(e4.z, v2));
+                acc = __fadd_rn(acc, __fmul_rn(e4.w, v3));
+            }
+            for (; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(es[t], h2f(vs[t * HD + l])));
+            a.out[(int64_t)h * HD + l] = __fmul_rn(acc, rs);
+        }
+        return;
+    }
+    // short spans (the sliding windows, early positions) take a two-tile
+    // ring, so few rounds are padded
+    const int ntiles = (count + D::T - 1) / D::T;
+    const float acc = !elds ? combine_pv<HD, 6>(a, pgs, sc, prod, count, from, kvh)
+                      : ntiles <= 4 ? combine_pv<HD, 2>(a, pgs, es, prod, count, from, kvh)
+                                    : combine_pv<HD, 6>(a, pgs, es, prod, count, from, kvh);
+    if (l < 64 * D::A) a.out[(int64_t)h * HD + l] = __fmul_rn(acc, rs);
 }
 
 extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a); }

@@ -222,13 +222,18 @@ DEV float wave_shr1(float v, float first) {
 // of LDS.
 DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     const int t = threadIdx.x;
-    // the row's values loaded at once (up to 64 a thread), then summed in order
+    // the row's values loaded at once (up to 64 a thread), then summed in
+    // order: kn whole rounds (a uniform bound), then the ragged one
     float xv[64];
+    const int kn = (int)min(n >> 8, (int64_t)64);
 #pragma unroll
-    for (int k = 0; k < 64; k++) xv[k] = t + 256 * k < n ? x[t + 256 * k] : 0.0f;
+    for (int k = 0; k < 64; k++) xv[k] = k < kn ? x[t + 256 * k] : 0.0f;
+    const int64_t er = t + 256 * (int64_t)kn;
+    const float xr = kn < 64 && er < n ? x[er] : 0.0f;
     float p = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 64; k++) if (t + 256 * k < n) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
+    for (int k = 0; k < 64; k++) if (k < kn) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
+    if (kn < 64 && er < n) p = __fadd_rn(p, __fmul_rn(xr, xr));
     for (int64_t e = t + 256 * 64; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
     __syncthreads();
@@ -318,7 +323,39 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
 
 // The staged values as f32 into LDS (formats that read f32 activations).
 DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form, float *xf) {
-    for (int64_t e = threadIdx.x; e < (int64_t)nblk * 256; e += 256) xf[e] = stage_value(x, n, e, norm, scale, w, form);
+    // 16 values a thread a round, all loads issued before the first use
+    const int64_t total = (int64_t)nblk * 256;
+    for (int64_t e0 = 16 * threadIdx.x; e0 < total; e0 += 4096) {
+        float v[16];
+        if (e0 + 16 <= n) {
+            float4 xv[4], wv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) xv[k] = *(const float4 *)(x + e0 + 4 * k);
+            if (norm) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) wv[k] = *(const float4 *)(w + e0 + 4 * k);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float xs[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (norm) {
+                        const float wc = c == 0 ? wv[k].x : c == 1 ? wv[k].y : c == 2 ? wv[k].z : wv[k].w;
+                        const float wi = form == 1 ? __fadd_rn(1.0f, wc) : wc;
+                        v[4 * k + c] = __fmul_rn(__fmul_rn(xs[c], scale), wi);
+                    } else {
+                        v[4 * k + c] = xs[c];
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = stage_value(x, n, e0 + k, norm, scale, w, form);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) *(float4 *)(xf + e0 + 4 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+    }
     __syncthreads();
 }
 
@@ -326,8 +363,18 @@ DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, 
 // block b at sx + b·bstride.
 DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx, int bstride = 320) {
     const int t = threadIdx.x;
-    int n16 = nblk * 20;
-    for (int i = t; i < n16; i += 256) *(uint4 *)(sx + (i / 20) * bstride + (i % 20) * 16) = ((const uint4 *)xp)[i];
+    const int n16 = nblk * 20;
+    // four 16-byte words a thread a round, loaded before any is stored
+    for (int i0 = t; i0 < n16; i0 += 1024) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ((const u32x4 *)xp)[min(i0 + 256 * k, n16 - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = i0 + 256 * k;
+            if (i < n16) *(u32x4 *)(sx + (i / 20) * bstride + (i % 20) * 16) = v[k];
+        }
+    }
     __syncthreads();
 }
 

@@ -525,13 +525,19 @@ DEV SeqItem<FMT> seq_fetch(const uint8_t *wr, int nb32, int blk) {
     return it;
 }
 
+// The block's 32 x values from LDS into registers.
+DEV void seq_xload(const float *xs, int blk, float4 (&x)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) x[j] = *(const float4 *)(xs + 32 * blk + 4 * j);
+}
+
 // The block's 32 rounded products in add order into dst (and Q4_0's d).
 template <int FMT>
-DEV void seq_products(const SeqItem<FMT> &it, const float *xb, float *dst, float *dv) {
+DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst, float *dv) {
     if constexpr (FMT == CJ_F32) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float4 x = *(const float4 *)(xb + 4 * j);
+            const float4 x = xr[j];
             float4 o;
             o.x = __fmul_rn(__uint_as_float(it.q[j].x), x.x);
             o.y = __fmul_rn(__uint_as_float(it.q[j].y), x.y);
@@ -551,7 +557,7 @@ DEV void seq_products(const SeqItem<FMT> &it, const float *xb, float *dst, float
         for (int g = 0; g < 8; g++) {
             const uint32_t nibs = g < 4 ? (ws[g & 3] & 0x0f0f0f0fu) : ((ws[g & 3] >> 4) & 0x0f0f0f0fu);
             const uint32_t mag = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, nibs & 0x07070707u);
-            const float4 x = *(const float4 *)(xb + 4 * g);
+            const float4 x = xr[g];
             const float xv[4] = {x.x, x.y, x.z, x.w};
             float ov[4];
 #pragma unroll
@@ -569,7 +575,7 @@ DEV void seq_products(const SeqItem<FMT> &it, const float *xb, float *dst, float
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const uint32_t word = ws[g >> 1], sh = 16 * (g & 1);
-            const float4 xl = *(const float4 *)(xb + 4 * (g >> 1)), xh = *(const float4 *)(xb + 16 + 4 * (g >> 1));
+            const float4 xl = xr[g >> 1], xh = xr[4 + (g >> 1)];
             const uint32_t b0 = (word >> sh) & 255u, b1 = (word >> (sh + 8)) & 255u;
             float4 o;
             o.x = __fmul_rn((float)(int)(b0 & 15u) - 8.0f, g & 1 ? xl.z : xl.x);
@@ -584,10 +590,15 @@ DEV void seq_products(const SeqItem<FMT> &it, const float *xb, float *dst, float
 // Row threadIdx.x (< 64) of the workgroup's rows summed; x staged in LDS.
 // Every thread of the workgroup must call it (it holds barriers). A producer
 // lane keeps D tiles of its weights in flight (a ring indexed at compile
-// time: the tile loop is unrolled by D).
+// time: the tile loop is unrolled by D) and reads its next block of x from
+// LDS a tile ahead, so its products wait on neither; the adder reads a whole
+// tile of products before its first add.
+#ifndef SEQ_D
+#define SEQ_D 8
+#endif
 template <int FMT>
 DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
-    constexpr int D = FMT == CJ_F32 ? 4 : 8;
+    constexpr int D = SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
     __shared__ __align__(16) float prod[2][64 * SEQ_S];
     __shared__ float dvs[2][64 * SEQ_TB];
@@ -597,62 +608,91 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
     const uint8_t *wr = sl.W + min(sl.row0 + lane, a.rows - 1) * a.row_bytes;
     float *pdst = prod[0] + lane * SEQ_S + 32 * pb, *pdv = dvs[0] + lane * SEQ_TB + pb;
     constexpr int PBUF = 64 * SEQ_S, DBUF = 64 * SEQ_TB;
-    SeqItem<FMT> ring[D];
-    if (w > 0) {
-#pragma unroll
-        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * SEQ_TB + pb);
-        seq_products<FMT>(ring[0], xs + 32 * min(pb, nb32 - 1), pdst, pdv);
-        ring[0] = seq_fetch<FMT>(wr, nb32, D * SEQ_TB + pb);
-    }
-    __syncthreads();
-    // the roles run separate loops (the same barriers in the same number), so
-    // no branch sits between a producer's loads and their use and the loads
-    // of the ring stay in flight across tiles
-    float acc = 0.0f;
     // both loops run a whole number of D-tile rounds: the producer's body
     // is then free of branches (tiles past the end are formed into the idle
     // buffer and never read)
     const int nit = (ntiles + D - 1) / D * D;
+    float acc = 0.0f;
     if (w == 0) {
+        __syncthreads();
         const float *pr0 = prod[0] + lane * SEQ_S;
         const float *dv0 = dvs[0] + lane * SEQ_TB;
         for (int i = 0; i < nit; i++) {
             const float *pr = pr0 + (i & 1) * PBUF;
             const int nb = i < ntiles ? min(SEQ_TB, nb32 - i * SEQ_TB) : 0;
-            for (int b = 0; b < nb; b++) {
-                if constexpr (FMT == CJ_Q4_0) {
-                    float dot = 0.0f;
+            if (nb == SEQ_TB) {
+                float4 p[8 * SEQ_TB];
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                        dot = __fadd_rn(dot, p.x);
-                        dot = __fadd_rn(dot, p.y);
-                        dot = __fadd_rn(dot, p.z);
-                        dot = __fadd_rn(dot, p.w);
+                for (int q = 0; q < 8 * SEQ_TB; q++) p[q] = *(const float4 *)(pr + 4 * q);
+#pragma unroll
+                for (int b = 0; b < SEQ_TB; b++) {
+                    if constexpr (FMT == CJ_Q4_0) {
+                        float dot = 0.0f;
+#pragma unroll
+                        for (int q = 8 * b; q < 8 * b + 8; q++) {
+                            dot = __fadd_rn(dot, p[q].x);
+                            dot = __fadd_rn(dot, p[q].y);
+                            dot = __fadd_rn(dot, p[q].z);
+                            dot = __fadd_rn(dot, p[q].w);
+                        }
+                        acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
+                    } else {
+#pragma unroll
+                        for (int q = 8 * b; q < 8 * b + 8; q++) {
+                            acc = __fadd_rn(acc, p[q].x);
+                            acc = __fadd_rn(acc, p[q].y);
+                            acc = __fadd_rn(acc, p[q].z);
+                            acc = __fadd_rn(acc, p[q].w);
+                        }
                     }
-                    acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
-                } else {
+                }
+            } else {
+                for (int b = 0; b < nb; b++) {
+                    if constexpr (FMT == CJ_Q4_0) {
+                        float dot = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                        acc = __fadd_rn(acc, p.x);
-                        acc = __fadd_rn(acc, p.y);
-                        acc = __fadd_rn(acc, p.z);
-                        acc = __fadd_rn(acc, p.w);
+                        for (int q = 0; q < 8; q++) {
+                            const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                            dot = __fadd_rn(dot, p.x);
+                            dot = __fadd_rn(dot, p.y);
+                            dot = __fadd_rn(dot, p.z);
+                            dot = __fadd_rn(dot, p.w);
+                        }
+                        acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) {
+                            const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                            acc = __fadd_rn(acc, p.x);
+                            acc = __fadd_rn(acc, p.y);
+                            acc = __fadd_rn(acc, p.z);
+                            acc = __fadd_rn(acc, p.w);
+                        }
                     }
                 }
             }
             __syncthreads();
         }
     } else {
+        SeqItem<FMT> ring[D];
+        float4 xr[2][8];
+#pragma unroll
+        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * SEQ_TB + pb);
+        seq_xload(xs, min(pb, nb32 - 1), xr[0]);
+        seq_xload(xs, min(SEQ_TB + pb, nb32 - 1), xr[1]);
+        seq_products<FMT>(ring[0], xr[0], pdst, pdv);
+        ring[0] = seq_fetch<FMT>(wr, nb32, D * SEQ_TB + pb);
+        __syncthreads();
+        // round j of an iteration forms tile i + 1 from ring[(j + 1) % D] and
+        // x registers xr[(j + 1) & 1], then loads x of tile i + 2 into xr[j & 1]
         for (int i0 = 0; i0 < nit; i0 += D) {
 #pragma unroll
             for (int j = 0; j < D; j++) {
                 const int i = i0 + j;
                 const int r = (j + 1) % D;
-                const int blk = min((i + 1) * SEQ_TB + pb, nb32 - 1);
                 const int nbuf = (j + 1) & 1;      // D is even, so (i + 1) & 1
-                seq_products<FMT>(ring[r], xs + 32 * blk, pdst + nbuf * PBUF, pdv + nbuf * DBUF);
+                seq_xload(xs, min((i + 2) * SEQ_TB + pb, nb32 - 1), xr[j & 1]);
+                seq_products<FMT>(ring[r], xr[nbuf], pdst + nbuf * PBUF, pdv + nbuf * DBUF);
                 ring[r] = seq_fetch<FMT>(wr, nb32, (i + 1 + D) * SEQ_TB + pb);
                 __syncthreads();
             }

@@ -300,6 +300,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     layers.resize(n_layers);
     const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim;
     pages_per_seq = (ctx + 63) / 64;
+    if (!(head_dim == 128 && (grp == 4 || grp == 8)) && pages_per_seq > 2048)
+        return fail(CJ_ERR_ARG, "model: context %d exceeds the two-pass attention's 2048 pages", ctx);
     const int64_t plane = (int64_t)pages_per_seq * max_seqs * n_kv * 64 * head_dim * 2;
     int rc;
     for (int l = 0; l < n_layers; l++) {

@@ -623,6 +623,8 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     const int grp = n_q / n_kv;
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
     const int64_t pages = ((int64_t)from + count + 63) / 64;
+    if (!split && (from + count - 1) / 64 - from / 64 + 1 > 2048)
+        return fail(CJ_ERR_ARG, "cj_attend: %d positions from %d span more than 2048 pages", count, from);
     const int64_t part_bytes = split ? (int64_t)n_q * 64 * (head_dim + 2) * 4 : (int64_t)n_q * count * 4;
     if (!in_buffer(dptr(pgtab + 4 * pg_base), pages * 4) || !in_buffer(dptr(q), (int64_t)n_q * head_dim * 4) ||
         !in_buffer(dptr(part), part_bytes) || (!split && !out) ||

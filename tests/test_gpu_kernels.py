@@ -220,7 +220,7 @@ def to_paged(plane, n_kv, hd, pages):
 
 @pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (128, 4, 1), (128, 8, 1), (64, 8, 2), (64, 64, 8), (128, 8, 8)])
 @pytest.mark.parametrize("count,frm,workers", [(1, 0, 512), (37, 0, 16), (300, 5, 16), (2049, 0, 512), (130, 70, 3),
-                                               (4133, 3, 512)])
+                                               (4133, 3, 512), (6300, 70, 512)])
 def test_attend_matches_oracle(gpu, O, hd, n_q, n_kv, count, frm, workers):
     say("attend", hd, n_q, n_kv, count, frm, workers)
     rng = np.random.default_rng(count * 7 + hd + n_q)
