@@ -721,6 +721,118 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_ar
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a); }
 
+// The two-pass form in one launch for spans of at most FUSED_SPAN(HD)
+// positions (sliding windows, small contexts): a workgroup per kv head
+// stages q, K and V of the span in LDS, then forms each query head's scores,
+// softmax and p·V with exactly the two kernels' operations — a score per
+// lane (the butterfly's fixed tree of 32 strided partials, then ·scale), the
+// max, the 128-lane ordered sums and their stride-halving tree, and each
+// output dimension's ascending-t sum — so its results are theirs bit for bit.
+#define FUSED_SPAN(HD) ((HD) == 64 ? 256 : 128)
+template <int HD>
+DEV void fused_body(const cj_attn_args &a) {
+    constexpr int SPAN = FUSED_SPAN(HD);
+    __shared__ __align__(16) uint16_t ks[SPAN * HD], vs[SPAN * HD];
+    __shared__ __align__(16) float qs[8 * HD];
+    __shared__ float sc[8][SPAN];
+    __shared__ float red[2][128], mred[8];
+    __shared__ float rsv[8];
+    int count, from;
+    attn_window(a, count, from);
+    const int kvh = blockIdx.x, l = threadIdx.x, grp = a.n_q / a.n_kv;
+    // q of the group, then K and V rows of the span (chunk c of row t: the
+    // page entry of the row, then its 16 bytes), all loads issued together
+    for (int i = l; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
+    constexpr int CH = HD / 8, NC = SPAN * CH / 256;
+    u32x4 kr[NC], vr[NC];
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = l + 256 * k, t = min(c / CH, count - 1), pos = from + t;
+        const int page = a.pgtab[a.pg_base + (pos >> 6)];
+        const int64_t off = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * (c % CH);
+        kr[k] = *(const u32x4 *)(a.kc + off);
+        vr[k] = *(const u32x4 *)(a.vc + off);
+    }
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = l + 256 * k;
+        *(u32x4 *)(ks + 8 * c) = kr[k];
+        *(u32x4 *)(vs + 8 * c) = vr[k];
+    }
+    __syncthreads();
+    // scores: lane t, every head of the group
+    if (l < count) {
+        float k[HD];
+#pragma unroll
+        for (int d = 0; d < HD; d++) k[d] = h2f(ks[l * HD + d]);
+        for (int g = 0; g < grp; g++) {
+            const float *q = qs + g * HD;
+            float p[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) p[i] = 0.0f;
+#pragma unroll
+            for (int d0 = 0; d0 < HD; d0 += 32) {
+#pragma unroll
+                for (int i = 0; i < 32; i++) p[i] = __fadd_rn(p[i], __fmul_rn(q[d0 + i], k[d0 + i]));
+            }
+#pragma unroll
+            for (int m = 16; m > 0; m >>= 1) {
+#pragma unroll
+                for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
+            }
+            sc[g][l] = __fmul_rn(p[0], a.scale);
+        }
+    }
+    __syncthreads();
+    // softmax, two heads at a time (128 lanes each: lane j takes t = j, j + 128)
+    for (int g0 = 0; g0 < grp; g0 += 2) {
+        const int g = g0 + (l >> 7), j = l & 127;
+        const bool on = g < grp;
+        float mx = -3.0e38f;
+        if (on) {
+            for (int t = j; t < count; t += 128) if (sc[g][t] > mx) mx = sc[g][t];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float y = __shfl_xor(mx, o);
+            if (y > mx) mx = y;
+        }
+        if ((l & 63) == 0) mred[l >> 6] = mx;
+        __syncthreads();
+        const float m = mred[2 * (l >> 7)] > mred[2 * (l >> 7) + 1] ? mred[2 * (l >> 7)] : mred[2 * (l >> 7) + 1];
+        float s = 0.0f;
+        if (on) {
+            for (int t = j; t < count; t += 128) {
+                const float e = cj_expf(sc[g][t] - m);
+                sc[g][t] = e;
+                s = __fadd_rn(s, e);
+            }
+        }
+        red[l >> 7][j] = s;
+        __syncthreads();
+        if ((l & 127) < 64) {
+            float v2 = __fadd_rn(red[l >> 7][j], red[l >> 7][j + 64]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+            if (j == 0 && on) rsv[g] = __fdiv_rn(1.0f, v2);
+        }
+        __syncthreads();
+    }
+    // p·V: chain (g, d) on thread (g·HD + d) mod 256, heads in turn
+    for (int c0 = 0; c0 < grp * HD; c0 += 256) {
+        const int c = c0 + l;
+        if (c < grp * HD) {
+            const int g = c / HD, d = c % HD;
+            float acc = 0.0f;
+            for (int t = 0; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(sc[g][t], h2f(vs[t * HD + d])));
+            a.out[((int64_t)kvh * grp + g) * HD + d] = __fmul_rn(acc, rsv[g]);
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) { fused_body<64>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) { fused_body<128>(a); }
+
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
 // 256 per 256 output values (the reference's attnReducePackQ8Kernel
 // contract), the merge in reducePackBlockCpu's order: the global max, then

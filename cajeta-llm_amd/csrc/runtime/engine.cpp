@@ -451,10 +451,11 @@ int Engine::enqueue_step(int s) {
     // the reference's choice of form: split-K for hd 128 with 4 or 8 query
     // heads a kv head, else the two-pass score/combine
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
-    char attn_kernel[64], combine_kernel[64];
+    char attn_kernel[64], combine_kernel[64], fused_kernel[64];
     if (split) snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_split_h128_g%d", grp);
     else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
     snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
+    snprintf(fused_kernel, sizeof fused_kernel, "cj_attn_fused_h%d", head_dim);
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
         // Q4_K projections fold the RMSNorm + pack into their prologue (the
@@ -490,13 +491,18 @@ int Engine::enqueue_step(int s) {
                 if ((rc = launch("cj_attn_merge", (uint32_t)(((int64_t)n_heads * head_dim + 255) / 256), 256, 0, m)))
                     return rc;
             } else if (want(K_ATTN, l)) {
-                // the grid covers the longest window; the kernel idles past count
                 a.splits = ctx;
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
-                if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_kv, 256,
-                                  (uint32_t)(grp * head_dim * 4), a)))
-                    return rc;
-                if ((rc = launch(combine_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
+                if (span <= (head_dim == 64 ? 256 : 128)) {
+                    // every step's span fits one workgroup: the one-launch form
+                    if ((rc = launch(fused_kernel, (uint32_t)n_kv, 256, 0, a))) return rc;
+                } else {
+                    // the grid covers the longest window; the kernel idles past count
+                    if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_kv, 256,
+                                      (uint32_t)(grp * head_dim * 4), a)))
+                        return rc;
+                    if ((rc = launch(combine_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
+                }
             }
         }
         if (want(K_O, l)) {   // 3. o projection, residual into hs
