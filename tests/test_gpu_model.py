@@ -223,6 +223,36 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+def test_c3_full_depth_greedy_parity(gpu):
+    """BASELINE config 3 at its full depth (32 layers, the benchmarked model):
+    a 40-token prompt through the prefill chunk, then 6 greedy steps; every
+    step's logits bit for bit against the oracle."""
+    say("model c3 full")
+    path, img = synth(gpu, "c3", "t_c3full", 1)
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, 128256, 40).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 7, 64)
+    gpu.image_free("t_c3full")
+    assert g == o
+    assert err <= LOGIT_TOL, err
+    assert run_pair.bit_identical
+
+
+def test_c5_full_depth_greedy_parity(gpu):
+    """BASELINE config 5 at its full depth (24 layers, 32 MXFP4 experts top-4,
+    the 201,088 vocabulary): a 130-token prompt (past the 128 window) and 4
+    greedy steps, logits bit for bit against the oracle."""
+    say("model c5 full")
+    path, img = synth(gpu, "c5", "t_c5full", 1)
+    rng = np.random.default_rng(13)
+    prompt = rng.integers(0, 201088, 130).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 5, 160, check_every=2)
+    gpu.image_free("t_c5full")
+    assert g == o
+    assert err <= LOGIT_TOL, err
+    assert run_pair.bit_identical
+
+
 def test_engine_request_surface(gpu):
     """submitTokens / runAll / request / cancel and an end-of-generation stop."""
     path = os.path.join(GOLD, "toy-routable.gguf")
