@@ -596,17 +596,20 @@ DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst,
 #ifndef SEQ_D
 #define SEQ_D 8
 #endif
-template <int FMT>
+template <int FMT, int ROWS>
 DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
     constexpr int D = SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
-    __shared__ __align__(16) float prod[2][64 * SEQ_S];
-    __shared__ float dvs[2][64 * SEQ_TB];
+    static_assert(ROWS == 64 || ROWS == 32, "64 or 32 rows a workgroup");
+    constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
+    constexpr int S = 32 * TB + 4;            // product row stride (floats): 16-byte reads by 16 lanes, distinct banks
+    __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
+    __shared__ float dvs[2][64 * SEQ_TB];                 // ROWS·TB = 192
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int nb32 = (int)(a.cols / 32), ntiles = (nb32 + SEQ_TB - 1) / SEQ_TB;
-    const int pb = w - 1;
-    const uint8_t *wr = sl.W + min(sl.row0 + lane, a.rows - 1) * a.row_bytes;
-    float *pdst = prod[0] + lane * SEQ_S + 32 * pb, *pdv = dvs[0] + lane * SEQ_TB + pb;
+    const int nb32 = (int)(a.cols / 32), ntiles = (nb32 + TB - 1) / TB;
+    const int pl = t - 64, prow = pl % ROWS, pb = pl / ROWS;
+    const uint8_t *wr = sl.W + min(sl.row0 + prow, a.rows - 1) * a.row_bytes;
+    float *pdst = prod[0] + prow * S + 32 * pb, *pdv = dvs[0] + prow * TB + pb;
     constexpr int PBUF = 64 * SEQ_S, DBUF = 64 * SEQ_TB;
     // both loops run a whole number of D-tile rounds: the producer's body
     // is then free of branches (tiles past the end are formed into the idle
@@ -615,34 +618,39 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
     float acc = 0.0f;
     if (w == 0) {
         __syncthreads();
-        const float *pr0 = prod[0] + lane * SEQ_S;
-        const float *dv0 = dvs[0] + lane * SEQ_TB;
+        const float *pr0 = prod[0] + min(lane, ROWS - 1) * S;
+        const float *dv0 = dvs[0] + min(lane, ROWS - 1) * TB;
         for (int i = 0; i < nit; i++) {
             const float *pr = pr0 + (i & 1) * PBUF;
-            const int nb = i < ntiles ? min(SEQ_TB, nb32 - i * SEQ_TB) : 0;
-            if (nb == SEQ_TB) {
-                float4 p[8 * SEQ_TB];
+            const int nb = i < ntiles ? min(TB, nb32 - i * TB) : 0;
+            if (nb == TB) {
+                // three blocks' products read before their first add
 #pragma unroll
-                for (int q = 0; q < 8 * SEQ_TB; q++) p[q] = *(const float4 *)(pr + 4 * q);
+                for (int b0 = 0; b0 < TB; b0 += 3) {
+                    float4 p[24];
 #pragma unroll
-                for (int b = 0; b < SEQ_TB; b++) {
-                    if constexpr (FMT == CJ_Q4_0) {
-                        float dot = 0.0f;
+                    for (int q = 0; q < 24; q++) p[q] = *(const float4 *)(pr + 32 * b0 + 4 * q);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int q = 8 * b; q < 8 * b + 8; q++) {
-                            dot = __fadd_rn(dot, p[q].x);
-                            dot = __fadd_rn(dot, p[q].y);
-                            dot = __fadd_rn(dot, p[q].z);
-                            dot = __fadd_rn(dot, p[q].w);
-                        }
-                        acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
-                    } else {
+                    for (int b = 0; b < 3; b++) {
+                        if constexpr (FMT == CJ_Q4_0) {
+                            float dot = 0.0f;
 #pragma unroll
-                        for (int q = 8 * b; q < 8 * b + 8; q++) {
-                            acc = __fadd_rn(acc, p[q].x);
-                            acc = __fadd_rn(acc, p[q].y);
-                            acc = __fadd_rn(acc, p[q].z);
-                            acc = __fadd_rn(acc, p[q].w);
+                            for (int q = 8 * b; q < 8 * b + 8; q++) {
+                                dot = __fadd_rn(dot, p[q].x);
+                                dot = __fadd_rn(dot, p[q].y);
+                                dot = __fadd_rn(dot, p[q].z);
+                                dot = __fadd_rn(dot, p[q].w);
+                            }
+                            acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b0 + b], dot));
+                        } else {
+#pragma unroll
+                            for (int q = 8 * b; q < 8 * b + 8; q++) {
+                                acc = __fadd_rn(acc, p[q].x);
+                                acc = __fadd_rn(acc, p[q].y);
+                                acc = __fadd_rn(acc, p[q].z);
+                                acc = __fadd_rn(acc, p[q].w);
+                            }
                         }
                     }
                 }
@@ -677,11 +685,11 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
         SeqItem<FMT> ring[D];
         float4 xr[2][8];
 #pragma unroll
-        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * SEQ_TB + pb);
+        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * TB + pb);
         seq_xload(xs, min(pb, nb32 - 1), xr[0]);
-        seq_xload(xs, min(SEQ_TB + pb, nb32 - 1), xr[1]);
+        seq_xload(xs, min(TB + pb, nb32 - 1), xr[1]);
         seq_products<FMT>(ring[0], xr[0], pdst, pdv);
-        ring[0] = seq_fetch<FMT>(wr, nb32, D * SEQ_TB + pb);
+        ring[0] = seq_fetch<FMT>(wr, nb32, D * TB + pb);
         __syncthreads();
         // round j of an iteration forms tile i + 1 from ring[(j + 1) % D] and
         // x registers xr[(j + 1) & 1], then loads x of tile i + 2 into xr[j & 1]
@@ -691,9 +699,9 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
                 const int i = i0 + j;
                 const int r = (j + 1) % D;
                 const int nbuf = (j + 1) & 1;      // D is even, so (i + 1) & 1
-                seq_xload(xs, min((i + 2) * SEQ_TB + pb, nb32 - 1), xr[j & 1]);
+                seq_xload(xs, min((i + 2) * TB + pb, nb32 - 1), xr[j & 1]);
                 seq_products<FMT>(ring[r], xr[nbuf], pdst + nbuf * PBUF, pdv + nbuf * DBUF);
-                ring[r] = seq_fetch<FMT>(wr, nb32, (i + 1 + D) * SEQ_TB + pb);
+                ring[r] = seq_fetch<FMT>(wr, nb32, (i + 1 + D) * TB + pb);
                 __syncthreads();
             }
         }
@@ -727,7 +735,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
     const bool live = t < R && r < a.rows;
     if constexpr (f32act) {
         // ---- one adder lane a row, in element order (64 rows a workgroup)
-        const float sv = seq_body<FMT>(a, sl, (const float *)sx);
+        // (for these formats LPR is the rows a workgroup: 64, or 32 where
+        // the matrix is short and more workgroups fill the chip)
+        const float sv = seq_body<FMT, LPR>(a, sl, (const float *)sx);
         if (live) v = sv;
     } else {
     // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
@@ -1064,3 +1074,6 @@ GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)
 GEMV_KERNEL(cj_gemv_q40, CJ_Q4_0, 64, 1)
 GEMV_KERNEL(cj_gemv_mxfp4, CJ_MXFP4, 64, 1)
 GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64, 1)
+GEMV_KERNEL(cj_gemv_q40_r32, CJ_Q4_0, 32, 1)
+GEMV_KERNEL(cj_gemv_mxfp4_r32, CJ_MXFP4, 32, 1)
+GEMV_KERNEL(cj_gemv_f32_r32, CJ_F32, 32, 1)
