@@ -600,7 +600,7 @@ template <int FMT, int ROWS>
 DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
     constexpr int D = SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
-    static_assert(ROWS == 64 || ROWS == 32, "64 or 32 rows a workgroup");
+    static_assert(ROWS == 64 || ROWS == 32 || ROWS == 1, "64, 32 or 1 rows a workgroup");
     constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
     constexpr int S = 32 * TB + 4;            // product row stride (floats): 16-byte reads by 16 lanes, distinct banks
     __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
@@ -625,7 +625,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
             const int nb = i < ntiles ? min(TB, nb32 - i * TB) : 0;
             if (nb == TB) {
                 // three blocks' products read before their first add
-#pragma unroll
+#pragma unroll(TB <= 6 ? TB / 3 : 2)
                 for (int b0 = 0; b0 < TB; b0 += 3) {
                     float4 p[24];
 #pragma unroll
@@ -735,8 +735,8 @@ DEV void gemv_body(const cj_gemv_args &a) {
     const bool live = t < R && r < a.rows;
     if constexpr (f32act) {
         // ---- one adder lane a row, in element order (64 rows a workgroup)
-        // (for these formats LPR is the rows a workgroup: 64, or 32 where
-        // the matrix is short and more workgroups fill the chip)
+        // (for these formats LPR is the rows a workgroup: 64, or 32 / 1
+        // where the matrix is short and more workgroups fill the chip)
         const float sv = seq_body<FMT, LPR>(a, sl, (const float *)sx);
         if (live) v = sv;
     } else {
@@ -1077,3 +1077,6 @@ GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64, 1)
 GEMV_KERNEL(cj_gemv_q40_r32, CJ_Q4_0, 32, 1)
 GEMV_KERNEL(cj_gemv_mxfp4_r32, CJ_MXFP4, 32, 1)
 GEMV_KERNEL(cj_gemv_f32_r32, CJ_F32, 32, 1)
+GEMV_KERNEL(cj_gemv_q40_r1, CJ_Q4_0, 1, 1)
+GEMV_KERNEL(cj_gemv_mxfp4_r1, CJ_MXFP4, 1, 1)
+GEMV_KERNEL(cj_gemv_f32_r1, CJ_F32, 1, 1)

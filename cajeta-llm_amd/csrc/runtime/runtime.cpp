@@ -209,8 +209,10 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
         // (six blocks a tile for the producers, half the tiles) where 64-row
         // workgroups would leave a quarter of the CUs idle. Measured: MXFP4
         // 11520×2880 22.7 → 19.8 µs at 32; Q4_0 14336×4096 31 → 40 µs at 32
-        const int R = rows <= 48 * (int64_t)std::max(1, g.cus) ? 32 : 64;
-        p.kernel = std::string(fam) + (R == 32 ? "_r32" : "");
+        // (1 for at most 64 rows — a router: every producer lane on one row,
+        // a 2880-wide row in one tile, a workgroup a row)
+        const int R = rows <= 64 ? 1 : rows <= 48 * (int64_t)std::max(1, g.cus) ? 32 : 64;
+        p.kernel = std::string(fam) + (R == 32 ? "_r32" : R == 1 ? "_r1" : "");
         p.rows_per_wg = R;
         p.grid = (uint32_t)((rows + R - 1) / R);
         p.per_copy = p.grid;
@@ -309,6 +311,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
         "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
         "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_gemv_q40_r32", "cj_gemv_mxfp4_r32", "cj_gemv_f32_r32",
+        "cj_gemv_q40_r1", "cj_gemv_mxfp4_r1", "cj_gemv_f32_r1",
         "cj_moe_combine",
         "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",

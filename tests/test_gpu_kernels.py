@@ -153,7 +153,7 @@ def matvec_case(gpu, O, ty, rows, cols, seed, accum=False):
 
 
 @pytest.mark.parametrize("name,ty", FORMATS)
-@pytest.mark.parametrize("rows,cols", [(300, 512), (1024, 4096), (96, 14336), (70, 2880), (32800, 96)])
+@pytest.mark.parametrize("rows,cols", [(300, 512), (1024, 4096), (96, 14336), (70, 2880), (32800, 96), (40, 2880)])
 def test_matvec_matches_oracle(gpu, O, name, ty, rows, cols):
     if cols % 256 and ty in (12, 14):
         pytest.skip("K-quant rows are whole 256-element blocks")
