@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """bench.py — greedy decode throughput of the MI355X path on the reference's
-headline workload: a Llama-3-8B-shape decoder (32 layers,
+headline workload (benchmark configuration C3): a Llama-3-8B-shape decoder (32 layers,
 d 4096, 32 query / 8 kv heads of 128, SwiGLU FFN 14336, vocab 128256, RoPE
 θ 500000) with seeded random-init Q4_K weights and a Q6_K output head, fp16
 paged K/V prefilled to 2048 positions from random tokens, then greedy decode
@@ -122,7 +122,7 @@ C4_WORKLOAD = ("C4: Llama-3-8B shape (32 layers, d 4096, 32/8 heads of 128, FFN 
 
 
 def run_c4(args, pkg, native):
-    """32 sequences prefilled to `ctx` positions (prefill
+    """benchmark configuration C4: 32 sequences prefilled to `ctx` positions (prefill
     chunks of 512), then batched greedy decode of all 32 at once; and the
     prefill rate of one 512-token chunk from position 0."""
     nseq, ctx = args.seqs, args.ctx
@@ -236,7 +236,7 @@ def c2_blocks(ty, nblocks, rng):
 
 
 def run_c2(args, native):
-    """each format × shape × batch, weights rotated over a
+    """benchmark configuration C2: each format × shape × batch, weights rotated over a
     pool of >= 512 MB of distinct prepared copies so the 256 MB last-level
     cache cannot serve them; one captured graph of launches, timed whole.
     Batch 1 is the decode GEMV; batch > 1 the int8 matrix-core product where

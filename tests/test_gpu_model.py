@@ -1,6 +1,6 @@
 """Model-level parity: the graph-captured decode step on the MI355X against
 the CPU oracle's restatement of the reference CPU backend, on the same GGUF
-bytes. Bars: greedy token ids identical; logits within
+bytes. Bars (the decode path's parity bar): greedy token ids identical; logits within
 max-abs 1e-3 (f32 accumulation). A non-degeneracy control requires more than
 one distinct generated token (T/BackendParityTest.cajeta:158-178)."""
 import os
@@ -145,7 +145,7 @@ def synth(pkg, spec, name, seed):
 
 
 def test_c1_tiny_q8_0_greedy_parity(gpu):
-    """4 layers, d 512, 8/2 heads of 64, FFN 1408, V 32000,
+    """benchmark configuration C1: 4 layers, d 512, 8/2 heads of 64, FFN 1408, V 32000,
     Q8_0, f32 embeddings; 16-token prompt, 64 greedy tokens."""
     say("model c1")
     path, img = synth(gpu, "c1", "t_c1", 1234)
@@ -162,7 +162,7 @@ def test_c1_tiny_q8_0_greedy_parity(gpu):
 
 
 def test_c3_shape_two_layers_greedy_parity(gpu):
-    """BASELINE config 3's Llama-3-8B shapes (d 4096, 32/8 heads of 128, FFN
+    """Benchmark configuration C3's Llama-3-8B shapes (d 4096, 32/8 heads of 128, FFN
     14336, V 128256, Q4_K + Q6_K head, θ 500000) at two layers."""
     say("model c3x2")
     spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=128256;eps=1e-5;theta=500000;" \
@@ -178,7 +178,7 @@ def test_c3_shape_two_layers_greedy_parity(gpu):
 
 
 def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
-    """BASELINE config 4's Q8_0 weights on the 8B shapes, at two layers."""
+    """Benchmark configuration C4's Q8_0 weights on the 8B shapes, at two layers."""
     say("model c4x2")
     spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=32000;eps=1e-5;theta=500000;" \
            "wtype=q8_0;head=q8_0;embd=q8_0;ctx=512"
@@ -193,7 +193,7 @@ def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
 
 
 def test_c4_shape_q8_0_batched_decode_parity(gpu):
-    """BASELINE config 4's batched decode at small scale: Q8_0 8B shapes at two
+    """Benchmark configuration C4's batched decode at small scale: Q8_0 8B shapes at two
     layers, three sequences at different positions decoded together."""
     say("model c4x2 batch")
     spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=32000;eps=1e-5;theta=500000;" \
@@ -207,7 +207,7 @@ def test_c4_shape_q8_0_batched_decode_parity(gpu):
 
 
 def test_c5_moe_shape_two_layers_greedy_parity(gpu):
-    """BASELINE config 5's gpt-oss-20b shapes (d 2880, 64/8 heads of 64, 32
+    """Benchmark configuration C5's gpt-oss-20b shapes (d 2880, 64/8 heads of 64, 32
     MXFP4 experts top-4 of FFN 2880, alternating 128-window attention) at two
     layers and a 32000 vocabulary."""
     say("model c5x2")
@@ -224,7 +224,7 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
 
 
 def test_c3_full_depth_greedy_parity(gpu):
-    """BASELINE config 3 at its full depth (32 layers, the benchmarked model):
+    """benchmark configuration C3 at its full depth (32 layers, the benchmarked model):
     a 40-token prompt through the prefill chunk, then 6 greedy steps; every
     step's logits bit for bit against the oracle."""
     say("model c3 full")
@@ -239,7 +239,7 @@ def test_c3_full_depth_greedy_parity(gpu):
 
 
 def test_c5_full_depth_greedy_parity(gpu):
-    """BASELINE config 5 at its full depth (24 layers, 32 MXFP4 experts top-4,
+    """benchmark configuration C5 at its full depth (24 layers, 32 MXFP4 experts top-4,
     the 201,088 vocabulary): a 130-token prompt (past the 128 window) and 4
     greedy steps, logits bit for bit against the oracle."""
     say("model c5 full")
