@@ -122,7 +122,7 @@ C4_WORKLOAD = ("C4: Llama-3-8B shape (32 layers, d 4096, 32/8 heads of 128, FFN 
 
 
 def run_c4(args, pkg, native):
-    """benchmark configuration C4: 32 sequences prefilled to `ctx` positions (prefill
+    """Benchmark configuration C4: 32 sequences prefilled to `ctx` positions (prefill
     chunks of 512), then batched greedy decode of all 32 at once; and the
     prefill rate of one 512-token chunk from position 0."""
     nseq, ctx = args.seqs, args.ctx
@@ -236,7 +236,7 @@ def c2_blocks(ty, nblocks, rng):
 
 
 def run_c2(args, native):
-    """benchmark configuration C2: each format × shape × batch, weights rotated over a
+    """Benchmark configuration C2: each format × shape × batch, weights rotated over a
     pool of >= 512 MB of distinct prepared copies so the 256 MB last-level
     cache cannot serve them; one captured graph of launches, timed whole.
     Batch 1 is the decode GEMV; batch > 1 the int8 matrix-core product where

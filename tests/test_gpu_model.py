@@ -145,7 +145,7 @@ def synth(pkg, spec, name, seed):
 
 
 def test_c1_tiny_q8_0_greedy_parity(gpu):
-    """benchmark configuration C1: 4 layers, d 512, 8/2 heads of 64, FFN 1408, V 32000,
+    """Benchmark configuration C1: 4 layers, d 512, 8/2 heads of 64, FFN 1408, V 32000,
     Q8_0, f32 embeddings; 16-token prompt, 64 greedy tokens."""
     say("model c1")
     path, img = synth(gpu, "c1", "t_c1", 1234)
@@ -224,7 +224,7 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
 
 
 def test_c3_full_depth_greedy_parity(gpu):
-    """benchmark configuration C3 at its full depth (32 layers, the benchmarked model):
+    """Benchmark configuration C3 at its full depth (32 layers, the benchmarked model):
     a 40-token prompt through the prefill chunk, then 6 greedy steps; every
     step's logits bit for bit against the oracle."""
     say("model c3 full")
@@ -239,7 +239,7 @@ def test_c3_full_depth_greedy_parity(gpu):
 
 
 def test_c5_full_depth_greedy_parity(gpu):
-    """benchmark configuration C5 at its full depth (24 layers, 32 MXFP4 experts top-4,
+    """Benchmark configuration C5 at its full depth (24 layers, 32 MXFP4 experts top-4,
     the 201,088 vocabulary): a 130-token prompt (past the 128 window) and 4
     greedy steps, logits bit for bit against the oracle."""
     say("model c5 full")
