@@ -78,27 +78,99 @@ int64_t ggml_row_bytes(int type, int64_t cols) {
 }
 
 Gguf::~Gguf() {
-    if (map_) munmap(map_, map_size_);
+    for (auto &m : maps_) munmap(m.first, m.second);
+}
+
+namespace {
+// The shard number and count a split name carries ("-00002-of-00004.gguf":
+// 2 of 4, numbered from 1), or 0 when the name is not a shard's.
+int split_in_name(const std::string &p, int *count) {
+    const size_t tail = 20;   // "-00001-of-00004.gguf"
+    if (p.size() < tail) return 0;
+    const std::string t = p.substr(p.size() - tail);
+    if (t[0] != '-' || t.compare(6, 4, "-of-") != 0 || t.compare(15, 5, ".gguf") != 0) return 0;
+    for (int i : {1, 2, 3, 4, 5, 10, 11, 12, 13, 14})
+        if (t[i] < '0' || t[i] > '9') return 0;
+    *count = std::stoi(t.substr(10, 5));
+    return std::stoi(t.substr(1, 5));
+}
+
+std::string shard_path(const std::string &prefix, int no, int count) {
+    char tail[32];
+    snprintf(tail, sizeof tail, "-%05d-of-%05d.gguf", no, count);
+    return prefix + tail;
+}
+}  // namespace
+
+bool Gguf::map_file(const std::string &path, const uint8_t **p, size_t *n, std::string &err) {
+    int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) { err = "cannot open " + path; return false; }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 24) { ::close(fd); err = "cannot stat " + path; return false; }
+    void *m = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (m == MAP_FAILED) { err = "mmap failed for " + path; return false; }
+    maps_.push_back({m, (size_t)st.st_size});
+    *p = (const uint8_t *)m;
+    *n = (size_t)st.st_size;
+    return true;
 }
 
 bool Gguf::open(const std::string &path, std::string &err) {
     if (path.rfind("mem:", 0) == 0) {
         const uint8_t *p; size_t n;
         if (!image_get(path.substr(4), &p, &n)) { err = "no in-process image " + path; return false; }
-        return parse(p, n, err);
+        return parse(p, n, kv_, err);
     }
-    int fd = ::open(path.c_str(), O_RDONLY);
-    if (fd < 0) { err = "cannot open " + path; return false; }
-    struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size < 24) { ::close(fd); err = "cannot stat " + path; return false; }
-    map_size_ = (size_t)st.st_size;
-    map_ = mmap(nullptr, map_size_, PROT_READ, MAP_PRIVATE, fd, 0);
-    ::close(fd);
-    if (map_ == MAP_FAILED) { map_ = nullptr; err = "mmap failed for " + path; return false; }
-    return parse((const uint8_t *)map_, map_size_, err);
+    // a later shard's name leads to shard 1, which carries the metadata
+    int named = 0;
+    const int no = split_in_name(path, &named);
+    const std::string prefix = no > 0 ? path.substr(0, path.size() - 20) : path;
+    const std::string root = no > 1 ? shard_path(prefix, 1, named) : path;
+    const uint8_t *p; size_t n;
+    if (!map_file(root, &p, &n, err)) {
+        if (no > 1) err = "gguf: '" + path + "' is shard " + std::to_string(no) + " of " + std::to_string(named) +
+                          " and shard 1, which carries the model metadata, is missing - expected '" + root + "'";
+        return false;
+    }
+    if (!parse(p, n, kv_, err)) return false;
+    const int64_t count = get_int("split.count", 1);
+    if (count <= 1) return true;
+    if (get_int("split.no", 0) != 0) { err = "gguf: '" + root + "' carries the model metadata but is not split 0"; return false; }
+    if (no == 0 || named != count) {
+        err = "gguf: '" + root + "' declares split.count " + std::to_string(count) +
+              " but its name does not follow <base>-%05d-of-%05d.gguf for that count";
+        return false;
+    }
+    for (int k = 2; k <= (int)count; k++) {
+        const std::string sp = shard_path(prefix, k, (int)count);
+        std::string e2;
+        if (!map_file(sp, &p, &n, e2)) {
+            int have = 1;
+            for (int j = 2; j <= (int)count; j++) if (::access(shard_path(prefix, j, (int)count).c_str(), R_OK) == 0) have++;
+            err = "gguf: shard " + std::to_string(k) + " of " + std::to_string(count) + " is missing - expected '" + sp +
+                  "'; found " + std::to_string(have) + " of " + std::to_string(count) +
+                  " shards. Refusing to load a truncated model.";
+            return false;
+        }
+        std::map<std::string, GgufValue> skv;
+        if (!parse(p, n, skv, err)) return false;
+        auto it = skv.find("split.no");
+        if (it == skv.end() || it->second.i != k - 1) {
+            err = "gguf: '" + sp + "' does not declare split.no " + std::to_string(k - 1);
+            return false;
+        }
+    }
+    const int64_t want = get_int("split.tensors.count", (int64_t)tensors_.size());
+    if (want != (int64_t)tensors_.size()) {
+        err = "gguf: the shards hold " + std::to_string(tensors_.size()) + " tensors, split.tensors.count says " +
+              std::to_string(want);
+        return false;
+    }
+    return true;
 }
 
-bool Gguf::parse(const uint8_t *p, size_t n, std::string &err) {
+bool Gguf::parse(const uint8_t *p, size_t n, std::map<std::string, GgufValue> &kv, std::string &err) {
     Rd r{p, n};
     if (r.get<uint32_t>() != 0x46554747u) { err = "not a GGUF file (magic)"; return false; }
     uint32_t ver = r.get<uint32_t>();
@@ -109,8 +181,9 @@ bool Gguf::parse(const uint8_t *p, size_t n, std::string &err) {
         int ty = (int)r.get<uint32_t>();
         GgufValue v;
         if (!read_value(r, ty, v)) { err = "bad metadata value for " + k; return false; }
-        kv_[k] = std::move(v);
+        kv[k] = std::move(v);
     }
+    const size_t first = tensors_.size();
     for (uint64_t i = 0; i < nt && r.ok; i++) {
         GgufTensor t;
         t.name = r.str();
@@ -122,17 +195,19 @@ bool Gguf::parse(const uint8_t *p, size_t n, std::string &err) {
         tensors_.push_back(std::move(t));
     }
     if (!r.ok) { err = "truncated GGUF header"; return false; }
-    // alignment: io/GgufFile.cajeta:773-777
-    uint64_t align = (uint64_t)get_int("general.alignment", 32);
+    // alignment: io/GgufFile.cajeta:773-777 (each file's own)
+    auto al = kv.find("general.alignment");
+    uint64_t align = al != kv.end() ? (uint64_t)al->second.i : 32;
     if (align == 0) align = 32;
     uint64_t data = (r.at + align - 1) / align * align;
-    for (size_t i = 0; i < tensors_.size(); i++) {
+    for (size_t i = first; i < tensors_.size(); i++) {
         GgufTensor &t = tensors_[i];
         int64_t rb = ggml_row_bytes(t.type, t.cols());
         if (rb < 0) { err = "tensor " + t.name + ": type " + std::to_string(t.type) + " is not served"; return false; }
         t.bytes = rb * t.rows();
         if (data + t.offset + (uint64_t)t.bytes > n) { err = "tensor " + t.name + " runs past the end of the file"; return false; }
         t.data = p + data + t.offset;
+        if (index_.count(t.name)) { err = "tensor " + t.name + " appears twice"; return false; }
         index_[t.name] = i;
     }
     return true;

@@ -33,8 +33,13 @@ struct GgufValue {
 
 class Gguf {
 public:
-    // Open a file (mmap) or "mem:<name>" (an image from the registry).
+    // Open a file (mmap) or "mem:<name>" (an image from the registry). A
+    // split model (<base>-%05d-of-%05d.gguf, split.no / split.count) opens
+    // from any of its shards as one name→tensor map: shard 1 carries the
+    // metadata, every shard its own tensor directory and data
+    // (io/GgufFile.cajeta:45-55, :467-560).
     bool open(const std::string &path, std::string &err);
+    int shards() const { return (int)maps_.size() > 0 ? (int)maps_.size() : 1; }
     ~Gguf();
     const GgufTensor *tensor(const std::string &name) const;
     bool has(const std::string &key) const { return kv_.count(key) != 0; }
@@ -45,12 +50,14 @@ public:
     const std::vector<GgufTensor> &tensors() const { return tensors_; }
 
 private:
-    bool parse(const uint8_t *p, size_t n, std::string &err);
+    // parse one file's header; metadata into kv (the model's for shard 1,
+    // a scratch map for the others), tensors appended to the directory
+    bool parse(const uint8_t *p, size_t n, std::map<std::string, GgufValue> &kv, std::string &err);
+    bool map_file(const std::string &path, const uint8_t **p, size_t *n, std::string &err);
     std::map<std::string, GgufValue> kv_;
     std::vector<GgufTensor> tensors_;
     std::map<std::string, size_t> index_;
-    void *map_ = nullptr;
-    size_t map_size_ = 0;
+    std::vector<std::pair<void *, size_t>> maps_;
 };
 
 int64_t ggml_row_bytes(int type, int64_t cols);   // -1 when not whole blocks

@@ -371,4 +371,13 @@ int32_t cj_image_info(const int8_t *name, int64_t *addr, int64_t *size) {
 int32_t cj_image_free(const int8_t *name) {
     return name && cj::image_free((const char *)name) ? CJ_OK : cj::fail(CJ_ERR_ARG, "cj_image_free: no image");
 }
+int32_t cj_gguf_info(const int8_t *path, int64_t *n_tensors, int64_t *n_shards) {
+    if (!path || !n_tensors || !n_shards) return cj::fail(CJ_ERR_ARG, "cj_gguf_info: null argument");
+    cj::Gguf f;
+    std::string err;
+    if (!f.open((const char *)path, err)) return cj::fail(CJ_ERR_IO, "%s", err.c_str());
+    *n_tensors = (int64_t)f.tensors().size();
+    *n_shards = f.shards();
+    return CJ_OK;
+}
 }

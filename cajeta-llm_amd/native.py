@@ -78,6 +78,7 @@ SIGNATURES = {
     "cj_engine_set_graphs": (I32, [I64, I32]),
     "cj_synth_gguf": (I32, [CP, CP, I64]),
     "cj_image_info": (I32, [CP, P, P]),
+    "cj_gguf_info": (I32, [CP, P, P]),
     "cj_image_free": (I32, [CP]),
 }
 

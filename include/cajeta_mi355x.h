@@ -286,6 +286,12 @@ int32_t cj_synth_gguf(const int8_t *spec, const int8_t *path, int64_t seed);
 /* Host address and size of an in-process image (for checkers). */
 int32_t cj_image_info(const int8_t *name, int64_t *addr, int64_t *size);
 int32_t cj_image_free(const int8_t *name);
+/* Open a GGUF as the engine's loader does — one file, or a split model
+ * (<base>-%05d-of-%05d.gguf) from any of its shards — and report its tensor
+ * and shard counts; no GPU needed (GgufFile's directory,
+ * io/GgufFile.cajeta:45-55, :467-560). Missing or mismatched shards fail
+ * with the reason. */
+int32_t cj_gguf_info(const int8_t *path, int64_t *n_tensors, int64_t *n_shards);
 
 #ifdef __cplusplus
 }

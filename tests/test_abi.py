@@ -52,3 +52,29 @@ def test_prepared_row_bytes(pkg):
     assert lib.cj_prepared_row_bytes(8, 1408) == 44 * 32 + 96       # 88 bytes of scales, padded to 96
     assert lib.cj_prepared_row_bytes(39, 2880) == 90 * 16 + 96
     assert lib.cj_prepared_row_bytes(12, 1000) < 0
+
+
+def _gguf_info(pkg, path):
+    import ctypes
+    nt, ns = ctypes.c_int64(0), ctypes.c_int64(0)
+    rc = pkg.native.lib().cj_gguf_info(path.encode(), ctypes.byref(nt), ctypes.byref(ns))
+    return rc, nt.value, ns.value
+
+
+def test_split_gguf_opens_as_one_model(pkg, tmp_path):
+    """A model split into <base>-%05d-of-%05d.gguf shards opens from any
+    shard as the whole directory (io/GgufFile.cajeta:45-55, :467-560); a
+    missing shard is refused by name."""
+    from gguf_split import split_gguf
+    src = os.path.join(os.path.dirname(__file__), "golden", "gguf", "toy-routable.gguf")
+    rc, n_one, s_one = _gguf_info(pkg, src)
+    assert rc == 0 and s_one == 1 and n_one > 3
+    paths = split_gguf(src, str(tmp_path / "toy"), 3)
+    for p in paths:
+        rc, n, s = _gguf_info(pkg, p)
+        assert (rc, n, s) == (0, n_one, 3), p
+    os.remove(paths[2])
+    rc, _, _ = _gguf_info(pkg, paths[0])
+    assert rc != 0
+    msg = pkg.native.last_error()
+    assert "missing" in msg and "00003-of-00003" in msg, msg

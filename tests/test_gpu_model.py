@@ -75,6 +75,18 @@ def test_reference_toy_fixture_greedy_parity(gpu, name):
     assert len(set(g)) > 1
 
 
+def test_split_gguf_decodes_as_the_whole_file(gpu, tmp_path):
+    """The reference's toy GGUF split into three shards and loaded from the
+    middle one decodes exactly as the oracle does on the unsplit file."""
+    from gguf_split import split_gguf
+    src = os.path.join(GOLD, "toy-routable.gguf")
+    paths = split_gguf(src, str(tmp_path / "toy"), 3)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, 256, 10).tolist()
+    g, o, err = run_pair(gpu, paths[1], src, prompt, 12, 256)
+    assert g == o and run_pair.bit_identical, (g, o, err)
+
+
 def test_prefill_chunks_are_invisible(gpu):
     """A 45-token prompt as one chunk and as chunks of 7: chunking changes
     nothing (every row's arithmetic is the same), both against the oracle's
