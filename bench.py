@@ -394,14 +394,65 @@ def run_single(args, pkg, native, which):
     print(json.dumps(line), flush=True)
 
 
+def run_c5k(args, native):
+    """The C5 kernels at their shapes through the launch seam (weights
+    prepared once with cj_prepare_weight, seeded random blocks): the expert
+    products, the router and the two-pass attention at 4096 positions. Host
+    launches back to back, timed over the batch of calls."""
+    lib = native.lib()
+    rng = np.random.default_rng(args.seed)
+    out = {}
+    for name, ty, rows, cols, bb, be in (("mxfp4 experts down 4x2880x2880", 39, 11520, 2880, 17, 32),
+                                         ("mxfp4 experts gate|up 4x5760x2880", 39, 23040, 2880, 17, 32),
+                                         ("f32 router 32x2880", 0, 32, 2880, 4, 1)):
+        raw = rng.integers(0, 256, rows * cols // be * bb, dtype=np.uint8)
+        if ty == 0:
+            raw = rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+        else:
+            r = raw.reshape(-1, bb)
+            r[:, 0] = rng.integers(110, 130, r.shape[0])
+        prb = lib.cj_prepared_row_bytes(ty, cols)
+        src, w = native.Buffer.of(raw), native.Buffer(prb * rows)
+        native.check(lib.cj_prepare_weight(w.h, src.h, ty, rows, cols), "prepare")
+        x = native.Buffer.of(rng.standard_normal(cols).astype(np.float32))
+        y = native.Buffer(rows * 4)
+        for _ in range(5):
+            native.check(lib.cj_matvec(ty, y.h, w.h, x.h, rows, cols, 0, 0), "matvec")
+        native.sync()
+        t = time.perf_counter()
+        for _ in range(200):
+            lib.cj_matvec(ty, y.h, w.h, x.h, rows, cols, 0, 0)
+        native.sync()
+        us = (time.perf_counter() - t) / 200 * 1e6
+        out[name] = {"us": round(us, 2), "GB/s": round(prb * rows / (us * 1e-6) / 1e9, 1)}
+        log("%-36s %8.2f us" % (name, us))
+    n_q, n_kv, hd, count = 64, 8, 64, 4096
+    pages = (count + 63) // 64
+    kb = native.Buffer.of((rng.standard_normal(pages * n_kv * 64 * hd) * 0.5).astype(np.float16).view(np.uint16))
+    vb = native.Buffer.of((rng.standard_normal(pages * n_kv * 64 * hd) * 0.5).astype(np.float16).view(np.uint16))
+    tb = native.Buffer.of(np.arange(pages, dtype=np.int32))
+    qb = native.Buffer.of(rng.standard_normal(n_q * hd).astype(np.float32))
+    part = native.Buffer(n_q * max(64 * (hd + 2), count) * 4)
+    ob, cnt = native.Buffer(n_q * hd * 4), native.Buffer(4 * n_kv)
+    for _ in range(103):
+        native.check(lib.cj_attend(part.h, ob.h, qb.h, kb.h, vb.h, tb.h, 0, cnt.h, n_q, n_kv, hd, count, 0, 512, 0.125),
+                     "attend")
+    native.sync()
+    print(json.dumps({"metric": "C5 kernels at their shapes (launch seam; per-kernel durations from rocprofv3)",
+                      "value": out["mxfp4 experts down 4x2880x2880"]["us"], "unit": "us", "n_gpus": 1,
+                      "higher_is_better": False, "data": "synthetic: seeded random blocks",
+                      "config": {"workload": "C5 kernel shapes"}, "kernels": out}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps (K)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before (W)")
-    ap.add_argument("--workload", choices=("c3", "c4", "c2", "c1", "c5"), default="c3",
+    ap.add_argument("--workload", choices=("c3", "c4", "c2", "c1", "c5", "c5k"), default="c3",
                     help="c3: the headline batch-1 Q4_K decode; c4: batched Q8_0 decode + prefill; "
-                         "c2: the quantised GEMV microbench; c1: tiny Q8_0 decode; c5: MoE decode")
+                         "c2: the quantised GEMV microbench; c1: tiny Q8_0 decode; c5: MoE decode; "
+                         "c5k: the C5 kernels at their shapes through the launch seam")
     ap.add_argument("--ctx", type=int, default=None, help="positions prefilled before decoding (c3 2048, c4 4096)")
     ap.add_argument("--seqs", type=int, default=32, help="c4: sequences decoded together")
     ap.add_argument("--cpu-threads", type=int, default=0,
@@ -429,6 +480,9 @@ def main():
     native.init()
     if args.workload == "c2":
         run_c2(args, native)
+        return
+    if args.workload == "c5k":
+        run_c5k(args, native)
         return
     if args.workload in SINGLE:
         run_single(args, pkg, native, args.workload)
