@@ -453,14 +453,14 @@ struct CombineItem {
 // (entry j for page from/64 + j), so no V load waits on a page-table load.
 template <int HD, int T>
 DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, int count, int from, int kvh,
-                              int dg, int tq, int I) {
+                              int d0, int dg, int tq, int I) {
     CombineItem it;
     const int t0 = I * T + 4 * tq;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int t = min(t0 + k, count - 1), pos = from + t;
         const int page = pgs[(pos >> 6) - (from >> 6)];
-        it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * dg);
+        it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + 8 * dg);
         it.e[k] = ev[t];
     }
     return it;
@@ -485,7 +485,8 @@ DEV void combine_store(float *pb, const CombineItem &it, int I, int count, int t
 }
 
 // softmax over scores[h][0..count) in place and out[h] = Σ_t p_t·V_t / Σ p:
-// one workgroup of 256 per query head, spans of up to COMBINE_PAGES pages.
+// one workgroup of 256 per query head and 32 output dimensions, spans of up
+// to COMBINE_PAGES pages.
 //   max   lanes 0..127 (max is exact, so any grouping gives the same value);
 //   sum   lanes 0..127 as the reference's 128: lane l adds e_t for t = l,
 //         l+128, ... in order (e_t kept in LDS, or past COMBINE_ES positions
@@ -505,9 +506,11 @@ DEV void combine_store(float *pb, const CombineItem &it, int I, int count, int t
 
 template <int HD>
 struct CombineDims {
-    static constexpr int A = HD / 64;               // adder waves
+    static constexpr int DH = 32;                   // output dimensions a workgroup (HD/DH workgroups a head)
+    static constexpr int NSPLIT = HD / DH;
+    static constexpr int A = 1;                     // adder wave (DH lanes)
     static constexpr int P = 256 - 64 * A;          // producer lanes
-    static constexpr int DG = HD / 8;               // 8-dimension groups of a V row
+    static constexpr int DG = DH / 8;               // 8-dimension groups of the workgroup's slice of a V row
     static constexpr int TQ = P / DG;               // 4-position groups a tile: one 4 × 8 item a producer lane
     static constexpr int T = 4 * TQ;                // positions a tile
     static constexpr int S = T + 4;                 // product row stride (floats): 16 lanes' 16-byte reads, distinct banks
@@ -518,7 +521,8 @@ struct CombineDims {
 // (even) tiles of V are in flight per producer; both roles run a whole
 // number of CD-tile rounds.
 template <int HD, int CD>
-DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float *prod, int count, int from, int kvh) {
+DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float *prod, int count, int from, int kvh,
+                     int d0) {
     using D = CombineDims<HD>;
     constexpr int T = D::T, S = D::S;
     const int l = threadIdx.x, w = l >> 6, ntiles = (count + T - 1) / T;
@@ -529,9 +533,9 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
     float acc = 0.0f;
     if (w < D::A) {
         __syncthreads();
-        const float *pr = prod + (64 * w + (l & 63)) * S;
+        const float *pr = prod + min(l, D::DH - 1) * S;
         for (int i = 0; i < nit; i++) {
-            const float *pt = pr + (i & 1) * (HD * S);
+            const float *pt = pr + (i & 1) * (D::DH * S);
             const int n = i < ntiles ? min(T, count - i * T) : 0;
             if (n == T) {
                 // every read issued before the first add (the scheduler would
@@ -562,17 +566,17 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
         // CD tiles of V rows and weights in flight, ring slot = tile mod CD
         CombineItem ring[CD];
 #pragma unroll
-        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, j);
+        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, j);
         float *pb = prod + 8 * dg * S + 4 * tq;
         combine_store<T, S>(pb, ring[0], 0, count, tq);
-        ring[0] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, CD);
+        ring[0] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, CD);
         __syncthreads();
         for (int i0 = 0; i0 < nit; i0 += CD) {
 #pragma unroll
             for (int j = 0; j < CD; j++) {
                 const int i = i0 + j, r = (j + 1) % CD;
-                combine_store<T, S>(pb + ((j + 1) & 1) * (HD * S), ring[r], i + 1, count, tq);
-                ring[r] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, dg, tq, i + 1 + CD);
+                combine_store<T, S>(pb + ((j + 1) & 1) * (D::DH * S), ring[r], i + 1, count, tq);
+                ring[r] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, i + 1 + CD);
                 __syncthreads();
             }
         }
@@ -584,12 +588,12 @@ template <int HD>
 DEV void combine_body(const cj_attn_args &a) {
     using D = CombineDims<HD>;
     __shared__ float red[4 + 128];
-    __shared__ __align__(16) float prod[2 * HD * D::S];
+    __shared__ __align__(16) float prod[2 * D::DH * D::S];   // also V of a short span: 2048 chunks of 16 bytes
     __shared__ int pgs[COMBINE_PAGES];
     __shared__ __align__(16) float es[COMBINE_ES];
     int count, from;
     attn_window(a, count, from);
-    const int h = blockIdx.x, l = threadIdx.x;
+    const int h = blockIdx.x / D::NSPLIT, d0 = D::DH * (blockIdx.x % D::NSPLIT), l = threadIdx.x;
     const int grp = a.n_q / a.n_kv, kvh = h / grp;
     float *sc = a.part + (int64_t)h * a.splits;
     const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
@@ -690,30 +694,30 @@ DEV void combine_body(const cj_attn_args &a) {
             if (c < count * (HD / 8)) *(u32x4 *)(vs + 8 * c) = vst[k];
         }
         __syncthreads();
-        if (l < HD) {
+        if (l < D::DH) {
             float acc = 0.0f;
             int t = 0;
             for (; t + 4 <= count; t += 4) {
                 const float4 e4 = *(const float4 *)(es + t);
-                const float v0 = h2f(vs[t * HD + l]), v1 = h2f(vs[(t + 1) * HD + l]);
-                const float v2 = h2f(vs[(t + 2) * HD + l]), v3 = h2f(vs[(t + 3) * HD + l]);
+                const float v0 = h2f(vs[t * HD + d0 + l]), v1 = h2f(vs[(t + 1) * HD + d0 + l]);
+                const float v2 = h2f(vs[(t + 2) * HD + d0 + l]), v3 = h2f(vs[(t + 3) * HD + d0 + l]);
                 acc = __fadd_rn(acc, __fmul_rn(e4.x, v0));
                 acc = __fadd_rn(acc, __fmul_rn(e4.y, v1));
                 acc = __fadd_rn(acc, __fmul_rn(e4.z, v2));
                 acc = __fadd_rn(acc, __fmul_rn(e4.w, v3));
             }
-            for (; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(es[t], h2f(vs[t * HD + l])));
-            a.out[(int64_t)h * HD + l] = __fmul_rn(acc, rs);
+            for (; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(es[t], h2f(vs[t * HD + d0 + l])));
+            a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
         }
         return;
     }
     // short spans (the sliding windows, early positions) take a two-tile
     // ring, so few rounds are padded
     const int ntiles = (count + D::T - 1) / D::T;
-    const float acc = !elds ? combine_pv<HD, 6>(a, pgs, sc, prod, count, from, kvh)
-                      : ntiles <= 4 ? combine_pv<HD, 2>(a, pgs, es, prod, count, from, kvh)
-                                    : combine_pv<HD, 6>(a, pgs, es, prod, count, from, kvh);
-    if (l < 64 * D::A) a.out[(int64_t)h * HD + l] = __fmul_rn(acc, rs);
+    const float acc = !elds ? combine_pv<HD, 6>(a, pgs, sc, prod, count, from, kvh, d0)
+                      : ntiles <= 4 ? combine_pv<HD, 2>(a, pgs, es, prod, count, from, kvh, d0)
+                                    : combine_pv<HD, 6>(a, pgs, es, prod, count, from, kvh, d0);
+    if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
 extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a); }

@@ -501,7 +501,7 @@ int Engine::enqueue_step(int s) {
                     if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_kv, 256,
                                       (uint32_t)(grp * head_dim * 4), a)))
                         return rc;
-                    if ((rc = launch(combine_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
+                    if ((rc = launch(combine_kernel, (uint32_t)(n_heads * (head_dim / 32)), 256, 0, a))) return rc;
                 }
             }
         }
