@@ -598,7 +598,8 @@ DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst,
 #endif
 template <int FMT, int ROWS>
 DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
-    constexpr int D = SEQ_D;
+    // one row a workgroup: a tile is 192 blocks, so two in flight suffice
+    constexpr int D = ROWS == 1 ? 2 : SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
     static_assert(ROWS == 64 || ROWS == 32 || ROWS == 1, "64, 32 or 1 rows a workgroup");
     constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
@@ -620,64 +621,70 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
         __syncthreads();
         const float *pr0 = prod[0] + min(lane, ROWS - 1) * S;
         const float *dv0 = dvs[0] + min(lane, ROWS - 1) * TB;
+        // three blocks' products read before their first add
+        auto add3 = [&](const float *pr, const float *dv, int b0) {
+            float4 p[24];
+#pragma unroll
+            for (int q = 0; q < 24; q++) p[q] = *(const float4 *)(pr + 32 * b0 + 4 * q);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int b = 0; b < 3; b++) {
+                if constexpr (FMT == CJ_Q4_0) {
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int q = 8 * b; q < 8 * b + 8; q++) {
+                        dot = __fadd_rn(dot, p[q].x);
+                        dot = __fadd_rn(dot, p[q].y);
+                        dot = __fadd_rn(dot, p[q].z);
+                        dot = __fadd_rn(dot, p[q].w);
+                    }
+                    acc = __fadd_rn(acc, __fmul_rn(dv[b0 + b], dot));
+                } else {
+#pragma unroll
+                    for (int q = 8 * b; q < 8 * b + 8; q++) {
+                        acc = __fadd_rn(acc, p[q].x);
+                        acc = __fadd_rn(acc, p[q].y);
+                        acc = __fadd_rn(acc, p[q].z);
+                        acc = __fadd_rn(acc, p[q].w);
+                    }
+                }
+            }
+        };
+        auto add1 = [&](const float *pr, const float *dv, int b) {
+            if constexpr (FMT == CJ_Q4_0) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                    dot = __fadd_rn(dot, p.x);
+                    dot = __fadd_rn(dot, p.y);
+                    dot = __fadd_rn(dot, p.z);
+                    dot = __fadd_rn(dot, p.w);
+                }
+                acc = __fadd_rn(acc, __fmul_rn(dv[b], dot));
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                    acc = __fadd_rn(acc, p.x);
+                    acc = __fadd_rn(acc, p.y);
+                    acc = __fadd_rn(acc, p.z);
+                    acc = __fadd_rn(acc, p.w);
+                }
+            }
+        };
         for (int i = 0; i < nit; i++) {
             const float *pr = pr0 + (i & 1) * PBUF;
+            const float *dv = dv0 + (i & 1) * DBUF;
             const int nb = i < ntiles ? min(TB, nb32 - i * TB) : 0;
             if (nb == TB) {
-                // three blocks' products read before their first add
 #pragma unroll(TB <= 6 ? TB / 3 : 2)
-                for (int b0 = 0; b0 < TB; b0 += 3) {
-                    float4 p[24];
-#pragma unroll
-                    for (int q = 0; q < 24; q++) p[q] = *(const float4 *)(pr + 32 * b0 + 4 * q);
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int b = 0; b < 3; b++) {
-                        if constexpr (FMT == CJ_Q4_0) {
-                            float dot = 0.0f;
-#pragma unroll
-                            for (int q = 8 * b; q < 8 * b + 8; q++) {
-                                dot = __fadd_rn(dot, p[q].x);
-                                dot = __fadd_rn(dot, p[q].y);
-                                dot = __fadd_rn(dot, p[q].z);
-                                dot = __fadd_rn(dot, p[q].w);
-                            }
-                            acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b0 + b], dot));
-                        } else {
-#pragma unroll
-                            for (int q = 8 * b; q < 8 * b + 8; q++) {
-                                acc = __fadd_rn(acc, p[q].x);
-                                acc = __fadd_rn(acc, p[q].y);
-                                acc = __fadd_rn(acc, p[q].z);
-                                acc = __fadd_rn(acc, p[q].w);
-                            }
-                        }
-                    }
-                }
+                for (int b0 = 0; b0 < TB; b0 += 3) add3(pr, dv, b0);
             } else {
-                for (int b = 0; b < nb; b++) {
-                    if constexpr (FMT == CJ_Q4_0) {
-                        float dot = 0.0f;
-#pragma unroll
-                        for (int q = 0; q < 8; q++) {
-                            const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                            dot = __fadd_rn(dot, p.x);
-                            dot = __fadd_rn(dot, p.y);
-                            dot = __fadd_rn(dot, p.z);
-                            dot = __fadd_rn(dot, p.w);
-                        }
-                        acc = __fadd_rn(acc, __fmul_rn(dv0[(i & 1) * DBUF + b], dot));
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 8; q++) {
-                            const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                            acc = __fadd_rn(acc, p.x);
-                            acc = __fadd_rn(acc, p.y);
-                            acc = __fadd_rn(acc, p.z);
-                            acc = __fadd_rn(acc, p.w);
-                        }
-                    }
-                }
+                // a short tile (the row's last): whole chunks of three, then single blocks
+                int b0 = 0;
+                for (; b0 + 3 <= nb; b0 += 3) add3(pr, dv, b0);
+                for (int b = b0; b < nb; b++) add1(pr, dv, b);
             }
             __syncthreads();
         }
