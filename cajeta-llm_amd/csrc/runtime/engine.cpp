@@ -1006,13 +1006,14 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
     only = kind;
     only_layer = 0;
     const uint64_t before = launch_count();
+    launch_names_reset();
     int rc = enqueue_step(s);                     // one untimed launch
     if (!rc && launch_count() == before) rc = fail(CJ_ERR_ARG, "time: kind %d launches nothing in this model's step", kind);
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
         rc = fail(CJ_ERR_HIP, "time: event create");
     if (!rc) {
-        kernel = last_launch();
+        kernel = launch_names();
         // the reps as the step runs them: captured into one graph and
         // replayed (eager launches when graphs are off, for profilers)
         hipGraphExec_t ge = nullptr;

@@ -12,6 +12,8 @@ namespace cj {
 int fail(int code, const char *fmt, ...);
 const char *last_error();
 const char *last_launch();   // the name of the last kernel launched on this thread
+void launch_names_reset();    // start a new record of the kernels launched on this thread
+const char *launch_names();   // their distinct names in first-launch order, " + "-joined
 uint64_t launch_count();     // launches made so far
 
 bool ready();

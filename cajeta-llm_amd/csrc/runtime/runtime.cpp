@@ -31,6 +31,8 @@ struct Ctx {
 Ctx g;
 thread_local std::string g_err;
 thread_local std::string g_last_launch;
+thread_local std::string g_launch_names;    // distinct names since launch_names_reset, " + "-joined
+thread_local bool g_naming = false;         // recording them (until launch_names)
 uint64_t g_launches = 0;   // launches made (the timing seam checks a kind launched something)
 
 // The reference's kernel names (KernelCap.nameOf, model/KernelCap.cajeta:100-140
@@ -97,6 +99,8 @@ int fail(int code, const char *fmt, ...) {
 }
 const char *last_error() { return g_err.c_str(); }
 const char *last_launch() { return g_last_launch.c_str(); }
+void launch_names_reset() { g_launch_names.clear(); g_naming = true; }
+const char *launch_names() { g_naming = false; return g_launch_names.c_str(); }
 bool ready() { return g.module != nullptr; }
 hipStream_t stream() { return g.stream; }
 int device_cus() { return g.cus; }
@@ -142,6 +146,8 @@ int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, co
     hipError_t e = hipModuleLaunchKernel(it->second, grid, grid_y, 1, block, 1, 1, lds, g.stream, params, nullptr);
     if (e != hipSuccess) return fail(CJ_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e));
     g_last_launch = name;
+    if (g_naming && (" + " + g_launch_names + " + ").find(" + " + std::string(name) + " + ") == std::string::npos)
+        g_launch_names += (g_launch_names.empty() ? "" : " + ") + std::string(name);
     g_launches++;
     return CJ_OK;
 }
