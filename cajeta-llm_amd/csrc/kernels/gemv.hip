@@ -734,7 +734,11 @@ DEV void gemv_body(const cj_gemv_args &a) {
     const GemvSlice sl = gemv_slice(a);
     const int64_t row0 = sl.row0;
 
-    gemv_prologue(a, sl, f32act, sx, red, 320);
+    // one row a workgroup over plain f32 x: no two producer lanes share a
+    // block of x, so each reads its block from global memory beside its
+    // weights rather than after x is staged in LDS (one round trip fewer)
+    const bool xdirect = f32act && LPR == 1 && a.pro == CJ_PRO_F32 && ((uintptr_t)sl.X & 15) == 0;
+    if (!xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
     const EpiPre pre = epi_prefetch(a, sl);
 
     float v = 0.0f;
@@ -744,7 +748,7 @@ DEV void gemv_body(const cj_gemv_args &a) {
         // ---- one adder lane a row, in element order (64 rows a workgroup)
         // (for these formats LPR is the rows a workgroup: 64, or 32 / 1
         // where the matrix is short and more workgroups fill the chip)
-        const float sv = seq_body<FMT, LPR>(a, sl, (const float *)sx);
+        const float sv = seq_body<FMT, LPR>(a, sl, xdirect ? sl.X : (const float *)sx);
         if (live) v = sv;
     } else {
     // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
