@@ -192,6 +192,8 @@ typedef struct {
 typedef struct {
     float *out; const uint8_t *table; const int32_t *tokens; const cj_step_state *state;
     int32_t type; int64_t hidden; int64_t row_bytes; int32_t token;
+    int32_t vocab;           // > 0: a device-read token id outside [0, vocab) writes zeros and sets *status
+    int32_t *status;
 } cj_embed_args;
 
 typedef struct {
@@ -213,6 +215,9 @@ typedef struct {
 
 typedef struct {
     const float *logits; int32_t *sel; float *w; int32_t n_experts, n_used, norm_topk, rows;
+    float w_scale;           // expert_weights_scale: applied when neither 0 nor 1
+    int32_t pad;
+    int32_t *status;         // set to 1 when a row's logits are not finite (may be null)
 } cj_route_args;
 
 typedef struct {

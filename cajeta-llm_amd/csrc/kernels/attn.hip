@@ -451,9 +451,13 @@ struct CombineItem {
 
 // Pages are read from `pgs`, the sequence's page-table entries staged in LDS
 // (entry j for page from/64 + j), so no V load waits on a page-table load.
-template <int HD, int T>
-DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, int count, int from, int kvh,
-                              int d0, int dg, int tq, int I) {
+// EXP: `ev` holds the scores and e_t = exp(s_t − m) is formed here (the same
+// operation on the same operands as the sum pass, so the same bits): spans
+// longer than the LDS weight buffer never write the score row, which the
+// head's sibling workgroups read concurrently.
+template <int HD, int T, bool EXP>
+DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, float m, int count, int from,
+                              int kvh, int d0, int dg, int tq, int I) {
     CombineItem it;
     const int t0 = I * T + 4 * tq;
 #pragma unroll
@@ -461,7 +465,7 @@ DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float
         const int t = min(t0 + k, count - 1), pos = from + t;
         const int page = pgs[(pos >> 6) - (from >> 6)];
         it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + 8 * dg);
-        it.e[k] = ev[t];
+        it.e[k] = EXP ? cj_expf(ev[t] - m) : ev[t];
     }
     return it;
 }
@@ -517,12 +521,12 @@ struct CombineDims {
 };
 
 // p·V of the combine: returns the adder lane's sum (0 on producers). `ev` is
-// the weights e_t: in LDS or, past COMBINE_ES positions, over the scores. CD
-// (even) tiles of V are in flight per producer; both roles run a whole
-// number of CD-tile rounds.
-template <int HD, int CD>
-DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float *prod, int count, int from, int kvh,
-                     int d0) {
+// the weights e_t in LDS or (EXP, spans past COMBINE_ES positions) the scores
+// with their maximum m. CD (even) tiles of V are in flight per producer; both
+// roles run a whole number of CD-tile rounds.
+template <int HD, int CD, bool EXP>
+DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float m, float *prod, int count, int from,
+                     int kvh, int d0) {
     using D = CombineDims<HD>;
     constexpr int T = D::T, S = D::S;
     const int l = threadIdx.x, w = l >> 6, ntiles = (count + T - 1) / T;
@@ -566,17 +570,17 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
         // CD tiles of V rows and weights in flight, ring slot = tile mod CD
         CombineItem ring[CD];
 #pragma unroll
-        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, j);
+        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, j);
         float *pb = prod + 8 * dg * S + 4 * tq;
         combine_store<T, S>(pb, ring[0], 0, count, tq);
-        ring[0] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, CD);
+        ring[0] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, CD);
         __syncthreads();
         for (int i0 = 0; i0 < nit; i0 += CD) {
 #pragma unroll
             for (int j = 0; j < CD; j++) {
                 const int i = i0 + j, r = (j + 1) % CD;
                 combine_store<T, S>(pb + ((j + 1) & 1) * (D::DH * S), ring[r], i + 1, count, tq);
-                ring[r] = combine_fetch<HD, T>(a, pgs, ev, count, from, kvh, d0, dg, tq, i + 1 + CD);
+                ring[r] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, i + 1 + CD);
                 __syncthreads();
             }
         }
@@ -595,7 +599,7 @@ DEV void combine_body(const cj_attn_args &a) {
     attn_window(a, count, from);
     const int h = blockIdx.x / D::NSPLIT, d0 = D::DH * (blockIdx.x % D::NSPLIT), l = threadIdx.x;
     const int grp = a.n_q / a.n_kv, kvh = h / grp;
-    float *sc = a.part + (int64_t)h * a.splits;
+    const float *sc = a.part + (int64_t)h * a.splits;
     const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
     // the page entries and the first round of scores are requested together
     // (one memory round trip); lane l < 128 takes positions l + 128k
@@ -643,8 +647,9 @@ DEV void combine_body(const cj_attn_args &a) {
             vst[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j);
         }
     }
-    // e_t in order per lane; kept in LDS when the span fits, else written
-    // over the scores
+    // e_t in order per lane; kept in LDS when the span fits, else formed
+    // again from the scores where p·V needs it (the score row is shared by
+    // the head's HD/32 workgroups and stays read-only)
     const bool elds = count <= COMBINE_ES;
     float s = 0.0f;
     if (l < 128) {
@@ -654,7 +659,6 @@ DEV void combine_body(const cj_attn_args &a) {
             if (t < count) {
                 const float e = cj_expf(v[k] - m);
                 if (elds) es[t] = e;
-                else sc[t] = e;
                 s = __fadd_rn(s, e);
             }
         }
@@ -667,7 +671,6 @@ DEV void combine_body(const cj_attn_args &a) {
                 const int t = base + l + 128 * k;
                 if (t < count) {
                     const float e = cj_expf(u[k] - m);
-                    sc[t] = e;
                     s = __fadd_rn(s, e);
                 }
             }
@@ -714,9 +717,9 @@ DEV void combine_body(const cj_attn_args &a) {
     // short spans (the sliding windows, early positions) take a two-tile
     // ring, so few rounds are padded
     const int ntiles = (count + D::T - 1) / D::T;
-    const float acc = !elds ? combine_pv<HD, 6>(a, pgs, sc, prod, count, from, kvh, d0)
-                      : ntiles <= 4 ? combine_pv<HD, 2>(a, pgs, es, prod, count, from, kvh, d0)
-                                    : combine_pv<HD, 6>(a, pgs, es, prod, count, from, kvh, d0);
+    const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0)
+                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0)
+                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0);
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 

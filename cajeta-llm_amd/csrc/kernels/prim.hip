@@ -281,6 +281,12 @@ extern "C" __global__ void __launch_bounds__(256) cj_prepare(cj_prepare_args a) 
 // the token comes from the device token history at the step position.
 extern "C" __global__ void __launch_bounds__(256) cj_embed(cj_embed_args a) {
     const int token = a.tokens ? a.tokens[step_pos(a.state, a.token)] : a.token;
+    if (a.vocab > 0 && (token < 0 || token >= a.vocab)) {
+        // an id read from device memory that names no row: no read past the table
+        for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.hidden; e += (int64_t)gridDim.x * 256) a.out[e] = 0.0f;
+        if (a.status && blockIdx.x == 0 && threadIdx.x == 0) a.status[0] = 1;
+        return;
+    }
     const uint8_t *row = a.table + (int64_t)token * a.row_bytes;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.hidden; e += (int64_t)gridDim.x * 256)
         a.out[e] = decode_file(a.type, row, e);
@@ -425,7 +431,15 @@ extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
             const int oi = __shfl_xor(bi, m);
             if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
         }
-        if (bi < 0) { bi = 0; bv = 0.0f; }   // non-finite logits; the host checks the weights
+        if (bi < 0) {
+            // every probability failed >= 0: the logits are not finite. The
+            // reference refuses the row by name; here the status word says
+            // so (the host raises after the step) and expert 0 keeps every
+            // later index in bounds
+            bi = 0;
+            bv = 0.0f;
+            if (t == 0 && a.status) a.status[0] = 1;
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++)
             if (t + 64 * j == bi) v[j] = -1.0f;
@@ -439,6 +453,8 @@ extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
             if (ws < 0.00006103515625f) ws = 0.00006103515625f;
             for (int k = 0; k < a.n_used; k++) w_s[k] = __fdiv_rn(w_s[k], ws);
         }
+        if (a.w_scale != 0.0f && a.w_scale != 1.0f)
+            for (int k = 0; k < a.n_used; k++) w_s[k] = __fmul_rn(w_s[k], a.w_scale);
     }
     __syncthreads();
     if (t < a.n_used) {

@@ -55,12 +55,17 @@ struct Seq {
     int fixed_until = 0;
 };
 
+// A request of the scheduler (sched/Request.cajeta): its ids (prompt, then
+// generated), how many positions the model has consumed, and its state.
 struct Request {
-    int id = 0;
-    std::vector<int32_t> prompt, out;
-    int max_new = 0;
-    bool done = false;
-    int reason = 0;
+    enum { WAITING = 0, RUNNING = 1, DONE = 2 };
+    // Request.FINISH_* (sched/Request.cajeta:18-23)
+    enum { FINISH_NONE = 0, FINISH_BUDGET = 1, FINISH_EOS = 2, FINISH_CANCEL = 4 };
+    std::vector<int32_t> all;     // prompt then generated ids (Request.all)
+    std::vector<int32_t> stops;   // stop tokens: the model's EOG set unless the caller gave its own
+    int prompt_len = 0, max_new = 0, gen = 0;
+    int cached = 0;               // positions the model has consumed (Request.cachedLen)
+    int state = WAITING, slot = -1, finish = FINISH_NONE;
 };
 
 // The launches of one decode step, by kind (the timing seam addresses one).
@@ -77,6 +82,8 @@ struct Engine {
     Gguf file;
     int n_layers = 0, hidden = 0, n_heads = 0, n_kv = 0, head_dim = 0, ffn = 0, vocab = 0, ctx = 0, max_seqs = 1;
     int n_experts = 0, n_used = 0, expert_ffn = 0, norm_topk = 1;
+    float w_scale = 0.0f;      // expert_weights_scale (0: none)
+    int32_t *route_status = nullptr;   // set by the router when a row's logits are not finite
     float eps = 1e-5f, theta = 10000.0f, scale = 1.0f;
     int wtype = 0, head_type = 0, embd_type = 0;
     int64_t embd_row_bytes = 0;
@@ -98,8 +105,9 @@ struct Engine {
     int32_t *moe_sel = nullptr;
     std::vector<Seq> seqs;
     std::set<int> eog;
-    std::deque<int> queue;
     std::vector<Request> reqs;
+    std::vector<int> slot_req;   // the request in each sequence slot, or -1 (Scheduler.slotReq)
+    int64_t sched_steps = 0;
     float last_step_us = 0.0f;
     std::vector<void *> owned;
     int only = -1;             // enqueue only this kind, of layer only_layer (-1: the whole step)
@@ -120,8 +128,8 @@ struct Engine {
     int32_t *r_pi = nullptr, *r_tab_pf = nullptr, *r_tab_b = nullptr;
     uint8_t *r_xp = nullptr, *r_ap = nullptr, *r_actp = nullptr;
     int32_t *pinned_tab = nullptr;             // pinned staging of a row table
-    std::vector<int> batch_slots;              // the slots the batch graph was captured for
-    hipGraphExec_t batch_graph = nullptr;
+    int batch_rows = 0;                        // rows of the last batched decode step
+    std::vector<hipGraphExec_t> batch_graphs;  // [n]: the batched step of n rows (the row table is read at replay)
 
     bool want(int kind, int l) const {
         return only < 0 || (only == kind && l == (kind == K_EMBED || kind == K_HEAD ? 0 : only_layer));
@@ -135,7 +143,8 @@ struct Engine {
     ~Engine() {
         for (auto &s : seqs)
             if (s.graph) (void)hipGraphExecDestroy(s.graph);
-        if (batch_graph) (void)hipGraphExecDestroy(batch_graph);
+        for (auto &g : batch_graphs)
+            if (g) (void)hipGraphExecDestroy(g);
         (void)hipStreamSynchronize(stream());
         for (void *p : owned) dev_free(p);
         if (pinned) (void)hipHostFree(pinned);
@@ -159,7 +168,13 @@ struct Engine {
     int prefill(int s, const int32_t *toks, int n);
     int decode(int s, int steps, int32_t *out);
     int reset(int s);
-    int run_request(Request &r, int max_steps);
+    int check_route();
+    // the scheduler (sched/Scheduler.cajeta)
+    int submit(const int32_t *prompt, int n, int max_new, const int32_t *stops, int n_stops);
+    int admit();
+    void retire(Request &r, int finish);
+    void consume(Request &r, int32_t tok);
+    int step_once();
     int64_t kind_bytes(int kind, int count) const;
     int64_t step_bytes(int count) const;
     int time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel);
@@ -211,12 +226,17 @@ int Engine::fuse_rows(const std::vector<std::string> &names, DevW &w, bool inter
             return fail(CJ_ERR_IO, "model: %s and %s differ in type; the fused route needs one", names[0].c_str(), names[i].c_str());
     }
     const int64_t rb = parts[0].row_bytes;
+    const int64_t E = experts > 0 ? experts : 1;
+    if (interleave)
+        for (size_t i = 0; i < parts.size(); i++)
+            if (rows_each <= 0 || parts[i].rows != E * rows_each)   // the row copies below read E·rows_each rows of each part
+                return fail(CJ_ERR_IO, "model: %s has %lld rows, expected %lld (%lld experts x %lld)", names[i].c_str(),
+                            (long long)parts[i].rows, (long long)(E * rows_each), (long long)E, (long long)rows_each);
     int64_t total = 0;
     for (auto &p : parts) total += p.rows;
     w.type = parts[0].type; w.cols = parts[0].cols; w.row_bytes = rb; w.rows = total;
     w.p = alloc((size_t)(total * rb));
     if (!w.p) return fail(CJ_ERR_HIP, "model: out of device memory fusing %s", names[0].c_str());
-    const int64_t E = experts > 0 ? experts : 1;
     if (!interleave) {
         int64_t off = 0;
         for (auto &p : parts) {
@@ -263,9 +283,23 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     n_used = (int)file.get_int(kp + "expert_used_count", 0);
     expert_ffn = (int)file.get_int(kp + "expert_feed_forward_length", ffn);
     norm_topk = (int)file.get_int(kp + "expert_weights_norm", 1);
+    w_scale = (float)file.get_float(kp + "expert_weights_scale", 0.0);
+    if (n_experts > 0) {
+        // only softmax gating has a witness in the reference (MoeFfn ctor,
+        // model/MoeFfn.cajeta:417-432): anything else is refused by name
+        const int64_t gating = file.get_int(kp + "expert_gating_func", 1);
+        if (gating != 1)
+            return fail(CJ_ERR_IO, "moe: expert_gating_func %lld%s is not served; only softmax (1) is", (long long)gating,
+                        gating == 2 ? " (sigmoid)" : "");
+    }
     if (n_experts < 0 || n_experts > 256 || (n_experts > 0 && (n_used <= 0 || n_used > 16 || n_used > n_experts)))
         return fail(CJ_ERR_IO, "model: %d experts, %d used (served: up to 256, 1..16 used)", n_experts, n_used);
     const int swa = (int)file.get_int(kp + "attention.sliding_window", 0);
+    // every swa_pattern-th layer attends every position, (l + 1) % P == 0
+    // (ModelConfig.gemma3Gguf, model/ModelConfig.cajeta:570-576); gpt-oss
+    // alternates, so 2 where the key is absent
+    const int swa_pattern = (int)file.get_int(kp + "attention.sliding_window_pattern", 2);
+    if (swa > 0 && swa_pattern <= 0) return fail(CJ_ERR_IO, "model: sliding_window_pattern %d", swa_pattern);
     const GgufTensor *te = file.tensor("token_embd.weight");
     if (!te) return fail(CJ_ERR_IO, "model: token_embd.weight is missing");
     vocab = (int)file.get_int(kp + "vocab_size", te->rows());
@@ -321,7 +355,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
             if ((rc = fuse_rows({lname(l, "ffn_gate.weight"), lname(l, "ffn_up.weight")}, L.gu, true, ffn, 0))) return rc;
             if ((rc = upload_weight(lname(l, "ffn_down.weight"), L.down, hidden, ffn))) return rc;
         }
-        L.window = (swa > 0 && (l % 2) == 0) ? swa : 0;
+        L.window = (swa > 0 && ((l + 1) % swa_pattern) != 0) ? swa : 0;
         L.kc = (uint16_t *)alloc((size_t)plane);
         L.vc = (uint16_t *)alloc((size_t)plane);
         if (!L.kc || !L.vc) return fail(CJ_ERR_HIP, "model: out of device memory for the K/V planes");
@@ -364,13 +398,15 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     moe_logits = (float *)alloc((size_t)std::max(1, n_experts) * 4 + 64);
     moe_w = (float *)alloc(64 * 4);
     moe_sel = (int32_t *)alloc(64 * 4);
+    route_status = (int32_t *)alloc(64);
     moe_y = (float *)alloc((size_t)hidden * std::max(1, n_used) * 4);
     if (!hs || !q || !attn || !act || !act_pack || !attn_pack || !xpack || !xn || !logits || !part || !glu_counters || !argmax_counter ||
-        !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y)
+        !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y || !route_status)
         return fail(CJ_ERR_HIP, "model: out of device memory (scratch)");
     CJ_HIP(hipMemset(glu_counters, 0, (size_t)fpad / 256 * 4 + 64));
     CJ_HIP(hipMemset(argmax_counter, 0, 64));
     CJ_HIP(hipMemset(attn_counters, 0, (size_t)n_kv * 4 + 64));
+    CJ_HIP(hipMemset(route_status, 0, 64));
 
     if (hipHostMalloc((void **)&pinned, (size_t)(ctx + 2) * 4 + sizeof(cj_step_state) + 64, 0) != hipSuccess)
         return fail(CJ_ERR_HIP, "model: pinned staging buffer");
@@ -385,6 +421,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     CJ_HIP(hipMemset(preds_all, 0, hist * max_seqs * 4));
     CJ_HIP(hipMemset(states, 0, sizeof(cj_step_state) * (size_t)max_seqs));
     seqs.resize(max_seqs);
+    slot_req.assign((size_t)max_seqs, -1);
+    batch_graphs.assign((size_t)max_seqs + 1, nullptr);
     for (int s = 0; s < max_seqs; s++) {
         Seq &S = seqs[s];
         S.tokens = tokens_all + hist * s;
@@ -544,7 +582,7 @@ int Engine::enqueue_step(int s) {
                 if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
             }
             if (want(K_ROUTE, l)) {
-                cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1};
+                cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1, w_scale, 0, route_status};
                 if ((rc = launch("cj_moe_route", 1, 64, 0, a))) return rc;
             }
             if (want(K_EXP_GATE_UP, l)) {   // the selected experts' gate|up, SiLU·up into act[k]
@@ -817,14 +855,14 @@ int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
         }
         return CJ_OK;
     }
-    const std::vector<int> want(slots, slots + n);
-    if (want != batch_slots) {
-        if (batch_graph) { (void)hipGraphExecDestroy(batch_graph); batch_graph = nullptr; }
-        CJ_HIP(hipStreamSynchronize(stream()));
-        for (int r = 0; r < n; r++) { pinned_tab[2 * r] = slots[r]; pinned_tab[2 * r + 1] = 0; }
-        CJ_HIP(hipMemcpy(r_tab_b, pinned_tab, (size_t)n * 8, hipMemcpyHostToDevice));
-        batch_slots = want;
-    }
+    // the row table names each row's slot; the graphs read it at replay, so
+    // a new set of slots (admissions, retirements) reuses the graph of its
+    // row count instead of capturing again
+    CJ_HIP(hipStreamSynchronize(stream()));   // the staging and the table are free again
+    for (int r = 0; r < n; r++) { pinned_tab[2 * r] = slots[r]; pinned_tab[2 * r + 1] = 0; }
+    CJ_HIP(hipMemcpyAsync(r_tab_b, pinned_tab, (size_t)n * 8, hipMemcpyHostToDevice, stream()));
+    batch_rows = n;
+    hipGraphExec_t &batch_graph = batch_graphs[(size_t)n];
     if (graphs && !batch_graph) {
         CJ_HIP(hipStreamSynchronize(stream()));
         CJ_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal));
@@ -863,6 +901,18 @@ int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
         S.pos += steps;
     }
     return CJ_OK;
+}
+
+// After the stream is drained: an error when the router met a row whose
+// logits are not finite since the last check (the reference throws there,
+// MoeFfn.routeFromLogits, model/MoeFfn.cajeta:945-952). The word is cleared.
+int Engine::check_route() {
+    if (n_experts == 0) return CJ_OK;
+    int32_t st = 0;
+    CJ_HIP(hipMemcpy(&st, route_status, 4, hipMemcpyDeviceToHost));
+    if (!st) return CJ_OK;
+    CJ_HIP(hipMemset(route_status, 0, 4));
+    return fail(CJ_ERR_STATE, "moe router: the logits of a row are not finite (%d experts, top-%d)", n_experts, n_used);
 }
 
 // One decode step of slot s on the stream: the graph, or its launches.
@@ -911,7 +961,7 @@ int Engine::prefill(int s, const int32_t *toks, int n) {
     CJ_HIP(hipStreamSynchronize(stream()));
     S.pos += n;
     S.fixed_until = S.pos;
-    return CJ_OK;
+    return check_route();
 }
 
 int Engine::decode(int s, int steps, int32_t *out) {
@@ -941,7 +991,7 @@ int Engine::decode(int s, int steps, int32_t *out) {
     (void)hipEventDestroy(e1);
     if (out) CJ_HIP(hipMemcpy(out, S.tokens + S.pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost));
     S.pos += steps;
-    return CJ_OK;
+    return check_route();
 }
 
 // Algorithmic HBM bytes of one launch of `kind` (layer 0 shapes) with
@@ -1058,32 +1108,108 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
     return rc;
 }
 
-// One request to completion on slot 0: the prompt teacher-forced, then
-// greedy steps in groups, stopping at an end-of-generation id or max_new
-// (Scheduler.stepPipelined, sched/Scheduler.cajeta:640-676).
-int Engine::run_request(Request &r, int max_steps) {
+// ------------------------------------------------------------ scheduler
+//
+// Continuous batching over the sequence slots (Scheduler.stepOnce,
+// sched/Scheduler.cajeta:414-605): each step admits waiting requests into
+// free slots (FIFO), feeds every running request's pending rows — a prompt
+// chunk of up to the chunk size, or the one newest position of a decoding
+// request, all decoding requests together as one batched step — consumes the
+// greedy token a finished prompt or decode row produced, checks stops per
+// token (stop tokens, then the budget), retires finished requests and admits
+// again into the freed slots. Cancel takes effect between steps.
+
+int Engine::submit(const int32_t *prompt, int n, int max_new, const int32_t *stops, int n_stops) {
+    if (!prompt || n <= 0 || max_new <= 0) return fail(CJ_ERR_ARG, "submit: %d prompt tokens, max_new %d", n, max_new);
+    // the slot must hold the prompt and one decode position (admitPhase's
+    // tryDeviceKvRows(slot, totalLen + 1); nothing can make room for more)
+    if (n + 1 > ctx)
+        return fail(CJ_ERR_CAPACITY, "scheduler: the request needs %d positions of device KV, more than a sequence holds (%d)", n + 1, ctx);
+    for (int i = 0; i < n; i++)
+        if (prompt[i] < 0 || prompt[i] >= vocab) return fail(CJ_ERR_ARG, "submit: token %d outside the vocabulary", prompt[i]);
+    Request r;
+    r.all.assign(prompt, prompt + n);
+    r.prompt_len = n;
+    r.max_new = max_new;
+    // LlmEngine.defaultStops (LlmEngine.cajeta:458-474): the model's EOG set
+    // unless the caller gave stop tokens (an empty list means none)
+    if (n_stops < 0) r.stops.assign(eog.begin(), eog.end());
+    else if (n_stops > 0) r.stops.assign(stops, stops + n_stops);
+    reqs.push_back(std::move(r));
+    return (int)reqs.size() - 1;
+}
+
+int Engine::admit() {
+    for (size_t i = 0; i < reqs.size(); i++) {
+        Request &r = reqs[i];
+        if (r.state != Request::WAITING) continue;
+        int slot = -1;
+        for (int s = 0; s < max_seqs; s++)
+            if (slot_req[(size_t)s] < 0) { slot = s; break; }
+        if (slot < 0) return CJ_OK;
+        int rc = reset(slot);
+        if (rc) return rc;
+        slot_req[(size_t)slot] = (int)i;
+        r.slot = slot;
+        r.cached = 0;
+        r.state = Request::RUNNING;
+    }
+    return CJ_OK;
+}
+
+void Engine::retire(Request &r, int finish) {
+    if (r.slot >= 0) slot_req[(size_t)r.slot] = -1;
+    r.slot = -1;
+    r.state = Request::DONE;
+    r.finish = finish;
+}
+
+// The greedy token the newest consumed position produced (Scheduler.consume,
+// :705-760): appended, then the stops in the reference's order — a stop
+// token, then the budget. A sequence whose slot has no position left for the
+// next step also ends there (as a budget stop).
+void Engine::consume(Request &r, int32_t tok) {
+    r.all.push_back(tok);
+    r.gen++;
+    if (std::find(r.stops.begin(), r.stops.end(), tok) != r.stops.end()) retire(r, Request::FINISH_EOS);
+    else if (r.gen >= r.max_new || (int)r.all.size() > ctx) retire(r, Request::FINISH_BUDGET);
+}
+
+int Engine::step_once() {
+    sched_steps++;
     int rc;
-    if ((rc = reset(0))) return rc;
-    if ((rc = prefill(0, r.prompt.data(), (int)r.prompt.size()))) return rc;
-    Seq &S = seqs[0];
-    int32_t first = 0;
-    CJ_HIP(hipMemcpy(&first, S.tokens + S.pos, 4, hipMemcpyDeviceToHost));
-    r.out.push_back(first);
-    if (eog.count(first)) { r.done = true; r.reason = 1; return CJ_OK; }
-    int budget = max_steps > 0 ? max_steps : (1 << 30);
-    while ((int)r.out.size() < r.max_new && budget > 0) {
-        int want = std::min(8, std::min(r.max_new - (int)r.out.size(), budget));
-        if (S.pos + want > ctx) { r.done = true; r.reason = 0; return CJ_OK; }
-        std::vector<int32_t> got((size_t)want);
-        if ((rc = decode(0, want, got.data()))) return rc;
-        budget -= want;
-        for (int32_t t : got) {
-            r.out.push_back(t);
-            if (eog.count(t)) { r.done = true; r.reason = 1; return CJ_OK; }
+    if ((rc = admit())) return rc;
+    const int cap = rows_ok && chunk > 1 ? chunk : 512;   // prompt rows a request feeds per step
+    std::vector<int> batch;                             // requests decoding one position
+    for (size_t i = 0; i < reqs.size(); i++) {
+        Request &r = reqs[i];
+        if (r.state != Request::RUNNING) continue;
+        const int n = (int)r.all.size() - r.cached;
+        if (n == 1 && r.cached > 0) { batch.push_back((int)i); continue; }
+        const int m = std::min(n, cap);
+        if ((rc = prefill(r.slot, r.all.data() + r.cached, m))) return rc;
+        r.cached += m;
+        if (r.cached == (int)r.all.size()) {
+            // the prompt's last row was consumed: its argmax is the first token
+            int32_t tok = 0;
+            CJ_HIP(hipMemcpy(&tok, seqs[(size_t)r.slot].tokens + seqs[(size_t)r.slot].pos, 4, hipMemcpyDeviceToHost));
+            consume(r, tok);
         }
     }
-    if ((int)r.out.size() >= r.max_new) { r.done = true; r.reason = 0; }
-    return CJ_OK;
+    if (!batch.empty()) {
+        std::vector<int32_t> slots(batch.size()), out(batch.size());
+        for (size_t k = 0; k < batch.size(); k++) slots[k] = reqs[(size_t)batch[k]].slot;
+        if ((rc = decode_batch(slots.data(), (int)slots.size(), 1, out.data()))) return rc;
+        for (size_t k = 0; k < batch.size(); k++) {
+            Request &r = reqs[(size_t)batch[k]];
+            r.cached += 1;
+            consume(r, out[k]);
+        }
+    }
+    if ((rc = admit())) return rc;   // completions freed slots: same-step admission
+    for (auto &r : reqs)
+        if (r.state != Request::DONE) return 1;
+    return 0;
 }
 
 }  // namespace cj
@@ -1100,7 +1226,12 @@ int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs) {
     if (!cj::ready()) return cj::fail(CJ_ERR_STATE, "cj_init has not run"), 0;
     if (!path) return cj::fail(CJ_ERR_ARG, "cj_engine_load: null path"), 0;
     auto *e = new Engine();
-    int rc = e->load((const char *)path, ctx, max_seqs);
+    int rc;
+    try {
+        rc = e->load((const char *)path, ctx, max_seqs);
+    } catch (const std::exception &x) {   // nothing may unwind through the C-ABI
+        rc = cj::fail(CJ_ERR_IO, "model: %s", x.what());
+    }
     if (rc) { std::string m = cj::last_error(); delete e; cj::fail(rc, "%s", m.c_str()); return 0; }
     return (int64_t)(uintptr_t)e;
 }
@@ -1121,60 +1252,53 @@ int32_t cj_engine_config(int64_t h, int64_t *out, int32_t n) {
 
 int32_t cj_engine_submit(int64_t h, const int32_t *prompt, int32_t n, int32_t max_new) {
     Engine *e = eng_of(h);
-    if (!e || !prompt || n <= 0 || max_new <= 0) return cj::fail(CJ_ERR_ARG, "cj_engine_submit: bad arguments");
-    cj::Request r;
-    r.id = (int)e->reqs.size() + 1;
-    r.prompt.assign(prompt, prompt + n);
-    r.max_new = max_new;
-    e->reqs.push_back(r);
-    e->queue.push_back(r.id);
-    return r.id;
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    return e->submit(prompt, n, max_new, nullptr, -1);
+}
+
+int32_t cj_engine_submit_stops(int64_t h, const int32_t *prompt, int32_t n, int32_t max_new, const int32_t *stops,
+                               int32_t n_stops) {
+    Engine *e = eng_of(h);
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    if (n_stops < 0 || (n_stops > 0 && !stops)) return cj::fail(CJ_ERR_ARG, "cj_engine_submit_stops: %d stop tokens", n_stops);
+    return e->submit(prompt, n, max_new, stops, n_stops);
 }
 
 int32_t cj_engine_step_once(int64_t h) {
     Engine *e = eng_of(h);
     if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
-    while (!e->queue.empty()) {
-        cj::Request &r = e->reqs[(size_t)e->queue.front() - 1];
-        e->queue.pop_front();
-        if (r.done) continue;
-        int rc = e->run_request(r, 0);
-        if (rc) return rc;
-        return 1;
-    }
-    return 0;
+    return e->step_once();
 }
 
 int32_t cj_engine_run_all(int64_t h, int32_t max_steps) {
     Engine *e = eng_of(h);
     if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
-    while (!e->queue.empty()) {
-        cj::Request &r = e->reqs[(size_t)e->queue.front() - 1];
-        e->queue.pop_front();
-        if (r.done) continue;
-        int rc = e->run_request(r, max_steps);
-        if (rc) return rc;
+    if (max_steps <= 0) return cj::fail(CJ_ERR_ARG, "runAll: max_steps %d (a positive progress cap)", max_steps);
+    for (int s = 0; s < max_steps; s++) {
+        const int rc = e->step_once();
+        if (rc <= 0) return rc;
     }
-    return CJ_OK;
+    return cj::fail(CJ_ERR_STATE, "scheduler: not done after %d steps", max_steps);
 }
 
-int32_t cj_engine_request(int64_t h, int32_t id, int32_t *tokens, int32_t cap, int32_t *done, int32_t *reason) {
+int32_t cj_engine_request(int64_t h, int32_t id, int32_t *tokens, int32_t cap, int32_t *state, int32_t *finish) {
     Engine *e = eng_of(h);
-    if (!e || id <= 0 || id > (int)e->reqs.size()) return cj::fail(CJ_ERR_ARG, "cj_engine_request: unknown id %d", id);
-    cj::Request &r = e->reqs[(size_t)id - 1];
-    for (int i = 0; i < cap && i < (int)r.out.size(); i++) tokens[i] = r.out[(size_t)i];
-    if (done) *done = r.done ? 1 : 0;
-    if (reason) *reason = r.reason;
-    return (int32_t)r.out.size();
+    if (!e || id < 0 || id >= (int)e->reqs.size()) return cj::fail(CJ_ERR_ARG, "cj_engine_request: unknown id %d", id);
+    const cj::Request &r = e->reqs[(size_t)id];
+    for (int i = 0; i < cap && i < r.gen; i++) tokens[i] = r.all[(size_t)(r.prompt_len + i)];
+    if (state) *state = r.state;
+    if (finish) *finish = r.finish;
+    return (int32_t)r.gen;
 }
 
 int32_t cj_engine_cancel(int64_t h, int32_t id) {
     Engine *e = eng_of(h);
-    if (!e || id <= 0 || id > (int)e->reqs.size()) return cj::fail(CJ_ERR_ARG, "cj_engine_cancel: unknown id %d", id);
-    cj::Request &r = e->reqs[(size_t)id - 1];
-    if (r.done) return 0;
-    r.done = true;
-    r.reason = 2;
+    if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
+    // Scheduler.cancel (:288-315): false for an id never issued or already done
+    if (id < 0 || id >= (int)e->reqs.size()) return 0;
+    cj::Request &r = e->reqs[(size_t)id];
+    if (r.state == cj::Request::DONE) return 0;
+    e->retire(r, cj::Request::FINISH_CANCEL);
     return 1;
 }
 
@@ -1214,7 +1338,8 @@ int32_t cj_engine_set_cpu_threads(int64_t h, int32_t threads) {
     // the captured steps hold the old split rule
     for (auto &sq : e->seqs)
         if (sq.graph) { (void)hipGraphExecDestroy(sq.graph); sq.graph = nullptr; }
-    if (e->batch_graph) { (void)hipGraphExecDestroy(e->batch_graph); e->batch_graph = nullptr; }
+    for (auto &g : e->batch_graphs)
+        if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
     return CJ_OK;
 }
 int32_t cj_engine_set_prefill_chunk(int64_t h, int32_t rows) {
@@ -1253,7 +1378,7 @@ int32_t cj_engine_trace(int64_t h, int32_t what, float *out, int64_t n) {
     case 3: src = e->act; cap = e->ffn; break;
     case 4: src = e->logits; cap = e->vocab; break;
     case 5: src = (const float *)e->act_pack; cap = ((int64_t)e->ffn + 255) / 256 * 80; break;
-    case 6: src = e->r_logits; cap = e->r_logits ? (int64_t)e->batch_slots.size() * e->vocab : 0; break;
+    case 6: src = e->r_logits; cap = e->r_logits ? (int64_t)e->batch_rows * e->vocab : 0; break;
     default: return cj::fail(CJ_ERR_ARG, "cj_engine_trace: unknown tap %d", what);
     }
     if (n > cap) return cj::fail(CJ_ERR_ARG, "cj_engine_trace: %lld > %lld", (long long)n, (long long)cap);

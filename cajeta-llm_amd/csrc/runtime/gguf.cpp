@@ -4,6 +4,7 @@
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
+#include <climits>
 #include <cstring>
 #include <mutex>
 
@@ -26,14 +27,14 @@ struct Rd {
     }
     std::string str() {
         uint64_t len = get<uint64_t>();
-        if (!ok || at + len > n) { ok = false; return {}; }
+        if (!ok || len > n - at) { ok = false; return {}; }   // written so a huge len cannot wrap
         std::string s((const char *)p + at, (size_t)len);
         at += (size_t)len;
         return s;
     }
 };
 
-bool read_value(Rd &r, int type, GgufValue &v) {
+bool read_value(Rd &r, int type, GgufValue &v, int depth = 0) {
     v.type = type;
     switch (type) {
     case 0: v.i = r.get<uint8_t>(); break;
@@ -51,9 +52,10 @@ bool read_value(Rd &r, int type, GgufValue &v) {
     case 9: {
         int et = (int)r.get<uint32_t>();
         uint64_t cnt = r.get<uint64_t>();
+        if (depth >= 4) return false;   // nested arrays: bounded, so a crafted header cannot exhaust the stack
         for (uint64_t k = 0; k < cnt && r.ok; k++) {
             GgufValue e;
-            if (!read_value(r, et, e)) return false;
+            if (!read_value(r, et, e, depth + 1)) return false;
             if (et == 6 || et == 12) v.af.push_back(e.f);
             else if (et != 8) v.ai.push_back(e.i);
         }
@@ -189,7 +191,18 @@ bool Gguf::parse(const uint8_t *p, size_t n, std::map<std::string, GgufValue> &k
         t.name = r.str();
         uint32_t nd = r.get<uint32_t>();
         if (nd > 4) { err = "tensor " + t.name + " has " + std::to_string(nd) + " dims"; return false; }
-        for (uint32_t d = 0; d < nd; d++) t.dims.push_back((int64_t)r.get<uint64_t>());
+        int64_t elems = 1;
+        for (uint32_t d = 0; d < nd; d++) {
+            const uint64_t v = r.get<uint64_t>();
+            // every extent positive, and the element count representable
+            if (r.ok && (v == 0 || v > (uint64_t)INT64_MAX / (uint64_t)elems)) {
+                err = "tensor " + t.name + ": dimension " + std::to_string(d) + " is " + std::to_string(v) +
+                      (v == 0 ? "" : ", which overflows the element count");
+                return false;
+            }
+            elems *= (int64_t)v;
+            t.dims.push_back((int64_t)v);
+        }
         t.type = (int)r.get<uint32_t>();
         t.offset = r.get<uint64_t>();
         tensors_.push_back(std::move(t));
@@ -199,13 +212,20 @@ bool Gguf::parse(const uint8_t *p, size_t n, std::map<std::string, GgufValue> &k
     auto al = kv.find("general.alignment");
     uint64_t align = al != kv.end() ? (uint64_t)al->second.i : 32;
     if (align == 0) align = 32;
+    if (align > (1u << 20)) { err = "general.alignment " + std::to_string(align) + " is not served (at most 1 MiB)"; return false; }
     uint64_t data = (r.at + align - 1) / align * align;
+    if (data > n) { err = "truncated GGUF: no tensor data"; return false; }
     for (size_t i = first; i < tensors_.size(); i++) {
         GgufTensor &t = tensors_[i];
         int64_t rb = ggml_row_bytes(t.type, t.cols());
         if (rb < 0) { err = "tensor " + t.name + ": type " + std::to_string(t.type) + " is not served"; return false; }
+        if (t.dims.empty() || t.rows() > INT64_MAX / rb) { err = "tensor " + t.name + ": byte size overflows"; return false; }
         t.bytes = rb * t.rows();
-        if (data + t.offset + (uint64_t)t.bytes > n) { err = "tensor " + t.name + " runs past the end of the file"; return false; }
+        // written so that no sum can wrap: data <= n is checked above
+        if (t.offset > n - data || (uint64_t)t.bytes > n - data - t.offset) {
+            err = "tensor " + t.name + " runs past the end of the file";
+            return false;
+        }
         t.data = p + data + t.offset;
         if (index_.count(t.name)) { err = "tensor " + t.name + " appears twice"; return false; }
         index_[t.name] = i;

@@ -36,7 +36,11 @@ thread_local bool g_naming = false;         // recording them (until launch_name
 uint64_t g_launches = 0;   // launches made (the timing seam checks a kind launched something)
 
 // The reference's kernel names (KernelCap.nameOf, model/KernelCap.cajeta:100-140
-// and the launch sites) answered by the kernels of this code object.
+// and the launch sites) answered by the kernels of this code object. A name
+// is listed only where the kernel here computes what the named one computes
+// and a parity test covers it; the reference's CPU-backend kernel names and
+// the fused MoE id kernels (whose combine and Q4_K experts this backend does
+// not serve) are answered "no".
 const std::unordered_map<std::string, std::string> &name_map() {
     static const std::unordered_map<std::string, std::string> m = {
         {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_cs_b16"},
@@ -54,24 +58,20 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"qkPrepKernel", "cj_qkprep"},
         {"attnFlashDecodeGqa4Kernel", "cj_attn_split_h128_g4"},
         {"attnFlashDecodeGqa8Kernel", "cj_attn_split_h128_g8"},
-        {"attnDecodeCpuGqaKernel", "cj_attn_split_h128_g4"},
         {"attnScoreKernel", "cj_attn_scores_h64"},
         {"attnCombineKernel", "cj_attn_combine_h64"},
         {"attnReducePackQ8Kernel", "cj_attn_merge"},
         {"attnReducePackQ8BatchKernel", "cj_attn_merge_rows"},
         {"attnFlashDecodeGqa4BatchKernel", "cj_attn_split_rows_h128_g4"},
-        {"attnPrefillCpuGqaKernel", "cj_attn_prefill_h128_g4"},
         {"argmaxRowKernel", "cj_argmax"},
         {"embedRowQ4kKernel", "cj_embed"},
         {"embedRowQ6kKernel", "cj_embed"},
         {"embedRowQ80Kernel", "cj_embed"},
         {"gatherRowsF32Kernel", "cj_embed"},
         {"routerTopKKernel", "cj_moe_route"},
-        {"q4kQ8IdGateUpGluKernel", "cj_gemv_q4k_cg_b16"},
         {"q4kQ8WaveMatVecColsKernel", "cj_gemm_sk_q4k_n1"},
         {"q80Q8X8RowsKernel", "cj_gemm_sk_q80_n1"},
         {"q4kQ8X8RowsKernel", "cj_gemm_sk_q4k_n1"},
-        {"q4kQ8IdDownCombineKernel", "cj_gemv_q4k_cs_b16"},
     };
     return m;
 }
@@ -703,6 +703,24 @@ int32_t cj_embed_row(int64_t out, int64_t table, int32_t type, int64_t hidden, i
     return launch("cj_embed", (uint32_t)((hidden + 255) / 256), 256, 0, a);
 }
 
+int32_t cj_embed_row_slot(int64_t out, int64_t table, int32_t type, int64_t hidden, int32_t vocab, int64_t tokens,
+                          int32_t slot, int64_t status) {
+    const int64_t be = (type == CJ_Q4_K || type == CJ_Q6_K) ? 256 : (type == CJ_F32 || type == CJ_F16) ? 1 : 32;
+    const int64_t bb = type == CJ_F32 ? 4 : type == CJ_F16 ? 2 : type == CJ_Q4_K ? 144 : type == CJ_Q6_K ? 210
+                     : type == CJ_Q8_0 ? 34 : type == CJ_Q4_0 ? 18 : type == CJ_MXFP4 ? 17 : -1;
+    if (bb < 0 || hidden <= 0 || hidden % be || vocab <= 0 || slot < 0)
+        return fail(CJ_ERR_ARG, "cj_embed_row_slot: type %d hidden %lld vocab %d slot %d", type, (long long)hidden, vocab, slot);
+    const int64_t rb = hidden / be * bb;
+    if (!in_buffer(dptr(table), (int64_t)vocab * rb) || !in_buffer(dptr(out), hidden * 4) ||
+        !in_buffer(dptr(tokens + 4 * (int64_t)slot), 4) || (status && !in_buffer(dptr(status), 4)))
+        return fail(CJ_ERR_ARG, "cj_embed_row_slot: a buffer is smaller than its extent");
+    cj_embed_args a{};
+    a.out = (float *)dptr(out); a.table = (const uint8_t *)dptr(table); a.type = type; a.hidden = hidden; a.row_bytes = rb;
+    a.tokens = (const int32_t *)dptr(tokens); a.state = nullptr; a.token = slot; a.vocab = vocab;
+    a.status = status ? (int32_t *)dptr(status) : nullptr;
+    return launch("cj_embed", (uint32_t)((hidden + 255) / 256), 256, 0, a);
+}
+
 int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n) {
     if (n <= 0 || row < 0 || !in_buffer(dptr(tok + 4 * row), 4) || !in_buffer(dptr(v), n * 4))
         return fail(CJ_ERR_ARG, "cj_argmax_row: n %lld row %d", (long long)n, row);
@@ -743,12 +761,14 @@ int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t
     return launch("cj_dequant", (uint32_t)grid, 256, 0, a);
 }
 
-int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts, int32_t n_used, int32_t norm_topk) {
+int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts, int32_t n_used, int32_t norm_topk,
+                     float w_scale, int64_t status) {
     if (rows <= 0 || n_experts <= 0 || n_experts > 256 || n_used <= 0 || n_used > n_experts || n_used > 16 ||
         !in_buffer(dptr(logits), (int64_t)rows * n_experts * 4) || !in_buffer(dptr(sel), (int64_t)rows * n_used * 4) ||
-        !in_buffer(dptr(weights), (int64_t)rows * n_used * 4))
+        !in_buffer(dptr(weights), (int64_t)rows * n_used * 4) || (status && !in_buffer(dptr(status), 4)))
         return fail(CJ_ERR_ARG, "cj_moe_route: rows %d experts %d used %d", rows, n_experts, n_used);
-    cj_route_args a{(const float *)dptr(logits), (int32_t *)dptr(sel), (float *)dptr(weights), n_experts, n_used, norm_topk, rows};
+    cj_route_args a{(const float *)dptr(logits), (int32_t *)dptr(sel), (float *)dptr(weights), n_experts, n_used, norm_topk, rows,
+                    w_scale, 0, status ? (int32_t *)dptr(status) : nullptr};
     return launch("cj_moe_route", (uint32_t)rows, 64, 0, a);
 }
 

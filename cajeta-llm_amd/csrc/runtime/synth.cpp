@@ -373,11 +373,15 @@ int32_t cj_image_free(const int8_t *name) {
 }
 int32_t cj_gguf_info(const int8_t *path, int64_t *n_tensors, int64_t *n_shards) {
     if (!path || !n_tensors || !n_shards) return cj::fail(CJ_ERR_ARG, "cj_gguf_info: null argument");
-    cj::Gguf f;
-    std::string err;
-    if (!f.open((const char *)path, err)) return cj::fail(CJ_ERR_IO, "%s", err.c_str());
-    *n_tensors = (int64_t)f.tensors().size();
-    *n_shards = f.shards();
-    return CJ_OK;
+    try {
+        cj::Gguf f;
+        std::string err;
+        if (!f.open((const char *)path, err)) return cj::fail(CJ_ERR_IO, "%s", err.c_str());
+        *n_tensors = (int64_t)f.tensors().size();
+        *n_shards = f.shards();
+        return CJ_OK;
+    } catch (const std::exception &x) {   // nothing may unwind through the C-ABI
+        return cj::fail(CJ_ERR_IO, "gguf: %s", x.what());
+    }
 }
 }

@@ -44,12 +44,15 @@ class SampleParams:
 
 
 class Request:
-    FINISH_LENGTH, FINISH_EOG, FINISH_CANCEL = 0, 1, 2
+    """A request's state as the scheduler left it (sched/Request.cajeta)."""
+    WAITING, RUNNING, DONE = 0, 1, 2
+    FINISH_NONE, FINISH_BUDGET, FINISH_EOS, FINISH_CANCEL = 0, 1, 2, 4
 
-    def __init__(self, rid, tokens, done, reason):
+    def __init__(self, rid, tokens, state, reason):
         self.id = rid
         self.tokens = tokens
-        self.done = done
+        self.state = state
+        self.done = state == Request.DONE
         self.finishReason = reason
 
     def generatedCount(self):
@@ -124,27 +127,31 @@ class LlmEngine:
         if not params.isGreedy():
             raise LlmException("engine: the MI355X decode path serves greedy sampling only")
         p = np.ascontiguousarray(prompt[: promptLen if promptLen is not None else len(prompt)], dtype=np.int32)
-        if params.stopTokens:
-            self.setEog(params.stopTokens)
-        return check(lib().cj_engine_submit(self.h, ptr(p), int(p.size), int(maxNew)), "submitTokens")
+        if params.stopTokens is None:   # LlmEngine.defaultStops: the model's EOG set
+            return check(lib().cj_engine_submit(self.h, ptr(p), int(p.size), int(maxNew)), "submitTokens")
+        st = np.ascontiguousarray(params.stopTokens, dtype=np.int32)
+        return check(lib().cj_engine_submit_stops(self.h, ptr(p), int(p.size), int(maxNew), ptr(st), int(st.size)),
+                     "submitTokens")
 
     def submitText(self, prompt, params=None, maxNew=16):
         raise LlmException("engine: no tokenizer - load a GGUF or submit token ids")
 
-    def runAll(self, maxSteps=0):
+    def runAll(self, maxSteps=1 << 20):
+        """Step until every request is done; raises past maxSteps (Scheduler.runAll)."""
         check(lib().cj_engine_run_all(self.h, int(maxSteps)), "runAll")
 
     def stepOnce(self):
+        """One scheduler step; True while a request is unfinished."""
         return check(lib().cj_engine_step_once(self.h), "stepOnce") == 1
 
     def request(self, rid):
         cap = 1 << 16
         out = np.zeros(cap, np.int32)
-        done = ctypes.c_int32(0)
+        state = ctypes.c_int32(0)
         reason = ctypes.c_int32(0)
-        n = check(lib().cj_engine_request(self.h, int(rid), ptr(out), cap, ctypes.byref(done), ctypes.byref(reason)),
+        n = check(lib().cj_engine_request(self.h, int(rid), ptr(out), cap, ctypes.byref(state), ctypes.byref(reason)),
                   "request")
-        return Request(rid, out[:n].tolist(), bool(done.value), int(reason.value))
+        return Request(rid, out[:n].tolist(), int(state.value), int(reason.value))
 
     def cancel(self, rid):
         return check(lib().cj_engine_cancel(self.h, int(rid)), "cancel") == 1

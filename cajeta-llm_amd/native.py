@@ -15,6 +15,9 @@ HSACO_PATH = os.path.join(HERE, "kernels.hsaco")
 P, I32, I64, F32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 CP = ctypes.c_char_p
 
+# status codes (include/cajeta_mi355x.h)
+CJ_OK, CJ_ERR_ARG, CJ_ERR_HIP, CJ_ERR_NOKERNEL, CJ_ERR_STATE, CJ_ERR_CAPACITY, CJ_ERR_IO = 0, -1, -2, -3, -4, -5, -6
+
 # name: (restype, argtypes) — one entry per declaration in include/cajeta_mi355x.h
 SIGNATURES = {
     "cj_init": (I32, [I32]),
@@ -53,11 +56,13 @@ SIGNATURES = {
     "cj_embed_row": (I32, [I64, I64, I32, I64, I32]),
     "cj_argmax_row": (I32, [I64, I32, I64, I64]),
     "cj_dequant": (I32, [I64, I64, I32, I64, I64, I32]),
-    "cj_moe_route": (I32, [I64, I64, I64, I32, I32, I32, I32]),
+    "cj_moe_route": (I32, [I64, I64, I64, I32, I32, I32, I32, F32, I64]),
+    "cj_embed_row_slot": (I32, [I64, I64, I32, I64, I32, I64, I32, I64]),
     "cj_engine_load": (I64, [CP, I32, I32]),
     "cj_engine_close": (I32, [I64]),
     "cj_engine_config": (I32, [I64, P, I32]),
     "cj_engine_submit": (I32, [I64, P, I32, I32]),
+    "cj_engine_submit_stops": (I32, [I64, P, I32, I32, P, I32]),
     "cj_engine_run_all": (I32, [I64, I32]),
     "cj_engine_step_once": (I32, [I64]),
     "cj_engine_request": (I32, [I64, I32, P, I32, P, P]),

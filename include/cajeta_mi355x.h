@@ -184,6 +184,15 @@ int32_t cj_attn_merge(int64_t out, int64_t packed, int64_t part, int32_t n_q, in
  * EmbedKernel.embedRowLaunchNoSync (model/EmbedKernel.cajeta:69-265). */
 int32_t cj_embed_row(int64_t out, int64_t table, int32_t type, int64_t hidden, int32_t token);
 
+/* The same with the token id read on the device from the int32 `tokens[slot]`
+ * — the slot the previous step's argmax wrote — so a per-launch route needs
+ * no host round trip: EmbedKernel.embedRowLaunchNoSync(ty, hs, packed, tok,
+ * blocksPerRow) (model/EmbedKernel.cajeta:306-311). The table holds `vocab`
+ * rows; an id outside [0, vocab) writes zeros and sets the int32 at `status`
+ * (a buffer handle, or 0 for none) to 1 instead of reading past the table. */
+int32_t cj_embed_row_slot(int64_t out, int64_t table, int32_t type, int64_t hidden, int32_t vocab, int64_t tokens,
+                          int32_t slot, int64_t status);
+
 /* tok[row] = first-occurrence argmax of v[0..n) (argmaxRowLaunchNoSync,
  * io/QuantKernel.cajeta:41520-41527). */
 int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n);
@@ -193,10 +202,14 @@ int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n);
 int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t cols, int32_t prepared);
 
 /* MoE router selection over `rows` rows of n_experts logits: softmax,
- * top-k by probability (ties to the lower index), optional renormalisation.
- * MoeFfn.routeFromLogits (model/MoeFfn.cajeta:908-960). */
+ * top-k by probability (ties to the lower index), optional renormalisation,
+ * then ×w_scale when w_scale is neither 0 nor 1 (expert_weights_scale).
+ * A row whose logits are not finite sets the int32 at `status` (a buffer
+ * handle, or 0 for none) to 1, where the reference throws
+ * "moe router: the logits of this row are not finite".
+ * MoeFfn.routeFromLogits (model/MoeFfn.cajeta:908-986). */
 int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts,
-                     int32_t n_used, int32_t norm_topk);
+                     int32_t n_used, int32_t norm_topk, float w_scale, int64_t status);
 
 /* ------------------------------------------------------------ engine */
 
@@ -209,15 +222,39 @@ int32_t cj_engine_close(int64_t eng);
  * ctx, n_experts, n_used, weight type, head type, expert ffn, and the CPU
  * worker count the split-K attention rule is evaluated for (512). */
 int32_t cj_engine_config(int64_t eng, int64_t *out, int32_t n);
-/* LlmEngine.submitTokens (:477): a greedy request; returns the request id. */
+/* LlmEngine.submitTokens (:477) → Scheduler.submitSampled (sched/Scheduler.cajeta:267):
+ * a greedy request whose stop tokens are the model's end-of-generation set
+ * (LlmEngine.defaultStops, :458-474); returns its id (0, 1, ... in
+ * submission order). A prompt that cannot fit a sequence slot with one
+ * decode position is refused (CJ_ERR_CAPACITY). */
 int32_t cj_engine_submit(int64_t eng, const int32_t *prompt, int32_t n, int32_t max_new);
-/* LlmEngine.runAll (:500) / stepOnce (:504): drive requests (bounded). */
-int32_t cj_engine_run_all(int64_t eng, int32_t max_steps);
+/* The same with the caller's SampleParams.stopTokens (n_stops >= 0; an empty
+ * list means no stop token). */
+int32_t cj_engine_submit_stops(int64_t eng, const int32_t *prompt, int32_t n, int32_t max_new, const int32_t *stops,
+                               int32_t n_stops);
+/* LlmEngine.stepOnce (:504) → Scheduler.stepOnce (sched/Scheduler.cajeta:414-605):
+ * ONE scheduler step — admit waiting requests into free sequence slots
+ * (FIFO), feed each running request's pending rows (a prompt chunk of up to
+ * the prefill chunk size, or one decode position; every decoding request
+ * together as one batched step), append each produced greedy token, check
+ * its stops (stop token → FINISH_EOS, then the budget → FINISH_BUDGET),
+ * retire finished requests and admit again. Returns 1 while a request is
+ * unfinished, 0 when all are done, < 0 on error. */
 int32_t cj_engine_step_once(int64_t eng);
-/* Request state: writes up to cap generated ids; *done = 1 when finished,
- * *reason 0 length, 1 EOG, 2 cancelled. Returns the generated count. */
-int32_t cj_engine_request(int64_t eng, int32_t id, int32_t *tokens, int32_t cap, int32_t *done, int32_t *reason);
+/* LlmEngine.runAll (:500) → Scheduler.runAll (:1005): stepOnce until every
+ * request is done; CJ_ERR_STATE ("not done after N steps") past max_steps. */
+int32_t cj_engine_run_all(int64_t eng, int32_t max_steps);
+/* LlmEngine.request (:508): writes up to cap generated ids, *state
+ * (0 waiting, 1 running, 2 done) and *finish (Request.FINISH_*: 0 none,
+ * 1 budget, 2 end-of-generation token, 4 cancelled; sched/Request.cajeta:18-23).
+ * Returns the generated count. */
+int32_t cj_engine_request(int64_t eng, int32_t id, int32_t *tokens, int32_t cap, int32_t *state, int32_t *finish);
+/* LlmEngine.cancel (:512) → Scheduler.cancel (:288-315), between steps:
+ * 1 when cancelled (DONE with FINISH_CANCEL, its slot freed), 0 when the id
+ * was never issued or is already done. */
 int32_t cj_engine_cancel(int64_t eng, int32_t id);
+/* The model's end-of-generation set (LlmEngine.eogTokens), which requests
+ * submitted afterwards take as their stop tokens. */
 int32_t cj_engine_set_eog(int64_t eng, const int32_t *ids, int32_t n);
 
 /* CausalLM seam: prefill and free greedy decode of one sequence slot.

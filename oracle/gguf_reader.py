@@ -93,6 +93,8 @@ def model_config(r, workers=512, kv_f32=False, ctx=None, attn_rows=1):
         expert_ffn=int(m.get(kp + "expert_feed_forward_length", m[kp + "feed_forward_length"])),
         swa_window=int(m.get(kp + "attention.sliding_window", 0)),
         attn_rows=int(attn_rows),
+        w_scale=float(m.get(kp + "expert_weights_scale", 0.0)),
+        swa_pattern=int(m.get(kp + "attention.sliding_window_pattern", 2)),
     )
     return cfg
 

@@ -541,10 +541,11 @@ int or_argmax(const float *v, int64_t n) {
     return best;
 }
 
-/* MoeFfn.routeFromLogits (L/model/MoeFfn.cajeta:908-960): full softmax over
+/* MoeFfn.routeFromLogits (L/model/MoeFfn.cajeta:908-986): full softmax over
  * the experts, top-k by probability (strict >, ties keep the lower index),
- * optional renormalisation by the clamped sum. Returns -1 on NaN logits. */
-int or_moe_route(const float *lb, int ne, int k, int norm, int32_t *sel, float *w) {
+ * optional renormalisation by the clamped sum, then the expert_weights_scale
+ * factor when it is neither 0 nor 1. Returns -1 on NaN logits. */
+int or_moe_route(const float *lb, int ne, int k, int norm, float w_scale, int32_t *sel, float *w) {
     float probs[512];
     if (ne > 512) return -2;
     float mx = lb[0];
@@ -555,16 +556,25 @@ int or_moe_route(const float *lb, int ne, int k, int norm, int32_t *sel, float *
     for (int j = 0; j < k; j++) {
         int best = -1; float bp = 0.0f;
         for (int e = 0; e < ne; e++)
+#if OR_PLANT == 11
+            if (probs[e] >= 0.0f && (best < 0 || probs[e] >= bp)) { best = e; bp = probs[e]; }   /* planted: ties keep the higher index */
+#else
             if (probs[e] >= 0.0f && (best < 0 || probs[e] > bp)) { best = e; bp = probs[e]; }
+#endif
         if (best < 0) return -1;
         sel[j] = best; w[j] = bp; probs[best] = -1.0f;
     }
+#if OR_PLANT == 12
+    norm = 0;                                   /* planted: the renormalisation dropped */
+#endif
     if (norm) {
         float ws = 0.0f;
         for (int j = 0; j < k; j++) ws = ws + w[j];
         if (ws < 0.00006103515625f) ws = 0.00006103515625f;
         for (int j = 0; j < k; j++) w[j] = w[j] / ws;
     }
+    if (w_scale != 0.0f && w_scale != 1.0f)
+        for (int j = 0; j < k; j++) w[j] = w[j] * w_scale;
     return 0;
 }
 
@@ -960,7 +970,7 @@ static void moe_ffn(or_model *m, or_layer *L, const float *xn, float *out) {
     int64_t h = m->c.hidden, ef = m->c.expert_ffn;
     float lg[512]; int32_t sel[64]; float w[64];
     or_matvec(L->router.type, L->router.data, ne, h, NULL, xn, lg);
-    or_moe_route(lg, ne, nu, m->c.norm_topk, sel, w);
+    or_moe_route(lg, ne, nu, m->c.norm_topk, m->c.w_scale, sel, w);
     for (int64_t j = 0; j < h; j++) m->acc[j] = 0.0f;
     for (int k = 0; k < nu; k++) {
         int e = sel[k];
@@ -976,6 +986,15 @@ static void moe_ffn(or_model *m, or_layer *L, const float *xn, float *out) {
         for (int64_t j = 0; j < h; j++) m->acc[j] = m->acc[j] + w[k] * m->eo[j];
     }
     memcpy(out, m->acc, sizeof(float) * (size_t)h);
+}
+
+/* The attention window of layer l: the configured window on windowed layers,
+ * 0 (every position) on the global ones. A pattern P makes every P-th layer
+ * global, (l + 1) % P == 0 (ModelConfig.gemma3Gguf,
+ * L/model/ModelConfig.cajeta:570-576); gpt-oss alternates, P = 2. */
+static int layer_window(const or_config *c, int l) {
+    int p = c->swa_pattern > 0 ? c->swa_pattern : 2;
+    return c->swa_window > 0 && ((l + 1) % p) != 0 ? c->swa_window : 0;
 }
 
 /* One decode token through every layer and the tail, in the order
@@ -1001,8 +1020,15 @@ int or_model_step(or_model *m, int token, int pos, float *logits) {
             if (c->kv_f32) { ((float *)m->kc[l])[at] = m->k[i]; ((float *)m->vc[l])[at] = m->v[i]; }
             else { ((uint16_t *)m->kc[l])[at] = or_f32_to_f16(m->k[i]); ((uint16_t *)m->vc[l])[at] = or_f32_to_f16(m->v[i]); }
         }
+        /* the window clamps the range: PagedKvCache.attendRow
+         * (L/model/PagedKvCache.cajeta:380-388), from = p + 1 - w */
         int count = pos + 1, from = 0;
-        if (c->swa_window > 0 && (l % 2) == 0 && count > c->swa_window) { from = count - c->swa_window; count = c->swa_window; }
+        const int win = layer_window(c, l);
+#if OR_PLANT == 13
+        if (win > 0 && count > win) { from = count - win + 1; count = win - 1; }   /* planted: one position short */
+#else
+        if (win > 0 && count > win) { from = count - win; count = win; }
+#endif
         size_t es = c->kv_f32 ? 4 : 2;
         const uint8_t *kb = (const uint8_t *)m->kc[l] + (size_t)from * kvd * es;
         const uint8_t *vb = (const uint8_t *)m->vc[l] + (size_t)from * kvd * es;
@@ -1099,7 +1125,7 @@ int or_model_prefill(or_model *m, const int32_t *tokens, int n, int start, float
                 else { ((uint16_t *)m->kc[l])[at] = or_f32_to_f16(m->k[i]); ((uint16_t *)m->vc[l])[at] = or_f32_to_f16(m->v[i]); }
             }
         }
-        int window = (c->swa_window > 0 && (l % 2) == 0) ? c->swa_window : 0;
+        int window = layer_window(c, l);
         or_prefill_attend(Q, m->kc[l], m->vc[l], c->kv_f32, (int)nh, (int)nkv, (int)hd, start, n, window, scale, AO);
         for (int r = 0; r < n; r++) {
             float *hs = HS + (int64_t)r * h;

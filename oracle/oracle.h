@@ -65,7 +65,7 @@ void  or_inv_freq(int hd, float theta, float *inv);
 void  or_rope(float *t, int nheads, int hd, int pos, const float *inv);
 int   or_argmax(const float *v, int64_t n);
 int   or_moe_route(const float *logits, int n_experts, int n_used, int norm_topk,
-                   int32_t *sel, float *w);
+                   float w_scale, int32_t *sel, float *w);
 void  or_unpermute_rows(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t row_bytes, int n_head);
 
 /* decode attention over an fp16 (or f32) KV plane for ONE layer.
@@ -101,8 +101,10 @@ typedef struct {
     int32_t kv_f32;        /* 1: f32 KV (config-literal), 0: fp16 (resident path) */
     int32_t workers;       /* CPU worker count the attention split choice uses */
     int32_t n_experts, n_used, norm_topk, expert_ffn;
-    int32_t swa_window;    /* >0: layers with (layer % 2 == 0) attend the last swa_window positions */
+    int32_t swa_window;    /* >0: windowed layers (swa_pattern) attend the last swa_window positions */
     int32_t attn_rows;     /* rows of the decode batch the split rule divides the workers over (0: 1) */
+    float   w_scale;       /* expert_weights_scale (0: none) */
+    int32_t swa_pattern;   /* layer l attends every position when (l + 1) % swa_pattern == 0 (<= 0: 2) */
 } or_config;
 
 or_model *or_model_new(const or_config *cfg);

@@ -29,7 +29,8 @@ class Config(ctypes.Structure):
                 ("n_layers", "hidden", "n_heads", "n_kv", "head_dim", "ffn", "vocab", "ctx")] + \
                [("eps", ctypes.c_float), ("theta", ctypes.c_float)] + \
                [(n, ctypes.c_int32) for n in
-                ("kv_f32", "workers", "n_experts", "n_used", "norm_topk", "expert_ffn", "swa_window", "attn_rows")]
+                ("kv_f32", "workers", "n_experts", "n_used", "norm_topk", "expert_ffn", "swa_window", "attn_rows")] + \
+               [("w_scale", ctypes.c_float), ("swa_pattern", ctypes.c_int32)]
 
 
 def load(path):
@@ -68,7 +69,7 @@ def _configure(L):
             "or_rmsnorm": (None, [P, P, I64, F, I32, P]),
             "or_glu_exp": (None, [P, P, I64, P]), "or_glu_tanh": (None, [P, P, I64, P]),
             "or_inv_freq": (None, [I32, F, P]), "or_rope": (None, [P, I32, I32, I32, P]),
-            "or_argmax": (I32, [P, I64]), "or_moe_route": (I32, [P, I32, I32, I32, P, P]),
+            "or_argmax": (I32, [P, I64]), "or_moe_route": (I32, [P, I32, I32, I32, F, P, P]),
             "or_unpermute_rows": (None, [P, P, I64, I64, I32]),
             "or_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, F, I32, P]),
             "or_cpu_decode_splits": (I32, [I32, I32, I32, I32]),
@@ -178,11 +179,11 @@ def argmax(v):
     return lib().or_argmax(_p(v), v.size)
 
 
-def moe_route(logits, k, norm=True):
+def moe_route(logits, k, norm=True, w_scale=0.0):
     logits = np.ascontiguousarray(logits, np.float32)
     sel = np.empty(k, np.int32)
     w = np.empty(k, np.float32)
-    rc = lib().or_moe_route(_p(logits), logits.size, k, int(norm), _p(sel), _p(w))
+    rc = lib().or_moe_route(_p(logits), logits.size, k, int(norm), float(w_scale), _p(sel), _p(w))
     if rc != 0:
         raise ValueError("moe router: logits are not finite")
     return sel, w

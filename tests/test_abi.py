@@ -78,3 +78,46 @@ def test_split_gguf_opens_as_one_model(pkg, tmp_path):
     assert rc != 0
     msg = pkg.native.last_error()
     assert "missing" in msg and "00003-of-00003" in msg, msg
+
+
+def _gguf(kvs=b"", nkv=0, tensors=(), data=b"", align=32):
+    """A GGUF v3 image from raw key/value bytes and (name, dims, type, offset) tensors."""
+    import struct
+    s = lambda x: struct.pack("<Q", len(x)) + x
+    head = struct.pack("<IIQQ", 0x46554747, 3, len(tensors), nkv) + kvs
+    for name, dims, ty, off in tensors:
+        head += s(name.encode()) + struct.pack("<I", len(dims)) + struct.pack("<%dQ" % len(dims), *dims)
+        head += struct.pack("<IQ", ty, off)
+    head += b"\0" * ((-len(head)) % align)
+    return head + data
+
+
+def test_crafted_gguf_headers_are_refused_not_trusted(pkg, tmp_path):
+    """Header values that would wrap an extent check (a huge string length, a
+    huge tensor offset, an element count past int64, a zero dimension,
+    deeply nested arrays) are refused with a message; none reads past the
+    file or unwinds through the C-ABI."""
+    import struct
+    ok = _gguf(tensors=[("t", (32, 2), 0, 0)], data=b"\0" * 256)
+    cases = {
+        "ok": ok,
+        "string length": struct.pack("<IIQQ", 0x46554747, 3, 0, 1) + struct.pack("<Q", 2 ** 64 - 8) + b"key",
+        "tensor offset": _gguf(tensors=[("t", (32, 2), 0, 2 ** 64 - 16)], data=b"\0" * 256),
+        "element count": _gguf(tensors=[("t", (2 ** 40, 2 ** 40), 0, 0)], data=b"\0" * 256),
+        "zero dimension": _gguf(tensors=[("t", (32, 0), 0, 0)], data=b"\0" * 256),
+        "byte size": _gguf(tensors=[("t", (2 ** 61, 2), 0, 0)], data=b"\0" * 256),
+        "past the end": _gguf(tensors=[("t", (64, 2), 0, 0)], data=b"\0" * 256),
+        "nested arrays": _gguf(kvs=struct.pack("<Q", 1) + b"k" + struct.pack("<I", 9)
+                               + b"".join(struct.pack("<IQ", 9, 1) for _ in range(64)) + struct.pack("<IQ", 5, 0),
+                               nkv=1),
+        "alignment": _gguf(kvs=struct.pack("<Q", 17) + b"general.alignment" + struct.pack("<II", 4, 2 ** 31), nkv=1),
+    }
+    for name, blob in cases.items():
+        p = tmp_path / ("%s.gguf" % name.replace(" ", "_"))
+        p.write_bytes(blob)
+        rc, nt, _ = _gguf_info(pkg, str(p))
+        if name == "ok":
+            assert rc == 0 and nt == 1, pkg.native.last_error()
+        else:
+            assert rc == pkg.native.CJ_ERR_IO, (name, rc)
+            assert pkg.native.last_error(), name

@@ -295,7 +295,7 @@ def test_moe_route(gpu, O, ne, k):
     lg = rng.standard_normal((rows, ne)).astype(np.float32)
     lg[2, 3] = lg[2, 5] = 7.0                     # tie: the lower index first
     lb, sb, wb = gpu.Buffer.of(lg), gpu.Buffer(rows * k * 4), gpu.Buffer(rows * k * 4)
-    gpu.native.check(gpu.native.lib().cj_moe_route(sb.h, wb.h, lb.h, rows, ne, k, 1), "route")
+    gpu.native.check(gpu.native.lib().cj_moe_route(sb.h, wb.h, lb.h, rows, ne, k, 1, 0.0, 0), "route")
     sel = sb.download(np.int32, rows * k).reshape(rows, k)
     w = wb.download(np.float32, rows * k).reshape(rows, k)
     for r in range(rows):
@@ -320,6 +320,30 @@ def test_embed_row(gpu, O, ty):
     assert np.array_equal(ob.download(np.float32, hidden).view(np.uint32), ref.view(np.uint32))
 
 
+def test_embed_row_from_a_device_token_slot(gpu, O):
+    """cj_embed_row_slot reads the id the previous argmax left in a device
+    slot (EmbedKernel.embedRowLaunchNoSync); an id naming no row writes zeros
+    and raises the status word instead of reading past the table."""
+    rng = np.random.default_rng(3)
+    hidden, vocab = 512, 40
+    raw = rand_blocks(O, 12, vocab * hidden // 256, rng)
+    tb, ob = gpu.Buffer.of(raw), gpu.Buffer(hidden * 4)
+    toks = gpu.Buffer.of(np.array([5, 33, vocab, -1], np.int32))
+    st = gpu.Buffer.of(np.zeros(1, np.int32))
+    lib = gpu.native.lib()
+    gpu.native.check(lib.cj_embed_row_slot(ob.h, tb.h, 12, hidden, vocab, toks.h, 1, st.h), "embed slot")
+    rb = hidden // 256 * 144
+    ref = O.dequant(12, raw[33 * rb:34 * rb])
+    assert np.array_equal(ob.download(np.float32, hidden).view(np.uint32), ref.view(np.uint32))
+    assert st.download(np.int32, 1)[0] == 0
+    for slot in (2, 3):
+        gpu.native.check(lib.cj_embed_row_slot(ob.h, tb.h, 12, hidden, vocab, toks.h, slot, st.h), "embed slot")
+        assert not ob.download(np.float32, hidden).any()
+        assert st.download(np.int32, 1)[0] == 1
+    # extents: a slot past the token buffer is refused on the host
+    assert lib.cj_embed_row_slot(ob.h, tb.h, 12, hidden, vocab, toks.h, 4, 0) == gpu.native.CJ_ERR_ARG
+
+
 def test_kernel_registry_answers_reference_names(gpu):
     for name in ("q4kQ8WaveMatVecKernel", "q6kQ8WaveMatVecKernel", "q80Q8WaveMatVecKernel", "q8kPackKernel",
                  "rmsnormPackRowF32", "gluPackF32", "qkPrepKernel", "attnFlashDecodeGqa4Kernel",
@@ -327,6 +351,11 @@ def test_kernel_registry_answers_reference_names(gpu):
                  "routerTopKKernel", "mxfp4MatVecKernel"):
         assert gpu.KernelCap.usable(name), name
     assert not gpu.KernelCap.usable("iq2xxsQ8WaveMatVecKernel")
+    # names whose semantics this backend does not serve are refused: the
+    # fused MoE id kernels (their combine, Q4_K experts) and CPU-backend kernels
+    for name in ("q4kQ8IdDownCombineKernel", "q4kQ8IdGateUpGluKernel", "attnDecodeCpuGqaKernel",
+                 "attnPrefillCpuGqaKernel"):
+        assert not gpu.KernelCap.usable(name), name
     gpu.KernelCap.setOverride("q4kQ8WaveMatVecKernel", False)
     assert not gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
     gpu.KernelCap.clearOverrides()

@@ -265,29 +265,83 @@ def test_c5_full_depth_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
-def test_engine_request_surface(gpu):
-    """submitTokens / runAll / request / cancel and an end-of-generation stop."""
-    path = os.path.join(GOLD, "toy-routable.gguf")
-    eng = gpu.LlmEngine.load(gpu.EngineOptions(path))
+def oracle_stream(r, prompt, n_gen, ctx, stops=()):
+    """The oracle's greedy continuation of `prompt`: the prompt through its
+    prefill, then decode steps until n_gen ids or a stop token."""
+    from oracle.gguf_reader import oracle_model
+    om, _ = oracle_model(r, ctx=ctx)
+    t, _ = om.prefill(prompt, 0)
+    toks = [t]
+    while len(toks) < n_gen and t not in stops:
+        t, _ = om.step(toks[-1], len(prompt) + len(toks) - 1)
+        toks.append(t)
+    om.close()
+    return toks
+
+
+def test_scheduler_steps_interleave_requests_like_the_oracle(gpu):
+    """LlmEngine.stepOnce is one scheduler step (Scheduler.stepOnce): with two
+    sequence slots, four requests are admitted FIFO as slots free, decode
+    together in batched steps, stop on their budget or a stop token, and a
+    cancel between steps freezes one; every token stream equals the oracle's
+    greedy continuation of that prompt alone."""
+    from oracle.gguf_reader import GgufReader
+    path = os.path.join(GOLD, "toy-routable-gqa8.gguf")
+    r = GgufReader(path)
+    ctx = 96
+    P = gpu.Request
+    prompts = {"a": [1, 2, 3, 4], "b": [5, 6, 7, 8, 9, 10, 11], "c": [9, 9, 40], "d": [3, 1, 4, 1, 5]}
+    budget = {"a": 10, "b": 6, "c": 8, "d": 12}
+    want = {k: oracle_stream(r, prompts[k], budget[k], ctx) for k in prompts}
+    opts = gpu.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = 2
+    eng = gpu.LlmEngine.load(opts)
     try:
-        a = eng.submitTokens([1, 2, 3, 4], maxNew=10)
-        b = eng.submitTokens([5, 6, 7], maxNew=6)
-        c = eng.submitTokens([9, 9], maxNew=4)
-        assert eng.cancel(c)
-        eng.runAll(0)
-        ra, rb, rc = eng.request(a), eng.request(b), eng.request(c)
-        assert ra.done and len(ra.tokens) == 10 and ra.finishReason == 0
-        assert rb.done and len(rb.tokens) == 6
-        assert rc.finishReason == 2 and rc.tokens == []
-        # stop at the first generated id when it is declared end-of-generation
-        stop = ra.tokens[2]
+        ids = {k: eng.submitTokens(prompts[k], maxNew=budget[k], params=gpu.SampleParams(stopTokens=[]))
+               for k in ("a", "b", "c", "d")}
+        assert [ids[k] for k in "abcd"] == [0, 1, 2, 3]
+        assert eng.request(ids["a"]).state == P.WAITING
+        more, steps, seen_running = True, 0, []
+        while more:
+            more = eng.stepOnce()
+            steps += 1
+            st = {k: eng.request(ids[k]) for k in ids}
+            seen_running.append(sorted(k for k in st if st[k].state == P.RUNNING))
+            if steps == 1:
+                # two slots: a and b admitted, the others wait
+                assert st["a"].state == P.RUNNING and st["b"].state == P.RUNNING
+                assert st["c"].state == P.WAITING and st["d"].state == P.WAITING
+                assert len(st["a"].tokens) == 1 and len(st["b"].tokens) == 1
+            if steps == 3:
+                assert eng.cancel(ids["d"])          # a waiting request never admits
+                assert not eng.cancel(ids["d"])      # already done
+            if steps == 8:
+                assert st["c"].state == P.RUNNING   # admitted in the step b finished
+                assert eng.cancel(ids["a"])          # a running one: frozen where it is
+            assert steps < 200
+        got = {k: eng.request(ids[k]) for k in ids}
+        say("  scheduler: %d steps; running sets %s" % (steps, seen_running))
+        assert got["b"].tokens == want["b"] and got["b"].finishReason == P.FINISH_BUDGET
+        assert got["c"].tokens == want["c"] and got["c"].finishReason == P.FINISH_BUDGET
+        assert got["d"].tokens == [] and got["d"].finishReason == P.FINISH_CANCEL
+        assert got["a"].finishReason == P.FINISH_CANCEL and len(got["a"].tokens) == 8
+        assert got["a"].tokens == want["a"][:8]
+        assert not eng.cancel(99)                    # never issued
+        # a stop token ends the stream on that token (FINISH_EOS)
+        stop = want["a"][3]
+        e = eng.submitTokens(prompts["a"], maxNew=10, params=gpu.SampleParams(stopTokens=[stop]))
+        eng.runAll(100)
+        re_ = eng.request(e)
+        assert re_.finishReason == P.FINISH_EOS and re_.tokens == want["a"][:want["a"].index(stop) + 1]
+        # the model's end-of-generation set is the default stop set
         eng.setEog([stop])
-        d = eng.submitTokens([1, 2, 3, 4], maxNew=10)
-        eng.runAll(0)
-        rd = eng.request(d)
-        first = ra.tokens.index(stop)
-        assert rd.finishReason == 1 and rd.tokens == ra.tokens[:first + 1]
+        f = eng.submitTokens(prompts["a"], maxNew=10)
+        eng.runAll(100)
+        assert eng.request(f).tokens == re_.tokens
         with pytest.raises(gpu.LlmException):
             eng.submitTokens([1, 2], maxNew=2, params=gpu.SampleParams(temperature=0.7))
+        with pytest.raises(gpu.LlmException):
+            eng.submitTokens(list(range(ctx)), maxNew=2)   # no decode position left in a slot
     finally:
         eng.close()

@@ -94,10 +94,13 @@ def check_matvec(O, ty, rows=24, cols=1024, seed=3):
     f32-activation formats): only fp32 accumulation rounding may differ."""
     rng = np.random.default_rng(seed + ty)
     be, bb = O.BLOCK[ty]
-    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    if ty == O.F32:          # the MoE router's plain f32 rows
+        raw = rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+    else:
+        raw = rand_blocks(O, ty, rows * cols // be, rng)
     x = rng.standard_normal(cols).astype(np.float32)
     W = O.dequant(ty, raw).astype(np.float64).reshape(rows, cols)
-    if ty in (O.Q4_0, O.MXFP4):
+    if ty in (O.Q4_0, O.MXFP4, O.F32):
         got = O.matvec(ty, raw, rows, cols, x)
         ref = W @ x.astype(np.float64)
     else:
@@ -262,6 +265,153 @@ def check_reference_cpu_goldens(O):
     return not bad, bad
 
 
+def check_moe_route(O):
+    """MoeFfn.routeFromLogits against float64: softmax over every expert,
+    top-k by probability with ties to the lower index, renormalised by the
+    sum, scaled by expert_weights_scale (neither 0 nor 1); non-finite logits
+    are refused."""
+    bad = []
+    rng = np.random.default_rng(4)
+    for ne, k, scale in ((32, 4, 0.0), (128, 8, 0.0), (32, 4, 2.5)):
+        lg = rng.standard_normal(ne).astype(np.float32)
+        lg[5] = lg[6] = np.float32(lg.max() + 1)          # a tie: the lower index first
+        sel, w = O.moe_route(lg, k, norm=True, w_scale=scale)
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = sorted(range(ne), key=lambda i: (-p[i], i))[:k]
+        want = p[order] / p[order].sum() * (scale if scale else 1.0)
+        if list(sel) != order or rel_err(w, want) > 1e-6:
+            bad.append((ne, k, scale, list(sel), order))
+        _, w1 = O.moe_route(lg, k, norm=True, w_scale=1.0)   # a scale of 1 changes nothing
+        _, w0 = O.moe_route(lg, k, norm=True, w_scale=0.0)
+        if not np.array_equal(w1, w0):
+            bad.append(("scale 1", ne))
+    nan = np.full(8, np.nan, np.float32)
+    try:
+        O.moe_route(nan, 2, norm=True)
+        bad.append("non-finite logits routed")
+    except ValueError:
+        pass
+    return not bad, bad
+
+
+def moe_toy(O, seed=11):
+    """A small gpt-oss-like MoE decoder bound straight into the oracle (no
+    GGUF): 2 layers, hidden 256, 8 query / 2 kv heads of 64, vocab 512, 8
+    experts top-3 (MXFP4 gate/up/down, an f32 router), f32 attention, head
+    and embeddings, f32 norms, an 8-position window on layer 0 (pattern 2).
+    Every product reads f32 activations, so no int8 pack can round one way
+    in f32 and the other in float64: the comparison is of the layer
+    composition at f32 accumulation rounding."""
+    rng = np.random.default_rng(seed)
+    c = dict(n_layers=2, hidden=256, n_heads=8, n_kv=2, head_dim=64, ffn=256, vocab=512, ctx=32, eps=1e-5,
+             theta=10000.0, kv_f32=0, workers=512, n_experts=8, n_used=3, norm_topk=1, expert_ffn=256,
+             swa_window=8, attn_rows=0, w_scale=0.0, swa_pattern=2)
+    H, E, F = c["hidden"], c["n_experts"], c["expert_ffn"]
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv"] * c["head_dim"]
+
+    def mx(rows, cols):
+        raw = rand_blocks(O, O.MXFP4, rows * cols // 32, rng).reshape(-1, 17)
+        raw[:, 0] = rng.integers(118, 121, raw.shape[0])
+        return (O.MXFP4, raw.reshape(-1), rows, cols)
+
+    def f32(rows, cols, scale, base=0.0):
+        v = (base + scale * rng.standard_normal(rows * cols)).astype(np.float32)
+        return (O.F32, v.view(np.uint8), rows, cols)
+
+    t = {"token_embd.weight": f32(c["vocab"], H, 1.0), "output_norm.weight": f32(1, H, 0.05, 1.0),
+         "output.weight": f32(c["vocab"], H, 0.06)}
+    for l in range(c["n_layers"]):
+        p = "blk.%d." % l
+        t.update({p + "attn_norm.weight": f32(1, H, 0.05, 1.0), p + "ffn_norm.weight": f32(1, H, 0.05, 1.0),
+                  p + "attn_q.weight": f32(qd, H, 0.15), p + "attn_k.weight": f32(kvd, H, 0.15),
+                  p + "attn_v.weight": f32(kvd, H, 0.06), p + "attn_output.weight": f32(H, qd, 0.06),
+                  p + "ffn_gate_inp.weight": f32(E, H, 0.3),
+                  p + "ffn_gate_exps.weight": mx(E * F, H), p + "ffn_up_exps.weight": mx(E * F, H),
+                  p + "ffn_down_exps.weight": mx(E * H, F)})
+    return c, t
+
+
+def moe_forward64(O, c, t, toks):
+    """float64 forward of moe_toy's model over `toks` (positions 0..): f16
+    K/V, the window clamp
+    from = p + 1 - w (PagedKvCache.attendRow), routing on f64 probabilities."""
+    H, nh, nkv, hd, eps = c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["eps"]
+    E, K, F = c["n_experts"], c["n_used"], c["expert_ffn"]
+    W = {k: O.dequant(ty, raw).astype(np.float64).reshape(rows, cols) for k, (ty, raw, rows, cols) in t.items()}
+
+    def lin(name, xv):
+        return W[name] @ xv
+
+    def norm(xv, w):
+        return xv / np.sqrt(np.mean(xv * xv) + eps) * w.ravel()
+
+    half = hd // 2
+    invd = c["theta"] ** (-np.arange(half, dtype=np.float64) * 2.0 / hd)
+
+    def rope(v, n, pos):
+        z = v.reshape(n, hd)
+        zc = (z[:, :half] + 1j * z[:, half:]) * np.exp(1j * pos * invd)
+        return np.concatenate([zc.real, zc.imag], 1).ravel()
+
+    kc = [[] for _ in range(c["n_layers"])]
+    vc = [[] for _ in range(c["n_layers"])]
+    out = []
+    for pos, tok in enumerate(toks):
+        hs = W["token_embd.weight"][tok].copy()
+        for l in range(c["n_layers"]):
+            p = "blk.%d." % l
+            xn = norm(hs, W[p + "attn_norm.weight"])
+            q = rope(lin(p + "attn_q.weight", xn), nh, pos)
+            k = rope(lin(p + "attn_k.weight", xn), nkv, pos)
+            v = lin(p + "attn_v.weight", xn)
+            # K/V stored as fp16 of the f32 value the step computes
+            kc[l].append(k.astype(np.float32).astype(np.float16).astype(np.float64))
+            vc[l].append(v.astype(np.float32).astype(np.float16).astype(np.float64))
+            win = c["swa_window"] if (l + 1) % c["swa_pattern"] else 0
+            t0 = pos + 1 - win if win and pos + 1 > win else 0
+            Kk, Vv = np.array(kc[l][t0:]), np.array(vc[l][t0:])
+            ao = np.zeros(nh * hd)
+            for h in range(nh):
+                g = h // (nh // nkv)
+                sc = Kk[:, g * hd:(g + 1) * hd] @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
+                pr = np.exp(sc - sc.max())
+                ao[h * hd:(h + 1) * hd] = (pr / pr.sum()) @ Vv[:, g * hd:(g + 1) * hd]
+            hs = hs + lin(p + "attn_output.weight", ao)
+            xn = norm(hs, W[p + "ffn_norm.weight"])
+            lg = W[p + "ffn_gate_inp.weight"] @ xn
+            pr = np.exp(lg - lg.max())
+            pr /= pr.sum()
+            sel = sorted(range(E), key=lambda i: (-pr[i], i))[:K]
+            wts = pr[sel] / pr[sel].sum()
+            y = np.zeros(H)
+            for e, we in zip(sel, wts):
+                gg = W[p + "ffn_gate_exps.weight"][e * F:(e + 1) * F] @ xn
+                uu = W[p + "ffn_up_exps.weight"][e * F:(e + 1) * F] @ xn
+                y += we * (W[p + "ffn_down_exps.weight"][e * H:(e + 1) * H] @ (gg / (1 + np.exp(-gg)) * uu))
+            hs = hs + y
+        out.append(lin("output.weight", norm(hs, W["output_norm.weight"])))
+    return out
+
+
+def check_moe_model(O):
+    """The oracle's whole MoE decode step (router, top-k, renormalisation,
+    MXFP4 experts, SiLU·up, down, weighted combine, a sliding window on
+    alternate layers) against moe_forward64, past the window's length."""
+    c, t = moe_toy(O)
+    m = O.Model(c)
+    for name, (ty, raw, rows, cols) in t.items():
+        m.bind(name, ty, raw, rows, cols)
+    toks = [3, 141, 59, 26, 5, 77, 200, 13, 9, 300, 42, 7, 99, 1]
+    ref = moe_forward64(O, c, t, toks)
+    worst = 0.0
+    for pos, tok in enumerate(toks):
+        _, lg = m.step(tok, pos)
+        worst = max(worst, float(np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))))
+    m.close()
+    return worst < 1e-4, worst
+
+
 def check_unpermute(O):
     """Checkpoint.unpermuteRows undoes the GGUF llama q/k row permutation:
     HF row (h, a, b) sits at GGUF row (h, b, a) — built here by reshape."""
@@ -329,7 +479,7 @@ def test_pack_closed_form(O, per32):
     assert np.max(np.abs(unpack(O, rp, 700, per32) - r)) <= step * 0.5000001
 
 
-@pytest.mark.parametrize("ty", [8, 2, 12, 14, 39])
+@pytest.mark.parametrize("ty", [8, 2, 12, 14, 39, 0])
 def test_matvec_against_float64(O, ty):
     ok, e = check_matvec(O, ty)
     assert ok, e
@@ -471,17 +621,42 @@ def test_decode_splits_closed_form(O):
 
 
 def test_moe_route_against_float64(O):
-    rng = np.random.default_rng(4)
-    for ne, k in ((32, 4), (128, 8)):
-        lg = rng.standard_normal(ne).astype(np.float32)
-        lg[5] = lg[6] = np.float32(lg.max() + 1)          # a tie: the lower index first
-        sel, w = O.moe_route(lg, k, norm=True)
-        p = np.exp(lg.astype(np.float64) - lg.max())
-        p /= p.sum()
-        order = sorted(range(ne), key=lambda i: (-p[i], i))[:k]
-        assert list(sel) == order
-        assert abs(float(np.sum(w)) - 1.0) < 1e-6
-        assert rel_err(w, p[order] / p[order].sum()) < 1e-6
+    ok, bad = check_moe_route(O)
+    assert ok, bad
+
+
+def test_moe_model_forward_against_float64(O):
+    """The MoE layer composition and the sliding window, at model level."""
+    ok, worst = check_moe_model(O)
+    print("moe forward: worst relative logit difference %.3g" % worst)
+    assert ok, worst
+
+
+def test_attention_with_f32_kv_against_float64(O):
+    """The config-literal f32 K/V planes (the reference's non-resident
+    PagedKvCache path) through both decode forms and the prefill attend."""
+    bad = []
+    for nh, nkv, hd, count, mode in ((8, 2, 128, 300, 0), (8, 2, 64, 70, 1)):
+        rng = np.random.default_rng(count)
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        k = rng.standard_normal((count, nkv * hd)).astype(np.float32)
+        v = rng.standard_normal((count, nkv * hd)).astype(np.float32)
+        scale = float(np.float32(1.0 / math.sqrt(hd)))
+        splits = O.cpu_decode_splits(count, 1, nkv, 512) if mode == 0 else 1
+        got = O.attend(q, k, v, nh, nkv, hd, count, splits, scale, mode, kv_f32=True)
+        e = rel_err(got, attention_ref(q, k, v, nh, nkv, hd, count, scale))
+        if e > 2e-5:
+            bad.append((hd, mode, e))
+    rng = np.random.default_rng(5)
+    nh, nkv, hd, start, rows = 8, 2, 128, 10, 12
+    q = rng.standard_normal(rows * nh * hd).astype(np.float32)
+    k = rng.standard_normal((start + rows, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((start + rows, nkv * hd)).astype(np.float32)
+    got = O.prefill_attend(q, k, v, nh, nkv, hd, start, rows, 0, 0.088, kv_f32=True)
+    e = rel_err(got, prefill_ref(q, k, v, nh, nkv, hd, start, rows, 0, 0.088))
+    if e > 2e-5:
+        bad.append(("prefill", e))
+    assert not bad, bad
 
 
 def test_unpermute_rows_inverts_the_gguf_permutation(O):
@@ -589,7 +764,14 @@ PLANTS = {
     8: ("q/k rows unpermuted with the halves swapped", check_unpermute),
     9: ("prefill scores from one lane partial", check_prefill_attention),
     10: ("QK-norm 32-sums folded from the end", check_reference_cpu_goldens),
+    11: ("router ties keep the higher expert index", check_moe_route),
+    12: ("router weights not renormalised", check_moe_route),
+    13: ("sliding window one position short", check_moe_model),
+    14: ("MoE model without the renormalisation", check_moe_model),
 }
+# 14 is plant 12 again, caught at model level as well (the tie order of plant
+# 11 needs an exact tie, which only check_moe_route constructs)
+PLANT_DEFINE = {14: 12}
 
 
 @pytest.mark.parametrize("plant", sorted(PLANTS))
@@ -597,7 +779,8 @@ def test_planted_mistakes_are_caught(O, tmp_path, plant):
     what, check = PLANTS[plant]
     so = str(tmp_path / ("liboracle_plant%d.so" % plant))
     subprocess.check_call(["gcc", "-O2", "-std=gnu11", "-fPIC", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
-                           "-DOR_PLANT=%d" % plant, "-shared", "-o", so, os.path.join(ROOT, "oracle", "oracle.c"), "-lm"])
+                           "-DOR_PLANT=%d" % PLANT_DEFINE.get(plant, plant), "-shared", "-o", so,
+                           os.path.join(ROOT, "oracle", "oracle.c"), "-lm"])
     assert check(O)[0], "the check must pass on the real oracle first"
     prev = O.use(O.load(so))
     try:
