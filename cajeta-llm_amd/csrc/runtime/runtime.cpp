@@ -14,6 +14,16 @@
 #include <unordered_map>
 #include <vector>
 
+// The scratch of cj_argmax_row_noalloc: the per-workgroup (value, index)
+// partials and the ticket counter of the argmax kernel, in one file-scope
+// device array so that entry point allocates nothing. Every GPU the library
+// runs on holds its own copy until the process ends; host code reaches it
+// only through the per-device address hipGetSymbolAddress returns (the
+// array's name is a host-side stand-in, not a device address).
+#define CJ_NOALLOC_ARGMAX_MAX (1 << 22)                    // values a row may hold
+#define CJ_NOALLOC_GROUPS (CJ_NOALLOC_ARGMAX_MAX / 1024)   // workgroups of 1024 values
+static __device__ __align__(256) uint8_t scratch[CJ_NOALLOC_GROUPS * 8 + 256];
+
 namespace cj {
 
 namespace {
@@ -27,6 +37,7 @@ struct Ctx {
     int cus = 0;
     int64_t hbm = 0;
     int64_t lds = 0;
+    std::map<int, void *> scratch_at;   // device → address of `scratch` on it
 };
 Ctx g;
 thread_local std::string g_err;
@@ -133,6 +144,24 @@ void dev_free(void *p) {
 }
 
 bool has_kernel(const char *name) { return g.fns.count(name) != 0; }
+
+// The address of `scratch` on the current device, resolved once per device
+// with that device current; its counter word is zeroed then (the argmax
+// kernel leaves it zero after every launch).
+int scratch_here(void **out) {
+    int dev = -1;
+    CJ_HIP(hipGetDevice(&dev));
+    auto it = g.scratch_at.find(dev);
+    if (it != g.scratch_at.end()) { *out = it->second; return CJ_OK; }
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(CJ_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    CJ_HIP(hipMemset(p, 0, sizeof(scratch)));
+    CJ_HIP(hipDeviceSynchronize());
+    g.scratch_at[dev] = p;
+    *out = p;
+    return CJ_OK;
+}
 
 int launch_raw(const char *name, uint32_t grid, uint32_t block, uint32_t lds, const void *args, size_t size,
                uint32_t grid_y) {
@@ -343,6 +372,9 @@ int32_t cj_init(int32_t device) {
             }
     CJ_HIP(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
     g.device = device;
+    void *sp = nullptr;
+    int rc = scratch_here(&sp);   // the allocation-free entry point's scratch, set up with the device current
+    if (rc) return rc;
     return CJ_OK;
 }
 
@@ -740,6 +772,25 @@ int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n) {
     a.pi = (int32_t *)((char *)scratch + scratch_groups * 4); a.counter = (int32_t *)((char *)scratch + scratch_groups * 8);
     a.n = n; a.row = row;
     return launch("cj_argmax", (uint32_t)groups, 256, 0, a);
+}
+
+int32_t cj_argmax_row_noalloc(int64_t tok, int32_t row, int64_t v, int64_t n) {
+    if (!ready()) return fail(CJ_ERR_STATE, "cj_init has not run");
+    if (n <= 0 || n > CJ_NOALLOC_ARGMAX_MAX)
+        return fail(CJ_ERR_ARG, "cj_argmax_row_noalloc: n %lld outside 1..%d (the static scratch's limit)", (long long)n,
+                    CJ_NOALLOC_ARGMAX_MAX);
+    if (row < 0 || !in_buffer(dptr(tok + 4 * (int64_t)row), 4) || !in_buffer(dptr(v), n * 4))
+        return fail(CJ_ERR_ARG, "cj_argmax_row_noalloc: n %lld row %d", (long long)n, row);
+    void *sp = nullptr;
+    int rc = scratch_here(&sp);
+    if (rc) return rc;
+    cj_argmax_args a{};
+    a.tok = (int32_t *)dptr(tok); a.v = (const float *)dptr(v);
+    a.pv = (float *)sp;
+    a.pi = (int32_t *)((char *)sp + CJ_NOALLOC_GROUPS * 4);
+    a.counter = (int32_t *)((char *)sp + CJ_NOALLOC_GROUPS * 8);
+    a.n = n; a.row = row;
+    return launch("cj_argmax", (uint32_t)((n + 1023) / 1024), 256, 0, a);
 }
 
 int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t cols, int32_t prepared) {

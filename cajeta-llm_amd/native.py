@@ -58,6 +58,7 @@ SIGNATURES = {
     "cj_dequant": (I32, [I64, I64, I32, I64, I64, I32]),
     "cj_moe_route": (I32, [I64, I64, I64, I32, I32, I32, I32, F32, I64]),
     "cj_embed_row_slot": (I32, [I64, I64, I32, I64, I32, I64, I32, I64]),
+    "cj_argmax_row_noalloc": (I32, [I64, I32, I64, I64]),
     "cj_engine_load": (I64, [CP, I32, I32]),
     "cj_engine_close": (I32, [I64]),
     "cj_engine_config": (I32, [I64, P, I32]),

@@ -197,6 +197,16 @@ int32_t cj_embed_row_slot(int64_t out, int64_t table, int32_t type, int64_t hidd
  * io/QuantKernel.cajeta:41520-41527). */
 int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n);
 
+/* cj_argmax_row without any allocation: no counterpart in the reference. It
+ * is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * argmax's per-workgroup partials and ticket counter live in a static
+ * 33 KB device array the library holds on each GPU until the process ends,
+ * so n is limited to 4,194,304 values (CJ_ERR_ARG beyond). Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU race. The
+ * result equals cj_argmax_row's (the same kernel). */
+int32_t cj_argmax_row_noalloc(int64_t tok, int32_t row, int64_t v, int64_t n);
+
 /* Dequantize rows·cols elements of a weight, GGUF layout (prepared = 0) or
  * the prepared layout (1). Quant.dequantize (io/Quant.cajeta:693-734). */
 int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t cols, int32_t prepared);
