@@ -9,6 +9,14 @@
 // fp16 bits <-> f32 through the hardware converts (exact / round-to-nearest-even).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));   // a native 16-byte vector
 
+// A 16-byte load of weights a decode step reads once: nontemporal, so the
+// stream does not displace what the caches hold for reuse (measured on
+// MI355X: a 66 MB row stream 12.5 -> 11.4 us).
+DEV uint4 ld_stream16(const uint8_t *p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 DEV float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu))); }
 DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 

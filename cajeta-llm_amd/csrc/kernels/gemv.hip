@@ -58,8 +58,8 @@ struct Q4kBlock { uint4 q[8]; uint4 h; };
 
 DEV void q4k_fetch(Q4kBlock &x, const uint8_t *row, int nb, int b) {
 #pragma unroll
-    for (int c = 0; c < 8; c++) x.q[c] = *(const uint4 *)(row + ((int64_t)c * nb + b) * 16);
-    x.h = *(const uint4 *)(row + (int64_t)nb * 128 + (int64_t)b * 16);
+    for (int c = 0; c < 8; c++) x.q[c] = ld_stream16(row + ((int64_t)c * nb + b) * 16);
+    x.h = ld_stream16(row + (int64_t)nb * 128 + (int64_t)b * 16);
 }
 
 // The activation a lane needs for one block: the 256 int8 codes, the eight
@@ -127,9 +127,9 @@ DEV void terms_q6k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             const uint8_t *row = wr[r];
-            qa[r] = *(const uint4 *)(row + (int64_t)b * 128 + 64 * g + 16 * hl);
-            qb[r] = *(const uint4 *)(row + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
-            qh[r] = *(const uint4 *)(row + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
+            qa[r] = ld_stream16(row + (int64_t)b * 128 + 64 * g + 16 * hl);
+            qb[r] = ld_stream16(row + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
+            qh[r] = ld_stream16(row + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
             sc[r] = *(const uint2 *)(row + (int64_t)nb * 192 + (int64_t)b * 16 + 8 * g);
             dh[r] = *(const uint16_t *)(row + (int64_t)nb * 208 + 2 * b);
         }
@@ -187,8 +187,8 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
         uint32_t dh[NR];
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            w0[r] = *(const uint4 *)(wr[r] + (int64_t)uu * 32);
-            w1[r] = *(const uint4 *)(wr[r] + (int64_t)uu * 32 + 16);
+            w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
+            w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
             dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
         }
         const uint8_t *ab = sx + (uu >> 3) * 320;
@@ -942,7 +942,13 @@ DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PR
 // pack run while the weight stream is in flight. The block terms go to LDS;
 // thread t then folds row t's in block order, acc = (acc + A_b) − B_b
 // (Quant.q4kMatVecIntoQ8), and runs the epilogue.
-template <int LPR, int PRO, int RND, int EPI, int RING>
+// IT > 0: the workgroup's items a lane are exactly IT (the planner's
+// choice), and the item loop is fully unrolled with every weight load
+// unconditional (clamped addresses): the compiler then knows at each use
+// exactly which loads are younger, and waits only for the item it consumes
+// — in the runtime loop (IT = 0) its waits are conservative and the ring
+// drains to one item in flight.
+template <int LPR, int PRO, int RND, int EPI, int RING, int IT = 0>
 DEV void gemv_q4k_body(const cj_gemv_args &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *red = (float *)smem;
@@ -958,7 +964,7 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
     constexpr int RG = 64 / LPR;                 // rows a wave covers in one pass
     const int rg = lane / LPR, li = lane % LPR;
     const int K = (nb + LPR - 1) / LPR;          // items a pass (the last may leave lanes idle)
-    const int items = (R / (4 * RG)) * K;        // R is a multiple of 4·RG
+    const int items = IT > 0 ? IT : (R / (4 * RG)) * K;   // R is a multiple of 4·RG
     auto row_of = [&](int it) { return (it / K) * (4 * RG) + wave * RG + rg; };
     auto blk_of = [&](int it) { return li + LPR * (it % K); };
     auto fetch = [&](Q4kBlock &x, int it) {
@@ -1001,13 +1007,21 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
     __builtin_amdgcn_sched_barrier(0);
     q4k_pro_compute<PRO, RND>(a, px, pw, pxs, ppk, sx, red);
     if (fixed) q4k_act_load(act, sx + min(li, nb - 1) * Q4K_LDS_STRIDE);
-    for (int it0 = 0; it0 < items; it0 += RING) {
+    if constexpr (IT > 0) {
 #pragma unroll
-        for (int j = 0; j < RING; j++) {
-            const int it = it0 + j;
-            if (it < items) {
-                consume(ring[j], it);
-                if (it + RING < items) fetch(ring[j], it + RING);
+        for (int it = 0; it < IT; it++) {
+            consume(ring[it % RING], it);
+            if (it + RING < IT) fetch(ring[it % RING], it + RING);
+        }
+    } else {
+        for (int it0 = 0; it0 < items; it0 += RING) {
+#pragma unroll
+            for (int j = 0; j < RING; j++) {
+                const int it = it0 + j;
+                if (it < items) {
+                    consume(ring[j], it);
+                    if (it + RING < items) fetch(ring[j], it + RING);
+                }
             }
         }
     }
@@ -1079,6 +1093,36 @@ Q4K_EPIS(n, 8, CJ_PRO_NORM_PACK)
     Q4K_KERNEL(cj_gemv_q4k_##P##m_b16_w, 16, PRO, 4, CJ_EPI_ARGMAX)
 Q4K_EPIS_W(c, CJ_PRO_PACKED)
 Q4K_EPIS_W(p, CJ_PRO_PACK)
+// _b64_w: 64 lanes a row for wide rows (56 blocks at 14336 columns: one
+// wave instruction reads 896 contiguous bytes of a row, and each lane keeps
+// one block's activation in registers)
+#define Q4K_EPIS_W64(P, PRO)                                                     \
+    Q4K_KERNEL(cj_gemv_q4k_##P##s_b64_w, 64, PRO, 4, CJ_EPI_STORE)               \
+    Q4K_KERNEL(cj_gemv_q4k_##P##a_b64_w, 64, PRO, 4, CJ_EPI_ACCUM)               \
+    Q4K_KERNEL(cj_gemv_q4k_##P##q_b64_w, 64, PRO, 4, CJ_EPI_QKV_ROPE)            \
+    Q4K_KERNEL(cj_gemv_q4k_##P##g_b64_w, 64, PRO, 4, CJ_EPI_GLU)                 \
+    Q4K_KERNEL(cj_gemv_q4k_##P##m_b64_w, 64, PRO, 4, CJ_EPI_ARGMAX)
+Q4K_EPIS_W64(c, CJ_PRO_PACKED)
+Q4K_EPIS_W64(p, CJ_PRO_PACK)
+// _i<IT>: exactly IT items a lane, fully unrolled (ring min(IT, 3))
+#define Q4KI_KERNEL(NAME, LPR, PRO, RND, EPI, IT) \
+    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) { \
+        gemv_q4k_body<LPR, PRO, RND, EPI, (IT < 3 ? IT : 3), IT>(a); }
+#define Q4KI_EPIS(P, PRO, LPR, SFX, RND, IT)                                                      \
+    Q4KI_KERNEL(cj_gemv_q4k_##P##s_b##LPR##SFX##_i##IT, LPR, PRO, RND, CJ_EPI_STORE, IT)           \
+    Q4KI_KERNEL(cj_gemv_q4k_##P##a_b##LPR##SFX##_i##IT, LPR, PRO, RND, CJ_EPI_ACCUM, IT)           \
+    Q4KI_KERNEL(cj_gemv_q4k_##P##q_b##LPR##SFX##_i##IT, LPR, PRO, RND, CJ_EPI_QKV_ROPE, IT)        \
+    Q4KI_KERNEL(cj_gemv_q4k_##P##g_b##LPR##SFX##_i##IT, LPR, PRO, RND, CJ_EPI_GLU, IT)             \
+    Q4KI_KERNEL(cj_gemv_q4k_##P##m_b##LPR##SFX##_i##IT, LPR, PRO, RND, CJ_EPI_ARGMAX, IT)
+#define Q4KI_ITS(P, PRO)                                                                               \
+    Q4KI_EPIS(P, PRO, 16, , 1, 1) Q4KI_EPIS(P, PRO, 16, , 1, 2) Q4KI_EPIS(P, PRO, 16, , 1, 4)            \
+    Q4KI_EPIS(P, PRO, 16, , 1, 7)
+Q4KI_ITS(c, CJ_PRO_PACKED)
+Q4KI_ITS(p, CJ_PRO_PACK)
+Q4KI_ITS(n, CJ_PRO_NORM_PACK)
+Q4KI_EPIS(c, CJ_PRO_PACKED, 64, _w, 4, 4)
+Q4KI_EPIS(p, CJ_PRO_PACK, 64, _w, 4, 4)
+
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)

@@ -36,6 +36,7 @@ int launch2(const char *name, uint32_t grid_x, uint32_t grid_y, uint32_t block, 
     return launch_raw(name, grid_x, block, lds, &a, sizeof(A), grid_y);
 }
 bool has_kernel(const char *name);
+bool q4k_unrolled();
 
 // GEMV planning shared by the launch seam and the engine.
 struct GemvPlan {

@@ -145,6 +145,13 @@ void dev_free(void *p) {
 
 bool has_kernel(const char *name) { return g.fns.count(name) != 0; }
 
+// Whether Q4_K GEMVs take the fully unrolled forms where built
+// (CJ_Q4K_UNROLL=0 keeps the runtime-loop forms, for comparisons).
+bool q4k_unrolled() {
+    static const bool on = [] { const char *e = getenv("CJ_Q4K_UNROLL"); return !e || strcmp(e, "0") != 0; }();
+    return on;
+}
+
 // The address of `scratch` on the current device, resolved once per device
 // with that device current; its counter word is zeroed then (the argmax
 // kernel leaves it zero after every launch).
@@ -214,7 +221,8 @@ bool gemv_supported(int type, int64_t cols) {
 GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
     GemvPlan p;
     const int64_t nb = cols / 256;
-    const int lpr = nb >= 16 ? 16 : 8;
+    // wide rows (the FFN down projection) take a row a wave
+    const int lpr = nb > 32 && cols > 4096 ? 64 : nb >= 16 ? 16 : 8;
     const int64_t pass = 4 * (64 / lpr);
     // the RMSNorm prologue runs once a workgroup: round up (fewer, longer
     // workgroups); otherwise round down (every CU busy)
@@ -226,7 +234,11 @@ GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
     const char pc = pro == CJ_PRO_PACKED ? 'c' : pro == CJ_PRO_PACK ? 'p' : pro == CJ_PRO_NORM_PACK ? 'n' : '?';
     const char ec = epi == CJ_EPI_STORE ? 's' : epi == CJ_EPI_ACCUM ? 'a' : epi == CJ_EPI_QKV_ROPE ? 'q'
                   : epi == CJ_EPI_GLU ? 'g' : epi == CJ_EPI_ARGMAX ? 'm' : '?';
-    p.kernel = std::string("cj_gemv_q4k_") + pc + ec + (lpr == 16 ? "_b16" : "_b8") + (cols > 4096 ? "_w" : "");
+    p.kernel = std::string("cj_gemv_q4k_") + pc + ec + (lpr == 64 ? "_b64" : lpr == 16 ? "_b16" : "_b8") + (cols > 4096 ? "_w" : "");
+    // the fully unrolled form where one is built for this item count
+    const int64_t K = (nb + lpr - 1) / lpr, items = (R / pass) * K;
+    const std::string unrolled = p.kernel + "_i" + std::to_string(items);
+    if (q4k_unrolled() && has_kernel(unrolled.c_str())) p.kernel = unrolled;
     p.rows_per_wg = (int)R;
     p.grid = (uint32_t)((rows + R - 1) / R);
     p.per_copy = p.grid;
@@ -365,11 +377,12 @@ int32_t cj_init(int32_t device) {
     // the Q4_K family: prologue {c, p, n} × epilogue {s, a, q, g, m} × width
     for (const char *pro : {"c", "p", "n"})
         for (const char *epi : {"s", "a", "q", "g", "m"})
-            for (const char *w : {"_b16", "_b8", "_b16_w"}) {
-                const std::string k = std::string("cj_gemv_q4k_") + pro + epi + w;
-                hipFunction_t f;
-                if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
-            }
+            for (const char *w : {"_b16", "_b8", "_b16_w", "_b64_w"})
+                for (const char *it : {"", "_i1", "_i2", "_i4", "_i7"}) {
+                    const std::string k = std::string("cj_gemv_q4k_") + pro + epi + w + it;
+                    hipFunction_t f;
+                    if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+                }
     CJ_HIP(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
     g.device = device;
     void *sp = nullptr;
