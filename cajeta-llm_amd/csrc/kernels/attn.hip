@@ -911,6 +911,46 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     if (a.packed) pack256(x, a.per32, a.packed + (int64_t)blockIdx.x * 320, bmax);
 }
 
+// The merge as one wave per (query head, 64 output dimensions): lane d
+// merges dimension d over the head's splits in cj_attn_merge's order and
+// writes the f32 output (the consumer packs it). n_q·hd/64 workgroups of 64
+// read the partials in parallel where cj_attn_merge's n_q·hd/256 workgroups
+// each read a quarter megabyte.
+extern "C" __global__ void __launch_bounds__(64) cj_attn_merge_w(cj_merge_args a) {
+    const int lane = threadIdx.x, hd = a.head_dim, per = hd / 64;
+    const int h = blockIdx.x / per, d = (blockIdx.x % per) * 64 + lane;
+    const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
+    float pv[ATTN_MAX_SPLITS];
+#pragma unroll
+    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
+    const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
+    int splits = a.splits;
+    if (a.state) {
+        int count = a.state->pos + 1;
+        if (a.window > 0 && count > a.window) count = a.window;
+        splits = decode_splits(count, a.n_kv, a.workers);
+    }
+    const bool in = lane < splits;
+    const float mv = in ? ml.x : -3.0e38f;
+    const float gm = group_max<64>(mv);
+    const bool on = in && ml.y > 0.0f;
+    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    const uint64_t ons = __ballot(on);
+    float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
+        const float w = lane_f(wt, s2), lv = lane_f(ml.y, s2);
+        const bool use = (ons >> s2) & 1;
+        const float g2 = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lv));
+        const float a2 = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
+        gl[s2 & 3] = use ? g2 : gl[s2 & 3];
+        ac[s2 & 3] = use ? a2 : ac[s2 & 3];
+    }
+    const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
+    const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
+    a.out[(int64_t)h * hd + d] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
+}
+
 // The many-row form: row r's blocks (a row is whole blocks of 256), its
 // partials and split count from the row table, its output and pack at the
 // row strides.

@@ -113,6 +113,9 @@ struct Engine {
     int only = -1;             // enqueue only this kind, of layer only_layer (-1: the whole step)
     int only_layer = 0;
     bool graphs = true;        // replay the captured step (false: enqueue its launches each token)
+    // the split-K merge as a wave per 64 dimensions, f32 out packed by the o
+    // projection (CJ_MERGE_W=0: the 256-wide merge + pack, for comparisons)
+    bool merge_w = [] { const char *e = getenv("CJ_MERGE_W"); return !e || strcmp(e, "0") != 0; }();
     int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
     int64_t embd_row_file_bytes = 0;
     // the many-row path: batched decode (a row a sequence) and prefill
@@ -516,18 +519,23 @@ int Engine::enqueue_step(int s) {
             a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
             a.pg_base = S.pg_base; a.pg_n = pages_per_seq; a.window = L.window; a.scale = scale;
             if (split) {
-                // partials, then the merge + the pack the o projection reads
-                // (a launch boundary orders them: a merge by the last
-                // workgroup of each kv head would need device-scope fences,
-                // which cost far more than the launch on this part)
+                // partials, then the merge (a launch boundary orders them: a
+                // merge by the last workgroup of each kv head would need
+                // device-scope fences, which cost far more than the launch on
+                // this part): a wave per 64 output dimensions writing f32,
+                // which the o projection packs, or the 256-wide merge + pack
                 a.out = nullptr;
                 if (want(K_ATTN, l) && (rc = launch(attn_kernel, (uint32_t)(n_kv * 64), 256, 0, a))) return rc;
                 cj_merge_args m{};
                 m.out = attn; m.packed = attn_pack; m.part = part; m.state = S.state; m.n_q = n_heads;
                 m.head_dim = head_dim; m.per32 = L.o.type == CJ_Q8_0; m.n_kv = n_kv; m.workers = workers;
                 m.window = L.window;
-                if ((rc = launch("cj_attn_merge", (uint32_t)(((int64_t)n_heads * head_dim + 255) / 256), 256, 0, m)))
+                if (merge_w) {
+                    m.packed = nullptr;
+                    if ((rc = launch("cj_attn_merge_w", (uint32_t)(n_heads * (head_dim / 64)), 64, 0, m))) return rc;
+                } else if ((rc = launch("cj_attn_merge", (uint32_t)(((int64_t)n_heads * head_dim + 255) / 256), 256, 0, m))) {
                     return rc;
+                }
             } else if (want(K_ATTN, l)) {
                 a.splits = ctx;
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
@@ -546,7 +554,8 @@ int Engine::enqueue_step(int s) {
         if (want(K_O, l)) {   // 3. o projection, residual into hs
             cj_gemv_args a{};
             a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
-            a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split ? CJ_PRO_PACKED : CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
+            a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split && !merge_w ? CJ_PRO_PACKED : CJ_PRO_PACK;
+            a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
@@ -1005,7 +1014,7 @@ int64_t Engine::kind_bytes(int kind, int count) const {
     case K_EMBED: return embd_row_file_bytes + h * 4;
     case K_QKV: return wb(L.qkv) + ((h + 255) / 256) * 320 + qd * 4 + 2 * kvd * 2;
     case K_ATTN: return (int64_t)count * kvd * 2 * 2 + qd * 8 + ((qd + 255) / 256) * 320;
-    case K_O: return wb(L.o) + ((qd + 255) / 256) * 320 + h * 8;
+    case K_O: return wb(L.o) + (merge_w ? qd * 4 : ((qd + 255) / 256) * 320) + h * 8;
     case K_GATE_UP: return wb(L.gu) + ((h + 255) / 256) * 320 + (int64_t)ffn * 4;
     case K_DOWN: return wb(L.down) + (int64_t)ffn * 4 + h * 8;
     case K_ROUTER: return wb(L.router) + h * 8 + (int64_t)n_experts * 4;
@@ -1017,7 +1026,7 @@ int64_t Engine::kind_bytes(int kind, int count) const {
     case K_COMBINE: return (int64_t)n_used * h * 4 + h * 8;
     case K_HEAD: return wb(head) + ((h + 255) / 256) * 320 + (int64_t)vocab * 4;
     case K_NORM: return h * 8 + ((h + 255) / 256) * 320;
-    case K_MERGE: return (int64_t)n_heads * 64 * (head_dim + 2) * 4 + qd * 4 + ((qd + 255) / 256) * 320;
+    case K_MERGE: return (int64_t)n_heads * 64 * (head_dim + 2) * 4 + qd * 4 + (merge_w ? 0 : ((qd + 255) / 256) * 320);
     default: return 0;
     }
 }
