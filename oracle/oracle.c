@@ -800,6 +800,19 @@ void or_prefill_attend(const float *q, const void *kp, const void *vp, int f32, 
                        int start, int rows, int window, float scale, float *out) {
     int64_t kvdim = (int64_t)nkv * hd;
     int group = nh / nkv;
+    /* fp16 planes are widened to f32 once (exact), then read as f32 */
+    float *kw = NULL, *vw = NULL;
+    if (!f32) {
+        int64_t n = (int64_t)(start + rows) * kvdim;
+        kw = (float *)malloc(sizeof(float) * (size_t)n);
+        vw = (float *)malloc(sizeof(float) * (size_t)n);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; i++) {
+            kw[i] = or_f16_to_f32(((const uint16_t *)kp)[i]);
+            vw[i] = or_f16_to_f32(((const uint16_t *)vp)[i]);
+        }
+        kp = kw; vp = vw; f32 = 1;
+    }
 #pragma omp parallel for collapse(2) schedule(dynamic, 4)
     for (int kvh = 0; kvh < nkv; kvh++)
         for (int r = 0; r < rows; r++) {
@@ -838,6 +851,7 @@ void or_prefill_attend(const float *q, const void *kp, const void *vp, int f32, 
                 for (int d = 0; d < hd; d++) o[d] = acc[d] * inv;
             }
         }
+    free(kw); free(vw);
 }
 
 /* ------------------------------------------------------------------ model */
@@ -896,6 +910,11 @@ void or_model_reset(or_model *m) {
     size_t plane = (size_t)m->c.ctx * m->c.n_kv * m->c.head_dim * es;
     for (int l = 0; l < m->c.n_layers; l++) { memset(m->kc[l], 0, plane); memset(m->vc[l], 0, plane); }
 }
+
+/* The CPU worker count the decode split rule divides (the reference's
+ * EngineOptions.cpuThreads, AttnKernel.cpuDecodeSplits :4879-4889); the
+ * KV planes are kept, so decode steps can be replayed at another count. */
+void or_model_set_workers(or_model *m, int workers) { m->c.workers = workers; }
 
 int64_t or_model_trace(or_model *m, int what, float *out, int64_t n) {
     const or_config *c = &m->c;

@@ -81,6 +81,7 @@ def _configure(L):
             "or_model_new": (P, [ctypes.POINTER(Config)]), "or_model_free": (None, [P]),
             "or_model_bind": (I32, [P, ctypes.c_char_p, I32, P, I64, I64]),
             "or_model_step": (I32, [P, I32, I32, P]), "or_model_reset": (None, [P]),
+            "or_model_set_workers": (None, [P, I32]),
             "or_model_threads": (I32, []),
             "or_model_trace": (I64, [P, I32, P, I64]),
         }
@@ -273,6 +274,11 @@ class Model:
 
     def reset(self):
         lib().or_model_reset(self.h)
+
+    def set_workers(self, workers):
+        """The split rule's worker count for the steps that follow (KV kept)."""
+        lib().or_model_set_workers(self.h, int(workers))
+        self.cfg.workers = int(workers)
 
     def trace(self, what, n):
         out = np.empty(n, np.float32)

@@ -189,6 +189,67 @@ def test_c3_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+def test_c3_attention_at_the_benchmarked_context(gpu):
+    """Benchmark configuration C3 at the context it is timed at: a 2048-token prompt
+    through four 512-row prefill chunks, then 9 greedy steps at positions 2048 to
+    2056 (2049 to 2057 keys a step), every step's logits bit for bit against the
+    oracle, at the default 512 workers (64 splits a kv head) and at 16 (4
+    splits, a 16-thread reference CPU run). The attention shapes are C3's (d 4096,
+    32/8 heads of 128, θ 500000, Q4_K + Q6_K head, V 128256); two layers and a
+    1024-wide FFN keep the oracle's 2048-row prefill to seconds, and the FFN
+    width does not reach the context-dependent path (the 14336-wide FFN is
+    checked above and at full depth)."""
+    from oracle import oracle as O
+    from oracle.gguf_reader import GgufReader, oracle_model
+    say("model c3 ctx 2048")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=1024;vocab=128256;eps=1e-5;theta=500000;" \
+           "wtype=q4_k;head=q6_k;embd=q4_k;ctx=2304"
+    path, img = synth(gpu, spec, "t_c3ctx", 91)
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, 128256, 2048).tolist()
+    n_gen, ctx = 9, 2304
+    om, cfg = oracle_model(GgufReader(img), ctx=ctx)
+    try:
+        say("  oracle prefill of 2048 rows")
+        first, first_lg = om.prefill(prompt, 0)
+        ref = {}
+        for w in (512, 16):
+            # the KV planes of the prompt are kept; the steps overwrite 2048..
+            om.set_workers(w)
+            toks, lgs = [first], [first_lg]
+            for p in range(len(prompt), len(prompt) + n_gen - 1):
+                t, lg = om.step(toks[-1], p)
+                toks.append(t)
+                lgs.append(lg)
+            ref[w] = (toks, lgs)
+    finally:
+        om.close()
+    assert O.cpu_decode_splits(2049, 1, 8, 512) == 64 and O.cpu_decode_splits(2049, 1, 8, 16) == 4
+    # the worker count reaches the logits' last bits: both counts are checked
+    assert any(not np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(ref[512][1], ref[16][1]))
+    for w in (512, 16):
+        say("  engine, %d workers" % w)
+        opts = gpu.EngineOptions(path)
+        opts.ctx, opts.maxSeqs, opts.cpuThreads = ctx, 1, w
+        eng = gpu.LlmEngine.load(opts)
+        try:
+            eng.reset()
+            eng.prefill(prompt)
+            toks, lgs = [int(eng.preds(len(prompt))[-1])], [eng.logits()]
+            for _ in range(n_gen - 1):
+                toks.append(int(eng.decode(1)[0]))
+                lgs.append(eng.logits())
+        finally:
+            eng.close()
+        rt, rl = ref[w]
+        assert toks == rt, (w, toks, rt)
+        for i, (g, o) in enumerate(zip(lgs, rl)):
+            assert np.array_equal(g.view(np.uint32), o.view(np.uint32)), \
+                (w, i, float(np.max(np.abs(g - o))))
+        assert len(set(toks)) > 1
+    gpu.image_free("t_c3ctx")
+
+
 def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
     """Benchmark configuration C4's Q8_0 weights on the 8B shapes, at two layers."""
     say("model c4x2")
