@@ -394,6 +394,82 @@ def run_single(args, pkg, native, which):
     print(json.dumps(line), flush=True)
 
 
+C5B_METRIC = "batched decode tok/s, gpt-oss-20b-shape MXFP4 MoE, 16 seqs x 4096 ctx"
+
+
+def run_c5_batch(args, pkg, native):
+    """Benchmark configuration C5 at batch > 1: `seqs` sequences prefilled to `ctx`
+    positions (prefill chunks of decode-attention rows), then batched greedy
+    decode of all of them through the captured batch step; beside it the
+    same engine's batch-1 step on one of the sequences, for the per-token
+    comparison with decoding the sequences one at a time."""
+    nseq, ctx = args.seqs, args.ctx or 4096
+    steps = 32 if args.steps == 256 else args.steps
+    t = time.perf_counter()
+    pkg.synth_gguf("c5", "mem:bench_c5b", args.seed)
+    log("synthesised C5 (seed %d) in %.1f s" % (args.seed, time.perf_counter() - t))
+    opts = pkg.EngineOptions("mem:bench_c5b")
+    opts.ctx = ctx + 2 * (args.warmup + steps) + 1
+    opts.maxSeqs = nseq
+    opts.graphs = not args.eager
+    eng = pkg.LlmEngine.load(opts)
+    cfg = eng.config
+    vocab = cfg["vocabSize"]
+    log("loaded: %s" % cfg)
+    rng = np.random.default_rng(args.seed)
+    t = time.perf_counter()
+    for s in range(nseq):
+        eng.reset(s)
+        eng.prefill(rng.integers(0, vocab, ctx).tolist(), seq=s)
+    native.sync()
+    pf_s = time.perf_counter() - t
+    log("prefilled %d sequences x %d positions in %.1f s (%.0f tok/s)" % (nseq, ctx, pf_s, nseq * ctx / pf_s))
+    slots = list(range(nseq))
+    eng.decodeBatch(slots, args.warmup)
+    native.sync()
+    t0 = time.perf_counter()
+    out = eng.decodeBatch(slots, steps)
+    native.sync()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1000.0 / steps
+    dev_us = eng.lastStepMicros()
+    log("timed %d batched steps of %d rows: %.3f ms/step wall, %.1f us/step device; %d distinct tokens"
+        % (steps, nseq, ms_per_step, dev_us, len(set(out.ravel().tolist()))))
+    # the batch-1 step of slot 0 (the same positions' cost, one sequence a step)
+    eng.decode(args.warmup, seq=0)
+    native.sync()
+    t0 = time.perf_counter()
+    eng.decode(steps, seq=0)
+    native.sync()
+    one_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    log("batch-1 step of the same model: %.3f ms/token; batched: %.3f ms/token (%.1fx)"
+        % (one_ms, ms_per_step / nseq, one_ms / (ms_per_step / nseq)))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(pkg, "bench_c5b", vocab, args.cpu_seconds, args.seed)
+        cpu["sample"] = cpu["sample"].replace("C3", "C5")
+        log("cpu baseline: %s" % cpu)
+    eng.close()
+    pkg.image_free("bench_c5b")
+    line = {
+        "metric": C5B_METRIC,
+        "value": round(nseq * steps / wall, 2),
+        "unit": "tok/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded random-init GGUF (N(0,0.02) weights), uniform random prompt ids",
+        "config": {"workload": "C5: gpt-oss-20b shape (24 layers, d 2880, 64/8 heads of 64, 32 MXFP4 experts "
+                               "top-4 of FFN 2880, alternating 128-window attention, vocab 201088), batched "
+                               "greedy decode", "batch": nseq, "prefill_positions": ctx,
+                   "step": "eager launches" if args.eager else "hipGraph replay", "seed": args.seed},
+        "batch1": {"ms_per_token": round(one_ms, 4), "speedup_per_token": round(one_ms / (ms_per_step / nseq), 2)},
+        "prefill": {"value": round(nseq * ctx / pf_s, 1), "unit": "tok/s", "positions": nseq * ctx},
+        "device_us_per_step": round(dev_us, 2),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def run_c5k(args, native):
     """The C5 kernels at their shapes through the launch seam (weights
     prepared once with cj_prepare_weight, seeded random blocks): the expert
@@ -454,7 +530,8 @@ def main():
                          "c2: the quantised GEMV microbench; c1: tiny Q8_0 decode; c5: MoE decode; "
                          "c5k: the C5 kernels at their shapes through the launch seam")
     ap.add_argument("--ctx", type=int, default=None, help="positions prefilled before decoding (c3 2048, c4 4096)")
-    ap.add_argument("--seqs", type=int, default=32, help="c4: sequences decoded together")
+    ap.add_argument("--seqs", type=int, default=None,
+                    help="sequences decoded together: c4 (default 32); c5 above 1 times the batched decode")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="the CPU worker count the attention split rule follows (0: the engine's 512)")
     ap.add_argument("--prefill-reps", type=int, default=3, help="c4: timed 512-row prefill chunks")
@@ -484,6 +561,9 @@ def main():
     if args.workload == "c5k":
         run_c5k(args, native)
         return
+    if args.workload == "c5" and (args.seqs or 1) > 1:
+        run_c5_batch(args, pkg, native)
+        return
     if args.workload in SINGLE:
         run_single(args, pkg, native, args.workload)
         return
@@ -492,6 +572,8 @@ def main():
             args.ctx = 4096
         if args.steps == 256:
             args.steps = 32
+        if args.seqs is None:
+            args.seqs = 32
         run_c4(args, pkg, native)
         return
     if args.ctx is None:

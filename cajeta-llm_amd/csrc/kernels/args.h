@@ -76,11 +76,12 @@ typedef struct {
     int64_t xp_stride;      // bytes between packed activation vectors
     int64_t y_stride;       // floats between output vectors (y, act) per batch / expert k
     // MoE indirection: workgroups cover n_sel copies of the rows; copy k reads
-    // weight w + sel[k]·expert_bytes, activation x + k·x_stride, writes at k·y_stride
+    // weight w + sel[k]·expert_bytes, activation x + (k / sel_per_x)·x_stride
+    // (the pack likewise), writes at k·y_stride
     const int32_t *sel;
     int64_t expert_bytes;
     int32_t n_sel;
-    int32_t pad2;
+    int32_t sel_per_x;      // copies sharing one activation (many rows: n_used); ≤ 1: activation k
 } cj_gemv_args;
 
 typedef struct {

@@ -391,13 +391,13 @@ SPLIT_KERNEL(8)
 // row once and scores it against every query head of the group (q in LDS,
 // read as broadcasts). Dynamic LDS: group × HD floats.
 template <int HD>
-DEV void scores_body(const cj_attn_args &a) {
+DEV void scores_body(const cj_attn_args &a, int bx, int kvh) {
     extern __shared__ __align__(16) float qs[];
     int count, from;
     attn_window(a, count, from);
-    const int grp = a.n_q / a.n_kv, kvh = blockIdx.y;
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (blockIdx.x * 256 >= count) return;      // the whole workgroup idles past count
+    const int grp = a.n_q / a.n_kv;
+    const int t = bx * 256 + threadIdx.x;
+    if (bx * 256 >= count) return;      // the whole workgroup idles past count
     // the page entry is requested with q (the K row's address waits on it)
     const int pos = from + min(t, count - 1);
     const int page = a.pgtab[a.pg_base + (pos >> 6)];
@@ -589,7 +589,7 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
 }
 
 template <int HD>
-DEV void combine_body(const cj_attn_args &a) {
+DEV void combine_body(const cj_attn_args &a, int bx) {
     using D = CombineDims<HD>;
     __shared__ float red[4 + 128];
     __shared__ __align__(16) float prod[2 * D::DH * D::S];   // also V of a short span: 2048 chunks of 16 bytes
@@ -597,7 +597,7 @@ DEV void combine_body(const cj_attn_args &a) {
     __shared__ __align__(16) float es[COMBINE_ES];
     int count, from;
     attn_window(a, count, from);
-    const int h = blockIdx.x / D::NSPLIT, d0 = D::DH * (blockIdx.x % D::NSPLIT), l = threadIdx.x;
+    const int h = bx / D::NSPLIT, d0 = D::DH * (bx % D::NSPLIT), l = threadIdx.x;
     const int grp = a.n_q / a.n_kv, kvh = h / grp;
     const float *sc = a.part + (int64_t)h * a.splits;
     const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
@@ -723,10 +723,37 @@ DEV void combine_body(const cj_attn_args &a) {
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
-extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a); }
+// Row r of a many-row launch as the one-row kernels see it: its sequence
+// slot's pages and position, its q, output and score rows.
+DEV cj_attn_args attn_row_args(const cj_attn_args &a, int r) {
+    cj_attn_args b = a;
+    const int slot = a.rowtab[2 * r];
+    b.state = nullptr;
+    b.count = a.states[slot].pos + a.rowtab[2 * r + 1] + 1;
+    b.from = 0;
+    b.pg_base = slot * a.pg_n;
+    b.q = a.q + (int64_t)r * a.q_stride;
+    b.out = a.out + (int64_t)r * a.q_stride;
+    b.part = a.part + (int64_t)r * a.part_stride;
+    return b;
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a, blockIdx.x, blockIdx.y); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a, blockIdx.x, blockIdx.y); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a, blockIdx.x); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a, blockIdx.x); }
+// The many-row forms (batched decode, and prefill chunks of the models that
+// prefill a decode step a position): grid y is row · n_kv + kv head for the
+// scores, the row for the combine.
+#define TWO_PASS_ROWS(HD)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_rows_h##HD(cj_attn_args a) {          \
+        scores_body<HD>(attn_row_args(a, blockIdx.y / a.n_kv), blockIdx.x, blockIdx.y % a.n_kv);           \
+    }                                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_rows_h##HD(cj_attn_args a) {         \
+        combine_body<HD>(attn_row_args(a, blockIdx.y), blockIdx.x);                                         \
+    }
+TWO_PASS_ROWS(64)
+TWO_PASS_ROWS(128)
 
 // The two-pass form in one launch for spans of at most FUSED_SPAN(HD)
 // positions (sliding windows, small contexts): a workgroup per kv head
@@ -737,7 +764,7 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_a
 // output dimension's ascending-t sum — so its results are theirs bit for bit.
 #define FUSED_SPAN(HD) ((HD) == 64 ? 256 : 128)
 template <int HD>
-DEV void fused_body(const cj_attn_args &a) {
+DEV void fused_body(const cj_attn_args &a, int kvh) {
     constexpr int SPAN = FUSED_SPAN(HD);
     __shared__ __align__(16) uint16_t ks[SPAN * HD], vs[SPAN * HD];
     __shared__ __align__(16) float qs[8 * HD];
@@ -746,7 +773,7 @@ DEV void fused_body(const cj_attn_args &a) {
     __shared__ float rsv[8];
     int count, from;
     attn_window(a, count, from);
-    const int kvh = blockIdx.x, l = threadIdx.x, grp = a.n_q / a.n_kv;
+    const int l = threadIdx.x, grp = a.n_q / a.n_kv;
     // q of the group, then K and V rows of the span (chunk c of row t: the
     // page entry of the row, then its 16 bytes), all loads issued together
     for (int i = l; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
@@ -837,8 +864,15 @@ DEV void fused_body(const cj_attn_args &a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) { fused_body<64>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) { fused_body<128>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) { fused_body<64>(a, blockIdx.x); }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) { fused_body<128>(a, blockIdx.x); }
+// many rows: grid (n_kv, rows)
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h64(cj_attn_args a) {
+    fused_body<64>(attn_row_args(a, blockIdx.y), blockIdx.x);
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h128(cj_attn_args a) {
+    fused_body<128>(attn_row_args(a, blockIdx.y), blockIdx.x);
+}
 
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
 // 256 per 256 output values (the reference's attnReducePackQ8Kernel

@@ -259,13 +259,15 @@ DEV bool argmax_take(float ov, int oi, float mv, int mi) {
 // ------------------------------------------------------------------ body
 
 // Where a workgroup's rows come from: with MoE indirection (`sel`), copy k
-// of the rows reads expert sel[k]'s weight, activation k and output k.
+// of the rows reads expert sel[k]'s weight, activation k / sel_per_x (k
+// where sel_per_x ≤ 1: many rows' selections share their row's activation)
+// and writes output k.
 struct GemvSlice {
     const uint8_t *W;
     const float *X;
     float *Y, *ACT;
     int64_t row0;
-    int kidx;
+    int kidx, xidx;
 };
 
 DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
@@ -279,7 +281,8 @@ DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
         wg = wg % wpk;
     }
     s.W = a.w + (a.sel ? (int64_t)a.sel[s.kidx] * a.expert_bytes : 0);
-    s.X = a.x ? a.x + s.kidx * a.x_stride : nullptr;
+    s.xidx = a.sel_per_x > 1 ? s.kidx / a.sel_per_x : s.kidx;
+    s.X = a.x ? a.x + s.xidx * a.x_stride : nullptr;
     s.Y = a.y ? a.y + s.kidx * a.y_stride : nullptr;
     s.ACT = a.act ? a.act + s.kidx * a.y_stride : nullptr;
     s.row0 = wg * R;
@@ -293,7 +296,7 @@ DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, 
     const int64_t cols = a.cols;
     const int nblk = (int)((cols + 255) / 256);
     if (a.pro == CJ_PRO_PACKED) {
-        stage_copy(a.xp + sl.kidx * a.xp_stride, nblk, sx, bstride);
+        stage_copy(a.xp + sl.xidx * a.xp_stride, nblk, sx, bstride);
     } else {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
         const float scale = norm ? stage_norm_scale(sl.X, cols, a.eps, red) : 1.0f;
@@ -809,7 +812,7 @@ DEV void q4k_pro_load(const cj_gemv_args &a, const GemvSlice &sl, float4 (&px)[Q
     const int t = threadIdx.x;
     const int64_t n = a.cols;
     if constexpr (PRO == CJ_PRO_PACKED) {
-        const u32x4 *src = (const u32x4 *)(a.xp + sl.kidx * a.xp_stride);
+        const u32x4 *src = (const u32x4 *)(a.xp + sl.xidx * a.xp_stride);
         const int n16 = (int)(n / 256) * 20;
 #pragma unroll
         for (int i = 0; i < D::NPK; i++) ppk[i] = src[min(t + 256 * i, n16 - 1)];

@@ -465,10 +465,14 @@ extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
 
 // MoE combine (MoeFfn.forwardRow, model/MoeFfn.cajeta:1849-1913): the
 // selected experts' rows weighted and summed in k order, then onto hs.
+// Grid y is the row of a many-row step: row r's hs, its n_used outputs and
+// weights follow row r − 1's.
 extern "C" __global__ void __launch_bounds__(256) cj_moe_combine(cj_combine_args a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (i >= a.n) return;
+    const float *w = a.w + r * a.n_used, *y = a.y + r * a.n_used * a.n;
     float acc = 0.0f;
-    for (int k = 0; k < a.n_used; k++) acc = __fadd_rn(acc, __fmul_rn(a.w[k], a.y[k * a.n + i]));
-    a.hs[i] = __fadd_rn(a.hs[i], acc);
+    for (int k = 0; k < a.n_used; k++) acc = __fadd_rn(acc, __fmul_rn(w[k], y[k * a.n + i]));
+    float *hs = a.hs + r * a.n;
+    hs[i] = __fadd_rn(hs[i], acc);
 }

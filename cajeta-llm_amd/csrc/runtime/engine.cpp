@@ -122,11 +122,18 @@ struct Engine {
     // chunks (a row a position)
     cj_step_state *states = nullptr;           // [max_seqs]; seqs[s].state = states + s
     int32_t *tokens_all = nullptr, *preds_all = nullptr;   // [max_seqs][ctx + 2]
-    bool rows_ok = false;      // dense, head size 128, projections served as many-row products
-    bool batch_split = false;  // batched decode attention takes the split-K rows kernel
+    bool rows_ok = false;      // the many-row path serves the model (int8-pack projections; MoE experts indirected)
+    bool rows_split = false;   // decode attention rows take the split-K rows kernel (else the two-pass rows)
+    bool rows_prefill = false; // prompts go through prefill chunks of rows
+    bool rows_pf_attend = false;   // a chunk's attention is the prefill attend (else each row's decode attention)
     int chunk = 512;           // prefill rows a chunk (CausalLM.CHUNK_MAX)
     int rows_cap = 0;          // rows the row buffers hold
     float *r_hs = nullptr, *r_qkv = nullptr, *r_q = nullptr, *r_attn = nullptr, *r_gu = nullptr;
+    // MoE rows: the normed rows (f32), router logits, selections, weights,
+    // the selections' SiLU·up activations and down outputs, and an all-zero
+    // selection list (the router's indirection: every row reads one weight)
+    float *r_xn = nullptr, *r_moe_logits = nullptr, *r_moe_w = nullptr, *r_act = nullptr, *r_moe_y = nullptr;
+    int32_t *r_moe_sel = nullptr, *r_zero_sel = nullptr;
     float *r_logits = nullptr, *r_part = nullptr, *r_pv = nullptr;
     int32_t *r_pi = nullptr, *r_tab_pf = nullptr, *r_tab_b = nullptr;
     uint8_t *r_xp = nullptr, *r_ap = nullptr, *r_actp = nullptr;
@@ -165,6 +172,8 @@ struct Engine {
     int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
     int rows_norm_pack(const float *w, int per32, int n);
     int rows_forward(const int32_t *tab, int n, bool prefill);
+    int rows_pack(const float *x, int64_t n, int per32, int rows);
+    int rows_moe(const Layer &L, int n);
     int enqueue_batch(int n);
     int prefill_rows(int s, const int32_t *toks, int n);
     int decode_batch(const int32_t *slots, int n, int steps, int32_t *out);
@@ -434,14 +443,26 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
         S.pg_base = s * pages_per_seq;
     }
 
-    // the many-row path: dense layers at head size 128 whose projections
-    // read int8 packs (the CPU prefill attend serves head size 128,
-    // AttnKernel.cpuAttnServes, model/AttnKernel.cajeta:4439-4447)
-    rows_ok = n_experts == 0 && head_dim == 128;
-    for (auto &L : layers)
-        for (const DevW *w : {&L.qkv, &L.o, &L.gu, &L.down})
+    // the many-row path (batched decode: a row a sequence; prefill chunks: a
+    // row a position) where the projections read int8 packs; MoE experts go
+    // through the indirected GEMV over every row's selections
+    rows_ok = !is_f32_act(head.type);
+    for (auto &L : layers) {
+        for (const DevW *w : {&L.qkv, &L.o})
             if (is_f32_act(w->type)) rows_ok = false;
-    batch_split = rows_ok && (grp == 4 || grp == 8);
+        if (n_experts == 0)
+            for (const DevW *w : {&L.gu, &L.down})
+                if (is_f32_act(w->type)) rows_ok = false;
+    }
+    rows_split = head_dim == 128 && (grp == 4 || grp == 8);
+    // prompts: the prefill attend where the reference's CPU prefill serves
+    // the shape (dense, head size 128: AttnKernel.cpuAttnServes,
+    // model/AttnKernel.cajeta:4439-4447); the other models prefill a decode
+    // step a position, which rows of the two-pass decode attention repeat
+    // row for row (a split-K row's split count follows the rows, so MoE
+    // models at head size 128 keep the step a position)
+    rows_pf_attend = n_experts == 0 && head_dim == 128;
+    rows_prefill = rows_ok && (rows_pf_attend || !rows_split);
     if (rows_ok && (rc = rows_alloc(std::max(chunk, max_seqs)))) return rc;
     CJ_HIP(hipDeviceSynchronize());
     return CJ_OK;
@@ -463,7 +484,22 @@ int Engine::rows_alloc(int cap) {
     r_ap = (uint8_t *)alloc((size_t)(cap * qb));
     r_actp = (uint8_t *)alloc((size_t)(cap * fb));
     r_logits = (float *)alloc((size_t)(b * vocab * 4));
-    r_part = (float *)alloc((size_t)(b * n_heads * 64 * (head_dim + 2) * 4));
+    // split-K partials [b][n_heads][64][hd + 2], or the two-pass score rows [cap][n_heads][ctx]
+    r_part = (float *)alloc((size_t)std::max<int64_t>(b * n_heads * 64 * (head_dim + 2),
+                                                      rows_split ? 0 : (int64_t)cap * n_heads * ctx) * 4);
+    if (n_experts > 0) {
+        const int64_t sels = (int64_t)cap * n_used;
+        r_xn = (float *)alloc((size_t)((int64_t)cap * hidden * 4));
+        r_moe_logits = (float *)alloc((size_t)((int64_t)cap * n_experts * 4));
+        r_moe_sel = (int32_t *)alloc((size_t)(sels * 4));
+        r_moe_w = (float *)alloc((size_t)(sels * 4));
+        r_act = (float *)alloc((size_t)(sels * expert_ffn * 4 + 1024));
+        r_moe_y = (float *)alloc((size_t)(sels * hidden * 4));
+        r_zero_sel = (int32_t *)alloc((size_t)(cap * 4));
+        if (!r_xn || !r_moe_logits || !r_moe_sel || !r_moe_w || !r_act || !r_moe_y || !r_zero_sel)
+            return fail(CJ_ERR_HIP, "model: out of device memory (MoE row buffers for %d rows)", cap);
+        CJ_HIP(hipMemset(r_zero_sel, 0, (size_t)(cap * 4)));
+    }
     r_pv = (float *)alloc((size_t)(b * nch * 4));
     r_pi = (int32_t *)alloc((size_t)(b * nch * 4));
     r_tab_pf = (int32_t *)alloc((size_t)cap * 8);
@@ -701,6 +737,66 @@ int Engine::rows_norm_pack(const float *w, int per32, int n) {
     return launch("cj_pack", (uint32_t)n, 256, (uint32_t)(npad / 256 * 320), a);
 }
 
+// The f32 rows x (n wide) packed into r_ap, a workgroup a row.
+int Engine::rows_pack(const float *x, int64_t n, int per32, int rows) {
+    cj_pack_args p{};
+    p.out = r_ap; p.x = x; p.n = n; p.npad = (n + 255) / 256 * 256; p.rows = rows; p.per32 = per32;
+    return launch("cj_pack", (uint32_t)rows, 256, (uint32_t)(p.npad / 256 * 320), p);
+}
+
+// The MoE FFN of n rows (MoeFfn.forwardRowsZeroSync, model/MoeFfn.cajeta:1559
+// and its comment at :1510-1515: one router product and one top-k over the
+// rows, one indirected product per expert bank over every row's
+// selections, one combine), each row computed exactly as the one-row step
+// computes it: the FFN norm (f32 rows for the router and f32-activation
+// experts, the pack for int8 experts), the f32 router of every row, top-k,
+// gate|up + SiLU·up of selection (r, k) from row r's activation, down of
+// each selection, the weighted sum onto the residual rows in k order.
+int Engine::rows_moe(const Layer &L, int n) {
+    int rc;
+    const int64_t npad = ((int64_t)hidden + 255) / 256 * 256, hb = npad / 256 * 320;
+    const int sels = n * n_used;
+    {
+        cj_pack_args p{};
+        p.out = r_xp; p.x = r_hs; p.w = L.ffn_norm; p.xout = r_xn; p.n = hidden; p.npad = npad; p.rows = n;
+        p.eps = eps; p.form = 0; p.per32 = L.gu_exps.type == CJ_Q8_0; p.do_norm = 1;
+        if ((rc = launch("cj_pack", (uint32_t)n, 256, (uint32_t)hb, p))) return rc;
+    }
+    {   // router logits of every row: the indirection's copies all read the router (expert_bytes 0)
+        cj_gemv_args a{};
+        a.w = (const uint8_t *)L.router.p; a.x = r_xn; a.y = r_moe_logits; a.rows = n_experts; a.cols = hidden;
+        a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_F32; a.epi = CJ_EPI_STORE; a.eps = eps;
+        a.batch = 1; a.sel = r_zero_sel; a.n_sel = n; a.sel_per_x = 1; a.expert_bytes = 0; a.x_stride = hidden;
+        a.y_stride = n_experts;
+        if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
+    }
+    {
+        cj_route_args a{r_moe_logits, r_moe_sel, r_moe_w, n_experts, n_used, norm_topk, n, w_scale, 0, route_status};
+        if ((rc = launch("cj_moe_route", (uint32_t)n, 64, 0, a))) return rc;
+    }
+    {   // gate|up + SiLU·up of selection (r, k) = r·n_used + k over row r
+        cj_gemv_args a{};
+        a.w = (const uint8_t *)L.gu_exps.p; a.x = r_xn; a.xp = r_xp; a.act = r_act; a.rows = 2 * (int64_t)expert_ffn;
+        a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
+        a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.eps = eps;
+        a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
+        a.sel = r_moe_sel; a.n_sel = sels; a.sel_per_x = n_used; a.x_stride = hidden; a.xp_stride = hb;
+        a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes; a.y_stride = expert_ffn;
+        if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
+    }
+    {   // down of every selection
+        cj_gemv_args a{};
+        a.w = (const uint8_t *)L.down_exps.p; a.x = r_act; a.y = r_moe_y; a.rows = hidden; a.cols = expert_ffn;
+        a.row_bytes = L.down_exps.row_bytes; a.type = L.down_exps.type;
+        a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
+        a.batch = 1; a.sel = r_moe_sel; a.n_sel = sels; a.sel_per_x = 1;
+        a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes; a.x_stride = expert_ffn; a.y_stride = hidden;
+        if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
+    }
+    cj_combine_args c{r_hs, r_moe_y, r_moe_w, hidden, n_used};
+    return launch2("cj_moe_combine", (uint32_t)((hidden + 255) / 256), (uint32_t)n, 256, 0, c);
+}
+
 // The layers over n rows (row table `tab` on the device): embedding, then per
 // layer the norm + pack rows, q|k|v product, RoPE + K/V append rows, the
 // attention (prefill: the prefill attend + pack; batched decode: split-K
@@ -737,15 +833,31 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
         a.q = r_q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
         a.workers = workers; a.scale = scale; a.pg_n = pages_per_seq; a.window = L.window; a.rowtab = tab;
         a.states = states; a.nrows = n; a.q_stride = qd;
-        if (prefill) {
+        if (prefill && rows_pf_attend) {
             a.out = r_attn;
             const int ns = grp >= 8 ? grp / 4 : 1, rb = 16 * ns / grp;
             char kname[48];
             snprintf(kname, sizeof kname, "cj_attn_prefill_h128_g%d", grp);
             if ((rc = launch(kname, (uint32_t)(n_kv * ((n + rb - 1) / rb)), 256, 0, a))) return rc;
-            cj_pack_args p{};
-            p.out = r_ap; p.x = r_attn; p.n = qd; p.npad = (qd + 255) / 256 * 256; p.rows = n; p.per32 = L.o.type == CJ_Q8_0;
-            if ((rc = launch("cj_pack", (uint32_t)n, 256, (uint32_t)qb, p))) return rc;
+            if ((rc = rows_pack(r_attn, qd, L.o.type == CJ_Q8_0, n))) return rc;
+        } else if (!rows_split) {
+            // each row's two-pass decode attention (the fused form where
+            // every span fits one workgroup), then the pack of the rows
+            a.out = r_attn; a.part = r_part; a.splits = ctx; a.part_stride = (int64_t)n_heads * ctx;
+            const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
+            char kname[48];
+            if (span <= (head_dim == 64 ? 256 : 128)) {
+                snprintf(kname, sizeof kname, "cj_attn_fused_rows_h%d", head_dim);
+                if ((rc = launch2(kname, (uint32_t)n_kv, (uint32_t)n, 256, 0, a))) return rc;
+            } else {
+                snprintf(kname, sizeof kname, "cj_attn_scores_rows_h%d", head_dim);
+                if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_kv), 256,
+                                  (uint32_t)(grp * head_dim * 4), a)))
+                    return rc;
+                snprintf(kname, sizeof kname, "cj_attn_combine_rows_h%d", head_dim);
+                if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;
+            }
+            if ((rc = rows_pack(r_attn, qd, L.o.type == CJ_Q8_0, n))) return rc;
         } else {
             // split slots a row: the rule's count over every row's kv heads
             const int rk = n * n_kv;
@@ -761,6 +873,10 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             if ((rc = launch("cj_attn_merge_rows", (uint32_t)(n * (qd / 256)), 256, 0, m))) return rc;
         }
         if ((rc = rows_linear(L.o, r_ap, qb, r_hs, hidden, true, n))) return rc;
+        if (n_experts > 0) {
+            if ((rc = rows_moe(L, n))) return rc;
+            continue;
+        }
         if ((rc = rows_norm_pack(L.ffn_norm, L.gu.type == CJ_Q8_0, n))) return rc;
         if ((rc = rows_linear(L.gu, r_xp, hb, r_gu, L.gu.rows, false, n))) return rc;
         {
@@ -840,8 +956,9 @@ int Engine::prefill_rows(int s, const int32_t *toks, int n) {
 }
 
 // `steps` greedy tokens for each of n prefilled slots at once (one row a
-// slot): out[i·n + r] is slot r's token i. Shapes without the split-K
-// attention decode slot by slot (the same tokens: rows only share weights).
+// slot): out[i·n + r] is slot r's token i. Models the many-row path does
+// not serve (f32-activation projections) decode slot by slot (the same
+// tokens: rows only share weights).
 int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
     if (n <= 0 || n > max_seqs) return fail(CJ_ERR_ARG, "decode batch of %d slots (1..%d)", n, max_seqs);
     for (int r = 0; r < n; r++) {
@@ -855,7 +972,7 @@ int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
     }
     if (steps <= 0) return CJ_OK;
     int rc;
-    if (!batch_split || n > rows_cap) {
+    if (!rows_ok || n > rows_cap) {
         std::vector<int32_t> tmp((size_t)steps);
         for (int r = 0; r < n; r++) {
             if ((rc = decode(slots[r], steps, tmp.data()))) return rc;
@@ -949,7 +1066,7 @@ int Engine::prefill(int s, const int32_t *toks, int n) {
     if (S.pos + n > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + n, ctx);
     for (int i = 0; i < n; i++)
         if (toks[i] < 0 || toks[i] >= vocab) return fail(CJ_ERR_ARG, "token %d outside the vocabulary", toks[i]);
-    if (n > 1 && rows_ok && chunk > 1) return prefill_rows(s, toks, n);
+    if (n > 1 && rows_prefill && chunk > 1) return prefill_rows(s, toks, n);
     int rc;
     if (graphs && (rc = capture(s))) return rc;
     // through pinned staging: the copies are ordered on the stream and the
@@ -1188,7 +1305,7 @@ int Engine::step_once() {
     sched_steps++;
     int rc;
     if ((rc = admit())) return rc;
-    const int cap = rows_ok && chunk > 1 ? chunk : 512;   // prompt rows a request feeds per step
+    const int cap = rows_prefill && chunk > 1 ? chunk : 512;   // prompt rows a request feeds per step
     std::vector<int> batch;                             // requests decoding one position
     for (size_t i = 0; i < reqs.size(); i++) {
         Request &r = reqs[i];

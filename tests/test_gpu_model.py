@@ -296,6 +296,40 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+def test_c5_moe_shape_batched_decode_parity(gpu):
+    """Benchmark configuration C5's batch-16 decode at two layers: 16 slots (two past the
+    128 window) decode together — one router product and one top-k over the
+    rows, one indirected gate|up and one down launch over all 64 selections,
+    the two-pass attention as rows — every slot's tokens and last logits bit
+    for bit against the oracle decoding it alone. The prompts go through
+    prefill chunks of decode-attention rows."""
+    say("model c5x2 batch 16")
+    spec = "layers=2;hidden=2880;heads=64;kv=8;hd=64;ffn=2880;vocab=32000;eps=1e-5;theta=150000;wtype=q8_0;" \
+           "head=q8_0;embd=q8_0;experts=32;used=4;expert_ffn=2880;expert_type=mxfp4;swa=128;ctx=512"
+    path, img = synth(gpu, spec, "t_c5x2b", 83)
+    rng = np.random.default_rng(16)
+    lens = [int(rng.integers(2, 40)) for _ in range(14)] + [131, 150]
+    prompts = [rng.integers(0, 32000, k).tolist() for k in lens]
+    out, err, same = batch_case(gpu, path, img, prompts, 6, 256)
+    gpu.image_free("t_c5x2b")
+    assert err <= LOGIT_TOL and same
+    assert len(set(out.ravel().tolist())) > 1
+
+
+def test_c1_batched_decode_parity(gpu):
+    """Benchmark configuration C1's shapes (head size 64, 4 query heads a kv head, the
+    tanh-form GLU of the 1408-wide FFN) as a batch of 8 slots: the two-pass
+    attention rows, every slot against the oracle decoding it alone."""
+    say("model c1 batch 8")
+    path, img = synth(gpu, "c1", "t_c1b", 1235)
+    rng = np.random.default_rng(17)
+    prompts = [rng.integers(0, 32000, int(rng.integers(2, 30))).tolist() for _ in range(8)]
+    out, err, same = batch_case(gpu, path, img, prompts, 8, 128)
+    gpu.image_free("t_c1b")
+    assert err <= LOGIT_TOL and same
+    assert len(set(out.ravel().tolist())) > 1
+
+
 def test_c3_full_depth_greedy_parity(gpu):
     """Benchmark configuration C3 at its full depth (32 layers, the benchmarked model):
     a 40-token prompt through the prefill chunk, then 6 greedy steps; every
