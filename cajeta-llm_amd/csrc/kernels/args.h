@@ -20,6 +20,7 @@
 #define CJ_PRO_NORM_PACK 2  // f32 x in HBM, RMSNorm'd then packed into LDS
 #define CJ_PRO_F32 3        // f32 x in HBM, used as f32 (Q4_0, MXFP4)
 #define CJ_PRO_NORM_F32 4   // f32 x in HBM, RMSNorm'd, used as f32
+#define CJ_PRO_MXQ8 5       // f32 x in HBM, per-32 int8 codes + scales in LDS (MXFP4 device Q8 form)
 
 // GEMV epilogue: what happens to each output row.
 #define CJ_EPI_STORE 0      // y[row] = v

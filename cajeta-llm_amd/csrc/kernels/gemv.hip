@@ -1126,6 +1126,143 @@ Q4KI_ITS(n, CJ_PRO_NORM_PACK)
 Q4KI_EPIS(c, CJ_PRO_PACKED, 64, _w, 4, 4)
 Q4KI_EPIS(p, CJ_PRO_PACK, 64, _w, 4, 4)
 
+// ------------------------------------------------------------ MXFP4 × q8
+
+// MXFP4 in the reference's device Q8 form (QuantKernel.mxfp4MatVecCoopQ8Launch,
+// io/QuantKernel.cajeta:43699-43713). Every workgroup quantizes the f32
+// activation per 32 elements into LDS (mxfp4QuantActKernel, :43614-43636:
+// bmax = max|x|, q = round-half-away(x · 127/bmax), d = bmax/127), then a
+// 32-lane half-wave takes a row (mxfp4MatVecKernelCoopQ8, :43660-43697):
+// lane L the blocks L, L+32, ..., each block's 32 E2M1 codes decoded to int8
+// and dotted with the q8 codes in v_dot4 steps (an exact integer s), then
+// acc = acc + s·d_w·d_x; the half-wave's xor butterfly (strides 16..1) sums
+// the lanes. Row values go through LDS to the common epilogue (thread t =
+// row t). The weight rows are the prepared [codes nb·16][scales nb] layout:
+// a half-wave's 16-byte code loads are one 512-byte sweep.
+
+// Four E2M1 codes (the low nibbles of v's bytes) as four int8 values of the
+// reference's table {0, 1, 2, 3, 4, 6, 8, 12} with the sign bit (Quant.mxfp4Kv):
+// the magnitude through a byte permute of the positive and of the negated
+// table, the sign bit choosing between them per byte (permute selector 12
+// gives 0x00, 13 gives 0xFF).
+DEV uint32_t e2m1_x4(uint32_t v) {
+    const uint32_t idx = v & 0x07070707u;
+    const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, idx);
+    const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, idx);
+    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((v >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+    return (neg & mask) | (pos & ~mask);
+}
+
+// The LDS layout after the scratch: codes [cols], scales [nb], row values [R].
+DEV int mxq8_xd_off(int64_t cols) { return (int)((cols + 15) & ~15); }
+
+template <int EPI, int KB>
+DEV void mxq8_body(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *red = (float *)smem;
+    float *bmax = red + 256;
+    int8_t *xq = (int8_t *)(smem + LDS_SCRATCH);
+    const int64_t cols = a.cols;
+    const int nb = (int)(cols / 32);
+    float *xd = (float *)(smem + LDS_SCRATCH + mxq8_xd_off(cols));
+    float *res = xd + ((nb + 3) & ~3);
+    const int t = threadIdx.x, hw = t >> 5, hl = t & 31;
+    const int R = a.rows_per_wg;
+    const GemvSlice sl = gemv_slice(a);
+    const EpiPre pre = epi_prefetch_t<EPI>(a, sl);
+    (void)red;
+    // the activation's codes: a thread a 32-block
+    for (int b = t; b < nb; b += 256) {
+        const float4 *xs = (const float4 *)(sl.X + 32 * (int64_t)b);
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 f = xs[k];
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+        float bm = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const float av = fabsf(v[k]);
+            if (av > bm) bm = av;
+        }
+        const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) w |= ((uint32_t)round_away(__fmul_rn(v[4 * k + j], inv)) & 0xFFu) << (8 * j);
+            q[k] = w;
+        }
+        *(u32x4 *)(xq + 32 * b) = u32x4{q[0], q[1], q[2], q[3]};
+        *(u32x4 *)(xq + 32 * b + 16) = u32x4{q[4], q[5], q[6], q[7]};
+        xd[b] = __fdiv_rn(bm, 127.0f);
+    }
+    __syncthreads();
+    // rows: half-wave hw takes rows hw·RW .. +RW−1 of each 8·RW-row pass;
+    // every load is issued (clamped into range) before the first is used
+    constexpr int RW = 4;
+    for (int i0 = hw * RW; i0 < R; i0 += 8 * RW) {
+        float acc[RW];
+#pragma unroll
+        for (int i = 0; i < RW; i++) acc[i] = 0.0f;
+        for (int c0 = 0; c0 < nb; c0 += 32 * KB) {
+            u32x4 wv[RW][KB];
+            uint32_t sc[RW][KB];
+#pragma unroll
+            for (int i = 0; i < RW; i++) {
+                const int64_t r = min(sl.row0 + i0 + i, a.rows - 1);
+                const uint8_t *wr = sl.W + r * a.row_bytes;
+#pragma unroll
+                for (int k = 0; k < KB; k++) {
+                    const int b = min(c0 + hl + 32 * k, nb - 1);
+                    wv[i][k] = __builtin_nontemporal_load((const u32x4 *)(wr + 16 * b));
+                    sc[i][k] = wr[16 * nb + b];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RW; i++) {
+#pragma unroll
+                for (int k = 0; k < KB; k++) {
+                    const int b = c0 + hl + 32 * k, bc = min(b, nb - 1);
+                    const u32x4 w = wv[i][k];
+                    const u32x4 x0 = *(const u32x4 *)(xq + 32 * bc), x1 = *(const u32x4 *)(xq + 32 * bc + 16);
+                    int sd = 0;
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.x), (int)x0.x, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.y), (int)x0.y, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.z), (int)x0.z, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.w), (int)x0.w, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.x >> 4), (int)x1.x, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.y >> 4), (int)x1.y, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.z >> 4), (int)x1.z, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)e2m1_x4(w.w >> 4), (int)x1.w, sd, false);
+                    const float term = __fmul_rn(__fmul_rn((float)sd, mxfp4_scale(sc[i][k])), xd[bc]);
+                    if (b < nb) acc[i] = __fadd_rn(acc[i], term);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            float v = acc[i];
+#pragma unroll
+            for (int m = 16; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_xor(v, m));
+            if (hl == 0 && i0 + i < R) res[i0 + i] = v;
+        }
+    }
+    __syncthreads();
+    gemv_epilogue_t<EPI>(a, sl, t < R ? res[t] : 0.0f, bmax, pre);
+}
+
+#define MXQ8_KERNEL(E, EPI, KB)                                                                     \
+    extern "C" __global__ void __launch_bounds__(256) cj_gemv_mxq8_##E##_k##KB(cj_gemv_args a) {    \
+        mxq8_body<EPI, KB>(a);                                                                      \
+    }
+#define MXQ8_KBS(E, EPI) MXQ8_KERNEL(E, EPI, 1) MXQ8_KERNEL(E, EPI, 2) MXQ8_KERNEL(E, EPI, 3) MXQ8_KERNEL(E, EPI, 4)
+MXQ8_KBS(s, CJ_EPI_STORE)
+MXQ8_KBS(a, CJ_EPI_ACCUM)
+MXQ8_KBS(g, CJ_EPI_GLU)
+
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)

@@ -513,6 +513,14 @@ int Engine::rows_alloc(int cap) {
     return CJ_OK;
 }
 
+// The prologue of an expert product: MXFP4 experts read their f32 input
+// through the device Q8 form (per-32 codes in LDS, mxfp4MatVecCoopQ8Launch,
+// io/QuantKernel.cajeta:43699); other f32-activation formats read it as
+// f32; int8 formats read `pack_pro`.
+static int expert_pro(int type, int pack_pro) {
+    return type == CJ_MXFP4 ? CJ_PRO_MXQ8 : is_f32_act(type) ? CJ_PRO_F32 : pack_pro;
+}
+
 // One decode step of sequence s on the stream (captured once into a graph).
 int Engine::enqueue_step(int s) {
     Seq &S = seqs[s];
@@ -634,7 +642,7 @@ int Engine::enqueue_step(int s) {
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.gu_exps.p; a.x = xn; a.xp = xpack; a.act = act; a.rows = 2 * (int64_t)expert_ffn;
                 a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
-                a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.eps = eps;
+                a.pro = expert_pro(a.type, CJ_PRO_PACKED); a.epi = CJ_EPI_GLU; a.eps = eps;
                 a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
                 a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
                 a.y_stride = expert_ffn;
@@ -644,7 +652,7 @@ int Engine::enqueue_step(int s) {
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.down_exps.p; a.x = act; a.y = moe_y; a.rows = hidden; a.cols = expert_ffn;
                 a.row_bytes = L.down_exps.row_bytes; a.type = L.down_exps.type;
-                a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
+                a.pro = expert_pro(a.type, CJ_PRO_PACK); a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
                 a.batch = 1; a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes;
                 a.x_stride = expert_ffn; a.y_stride = hidden;
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
@@ -778,7 +786,7 @@ int Engine::rows_moe(const Layer &L, int n) {
         cj_gemv_args a{};
         a.w = (const uint8_t *)L.gu_exps.p; a.x = r_xn; a.xp = r_xp; a.act = r_act; a.rows = 2 * (int64_t)expert_ffn;
         a.cols = hidden; a.row_bytes = L.gu_exps.row_bytes; a.type = L.gu_exps.type;
-        a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.eps = eps;
+        a.pro = expert_pro(a.type, CJ_PRO_PACKED); a.epi = CJ_EPI_GLU; a.eps = eps;
         a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
         a.sel = r_moe_sel; a.n_sel = sels; a.sel_per_x = n_used; a.x_stride = hidden; a.xp_stride = hb;
         a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes; a.y_stride = expert_ffn;
@@ -788,7 +796,7 @@ int Engine::rows_moe(const Layer &L, int n) {
         cj_gemv_args a{};
         a.w = (const uint8_t *)L.down_exps.p; a.x = r_act; a.y = r_moe_y; a.rows = hidden; a.cols = expert_ffn;
         a.row_bytes = L.down_exps.row_bytes; a.type = L.down_exps.type;
-        a.pro = is_f32_act(a.type) ? CJ_PRO_F32 : CJ_PRO_PACK; a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
+        a.pro = expert_pro(a.type, CJ_PRO_PACK); a.epi = CJ_EPI_STORE; a.per32 = a.type == CJ_Q8_0;
         a.batch = 1; a.sel = r_moe_sel; a.n_sel = sels; a.sel_per_x = 1;
         a.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes; a.x_stride = expert_ffn; a.y_stride = hidden;
         if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;

@@ -59,6 +59,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
         {"q40F32WaveMatVecKernel", "cj_gemv_q40"},
         {"mxfp4MatVecKernel", "cj_gemv_mxfp4"},
+        {"mxfp4MatVecKernelCoopQ8", "cj_gemv_mxq8_s_k3"},
+        {"mxfp4QuantActKernel", "cj_gemv_mxq8_s_k3"},   // the quant is that kernel's prologue
         {"q8kPackKernel", "cj_pack"},
         {"q8kPack32Kernel", "cj_pack"},
         {"rmsnormPackRowF32", "cj_pack"},
@@ -249,6 +251,19 @@ GemvPlan plan_gemv_q4k(int64_t rows, int64_t cols, int pro, int epi) {
 GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, int epi) {
     if (type == CJ_Q4_K) return plan_gemv_q4k(rows, cols, pro, epi);
     GemvPlan p;
+    if (type == CJ_MXFP4 && pro == CJ_PRO_MXQ8) {
+        // 32 rows a workgroup (four a 32-lane half-wave, their 16-byte
+        // code loads in flight together); KB blocks a lane a sweep
+        const int64_t nb = cols / 32;
+        const int kb = (int)std::min<int64_t>(4, std::max<int64_t>(1, (nb + 31) / 32));
+        const char ec = epi == CJ_EPI_STORE ? 's' : epi == CJ_EPI_ACCUM ? 'a' : epi == CJ_EPI_GLU ? 'g' : '?';
+        p.kernel = std::string("cj_gemv_mxq8_") + ec + "_k" + std::to_string(kb);
+        p.rows_per_wg = 32;
+        p.grid = (uint32_t)((rows + 31) / 32);
+        p.per_copy = p.grid;
+        p.lds = 3072 + (uint32_t)((cols + 15) & ~15) + (uint32_t)((nb + 3) & ~3) * 4 + 32 * 4;
+        return p;
+    }
     const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
                       : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
     if (is_f32_act(type)) {
@@ -376,6 +391,13 @@ int32_t cj_init(int32_t device) {
         hipFunction_t f;
         if (hipModuleGetFunction(&f, g.module, k) == hipSuccess) g.fns[k] = f;
     }
+    // MXFP4 × q8: epilogue {s, a, g} × blocks a lane a sweep
+    for (const char *e : {"s", "a", "g"})
+        for (const char *kb : {"1", "2", "3", "4"}) {
+            const std::string k = std::string("cj_gemv_mxq8_") + e + "_k" + kb;
+            hipFunction_t f;
+            if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+        }
     // the Q4_K family: prologue {c, p, n} × epilogue {s, a, q, g, m} × width
     for (const char *pro : {"c", "p", "n"})
         for (const char *epi : {"s", "a", "q", "g", "m"})
@@ -588,6 +610,20 @@ int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows,
     a.y = (float *)dptr(y); a.y_off = y_off; a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type;
     a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.per32 = type == CJ_Q8_0; a.batch = 1;
     return run_gemv(a, plan_gemv(type, rows, cols, 32, a.pro, a.epi));
+}
+
+int32_t cj_matvec_mxfp4_q8(int64_t y, int64_t w, int64_t x, int64_t rows, int64_t cols, int64_t y_off, int32_t accum) {
+    const int64_t prb = prepared_row_bytes(CJ_MXFP4, cols);
+    if (prb <= 0 || rows <= 0) return fail(CJ_ERR_ARG, "cj_matvec_mxfp4_q8: %lld columns are not whole 32-element blocks", (long long)cols);
+    if (!in_buffer(dptr(w), rows * prb)) return fail(CJ_ERR_ARG, "cj_matvec_mxfp4_q8: weight smaller than %lld prepared rows", (long long)rows);
+    if (!in_buffer(dptr(x), cols * 4) || ((uintptr_t)dptr(x) & 15))
+        return fail(CJ_ERR_ARG, "cj_matvec_mxfp4_q8: activation smaller than %lld floats or not 16-byte aligned", (long long)cols);
+    if (y_off < 0 || !in_buffer(dptr(y + 4 * y_off), rows * 4)) return fail(CJ_ERR_ARG, "cj_matvec_mxfp4_q8: output smaller than y_off + rows");
+    cj_gemv_args a{};
+    a.w = (const uint8_t *)dptr(w); a.x = (const float *)dptr(x); a.y = (float *)dptr(y); a.y_off = y_off;
+    a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = CJ_MXFP4; a.pro = CJ_PRO_MXQ8;
+    a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.batch = 1;
+    return run_gemv(a, plan_gemv(CJ_MXFP4, rows, cols, 32, a.pro, a.epi));
 }
 
 int32_t cj_matmul(int32_t type, int64_t y, int64_t w, int64_t xp, int64_t rows, int64_t cols, int32_t ncols,

@@ -44,6 +44,7 @@ SIGNATURES = {
     "cj_prepared_row_bytes": (I64, [I32, I64]),
     "cj_prepare_weight": (I32, [I64, I64, I32, I64, I64]),
     "cj_matvec": (I32, [I32, I64, I64, I64, I64, I64, I64, I32]),
+    "cj_matvec_mxfp4_q8": (I32, [I64, I64, I64, I64, I64, I64, I32]),
     "cj_matmul": (I32, [I32, I64, I64, I64, I64, I64, I32, I64, I64, I64, I32]),
     "cj_glu": (I32, [I64, I64, I64, I64, I64, I32, I32]),
     "cj_add": (I32, [I64, I64, I64]),

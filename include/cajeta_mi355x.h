@@ -118,6 +118,17 @@ int32_t cj_prepare_weight(int64_t dst, int64_t src, int32_t type, int64_t rows, 
 int32_t cj_matvec(int32_t type, int64_t y, int64_t w, int64_t act, int64_t rows, int64_t cols,
                   int64_t y_off, int32_t accum);
 
+/* y[y_off + r] (+)= the MXFP4 mat-vec in the reference's device Q8 form over
+ * a PREPARED MXFP4 weight and f32 x (16-byte aligned, cols a multiple of
+ * 32): x quantized per 32 elements (q = round-half-away(x·127/max|x|),
+ * scale max|x|/127), each row an exact integer dot a block folded by 32
+ * lanes and their xor-butterfly sum — the arithmetic the engine's MoE
+ * experts use. Replaces QuantKernel.mxfp4MatVecCoopQ8Launch
+ * (io/QuantKernel.cajeta:43699-43713: mxfp4QuantActKernel :43614 and
+ * mxfp4MatVecKernelCoopQ8 :43660). */
+int32_t cj_matvec_mxfp4_q8(int64_t y, int64_t w, int64_t x, int64_t rows, int64_t cols, int64_t y_off,
+                           int32_t accum);
+
 /* Y[c][y_off + r] (+)= Σ_k W[r][k]·x_c[k] for ncols activation columns at once,
  * on the int8 matrix cores, each column bit-for-bit what cj_matvec gives it.
  * `xp` holds the columns' packs (per-256 for Q4_K, per-32 for Q8_0)

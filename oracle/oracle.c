@@ -377,7 +377,86 @@ static void mv_mxfp4(const uint8_t *w, int64_t rows, int64_t cols, const float *
     }
 }
 
-/* F32 weights (the MoE router): plain row dot in column order. */
+/* MXFP4 in the reference's device Q8 form, the two kernels of
+ * QuantKernel.mxfp4MatVecCoopQ8Launch (L/io/QuantKernel.cajeta:43699-43713).
+ *
+ * mxfp4QuantActKernel (:43614-43636): per 32-element block the largest
+ * |x| (order free: max is exact), inv = 127 / bmax (0 for an all-zero
+ * block), q = Math.round(x·inv) (half away from zero, as the packs),
+ * d = bmax / 127. */
+void or_mxfp4_quant_act(const float *x, int64_t cols, int8_t *xq, float *xd) {
+    for (int64_t b = 0; b < cols / 32; b++) {
+        float bmax = 0.0f;
+        for (int k = 0; k < 32; k++) {
+            float v = fabsf(x[32 * b + k]);
+            if (v > bmax) bmax = v;
+        }
+        float inv = bmax > 0.0f ? 127.0f / bmax : 0.0f;
+        for (int k = 0; k < 32; k++) {
+#if OR_PLANT == 15
+            xq[32 * b + k] = (int8_t)round_away(x[32 * b + k] * inv * 0.5f);   /* planted: half the codes */
+#else
+            xq[32 * b + k] = (int8_t)round_away(x[32 * b + k] * inv);
+#endif
+        }
+        xd[b] = bmax / 127.0f;
+    }
+}
+
+/* mxfp4MatVecKernelCoopQ8 (:43660-43697): a row is a wave of 32 lanes; lane
+ * L takes blocks L, L+32, ... in turn: s = the exact integer dot of the
+ * block's 32 codes (Quant.mxfp4Kv's int8 table, :43273-43276; low nibbles
+ * are elements 0..15, high 16..31) with the q8 codes, then
+ * acc = acc + (float)s·d_w·d_x (left to right). The lanes' sums are folded
+ * by Wave.reduceSumF32 over the 32 lanes, the xor butterfly (strides 16, 8,
+ * 4, 2, 1: lane L adds lane L^k; specs/archive/wave-agnostic-coop-kernels-
+ * spec.md:22-25 describes the wave reduces as that butterfly). */
+static void mv_mxfp4_q8(const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq, const float *xd, float *y) {
+    static const int8_t kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+    int64_t bpr = cols / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; i++) {
+        float acc[32];
+        for (int l = 0; l < 32; l++) {
+            acc[l] = 0.0f;
+            for (int64_t b = l; b < bpr; b += 32) {
+                const uint8_t *r = w + (i * bpr + b) * 17;
+                float dw = mxfp4_scale(r[0]);
+                const int8_t *xb = xq + b * 32;
+                int32_t sdot = 0;
+                for (int j = 0; j < 16; j++) {
+                    sdot += kv[r[1 + j] & 15] * xb[j];
+#if OR_PLANT == 16
+                    sdot += kv[(r[1 + j] >> 4) & 15] * xb[j];          /* planted: high nibbles on the low half */
+#else
+                    sdot += kv[(r[1 + j] >> 4) & 15] * xb[16 + j];
+#endif
+                }
+                acc[l] = acc[l] + (float)sdot * dw * xd[b];
+            }
+        }
+        for (int k = 16; k > 0; k >>= 1)
+            for (int l = 0; l < 32; l++)
+                if (l < k) acc[l] = acc[l] + acc[l + k];
+        y[i] = acc[0];
+    }
+}
+
+/* Both kernels over an f32 activation: the MXFP4 mat-vec the engine's MoE
+ * experts use. */
+int or_matvec_mxfp4_q8(const uint8_t *w, int64_t rows, int64_t cols, const float *x, float *y) {
+    if (cols % 32) return -1;
+    int8_t *xq = (int8_t *)malloc((size_t)cols);
+    float *xd = (float *)malloc(sizeof(float) * (size_t)(cols / 32));
+    or_mxfp4_quant_act(x, cols, xq, xd);
+    mv_mxfp4_q8(w, rows, cols, xq, xd, y);
+    free(xq); free(xd);
+    return 0;
+}
+
+/* F32 weights (the MoE router): HostOps.matvecRow (L/model/HostOps.cajeta:52-89),
+ * the CPU backend's unpacked f32 Linear (Linear.matvecInto, L/model/Linear.cajeta:1996):
+ * each output starts at 0 and adds x_i·w_i for i ascending. */
 static void mv_f32(const float *w, int64_t rows, int64_t cols, const float *x, float *y) {
     for (int64_t i = 0; i < rows; i++) {
         float acc = 0.0f;
@@ -964,7 +1043,11 @@ static int act32(int type) { return type == OR_Q8_0; }
 /* Stage x (n values) as the activation `type` reads, then y = W·x. */
 static void linear(or_model *m, const or_tensor *w, const float *x, float *y) {
     int64_t npad = (w->cols + 255) / 256 * 256;
-    if (w->type == OR_Q4_0 || w->type == OR_MXFP4 || w->type == OR_F32) {
+    if (w->type == OR_MXFP4) {   /* the device Q8 form (mxfp4MatVecCoopQ8Launch) */
+        or_matvec_mxfp4_q8(w->data, w->rows, w->cols, x, y);
+        return;
+    }
+    if (w->type == OR_Q4_0 || w->type == OR_F32) {
         or_matvec(w->type, w->data, w->rows, w->cols, NULL, x, y);
         return;
     }

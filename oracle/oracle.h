@@ -54,6 +54,10 @@ void or_q8k_pack32(const float *x, int64_t n, int64_t npad, uint8_t *out);
  * per-32 pack (xp); Q4_0 and MXFP4 read f32 activations (xf). */
 int or_matvec(int type, const uint8_t *w, int64_t rows, int64_t cols,
               const uint8_t *xp, const float *xf, float *y);
+/* MXFP4 in the reference's device Q8 form: the per-32 activation quant
+ * (xq: cols int8, xd: cols/32 scales) and the mat-vec over it. */
+void or_mxfp4_quant_act(const float *x, int64_t cols, int8_t *xq, float *xd);
+int or_matvec_mxfp4_q8(const uint8_t *w, int64_t rows, int64_t cols, const float *x, float *y);
 
 /* primitives */
 void  or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out);

@@ -66,6 +66,8 @@ def _configure(L):
             "or_dequant": (I32, [I32, P, I64, P]),
             "or_q8k_pack": (None, [P, I64, I64, P]), "or_q8k_pack32": (None, [P, I64, I64, P]),
             "or_matvec": (I32, [I32, P, I64, I64, P, P, P]),
+            "or_mxfp4_quant_act": (None, [P, I64, P, P]),
+            "or_matvec_mxfp4_q8": (I32, [P, I64, I64, P, P]),
             "or_rmsnorm": (None, [P, P, I64, F, I32, P]),
             "or_glu_exp": (None, [P, P, I64, P]), "or_glu_tanh": (None, [P, P, I64, P]),
             "or_inv_freq": (None, [I32, F, P]), "or_rope": (None, [P, I32, I32, I32, P]),
@@ -134,6 +136,25 @@ def matvec(ty, w, rows, cols, x):
     elif ty == Q8_0:
         xp = q8k_pack(x, per32=True)
     assert lib().or_matvec(ty, _p(w), rows, cols, _p(xp), _p(x), _p(y)) == 0
+    return y
+
+
+def mxfp4_quant_act(x):
+    """The per-32 activation quant of the MXFP4 device Q8 form: (int8 codes, scales)."""
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.empty(x.size, np.int8)
+    xd = np.empty(x.size // 32, np.float32)
+    lib().or_mxfp4_quant_act(_p(x), x.size, _p(xq), _p(xd))
+    return xq, xd
+
+
+def matvec_mxfp4_q8(w, rows, cols, x):
+    """y = W x in the MXFP4 device Q8 form (activation quant, then the
+    32-lane integer dot and butterfly)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    assert lib().or_matvec_mxfp4_q8(_p(w), rows, cols, _p(x), _p(y)) == 0
     return y
 
 

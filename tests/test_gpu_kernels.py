@@ -172,6 +172,35 @@ def test_matvec_accumulate_store(gpu, O, name, ty):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,cols,accum", [(5760, 2880, 0), (2880, 2880, 1), (24, 32, 0), (40, 96, 0),
+                                             (7, 4096, 1), (9, 4128, 0), (33, 8192, 0), (11520, 2880, 0)])
+def test_matvec_mxfp4_q8_matches_oracle(gpu, O, rows, cols, accum):
+    """The MXFP4 device Q8 form (the engine's MoE experts): per-32 activation
+    codes, the integer block dots over 32 lanes and their butterfly, bit for
+    bit the oracle's restatement; 1 to 4 blocks a lane a sweep, and more
+    sweeps past 4096 columns. Activations with a spread of block scales and
+    exact zeros (an all-zero block quantizes to zeros with scale 0)."""
+    say("mxfp4 q8", rows, cols, accum)
+    rng = np.random.default_rng(rows * 7 + cols)
+    raw = rand_blocks(O, O.MXFP4, rows * cols // 32, rng)
+    x = (rng.standard_normal(cols) * rng.uniform(0.05, 5, cols // 32).repeat(32)).astype(np.float32)
+    x[:32] = 0.0
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(O.MXFP4, cols)
+    src, w = gpu.Buffer.of(raw), gpu.Buffer(prb * rows)
+    gpu.native.check(lib.cj_prepare_weight(w.h, src.h, O.MXFP4, rows, cols), "prepare")
+    y0 = rng.standard_normal(rows + 3).astype(np.float32)
+    xb, y = gpu.Buffer.of(x), gpu.Buffer.of(y0)
+    gpu.native.check(lib.cj_matvec_mxfp4_q8(y.h, w.h, xb.h, rows, cols, 3, accum), "matvec_mxfp4_q8")
+    got = y.download(np.float32, rows + 3)
+    ref = O.matvec_mxfp4_q8(raw, rows, cols, x)
+    if accum:
+        ref = (y0[3:] + ref).astype(np.float32)
+    assert np.array_equal(got[:3].view(np.uint32), y0[:3].view(np.uint32)), "y_off prefix touched"
+    assert np.array_equal(got[3:].view(np.uint32), ref.view(np.uint32)), \
+        "%dx%d: %d rows differ" % (rows, cols, int((got[3:] != ref).sum()))
+
+
 def test_matvec_refuses_short_buffers(gpu, O):
     lib = gpu.native.lib()
     w, act, y = gpu.Buffer(1024), gpu.Buffer(320), gpu.Buffer(16)

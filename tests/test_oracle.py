@@ -112,6 +112,46 @@ def check_matvec(O, ty, rows=24, cols=1024, seed=3):
     return e < 2e-6, e
 
 
+def check_mxfp4_q8(O):
+    """The MXFP4 device Q8 form. The activation quant: closed forms (the
+    block maximum maps to ±127, exact halves away from zero, an all-zero
+    block to zeros with scale 0) and, on random blocks, every value within
+    half a step of its code. The mat-vec: against a float64 product of the
+    dequantised weights (pinned by mxfp4_ref.bin) with the values the codes
+    stand for — only f32 accumulation rounding may differ — and against the
+    unquantised x within the quantisation bound Σ|w|·d/2."""
+    bad = []
+    x = np.zeros(96, np.float32)
+    x[0], x[1], x[2], x[3], x[4] = 127.0, 2.5, -2.5, 0.5, -126.5
+    x[33], x[40] = -254.0, 127.0          # block 1: scale 2, 127 -> 63.5 -> 64
+    xq, xd = O.mxfp4_quant_act(x)
+    if list(xq[:5]) != [127, 3, -3, 1, -127] or xd[0] != np.float32(1.0):
+        bad.append(("block 0", list(xq[:5]), float(xd[0])))
+    if xq[33] != -127 or xq[40] != 64 or xd[1] != np.float32(2.0):
+        bad.append(("block 1", int(xq[33]), int(xq[40]), float(xd[1])))
+    if np.any(xq[64:]) or xd[2] != 0.0:
+        bad.append(("zero block", float(xd[2])))
+    rng = np.random.default_rng(39)
+    for rows, cols in ((24, 2880), (8, 32), (5, 1056), (3, 4096)):
+        xr = (rng.standard_normal(cols) * rng.uniform(0.1, 10, cols // 32).repeat(32)).astype(np.float32)
+        xq, xd = O.mxfp4_quant_act(xr)
+        step = np.repeat(xd.astype(np.float64), 32)
+        xhat = xq.astype(np.float64) * step
+        if np.max(np.abs(xhat - xr) - step / 2) > 1e-6 * np.max(np.abs(xr)) or \
+                np.any(np.abs(xq.reshape(-1, 32)).max(1) != 127):
+            bad.append(("quant bound", cols))
+        raw = rand_blocks(O, O.MXFP4, rows * cols // 32, rng)
+        W = O.dequant(O.MXFP4, raw).astype(np.float64).reshape(rows, cols)
+        got = O.matvec_mxfp4_q8(raw, rows, cols, xr)
+        e = rel_err(got, W @ xhat)
+        if e > 2e-6:
+            bad.append(("dot", rows, cols, e))
+        lim = np.abs(W) @ (step / 2) + 1e-5 * np.max(np.abs(W @ xhat))
+        if np.any(np.abs(got - W @ xr.astype(np.float64)) > lim):
+            bad.append(("bound", rows, cols))
+    return not bad, bad
+
+
 def check_rmsnorm(O):
     bad = []
     for n, scale in ((4096, 1.0), (2880, 1.0), (512, 3e-3)):   # the last: eps matters
@@ -332,10 +372,21 @@ def moe_toy(O, seed=11):
     return c, t
 
 
+def q8_32(v):
+    """The values the MXFP4 experts' per-32 activation codes stand for, in
+    float64: q = round-half-away(v·127/max|v|) per block, times max|v|/127."""
+    b = v.reshape(-1, 32)
+    amax = np.abs(b).max(1, keepdims=True)
+    inv = np.where(amax > 0, 127.0 / np.where(amax > 0, amax, 1.0), 0.0)
+    q = np.sign(b) * np.floor(np.abs(b) * inv + 0.5)
+    return (q * amax / 127.0).ravel()
+
+
 def moe_forward64(O, c, t, toks):
     """float64 forward of moe_toy's model over `toks` (positions 0..): f16
     K/V, the window clamp
-    from = p + 1 - w (PagedKvCache.attendRow), routing on f64 probabilities."""
+    from = p + 1 - w (PagedKvCache.attendRow), routing on f64 probabilities,
+    the experts' inputs at their per-32 codes' values (the MXFP4 Q8 form)."""
     H, nh, nkv, hd, eps = c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["eps"]
     E, K, F = c["n_experts"], c["n_used"], c["expert_ffn"]
     W = {k: O.dequant(ty, raw).astype(np.float64).reshape(rows, cols) for k, (ty, raw, rows, cols) in t.items()}
@@ -385,10 +436,11 @@ def moe_forward64(O, c, t, toks):
             sel = sorted(range(E), key=lambda i: (-pr[i], i))[:K]
             wts = pr[sel] / pr[sel].sum()
             y = np.zeros(H)
+            xq = q8_32(xn)
             for e, we in zip(sel, wts):
-                gg = W[p + "ffn_gate_exps.weight"][e * F:(e + 1) * F] @ xn
-                uu = W[p + "ffn_up_exps.weight"][e * F:(e + 1) * F] @ xn
-                y += we * (W[p + "ffn_down_exps.weight"][e * H:(e + 1) * H] @ (gg / (1 + np.exp(-gg)) * uu))
+                gg = W[p + "ffn_gate_exps.weight"][e * F:(e + 1) * F] @ xq
+                uu = W[p + "ffn_up_exps.weight"][e * F:(e + 1) * F] @ xq
+                y += we * (W[p + "ffn_down_exps.weight"][e * H:(e + 1) * H] @ q8_32(gg / (1 + np.exp(-gg)) * uu))
             hs = hs + y
         out.append(lin("output.weight", norm(hs, W["output_norm.weight"])))
     return out
@@ -620,6 +672,11 @@ def test_decode_splits_closed_form(O):
     assert O.cpu_decode_splits(100, 2, 8, 24) == 3
 
 
+def test_mxfp4_device_q8_form(O):
+    ok, bad = check_mxfp4_q8(O)
+    assert ok, bad
+
+
 def test_moe_route_against_float64(O):
     ok, bad = check_moe_route(O)
     assert ok, bad
@@ -768,6 +825,8 @@ PLANTS = {
     12: ("router weights not renormalised", check_moe_route),
     13: ("sliding window one position short", check_moe_model),
     14: ("MoE model without the renormalisation", check_moe_model),
+    15: ("MXFP4 activation codes at half scale", check_mxfp4_q8),
+    16: ("MXFP4 high nibbles against the low activation half", check_mxfp4_q8),
 }
 # 14 is plant 12 again, caught at model level as well (the tie order of plant
 # 11 needs an exact tie, which only check_moe_route constructs)
