@@ -387,21 +387,23 @@ SPLIT_KERNEL(8)
 // partial i (i < 32) adds q[d]·k[d] for d = i, i+32, ... from 0, then the
 // xor-butterfly's pairs (16, 8, 4, 2, 1) fold the partials — a fixed tree, so
 // one lane can form all of it. Lane = position: a workgroup takes 256
-// positions of one kv head (grid: position blocks × kv heads), loads each K
-// row once and scores it against every query head of the group (q in LDS,
-// read as broadcasts). Dynamic LDS: group × HD floats.
+// positions of one query head (grid: position blocks × query heads; the
+// group's heads read the same K rows, from L2 after the first), q in LDS
+// read as broadcasts. A head a workgroup keeps each lane's chain of
+// products short: the scores of a 4096-position span take 8× fewer
+// dependent steps than a workgroup per kv head.
 template <int HD>
-DEV void scores_body(const cj_attn_args &a, int bx, int kvh) {
-    extern __shared__ __align__(16) float qs[];
+DEV void scores_body(const cj_attn_args &a, int bx, int h) {
+    __shared__ __align__(16) float qs[HD];
     int count, from;
     attn_window(a, count, from);
-    const int grp = a.n_q / a.n_kv;
+    const int grp = a.n_q / a.n_kv, kvh = h / grp;
     const int t = bx * 256 + threadIdx.x;
     if (bx * 256 >= count) return;      // the whole workgroup idles past count
     // the page entry is requested with q (the K row's address waits on it)
     const int pos = from + min(t, count - 1);
     const int page = a.pgtab[a.pg_base + (pos >> 6)];
-    for (int i = threadIdx.x; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
+    for (int i = threadIdx.x; i < HD; i += 256) qs[i] = a.q[(int64_t)h * HD + i];
     __syncthreads();
     if (t >= count) return;
     const uint16_t *kr = a.kc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD;
@@ -414,29 +416,26 @@ DEV void scores_body(const cj_attn_args &a, int bx, int kvh) {
         k[8 * j + 4] = h2f(v.z); k[8 * j + 5] = h2f(v.z >> 16);
         k[8 * j + 6] = h2f(v.w); k[8 * j + 7] = h2f(v.w >> 16);
     }
-    for (int g = 0; g < grp; g++) {
-        const float *q = qs + g * HD;
-        float p[32];
+    float p[32];
 #pragma unroll
-        for (int i = 0; i < 32; i++) p[i] = 0.0f;
+    for (int i = 0; i < 32; i++) p[i] = 0.0f;
 #pragma unroll
-        for (int d0 = 0; d0 < HD; d0 += 32) {
+    for (int d0 = 0; d0 < HD; d0 += 32) {
 #pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                const float4 qv = *(const float4 *)(q + d0 + i);
-                p[i] = __fadd_rn(p[i], __fmul_rn(qv.x, k[d0 + i]));
-                p[i + 1] = __fadd_rn(p[i + 1], __fmul_rn(qv.y, k[d0 + i + 1]));
-                p[i + 2] = __fadd_rn(p[i + 2], __fmul_rn(qv.z, k[d0 + i + 2]));
-                p[i + 3] = __fadd_rn(p[i + 3], __fmul_rn(qv.w, k[d0 + i + 3]));
-            }
+        for (int i = 0; i < 32; i += 4) {
+            const float4 qv = *(const float4 *)(qs + d0 + i);
+            p[i] = __fadd_rn(p[i], __fmul_rn(qv.x, k[d0 + i]));
+            p[i + 1] = __fadd_rn(p[i + 1], __fmul_rn(qv.y, k[d0 + i + 1]));
+            p[i + 2] = __fadd_rn(p[i + 2], __fmul_rn(qv.z, k[d0 + i + 2]));
+            p[i + 3] = __fadd_rn(p[i + 3], __fmul_rn(qv.w, k[d0 + i + 3]));
         }
-#pragma unroll
-        for (int m = 16; m > 0; m >>= 1) {
-#pragma unroll
-            for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
-        }
-        a.part[(int64_t)(kvh * grp + g) * a.splits + t] = __fmul_rn(p[0], a.scale);
     }
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) {
+#pragma unroll
+        for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
+    }
+    a.part[(int64_t)h * a.splits + t] = __fmul_rn(p[0], a.scale);
 }
 
 #define COMBINE_PAGES 2048   // K/V pages a two-pass span covers (131072 positions)
@@ -743,11 +742,11 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_ar
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a, blockIdx.x); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a, blockIdx.x); }
 // The many-row forms (batched decode, and prefill chunks of the models that
-// prefill a decode step a position): grid y is row · n_kv + kv head for the
-// scores, the row for the combine.
+// prefill a decode step a position): grid y is row · n_q + query head for
+// the scores, the row for the combine.
 #define TWO_PASS_ROWS(HD)                                                                                   \
     extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_rows_h##HD(cj_attn_args a) {          \
-        scores_body<HD>(attn_row_args(a, blockIdx.y / a.n_kv), blockIdx.x, blockIdx.y % a.n_kv);           \
+        scores_body<HD>(attn_row_args(a, blockIdx.y / a.n_q), blockIdx.x, blockIdx.y % a.n_q);             \
     }                                                                                                       \
     extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_rows_h##HD(cj_attn_args a) {         \
         combine_body<HD>(attn_row_args(a, blockIdx.y), blockIdx.x);                                         \
@@ -756,27 +755,27 @@ TWO_PASS_ROWS(64)
 TWO_PASS_ROWS(128)
 
 // The two-pass form in one launch for spans of at most FUSED_SPAN(HD)
-// positions (sliding windows, small contexts): a workgroup per kv head
-// stages q, K and V of the span in LDS, then forms each query head's scores,
+// positions (sliding windows, small contexts): a workgroup per query head
+// stages q, K and V of the span in LDS, then forms the head's scores,
 // softmax and p·V with exactly the two kernels' operations — a score per
 // lane (the butterfly's fixed tree of 32 strided partials, then ·scale), the
 // max, the 128-lane ordered sums and their stride-halving tree, and each
 // output dimension's ascending-t sum — so its results are theirs bit for bit.
 #define FUSED_SPAN(HD) ((HD) == 64 ? 256 : 128)
 template <int HD>
-DEV void fused_body(const cj_attn_args &a, int kvh) {
+DEV void fused_body(const cj_attn_args &a, int h) {
     constexpr int SPAN = FUSED_SPAN(HD);
     __shared__ __align__(16) uint16_t ks[SPAN * HD], vs[SPAN * HD];
-    __shared__ __align__(16) float qs[8 * HD];
-    __shared__ float sc[8][SPAN];
-    __shared__ float red[2][128], mred[8];
-    __shared__ float rsv[8];
+    __shared__ __align__(16) float qs[HD];
+    __shared__ float sc[SPAN];
+    __shared__ float red[128], mred[2];
+    __shared__ float rsv;
     int count, from;
     attn_window(a, count, from);
-    const int l = threadIdx.x, grp = a.n_q / a.n_kv;
-    // q of the group, then K and V rows of the span (chunk c of row t: the
-    // page entry of the row, then its 16 bytes), all loads issued together
-    for (int i = l; i < grp * HD; i += 256) qs[i] = a.q[(int64_t)kvh * grp * HD + i];
+    const int l = threadIdx.x, grp = a.n_q / a.n_kv, kvh = h / grp;
+    // q, then K and V rows of the span (chunk c of row t: the page entry of
+    // the row, then its 16 bytes), all loads issued together
+    for (int i = l; i < HD; i += 256) qs[i] = a.q[(int64_t)h * HD + i];
     constexpr int CH = HD / 8, NC = SPAN * CH / 256;
     u32x4 kr[NC], vr[NC];
 #pragma unroll
@@ -794,79 +793,69 @@ DEV void fused_body(const cj_attn_args &a, int kvh) {
         *(u32x4 *)(vs + 8 * c) = vr[k];
     }
     __syncthreads();
-    // scores: lane t, every head of the group
+    // scores: lane t
     if (l < count) {
         float k[HD];
 #pragma unroll
         for (int d = 0; d < HD; d++) k[d] = h2f(ks[l * HD + d]);
-        for (int g = 0; g < grp; g++) {
-            const float *q = qs + g * HD;
-            float p[32];
+        float p[32];
 #pragma unroll
-            for (int i = 0; i < 32; i++) p[i] = 0.0f;
+        for (int i = 0; i < 32; i++) p[i] = 0.0f;
 #pragma unroll
-            for (int d0 = 0; d0 < HD; d0 += 32) {
+        for (int d0 = 0; d0 < HD; d0 += 32) {
 #pragma unroll
-                for (int i = 0; i < 32; i++) p[i] = __fadd_rn(p[i], __fmul_rn(q[d0 + i], k[d0 + i]));
-            }
-#pragma unroll
-            for (int m = 16; m > 0; m >>= 1) {
-#pragma unroll
-                for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
-            }
-            sc[g][l] = __fmul_rn(p[0], a.scale);
+            for (int i = 0; i < 32; i++) p[i] = __fadd_rn(p[i], __fmul_rn(qs[d0 + i], k[d0 + i]));
         }
+#pragma unroll
+        for (int m = 16; m > 0; m >>= 1) {
+#pragma unroll
+            for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
+        }
+        sc[l] = __fmul_rn(p[0], a.scale);
     }
     __syncthreads();
-    // softmax, two heads at a time (128 lanes each: lane j takes t = j, j + 128)
-    for (int g0 = 0; g0 < grp; g0 += 2) {
-        const int g = g0 + (l >> 7), j = l & 127;
-        const bool on = g < grp;
-        float mx = -3.0e38f;
-        if (on) {
-            for (int t = j; t < count; t += 128) if (sc[g][t] > mx) mx = sc[g][t];
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float y = __shfl_xor(mx, o);
-            if (y > mx) mx = y;
-        }
-        if ((l & 63) == 0) mred[l >> 6] = mx;
-        __syncthreads();
-        const float m = mred[2 * (l >> 7)] > mred[2 * (l >> 7) + 1] ? mred[2 * (l >> 7)] : mred[2 * (l >> 7) + 1];
-        float s = 0.0f;
-        if (on) {
-            for (int t = j; t < count; t += 128) {
-                const float e = cj_expf(sc[g][t] - m);
-                sc[g][t] = e;
-                s = __fadd_rn(s, e);
-            }
-        }
-        red[l >> 7][j] = s;
-        __syncthreads();
-        if ((l & 127) < 64) {
-            float v2 = __fadd_rn(red[l >> 7][j], red[l >> 7][j + 64]);
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
-            if (j == 0 && on) rsv[g] = __fdiv_rn(1.0f, v2);
-        }
-        __syncthreads();
+    // softmax over lanes 0..127 (lane j takes t = j, j + 128)
+    const int j = l & 127;
+    float mx = -3.0e38f;
+    if (l < 128) {
+        for (int t = j; t < count; t += 128) if (sc[t] > mx) mx = sc[t];
     }
-    // p·V: chain (g, d) on thread (g·HD + d) mod 256, heads in turn
-    for (int c0 = 0; c0 < grp * HD; c0 += 256) {
-        const int c = c0 + l;
-        if (c < grp * HD) {
-            const int g = c / HD, d = c % HD;
-            float acc = 0.0f;
-            for (int t = 0; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(sc[g][t], h2f(vs[t * HD + d])));
-            a.out[((int64_t)kvh * grp + g) * HD + d] = __fmul_rn(acc, rsv[g]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float y = __shfl_xor(mx, o);
+        if (y > mx) mx = y;
+    }
+    if (l < 128 && (l & 63) == 0) mred[l >> 6] = mx;
+    __syncthreads();
+    const float m = mred[1] > mred[0] ? mred[1] : mred[0];
+    float s = 0.0f;
+    if (l < 128) {
+        for (int t = j; t < count; t += 128) {
+            const float e = cj_expf(sc[t] - m);
+            sc[t] = e;
+            s = __fadd_rn(s, e);
         }
+        red[j] = s;
+    }
+    __syncthreads();
+    if (l < 64) {
+        float v2 = __fadd_rn(red[l], red[l + 64]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        if (l == 0) rsv = __fdiv_rn(1.0f, v2);
+    }
+    __syncthreads();
+    // p·V: output dimension d's ascending-t chain on lane d
+    if (l < HD) {
+        float acc = 0.0f;
+        for (int t = 0; t < count; t++) acc = __fadd_rn(acc, __fmul_rn(sc[t], h2f(vs[t * HD + l])));
+        a.out[(int64_t)h * HD + l] = __fmul_rn(acc, rsv);
     }
 }
 
 extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) { fused_body<64>(a, blockIdx.x); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) { fused_body<128>(a, blockIdx.x); }
-// many rows: grid (n_kv, rows)
+// many rows: grid (n_q, rows)
 extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h64(cj_attn_args a) {
     fused_body<64>(attn_row_args(a, blockIdx.y), blockIdx.x);
 }

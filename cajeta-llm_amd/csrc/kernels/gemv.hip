@@ -1156,7 +1156,7 @@ DEV uint32_t e2m1_x4(uint32_t v) {
 // The LDS layout after the scratch: codes [cols], scales [nb], row values [R].
 DEV int mxq8_xd_off(int64_t cols) { return (int)((cols + 15) & ~15); }
 
-template <int EPI, int KB>
+template <int EPI, int KB, int RW>
 DEV void mxq8_body(const cj_gemv_args &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *red = (float *)smem;
@@ -1171,56 +1171,60 @@ DEV void mxq8_body(const cj_gemv_args &a) {
     const GemvSlice sl = gemv_slice(a);
     const EpiPre pre = epi_prefetch_t<EPI>(a, sl);
     (void)red;
-    // the activation's codes: a thread a 32-block
-    for (int b = t; b < nb; b += 256) {
-        const float4 *xs = (const float4 *)(sl.X + 32 * (int64_t)b);
-        float v[32];
+    u32x4 wv[RW][KB];
+    uint32_t sc[RW][KB];
+    auto fetch = [&](int i0, int c0) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 f = xs[k];
-            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        for (int i = 0; i < RW; i++) {
+            const int64_t r = min(sl.row0 + i0 + i, a.rows - 1);
+            const uint8_t *wr = sl.W + r * a.row_bytes;
+#pragma unroll
+            for (int k = 0; k < KB; k++) {
+                const int b = min(c0 + hl + 32 * k, nb - 1);
+                wv[i][k] = __builtin_nontemporal_load((const u32x4 *)(wr + 16 * b));
+                sc[i][k] = wr[16 * nb + b];
+            }
         }
-        float bm = 0.0f;
+    };
+    // the activation's codes: eight lanes a 32-block, four values a lane;
+    // the block maximum by an xor exchange over the eight (max is exact)
+    {
+        constexpr int PR = 3;    // rounds of 32 blocks whose loads are issued together
+        for (int b0 = 0; b0 < nb; b0 += 32 * PR) {
+            float4 f[PR];
 #pragma unroll
-        for (int k = 0; k < 32; k++) {
-            const float av = fabsf(v[k]);
-            if (av > bm) bm = av;
+            for (int k = 0; k < PR; k++) {
+                const int b = min(b0 + 32 * k + (t >> 3), nb - 1);
+                f[k] = *(const float4 *)(sl.X + 32 * (int64_t)b + 4 * (t & 7));
+            }
+#pragma unroll
+            for (int k = 0; k < PR; k++) {
+                const int b = b0 + 32 * k + (t >> 3);
+                float bm = fmaxf(fmaxf(fabsf(f[k].x), fabsf(f[k].y)), fmaxf(fabsf(f[k].z), fabsf(f[k].w)));
+#pragma unroll
+                for (int m = 1; m < 8; m <<= 1) bm = fmaxf(bm, __shfl_xor(bm, m));
+                const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
+                const uint32_t q = ((uint32_t)round_away(__fmul_rn(f[k].x, inv)) & 0xFFu) |
+                                   (((uint32_t)round_away(__fmul_rn(f[k].y, inv)) & 0xFFu) << 8) |
+                                   (((uint32_t)round_away(__fmul_rn(f[k].z, inv)) & 0xFFu) << 16) |
+                                   (((uint32_t)round_away(__fmul_rn(f[k].w, inv)) & 0xFFu) << 24);
+                if (b < nb) {
+                    *(uint32_t *)(xq + 32 * b + 4 * (t & 7)) = q;
+                    if ((t & 7) == 0) xd[b] = __fdiv_rn(bm, 127.0f);
+                }
+            }
         }
-        const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
-        uint32_t q[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) w |= ((uint32_t)round_away(__fmul_rn(v[4 * k + j], inv)) & 0xFFu) << (8 * j);
-            q[k] = w;
-        }
-        *(u32x4 *)(xq + 32 * b) = u32x4{q[0], q[1], q[2], q[3]};
-        *(u32x4 *)(xq + 32 * b + 16) = u32x4{q[4], q[5], q[6], q[7]};
-        xd[b] = __fdiv_rn(bm, 127.0f);
     }
     __syncthreads();
     // rows: half-wave hw takes rows hw·RW .. +RW−1 of each 8·RW-row pass;
-    // every load is issued (clamped into range) before the first is used
-    constexpr int RW = 4;
+    // every load of a sweep is issued (clamped into range) before the first
+    // is used
     for (int i0 = hw * RW; i0 < R; i0 += 8 * RW) {
         float acc[RW];
 #pragma unroll
         for (int i = 0; i < RW; i++) acc[i] = 0.0f;
         for (int c0 = 0; c0 < nb; c0 += 32 * KB) {
-            u32x4 wv[RW][KB];
-            uint32_t sc[RW][KB];
-#pragma unroll
-            for (int i = 0; i < RW; i++) {
-                const int64_t r = min(sl.row0 + i0 + i, a.rows - 1);
-                const uint8_t *wr = sl.W + r * a.row_bytes;
-#pragma unroll
-                for (int k = 0; k < KB; k++) {
-                    const int b = min(c0 + hl + 32 * k, nb - 1);
-                    wv[i][k] = __builtin_nontemporal_load((const u32x4 *)(wr + 16 * b));
-                    sc[i][k] = wr[16 * nb + b];
-                }
-            }
+            fetch(i0, c0);
 #pragma unroll
             for (int i = 0; i < RW; i++) {
 #pragma unroll
@@ -1254,14 +1258,18 @@ DEV void mxq8_body(const cj_gemv_args &a) {
     gemv_epilogue_t<EPI>(a, sl, t < R ? res[t] : 0.0f, bmax, pre);
 }
 
-#define MXQ8_KERNEL(E, EPI, KB)                                                                     \
-    extern "C" __global__ void __launch_bounds__(256) cj_gemv_mxq8_##E##_k##KB(cj_gemv_args a) {    \
-        mxq8_body<EPI, KB>(a);                                                                      \
+#define MXQ8_KERNEL(E, EPI, KB, RW)                                                                    \
+    extern "C" __global__ void __launch_bounds__(256) cj_gemv_mxq8_##E##_k##KB##_r##RW(cj_gemv_args a) {  \
+        mxq8_body<EPI, KB, RW>(a);                                                                        \
     }
-#define MXQ8_KBS(E, EPI) MXQ8_KERNEL(E, EPI, 1) MXQ8_KERNEL(E, EPI, 2) MXQ8_KERNEL(E, EPI, 3) MXQ8_KERNEL(E, EPI, 4)
-MXQ8_KBS(s, CJ_EPI_STORE)
-MXQ8_KBS(a, CJ_EPI_ACCUM)
-MXQ8_KBS(g, CJ_EPI_GLU)
+#define MXQ8_KBS(E, EPI, RW) \
+    MXQ8_KERNEL(E, EPI, 1, RW) MXQ8_KERNEL(E, EPI, 2, RW) MXQ8_KERNEL(E, EPI, 3, RW) MXQ8_KERNEL(E, EPI, 4, RW)
+MXQ8_KBS(s, CJ_EPI_STORE, 2)
+MXQ8_KBS(s, CJ_EPI_STORE, 4)
+MXQ8_KBS(a, CJ_EPI_ACCUM, 2)
+MXQ8_KBS(a, CJ_EPI_ACCUM, 4)
+MXQ8_KBS(g, CJ_EPI_GLU, 2)
+MXQ8_KBS(g, CJ_EPI_GLU, 4)
 
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)

@@ -585,11 +585,10 @@ int Engine::enqueue_step(int s) {
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
                 if (span <= (head_dim == 64 ? 256 : 128)) {
                     // every step's span fits one workgroup: the one-launch form
-                    if ((rc = launch(fused_kernel, (uint32_t)n_kv, 256, 0, a))) return rc;
+                    if ((rc = launch(fused_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
                 } else {
                     // the grid covers the longest window; the kernel idles past count
-                    if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_kv, 256,
-                                      (uint32_t)(grp * head_dim * 4), a)))
+                    if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_heads, 256, 0, a)))
                         return rc;
                     if ((rc = launch(combine_kernel, (uint32_t)(n_heads * (head_dim / 32)), 256, 0, a))) return rc;
                 }
@@ -856,11 +855,10 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             char kname[48];
             if (span <= (head_dim == 64 ? 256 : 128)) {
                 snprintf(kname, sizeof kname, "cj_attn_fused_rows_h%d", head_dim);
-                if ((rc = launch2(kname, (uint32_t)n_kv, (uint32_t)n, 256, 0, a))) return rc;
+                if ((rc = launch2(kname, (uint32_t)n_heads, (uint32_t)n, 256, 0, a))) return rc;
             } else {
                 snprintf(kname, sizeof kname, "cj_attn_scores_rows_h%d", head_dim);
-                if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_kv), 256,
-                                  (uint32_t)(grp * head_dim * 4), a)))
+                if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_heads), 256, 0, a)))
                     return rc;
                 snprintf(kname, sizeof kname, "cj_attn_combine_rows_h%d", head_dim);
                 if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;

@@ -59,8 +59,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
         {"q40F32WaveMatVecKernel", "cj_gemv_q40"},
         {"mxfp4MatVecKernel", "cj_gemv_mxfp4"},
-        {"mxfp4MatVecKernelCoopQ8", "cj_gemv_mxq8_s_k3"},
-        {"mxfp4QuantActKernel", "cj_gemv_mxq8_s_k3"},   // the quant is that kernel's prologue
+        {"mxfp4MatVecKernelCoopQ8", "cj_gemv_mxq8_s_k3_r4"},
+        {"mxfp4QuantActKernel", "cj_gemv_mxq8_s_k3_r4"},   // the quant is that kernel's prologue
         {"q8kPackKernel", "cj_pack"},
         {"q8kPack32Kernel", "cj_pack"},
         {"rmsnormPackRowF32", "cj_pack"},
@@ -252,14 +252,16 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
     if (type == CJ_Q4_K) return plan_gemv_q4k(rows, cols, pro, epi);
     GemvPlan p;
     if (type == CJ_MXFP4 && pro == CJ_PRO_MXQ8) {
-        // 32 rows a workgroup (four a 32-lane half-wave, their 16-byte
-        // code loads in flight together); KB blocks a lane a sweep
+        // RW rows a 32-lane half-wave (their 16-byte code loads in flight
+        // together), 8·RW rows a workgroup: 32, or 16 for matrices of at
+        // most 4096 rows (twice the workgroups); KB blocks a lane a sweep
         const int64_t nb = cols / 32;
         const int kb = (int)std::min<int64_t>(4, std::max<int64_t>(1, (nb + 31) / 32));
+        const int rw = rows <= 4096 ? 2 : 4;
         const char ec = epi == CJ_EPI_STORE ? 's' : epi == CJ_EPI_ACCUM ? 'a' : epi == CJ_EPI_GLU ? 'g' : '?';
-        p.kernel = std::string("cj_gemv_mxq8_") + ec + "_k" + std::to_string(kb);
-        p.rows_per_wg = 32;
-        p.grid = (uint32_t)((rows + 31) / 32);
+        p.kernel = std::string("cj_gemv_mxq8_") + ec + "_k" + std::to_string(kb) + "_r" + std::to_string(rw);
+        p.rows_per_wg = 8 * rw;
+        p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
         p.per_copy = p.grid;
         p.lds = 3072 + (uint32_t)((cols + 15) & ~15) + (uint32_t)((nb + 3) & ~3) * 4 + 32 * 4;
         return p;
@@ -393,11 +395,12 @@ int32_t cj_init(int32_t device) {
     }
     // MXFP4 × q8: epilogue {s, a, g} × blocks a lane a sweep
     for (const char *e : {"s", "a", "g"})
-        for (const char *kb : {"1", "2", "3", "4"}) {
-            const std::string k = std::string("cj_gemv_mxq8_") + e + "_k" + kb;
-            hipFunction_t f;
-            if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
-        }
+        for (const char *kb : {"1", "2", "3", "4"})
+            for (const char *rw : {"2", "4"}) {
+                const std::string k = std::string("cj_gemv_mxq8_") + e + "_k" + kb + "_r" + rw;
+                hipFunction_t f;
+                if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+            }
     // the Q4_K family: prologue {c, p, n} × epilogue {s, a, q, g, m} × width
     for (const char *pro : {"c", "p", "n"})
         for (const char *epi : {"s", "a", "q", "g", "m"})
@@ -751,8 +754,7 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     }
     a.splits = count;   // the scores row stride
     snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
-    if (int32_t rc = launch2(name, (uint32_t)((count + 255) / 256), (uint32_t)n_kv, 256, (uint32_t)(grp * head_dim * 4), a))
-        return rc;
+    if (int32_t rc = launch2(name, (uint32_t)((count + 255) / 256), (uint32_t)n_q, 256, 0, a)) return rc;
     snprintf(name, sizeof name, "cj_attn_combine_h%d", head_dim);
     return launch(name, (uint32_t)(n_q * (head_dim / 32)), 256, 0, a);
 }
