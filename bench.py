@@ -89,15 +89,34 @@ def copy_reference(native, reps=20):
     return {"kernel": "cj_copy", "avg_us": round(us, 2), "bytes": moved, "GB/s": round(moved / (us * 1e-6) / 1e9, 1)}
 
 
-def cpu_baseline(pkg, image_name, vocab, budget_s, seed):
+def token_macs(cfg, count):
+    """Multiply-adds of one decode token of a model (GGUF-derived config) at
+    `count` attended positions: (weights, attention)."""
+    L, h, nh, nkv, hd = cfg["n_layers"], cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"]
+    proj = h * (nh * hd + 2 * nkv * hd) + nh * hd * h
+    if cfg["n_experts"]:
+        ffn = cfg["n_experts"] * h + cfg["n_used"] * 3 * h * cfg["expert_ffn"]
+    else:
+        ffn = 3 * h * cfg["ffn"]
+    weights = L * (proj + ffn) + cfg["vocab"] * h
+    attn = 0
+    for layer in range(L):
+        w = cfg["swa_window"] if cfg["swa_window"] and (layer + 1) % max(1, cfg["swa_pattern"]) else 0
+        attn += 2 * nh * hd * (min(w, count) if w else count)
+    return weights, attn
+
+
+def cpu_baseline(pkg, image_name, vocab, budget_s, seed, context):
     """Time the oracle's decode of the same model on the host cores: tokens
-    at positions 0, 1, ... until `budget_s` of work is done (at least 2).
-    The attention share at 2048 positions is 16.8 M of 7.5 G multiply-adds a
-    token (0.2%), so short-context steps stand for the context-2048 ones."""
+    at positions 1, 2, ... until `budget_s` of work is done (at least 2).
+    The benchmarked context adds its attention's multiply-adds to the
+    weights'; the rate there is estimated in proportion
+    (`at_context_estimate`)."""
     from oracle import oracle as O
-    from oracle.gguf_reader import GgufReader, oracle_model
+    from oracle.gguf_reader import GgufReader, oracle_model, model_config
     img = pkg.image_bytes(image_name)
-    om, _ = oracle_model(GgufReader(img), ctx=64)
+    reader = GgufReader(img)
+    om, _ = oracle_model(reader, ctx=64)
     try:
         rng = np.random.default_rng(seed + 1)
         toks = rng.integers(0, vocab, 64).tolist()
@@ -111,10 +130,16 @@ def cpu_baseline(pkg, image_name, vocab, budget_s, seed):
         om.close()
     cores = int(O.lib().or_model_threads())
     nproc, physical = host_cores()
+    cfg = model_config(reader)
+    w_short, a_short = token_macs(cfg, n // 2 + 1)
+    w_ctx, a_ctx = token_macs(cfg, context)
+    est = n / dt * (w_short + a_short) / (w_ctx + a_ctx)
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
             "nproc": nproc, "physical_cores": physical,
-            "context": "positions 1..%d; the benchmarked context is extrapolated at the same rate (its attention "
-                       "is 16.8 M of the 7.5 G multiply-adds a token at 2048 positions, 0.2%%)" % n,
+            "at_context_estimate": round(est, 3),
+            "context": "sampled at positions 1..%d; at %d positions a token is %.3g G multiply-adds of weights and "
+                       "%.3g G of attention (%.1f%%), so the rate there is estimated at %.3g tok/s"
+                       % (n, context, w_ctx / 1e9, a_ctx / 1e9, 100.0 * a_ctx / (w_ctx + a_ctx), est),
             "sample": "%d greedy decode steps of the same C3 model at positions 1..%d (C restatement of the "
                       "reference CPU backend, oracle/oracle.c, OpenMP %d threads), %.1f s" % (n, n, cores, dt)}
 
@@ -210,7 +235,7 @@ def run_c4(args, pkg, native):
     cpu = None
     if not args.no_cpu:
         t = time.perf_counter()
-        cpu = cpu_baseline(pkg, "bench_c4", vocab, args.cpu_seconds, args.seed)
+        cpu = cpu_baseline(pkg, "bench_c4", vocab, args.cpu_seconds, args.seed, ctx + args.warmup + args.steps // 2)
         cpu["sample"] = cpu["sample"].replace("C3", "C4")
         log("cpu baseline: %s (%.1f s)" % (cpu, time.perf_counter() - t))
     eng.close()
@@ -401,7 +426,7 @@ def run_single(args, pkg, native, which):
         log("  %-13s %-26s %9.2f us  %12d B  %7.1f GB/s" % (kname, kn, us, nbytes, nbytes / (us * 1e-6) / 1e9))
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pkg, name, vocab, args.cpu_seconds, args.seed)
+        cpu = cpu_baseline(pkg, name, vocab, args.cpu_seconds, args.seed, ctx + args.warmup + steps // 2)
         cpu["sample"] = cpu["sample"].replace("C3", which.upper())
         log("cpu baseline: %s" % cpu)
     eng.close()
@@ -477,7 +502,7 @@ def run_c5_batch(args, pkg, native):
         % (one_ms, ms_per_step / nseq, one_ms / (ms_per_step / nseq)))
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pkg, "bench_c5b", vocab, args.cpu_seconds, args.seed)
+        cpu = cpu_baseline(pkg, "bench_c5b", vocab, args.cpu_seconds, args.seed, ctx + args.warmup + steps // 2)
         cpu["sample"] = cpu["sample"].replace("C3", "C5")
         log("cpu baseline: %s" % cpu)
     eng.close()
@@ -672,7 +697,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         t = time.perf_counter()
-        cpu = cpu_baseline(pkg, "bench_c3", vocab, args.cpu_seconds, args.seed)
+        cpu = cpu_baseline(pkg, "bench_c3", vocab, args.cpu_seconds, args.seed, args.ctx + args.warmup + args.steps // 2)
         log("cpu baseline: %s (%.1f s)" % (cpu, time.perf_counter() - t))
     eng.close()
     pkg.image_free("bench_c3")

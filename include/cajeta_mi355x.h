@@ -279,13 +279,15 @@ int32_t cj_engine_cancel(int64_t eng, int32_t id);
 int32_t cj_engine_set_eog(int64_t eng, const int32_t *ids, int32_t n);
 
 /* CausalLM seam: prefill and free greedy decode of one sequence slot.
- * prefill feeds tokens[0..n) at positions pos0..: with n > 1 on dense
- * head-size-128 models as prefill chunks of up to the chunk size
- * (CausalLM.stepSeq, model/CausalLM.cajeta:801-883: every row through a
- * layer, the prefill attend, the tail on the last row only), otherwise one
- * graph-captured decode step a position; decode runs `steps` greedy steps
- * from the state prefill left and writes the generated ids. logits: the
- * last step's (or the prompt's last row's) logits. */
+ * prefill feeds tokens[0..n) at positions pos0..: with n > 1 as prefill
+ * chunks of up to the chunk size (CausalLM.stepSeq, model/CausalLM.cajeta:
+ * 801-883: every row through a layer, the tail on the last row only) — the
+ * prefill attend on dense head-size-128 models, each row's decode attention
+ * on the others (head size 64, MoE), which the reference prefills a decode
+ * step a position — and one graph-captured decode step a position where
+ * the many-row path does not serve the model; decode runs `steps` greedy
+ * steps from the state prefill left and writes the generated ids. logits:
+ * the last step's (or the prompt's last row's) logits. */
 int32_t cj_engine_reset(int64_t eng, int32_t seq);
 int32_t cj_engine_prefill(int64_t eng, int32_t seq, const int32_t *tokens, int32_t n);
 int32_t cj_engine_decode(int64_t eng, int32_t seq, int32_t steps, int32_t *out_tokens);
