@@ -83,6 +83,16 @@ typedef struct {
     int64_t expert_bytes;
     int32_t n_sel;
     int32_t sel_per_x;      // copies sharing one activation (many rows: n_used); ≤ 1: activation k
+    // the MoE route inside the expert gate|up launch (route_logits non-null):
+    // copy c = r·n_sel_row + k routes row r from its logits, takes expert
+    // sel_r[k] itself, and the row's first workgroup writes the row's
+    // selections and weights for the down and combine launches
+    const float *route_logits;
+    int32_t *route_sel;
+    float *route_w;
+    int32_t *route_status;
+    int32_t route_experts, route_used, route_norm_topk;
+    float route_scale;
 } cj_gemv_args;
 
 typedef struct {
@@ -99,6 +109,14 @@ typedef struct {
     float eps;
     int32_t form, per32, do_norm;
 } cj_pack_args;
+
+// The MoE combine with the next RMSNorm + pack: hs_out = hs_in + Σ_k w_k·y_k
+// (k order), then `p`'s norm and pack of hs_out (p.x unused).
+typedef struct {
+    float *hs_out; const float *hs_in; const float *y; const float *w;
+    int64_t n; int32_t n_used; int32_t pad;
+    cj_pack_args p;
+} cj_combine_norm_args;
 
 typedef struct {
     float *out; const float *g, *u;

@@ -387,3 +387,90 @@ DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx, int bstride = 320)
 }
 
 DEV int32_t step_pos(const cj_step_state *st, int32_t pos) { return st ? st->pos : pos; }
+
+// MoeFfn.routeFromLogits (model/MoeFfn.cajeta:908-986) for one row of
+// logits: softmax over the experts, top-k by probability with strict >
+// (ties keep the lower index), the optional renormalisation by the sum
+// clamped at 2^-14, then ×w_scale when it is neither 0 nor 1. The first wave
+// of the workgroup computes (up to 256 experts); every thread passes the
+// barriers. The logits and probabilities live in LDS; the max and the sum
+// run on one lane in expert order as the reference forms them, the exps and
+// the divides a lane an expert, and each top-k pick is a wave reduction —
+// the largest valid probability, the lowest index among equals, which is the
+// first strict maximum of the reference's scan whatever order finds it.
+// Result in s.sel / s.w (n_used entries). Logits that are not finite leave
+// no valid probability: the reference refuses the row by name; here
+// `status` (may be null) is set to 1 (the host raises after the step) and
+// expert 0 keeps every later index in bounds.
+struct RouteLds {
+    float lgs[256], pr[256];
+    float bc[2];
+    int sel[64];
+    float w[64];
+};
+DEV void route_row(const float *lg, int ne, int n_used, int norm_topk, float w_scale, int32_t *status, RouteLds &s) {
+    const int t = threadIdx.x;
+    if (t < 64)
+        for (int e = t; e < ne; e += 64) s.lgs[e] = lg[e];
+    __syncthreads();
+    if (t == 0) {
+        float mx = s.lgs[0];
+        for (int e = 1; e < ne; e++) if (s.lgs[e] > mx) mx = s.lgs[e];
+        s.bc[0] = mx;
+    }
+    __syncthreads();
+    if (t < 64) {
+        const float mx = s.bc[0];
+        for (int e = t; e < ne; e += 64) s.pr[e] = cj_expf(s.lgs[e] - mx);
+    }
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (int e = 0; e < ne; e++) sum = __fadd_rn(sum, s.pr[e]);
+        s.bc[1] = sum;
+    }
+    __syncthreads();
+    if (t < 64) {
+        const float sum = s.bc[1];
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = t + 64 * j;
+            v[j] = e < ne ? __fdiv_rn(s.pr[e], sum) : -1.0f;   // -1: no expert (never valid)
+        }
+        for (int k = 0; k < n_used; k++) {
+            float bv = 0.0f;
+            int bi = -1;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (v[j] >= 0.0f && (bi < 0 || v[j] > bv)) { bv = v[j]; bi = t + 64 * j; }
+#pragma unroll
+            for (int m = 32; m > 0; m >>= 1) {
+                const float ov = __shfl_xor(bv, m);
+                const int oi = __shfl_xor(bi, m);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            }
+            if (bi < 0) {
+                bi = 0;
+                bv = 0.0f;
+                if (t == 0 && status) status[0] = 1;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (t + 64 * j == bi) v[j] = -1.0f;
+            if (t == 0) { s.sel[k] = bi; s.w[k] = bv; }
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (norm_topk) {
+            float ws = 0.0f;
+            for (int k = 0; k < n_used; k++) ws = __fadd_rn(ws, s.w[k]);
+            if (ws < 0.00006103515625f) ws = 0.00006103515625f;
+            for (int k = 0; k < n_used; k++) s.w[k] = __fdiv_rn(s.w[k], ws);
+        }
+        if (w_scale != 0.0f && w_scale != 1.0f)
+            for (int k = 0; k < n_used; k++) s.w[k] = __fmul_rn(s.w[k], w_scale);
+    }
+    __syncthreads();
+}

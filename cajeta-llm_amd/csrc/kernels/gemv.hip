@@ -275,7 +275,7 @@ DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
     const int R = a.rows_per_wg;
     int64_t wg = blockIdx.x;
     s.kidx = 0;
-    if (a.sel) {
+    if (a.sel || a.route_logits) {
         const int64_t wpk = (a.rows + R - 1) / R;
         s.kidx = (int)(wg / wpk);
         wg = wg % wpk;
@@ -1168,7 +1168,20 @@ DEV void mxq8_body(const cj_gemv_args &a) {
     float *res = xd + ((nb + 3) & ~3);
     const int t = threadIdx.x, hw = t >> 5, hl = t & 31;
     const int R = a.rows_per_wg;
-    const GemvSlice sl = gemv_slice(a);
+    GemvSlice sl = gemv_slice(a);
+    if (a.route_logits) {
+        // the route of this copy's row, then its expert (the row's first
+        // workgroup publishes the row's selections and weights)
+        __shared__ RouteLds rl;
+        const int nu = a.route_used, r = sl.kidx / nu, k = sl.kidx % nu;
+        route_row(a.route_logits + (int64_t)r * a.route_experts, a.route_experts, nu, a.route_norm_topk,
+                  a.route_scale, a.route_status, rl);
+        sl.W = a.w + (int64_t)rl.sel[k] * a.expert_bytes;
+        if (k == 0 && sl.row0 == 0 && t < nu) {
+            a.route_sel[r * nu + t] = rl.sel[t];
+            a.route_w[r * nu + t] = rl.w[t];
+        }
+    }
     const EpiPre pre = epi_prefetch_t<EPI>(a, sl);
     (void)red;
     u32x4 wv[RW][KB];

@@ -30,14 +30,14 @@ extern "C" __global__ void __launch_bounds__(256) cj_pack(cj_pack_args a) {
 // (thread t: x[t + 256k], k ascending, ragged past the width, then the
 // 128..1 tree) from loads it issues at once, then packs its own block: no
 // workgroup waits on another.
-extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) {
+DEV void norm_pack_block(const cj_pack_args &a, const float *x) {
     __shared__ float red[256];
     __shared__ float bmax[8];
     const int t = threadIdx.x, lane = t & 63;
     const int64_t blk = blockIdx.x, e = blk * 256 + t;
-    const float xe = e < a.n ? a.x[e] : 0.0f;
+    const float xe = e < a.n ? x[e] : 0.0f;
     const float we = e < a.n ? a.w[e] : 0.0f;
-    const float scale = stage_norm_scale(a.x, a.n, a.eps, red);
+    const float scale = stage_norm_scale(x, a.n, a.eps, red);
     const float wi = a.form == 1 ? __fadd_rn(1.0f, we) : we;
     const float v = e < a.n ? __fmul_rn(__fmul_rn(xe, scale), wi) : 0.0f;
     if (a.xout && e < a.n) a.xout[e] = v;
@@ -67,6 +67,57 @@ extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) {
         if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
         pack_zero_pad(ob, t);
     }
+}
+extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) { norm_pack_block(a, a.x); }
+
+// The MoE combine (MoeFfn.forwardRow, model/MoeFfn.cajeta:1896-1901: the
+// selected experts' rows weighted and summed in k order, then onto the
+// residual) and the RMSNorm + pack that follows it (the next layer's
+// attention norm or the final norm) in one launch, one workgroup per 256
+// outputs as cj_norm_pack: every workgroup forms the whole combined row in
+// LDS (each value as cj_moe_combine forms it), writes its own block of it
+// to hs_out — a buffer other than hs_in, so no workgroup reads a value
+// another has already replaced — and norms and packs its block from the LDS
+// row exactly as cj_norm_pack does from global memory. Dynamic LDS: n floats.
+// Thread t takes the 4-value groups t, t+256, t+512, t+768 (n ≤ 4096, n a
+// multiple of 4, up to 8 experts a row: the host checks), every load of
+// the row issued before the first sum.
+extern "C" __global__ void __launch_bounds__(256) cj_moe_combine_norm(cj_combine_norm_args a) {
+    extern __shared__ __align__(16) float xs[];
+    const int t = threadIdx.x, nu = a.n_used;
+    const int64_t n4 = a.n / 4;
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wk[k] = k < nu ? a.w[k] : 0.0f;
+    float4 hv[4], yv[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t g = min((int64_t)t + 256 * j, n4 - 1);
+        hv[j] = ((const float4 *)a.hs_in)[g];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (k < nu) yv[j][k] = ((const float4 *)(a.y + k * a.n))[g];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t g = (int64_t)t + 256 * j;
+        if (g >= n4) continue;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k >= nu) break;
+            acc.x = __fadd_rn(acc.x, __fmul_rn(wk[k], yv[j][k].x));
+            acc.y = __fadd_rn(acc.y, __fmul_rn(wk[k], yv[j][k].y));
+            acc.z = __fadd_rn(acc.z, __fmul_rn(wk[k], yv[j][k].z));
+            acc.w = __fadd_rn(acc.w, __fmul_rn(wk[k], yv[j][k].w));
+        }
+        const float4 h = make_float4(__fadd_rn(hv[j].x, acc.x), __fadd_rn(hv[j].y, acc.y),
+                                     __fadd_rn(hv[j].z, acc.z), __fadd_rn(hv[j].w, acc.w));
+        ((float4 *)xs)[g] = h;
+        if (((4 * g) >> 8) == (int64_t)blockIdx.x) ((float4 *)a.hs_out)[g] = h;
+    }
+    __syncthreads();
+    norm_pack_block(a.p, xs);
 }
 
 // Device copy of n16 16-byte words (grid-stride, one uint4 a thread a step).
@@ -380,86 +431,15 @@ extern "C" __global__ void __launch_bounds__(256) cj_zero(cj_zero_args a) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.words; i += (int64_t)gridDim.x * 256) a.p[i] = 0u;
 }
 
-// MoeFfn.routeFromLogits per row: softmax over the experts, top-k by
-// probability with strict > (ties keep the lower index), then the optional
-// renormalisation by the sum clamped at 2^-14. One wave per row (up to 256
-// experts): the logits and probabilities live in LDS; the max and the sum run
-// on one lane in expert order as the reference forms them, the exps and the
-// divides a lane an expert, and each top-k pick is a wave reduction — the
-// largest valid probability, the lowest index among equals, which is the
-// first strict maximum of the reference's scan whatever order finds it.
+// MoeFfn.routeFromLogits per row (route_row, common.h): a workgroup of one
+// wave a row.
 extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
-    __shared__ float lgs[256], pr[256];
-    __shared__ float bc[2];
-    __shared__ int sel_s[64];
-    __shared__ float w_s[64];
-    const int row = blockIdx.x, t = threadIdx.x, ne = a.n_experts;
-    const float *lg = a.logits + (int64_t)row * ne;
-    for (int e = t; e < ne; e += 64) lgs[e] = lg[e];
-    __syncthreads();
-    if (t == 0) {
-        float mx = lgs[0];
-        for (int e = 1; e < ne; e++) if (lgs[e] > mx) mx = lgs[e];
-        bc[0] = mx;
-    }
-    __syncthreads();
-    const float mx = bc[0];
-    for (int e = t; e < ne; e += 64) pr[e] = cj_expf(lgs[e] - mx);
-    __syncthreads();
-    if (t == 0) {
-        float sum = 0.0f;
-        for (int e = 0; e < ne; e++) sum = __fadd_rn(sum, pr[e]);
-        bc[1] = sum;
-    }
-    __syncthreads();
-    const float sum = bc[1];
-    float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = t + 64 * j;
-        v[j] = e < ne ? __fdiv_rn(pr[e], sum) : -1.0f;   // -1: no expert (never valid)
-    }
-    for (int k = 0; k < a.n_used; k++) {
-        float bv = 0.0f;
-        int bi = -1;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (v[j] >= 0.0f && (bi < 0 || v[j] > bv)) { bv = v[j]; bi = t + 64 * j; }
-#pragma unroll
-        for (int m = 32; m > 0; m >>= 1) {
-            const float ov = __shfl_xor(bv, m);
-            const int oi = __shfl_xor(bi, m);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-        }
-        if (bi < 0) {
-            // every probability failed >= 0: the logits are not finite. The
-            // reference refuses the row by name; here the status word says
-            // so (the host raises after the step) and expert 0 keeps every
-            // later index in bounds
-            bi = 0;
-            bv = 0.0f;
-            if (t == 0 && a.status) a.status[0] = 1;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (t + 64 * j == bi) v[j] = -1.0f;
-        if (t == 0) { sel_s[k] = bi; w_s[k] = bv; }
-    }
-    __syncthreads();
-    if (t == 0) {
-        if (a.norm_topk) {
-            float ws = 0.0f;
-            for (int k = 0; k < a.n_used; k++) ws = __fadd_rn(ws, w_s[k]);
-            if (ws < 0.00006103515625f) ws = 0.00006103515625f;
-            for (int k = 0; k < a.n_used; k++) w_s[k] = __fdiv_rn(w_s[k], ws);
-        }
-        if (a.w_scale != 0.0f && a.w_scale != 1.0f)
-            for (int k = 0; k < a.n_used; k++) w_s[k] = __fmul_rn(w_s[k], a.w_scale);
-    }
-    __syncthreads();
+    __shared__ RouteLds rl;
+    const int row = blockIdx.x, t = threadIdx.x;
+    route_row(a.logits + (int64_t)row * a.n_experts, a.n_experts, a.n_used, a.norm_topk, a.w_scale, a.status, rl);
     if (t < a.n_used) {
-        a.sel[row * a.n_used + t] = sel_s[t];
-        a.w[row * a.n_used + t] = w_s[t];
+        a.sel[row * a.n_used + t] = rl.sel[t];
+        a.w[row * a.n_used + t] = rl.w[t];
     }
 }
 

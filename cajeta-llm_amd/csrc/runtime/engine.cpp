@@ -96,6 +96,8 @@ struct Engine {
     float *rope = nullptr;
     // scratch
     float *hs = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *part = nullptr;
+    float *hs2 = nullptr;      // MoE models: the combine writes the residual here and back, alternately
+    float *hs_last = nullptr;  // the buffer the last enqueued step's residual ended in
     uint8_t *act_pack = nullptr, *attn_pack = nullptr, *xpack = nullptr;
     float *xn = nullptr;       // the normed residual as f32 (f32-activation consumers)
     int32_t *glu_counters = nullptr, *argmax_counter = nullptr, *attn_counters = nullptr;
@@ -116,6 +118,19 @@ struct Engine {
     // the split-K merge as a wave per 64 dimensions, f32 out packed by the o
     // projection (CJ_MERGE_W=0: the 256-wide merge + pack, for comparisons)
     bool merge_w = [] { const char *e = getenv("CJ_MERGE_W"); return !e || strcmp(e, "0") != 0; }();
+    // the one-row step's MoE route inside the MXFP4 experts' gate|up launch
+    // (each workgroup routes the row, then streams its expert): one launch
+    // fewer a layer, C5 2.372 -> 2.337 ms a token (CJ_ROUTE_FUSED=0: the
+    // route as its own launch, for comparisons)
+    bool fuse_route = [] { const char *e = getenv("CJ_ROUTE_FUSED"); return !e || strcmp(e, "0") != 0; }();
+    // the MoE combine with the next RMSNorm + pack in one launch
+    // (CJ_COMBINE_NORM=0: two launches, for comparisons)
+    bool combine_norm = [] { const char *e = getenv("CJ_COMBINE_NORM"); return !e || strcmp(e, "0") != 0; }();
+    bool route_fused(const Layer &L) const { return fuse_route && L.gu_exps.type == CJ_MXFP4; }
+    void route_into(cj_gemv_args &a, const float *logits, int32_t *sel, float *w) const {
+        a.sel = nullptr; a.route_logits = logits; a.route_sel = sel; a.route_w = w; a.route_status = route_status;
+        a.route_experts = n_experts; a.route_used = n_used; a.route_norm_topk = norm_topk; a.route_scale = w_scale;
+    }
     int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
     int64_t embd_row_file_bytes = 0;
     // the many-row path: batched decode (a row a sequence) and prefill
@@ -391,6 +406,8 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     const int64_t fmax = std::max<int64_t>(ffn, (int64_t)expert_ffn * std::max(1, n_used));
     const int64_t fpad = (std::max<int64_t>(ffn, expert_ffn) + 255) / 256 * 256;
     hs = (float *)alloc((size_t)hidden * 4);
+    hs2 = (float *)alloc((size_t)hidden * 4);
+    hs_last = hs;
     q = (float *)alloc((size_t)qd * 4);
     attn = (float *)alloc((size_t)qd * 4);
     act = (float *)alloc((size_t)fmax * 4 + 1024);
@@ -412,7 +429,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     moe_sel = (int32_t *)alloc(64 * 4);
     route_status = (int32_t *)alloc(64);
     moe_y = (float *)alloc((size_t)hidden * std::max(1, n_used) * 4);
-    if (!hs || !q || !attn || !act || !act_pack || !attn_pack || !xpack || !xn || !logits || !part || !glu_counters || !argmax_counter ||
+    if (!hs || !hs2 || !q || !attn || !act || !act_pack || !attn_pack || !xpack || !xn || !logits || !part || !glu_counters || !argmax_counter ||
         !attn_counters || !part_v || !part_i || !moe_logits || !moe_w || !moe_sel || !moe_y || !route_status)
         return fail(CJ_ERR_HIP, "model: out of device memory (scratch)");
     CJ_HIP(hipMemset(glu_counters, 0, (size_t)fpad / 256 * 4 + 64));
@@ -541,18 +558,24 @@ int Engine::enqueue_step(int s) {
     else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
     snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
     snprintf(fused_kernel, sizeof fused_kernel, "cj_attn_fused_h%d", head_dim);
+    // the residual: hs, or on MoE models the buffer the last combine wrote
+    // (it alternates between hs and hs2, see K_COMBINE below)
+    float *cur = hs;
+    bool normed = false;   // the previous combine already formed this norm's pack
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
         // Q4_K projections fold the RMSNorm + pack into their prologue (the
         // weight stream is in flight while it runs); others read a pack
         const bool qkv_norm = L.qkv.type == CJ_Q4_K && hidden <= 4096;
-        if (!qkv_norm && want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false))) return rc;
+        if (!qkv_norm && !normed && want(K_NORM, l) && (rc = norm_pack(L.attn_norm, L.qkv.type == CJ_Q8_0, false, cur)))
+            return rc;
+        normed = false;
         if (want(K_QKV, l)) {   // 1. q|k|v over the normed residual, RoPE + K/V append epilogue
             cj_gemv_args a{};
             a.w = (const uint8_t *)L.qkv.p; a.xp = xpack; a.q_out = q; a.kc = L.kc; a.vc = L.vc;
             a.pgtab = pgtab; a.rope_cs = rope; a.state = S.state; a.rows = L.qkv.rows; a.cols = hidden;
             a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_QKV_ROPE;
-            if (qkv_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = hs; a.nw = L.attn_norm; a.norm_form = 0; }
+            if (qkv_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = cur; a.nw = L.attn_norm; a.norm_form = 0; }
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
             a.batch = 1;
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
@@ -596,7 +619,7 @@ int Engine::enqueue_step(int s) {
         }
         if (want(K_O, l)) {   // 3. o projection, residual into hs
             cj_gemv_args a{};
-            a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = hs; a.rows = L.o.rows; a.cols = L.o.cols;
+            a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = cur; a.rows = L.o.rows; a.cols = L.o.cols;
             a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split && !merge_w ? CJ_PRO_PACKED : CJ_PRO_PACK;
             a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
@@ -605,7 +628,7 @@ int Engine::enqueue_step(int s) {
         const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096;
         if (!gu_norm && want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
             const int ct = n_experts ? L.gu_exps.type : L.gu.type;
-            if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0))) return rc;
+            if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0, cur))) return rc;
         }
         if (n_experts == 0) {
             if (want(K_GATE_UP, l)) {   // 4. gate|up over the pack, SiLU·up epilogue
@@ -615,12 +638,12 @@ int Engine::enqueue_step(int s) {
                 a.type = L.gu.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_GLU; a.per32 = L.gu.type == CJ_Q8_0;
                 a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
                 a.batch = 1;
-                if (gu_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = hs; a.nw = L.ffn_norm; a.norm_form = 0; }
+                if (gu_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = cur; a.nw = L.ffn_norm; a.norm_form = 0; }
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16, a.pro, a.epi)))) return rc;
             }
             if (want(K_DOWN, l)) {   // 5. down, residual into hs
                 cj_gemv_args a{};
-                a.w = (const uint8_t *)L.down.p; a.x = act; a.y = hs; a.rows = L.down.rows; a.cols = L.down.cols;
+                a.w = (const uint8_t *)L.down.p; a.x = act; a.y = cur; a.rows = L.down.rows; a.cols = L.down.cols;
                 a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
                 a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
@@ -633,7 +656,8 @@ int Engine::enqueue_step(int s) {
                 a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
                 if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
             }
-            if (want(K_ROUTE, l)) {
+            const bool fused = route_fused(L);
+            if (!fused && want(K_ROUTE, l)) {
                 cj_route_args a{moe_logits, moe_sel, moe_w, n_experts, n_used, norm_topk, 1, w_scale, 0, route_status};
                 if ((rc = launch("cj_moe_route", 1, 64, 0, a))) return rc;
             }
@@ -645,6 +669,7 @@ int Engine::enqueue_step(int s) {
                 a.per32 = a.type == CJ_Q8_0; a.act_n = expert_ffn; a.glu_form = 0; a.batch = 1;
                 a.sel = moe_sel; a.n_sel = n_used; a.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes;
                 a.y_stride = expert_ffn;
+                if (fused) route_into(a, moe_logits, moe_sel, moe_w);
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
             }
             if (want(K_EXP_DOWN, l)) {   // the selected experts' down into moe_y[k]
@@ -657,12 +682,32 @@ int Engine::enqueue_step(int s) {
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 32, a.pro, a.epi)))) return rc;
             }
             if (want(K_COMBINE, l)) {   // hs += Σ_k w_k · y_k in k order
-                cj_combine_args a{hs, moe_y, moe_w, hidden, n_used};
-                if ((rc = launch("cj_moe_combine", (uint32_t)((hidden + 255) / 256), 256, 0, a))) return rc;
+                // with the next RMSNorm + pack where that is a launch of its
+                // own (the next layer's attention norm, or the final norm):
+                // the combined residual goes to the other buffer
+                const bool last = l + 1 == n_layers;
+                const bool next_fused = !last && layers[l + 1].qkv.type == CJ_Q4_K && hidden <= 4096;
+                if (combine_norm && only < 0 && !next_fused && hidden % 4 == 0 && hidden <= 4096 && n_used <= 8) {
+                    float *nxt = cur == hs ? hs2 : hs;
+                    cj_combine_norm_args a{};
+                    a.hs_out = nxt; a.hs_in = cur; a.y = moe_y; a.w = moe_w; a.n = hidden; a.n_used = n_used;
+                    a.p.out = xpack; a.p.w = last ? out_norm : layers[l + 1].attn_norm;
+                    a.p.xout = last && is_f32_act(head.type) ? xn : nullptr; a.p.n = hidden;
+                    a.p.npad = ((int64_t)hidden + 255) / 256 * 256; a.p.rows = 1; a.p.eps = eps; a.p.form = 0;
+                    a.p.per32 = last ? head.type == CJ_Q8_0 : layers[l + 1].qkv.type == CJ_Q8_0; a.p.do_norm = 1;
+                    if ((rc = launch("cj_moe_combine_norm", (uint32_t)(a.p.npad / 256), 256, (uint32_t)(hidden * 4), a)))
+                        return rc;
+                    cur = nxt;
+                    normed = true;
+                } else {
+                    cj_combine_args a{cur, moe_y, moe_w, hidden, n_used};
+                    if ((rc = launch("cj_moe_combine", (uint32_t)((hidden + 255) / 256), 256, 0, a))) return rc;
+                }
             }
         }
     }
-    if (only < 0 && (rc = norm_pack(out_norm, head.type == CJ_Q8_0, is_f32_act(head.type)))) return rc;
+    hs_last = cur;
+    if (only < 0 && !normed && (rc = norm_pack(out_norm, head.type == CJ_Q8_0, is_f32_act(head.type), cur))) return rc;
     if (want(K_HEAD, 0)) {   // head over the final norm's pack + greedy argmax; advances the step
         cj_gemv_args a{};
         a.w = (const uint8_t *)head.p; a.x = xn; a.xp = xpack; a.y = logits;
@@ -777,7 +822,8 @@ int Engine::rows_moe(const Layer &L, int n) {
         a.y_stride = n_experts;
         if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
     }
-    {
+    {   // the route as its own launch: inside the gate|up launch every one
+        // of the rows' many workgroups would wait out its row's route
         cj_route_args a{r_moe_logits, r_moe_sel, r_moe_w, n_experts, n_used, norm_topk, n, w_scale, 0, route_status};
         if ((rc = launch("cj_moe_route", (uint32_t)n, 64, 0, a))) return rc;
     }
@@ -1504,7 +1550,7 @@ int32_t cj_engine_trace(int64_t h, int32_t what, float *out, int64_t n) {
     const float *src = nullptr;
     int64_t cap = 0;
     switch (what) {
-    case 0: src = e->hs; cap = e->hidden; break;
+    case 0: src = e->hs_last; cap = e->hidden; break;
     case 1: src = e->q; cap = qd; break;
     case 2: src = e->attn; cap = qd; break;
     case 3: src = e->act; cap = e->ffn; break;

@@ -343,7 +343,7 @@ int run_gemv(const cj_gemv_args &a0, const GemvPlan &p) {
     if (p.lds > 65536) return fail(CJ_ERR_ARG, "gemv %s: %u bytes of LDS exceed 64 KB", p.kernel.c_str(), p.lds);
     if (is_f32_act(a.type) && a.cols % 32)
         return fail(CJ_ERR_ARG, "gemv %s: %lld columns are not whole 32-element blocks", p.kernel.c_str(), (long long)a.cols);
-    const uint32_t grid = a.sel ? p.per_copy * (uint32_t)a.n_sel : p.grid;
+    const uint32_t grid = (a.sel || a.route_logits) ? p.per_copy * (uint32_t)a.n_sel : p.grid;
     return launch(p.kernel.c_str(), grid, 256, p.lds, a);
 }
 
@@ -376,7 +376,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
         "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_gemv_q40_r32", "cj_gemv_mxfp4_r32", "cj_gemv_f32_r32",
         "cj_gemv_q40_r1", "cj_gemv_mxfp4_r1", "cj_gemv_f32_r1",
-        "cj_moe_combine",
+        "cj_moe_combine", "cj_moe_combine_norm",
         "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
