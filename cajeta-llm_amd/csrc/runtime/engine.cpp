@@ -401,7 +401,18 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     rope = (float *)alloc((size_t)ctx * head_dim * 4);
     if (!pgtab || !rope) return fail(CJ_ERR_HIP, "model: out of device memory");
     CJ_HIP(hipMemcpy(pgtab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
-    if ((rc = cj_rope_table((int64_t)(uintptr_t)rope, head_dim, theta, ctx))) return rc;
+    // Llama-3.1-style precomputed RoPE factors (ModelConfig, model/ModelConfig.cajeta:307-316)
+    const GgufTensor *rf = file.tensor("rope_freqs.weight");
+    if (rf && rf->type != CJ_F32) return fail(CJ_ERR_IO, "model: rope_freqs.weight is type %d, not f32", rf->type);
+    if (rf && rf->bytes < rf->cols() * rf->rows() * 4) return fail(CJ_ERR_IO, "model: rope_freqs.weight is truncated");
+    std::vector<float> factors;
+    if (rf) {
+        factors.resize((size_t)(rf->cols() * rf->rows()));
+        memcpy(factors.data(), rf->data, factors.size() * 4);
+    }
+    if ((rc = cj_rope_table_freqs((int64_t)(uintptr_t)rope, head_dim, theta, ctx, rf ? factors.data() : nullptr,
+                                  (int32_t)factors.size())))
+        return rc;
 
     const int64_t fmax = std::max<int64_t>(ffn, (int64_t)expert_ffn * std::max(1, n_used));
     const int64_t fpad = (std::max<int64_t>(ffn, expert_ffn) + 255) / 256 * 256;

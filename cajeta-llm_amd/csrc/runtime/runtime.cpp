@@ -675,11 +675,22 @@ int32_t cj_add(int64_t ab, int64_t bb, int64_t n) {
 }
 
 int32_t cj_rope_table(int64_t out, int32_t head_dim, float theta, int32_t ctx) {
+    return cj_rope_table_freqs(out, head_dim, theta, ctx, nullptr, 0);
+}
+
+int32_t cj_rope_table_freqs(int64_t out, int32_t head_dim, float theta, int32_t ctx, const float *freqs, int32_t n_freqs) {
     const int half = head_dim / 2;
     if (head_dim <= 0 || head_dim % 2 || ctx <= 0 || !in_buffer(dptr(out), (int64_t)ctx * half * 8))
         return fail(CJ_ERR_ARG, "cj_rope_table: head_dim %d ctx %d", head_dim, ctx);
+    if (freqs && n_freqs != half)
+        return fail(CJ_ERR_ARG, "rope_freqs has %d entries; expected %d (headDim/2)", n_freqs, half);
     std::vector<float> inv(half), tab((size_t)ctx * half * 2);
     for (int d = 0; d < half; d++) inv[d] = powf(theta, (0.0f - (float)(2 * d)) / (float)head_dim);
+    // precomputed per-dimension factors: theta_d /= factor_d (a zero factor
+    // leaves the dimension as it is)
+    if (freqs)
+        for (int d = 0; d < half; d++)
+            if (freqs[d] != 0.0f) inv[d] = inv[d] / freqs[d];
     for (int p = 0; p < ctx; p++)
         for (int d = 0; d < half; d++) {
             const float ang = (float)p * inv[d];

@@ -169,6 +169,7 @@ struct Spec {
     float eps = 1e-5f, theta = 10000.0f;
     int wtype = CJ_Q8_0, head = CJ_Q8_0, embd = CJ_F32;
     int experts = 0, used = 0, expert_ffn = 0, expert_type = CJ_MXFP4, norm_topk = 1, swa = 0, eos = -1;
+    int rope_freqs = 0;   // 1: a rope_freqs.weight tensor of hd/2 factors (Llama-3.1's scaled RoPE)
 };
 
 int type_of(const std::string &s) {
@@ -216,13 +217,14 @@ bool parse_spec(const std::string &in, Spec &sp, std::string &err) {
         else if (k == "norm_topk") sp.norm_topk = I();
         else if (k == "swa") sp.swa = I();
         else if (k == "eos") sp.eos = I();
+        else if (k == "rope_freqs") sp.rope_freqs = I();
         else { err = "unknown spec key " + k; return false; }
     }
     if (sp.wtype < 0 || sp.head < 0 || sp.embd < 0 || sp.expert_type < 0) { err = "unknown weight type in spec"; return false; }
     return true;
 }
 
-struct Job { std::string name; int type; int64_t rows, cols; int kind; };  // kind 0 weight, 1 norm, 2 router
+struct Job { std::string name; int type; int64_t rows, cols; int kind; };  // kind 0 weight, 1 norm, 2 router, 3 rope factors
 
 void fill_tensor(uint8_t *dst, const Job &j, uint64_t seed, int hidden, int nthreads) {
     const uint64_t key = splitmix(seed ^ name_hash(j.name));
@@ -233,7 +235,13 @@ void fill_tensor(uint8_t *dst, const Job &j, uint64_t seed, int hidden, int nthr
         for (int64_t r = r0; r < r1; r++) {
             for (int64_t c = 0; c < j.cols; c++) {
                 const float z = gauss(key, (uint64_t)(r * j.cols + c));
-                row[(size_t)c] = j.kind == 1 ? 1.0f + 0.02f * z : j.kind == 2 ? z / std::sqrt((float)hidden) : 0.02f * z;
+                // rope factors: 1 on the fast dimensions rising to 8 on the
+                // slow ones, with a seeded wobble (the shape of Llama-3.1's)
+                const float fr = 1.0f + 7.0f * (float)c / (float)std::max<int64_t>(1, j.cols - 1);
+                row[(size_t)c] = j.kind == 1   ? 1.0f + 0.02f * z
+                                 : j.kind == 2 ? z / std::sqrt((float)hidden)
+                                 : j.kind == 3 ? fr * (1.0f + 0.05f * z)
+                                               : 0.02f * z;
             }
             uint8_t *o = dst + r * rb;
             if (j.type == CJ_F32) { memcpy(o, row.data(), (size_t)j.cols * 4); continue; }
@@ -316,6 +324,7 @@ int synth_gguf(const std::string &spec, const std::string &path, int64_t seed) {
     }
     jobs.push_back({"output_norm.weight", CJ_F32, 1, h, 1});
     jobs.push_back({"output.weight", sp.head, sp.vocab, h, 0});
+    if (sp.rope_freqs) jobs.push_back({"rope_freqs.weight", CJ_F32, 1, sp.hd / 2, 3});
     for (auto &j : jobs) {
         if (ggml_row_bytes(j.type, j.cols) < 0)
             return fail(CJ_ERR_ARG, "cj_synth_gguf: %s has %lld columns, not whole blocks of its type", j.name.c_str(), (long long)j.cols);

@@ -50,6 +50,7 @@ SIGNATURES = {
     "cj_add": (I32, [I64, I64, I64]),
     "cj_buf_copy": (I32, [I64, I64, I64]),
     "cj_rope_table": (I32, [I64, I32, F32, I32]),
+    "cj_rope_table_freqs": (I32, [I64, I32, F32, I32, P, I32]),
     "cj_qk_prep": (I32, [I64, I64, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32, I32, F32, I32, I32]),
     "cj_attend": (I32, [I64, I64, I64, I64, I64, I64, I32, I64, I32, I32, I32, I32, I32, I32, F32]),
     "cj_decode_splits": (I32, [I32, I32, I32]),

@@ -153,6 +153,14 @@ int32_t cj_add(int64_t a, int64_t b, int64_t n);
  * (cos(p·inv[d]), sin(p·inv[d])) with inv[d] = theta^(-2d/hd)
  * (Prim.invFreq, model/Prim.cajeta:1866-1909). Writes ctx·hd floats. */
 int32_t cj_rope_table(int64_t out, int32_t head_dim, float theta, int32_t ctx);
+/* The same with a model's precomputed per-dimension factors (GGUF
+ * `rope_freqs.weight`, n_freqs = head_dim/2 host floats): each dimension's
+ * inverse frequency is divided by its factor where the factor is not 0
+ * (Attention's constructor, model/Attention.cajeta:80-100; ModelConfig's
+ * load of the tensor, model/ModelConfig.cajeta:307-316). A count other
+ * than head_dim/2 is refused with the reference's message. */
+int32_t cj_rope_table_freqs(int64_t out, int32_t head_dim, float theta, int32_t ctx, const float *freqs,
+                            int32_t n_freqs);
 
 /* QK-norm (norm != 0) + RoPE + fp16 K/V append at position pos through the
  * page table. q [n_q·hd], k/v [n_kv·hd] f32 in HF (split-half) order.

@@ -117,4 +117,9 @@ def oracle_model(r, **kw):
     if "output.weight" not in r.tensors:
         ty, dims, rows, cols, data = r.tensors["token_embd.weight"]
         m.bind("output.weight", ty, np.ascontiguousarray(data), rows, cols)
+    if "rope_freqs.weight" in r.tensors:   # ModelConfig, model/ModelConfig.cajeta:307-316
+        ty, dims, rows, cols, data = r.tensors["rope_freqs.weight"]
+        if ty != O.F32:
+            raise ValueError("rope_freqs.weight is type %d, not f32" % ty)
+        m.set_rope_freqs(np.frombuffer(np.ascontiguousarray(data).tobytes(), np.float32))
     return m, cfg

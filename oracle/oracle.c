@@ -990,6 +990,22 @@ void or_model_reset(or_model *m) {
     for (int l = 0; l < m->c.n_layers; l++) { memset(m->kc[l], 0, plane); memset(m->vc[l], 0, plane); }
 }
 
+/* A model's precomputed RoPE factors (GGUF rope_freqs.weight, hd/2 of
+ * them): inv[d] = inv[d] / f[d] where f[d] != 0 (Attention's constructor,
+ * L/model/Attention.cajeta:80-100; read by ModelConfig,
+ * L/model/ModelConfig.cajeta:307-316). Refused (-1) unless n = hd/2. */
+int or_model_set_rope_freqs(or_model *m, const float *f, int n) {
+    int half = m->c.head_dim / 2;
+    if (n != half) return -1;
+    for (int d = 0; d < half; d++)
+#if OR_PLANT == 17
+        if (f[d] != 0.0f) m->inv[d] = m->inv[d] * f[d];      /* planted: multiplied, not divided */
+#else
+        if (f[d] != 0.0f) m->inv[d] = m->inv[d] / f[d];
+#endif
+    return 0;
+}
+
 /* The CPU worker count the decode split rule divides (the reference's
  * EngineOptions.cpuThreads, AttnKernel.cpuDecodeSplits :4879-4889); the
  * KV planes are kept, so decode steps can be replayed at another count. */
@@ -1004,6 +1020,7 @@ int64_t or_model_trace(or_model *m, int what, float *out, int64_t n) {
     case 2: src = m->ao; cap = (int64_t)c->n_heads * c->head_dim; break;
     case 3: src = m->g; cap = c->ffn; break;
     case 4: src = m->logits; cap = c->vocab; break;
+    case 5: src = m->inv; cap = c->head_dim / 2; break;
     default: return -1;
     }
     if (n > cap) n = cap;

@@ -121,6 +121,7 @@ int       or_model_bind(or_model *m, const char *name, int type, const void *dat
 int       or_model_step(or_model *m, int token, int pos, float *logits);
 void      or_model_reset(or_model *m);
 void      or_model_set_workers(or_model *m, int workers);
+int       or_model_set_rope_freqs(or_model *m, const float *f, int n);
 /* A prefill chunk: tokens[0..n) at positions start .. start+n-1 through
  * every layer as rows (head size 128: the prefill attention; otherwise one
  * decode step a row), then the tail on the last row. Writes its logits if

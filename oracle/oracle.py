@@ -84,6 +84,7 @@ def _configure(L):
             "or_model_bind": (I32, [P, ctypes.c_char_p, I32, P, I64, I64]),
             "or_model_step": (I32, [P, I32, I32, P]), "or_model_reset": (None, [P]),
             "or_model_set_workers": (None, [P, I32]),
+            "or_model_set_rope_freqs": (I32, [P, P, I32]),
             "or_model_threads": (I32, []),
             "or_model_trace": (I64, [P, I32, P, I64]),
         }
@@ -295,6 +296,13 @@ class Model:
 
     def reset(self):
         lib().or_model_reset(self.h)
+
+    def set_rope_freqs(self, factors):
+        """A model's rope_freqs.weight factors (head_dim/2 of them)."""
+        f = np.ascontiguousarray(factors, np.float32)
+        self._keep.append(f)
+        if lib().or_model_set_rope_freqs(self.h, _p(f), int(f.size)) != 0:
+            raise ValueError("rope_freqs has %d entries; expected %d (headDim/2)" % (f.size, self.cfg.head_dim // 2))
 
     def set_workers(self, workers):
         """The split rule's worker count for the steps that follow (KV kept)."""

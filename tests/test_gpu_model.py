@@ -250,6 +250,25 @@ def test_c3_attention_at_the_benchmarked_context(gpu):
     gpu.image_free("t_c3ctx")
 
 
+@pytest.mark.parametrize("hd", [128, 64])
+def test_rope_freqs_model_parity(gpu, hd):
+    """A model carrying Llama-3.1's precomputed RoPE factors (`rope_freqs.weight`,
+    hd/2 of them, 1 rising to 8 with a seeded wobble): every dimension's
+    inverse frequency divided by its factor on both sides, through prefill
+    chunks and decode steps, bit for bit."""
+    say("model rope_freqs hd", hd)
+    heads = 8 if hd == 128 else 16
+    spec = "layers=2;hidden=1024;heads=%d;kv=2;hd=%d;ffn=2048;vocab=4096;eps=1e-5;theta=500000;" \
+           "wtype=q4_k;head=q6_k;embd=q4_k;ctx=512;rope_freqs=1" % (heads, hd)
+    path, img = synth(gpu, spec, "t_rf%d" % hd, 93)
+    rng = np.random.default_rng(hd)
+    prompt = rng.integers(0, 4096, 300).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 8, 512)
+    gpu.image_free("t_rf%d" % hd)
+    assert g == o
+    assert run_pair.bit_identical, err
+
+
 def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
     """Benchmark configuration C4's Q8_0 weights on the 8B shapes, at two layers."""
     say("model c4x2")

@@ -189,6 +189,37 @@ def check_rope(O):
     return not bad, bad
 
 
+def check_rope_freqs(O):
+    """A model's rope_freqs factors: each inverse frequency θ^(−2d/hd)
+    divided by its factor (a zero factor leaves it), against float64; a
+    count other than hd/2 refused."""
+    bad = []
+    for hd, theta in ((128, 500000.0), (64, 10000.0)):
+        half = hd // 2
+        c = dict(n_layers=1, hidden=hd, n_heads=1, n_kv=1, head_dim=hd, ffn=256, vocab=8, ctx=8, eps=1e-5,
+                 theta=theta, kv_f32=0, workers=512, n_experts=0, n_used=0, norm_topk=1, expert_ffn=256,
+                 swa_window=0, attn_rows=0, w_scale=0.0, swa_pattern=2)
+        m = O.Model(c)
+        rng = np.random.default_rng(hd)
+        f = (1.0 + 7.0 * np.arange(half) / (half - 1)) * (1.0 + 0.05 * rng.standard_normal(half))
+        f = f.astype(np.float32)
+        f[3] = 0.0
+        m.set_rope_freqs(f)
+        got = m.trace(5, half).astype(np.float64)
+        ref = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / hd)
+        ref = np.where(f != 0, ref / np.where(f != 0, f.astype(np.float64), 1.0), ref)
+        e = float(np.max(np.abs(got - ref) / ref))
+        if e > 1e-6:
+            bad.append((hd, e))
+        try:
+            m.set_rope_freqs(f[:-1])
+            bad.append((hd, "short factor list accepted"))
+        except ValueError:
+            pass
+        m.close()
+    return not bad, bad
+
+
 def check_argmax(O):
     v = np.array([0.5, 3.0, -1.0, 3.0, 2.0, 3.0], np.float32)
     cases = [(v, 1), (np.zeros(7, np.float32), 0), (np.array([-5, -2, -2], np.float32), 1)]
@@ -672,6 +703,11 @@ def test_decode_splits_closed_form(O):
     assert O.cpu_decode_splits(100, 2, 8, 24) == 3
 
 
+def test_rope_freqs_factors(O):
+    ok, bad = check_rope_freqs(O)
+    assert ok, bad
+
+
 def test_mxfp4_device_q8_form(O):
     ok, bad = check_mxfp4_q8(O)
     assert ok, bad
@@ -827,6 +863,7 @@ PLANTS = {
     14: ("MoE model without the renormalisation", check_moe_model),
     15: ("MXFP4 activation codes at half scale", check_mxfp4_q8),
     16: ("MXFP4 high nibbles against the low activation half", check_mxfp4_q8),
+    17: ("rope_freqs factors multiplied, not divided", check_rope_freqs),
 }
 # 14 is plant 12 again, caught at model level as well (the tie order of plant
 # 11 needs an exact tie, which only check_moe_route constructs)
