@@ -87,6 +87,31 @@ def test_split_gguf_decodes_as_the_whole_file(gpu, tmp_path):
     assert g == o and run_pair.bit_identical, (g, o, err)
 
 
+@pytest.mark.parametrize("key,moe", [("llama.feed_forward_length", False),
+                                     ("llama.expert_feed_forward_length", True)])
+def test_feed_forward_metadata_that_disagrees_with_the_tensors_is_refused(gpu, tmp_path, key, moe):
+    """A GGUF whose FFN width key disagrees with its gate/up tensors' rows is
+    refused by name at load, before any copy reads past a tensor."""
+    spec = ("layers=1;hidden=256;heads=4;kv=2;hd=64;ffn=512;vocab=256;wtype=q8_0;head=q8_0;embd=q8_0;ctx=64" +
+            (";experts=4;used=2;expert_ffn=512" if moe else ""))
+    gpu.synth_gguf(spec, "mem:t_ffbad", 5)
+    img = bytearray(gpu.image_bytes("t_ffbad").tobytes())
+    gpu.image_free("t_ffbad")
+    k = key.encode()
+    at = img.find(len(k).to_bytes(8, "little") + k)
+    assert at >= 0
+    vt = at + 8 + len(k)
+    assert int.from_bytes(img[vt:vt + 4], "little") == 4      # a u32 value
+    img[vt + 4:vt + 8] = (768).to_bytes(4, "little")          # rows of gate/up stay 512
+    path = tmp_path / "ffbad.gguf"
+    path.write_bytes(bytes(img))
+    opts = gpu.EngineOptions(str(path))
+    opts.ctx, opts.maxSeqs = 64, 1
+    with pytest.raises(gpu.LlmException) as e:
+        gpu.LlmEngine.load(opts).close()
+    assert "rows" in str(e.value), str(e.value)
+
+
 def test_prefill_chunks_are_invisible(gpu):
     """A 45-token prompt as one chunk and as chunks of 7: chunking changes
     nothing (every row's arithmetic is the same), both against the oracle's
