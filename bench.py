@@ -321,7 +321,7 @@ def run_c2(args, native):
             f32act = ty == 2
             for B in C2_BATCHES:
                 reps = max(ncopy, 32)
-                per = B if (B > 1 and ty in (2, 14)) else 1
+                per = B if (B > 1 and ty == 2) else 1
                 native.check(lib.cj_graph_begin(), "graph")
                 for r in range(reps):
                     w = pool.h + (r % ncopy) * rows * prb
@@ -343,7 +343,8 @@ def run_c2(args, native):
                 gbs = nbytes / (us * 1e-6) / 1e9
                 table.append({"format": fname, "rows": rows, "cols": cols, "batch": B, "us": round(us, 2),
                               "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
-                              "kernel": "gemv" if B == 1 else ("gemv per column" if per > 1 else "int8 mfma"),
+                              "kernel": "gemv" if B == 1 else ("gemv per column" if per > 1 else
+                                                               "many-column gemv" if ty == 14 else "int8 mfma"),
                               "pool_copies": ncopy})
                 log("  %-5s %6d x %5d B %2d: %9.2f us  %7.1f GB/s  (%s, %d copies)" % (
                     fname, rows, cols, B, us, gbs, table[-1]["kernel"], ncopy))

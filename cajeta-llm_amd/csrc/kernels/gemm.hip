@@ -600,3 +600,92 @@ extern "C" __global__ void __launch_bounds__(256) cj_gemm_q80_n4(cj_gemv_args a)
 extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q80_n1(cj_gemv_args a) { gemm_sk_q80<1, 8>(a); }
 extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q80_n2(cj_gemv_args a) { gemm_sk_q80<2, 8>(a); }
 extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q4k_n1(cj_gemv_args a) { gemm_sk_q4k<1, 8>(a); }
+
+// ------------------------------------------------------------------- Q6_K
+
+// Many columns of Q6_K × q8_K (no matrix-core form: the 16-element
+// sub-block scales sit inside the 32-element dot an MFMA forms). A wave
+// takes a row at a time (4 rows a workgroup pass, 16 a workgroup), its lanes
+// the row's units (block b, quarter j: 64 elements); each unit's weights are
+// loaded and decoded once and then dotted with the NC columns' packs, which
+// every wave reads from the cache (the codes decoded once to signed q − 32,
+// so a column costs only its dots). Per (row, column) the block terms are
+// the one-column GEMV's — sumi = Σ_sb sc_sb·dot_sb over q − 32, an exact
+// integer, then (d·xs)·sumi — kept in the wave's LDS rows, and lane c folds column c's
+// terms in block order (Quant.q6kMatVecIntoQ8, io/Quant.cajeta:3448-3486):
+// each column is bit for bit what cj_matvec gives it.
+// Four 6-bit codes q (0..63, one a byte) as the int8 values q − 32: bit 5
+// set, clearing it subtracts 32; clear, q − 32 = q + 224 is q + 32 with bits
+// 6 and 7 set. (0x20·6 = 0xC0, so the multiply cannot carry between bytes.)
+DEV uint32_t q6_signed(uint32_t q) { return (q ^ 0x20202020u) | ((~q & 0x20202020u) * 6u); }
+
+template <int NC>
+DEV void gemm_q6k_cols(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) float tsm[];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nb = (int)(a.cols / 256), units = nb * 4, ts = nb + 1;
+    float *terms = tsm + wave * NC * ts;               // [NC][nb + 1] a wave
+    const int64_t c0 = (int64_t)blockIdx.y * NC;
+    const uint8_t *xcol[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) xcol[c] = a.xp + min(c0 + c, (int64_t)a.batch - 1) * a.xp_stride;
+    for (int rr = 0; rr < 4; rr++) {
+        const int64_t row_i = (int64_t)blockIdx.x * 16 + 4 * wave + rr;
+        const bool live = row_i < a.rows;              // every wave passes the barriers below
+        const int64_t row = live ? row_i : a.rows - 1;
+        const uint8_t *w = a.w + row * a.row_bytes;
+        for (int u0 = 0; u0 < units; u0 += 64) {
+            const int u = min(u0 + lane, units - 1);
+            const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
+            const uint4 qa = ld_stream16(w + (int64_t)b * 128 + 64 * g + 16 * hl);
+            const uint4 qb = ld_stream16(w + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
+            const uint4 qh = ld_stream16(w + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
+            const uint2 sc = *(const uint2 *)(w + (int64_t)nb * 192 + (int64_t)b * 16 + 8 * g);
+            const uint32_t dh = *(const uint16_t *)(w + (int64_t)nb * 208 + 2 * b);
+            uint32_t v[4][4];
+            int scv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint4 ql = (k & 1) ? qb : qa;
+                const int sh = (k >> 1) * 4;
+                const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
+                v[k][0] = q6_signed(((ql.x >> sh) & M) | (((qh.x >> (2 * k)) & H) << 4));
+                v[k][1] = q6_signed(((ql.y >> sh) & M) | (((qh.y >> (2 * k)) & H) << 4));
+                v[k][2] = q6_signed(((ql.z >> sh) & M) | (((qh.z >> (2 * k)) & H) << 4));
+                v[k][3] = q6_signed(((ql.w >> sh) & M) | (((qh.w >> (2 * k)) & H) << 4));
+                const int byte_i = 2 * k + hl;
+                const uint32_t word = byte_i < 4 ? sc.x : sc.y;
+                scv[k] = (int)(int8_t)((word >> (8 * (byte_i & 3))) & 255);
+            }
+            const float d = h2f(dh);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const uint8_t *ab = xcol[c] + b * 320 + 128 * g + 16 * hl;
+                const float xs = *(const float *)(xcol[c] + b * 320 + 288);
+                int sumi = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint4 av = *(const uint4 *)(ab + 32 * k);
+                    int dt = 0;
+                    dt = sdot4(v[k][0], av.x, dt); dt = sdot4(v[k][1], av.y, dt);
+                    dt = sdot4(v[k][2], av.z, dt); dt = sdot4(v[k][3], av.w, dt);
+                    sumi += scv[k] * dt;
+                }
+                sumi += quad_xor1(sumi);
+                sumi += quad_xor2(sumi);
+                if (u0 + lane < units && j == 0) terms[c * ts + b] = __fmul_rn(__fmul_rn(d, xs), (float)sumi);
+            }
+        }
+        __syncthreads();                               // the terms are written
+        if (live && lane < NC && c0 + lane < a.batch) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) acc = __fadd_rn(acc, terms[lane * ts + b]);
+            float *y = a.y + (c0 + lane) * a.y_stride + a.y_off + row;
+            *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
+        }
+        __syncthreads();                               // and read before the next row writes them
+    }
+}
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c4(cj_gemv_args a) { gemm_q6k_cols<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c8(cj_gemv_args a) { gemm_q6k_cols<8>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c16(cj_gemv_args a) { gemm_q6k_cols<16>(a); }

@@ -306,7 +306,7 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
     return p;
 }
 
-bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K; }
+bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K || type == CJ_Q6_K; }
 
 // Two kernels, chosen by shape. The tiled kernel (4 waves a 64-row ×
 // 16·NT-column tile over LDS-staged packs) when the row blocks and column
@@ -319,8 +319,17 @@ bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K; }
 int run_gemm(const cj_gemv_args &a) {
     if (!gemm_supported(a.type)) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
     if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
-    const char *fmt = a.type == CJ_Q8_0 ? "q80" : "q4k";
     char name[32];
+    if (a.type == CJ_Q6_K) {
+        // many-column GEMV: 16 rows a workgroup, NC columns a grid row
+        const int nc = a.batch <= 4 ? 4 : a.batch <= 8 ? 8 : 16;
+        const int64_t nb = a.cols / 256;
+        if (a.cols % 256) return fail(CJ_ERR_ARG, "gemm: Q6_K rows are whole 256-element blocks");
+        snprintf(name, sizeof name, "cj_gemm_q6k_c%d", nc);
+        return launch2(name, (uint32_t)((a.rows + 15) / 16), (uint32_t)((a.batch + nc - 1) / nc), 256,
+                       (uint32_t)(4 * nc * (nb + 1) * 4), a);
+    }
+    const char *fmt = a.type == CJ_Q8_0 ? "q80" : "q4k";
     // Q4_K's 64-column tile needs more registers than two waves a SIMD leave
     const int nt = (a.batch <= 32 || a.type == CJ_Q4_K) ? 2 : 4;
     const int64_t tiles = ((a.rows + 63) / 64) * ((a.batch + 16 * nt - 1) / (16 * nt));
@@ -381,7 +390,7 @@ int32_t cj_init(int32_t device) {
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
         "cj_attn_merge", "cj_attn_merge_w", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
-        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4",
+        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_c16",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
         "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8", "cj_attn_merge_rows",

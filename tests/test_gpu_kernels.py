@@ -391,16 +391,17 @@ def test_kernel_registry_answers_reference_names(gpu):
     assert gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
 
 
-@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12)])
+@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12), ("q6_k", 14)])
 @pytest.mark.parametrize("rows,cols,ncols", [(300, 512, 1), (1024, 4096, 4), (64, 1408, 8), (272, 4096, 17),
                                              (96, 14336, 16), (160, 2048, 70), (100, 1408, 80), (40, 512, 33),
-                                             (130, 768, 200)])
+                                             (130, 768, 200), (37, 4096, 5)])
 def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
-    """The batched int8 matrix-core product: every output column is the
-    one-column product of its activation pack, bit for bit (integer sub-block
-    dots are exact; the float fold runs in the reference's block order)."""
-    if ty == O.Q4_K and cols % 256:
-        pytest.skip("Q4_K rows are whole 256-element blocks")
+    """The batched product (int8 matrix cores for Q8_0 and Q4_K, the
+    many-column GEMV for Q6_K): every output column is the one-column product
+    of its activation pack, bit for bit (integer sub-block dots are exact;
+    the float fold runs in the reference's block order)."""
+    if ty in (O.Q4_K, O.Q6_K) and cols % 256:
+        pytest.skip("K-quant rows are whole 256-element blocks")
     say("matmul", name, rows, cols, ncols)
     rng = np.random.default_rng(rows * 7 + cols + ncols + ty)
     be, bb = O.BLOCK[ty]

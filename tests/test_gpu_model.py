@@ -340,6 +340,22 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+def test_c3_shape_batched_decode_parity(gpu):
+    """Benchmark configuration C3's formats in a batch: Q4_K projections on the int8
+    matrix cores and the Q6_K head as the many-column GEMV, 5 slots at
+    different positions, against the oracle decoding each alone."""
+    say("model c3x2 batch 5")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=32000;eps=1e-5;theta=500000;" \
+           "wtype=q4_k;head=q6_k;embd=q4_k;ctx=512"
+    path, img = synth(gpu, spec, "t_c3x2b", 84)
+    rng = np.random.default_rng(19)
+    prompts = [rng.integers(0, 32000, k).tolist() for k in (5, 12, 40, 3, 70)]
+    out, err, same = batch_case(gpu, path, img, prompts, 6, 160)
+    gpu.image_free("t_c3x2b")
+    assert err <= LOGIT_TOL and same
+    assert len(set(out.ravel().tolist())) > 1
+
+
 def test_c5_moe_shape_batched_decode_parity(gpu):
     """Benchmark configuration C5's batch-16 decode at two layers: 16 slots (two past the
     128 window) decode together — one router product and one top-k over the
