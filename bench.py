@@ -291,12 +291,40 @@ def c2_blocks(ty, nblocks, rng):
     return raw.reshape(-1)
 
 
+def c2_cpu_baseline(seed, budget_s):
+    """The oracle's Q4_K 14336x4096 mat-vec (C2's value row) timed on the host
+    cores: repeated until `budget_s` of work is done (at least 3), rotating
+    over 16 copies of the matrix (528 MB, past any host cache, as the GPU's
+    pool is), weight GB/s."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(seed + 2)
+    rows, cols, copies = 14336, 4096, 16
+    one = c2_blocks(12, rows * cols // 256, rng)
+    pool = np.tile(one, copies).reshape(copies, -1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    for c in range(copies):
+        O.matvec(12, pool[c], rows, cols, x)          # first touch, untimed
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < budget_s:
+        O.matvec(12, pool[n % copies], rows, cols, x)
+        n += 1
+    dt = time.perf_counter() - t0
+    cores = int(O.lib().or_model_threads())
+    nproc, physical = host_cores()
+    return {"value": round(rows * cols // 256 * 144 * n / dt / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port", "nproc": nproc, "physical_cores": physical,
+            "sample": "%d mat-vecs of a Q4_K 14336x4096 matrix at batch 1 over 16 copies (pack + block dots, C "
+                      "restatement of the reference CPU backend, oracle/oracle.c, OpenMP %d threads), %.1f s"
+                      % (n, cores, dt)}
+
+
 def run_c2(args, native):
     """Benchmark configuration C2: each format × shape × batch, weights rotated over a
     pool of >= 512 MB of distinct prepared copies so the 256 MB last-level
     cache cannot serve them; one captured graph of launches, timed whole.
     Batch 1 is the decode GEMV; batch > 1 the int8 matrix-core product where
-    the format has one (Q8_0, Q4_K), else one GEMV a column."""
+    the format has one (Q8_0, Q4_K), else the many-column GEMV (Q6_K over
+    packs, Q4_0 over the f32 columns)."""
     lib = native.lib()
     rng = np.random.default_rng(args.seed)
     table = []
@@ -321,14 +349,14 @@ def run_c2(args, native):
             f32act = ty == 2
             for B in C2_BATCHES:
                 reps = max(ncopy, 32)
-                per = B if (B > 1 and ty == 2) else 1
                 native.check(lib.cj_graph_begin(), "graph")
                 for r in range(reps):
                     w = pool.h + (r % ncopy) * rows * prb
-                    if B == 1 or per > 1:
-                        for c in range(B):
-                            act = (xb.h + c * cols * 4) if f32act else (xp.h + c * xs)
-                            native.check(lib.cj_matvec(ty, y.h + c * rows * 4, w, act, rows, cols, 0, 0), "matvec")
+                    if B == 1:
+                        act = xb.h if f32act else xp.h
+                        native.check(lib.cj_matvec(ty, y.h, w, act, rows, cols, 0, 0), "matvec")
+                    elif f32act:
+                        native.check(lib.cj_matmul(ty, y.h, w, xb.h, rows, cols, B, cols * 4, rows, 0, 0), "matmul")
                     else:
                         native.check(lib.cj_matmul(ty, y.h, w, xp.h, rows, cols, B, xs, rows, 0, 0), "matmul")
                 g = native.handle(lib.cj_graph_end(), "graph")
@@ -343,8 +371,7 @@ def run_c2(args, native):
                 gbs = nbytes / (us * 1e-6) / 1e9
                 table.append({"format": fname, "rows": rows, "cols": cols, "batch": B, "us": round(us, 2),
                               "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
-                              "kernel": "gemv" if B == 1 else ("gemv per column" if per > 1 else
-                                                               "many-column gemv" if ty == 14 else "int8 mfma"),
+                              "kernel": "gemv" if B == 1 else ("many-column gemv" if ty in (2, 14) else "int8 mfma"),
                               "pool_copies": ncopy})
                 log("  %-5s %6d x %5d B %2d: %9.2f us  %7.1f GB/s  (%s, %d copies)" % (
                     fname, rows, cols, B, us, gbs, table[-1]["kernel"], ncopy))
@@ -364,7 +391,7 @@ def run_c2(args, native):
         "roofline": {"bound": "hbm", "achieved": head["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": head["frac"], "traffic": None},
         "table": table,
-        "cpu_baseline": None,
+        "cpu_baseline": c2_cpu_baseline(args.seed, args.cpu_seconds),
     }
     print(json.dumps(line), flush=True)
 

@@ -8,6 +8,7 @@
 
 // fp16 bits <-> f32 through the hardware converts (exact / round-to-nearest-even).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));   // a native 16-byte vector
+typedef float f32x4 __attribute__((ext_vector_type(4)));          // the same for f32 (HIP's float4 is a struct, copied by memcpy)
 
 // A 16-byte load of weights a decode step reads once: nontemporal, so the
 // stream does not displace what the caches hold for reuse (measured on
@@ -329,8 +330,20 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
     __syncthreads();
 }
 
-// The staged values as f32 into LDS (formats that read f32 activations).
-DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form, float *xf) {
+// An f32 activation in LDS by 32-element blocks, swizzled: float4 i of block
+// b at float4 slot 8b + (i ^ (b & 7)). Lanes that read float4 i of eight
+// consecutive blocks then touch every bank once (unswizzled, a lane a block
+// puts all 64 lanes on the same four banks).
+DEV int64_t swz32(int64_t idx) {
+    const int64_t b = idx >> 5;
+    const int i = (int)(idx >> 2) & 7;
+    return (b << 5) + ((i ^ (int)(b & 7)) << 2) + (idx & 3);
+}
+
+// The staged values as f32 into LDS (formats that read f32 activations);
+// swz: in the block-swizzled order above.
+DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, const float *w, int form, float *xf,
+                   bool swz = false) {
     // 16 values a thread a round, all loads issued before the first use
     const int64_t total = (int64_t)nblk * 256;
     for (int64_t e0 = 16 * threadIdx.x; e0 < total; e0 += 4096) {
@@ -362,9 +375,85 @@ DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, 
             for (int k = 0; k < 16; k++) v[k] = stage_value(x, n, e0 + k, norm, scale, w, form);
         }
 #pragma unroll
-        for (int k = 0; k < 4; k++) *(float4 *)(xf + e0 + 4 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        for (int k = 0; k < 4; k++)
+            *(float4 *)(xf + (swz ? swz32(e0 + 4 * k) : e0 + 4 * k)) =
+                make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
     }
     __syncthreads();
+}
+
+// ---- Q4_0, block by block (Quant.q40MatVecIntoAt, L/io/Quant.cajeta:1516-1545)
+// A block's dot starts at 0 and adds its 32 rounded products in the order
+// (lo_j − 8)·x[j], (hi_j − 8)·x[j + 16], j ascending; the row then adds the
+// rounded d·dot block after block. Blocks are independent until that fold.
+
+// Block b's 32 x values from the swizzled LDS row.
+DEV void q40_xblock(const float *xs, int b, float4 (&x)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = *(const float4 *)(xs + 32 * b + 4 * (i ^ (b & 7)));
+}
+
+// The block's 16 code bytes as the exact floats q − 8 (element order: the
+// low nibbles are elements 0..15, the high ones 16..31). q ^ 8 read as a
+// signed 4-bit field is q − 8.
+DEV void q40_decode(const uint4 &q, float (&v)[32]) {
+    const uint32_t ws[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            v[4 * g + jj] = (float)((int)(ws[g] << (28 - 8 * jj)) >> 28);
+            v[16 + 4 * g + jj] = (float)((int)(ws[g] << (24 - 8 * jj)) >> 28);
+        }
+    }
+}
+
+// The block's dot, from 0, in the reference's order.
+DEV float q40_dot(const float (&v)[32], const float4 (&x)[8]) {
+    float xf[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        xf[4 * i] = x[i].x; xf[4 * i + 1] = x[i].y; xf[4 * i + 2] = x[i].z; xf[4 * i + 3] = x[i].w;
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        dot = __fadd_rn(dot, __fmul_rn(v[j], xf[j]));
+        dot = __fadd_rn(dot, __fmul_rn(v[16 + j], xf[16 + j]));
+    }
+    return dot;
+}
+
+#define Q40_TS 68   // a wave's term row stride (floats): 16-byte reads, rows on distinct banks
+
+// A chain's n new terms (its LDS row) folded onto acc in block order.
+DEV float q40_fold(const float *row, int n, float acc) {
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        const float4 p = *(const float4 *)(row + i);
+        acc = __fadd_rn(acc, p.x);
+        acc = __fadd_rn(acc, p.y);
+        acc = __fadd_rn(acc, p.z);
+        acc = __fadd_rn(acc, p.w);
+    }
+    for (; i < n; i++) acc = __fadd_rn(acc, row[i]);
+    return acc;
+}
+
+// A whole sweep's 64 terms, unrolled: the reads all issued before the adds,
+// which the compiler can then interleave with other work.
+DEV float q40_fold64(const float *row, float acc) {
+    f32x4 p[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) p[i] = *(const f32x4 *)(row + 4 * i);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        acc = __fadd_rn(acc, p[i].x);
+        acc = __fadd_rn(acc, p[i].y);
+        acc = __fadd_rn(acc, p[i].z);
+        acc = __fadd_rn(acc, p[i].w);
+    }
+    return acc;
 }
 
 // Copy an already-packed activation (nblk blocks of 320 bytes) into LDS,

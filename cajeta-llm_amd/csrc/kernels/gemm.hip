@@ -689,3 +689,130 @@ DEV void gemm_q6k_cols(const cj_gemv_args &a) {
 extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c4(cj_gemv_args a) { gemm_q6k_cols<4>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c8(cj_gemv_args a) { gemm_q6k_cols<8>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c16(cj_gemv_args a) { gemm_q6k_cols<16>(a); }
+
+// Q4_0 many-column GEMV (cj_matmul over f32 activation columns): the
+// one-column kernel's sweeps for NC columns a workgroup, RW rows a wave
+// (4·RW a workgroup). A sweep's 64 blocks of every column are staged in LDS
+// (swizzled) once for the four waves. A lane runs its block's RW·NC dot
+// chains side by side, four code bytes at a time: the rows' 8 codes of those
+// bytes decoded once, then each column's 8 x values read once for all RW
+// rows; each chain still adds its products in the block's element order.
+// Lane l < RW·NC folds chain l (row l / NC, column l % NC) a sweep behind,
+// as the one-column kernel does. The next sweep's x is requested before its
+// codes, so staging it (at the end of a sweep) never waits for the weight
+// stream, and forming a sweep waits only for codes requested a sweep earlier.
+// A sweep's x for NC columns: float4 f = threadIdx.x + 256·m of its NC·512
+// (column f / 512, block (f % 512) / 8, float4 f % 8), into registers, then
+// swizzled into LDS. Unrolled by template recursion, so every index is a
+// constant from the start and the array lives in registers.
+template <int M, int NC>
+struct Q40X {
+    static DEV void load(f32x4 (&xr)[2 * NC], const cj_gemv_args &a, int64_t c0, int nb, int j) {
+        const int f = threadIdx.x + 256 * M, c = f >> 9, bb = (f & 511) >> 3, i = f & 7;
+        const int blk = min(64 * j + bb, nb - 1);
+        const float *col = (const float *)(a.xp + min(c0 + c, (int64_t)a.batch - 1) * a.xp_stride);
+        xr[M] = *(const f32x4 *)(col + 32 * (int64_t)blk + 4 * i);
+        if constexpr (M + 1 < 2 * NC) Q40X<M + 1, NC>::load(xr, a, c0, nb, j);
+    }
+    static DEV void store(const f32x4 (&xr)[2 * NC], float *xsm) {
+        const int f = threadIdx.x + 256 * M, c = f >> 9, bb = (f & 511) >> 3, i = f & 7;
+        *(f32x4 *)(xsm + c * 2048 + 32 * bb + 4 * (i ^ (bb & 7))) = xr[M];
+        if constexpr (M + 1 < 2 * NC) Q40X<M + 1, NC>::store(xr, xsm);
+    }
+};
+// A sweep's codes and scales for the wave's rows (blocks past the row re-read the last one).
+template <int RW>
+DEV void q40_fetch(uint4 (&q)[RW], uint32_t (&d)[RW], const uint8_t *const (&wr)[RW], int nb, int j, int lane) {
+    const int b = min(64 * j + lane, nb - 1);
+#pragma unroll
+    for (int k = 0; k < RW; k++) {
+        q[k] = ld_stream16(wr[k] + 16 * (int64_t)b);
+        d[k] = *(const uint16_t *)(wr[k] + 16 * (int64_t)nb + 2 * b);
+    }
+}
+
+template <int RW, int NC>
+DEV void gemm_q40_cols(const cj_gemv_args &a) {
+    constexpr int CH = RW * NC;
+    __shared__ __align__(16) float xsm[NC * 2048];
+    __shared__ __align__(16) float tb[4][2][CH][Q40_TS];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int nb = (int)(a.cols / 32), sweeps = (nb + 63) >> 6;
+    const int fr = min(lane, CH - 1);
+#pragma unroll
+    for (int k = 0; k < CH; k++) tb[w][1][k][lane] = 0.0f;
+    const int64_t c0 = (int64_t)blockIdx.y * NC;
+    const int64_t rbase = (int64_t)blockIdx.x * (4 * RW) + w * RW;
+    const uint8_t *wr[RW];
+#pragma unroll
+    for (int k = 0; k < RW; k++) wr[k] = a.w + min(rbase + k, a.rows - 1) * a.row_bytes;
+    f32x4 xr[2 * NC];
+    uint4 qn[RW];
+    uint32_t dn[RW];
+    Q40X<0, NC>::load(xr, a, c0, nb, 0);
+    q40_fetch<RW>(qn, dn, wr, nb, 0, lane);
+    Q40X<0, NC>::store(xr, xsm);
+    __syncthreads();
+    float acc = 0.0f;
+    const float *xb = xsm + 32 * lane;     // this lane's block of column 0
+    const int sw = lane & 7;               // its swizzle
+    for (int j = 0; j < sweeps; j++) {
+        uint4 q[RW];
+        uint32_t d[RW];
+#pragma unroll
+        for (int k = 0; k < RW; k++) { q[k] = qn[k]; d[k] = dn[k]; }
+        Q40X<0, NC>::load(xr, a, c0, nb, j + 1);    // past the last sweep: re-reads of the last block, never used
+        q40_fetch<RW>(qn, dn, wr, nb, j + 1, lane);
+        float dot[RW][NC];
+#pragma unroll
+        for (int k = 0; k < RW; k++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) dot[k][c] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            // code bytes 4g..4g+3 of each row: elements 4g+jj (low nibble) and 16+4g+jj (high)
+            float wl[RW][4], wh[RW][4];
+#pragma unroll
+            for (int k = 0; k < RW; k++) {
+                const uint32_t word = (g == 0 ? q[k].x : g == 1 ? q[k].y : g == 2 ? q[k].z : q[k].w) ^ 0x88888888u;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    wl[k][jj] = (float)((int)(word << (28 - 8 * jj)) >> 28);
+                    wh[k][jj] = (float)((int)(word << (24 - 8 * jj)) >> 28);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const f32x4 xl = *(const f32x4 *)(xb + c * 2048 + 4 * (g ^ sw));
+                const f32x4 xh = *(const f32x4 *)(xb + c * 2048 + 4 * ((4 + g) ^ sw));
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                    for (int k = 0; k < RW; k++) {
+                        dot[k][c] = __fadd_rn(dot[k][c], __fmul_rn(wl[k][jj], xl[jj]));
+                        dot[k][c] = __fadd_rn(dot[k][c], __fmul_rn(wh[k][jj], xh[jj]));
+                    }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < RW; k++) {
+            const float dk = h2f(d[k]);
+#pragma unroll
+            for (int c = 0; c < NC; c++) tb[w][j & 1][k * NC + c][lane] = __fmul_rn(dk, dot[k][c]);
+        }
+        acc = q40_fold64(tb[w][(j + 1) & 1][fr], acc);   // sweep j − 1 (a zeroed row before the first)
+        __syncthreads();               // every wave has read this sweep's x
+        Q40X<0, NC>::store(xr, xsm);
+        __syncthreads();
+    }
+    acc = q40_fold(tb[w][(sweeps - 1) & 1][fr], nb - 64 * (sweeps - 1), acc);
+    if (lane < CH) {
+        const int64_t row = rbase + lane / NC, col = c0 + lane % NC;
+        if (row < a.rows && col < a.batch) {
+            float *y = a.y + col * a.y_stride + a.y_off + row;
+            *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
+        }
+    }
+}
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q40_r2_c4(cj_gemv_args a) { gemm_q40_cols<2, 4>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q40_r4_c4(cj_gemv_args a) { gemm_q40_cols<4, 4>(a); }

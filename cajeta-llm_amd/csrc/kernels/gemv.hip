@@ -15,8 +15,11 @@
 //            epilogue: store, residual accumulate, RoPE + the fp16 K/V append,
 //            SiLU·up + the pack of the result, or the greedy argmax.
 //
-// The f32-activation formats (Q4_0, MXFP4, the f32 router) are summed in the
-// reference's element order, one adder lane a row fed products through LDS.
+// The f32-activation formats are summed in the reference's orders: Q4_0
+// block by block (its block dots are independent until the row's fold, so
+// lanes form them in parallel: q40_rows), MXFP4 in its scalar form and the
+// f32 router element by element, one adder lane a row fed products through
+// LDS (seq_body).
 //
 // Q4_K has its own body (gemv_q4k_body): one lane a whole 256-element block,
 // the first weight block of every lane in flight before the prologue, and
@@ -292,7 +295,8 @@ DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
 // The activation into LDS: a copied pack, the pack of an f32 vector, RMSNorm
 // + pack, or (f32-activation formats) the f32 values, normed or not. Ends on
 // a barrier.
-DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, uint8_t *sx, float *red, int bstride) {
+DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, uint8_t *sx, float *red, int bstride,
+                       bool swz = false) {
     const int64_t cols = a.cols;
     const int nblk = (int)((cols + 255) / 256);
     if (a.pro == CJ_PRO_PACKED) {
@@ -300,7 +304,7 @@ DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, 
     } else {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
         const float scale = norm ? stage_norm_scale(sl.X, cols, a.eps, red) : 1.0f;
-        if (f32act) stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx);
+        if (f32act) stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx, swz);
         else stage_pack(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr, bstride);
     }
 }
@@ -487,10 +491,7 @@ DEV void gemv_epilogue(const cj_gemv_args &a, const GemvSlice &sl, float v, floa
     }
 }
 
-// f32-activation formats, summed in the reference's element order:
-//   Q4_0  : Quant.q40MatVecIntoAt (io/Quant.cajeta:1516-1545): per block, dot
-//           from 0 over the 16 byte pairs (low nibble then high), then
-//           acc + d·dot;
+// The element-order chains:
 //   MXFP4 : Quant.mxfp4MatVecIntoScalar (io/Quant.cajeta:1146-1182):
 //           acc + (code·d)·x element by element;
 //   F32   : the router's plain row dot in column order.
@@ -522,8 +523,7 @@ DEV SeqItem<FMT> seq_fetch(const uint8_t *wr, int nb32, int blk) {
         it.s = 0;
     } else {
         it.q[0] = *(const u32x4 *)(wr + (int64_t)blk * 16);
-        if constexpr (FMT == CJ_Q4_0) it.s = *(const uint16_t *)(wr + (int64_t)nb32 * 16 + 2 * blk);
-        else it.s = wr[(int64_t)nb32 * 16 + blk];
+        it.s = wr[(int64_t)nb32 * 16 + blk];
     }
     return it;
 }
@@ -534,9 +534,9 @@ DEV void seq_xload(const float *xs, int blk, float4 (&x)[8]) {
     for (int j = 0; j < 8; j++) x[j] = *(const float4 *)(xs + 32 * blk + 4 * j);
 }
 
-// The block's 32 rounded products in add order into dst (and Q4_0's d).
+// The block's 32 rounded products in add order into dst.
 template <int FMT>
-DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst, float *dv) {
+DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst) {
     if constexpr (FMT == CJ_F32) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -548,7 +548,7 @@ DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst,
             o.w = __fmul_rn(__uint_as_float(it.q[j].w), x.w);
             *(float4 *)(dst + 4 * j) = o;
         }
-    } else if constexpr (FMT == CJ_MXFP4) {
+    } else {
         // element k: code byte k & 15, low nibble for k < 16, high after;
         // |code| from the low three bits by a byte permute of {0,1,2,3,4,6,8,12},
         // the sign from bit 3. Code 8 comes out as -0 where the reference has
@@ -571,22 +571,6 @@ DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst,
             }
             *(float4 *)(dst + 4 * g) = make_float4(ov[0], ov[1], ov[2], ov[3]);
         }
-    } else {
-        // products (lo_j − 8)·x[j], (hi_j − 8)·x[j + 16], j ascending
-        *dv = h2f(it.s);
-        const uint32_t ws[4] = {it.q[0].x, it.q[0].y, it.q[0].z, it.q[0].w};
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const uint32_t word = ws[g >> 1], sh = 16 * (g & 1);
-            const float4 xl = xr[g >> 1], xh = xr[4 + (g >> 1)];
-            const uint32_t b0 = (word >> sh) & 255u, b1 = (word >> (sh + 8)) & 255u;
-            float4 o;
-            o.x = __fmul_rn((float)(int)(b0 & 15u) - 8.0f, g & 1 ? xl.z : xl.x);
-            o.y = __fmul_rn((float)(int)(b0 >> 4) - 8.0f, g & 1 ? xh.z : xh.x);
-            o.z = __fmul_rn((float)(int)(b1 & 15u) - 8.0f, g & 1 ? xl.w : xl.y);
-            o.w = __fmul_rn((float)(int)(b1 >> 4) - 8.0f, g & 1 ? xh.w : xh.y);
-            *(float4 *)(dst + 4 * g) = o;
-        }
     }
 }
 
@@ -608,13 +592,12 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
     constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
     constexpr int S = 32 * TB + 4;            // product row stride (floats): 16-byte reads by 16 lanes, distinct banks
     __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
-    __shared__ float dvs[2][64 * SEQ_TB];                 // ROWS·TB = 192
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int nb32 = (int)(a.cols / 32), ntiles = (nb32 + TB - 1) / TB;
     const int pl = t - 64, prow = pl % ROWS, pb = pl / ROWS;
     const uint8_t *wr = sl.W + min(sl.row0 + prow, a.rows - 1) * a.row_bytes;
-    float *pdst = prod[0] + prow * S + 32 * pb, *pdv = dvs[0] + prow * TB + pb;
-    constexpr int PBUF = 64 * SEQ_S, DBUF = 64 * SEQ_TB;
+    float *pdst = prod[0] + prow * S + 32 * pb;
+    constexpr int PBUF = 64 * SEQ_S;
     // both loops run a whole number of D-tile rounds: the producer's body
     // is then free of branches (tiles past the end are formed into the idle
     // buffer and never read)
@@ -623,71 +606,41 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
     if (w == 0) {
         __syncthreads();
         const float *pr0 = prod[0] + min(lane, ROWS - 1) * S;
-        const float *dv0 = dvs[0] + min(lane, ROWS - 1) * TB;
         // three blocks' products read before their first add
-        auto add3 = [&](const float *pr, const float *dv, int b0) {
+        auto add3 = [&](const float *pr, int b0) {
             float4 p[24];
 #pragma unroll
             for (int q = 0; q < 24; q++) p[q] = *(const float4 *)(pr + 32 * b0 + 4 * q);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int b = 0; b < 3; b++) {
-                if constexpr (FMT == CJ_Q4_0) {
-                    float dot = 0.0f;
-#pragma unroll
-                    for (int q = 8 * b; q < 8 * b + 8; q++) {
-                        dot = __fadd_rn(dot, p[q].x);
-                        dot = __fadd_rn(dot, p[q].y);
-                        dot = __fadd_rn(dot, p[q].z);
-                        dot = __fadd_rn(dot, p[q].w);
-                    }
-                    acc = __fadd_rn(acc, __fmul_rn(dv[b0 + b], dot));
-                } else {
-#pragma unroll
-                    for (int q = 8 * b; q < 8 * b + 8; q++) {
-                        acc = __fadd_rn(acc, p[q].x);
-                        acc = __fadd_rn(acc, p[q].y);
-                        acc = __fadd_rn(acc, p[q].z);
-                        acc = __fadd_rn(acc, p[q].w);
-                    }
-                }
+            for (int q = 0; q < 24; q++) {
+                acc = __fadd_rn(acc, p[q].x);
+                acc = __fadd_rn(acc, p[q].y);
+                acc = __fadd_rn(acc, p[q].z);
+                acc = __fadd_rn(acc, p[q].w);
             }
         };
-        auto add1 = [&](const float *pr, const float *dv, int b) {
-            if constexpr (FMT == CJ_Q4_0) {
-                float dot = 0.0f;
+        auto add1 = [&](const float *pr, int b) {
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                    dot = __fadd_rn(dot, p.x);
-                    dot = __fadd_rn(dot, p.y);
-                    dot = __fadd_rn(dot, p.z);
-                    dot = __fadd_rn(dot, p.w);
-                }
-                acc = __fadd_rn(acc, __fmul_rn(dv[b], dot));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
-                    acc = __fadd_rn(acc, p.x);
-                    acc = __fadd_rn(acc, p.y);
-                    acc = __fadd_rn(acc, p.z);
-                    acc = __fadd_rn(acc, p.w);
-                }
+            for (int q = 0; q < 8; q++) {
+                const float4 p = *(const float4 *)(pr + 32 * b + 4 * q);
+                acc = __fadd_rn(acc, p.x);
+                acc = __fadd_rn(acc, p.y);
+                acc = __fadd_rn(acc, p.z);
+                acc = __fadd_rn(acc, p.w);
             }
         };
         for (int i = 0; i < nit; i++) {
             const float *pr = pr0 + (i & 1) * PBUF;
-            const float *dv = dv0 + (i & 1) * DBUF;
             const int nb = i < ntiles ? min(TB, nb32 - i * TB) : 0;
             if (nb == TB) {
 #pragma unroll(TB <= 6 ? TB / 3 : 2)
-                for (int b0 = 0; b0 < TB; b0 += 3) add3(pr, dv, b0);
+                for (int b0 = 0; b0 < TB; b0 += 3) add3(pr, b0);
             } else {
                 // a short tile (the row's last): whole chunks of three, then single blocks
                 int b0 = 0;
-                for (; b0 + 3 <= nb; b0 += 3) add3(pr, dv, b0);
-                for (int b = b0; b < nb; b++) add1(pr, dv, b);
+                for (; b0 + 3 <= nb; b0 += 3) add3(pr, b0);
+                for (int b = b0; b < nb; b++) add1(pr, b);
             }
             __syncthreads();
         }
@@ -698,7 +651,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
         for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * TB + pb);
         seq_xload(xs, min(pb, nb32 - 1), xr[0]);
         seq_xload(xs, min(TB + pb, nb32 - 1), xr[1]);
-        seq_products<FMT>(ring[0], xr[0], pdst, pdv);
+        seq_products<FMT>(ring[0], xr[0], pdst);
         ring[0] = seq_fetch<FMT>(wr, nb32, D * TB + pb);
         __syncthreads();
         // round j of an iteration forms tile i + 1 from ring[(j + 1) % D] and
@@ -710,13 +663,87 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
                 const int r = (j + 1) % D;
                 const int nbuf = (j + 1) & 1;      // D is even, so (i + 1) & 1
                 seq_xload(xs, min((i + 2) * TB + pb, nb32 - 1), xr[j & 1]);
-                seq_products<FMT>(ring[r], xr[nbuf], pdst + nbuf * PBUF, pdv + nbuf * DBUF);
+                seq_products<FMT>(ring[r], xr[nbuf], pdst + nbuf * PBUF);
                 ring[r] = seq_fetch<FMT>(wr, nb32, (i + 1 + D) * TB + pb);
                 __syncthreads();
             }
         }
     }
     return acc;
+}
+
+// Q4_0, block-parallel: wave w owns RW rows of the workgroup's 4·RW, and
+// lane L forms the block terms d·dot of blocks L, L + 64, … (a sweep of 64
+// blocks at a time) for all RW rows from one read of each x block; lane k <
+// RW folds row k's terms in block order from the wave's LDS rows, a sweep
+// behind, in the same straight-line code as the next sweep's products so the
+// fold's dependent adds fill their gaps. (Before the first sweep it folds a
+// zeroed row: +0 added to the +0 start changes no bit. Lanes past RW fold a
+// copy of the last row and drop it.) The next sweep's codes and scales are in
+// flight while a sweep is formed; x comes from LDS, so the two never wait on
+// each other. Returns row t's sum on thread t < 4·RW.
+template <int RW>
+DEV float q40_rows(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
+    __shared__ __align__(16) float tb[4][2][RW][Q40_TS];
+    __shared__ float rv[4 * RW];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int nb = (int)(a.cols / 32), sweeps = (nb + 63) >> 6;
+    const int fr = min(lane, RW - 1);
+#pragma unroll
+    for (int k = 0; k < RW; k++) tb[w][1][k][lane] = 0.0f;
+    const uint8_t *wr[RW];
+#pragma unroll
+    for (int k = 0; k < RW; k++) wr[k] = sl.W + min(sl.row0 + w * RW + k, a.rows - 1) * a.row_bytes;
+    uint4 qn[RW];
+    uint32_t dn[RW];
+    // a sweep's codes and scales (blocks past the row re-read the last one, never folded)
+    auto fetch = [&](int j) {
+        const int b = min(64 * j + lane, nb - 1);
+#pragma unroll
+        for (int k = 0; k < RW; k++) {
+            qn[k] = ld_stream16(wr[k] + 16 * (int64_t)b);
+            dn[k] = *(const uint16_t *)(wr[k] + 16 * (int64_t)nb + 2 * b);
+        }
+    };
+    fetch(0);
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f;
+    for (int j = 0; j < sweeps; j++) {
+        uint4 q[RW];
+        uint32_t d[RW];
+#pragma unroll
+        for (int k = 0; k < RW; k++) { q[k] = qn[k]; d[k] = dn[k]; }
+        fetch(j + 1);
+        float4 x[8];
+        q40_xblock(xs, min(64 * j + lane, nb - 1), x);
+#pragma unroll
+        for (int k = 0; k < RW; k++) {
+            float v[32];
+            q40_decode(q[k], v);
+            tb[w][j & 1][k][lane] = __fmul_rn(h2f(d[k]), q40_dot(v, x));
+        }
+        acc = q40_fold64(tb[w][(j + 1) & 1][fr], acc);   // sweep j − 1: whole (only the last can be short)
+        __builtin_amdgcn_wave_barrier();
+    }
+    acc = q40_fold(tb[w][(sweeps - 1) & 1][fr], nb - 64 * (sweeps - 1), acc);
+    if (lane < RW) rv[w * RW + lane] = acc;
+    __syncthreads();
+    return t < 4 * RW ? rv[t] : 0.0f;
+}
+
+// The Q4_0 GEMV: prologue (x, or its RMSNorm, staged swizzled), the rows,
+// and the common epilogues.
+template <int RW>
+DEV void q40_gemv(const cj_gemv_args &a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *red = (float *)smem;
+    float *bmax = red + 256;
+    uint8_t *sx = smem + LDS_SCRATCH;
+    const GemvSlice sl = gemv_slice(a);
+    gemv_prologue(a, sl, true, sx, red, 320, true);
+    const EpiPre pre = epi_prefetch(a, sl);
+    const float v = q40_rows<RW>(a, sl, (const float *)sx);
+    gemv_epilogue(a, sl, v, bmax, pre);
 }
 
 // Generic body (Q6_K, Q8_0 and the f32-activation formats).
@@ -1287,12 +1314,12 @@ MXQ8_KBS(g, CJ_EPI_GLU, 4)
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)
-GEMV_KERNEL(cj_gemv_q40, CJ_Q4_0, 64, 1)
+// cj_gemv_q40b_r<RW>: Q4_0 block-parallel, RW rows a wave (4·RW a workgroup)
+extern "C" __global__ void __launch_bounds__(256) cj_gemv_q40b_r2(cj_gemv_args a) { q40_gemv<2>(a); }
+extern "C" __global__ void __launch_bounds__(256) cj_gemv_q40b_r4(cj_gemv_args a) { q40_gemv<4>(a); }
 GEMV_KERNEL(cj_gemv_mxfp4, CJ_MXFP4, 64, 1)
 GEMV_KERNEL(cj_gemv_f32, CJ_F32, 64, 1)
-GEMV_KERNEL(cj_gemv_q40_r32, CJ_Q4_0, 32, 1)
 GEMV_KERNEL(cj_gemv_mxfp4_r32, CJ_MXFP4, 32, 1)
 GEMV_KERNEL(cj_gemv_f32_r32, CJ_F32, 32, 1)
-GEMV_KERNEL(cj_gemv_q40_r1, CJ_Q4_0, 1, 1)
 GEMV_KERNEL(cj_gemv_mxfp4_r1, CJ_MXFP4, 1, 1)
 GEMV_KERNEL(cj_gemv_f32_r1, CJ_F32, 1, 1)

@@ -57,7 +57,7 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"q4kQ8WaveMatVecKernel", "cj_gemv_q4k_cs_b16"},
         {"q6kQ8WaveMatVecKernel", "cj_gemv_q6k_l64"},
         {"q80Q8WaveMatVecKernel", "cj_gemv_q80_l64"},
-        {"q40F32WaveMatVecKernel", "cj_gemv_q40"},
+        {"q40F32WaveMatVecKernel", "cj_gemv_q40b_r4"},
         {"mxfp4MatVecKernel", "cj_gemv_mxfp4"},
         {"mxfp4MatVecKernelCoopQ8", "cj_gemv_mxq8_s_k3_r4"},
         {"mxfp4QuantActKernel", "cj_gemv_mxq8_s_k3_r4"},   // the quant is that kernel's prologue
@@ -267,12 +267,23 @@ GemvPlan plan_gemv(int type, int64_t rows, int64_t cols, int target, int pro, in
         return p;
     }
     const char *fam = type == CJ_Q4_K ? "cj_gemv_q4k" : type == CJ_Q6_K ? "cj_gemv_q6k" : type == CJ_Q8_0 ? "cj_gemv_q80"
-                      : type == CJ_Q4_0 ? "cj_gemv_q40" : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
+                      : type == CJ_MXFP4 ? "cj_gemv_mxfp4" : "cj_gemv_f32";
+    if (type == CJ_Q4_0) {
+        // block-parallel: RW rows a wave, 4·RW a workgroup; 2 where 4 would
+        // leave the matrix under two workgroups a CU
+        const int rw = rows <= 8 * (int64_t)std::max(1, g.cus) * 2 ? 2 : 4;
+        p.kernel = std::string("cj_gemv_q40b_r") + std::to_string(rw);
+        p.rows_per_wg = 4 * rw;
+        p.grid = (uint32_t)((rows + p.rows_per_wg - 1) / p.rows_per_wg);
+        p.per_copy = p.grid;
+        p.lds = 3072 + (uint32_t)((cols + 255) / 256 * 1024);
+        return p;
+    }
     if (is_f32_act(type)) {
         // 64 rows a workgroup, each summed in element order by one lane; 32
         // (six blocks a tile for the producers, half the tiles) where 64-row
         // workgroups would leave a quarter of the CUs idle. Measured: MXFP4
-        // 11520×2880 22.7 → 19.8 µs at 32; Q4_0 14336×4096 31 → 40 µs at 32
+        // 11520×2880 22.7 → 19.8 µs at 32; a 14336×4096 chain 31 → 40 µs at 32
         // (1 for at most 64 rows — a router: every producer lane on one row,
         // a 2880-wide row in one tile, a workgroup a row)
         const int R = rows <= 64 ? 1 : rows <= 48 * (int64_t)std::max(1, g.cus) ? 32 : 64;
@@ -317,14 +328,26 @@ bool gemm_supported(int type) { return type == CJ_Q8_0 || type == CJ_Q4_K || typ
 // gate|up and head 2.1-2.3 TB/s tiled vs 1.1 split-K; q|k|v, o and down
 // 0.8-1.1 TB/s split-K vs 0.3-0.5 tiled.
 int run_gemm(const cj_gemv_args &a) {
-    if (!gemm_supported(a.type)) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
+    if (!gemm_supported(a.type) && a.type != CJ_Q4_0) return fail(CJ_ERR_ARG, "gemm: type %d is not served", a.type);
     if (a.batch <= 0 || a.rows <= 0) return fail(CJ_ERR_ARG, "gemm: %d columns, %lld rows", a.batch, (long long)a.rows);
     char name[32];
+    if (a.type == CJ_Q4_0) {
+        // many-column GEMV over f32 columns: 4·RW rows a workgroup, 4 columns a
+        // grid row; RW = 4, or 2 where 4 would leave under two workgroups a CU
+        // (measured at 4096x4096: 4 columns 11.3 -> 10.7 us; 16 columns 4 rows a wave 24.4 us, 2: 28.6)
+        if (a.cols % 32) return fail(CJ_ERR_ARG, "gemm: Q4_0 rows are whole 32-element blocks");
+        const int64_t cgroups = (a.batch + 3) / 4;
+        if (cgroups > 65535) return fail(CJ_ERR_ARG, "gemm: %d columns exceed the grid", a.batch);
+        const int rw = (a.rows + 15) / 16 * cgroups >= 2 * (int64_t)std::max(1, g.cus) ? 4 : 2;
+        snprintf(name, sizeof name, "cj_gemm_q40_r%d_c4", rw);
+        return launch2(name, (uint32_t)((a.rows + 4 * rw - 1) / (4 * rw)), (uint32_t)cgroups, 256, 0, a);
+    }
     if (a.type == CJ_Q6_K) {
         // many-column GEMV: 16 rows a workgroup, NC columns a grid row
         const int nc = a.batch <= 4 ? 4 : a.batch <= 8 ? 8 : 16;
         const int64_t nb = a.cols / 256;
         if (a.cols % 256) return fail(CJ_ERR_ARG, "gemm: Q6_K rows are whole 256-element blocks");
+        if ((a.batch + nc - 1) / nc > 65535) return fail(CJ_ERR_ARG, "gemm: %d columns exceed the grid", a.batch);
         snprintf(name, sizeof name, "cj_gemm_q6k_c%d", nc);
         return launch2(name, (uint32_t)((a.rows + 15) / 16), (uint32_t)((a.batch + nc - 1) / nc), 256,
                        (uint32_t)(4 * nc * (nb + 1) * 4), a);
@@ -383,8 +406,8 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q6k_l64", "cj_gemv_q6k_l32", "cj_gemv_q6k_l16", "cj_gemv_q6k_l8",
         "cj_gemv_q80_l64", "cj_gemv_q80_l32", "cj_gemv_q80_l16", "cj_gemv_q80_l8",
         "cj_gemv_q80_l64_n2", "cj_gemv_q80_l32_n2", "cj_gemv_q80_l16_n2", "cj_gemv_q80_l8_n2",
-        "cj_gemv_q40", "cj_gemv_mxfp4", "cj_gemv_f32", "cj_gemv_q40_r32", "cj_gemv_mxfp4_r32", "cj_gemv_f32_r32",
-        "cj_gemv_q40_r1", "cj_gemv_mxfp4_r1", "cj_gemv_f32_r1",
+        "cj_gemv_q40b_r2", "cj_gemv_q40b_r4", "cj_gemm_q40_r2_c4", "cj_gemm_q40_r4_c4",
+        "cj_gemv_mxfp4", "cj_gemv_f32", "cj_gemv_mxfp4_r32", "cj_gemv_f32_r32", "cj_gemv_mxfp4_r1", "cj_gemv_f32_r1",
         "cj_moe_combine", "cj_moe_combine_norm",
         "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
@@ -641,9 +664,10 @@ int32_t cj_matvec_mxfp4_q8(int64_t y, int64_t w, int64_t x, int64_t rows, int64_
 int32_t cj_matmul(int32_t type, int64_t y, int64_t w, int64_t xp, int64_t rows, int64_t cols, int32_t ncols,
                   int64_t xp_stride, int64_t y_stride, int64_t y_off, int32_t accum) {
     const int64_t prb = prepared_row_bytes(type, cols);
-    if (!gemm_supported(type) || prb <= 0 || rows <= 0 || ncols <= 0)
+    const bool f32cols = type == CJ_Q4_0;      // f32 activation columns (the format reads f32)
+    if (!(gemm_supported(type) || f32cols) || prb <= 0 || rows <= 0 || ncols <= 0)
         return fail(CJ_ERR_ARG, "cj_matmul: type %d with %lld columns x %d is not served", type, (long long)cols, ncols);
-    const int64_t pack_bytes = (cols + 255) / 256 * 320;
+    const int64_t pack_bytes = f32cols ? cols * 4 : (cols + 255) / 256 * 320;
     if (xp_stride < pack_bytes || y_stride < y_off + rows || y_off < 0)
         return fail(CJ_ERR_ARG, "cj_matmul: strides %lld/%lld smaller than one column", (long long)xp_stride, (long long)y_stride);
     if (!in_buffer(dptr(w), rows * prb)) return fail(CJ_ERR_ARG, "cj_matmul: weight smaller than %lld prepared rows", (long long)rows);
@@ -653,7 +677,7 @@ int32_t cj_matmul(int32_t type, int64_t y, int64_t w, int64_t xp, int64_t rows, 
     a.w = (const uint8_t *)dptr(w); a.xp = (const uint8_t *)dptr(xp); a.y = (float *)dptr(y);
     a.rows = rows; a.cols = cols; a.row_bytes = prb; a.type = type; a.batch = ncols;
     a.xp_stride = xp_stride; a.y_stride = y_stride; a.y_off = y_off;
-    a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.pro = CJ_PRO_PACKED;
+    a.epi = accum ? CJ_EPI_ACCUM : CJ_EPI_STORE; a.pro = f32cols ? CJ_PRO_F32 : CJ_PRO_PACKED;
     return run_gemm(a);
 }
 

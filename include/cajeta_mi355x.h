@@ -132,9 +132,10 @@ int32_t cj_matvec_mxfp4_q8(int64_t y, int64_t w, int64_t x, int64_t rows, int64_
 /* Y[c][y_off + r] (+)= Σ_k W[r][k]·x_c[k] for ncols activation columns at once,
  * each column bit-for-bit what cj_matvec gives it: on the int8 matrix cores
  * for Q8_0 and Q4_K, as a many-column GEMV (each weight read once for up to
- * 16 columns) for Q6_K. `xp` holds the columns' packs (per-256 for Q4_K and
- * Q6_K, per-32 for Q8_0) xp_stride bytes apart; y holds the outputs y_stride
- * floats apart. Replaces the many-column kernels the reference routes
+ * 16 columns, 4 for Q4_0) for Q6_K and Q4_0. `xp` holds the columns' packs
+ * (per-256 for Q4_K and Q6_K, per-32 for Q8_0; for Q4_0 the f32 columns
+ * themselves, at least cols·4 bytes a column) xp_stride bytes apart; y holds
+ * the outputs y_stride floats apart. Replaces the many-column kernels the reference routes
  * batched decode and prefill rows through: Linear.matmulBatchKeep
  * (model/Linear.cajeta:3576) over q4kQ8WaveMatVecColsKernel
  * (io/QuantKernel.cajeta:33646), q4kQ8X8RowsKernel (:1479) and

@@ -391,15 +391,16 @@ def test_kernel_registry_answers_reference_names(gpu):
     assert gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
 
 
-@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12), ("q6_k", 14)])
+@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12), ("q6_k", 14), ("q4_0", 2)])
 @pytest.mark.parametrize("rows,cols,ncols", [(300, 512, 1), (1024, 4096, 4), (64, 1408, 8), (272, 4096, 17),
                                              (96, 14336, 16), (160, 2048, 70), (100, 1408, 80), (40, 512, 33),
                                              (130, 768, 200), (37, 4096, 5)])
 def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
     """The batched product (int8 matrix cores for Q8_0 and Q4_K, the
-    many-column GEMV for Q6_K): every output column is the one-column product
-    of its activation pack, bit for bit (integer sub-block dots are exact;
-    the float fold runs in the reference's block order)."""
+    many-column GEMV for Q6_K and Q4_0): every output column is the one-column
+    product of its activation pack (Q4_0: of its f32 column), bit for bit
+    (integer sub-block dots are exact; the float fold runs in the reference's
+    block order; Q4_0's block dots in its element order)."""
     if ty in (O.Q4_K, O.Q6_K) and cols % 256:
         pytest.skip("K-quant rows are whole 256-element blocks")
     say("matmul", name, rows, cols, ncols)
@@ -411,11 +412,13 @@ def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
     src, w = gpu.Buffer.of(raw), gpu.Buffer(prb * rows)
     gpu.native.check(lib.cj_prepare_weight(w.h, src.h, ty, rows, cols), "prepare")
     npad = (cols + 255) // 256 * 256
-    stride = npad // 256 * 320 + 64                     # a gap between columns the kernel must skip
+    f32cols = ty == O.Q4_0
+    used = cols * 4 if f32cols else npad // 256 * 320
+    stride = used + 64                                  # a gap between columns the kernel must skip
     packs = np.zeros((ncols, stride), np.uint8)
     for c in range(ncols):
         x = (rng.standard_normal(cols) * rng.uniform(0.1, 4)).astype(np.float32)
-        packs[c, :npad // 256 * 320] = O.q8k_pack(x, per32=(ty == O.Q8_0), npad=npad)
+        packs[c, :used] = x.view(np.uint8) if f32cols else O.q8k_pack(x, per32=(ty == O.Q8_0), npad=npad)
     ystride, yoff = rows + 5, 3
     y0 = rng.standard_normal((ncols, ystride)).astype(np.float32)
     xb = gpu.Buffer.of(packs.reshape(-1))
@@ -424,7 +427,8 @@ def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
         gpu.native.check(lib.cj_matmul(ty, yb.h, w.h, xb.h, rows, cols, ncols, stride, ystride, yoff, accum), "matmul")
         got = yb.download(np.float32, ncols * ystride).reshape(ncols, ystride)
         for c in range(ncols):
-            ref = O.matvec_packed(ty, raw, rows, cols, packs[c, :npad // 256 * 320])
+            ref = (O.matvec(ty, raw, rows, cols, packs[c, :used].view(np.float32)) if f32cols
+                   else O.matvec_packed(ty, raw, rows, cols, packs[c, :used]))
             if accum:
                 ref = (y0[c, yoff:yoff + rows] + ref).astype(np.float32)
             assert np.array_equal(got[c, yoff:yoff + rows].view(np.uint32), ref.view(np.uint32)), \
@@ -432,6 +436,44 @@ def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
             # outside the column's rows nothing is written
             assert np.array_equal(got[c, :yoff], y0[c, :yoff]) and np.array_equal(got[c, yoff + rows:], y0[c, yoff + rows:])
         yb.free()
+
+
+@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_0", 2), ("q4_k", 12), ("q6_k", 14)])
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)])
+def test_c2_shapes_match_oracle(gpu, O, name, ty, rows, cols):
+    """The C2 microbenchmark's shapes and kernels, outputs checked: the
+    batch-1 GEMV and the 16-column product (the launches bench.py times),
+    every output bit for bit the oracle's mat-vec of its column."""
+    say("c2 shape", name, rows, cols)
+    rng = np.random.default_rng(rows + cols + ty)
+    be, bb = O.BLOCK[ty]
+    raw = rand_blocks(O, ty, rows * cols // be, rng)
+    lib = gpu.native.lib()
+    prb = lib.cj_prepared_row_bytes(ty, cols)
+    src, w = gpu.Buffer.of(raw), gpu.Buffer(prb * rows)
+    gpu.native.check(lib.cj_prepare_weight(w.h, src.h, ty, rows, cols), "prepare")
+    src.free()
+    B = 16
+    x = rng.standard_normal((B, cols)).astype(np.float32)
+    f32cols = ty == O.Q4_0
+    if f32cols:
+        act, stride = gpu.Buffer.of(x.reshape(-1)), cols * 4
+    else:
+        packs = np.stack([O.q8k_pack(x[c], per32=(ty == O.Q8_0)) for c in range(B)])
+        act, stride = gpu.Buffer.of(packs.reshape(-1)), packs.shape[1]
+    refs = [O.matvec(ty, raw, rows, cols, x[c]) for c in range(B)]
+    y = gpu.Buffer(B * rows * 4)
+    gpu.native.check(lib.cj_matvec(ty, y.h, w.h, act.h, rows, cols, 0, 0), "matvec")
+    got = y.download(np.float32, rows)
+    assert np.array_equal(got.view(np.uint32), refs[0].view(np.uint32)), \
+        "%s %dx%d batch 1: %d rows differ" % (name, rows, cols, int((got != refs[0]).sum()))
+    gpu.native.check(lib.cj_matmul(ty, y.h, w.h, act.h, rows, cols, B, stride, rows, 0, 0), "matmul")
+    got = y.download(np.float32, B * rows).reshape(B, rows)
+    for c in range(B):
+        assert np.array_equal(got[c].view(np.uint32), refs[c].view(np.uint32)), \
+            "%s %dx%d batch %d column %d: %d rows differ" % (name, rows, cols, B, c, int((got[c] != refs[c]).sum()))
+    for b in (w, act, y):
+        b.free()
 
 
 def test_matmul_refuses_short_buffers(gpu, O):
