@@ -376,8 +376,11 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
             if ((rc = upload_weight(lname(l, "ffn_gate_inp.weight"), L.router, n_experts, hidden))) return rc;
             if ((rc = fuse_rows({lname(l, "ffn_gate_exps.weight"), lname(l, "ffn_up_exps.weight")}, L.gu_exps, true, expert_ffn, n_experts))) return rc;
             if ((rc = upload_weight(lname(l, "ffn_down_exps.weight"), L.down_exps, (int)((int64_t)n_experts * hidden), expert_ffn))) return rc;
-            if (L.down_exps.type != CJ_MXFP4 && L.down_exps.type != CJ_Q4_0 && L.down_exps.type != CJ_Q8_0)
-                return fail(CJ_ERR_IO, "model: expert type %d not served", L.down_exps.type);
+            // every GEMV format serves an expert bank through the indirected
+            // launch (the K-quants need whole 256-element rows)
+            for (const DevW *e : {&L.gu_exps, &L.down_exps})
+                if (!gemv_supported(e->type, e->cols) || e->type == CJ_F32)
+                    return fail(CJ_ERR_IO, "model: expert type %d x %lld columns not served", e->type, (long long)e->cols);
         } else {
             if ((rc = fuse_rows({lname(l, "ffn_gate.weight"), lname(l, "ffn_up.weight")}, L.gu, true, ffn, 0))) return rc;
             if ((rc = upload_weight(lname(l, "ffn_down.weight"), L.down, hidden, ffn))) return rc;

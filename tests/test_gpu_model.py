@@ -340,6 +340,29 @@ def test_c5_moe_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+@pytest.mark.parametrize("expert_type", ["q8_0", "q4_0", "q4_k", "q6_k"])
+def test_moe_expert_formats_greedy_and_batched_parity(gpu, expert_type):
+    """MoE experts in the other GEMV formats (the benchmark models use MXFP4):
+    Q8_0, Q4_K and Q6_K over int8 packs, Q4_0 over the f32 rows through the
+    block-parallel GEMV, all indirected over the selections; 8 experts top-2
+    at d 512, one sequence and a batch of three against the oracle, bit for
+    bit."""
+    say("model moe experts", expert_type)
+    spec = ("layers=2;hidden=512;heads=8;kv=2;hd=64;ffn=512;vocab=2048;eps=1e-5;theta=10000;wtype=q8_0;"
+            "head=q8_0;embd=q8_0;experts=8;used=2;expert_ffn=512;expert_type=%s;ctx=256" % expert_type)
+    name = "t_moe_" + expert_type
+    path, img = synth(gpu, spec, name, 91)
+    rng = np.random.default_rng(23)
+    prompt = rng.integers(0, 2048, 9).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 12, 128)
+    assert g == o and run_pair.bit_identical, (g, o, err)
+    prompts = [rng.integers(0, 2048, k).tolist() for k in (4, 11, 7)]
+    out, err, same = batch_case(gpu, path, img, prompts, 5, 128)
+    gpu.image_free(name)
+    assert err <= LOGIT_TOL and same
+    assert len(set(out.ravel().tolist())) > 1
+
+
 def test_c3_shape_batched_decode_parity(gpu):
     """Benchmark configuration C3's formats in a batch: Q4_K projections on the int8
     matrix cores and the Q6_K head as the many-column GEMV, 5 slots at
