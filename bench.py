@@ -391,7 +391,7 @@ def run_c2(args, native):
         "roofline": {"bound": "hbm", "achieved": head["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": head["frac"], "traffic": None},
         "table": table,
-        "cpu_baseline": c2_cpu_baseline(args.seed, args.cpu_seconds),
+        "cpu_baseline": None if args.no_cpu else c2_cpu_baseline(args.seed, args.cpu_seconds),
     }
     print(json.dumps(line), flush=True)
 

@@ -40,6 +40,16 @@ DEV v4i mfma_i8(long a, long b) {
 
 DEV long ld8(const uint8_t *p) { return *(const long *)p; }
 
+// K loops run every group but the last with an unconditional prefetch of the
+// next, then the last without one: a load under a branch would make the
+// compiler wait at the join for every load in flight (the prefetch
+// included), and a prefetch in the last group would only re-read data and
+// delay the end. PF<true> / PF<false> pick the form at compile time.
+template <bool B>
+struct PF {
+    static constexpr bool on = B;
+};
+
 #define GEMM_CS 336   // LDS bytes a staged column (the 320-byte block, padded against bank conflicts)
 
 // The group's activation blocks of the tile's columns into registers (NV
@@ -155,22 +165,24 @@ DEV void gemm_q80(const cj_gemv_args &a, uint8_t *lds) {
 #pragma unroll
     for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)bsrc[i];
     q80_fetch(A, wa, wd, 0, (int)min((int64_t)8, nb32));
-    for (int64_t g = 0; g < ngrp; g++) {
+    auto group = [&](int64_t g, auto pf) {
         const int nj = (int)min((int64_t)8, nb32 - 8 * g);
         __syncthreads();   // the previous group's LDS reads are done
 #pragma unroll
         for (int i = 0; i < BStage<NT>::NV; i++)
             if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
         __syncthreads();
-        if (g + 1 < ngrp) {
+        if constexpr (decltype(pf)::on) {
 #pragma unroll
             for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + (g + 1) * 320);
             q80_fetch(An, wa, wd, g + 1, (int)min((int64_t)8, nb32 - 8 * (g + 1)));
         }
         if (nj == 8) q80_tile_group<NT, true>(A, lds, q, m, 8, acc);
         else q80_tile_group<NT, false>(A, lds, q, m, nj, acc);
-        if (g + 1 < ngrp) A = An;
-    }
+        if constexpr (decltype(pf)::on) A = An;
+    };
+    for (int64_t g = 0; g + 1 < ngrp; g++) group(g, PF<true>{});
+    group(ngrp - 1, PF<false>{});
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int64_t c = c0 + 16 * n + m;
@@ -235,13 +247,13 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 #pragma unroll
     for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)bsrc[i];
     q4k_fetch_a(A, wa, wh, nb, 0, q);
-    for (int64_t b = 0; b < nb; b++) {
+    auto block = [&](int64_t b, auto pf) {
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < BStage<NT>::NV; i++)
             if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
         __syncthreads();
-        if (b + 1 < nb) {
+        if constexpr (decltype(pf)::on) {
 #pragma unroll
             for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + (b + 1) * 320);
             q4k_fetch_a(An, wa, wh, nb, b + 1, q);
@@ -302,8 +314,10 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
                                       __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins));
             }
         }
-        if (b + 1 < nb) A = An;
-    }
+        if constexpr (decltype(pf)::on) A = An;
+    };
+    for (int64_t b = 0; b + 1 < nb; b++) block(b, PF<true>{});
+    block(nb - 1, PF<false>{});
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int64_t c = c0 + 16 * n + m;
@@ -328,20 +342,30 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 // exactly) through LDS, W groups a round.
 //   Q8_0: the group's fs (one value an output);
 //   Q4_K: the block's (d·xs)·sumi and (dmin·xs)·dmins (two values an output).
-// One K-group of the split-K Q8_0 kernel: the columns' pack blocks (hot in
-// cache) and the f32 terms of the 8 blocks (FULL: all 8 exist).
-template <int NT, bool FULL>
-DEV void q80_sk_group(const Q80A &A, const uint8_t *const (&xc)[NT], int64_t g, int nj, int q, float (&fs)[NT][4]) {
-    long bq[NT][8];
-    float4 bx[NT][2];
+// The columns' pack blocks of a K-group (hot in cache), fetched a group
+// ahead with the weights.
+template <int NT>
+struct Q80B {
+    long q[NT][8];
+    float4 x[NT][2];
+};
+
+template <int NT>
+DEV void q80_fetch_b(Q80B<NT> &B, const uint8_t *const (&xc)[NT], int64_t g, int q) {
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const uint8_t *col = xc[n] + g * 320;
 #pragma unroll
-        for (int j = 0; j < 8; j++) bq[n][j] = ld8(col + 32 * j + 8 * q);
-        bx[n][0] = *(const float4 *)(col + 288);
-        bx[n][1] = *(const float4 *)(col + 304);
+        for (int j = 0; j < 8; j++) B.q[n][j] = ld8(col + 32 * j + 8 * q);
+        B.x[n][0] = *(const float4 *)(col + 288);
+        B.x[n][1] = *(const float4 *)(col + 304);
     }
+}
+
+// One K-group of the split-K Q8_0 kernel: the f32 terms of the 8 blocks
+// (FULL: all 8 exist).
+template <int NT, bool FULL>
+DEV void q80_sk_group(const Q80A &A, const Q80B<NT> &B, int nj, float (&fs)[NT][4]) {
     float dr[4][8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -351,11 +375,11 @@ DEV void q80_sk_group(const Q80A &A, const uint8_t *const (&xc)[NT], int64_t g, 
     }
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const float xs[8] = {bx[n][0].x, bx[n][0].y, bx[n][0].z, bx[n][0].w,
-                             bx[n][1].x, bx[n][1].y, bx[n][1].z, bx[n][1].w};
+        const float xs[8] = {B.x[n][0].x, B.x[n][0].y, B.x[n][0].z, B.x[n][0].w,
+                             B.x[n][1].x, B.x[n][1].y, B.x[n][1].z, B.x[n][1].w};
         v4i d[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[n][j]);
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], B.q[n][j]);
 #pragma unroll
         for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
 #pragma unroll
@@ -388,17 +412,31 @@ DEV void gemm_sk_q80(const cj_gemv_args &a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
     Q80A A, An;
-    if (wave < ngrp) q80_fetch(A, wa, wd, wave, (int)min((int64_t)8, nb32 - 8 * wave));
+    Q80B<NT> B, Bn;
+    {
+        const int64_t g0 = min((int64_t)wave, ngrp - 1);
+        q80_fetch(A, wa, wd, g0, (int)min((int64_t)8, nb32 - 8 * g0));
+        q80_fetch_b<NT>(B, xc, g0, q);
+    }
     const int64_t rounds = (ngrp + W - 1) / W;
-    for (int64_t rd = 0; rd < rounds; rd++) {
+    auto round = [&](int64_t rd, auto pf) {
         const int64_t g = rd * W + wave;
+        if constexpr (decltype(pf)::on) {
+            // the wave's next group (clamped: past the end it re-reads the
+            // last), before the branch below
+            const int64_t gn = min(g + W, ngrp - 1);
+            q80_fetch(An, wa, wd, gn, (int)min((int64_t)8, nb32 - 8 * gn));
+            q80_fetch_b<NT>(Bn, xc, gn, q);
+        }
         float fs[NT][4];
         if (g < ngrp) {
             const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-            if (g + W < ngrp) q80_fetch(An, wa, wd, g + W, (int)min((int64_t)8, nb32 - 8 * (g + W)));
-            if (nj == 8) q80_sk_group<NT, true>(A, xc, g, 8, q, fs);
-            else q80_sk_group<NT, false>(A, xc, g, nj, q, fs);
-            if (g + W < ngrp) A = An;
+            if (nj == 8) q80_sk_group<NT, true>(A, B, 8, fs);
+            else q80_sk_group<NT, false>(A, B, nj, fs);
+        }
+        if constexpr (decltype(pf)::on) {
+            A = An;
+            B = Bn;
         }
         if (wave > 0 && g < ngrp) {
 #pragma unroll
@@ -420,7 +458,9 @@ DEV void gemm_sk_q80(const cj_gemv_args &a) {
                     for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], hand[w][4 * n + i][lane]);
         }
         __syncthreads();
-    }
+    };
+    for (int64_t rd = 0; rd + 1 < rounds; rd++) round(rd, PF<true>{});
+    round(rounds - 1, PF<false>{});
     if (wave != 0) return;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
@@ -476,19 +516,21 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
     Q4kA A, An;
     Q4kB<NT> B, Bn;
-    if (wave < nb) {
-        q4k_fetch_a(A, wa, wh, nb, wave, q);
-        q4k_fetch_b<NT>(B, a, c0, wave, q, m);
+    {
+        const int64_t b0 = min((int64_t)wave, nb - 1);
+        q4k_fetch_a(A, wa, wh, nb, b0, q);
+        q4k_fetch_b<NT>(B, a, c0, b0, q, m);
     }
     const int64_t rounds = (nb + W - 1) / W;
-    for (int64_t rd = 0; rd < rounds; rd++) {
+    auto round = [&](int64_t rd, auto pf) {
         const int64_t b = rd * W + wave;
         float t1[NT][4], t2[NT][4];
+        if constexpr (decltype(pf)::on) {   // the wave's next block, before the branch (as in gemm_sk_q80)
+            const int64_t bn = min(b + W, nb - 1);
+            q4k_fetch_a(An, wa, wh, nb, bn, q);
+            q4k_fetch_b<NT>(Bn, a, c0, bn, q, m);
+        }
         if (b < nb) {
-            if (b + W < nb) {
-                q4k_fetch_a(An, wa, wh, nb, b + W, q);
-                q4k_fetch_b<NT>(Bn, a, c0, b + W, q, m);
-            }
             int sc[4][8], mn[4][8];
             float dd[4], dm[4];
 #pragma unroll
@@ -538,7 +580,10 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
                     t2[n][i] = __fmul_rn(__fmul_rn(dm[i], B.xs[n]), (float)dmins);
                 }
             }
-            if (b + W < nb) { A = An; B = Bn; }
+        }
+        if constexpr (decltype(pf)::on) {
+            A = An;
+            B = Bn;
         }
         if (wave > 0 && b < nb) {
 #pragma unroll
@@ -564,7 +609,9 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
                         acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], hand[w][8 * n + i][lane]), hand[w][8 * n + 4 + i][lane]);
         }
         __syncthreads();
-    }
+    };
+    for (int64_t rd = 0; rd + 1 < rounds; rd++) round(rd, PF<true>{});
+    round(rounds - 1, PF<false>{});
     if (wave != 0) return;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
