@@ -273,19 +273,29 @@ DEV void split_rows_body(const cj_attn_args &a) {
         for (int hh = 0; hh < HW; hh++) { m[hh] = -3.0e38f; l[hh] = 0.0f; acc0[hh] = 0.0f; acc1[hh] = 0.0f; }
         // a tile's K and V rows as 16-byte chunks (rows past the split's end
         // repeat its last row); the next tile's are requested before this
-        // tile's arithmetic, so a long split streams without a gap
+        // tile's arithmetic, so a long split streams without a gap. The four
+        // chunks' pages are resolved before any K/V load is issued: a page
+        // read from global memory (past the staged table) waits for every
+        // load in flight, so resolving it between loads would serialize them.
+        // (Measured and rejected for this VALU-bound form: widening K and V
+        // to f32 once at staging — twice the LDS, half the workgroups a CU,
+        // 12.8 ms a C4 step against 11.0; each position's weight from an LDS
+        // row instead of its lane — 129 VGPRs, one wave a SIMD fewer, 12.1.)
         u32x4 kr[4], vr[4];   // native vectors: stay in registers across the loop
 #define SPLIT_FETCH(TB)                                                                                   \
     do {                                                                                                  \
         const int n_ = t1 - (TB) < TP ? t1 - (TB) : TP;                                                   \
+        int64_t base_[4];                                                                                 \
         _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                  \
             const int c = t + 256 * i, j = c & 15;                                                        \
             const int p = (c >> 4) < n_ ? (c >> 4) : n_ - 1;                                              \
             const int pos = from + (TB) + p, pi = pos >> 6;                                               \
             const int page = pi < PGMAX ? pgs[pi] : a.pgtab[pg_base + pi];                                \
-            const int64_t base = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;         \
-            kr[i] = *(const u32x4 *)(a.kc + base);                                                        \
-            vr[i] = *(const u32x4 *)(a.vc + base);                                                        \
+            base_[i] = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j;                   \
+        }                                                                                                 \
+        _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                  \
+            kr[i] = *(const u32x4 *)(a.kc + base_[i]);                                                    \
+            vr[i] = *(const u32x4 *)(a.vc + base_[i]);                                                    \
         }                                                                                                 \
     } while (0)
         __syncthreads();   // q and pages visible
