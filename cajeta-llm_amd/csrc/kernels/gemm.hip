@@ -336,36 +336,55 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 // For a handful of columns (batched decode) the weights dominate and the
 // output tile is small, so the K dimension is shared out: a workgroup of W
 // waves owns 16 rows × 16·NT columns, wave w takes the groups g ≡ w (mod W),
-// streaming its weights and the columns' pack blocks straight into registers
-// one group ahead, and hands each group's per-output terms to wave 0, which
-// folds them into the accumulators in group order (the reference's order,
-// exactly) through LDS, W groups a round.
+// streaming its weights straight into registers one group ahead, and hands
+// each group's per-output terms to wave 0, which folds them into the
+// accumulators in group order (the reference's order, exactly) through LDS,
+// W groups a round. The columns' pack blocks reach the waves through LDS: a
+// round's blocks are staged by coalesced 16-byte loads a round ahead (the
+// per-lane 8-byte loads they replace kept the address unit 63% busy).
 //   Q8_0: the group's fs (one value an output);
 //   Q4_K: the block's (d·xs)·sumi and (dmin·xs)·dmins (two values an output).
-// The columns' pack blocks of a K-group (hot in cache), fetched a group
-// ahead with the weights.
-template <int NT>
-struct Q80B {
-    long q[NT][8];
-    float4 x[NT][2];
+
+// A round's pack blocks — the W groups' blocks of the tile's 16·NT columns,
+// 20 16-byte words each — as NW words a thread: loaded a round ahead into
+// registers (coalesced 16-byte loads), stored to LDS once the round's reads
+// are done. Word i of thread t is word (t + 64·W·i) of the round.
+template <int NT, int W>
+struct SkStage {
+    static constexpr int CT = 16 * NT, WORDS = W * CT * 20, NW = (WORDS + 64 * W - 1) / (64 * W);
 };
 
-template <int NT>
-DEV void q80_fetch_b(Q80B<NT> &B, const uint8_t *const (&xc)[NT], int64_t g, int q) {
+template <int NT, int W, int NW>
+DEV void sk_b_load(u32x4 (&sv)[NW], const cj_gemv_args &a, int64_t c0, int64_t rd, int64_t ngrp) {
+    using S = SkStage<NT, W>;
+    static_assert(NW == S::NW, "a round's words a thread");
 #pragma unroll
-    for (int n = 0; n < NT; n++) {
-        const uint8_t *col = xc[n] + g * 320;
+    for (int i = 0; i < NW; i++) {
+        const int idx = min((int)threadIdx.x + 64 * W * i, S::WORDS - 1);
+        const int gw = idx / (S::CT * 20), rem = idx % (S::CT * 20), col = rem / 20, word = rem % 20;
+        const int64_t gg = min(rd * W + gw, ngrp - 1), cc = min(c0 + col, (int64_t)a.batch - 1);
+        sv[i] = *(const u32x4 *)(a.xp + cc * a.xp_stride + gg * 320 + 16 * word);
+    }
+}
+
+template <int NT, int W, int NW>
+DEV void sk_b_store(const u32x4 (&sv)[NW], uint8_t *bl) {
+    using S = SkStage<NT, W>;
+    static_assert(NW == S::NW, "a round's words a thread");
 #pragma unroll
-        for (int j = 0; j < 8; j++) B.q[n][j] = ld8(col + 32 * j + 8 * q);
-        B.x[n][0] = *(const float4 *)(col + 288);
-        B.x[n][1] = *(const float4 *)(col + 304);
+    for (int i = 0; i < NW; i++) {
+        const int idx = (int)threadIdx.x + 64 * W * i;
+        if (idx < S::WORDS) {
+            const int gw = idx / (S::CT * 20), rem = idx % (S::CT * 20), col = rem / 20, word = rem % 20;
+            *(u32x4 *)(bl + (gw * S::CT + col) * GEMM_CS + 16 * word) = sv[i];
+        }
     }
 }
 
 // One K-group of the split-K Q8_0 kernel: the f32 terms of the 8 blocks
 // (FULL: all 8 exist).
 template <int NT, bool FULL>
-DEV void q80_sk_group(const Q80A &A, const Q80B<NT> &B, int nj, float (&fs)[NT][4]) {
+DEV void q80_sk_group(const Q80A &A, const uint8_t *slot, int q, int m, int nj, float (&fs)[NT][4]) {
     float dr[4][8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -375,11 +394,17 @@ DEV void q80_sk_group(const Q80A &A, const Q80B<NT> &B, int nj, float (&fs)[NT][
     }
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const float xs[8] = {B.x[n][0].x, B.x[n][0].y, B.x[n][0].z, B.x[n][0].w,
-                             B.x[n][1].x, B.x[n][1].y, B.x[n][1].z, B.x[n][1].w};
+        // the tile's column blocks from the round's LDS stage (column c's
+        // 320-byte block at c·GEMM_CS of the wave's slot)
+        const uint8_t *col = slot + (16 * n + m) * GEMM_CS;
+        const float4 x0 = *(const float4 *)(col + 288), x1 = *(const float4 *)(col + 304);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        long bq[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) bq[j] = *(const long *)(col + 32 * j + 8 * q);
         v4i d[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], B.q[n][j]);
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[j]);
 #pragma unroll
         for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
 #pragma unroll
@@ -395,7 +420,9 @@ DEV void q80_sk_group(const Q80A &A, const Q80B<NT> &B, int nj, float (&fs)[NT][
 
 template <int NT, int W>
 DEV void gemm_sk_q80(const cj_gemv_args &a) {
+    using S = SkStage<NT, W>;
     __shared__ __align__(16) float hand[W][NT * 4][64];
+    __shared__ __align__(16) uint8_t bl[W * S::CT * GEMM_CS];   // the round's pack blocks, a slot a wave
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
     const int64_t nb32 = a.cols / 32, ngrp = (a.cols + 255) / 256;
@@ -403,48 +430,47 @@ DEV void gemm_sk_q80(const cj_gemv_args &a) {
     const uint8_t *wd[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
-    const uint8_t *xc[NT];
-#pragma unroll
-    for (int n = 0; n < NT; n++) xc[n] = a.xp + min(c0 + 16 * n + m, (int64_t)a.batch - 1) * a.xp_stride;
     float acc[NT][4];
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
     Q80A A, An;
-    Q80B<NT> B, Bn;
+    u32x4 sv[S::NW];
     {
+        sk_b_load<NT, W, S::NW>(sv, a, c0, 0, ngrp);
         const int64_t g0 = min((int64_t)wave, ngrp - 1);
         q80_fetch(A, wa, wd, g0, (int)min((int64_t)8, nb32 - 8 * g0));
-        q80_fetch_b<NT>(B, xc, g0, q);
+        sk_b_store<NT, W, S::NW>(sv, bl);
+        __syncthreads();
     }
     const int64_t rounds = (ngrp + W - 1) / W;
     auto round = [&](int64_t rd, auto pf) {
         const int64_t g = rd * W + wave;
         if constexpr (decltype(pf)::on) {
-            // the wave's next group (clamped: past the end it re-reads the
-            // last), before the branch below
+            // the next round's pack blocks, then the wave's next group
+            // (clamped: past the end it re-reads the last), before the
+            // branch below
+            sk_b_load<NT, W, S::NW>(sv, a, c0, rd + 1, ngrp);
             const int64_t gn = min(g + W, ngrp - 1);
             q80_fetch(An, wa, wd, gn, (int)min((int64_t)8, nb32 - 8 * gn));
-            q80_fetch_b<NT>(Bn, xc, gn, q);
         }
         float fs[NT][4];
         if (g < ngrp) {
+            const uint8_t *slot = bl + wave * S::CT * GEMM_CS;
             const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-            if (nj == 8) q80_sk_group<NT, true>(A, B, 8, fs);
-            else q80_sk_group<NT, false>(A, B, nj, fs);
+            if (nj == 8) q80_sk_group<NT, true>(A, slot, q, m, 8, fs);
+            else q80_sk_group<NT, false>(A, slot, q, m, nj, fs);
         }
-        if constexpr (decltype(pf)::on) {
-            A = An;
-            B = Bn;
-        }
+        if constexpr (decltype(pf)::on) A = An;
         if (wave > 0 && g < ngrp) {
 #pragma unroll
             for (int n = 0; n < NT; n++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) hand[wave][4 * n + i][lane] = fs[n][i];
         }
-        __syncthreads();
+        __syncthreads();   // every wave has read this round's blocks and handed its terms
+        if constexpr (decltype(pf)::on) sk_b_store<NT, W, S::NW>(sv, bl);
         if (wave == 0) {
             const int live = (int)min((int64_t)W, ngrp - rd * W);
 #pragma unroll
@@ -475,32 +501,11 @@ DEV void gemm_sk_q80(const cj_gemv_args &a) {
     }
 }
 
-template <int NT>
-struct Q4kB {
-    long lo[NT][4], hi[NT][4];
-    int4 s0[NT], s1[NT];
-    float xs[NT];
-};
-
-template <int NT>
-DEV void q4k_fetch_b(Q4kB<NT> &B, const cj_gemv_args &a, int64_t c0, int64_t b, int q, int m) {
-#pragma unroll
-    for (int n = 0; n < NT; n++) {
-        const uint8_t *col = a.xp + min(c0 + 16 * n + m, (int64_t)a.batch - 1) * a.xp_stride + b * 320;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            B.lo[n][g4] = ld8(col + 64 * g4 + 8 * q);
-            B.hi[n][g4] = ld8(col + 64 * g4 + 32 + 8 * q);
-        }
-        B.s0[n] = *(const int4 *)(col + 256);
-        B.s1[n] = *(const int4 *)(col + 272);
-        B.xs[n] = *(const float *)(col + 288);
-    }
-}
-
 template <int NT, int W>
 DEV void gemm_sk_q4k(const cj_gemv_args &a) {
+    using S = SkStage<NT, W>;
     __shared__ __align__(16) float hand[W][NT * 8][64];
+    __shared__ __align__(16) uint8_t bl[W * S::CT * GEMM_CS];   // the round's pack blocks, a slot a wave
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
     const int64_t nb = a.cols / 256;
@@ -515,20 +520,22 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
     Q4kA A, An;
-    Q4kB<NT> B, Bn;
+    u32x4 sv[S::NW];
     {
+        sk_b_load<NT, W, S::NW>(sv, a, c0, 0, nb);
         const int64_t b0 = min((int64_t)wave, nb - 1);
         q4k_fetch_a(A, wa, wh, nb, b0, q);
-        q4k_fetch_b<NT>(B, a, c0, b0, q, m);
+        sk_b_store<NT, W, S::NW>(sv, bl);
+        __syncthreads();
     }
     const int64_t rounds = (nb + W - 1) / W;
     auto round = [&](int64_t rd, auto pf) {
         const int64_t b = rd * W + wave;
         float t1[NT][4], t2[NT][4];
-        if constexpr (decltype(pf)::on) {   // the wave's next block, before the branch (as in gemm_sk_q80)
+        if constexpr (decltype(pf)::on) {   // the next round's blocks and the wave's next block (as in gemm_sk_q80)
+            sk_b_load<NT, W, S::NW>(sv, a, c0, rd + 1, nb);
             const int64_t bn = min(b + W, nb - 1);
             q4k_fetch_a(An, wa, wh, nb, bn, q);
-            q4k_fetch_b<NT>(Bn, a, c0, bn, q, m);
         }
         if (b < nb) {
             int sc[4][8], mn[4][8];
@@ -556,12 +563,22 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
             }
 #pragma unroll
             for (int n = 0; n < NT; n++) {
+                // the tile's column blocks from the round's LDS stage
+                const uint8_t *col = bl + (wave * S::CT + 16 * n + m) * GEMM_CS;
+                long bl8[4], bh8[4];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    bl8[g4] = *(const long *)(col + 64 * g4 + 8 * q);
+                    bh8[g4] = *(const long *)(col + 64 * g4 + 32 + 8 * q);
+                }
+                const int4 s0 = *(const int4 *)(col + 256), s1 = *(const int4 *)(col + 272);
+                const float xs = *(const float *)(col + 288);
                 // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
                 v4i dl[4], dh[4];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
-                    dl[g4] = mfma_i8(lo[g4], B.lo[n][g4]);
-                    dh[g4] = mfma_i8(hi[g4], B.hi[n][g4]);
+                    dl[g4] = mfma_i8(lo[g4], bl8[g4]);
+                    dh[g4] = mfma_i8(hi[g4], bh8[g4]);
                 }
                 int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -569,22 +586,18 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         sumi[i] += __mul24(dl[g4][i], sc[i][2 * g4]) + __mul24(dh[g4][i], sc[i][2 * g4 + 1]);
-                const int bsum[8] = {B.s0[n].x, B.s0[n].y, B.s0[n].z, B.s0[n].w,
-                                     B.s1[n].x, B.s1[n].y, B.s1[n].z, B.s1[n].w};
+                const int bsum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     int dmins = 0;
 #pragma unroll
                     for (int s2 = 0; s2 < 8; s2++) dmins += __mul24(bsum[s2], mn[i][s2]);
-                    t1[n][i] = __fmul_rn(__fmul_rn(dd[i], B.xs[n]), (float)sumi[i]);
-                    t2[n][i] = __fmul_rn(__fmul_rn(dm[i], B.xs[n]), (float)dmins);
+                    t1[n][i] = __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi[i]);
+                    t2[n][i] = __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins);
                 }
             }
         }
-        if constexpr (decltype(pf)::on) {
-            A = An;
-            B = Bn;
-        }
+        if constexpr (decltype(pf)::on) A = An;
         if (wave > 0 && b < nb) {
 #pragma unroll
             for (int n = 0; n < NT; n++)
@@ -594,7 +607,8 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
                     hand[wave][8 * n + 4 + i][lane] = t2[n][i];
                 }
         }
-        __syncthreads();
+        __syncthreads();   // every wave has read this round's blocks and handed its terms
+        if constexpr (decltype(pf)::on) sk_b_store<NT, W, S::NW>(sv, bl);
         if (wave == 0) {
             const int live = (int)min((int64_t)W, nb - rd * W);
 #pragma unroll
