@@ -123,13 +123,12 @@ DEV void split_body(const cj_attn_args &a) {
                 for (int c = 0; c < 16; c++) {
                     const uint4 kk = *(const uint4 *)&ks[lane][8 * c];
                     const float4 qa = *(const float4 *)(qh + 8 * c), qb = *(const float4 *)(qh + 8 * c + 4);
-                    const float kf[8] = {h2f(kk.x), h2f(kk.x >> 16), h2f(kk.y), h2f(kk.y >> 16),
-                                         h2f(kk.z), h2f(kk.z >> 16), h2f(kk.w), h2f(kk.w >> 16)};
+                    const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
                     const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
                         const int j = 8 * (c & 1) + i;
-                        const float pr = __fmul_rn(qv[i], kf[i]);
+                        const float pr = (i & 1) ? mul_h16hi(kw[i >> 1], qv[i]) : mul_h16lo(kw[i >> 1], qv[i]);
                         part[j] = c < 2 ? pr : __fadd_rn(part[j], pr);
                     }
                 }
@@ -169,8 +168,8 @@ DEV void split_body(const cj_attn_args &a) {
                             ls = __fmul_rn(ls, c);
                         }
                         ls = __fadd_rn(ls, w);
-                        x0 = __fadd_rn(x0, __fmul_rn(h2f(vv[p]), w));
-                        x1 = __fadd_rn(x1, __fmul_rn(h2f(vv[p] >> 16), w));
+                        x0 = __fadd_rn(x0, mul_h16lo(vv[p], w));
+                        x1 = __fadd_rn(x1, mul_h16hi(vv[p], w));
                     }
                 }
                 acc0[hh] = x0; acc1[hh] = x1; l[hh] = ls;
