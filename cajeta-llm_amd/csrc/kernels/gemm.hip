@@ -24,11 +24,11 @@
 // Tiling: a workgroup of 4 waves owns 64 weight rows (16 a wave) × 16·NT
 // columns. The K dimension runs in groups of 256 elements (8 Q8_0 blocks, one
 // Q4_K block). Each group's activation packs (the 320-byte block of every
-// column of the tile, verbatim) are staged in LDS once for the 4 waves; each
-// wave streams its own 16 rows' weights straight into registers. Both are
-// requested one group ahead, so the loads of group g+1 are in flight while
-// group g computes. Column tiles of one row block are adjacent in dispatch
-// order and share the rows' weights in cache.
+// column of the tile, verbatim) are staged in LDS once for the 4 waves; the
+// weights are staged in LDS too for Q8_0 and stream straight into registers
+// for Q4_K. Both are requested one group ahead, so the loads of group g+1 are
+// in flight while group g computes. Column tiles of one row block are
+// adjacent in dispatch order and share the rows' weights in cache.
 #include "common.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -99,18 +99,34 @@ DEV void q80_fetch(Q80A &A, const uint8_t *wa, const uint8_t *const (&wd)[4], in
     for (int i = 0; i < 4; i++) A.d[i] = *(const uint4 *)(wd[i] + 16 * g);
 }
 
-// One K-group of a wave's 16 rows × 16·NT columns: the f32 steps of the 8
-// blocks (FULL: all 8 exist; else the first nj). Each tile's 8 operand reads
-// and 8 products issue back to back, then its f32 steps.
+
+
+// Q8_0, tiled: a group's 64 weight rows × (256 code bytes + 16 scale bytes)
+// are staged in LDS beside the columns' pack blocks, as 1088 16-byte words
+// loaded coalesced one group ahead (per-lane 8-byte row loads straight into
+// registers queued on the address unit: 32 columns 55.6 → 42.5 µs at
+// 28672×4096, a 512-row prefill chunk 30.4 → 27.6 ms), and read back as the
+// MFMA operands. Row stride 264 bytes: 16 consecutive lanes' 8-byte reads
+// of 16 rows fall on distinct banks. Per 32-element block and output the f32
+// steps are the reference's, fs = Σ_j (d_j·xs_j)·isum_j over the group's 8
+// blocks (the first nj of a short last group), then acc += fs.
+#define GEMM_AS 264
+#define GEMM_AW 1088     // staged words a group: 64 rows × 16 code words + 64 scale words
+
 template <int NT, bool FULL>
-DEV void q80_tile_group(const Q80A &A, const uint8_t *lds, int q, int m, int nj, float (&acc)[NT][4]) {
+DEV void q80_tile_group(const uint8_t *aq, const uint8_t *ad, const uint8_t *lds, int q, int m, int nj,
+                          float (&acc)[NT][4]) {
     float dr[4][8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
+        const uint4 dw = *(const uint4 *)(ad + (4 * q + i) * 16);
+        const uint32_t hw[4] = {dw.x, dw.y, dw.z, dw.w};
 #pragma unroll
         for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
     }
+    long aw[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) aw[j] = *(const long *)(aq + m * GEMM_AS + 32 * j + 8 * q);
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const uint8_t *col = lds + (16 * n + m) * GEMM_CS;
@@ -121,7 +137,7 @@ DEV void q80_tile_group(const Q80A &A, const uint8_t *lds, int q, int m, int nj,
         for (int j = 0; j < 8; j++) bq[j] = *(const long *)(col + 32 * j + 8 * q);
         v4i d[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[j]);
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(aw[j], bq[j]);
         float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -138,48 +154,78 @@ DEV void q80_tile_group(const Q80A &A, const uint8_t *lds, int q, int m, int nj,
 
 template <int NT>
 DEV void gemm_q80(const cj_gemv_args &a, uint8_t *lds) {
+    constexpr int NV = BStage<NT>::NV, AV = (GEMM_AW + 255) / 256;
+    __shared__ __align__(16) uint8_t aq[64 * GEMM_AS];
+    __shared__ __align__(16) uint8_t ad[64 * 16];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * 16 * NT;
-    const int64_t r0 = (int64_t)blockIdx.y * 64 + 16 * wave;
+    const int64_t rw0 = (int64_t)blockIdx.y * 64, r0 = rw0 + 16 * wave;
     const int64_t nb32 = a.cols / 32, ngrp = (a.cols + 255) / 256;
-    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + 8 * q;
-    const uint8_t *wd[4];
+    const uint8_t *bsrc[NV];
+    int bdst[NV];
 #pragma unroll
-    for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
-    // this thread's pack words of the column tile: source and LDS slot
-    const uint8_t *bsrc[BStage<NT>::NV];
-    int bdst[BStage<NT>::NV];
-#pragma unroll
-    for (int i = 0; i < BStage<NT>::NV; i++) {
+    for (int i = 0; i < NV; i++) {
         const int w = min(t + 256 * i, BStage<NT>::WORDS - 1);
         bsrc[i] = a.xp + min(c0 + w / 20, (int64_t)a.batch - 1) * a.xp_stride + 16 * (w % 20);
         bdst[i] = t + 256 * i < BStage<NT>::WORDS ? (w / 20) * GEMM_CS + 16 * (w % 20) : -1;
+    }
+    // this thread's weight words: row base and word of the group
+    const uint8_t *arow[AV];
+    int aword[AV];
+#pragma unroll
+    for (int i = 0; i < AV; i++) {
+        const int idx = min(t + 256 * i, GEMM_AW - 1);
+        const int row = idx < 1024 ? idx >> 4 : idx - 1024;
+        arow[i] = a.w + min(rw0 + row, a.rows - 1) * a.row_bytes;
+        aword[i] = idx;
     }
     float acc[NT][4];
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
-    u32x4 bv[BStage<NT>::NV];
-    Q80A A, An;
+    u32x4 bv[NV], av[AV];
+    auto fetch = [&](int64_t g) {
 #pragma unroll
-    for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)bsrc[i];
-    q80_fetch(A, wa, wd, 0, (int)min((int64_t)8, nb32));
-    auto group = [&](int64_t g, auto pf) {
-        const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-        __syncthreads();   // the previous group's LDS reads are done
+        for (int i = 0; i < NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + g * 320);
 #pragma unroll
-        for (int i = 0; i < BStage<NT>::NV; i++)
-            if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
-        __syncthreads();
-        if constexpr (decltype(pf)::on) {
-#pragma unroll
-            for (int i = 0; i < BStage<NT>::NV; i++) bv[i] = *(const u32x4 *)(bsrc[i] + (g + 1) * 320);
-            q80_fetch(An, wa, wd, g + 1, (int)min((int64_t)8, nb32 - 8 * (g + 1)));
+        for (int i = 0; i < AV; i++) {
+            const int idx = aword[i];
+            if (idx < 1024) {   // code word: block 8g + w/2 (the last block repeats past the row)
+                const int w16 = idx & 15;
+                const int64_t blk = min(8 * g + (w16 >> 1), nb32 - 1);
+                av[i] = *(const u32x4 *)(arow[i] + blk * 32 + 16 * (w16 & 1));
+            } else {            // the row's 8 block scales of the group (the scale array is padded to 16)
+                av[i] = *(const u32x4 *)(arow[i] + nb32 * 32 + 16 * g);
+            }
         }
-        if (nj == 8) q80_tile_group<NT, true>(A, lds, q, m, 8, acc);
-        else q80_tile_group<NT, false>(A, lds, q, m, nj, acc);
-        if constexpr (decltype(pf)::on) A = An;
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (bdst[i] >= 0) *(u32x4 *)(lds + bdst[i]) = bv[i];
+#pragma unroll
+        for (int i = 0; i < AV; i++) {
+            const int idx = t + 256 * i;
+            if (idx < 1024) {
+                uint8_t *dst = aq + (idx >> 4) * GEMM_AS + 16 * (idx & 15);
+                *(uint2 *)dst = make_uint2(av[i].x, av[i].y);
+                *(uint2 *)(dst + 8) = make_uint2(av[i].z, av[i].w);
+            } else if (idx < GEMM_AW) {
+                *(u32x4 *)(ad + (idx - 1024) * 16) = av[i];
+            }
+        }
+    };
+    fetch(0);
+    auto group = [&](int64_t g, auto pf) {
+        __syncthreads();   // the previous group's LDS reads are done
+        stage();
+        __syncthreads();
+        if constexpr (decltype(pf)::on) fetch(g + 1);
+        const int nj = (int)min((int64_t)8, nb32 - 8 * g);
+        const uint8_t *aqw = aq + 16 * wave * GEMM_AS, *adw = ad + 16 * wave * 16;
+        if (nj == 8) q80_tile_group<NT, true>(aqw, adw, lds, q, m, 8, acc);
+        else q80_tile_group<NT, false>(aqw, adw, lds, q, m, nj, acc);
     };
     for (int64_t g = 0; g + 1 < ngrp; g++) group(g, PF<true>{});
     group(ngrp - 1, PF<false>{});
@@ -644,7 +690,7 @@ DEV void gemm_sk_q4k(const cj_gemv_args &a) {
 #define GEMM_KERNELS(NT)                                                                   \
     extern "C" __global__ void __launch_bounds__(256) cj_gemm_q80_n##NT(cj_gemv_args a) { \
         __shared__ __align__(16) uint8_t lds[16 * NT * GEMM_CS];                           \
-        gemm_q80<NT>(a, lds);                                                              \
+        gemm_q80<NT>(a, lds);                                                             \
     }                                                                                      \
     extern "C" __global__ void __launch_bounds__(256) cj_gemm_q4k_n##NT(cj_gemv_args a) { \
         __shared__ __align__(16) uint8_t lds[16 * NT * GEMM_CS];                           \
