@@ -70,6 +70,18 @@ DEV void norm_pack_block(const cj_pack_args &a, const float *x) {
 }
 extern "C" __global__ void __launch_bounds__(256) cj_norm_pack(cj_pack_args a) { norm_pack_block(a, a.x); }
 
+// The same for many rows: workgroup (256-block, row), row r of x, out and
+// xout a.n floats / npad/256 blocks / a.n floats apart. (A workgroup a row
+// puts a batch of 32 rows on 32 CUs.)
+extern "C" __global__ void __launch_bounds__(256) cj_norm_pack_rows(cj_pack_args a) {
+    const int64_t row = blockIdx.y;
+    cj_pack_args r = a;
+    r.x = a.x + row * a.n;
+    r.out = a.out ? a.out + row * (a.npad / 256) * 320 : nullptr;
+    r.xout = a.xout ? a.xout + row * a.n : nullptr;
+    norm_pack_block(r, r.x);
+}
+
 // The MoE combine (MoeFfn.forwardRow, model/MoeFfn.cajeta:1896-1901: the
 // selected experts' rows weighted and summed in k order, then onto the
 // residual) and the RMSNorm + pack that follows it (the next layer's

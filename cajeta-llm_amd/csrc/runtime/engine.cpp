@@ -186,6 +186,7 @@ struct Engine {
     int rows_alloc(int cap);
     int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
     int rows_norm_pack(const float *w, int per32, int n);
+    int launch_norm_pack_rows(cj_pack_args &a, int n);
     int rows_forward(const int32_t *tab, int n, bool prefill);
     int rows_pack(const float *x, int64_t n, int per32, int rows);
     int rows_moe(const Layer &L, int n);
@@ -794,13 +795,23 @@ int Engine::rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, flo
     return CJ_OK;
 }
 
-// RMSNorm + pack of n residual rows (the row form: one workgroup a row).
+// RMSNorm + pack of n residual rows. A few rows (batched decode): a
+// workgroup a 256-block and row, each forming its row's sum of squares (the
+// one-row norm + pack's arithmetic), so the launch fills the chip; many rows
+// (prefill chunks): a workgroup a row, which reads each row once (C4:
+// batched step 9.14 → 8.93 ms with the first, a 512-row chunk 27.6 → 28.4
+// ms with it, hence the split).
+int Engine::launch_norm_pack_rows(cj_pack_args &a, int n) {
+    if (n <= 64) return launch2("cj_norm_pack_rows", (uint32_t)(a.npad / 256), (uint32_t)n, 256, 0, a);
+    return launch("cj_pack", (uint32_t)n, 256, (uint32_t)(a.npad / 256 * 320), a);
+}
+
 int Engine::rows_norm_pack(const float *w, int per32, int n) {
     cj_pack_args a{};
     const int64_t npad = ((int64_t)hidden + 255) / 256 * 256;
     a.out = r_xp; a.x = r_hs; a.w = w; a.n = hidden; a.npad = npad; a.rows = n; a.eps = eps; a.form = 0;
     a.per32 = per32; a.do_norm = 1;
-    return launch("cj_pack", (uint32_t)n, 256, (uint32_t)(npad / 256 * 320), a);
+    return launch_norm_pack_rows(a, n);
 }
 
 // The f32 rows x (n wide) packed into r_ap, a workgroup a row.
@@ -826,7 +837,7 @@ int Engine::rows_moe(const Layer &L, int n) {
         cj_pack_args p{};
         p.out = r_xp; p.x = r_hs; p.w = L.ffn_norm; p.xout = r_xn; p.n = hidden; p.npad = npad; p.rows = n;
         p.eps = eps; p.form = 0; p.per32 = L.gu_exps.type == CJ_Q8_0; p.do_norm = 1;
-        if ((rc = launch("cj_pack", (uint32_t)n, 256, (uint32_t)hb, p))) return rc;
+        if ((rc = launch_norm_pack_rows(p, n))) return rc;
     }
     {   // router logits of every row: the indirection's copies all read the router (expert_bytes 0)
         cj_gemv_args a{};

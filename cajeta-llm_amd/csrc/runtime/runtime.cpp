@@ -409,7 +409,7 @@ int32_t cj_init(int32_t device) {
         "cj_gemv_q40b_r2", "cj_gemv_q40b_r4", "cj_gemm_q40_r2_c4", "cj_gemm_q40_r4_c4",
         "cj_gemv_mxfp4", "cj_gemv_f32", "cj_gemv_mxfp4_r32", "cj_gemv_f32_r32", "cj_gemv_mxfp4_r1", "cj_gemv_f32_r1",
         "cj_moe_combine", "cj_moe_combine_norm",
-        "cj_pack", "cj_norm_pack", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
+        "cj_pack", "cj_norm_pack", "cj_norm_pack_rows", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
         "cj_attn_merge", "cj_attn_merge_w", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
