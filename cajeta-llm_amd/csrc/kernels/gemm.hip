@@ -83,23 +83,9 @@ DEV void b_store(const BStage<NT> &s, uint8_t *lds) {
 
 // ------------------------------------------------------------------- Q8_0
 
-// Prepared row: [qs nb32·32][d nb32·2 → padded to 16]. A lane's weights of a
-// group: 8 bytes of each of the 8 blocks of its A row, and the 8 f16 scales
-// of each of its 4 output rows (one 16-byte word a row; the scale array is
+// Prepared row: [qs nb32·32][d nb32·2 → padded to 16]. A group of 8 blocks
+// is 256 code bytes and one 16-byte scale word a row (the scale array is
 // padded to 16 bytes, so a short last group stays inside it).
-struct Q80A {
-    long q[8];
-    uint4 d[4];
-};
-
-DEV void q80_fetch(Q80A &A, const uint8_t *wa, const uint8_t *const (&wd)[4], int64_t g, int nj) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) A.q[j] = ld8(wa + (8 * g + min(j, nj - 1)) * 32);
-#pragma unroll
-    for (int i = 0; i < 4; i++) A.d[i] = *(const uint4 *)(wd[i] + 16 * g);
-}
-
-
 
 // Q8_0, tiled: a group's 64 weight rows × (256 code bytes + 16 scale bytes)
 // are staged in LDS beside the columns' pack blocks, as 1088 16-byte words
@@ -391,53 +377,21 @@ DEV void gemm_q4k(const cj_gemv_args &a, uint8_t *lds) {
 //   Q8_0: the group's fs (one value an output);
 //   Q4_K: the block's (d·xs)·sumi and (dmin·xs)·dmins (two values an output).
 
-// A round's pack blocks — the W groups' blocks of the tile's 16·NT columns,
-// 20 16-byte words each — as NW words a thread: loaded a round ahead into
-// registers (coalesced 16-byte loads), stored to LDS once the round's reads
-// are done. Word i of thread t is word (t + 64·W·i) of the round.
-template <int NT, int W>
-struct SkStage {
-    static constexpr int CT = 16 * NT, WORDS = W * CT * 20, NW = (WORDS + 64 * W - 1) / (64 * W);
-};
-
-template <int NT, int W, int NW>
-DEV void sk_b_load(u32x4 (&sv)[NW], const cj_gemv_args &a, int64_t c0, int64_t rd, int64_t ngrp) {
-    using S = SkStage<NT, W>;
-    static_assert(NW == S::NW, "a round's words a thread");
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-        const int idx = min((int)threadIdx.x + 64 * W * i, S::WORDS - 1);
-        const int gw = idx / (S::CT * 20), rem = idx % (S::CT * 20), col = rem / 20, word = rem % 20;
-        const int64_t gg = min(rd * W + gw, ngrp - 1), cc = min(c0 + col, (int64_t)a.batch - 1);
-        sv[i] = *(const u32x4 *)(a.xp + cc * a.xp_stride + gg * 320 + 16 * word);
-    }
-}
-
-template <int NT, int W, int NW>
-DEV void sk_b_store(const u32x4 (&sv)[NW], uint8_t *bl) {
-    using S = SkStage<NT, W>;
-    static_assert(NW == S::NW, "a round's words a thread");
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-        const int idx = (int)threadIdx.x + 64 * W * i;
-        if (idx < S::WORDS) {
-            const int gw = idx / (S::CT * 20), rem = idx % (S::CT * 20), col = rem / 20, word = rem % 20;
-            *(u32x4 *)(bl + (gw * S::CT + col) * GEMM_CS + 16 * word) = sv[i];
-        }
-    }
-}
-
 // One K-group of the split-K Q8_0 kernel: the f32 terms of the 8 blocks
-// (FULL: all 8 exist).
+// (FULL: all 8 exist), from the wave's staged weights (codes of row r at
+// r·GEMM_AS, the rows' scale words after them) and the round's column blocks.
 template <int NT, bool FULL>
-DEV void q80_sk_group(const Q80A &A, const uint8_t *slot, int q, int m, int nj, float (&fs)[NT][4]) {
-    float dr[4][8];
+DEV void q80_sk_group(const uint8_t *aq, const uint8_t *slot, int q, int m, int nj, float (&fs)[NT][4]) {
+    const uint8_t *ad = aq + 16 * GEMM_AS;
+    uint32_t hw[4][4];   // the f16 scales of rows 4q + i, two a word
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t hw[4] = {A.d[i].x, A.d[i].y, A.d[i].z, A.d[i].w};
-#pragma unroll
-        for (int j = 0; j < 8; j++) dr[i][j] = h2f(hw[j >> 1] >> (16 * (j & 1)));
+        const uint4 dw = *(const uint4 *)(ad + (4 * q + i) * 16);
+        hw[i][0] = dw.x; hw[i][1] = dw.y; hw[i][2] = dw.z; hw[i][3] = dw.w;
     }
+    long aw[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) aw[j] = *(const long *)(aq + m * GEMM_AS + 32 * j + 8 * q);
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         // the tile's column blocks from the round's LDS stage (column c's
@@ -450,239 +404,305 @@ DEV void q80_sk_group(const Q80A &A, const uint8_t *slot, int q, int m, int nj, 
         for (int j = 0; j < 8; j++) bq[j] = *(const long *)(col + 32 * j + 8 * q);
         v4i d[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) d[j] = mfma_i8(A.q[j], bq[j]);
+        for (int j = 0; j < 8; j++) d[j] = mfma_i8(aw[j], bq[j]);
 #pragma unroll
         for (int i = 0; i < 4; i++) fs[n][i] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (FULL || j < nj) {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    fs[n][i] = __fadd_rn(fs[n][i], __fmul_rn(__fmul_rn(dr[i][j], xs[j]), (float)d[j][i]));
+                for (int i = 0; i < 4; i++) {
+                    // d_j·xs_j: the f16 scale times xs in one rounding (v_fma_mix with a −0 addend)
+                    const float dx = (j & 1) ? mul_h16hi(hw[i][j >> 1], xs[j]) : mul_h16lo(hw[i][j >> 1], xs[j]);
+                    fs[n][i] = __fadd_rn(fs[n][i], __fmul_rn(dx, (float)d[j][i]));
+                }
             }
         }
     }
 }
 
+// A wave's weights of one group — 16 rows × 16 code words + 16 scale words —
+// as 5 coalesced 16-byte words a lane: code word i (< 4) is word lane % 16 of
+// row 4i + lane / 16 (block 8g + word/2; a short last group repeats the
+// row's last block), word 4 is row lane % 16's scale word (lanes 16.. repeat
+// lanes 0..15). Staged in the wave's own LDS slot (GEMM_AS-byte rows).
+#define SK_AS (16 * GEMM_AS + 256)   // LDS bytes a wave's staged group
+
+DEV void sk_a_load(u32x4 (&v)[5], const uint8_t *const (&arow)[4], const uint8_t *srow, int64_t g, int64_t nb32,
+                   int lane) {
+    const int w16 = lane & 15;
+    const int64_t blk = min(8 * g + (w16 >> 1), nb32 - 1);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = *(const u32x4 *)(arow[i] + blk * 32 + 16 * (w16 & 1));
+    v[4] = *(const u32x4 *)(srow + 16 * g);
+}
+
+DEV void sk_a_store(const u32x4 (&v)[5], uint8_t *al, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint8_t *dst = al + (4 * i + (lane >> 4)) * GEMM_AS + 16 * (lane & 15);
+        *(uint2 *)dst = make_uint2(v[i].x, v[i].y);
+        *(uint2 *)(dst + 8) = make_uint2(v[i].z, v[i].w);
+    }
+    if (lane < 16) *(u32x4 *)(al + 16 * GEMM_AS + 16 * lane) = v[4];
+}
+
+// A wave's share of the pack blocks: the 16·NT columns' 320-byte blocks of
+// its own group, 20·16·NT words, as 5·NT coalesced 16-byte words a lane —
+// word i = 5n + k is word (lane + 64k) of column tile n: column
+// (lane + 64k) / 20, word (lane + 64k) % 20 — staged in the wave's own LDS
+// slot (column c at c·GEMM_CS). The offsets are worked out once.
+template <int NT>
+struct SkB {
+    uint32_t off[5 * NT];   // bytes from the group's block of column c0
+    uint32_t dst[5];        // slot offsets in column tile 0
+    DEV void init(const cj_gemv_args &a, int64_t c0, int lane) {
+#pragma unroll
+        for (int k = 0; k < 5; k++) {
+            const int idx = lane + 64 * k, col = idx / 20, word = idx % 20;
+            dst[k] = col * GEMM_CS + 16 * word;
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const int64_t c = min(c0 + col + 16 * n, (int64_t)a.batch - 1);
+                off[5 * n + k] = (uint32_t)((c - c0) * a.xp_stride + 16 * word);
+            }
+        }
+    }
+    DEV void load(u32x4 (&v)[5 * NT], const uint8_t *base) const {
+#pragma unroll
+        for (int i = 0; i < 5 * NT; i++) v[i] = *(const u32x4 *)(base + off[i]);
+    }
+    DEV void store(const u32x4 (&v)[5 * NT], uint8_t *slot) const {
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int k = 0; k < 5; k++) *(u32x4 *)(slot + 16 * n * GEMM_CS + dst[k]) = v[5 * n + k];
+    }
+};
+
+// Split-K Q8_0: every wave stages its own group's weights and column blocks
+// (no workgroup barrier between the staging and the reads: a wave's LDS
+// operations complete in order), so a round needs one barrier, for the
+// hand-off of the terms. The fold is shared out: output slot v = 4n + i of
+// every lane (column 16n + m, row 4q + i) belongs to wave v, which adds the
+// round's terms of the waves in group order; the hand-off buffer alternates
+// by round (buffer rd & 1 is rewritten two rounds on, after the next
+// barrier, which a wave reaches only once it has folded round rd).
 template <int NT, int W>
 DEV void gemm_sk_q80(const cj_gemv_args &a) {
-    using S = SkStage<NT, W>;
-    __shared__ __align__(16) float hand[W][NT * 4][64];
-    __shared__ __align__(16) uint8_t bl[W * S::CT * GEMM_CS];   // the round's pack blocks, a slot a wave
+    static_assert(NT * 4 <= W, "an output slot a wave");
+    constexpr int BS = 16 * NT * GEMM_CS;   // a wave's column-block slot
+    __shared__ __align__(16) float hand[2][W][NT * 4][64];
+    __shared__ __align__(16) uint8_t bl[W * BS];
+    __shared__ __align__(16) uint8_t al[W * SK_AS];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
     const int64_t nb32 = a.cols / 32, ngrp = (a.cols + 255) / 256;
-    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + 8 * q;
-    const uint8_t *wd[4];
+    const uint8_t *arow[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) wd[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb32 * 32;
-    float acc[NT][4];
-#pragma unroll
-    for (int n = 0; n < NT; n++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
-    Q80A A, An;
-    u32x4 sv[S::NW];
+    for (int i = 0; i < 4; i++) arow[i] = a.w + min(r0 + 4 * i + q, a.rows - 1) * a.row_bytes;
+    const uint8_t *srow = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + nb32 * 32;
+    const uint8_t *xb = a.xp + c0 * a.xp_stride;
+    uint8_t *bw = bl + wave * BS, *aw = al + wave * SK_AS;
+    float acc = 0.0f;   // output slot `wave` of this lane (waves past NT·4 hold none)
+    SkB<NT> B;
+    B.init(a, c0, lane);
+    u32x4 bv[5 * NT], av[5];
     {
-        sk_b_load<NT, W, S::NW>(sv, a, c0, 0, ngrp);
         const int64_t g0 = min((int64_t)wave, ngrp - 1);
-        q80_fetch(A, wa, wd, g0, (int)min((int64_t)8, nb32 - 8 * g0));
-        sk_b_store<NT, W, S::NW>(sv, bl);
-        __syncthreads();
+        B.load(bv, xb + g0 * 320);
+        sk_a_load(av, arow, srow, g0, nb32, lane);
+        B.store(bv, bw);
+        sk_a_store(av, aw, lane);
     }
     const int64_t rounds = (ngrp + W - 1) / W;
     auto round = [&](int64_t rd, auto pf) {
         const int64_t g = rd * W + wave;
         if constexpr (decltype(pf)::on) {
-            // the next round's pack blocks, then the wave's next group
-            // (clamped: past the end it re-reads the last), before the
-            // branch below
-            sk_b_load<NT, W, S::NW>(sv, a, c0, rd + 1, ngrp);
+            // the wave's next group (clamped: past the end it re-reads the
+            // last), before the branch below
             const int64_t gn = min(g + W, ngrp - 1);
-            q80_fetch(An, wa, wd, gn, (int)min((int64_t)8, nb32 - 8 * gn));
+            B.load(bv, xb + gn * 320);
+            sk_a_load(av, arow, srow, gn, nb32, lane);
         }
-        float fs[NT][4];
         if (g < ngrp) {
-            const uint8_t *slot = bl + wave * S::CT * GEMM_CS;
+            float fs[NT][4];
             const int nj = (int)min((int64_t)8, nb32 - 8 * g);
-            if (nj == 8) q80_sk_group<NT, true>(A, slot, q, m, 8, fs);
-            else q80_sk_group<NT, false>(A, slot, q, m, nj, fs);
-        }
-        if constexpr (decltype(pf)::on) A = An;
-        if (wave > 0 && g < ngrp) {
+            if (nj == 8) q80_sk_group<NT, true>(aw, bw, q, m, 8, fs);
+            else q80_sk_group<NT, false>(aw, bw, q, m, nj, fs);
 #pragma unroll
             for (int n = 0; n < NT; n++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) hand[wave][4 * n + i][lane] = fs[n][i];
+                for (int i = 0; i < 4; i++) hand[rd & 1][wave][4 * n + i][lane] = fs[n][i];
         }
-        __syncthreads();   // every wave has read this round's blocks and handed its terms
-        if constexpr (decltype(pf)::on) sk_b_store<NT, W, S::NW>(sv, bl);
-        if (wave == 0) {
+        if constexpr (decltype(pf)::on) {   // the wave's own slots: its reads above come first
+            B.store(bv, bw);
+            sk_a_store(av, aw, lane);
+        }
+        __syncthreads();   // round rd's terms are handed
+        if (wave < NT * 4) {
             const int live = (int)min((int64_t)W, ngrp - rd * W);
-#pragma unroll
-            for (int n = 0; n < NT; n++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], fs[n][i]);
-            for (int w = 1; w < live; w++)
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[n][i] = __fadd_rn(acc[n][i], hand[w][4 * n + i][lane]);
+            for (int w = 0; w < live; w++) acc = __fadd_rn(acc, hand[rd & 1][w][wave][lane]);
         }
-        __syncthreads();
     };
     for (int64_t rd = 0; rd + 1 < rounds; rd++) round(rd, PF<true>{});
     round(rounds - 1, PF<false>{});
-    if (wave != 0) return;
+    if (wave >= NT * 4) return;
+    const int n = wave >> 2, i = wave & 3;
+    const int64_t c = c0 + 16 * n + m, r = r0 + 4 * q + i;
+    if (c < a.batch && r < a.rows) {
+        float *y = a.y + c * a.y_stride + a.y_off + r;
+        *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
+    }
+}
+
+// Split-K Q4_K, staged and folded as the Q8_0 form. A wave's weights of one
+// block: 16 rows × (8 code chunks + the header), 144 16-byte words, as 3
+// words a lane — word idx = lane + 64k: code chunk idx % 8 of row idx / 8
+// (idx < 128), the header of row idx − 128 (idx < 144) — staged as rows of
+// Q4S bytes (the row's 128 code bytes in order) and the 16 headers after.
+#define Q4S 136
+#define SK4_AS (16 * Q4S + 256)
+
+DEV void q4k_sk_group(const uint8_t *aq, const uint8_t *col, int q, int m, float (&t1)[4], float (&t2)[4]) {
+    const uint64_t M = 0x0F0F0F0F0F0F0F0Full;
+    int sc[4][8], mn[4][8];
+    float dd[4], dm[4];
 #pragma unroll
-    for (int n = 0; n < NT; n++) {
-        const int64_t c = c0 + 16 * n + m;
-        if (c >= a.batch) continue;
-        float *y = a.y + c * a.y_stride + a.y_off;
+    for (int i = 0; i < 4; i++) {
+        const uint4 h = *(const uint4 *)(aq + 16 * Q4S + (4 * q + i) * 16);
+        const uint32_t X = h.y, Y = h.z, Z = h.w;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t r = r0 + 4 * q + i;
-            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
+        for (int j = 0; j < 4; j++) {
+            const uint32_t a8 = (X >> (8 * j)) & 255, b8 = (Y >> (8 * j)) & 255, c8 = (Z >> (8 * j)) & 255;
+            sc[i][j] = (int)(a8 & 63);
+            mn[i][j] = (int)(b8 & 63);
+            sc[i][j + 4] = (int)((c8 & 15) | ((a8 >> 2) & 48));
+            mn[i][j + 4] = (int)((c8 >> 4) | ((b8 >> 2) & 48));
         }
+        dd[i] = h2f(h.x);
+        dm[i] = h2f(h.x >> 16);
+    }
+    long lo[4], hi[4], bl8[4], bh8[4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++) {
+        const uint64_t w = *(const uint64_t *)(aq + m * Q4S + 32 * g4 + 8 * q);
+        lo[g4] = (long)(w & M);
+        hi[g4] = (long)((w >> 4) & M);
+        bl8[g4] = *(const long *)(col + 64 * g4 + 8 * q);
+        bh8[g4] = *(const long *)(col + 64 * g4 + 32 + 8 * q);
+    }
+    const int4 s0 = *(const int4 *)(col + 256), s1 = *(const int4 *)(col + 272);
+    const float xs = *(const float *)(col + 288);
+    // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
+    v4i dl[4], dh[4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++) {
+        dl[g4] = mfma_i8(lo[g4], bl8[g4]);
+        dh[g4] = mfma_i8(hi[g4], bh8[g4]);
+    }
+    int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            sumi[i] += __mul24(dl[g4][i], sc[i][2 * g4]) + __mul24(dh[g4][i], sc[i][2 * g4 + 1]);
+    const int bsum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int dmins = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++) dmins += __mul24(bsum[s2], mn[i][s2]);
+        t1[i] = __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi[i]);
+        t2[i] = __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins);
     }
 }
 
 template <int NT, int W>
 DEV void gemm_sk_q4k(const cj_gemv_args &a) {
-    using S = SkStage<NT, W>;
-    __shared__ __align__(16) float hand[W][NT * 8][64];
-    __shared__ __align__(16) uint8_t bl[W * S::CT * GEMM_CS];   // the round's pack blocks, a slot a wave
+    static_assert(NT * 4 <= W, "an output slot a wave");
+    constexpr int BS = 16 * NT * GEMM_CS;
+    __shared__ __align__(16) float hand[2][W][NT * 4][2][64];
+    __shared__ __align__(16) uint8_t bl[W * BS];
+    __shared__ __align__(16) uint8_t al[W * SK4_AS];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, m = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * 16 * NT, r0 = (int64_t)blockIdx.y * 16;
     const int64_t nb = a.cols / 256;
-    const uint8_t *wa = a.w + min(r0 + m, a.rows - 1) * a.row_bytes;
-    const uint8_t *wh[4];
+    // this lane's three weight words: code chunks of rows lane/8 and 8 + lane/8,
+    // the header of row lane % 16 (lanes 16.. repeat it)
+    const uint8_t *ap[3];
+    int adst[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) wh[i] = a.w + min(r0 + 4 * q + i, a.rows - 1) * a.row_bytes + nb * 128;
-    const uint64_t M = 0x0F0F0F0F0F0F0F0Full;
-    float acc[NT][4];
+    for (int k = 0; k < 2; k++) {
+        const int row = 8 * k + (lane >> 3), chunk = lane & 7;
+        ap[k] = a.w + min(r0 + row, a.rows - 1) * a.row_bytes + (int64_t)chunk * nb * 16;
+        adst[k] = row * Q4S + 16 * chunk;
+    }
+    ap[2] = a.w + min(r0 + m, a.rows - 1) * a.row_bytes + nb * 128;
+    const uint8_t *xb = a.xp + c0 * a.xp_stride;
+    uint8_t *bw = bl + wave * BS, *aw = al + wave * SK4_AS;
+    auto aload = [&](u32x4 (&v)[3], int64_t b) {
 #pragma unroll
-    for (int n = 0; n < NT; n++)
+        for (int k = 0; k < 3; k++) v[k] = *(const u32x4 *)(ap[k] + b * 16);
+    };
+    auto astore = [&](const u32x4 (&v)[3]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
-    Q4kA A, An;
-    u32x4 sv[S::NW];
+        for (int k = 0; k < 2; k++) {
+            *(uint2 *)(aw + adst[k]) = make_uint2(v[k].x, v[k].y);
+            *(uint2 *)(aw + adst[k] + 8) = make_uint2(v[k].z, v[k].w);
+        }
+        if (lane < 16) *(u32x4 *)(aw + 16 * Q4S + 16 * lane) = v[2];
+    };
+    float acc = 0.0f;   // output slot `wave` of this lane (waves past NT·4 hold none)
+    SkB<NT> B;
+    B.init(a, c0, lane);
+    u32x4 bv[5 * NT], av[3];
     {
-        sk_b_load<NT, W, S::NW>(sv, a, c0, 0, nb);
         const int64_t b0 = min((int64_t)wave, nb - 1);
-        q4k_fetch_a(A, wa, wh, nb, b0, q);
-        sk_b_store<NT, W, S::NW>(sv, bl);
-        __syncthreads();
+        B.load(bv, xb + b0 * 320);
+        aload(av, b0);
+        B.store(bv, bw);
+        astore(av);
     }
     const int64_t rounds = (nb + W - 1) / W;
     auto round = [&](int64_t rd, auto pf) {
         const int64_t b = rd * W + wave;
-        float t1[NT][4], t2[NT][4];
-        if constexpr (decltype(pf)::on) {   // the next round's blocks and the wave's next block (as in gemm_sk_q80)
-            sk_b_load<NT, W, S::NW>(sv, a, c0, rd + 1, nb);
+        if constexpr (decltype(pf)::on) {   // the wave's next block (clamped past the end)
             const int64_t bn = min(b + W, nb - 1);
-            q4k_fetch_a(An, wa, wh, nb, bn, q);
+            B.load(bv, xb + bn * 320);
+            aload(av, bn);
         }
         if (b < nb) {
-            int sc[4][8], mn[4][8];
-            float dd[4], dm[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t X = A.h[i].y, Y = A.h[i].z, Z = A.h[i].w;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t a8 = (X >> (8 * j)) & 255, b8 = (Y >> (8 * j)) & 255, c8 = (Z >> (8 * j)) & 255;
-                    sc[i][j] = (int)(a8 & 63);
-                    mn[i][j] = (int)(b8 & 63);
-                    sc[i][j + 4] = (int)((c8 & 15) | ((a8 >> 2) & 48));
-                    mn[i][j + 4] = (int)((c8 >> 4) | ((b8 >> 2) & 48));
-                }
-                dd[i] = h2f(A.h[i].x);
-                dm[i] = h2f(A.h[i].x >> 16);
-            }
-            long lo[4], hi[4];
-#pragma unroll
-            for (int g4 = 0; g4 < 4; g4++) {
-                const uint64_t w = (uint64_t)A.q[g4];
-                lo[g4] = (long)(w & M);
-                hi[g4] = (long)((w >> 4) & M);
-            }
 #pragma unroll
             for (int n = 0; n < NT; n++) {
-                // the tile's column blocks from the round's LDS stage
-                const uint8_t *col = bl + (wave * S::CT + 16 * n + m) * GEMM_CS;
-                long bl8[4], bh8[4];
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    bl8[g4] = *(const long *)(col + 64 * g4 + 8 * q);
-                    bh8[g4] = *(const long *)(col + 64 * g4 + 32 + 8 * q);
-                }
-                const int4 s0 = *(const int4 *)(col + 256), s1 = *(const int4 *)(col + 272);
-                const float xs = *(const float *)(col + 288);
-                // Σ_s sc_s·dot_s and Σ_s mn_s·bsum_s are exact int32 sums: any order
-                v4i dl[4], dh[4];
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    dl[g4] = mfma_i8(lo[g4], bl8[g4]);
-                    dh[g4] = mfma_i8(hi[g4], bh8[g4]);
-                }
-                int sumi[4] = {0, 0, 0, 0};
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        sumi[i] += __mul24(dl[g4][i], sc[i][2 * g4]) + __mul24(dh[g4][i], sc[i][2 * g4 + 1]);
-                const int bsum[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                float t1[4], t2[4];
+                q4k_sk_group(aw, bw + (16 * n + m) * GEMM_CS, q, m, t1, t2);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    int dmins = 0;
-#pragma unroll
-                    for (int s2 = 0; s2 < 8; s2++) dmins += __mul24(bsum[s2], mn[i][s2]);
-                    t1[n][i] = __fmul_rn(__fmul_rn(dd[i], xs), (float)sumi[i]);
-                    t2[n][i] = __fmul_rn(__fmul_rn(dm[i], xs), (float)dmins);
+                    hand[rd & 1][wave][4 * n + i][0][lane] = t1[i];
+                    hand[rd & 1][wave][4 * n + i][1][lane] = t2[i];
                 }
             }
         }
-        if constexpr (decltype(pf)::on) A = An;
-        if (wave > 0 && b < nb) {
-#pragma unroll
-            for (int n = 0; n < NT; n++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    hand[wave][8 * n + i][lane] = t1[n][i];
-                    hand[wave][8 * n + 4 + i][lane] = t2[n][i];
-                }
+        if constexpr (decltype(pf)::on) {   // the wave's own slots: its reads above come first
+            B.store(bv, bw);
+            astore(av);
         }
-        __syncthreads();   // every wave has read this round's blocks and handed its terms
-        if constexpr (decltype(pf)::on) sk_b_store<NT, W, S::NW>(sv, bl);
-        if (wave == 0) {
+        __syncthreads();   // round rd's terms are handed
+        if (wave < NT * 4) {
             const int live = (int)min((int64_t)W, nb - rd * W);
-#pragma unroll
-            for (int n = 0; n < NT; n++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], t1[n][i]), t2[n][i]);
-            for (int w = 1; w < live; w++)
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[n][i] = __fsub_rn(__fadd_rn(acc[n][i], hand[w][8 * n + i][lane]), hand[w][8 * n + 4 + i][lane]);
+            for (int w = 0; w < live; w++)
+                acc = __fsub_rn(__fadd_rn(acc, hand[rd & 1][w][wave][0][lane]), hand[rd & 1][w][wave][1][lane]);
         }
-        __syncthreads();
     };
     for (int64_t rd = 0; rd + 1 < rounds; rd++) round(rd, PF<true>{});
     round(rounds - 1, PF<false>{});
-    if (wave != 0) return;
-#pragma unroll
-    for (int n = 0; n < NT; n++) {
-        const int64_t c = c0 + 16 * n + m;
-        if (c >= a.batch) continue;
-        float *y = a.y + c * a.y_stride + a.y_off;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t r = r0 + 4 * q + i;
-            if (r < a.rows) y[r] = a.epi == CJ_EPI_ACCUM ? __fadd_rn(y[r], acc[n][i]) : acc[n][i];
-        }
+    if (wave >= NT * 4) return;
+    const int n = wave >> 2, i = wave & 3;
+    const int64_t c = c0 + 16 * n + m, r = r0 + 4 * q + i;
+    if (c < a.batch && r < a.rows) {
+        float *y = a.y + c * a.y_stride + a.y_off + r;
+        *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
     }
 }
 
