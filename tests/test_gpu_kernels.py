@@ -394,7 +394,7 @@ def test_kernel_registry_answers_reference_names(gpu):
 @pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_k", 12), ("q6_k", 14), ("q4_0", 2)])
 @pytest.mark.parametrize("rows,cols,ncols", [(300, 512, 1), (1024, 4096, 4), (64, 1408, 8), (272, 4096, 17),
                                              (96, 14336, 16), (160, 2048, 70), (100, 1408, 80), (40, 512, 33),
-                                             (130, 768, 200), (37, 4096, 5)])
+                                             (130, 768, 200), (37, 4096, 5), (48, 2560, 24)])
 def test_matmul_columns_equal_matvec(gpu, O, name, ty, rows, cols, ncols):
     """The batched product (int8 matrix cores for Q8_0 and Q4_K, the
     many-column GEMV for Q6_K and Q4_0): every output column is the one-column
