@@ -294,6 +294,24 @@ def test_rope_freqs_model_parity(gpu, hd):
     assert run_pair.bit_identical, err
 
 
+@pytest.mark.parametrize("heads,kv", [(8, 8), (8, 4), (16, 2)])
+def test_prefill_attend_query_groups(gpu, heads, kv):
+    """The prefill attend at head size 128 for 1, 2 and 8 query heads a kv
+    head (the benchmark shapes have 4): a 300-token prompt through 128-row
+    chunks (the last one partial), then decode steps, bit for bit."""
+    say("prefill attend heads", heads, "kv", kv)
+    name = "t_pfg%d" % (heads // kv)
+    spec = "layers=1;hidden=1024;heads=%d;kv=%d;hd=128;ffn=1024;vocab=2048;eps=1e-5;theta=10000;" \
+           "wtype=q8_0;head=q8_0;embd=q8_0;ctx=512" % (heads, kv)
+    path, img = synth(gpu, spec, name, 95 + kv)
+    rng = np.random.default_rng(heads * 10 + kv)
+    prompt = rng.integers(0, 2048, 300).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 6, 512, chunk=128)
+    gpu.image_free(name)
+    assert g == o
+    assert run_pair.bit_identical, err
+
+
 def test_c4_shape_q8_0_two_layers_greedy_parity(gpu):
     """Benchmark configuration C4's Q8_0 weights on the 8B shapes, at two layers."""
     say("model c4x2")
