@@ -986,28 +986,17 @@ extern "C" __global__ void __launch_bounds__(64) cj_attn_merge_w(cj_merge_args a
 // The many-row form: row r's blocks (a row is whole blocks of 256), its
 // partials and split count from the row table, its output and pack at the
 // row strides.
-extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_args a) {
-    __shared__ float bmax[8];
-    __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
-    const int t = threadIdx.x, lane = t & 63;
-    const int64_t n = (int64_t)a.n_q * a.head_dim;
-    const int hd = a.head_dim;
-    const int64_t per = n / 256, r = blockIdx.x / per, blk = blockIdx.x % per;
-    const float *part = a.part + r * a.part_stride;
-    float *out = a.out ? a.out + r * a.out_stride : nullptr;
-    uint8_t *packed = a.packed ? a.packed + r * a.pack_stride : nullptr;
-    int count = a.states[a.rowtab[2 * r]].pos + a.rowtab[2 * r + 1] + 1;
-    const int64_t e = blk * 256 + t;
-    // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
-    const int64_t ew = min(blk * 256 + (t & ~63), n - 1);
-    const int h = (int)(ew / hd), d = (int)(min(e, n - 1) % hd);
-    const float *pb0 = part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
-    float pv[ATTN_MAX_SPLITS];
+// The merge of one output of a batch row over its first NS splits (the row
+// takes at most NS; the rest hold no part).
+template <int NS>
+DEV void merge_rows_fold(const cj_merge_args &a, const float *pb0, int lane, int d, int splits, int64_t e, int64_t n,
+                         float *out, uint8_t *packed, int64_t blk, float *bmax, float (*sw)[ATTN_MAX_SPLITS],
+                         float (*sl)[ATTN_MAX_SPLITS]) {
+    const int hd = a.head_dim, t = threadIdx.x;
+    float pv[NS];
 #pragma unroll
-    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
+    for (int s2 = 0; s2 < NS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
     const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
-    if (a.window > 0 && count > a.window) count = a.window;
-    const int splits = decode_splits(count, a.nrows * a.n_kv, a.workers);
     const bool in = lane < splits;
     const float mv = in ? ml.x : -3.0e38f;
     const float gm = group_max<64>(mv);
@@ -1023,7 +1012,7 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_ar
     __builtin_amdgcn_wave_barrier();
     float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s0 = 0; s0 < ATTN_MAX_SPLITS; s0 += 16) {
+    for (int s0 = 0; s0 < NS; s0 += 16) {
         float w[16], lv[16];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -1047,6 +1036,30 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_ar
     const float x = e < n ? __fmul_rn(tacc, __fdiv_rn(1.0f, gt)) : 0.0f;
     if (out && e < n) out[e] = x;
     if (packed) pack256(x, a.per32, packed + blk * 320, bmax);
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_args a) {
+    __shared__ float bmax[8];
+    __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t n = (int64_t)a.n_q * a.head_dim;
+    const int hd = a.head_dim;
+    const int64_t per = n / 256, r = blockIdx.x / per, blk = blockIdx.x % per;
+    const float *part = a.part + r * a.part_stride;
+    float *out = a.out ? a.out + r * a.out_stride : nullptr;
+    uint8_t *packed = a.packed ? a.packed + r * a.pack_stride : nullptr;
+    int count = a.states[a.rowtab[2 * r]].pos + a.rowtab[2 * r + 1] + 1;
+    const int64_t e = blk * 256 + t;
+    // the wave's head (hd ≥ 64: a wave's 64 outputs share one head)
+    const int64_t ew = min(blk * 256 + (t & ~63), n - 1);
+    const int h = (int)(ew / hd), d = (int)(min(e, n - 1) % hd);
+    const float *pb0 = part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
+    if (a.window > 0 && count > a.window) count = a.window;
+    const int splits = decode_splits(count, a.nrows * a.n_kv, a.workers);
+    // a batch's rows take few splits (4 at 32 rows of 8 kv heads): read and
+    // fold only the first 16 where that covers them
+    if (splits <= 16) merge_rows_fold<16>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl);
+    else merge_rows_fold<ATTN_MAX_SPLITS>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl);
 }
 
 // QK-norm (optional) + split-half RoPE + fp16 K/V append, one workgroup of
