@@ -24,16 +24,18 @@ extern "C" __global__ void __launch_bounds__(256) cj_rows_embed(cj_rows_args a) 
 // q|k|v rows (GGUF pair order, the projection's stored output) through the
 // one-row epilogue: RoPE of each (2b, 2b+1) pair of q and k at the row's
 // position, q out in HF order, k and v appended to the fp16 pages of the
-// row's sequence (one workgroup a row).
+// row's sequence (grid: 512-value blocks of the row × rows, a pair a thread;
+// a workgroup a row looped over the row with its stores between the loads).
 extern "C" __global__ void __launch_bounds__(256) cj_rows_qkv(cj_rows_args a) {
-    const int r = blockIdx.x;
+    const int r = blockIdx.y;
     const int slot = row_slot(a, r), pos = row_pos(a, r);
     const int page = a.pgtab[(int64_t)slot * a.pg_n + (pos >> 6)];
     const int hd = a.head_dim, half = hd >> 1;
     const int64_t qrows = (int64_t)a.n_q * hd, krows = (int64_t)a.n_kv * hd, total = qrows + 2 * krows;
     const float *y = a.in + (int64_t)r * a.in_stride;
     float *qo = a.q_out + (int64_t)r * a.out_stride;
-    for (int64_t i = 2 * (int64_t)threadIdx.x; i < total; i += 512) {
+    const int64_t i = 512 * (int64_t)blockIdx.x + 2 * (int64_t)threadIdx.x;
+    if (i < total) {
         const float2 vv = *(const float2 *)(y + i);
         const float v = vv.x, vp = vv.y;
         if (i < qrows + krows) {

@@ -905,7 +905,8 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             q.in = r_qkv; q.in_stride = L.qkv.rows; q.q_out = r_q; q.out_stride = qd; q.kc = L.kc; q.vc = L.vc;
             q.pgtab = pgtab; q.rope_cs = rope; q.pg_n = pages_per_seq; q.n_q = n_heads; q.n_kv = n_kv;
             q.head_dim = head_dim; q.nrows = n;
-            if ((rc = launch("cj_rows_qkv", (uint32_t)n, 256, 0, q))) return rc;
+            const int64_t qkv_vals = (int64_t)(n_heads + 2 * n_kv) * head_dim;
+            if ((rc = launch2("cj_rows_qkv", (uint32_t)((qkv_vals + 511) / 512), (uint32_t)n, 256, 0, q))) return rc;
         }
         cj_attn_args a{};
         a.q = r_q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
