@@ -182,6 +182,9 @@ struct Engine {
     int enqueue_step(int s);
     int run_step(int s);
     int norm_pack(const float *w, int per32, bool f32_out, const float *x = nullptr);
+    // rows a workgroup the head's GEMV aims at: 64 where 128 would leave a
+    // workgroup a CU or fewer
+    int head_target() const { return (int64_t)vocab <= 128LL * 2 * std::max(1, device_cus()) ? 64 : 128; }
     // the many-row path
     int rows_alloc(int cap);
     int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
@@ -731,7 +734,7 @@ int Engine::enqueue_step(int s) {
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128, a.pro, a.epi);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(), a.pro, a.epi);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
         if (only < 0) {
@@ -1016,7 +1019,7 @@ int Engine::prefill_rows(int s, const int32_t *toks, int n) {
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, 128, a.pro, a.epi);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(), a.pro, a.epi);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
         cj_pick_args k{};
