@@ -177,23 +177,36 @@ DEV void terms_q6k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 // Q8_0 × per-32 int8. One 32-element block a lane, term (d·xs)·isum; the 8
 // lanes of a 256-wide group then sum their terms in block order (the
 // reference's fs) and the group's first lane writes it.
+template <int NR>
+struct Q80Item {
+    uint4 w0[NR], w1[NR];
+    uint32_t dh[NR];
+};
+
+template <int NR>
+DEV void q80_item(Q80Item<NR> &x, const uint8_t *const (&wr)[NR], int nb32, int uu) {
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        x.w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
+        x.w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
+        x.dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
+    }
+}
+
+// The next iteration's weights are requested before this one's arithmetic
+// (every iteration but the last, unconditionally: a load under a branch
+// would be waited for at the join), so a row wider than one sweep streams
+// without a round trip between sweeps.
 template <int NR, int LPR>
 DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
     const int lane = threadIdx.x & 63;
     const int base = lane & ~7;
     const int iters = (nb32 + LPR - 1) / LPR;
-    for (int it = 0; it < iters; it++) {
+    auto uu_of = [&](int it) { const int u = slot + it * LPR; return u < nb32 ? u : nb32 - 1; };
+    auto body = [&](const Q80Item<NR> &x, int it) {
         const int u = slot + it * LPR;
         const bool ok = u < nb32;
         const int uu = ok ? u : nb32 - 1;
-        uint4 w0[NR], w1[NR];
-        uint32_t dh[NR];
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
-            w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
-            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
-        }
         const uint8_t *ab = sx + (uu >> 3) * 320;
         const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
         const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
@@ -201,11 +214,11 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             int s = 0;
-            s = sdot4(w0[r].x, a0.x, s); s = sdot4(w0[r].y, a0.y, s);
-            s = sdot4(w0[r].z, a0.z, s); s = sdot4(w0[r].w, a0.w, s);
-            s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
-            s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
-            const float t = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
+            s = sdot4(x.w0[r].x, a0.x, s); s = sdot4(x.w0[r].y, a0.y, s);
+            s = sdot4(x.w0[r].z, a0.z, s); s = sdot4(x.w0[r].w, a0.w, s);
+            s = sdot4(x.w1[r].x, a1.x, s); s = sdot4(x.w1[r].y, a1.y, s);
+            s = sdot4(x.w1[r].z, a1.z, s); s = sdot4(x.w1[r].w, a1.w, s);
+            const float t = __fmul_rn(__fmul_rn(h2f(x.dh[r]), xs), (float)s);
             float fs = __shfl(t, base);
 #pragma unroll
             for (int k = 1; k < 8; k++) {
@@ -214,7 +227,15 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
             }
             if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
+    };
+    Q80Item<NR> cur, nxt;
+    q80_item(cur, wr, nb32, uu_of(0));
+    for (int it = 0; it + 1 < iters; it++) {
+        q80_item(nxt, wr, nb32, uu_of(it + 1));
+        body(cur, it);
+        cur = nxt;
     }
+    body(cur, iters - 1);
 }
 
 // ------------------------------------------------------------- epilogues
