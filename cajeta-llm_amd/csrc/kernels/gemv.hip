@@ -119,8 +119,89 @@ DEV float2 q4k_block_terms(const Q4kBlock &x, const Q4kAct &v) {
 // Q6_K × q8_K. Unit (block b, 64 elements): half g, lane half hl; four
 // 16-element scale groups; the 6-bit values 0..63 dot the int8 activation
 // and 32·Σa comes off per group. The leader writes d·xs·sumi.
+template <int NR>
+struct Q6kItem {
+    uint4 qa[NR], qb[NR], qh[NR];
+    uint2 sc[NR];
+    uint32_t dh[NR];
+};
+
+template <int NR>
+DEV void q6k_item(Q6kItem<NR> &x, const uint8_t *const (&wr)[NR], int nb, int u) {
+    const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const uint8_t *row = wr[r];
+        x.qa[r] = ld_stream16(row + (int64_t)b * 128 + 64 * g + 16 * hl);
+        x.qb[r] = ld_stream16(row + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
+        x.qh[r] = ld_stream16(row + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
+        x.sc[r] = *(const uint2 *)(row + (int64_t)nb * 192 + (int64_t)b * 16 + 8 * g);
+        x.dh[r] = *(const uint16_t *)(row + (int64_t)nb * 208 + 2 * b);
+    }
+}
+
+// Sweeps of LPR units (64-element quarter blocks); the next sweep's weights
+// are requested before this one's arithmetic, as in terms_q80. A quad of
+// lanes past the row's units (all four or none: units and LPR are multiples
+// of 4) re-reads the last unit and writes nothing.
 template <int NR, int LPR>
 DEV void terms_q6k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb, int slot) {
+    const int units = nb * 4, iters = (units + LPR - 1) / LPR;
+    auto u_of = [&](int it) { const int u = slot + it * LPR; return u < units ? u : units - 1; };
+    auto body = [&](const Q6kItem<NR> &x, int it) {
+        const bool ok = slot + it * LPR < units;
+        const int u = u_of(it);
+        const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
+        const uint8_t *ab = sx + b * 320 + 128 * g + 16 * hl;
+        uint4 a[4];
+        int S[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            a[k] = *(const uint4 *)(ab + 32 * k);
+            int s = 0;
+            s = sdot4(0x01010101u, a[k].x, s); s = sdot4(0x01010101u, a[k].y, s);
+            s = sdot4(0x01010101u, a[k].z, s); s = sdot4(0x01010101u, a[k].w, s);
+            S[k] = s;
+        }
+        const float xs = *(const float *)(sx + b * 320 + 288);
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            int sumi = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint4 ql = (k & 1) ? x.qb[r] : x.qa[r];
+                const int sh = (k >> 1) * 4;
+                const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
+                const uint32_t vx = ((ql.x >> sh) & M) | (((x.qh[r].x >> (2 * k)) & H) << 4);
+                const uint32_t vy = ((ql.y >> sh) & M) | (((x.qh[r].y >> (2 * k)) & H) << 4);
+                const uint32_t vz = ((ql.z >> sh) & M) | (((x.qh[r].z >> (2 * k)) & H) << 4);
+                const uint32_t vw = ((ql.w >> sh) & M) | (((x.qh[r].w >> (2 * k)) & H) << 4);
+                int dt = 0;
+                dt = sdot4(vx, a[k].x, dt); dt = sdot4(vy, a[k].y, dt);
+                dt = sdot4(vz, a[k].z, dt); dt = sdot4(vw, a[k].w, dt);
+                const int byte_i = 2 * k + hl;
+                const uint32_t word = byte_i < 4 ? x.sc[r].x : x.sc[r].y;
+                const int scv = (int)(int8_t)((word >> (8 * (byte_i & 3))) & 255);
+                sumi += scv * (dt - 32 * S[k]);
+            }
+            sumi += quad_xor1(sumi); sumi += quad_xor2(sumi);
+            if (ok && j == 0) tr[r][b] = __fmul_rn(__fmul_rn(h2f(x.dh[r]), xs), (float)sumi);
+        }
+    };
+    Q6kItem<NR> cur, nxt;
+    q6k_item(cur, wr, nb, u_of(0));
+    for (int it = 0; it + 1 < iters; it++) {
+        q6k_item(nxt, wr, nb, u_of(it + 1));
+        body(cur, it);
+        cur = nxt;
+    }
+    body(cur, iters - 1);
+}
+
+// Q6_K without the next sweep's prefetch, for rows that fit one sweep
+// (fewer registers: the one-sweep kernels keep their occupancy).
+template <int NR, int LPR>
+DEV void terms_q6k_1(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb, int slot) {
     const int units = nb * 4;
     for (int u = slot; u < units; u += LPR) {
         const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
@@ -177,36 +258,23 @@ DEV void terms_q6k(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 // Q8_0 × per-32 int8. One 32-element block a lane, term (d·xs)·isum; the 8
 // lanes of a 256-wide group then sum their terms in block order (the
 // reference's fs) and the group's first lane writes it.
-template <int NR>
-struct Q80Item {
-    uint4 w0[NR], w1[NR];
-    uint32_t dh[NR];
-};
-
-template <int NR>
-DEV void q80_item(Q80Item<NR> &x, const uint8_t *const (&wr)[NR], int nb32, int uu) {
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-        x.w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
-        x.w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
-        x.dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
-    }
-}
-
-// The next iteration's weights are requested before this one's arithmetic
-// (every iteration but the last, unconditionally: a load under a branch
-// would be waited for at the join), so a row wider than one sweep streams
-// without a round trip between sweeps.
 template <int NR, int LPR>
 DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
     const int lane = threadIdx.x & 63;
     const int base = lane & ~7;
     const int iters = (nb32 + LPR - 1) / LPR;
-    auto uu_of = [&](int it) { const int u = slot + it * LPR; return u < nb32 ? u : nb32 - 1; };
-    auto body = [&](const Q80Item<NR> &x, int it) {
+    for (int it = 0; it < iters; it++) {
         const int u = slot + it * LPR;
         const bool ok = u < nb32;
         const int uu = ok ? u : nb32 - 1;
+        uint4 w0[NR], w1[NR];
+        uint32_t dh[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
+            w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
+            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
+        }
         const uint8_t *ab = sx + (uu >> 3) * 320;
         const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
         const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
@@ -214,11 +282,11 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             int s = 0;
-            s = sdot4(x.w0[r].x, a0.x, s); s = sdot4(x.w0[r].y, a0.y, s);
-            s = sdot4(x.w0[r].z, a0.z, s); s = sdot4(x.w0[r].w, a0.w, s);
-            s = sdot4(x.w1[r].x, a1.x, s); s = sdot4(x.w1[r].y, a1.y, s);
-            s = sdot4(x.w1[r].z, a1.z, s); s = sdot4(x.w1[r].w, a1.w, s);
-            const float t = __fmul_rn(__fmul_rn(h2f(x.dh[r]), xs), (float)s);
+            s = sdot4(w0[r].x, a0.x, s); s = sdot4(w0[r].y, a0.y, s);
+            s = sdot4(w0[r].z, a0.z, s); s = sdot4(w0[r].w, a0.w, s);
+            s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
+            s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
+            const float t = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
             float fs = __shfl(t, base);
 #pragma unroll
             for (int k = 1; k < 8; k++) {
@@ -227,15 +295,7 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
             }
             if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
-    };
-    Q80Item<NR> cur, nxt;
-    q80_item(cur, wr, nb32, uu_of(0));
-    for (int it = 0; it + 1 < iters; it++) {
-        q80_item(nxt, wr, nb32, uu_of(it + 1));
-        body(cur, it);
-        cur = nxt;
     }
-    body(cur, iters - 1);
 }
 
 // ------------------------------------------------------------- epilogues
@@ -768,7 +828,7 @@ DEV void q40_gemv(const cj_gemv_args &a) {
 }
 
 // Generic body (Q6_K, Q8_0 and the f32-activation formats).
-template <int FMT, int LPR, int NR>
+template <int FMT, int LPR, int NR, bool MULTI = false>
 DEV void gemv_body(const cj_gemv_args &a) {
     extern __shared__ __align__(16) uint8_t smem[];
     float *red = (float *)smem;
@@ -819,8 +879,13 @@ DEV void gemv_body(const cj_gemv_args &a) {
                 wr[k] = sl.W + (rk < a.rows ? rk : a.rows - 1) * a.row_bytes;
                 tr[k] = terms + (rl0 + k) * TB;
             }
-            if (FMT == CJ_Q6_K) terms_q6k<NR, LPR>(wr, tr, sx, nb, slot);
-            else terms_q80<NR, LPR>(wr, tr, sx, nb32, slot);
+            if constexpr (MULTI) {
+                static_assert(FMT == CJ_Q6_K, "the multi-sweep form is Q6_K's");
+                terms_q6k<NR, LPR>(wr, tr, sx, nb, slot);
+            } else {
+                if (FMT == CJ_Q6_K) terms_q6k_1<NR, LPR>(wr, tr, sx, nb, slot);
+                else terms_q80<NR, LPR>(wr, tr, sx, nb32, slot);
+            }
         }
     }
     __syncthreads();
@@ -1100,6 +1165,13 @@ DEV void gemv_q4k_body(const cj_gemv_args &a) {
         gemv_body<FMT, LPR, NR>(a);                                                     \
     }
 
+// _s: Q6_K rows wider than one sweep of 64 lanes, the next sweep's weights
+// requested before the current sweep's arithmetic
+#define GEMV_KERNEL_S(NAME, FMT, NR)                                                   \
+    extern "C" __global__ void __launch_bounds__(256) NAME(cj_gemv_args a) {            \
+        gemv_body<FMT, 64, NR, true>(a);                                                \
+    }
+
 #define GEMV_FAMILY(PFX, FMT, NR)               \
     GEMV_KERNEL(PFX##_l64, FMT, 64, NR)         \
     GEMV_KERNEL(PFX##_l32, FMT, 32, NR)         \
@@ -1335,6 +1407,7 @@ MXQ8_KBS(g, CJ_EPI_GLU, 4)
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)
+GEMV_KERNEL_S(cj_gemv_q6k_l64_s, CJ_Q6_K, 2)
 // cj_gemv_q40b_r<RW>: Q4_0 block-parallel, RW rows a wave (4·RW a workgroup)
 extern "C" __global__ void __launch_bounds__(256) cj_gemv_q40b_r2(cj_gemv_args a) { q40_gemv<2>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_gemv_q40b_r4(cj_gemv_args a) { q40_gemv<4>(a); }
