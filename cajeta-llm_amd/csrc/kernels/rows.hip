@@ -64,19 +64,70 @@ extern "C" __global__ void __launch_bounds__(256) cj_rows_qkv(cj_rows_args a) {
 
 // SiLU(gate)·up of interleaved gate/up rows (row 2e gate, 2e+1 up: the fused
 // projection's layout), then the q8 pack of each 256-wide block for the down
-// projection (grid: blocks × rows). The f32 result is kept when `out` is set.
+// projection (grid: groups of four blocks × rows). A wave packs one block,
+// four consecutive values a lane (two 16-byte loads of gate/up pairs, one
+// 4-byte store of codes): the block and 32-group maxima, the codes, sums and
+// scales of pack256, reduced across lanes without LDS. The f32 result is kept
+// when `out` is set.
 extern "C" __global__ void __launch_bounds__(256) cj_rows_glu(cj_rows_args a) {
-    __shared__ float bmax[8];
-    const int r = blockIdx.y;
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int r = blockIdx.y, lane = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= a.npad / 256) return;   // whole waves past the last block
+    const int64_t e0 = blk * 256 + 4 * lane;
     const float *y = a.in + (int64_t)r * a.in_stride;
-    float v = 0.0f;
-    if (e < a.n) {
-        const float2 gu = *(const float2 *)(y + 2 * e);
-        v = glu_value(a.form, e, a.n, gu.x, gu.y);
-        if (a.out) a.out[(int64_t)r * a.out_stride + e] = v;
+    float v[4];
+    if (e0 + 4 <= a.n && ((uintptr_t)y & 15) == 0) {
+        const float4 p0 = *(const float4 *)(y + 2 * e0), p1 = *(const float4 *)(y + 2 * e0 + 4);
+        v[0] = glu_value(a.form, e0, a.n, p0.x, p0.y);
+        v[1] = glu_value(a.form, e0 + 1, a.n, p0.z, p0.w);
+        v[2] = glu_value(a.form, e0 + 2, a.n, p1.x, p1.y);
+        v[3] = glu_value(a.form, e0 + 3, a.n, p1.z, p1.w);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int64_t e = e0 + k;
+            v[k] = 0.0f;
+            if (e < a.n) {
+                const float2 gu = *(const float2 *)(y + 2 * e);
+                v[k] = glu_value(a.form, e, a.n, gu.x, gu.y);
+            }
+        }
     }
-    pack256(v, a.per32, a.packed + (int64_t)r * a.pack_stride + (int64_t)blockIdx.x * 320, bmax);
+    if (a.out) {
+        float *o = a.out + (int64_t)r * a.out_stride;
+#pragma unroll
+        for (int k = 0; k < 4; k++) if (e0 + k < a.n) o[e0 + k] = v[k];
+    }
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 4));    // the 32-group (eight lanes)
+    if (!a.per32) {
+        m = fmaxf(m, __shfl_xor(m, 8));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+    }
+    const float inv = m > 0.0f ? __fdiv_rn(127.0f, m) : 0.0f;
+    uint32_t w = 0u;
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int q = round_away(__fmul_rn(v[k], inv));
+        s += q;
+        w |= ((uint32_t)q & 255u) << (8 * k);
+    }
+    uint8_t *ob = a.packed + (int64_t)r * a.pack_stride + blk * 320;
+    *(uint32_t *)(ob + 4 * lane) = w;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if ((lane & 7) == 0) *(int32_t *)(ob + 256 + 4 * (lane >> 3)) = s;
+    if (a.per32) {
+        if ((lane & 7) == 0) *(float *)(ob + 288 + 4 * (lane >> 3)) = __fdiv_rn(m, 127.0f);
+    } else {
+        if (lane == 0) *(float *)(ob + 288) = __fdiv_rn(m, 127.0f);
+        pack_zero_pad(ob, lane);
+    }
 }
 
 // First-occurrence argmax partials: chunk c (1024 wide) of row r's logits →

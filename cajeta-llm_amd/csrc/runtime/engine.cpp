@@ -964,7 +964,7 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             cj_rows_args g = ra;
             g.in = r_gu; g.in_stride = L.gu.rows; g.packed = r_actp; g.pack_stride = fpad / 256 * 320;
             g.n = ffn; g.npad = fpad; g.form = (ffn % 256) ? 1 : 0; g.per32 = L.down.type == CJ_Q8_0; g.nrows = n;
-            if ((rc = launch2("cj_rows_glu", (uint32_t)(fpad / 256), (uint32_t)n, 256, 0, g))) return rc;
+            if ((rc = launch2("cj_rows_glu", (uint32_t)((fpad / 256 + 3) / 4), (uint32_t)n, 256, 0, g))) return rc;
         }
         if ((rc = rows_linear(L.down, r_actp, fpad / 256 * 320, r_hs, hidden, true, n))) return rc;
     }
