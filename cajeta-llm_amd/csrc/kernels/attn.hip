@@ -968,15 +968,26 @@ extern "C" __global__ void __launch_bounds__(64) cj_attn_merge_w(cj_merge_args a
     const bool on = in && ml.y > 0.0f;
     const float wt = on ? cj_expf(mv - gm) : 0.0f;
     const uint64_t ons = __ballot(on);
+    // the splits' weights and sums through LDS, back as broadcast 16-byte
+    // reads (four splits a read instead of a lane read each)
+    __shared__ __align__(16) float sw[ATTN_MAX_SPLITS], sl[ATTN_MAX_SPLITS];
+    sw[lane] = wt;
+    sl[lane] = ml.y;
+    __builtin_amdgcn_wave_barrier();
     float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) {
-        const float w = lane_f(wt, s2), lv = lane_f(ml.y, s2);
-        const bool use = (ons >> s2) & 1;
-        const float g2 = __fadd_rn(gl[s2 & 3], __fmul_rn(w, lv));
-        const float a2 = __fadd_rn(ac[s2 & 3], __fmul_rn(pv[s2], w));
-        gl[s2 & 3] = use ? g2 : gl[s2 & 3];
-        ac[s2 & 3] = use ? a2 : ac[s2 & 3];
+    for (int s0 = 0; s0 < ATTN_MAX_SPLITS; s0 += 4) {
+        const float4 w4 = *(const float4 *)&sw[s0], l4 = *(const float4 *)&sl[s0];
+        const float w[4] = {w4.x, w4.y, w4.z, w4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int s2 = s0 + j;
+            const bool use = (ons >> s2) & 1;
+            const float g2 = __fadd_rn(gl[j], __fmul_rn(w[j], lv[j]));
+            const float a2 = __fadd_rn(ac[j], __fmul_rn(pv[s2], w[j]));
+            gl[j] = use ? g2 : gl[j];
+            ac[j] = use ? a2 : ac[j];
+        }
     }
     const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
     const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
