@@ -93,6 +93,9 @@ typedef struct {
     int32_t *route_status;
     int32_t route_experts, route_used, route_norm_topk;
     float route_scale;
+    // NORM_F32 prologue: workgroup 0 also writes the normed f32 activation
+    // here (for the launches after it; may be null)
+    float *xout;
 } cj_gemv_args;
 
 typedef struct {

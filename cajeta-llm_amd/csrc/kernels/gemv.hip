@@ -385,8 +385,14 @@ DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, 
     } else {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
         const float scale = norm ? stage_norm_scale(sl.X, cols, a.eps, red) : 1.0f;
-        if (f32act) stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx, swz);
-        else stage_pack(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr, bstride);
+        if (f32act) {
+            stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx, swz);
+            if (a.xout && norm && !swz && blockIdx.x == 0) {   // the staged values (stage_f32 ends on a barrier)
+                for (int64_t e = threadIdx.x; e < cols; e += 256) a.xout[e] = ((const float *)sx)[e];
+            }
+        } else {
+            stage_pack(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, a.per32, sx, nullptr, bstride);
+        }
     }
 }
 

@@ -644,7 +644,12 @@ int Engine::enqueue_step(int s) {
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
         const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096;
-        if (!gu_norm && want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
+        // MoE with an f32 router and MXFP4 experts (both read the f32 norm,
+        // neither the pack): the router's prologue forms the norm and writes
+        // it for the experts
+        const bool router_norm = n_experts > 0 && L.router.type == CJ_F32 && L.gu_exps.type == CJ_MXFP4 &&
+                                 L.down_exps.type == CJ_MXFP4;
+        if (!gu_norm && !router_norm && want(K_NORM, l)) {   // the FFN norm: pack (int8 consumers) and/or f32 (router, f32-activation experts)
             const int ct = n_experts ? L.gu_exps.type : L.gu.type;
             if ((rc = norm_pack(L.ffn_norm, ct == CJ_Q8_0, n_experts > 0, cur))) return rc;
         }
@@ -672,6 +677,7 @@ int Engine::enqueue_step(int s) {
                 a.w = (const uint8_t *)L.router.p; a.x = xn; a.y = moe_logits; a.rows = n_experts;
                 a.cols = hidden; a.row_bytes = L.router.row_bytes; a.type = CJ_F32; a.pro = CJ_PRO_F32;
                 a.epi = CJ_EPI_STORE; a.eps = eps; a.batch = 1;
+                if (router_norm) { a.pro = CJ_PRO_NORM_F32; a.x = cur; a.nw = L.ffn_norm; a.norm_form = 0; a.xout = xn; }
                 if ((rc = run_gemv(a, plan_gemv(CJ_F32, a.rows, a.cols, 0, a.pro, a.epi)))) return rc;
             }
             const bool fused = route_fused(L);
