@@ -210,6 +210,7 @@ typedef struct {
     // the step's greedy pick from per-workgroup (value, index) partials
     const float *pv; const int32_t *pi; int32_t n, pos;
     int32_t *tokens, *preds; cj_step_state *state;
+    int32_t *host_tok;      // pinned host mirror of `tokens` (null: none): the host reads a step's token without a copy
 } cj_pick_args;
 
 typedef struct {
@@ -242,6 +243,15 @@ typedef struct {
     int32_t pad;
     int32_t *status;         // set to 1 when a row's logits are not finite (may be null)
 } cj_route_args;
+
+// routerTopKKernel's arguments (io/QuantKernel.cajeta:39850-39960): the
+// router mat-vec of one f32 row and its top-k in one launch.
+typedef struct {
+    int32_t *sel; float *w; float *logits; const float *w_router; const float *x;
+    int32_t *counter;        // zero before the launch; the selecting workgroup leaves it zero
+    int32_t experts, cols, used, norm_topk;
+    float w_scale;
+} cj_router_topk_args;
 
 typedef struct {
     // one MoE expert stage: rows of expert sel[k] for each k < n_used

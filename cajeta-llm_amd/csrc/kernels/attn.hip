@@ -1093,8 +1093,21 @@ extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
             for (int m = 1; m <= 8; m <<= 1) ss = __fadd_rn(ss, __shfl_xor(ss, m));
             ss = __fadd_rn(__fadd_rn(__fadd_rn(__shfl(ss, 0), __shfl(ss, 16)), __shfl(ss, 32)), __shfl(ss, 48));
         } else {
-            for (int i = t; i < hd; i += 64) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
-            ss = group_sum<64>(ss);
+            // the generic qkPrepKernel's order: reference lane l (of 128)
+            // sums x[l]², x[l+128]², ...; Workgroup.reduce folds each 32-lane
+            // wave by the butterfly from the adjacent lane up (1, 2, 4, 8,
+            // 16) and adds the four wave sums in order. Lane t holds
+            // reference lanes t (a) and t + 64 (b): lanes 0-31 end with waves
+            // 0 and 2, lanes 32-63 with waves 1 and 3.
+            float a = 0.0f, b = 0.0f;
+            for (int i = t; i < hd; i += 128) a = __fadd_rn(a, __fmul_rn(x[i], x[i]));
+            for (int i = t + 64; i < hd; i += 128) b = __fadd_rn(b, __fmul_rn(x[i], x[i]));
+#pragma unroll
+            for (int m = 1; m <= 16; m <<= 1) {
+                a = __fadd_rn(a, __shfl_xor(a, m));
+                b = __fadd_rn(b, __shfl_xor(b, m));
+            }
+            ss = __fadd_rn(__fadd_rn(__fadd_rn(__shfl(a, 0), __shfl(a, 32)), __shfl(b, 0)), __shfl(b, 32));
         }
         const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)hd), a.eps)));
         const float *w = isq ? a.qw : a.kw;

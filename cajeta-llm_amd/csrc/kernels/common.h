@@ -83,27 +83,45 @@ DEV float mxfp4_val(uint32_t nib) {
     return (float)v;
 }
 
-// exp(x) in f32 from correctly rounded steps only, so it gives the same bits
-// as the checker's restatement: n = rint(x·log2 e); r = x − n·ln2 by two fma
-// (Cody–Waite, ln2_hi with trailing zeros); e^r by the degree-7 Taylor
-// polynomial (Horner, fma); ·2^n in two exact power-of-two steps.
+// exp(x) in f32 as the reference CPU backend computes it: its Math.exp is
+// glibc's expf (the reference's recorded CPU softmax outputs,
+// attnScoreKernel h32kv4d128c256, are reproduced by glibc expf in all 8192
+// values and not by a correctly rounded exp), whose algorithm is ARM
+// optimized-routines' expf: k = round(x·32/ln2) and r = x·32/ln2 − k, each
+// from one fused multiply-add of the f64 x (the round by adding 1.5·2^52);
+// 2^(k/32) from a 32-entry table of 2^(i/32) rounded to f64, the integer
+// part added to its exponent bits; 2^(r/32) by the degree-3 polynomial
+// C0·r³ + C1·r² + C2·r + 1 in f64 with fused multiply-adds; one rounding to
+// f32 at the end. The table entries are 2^(i/32) correctly rounded to f64,
+// stored less i·2^47 in their bit patterns so that adding k·2^47 lands the
+// exponent. Over every f32 input this gives glibc 2.35's expf bit for bit.
+__device__ __constant__ uint64_t CJ_EXP2_TAB[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
 DEV float cj_expf(float x) {
-    if (x != x) return x;
-    if (x < -104.0f) return 0.0f;
-    if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
-    const float n = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
-    float r = __fmaf_rn(n, -0.693145751953125f, x);
-    r = __fmaf_rn(n, -1.428606765330187045e-06f, r);
-    float p = 1.98412698412698413e-04f;
-    p = __fmaf_rn(p, r, 1.38888888888888889e-03f);
-    p = __fmaf_rn(p, r, 8.33333333333333333e-03f);
-    p = __fmaf_rn(p, r, 4.16666666666666667e-02f);
-    p = __fmaf_rn(p, r, 1.66666666666666667e-01f);
-    p = __fmaf_rn(p, r, 0.5f);
-    p = __fmaf_rn(p, r, 1.0f);
-    p = __fmaf_rn(p, r, 1.0f);
-    const int ni = (int)n, n1 = ni / 2, n2 = ni - n1;
-    return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(n1 + 127) << 23)), __uint_as_float((uint32_t)(n2 + 127) << 23));
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32 * 32), c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32),
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __fma_rn(inv_ln2_n, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd = kd - shift;
+    const double r = __fma_rn(inv_ln2_n, xd, -kd);
+    const double s = __longlong_as_double((long long)(CJ_EXP2_TAB[ki & 31] + (ki << 47)));
+    const double z = __fma_rn(c0, r, c1), r2 = r * r;
+    double y = __fma_rn(c2, r, 1.0);
+    y = __fma_rn(z, r2, y);
+    return __double2float_rn(y * s);
 }
 
 // SiLU(x)·u, exp form: x / (1 + exp(−x)) · u (Prim.gluF32 / gluOne).

@@ -384,6 +384,7 @@ extern "C" __global__ void __launch_bounds__(256) cj_argmax_pick(cj_pick_args a)
         const int pos = a.state ? a.state->pos : a.pos;
         if (a.preds) a.preds[pos + 1] = bi[0];
         if (a.tokens && (!a.state || pos + 1 >= a.state->fixed_until)) a.tokens[pos + 1] = bi[0];
+        if (a.host_tok) __hip_atomic_store(a.host_tok + pos + 1, bi[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (a.state) a.state->pos = pos + 1;
     }
 }
@@ -452,6 +453,90 @@ extern "C" __global__ void __launch_bounds__(64) cj_moe_route(cj_route_args a) {
     if (t < a.n_used) {
         a.sel[row * a.n_used + t] = rl.sel[t];
         a.w[row * a.n_used + t] = rl.w[t];
+    }
+}
+
+// routerTopKKernel (io/QuantKernel.cajeta:39850-39960): the router mat-vec
+// and its top-k in one launch, for models whose router takes the device
+// route. Workgroup e forms logit e: thread l adds the rounded products
+// w[e][j]·x[j] for j = l, l+256, ... in order, and the 256 partials fold
+// 128, 64, ..., 1 (the reference's recorded e128h2048k8 logits fix that
+// order). It publishes the logit (device-scope release) and takes a ticket
+// on `counter`; the workgroup taking the last one selects in 32 lanes of its
+// first wave, the reference's wave width: lane l's experts l, l+32, ...; the
+// maximum; each lane's sum of exp(logit − max) in expert order, the 32 sums
+// by the butterfly (lane distance 16, 8, 4, 2, 1 — Wave.reduceSumF32's
+// order, fixed by the recorded two-pass scores); `used` picks, each the
+// largest probability below the previous pick (an equal probability: the
+// next index up), w = p/sum; the renormalisation by Σw in pick order clamped
+// at 2^-14, then ×w_scale unless it is 0 or 1; the counter back to zero.
+extern "C" __global__ void __launch_bounds__(256) cj_router_topk(cj_router_topk_args a) {
+    __shared__ float red[256];
+    __shared__ int last;
+    const int t = threadIdx.x, e = blockIdx.x;
+    float acc = 0.0f;
+    if (e < a.experts)
+        for (int j = t; j < a.cols; j += 256) acc = __fadd_rn(acc, __fmul_rn(a.w_router[(int64_t)e * a.cols + j], a.x[j]));
+    red[t] = acc;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s) red[t] = __fadd_rn(red[t], red[t + s]);
+        __syncthreads();
+    }
+    if (t == 0) {
+        if (e < a.experts) a.logits[e] = red[0];
+        __threadfence();
+        last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last || t >= 32) return;
+    __threadfence();
+    const int ne = a.experts;
+    float lm = -3.4028234663852886e38f;
+    for (int x = t; x < ne; x += 32) lm = fmaxf(lm, __hip_atomic_load(a.logits + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) lm = fmaxf(lm, __shfl_xor(lm, m));
+    const float mx = lm;
+    float ls = 0.0f;
+    for (int x = t; x < ne; x += 32)
+        ls = __fadd_rn(ls, cj_expf(__fsub_rn(__hip_atomic_load(a.logits + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), mx)));
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) ls = __fadd_rn(ls, __shfl_xor(ls, m));
+    const float sum = ls;
+    float vlast = 3.4028234663852886e38f;
+    int ilast = ne;
+    for (int k = 0; k < a.used; k++) {
+        float bv = -1.0f;
+        int bi = ne;
+        for (int x = t; x < ne; x += 32) {
+            const float p = cj_expf(__fsub_rn(__hip_atomic_load(a.logits + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), mx));
+            const bool ok = p < vlast || (p == vlast && x > ilast);
+            if (ok && (p > bv || (p == bv && x < bi))) { bv = p; bi = x; }
+        }
+        // the wave's largest probability, then the lowest index holding it
+        float vk = bv;
+#pragma unroll
+        for (int m = 16; m > 0; m >>= 1) vk = fmaxf(vk, __shfl_xor(vk, m));
+        int ik = bv == vk ? bi : ne;
+#pragma unroll
+        for (int m = 16; m > 0; m >>= 1) ik = min(ik, __shfl_xor(ik, m));
+        if (t == 0) {
+            a.sel[k] = ik;
+            a.w[k] = __fdiv_rn(vk, sum);
+        }
+        vlast = vk;
+        ilast = ik;
+    }
+    if (t == 0) {
+        if (a.norm_topk) {
+            float ws = 0.0f;
+            for (int k = 0; k < a.used; k++) ws = __fadd_rn(ws, a.w[k]);
+            if (ws < 0.00006103515625f) ws = 0.00006103515625f;
+            for (int k = 0; k < a.used; k++) a.w[k] = __fdiv_rn(a.w[k], ws);
+        }
+        if (a.w_scale != 0.0f && a.w_scale != 1.0f)
+            for (int k = 0; k < a.used; k++) a.w[k] = __fmul_rn(a.w[k], a.w_scale);
+        a.counter[0] = 0;
     }
 }
 

@@ -1,20 +1,23 @@
 // engine.cpp — the decode engine behind the LlmEngine surface: a GGUF model
-// loaded into prepared, fused device weights, paged fp16 K/V, and the whole
-// per-token decode step (embedding → layers → norm → head → argmax) captured
-// once per sequence slot into a hipGraph and replayed per token. Position and
-// token history live on the device, so step N+1 is enqueued without waiting
-// for step N (the reference's queueStep/awaitStep pipelining,
-// model/CausalLM.cajeta:1208-1256, taken to its end: the host reads tokens
-// only to check stops).
+// loaded into prepared, fused device weights, paged fp16 K/V drawn from a
+// shared page pool, and the whole per-token decode step (embedding → layers
+// → norm → head → argmax) captured once per sequence slot into a hipGraph
+// and replayed per token. Position and token history live on the device, so
+// step N+1 is enqueued without waiting for step N (the reference's
+// queueStep/awaitStep pipelining, model/CausalLM.cajeta:1208-1256): the
+// scheduler's pipelined greedy decode queues it before reading step N's
+// token, which the head's pick also writes to pinned host memory.
 //
-// Per dense layer the step is five launches:
+// Per dense layer the step is six launches:
 //   1. q|k|v GEMV, RMSNorm + pack in the prologue, RoPE + fp16 K/V append
 //      in the epilogue (residentLayer steps 1-3, CausalLM.cajeta:3636-3694)
-//   2. split-K flash decode, the last split merging (steps 4-5)
-//   3. o GEMV, pack prologue, residual-accumulate epilogue (step 6)
-//   4. gate|up GEMV, RMSNorm + pack prologue, SiLU·up + pack epilogue (7-9)
-//   5. down GEMV, residual-accumulate epilogue (step 10)
-// MoE layers (gpt-oss shape) replace 4-5 with router GEMV, top-k, indirected
+//   2. split-K flash decode partials (step 4; or the two-pass scores, then
+//      the softmax + p·V combine, where the reference takes that form)
+//   3. the split merge, f32 out (step 5)
+//   4. o GEMV, pack prologue, residual-accumulate epilogue (step 6)
+//   5. gate|up GEMV, RMSNorm + pack prologue, SiLU·up epilogue (7-9)
+//   6. down GEMV, pack prologue, residual-accumulate epilogue (step 10)
+// MoE layers (gpt-oss shape) replace 5-6 with router GEMV, top-k, indirected
 // expert gate|up, indirected expert down and the weighted combine.
 #include "gguf.h"
 #include "rt.h"
@@ -58,13 +61,19 @@ struct Seq {
 // A request of the scheduler (sched/Request.cajeta): its ids (prompt, then
 // generated), how many positions the model has consumed, and its state.
 struct Request {
-    enum { WAITING = 0, RUNNING = 1, DONE = 2 };
+    // Request.WAITING/RUNNING/PREEMPTED/DONE (sched/Request.cajeta:9-13)
+    enum { WAITING = 0, RUNNING = 1, PREEMPTED = 2, DONE = 3 };
     // Request.FINISH_* (sched/Request.cajeta:18-23)
     enum { FINISH_NONE = 0, FINISH_BUDGET = 1, FINISH_EOS = 2, FINISH_CANCEL = 4 };
     std::vector<int32_t> all;     // prompt then generated ids (Request.all)
     std::vector<int32_t> stops;   // stop tokens: the model's EOG set unless the caller gave its own
     int prompt_len = 0, max_new = 0, gen = 0;
     int cached = 0;               // positions the model has consumed (Request.cachedLen)
+    // ids all[0, feed) go to the model from the host (the prompt, or after a
+    // preemption the whole stream, recomputed); past that the device holds
+    // each id: the pick that produced it wrote it into the slot's history
+    int feed = 0;
+    int stamp = 0, pre_stamp = 0; // admission order (the preemption age), preemption order (the resume FIFO)
     int state = WAITING, slot = -1, finish = FINISH_NONE;
 };
 
@@ -132,6 +141,23 @@ struct Engine {
         a.route_experts = n_experts; a.route_used = n_used; a.route_norm_topk = norm_topk; a.route_scale = w_scale;
     }
     int32_t *pinned = nullptr; // pinned host staging: [ctx + 2] token ids, then a cj_step_state
+    // the K/V page pool (PagedKvCache's blocks, model/CausalLM.cajeta:64-94):
+    // a slot draws 64-position pages as its sequence grows and returns them
+    // when it is reset or its request leaves; the default pool holds every
+    // slot at its full context
+    int kv_pages = 0;
+    std::vector<int32_t> free_pages;
+    std::vector<std::vector<int32_t>> slot_pages;
+    int32_t *pinned_pg = nullptr;   // host mirror of the page table (pinned: the source of its uploads)
+    // the pipelined greedy decode (Scheduler.pipeFor/stepPipelined,
+    // sched/Scheduler.cajeta:613-702): the step in flight and the one before
+    bool pipe_in = false;
+    int pipe_req = -1, pipe_out = 0;
+    int pipe_pos[2] = {0, 0};       // the position each in-flight step consumes
+    hipEvent_t pipe_ev[2] = {nullptr, nullptr};
+    int32_t *host_tok = nullptr;    // pinned [max_seqs][ctx + 2]: the head's pick writes every token here too
+    int stamp_n = 0;
+    int64_t preempted_n = 0, resumed_n = 0;
     int64_t embd_row_file_bytes = 0;
     // the many-row path: batched decode (a row a sequence) and prefill
     // chunks (a row a position)
@@ -174,8 +200,16 @@ struct Engine {
         for (void *p : owned) dev_free(p);
         if (pinned) (void)hipHostFree(pinned);
         if (pinned_tab) (void)hipHostFree(pinned_tab);
+        if (pinned_pg) (void)hipHostFree(pinned_pg);
+        if (host_tok) (void)hipHostFree(host_tok);
+        for (auto &e : pipe_ev)
+            if (e) (void)hipEventDestroy(e);
     }
-    int load(const std::string &path, int ctx_, int max_seqs_);
+    int load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_);
+    // the page pool
+    int ensure_pages(int s, int64_t upto);
+    bool pages_fit(int s, int64_t upto) const;
+    void release_pages(int s);
     int upload_weight(const std::string &name, DevW &w, int expect_rows, int64_t expect_cols);
     int fuse_rows(const std::vector<std::string> &names, DevW &w, bool interleave, int64_t rows_each, int64_t experts);
     int capture(int s);
@@ -206,6 +240,16 @@ struct Engine {
     void retire(Request &r, int finish);
     void consume(Request &r, int32_t tok);
     int step_once();
+    int sole_running() const;
+    int youngest_running() const;
+    bool pipe_for(int i, const Request &r, int n);
+    int step_pipelined(int i, Request &r);
+    int queue_pipe_step(int s, int slot_ev);
+    int await_pipe(int32_t *tok);
+    int finish_pipe();
+    int drain_pipe();
+    int preempt(int i);
+    int cancel(int i);
     int64_t kind_bytes(int kind, int count) const;
     int64_t step_bytes(int count) const;
     int time_kind(int s, int kind, int reps, float *avg_us, std::string &kernel);
@@ -294,7 +338,7 @@ int Engine::fuse_rows(const std::vector<std::string> &names, DevW &w, bool inter
     return CJ_OK;
 }
 
-int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
+int Engine::load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_) {
     std::string err;
     if (!file.open(path, err)) return fail(CJ_ERR_IO, "model: %s", err.c_str());
     const std::string arch = file.get_str("general.architecture", "");
@@ -367,7 +411,12 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     pages_per_seq = (ctx + 63) / 64;
     if (!(head_dim == 128 && (grp == 4 || grp == 8)) && pages_per_seq > 2048)
         return fail(CJ_ERR_ARG, "model: context %d exceeds the two-pass attention's 2048 pages", ctx);
-    const int64_t plane = (int64_t)pages_per_seq * max_seqs * n_kv * 64 * head_dim * 2;
+    // the pool: numBlocks 0 holds every slot at its full context (CausalLM's
+    // constructor, model/CausalLM.cajeta:83-88); fewer pages share the pool
+    // and the scheduler preempts when it runs dry
+    if (kv_pages_ < 0) return fail(CJ_ERR_ARG, "model: %d K/V pages", kv_pages_);
+    kv_pages = kv_pages_ > 0 ? kv_pages_ : pages_per_seq * max_seqs;
+    const int64_t plane = (int64_t)kv_pages * n_kv * 64 * head_dim * 2;
     int rc;
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
@@ -401,13 +450,19 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
     head_type = head.type;
     if (is_f32_act(wtype)) return fail(CJ_ERR_IO, "model: attention weights of type %d are not served", wtype);
 
-    // K/V page table: sequence s owns pages [s·pages_per_seq, (s+1)·pages_per_seq)
-    std::vector<int32_t> tab((size_t)pages_per_seq * max_seqs);
-    for (size_t i = 0; i < tab.size(); i++) tab[i] = (int32_t)i;
-    pgtab = (int32_t *)alloc(tab.size() * 4);
+    // K/V page table: entry s·pages_per_seq + j is the pool page holding
+    // slot s's positions [64j, 64j + 64), drawn as the slot grows (entries
+    // not drawn yet read page 0 and are never dereferenced)
+    const size_t tab_n = (size_t)pages_per_seq * max_seqs;
+    pgtab = (int32_t *)alloc(tab_n * 4);
     rope = (float *)alloc((size_t)ctx * head_dim * 4);
     if (!pgtab || !rope) return fail(CJ_ERR_HIP, "model: out of device memory");
-    CJ_HIP(hipMemcpy(pgtab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+    if (hipHostMalloc((void **)&pinned_pg, tab_n * 4, 0) != hipSuccess) return fail(CJ_ERR_HIP, "model: pinned page table");
+    memset(pinned_pg, 0, tab_n * 4);
+    CJ_HIP(hipMemcpy(pgtab, pinned_pg, tab_n * 4, hipMemcpyHostToDevice));
+    free_pages.resize((size_t)kv_pages);
+    for (int i = 0; i < kv_pages; i++) free_pages[(size_t)i] = kv_pages - 1 - i;   // drawn from the back: 0, 1, 2, ...
+    slot_pages.assign((size_t)max_seqs, {});
     // Llama-3.1-style precomputed RoPE factors (ModelConfig, model/ModelConfig.cajeta:307-316)
     const GgufTensor *rf = file.tensor("rope_freqs.weight");
     if (rf && rf->type != CJ_F32) return fail(CJ_ERR_IO, "model: rope_freqs.weight is type %d, not f32", rf->type);
@@ -457,6 +512,10 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_) {
 
     if (hipHostMalloc((void **)&pinned, (size_t)(ctx + 2) * 4 + sizeof(cj_step_state) + 64, 0) != hipSuccess)
         return fail(CJ_ERR_HIP, "model: pinned staging buffer");
+    if (hipHostMalloc((void **)&host_tok, (size_t)(ctx + 2) * max_seqs * 4, 0) != hipSuccess)
+        return fail(CJ_ERR_HIP, "model: pinned token mirror");
+    memset(host_tok, 0xff, (size_t)(ctx + 2) * max_seqs * 4);
+    for (auto &e : pipe_ev) CJ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     // sequence slots: histories and step states side by side, so the
     // many-row kernels reach every slot's from one base
     const size_t hist = (size_t)(ctx + 2);
@@ -746,7 +805,7 @@ int Engine::enqueue_step(int s) {
         if (only < 0) {
             cj_pick_args k{};
             k.pv = part_v; k.pi = part_i; k.n = (int32_t)p.grid; k.tokens = S.tokens; k.preds = S.preds;
-            k.state = S.state;
+            k.state = S.state; k.host_tok = host_tok + (size_t)s * (ctx + 2);
             if ((rc = launch("cj_argmax_pick", 1, 256, 0, k))) return rc;
         }
     }
@@ -1039,7 +1098,7 @@ int Engine::prefill_rows(int s, const int32_t *toks, int n) {
     CJ_HIP(hipMemcpyAsync(S.state, st, sizeof *st, hipMemcpyHostToDevice, stream()));
     CJ_HIP(hipStreamSynchronize(stream()));
     S.fixed_until = S.pos;
-    return CJ_OK;
+    return check_route();
 }
 
 // `steps` greedy tokens for each of n prefilled slots at once (one row a
@@ -1059,6 +1118,8 @@ int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
     }
     if (steps <= 0) return CJ_OK;
     int rc;
+    for (int r = 0; r < n; r++)
+        if ((rc = ensure_pages(slots[r], (int64_t)seqs[slots[r]].pos + steps))) return rc;
     if (!rows_ok || n > rows_cap) {
         std::vector<int32_t> tmp((size_t)steps);
         for (int r = 0; r < n; r++) {
@@ -1113,7 +1174,7 @@ int Engine::decode_batch(const int32_t *slots, int n, int steps, int32_t *out) {
         }
         S.pos += steps;
     }
-    return CJ_OK;
+    return check_route();
 }
 
 // After the stream is drained: an error when the router met a row whose
@@ -1135,11 +1196,55 @@ int Engine::run_step(int s) {
     return CJ_OK;
 }
 
+// Slot s holds pages for positions [0, upto) once this returns: the pages
+// it lacks are drawn from the pool and their table entries uploaded, on the
+// stream ahead of the work that writes them (PagedKvCache / DeviceKv
+// tryEnsureRows, model/DeviceKv.cajeta:193-200). A dry pool is an error
+// that names the shortfall; the scheduler preempts before it gets here.
+int Engine::ensure_pages(int s, int64_t upto) {
+    if (upto > (int64_t)pages_per_seq * 64) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %lld of %d", (long long)upto, ctx);
+    std::vector<int32_t> &P = slot_pages[(size_t)s];
+    const size_t need = (size_t)((upto + 63) / 64);
+    if (need <= P.size()) return CJ_OK;
+    if (need - P.size() > free_pages.size())
+        return fail(CJ_ERR_CAPACITY, "kv pool exhausted: slot %d needs %zu more pages, %zu of %d free", s, need - P.size(),
+                    free_pages.size(), kv_pages);
+    const size_t j0 = P.size();
+    int32_t *mirror = pinned_pg + (size_t)s * pages_per_seq;
+    while (P.size() < need) {
+        mirror[P.size()] = free_pages.back();
+        P.push_back(free_pages.back());
+        free_pages.pop_back();
+    }
+    // the mirror's entries are not written again before the slot is reset,
+    // which drains the stream first: the copy may read them when it runs
+    CJ_HIP(hipMemcpyAsync(pgtab + (size_t)s * pages_per_seq + j0, mirror + j0, (need - j0) * 4, hipMemcpyHostToDevice,
+                          stream()));
+    return CJ_OK;
+}
+
+bool Engine::pages_fit(int s, int64_t upto) const {
+    if (upto > (int64_t)pages_per_seq * 64) return false;
+    const size_t need = (size_t)((upto + 63) / 64), have = slot_pages[(size_t)s].size();
+    return need <= have || need - have <= free_pages.size();
+}
+
+// The slot's pages back to the pool (the stream is drained first: work
+// queued for the slot may still read them).
+void Engine::release_pages(int s) {
+    std::vector<int32_t> &P = slot_pages[(size_t)s];
+    if (P.empty()) return;
+    (void)hipStreamSynchronize(stream());
+    for (size_t j = P.size(); j-- > 0;) free_pages.push_back(P[j]);
+    P.clear();
+}
+
 int Engine::reset(int s) {
     if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
     Seq &S = seqs[s];
     cj_step_state st{};
     CJ_HIP(hipStreamSynchronize(stream()));
+    release_pages(s);
     CJ_HIP(hipMemcpy(S.state, &st, sizeof st, hipMemcpyHostToDevice));
     S.pos = 0;
     S.fixed_until = 0;
@@ -1153,8 +1258,9 @@ int Engine::prefill(int s, const int32_t *toks, int n) {
     if (S.pos + n > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + n, ctx);
     for (int i = 0; i < n; i++)
         if (toks[i] < 0 || toks[i] >= vocab) return fail(CJ_ERR_ARG, "token %d outside the vocabulary", toks[i]);
-    if (n > 1 && rows_prefill && chunk > 1) return prefill_rows(s, toks, n);
     int rc;
+    if ((rc = ensure_pages(s, (int64_t)S.pos + n))) return rc;
+    if (n > 1 && rows_prefill && chunk > 1) return prefill_rows(s, toks, n);
     if (graphs && (rc = capture(s))) return rc;
     // through pinned staging: the copies are ordered on the stream and the
     // staging is not reused before the synchronize below
@@ -1184,6 +1290,7 @@ int Engine::decode(int s, int steps, int32_t *out) {
     if (steps <= 0) return CJ_OK;
     if (S.pos + steps > ctx) return fail(CJ_ERR_CAPACITY, "kv pool exhausted: position %d of %d", S.pos + steps, ctx);
     int rc;
+    if ((rc = ensure_pages(s, (int64_t)S.pos + steps))) return rc;
     if (graphs && (rc = capture(s))) return rc;
     hipEvent_t e0, e1;
     CJ_HIP(hipEventCreate(&e0));
@@ -1324,13 +1431,18 @@ int Engine::time_kind(int s, int kind, int reps, float *avg_us, std::string &ker
 // ------------------------------------------------------------ scheduler
 //
 // Continuous batching over the sequence slots (Scheduler.stepOnce,
-// sched/Scheduler.cajeta:414-605): each step admits waiting requests into
-// free slots (FIFO), feeds every running request's pending rows — a prompt
-// chunk of up to the chunk size, or the one newest position of a decoding
-// request, all decoding requests together as one batched step — consumes the
-// greedy token a finished prompt or decode row produced, checks stops per
-// token (stop tokens, then the budget), retires finished requests and admits
-// again into the freed slots. Cancel takes effect between steps.
+// sched/Scheduler.cajeta:414-605): each step admits requests into free
+// slots — preempted ones first, in preemption order, then waiting ones in
+// submission order (admitPhase, :1068-1150) — and feeds every running
+// request: a prompt chunk of up to the chunk size, or the newest position
+// of a decoding request (all of them as one batched step), or, for a sole
+// running greedy request, the pipelined step (pipeFor/stepPipelined,
+// :613-702). Each greedy token is consumed with the stop checks (stop
+// tokens, then the budget); finished requests retire and free their slot
+// and pages. A request whose next rows do not fit the page pool preempts
+// the youngest running request, itself if it is the youngest (:496-512);
+// a preempted request later resumes by recomputing its whole stream.
+// Cancel takes effect between steps.
 
 int Engine::submit(const int32_t *prompt, int n, int max_new, const int32_t *stops, int n_stops) {
     if (!prompt || n <= 0 || max_new <= 0) return fail(CJ_ERR_ARG, "submit: %d prompt tokens, max_new %d", n, max_new);
@@ -1343,6 +1455,7 @@ int Engine::submit(const int32_t *prompt, int n, int max_new, const int32_t *sto
     Request r;
     r.all.assign(prompt, prompt + n);
     r.prompt_len = n;
+    r.feed = n;
     r.max_new = max_new;
     // LlmEngine.defaultStops (LlmEngine.cajeta:458-474): the model's EOG set
     // unless the caller gave stop tokens (an empty list means none)
@@ -1352,26 +1465,72 @@ int Engine::submit(const int32_t *prompt, int n, int max_new, const int32_t *sto
     return (int)reqs.size() - 1;
 }
 
+// Scheduler.soleRunning (:364-377): the one running request, else -1.
+int Engine::sole_running() const {
+    int found = -1;
+    for (size_t i = 0; i < reqs.size(); i++)
+        if (reqs[i].state == Request::RUNNING) {
+            if (found >= 0) return -1;
+            found = (int)i;
+        }
+    return found;
+}
+
+// Scheduler.youngestRunning (:1263-1276): the running request admitted last.
+int Engine::youngest_running() const {
+    int best = -1, bs = -1;
+    for (size_t i = 0; i < reqs.size(); i++)
+        if (reqs[i].state == Request::RUNNING && reqs[i].stamp > bs) {
+            best = (int)i;
+            bs = reqs[i].stamp;
+        }
+    return best;
+}
+
 int Engine::admit() {
-    for (size_t i = 0; i < reqs.size(); i++) {
-        Request &r = reqs[i];
-        if (r.state != Request::WAITING) continue;
+    for (;;) {
+        int pick = -1, best_pre = 0x7fffffff;
+        for (size_t i = 0; i < reqs.size(); i++)
+            if (reqs[i].state == Request::PREEMPTED && reqs[i].pre_stamp < best_pre) {
+                pick = (int)i;
+                best_pre = reqs[i].pre_stamp;
+            }
+        const bool resume = pick >= 0;
+        if (pick < 0)
+            for (size_t i = 0; i < reqs.size(); i++)
+                if (reqs[i].state == Request::WAITING) { pick = (int)i; break; }
+        if (pick < 0) return CJ_OK;
         int slot = -1;
         for (int s = 0; s < max_seqs; s++)
             if (slot_req[(size_t)s] < 0) { slot = s; break; }
         if (slot < 0) return CJ_OK;
         int rc = reset(slot);
         if (rc) return rc;
-        slot_req[(size_t)slot] = (int)i;
+        Request &r = reqs[(size_t)pick];
+        // the whole stream plus one decode position (tryDeviceKvRows(slot, totalLen + 1))
+        const int64_t need = (int64_t)r.all.size() + 1;
+        if (!pages_fit(slot, need)) {
+            if (youngest_running() < 0)
+                return fail(CJ_ERR_CAPACITY,
+                            "scheduler: request %d needs %lld positions of device KV, more than the pool can hold with "
+                            "nothing else running (%d pages of 64)", pick, (long long)need, kv_pages);
+            return CJ_OK;
+        }
+        if ((rc = ensure_pages(slot, need))) return rc;
+        slot_req[(size_t)slot] = pick;
         r.slot = slot;
         r.cached = 0;
         r.state = Request::RUNNING;
+        r.stamp = ++stamp_n;
+        if (resume) resumed_n++;
     }
-    return CJ_OK;
 }
 
 void Engine::retire(Request &r, int finish) {
-    if (r.slot >= 0) slot_req[(size_t)r.slot] = -1;
+    if (r.slot >= 0) {
+        release_pages(r.slot);
+        slot_req[(size_t)r.slot] = -1;
+    }
     r.slot = -1;
     r.state = Request::DONE;
     r.finish = finish;
@@ -1388,22 +1547,175 @@ void Engine::consume(Request &r, int32_t tok) {
     else if (r.gen >= r.max_new || (int)r.all.size() > ctx) retire(r, Request::FINISH_BUDGET);
 }
 
+// Scheduler.preempt (:1291-1315): the request's pages go back to the pool,
+// its slot is freed, and it waits to resume by recomputing its stream (its
+// generated ids stay). A pipelined step in flight for it is awaited and its
+// token consumed first.
+int Engine::preempt(int i) {
+    Request &r = reqs[(size_t)i];
+    int rc;
+    if (pipe_in && pipe_req == i && (rc = finish_pipe())) return rc;
+    if (r.state != Request::RUNNING) return CJ_OK;
+    release_pages(r.slot);
+    slot_req[(size_t)r.slot] = -1;
+    r.slot = -1;
+    r.cached = 0;
+    r.feed = (int)r.all.size();
+    r.state = Request::PREEMPTED;
+    r.pre_stamp = ++stamp_n;
+    preempted_n++;
+    return CJ_OK;
+}
+
+// Scheduler.cancel (:288-315): false for an id never issued or already done.
+int Engine::cancel(int i) {
+    if (i < 0 || i >= (int)reqs.size()) return 0;
+    Request &r = reqs[(size_t)i];
+    if (r.state == Request::DONE) return 0;
+    if (pipe_in && pipe_req == i && drain_pipe()) return CJ_ERR_HIP;
+    retire(r, Request::FINISH_CANCEL);
+    return 1;
+}
+
+// One decode step of slot s queued (its graph), its event recorded in
+// pipe_ev[e]: the step consumes the id at the slot's position (written on
+// the device by the previous step's pick) and its pick writes the next one.
+int Engine::queue_pipe_step(int s, int e) {
+    Seq &S = seqs[(size_t)s];
+    int rc;
+    if ((rc = ensure_pages(s, (int64_t)S.pos + 1))) return rc;
+    if ((rc = run_step(s))) return rc;
+    CJ_HIP(hipEventRecord(pipe_ev[e], stream()));
+    pipe_pos[e] = S.pos;
+    S.pos += 1;
+    return CJ_OK;
+}
+
+// CausalLM.awaitStep (model/CausalLM.cajeta:1245-1256): wait for the oldest
+// in-flight step alone (a later queued one keeps running) and read its token
+// from the pinned mirror the pick wrote.
+int Engine::await_pipe(int32_t *tok) {
+    CJ_HIP(hipEventSynchronize(pipe_ev[pipe_out]));
+    const Request &r = reqs[(size_t)pipe_req];
+    *tok = __atomic_load_n(host_tok + (size_t)r.slot * (ctx + 2) + pipe_pos[pipe_out] + 1, __ATOMIC_ACQUIRE);
+    if (*tok < 0 || *tok >= vocab) return fail(CJ_ERR_STATE, "pipelined step: token %d read back", *tok);
+    return CJ_OK;
+}
+
+// Scheduler.pipeFor (:628-638): a sole running greedy request with one
+// position to feed whose id the device already holds. (MoE models keep the
+// synchronous step, which checks the router's status after every token.)
+bool Engine::pipe_for(int i, const Request &r, int n) {
+    if (pipe_in) return pipe_req == i;
+    if (n != 1 || !graphs || n_experts > 0) return false;
+    if (r.cached < r.feed) return false;
+    return sole_running() == i;
+}
+
+// Scheduler.stepPipelined (:640-676). The first call seeds: the step is
+// queued and no token is read. Each later call queues the speculative next
+// step (unless this token must be the last by budget or context), then
+// awaits the in-flight one and consumes its token; a finish leaves the
+// speculative step queued, and retiring the request drains it.
+int Engine::step_pipelined(int i, Request &r) {
+    int rc;
+    if (!pipe_in) {
+        if (graphs && (rc = capture(r.slot))) return rc;
+        if ((rc = queue_pipe_step(r.slot, 0))) return rc;
+        pipe_in = true;
+        pipe_out = 0;
+        pipe_req = i;
+        r.cached += 1;
+        return CJ_OK;
+    }
+    Seq &S = seqs[(size_t)r.slot];
+    const int in_e = pipe_out, out_e = 1 - in_e;
+    const bool spec = r.gen + 1 < r.max_new && S.pos < ctx && pages_fit(r.slot, (int64_t)S.pos + 1);
+    if (spec && (rc = queue_pipe_step(r.slot, out_e))) return rc;
+    int32_t tok = 0;
+    if ((rc = await_pipe(&tok))) return rc;
+    consume(r, tok);
+    if (r.state != Request::RUNNING) {   // retire released the slot, which drained the stream
+        pipe_in = false;
+        pipe_req = -1;
+        return CJ_OK;
+    }
+    if (spec) {
+        pipe_out = out_e;
+        r.cached += 1;
+    } else {
+        pipe_in = false;
+        pipe_req = -1;
+    }
+    return CJ_OK;
+}
+
+// Scheduler.finishPipe (:678-692): await the pending step, consume its
+// token, and take the plain steps from here.
+int Engine::finish_pipe() {
+    if (!pipe_in) return CJ_OK;
+    const int i = pipe_req;
+    int32_t tok = 0;
+    const int rc = await_pipe(&tok);
+    pipe_in = false;
+    pipe_req = -1;
+    if (rc) return rc;
+    Request &r = reqs[(size_t)i];
+    if (r.state == Request::RUNNING) consume(r, tok);
+    return CJ_OK;
+}
+
+// Scheduler.drainPipe (:694-702): let the pending step end (its token is
+// not consumed) and forget the pipeline.
+int Engine::drain_pipe() {
+    if (!pipe_in) return CJ_OK;
+    pipe_in = false;
+    pipe_req = -1;
+    CJ_HIP(hipEventSynchronize(pipe_ev[pipe_out]));
+    return CJ_OK;
+}
+
 int Engine::step_once() {
     sched_steps++;
     int rc;
     if ((rc = admit())) return rc;
+    // a pipeline serves one sole running request; the moment it is not sole,
+    // its pending step is finished here and the plain steps take over
+    if (pipe_in && sole_running() != pipe_req && (rc = finish_pipe())) return rc;
     const int cap = rows_prefill && chunk > 1 ? chunk : 512;   // prompt rows a request feeds per step
     std::vector<int> batch;                             // requests decoding one position
     for (size_t i = 0; i < reqs.size(); i++) {
         Request &r = reqs[i];
         if (r.state != Request::RUNNING) continue;
+        // a pipelined step in flight has consumed the newest position already
         const int n = (int)r.all.size() - r.cached;
-        if (n == 1 && r.cached > 0) { batch.push_back((int)i); continue; }
         const int m = std::min(n, cap);
+        // per-item headroom: preempt younger requests until this item fits;
+        // the youngest yields itself instead
+        while (m > 0 && !pages_fit(r.slot, (int64_t)r.cached + m)) {
+            const int v = youngest_running();
+            if (v < 0) return fail(CJ_ERR_CAPACITY, "scheduler: no preemptable sequence");
+            if ((rc = preempt(v))) return rc;
+            batch.erase(std::remove(batch.begin(), batch.end(), v), batch.end());
+            if (v == (int)i) break;
+        }
+        if (r.state != Request::RUNNING) continue;
+        if (pipe_for((int)i, r, n)) {
+            if ((rc = step_pipelined((int)i, r))) return rc;
+            continue;
+        }
+        if (pipe_in && (rc = finish_pipe())) return rc;
+        if (r.state != Request::RUNNING) continue;
+        // one position whose id the device holds (the pick that produced it
+        // wrote it into the slot's history): a row of the batched step
+        if (n == 1 && r.cached >= r.feed) {
+            batch.push_back((int)i);
+            continue;
+        }
         if ((rc = prefill(r.slot, r.all.data() + r.cached, m))) return rc;
         r.cached += m;
         if (r.cached == (int)r.all.size()) {
-            // the prompt's last row was consumed: its argmax is the first token
+            // the stream's last row was consumed: its argmax is the next token
             int32_t tok = 0;
             CJ_HIP(hipMemcpy(&tok, seqs[(size_t)r.slot].tokens + seqs[(size_t)r.slot].pos, 4, hipMemcpyDeviceToHost));
             consume(r, tok);
@@ -1436,12 +1748,16 @@ Engine *eng_of(int64_t h) { return (Engine *)(uintptr_t)h; }
 extern "C" {
 
 int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs) {
+    return cj_engine_load_pool(path, ctx, max_seqs, 0);
+}
+
+int64_t cj_engine_load_pool(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages) {
     if (!cj::ready()) return cj::fail(CJ_ERR_STATE, "cj_init has not run"), 0;
     if (!path) return cj::fail(CJ_ERR_ARG, "cj_engine_load: null path"), 0;
     auto *e = new Engine();
     int rc;
     try {
-        rc = e->load((const char *)path, ctx, max_seqs);
+        rc = e->load((const char *)path, ctx, max_seqs, kv_pages);
     } catch (const std::exception &x) {   // nothing may unwind through the C-ABI
         rc = cj::fail(CJ_ERR_IO, "model: %s", x.what());
     }
@@ -1508,11 +1824,7 @@ int32_t cj_engine_cancel(int64_t h, int32_t id) {
     Engine *e = eng_of(h);
     if (!e) return cj::fail(CJ_ERR_STATE, "null engine");
     // Scheduler.cancel (:288-315): false for an id never issued or already done
-    if (id < 0 || id >= (int)e->reqs.size()) return 0;
-    cj::Request &r = e->reqs[(size_t)id];
-    if (r.state == cj::Request::DONE) return 0;
-    e->retire(r, cj::Request::FINISH_CANCEL);
-    return 1;
+    return e->cancel(id);
 }
 
 int32_t cj_engine_set_eog(int64_t h, const int32_t *ids, int32_t n) {

@@ -60,7 +60,6 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"q40F32WaveMatVecKernel", "cj_gemv_q40b_r4"},
         {"mxfp4MatVecKernel", "cj_gemv_mxfp4"},
         {"mxfp4MatVecKernelCoopQ8", "cj_gemv_mxq8_s_k3_r4"},
-        {"mxfp4QuantActKernel", "cj_gemv_mxq8_s_k3_r4"},   // the quant is that kernel's prologue
         {"q8kPackKernel", "cj_pack"},
         {"q8kPack32Kernel", "cj_pack"},
         {"rmsnormPackRowF32", "cj_pack"},
@@ -81,10 +80,8 @@ const std::unordered_map<std::string, std::string> &name_map() {
         {"embedRowQ6kKernel", "cj_embed"},
         {"embedRowQ80Kernel", "cj_embed"},
         {"gatherRowsF32Kernel", "cj_embed"},
-        {"routerTopKKernel", "cj_moe_route"},
+        {"routerTopKKernel", "cj_router_topk"},
         {"q4kQ8WaveMatVecColsKernel", "cj_gemm_sk_q4k_n1"},
-        {"q80Q8X8RowsKernel", "cj_gemm_sk_q80_n1"},
-        {"q4kQ8X8RowsKernel", "cj_gemm_sk_q4k_n1"},
     };
     return m;
 }
@@ -417,7 +414,7 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_norm_pack", "cj_norm_pack_rows", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
-        "cj_attn_merge", "cj_attn_merge_w", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route",
+        "cj_attn_merge", "cj_attn_merge_w", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
         "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_c16",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
@@ -858,6 +855,12 @@ int32_t cj_embed_row_slot(int64_t out, int64_t table, int32_t type, int64_t hidd
 int32_t cj_argmax_row(int64_t tok, int32_t row, int64_t v, int64_t n) {
     if (n <= 0 || row < 0 || !in_buffer(dptr(tok + 4 * row), 4) || !in_buffer(dptr(v), n * 4))
         return fail(CJ_ERR_ARG, "cj_argmax_row: n %lld row %d", (long long)n, row);
+    // its scratch may grow (a synchronize, an allocation and a memset),
+    // none of which a stream capture may record
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    CJ_HIP(hipStreamIsCapturing(g.stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(CJ_ERR_STATE, "cj_argmax_row: the stream is capturing a graph; cj_argmax_row_noalloc allocates nothing");
     static void *scratch = nullptr;
     static int64_t scratch_groups = 0;
     const int64_t groups = (n + 1023) / 1024;
@@ -912,6 +915,47 @@ int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t
     a.type = type; a.prepared = prepared;
     const int64_t grid = std::min<int64_t>((a.elems + 255) / 256, 16384);
     return launch("cj_dequant", (uint32_t)grid, 256, 0, a);
+}
+
+int32_t cj_router_topk(int64_t sel, int64_t w, int64_t logits, int64_t w_router, int64_t x, int64_t counter,
+                       int32_t experts, int32_t cols, int32_t used, int32_t norm_topk, float w_scale) {
+    if (experts <= 0 || experts > 4096 || cols <= 0 || used <= 0 || used > experts ||
+        !in_buffer(dptr(sel), (int64_t)used * 4) || !in_buffer(dptr(w), (int64_t)used * 4) ||
+        !in_buffer(dptr(logits), (int64_t)experts * 4) || !in_buffer(dptr(w_router), (int64_t)experts * cols * 4) ||
+        !in_buffer(dptr(x), (int64_t)cols * 4) || !in_buffer(dptr(counter), 4))
+        return fail(CJ_ERR_ARG, "cj_router_topk: experts %d cols %d used %d", experts, cols, used);
+    cj_router_topk_args a{};
+    a.sel = (int32_t *)dptr(sel); a.w = (float *)dptr(w); a.logits = (float *)dptr(logits);
+    a.w_router = (const float *)dptr(w_router); a.x = (const float *)dptr(x); a.counter = (int32_t *)dptr(counter);
+    a.experts = experts; a.cols = cols; a.used = used; a.norm_topk = norm_topk ? 1 : 0; a.w_scale = w_scale;
+    return launch("cj_router_topk", (uint32_t)experts, 256, 0, a);
+}
+
+int32_t cj_attn_scores(int64_t scores, int64_t q, int64_t kcache, int64_t pgtab, int32_t pg_base, int32_t n_q,
+                       int32_t n_kv, int32_t head_dim, int32_t count, int32_t from, float scale) {
+    if (n_kv <= 0 || n_q <= 0 || n_q % n_kv || (head_dim != 64 && head_dim != 128) || count <= 0 || from < 0)
+        return fail(CJ_ERR_ARG, "cj_attn_scores: heads %d/%d hd %d count %d", n_q, n_kv, head_dim, count);
+    const int64_t pages = ((int64_t)from + count + 63) / 64;
+    if (!in_buffer(dptr(pgtab + 4 * (int64_t)pg_base), pages * 4) || !in_buffer(dptr(q), (int64_t)n_q * head_dim * 4) ||
+        !in_buffer(dptr(scores), (int64_t)n_q * count * 4))
+        return fail(CJ_ERR_ARG, "cj_attn_scores: a buffer is smaller than the shapes need");
+    std::vector<int32_t> tab((size_t)pages);
+    CJ_HIP(hipMemcpyAsync(tab.data(), dptr(pgtab + 4 * (int64_t)pg_base), (size_t)pages * 4, hipMemcpyDeviceToHost, g.stream));
+    CJ_HIP(hipStreamSynchronize(g.stream));
+    int32_t maxpg = 0;
+    for (int32_t p : tab) {
+        if (p < 0) return fail(CJ_ERR_ARG, "cj_attn_scores: negative page in the table");
+        maxpg = std::max(maxpg, p);
+    }
+    if (!in_buffer(dptr(kcache), (((int64_t)maxpg + 1) * n_kv * 64) * head_dim * 2))
+        return fail(CJ_ERR_ARG, "cj_attn_scores: page %d outside the K plane", maxpg);
+    cj_attn_args a{};
+    a.part = (float *)dptr(scores); a.q = (const float *)dptr(q); a.kc = (const uint16_t *)dptr(kcache);
+    a.pgtab = (const int32_t *)dptr(pgtab); a.n_q = n_q; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = pg_base;
+    a.pg_n = (int32_t)pages; a.count = count; a.from = from; a.scale = scale; a.splits = count;   // the row stride
+    char name[64];
+    snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
+    return launch2(name, (uint32_t)((count + 255) / 256), (uint32_t)n_q, 256, 0, a);
 }
 
 int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts, int32_t n_used, int32_t norm_topk,

@@ -26,6 +26,8 @@ class EngineOptions:
         self.cpuThreads = 0      # the CPU worker count the attention split rule follows (0: 512)
         self.graphs = True       # replay the captured decode step (False: eager launches)
         self.prefillChunk = 512  # rows a prefill chunk (CausalLM.CHUNK_MAX); 0: one decode step a position
+        self.kvBlocks = 0        # K/V pool pages of 64 positions shared by the slots (0: every slot at full context;
+                                 # CausalLM's numBlocks): a smaller pool preempts under pressure
 
 
 class SampleParams:
@@ -45,7 +47,7 @@ class SampleParams:
 
 class Request:
     """A request's state as the scheduler left it (sched/Request.cajeta)."""
-    WAITING, RUNNING, DONE = 0, 1, 2
+    WAITING, RUNNING, PREEMPTED, DONE = 0, 1, 2, 3
     FINISH_NONE, FINISH_BUDGET, FINISH_EOS, FINISH_CANCEL = 0, 1, 2, 4
 
     def __init__(self, rid, tokens, state, reason):
@@ -110,7 +112,8 @@ class LlmEngine:
             else:
                 raise LlmException("engine: device '%s' is not served by the MI355X backend" % opts.device)
         native.init(dev)
-        h = lib().cj_engine_load(opts.model.encode(), int(opts.ctx), int(opts.maxSeqs))
+        h = lib().cj_engine_load_pool(opts.model.encode(), int(opts.ctx), int(opts.maxSeqs),
+                                      int(getattr(opts, "kvBlocks", 0)))
         handle(h, "LlmEngine.load(%s)" % opts.model)
         if not getattr(opts, "graphs", True):
             check(lib().cj_engine_set_graphs(h, 0), "cj_engine_set_graphs")

@@ -242,12 +242,39 @@ int32_t cj_dequant(int64_t out, int64_t raw, int32_t type, int64_t rows, int64_t
 int32_t cj_moe_route(int64_t sel, int64_t weights, int64_t logits, int32_t rows, int32_t n_experts,
                      int32_t n_used, int32_t norm_topk, float w_scale, int64_t status);
 
+/* The router mat-vec and its top-k in one launch: logits[e] = w_router[e]·x
+ * (experts rows of cols f32), then sel[used] and w[used] as the reference's
+ * device router selects them (softmax over the experts, top-k by
+ * probability, ties to the lower index, renormalised when norm_topk, then
+ * ×w_scale unless it is 0 or 1). counter: one int32, zero before the call
+ * and left zero. Replaces QuantKernel.routerTopKLaunchNoSync(sel, w, logits,
+ * wRouter, x, counter, experts, cols, used, normTopk, wScale)
+ * (io/QuantKernel.cajeta:40701-40709; routerTopKKernel :39850-39960). */
+int32_t cj_router_topk(int64_t sel, int64_t w, int64_t logits, int64_t w_router, int64_t x, int64_t counter,
+                       int32_t experts, int32_t cols, int32_t used, int32_t norm_topk, float w_scale);
+
+/* The two-pass decode attention's score pass alone: scores[h][t] =
+ * (q_h · K_t)·scale for t < count over positions [from, from + count) of the
+ * paged fp16 K plane, kv head h / (n_q/n_kv). Replaces attnScoreKernel's
+ * launch (model/AttnKernel.cajeta:397-425, the first half of
+ * attendDecodeLaunchNoSync's two-pass form). */
+int32_t cj_attn_scores(int64_t scores, int64_t q, int64_t kcache, int64_t pgtab, int32_t pg_base, int32_t n_q,
+                       int32_t n_kv, int32_t head_dim, int32_t count, int32_t from, float scale);
+
 /* ------------------------------------------------------------ engine */
 
 /* The LlmEngine surface (LlmEngine.cajeta:165-546) over a GGUF model:
  * path "mem:<name>" loads an image made by cj_synth_gguf. ctx is the KV
  * capacity per sequence, max_seqs the sequence slots. */
 int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs);
+/* cj_engine_load with the K/V pool's size: kv_pages pages of 64 positions
+ * shared by every slot (0: every slot at its full context, what
+ * cj_engine_load gives). A smaller pool holds more slots than it could at
+ * full context; the scheduler preempts the youngest running request when a
+ * request's next rows do not fit, and resumes it later by recomputing its
+ * stream. The CausalLM(cfg, maxSeq, maxSeqs, numBlocks) constructor's
+ * numBlocks (model/CausalLM.cajeta:64-94). */
+int64_t cj_engine_load_pool(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages);
 int32_t cj_engine_close(int64_t eng);
 /* Up to 14 values: n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab,
  * ctx, n_experts, n_used, weight type, head type, expert ffn, and the CPU
@@ -267,16 +294,22 @@ int32_t cj_engine_submit_stops(int64_t eng, const int32_t *prompt, int32_t n, in
  * ONE scheduler step — admit waiting requests into free sequence slots
  * (FIFO), feed each running request's pending rows (a prompt chunk of up to
  * the prefill chunk size, or one decode position; every decoding request
- * together as one batched step), append each produced greedy token, check
- * its stops (stop token → FINISH_EOS, then the budget → FINISH_BUDGET),
- * retire finished requests and admit again. Returns 1 while a request is
- * unfinished, 0 when all are done, < 0 on error. */
+ * together as one batched step; a sole running greedy request through the
+ * pipelined step, Scheduler.pipeFor/stepPipelined :613-702: its next step
+ * is queued before the previous one's token is read, so the first such call
+ * emits no token and a finish drains one queued step), append each produced
+ * greedy token, check its stops (stop token → FINISH_EOS, then the budget →
+ * FINISH_BUDGET), retire finished requests and admit again (preempted ones
+ * first). A request whose next rows do not fit the K/V pool preempts the
+ * youngest running request (itself, if youngest). Returns 1 while a request
+ * is unfinished, 0 when all are done, < 0 on error. */
 int32_t cj_engine_step_once(int64_t eng);
 /* LlmEngine.runAll (:500) → Scheduler.runAll (:1005): stepOnce until every
  * request is done; CJ_ERR_STATE ("not done after N steps") past max_steps. */
 int32_t cj_engine_run_all(int64_t eng, int32_t max_steps);
 /* LlmEngine.request (:508): writes up to cap generated ids, *state
- * (0 waiting, 1 running, 2 done) and *finish (Request.FINISH_*: 0 none,
+ * (0 waiting, 1 running, 2 preempted, 3 done: sched/Request.cajeta:9-13)
+ * and *finish (Request.FINISH_*: 0 none,
  * 1 budget, 2 end-of-generation token, 4 cancelled; sched/Request.cajeta:18-23).
  * Returns the generated count. */
 int32_t cj_engine_request(int64_t eng, int32_t id, int32_t *tokens, int32_t cap, int32_t *state, int32_t *finish);

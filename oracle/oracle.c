@@ -509,31 +509,56 @@ void or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, 
     }
 }
 
-/* exp(x) in f32, written out so that the kernels compute the same bits:
- * n = rint(x·log2 e); r = x − n·ln2 (Cody–Waite, two fma steps, ln2_hi with
- * trailing zeros); e^r by the degree-7 Taylor polynomial in Horner form with
- * fma (|r| ≤ ln2/2, truncation < 4e-9 relative); then ·2^n in two exact
- * power-of-two steps. Every step is an IEEE-754 correctly rounded operation,
- * so any conforming implementation gives these bits. The reference's
- * Cajeta stdlib Math.exp is not available; ULP parity with it is unpinned. */
+/* exp(x) in f32 as the reference CPU backend computes it. Its Math.exp is
+ * glibc's expf: the reference's recorded CPU softmax outputs
+ * (attnScoreKernel h32kv4d128c256, tests/golden/wave) are glibc expf's bits in
+ * all 8192 values. glibc's expf is ARM optimized-routines' algorithm
+ * (math/expf.c, EXP2F_TABLE_BITS 5): with z = x·32/ln2 in f64, k = round(z) by
+ * adding 1.5·2^52 and r = z − k, both as fused multiply-adds of x (as the
+ * FMA build of glibc computes them); 2^(k/32) from a table of 2^(i/32)
+ * rounded to f64 with k's integer part added to the exponent bits; 2^(r/32)
+ * as C0·r³ + C1·r² + C2·r + 1 in f64 by fused multiply-adds; rounded once to
+ * f32. The table holds 2^(i/32) correctly rounded to f64 less i·2^47 in the
+ * bit pattern. tests/test_oracle.py checks the table against 2^(i/32) and the
+ * function against the C library's expf. */
+static const uint64_t OR_EXP2_TAB[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
 float or_expf(float x) {
-    if (x != x) return x;
-    if (x < -104.0f) return 0.0f;
-    if (x > 88.72283935546875f) return INFINITY;
-    const float n = rintf(x * 1.44269502162933349609375f);
-    float r = fmaf(n, -0.693145751953125f, x);
-    r = fmaf(n, -1.428606765330187045e-06f, r);
-    float p = 1.98412698412698413e-04f;
-    p = fmaf(p, r, 1.38888888888888889e-03f);
-    p = fmaf(p, r, 8.33333333333333333e-03f);
-    p = fmaf(p, r, 4.16666666666666667e-02f);
-    p = fmaf(p, r, 1.66666666666666667e-01f);
-    p = fmaf(p, r, 0.5f);
-    p = fmaf(p, r, 1.0f);
-    p = fmaf(p, r, 1.0f);
-    const int ni = (int)n, n1 = ni / 2, n2 = ni - n1;
-    return p * bits_f((uint32_t)(n1 + 127) << 23) * bits_f((uint32_t)(n2 + 127) << 23);
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return INFINITY;
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32 * 32), c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32),
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd = kd - shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    const uint64_t sb = OR_EXP2_TAB[ki & 31] + (ki << 47);
+    double s;
+    memcpy(&s, &sb, 8);
+#if OR_PLANT == 21
+    const double z = c1, r2 = r * r;   /* planted: the cubic term dropped */
+#else
+    const double z = fma(c0, r, c1), r2 = r * r;
+#endif
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
 }
+
+/* The 2^(i/32) table of or_expf, for the check against its definition. */
+void or_exp2_table(uint64_t *out) { memcpy(out, OR_EXP2_TAB, sizeof OR_EXP2_TAB); }
 
 /* SwiGLU, exp form (Prim.gluF32/gluOne, L/model/Prim.cajeta:160-196):
  * silu(g) = g / (1 + exp(-g)). */
@@ -716,6 +741,123 @@ int or_qk_prep128(float *q, float *k, const float *qw, const float *kw, const fl
     return 0;
 }
 
+/* The generic qkPrepKernel (L/model/AttnKernel.cajeta:127-206), the CPU
+ * backend's prep where qkPrepCpuKernel (head size 128 only) does not serve:
+ * a workgroup of 128 lanes a head, lane l summing x[l]², x[l+128]², ... in
+ * order; Workgroup.reduce folds each 32-lane wave by the butterfly from the
+ * adjacent lane up (lane distance 1, 2, 4, 8, 16) and adds the four wave
+ * sums in wave order — the order cpuHeadNorm writes out for head size 128
+ * (:233-268) and the one the reference's recorded h6kv2d64 rows fix (the
+ * stride-halving tree gives other bits for k head 0); scale =
+ * 1/sqrt(tot/hd + eps); x·scale·w (form 1: w + 1); then RoPE. At head size
+ * 128 the CPU kernel's order applies (or_qk_prep128). */
+int or_qk_prep(float *q, float *k, const float *qw, const float *kw, const float *inv, int nh, int nkv, int hd,
+               int norm, float eps, int form, int pos) {
+    if (hd == 128) return or_qk_prep128(q, k, qw, kw, inv, nh, nkv, norm, eps, form, pos);
+    if (hd > 256 || hd % 2) return -1;
+    if (norm) {
+        for (int h = 0; h < nh + nkv; h++) {
+            float *x = h < nh ? q + (int64_t)h * hd : k + (int64_t)(h - nh) * hd;
+            const float *w = h < nh ? qw : kw;
+            float red[128];
+            for (int l = 0; l < 128; l++) {
+                float ss = 0.0f;
+                for (int i = l; i < hd; i += 128) ss = ss + x[i] * x[i];
+                red[l] = ss;
+            }
+            float tot = 0.0f;
+            for (int wv = 0; wv < 4; wv++) {
+                float *v = red + 32 * wv;
+#if OR_PLANT == 19
+                for (int l = 1; l < 32; l++) v[0] = v[0] + v[l];   /* planted: a wave's lanes summed in order */
+#else
+                for (int d = 1; d < 32; d <<= 1)
+                    for (int l = 0; l < 32; l += 2 * d) v[l] = v[l] + v[l + d];
+#endif
+                tot = tot + v[0];
+            }
+            float scale = 1.0f / sqrtf(tot / (float)hd + eps);
+            for (int j = 0; j < hd; j++) {
+                float wi = form == 1 ? 1.0f + w[j] : w[j];
+                x[j] = x[j] * scale * wi;
+            }
+        }
+    }
+    or_rope(q, nh, hd, pos, inv);
+    or_rope(k, nkv, hd, pos, inv);
+    return 0;
+}
+
+/* routerTopKKernel (L/io/QuantKernel.cajeta:39850-39960; launch :40701-40709)
+ * on the CPU backend: block e's 256 lanes each sum w[e][j]·x[j] for j = lane,
+ * lane+256, ... (each product rounded, then added), the lanes folded by the
+ * stride-halving tree (128, ..., 1) — the order the reference's recorded
+ * e128h2048k8 logits fix; then the last block's first wave of 32 lanes: the
+ * max, each lane's sum of exp(logit − max) over its experts lane, lane+32,
+ * ... in order, the 32 sums by the butterfly; `used` picks, each the largest
+ * probability below the previous pick (equal probability: the next index
+ * up), w = p/sum; the renormalisation by the ordered sum of w clamped at
+ * 2^-14 (normTopk), then ×wScale unless it is 0 or 1. */
+void or_router_topk(const float *w_router, const float *x, int experts, int cols, int used, int norm_topk,
+                    float w_scale, float *logits, int32_t *sel, float *w) {
+    for (int e = 0; e < experts; e++) {
+        float red[256];
+        for (int l = 0; l < 256; l++) {
+            float acc = 0.0f;
+            for (int j = l; j < cols; j += 256) acc = acc + w_router[(int64_t)e * cols + j] * x[j];
+            red[l] = acc;
+        }
+#if OR_PLANT == 20
+        for (int l = 1; l < 256; l++) red[0] = red[0] + red[l];   /* planted: the lanes summed in order */
+#else
+        for (int r = 128; r > 0; r >>= 1)
+            for (int l = 0; l < r; l++) red[l] = red[l] + red[l + r];
+#endif
+        logits[e] = red[0];
+    }
+    float mx = -3.4028234663852886e38f;
+    for (int e = 0; e < experts; e++) if (logits[e] > mx) mx = logits[e];
+    float ls[32];
+    for (int l = 0; l < 32; l++) {
+        float s = 0.0f;
+        for (int e = l; e < experts; e += 32) s = s + or_expf(logits[e] - mx);
+        ls[l] = s;
+    }
+    for (int m = 16; m > 0; m >>= 1) {
+        float nx[32];
+        for (int i = 0; i < 32; i++) nx[i] = ls[i] + ls[i ^ m];
+        memcpy(ls, nx, sizeof nx);
+    }
+    const float sum = ls[0];
+    float vlast = 3.4028234663852886e38f;
+    int ilast = experts;
+    for (int k = 0; k < used; k++) {
+        float vk = -1.0f;
+        int ik = experts;
+        for (int e = 0; e < experts; e++) {
+            const float p = or_expf(logits[e] - mx);
+            const int ok = p < vlast || (p == vlast && e > ilast);
+#if OR_PLANT == 18
+            if (ok && (p > vk || (p == vk && e > ik))) { vk = p; ik = e; }   /* planted: ties to the higher index */
+#else
+            if (ok && (p > vk || (p == vk && e < ik))) { vk = p; ik = e; }
+#endif
+        }
+        sel[k] = ik;
+        w[k] = vk / sum;
+        vlast = vk;
+        ilast = ik;
+    }
+    if (norm_topk) {
+        float ws = 0.0f;
+        for (int k = 0; k < used; k++) ws = ws + w[k];
+        if (ws < 0.00006103515625f) ws = 0.00006103515625f;
+        for (int k = 0; k < used; k++) w[k] = w[k] / ws;
+    }
+    if (w_scale != 0.0f && w_scale != 1.0f)
+        for (int k = 0; k < used; k++) w[k] = w[k] * w_scale;
+}
+
 /* AttnKernel.cpuDecodeSplits (L/model/AttnKernel.cajeta:4879-4889). */
 int or_cpu_decode_splits(int count, int rows, int nkv, int workers) {
     int w = workers < 1 ? 1 : workers, rk = rows * nkv < 1 ? 1 : rows * nkv;
@@ -793,6 +935,41 @@ void or_attn_merge(const float *part, int nh, int splits, int hd, float *out) {
     }
 }
 
+/* attnScoreKernel's score (L/model/AttnKernel.cajeta:397-425): lane i of 32
+ * sums q[d]·k[d] over d = i, i+32, ... in order; the 32 lane sums fold as the
+ * butterfly (lane distance 16, 8, 4, 2, 1 — Wave.reduceSumF32; pinned by the
+ * reference's recorded h32kv4d128c256 row); × scale. */
+static float score32(const float *qh, const void *kp, int f32, int64_t ko, int hd, float scale) {
+    float ls[32];
+    for (int i = 0; i < 32; i++) {
+        float s = 0.0f;
+        for (int d = i; d < hd; d += 32) s = s + qh[d] * kv_at(kp, f32, ko + d);
+        ls[i] = s;
+    }
+    for (int m = 16; m > 0; m >>= 1) {
+        float nx[32];
+        for (int i = 0; i < 32; i++) nx[i] = ls[i] + ls[i ^ m];
+        memcpy(ls, nx, sizeof nx);
+    }
+    return ls[0] * scale;
+}
+
+void or_attn_scores(const float *q, const void *kp, int f32, int nh, int nkv, int hd, int count, float scale,
+                    int softmax, float *scores) {
+    const int group = nh / nkv;
+    const int64_t kvdim = (int64_t)nkv * hd;
+    for (int h = 0; h < nh; h++) {
+        float *sc = scores + (int64_t)h * count;
+        for (int t = 0; t < count; t++) sc[t] = score32(q + (int64_t)h * hd, kp, f32, (int64_t)t * kvdim + (h / group) * hd, hd, scale);
+        if (!softmax) continue;
+        /* attnCombineKernel passes 1-2 (:441-486): the max (exact in any
+         * order), then exp(s − max) in place */
+        float mx = -3.0e38f;
+        for (int t = 0; t < count; t++) if (sc[t] > mx) mx = sc[t];
+        for (int t = 0; t < count; t++) sc[t] = or_expf(sc[t] - mx);
+    }
+}
+
 void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, int nkv, int hd,
                int count, int splits, float scale, int mode, float *out) {
     int64_t kvdim = (int64_t)nkv * hd;
@@ -830,21 +1007,7 @@ void or_attend(const float *q, const void *kp, const void *vp, int f32, int nh, 
         float *sc = (float *)malloc(sizeof(float) * (size_t)count);
         for (int h = 0; h < nh; h++) {
             int kvh = h / group;
-            const float *qh = q + (int64_t)h * hd;
-            for (int t = 0; t < count; t++) {
-                float ls[32];
-                for (int i = 0; i < 32; i++) {
-                    float s = 0.0f;
-                    for (int d = i; d < hd; d += 32) s = s + qh[d] * kv_at(kp, f32, (int64_t)t * kvdim + kvh * hd + d);
-                    ls[i] = s;
-                }
-                for (int m = 16; m > 0; m >>= 1) {
-                    float nx[32];
-                    for (int i = 0; i < 32; i++) nx[i] = ls[i] + ls[i ^ m];
-                    memcpy(ls, nx, sizeof nx);
-                }
-                sc[t] = ls[0] * scale;
-            }
+            for (int t = 0; t < count; t++) sc[t] = score32(q + (int64_t)h * hd, kp, f32, (int64_t)t * kvdim + kvh * hd, hd, scale);
             float mx = -3.0e38f;
             for (int t = 0; t < count; t++) if (sc[t] > mx) mx = sc[t];
             float red[128];

@@ -19,13 +19,20 @@
  *     argmax, MoE route, split count, q/k row permutation: closed forms,
  *     invariants and float64 brute force on small inputs; the whole decode
  *     step against a float64 forward of the reference's toy GGUF.
- *   - or_expf: within 2 ulp of exp over its range (a written-out exp shared
- *     with the kernels, so both sides give the same bits).
- *   - parity unpinned: the ULPs of the Cajeta stdlib's exp/sin/cos/pow (this
- *     file uses or_expf and glibc's sinf/cosf/powf), the stdlib's reduction
- *     trees beyond what the reference's own code fixes, FMA contraction by
- *     the Cajeta compiler, and end-to-end logits of the real reference binary
- *     (the cajeta toolchain is absent, so end-to-end is the restatement).
+ *   - or_expf: the reference CPU backend's Math.exp is glibc's expf (its
+ *     recorded softmax outputs are glibc expf's bits); or_expf restates that
+ *     algorithm and equals the C library's expf (checked on a sample here and
+ *     over every f32 input when it was written), and the kernels compute the
+ *     same steps.
+ *   - the reference's recorded CPU-backend outputs (tests/golden/wave):
+ *     two-pass scores + softmax exps, QK-norm + RoPE at head sizes 128 and 64,
+ *     the split merge + pack, the router mat-vec + top-k, bit for bit (the
+ *     router's last pick weights to the ulp that exp's rounding leaves).
+ *   - parity unpinned: the stdlib's reduction trees beyond what the
+ *     reference's own code and recorded rows fix, FMA contraction by the
+ *     Cajeta compiler elsewhere, and end-to-end logits of the real reference
+ *     binary (the cajeta toolchain is absent, so end-to-end is the
+ *     restatement).
  */
 #ifndef CJ_ORACLE_H
 #define CJ_ORACLE_H
@@ -63,6 +70,22 @@ int or_matvec_mxfp4_q8(const uint8_t *w, int64_t rows, int64_t cols, const float
 void  or_rmsnorm(const float *x, const float *w, int64_t n, float eps, int form, float *out);
 /* exp(x) in f32 from correctly rounded steps (shared with the kernels). */
 float or_expf(float x);
+void or_exp2_table(uint64_t *out);
+/* routerTopKKernel (io/QuantKernel.cajeta:39850-39960): logits[e] = W[e]·x by
+ * 256 lane partials and the stride-halving tree; softmax by 32 lanes; top-k
+ * picks, renormalised and scaled. Writes logits[experts], sel[used], w[used]. */
+void or_router_topk(const float *w_router, const float *x, int experts, int cols, int used, int norm_topk,
+                    float w_scale, float *logits, int32_t *sel, float *w);
+/* attnScoreKernel (model/AttnKernel.cajeta:397-425) over a position-major
+ * K plane [t][n_kv·hd]: scores[h][t] = the 32-lane score × scale; with
+ * softmax != 0, attnCombineKernel's in-place pass 1-2 follows (each row's
+ * max, then exp(s − max)). */
+void or_attn_scores(const float *q, const void *kp, int f32, int nh, int nkv, int hd, int count, float scale,
+                    int softmax, float *scores);
+/* The generic qkPrepKernel (model/AttnKernel.cajeta:127-206) at any head size:
+ * QK-norm by 128 lane partials and the stride-halving tree, then RoPE. */
+int or_qk_prep(float *q, float *k, const float *qw, const float *kw, const float *inv, int nh, int nkv, int hd,
+               int norm, float eps, int form, int pos);
 void  or_glu_exp(const float *g, const float *u, int64_t n, float *out);
 void  or_glu_tanh(const float *g, const float *u, int64_t n, float *out);
 void  or_inv_freq(int hd, float theta, float *inv);

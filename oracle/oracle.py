@@ -78,6 +78,10 @@ def _configure(L):
             "or_prefill_attend": (None, [P, P, P, I32, I32, I32, I32, I32, I32, I32, F, P]),
             "or_attn_merge": (None, [P, I32, I32, I32, P]),
             "or_qk_prep128": (I32, [P, P, P, P, P, I32, I32, I32, F, I32, I32]),
+            "or_qk_prep": (I32, [P, P, P, P, P, I32, I32, I32, I32, F, I32, I32]),
+            "or_router_topk": (None, [P, P, I32, I32, I32, I32, F, P, P, P]),
+            "or_attn_scores": (None, [P, P, I32, I32, I32, I32, I32, F, I32, P]),
+            "or_exp2_table": (None, [P]),
             "or_model_prefill": (I32, [P, P, I32, I32, P]),
             "or_expf": (F, [F]),
             "or_model_new": (P, [ctypes.POINTER(Config)]), "or_model_free": (None, [P]),
@@ -257,6 +261,43 @@ def qk_prep128(q, k, qw, kw, inv, n_h, n_kv, norm, eps, form, pos):
     lib().or_qk_prep128(_p(q), _p(k), _p(np.ascontiguousarray(qw, np.float32)), _p(np.ascontiguousarray(kw, np.float32)),
                         _p(np.ascontiguousarray(inv, np.float32)), n_h, n_kv, int(norm), float(eps), int(form), int(pos))
     return q, k
+
+
+def qk_prep(q, k, qw, kw, inv, n_h, n_kv, hd, norm, eps, form, pos):
+    """The generic qkPrepKernel at any head size (head size 128: the CPU kernel)."""
+    q = np.array(q, np.float32)
+    k = np.array(k, np.float32)
+    rc = lib().or_qk_prep(_p(q), _p(k), _p(np.asarray(qw, np.float32)), _p(np.asarray(kw, np.float32)),
+                          _p(np.asarray(inv, np.float32)), n_h, n_kv, hd, int(norm), float(eps), form, pos)
+    assert rc == 0
+    return q, k
+
+
+def router_topk(w, x, experts, cols, used, norm_topk=True, w_scale=0.0):
+    """routerTopKKernel: (logits, sel, weights)."""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    lg = np.zeros(experts, np.float32)
+    sel = np.zeros(used, np.int32)
+    wt = np.zeros(used, np.float32)
+    lib().or_router_topk(_p(w), _p(x), experts, cols, used, int(norm_topk), float(w_scale), _p(lg), _p(sel), _p(wt))
+    return lg, sel, wt
+
+
+def attn_scores(q, kplane, n_h, n_kv, hd, count, scale, softmax=False, kv_f32=False):
+    """attnScoreKernel's scores [n_h][count] over a position-major K plane
+    (fp16 bits, or f32); softmax: attnCombineKernel's in-place exp(s − max)."""
+    q = np.ascontiguousarray(q, np.float32)
+    kplane = np.ascontiguousarray(kplane)
+    out = np.zeros((n_h, count), np.float32)
+    lib().or_attn_scores(_p(q), _p(kplane), int(kv_f32), n_h, n_kv, hd, count, float(scale), int(softmax), _p(out))
+    return out
+
+
+def exp2_table():
+    t = np.zeros(32, np.uint64)
+    lib().or_exp2_table(_p(t))
+    return t
 
 
 def cpu_decode_splits(count, rows, n_kv, workers):

@@ -34,3 +34,23 @@ def reduce_pack_partials():
     m = (seg % 5).astype(np.float32) * np.float32(0.25) - np.float32(0.5)
     l = np.float32(1.0) + (seg % 3).astype(np.float32) * np.float32(0.5)
     return np.where(slot < 128, acc, np.where(slot == 128, m, l)).astype(np.float32)
+
+
+def spread(n, seed):
+    """TreeSiteReferenceTest.spread (AttnKernelTest.spread's generator): an
+    int32 linear congruential state s ← s·1103515245 + 12345 (wrapping), made
+    non-negative (the state keeps the negation), then ((s mod 2000) − 1000) / 700
+    in f32."""
+    out = np.empty(n, np.float32)
+    s = seed
+    for i in range(n):
+        s = (s * 1103515245 + 12345) & 0xFFFFFFFF
+        if s >= 0x80000000:
+            s -= 1 << 32
+        if s < 0:
+            s = -s
+            if s == 1 << 31:      # 0 − INT_MIN wraps to INT_MIN
+                s = -(1 << 31)
+        m = int(np.fmod(s, 2000)) if s < 0 else s % 2000
+        out[i] = np.float32(np.float32(m) - np.float32(1000.0)) / np.float32(700.0)
+    return out

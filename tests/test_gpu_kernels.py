@@ -377,13 +377,16 @@ def test_kernel_registry_answers_reference_names(gpu):
     for name in ("q4kQ8WaveMatVecKernel", "q6kQ8WaveMatVecKernel", "q80Q8WaveMatVecKernel", "q8kPackKernel",
                  "rmsnormPackRowF32", "gluPackF32", "qkPrepKernel", "attnFlashDecodeGqa4Kernel",
                  "attnFlashDecodeGqa8Kernel", "attnReducePackQ8Kernel", "argmaxRowKernel", "embedRowQ4kKernel",
-                 "routerTopKKernel", "mxfp4MatVecKernel"):
+                 "routerTopKKernel", "mxfp4MatVecKernel", "attnScoreKernel"):
         assert gpu.KernelCap.usable(name), name
     assert not gpu.KernelCap.usable("iq2xxsQ8WaveMatVecKernel")
     # names whose semantics this backend does not serve are refused: the
-    # fused MoE id kernels (their combine, Q4_K experts) and CPU-backend kernels
+    # fused MoE id kernels (their combine, Q4_K experts), CPU-backend kernels
+    # (the 8-row interleave products among them) and the MXFP4 activation
+    # quant as a launch of its own (here it is a GEMV's prologue, and no
+    # kernel writes the codes a following launch would read)
     for name in ("q4kQ8IdDownCombineKernel", "q4kQ8IdGateUpGluKernel", "attnDecodeCpuGqaKernel",
-                 "attnPrefillCpuGqaKernel"):
+                 "attnPrefillCpuGqaKernel", "q4kQ8X8RowsKernel", "q80Q8X8RowsKernel", "mxfp4QuantActKernel"):
         assert not gpu.KernelCap.usable(name), name
     gpu.KernelCap.setOverride("q4kQ8WaveMatVecKernel", False)
     assert not gpu.KernelCap.usable("q4kQ8WaveMatVecKernel")
@@ -530,3 +533,122 @@ def test_attn_merge_pack_matches_the_reference_cpu_golden(gpu, O):
     gpu.native.check(gpu.native.lib().cj_attn_merge(ob.h, packed.h, pb.h, n_q, hd, splits, 0), "merge")
     got = packed.download(np.uint8, n_q * hd // 256 * 320).view(np.int8).astype(np.float32)
     assert np.array_equal(got, want)
+
+
+def test_router_topk_matches_the_reference_cpu_golden(gpu, O):
+    """routerTopKKernel's launch (the router mat-vec and its top-k in one)
+    against the reference CPU backend's recorded e128h2048k8 logits, picks and
+    weights (TreeSiteReferenceTest.routerTopKKernelStaysWithinItsBar: 128
+    experts, 2048 columns, top-8, renormalised), bit for bit, and against the
+    oracle on a case with an exact tie and a w_scale; the counter is left
+    zero for the next launch."""
+    from reference_goldens import cpu_golden_rows, spread
+    g = cpu_golden_rows()
+    lib = gpu.native.lib()
+
+    def run(w, x, E, H, k, norm, scale):
+        wb, xb = gpu.Buffer.of(w.reshape(-1)), gpu.Buffer.of(x)
+        lg, sel, wt = gpu.Buffer(E * 4), gpu.Buffer(k * 4), gpu.Buffer(k * 4)
+        ctr = gpu.Buffer.of(np.zeros(4, np.int32))
+        gpu.native.check(lib.cj_router_topk(sel.h, wt.h, lg.h, wb.h, xb.h, ctr.h, E, H, k, int(norm), scale), "router")
+        out = lg.download(np.float32, E), sel.download(np.int32, k), wt.download(np.float32, k)
+        assert ctr.download(np.int32, 1)[0] == 0
+        return out
+
+    say("router top-k e128h2048k8")
+    w, x = spread(128 * 2048, 7), spread(2048, 11)
+    lg, sel, wt = run(w, x, 128, 2048, 8, True, 0.0)
+    assert np.array_equal(lg.view(np.uint32), g[("routerTopKKernel", "e128h2048k8-logits")].view(np.uint32))
+    assert np.array_equal(sel.astype(np.float32), g[("routerTopKKernel", "e128h2048k8-sel")])
+    assert np.array_equal(wt.view(np.uint32), g[("routerTopKKernel", "e128h2048k8-w")].view(np.uint32))
+    rng = np.random.default_rng(21)
+    E, H, k = 40, 512, 6
+    w = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    w[9] = w[4] = (np.abs(w[4]) * 2).astype(np.float32)
+    x = np.abs(rng.standard_normal(H)).astype(np.float32)
+    for norm, scale in ((True, 2.5), (False, 0.0)):
+        got = run(w, x, E, H, k, norm, scale)
+        want = O.router_topk(w, x, E, H, k, norm, scale)
+        for a, b in zip(got, want):
+            assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+        assert list(got[1][:2]) == [4, 9]
+
+
+def test_attn_scores_match_the_reference_cpu_golden(gpu, O):
+    """attnScoreKernel's launch (the two-pass decode attention's score pass)
+    at the reference's recorded shape — 32 query heads, 4 kv heads of 128,
+    256 positions, TreeSiteReferenceTest.attnScoreKernelStaysWithinItsBar's
+    inputs — bit for bit against the oracle's scores, whose softmax exps are
+    the recorded row bit for bit (tests/test_oracle.py); the K rows sit in
+    this backend's paged layout, the pages in a shuffled order."""
+    from reference_goldens import spread
+    say("attention scores h32kv4d128c256")
+    nh, nkv, hd, count = 32, 4, 128, 256
+    q = spread(nh * hd, 3)
+    kh = spread(count * nkv * hd, 5).astype(np.float16).reshape(count, nkv, hd)
+    pages = np.array([3, 0, 2, 1], np.int32)             # position block j lives in page pages[j]
+    plane = np.zeros((4, nkv, 64, hd), np.float16)
+    for t in range(count):
+        plane[pages[t // 64], :, t % 64, :] = kh[t]
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    qb, kb, tb, sb = gpu.Buffer.of(q), gpu.Buffer.of(plane.view(np.uint16).reshape(-1)), gpu.Buffer.of(pages), \
+        gpu.Buffer(nh * count * 4)
+    gpu.native.check(gpu.native.lib().cj_attn_scores(sb.h, qb.h, kb.h, tb.h, 0, nh, nkv, hd, count, 0, scale), "scores")
+    got = sb.download(np.float32, nh * count)
+    want = O.attn_scores(q, kh.reshape(count, nkv * hd).view(np.uint16), nh, nkv, hd, count, scale)
+    assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32))
+
+
+def test_qk_prep_hd64_with_norm_matches_the_reference_cpu_golden(gpu, O):
+    """QK-norm + RoPE at head size 64 — the generic qkPrepKernel, whose norm
+    sums in 32-lane waves from the adjacent lane up — against the reference
+    CPU backend's recorded q and k (QkPrepTest.run(6, 2, 64, true)), bit for
+    bit, and the fp16 K row appended."""
+    import ctypes
+    from reference_goldens import cpu_golden_rows, qkprep_fill
+    g = cpu_golden_rows()
+    n_q, n_kv, hd, pos = 6, 2, 64, 11
+    q, k, v = qkprep_fill(n_q * hd, 1), qkprep_fill(n_kv * hd, 2), qkprep_fill(n_kv * hd, 3)
+    qw, kw, inv = qkprep_fill(hd, 4), qkprep_fill(hd, 5), qkprep_fill(hd // 2, 6)
+    libm = ctypes.CDLL("libm.so.6")
+    libm.cosf.restype = libm.sinf.restype = ctypes.c_float
+    libm.cosf.argtypes = libm.sinf.argtypes = [ctypes.c_float]
+    tab = np.zeros((pos + 1, hd // 2, 2), np.float32)
+    for d in range(hd // 2):
+        ang = float(np.float32(pos) * inv[d])
+        tab[pos, d] = (libm.cosf(ang), libm.sinf(ang))
+    lib = gpu.native.lib()
+    qb, kb, vb = gpu.Buffer.of(q), gpu.Buffer.of(k), gpu.Buffer.of(v)
+    qwb, kwb, rope = gpu.Buffer.of(qw), gpu.Buffer.of(kw), gpu.Buffer.of(tab.reshape(-1))
+    kc, vc = gpu.Buffer(n_kv * 64 * hd * 2), gpu.Buffer(n_kv * 64 * hd * 2)
+    pg = gpu.Buffer.of(np.zeros(1, np.int32))
+    gpu.native.check(lib.cj_qk_prep(qb.h, kb.h, vb.h, kc.h, vc.h, qwb.h, kwb.h, rope.h, pg.h, 0, n_q, n_kv, hd, 1,
+                                    1e-6, 0, pos), "qk_prep")
+    gq, gk = qb.download(np.float32, q.size), kb.download(np.float32, k.size)
+    assert np.array_equal(gq.view(np.uint32), g[("qkPrepKernel", "h6kv2d64-q")].view(np.uint32))
+    assert np.array_equal(gk.view(np.uint32), g[("qkPrepKernel", "h6kv2d64-k")].view(np.uint32))
+    kcache = kc.download(np.uint16, n_kv * 64 * hd).reshape(n_kv, 64, hd)
+    assert np.array_equal(kcache[:, pos % 64, :].reshape(-1), O.f32_to_f16_bits(gk))
+
+
+def test_allocating_argmax_refuses_a_graph_capture(gpu):
+    """cj_argmax_row may grow its scratch (a synchronize, an allocation and a
+    memset, none of which a capture may record): it refuses while the stream
+    is capturing and leaves the capture intact; the allocation-free entry
+    point serves there."""
+    lib = gpu.native.lib()
+    v = gpu.Buffer.of(np.arange(5000, dtype=np.float32))
+    tb = gpu.Buffer.of(np.full(2, -1, np.int32))
+    gpu.native.check(lib.cj_graph_begin(), "graph begin")
+    rc = lib.cj_argmax_row(tb.h, 0, v.h, 5000)
+    msg = gpu.native.last_error()
+    rc2 = lib.cj_argmax_row_noalloc(tb.h, 1, v.h, 5000)
+    gh = lib.cj_graph_end()
+    assert rc == gpu.native.CJ_ERR_STATE and "capturing" in msg
+    assert rc2 == 0 and gh > 0
+    gpu.native.check(lib.cj_graph_launch(gh), "graph launch")
+    gpu.native.check(lib.cj_stream_sync(), "sync")
+    assert list(tb.download(np.int32, 2)) == [-1, 4999]
+    gpu.native.check(lib.cj_graph_free(gh), "graph free")
+    gpu.native.check(lib.cj_argmax_row(tb.h, 0, v.h, 5000), "argmax")
+    assert tb.download(np.int32, 1)[0] == 4999

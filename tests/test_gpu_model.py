@@ -541,3 +541,200 @@ def test_scheduler_steps_interleave_requests_like_the_oracle(gpu):
             eng.submitTokens(list(range(ctx)), maxNew=2)   # no decode position left in a slot
     finally:
         eng.close()
+
+
+def sched_run(pkg, eng, prompts, budgets, stops=None, watch=None):
+    """Submit every prompt, step until done; returns {key: Request}. watch(step,
+    states) sees every step's request states."""
+    ids = {}
+    for k in prompts:
+        st = [] if stops is None or k not in stops else stops[k]
+        ids[k] = eng.submitTokens(prompts[k], maxNew=budgets[k], params=pkg.SampleParams(stopTokens=st))
+    steps, more = 0, True
+    while more:
+        more = eng.stepOnce()
+        steps += 1
+        if watch:
+            watch(steps, {k: eng.request(ids[k]) for k in ids})
+        assert steps < 2000
+    return {k: eng.request(ids[k]) for k in ids}
+
+
+def test_scheduler_feeds_the_prompt_row_a_chunk_left(gpu):
+    """A prompt one row longer than whole prefill chunks (chunk + 1, 2·chunk + 1):
+    its last prompt row is fed from the host in the next step, not taken for a
+    decode row (the chunk's pick has already written its own guess into that
+    position), so every stream equals the oracle's greedy continuation."""
+    from oracle.gguf_reader import GgufReader
+    path = os.path.join(GOLD, "toy-routable-gqa8.gguf")
+    r = GgufReader(path)
+    ctx = 96
+    prompts = {"a": [1, 2, 3, 4, 5], "b": [5, 6, 7, 8, 9, 10, 11, 12, 13], "c": [9, 9, 40, 7]}
+    budget = {"a": 6, "b": 5, "c": 7}
+    want = {k: oracle_stream(r, prompts[k], budget[k], ctx) for k in prompts}
+    opts = gpu.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = 3
+    opts.prefillChunk = 4
+    eng = gpu.LlmEngine.load(opts)
+    try:
+        got = sched_run(gpu, eng, prompts, budget)
+        for k in prompts:
+            assert got[k].tokens == want[k], (k, got[k].tokens, want[k])
+        # alone (the pipelined step takes over once its prompt is in)
+        e = eng.submitTokens(prompts["b"], maxNew=5, params=gpu.SampleParams(stopTokens=[]))
+        eng.runAll(100)
+        assert eng.request(e).tokens == want["b"]
+    finally:
+        eng.close()
+
+
+def test_scheduler_pipelines_a_sole_greedy_request(gpu):
+    """A sole running greedy request takes the pipelined step
+    (Scheduler.stepPipelined): the seed step queues a decode step and emits no
+    token, each later step queues the next before reading the last, a stop
+    token ends the stream on that token (the queued step drained) and a budget
+    on its last token; a second request arriving mid-stream finishes the
+    pipeline and both go on batched. Every stream equals the oracle's."""
+    from oracle.gguf_reader import GgufReader
+    path = os.path.join(GOLD, "toy-routable.gguf")
+    r = GgufReader(path)
+    ctx = 128
+    P = gpu.Request
+    prompt = [7, 3, 99, 12, 1, 200]
+    want = oracle_stream(r, prompt, 20, ctx)
+    opts = gpu.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = 2
+    eng = gpu.LlmEngine.load(opts)
+    try:
+        counts = []
+        got = sched_run(gpu, eng, {"a": prompt}, {"a": 9}, watch=lambda s, st: counts.append(len(st["a"].tokens)))
+        assert got["a"].tokens == want[:9] and got["a"].finishReason == P.FINISH_BUDGET
+        # prefill emits token 1; the seed emits none; then one a step
+        assert counts[:4] == [1, 1, 2, 3], counts
+        stop = want[5]
+        got = sched_run(gpu, eng, {"a": prompt}, {"a": 20}, stops={"a": [stop]})
+        assert got["a"].finishReason == P.FINISH_EOS and got["a"].tokens == want[:want.index(stop) + 1]
+        # a second request mid-stream: the pipeline's pending token is consumed, then batched steps
+        other = [4, 4, 8]
+        want_b = oracle_stream(r, other, 6, ctx)
+        a = eng.submitTokens(prompt, maxNew=12, params=gpu.SampleParams(stopTokens=[]))
+        for _ in range(5):
+            eng.stepOnce()
+        b = eng.submitTokens(other, maxNew=6, params=gpu.SampleParams(stopTokens=[]))
+        eng.runAll(200)
+        assert eng.request(a).tokens == want[:12]
+        assert eng.request(b).tokens == want_b
+        # cancel while a step is in flight
+        c = eng.submitTokens(prompt, maxNew=15, params=gpu.SampleParams(stopTokens=[]))
+        for _ in range(4):
+            eng.stepOnce()
+        n = len(eng.request(c).tokens)
+        assert eng.cancel(c)
+        rc = eng.request(c)
+        assert rc.finishReason == P.FINISH_CANCEL and rc.tokens == want[:n]
+    finally:
+        eng.close()
+
+
+def test_scheduler_preempts_when_the_kv_pool_runs_dry(gpu):
+    """A K/V pool smaller than every slot at full context (CausalLM's
+    numBlocks): when a request's next rows do not fit, the youngest running
+    request is preempted (Scheduler.preempt), its pages freed, and it resumes
+    later by recomputing its whole stream. On a head-size-64 model the
+    recompute's prefill rows run the decode step's attention, so every
+    stream equals the oracle's uninterrupted greedy continuation; a request
+    that cannot fit the pool with nothing else running is refused."""
+    say("scheduler preemption")
+    spec = ("layers=2;hidden=256;heads=4;kv=2;hd=64;ffn=512;vocab=512;eps=1e-5;theta=10000;wtype=q8_0;"
+            "head=q8_0;embd=q8_0;ctx=256")
+    path, img = synth(gpu, spec, "t_preempt", 17)
+    from oracle.gguf_reader import GgufReader
+    r = GgufReader(img)
+    ctx = 256
+    rng = np.random.default_rng(31)
+    prompts = {k: rng.integers(0, 512, n).tolist() for k, n in (("a", 50), ("b", 40), ("c", 30))}
+    budget = {"a": 60, "b": 70, "c": 50}
+    want = {k: oracle_stream(r, prompts[k], budget[k], ctx) for k in prompts}
+    opts = gpu.EngineOptions(path)
+    opts.ctx = ctx
+    opts.maxSeqs = 3
+    opts.kvBlocks = 5           # 320 positions for three streams of 100-120
+    eng = gpu.LlmEngine.load(opts)
+    P = gpu.Request
+    try:
+        seen = set()
+        got = sched_run(gpu, eng, prompts, budget,
+                        watch=lambda s, st: seen.update(k for k in st if st[k].state == P.PREEMPTED))
+        assert seen, "no request was preempted"
+        say("  preempted: %s" % sorted(seen))
+        for k in prompts:
+            assert got[k].tokens == want[k], k
+            assert got[k].finishReason == P.FINISH_BUDGET
+    finally:
+        eng.close()
+    opts.kvBlocks = 2           # 128 positions: a 200-token prompt never fits
+    eng = gpu.LlmEngine.load(opts)
+    try:
+        eng.submitTokens(rng.integers(0, 512, 200).tolist(), maxNew=4, params=gpu.SampleParams(stopTokens=[]))
+        with pytest.raises(gpu.LlmException) as ex:
+            eng.runAll(50)
+        assert "pool" in str(ex.value)
+    finally:
+        eng.close()
+        gpu.image_free("t_preempt")
+
+
+def test_router_status_is_raised_by_batched_and_row_paths(gpu, tmp_path):
+    """A MoE router whose logits are not finite raises in the call that
+    routed them (MoeFfn.routeFromLogits throws): the embedding row of the
+    token the model predicts first is made NaN, so the prefill is clean and
+    the first decode routes NaN — through the batched decode (decodeBatch and
+    stepOnce) and through prefill rows (a prompt holding that token)."""
+    say("router status")
+    spec = ("layers=2;hidden=512;heads=8;kv=2;hd=64;ffn=512;vocab=1024;eps=1e-5;theta=10000;wtype=q8_0;"
+            "head=q8_0;embd=q8_0;experts=8;used=2;expert_ffn=512;expert_type=q8_0;ctx=128")
+    path, img = synth(gpu, spec, "t_nanroute", 41)
+    prompt = [3, 17, 250, 9, 77]
+    opts = gpu.EngineOptions(path)
+    opts.ctx = 128
+    opts.maxSeqs = 2
+    eng = gpu.LlmEngine.load(opts)
+    eng.reset()
+    eng.prefill(prompt)
+    t0 = int(eng.preds(len(prompt))[-1])
+    eng.close()
+    assert t0 not in prompt
+    from oracle.gguf_reader import GgufReader
+    buf = np.array(img, np.uint8)
+    gpu.image_free("t_nanroute")
+    rd = GgufReader(buf)
+    ty, dims, rows, cols, data = rd.tensors["token_embd.weight"]
+    rb = cols // 32 * 34
+    row = data[t0 * rb:(t0 + 1) * rb].reshape(-1, 34)
+    row[:, 0:2] = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)   # every block scale NaN
+    f = tmp_path / "nanroute.gguf"
+    buf.tofile(str(f))
+    opts = gpu.EngineOptions(str(f))
+    opts.ctx = 128
+    opts.maxSeqs = 2
+    eng = gpu.LlmEngine.load(opts)
+    try:
+        for s in (0, 1):
+            eng.reset(s)
+            eng.prefill(prompt, s)
+        with pytest.raises(gpu.LlmException) as ex:
+            eng.decodeBatch([0, 1], 1)
+        assert "not finite" in str(ex.value)
+        eng.reset(0)
+        with pytest.raises(gpu.LlmException):
+            eng.prefill(prompt + [t0, 5], 0)         # prefill rows route the NaN row
+        eng.reset(0)
+        eng.reset(1)
+        for _ in range(2):
+            eng.submitTokens(prompt, maxNew=4, params=gpu.SampleParams(stopTokens=[]))
+        with pytest.raises(gpu.LlmException):
+            eng.runAll(20)
+    finally:
+        eng.close()
