@@ -106,7 +106,7 @@ def token_macs(cfg, count):
     return weights, attn
 
 
-def cpu_baseline(pkg, image_name, vocab, budget_s, seed, context):
+def cpu_baseline(pkg, image_name, vocab, budget_s, seed, context, kv_f32=False):
     """Time the oracle's decode of the same model on the host cores: tokens
     at positions 1, 2, ... until `budget_s` of work is done (at least 2).
     The benchmarked context adds its attention's multiply-adds to the
@@ -116,7 +116,7 @@ def cpu_baseline(pkg, image_name, vocab, budget_s, seed, context):
     from oracle.gguf_reader import GgufReader, oracle_model, model_config
     img = pkg.image_bytes(image_name)
     reader = GgufReader(img)
-    om, _ = oracle_model(reader, ctx=64)
+    om, _ = oracle_model(reader, ctx=64, kv_f32=kv_f32)
     try:
         rng = np.random.default_rng(seed + 1)
         toks = rng.integers(0, vocab, 64).tolist()
@@ -422,6 +422,7 @@ def run_single(args, pkg, native, which):
     opts.maxSeqs = 1
     opts.graphs = not args.eager
     opts.cpuThreads = args.cpu_threads
+    opts.kvF32 = args.kv == "f32"
     eng = pkg.LlmEngine.load(opts)
     vocab = eng.config["vocabSize"]
     rng = np.random.default_rng(args.seed)
@@ -454,7 +455,8 @@ def run_single(args, pkg, native, which):
         log("  %-13s %-26s %9.2f us  %12d B  %7.1f GB/s" % (kname, kn, us, nbytes, nbytes / (us * 1e-6) / 1e9))
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pkg, name, vocab, args.cpu_seconds, args.seed, ctx + args.warmup + steps // 2)
+        cpu = cpu_baseline(pkg, name, vocab, args.cpu_seconds, args.seed, ctx + args.warmup + steps // 2,
+                           kv_f32=args.kv == "f32")
         cpu["sample"] = cpu["sample"].replace("C3", which.upper())
         log("cpu baseline: %s" % cpu)
     eng.close()
@@ -467,7 +469,9 @@ def run_single(args, pkg, native, which):
         "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us_tok / 1e3, 4),
         "higher_is_better": not c1, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic: seeded random-init GGUF (N(0,0.02) weights), uniform random prompt ids",
-        "config": {"workload": workload, "batch": 1, "prefill_positions": ctx,
+        "config": {"workload": workload + ("; f32 K/V cache (PagedKvCache's mode, as the config states it)"
+                                           if args.kv == "f32" else "; fp16 paged K/V"),
+                   "batch": 1, "prefill_positions": ctx, "kv": args.kv,
                    "step": "eager launches" if args.eager else "hipGraph replay", "seed": args.seed},
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS,
                           "unit": "GB/s", "frac": round(step_gbs / PEAK_HBM_GBS, 4),
@@ -623,6 +627,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kv", choices=("f16", "f32"), default="f16",
+                    help="c1: the K/V cache's element type (f32: BASELINE.json's C1 as stated)")
     ap.add_argument("--eager", action="store_true",
                     help="enqueue each step's launches instead of replaying the graph (for profilers)")
     args = ap.parse_args()
@@ -666,7 +672,7 @@ def main():
     pkg.synth_gguf("c3", "mem:bench_c3", args.seed)
     log("synthesised C3 (seed %d) in %.1f s" % (args.seed, time.perf_counter() - t))
 
-    total = args.ctx + args.warmup + args.steps + 1
+    total = args.ctx + args.warmup + args.steps + 8    # room for the LlmEngine leg's request too
     opts = pkg.EngineOptions("mem:bench_c3")
     opts.ctx = total
     opts.maxSeqs = 1
@@ -722,6 +728,28 @@ def main():
     log("  copy      cj_copy                   %9.2f us  %12d B  %7.1f GB/s" % (copy["avg_us"], copy["bytes"],
                                                                               copy["GB/s"]))
 
+    # the same decode through the LlmEngine surface: one greedy request,
+    # stepOnce per token (the scheduler's pipelined step: the next token's
+    # step is queued before the last one's token is read)
+    api = None
+    if not args.eager:
+        rid = eng.submitTokens(prompt, maxNew=args.warmup + args.steps + 4, params=pkg.SampleParams(stopTokens=[]))
+        for _ in range(2 + args.warmup):             # the prompt (its first token), the pipeline's seed, warmup
+            eng.stepOnce()
+        native.sync()
+        n0 = len(eng.request(rid).tokens)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            eng.stepOnce()
+        api_wall = time.perf_counter() - t0
+        n1 = len(eng.request(rid).tokens)
+        eng.cancel(rid)
+        api = {"path": "LlmEngine.submitTokens + stepOnce (pipelined greedy step)", "tokens": n1 - n0,
+               "ms_per_step": round(api_wall * 1000.0 / max(1, n1 - n0), 4),
+               "tok/s": round((n1 - n0) / api_wall, 2), "vs_decode": round((n1 - n0) / api_wall / (args.steps / wall), 4)}
+        log("api: %d tokens through stepOnce, %.3f ms/step (%.1f%% of the decode rate)"
+            % (n1 - n0, api["ms_per_step"], 100 * api["vs_decode"]))
+
     cpu = None
     if not args.no_cpu:
         t = time.perf_counter()
@@ -754,6 +782,7 @@ def main():
                           "device_us_per_step": round(dev_us, 2)},
         "kernels": kernels,
         "copy": copy,
+        "api": api,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

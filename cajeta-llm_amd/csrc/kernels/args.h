@@ -45,7 +45,7 @@ typedef struct {
     float *y;               // output rows (STORE / ACCUM / ARGMAX logits)
     // epilogue extras
     float *q_out;           // QKV: rotated q (HF order)
-    uint16_t *kc, *vc;      // QKV: fp16 K/V planes (page-blocked, head-major)
+    uint16_t *kc, *vc;      // QKV: K/V planes (page-blocked, head-major), fp16 (or f32: kv_f32)
     const int32_t *pgtab;   // QKV: KV page table
     const float *rope_cs;   // QKV: [ctx][half] (cos, sin) pairs
     float *act;             // GLU: silu(g)·u out (f32)
@@ -96,6 +96,8 @@ typedef struct {
     // NORM_F32 prologue: workgroup 0 also writes the normed f32 activation
     // here (for the launches after it; may be null)
     float *xout;
+    int32_t kv_f32;         // QKV: the K/V planes hold f32 (kc, vc point at floats)
+    int32_t pad_kv;
 } cj_gemv_args;
 
 typedef struct {
@@ -142,6 +144,7 @@ typedef struct {
     const cj_step_state *state;
     int32_t n_q, n_kv, head_dim, norm, form, pg_base, pos;
     float eps;
+    int32_t kv_f32;          // the K/V planes hold f32
 } cj_qkprep_args;
 
 typedef struct {
@@ -203,7 +206,8 @@ typedef struct {
     int64_t n, npad;
     int32_t form, per32;
     // argmax partials: [rows][nchunks] of 1024-wide chunks
-    float *pv; int32_t *pi; int32_t nchunks; int32_t pad;
+    float *pv; int32_t *pi; int32_t nchunks;
+    int32_t kv_f32;          // q|k|v: the K/V planes hold f32
 } cj_rows_args;
 
 typedef struct {

@@ -401,7 +401,7 @@ SPLIT_KERNEL(8)
 // read as broadcasts. A head a workgroup keeps each lane's chain of
 // products short: the scores of a 4096-position span take 8× fewer
 // dependent steps than a workgroup per kv head.
-template <int HD>
+template <int HD, bool KF32 = false>
 DEV void scores_body(const cj_attn_args &a, int bx, int h) {
     __shared__ __align__(16) float qs[HD];
     int count, from;
@@ -415,15 +415,25 @@ DEV void scores_body(const cj_attn_args &a, int bx, int h) {
     for (int i = threadIdx.x; i < HD; i += 256) qs[i] = a.q[(int64_t)h * HD + i];
     __syncthreads();
     if (t >= count) return;
-    const uint16_t *kr = a.kc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD;
+    const int64_t koff = (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD;
     float k[HD];
+    if constexpr (KF32) {
+        const float *kr = (const float *)a.kc + koff;
 #pragma unroll
-    for (int j = 0; j < HD / 8; j++) {
-        const u32x4 v = *(const u32x4 *)(kr + 8 * j);
-        k[8 * j + 0] = h2f(v.x); k[8 * j + 1] = h2f(v.x >> 16);
-        k[8 * j + 2] = h2f(v.y); k[8 * j + 3] = h2f(v.y >> 16);
-        k[8 * j + 4] = h2f(v.z); k[8 * j + 5] = h2f(v.z >> 16);
-        k[8 * j + 6] = h2f(v.w); k[8 * j + 7] = h2f(v.w >> 16);
+        for (int j = 0; j < HD / 4; j++) {
+            const float4 v = *(const float4 *)(kr + 4 * j);
+            k[4 * j + 0] = v.x; k[4 * j + 1] = v.y; k[4 * j + 2] = v.z; k[4 * j + 3] = v.w;
+        }
+    } else {
+        const uint16_t *kr = a.kc + koff;
+#pragma unroll
+        for (int j = 0; j < HD / 8; j++) {
+            const u32x4 v = *(const u32x4 *)(kr + 8 * j);
+            k[8 * j + 0] = h2f(v.x); k[8 * j + 1] = h2f(v.x >> 16);
+            k[8 * j + 2] = h2f(v.y); k[8 * j + 3] = h2f(v.y >> 16);
+            k[8 * j + 4] = h2f(v.z); k[8 * j + 5] = h2f(v.z >> 16);
+            k[8 * j + 6] = h2f(v.w); k[8 * j + 7] = h2f(v.w >> 16);
+        }
     }
     float p[32];
 #pragma unroll
@@ -731,6 +741,76 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
+// The combine over f32 K/V planes (the reference's PagedKvCache mode, where
+// the host path keeps f32 K/V): the same operations in the same order as
+// combine_body — the max, e_t = exp(s_t − max) with lane l of 128 adding its
+// positions t = l, l+128, ... in order and the 128 sums folded by the
+// stride-halving tree, then each output dimension's ascending-t sum of the
+// rounded products e_t·v_t[d], scaled once by 1/Σ — a workgroup of 256 per
+// query head and 32 output dimensions, V staged through LDS 64 positions at
+// a time (coalesced 128-byte rows) for the 32 chain lanes. Spans up to
+// COMBINE_ES positions (the engine's f32 mode caps its context there).
+template <int HD>
+DEV void combine_f32_body(const cj_attn_args &a, int bx) {
+    constexpr int DH = 32, NSPLIT = HD / DH, TV = 64;
+    __shared__ float red[4 + 128];
+    __shared__ __align__(16) float es[COMBINE_ES];
+    __shared__ __align__(16) float vt[TV][DH];
+    __shared__ int pgs[COMBINE_ES / 64];
+    int count, from;
+    attn_window(a, count, from);
+    const int h = bx / NSPLIT, d0 = DH * (bx % NSPLIT), l = threadIdx.x;
+    const int grp = a.n_q / a.n_kv, kvh = h / grp;
+    const float *sc = a.part + (int64_t)h * a.splits;
+    const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
+    for (int j = l; j < npg; j += 256) pgs[j] = a.pgtab[a.pg_base + (from >> 6) + j];
+    float mx = -3.0e38f;
+    if (l < 128)
+        for (int t = l; t < count; t += 128) mx = fmaxf(mx, sc[t]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((l & 63) == 0) red[l >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(red[0], red[1]);
+    float s = 0.0f;
+    if (l < 128)
+        for (int t = l; t < count; t += 128) {
+            const float e = cj_expf(__fsub_rn(sc[t], m));
+            es[t] = e;
+            s = __fadd_rn(s, e);
+        }
+    __syncthreads();                 // red[0..1] read by every lane above
+    if (l < 128) red[4 + l] = s;
+    __syncthreads();
+    if (l < 64) {
+        float v2 = __fadd_rn(red[4 + l], red[4 + l + 64]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        if (l == 0) red[2] = v2;
+    }
+    __syncthreads();
+    const float rs = __fdiv_rn(1.0f, red[2]);
+    const float *vp = (const float *)a.vc;
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < count; t0 += TV) {
+        // 64 positions × 32 dimensions: thread l loads 8 of them
+#pragma unroll
+        for (int k = 0; k < TV * DH / 256; k++) {
+            const int c = l + 256 * k, p = c / DH, d = c % DH;
+            const int pos = from + min(t0 + p, count - 1);
+            const int page = pgs[(pos >> 6) - (from >> 6)];
+            vt[p][d] = vp[(((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + d];
+        }
+        __syncthreads();
+        if (l < DH) {
+            const int n = min(TV, count - t0);
+            for (int p = 0; p < n; p++) acc = __fadd_rn(acc, __fmul_rn(es[t0 + p], vt[p][l]));
+        }
+        __syncthreads();
+    }
+    if (l < DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
+}
+
 // Row r of a many-row launch as the one-row kernels see it: its sequence
 // slot's pages and position, its q, output and score rows.
 DEV cj_attn_args attn_row_args(const cj_attn_args &a, int r) {
@@ -750,6 +830,22 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_arg
 extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a, blockIdx.x, blockIdx.y); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a, blockIdx.x); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a, blockIdx.x); }
+// f32 K/V planes: the two-pass pair, one row and many rows
+#define TWO_PASS_F32(HD)                                                                                    \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_f32_h##HD(cj_attn_args a) {           \
+        scores_body<HD, true>(a, blockIdx.x, blockIdx.y);                                                   \
+    }                                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_f32_h##HD(cj_attn_args a) {          \
+        combine_f32_body<HD>(a, blockIdx.x);                                                                \
+    }                                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_rows_f32_h##HD(cj_attn_args a) {      \
+        scores_body<HD, true>(attn_row_args(a, blockIdx.y / a.n_q), blockIdx.x, blockIdx.y % a.n_q);       \
+    }                                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_rows_f32_h##HD(cj_attn_args a) {     \
+        combine_f32_body<HD>(attn_row_args(a, blockIdx.y), blockIdx.x);                                     \
+    }
+TWO_PASS_F32(64)
+TWO_PASS_F32(128)
 // The many-row forms (batched decode, and prefill chunks of the models that
 // prefill a decode step a position): grid y is row · n_q + query head for
 // the scores, the row for the combine.
@@ -1126,13 +1222,16 @@ extern "C" __global__ void __launch_bounds__(64) cj_qkprep(cj_qkprep_args a) {
         x[d + half] = rb;
         if (!isq) {
             const int64_t ki = kv_at(a.pgtab, a.pg_base, pos, a.n_kv, kh, hd);
-            a.kc[ki + d] = f2h(ra);
-            a.kc[ki + d + half] = f2h(rb);
+            kv_store2(a.kc, a.kv_f32, ki + d, ra, ki + d + half, rb);
         }
     }
     if (!isq) {
         const int64_t vi = kv_at(a.pgtab, a.pg_base, pos, a.n_kv, kh, hd);
-        for (int e = t; e < hd; e += 64) a.vc[vi + e] = f2h(a.v[(int64_t)kh * hd + e]);
+        for (int e = t; e < hd; e += 64) {
+            const float x = a.v[(int64_t)kh * hd + e];
+            if (a.kv_f32) ((float *)a.vc)[vi + e] = x;
+            else a.vc[vi + e] = f2h(x);
+        }
     }
 }
 

@@ -39,6 +39,19 @@ DEV float mul_h16hi(uint32_t w, float b) {
 }
 DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
+// Two values into a K/V plane: fp16 (rounded to nearest even), or f32 as
+// they are where the plane holds f32 (the reference's PagedKvCache keeps
+// f32 K/V, model/PagedKvCache.cajeta).
+DEV void kv_store2(uint16_t *plane, int f32, int64_t i0, float x0, int64_t i1, float x1) {
+    if (f32) {
+        ((float *)plane)[i0] = x0;
+        ((float *)plane)[i1] = x1;
+    } else {
+        plane[i0] = f2h(x0);
+        plane[i1] = f2h(x1);
+    }
+}
+
 // Correctly rounded f32 square root. (HIP's __fsqrt_rn is the hardware's
 // approximate v_sqrt_f32 unless OCML's rounded operations are enabled; the
 // llvm.sqrt expansion for gfx950 rounds to nearest even.)

@@ -469,15 +469,13 @@ DEV void gemv_epilogue_t(const cj_gemv_args &a, const GemvSlice &sl, float v, fl
                 a.q_out[(int64_t)h * hd + half + bb] = rb;
             } else {
                 const int64_t ki = (((int64_t)pre.page * a.n_kv + h) * 64 + (pos & 63)) * hd;
-                a.kc[ki + bb] = f2h(ra);
-                a.kc[ki + half + bb] = f2h(rb);
+                kv_store2(a.kc, a.kv_f32, ki + bb, ra, ki + half + bb, rb);
             }
         } else {
             const int64_t rr = r - qrows - krows;
             const int h = (int)(rr / hd), d = (int)(rr % hd);
             const int64_t vi = (((int64_t)pre.page * a.n_kv + h) * 64 + (pos & 63)) * hd;
-            a.vc[vi + d] = f2h(v);
-            a.vc[vi + d + 1] = f2h(vp);
+            kv_store2(a.vc, a.kv_f32, vi + d, v, vi + d + 1, vp);
         }
     } break;
     case CJ_EPI_GLU:

@@ -49,15 +49,13 @@ extern "C" __global__ void __launch_bounds__(256) cj_rows_qkv(cj_rows_args a) {
                 qo[(int64_t)h * hd + half + bb] = rb;
             } else {
                 const int64_t ki = (((int64_t)page * a.n_kv + h) * 64 + (pos & 63)) * hd;
-                a.kc[ki + bb] = f2h(ra);
-                a.kc[ki + half + bb] = f2h(rb);
+                kv_store2(a.kc, a.kv_f32, ki + bb, ra, ki + half + bb, rb);
             }
         } else {
             const int64_t rr = i - qrows - krows;
             const int h = (int)(rr / hd), d = (int)(rr % hd);
             const int64_t vi = (((int64_t)page * a.n_kv + h) * 64 + (pos & 63)) * hd;
-            a.vc[vi + d] = f2h(v);
-            a.vc[vi + d + 1] = f2h(vp);
+            kv_store2(a.vc, a.kv_f32, vi + d, v, vi + d + 1, vp);
         }
     }
 }

@@ -146,6 +146,9 @@ struct Engine {
     // when it is reset or its request leaves; the default pool holds every
     // slot at its full context
     int kv_pages = 0;
+    // the K/V planes hold f32 (the reference's PagedKvCache mode), where the
+    // attention takes the two-pass form
+    bool kv_f32 = false;
     std::vector<int32_t> free_pages;
     std::vector<std::vector<int32_t>> slot_pages;
     int32_t *pinned_pg = nullptr;   // host mirror of the page table (pinned: the source of its uploads)
@@ -205,7 +208,7 @@ struct Engine {
         for (auto &e : pipe_ev)
             if (e) (void)hipEventDestroy(e);
     }
-    int load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_);
+    int load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_, bool kv_f32_);
     // the page pool
     int ensure_pages(int s, int64_t upto);
     bool pages_fit(int s, int64_t upto) const;
@@ -338,7 +341,7 @@ int Engine::fuse_rows(const std::vector<std::string> &names, DevW &w, bool inter
     return CJ_OK;
 }
 
-int Engine::load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_) {
+int Engine::load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_, bool kv_f32_) {
     std::string err;
     if (!file.open(path, err)) return fail(CJ_ERR_IO, "model: %s", err.c_str());
     const std::string arch = file.get_str("general.architecture", "");
@@ -416,7 +419,14 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_
     // and the scheduler preempts when it runs dry
     if (kv_pages_ < 0) return fail(CJ_ERR_ARG, "model: %d K/V pages", kv_pages_);
     kv_pages = kv_pages_ > 0 ? kv_pages_ : pages_per_seq * max_seqs;
-    const int64_t plane = (int64_t)kv_pages * n_kv * 64 * head_dim * 2;
+    // f32 K/V (PagedKvCache's mode): the two-pass attention reads it; the
+    // split-K and prefill-attend forms (head size 128 with 4 or 8 query
+    // heads a kv head) keep fp16, as the reference's resident decode does
+    kv_f32 = kv_f32_;
+    if (kv_f32 && ((head_dim == 128 && (grp == 4 || grp == 8)) || ctx > 6144))
+        return fail(CJ_ERR_ARG, "model: f32 K/V is served by the two-pass attention (head size 64, or GQA other than 4 "
+                                "and 8 at 128) up to 6144 positions; this model takes the fp16 split-K form");
+    const int64_t plane = (int64_t)kv_pages * n_kv * 64 * head_dim * (kv_f32 ? 4 : 2);
     int rc;
     for (int l = 0; l < n_layers; l++) {
         Layer &L = layers[l];
@@ -555,7 +565,7 @@ int Engine::load(const std::string &path, int ctx_, int max_seqs_, int kv_pages_
     // step a position, which rows of the two-pass decode attention repeat
     // row for row (a split-K row's split count follows the rows, so MoE
     // models at head size 128 keep the step a position)
-    rows_pf_attend = n_experts == 0 && head_dim == 128;
+    rows_pf_attend = n_experts == 0 && head_dim == 128 && !kv_f32;
     rows_prefill = rows_ok && (rows_pf_attend || !rows_split);
     if (rows_ok && (rc = rows_alloc(std::max(chunk, max_seqs)))) return rc;
     CJ_HIP(hipDeviceSynchronize());
@@ -631,9 +641,10 @@ int Engine::enqueue_step(int s) {
     // heads a kv head, else the two-pass score/combine
     const bool split = head_dim == 128 && (grp == 4 || grp == 8);
     char attn_kernel[64], combine_kernel[64], fused_kernel[64];
+    const char *kvs = kv_f32 ? "f32_" : "";
     if (split) snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_split_h128_g%d", grp);
-    else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_h%d", head_dim);
-    snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_h%d", head_dim);
+    else snprintf(attn_kernel, sizeof attn_kernel, "cj_attn_scores_%sh%d", kvs, head_dim);
+    snprintf(combine_kernel, sizeof combine_kernel, "cj_attn_combine_%sh%d", kvs, head_dim);
     snprintf(fused_kernel, sizeof fused_kernel, "cj_attn_fused_h%d", head_dim);
     // the residual: hs, or on MoE models the buffer the last combine wrote
     // (it alternates between hs and hs2, see K_COMBINE below)
@@ -654,7 +665,7 @@ int Engine::enqueue_step(int s) {
             a.row_bytes = L.qkv.row_bytes; a.type = L.qkv.type; a.pro = CJ_PRO_PACKED; a.epi = CJ_EPI_QKV_ROPE;
             if (qkv_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = cur; a.nw = L.attn_norm; a.norm_form = 0; }
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
-            a.batch = 1;
+            a.batch = 1; a.kv_f32 = kv_f32;
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
         }
         if (want(K_ATTN, l) || want(K_MERGE, l)) {   // 2. attention
@@ -683,7 +694,7 @@ int Engine::enqueue_step(int s) {
             } else if (want(K_ATTN, l)) {
                 a.splits = ctx;
                 const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
-                if (span <= (head_dim == 64 ? 256 : 128)) {
+                if (!kv_f32 && span <= (head_dim == 64 ? 256 : 128)) {
                     // every step's span fits one workgroup: the one-launch form
                     if ((rc = launch(fused_kernel, (uint32_t)n_heads, 256, 0, a))) return rc;
                 } else {
@@ -972,7 +983,7 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             cj_rows_args q = ra;
             q.in = r_qkv; q.in_stride = L.qkv.rows; q.q_out = r_q; q.out_stride = qd; q.kc = L.kc; q.vc = L.vc;
             q.pgtab = pgtab; q.rope_cs = rope; q.pg_n = pages_per_seq; q.n_q = n_heads; q.n_kv = n_kv;
-            q.head_dim = head_dim; q.nrows = n;
+            q.head_dim = head_dim; q.nrows = n; q.kv_f32 = kv_f32;
             const int64_t qkv_vals = (int64_t)(n_heads + 2 * n_kv) * head_dim;
             if ((rc = launch2("cj_rows_qkv", (uint32_t)((qkv_vals + 511) / 512), (uint32_t)n, 256, 0, q))) return rc;
         }
@@ -992,15 +1003,16 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
             // every span fits one workgroup), then the pack of the rows
             a.out = r_attn; a.part = r_part; a.splits = ctx; a.part_stride = (int64_t)n_heads * ctx;
             const int64_t span = L.window > 0 ? std::min(L.window, ctx) : ctx;
+            const char *kvs = kv_f32 ? "f32_" : "";
             char kname[48];
-            if (span <= (head_dim == 64 ? 256 : 128)) {
+            if (!kv_f32 && span <= (head_dim == 64 ? 256 : 128)) {
                 snprintf(kname, sizeof kname, "cj_attn_fused_rows_h%d", head_dim);
                 if ((rc = launch2(kname, (uint32_t)n_heads, (uint32_t)n, 256, 0, a))) return rc;
             } else {
-                snprintf(kname, sizeof kname, "cj_attn_scores_rows_h%d", head_dim);
+                snprintf(kname, sizeof kname, "cj_attn_scores_rows_%sh%d", kvs, head_dim);
                 if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_heads), 256, 0, a)))
                     return rc;
-                snprintf(kname, sizeof kname, "cj_attn_combine_rows_h%d", head_dim);
+                snprintf(kname, sizeof kname, "cj_attn_combine_rows_%sh%d", kvs, head_dim);
                 if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;
             }
             if ((rc = rows_pack(r_attn, qd, L.o.type == CJ_Q8_0, n))) return rc;
@@ -1320,11 +1332,12 @@ int Engine::decode(int s, int steps, int32_t *out) {
 int64_t Engine::kind_bytes(int kind, int count) const {
     const Layer &L = layers[0];
     const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv * head_dim, h = hidden;
+    const int64_t kvb = kv_f32 ? 4 : 2;   // bytes a K/V element
     auto wb = [](const DevW &w) { return w.rows * ggml_row_bytes(w.type, w.cols); };
     switch (kind) {
     case K_EMBED: return embd_row_file_bytes + h * 4;
-    case K_QKV: return wb(L.qkv) + ((h + 255) / 256) * 320 + qd * 4 + 2 * kvd * 2;
-    case K_ATTN: return (int64_t)count * kvd * 2 * 2 + qd * 8 + ((qd + 255) / 256) * 320;
+    case K_QKV: return wb(L.qkv) + ((h + 255) / 256) * 320 + qd * 4 + 2 * kvd * kvb;
+    case K_ATTN: return (int64_t)count * kvd * 2 * kvb + qd * 8 + ((qd + 255) / 256) * 320;
     case K_O: return wb(L.o) + (merge_w ? qd * 4 : ((qd + 255) / 256) * 320) + h * 8;
     case K_GATE_UP: return wb(L.gu) + ((h + 255) / 256) * 320 + (int64_t)ffn * 4;
     case K_DOWN: return wb(L.down) + (int64_t)ffn * 4 + h * 8;
@@ -1748,16 +1761,16 @@ Engine *eng_of(int64_t h) { return (Engine *)(uintptr_t)h; }
 extern "C" {
 
 int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs) {
-    return cj_engine_load_pool(path, ctx, max_seqs, 0);
+    return cj_engine_load_kv(path, ctx, max_seqs, 0, 0);
 }
 
-int64_t cj_engine_load_pool(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages) {
+int64_t cj_engine_load_kv(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages, int32_t kv_f32) {
     if (!cj::ready()) return cj::fail(CJ_ERR_STATE, "cj_init has not run"), 0;
     if (!path) return cj::fail(CJ_ERR_ARG, "cj_engine_load: null path"), 0;
     auto *e = new Engine();
     int rc;
     try {
-        rc = e->load((const char *)path, ctx, max_seqs, kv_pages);
+        rc = e->load((const char *)path, ctx, max_seqs, kv_pages, kv_f32 != 0);
     } catch (const std::exception &x) {   // nothing may unwind through the C-ABI
         rc = cj::fail(CJ_ERR_IO, "model: %s", x.what());
     }

@@ -422,6 +422,9 @@ int32_t cj_init(int32_t device) {
         "cj_attn_prefill_h128_g1", "cj_attn_prefill_h128_g2", "cj_attn_prefill_h128_g4", "cj_attn_prefill_h128_g8",
         "cj_attn_scores_rows_h64", "cj_attn_scores_rows_h128", "cj_attn_combine_rows_h64", "cj_attn_combine_rows_h128",
         "cj_attn_fused_rows_h64", "cj_attn_fused_rows_h128",
+        "cj_attn_scores_f32_h64", "cj_attn_scores_f32_h128", "cj_attn_combine_f32_h64", "cj_attn_combine_f32_h128",
+        "cj_attn_scores_rows_f32_h64", "cj_attn_scores_rows_f32_h128", "cj_attn_combine_rows_f32_h64",
+        "cj_attn_combine_rows_f32_h128",
     };
     for (const char *k : kernels) {
         hipFunction_t f;

@@ -28,6 +28,7 @@ class EngineOptions:
         self.prefillChunk = 512  # rows a prefill chunk (CausalLM.CHUNK_MAX); 0: one decode step a position
         self.kvBlocks = 0        # K/V pool pages of 64 positions shared by the slots (0: every slot at full context;
                                  # CausalLM's numBlocks): a smaller pool preempts under pressure
+        self.kvF32 = False       # f32 K/V planes (PagedKvCache's mode; the two-pass attention models)
 
 
 class SampleParams:
@@ -112,8 +113,8 @@ class LlmEngine:
             else:
                 raise LlmException("engine: device '%s' is not served by the MI355X backend" % opts.device)
         native.init(dev)
-        h = lib().cj_engine_load_pool(opts.model.encode(), int(opts.ctx), int(opts.maxSeqs),
-                                      int(getattr(opts, "kvBlocks", 0)))
+        h = lib().cj_engine_load_kv(opts.model.encode(), int(opts.ctx), int(opts.maxSeqs),
+                                    int(getattr(opts, "kvBlocks", 0)), int(bool(getattr(opts, "kvF32", False))))
         handle(h, "LlmEngine.load(%s)" % opts.model)
         if not getattr(opts, "graphs", True):
             check(lib().cj_engine_set_graphs(h, 0), "cj_engine_set_graphs")

@@ -64,7 +64,7 @@ SIGNATURES = {
     "cj_router_topk": (I32, [I64, I64, I64, I64, I64, I64, I32, I32, I32, I32, F32]),
     "cj_attn_scores": (I32, [I64, I64, I64, I64, I32, I32, I32, I32, I32, I32, F32]),
     "cj_engine_load": (I64, [CP, I32, I32]),
-    "cj_engine_load_pool": (I64, [CP, I32, I32, I32]),
+    "cj_engine_load_kv": (I64, [CP, I32, I32, I32, I32]),
     "cj_engine_close": (I32, [I64]),
     "cj_engine_config": (I32, [I64, P, I32]),
     "cj_engine_submit": (I32, [I64, P, I32, I32]),

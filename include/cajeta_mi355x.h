@@ -267,14 +267,18 @@ int32_t cj_attn_scores(int64_t scores, int64_t q, int64_t kcache, int64_t pgtab,
  * path "mem:<name>" loads an image made by cj_synth_gguf. ctx is the KV
  * capacity per sequence, max_seqs the sequence slots. */
 int64_t cj_engine_load(const int8_t *path, int32_t ctx, int32_t max_seqs);
-/* cj_engine_load with the K/V pool's size: kv_pages pages of 64 positions
- * shared by every slot (0: every slot at its full context, what
- * cj_engine_load gives). A smaller pool holds more slots than it could at
- * full context; the scheduler preempts the youngest running request when a
- * request's next rows do not fit, and resumes it later by recomputing its
- * stream. The CausalLM(cfg, maxSeq, maxSeqs, numBlocks) constructor's
- * numBlocks (model/CausalLM.cajeta:64-94). */
-int64_t cj_engine_load_pool(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages);
+/* cj_engine_load with the K/V cache's options. kv_pages: the pool's size in
+ * pages of 64 positions shared by every slot (0: every slot at its full
+ * context, what cj_engine_load gives) — the CausalLM(cfg, maxSeq, maxSeqs,
+ * numBlocks) constructor's numBlocks (model/CausalLM.cajeta:64-94). A
+ * smaller pool holds more slots than it could at full context; the
+ * scheduler preempts the youngest running request when a request's next
+ * rows do not fit, and resumes it later by recomputing its stream.
+ * kv_f32 != 0: the K/V planes hold f32, the reference's PagedKvCache mode
+ * (model/PagedKvCache.cajeta), read by the two-pass attention (head size
+ * 64, or GQA other than 4 and 8 at 128; up to 6144 positions); other models
+ * are refused with the reason. */
+int64_t cj_engine_load_kv(const int8_t *path, int32_t ctx, int32_t max_seqs, int32_t kv_pages, int32_t kv_f32);
 int32_t cj_engine_close(int64_t eng);
 /* Up to 14 values: n_layers, hidden, n_heads, n_kv, head_dim, ffn, vocab,
  * ctx, n_experts, n_used, weight type, head type, expert ffn, and the CPU

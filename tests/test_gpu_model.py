@@ -18,17 +18,18 @@ def say(*a):
     print(*a, flush=True)
 
 
-def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1, chunk=512):
+def run_pair(pkg, path, image, prompt, n_gen, ctx, check_every=1, chunk=512, kv_f32=False):
     """Greedy-decode `prompt` + n_gen on both sides; compare every step. The
     prompt goes through each side's prefill (prefill chunks on dense head-size-
-    128 models, decode steps otherwise)."""
+    128 models, decode steps otherwise). kv_f32: both sides keep f32 K/V."""
     from oracle.gguf_reader import GgufReader, oracle_model
     r = GgufReader(image if image is not None else path)
-    om, cfg = oracle_model(r, ctx=ctx)
+    om, cfg = oracle_model(r, ctx=ctx, kv_f32=kv_f32)
     opts = pkg.EngineOptions(path)
     opts.ctx = ctx
     opts.maxSeqs = 1
     opts.prefillChunk = chunk
+    opts.kvF32 = kv_f32
     eng = pkg.LlmEngine.load(opts)
     try:
         eng.reset()
@@ -128,7 +129,7 @@ def test_prefill_chunks_are_invisible(gpu):
     assert b1 and b7, (e1, e7)
 
 
-def batch_case(gpu, path, image, prompts, steps, ctx):
+def batch_case(gpu, path, image, prompts, steps, ctx, kv_f32=False):
     """Prefill every prompt into its own slot, decode all slots together;
     the oracle decodes each sequence alone with the batch's split rule."""
     from oracle.gguf_reader import GgufReader, oracle_model
@@ -136,6 +137,7 @@ def batch_case(gpu, path, image, prompts, steps, ctx):
     opts = gpu.EngineOptions(path)
     opts.ctx = ctx
     opts.maxSeqs = n
+    opts.kvF32 = kv_f32
     eng = gpu.LlmEngine.load(opts)
     try:
         first = []
@@ -149,7 +151,7 @@ def batch_case(gpu, path, image, prompts, steps, ctx):
     r = GgufReader(image if image is not None else path)
     worst, same = 0.0, True
     for s, p in enumerate(prompts):
-        om, _ = oracle_model(r, ctx=ctx, attn_rows=n)
+        om, _ = oracle_model(r, ctx=ctx, attn_rows=n, kv_f32=kv_f32)
         t, _ = om.prefill(p, 0)
         toks, lg = [t], None
         for i in range(steps):
@@ -179,6 +181,34 @@ def test_batched_decode_parity_toy_gqa8(gpu, n):
 def synth(pkg, spec, name, seed):
     pkg.synth_gguf(spec, "mem:" + name, seed)
     return "mem:" + name, pkg.image_bytes(name)
+
+
+def test_c1_config_literal_f32_kv_greedy_parity(gpu):
+    """Benchmark configuration C1 as BASELINE.json states it: an f32 K/V cache (the
+    reference's PagedKvCache mode) — 4 layers, d 512, 8/2 heads of 64, FFN 1408,
+    V 32000, Q8_0, f32 embeddings; a 16-token prompt and 64 greedy tokens,
+    logits bit for bit against the oracle's f32-K/V decode; then 5 slots
+    decoding together in f32 K/V."""
+    say("model c1 f32 K/V")
+    path, img = synth(gpu, "c1", "t_c1f", 1234)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, 32000, 16).tolist()
+    g, o, err = run_pair(gpu, path, img, prompt, 64, 128, kv_f32=True)
+    assert g == o, "tokens differ at %d" % next(i for i, (a, b) in enumerate(zip(g, o)) if a != b)
+    assert err <= LOGIT_TOL and run_pair.bit_identical, err
+    assert len(set(g)) > 1
+    prompts = [rng.integers(0, 32000, k).tolist() for k in (16, 3, 40, 9, 25)]
+    out, err, same = batch_case(gpu, path, img, prompts, 6, 128, kv_f32=True)
+    gpu.image_free("t_c1f")
+    assert err <= LOGIT_TOL and same
+    # the split-K models keep fp16 K/V: f32 is refused by name
+    opts = gpu.EngineOptions(os.path.join(GOLD, "toy-routable.gguf"))
+    opts.ctx = 64
+    opts.maxSeqs = 1
+    opts.kvF32 = True
+    with pytest.raises(gpu.LlmException) as ex:
+        gpu.LlmEngine.load(opts)
+    assert "f32 K/V" in str(ex.value)
 
 
 def test_c1_tiny_q8_0_greedy_parity(gpu):
