@@ -1039,18 +1039,22 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     if (a.packed) pack256(x, a.per32, a.packed + (int64_t)blockIdx.x * 320, bmax);
 }
 
-// The merge as one wave per (query head, 64 output dimensions): lane d
-// merges dimension d over the head's splits in cj_attn_merge's order and
-// writes the f32 output (the consumer packs it). n_q·hd/64 workgroups of 64
-// read the partials in parallel where cj_attn_merge's n_q·hd/256 workgroups
-// each read a quarter megabyte.
-extern "C" __global__ void __launch_bounds__(64) cj_attn_merge_w(cj_merge_args a) {
-    const int lane = threadIdx.x, hd = a.head_dim, per = hd / 64;
-    const int h = blockIdx.x / per, d = (blockIdx.x % per) * 64 + lane;
+// The merge with its four sub-sums on four lanes: a workgroup of two waves
+// per (query head, 32 output dimensions); lane (j, i) of a wave, j = lane/16,
+// forms sub-sum j of dimension i — splits j, j+4, j+8, ... in ascending
+// order, the chain cj_attn_merge's sub j runs — and lane (0, i) adds the four
+// in sub order and scales by 1/Σ. A lane loads 16 partials and runs a chain
+// of 16 where the wave-per-64-dimensions form runs all 64 splits on every
+// lane; the splits' weights and sums come from LDS ordered sub-major, so a
+// lane's 16 are four 16-byte reads.
+extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args a) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, hd = a.head_dim, per = hd / 32;
+    const int h = blockIdx.x / per, j = lane >> 4, i = lane & 15;
+    const int d = (blockIdx.x % per) * 32 + 16 * wave + i;
     const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
-    float pv[ATTN_MAX_SPLITS];
+    float pv[16];
 #pragma unroll
-    for (int s2 = 0; s2 < ATTN_MAX_SPLITS; s2++) pv[s2] = pb0[s2 * (hd + 2) + d];
+    for (int k = 0; k < 16; k++) pv[k] = pb0[(4 * k + j) * (hd + 2) + d];
     const float2 ml = *(const float2 *)(pb0 + lane * (hd + 2) + hd);
     int splits = a.splits;
     if (a.state) {
@@ -1063,31 +1067,35 @@ extern "C" __global__ void __launch_bounds__(64) cj_attn_merge_w(cj_merge_args a
     const float gm = group_max<64>(mv);
     const bool on = in && ml.y > 0.0f;
     const float wt = on ? cj_expf(mv - gm) : 0.0f;
-    const uint64_t ons = __ballot(on);
-    // the splits' weights and sums through LDS, back as broadcast 16-byte
-    // reads (four splits a read instead of a lane read each)
-    __shared__ __align__(16) float sw[ATTN_MAX_SPLITS], sl[ATTN_MAX_SPLITS];
-    sw[lane] = wt;
-    sl[lane] = ml.y;
+    const uint64_t mine = __ballot(on) >> j;   // bit 4k: split 4k + j takes part
+    __shared__ __align__(16) float sw[2][ATTN_MAX_SPLITS], sl[2][ATTN_MAX_SPLITS];
+    const int si = (lane & 3) * 16 + (lane >> 2);   // split s at (s mod 4)·16 + s/4
+    sw[wave][si] = wt;
+    sl[wave][si] = ml.y;
     __builtin_amdgcn_wave_barrier();
-    float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float g = 0.0f, ac = 0.0f;
 #pragma unroll
-    for (int s0 = 0; s0 < ATTN_MAX_SPLITS; s0 += 4) {
-        const float4 w4 = *(const float4 *)&sw[s0], l4 = *(const float4 *)&sl[s0];
+    for (int k4 = 0; k4 < 4; k4++) {
+        const float4 w4 = *(const float4 *)&sw[wave][16 * j + 4 * k4];
+        const float4 l4 = *(const float4 *)&sl[wave][16 * j + 4 * k4];
         const float w[4] = {w4.x, w4.y, w4.z, w4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int s2 = s0 + j;
-            const bool use = (ons >> s2) & 1;
-            const float g2 = __fadd_rn(gl[j], __fmul_rn(w[j], lv[j]));
-            const float a2 = __fadd_rn(ac[j], __fmul_rn(pv[s2], w[j]));
-            gl[j] = use ? g2 : gl[j];
-            ac[j] = use ? a2 : ac[j];
+        for (int q = 0; q < 4; q++) {
+            const int k = 4 * k4 + q;
+            const bool use = (mine >> (4 * k)) & 1;
+            const float g2 = __fadd_rn(g, __fmul_rn(w[q], lv[q]));
+            const float a2 = __fadd_rn(ac, __fmul_rn(pv[k], w[q]));
+            g = use ? g2 : g;
+            ac = use ? a2 : ac;
         }
     }
-    const float gt = __fadd_rn(__fadd_rn(__fadd_rn(gl[0], gl[1]), gl[2]), gl[3]);
-    const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac[0], ac[1]), ac[2]), ac[3]);
-    a.out[(int64_t)h * hd + d] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
+    const float g1 = __shfl(g, i + 16), g2 = __shfl(g, i + 32), g3 = __shfl(g, i + 48);
+    const float a1 = __shfl(ac, i + 16), a2 = __shfl(ac, i + 32), a3 = __shfl(ac, i + 48);
+    if (j == 0) {
+        const float gt = __fadd_rn(__fadd_rn(__fadd_rn(g, g1), g2), g3);
+        const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac, a1), a2), a3);
+        a.out[(int64_t)h * hd + d] = __fmul_rn(tacc, __fdiv_rn(1.0f, gt));
+    }
 }
 
 // The many-row form: row r's blocks (a row is whole blocks of 256), its

@@ -677,8 +677,8 @@ int Engine::enqueue_step(int s) {
                 // partials, then the merge (a launch boundary orders them: a
                 // merge by the last workgroup of each kv head would need
                 // device-scope fences, which cost far more than the launch on
-                // this part): a wave per 64 output dimensions writing f32,
-                // which the o projection packs, or the 256-wide merge + pack
+                // this part): a lane per (output dimension, sub-sum) writing
+                // f32, which the o projection packs, or the 256-wide merge + pack
                 a.out = nullptr;
                 if (want(K_ATTN, l) && (rc = launch(attn_kernel, (uint32_t)(n_kv * 64), 256, 0, a))) return rc;
                 cj_merge_args m{};
@@ -687,7 +687,7 @@ int Engine::enqueue_step(int s) {
                 m.window = L.window;
                 if (merge_w) {
                     m.packed = nullptr;
-                    if ((rc = launch("cj_attn_merge_w", (uint32_t)(n_heads * (head_dim / 64)), 64, 0, m))) return rc;
+                    if ((rc = launch("cj_attn_merge_q", (uint32_t)(n_heads * (head_dim / 32)), 128, 0, m))) return rc;
                 } else if ((rc = launch("cj_attn_merge", (uint32_t)(((int64_t)n_heads * head_dim + 255) / 256), 256, 0, m))) {
                     return rc;
                 }

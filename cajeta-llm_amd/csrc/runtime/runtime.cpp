@@ -414,7 +414,7 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_norm_pack", "cj_norm_pack_rows", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
-        "cj_attn_merge", "cj_attn_merge_w", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
+        "cj_attn_merge", "cj_attn_merge_q", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
         "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_c16",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
