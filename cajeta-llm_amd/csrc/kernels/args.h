@@ -248,6 +248,30 @@ typedef struct {
     int32_t *status;         // set to 1 when a row's logits are not finite (may be null)
 } cj_route_args;
 
+// The rows' expert selections grouped by expert (MoeFfn.forwardRowsZeroSync
+// reads each selected expert once for all the rows that chose it).
+typedef struct {
+    const int32_t *sel;      // [n_sel] expert of selection i (= r·n_used + k)
+    int32_t *cnt;            // [n_experts] selections of each expert
+    int32_t *mem;            // [n_experts][cap] expert e's selections (any order)
+    int32_t n_sel, n_experts, cap, pad;
+} cj_moe_group_args;
+
+// A grouped MXFP4 expert product (the device Q8 form) over the selections of
+// each expert: workgroup (row tile, expert) streams its 64 weight rows once
+// and dots them with every member selection's per-32 activation codes.
+typedef struct {
+    const uint8_t *w;        // expert bank of prepared MXFP4 rows: expert e at w + e·expert_bytes
+    const uint8_t *xp;       // input per-32 packs (320-byte blocks), xp_stride bytes a row
+    uint8_t *outp;           // SiLU·up form: each selection's activation as per-32 packs, outp_stride bytes apart
+    float *y;                // store form: each selection's outputs, y_stride floats apart
+    const int32_t *cnt, *mem;   // from cj_moe_group
+    int64_t expert_bytes, row_bytes, rows, cols;
+    int64_t xp_stride, outp_stride, y_stride;
+    int32_t cap, x_per;      // selection i reads input row i / x_per
+    int32_t glu_form, act_n;
+} cj_moe_grp_args;
+
 // routerTopKKernel's arguments (io/QuantKernel.cajeta:39850-39960): the
 // router mat-vec of one f32 row and its top-k in one launch.
 typedef struct {

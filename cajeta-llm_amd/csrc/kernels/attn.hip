@@ -457,6 +457,60 @@ DEV void scores_body(const cj_attn_args &a, int bx, int h) {
     a.part[(int64_t)h * a.splits + t] = __fmul_rn(p[0], a.scale);
 }
 
+// The scores of all the query heads of one kv head (at most 16): a lane a
+// position whose K row is read once and kept in registers while it is dotted
+// with each head's q (staged in LDS) in scores_body's order — the 32 lane
+// partials p_i = Σ q[d]·k[d] over d = i, i+32, ... from 0, the fixed
+// pairwise tree, ·scale. Grid y is row · n_kv + kv head.
+template <int HD>
+DEV void scores_grp_body(const cj_attn_args &a, int bx, int kvh) {
+    __shared__ __align__(16) float qs[16][HD];
+    int count, from;
+    attn_window(a, count, from);
+    const int grp = a.n_q / a.n_kv;
+    const int t = bx * 256 + threadIdx.x;
+    if (bx * 256 >= count) return;      // the whole workgroup idles past count
+    const int pos = from + min(t, count - 1);
+    const int page = a.pgtab[a.pg_base + (pos >> 6)];
+    for (int i = threadIdx.x; i < grp * HD; i += 256) qs[i / HD][i % HD] = a.q[(int64_t)kvh * grp * HD + i];
+    __syncthreads();
+    if (t >= count) return;
+    const uint16_t *kr = a.kc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD;
+    float k[HD];
+#pragma unroll
+    for (int j = 0; j < HD / 8; j++) {
+        const u32x4 v = *(const u32x4 *)(kr + 8 * j);
+        k[8 * j + 0] = h2f(v.x); k[8 * j + 1] = h2f(v.x >> 16);
+        k[8 * j + 2] = h2f(v.y); k[8 * j + 3] = h2f(v.y >> 16);
+        k[8 * j + 4] = h2f(v.z); k[8 * j + 5] = h2f(v.z >> 16);
+        k[8 * j + 6] = h2f(v.w); k[8 * j + 7] = h2f(v.w >> 16);
+    }
+#pragma unroll 1
+    for (int hh = 0; hh < grp; hh++) {
+        const float *qh = qs[hh];
+        float p[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) p[i] = 0.0f;
+#pragma unroll
+        for (int d0 = 0; d0 < HD; d0 += 32) {
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 qv = *(const float4 *)(qh + d0 + i);
+                p[i] = __fadd_rn(p[i], __fmul_rn(qv.x, k[d0 + i]));
+                p[i + 1] = __fadd_rn(p[i + 1], __fmul_rn(qv.y, k[d0 + i + 1]));
+                p[i + 2] = __fadd_rn(p[i + 2], __fmul_rn(qv.z, k[d0 + i + 2]));
+                p[i + 3] = __fadd_rn(p[i + 3], __fmul_rn(qv.w, k[d0 + i + 3]));
+            }
+        }
+#pragma unroll
+        for (int m = 16; m > 0; m >>= 1) {
+#pragma unroll
+            for (int i = 0; i < m; i++) p[i] = __fadd_rn(p[i], p[i + m]);
+        }
+        a.part[(int64_t)(kvh * grp + hh) * a.splits + t] = __fmul_rn(p[0], a.scale);
+    }
+}
+
 #define COMBINE_PAGES 2048   // K/V pages a two-pass span covers (131072 positions)
 
 // A combine producer's item of tile I: positions I·T + 4·tq + k (k < 4),
@@ -811,6 +865,202 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     if (l < DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
+// The combine for a group of query heads sharing a kv head: a workgroup of
+// 256 per 256/HD query heads (all HD output dimensions of each), so the
+// group's V rows are staged once for all its heads. The operations and their
+// order are combine_body's:
+//   softmax  two heads at a time, lanes 0..127 and 128..255 each the
+//            reference's 128: the max (exact in any grouping), then lane l
+//            forms e_t = exp(s_t − max) for t = l, l+128, ... in order, adds
+//            them in that order and writes e_t over s_t (each score row is
+//            this workgroup's alone), the 128 sums folded by the
+//            stride-halving tree;
+//   p·V      lane (head j, dimension d) runs its ascending-t chain
+//            acc + e_t·v_t[d] (the product rounded, then added) over tiles of
+//            CGT positions whose weights and V rows are staged in LDS, the
+//            next tile's loads in flight during the current tile's chain;
+//            out = acc·(1/Σ).
+#define CGT(HD) (16384 / (HD))   // positions a tile: 32 KB of V rows
+
+template <int HD>
+DEV void combine_grp_body(const cj_attn_args &a, int hq) {
+    constexpr int HPW = 256 / HD, T = CGT(HD), VCH = T * HD / 8 / 256;   // 16-byte V chunks a thread a tile
+    __shared__ float tree[256];
+    __shared__ float gmax[4];
+    __shared__ float rsum[HPW];
+    __shared__ int pgs[COMBINE_PAGES];
+    __shared__ __align__(16) float es[2][HPW][T];
+    __shared__ __align__(16) uint16_t vs[2][T][HD];
+    int count, from;
+    attn_window(a, count, from);
+    const int t = threadIdx.x, l = t & 127, g = t >> 7;
+    const int grp = a.n_q / a.n_kv, h0 = hq * HPW, kvh = h0 / grp;
+    const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
+    for (int j = t; j < npg; j += 256) pgs[j] = a.pgtab[a.pg_base + (from >> 6) + j];
+    for (int j0 = 0; j0 < HPW; j0 += 2) {
+        float *sc = a.part + (int64_t)(h0 + j0 + g) * a.splits;
+        // a lane's scores in one round of loads where the span allows
+        // (128·PK positions), else in rounds of 8 a lane
+        constexpr int PK = 40;
+        const bool one = count <= 128 * PK;
+        float v[PK];
+        float mx = -3.0e38f;
+        if (one) {
+#pragma unroll
+            for (int k = 0; k < PK; k++) v[k] = sc[min(l + 128 * k, count - 1)];
+#pragma unroll
+            for (int k = 0; k < PK; k++) if (l + 128 * k < count && v[k] > mx) mx = v[k];
+        } else {
+            for (int b = 0; b < count; b += 128 * 8) {
+                float u[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) u[k] = sc[min(b + l + 128 * k, count - 1)];
+#pragma unroll
+                for (int k = 0; k < 8; k++) if (b + l + 128 * k < count && u[k] > mx) mx = u[k];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float y = __shfl_xor(mx, o);
+            if (y > mx) mx = y;
+        }
+        if ((t & 63) == 0) gmax[t >> 6] = mx;
+        __syncthreads();
+        const float m = gmax[2 * g + 1] > gmax[2 * g] ? gmax[2 * g + 1] : gmax[2 * g];
+        float s = 0.0f;
+        if (one) {
+#pragma unroll
+            for (int k = 0; k < PK; k++) {
+                const int p = l + 128 * k;
+                if (p < count) {
+                    const float e = cj_expf(v[k] - m);
+                    sc[p] = e;
+                    s = __fadd_rn(s, e);
+                }
+            }
+        } else {
+            for (int b = 0; b < count; b += 128 * 8) {
+                float u[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) u[k] = sc[min(b + l + 128 * k, count - 1)];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int p = b + l + 128 * k;
+                    if (p < count) {
+                        const float e = cj_expf(u[k] - m);
+                        sc[p] = e;
+                        s = __fadd_rn(s, e);
+                    }
+                }
+            }
+        }
+        tree[t] = s;
+        __syncthreads();
+        if (l < 64) {
+            float v2 = __fadd_rn(tree[128 * g + l], tree[128 * g + l + 64]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+            if (l == 0) rsum[j0 + g] = __fdiv_rn(1.0f, v2);
+        }
+        __syncthreads();   // the weights written over the scores are visible to the workgroup
+    }
+
+    // p·V over tiles: the weights of the HPW heads (a float4 a thread) and the
+    // V rows (VCH 16-byte chunks a thread), loaded a tile ahead
+    const int ntiles = (count + T - 1) / T;
+    float4 er;
+    u32x4 vr[VCH];
+    // HPW·T weights a tile, four a thread for the first HPW·T/4 threads (the
+    // rest repeat the last head's, unstored); the score rows are only
+    // 4-byte aligned, so four word loads
+    constexpr int EF = HPW * T / 4;
+    auto load = [&](int i) {
+        const int jj = min(t / (T / 4), HPW - 1), o = 4 * (t % (T / 4));
+        const float *er0 = a.part + (int64_t)(h0 + jj) * a.splits;
+        const int q0 = i * T + o;
+        er.x = er0[min(q0, a.splits - 1)];
+        er.y = er0[min(q0 + 1, a.splits - 1)];
+        er.z = er0[min(q0 + 2, a.splits - 1)];
+        er.w = er0[min(q0 + 3, a.splits - 1)];
+#pragma unroll
+        for (int k = 0; k < VCH; k++) {
+            const int c = t + 256 * k, p = c / (HD / 8), j = c % (HD / 8);
+            const int pos = from + min(i * T + p, count - 1);
+            const int page = pgs[(pos >> 6) - (from >> 6)];
+            vr[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j);
+        }
+    };
+    auto store = [&](int buf) {
+        const int jj = min(t / (T / 4), HPW - 1), o = 4 * (t % (T / 4));
+        if (t < EF) *(float4 *)&es[buf][jj][o] = er;
+#pragma unroll
+        for (int k = 0; k < VCH; k++) {
+            const int c = t + 256 * k;
+            *(u32x4 *)&vs[buf][c / (HD / 8)][8 * (c % (HD / 8))] = vr[k];
+        }
+    };
+    const int jj = t / HD, d = t % HD;
+    float acc = 0.0f;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int i = 0; i < ntiles; i++) {
+        load(min(i + 1, ntiles - 1));
+        const int buf = i & 1, n = min(T, count - i * T);
+        const float *ew = &es[buf][jj][0];
+        const uint16_t *vw = &vs[buf][0][d];
+        // blocks of 16 positions, the next block's LDS reads issued before
+        // the current block's adds (one wave a SIMD leaves nothing else to
+        // cover their latency); the product e_t·v_t[d] by the mixed multiply
+        // with a −0 addend (the rounded product), then the add
+        const int nb16 = n / 16;
+        float4 ea[4], eb[4];
+        uint32_t va[16], vb[16];
+        auto rd = [&](float4 (&e)[4], uint32_t (&v)[16], int blk) {
+            const int p0 = 16 * min(blk, nb16 - 1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) e[q] = *(const float4 *)(ew + p0 + 4 * q);
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = vw[(p0 + k) * HD];
+        };
+        auto run = [&](const float4 (&e)[4], const uint32_t (&v)[16]) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                acc = __fadd_rn(acc, mul_h16lo(v[4 * q], e[q].x));
+                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 1], e[q].y));
+                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 2], e[q].z));
+                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 3], e[q].w));
+            }
+        };
+        if (nb16 > 0) {
+            rd(ea, va, 0);
+            for (int b = 0; b < nb16; b += 2) {
+                rd(eb, vb, b + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                run(ea, va);
+                if (b + 1 >= nb16) break;
+                rd(ea, va, b + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                run(eb, vb);
+            }
+        }
+        int p = 16 * nb16;
+        for (; p + 4 <= n; p += 4) {
+            const float4 e4 = *(const float4 *)(ew + p);
+            const float v0 = h2f(vw[p * HD]), v1 = h2f(vw[(p + 1) * HD]);
+            const float v2 = h2f(vw[(p + 2) * HD]), v3 = h2f(vw[(p + 3) * HD]);
+            acc = __fadd_rn(acc, __fmul_rn(e4.x, v0));
+            acc = __fadd_rn(acc, __fmul_rn(e4.y, v1));
+            acc = __fadd_rn(acc, __fmul_rn(e4.z, v2));
+            acc = __fadd_rn(acc, __fmul_rn(e4.w, v3));
+        }
+        for (; p < n; p++) acc = __fadd_rn(acc, __fmul_rn(ew[p], h2f(vw[p * HD])));
+        store(buf ^ 1);
+        __syncthreads();
+    }
+    a.out[(int64_t)(h0 + jj) * HD + d] = __fmul_rn(acc, rsum[jj]);
+}
+
 // Row r of a many-row launch as the one-row kernels see it: its sequence
 // slot's pages and position, its q, output and score rows.
 DEV cj_attn_args attn_row_args(const cj_attn_args &a, int r) {
@@ -858,6 +1108,20 @@ TWO_PASS_F32(128)
     }
 TWO_PASS_ROWS(64)
 TWO_PASS_ROWS(128)
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_grp_rows_h64(cj_attn_args a) {
+    scores_grp_body<64>(attn_row_args(a, blockIdx.y / a.n_kv), blockIdx.x, blockIdx.y % a.n_kv);
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_grp_rows_h128(cj_attn_args a) {
+    scores_grp_body<128>(attn_row_args(a, blockIdx.y / a.n_kv), blockIdx.x, blockIdx.y % a.n_kv);
+}
+// the grouped combine: grid x is the head group (256/HD query heads of one
+// kv head), y the row
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_grp_rows_h64(cj_attn_args a) {
+    combine_grp_body<64>(attn_row_args(a, blockIdx.y), blockIdx.x);
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_grp_rows_h128(cj_attn_args a) {
+    combine_grp_body<128>(attn_row_args(a, blockIdx.y), blockIdx.x);
+}
 
 // The two-pass form in one launch for spans of at most FUSED_SPAN(HD)
 // positions (sliding windows, small contexts): a workgroup per query head

@@ -1408,6 +1408,200 @@ MXQ8_KBS(a, CJ_EPI_ACCUM, 4)
 MXQ8_KBS(g, CJ_EPI_GLU, 2)
 MXQ8_KBS(g, CJ_EPI_GLU, 4)
 
+// ------------------------------------------- MXFP4 experts grouped by expert
+
+// The rows' selections by expert: a counter an expert in LDS, each selection
+// appended to its expert's list (the order inside a list changes no result:
+// every selection's products and epilogue are its own).
+extern "C" __global__ void __launch_bounds__(256) cj_moe_group(cj_moe_group_args a) {
+    __shared__ int c[256];
+    const int t = threadIdx.x;
+    for (int e = t; e < a.n_experts; e += 256) c[e] = 0;
+    __syncthreads();
+    for (int i = t; i < a.n_sel; i += 256) {
+        const int e = a.sel[i];
+        if (e >= 0 && e < a.n_experts) {
+            const int p = atomicAdd(&c[e], 1);
+            if (p < a.cap) a.mem[(int64_t)e * a.cap + p] = i;
+        }
+    }
+    __syncthreads();
+    for (int e = t; e < a.n_experts; e += 256) a.cnt[e] = min(c[e], a.cap);
+}
+
+#define GRP_CC 16   // member selections a column chunk
+#define GRP_RT 64   // weight rows a workgroup (gate|up: one 32-block of the activation)
+#define GRP_RS (GRP_CC + 1)
+
+// Workgroup (row tile, expert e): the 64 rows run as four passes of 16 (a
+// 32-lane half-wave two rows, as cj_gemv_mxq8_*; rows of at most 32·KB
+// blocks, one sweep), the next pass's weights in flight during the current
+// one's arithmetic. Each 32-block's E2M1 codes are
+// decoded once and dotted with every member's q8 codes, so a member's row
+// value is cj_gemv_mxq8_*'s bit for bit: acc = acc + (s·d_w)·d_x over the
+// lane's blocks in order, the half-wave's xor butterfly. Members run in
+// chunks of 16 (their codes staged in LDS); a chunk past the first re-reads
+// the tile (L2). EPI: CJ_EPI_GLU — SiLU·up of each gate/up row pair, then
+// the member's 32 activation values quantized per 32 (mxfp4QuantActKernel's
+// arithmetic) into its pack; CJ_EPI_STORE — the row values.
+template <int EPI, int KB>
+DEV void moe_grp_body(const cj_moe_grp_args &a) {
+    constexpr int RW = 2, PASSES = GRP_RT / (8 * RW);
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int mi[GRP_CC];
+    const int e = blockIdx.y;
+    const int c = a.cnt[e];
+    if (c == 0) return;
+    const int t = threadIdx.x, hw = t >> 5, hl = t & 31;
+    const int nb = (int)(a.cols / 32);
+    const int cpad = (int)((a.cols + 15) & ~15), nbp = (nb + 3) & ~3;
+    int8_t *xq = (int8_t *)smem;
+    float *xd = (float *)(smem + GRP_CC * cpad);
+    float *res = xd + GRP_CC * nbp;
+    const uint8_t *W = a.w + (int64_t)e * a.expert_bytes;
+    const int64_t row0 = (int64_t)blockIdx.x * GRP_RT;
+
+    auto fetch = [&](u32x4 (&wv)[RW][KB], uint32_t (&sc)[RW][KB], int p) {
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int64_t r = min(row0 + p * 8 * RW + hw * RW + i, a.rows - 1);
+            const uint8_t *wr = W + r * a.row_bytes;
+#pragma unroll
+            for (int k = 0; k < KB; k++) {
+                const int b = min(hl + 32 * k, nb - 1);
+                wv[i][k] = __builtin_nontemporal_load((const u32x4 *)(wr + 16 * b));
+                sc[i][k] = wr[16 * nb + b];
+            }
+        }
+    };
+    for (int j0 = 0; j0 < c; j0 += GRP_CC) {
+        const int nc = min(GRP_CC, c - j0);
+        __syncthreads();   // the previous chunk's LDS reads are done
+        if (t < nc) mi[t] = a.mem[(int64_t)e * a.cap + j0 + t];
+        __syncthreads();
+        // the chunk's codes and scales: 32-block b of a pack row at
+        // (b/8)·320 + (b%8)·32, its scale at (b/8)·320 + 288 + 4·(b%8)
+        for (int idx = t; idx < nc * nb * 2; idx += 256) {
+            const int jj = idx / (nb * 2), b = (idx % (nb * 2)) >> 1, h = idx & 1;
+            const uint8_t *row = a.xp + (int64_t)(mi[jj] / a.x_per) * a.xp_stride + (b >> 3) * 320;
+            *(u32x4 *)(xq + jj * cpad + 32 * b + 16 * h) = *(const u32x4 *)(row + (b & 7) * 32 + 16 * h);
+            if (!h) xd[jj * nbp + b] = *(const float *)(row + 288 + 4 * (b & 7));
+        }
+        __syncthreads();
+
+        // one pass: its blocks decoded once, then the members one at a time
+        // (a member's two row values finish before the next member starts)
+        auto compute = [&](const u32x4 (&wv)[RW][KB], const uint32_t (&sc)[RW][KB], int p) {
+            int dw[RW][KB][8];
+            float ws[RW][KB];
+#pragma unroll
+            for (int i = 0; i < RW; i++)
+#pragma unroll
+                for (int k = 0; k < KB; k++) {
+                    const u32x4 w = wv[i][k];
+                    dw[i][k][0] = (int)e2m1_x4(w.x); dw[i][k][1] = (int)e2m1_x4(w.y);
+                    dw[i][k][2] = (int)e2m1_x4(w.z); dw[i][k][3] = (int)e2m1_x4(w.w);
+                    dw[i][k][4] = (int)e2m1_x4(w.x >> 4); dw[i][k][5] = (int)e2m1_x4(w.y >> 4);
+                    dw[i][k][6] = (int)e2m1_x4(w.z >> 4); dw[i][k][7] = (int)e2m1_x4(w.w >> 4);
+                    ws[i][k] = mxfp4_scale(sc[i][k]);
+                }
+#pragma unroll 1
+            for (int jj = 0; jj < nc; jj++) {
+                float acc[RW];
+#pragma unroll
+                for (int i = 0; i < RW; i++) acc[i] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KB; k++) {
+                    const int b = hl + 32 * k, bc = min(b, nb - 1);
+                    const u32x4 x0 = *(const u32x4 *)(xq + jj * cpad + 32 * bc);
+                    const u32x4 x1 = *(const u32x4 *)(xq + jj * cpad + 32 * bc + 16);
+                    const float xs = xd[jj * nbp + bc];
+#pragma unroll
+                    for (int i = 0; i < RW; i++) {
+                        int sd = 0;
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][0], (int)x0.x, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][1], (int)x0.y, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][2], (int)x0.z, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][3], (int)x0.w, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][4], (int)x1.x, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][5], (int)x1.y, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][6], (int)x1.z, sd, false);
+                        sd = __builtin_amdgcn_sdot4(dw[i][k][7], (int)x1.w, sd, false);
+                        const float term = __fmul_rn(__fmul_rn((float)sd, ws[i][k]), xs);
+                        if (b < nb) acc[i] = __fadd_rn(acc[i], term);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < RW; i++) {
+                    float v = acc[i];
+#pragma unroll
+                    for (int m = 16; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_xor(v, m));
+                    if (hl == 0) res[(p * 8 * RW + hw * RW + i) * GRP_RS + jj] = v;
+                }
+            }
+        };
+        // two passes in flight: fetch 0 and 1, then compute one and fetch
+        // the one two ahead
+        u32x4 wa[RW][KB], wb[RW][KB];
+        uint32_t sa[RW][KB], sb[RW][KB];
+        fetch(wa, sa, 0);
+        fetch(wb, sb, 1);
+#pragma unroll
+        for (int p = 0; p + 2 < PASSES; p += 2) {
+            compute(wa, sa, p);
+            fetch(wa, sa, p + 2);
+            compute(wb, sb, p + 1);
+            fetch(wb, sb, p + 3);
+        }
+        compute(wa, sa, PASSES - 2);
+        compute(wb, sb, PASSES - 1);
+        __syncthreads();
+
+        if (EPI == CJ_EPI_GLU) {
+            // output o (rows 2o, 2o+1) of member jj: thread t is (jj = t/32 + jb, o = t%32);
+            // the 32 values of a member are one 32-block of its activation
+            const int64_t ab = row0 / GRP_RT;
+#pragma unroll 1
+            for (int jb = 0; jb < nc; jb += 8) {
+                const int jj = jb + (t >> 5), o = t & 31;
+                const bool on = jj < nc;
+                const int64_t ai = row0 / 2 + o;
+                float v = 0.0f;
+                if (on && ai < a.act_n) v = glu_value(a.glu_form, ai, a.act_n, res[(2 * o) * GRP_RS + jj], res[(2 * o + 1) * GRP_RS + jj]);
+                float bm = fabsf(v);
+#pragma unroll
+                for (int m = 16; m > 0; m >>= 1) bm = fmaxf(bm, __shfl_xor(bm, m));
+                const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
+                const int q = round_away(__fmul_rn(v, inv));
+                int sq = q;
+#pragma unroll
+                for (int m = 16; m > 0; m >>= 1) sq += __shfl_xor(sq, m);
+                if (on) {
+                    uint8_t *ob = a.outp + (int64_t)mi[jj] * a.outp_stride + (ab >> 3) * 320;
+                    ob[(ab & 7) * 32 + o] = (uint8_t)(int8_t)q;
+                    if (o == 0) {
+                        *(int32_t *)(ob + 256 + 4 * (ab & 7)) = sq;
+                        *(float *)(ob + 288 + 4 * (ab & 7)) = __fdiv_rn(bm, 127.0f);
+                    }
+                }
+            }
+        } else {
+            for (int idx = t; idx < nc * GRP_RT; idx += 256) {
+                const int jj = idx / GRP_RT, rl = idx % GRP_RT;
+                const int64_t r = row0 + rl;
+                if (r < a.rows) a.y[(int64_t)mi[jj] * a.y_stride + r] = res[rl * GRP_RS + jj];
+            }
+        }
+    }
+}
+
+#define MOE_GRP_KERNEL(E, EPI, KB)                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) cj_moe_mxq8_##E##_k##KB(cj_moe_grp_args a) {      \
+        moe_grp_body<EPI, KB>(a);                                                                       \
+    }
+MOE_GRP_KERNEL(g, CJ_EPI_GLU, 1) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 2) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 3) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 4)
+MOE_GRP_KERNEL(s, CJ_EPI_STORE, 1) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 2) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 3) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 4)
+
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)
 GEMV_FAMILY_N2(cj_gemv_q80, CJ_Q8_0)

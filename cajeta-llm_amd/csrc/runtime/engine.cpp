@@ -178,6 +178,8 @@ struct Engine {
     // selection list (the router's indirection: every row reads one weight)
     float *r_xn = nullptr, *r_moe_logits = nullptr, *r_moe_w = nullptr, *r_act = nullptr, *r_moe_y = nullptr;
     int32_t *r_moe_sel = nullptr, *r_zero_sel = nullptr;
+    int32_t *r_grp_cnt = nullptr, *r_grp_mem = nullptr;   // the rows' selections grouped by expert
+    uint8_t *r_exp_pack = nullptr;                         // each selection's SiLU·up as per-32 packs
     float *r_logits = nullptr, *r_part = nullptr, *r_pv = nullptr;
     int32_t *r_pi = nullptr, *r_tab_pf = nullptr, *r_tab_b = nullptr;
     uint8_t *r_xp = nullptr, *r_ap = nullptr, *r_actp = nullptr;
@@ -600,7 +602,11 @@ int Engine::rows_alloc(int cap) {
         r_act = (float *)alloc((size_t)(sels * expert_ffn * 4 + 1024));
         r_moe_y = (float *)alloc((size_t)(sels * hidden * 4));
         r_zero_sel = (int32_t *)alloc((size_t)(cap * 4));
-        if (!r_xn || !r_moe_logits || !r_moe_sel || !r_moe_w || !r_act || !r_moe_y || !r_zero_sel)
+        r_grp_cnt = (int32_t *)alloc((size_t)std::max(1, n_experts) * 4);
+        r_grp_mem = (int32_t *)alloc((size_t)std::max(1, n_experts) * sels * 4);
+        r_exp_pack = (uint8_t *)alloc((size_t)(sels * (((int64_t)expert_ffn + 255) / 256 * 320)));
+        if (!r_xn || !r_moe_logits || !r_moe_sel || !r_moe_w || !r_act || !r_moe_y || !r_zero_sel || !r_grp_cnt ||
+            !r_grp_mem || !r_exp_pack)
             return fail(CJ_ERR_HIP, "model: out of device memory (MoE row buffers for %d rows)", cap);
         CJ_HIP(hipMemset(r_zero_sel, 0, (size_t)(cap * 4)));
     }
@@ -912,10 +918,16 @@ int Engine::rows_moe(const Layer &L, int n) {
     int rc;
     const int64_t npad = ((int64_t)hidden + 255) / 256 * 256, hb = npad / 256 * 320;
     const int sels = n * n_used;
+    // MXFP4 banks read each selected expert once for all its rows: the rows'
+    // per-32 packs are the codes the device Q8 form quantizes (the same
+    // per-32 maximum, 127/max, round-half-away, max/127)
+    const bool grouped = L.gu_exps.type == CJ_MXFP4 && L.down_exps.type == CJ_MXFP4 && n_experts <= 256 &&
+                         n <= rows_cap && hidden % 32 == 0 && expert_ffn % 32 == 0 && hidden <= 4096 &&
+                         expert_ffn <= 4096;
     {
         cj_pack_args p{};
         p.out = r_xp; p.x = r_hs; p.w = L.ffn_norm; p.xout = r_xn; p.n = hidden; p.npad = npad; p.rows = n;
-        p.eps = eps; p.form = 0; p.per32 = L.gu_exps.type == CJ_Q8_0; p.do_norm = 1;
+        p.eps = eps; p.form = 0; p.per32 = L.gu_exps.type == CJ_Q8_0 || grouped; p.do_norm = 1;
         if ((rc = launch_norm_pack_rows(p, n))) return rc;
     }
     {   // router logits of every row: the indirection's copies all read the router (expert_bytes 0)
@@ -930,6 +942,35 @@ int Engine::rows_moe(const Layer &L, int n) {
         // of the rows' many workgroups would wait out its row's route
         cj_route_args a{r_moe_logits, r_moe_sel, r_moe_w, n_experts, n_used, norm_topk, n, w_scale, 0, route_status};
         if ((rc = launch("cj_moe_route", (uint32_t)n, 64, 0, a))) return rc;
+    }
+    if (grouped) {
+        cj_moe_group_args g{r_moe_sel, r_grp_cnt, r_grp_mem, sels, n_experts, sels, 0};
+        if ((rc = launch("cj_moe_group", 1, 256, 0, g))) return rc;
+        const int64_t efb = ((int64_t)expert_ffn + 255) / 256 * 320;
+        auto grp = [&](const char *form, cj_moe_grp_args &q) {
+            const int nbq = (int)(q.cols / 32), kb = std::min(4, std::max(1, (nbq + 31) / 32));
+            const uint32_t lds = (uint32_t)(16 * ((q.cols + 15) & ~15) + 16 * ((nbq + 3) & ~3) * 4 + 64 * 17 * 4);
+            char kname[40];
+            snprintf(kname, sizeof kname, "cj_moe_mxq8_%s_k%d", form, kb);
+            return launch2(kname, (uint32_t)((q.rows + 63) / 64), (uint32_t)n_experts, 256, lds, q);
+        };
+        {   // gate|up + SiLU·up of each selection (r, k) = r·n_used + k over row r, into its pack
+            cj_moe_grp_args q{};
+            q.w = (const uint8_t *)L.gu_exps.p; q.xp = r_xp; q.outp = r_exp_pack; q.cnt = r_grp_cnt; q.mem = r_grp_mem;
+            q.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes; q.row_bytes = L.gu_exps.row_bytes;
+            q.rows = 2 * (int64_t)expert_ffn; q.cols = hidden; q.xp_stride = hb; q.outp_stride = efb; q.cap = sels;
+            q.x_per = n_used; q.glu_form = 0; q.act_n = expert_ffn;
+            if ((rc = grp("g", q))) return rc;
+        }
+        {   // down of every selection
+            cj_moe_grp_args q{};
+            q.w = (const uint8_t *)L.down_exps.p; q.xp = r_exp_pack; q.y = r_moe_y; q.cnt = r_grp_cnt; q.mem = r_grp_mem;
+            q.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes; q.row_bytes = L.down_exps.row_bytes;
+            q.rows = hidden; q.cols = expert_ffn; q.xp_stride = efb; q.y_stride = hidden; q.cap = sels; q.x_per = 1;
+            if ((rc = grp("s", q))) return rc;
+        }
+        cj_combine_args c{r_hs, r_moe_y, r_moe_w, hidden, n_used};
+        return launch2("cj_moe_combine", (uint32_t)((hidden + 255) / 256), (uint32_t)n, 256, 0, c);
     }
     {   // gate|up + SiLU·up of selection (r, k) = r·n_used + k over row r
         cj_gemv_args a{};
@@ -1009,11 +1050,25 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
                 snprintf(kname, sizeof kname, "cj_attn_fused_rows_h%d", head_dim);
                 if ((rc = launch2(kname, (uint32_t)n_heads, (uint32_t)n, 256, 0, a))) return rc;
             } else {
-                snprintf(kname, sizeof kname, "cj_attn_scores_rows_%sh%d", kvs, head_dim);
-                if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_heads), 256, 0, a)))
-                    return rc;
-                snprintf(kname, sizeof kname, "cj_attn_combine_rows_%sh%d", kvs, head_dim);
-                if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;
+                if (!kv_f32 && n_heads / n_kv <= 16 && !getenv("CJ_SCORES_OLD")) {
+                    // a lane a position, its K row read once for the kv head's query heads
+                    snprintf(kname, sizeof kname, "cj_attn_scores_grp_rows_h%d", head_dim);
+                    if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_kv), 256, 0, a)))
+                        return rc;
+                } else {
+                    snprintf(kname, sizeof kname, "cj_attn_scores_rows_%sh%d", kvs, head_dim);
+                    if ((rc = launch2(kname, (uint32_t)((span + 255) / 256), (uint32_t)(n * n_heads), 256, 0, a)))
+                        return rc;
+                }
+                const int hpw = 256 / head_dim;
+                if (!kv_f32 && (n_heads / n_kv) % hpw == 0 && !getenv("CJ_COMBINE_OLD")) {
+                    // a workgroup per kv head's group of 256/hd query heads: V staged once for them
+                    snprintf(kname, sizeof kname, "cj_attn_combine_grp_rows_h%d", head_dim);
+                    if ((rc = launch2(kname, (uint32_t)(n_heads / hpw), (uint32_t)n, 256, 0, a))) return rc;
+                } else {
+                    snprintf(kname, sizeof kname, "cj_attn_combine_rows_%sh%d", kvs, head_dim);
+                    if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;
+                }
             }
             if ((rc = rows_pack(r_attn, qd, L.o.type == CJ_Q8_0, n))) return rc;
         } else {

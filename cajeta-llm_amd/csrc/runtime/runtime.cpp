@@ -414,14 +414,15 @@ int32_t cj_init(int32_t device) {
         "cj_pack", "cj_norm_pack", "cj_norm_pack_rows", "cj_copy", "cj_glu", "cj_add", "cj_dequant", "cj_prepare", "cj_embed", "cj_argmax",
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
-        "cj_attn_merge", "cj_attn_merge_q", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
+        "cj_attn_merge", "cj_attn_merge_q", "cj_moe_group", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
         "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_c16",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
         "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8", "cj_attn_merge_rows",
         "cj_attn_prefill_h128_g1", "cj_attn_prefill_h128_g2", "cj_attn_prefill_h128_g4", "cj_attn_prefill_h128_g8",
         "cj_attn_scores_rows_h64", "cj_attn_scores_rows_h128", "cj_attn_combine_rows_h64", "cj_attn_combine_rows_h128",
-        "cj_attn_fused_rows_h64", "cj_attn_fused_rows_h128",
+        "cj_attn_fused_rows_h64", "cj_attn_fused_rows_h128", "cj_attn_combine_grp_rows_h64", "cj_attn_combine_grp_rows_h128",
+        "cj_attn_scores_grp_rows_h64", "cj_attn_scores_grp_rows_h128",
         "cj_attn_scores_f32_h64", "cj_attn_scores_f32_h128", "cj_attn_combine_f32_h64", "cj_attn_combine_f32_h128",
         "cj_attn_scores_rows_f32_h64", "cj_attn_scores_rows_f32_h128", "cj_attn_combine_rows_f32_h64",
         "cj_attn_combine_rows_f32_h128",
@@ -430,6 +431,13 @@ int32_t cj_init(int32_t device) {
         hipFunction_t f;
         if (hipModuleGetFunction(&f, g.module, k) == hipSuccess) g.fns[k] = f;
     }
+    // MXFP4 experts grouped by expert: epilogue {g, s} × blocks a lane a sweep
+    for (const char *e : {"g", "s"})
+        for (const char *kb : {"1", "2", "3", "4"}) {
+            const std::string k = std::string("cj_moe_mxq8_") + e + "_k" + kb;
+            hipFunction_t f;
+            if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+        }
     // MXFP4 × q8: epilogue {s, a, g} × blocks a lane a sweep
     for (const char *e : {"s", "a", "g"})
         for (const char *kb : {"1", "2", "3", "4"})
