@@ -725,13 +725,16 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
     const bool elds = count <= COMBINE_ES;
     float s = 0.0f;
     if (l < 128) {
+        // every slot's exp formed (past count a repeat, unused), then the
+        // ordered sum
+#pragma unroll
+        for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m);
 #pragma unroll
         for (int k = 0; k < PK; k++) {
             const int t = l + 128 * k;
             if (t < count) {
-                const float e = cj_expf(v[k] - m);
-                if (elds) es[t] = e;
-                s = __fadd_rn(s, e);
+                if (elds) es[t] = v[k];
+                s = __fadd_rn(s, v[k]);
             }
         }
         for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
@@ -890,7 +893,11 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
     __shared__ float rsum[HPW];
     __shared__ int pgs[COMBINE_PAGES];
     __shared__ __align__(16) float es[2][HPW][T];
-    __shared__ __align__(16) uint16_t vs[2][T][HD];
+    // V of a tile transposed, [dimension][position], rows VR halves apart
+    // (16 bytes past a multiple of 256: 16 lanes' 16-byte reads of 16 rows
+    // cover the 64 banks once)
+    constexpr int VR = T + 8;
+    __shared__ __align__(16) uint16_t vs[2][HD * VR];
     int count, from;
     attn_window(a, count, from);
     const int t = threadIdx.x, l = t & 127, g = t >> 7;
@@ -901,7 +908,7 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
         float *sc = a.part + (int64_t)(h0 + j0 + g) * a.splits;
         // a lane's scores in one round of loads where the span allows
         // (128·PK positions), else in rounds of 8 a lane
-        constexpr int PK = 40;
+        constexpr int PK = 36;
         const bool one = count <= 128 * PK;
         float v[PK];
         float mx = -3.0e38f;
@@ -929,13 +936,16 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
         const float m = gmax[2 * g + 1] > gmax[2 * g] ? gmax[2 * g + 1] : gmax[2 * g];
         float s = 0.0f;
         if (one) {
+            // every slot's exp formed (past count a repeat, unused), then the
+            // ordered sum and the stores
+#pragma unroll
+            for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m);
 #pragma unroll
             for (int k = 0; k < PK; k++) {
                 const int p = l + 128 * k;
                 if (p < count) {
-                    const float e = cj_expf(v[k] - m);
-                    sc[p] = e;
-                    s = __fadd_rn(s, e);
+                    sc[p] = v[k];
+                    s = __fadd_rn(s, v[k]);
                 }
             }
         } else {
@@ -966,96 +976,123 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
     }
 
     // p·V over tiles: the weights of the HPW heads (a float4 a thread) and the
-    // V rows (VCH 16-byte chunks a thread), loaded a tile ahead
+    // V rows (VCH 16-byte chunks a thread); two tiles' loads in flight in two
+    // register sets while the chain runs over a third in LDS
     const int ntiles = (count + T - 1) / T;
-    float4 er;
-    u32x4 vr[VCH];
     // HPW·T weights a tile, four a thread for the first HPW·T/4 threads (the
     // rest repeat the last head's, unstored); the score rows are only
     // 4-byte aligned, so four word loads
     constexpr int EF = HPW * T / 4;
-    auto load = [&](int i) {
+    struct Tile {
+        float4 e;
+        u32x4 v[VCH];
+    };
+    auto load = [&](Tile &R, int i) {
         const int jj = min(t / (T / 4), HPW - 1), o = 4 * (t % (T / 4));
         const float *er0 = a.part + (int64_t)(h0 + jj) * a.splits;
         const int q0 = i * T + o;
-        er.x = er0[min(q0, a.splits - 1)];
-        er.y = er0[min(q0 + 1, a.splits - 1)];
-        er.z = er0[min(q0 + 2, a.splits - 1)];
-        er.w = er0[min(q0 + 3, a.splits - 1)];
+        R.e.x = er0[min(q0, a.splits - 1)];
+        R.e.y = er0[min(q0 + 1, a.splits - 1)];
+        R.e.z = er0[min(q0 + 2, a.splits - 1)];
+        R.e.w = er0[min(q0 + 3, a.splits - 1)];
+        // thread t: the VCH consecutive positions VCH·(t / (HD/8)) + k of the
+        // 8-dimension group t mod (HD/8) (a position past count reads position
+        // count − 1); they span at most two pages, whose entries are read once
+        const int lastpos = from + count - 1;
+        const int p0 = from + i * T + VCH * (t / (HD / 8)), j = t % (HD / 8);
+        const int f0 = min(p0, lastpos), f7 = min(p0 + VCH - 1, lastpos);
+        const uint16_t *b0 = a.vc + ((int64_t)pgs[(f0 >> 6) - (from >> 6)] * a.n_kv + kvh) * 64 * HD + 8 * j;
+        const uint16_t *b1 = a.vc + ((int64_t)pgs[(f7 >> 6) - (from >> 6)] * a.n_kv + kvh) * 64 * HD + 8 * j;
 #pragma unroll
         for (int k = 0; k < VCH; k++) {
-            const int c = t + 256 * k, p = c / (HD / 8), j = c % (HD / 8);
-            const int pos = from + min(i * T + p, count - 1);
-            const int page = pgs[(pos >> 6) - (from >> 6)];
-            vr[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j);
+            const int q = min(p0 + k, lastpos);
+            const uint16_t *b = (q >> 6) == (f0 >> 6) ? b0 : b1;
+            R.v[k] = *(const u32x4 *)(b + (q & 63) * HD);
         }
     };
-    auto store = [&](int buf) {
+    // the thread's 8 positions × 8 dimensions transposed: dimension 8j + i's
+    // 8 halves are one 16-byte row segment
+    static_assert(VCH == 8, "eight positions a thread");
+    auto store = [&](const Tile &R, int buf) {
         const int jj = min(t / (T / 4), HPW - 1), o = 4 * (t % (T / 4));
-        if (t < EF) *(float4 *)&es[buf][jj][o] = er;
+        if (t < EF) *(float4 *)&es[buf][jj][o] = R.e;
+        const int j = t % (HD / 8), p0 = VCH * (t / (HD / 8));
 #pragma unroll
-        for (int k = 0; k < VCH; k++) {
-            const int c = t + 256 * k;
-            *(u32x4 *)&vs[buf][c / (HD / 8)][8 * (c % (HD / 8))] = vr[k];
+        for (int i = 0; i < 8; i++) {
+            const int w = i >> 1;
+            const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;   // the high or the low halves
+            u32x4 o4;
+            o4.x = __builtin_amdgcn_perm(R.v[1][w], R.v[0][w], sel);
+            o4.y = __builtin_amdgcn_perm(R.v[3][w], R.v[2][w], sel);
+            o4.z = __builtin_amdgcn_perm(R.v[5][w], R.v[4][w], sel);
+            o4.w = __builtin_amdgcn_perm(R.v[7][w], R.v[6][w], sel);
+            *(u32x4 *)&vs[buf][(8 * j + i) * VR + p0] = o4;
         }
     };
     const int jj = t / HD, d = t % HD;
     float acc = 0.0f;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int i = 0; i < ntiles; i++) {
-        load(min(i + 1, ntiles - 1));
-        const int buf = i & 1, n = min(T, count - i * T);
+    // steps of 8 positions: one 16-byte read of the dimension's V row and two
+    // of the head's weights, the next step's three issued before the current
+    // step's adds (at most 15 LDS reads may be outstanding); the product
+    // e_t·v_t[d] by the mixed multiply with a −0 addend (the rounded
+    // product), then the add
+    auto chain = [&](int buf, int n) {
         const float *ew = &es[buf][jj][0];
-        const uint16_t *vw = &vs[buf][0][d];
-        // blocks of 16 positions, the next block's LDS reads issued before
-        // the current block's adds (one wave a SIMD leaves nothing else to
-        // cover their latency); the product e_t·v_t[d] by the mixed multiply
-        // with a −0 addend (the rounded product), then the add
-        const int nb16 = n / 16;
-        float4 ea[4], eb[4];
-        uint32_t va[16], vb[16];
-        auto rd = [&](float4 (&e)[4], uint32_t (&v)[16], int blk) {
-            const int p0 = 16 * min(blk, nb16 - 1);
-#pragma unroll
-            for (int q = 0; q < 4; q++) e[q] = *(const float4 *)(ew + p0 + 4 * q);
-#pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = vw[(p0 + k) * HD];
+        const uint16_t *vrow = &vs[buf][d * VR];
+        const int n8 = n / 8;
+        struct Step {
+            u32x4 v;
+            float4 e0, e1;
         };
-        auto run = [&](const float4 (&e)[4], const uint32_t (&v)[16]) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                acc = __fadd_rn(acc, mul_h16lo(v[4 * q], e[q].x));
-                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 1], e[q].y));
-                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 2], e[q].z));
-                acc = __fadd_rn(acc, mul_h16lo(v[4 * q + 3], e[q].w));
-            }
+        auto rd = [&](Step &S, int st) {
+            const int p0 = 8 * min(st, n8 - 1);
+            S.v = *(const u32x4 *)(vrow + p0);
+            S.e0 = *(const float4 *)(ew + p0);
+            S.e1 = *(const float4 *)(ew + p0 + 4);
         };
-        if (nb16 > 0) {
-            rd(ea, va, 0);
-            for (int b = 0; b < nb16; b += 2) {
-                rd(eb, vb, b + 1);
+        auto run = [&](const Step &S) {
+            acc = __fadd_rn(acc, mul_h16lo(S.v.x, S.e0.x));
+            acc = __fadd_rn(acc, mul_h16hi(S.v.x, S.e0.y));
+            acc = __fadd_rn(acc, mul_h16lo(S.v.y, S.e0.z));
+            acc = __fadd_rn(acc, mul_h16hi(S.v.y, S.e0.w));
+            acc = __fadd_rn(acc, mul_h16lo(S.v.z, S.e1.x));
+            acc = __fadd_rn(acc, mul_h16hi(S.v.z, S.e1.y));
+            acc = __fadd_rn(acc, mul_h16lo(S.v.w, S.e1.z));
+            acc = __fadd_rn(acc, mul_h16hi(S.v.w, S.e1.w));
+        };
+        if (n8 > 0) {
+            Step sa, sb;
+            rd(sa, 0);
+            for (int st = 0; st < n8; st += 2) {
+                rd(sb, st + 1);
                 __builtin_amdgcn_sched_barrier(0);
-                run(ea, va);
-                if (b + 1 >= nb16) break;
-                rd(ea, va, b + 2);
+                run(sa);
+                if (st + 1 >= n8) break;
+                rd(sa, st + 2);
                 __builtin_amdgcn_sched_barrier(0);
-                run(eb, vb);
+                run(sb);
             }
         }
-        int p = 16 * nb16;
-        for (; p + 4 <= n; p += 4) {
-            const float4 e4 = *(const float4 *)(ew + p);
-            const float v0 = h2f(vw[p * HD]), v1 = h2f(vw[(p + 1) * HD]);
-            const float v2 = h2f(vw[(p + 2) * HD]), v3 = h2f(vw[(p + 3) * HD]);
-            acc = __fadd_rn(acc, __fmul_rn(e4.x, v0));
-            acc = __fadd_rn(acc, __fmul_rn(e4.y, v1));
-            acc = __fadd_rn(acc, __fmul_rn(e4.z, v2));
-            acc = __fadd_rn(acc, __fmul_rn(e4.w, v3));
-        }
-        for (; p < n; p++) acc = __fadd_rn(acc, __fmul_rn(ew[p], h2f(vw[p * HD])));
-        store(buf ^ 1);
+        for (int p = 8 * n8; p < n; p++) acc = __fadd_rn(acc, __fmul_rn(ew[p], h2f(vrow[p])));
+    };
+    // tile i is in LDS buffer i mod 2; at its chain, register set (i+1) mod 2
+    // holds tile i+1 in flight and set i mod 2 takes tile i+2's loads (past
+    // the last tile: the last again, never stored)
+    Tile ra, rb;
+    load(ra, 0);
+    load(rb, min(1, ntiles - 1));
+    store(ra, 0);
+    __syncthreads();
+    for (int i = 0; i < ntiles; i += 2) {
+        load(ra, min(i + 2, ntiles - 1));
+        chain(0, min(T, count - i * T));
+        if (i + 1 >= ntiles) break;
+        store(rb, 1);
+        __syncthreads();
+        load(rb, min(i + 3, ntiles - 1));
+        chain(1, min(T, count - (i + 1) * T));
+        if (i + 2 >= ntiles) break;
+        store(ra, 0);
         __syncthreads();
     }
     a.out[(int64_t)(h0 + jj) * HD + d] = __fmul_rn(acc, rsum[jj]);

@@ -118,14 +118,16 @@ __device__ __constant__ uint64_t CJ_EXP2_TAB[32] = {
     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
 };
+// Branch-free: the main path runs on x clamped into its range (the same x
+// wherever the result is used) and the special cases are selected after, so
+// a caller's independent exps issue their table loads together.
 DEV float cj_expf(float x) {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
-    if (x < -0x1.9fe368p6f) return 0.0f;
+    const float hi = 0x1.62e42ep6f, lo = -0x1.9fe368p6f;
+    const float xc = fminf(fmaxf(x, lo), hi);
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32 * 32), c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32),
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    const double xd = (double)x;
+    const double xd = (double)xc;
     double kd = __fma_rn(inv_ln2_n, xd, shift);
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = kd - shift;
@@ -134,7 +136,10 @@ DEV float cj_expf(float x) {
     const double z = __fma_rn(c0, r, c1), r2 = r * r;
     double y = __fma_rn(c2, r, 1.0);
     y = __fma_rn(z, r2, y);
-    return __double2float_rn(y * s);
+    float e = __double2float_rn(y * s);
+    e = x > hi ? __uint_as_float(0x7f800000u) : e;
+    e = x < lo ? 0.0f : e;
+    return x != x ? x + x : e;
 }
 
 // SiLU(x)·u, exp form: x / (1 + exp(−x)) · u (Prim.gluF32 / gluOne).

@@ -1430,7 +1430,6 @@ extern "C" __global__ void __launch_bounds__(256) cj_moe_group(cj_moe_group_args
 }
 
 #define GRP_CC 16   // member selections a column chunk
-#define GRP_RT 64   // weight rows a workgroup (gate|up: one 32-block of the activation)
 #define GRP_RS (GRP_CC + 1)
 
 // Workgroup (row tile, expert e): the 64 rows run as four passes of 16 (a
@@ -1444,11 +1443,13 @@ extern "C" __global__ void __launch_bounds__(256) cj_moe_group(cj_moe_group_args
 // the tile (L2). EPI: CJ_EPI_GLU — SiLU·up of each gate/up row pair, then
 // the member's 32 activation values quantized per 32 (mxfp4QuantActKernel's
 // arithmetic) into its pack; CJ_EPI_STORE — the row values.
-template <int EPI, int KB>
+template <int EPI, int KB, int GRT, int RW = 2, int CC = GRP_CC>
 DEV void moe_grp_body(const cj_moe_grp_args &a) {
-    constexpr int RW = 2, PASSES = GRP_RT / (8 * RW);
+    constexpr int PASSES = GRT / (8 * RW), RS = CC + 1;
+    static_assert(PASSES % 2 == 0, "an even number of passes");
+    static_assert(EPI != CJ_EPI_GLU || GRT == 64, "the SiLU·up form: one 32-block of the activation a workgroup");
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int mi[GRP_CC];
+    __shared__ int mi[CC];
     const int e = blockIdx.y;
     const int c = a.cnt[e];
     if (c == 0) return;
@@ -1456,10 +1457,10 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
     const int nb = (int)(a.cols / 32);
     const int cpad = (int)((a.cols + 15) & ~15), nbp = (nb + 3) & ~3;
     int8_t *xq = (int8_t *)smem;
-    float *xd = (float *)(smem + GRP_CC * cpad);
-    float *res = xd + GRP_CC * nbp;
+    float *xd = (float *)(smem + CC * cpad);
+    float *res = xd + CC * nbp;
     const uint8_t *W = a.w + (int64_t)e * a.expert_bytes;
-    const int64_t row0 = (int64_t)blockIdx.x * GRP_RT;
+    const int64_t row0 = (int64_t)blockIdx.x * GRT;
 
     auto fetch = [&](u32x4 (&wv)[RW][KB], uint32_t (&sc)[RW][KB], int p) {
 #pragma unroll
@@ -1474,8 +1475,8 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
             }
         }
     };
-    for (int j0 = 0; j0 < c; j0 += GRP_CC) {
-        const int nc = min(GRP_CC, c - j0);
+    for (int j0 = 0; j0 < c; j0 += CC) {
+        const int nc = min(CC, c - j0);
         __syncthreads();   // the previous chunk's LDS reads are done
         if (t < nc) mi[t] = a.mem[(int64_t)e * a.cap + j0 + t];
         __syncthreads();
@@ -1536,7 +1537,7 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
                     float v = acc[i];
 #pragma unroll
                     for (int m = 16; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_xor(v, m));
-                    if (hl == 0) res[(p * 8 * RW + hw * RW + i) * GRP_RS + jj] = v;
+                    if (hl == 0) res[(p * 8 * RW + hw * RW + i) * RS + jj] = v;
                 }
             }
         };
@@ -1560,14 +1561,14 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
         if (EPI == CJ_EPI_GLU) {
             // output o (rows 2o, 2o+1) of member jj: thread t is (jj = t/32 + jb, o = t%32);
             // the 32 values of a member are one 32-block of its activation
-            const int64_t ab = row0 / GRP_RT;
+            const int64_t ab = row0 / GRT;
 #pragma unroll 1
             for (int jb = 0; jb < nc; jb += 8) {
                 const int jj = jb + (t >> 5), o = t & 31;
                 const bool on = jj < nc;
                 const int64_t ai = row0 / 2 + o;
                 float v = 0.0f;
-                if (on && ai < a.act_n) v = glu_value(a.glu_form, ai, a.act_n, res[(2 * o) * GRP_RS + jj], res[(2 * o + 1) * GRP_RS + jj]);
+                if (on && ai < a.act_n) v = glu_value(a.glu_form, ai, a.act_n, res[(2 * o) * RS + jj], res[(2 * o + 1) * RS + jj]);
                 float bm = fabsf(v);
 #pragma unroll
                 for (int m = 16; m > 0; m >>= 1) bm = fmaxf(bm, __shfl_xor(bm, m));
@@ -1586,21 +1587,35 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
                 }
             }
         } else {
-            for (int idx = t; idx < nc * GRP_RT; idx += 256) {
-                const int jj = idx / GRP_RT, rl = idx % GRP_RT;
+            for (int idx = t; idx < nc * GRT; idx += 256) {
+                const int jj = idx / GRT, rl = idx % GRT;
                 const int64_t r = row0 + rl;
-                if (r < a.rows) a.y[(int64_t)mi[jj] * a.y_stride + r] = res[rl * GRP_RS + jj];
+                if (r < a.rows) a.y[(int64_t)mi[jj] * a.y_stride + r] = res[rl * RS + jj];
             }
         }
     }
 }
 
-#define MOE_GRP_KERNEL(E, EPI, KB)                                                                      \
-    extern "C" __global__ void __launch_bounds__(256) cj_moe_mxq8_##E##_k##KB(cj_moe_grp_args a) {      \
-        moe_grp_body<EPI, KB>(a);                                                                       \
+#define MOE_GRP_KERNEL(E, EPI, KB, GRT)                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) cj_moe_mxq8_##E##_k##KB##_t##GRT(cj_moe_grp_args a) {  \
+        moe_grp_body<EPI, KB, GRT>(a);                                                                       \
     }
-MOE_GRP_KERNEL(g, CJ_EPI_GLU, 1) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 2) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 3) MOE_GRP_KERNEL(g, CJ_EPI_GLU, 4)
-MOE_GRP_KERNEL(s, CJ_EPI_STORE, 1) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 2) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 3) MOE_GRP_KERNEL(s, CJ_EPI_STORE, 4)
+// one row a half-wave a pass and members in chunks of CC (fewer registers and
+// less LDS: more workgroups a CU when each expert has few rows)
+#define MOE_GRP_KERNEL_RC(E, EPI, KB, GRT, RW, CC)                                                             \
+    extern "C" __global__ void __launch_bounds__(256)                                                          \
+        cj_moe_mxq8_##E##_k##KB##_t##GRT##_r##RW##_c##CC(cj_moe_grp_args a) {                                  \
+        moe_grp_body<EPI, KB, GRT, RW, CC>(a);                                                                 \
+    }
+MOE_GRP_KERNEL_RC(g, CJ_EPI_GLU, 3, 64, 1, 4)
+MOE_GRP_KERNEL_RC(g, CJ_EPI_GLU, 3, 64, 2, 4)
+MOE_GRP_KERNEL_RC(s, CJ_EPI_STORE, 3, 32, 1, 4)
+MOE_GRP_KERNEL_RC(s, CJ_EPI_STORE, 3, 32, 2, 4)
+#define MOE_GRP_KBS(E, EPI, GRT) \
+    MOE_GRP_KERNEL(E, EPI, 1, GRT) MOE_GRP_KERNEL(E, EPI, 2, GRT) MOE_GRP_KERNEL(E, EPI, 3, GRT) MOE_GRP_KERNEL(E, EPI, 4, GRT)
+MOE_GRP_KBS(g, CJ_EPI_GLU, 64)
+MOE_GRP_KBS(s, CJ_EPI_STORE, 32)
+MOE_GRP_KBS(s, CJ_EPI_STORE, 64)
 
 GEMV_FAMILY(cj_gemv_q6k, CJ_Q6_K, 2)
 GEMV_FAMILY(cj_gemv_q80, CJ_Q8_0, 4)

@@ -947,27 +947,32 @@ int Engine::rows_moe(const Layer &L, int n) {
         cj_moe_group_args g{r_moe_sel, r_grp_cnt, r_grp_mem, sels, n_experts, sels, 0};
         if ((rc = launch("cj_moe_group", 1, 256, 0, g))) return rc;
         const int64_t efb = ((int64_t)expert_ffn + 255) / 256 * 320;
-        auto grp = [&](const char *form, cj_moe_grp_args &q) {
+        const char *rcv = getenv("CJ_GRP_RC");   // "<rw><cc>": 14, 24
+        auto grp = [&](const char *form, int grt, cj_moe_grp_args &q) {
             const int nbq = (int)(q.cols / 32), kb = std::min(4, std::max(1, (nbq + 31) / 32));
-            const uint32_t lds = (uint32_t)(16 * ((q.cols + 15) & ~15) + 16 * ((nbq + 3) & ~3) * 4 + 64 * 17 * 4);
-            char kname[40];
-            snprintf(kname, sizeof kname, "cj_moe_mxq8_%s_k%d", form, kb);
-            return launch2(kname, (uint32_t)((q.rows + 63) / 64), (uint32_t)n_experts, 256, lds, q);
+            const int cc = rcv && kb == 3 ? 4 : 16;
+            const uint32_t lds = (uint32_t)(cc * ((q.cols + 15) & ~15) + cc * ((nbq + 3) & ~3) * 4 + grt * (cc + 1) * 4);
+            char kname[48];
+            if (rcv && kb == 3) snprintf(kname, sizeof kname, "cj_moe_mxq8_%s_k%d_t%d_r%c_c4", form, kb, grt, rcv[0]);
+            else snprintf(kname, sizeof kname, "cj_moe_mxq8_%s_k%d_t%d", form, kb, grt);
+            return launch2(kname, (uint32_t)((q.rows + grt - 1) / grt), (uint32_t)n_experts, 256, lds, q);
         };
+        const int grt_g = 64;
+        const int grt_s = getenv("CJ_GRT_S") ? atoi(getenv("CJ_GRT_S")) : 32;
         {   // gate|up + SiLU·up of each selection (r, k) = r·n_used + k over row r, into its pack
             cj_moe_grp_args q{};
             q.w = (const uint8_t *)L.gu_exps.p; q.xp = r_xp; q.outp = r_exp_pack; q.cnt = r_grp_cnt; q.mem = r_grp_mem;
             q.expert_bytes = 2 * (int64_t)expert_ffn * L.gu_exps.row_bytes; q.row_bytes = L.gu_exps.row_bytes;
             q.rows = 2 * (int64_t)expert_ffn; q.cols = hidden; q.xp_stride = hb; q.outp_stride = efb; q.cap = sels;
             q.x_per = n_used; q.glu_form = 0; q.act_n = expert_ffn;
-            if ((rc = grp("g", q))) return rc;
+            if ((rc = grp("g", grt_g, q))) return rc;
         }
         {   // down of every selection
             cj_moe_grp_args q{};
             q.w = (const uint8_t *)L.down_exps.p; q.xp = r_exp_pack; q.y = r_moe_y; q.cnt = r_grp_cnt; q.mem = r_grp_mem;
             q.expert_bytes = (int64_t)hidden * L.down_exps.row_bytes; q.row_bytes = L.down_exps.row_bytes;
             q.rows = hidden; q.cols = expert_ffn; q.xp_stride = efb; q.y_stride = hidden; q.cap = sels; q.x_per = 1;
-            if ((rc = grp("s", q))) return rc;
+            if ((rc = grp("s", grt_s, q))) return rc;
         }
         cj_combine_args c{r_hs, r_moe_y, r_moe_w, hidden, n_used};
         return launch2("cj_moe_combine", (uint32_t)((hidden + 255) / 256), (uint32_t)n, 256, 0, c);

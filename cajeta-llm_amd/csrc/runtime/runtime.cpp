@@ -433,11 +433,17 @@ int32_t cj_init(int32_t device) {
     }
     // MXFP4 experts grouped by expert: epilogue {g, s} × blocks a lane a sweep
     for (const char *e : {"g", "s"})
-        for (const char *kb : {"1", "2", "3", "4"}) {
-            const std::string k = std::string("cj_moe_mxq8_") + e + "_k" + kb;
-            hipFunction_t f;
-            if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
-        }
+        for (const char *kb : {"1", "2", "3", "4"})
+            for (const char *rt : {"32", "64", "128"}) {
+                const std::string k = std::string("cj_moe_mxq8_") + e + "_k" + kb + "_t" + rt;
+                hipFunction_t f;
+                if (hipModuleGetFunction(&f, g.module, k.c_str()) == hipSuccess) g.fns[k] = f;
+            }
+    for (const char *k : {"cj_moe_mxq8_g_k3_t64_r1_c4", "cj_moe_mxq8_g_k3_t64_r2_c4", "cj_moe_mxq8_s_k3_t32_r1_c4",
+                          "cj_moe_mxq8_s_k3_t32_r2_c4"}) {
+        hipFunction_t f;
+        if (hipModuleGetFunction(&f, g.module, k) == hipSuccess) g.fns[k] = f;
+    }
     // MXFP4 × q8: epilogue {s, a, g} × blocks a lane a sweep
     for (const char *e : {"s", "a", "g"})
         for (const char *kb : {"1", "2", "3", "4"})
