@@ -19,7 +19,11 @@ Beside the line's value it reports
                 the 256 MB last-level cache): algorithmic bytes per launch ÷
                 mean launch time, against 8 TB/s; `traffic` is the measured
                 HBM bytes per launch from the committed rocprofv3 counter
-                summary;
+                summary; `in_step_eager` the same launch timed inside whole
+                eagerly enqueued decode steps (an event before and after each
+                layer's launch: the kernel as the step runs it, plus its
+                eager dispatch — an upper bound on its share of the graph-
+                replayed step);
   copy          a plain 1 GiB device copy kernel (cj_buf_copy) timed the same
                 way: the practical streaming ceiling of the part, and the
                 known-size kernel the counter summaries are calibrated with;
@@ -724,6 +728,14 @@ def main():
                                                            nbytes / (us * 1e-6) / 1e9))
     dom = kernels["gate_up"]
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+    # the same kinds inside whole eager steps (every layer's launch between
+    # two events; each interval holds the launch's share of the boundary)
+    in_step = {}
+    for kind in (K_GATE_UP, 1, 2, 3, 5):
+        us = eng.timeKernelInStep(kind, 4)
+        in_step[KIND_NAMES[kind]] = round(us, 3)
+        log("  in step  %-9s %9.2f us" % (KIND_NAMES[kind], us))
+    dom_in = in_step["gate_up"]
     copy = copy_reference(native)
     log("  copy      cj_copy                   %9.2f us  %12d B  %7.1f GB/s" % (copy["avg_us"], copy["bytes"],
                                                                               copy["GB/s"]))
@@ -776,11 +788,17 @@ def main():
                    "timed_positions": [first, first + args.steps - 1], "seed": args.seed},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": dom["kernel"], "bytes_per_launch": dom["bytes"], "avg_us": dom["avg_us"]},
+                     "kernel": dom["kernel"], "bytes_per_launch": dom["bytes"], "avg_us": dom["avg_us"],
+                     "in_step_eager": {"avg_us": dom_in, "achieved": round(dom["bytes"] / (dom_in * 1e-6) / 1e9, 1),
+                                       "frac": round(dom["bytes"] / (dom_in * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                       "note": "events around each layer's launch in eagerly enqueued steps: "
+                                               "the kernel plus its eager dispatch (an upper bound on its "
+                                               "share of the graph-replayed step)"}},
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(step_gbs / PEAK_HBM_GBS, 4),
                           "device_us_per_step": round(dev_us, 2)},
         "kernels": kernels,
+        "kernels_in_step_eager_us": in_step,
         "copy": copy,
         "api": api,
         "cpu_baseline": cpu,

@@ -187,6 +187,14 @@ struct Engine {
     int batch_rows = 0;                        // rows of the last batched decode step
     std::vector<hipGraphExec_t> batch_graphs;  // [n]: the batched step of n rows (the row table is read at replay)
 
+    // in-step timing: an event before and after each launch of probe_kind
+    int probe_kind = -1, probe_n = 0;
+    std::vector<hipEvent_t> probe_ev;
+    void probe(int kind) {
+        if (kind == probe_kind && probe_n < (int)probe_ev.size()) (void)hipEventRecord(probe_ev[probe_n++], stream());
+    }
+    int time_in_step(int s, int kind, int steps, float *avg_us);
+
     bool want(int kind, int l) const {
         return only < 0 || (only == kind && l == (kind == K_EMBED || kind == K_HEAD ? 0 : only_layer));
     }
@@ -672,9 +680,12 @@ int Engine::enqueue_step(int s) {
             if (qkv_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = cur; a.nw = L.attn_norm; a.norm_form = 0; }
             a.per32 = per32; a.eps = eps; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.pg_base = S.pg_base;
             a.batch = 1; a.kv_f32 = kv_f32;
+            probe(K_QKV);
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
+            probe(K_QKV);
         }
         if (want(K_ATTN, l) || want(K_MERGE, l)) {   // 2. attention
+            probe(K_ATTN);
             cj_attn_args a{};
             a.part = part; a.out = attn; a.q = q; a.kc = L.kc; a.vc = L.vc; a.pgtab = pgtab; a.state = S.state;
             a.counters = attn_counters; a.n_q = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.workers = workers;
@@ -711,13 +722,16 @@ int Engine::enqueue_step(int s) {
                 }
             }
         }
+        if (want(K_ATTN, l) || want(K_MERGE, l)) probe(K_ATTN);
         if (want(K_O, l)) {   // 3. o projection, residual into hs
             cj_gemv_args a{};
             a.w = (const uint8_t *)L.o.p; a.x = attn; a.xp = attn_pack; a.y = cur; a.rows = L.o.rows; a.cols = L.o.cols;
             a.row_bytes = L.o.row_bytes; a.type = L.o.type; a.pro = split && !merge_w ? CJ_PRO_PACKED : CJ_PRO_PACK;
             a.epi = CJ_EPI_ACCUM;
             a.per32 = L.o.type == CJ_Q8_0; a.batch = 1;
+            probe(K_O);
             if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
+            probe(K_O);
         }
         const bool gu_norm = n_experts == 0 && L.gu.type == CJ_Q4_K && hidden <= 4096;
         // MoE with an f32 router and MXFP4 experts (both read the f32 norm,
@@ -738,14 +752,18 @@ int Engine::enqueue_step(int s) {
                 a.eps = eps; a.act_n = ffn; a.act_per32 = L.down.type == CJ_Q8_0; a.glu_form = (ffn % 256) ? 1 : 0;
                 a.batch = 1;
                 if (gu_norm) { a.pro = CJ_PRO_NORM_PACK; a.x = cur; a.nw = L.ffn_norm; a.norm_form = 0; }
+                probe(K_GATE_UP);
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 16, a.pro, a.epi)))) return rc;
+                probe(K_GATE_UP);
             }
             if (want(K_DOWN, l)) {   // 5. down, residual into hs
                 cj_gemv_args a{};
                 a.w = (const uint8_t *)L.down.p; a.x = act; a.y = cur; a.rows = L.down.rows; a.cols = L.down.cols;
                 a.row_bytes = L.down.row_bytes; a.type = L.down.type; a.pro = CJ_PRO_PACK; a.epi = CJ_EPI_ACCUM;
                 a.per32 = L.down.type == CJ_Q8_0; a.batch = 1;
+                probe(K_DOWN);
                 if ((rc = run_gemv(a, plan_gemv(a.type, a.rows, a.cols, 8, a.pro, a.epi)))) return rc;
+                probe(K_DOWN);
             }
         } else {
             if (want(K_ROUTER, l)) {   // router logits from the normed hidden (f32 weights)
@@ -1429,6 +1447,56 @@ int64_t Engine::step_bytes(int count) const {
     return b;
 }
 
+// The in-step duration of one launch kind: `steps` whole decode steps of
+// sequence s enqueued eagerly (the step's own launch order and data), an
+// event recorded on the stream before and after every launch of the kind;
+// the mean interval over the layers and steps (each includes the launch's
+// share of the kernel boundary, as in the step). The step state is left as
+// it was.
+int Engine::time_in_step(int s, int kind, int steps, float *avg_us) {
+    if (s < 0 || s >= (int)seqs.size()) return fail(CJ_ERR_ARG, "sequence slot %d out of range", s);
+    if (kind != K_QKV && kind != K_ATTN && kind != K_O && kind != K_GATE_UP && kind != K_DOWN)
+        return fail(CJ_ERR_ARG, "time in step: kind %d is not probed", kind);
+    if (n_experts > 0 && (kind == K_GATE_UP || kind == K_DOWN))
+        return fail(CJ_ERR_ARG, "time in step: kind %d is not part of this model's step", kind);
+    if (steps <= 0 || steps > 64) return fail(CJ_ERR_ARG, "time in step: %d steps", steps);
+    Seq &S = seqs[s];
+    if (S.pos == 0) return fail(CJ_ERR_STATE, "time: prefill first");
+    cj_step_state saved{};
+    CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipMemcpy(&saved, S.state, sizeof saved, hipMemcpyDeviceToHost));
+    const int per = 2 * n_layers;
+    probe_ev.assign((size_t)per, nullptr);
+    int rc = CJ_OK;
+    for (auto &e : probe_ev)
+        if (hipEventCreate(&e) != hipSuccess) { e = nullptr; rc = fail(CJ_ERR_HIP, "time in step: event create"); }
+    double sum = 0.0;
+    int n = 0;
+    for (int i = 0; i <= steps && !rc; i++) {   // step 0 warms up
+        CJ_HIP(hipMemcpy(S.state, &saved, sizeof saved, hipMemcpyHostToDevice));
+        probe_kind = kind;
+        probe_n = 0;
+        rc = enqueue_step(s);
+        probe_kind = -1;
+        if (rc) break;
+        CJ_HIP(hipStreamSynchronize(stream()));
+        if (probe_n != per) { rc = fail(CJ_ERR_STATE, "time in step: %d probes, %d expected", probe_n, per); break; }
+        for (int k = 0; i > 0 && k < per; k += 2) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, probe_ev[k], probe_ev[k + 1]) == hipSuccess) { sum += ms; n++; }
+        }
+    }
+    probe_kind = -1;
+    for (auto &e : probe_ev) if (e) (void)hipEventDestroy(e);
+    probe_ev.clear();
+    CJ_HIP(hipStreamSynchronize(stream()));
+    CJ_HIP(hipMemcpy(S.state, &saved, sizeof saved, hipMemcpyHostToDevice));
+    if (rc) return rc;
+    if (n == 0) return fail(CJ_ERR_HIP, "time in step: no interval measured");
+    *avg_us = (float)(sum * 1000.0 / n);
+    return CJ_OK;
+}
+
 // Time `reps` back-to-back eager launches of one kind of sequence s's step at
 // its current position, on the engine's stream, between two HIP events. The
 // launches rotate over the layers, so each reads weights the previous few did
@@ -2006,6 +2074,12 @@ int32_t cj_engine_time_kernel(int64_t h, int32_t seq, int32_t kind, int32_t reps
         name[n] = 0;
     }
     return CJ_OK;
+}
+
+int32_t cj_engine_time_kernel_in_step(int64_t h, int32_t seq, int32_t kind, int32_t steps, float *avg_us) {
+    Engine *e = eng_of(h);
+    if (!e || !avg_us) return cj::fail(CJ_ERR_ARG, "cj_engine_time_kernel_in_step: bad arguments");
+    return e->time_in_step(seq, kind, steps, avg_us);
 }
 
 int32_t cj_engine_set_graphs(int64_t h, int32_t on) {

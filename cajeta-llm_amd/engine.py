@@ -238,6 +238,13 @@ class LlmEngine:
               "time kernel")
         return float(us[0]), int(nb[0]), bytes(name.view(np.uint8)).split(b"\0")[0].decode()
 
+    def timeKernelInStep(self, kind, steps=4, seq=0):
+        """Mean µs of one launch kind inside whole eager decode steps (every
+        layer's launch, an event before and after each)."""
+        us = np.zeros(1, np.float32)
+        check(lib().cj_engine_time_kernel_in_step(self.h, seq, int(kind), int(steps), ptr(us)), "time kernel in step")
+        return float(us[0])
+
     def stepBytes(self, count):
         """Algorithmic HBM bytes of one decode step attending `count` positions."""
         v = int(lib().cj_engine_step_bytes(self.h, int(count)))

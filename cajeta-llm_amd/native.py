@@ -85,6 +85,7 @@ SIGNATURES = {
     "cj_engine_last_step_us": (F32, [I64]),
     "cj_engine_trace": (I32, [I64, I32, P, I64]),
     "cj_engine_time_kernel": (I32, [I64, I32, I32, I32, P, P, P, I32]),
+    "cj_engine_time_kernel_in_step": (I32, [I64, I32, I32, I32, P]),
     "cj_engine_step_bytes": (I64, [I64, I32]),
     "cj_engine_set_graphs": (I32, [I64, I32]),
     "cj_synth_gguf": (I32, [CP, CP, I64]),

@@ -374,6 +374,13 @@ int32_t cj_engine_trace(int64_t eng, int32_t what, float *out, int64_t n);
  * and the kernel's name (the last one for a two-launch kind). */
 int32_t cj_engine_time_kernel(int64_t eng, int32_t seq, int32_t kind, int32_t reps, float *avg_us, int64_t *bytes,
                               int8_t *name, int32_t name_cap);
+/* Measurement seam, no counterpart in the reference: the same launch kind
+ * timed inside the step — `steps` whole decode steps of the slot enqueued as
+ * the step runs them (after one warm-up step), an event before and after each
+ * of the kind's launches (every layer); writes the mean interval in µs (each
+ * includes the launch's share of the kernel boundary). kind: 1 q|k|v,
+ * 2 attention, 3 o, 4 gate|up, 5 down. The step state is left unchanged. */
+int32_t cj_engine_time_kernel_in_step(int64_t eng, int32_t seq, int32_t kind, int32_t steps, float *avg_us);
 /* Replay the captured step graph (on != 0, the default) or enqueue the
  * step's launches each token. The kernels and their arguments are the same;
  * the eager form is for tools that cannot follow graph launches. No

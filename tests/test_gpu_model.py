@@ -244,6 +244,37 @@ def test_c3_shape_two_layers_greedy_parity(gpu):
     assert run_pair.bit_identical
 
 
+def test_in_step_timing_leaves_the_decode_unchanged(gpu):
+    """The measurement seams (timing launches and in-step timing, which enqueue
+    whole steps) leave the slot's state as it was: decoding on afterwards gives
+    the tokens and logits of an engine that never timed anything."""
+    say("in-step timing")
+    spec = "layers=2;hidden=4096;heads=32;kv=8;hd=128;ffn=14336;vocab=128256;eps=1e-5;theta=500000;" \
+           "wtype=q4_k;head=q6_k;embd=q4_k;ctx=256"
+    path, img = synth(gpu, spec, "t_c3x2t", 79)
+    prompt = np.random.default_rng(4).integers(0, 128256, 20).tolist()
+    runs = []
+    for timed in (False, True):
+        opts = gpu.EngineOptions(path)
+        opts.ctx, opts.maxSeqs = 256, 1
+        eng = gpu.LlmEngine.load(opts)
+        try:
+            eng.reset()
+            eng.prefill(prompt)
+            toks = list(eng.decode(4))
+            if timed:
+                for kind in (1, 2, 3, 4, 5):
+                    assert eng.timeKernelInStep(kind, 2) > 0.0
+                assert eng.timeKernel(4, 8)[0] > 0.0
+            toks += list(eng.decode(4))
+            runs.append((toks, eng.logits()))
+        finally:
+            eng.close()
+    gpu.image_free("t_c3x2t")
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+
+
 def test_c3_attention_at_the_benchmarked_context(gpu):
     """Benchmark configuration C3 at the context it is timed at: a 2048-token prompt
     through four 512-row prefill chunks, then 9 greedy steps at positions 2048 to
