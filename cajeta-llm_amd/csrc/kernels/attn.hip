@@ -72,6 +72,8 @@ DEV void split_body(const cj_attn_args &a) {
     __shared__ int pgs[PGMAX];
     __shared__ float bmax[8];
     __shared__ int ticket;
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the tile loop's first barrier
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
     // q, the page table and the step state load together
@@ -145,9 +147,12 @@ DEV void split_body(const cj_attn_args &a) {
                 const float inc = fmaxf(m[hh], wave_prefix_max(live ? s[hh] : -3.0e38f));
                 const float exc = wave_shr1(inc, m[hh]);
                 const bool up = live && s[hh] > exc;
-                const float cf = up ? cj_expf(exc - s[hh]) : 1.0f;
-                const float pw = live ? cj_expf(s[hh] - inc) : 0.0f;
                 const uint64_t ups = __ballot(up);
+                // the rescale's exp only where a position raises the maximum
+                // (after the first tiles, rarely: the wave skips it)
+                float cf = 1.0f;
+                if (ups) cf = up ? cj_expf(exc - s[hh], etab) : 1.0f;
+                const float pw = live ? cj_expf(s[hh] - inc, etab) : 0.0f;
                 m[hh] = lane_f(inc, n - 1);
                 // the lane's V pair of every position of the tile first (all
                 // reads in flight at once), then the recurrence in position
@@ -202,7 +207,7 @@ DEV void split_body(const cj_attn_args &a) {
         const float mv = in ? ml.x : -3.0e38f;
         const float gm = group_max<64>(mv);
         const bool on = in && ml.y > 0.0f;
-        const float wt = on ? cj_expf(mv - gm) : 0.0f;
+        const float wt = on ? cj_expf(mv - gm, etab) : 0.0f;
         const uint64_t ons = __ballot(on);
         float gl[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ac1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int s0 = 0; s0 < splits; s0 += 16) {
@@ -249,6 +254,8 @@ DEV void split_rows_body(const cj_attn_args &a) {
     __shared__ __align__(16) uint16_t vs[TP][HD];
     __shared__ __align__(16) float qs[G][HD];
     __shared__ int pgs[PGMAX];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the "q and pages" barrier
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int per = a.n_kv * a.spl, r = blockIdx.x / per, rem = blockIdx.x % per;
     const int kvh = rem / a.spl, sp = rem % a.spl;
@@ -343,9 +350,12 @@ DEV void split_rows_body(const cj_attn_args &a) {
                 const float inc = fmaxf(m[hh], wave_prefix_max(live ? s[hh] : -3.0e38f));
                 const float exc = wave_shr1(inc, m[hh]);
                 const bool up = live && s[hh] > exc;
-                const float cf = up ? cj_expf(exc - s[hh]) : 1.0f;
-                const float pw = live ? cj_expf(s[hh] - inc) : 0.0f;
                 const uint64_t ups = __ballot(up);
+                // the rescale's exp only where a position raises the maximum
+                // (after the first tiles, rarely: the wave skips it)
+                float cf = 1.0f;
+                if (ups) cf = up ? cj_expf(exc - s[hh], etab) : 1.0f;
+                const float pw = live ? cj_expf(s[hh] - inc, etab) : 0.0f;
                 m[hh] = lane_f(inc, n - 1);
                 // the lane's V pair of every position of the tile first (all
                 // reads in flight at once), then the recurrence in position
@@ -384,11 +394,19 @@ DEV void split_rows_body(const cj_attn_args &a) {
 
 #undef SPLIT_FETCH
 
-#define SPLIT_KERNEL(G)                                                                                         \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_h128_g##G(cj_attn_args a) { split_body<G>(a); }      \
-    extern "C" __global__ void __launch_bounds__(256) cj_attn_split_rows_h128_g##G(cj_attn_args a) { split_rows_body<G>(a); }
-SPLIT_KERNEL(4)
-SPLIT_KERNEL(8)
+// Register budget of the four-heads-a-group forms: four waves a SIMD (128
+// VGPRs; the f64 steps of the exp had pushed them to 132 and three waves —
+// the rows form 132 -> 165 µs a C4 layer). The eight-heads forms hold two
+// heads a wave and would spill at that budget.
+#define SPLIT_KERNEL(G, ATTR)                                                                                  \
+    extern "C" __global__ void __launch_bounds__(256) ATTR cj_attn_split_h128_g##G(cj_attn_args a) {           \
+        split_body<G>(a);                                                                                      \
+    }                                                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) ATTR cj_attn_split_rows_h128_g##G(cj_attn_args a) {      \
+        split_rows_body<G>(a);                                                                                 \
+    }
+SPLIT_KERNEL(4, __attribute__((amdgpu_waves_per_eu(4))))
+SPLIT_KERNEL(8, )
 
 // ------------------------------------------------------------ two-pass form
 
@@ -529,7 +547,7 @@ struct CombineItem {
 // head's sibling workgroups read concurrently.
 template <int HD, int T, bool EXP>
 DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, float m, int count, int from,
-                              int kvh, int d0, int dg, int tq, int I) {
+                              int kvh, int d0, int dg, int tq, int I, const uint64_t *et) {
     CombineItem it;
     const int t0 = I * T + 4 * tq;
 #pragma unroll
@@ -537,7 +555,7 @@ DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float
         const int t = min(t0 + k, count - 1), pos = from + t;
         const int page = pgs[(pos >> 6) - (from >> 6)];
         it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + 8 * dg);
-        it.e[k] = EXP ? cj_expf(ev[t] - m) : ev[t];
+        it.e[k] = EXP ? cj_expf(ev[t] - m, et) : ev[t];
     }
     return it;
 }
@@ -598,7 +616,7 @@ struct CombineDims {
 // roles run a whole number of CD-tile rounds.
 template <int HD, int CD, bool EXP>
 DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float m, float *prod, int count, int from,
-                     int kvh, int d0) {
+                     int kvh, int d0, const uint64_t *et) {
     using D = CombineDims<HD>;
     constexpr int T = D::T, S = D::S;
     const int l = threadIdx.x, w = l >> 6, ntiles = (count + T - 1) / T;
@@ -642,17 +660,17 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
         // CD tiles of V rows and weights in flight, ring slot = tile mod CD
         CombineItem ring[CD];
 #pragma unroll
-        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, j);
+        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, j, et);
         float *pb = prod + 8 * dg * S + 4 * tq;
         combine_store<T, S>(pb, ring[0], 0, count, tq);
-        ring[0] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, CD);
+        ring[0] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, CD, et);
         __syncthreads();
         for (int i0 = 0; i0 < nit; i0 += CD) {
 #pragma unroll
             for (int j = 0; j < CD; j++) {
                 const int i = i0 + j, r = (j + 1) % CD;
                 combine_store<T, S>(pb + ((j + 1) & 1) * (D::DH * S), ring[r], i + 1, count, tq);
-                ring[r] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, i + 1 + CD);
+                ring[r] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, i + 1 + CD, et);
                 __syncthreads();
             }
         }
@@ -667,6 +685,8 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
     __shared__ __align__(16) float prod[2 * D::DH * D::S];   // also V of a short span: 2048 chunks of 16 bytes
     __shared__ int pgs[COMBINE_PAGES];
     __shared__ __align__(16) float es[COMBINE_ES];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the max's barrier
     int count, from;
     attn_window(a, count, from);
     const int h = bx / D::NSPLIT, d0 = D::DH * (bx % D::NSPLIT), l = threadIdx.x;
@@ -728,7 +748,7 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
         // every slot's exp formed (past count a repeat, unused), then the
         // ordered sum
 #pragma unroll
-        for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m);
+        for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m, etab);
 #pragma unroll
         for (int k = 0; k < PK; k++) {
             const int t = l + 128 * k;
@@ -745,7 +765,7 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
             for (int k = 0; k < PK; k++) {
                 const int t = base + l + 128 * k;
                 if (t < count) {
-                    const float e = cj_expf(u[k] - m);
+                    const float e = cj_expf(u[k] - m, etab);
                     s = __fadd_rn(s, e);
                 }
             }
@@ -792,9 +812,9 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
     // short spans (the sliding windows, early positions) take a two-tile
     // ring, so few rounds are padded
     const int ntiles = (count + D::T - 1) / D::T;
-    const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0)
-                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0)
-                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0);
+    const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0, etab)
+                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab)
+                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab);
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
@@ -814,6 +834,8 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     __shared__ __align__(16) float es[COMBINE_ES];
     __shared__ __align__(16) float vt[TV][DH];
     __shared__ int pgs[COMBINE_ES / 64];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the max's barrier
     int count, from;
     attn_window(a, count, from);
     const int h = bx / NSPLIT, d0 = DH * (bx % NSPLIT), l = threadIdx.x;
@@ -832,7 +854,7 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     float s = 0.0f;
     if (l < 128)
         for (int t = l; t < count; t += 128) {
-            const float e = cj_expf(__fsub_rn(sc[t], m));
+            const float e = cj_expf(__fsub_rn(sc[t], m), etab);
             es[t] = e;
             s = __fadd_rn(s, e);
         }
@@ -898,6 +920,8 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
     // cover the 64 banks once)
     constexpr int VR = T + 8;
     __shared__ __align__(16) uint16_t vs[2][HD * VR];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the first max's barrier
     int count, from;
     attn_window(a, count, from);
     const int t = threadIdx.x, l = t & 127, g = t >> 7;
@@ -939,7 +963,7 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
             // every slot's exp formed (past count a repeat, unused), then the
             // ordered sum and the stores
 #pragma unroll
-            for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m);
+            for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m, etab);
 #pragma unroll
             for (int k = 0; k < PK; k++) {
                 const int p = l + 128 * k;
@@ -957,7 +981,7 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
                 for (int k = 0; k < 8; k++) {
                     const int p = b + l + 128 * k;
                     if (p < count) {
-                        const float e = cj_expf(u[k] - m);
+                        const float e = cj_expf(u[k] - m, etab);
                         sc[p] = e;
                         s = __fadd_rn(s, e);
                     }
@@ -1176,6 +1200,8 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     __shared__ float sc[SPAN];
     __shared__ float red[128], mred[2];
     __shared__ float rsv;
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the staging barrier
     int count, from;
     attn_window(a, count, from);
     const int l = threadIdx.x, grp = a.n_q / a.n_kv, kvh = h / grp;
@@ -1237,7 +1263,7 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     float s = 0.0f;
     if (l < 128) {
         for (int t = j; t < count; t += 128) {
-            const float e = cj_expf(sc[t] - m);
+            const float e = cj_expf(sc[t] - m, etab);
             sc[t] = e;
             s = __fadd_rn(s, e);
         }
@@ -1281,6 +1307,8 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h128(cj_att
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a) {
     __shared__ float bmax[8];
     __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);
     const int t = threadIdx.x, lane = t & 63;
     const int64_t e = (int64_t)blockIdx.x * 256 + t;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
@@ -1303,7 +1331,8 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
     const float mv = in ? ml.x : -3.0e38f;
     const float gm = group_max<64>(mv);
     const bool on = in && ml.y > 0.0f;
-    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    __syncthreads();   // the exp table
+    const float wt = on ? cj_expf(mv - gm, etab) : 0.0f;
     const uint64_t ons = __ballot(on);
     // split weights and sums through the wave's LDS row, back as broadcast
     // 16-byte reads, 16 splits a chunk; selects (not branches): a split that
@@ -1349,6 +1378,8 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge(cj_merge_args a)
 // lane; the splits' weights and sums come from LDS ordered sub-major, so a
 // lane's 16 are four 16-byte reads.
 extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args a) {
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, hd = a.head_dim, per = hd / 32;
     const int h = blockIdx.x / per, j = lane >> 4, i = lane & 15;
     const int d = (blockIdx.x % per) * 32 + 16 * wave + i;
@@ -1367,7 +1398,8 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args 
     const float mv = in ? ml.x : -3.0e38f;
     const float gm = group_max<64>(mv);
     const bool on = in && ml.y > 0.0f;
-    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    __syncthreads();   // the exp table
+    const float wt = on ? cj_expf(mv - gm, etab) : 0.0f;
     const uint64_t mine = __ballot(on) >> j;   // bit 4k: split 4k + j takes part
     __shared__ __align__(16) float sw[2][ATTN_MAX_SPLITS], sl[2][ATTN_MAX_SPLITS];
     const int si = (lane & 3) * 16 + (lane >> 2);   // split s at (s mod 4)·16 + s/4
@@ -1407,7 +1439,7 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args 
 template <int NS>
 DEV void merge_rows_fold(const cj_merge_args &a, const float *pb0, int lane, int d, int splits, int64_t e, int64_t n,
                          float *out, uint8_t *packed, int64_t blk, float *bmax, float (*sw)[ATTN_MAX_SPLITS],
-                         float (*sl)[ATTN_MAX_SPLITS]) {
+                         float (*sl)[ATTN_MAX_SPLITS], const uint64_t *et) {
     const int hd = a.head_dim, t = threadIdx.x;
     float pv[NS];
 #pragma unroll
@@ -1417,7 +1449,7 @@ DEV void merge_rows_fold(const cj_merge_args &a, const float *pb0, int lane, int
     const float mv = in ? ml.x : -3.0e38f;
     const float gm = group_max<64>(mv);
     const bool on = in && ml.y > 0.0f;
-    const float wt = on ? cj_expf(mv - gm) : 0.0f;
+    const float wt = on ? cj_expf(mv - gm, et) : 0.0f;
     const uint64_t ons = __ballot(on);
     // split weights and sums through the wave's LDS row, back as broadcast
     // 16-byte reads, 16 splits a chunk; selects (not branches): a split that
@@ -1457,6 +1489,8 @@ DEV void merge_rows_fold(const cj_merge_args &a, const float *pb0, int lane, int
 extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_args a) {
     __shared__ float bmax[8];
     __shared__ __align__(16) float sw[4][ATTN_MAX_SPLITS], sl[4][ATTN_MAX_SPLITS];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);
     const int t = threadIdx.x, lane = t & 63;
     const int64_t n = (int64_t)a.n_q * a.head_dim;
     const int hd = a.head_dim;
@@ -1474,8 +1508,9 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_merge_rows(cj_merge_ar
     const int splits = decode_splits(count, a.nrows * a.n_kv, a.workers);
     // a batch's rows take few splits (4 at 32 rows of 8 kv heads): read and
     // fold only the first 16 where that covers them
-    if (splits <= 16) merge_rows_fold<16>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl);
-    else merge_rows_fold<ATTN_MAX_SPLITS>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl);
+    __syncthreads();   // the exp table
+    if (splits <= 16) merge_rows_fold<16>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl, etab);
+    else merge_rows_fold<ATTN_MAX_SPLITS>(a, pb0, lane, d, splits, e, n, out, packed, blk, bmax, sw, sl, etab);
 }
 
 // QK-norm (optional) + split-half RoPE + fp16 K/V append, one workgroup of
@@ -1572,6 +1607,8 @@ DEV void prefill_body(const cj_attn_args &a) {
     constexpr int HD = 128, TK = 32, NS = G >= 8 ? G / 4 : 1, RB = 16 * NS / G;
     __shared__ __align__(16) float kl[TK][16][8];
     __shared__ __align__(16) float vl[TK][16][8];
+    __shared__ uint64_t etab[32];
+    cj_exp_table(etab);   // visible after the first tile's barrier
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, j = lane & 15, grp = lane >> 4;
     const int nblk = (a.nrows + RB - 1) / RB;
     const int kvh = (int)(blockIdx.x % a.n_kv), rb = nblk - 1 - (int)(blockIdx.x / a.n_kv);
@@ -1651,13 +1688,13 @@ DEV void prefill_body(const cj_attn_args &a) {
                     d = __fadd_rn(d, dpp_rowf<0x141>(d));   // half-row mirror: the halves of 8
                     d = __fadd_rn(d, dpp_rowf<0x140>(d));   // row mirror: the 16
                     if (d > m[s]) {
-                        const float c = cj_expf(m[s] - d);
+                        const float c = cj_expf(m[s] - d, etab);
 #pragma unroll
                         for (int v = 0; v < 8; v++) acc[s][v] = __fmul_rn(acc[s][v], c);
                         l[s] = __fmul_rn(l[s], c);
                         m[s] = d;
                     }
-                    const float pw = cj_expf(d - m[s]);
+                    const float pw = cj_expf(d - m[s], etab);
                     l[s] = __fadd_rn(l[s], pw);
 #pragma unroll
                     for (int v = 0; v < 8; v++) acc[s][v] = __fadd_rn(acc[s][v], __fmul_rn(vf[v], pw));

@@ -120,8 +120,11 @@ __device__ __constant__ uint64_t CJ_EXP2_TAB[32] = {
 };
 // Branch-free: the main path runs on x clamped into its range (the same x
 // wherever the result is used) and the special cases are selected after, so
-// a caller's independent exps issue their table loads together.
-DEV float cj_expf(float x) {
+// a caller's independent exps issue their table loads together. `tab` is the
+// table: CJ_EXP2_TAB itself, or a kernel's LDS copy of it (cj_exp_table),
+// which keeps a global round trip off each exp where the exps sit on a
+// kernel's critical path.
+DEV float cj_expf(float x, const uint64_t *tab) {
     const float hi = 0x1.62e42ep6f, lo = -0x1.9fe368p6f;
     const float xc = fminf(fmaxf(x, lo), hi);
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
@@ -132,7 +135,7 @@ DEV float cj_expf(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = kd - shift;
     const double r = __fma_rn(inv_ln2_n, xd, -kd);
-    const double s = __longlong_as_double((long long)(CJ_EXP2_TAB[ki & 31] + (ki << 47)));
+    const double s = __longlong_as_double((long long)(tab[ki & 31] + (ki << 47)));
     const double z = __fma_rn(c0, r, c1), r2 = r * r;
     double y = __fma_rn(c2, r, 1.0);
     y = __fma_rn(z, r2, y);
@@ -140,6 +143,12 @@ DEV float cj_expf(float x) {
     e = x > hi ? __uint_as_float(0x7f800000u) : e;
     e = x < lo ? 0.0f : e;
     return x != x ? x + x : e;
+}
+DEV float cj_expf(float x) { return cj_expf(x, CJ_EXP2_TAB); }
+// A workgroup's LDS copy of the exp table (threads 0..31 write it; the
+// caller's next barrier makes it visible).
+DEV void cj_exp_table(uint64_t *tab) {
+    if (threadIdx.x < 32) tab[threadIdx.x] = CJ_EXP2_TAB[threadIdx.x];
 }
 
 // SiLU(x)·u, exp form: x / (1 + exp(−x)) · u (Prim.gluF32 / gluOne).
