@@ -1267,14 +1267,15 @@ Q4KI_EPIS(p, CJ_PRO_PACK, 64, _w, 4, 4)
 // Four E2M1 codes (the low nibbles of v's bytes) as four int8 values of the
 // reference's table {0, 1, 2, 3, 4, 6, 8, 12} with the sign bit (Quant.mxfp4Kv):
 // the magnitude through a byte permute of the positive and of the negated
-// table, the sign bit choosing between them per byte (permute selector 12
-// gives 0x00, 13 gives 0xFF).
+// table, then a third permute takes byte j from the negated result where the
+// code's sign bit (bit 3) is set — selector byte j + 4·sign — six operations
+// for four codes.
 DEV uint32_t e2m1_x4(uint32_t v) {
     const uint32_t idx = v & 0x07070707u;
     const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, idx);
     const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, idx);
-    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((v >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
-    return (neg & mask) | (pos & ~mask);
+    const uint32_t sel = ((v >> 1) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(neg, pos, sel);
 }
 
 // The LDS layout after the scratch: codes [cols], scales [nb], row values [R].
