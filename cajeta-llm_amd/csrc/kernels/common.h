@@ -63,23 +63,82 @@ DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((in
 DEV int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 DEV int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
 
+// Lane exchanges in the VALU, without an LDS round trip: DPP (quad
+// permutes and rotations inside each 16-lane row) and v_permlane16_swap /
+// v_permlane32_swap across rows. Every lane of the wave must be active.
+template <int CTRL>
+DEV float dpp_f(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)); }
+template <int CTRL>
+DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128 };
+// The two halves of a xor-16 exchange: a holds rows 0,0,2,2 of the wave and b
+// rows 1,1,3,3, so a + b (or max) is each lane's value with lane ^ 16's.
+// (The results are copied out as scalars: a bit cast of the builtin's vector
+// element reads element 0.)
+DEV void swap16(int v, int &a, int &b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+DEV void swap32(int v, int &a, int &b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+// The 32-lane xor butterfly v + v(lane ^ m) for m = 16, 8, 4, 2, 1 in that
+// order, every lane ending with its 32-lane group's sum — bit for bit the
+// __shfl_xor loop. ^8 is a rotation by 8 inside the 16-lane row; after it the
+// values repeat every 8 lanes, so a rotation by 4 brings lane ^ 4's value.
+DEV float xsum32(float v) {
+    int a, b;
+    swap16(__float_as_int(v), a, b);
+    v = __fadd_rn(__int_as_float(a), __int_as_float(b));
+    v = __fadd_rn(v, dpp_f<DPP_ROR8>(v));
+    v = __fadd_rn(v, dpp_f<DPP_ROR4>(v));
+    v = __fadd_rn(v, dpp_f<DPP_XOR2>(v));
+    return __fadd_rn(v, dpp_f<DPP_XOR1>(v));
+}
+DEV int xsum32_i(int v) {
+    int a, b;
+    swap16(v, a, b);
+    v = a + b;
+    v += dpp_i<DPP_ROR8>(v);
+    v += dpp_i<DPP_ROR4>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    return v + dpp_i<DPP_XOR1>(v);
+}
+DEV float xmax32(float v) {
+    int a, b;
+    swap16(__float_as_int(v), a, b);
+    v = fmaxf(__int_as_float(a), __int_as_float(b));
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    return fmaxf(v, dpp_f<DPP_XOR1>(v));
+}
+DEV float xmax64(float v) {
+    int a, b;
+    swap32(__float_as_int(xmax32(v)), a, b);
+    return fmaxf(__int_as_float(a), __int_as_float(b));
+}
+
 template <int W>
 DEV float group_sum(float v) {
 #pragma unroll
     for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m);
     return v;
 }
+// The integer sum and the maximum do not depend on the order.
 template <int W>
 DEV int group_sum_i(int v) {
-#pragma unroll
-    for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+    static_assert(W == 32, "32-lane groups");
+    return xsum32_i(v);
 }
 template <int W>
 DEV float group_max(float v) {
-#pragma unroll
-    for (int m = W / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+    static_assert(W == 32 || W == 64, "32- or 64-lane groups");
+    return W == 32 ? xmax32(v) : xmax64(v);
 }
 
 // Round half away from zero, the reference's Math.round on pack values.
@@ -209,16 +268,12 @@ DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
     const float av = fabsf(v);
     float am;
     if (per32) {
-        float m = av;
-#pragma unroll
-        for (int s = 16; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+        const float m = xmax32(av);
         if ((lane & 31) == 0) bmax[t >> 5] = m;
         __syncthreads();
         am = bmax[t >> 5];
     } else {
-        float m = av;
-#pragma unroll
-        for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+        const float m = xmax64(av);
         if (lane == 0) bmax[t >> 6] = m;
         __syncthreads();
         am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
@@ -226,9 +281,7 @@ DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
     const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
     const int q = round_away(__fmul_rn(v, inv));
     ob[t] = (uint8_t)(int8_t)q;
-    int s = q;
-#pragma unroll
-    for (int k = 16; k > 0; k >>= 1) s += __shfl_xor(s, k);
+    const int s = xsum32_i(q);
     if ((lane & 31) == 0) *(int32_t *)(ob + 256 + 4 * (t >> 5)) = s;
     if (per32) {
         if ((lane & 31) == 0) *(float *)(ob + 288 + 4 * (t >> 5)) = __fdiv_rn(am, 127.0f);

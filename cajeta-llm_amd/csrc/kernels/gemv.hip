@@ -1386,9 +1386,7 @@ DEV void mxq8_body(const cj_gemv_args &a) {
         }
 #pragma unroll
         for (int i = 0; i < RW; i++) {
-            float v = acc[i];
-#pragma unroll
-            for (int m = 16; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_xor(v, m));
+            const float v = xsum32(acc[i]);
             if (hl == 0 && i0 + i < R) res[i0 + i] = v;
         }
     }
@@ -1535,9 +1533,7 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
                 }
 #pragma unroll
                 for (int i = 0; i < RW; i++) {
-                    float v = acc[i];
-#pragma unroll
-                    for (int m = 16; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_xor(v, m));
+                    const float v = xsum32(acc[i]);
                     if (hl == 0) res[(p * 8 * RW + hw * RW + i) * RS + jj] = v;
                 }
             }
@@ -1570,14 +1566,10 @@ DEV void moe_grp_body(const cj_moe_grp_args &a) {
                 const int64_t ai = row0 / 2 + o;
                 float v = 0.0f;
                 if (on && ai < a.act_n) v = glu_value(a.glu_form, ai, a.act_n, res[(2 * o) * RS + jj], res[(2 * o + 1) * RS + jj]);
-                float bm = fabsf(v);
-#pragma unroll
-                for (int m = 16; m > 0; m >>= 1) bm = fmaxf(bm, __shfl_xor(bm, m));
+                const float bm = xmax32(fabsf(v));
                 const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
                 const int q = round_away(__fmul_rn(v, inv));
-                int sq = q;
-#pragma unroll
-                for (int m = 16; m > 0; m >>= 1) sq += __shfl_xor(sq, m);
+                const int sq = xsum32_i(q);
                 if (on) {
                     uint8_t *ob = a.outp + (int64_t)mi[jj] * a.outp_stride + (ab >> 3) * 320;
                     ob[(ab & 7) * 32 + o] = (uint8_t)(int8_t)q;
