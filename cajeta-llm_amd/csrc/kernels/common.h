@@ -70,7 +70,10 @@ template <int CTRL>
 DEV float dpp_f(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)); }
 template <int CTRL>
 DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
-enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128 };
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HMIRROR = 0x141, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128 };
+// row_shl:K — lane i reads lane i + K of its 16-lane row
+template <int K>
+DEV float dpp_shl(float v) { return dpp_f<0x100 + K>(v); }
 // The two halves of a xor-16 exchange: a holds rows 0,0,2,2 of the wave and b
 // rows 1,1,3,3, so a + b (or max) is each lane's value with lane ^ 16's.
 // (The results are copied out as scalars: a bit cast of the builtin's vector
@@ -116,6 +119,32 @@ DEV float xmax32(float v) {
     v = fmaxf(v, dpp_f<DPP_ROR4>(v));
     v = fmaxf(v, dpp_f<DPP_XOR2>(v));
     return fmaxf(v, dpp_f<DPP_XOR1>(v));
+}
+// The maximum over aligned groups of 8 and of 16 lanes. After the two quad
+// steps the four lanes of a quad agree, so lane 7 − i of the eight (the half
+// mirror) stands for lane i ^ 4.
+DEV float xmax8(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    return fmaxf(v, dpp_f<DPP_HMIRROR>(v));
+}
+DEV float xmax16(float v) {
+    v = xmax8(v);
+    return fmaxf(v, dpp_f<DPP_ROR8>(v));
+}
+// Lane 0's value of the fold v + v(lane + m), m = 32, 16, ..., 1 (the
+// __shfl_down loop): lane 0 of the xor butterfly in the same order adds the
+// same two values at every step.
+DEV float fold64_lane0(float v) {
+    int a, b;
+    swap32(__float_as_int(v), a, b);
+    v = __fadd_rn(__int_as_float(a), __int_as_float(b));
+    swap16(__float_as_int(v), a, b);
+    v = __fadd_rn(__int_as_float(a), __int_as_float(b));
+    v = __fadd_rn(v, dpp_f<DPP_ROR8>(v));
+    v = __fadd_rn(v, dpp_f<DPP_ROR4>(v));
+    v = __fadd_rn(v, dpp_f<DPP_XOR2>(v));
+    return __fadd_rn(v, dpp_f<DPP_XOR1>(v));
 }
 DEV float xmax64(float v) {
     int a, b;
@@ -365,9 +394,7 @@ DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
     __syncthreads();
     if (t < 64) {
-        float s = __fadd_rn(red[t], red[t + 64]);
-#pragma unroll
-        for (int m = 32; m > 0; m >>= 1) s = __fadd_rn(s, __shfl_down(s, m));
+        const float s = fold64_lane0(__fadd_rn(red[t], red[t + 64]));
         if (t == 0) red[0] = s;
     }
     __syncthreads();
@@ -414,12 +441,7 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
         float am = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; k++) am = fmaxf(am, fabsf(v[k]));
-        am = fmaxf(am, __shfl_xor(am, 1));
-        if (!per32) {
-            am = fmaxf(am, __shfl_xor(am, 2));
-            am = fmaxf(am, __shfl_xor(am, 4));
-            am = fmaxf(am, __shfl_xor(am, 8));
-        }
+        am = per32 ? fmaxf(am, dpp_f<DPP_XOR1>(am)) : xmax16(am);
         const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
         uint32_t wd[4] = {0u, 0u, 0u, 0u};
         int sum = 0;
@@ -429,7 +451,7 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
             sum += q;
             wd[k >> 2] |= ((uint32_t)q & 255u) << (8 * (k & 3));
         }
-        sum += __shfl_xor(sum, 1);
+        sum += quad_xor1(sum);
         const int64_t blk = e0 >> 8;
         const int in = (int)(e0 & 255);           // offset inside the block
         uint8_t *b = sx + blk * bstride;
@@ -600,9 +622,10 @@ DEV int32_t step_pos(const cj_step_state *st, int32_t pos) { return st ? st->pos
 // of the workgroup computes (up to 256 experts); every thread passes the
 // barriers. The logits and probabilities live in LDS; the max and the sum
 // run on one lane in expert order as the reference forms them, the exps and
-// the divides a lane an expert, and each top-k pick is a wave reduction —
-// the largest valid probability, the lowest index among equals, which is the
-// first strict maximum of the reference's scan whatever order finds it.
+// the divides a lane an expert. Each top-k pick of the reference is the first
+// strict maximum of its scan over the experts not yet picked — the largest
+// valid probability, the lowest index among equals — so pick k is the expert
+// with exactly k experts ahead of it in that order, counted a lane an expert.
 // Result in s.sel / s.w (n_used entries). Logits that are not finite leave
 // no valid probability: the reference refuses the row by name; here
 // `status` (may be null) is set to 1 (the host raises after the step) and
@@ -637,34 +660,40 @@ DEV void route_row(const float *lg, int ne, int n_used, int norm_topk, float w_s
     __syncthreads();
     if (t < 64) {
         const float sum = s.bc[1];
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int e = t; e < ne; e += 64) s.pr[e] = __fdiv_rn(s.pr[e], sum);   // the probabilities
+    }
+    __syncthreads();
+    if (t < 64) {
+        // The picks in order: the larger probability first, on a tie the
+        // lower index, an entry that is not a number never (the repeated
+        // arg-max of routeFromLogits). That is a total order, so expert e is
+        // pick number (experts ahead of e) when that is below n_used: one
+        // pass of comparisons instead of n_used rounds of a wave reduction.
+        int nvalid = 0;
+        for (int j = 0; 64 * j < ne; j++) {
             const int e = t + 64 * j;
-            v[j] = e < ne ? __fdiv_rn(s.pr[e], sum) : -1.0f;   // -1: no expert (never valid)
-        }
-        for (int k = 0; k < n_used; k++) {
-            float bv = 0.0f;
-            int bi = -1;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (v[j] >= 0.0f && (bi < 0 || v[j] > bv)) { bv = v[j]; bi = t + 64 * j; }
-#pragma unroll
-            for (int m = 32; m > 0; m >>= 1) {
-                const float ov = __shfl_xor(bv, m);
-                const int oi = __shfl_xor(bi, m);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            const float v = e < ne ? s.pr[e] : -1.0f;
+            const bool ok = v >= 0.0f;
+            nvalid += __popcll(__ballot(ok));
+            if (ok) {
+                int ahead = 0;
+                for (int x = 0; x < ne; x++) {
+                    const float o = s.pr[x];
+                    ahead += (o >= 0.0f && (o > v || (o == v && x < e))) ? 1 : 0;
+                }
+                if (ahead < n_used) {
+                    s.sel[ahead] = e;
+                    s.w[ahead] = v;
+                }
             }
-            if (bi < 0) {
-                bi = 0;
-                bv = 0.0f;
-                if (t == 0 && status) status[0] = 1;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (t + 64 * j == bi) v[j] = -1.0f;
-            if (t == 0) { s.sel[k] = bi; s.w[k] = bv; }
         }
+        // fewer valid experts than picks: expert 0 with weight 0, flagged
+        if (t == 0)
+            for (int k = nvalid; k < n_used; k++) {
+                s.sel[k] = 0;
+                s.w[k] = 0.0f;
+                if (status) status[0] = 1;
+            }
     }
     __syncthreads();
     if (t == 0) {

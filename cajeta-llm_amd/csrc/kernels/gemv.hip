@@ -260,8 +260,6 @@ DEV void terms_q6k_1(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], con
 // reference's fs) and the group's first lane writes it.
 template <int NR, int LPR>
 DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
-    const int lane = threadIdx.x & 63;
-    const int base = lane & ~7;
     const int iters = (nb32 + LPR - 1) / LPR;
     for (int it = 0; it < iters; it++) {
         const int u = slot + it * LPR;
@@ -287,12 +285,14 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
             s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
             s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
             const float t = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
-            float fs = __shfl(t, base);
+            // lane base + k's term reaches lane base by row_shl:k (base is a
+            // multiple of 8, so the eight stay inside one 16-lane row)
+            const float o[7] = {dpp_shl<1>(t), dpp_shl<2>(t), dpp_shl<3>(t), dpp_shl<4>(t),
+                                dpp_shl<5>(t), dpp_shl<6>(t), dpp_shl<7>(t)};
+            float fs = t;
 #pragma unroll
-            for (int k = 1; k < 8; k++) {
-                const float o = __shfl(t, base + k);
-                if (k < left) fs = __fadd_rn(fs, o);
-            }
+            for (int k = 1; k < 8; k++)
+                if (k < left) fs = __fadd_rn(fs, o[k - 1]);
             if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
     }
@@ -443,7 +443,7 @@ DEV void gemv_epilogue_t(const cj_gemv_args &a, const GemvSlice &sl, float v, fl
     const bool live = t < R && r < a.rows;
     float *Y = sl.Y, *ACT = sl.ACT;
     const int64_t row0 = sl.row0;
-    const float vp = __shfl_xor(v, 1);      // the paired row (RoPE pair, gate/up pair)
+    const float vp = dpp_f<DPP_XOR1>(v);    // the paired row (RoPE pair, gate/up pair)
     const int pos = EPI == CJ_EPI_QKV_ROPE ? pre.pos : EPI == CJ_EPI_ARGMAX ? step_pos(a.state, a.pos) : 0;
 
     switch (EPI) {
@@ -958,12 +958,7 @@ DEV void q4k_pack_slice(const float (&v)[16], int64_t e0, int per32, uint8_t *sx
     float am = 0.0f;
 #pragma unroll
     for (int k = 0; k < 16; k++) am = fmaxf(am, fabsf(v[k]));
-    am = fmaxf(am, __shfl_xor(am, 1));
-    if (!per32) {
-        am = fmaxf(am, __shfl_xor(am, 2));
-        am = fmaxf(am, __shfl_xor(am, 4));
-        am = fmaxf(am, __shfl_xor(am, 8));
-    }
+    am = per32 ? fmaxf(am, dpp_f<DPP_XOR1>(am)) : xmax16(am);
     const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
     uint32_t wd[4] = {0u, 0u, 0u, 0u};
     int sum = 0;
@@ -973,7 +968,7 @@ DEV void q4k_pack_slice(const float (&v)[16], int64_t e0, int per32, uint8_t *sx
         sum += q;
         wd[k >> 2] |= ((uint32_t)q & 255u) << (8 * (k & 3));
     }
-    sum += __shfl_xor(sum, 1);
+    sum += quad_xor1(sum);
     const int64_t blk = e0 >> 8;
     const int in = (int)(e0 & 255);
     uint8_t *b = sx + blk * bstride;
@@ -1018,9 +1013,7 @@ DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PR
             if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
             __syncthreads();
             if (t < 64) {
-                float v = __fadd_rn(red[t], red[t + 64]);
-#pragma unroll
-                for (int m = 32; m > 0; m >>= 1) v = __fadd_rn(v, __shfl_down(v, m));
+                const float v = fold64_lane0(__fadd_rn(red[t], red[t + 64]));
                 if (t == 0) red[0] = v;
             }
             __syncthreads();
@@ -1338,9 +1331,7 @@ DEV void mxq8_body(const cj_gemv_args &a) {
 #pragma unroll
             for (int k = 0; k < PR; k++) {
                 const int b = b0 + 32 * k + (t >> 3);
-                float bm = fmaxf(fmaxf(fabsf(f[k].x), fabsf(f[k].y)), fmaxf(fabsf(f[k].z), fabsf(f[k].w)));
-#pragma unroll
-                for (int m = 1; m < 8; m <<= 1) bm = fmaxf(bm, __shfl_xor(bm, m));
+                const float bm = xmax8(fmaxf(fmaxf(fabsf(f[k].x), fabsf(f[k].y)), fmaxf(fabsf(f[k].z), fabsf(f[k].w))));
                 const float inv = bm > 0.0f ? __fdiv_rn(127.0f, bm) : 0.0f;
                 const uint32_t q = ((uint32_t)round_away(__fmul_rn(f[k].x, inv)) & 0xFFu) |
                                    (((uint32_t)round_away(__fmul_rn(f[k].y, inv)) & 0xFFu) << 8) |
@@ -1363,6 +1354,10 @@ DEV void mxq8_body(const cj_gemv_args &a) {
         for (int i = 0; i < RW; i++) acc[i] = 0.0f;
         for (int c0 = 0; c0 < nb; c0 += 32 * KB) {
             fetch(i0, c0);
+            // keep the sweep's loads ahead of its arithmetic (the scheduler
+            // otherwise sinks them between the decodes, each then waited for
+            // in turn)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < RW; i++) {
 #pragma unroll

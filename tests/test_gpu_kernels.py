@@ -317,12 +317,14 @@ def test_qk_prep_rope_and_append(gpu, O, hd, n_q, n_kv, theta):
     assert np.array_equal(vcache[pos // 64, :, pos % 64, :].reshape(-1), O.f32_to_f16_bits(v))
 
 
-@pytest.mark.parametrize("ne,k", [(32, 4), (128, 8), (8, 2)])
+@pytest.mark.parametrize("ne,k", [(32, 4), (128, 8), (8, 2), (200, 4), (256, 8)])
 def test_moe_route(gpu, O, ne, k):
     rng = np.random.default_rng(ne)
     rows = 5
     lg = rng.standard_normal((rows, ne)).astype(np.float32)
     lg[2, 3] = lg[2, 5] = 7.0                     # tie: the lower index first
+    lg[3, :] = 0.5                                # every probability equal: 0, 1, ..., k-1
+    lg[4, ne - 1] = lg[4, ne - 2] = 9.0           # a tie at the top across lanes
     lb, sb, wb = gpu.Buffer.of(lg), gpu.Buffer(rows * k * 4), gpu.Buffer(rows * k * 4)
     gpu.native.check(gpu.native.lib().cj_moe_route(sb.h, wb.h, lb.h, rows, ne, k, 1, 0.0, 0), "route")
     sel = sb.download(np.int32, rows * k).reshape(rows, k)
