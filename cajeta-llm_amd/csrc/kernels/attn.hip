@@ -717,11 +717,9 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
         }
     }
     // max is exact, so a wave reduction and then the two waves' maxima
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float y = __shfl_xor(mx, o);
-        if (y > mx) mx = y;
-    }
+// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
+// comparison; a tie of -0 and +0 changes no exp(s - m))
+mx = xmax64(mx);
     if ((l & 63) == 0) red[l >> 6] = mx;
     __syncthreads();
     const float m = red[1] > red[0] ? red[1] : red[0];
@@ -777,9 +775,7 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
     if (l < 128) red[4 + l] = s;
     __syncthreads();
     if (l < 64) {
-        float v2 = __fadd_rn(red[4 + l], red[4 + l + 64]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        const float v2 = fold64_lane0(__fadd_rn(red[4 + l], red[4 + l + 64]));
         if (l == 0) red[2] = v2;
     }
     __syncthreads();
@@ -846,8 +842,7 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     float mx = -3.0e38f;
     if (l < 128)
         for (int t = l; t < count; t += 128) mx = fmaxf(mx, sc[t]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+mx = xmax64(mx);
     if ((l & 63) == 0) red[l >> 6] = mx;
     __syncthreads();
     const float m = fmaxf(red[0], red[1]);
@@ -862,9 +857,7 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     if (l < 128) red[4 + l] = s;
     __syncthreads();
     if (l < 64) {
-        float v2 = __fadd_rn(red[4 + l], red[4 + l + 64]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        const float v2 = fold64_lane0(__fadd_rn(red[4 + l], red[4 + l + 64]));
         if (l == 0) red[2] = v2;
     }
     __syncthreads();
@@ -950,11 +943,9 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
                 for (int k = 0; k < 8; k++) if (b + l + 128 * k < count && u[k] > mx) mx = u[k];
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float y = __shfl_xor(mx, o);
-            if (y > mx) mx = y;
-        }
+// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
+// comparison; a tie of -0 and +0 changes no exp(s - m))
+mx = xmax64(mx);
         if ((t & 63) == 0) gmax[t >> 6] = mx;
         __syncthreads();
         const float m = gmax[2 * g + 1] > gmax[2 * g] ? gmax[2 * g + 1] : gmax[2 * g];
@@ -991,9 +982,7 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
         tree[t] = s;
         __syncthreads();
         if (l < 64) {
-            float v2 = __fadd_rn(tree[128 * g + l], tree[128 * g + l + 64]);
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+            const float v2 = fold64_lane0(__fadd_rn(tree[128 * g + l], tree[128 * g + l + 64]));
             if (l == 0) rsum[j0 + g] = __fdiv_rn(1.0f, v2);
         }
         __syncthreads();   // the weights written over the scores are visible to the workgroup
@@ -1252,11 +1241,9 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     if (l < 128) {
         for (int t = j; t < count; t += 128) if (sc[t] > mx) mx = sc[t];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float y = __shfl_xor(mx, o);
-        if (y > mx) mx = y;
-    }
+// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
+// comparison; a tie of -0 and +0 changes no exp(s - m))
+mx = xmax64(mx);
     if (l < 128 && (l & 63) == 0) mred[l >> 6] = mx;
     __syncthreads();
     const float m = mred[1] > mred[0] ? mred[1] : mred[0];
@@ -1271,9 +1258,7 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     }
     __syncthreads();
     if (l < 64) {
-        float v2 = __fadd_rn(red[l], red[l + 64]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v2 = __fadd_rn(v2, __shfl_down(v2, o));
+        const float v2 = fold64_lane0(__fadd_rn(red[l], red[l + 64]));
         if (l == 0) rsv = __fdiv_rn(1.0f, v2);
     }
     __syncthreads();
@@ -1422,8 +1407,21 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args 
             ac = use ? a2 : ac;
         }
     }
-    const float g1 = __shfl(g, i + 16), g2 = __shfl(g, i + 32), g3 = __shfl(g, i + 48);
-    const float a1 = __shfl(ac, i + 16), a2 = __shfl(ac, i + 32), a3 = __shfl(ac, i + 48);
+    // lane i's partners i + 16, i + 32, i + 48 (rows 1, 2, 3 of the wave) by
+    // row swaps: the second half of a 16-row swap holds rows 1,1,3,3 and of a
+    // 32-lane swap rows 2,3,2,3; a 32-lane swap of the former brings row 3
+    auto rows123 = [](float v, float &v1, float &v2, float &v3) {
+        int a0, a1, b0, b1, c0, c1;
+        swap16(__float_as_int(v), a0, a1);
+        swap32(__float_as_int(v), b0, b1);
+        swap32(a1, c0, c1);
+        v1 = __int_as_float(a1);
+        v2 = __int_as_float(b1);
+        v3 = __int_as_float(c1);
+    };
+    float g1, g2, g3, a1, a2, a3;
+    rows123(g, g1, g2, g3);
+    rows123(ac, a1, a2, a3);
     if (j == 0) {
         const float gt = __fadd_rn(__fadd_rn(__fadd_rn(g, g1), g2), g3);
         const float tacc = __fadd_rn(__fadd_rn(__fadd_rn(ac, a1), a2), a3);

@@ -659,17 +659,21 @@ DEV void seq_products(const SeqItem<FMT> &it, const float4 (&xr)[8], float *dst)
     }
 }
 
-// Row threadIdx.x (< 64) of the workgroup's rows summed; x staged in LDS.
-// Every thread of the workgroup must call it (it holds barriers). A producer
-// lane keeps D tiles of its weights in flight (a ring indexed at compile
-// time: the tile loop is unrolled by D) and reads its next block of x from
-// LDS a tile ahead, so its products wait on neither; the adder reads a whole
-// tile of products before its first add.
+// Row threadIdx.x (< 64) of the workgroup's rows summed; x staged in LDS by
+// `pro`, the prologue, which every thread calls first. Every thread of the
+// workgroup must call it (it holds barriers). A producer lane keeps D tiles
+// of its weights in flight (a ring indexed at compile time: the tile loop is
+// unrolled by D) and reads its next block of x from LDS a tile ahead, so its
+// products wait on neither; the adder reads three blocks' products (24
+// 16-byte reads) before their 96 adds: measured against reads kept a fixed
+// distance ahead of the adds, each read then waited for in turn, the batch
+// is faster (a lone wave's chain: 6.9 against 8.3 cycles an add, 4.6 with
+// the operands in registers).
 #ifndef SEQ_D
 #define SEQ_D 8
 #endif
-template <int FMT, int ROWS>
-DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) {
+template <int FMT, int ROWS, class Pro>
+DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, Pro &&pro) {
     // one row a workgroup: a tile is 192 blocks, so two in flight suffice
     constexpr int D = ROWS == 1 ? 2 : SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
@@ -688,10 +692,10 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
     // buffer and never read)
     const int nit = (ntiles + D - 1) / D * D;
     float acc = 0.0f;
+    pro();
     if (w == 0) {
         __syncthreads();
         const float *pr0 = prod[0] + min(lane, ROWS - 1) * S;
-        // three blocks' products read before their first add
         auto add3 = [&](const float *pr, int b0) {
             float4 p[24];
 #pragma unroll
@@ -722,7 +726,6 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs) 
 #pragma unroll(TB <= 6 ? TB / 3 : 2)
                 for (int b0 = 0; b0 < TB; b0 += 3) add3(pr, b0);
             } else {
-                // a short tile (the row's last): whole chunks of three, then single blocks
                 int b0 = 0;
                 for (; b0 + 3 <= nb; b0 += 3) add3(pr, b0);
                 for (int b = b0; b < nb; b++) add1(pr, b);
@@ -853,7 +856,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
     // block of x, so each reads its block from global memory beside its
     // weights rather than after x is staged in LDS (one round trip fewer)
     const bool xdirect = f32act && LPR == 1 && a.pro == CJ_PRO_F32 && ((uintptr_t)sl.X & 15) == 0;
-    if (!xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
+    // (the f32-activation formats stage x inside seq_body, after a one-row
+    // workgroup's weights are requested)
+    if (!f32act && !xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
     const EpiPre pre = epi_prefetch(a, sl);
 
     float v = 0.0f;
@@ -863,7 +868,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
         // ---- one adder lane a row, in element order (64 rows a workgroup)
         // (for these formats LPR is the rows a workgroup: 64, or 32 / 1
         // where the matrix is short and more workgroups fill the chip)
-        const float sv = seq_body<FMT, LPR>(a, sl, xdirect ? sl.X : (const float *)sx);
+        const float sv = seq_body<FMT, LPR>(a, sl, xdirect ? sl.X : (const float *)sx, [&] {
+            if (!xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
+        });
         if (live) v = sv;
     } else {
     // ---- phase A: block terms of the workgroup's R rows, NR rows a group in flight
