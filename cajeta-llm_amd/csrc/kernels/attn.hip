@@ -545,18 +545,49 @@ struct CombineItem {
 // operation on the same operands as the sum pass, so the same bits): spans
 // longer than the LDS weight buffer never write the score row, which the
 // head's sibling workgroups read concurrently.
+// The item's four consecutive positions lie in at most two pages: the page
+// entries of its first and last position (two LDS reads, not four).
+struct CombinePages {
+    int first, last;
+};
+template <int T>
+DEV CombinePages combine_pages(const int *pgs, int count, int from, int tq, int I) {
+    const int t0 = I * T + 4 * tq;
+    const int pa = from + min(t0, count - 1), pb = from + min(t0 + 3, count - 1);
+    return CombinePages{pgs[(pa >> 6) - (from >> 6)], pgs[(pb >> 6) - (from >> 6)]};
+}
+template <int HD, int T>
+DEV void combine_fetch_v(CombineItem &it, const CombinePages &pg, const cj_attn_args &a, int count, int from, int kvh,
+                         int d0, int dg, int tq, int I) {
+    const int t0 = I * T + 4 * tq;
+    const int seg0 = (from + min(t0, count - 1)) >> 6;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int t = min(t0 + k, count - 1), pos = from + t;
+        const int page = (pos >> 6) == seg0 ? pg.first : pg.last;
+        it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + 8 * dg);
+    }
+}
+template <int HD, int T>
+DEV void combine_fetch_v(CombineItem &it, const cj_attn_args &a, const int *pgs, int count, int from, int kvh, int d0,
+                         int dg, int tq, int I) {
+    combine_fetch_v<HD, T>(it, combine_pages<T>(pgs, count, from, tq, I), a, count, from, kvh, d0, dg, tq, I);
+}
+template <int T, bool EXP>
+DEV void combine_fetch_e(CombineItem &it, const float *ev, float m, int count, int tq, int I, const uint64_t *et) {
+    const int t0 = I * T + 4 * tq;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int t = min(t0 + k, count - 1);
+        it.e[k] = EXP ? cj_expf(ev[t] - m, et) : ev[t];
+    }
+}
 template <int HD, int T, bool EXP>
 DEV CombineItem combine_fetch(const cj_attn_args &a, const int *pgs, const float *ev, float m, int count, int from,
                               int kvh, int d0, int dg, int tq, int I, const uint64_t *et) {
     CombineItem it;
-    const int t0 = I * T + 4 * tq;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int t = min(t0 + k, count - 1), pos = from + t;
-        const int page = pgs[(pos >> 6) - (from >> 6)];
-        it.v[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + d0 + 8 * dg);
-        it.e[k] = EXP ? cj_expf(ev[t] - m, et) : ev[t];
-    }
+    combine_fetch_v<HD, T>(it, a, pgs, count, from, kvh, d0, dg, tq, I);
+    combine_fetch_e<T, EXP>(it, ev, m, count, tq, I, et);
     return it;
 }
 
@@ -608,15 +639,16 @@ struct CombineDims {
     static constexpr int TQ = P / DG;               // 4-position groups a tile: one 4 × 8 item a producer lane
     static constexpr int T = 4 * TQ;                // positions a tile
     static constexpr int S = T + 4;                 // product row stride (floats): 16 lanes' 16-byte reads, distinct banks
+    static constexpr int PB = DH * S;               // a product buffer (floats)
 };
 
 // p·V of the combine: returns the adder lane's sum (0 on producers). `ev` is
 // the weights e_t in LDS or (EXP, spans past COMBINE_ES positions) the scores
 // with their maximum m. CD (even) tiles of V are in flight per producer; both
 // roles run a whole number of CD-tile rounds.
-template <int HD, int CD, bool EXP>
+template <int HD, int CD, bool EXP, class Exps, class Sums>
 DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, float m, float *prod, int count, int from,
-                     int kvh, int d0, const uint64_t *et) {
+                     int kvh, int d0, const uint64_t *et, Exps &&exps, Sums &&sums) {
     using D = CombineDims<HD>;
     constexpr int T = D::T, S = D::S;
     const int l = threadIdx.x, w = l >> 6, ntiles = (count + T - 1) / T;
@@ -625,11 +657,26 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
     // body has no branch (tiles past the end go to the idle buffer, unread)
     const int nit = (ntiles + CD - 1) / CD * CD;
     float acc = 0.0f;
+    // CD tiles of V rows in flight, ring slot = tile mod CD: the first CD
+    // tiles' rows are requested between the softmax's exps and its sums,
+    // which need none of them
+    CombineItem ring[CD];
+    exps();
+    if (w >= D::A) {
+        // every page entry first, then the rows: no load waits on an LDS read
+        // issued after an earlier load
+        CombinePages pg[CD];
+#pragma unroll
+        for (int j = 0; j < CD; j++) pg[j] = combine_pages<T>(pgs, count, from, tq, j);
+#pragma unroll
+        for (int j = 0; j < CD; j++) combine_fetch_v<HD, T>(ring[j], pg[j], a, count, from, kvh, d0, dg, tq, j);
+    }
+    sums();
     if (w < D::A) {
-        __syncthreads();
+        lds_barrier();
         const float *pr = prod + min(l, D::DH - 1) * S;
         for (int i = 0; i < nit; i++) {
-            const float *pt = pr + (i & 1) * (D::DH * S);
+            const float *pt = pr + (i & 1) * D::PB;
             const int n = i < ntiles ? min(T, count - i * T) : 0;
             if (n == T) {
                 // every read issued before the first add (the scheduler would
@@ -654,24 +701,22 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
                     acc = __fadd_rn(acc, p.w);
                 }
             }
-            __syncthreads();
+            lds_barrier();
         }
     } else {
-        // CD tiles of V rows and weights in flight, ring slot = tile mod CD
-        CombineItem ring[CD];
 #pragma unroll
-        for (int j = 0; j < CD; j++) ring[j] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, j, et);
+        for (int j = 0; j < CD; j++) combine_fetch_e<T, EXP>(ring[j], ev, m, count, tq, j, et);
         float *pb = prod + 8 * dg * S + 4 * tq;
         combine_store<T, S>(pb, ring[0], 0, count, tq);
         ring[0] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, CD, et);
-        __syncthreads();
+        lds_barrier();
         for (int i0 = 0; i0 < nit; i0 += CD) {
 #pragma unroll
             for (int j = 0; j < CD; j++) {
                 const int i = i0 + j, r = (j + 1) % CD;
-                combine_store<T, S>(pb + ((j + 1) & 1) * (D::DH * S), ring[r], i + 1, count, tq);
+                combine_store<T, S>(pb + ((j + 1) & 1) * D::PB, ring[r], i + 1, count, tq);
                 ring[r] = combine_fetch<HD, T, EXP>(a, pgs, ev, m, count, from, kvh, d0, dg, tq, i + 1 + CD, et);
-                __syncthreads();
+                lds_barrier();
             }
         }
     }
@@ -682,32 +727,37 @@ template <int HD>
 DEV void combine_body(const cj_attn_args &a, int bx) {
     using D = CombineDims<HD>;
     __shared__ float red[4 + 128];
-    __shared__ __align__(16) float prod[2 * D::DH * D::S];   // also V of a short span: 2048 chunks of 16 bytes
+    __shared__ __align__(16) float prod[2 * D::PB];   // also V of a short span: 2048 chunks of 16 bytes
     __shared__ int pgs[COMBINE_PAGES];
     __shared__ __align__(16) float es[COMBINE_ES];
     __shared__ uint64_t etab[32];
     cj_exp_table(etab);   // visible after the max's barrier
     int count, from;
     attn_window(a, count, from);
-    const int h = bx / D::NSPLIT, d0 = D::DH * (bx % D::NSPLIT), l = threadIdx.x;
-    const int grp = a.n_q / a.n_kv, kvh = h / grp;
+    // workgroups are dealt to the eight XCDs round-robin by id, so taking
+    // the kv head as id mod n_kv keeps the grp·NSPLIT workgroups that read one
+    // kv head's V rows on one XCD, whose L2 serves the repeats
+    const int grp = a.n_q / a.n_kv, kvh = bx % a.n_kv, r = bx / a.n_kv, l = threadIdx.x;
+    const int h = kvh * grp + r / D::NSPLIT, d0 = D::DH * (r % D::NSPLIT);
     const float *sc = a.part + (int64_t)h * a.splits;
     const int npg = ((from + count - 1) >> 6) - (from >> 6) + 1;
     // the page entries and the first round of scores are requested together
-    // (one memory round trip); lane l < 128 takes positions l + 128k
-    constexpr int PK = COMBINE_ES / 128;
+    // (one memory round trip). The max and the exps of the span's first
+    // COMBINE_ES positions are spread over the four waves: lane l holds the
+    // slots k = 2i + l/128 of reference lane l mod 128 (positions
+    // (l mod 128) + 128k)
+    constexpr int PK = COMBINE_ES / 128, PH = PK / 2;
+    const int j128 = l & 127, half = l >> 7;
     const int pg0 = l < npg ? a.pgtab[a.pg_base + (from >> 6) + l] : 0;
-    float v[PK];
-    if (l < 128) {
+    float v[PH];
 #pragma unroll
-        for (int k = 0; k < PK; k++) v[k] = sc[min(l + 128 * k, count - 1)];
-    }
+    for (int i = 0; i < PH; i++) v[i] = sc[min(j128 + 128 * (2 * i + half), count - 1)];
     if (l < npg) pgs[l] = pg0;
     for (int j = l + 256; j < npg; j += 256) pgs[j] = a.pgtab[a.pg_base + (from >> 6) + j];
     float mx = -3.0e38f;
-    if (l < 128) {
 #pragma unroll
-        for (int k = 0; k < PK; k++) if (l + 128 * k < count && v[k] > mx) mx = v[k];
+    for (int i = 0; i < PH; i++) if (j128 + 128 * (2 * i + half) < count && v[i] > mx) mx = v[i];
+    if (l < 128) {
         for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
             float u[PK];
 #pragma unroll
@@ -716,13 +766,13 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
             for (int k = 0; k < PK; k++) if (base + l + 128 * k < count && u[k] > mx) mx = u[k];
         }
     }
-    // max is exact, so a wave reduction and then the two waves' maxima
-// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
-// comparison; a tie of -0 and +0 changes no exp(s - m))
-mx = xmax64(mx);
+    // max is exact, so a wave reduction and then the waves' maxima (no lane
+    // holds a NaN here, so fmaxf agrees with the comparison; a tie of -0 and
+    // +0 changes no exp(s - m))
+    mx = xmax64(mx);
     if ((l & 63) == 0) red[l >> 6] = mx;
     __syncthreads();
-    const float m = red[1] > red[0] ? red[1] : red[0];
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     // short spans take V whole into LDS: the rows are requested here (their
     // page entries are visible after the barrier above) while the weights
     // form, and each adder lane then runs its chain from LDS
@@ -737,50 +787,65 @@ mx = xmax64(mx);
             vst[k] = *(const u32x4 *)(a.vc + (((int64_t)page * a.n_kv + kvh) * 64 + (pos & 63)) * HD + 8 * j);
         }
     }
-    // e_t in order per lane; kept in LDS when the span fits, else formed
-    // again from the scores where p·V needs it (the score row is shared by
-    // the head's HD/32 workgroups and stays read-only)
+    // e_t of the first COMBINE_ES positions in LDS (past them, formed again
+    // from the scores where the sum and p·V need it: the score row is shared
+    // by the head's HD/32 workgroups and stays read-only)
     const bool elds = count <= COMBINE_ES;
-    float s = 0.0f;
-    if (l < 128) {
-        // every slot's exp formed (past count a repeat, unused), then the
-        // ordered sum
+    auto exps = [&] {
 #pragma unroll
-        for (int k = 0; k < PK; k++) v[k] = cj_expf(v[k] - m, etab);
-#pragma unroll
-        for (int k = 0; k < PK; k++) {
-            const int t = l + 128 * k;
-            if (t < count) {
-                if (elds) es[t] = v[k];
-                s = __fadd_rn(s, v[k]);
+        for (int i = 0; i < PH; i++) {
+            const int k = 2 * i + half, t = j128 + 128 * k;
+            if (128 * k < count) {   // the same for the wave: a slot some lane needs
+                const float e = cj_expf(v[i] - m, etab);
+                if (t < count) es[t] = e;
             }
         }
-        for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
-            float u[PK];
+    };
+    float rs = 0.0f;
+    // lane l < 128 adds its positions l, l + 128, ... in order, as the
+    // reference's lane l does, then the 128 sums fold
+    auto sums = [&] {
+        lds_barrier();                 // the exps in LDS; red[0..3] read by every lane above
+        float s = 0.0f;
+        if (l < 128) {
+            // every read issued before the first add (kept two in flight, each
+            // pair's latency is waited out in turn)
+            float e[PK];
 #pragma unroll
-            for (int k = 0; k < PK; k++) u[k] = sc[min(base + l + 128 * k, count - 1)];
+            for (int k = 0; k < PK; k++)
+                if (128 * k < count) e[k] = es[min(l + 128 * k, COMBINE_ES - 1)];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int k = 0; k < PK; k++) {
-                const int t = base + l + 128 * k;
-                if (t < count) {
-                    const float e = cj_expf(u[k] - m, etab);
-                    s = __fadd_rn(s, e);
+            for (int k = 0; k < PK; k++)
+                if (128 * k < count) s = l + 128 * k < count ? __fadd_rn(s, e[k]) : s;
+            for (int base = COMBINE_ES; base < count; base += COMBINE_ES) {
+                float u[PK];
+#pragma unroll
+                for (int k = 0; k < PK; k++) u[k] = sc[min(base + l + 128 * k, count - 1)];
+#pragma unroll
+                for (int k = 0; k < PK; k++) {
+                    const int t = base + l + 128 * k;
+                    if (t < count) {
+                        const float e = cj_expf(u[k] - m, etab);
+                        s = __fadd_rn(s, e);
+                    }
                 }
             }
         }
-    }
-    // the reference's 128-lane stride-halving tree: the 64 stride crosses
-    // waves through LDS, the strides 32..1 are wave 0's shuffles
-    __syncthreads();                 // red[0..1] read by every lane above
-    if (l < 128) red[4 + l] = s;
-    __syncthreads();
-    if (l < 64) {
-        const float v2 = fold64_lane0(__fadd_rn(red[4 + l], red[4 + l + 64]));
-        if (l == 0) red[2] = v2;
-    }
-    __syncthreads();
-    const float rs = __fdiv_rn(1.0f, red[2]);
+        // the reference's 128-lane stride-halving tree: the 64 stride crosses
+        // waves through LDS, the strides 32..1 are wave 0's lanes
+        if (l < 128) red[4 + l] = s;
+        lds_barrier();
+        if (l < 64) {
+            const float v2 = fold64_lane0(__fadd_rn(red[4 + l], red[4 + l + 64]));
+            if (l == 0) red[2] = v2;
+        }
+        lds_barrier();
+        rs = __fdiv_rn(1.0f, red[2]);
+    };
     if (direct) {
+        exps();
+        sums();
         uint16_t *vs = (uint16_t *)prod;                    // [t][HD] halves
 #pragma unroll
         for (int k = 0; k < DCH; k++) {
@@ -808,9 +873,9 @@ mx = xmax64(mx);
     // short spans (the sliding windows, early positions) take a two-tile
     // ring, so few rounds are padded
     const int ntiles = (count + D::T - 1) / D::T;
-    const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0, etab)
-                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab)
-                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab);
+    const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0, etab, exps, sums)
+                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab, exps, sums)
+                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab, exps, sums);
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 
@@ -842,7 +907,7 @@ DEV void combine_f32_body(const cj_attn_args &a, int bx) {
     float mx = -3.0e38f;
     if (l < 128)
         for (int t = l; t < count; t += 128) mx = fmaxf(mx, sc[t]);
-mx = xmax64(mx);
+    mx = xmax64(mx);
     if ((l & 63) == 0) red[l >> 6] = mx;
     __syncthreads();
     const float m = fmaxf(red[0], red[1]);
@@ -943,9 +1008,9 @@ DEV void combine_grp_body(const cj_attn_args &a, int hq) {
                 for (int k = 0; k < 8; k++) if (b + l + 128 * k < count && u[k] > mx) mx = u[k];
             }
         }
-// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
-// comparison; a tie of -0 and +0 changes no exp(s - m))
-mx = xmax64(mx);
+        // the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
+        // comparison; a tie of -0 and +0 changes no exp(s - m))
+        mx = xmax64(mx);
         if ((t & 63) == 0) gmax[t >> 6] = mx;
         __syncthreads();
         const float m = gmax[2 * g + 1] > gmax[2 * g] ? gmax[2 * g + 1] : gmax[2 * g];
@@ -1126,14 +1191,42 @@ DEV cj_attn_args attn_row_args(const cj_attn_args &a, int r) {
     return b;
 }
 
-extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) { scores_body<64>(a, blockIdx.x, blockIdx.y); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) { scores_body<128>(a, blockIdx.x, blockIdx.y); }
+// Workgroups are dealt to the eight XCDs round-robin by linear id. The
+// one-row scores grid (position chunk x, query head y) is renumbered so that
+// the grp query heads reading one chunk of one kv head's K rows share an XCD
+// (id mod 8), whose L2 serves the repeats: id = 8·grp·(g/8) + 8·i + g mod 8
+// for (chunk, kv head) pair g and member i. A grid whose pair count is not a
+// multiple of 8 keeps the plain numbering.
+DEV void scores_xcd(const cj_attn_args &a, int &bx, int &h) {
+    const int nx = gridDim.x, grp = a.n_q / a.n_kv, ng = nx * a.n_kv;
+    if (ng % 8 != 0 || (int)gridDim.y != a.n_q) {
+        bx = blockIdx.x;
+        h = blockIdx.y;
+        return;
+    }
+    const int id = blockIdx.y * nx + blockIdx.x;
+    const int q = id >> 3, i = q % grp, g = (q / grp) * 8 + (id & 7);
+    bx = g / a.n_kv;
+    h = (g % a.n_kv) * grp + i;
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h64(cj_attn_args a) {
+    int bx, h;
+    scores_xcd(a, bx, h);
+    scores_body<64>(a, bx, h);
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_h128(cj_attn_args a) {
+    int bx, h;
+    scores_xcd(a, bx, h);
+    scores_body<128>(a, bx, h);
+}
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h64(cj_attn_args a) { combine_body<64>(a, blockIdx.x); }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_h128(cj_attn_args a) { combine_body<128>(a, blockIdx.x); }
 // f32 K/V planes: the two-pass pair, one row and many rows
 #define TWO_PASS_F32(HD)                                                                                    \
     extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_f32_h##HD(cj_attn_args a) {           \
-        scores_body<HD, true>(a, blockIdx.x, blockIdx.y);                                                   \
+        int bx, h;                                                                                         \
+        scores_xcd(a, bx, h);                                                                              \
+        scores_body<HD, true>(a, bx, h);                                                                   \
     }                                                                                                       \
     extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_f32_h##HD(cj_attn_args a) {          \
         combine_f32_body<HD>(a, blockIdx.x);                                                                \
@@ -1241,9 +1334,9 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     if (l < 128) {
         for (int t = j; t < count; t += 128) if (sc[t] > mx) mx = sc[t];
     }
-// the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
-// comparison; a tie of -0 and +0 changes no exp(s - m))
-mx = xmax64(mx);
+    // the wave's maximum (no lane holds a NaN here, so fmaxf agrees with the
+    // comparison; a tie of -0 and +0 changes no exp(s - m))
+    mx = xmax64(mx);
     if (l < 128 && (l & 63) == 0) mred[l >> 6] = mx;
     __syncthreads();
     const float m = mred[1] > mred[0] ? mred[1] : mred[0];

@@ -63,6 +63,16 @@ DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((in
 DEV int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 DEV int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
 
+// A workgroup barrier for exchanges through LDS only: global loads in flight
+// stay in flight across it (__syncthreads waits for them too, the vector
+// memory counter covering loads as well as stores), so a prefetch issued
+// before it keeps its distance. Global stores before it are not made visible.
+DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Lane exchanges in the VALU, without an LDS round trip: DPP (quad
 // permutes and rotations inside each 16-lane row) and v_permlane16_swap /
 // v_permlane32_swap across rows. Every lane of the wave must be active.
