@@ -309,12 +309,12 @@ DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
     if (per32) {
         const float m = xmax32(av);
         if ((lane & 31) == 0) bmax[t >> 5] = m;
-        __syncthreads();
+        lds_barrier();
         am = bmax[t >> 5];
     } else {
         const float m = xmax64(av);
         if (lane == 0) bmax[t >> 6] = m;
-        __syncthreads();
+        lds_barrier();
         am = fmaxf(fmaxf(bmax[0], bmax[1]), fmaxf(bmax[2], bmax[3]));
     }
     const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
@@ -328,7 +328,7 @@ DEV void pack256(float v, int per32, uint8_t *ob, float *bmax) {
         if (t == 0) *(float *)(ob + 288) = __fdiv_rn(am, 127.0f);
         pack_zero_pad(ob, t);
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Lane-uniform reads of another lane's value (the lane index must be the
@@ -400,16 +400,16 @@ DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
     if (kn < 64 && er < n) p = __fadd_rn(p, __fmul_rn(xr, xr));
     for (int64_t e = t + 256 * 64; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
-    __syncthreads();
+    lds_barrier();
     if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
         const float s = fold64_lane0(__fadd_rn(red[t], red[t + 64]));
         if (t == 0) red[0] = s;
     }
-    __syncthreads();
+    lds_barrier();
     const float ss = red[0];
-    __syncthreads();
+    lds_barrier();
     return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
 }
 
@@ -475,7 +475,7 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
             else if (j < 8) *(uint32_t *)(b + 288 + 4 * j) = 0u;   // pad bytes 292..319
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // An f32 activation in LDS by 32-element blocks, swizzled: float4 i of block
@@ -527,7 +527,7 @@ DEV void stage_f32(const float *x, int64_t n, int nblk, bool norm, float scale, 
             *(float4 *)(xf + (swz ? swz32(e0 + 4 * k) : e0 + 4 * k)) =
                 make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // ---- Q4_0, block by block (Quant.q40MatVecIntoAt, L/io/Quant.cajeta:1516-1545)
@@ -620,7 +620,7 @@ DEV void stage_copy(const uint8_t *xp, int nblk, uint8_t *sx, int bstride = 320)
             if (i < n16) *(u32x4 *)(sx + (i / 20) * bstride + (i % 20) * 16) = v[k];
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 DEV int32_t step_pos(const cj_step_state *st, int32_t pos) { return st ? st->pos : pos; }
@@ -650,29 +650,29 @@ DEV void route_row(const float *lg, int ne, int n_used, int norm_topk, float w_s
     const int t = threadIdx.x;
     if (t < 64)
         for (int e = t; e < ne; e += 64) s.lgs[e] = lg[e];
-    __syncthreads();
+    lds_barrier();
     if (t == 0) {
         float mx = s.lgs[0];
         for (int e = 1; e < ne; e++) if (s.lgs[e] > mx) mx = s.lgs[e];
         s.bc[0] = mx;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
         const float mx = s.bc[0];
         for (int e = t; e < ne; e += 64) s.pr[e] = cj_expf(s.lgs[e] - mx);
     }
-    __syncthreads();
+    lds_barrier();
     if (t == 0) {
         float sum = 0.0f;
         for (int e = 0; e < ne; e++) sum = __fadd_rn(sum, s.pr[e]);
         s.bc[1] = sum;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
         const float sum = s.bc[1];
         for (int e = t; e < ne; e += 64) s.pr[e] = __fdiv_rn(s.pr[e], sum);   // the probabilities
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
         // The picks in order: the larger probability first, on a tie the
         // lower index, an entry that is not a number never (the repeated
@@ -705,7 +705,7 @@ DEV void route_row(const float *lg, int ne, int n_used, int norm_topk, float w_s
                 if (status) status[0] = 1;
             }
     }
-    __syncthreads();
+    lds_barrier();
     if (t == 0) {
         if (norm_topk) {
             float ws = 0.0f;
@@ -716,5 +716,5 @@ DEV void route_row(const float *lg, int ne, int n_used, int norm_topk, float w_s
         if (w_scale != 0.0f && w_scale != 1.0f)
             for (int k = 0; k < n_used; k++) s.w[k] = __fmul_rn(s.w[k], w_scale);
     }
-    __syncthreads();
+    lds_barrier();
 }

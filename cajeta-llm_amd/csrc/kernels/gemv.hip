@@ -1016,14 +1016,14 @@ DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PR
             for (int k = 0; k < RND * 16; k++)
                 if (t + 256 * k < n) s = __fadd_rn(s, __fmul_rn(pxs[k], pxs[k]));
             red[t] = s;
-            __syncthreads();
+            lds_barrier();
             if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
-            __syncthreads();
+            lds_barrier();
             if (t < 64) {
                 const float v = fold64_lane0(__fadd_rn(red[t], red[t + 64]));
                 if (t == 0) red[0] = v;
             }
-            __syncthreads();
+            lds_barrier();
             scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(red[0], (float)n), a.eps)));
         }
 #pragma unroll
@@ -1051,7 +1051,7 @@ DEV void q4k_pro_compute(const cj_gemv_args &a, const float4 (&px)[Q4kProDims<PR
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Q4_K body. Lane (wave w, lane l) owns row group l / LPR of each pass and
