@@ -261,18 +261,23 @@ DEV void terms_q6k_1(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], con
 template <int NR, int LPR>
 DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
     const int iters = (nb32 + LPR - 1) / LPR;
-    for (int it = 0; it < iters; it++) {
+    struct Sweep {
+        uint4 w0[NR], w1[NR];
+        uint32_t dh[NR];
+    };
+    auto load = [&](int it, Sweep &sw) {
+        const int u = slot + it * LPR, uu = u < nb32 ? u : nb32 - 1;
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            sw.w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
+            sw.w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
+            sw.dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
+        }
+    };
+    auto compute = [&](int it, const Sweep &sw) {
         const int u = slot + it * LPR;
         const bool ok = u < nb32;
         const int uu = ok ? u : nb32 - 1;
-        uint4 w0[NR], w1[NR];
-        uint32_t dh[NR];
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
-            w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
-            dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
-        }
         const uint8_t *ab = sx + (uu >> 3) * 320;
         const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
         const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
@@ -280,11 +285,11 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             int s = 0;
-            s = sdot4(w0[r].x, a0.x, s); s = sdot4(w0[r].y, a0.y, s);
-            s = sdot4(w0[r].z, a0.z, s); s = sdot4(w0[r].w, a0.w, s);
-            s = sdot4(w1[r].x, a1.x, s); s = sdot4(w1[r].y, a1.y, s);
-            s = sdot4(w1[r].z, a1.z, s); s = sdot4(w1[r].w, a1.w, s);
-            const float t = __fmul_rn(__fmul_rn(h2f(dh[r]), xs), (float)s);
+            s = sdot4(sw.w0[r].x, a0.x, s); s = sdot4(sw.w0[r].y, a0.y, s);
+            s = sdot4(sw.w0[r].z, a0.z, s); s = sdot4(sw.w0[r].w, a0.w, s);
+            s = sdot4(sw.w1[r].x, a1.x, s); s = sdot4(sw.w1[r].y, a1.y, s);
+            s = sdot4(sw.w1[r].z, a1.z, s); s = sdot4(sw.w1[r].w, a1.w, s);
+            const float t = __fmul_rn(__fmul_rn(h2f(sw.dh[r]), xs), (float)s);
             // lane base + k's term reaches lane base by row_shl:k (base is a
             // multiple of 8, so the eight stay inside one 16-lane row)
             const float o[7] = {dpp_shl<1>(t), dpp_shl<2>(t), dpp_shl<3>(t), dpp_shl<4>(t),
@@ -295,6 +300,21 @@ DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const
                 if (k < left) fs = __fadd_rn(fs, o[k - 1]);
             if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
         }
+    };
+    if (iters == 2) {
+        // rows of two sweeps: both sweeps' weights requested before either's
+        // arithmetic (one memory round trip, not two)
+        Sweep s0, s1;
+        load(0, s0);
+        load(1, s1);
+        compute(0, s0);
+        compute(1, s1);
+        return;
+    }
+    for (int it = 0; it < iters; it++) {
+        Sweep sw;
+        load(it, sw);
+        compute(it, sw);
     }
 }
 
