@@ -1258,12 +1258,19 @@ extern "C" __global__ void __launch_bounds__(256) cj_attn_scores_grp_rows_h128(c
     scores_grp_body<128>(attn_row_args(a, blockIdx.y / a.n_kv), blockIdx.x, blockIdx.y % a.n_kv);
 }
 // the grouped combine: grid x is the head group (256/HD query heads of one
-// kv head), y the row
+// kv head), y the row. The m head groups of a kv head read the same V rows:
+// x = j·n_kv + kv head puts them on one XCD (id mod 8 is x mod 8 while the
+// row's n_q/(256/HD) groups are a multiple of 8) for its L2 to serve.
+template <int HD>
+DEV int combine_grp_head(const cj_attn_args &a) {
+    const int m = (a.n_q / a.n_kv) / (256 / HD), x = blockIdx.x;
+    return m > 0 ? (x % a.n_kv) * m + x / a.n_kv : x;
+}
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_grp_rows_h64(cj_attn_args a) {
-    combine_grp_body<64>(attn_row_args(a, blockIdx.y), blockIdx.x);
+    combine_grp_body<64>(attn_row_args(a, blockIdx.y), combine_grp_head<64>(a));
 }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_combine_grp_rows_h128(cj_attn_args a) {
-    combine_grp_body<128>(attn_row_args(a, blockIdx.y), blockIdx.x);
+    combine_grp_body<128>(attn_row_args(a, blockIdx.y), combine_grp_head<128>(a));
 }
 
 // The two-pass form in one launch for spans of at most FUSED_SPAN(HD)
