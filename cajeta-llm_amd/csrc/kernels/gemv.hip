@@ -258,63 +258,67 @@ DEV void terms_q6k_1(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], con
 // Q8_0 × per-32 int8. One 32-element block a lane, term (d·xs)·isum; the 8
 // lanes of a 256-wide group then sum their terms in block order (the
 // reference's fs) and the group's first lane writes it.
+template <int NR>
+struct Q80Sweep {
+    uint4 w0[NR], w1[NR];
+    uint32_t dh[NR];
+};
+// sweep `it` of the lane's block (slot + it·LPR; past the row, the last block)
+template <int NR, int LPR>
+DEV void q80_load(const uint8_t *const (&wr)[NR], int nb32, int slot, int it, Q80Sweep<NR> &sw) {
+    const int u = slot + it * LPR, uu = u < nb32 ? u : nb32 - 1;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        sw.w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
+        sw.w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
+        sw.dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
+    }
+}
+template <int NR, int LPR>
+DEV void q80_compute(float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot, int it, const Q80Sweep<NR> &sw) {
+    const int u = slot + it * LPR;
+    const bool ok = u < nb32;
+    const int uu = ok ? u : nb32 - 1;
+    const uint8_t *ab = sx + (uu >> 3) * 320;
+    const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
+    const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
+    const int left = nb32 - (u & ~7);          // real blocks in this group of 8
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        int s = 0;
+        s = sdot4(sw.w0[r].x, a0.x, s); s = sdot4(sw.w0[r].y, a0.y, s);
+        s = sdot4(sw.w0[r].z, a0.z, s); s = sdot4(sw.w0[r].w, a0.w, s);
+        s = sdot4(sw.w1[r].x, a1.x, s); s = sdot4(sw.w1[r].y, a1.y, s);
+        s = sdot4(sw.w1[r].z, a1.z, s); s = sdot4(sw.w1[r].w, a1.w, s);
+        const float t = __fmul_rn(__fmul_rn(h2f(sw.dh[r]), xs), (float)s);
+        // lane base + k's term reaches lane base by row_shl:k (base is a
+        // multiple of 8, so the eight stay inside one 16-lane row)
+        const float o[7] = {dpp_shl<1>(t), dpp_shl<2>(t), dpp_shl<3>(t), dpp_shl<4>(t),
+                            dpp_shl<5>(t), dpp_shl<6>(t), dpp_shl<7>(t)};
+        float fs = t;
+#pragma unroll
+        for (int k = 1; k < 8; k++)
+            if (k < left) fs = __fadd_rn(fs, o[k - 1]);
+        if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
+    }
+}
 template <int NR, int LPR>
 DEV void terms_q80(const uint8_t *const (&wr)[NR], float *const (&tr)[NR], const uint8_t *sx, int nb32, int slot) {
     const int iters = (nb32 + LPR - 1) / LPR;
-    struct Sweep {
-        uint4 w0[NR], w1[NR];
-        uint32_t dh[NR];
-    };
-    auto load = [&](int it, Sweep &sw) {
-        const int u = slot + it * LPR, uu = u < nb32 ? u : nb32 - 1;
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            sw.w0[r] = ld_stream16(wr[r] + (int64_t)uu * 32);
-            sw.w1[r] = ld_stream16(wr[r] + (int64_t)uu * 32 + 16);
-            sw.dh[r] = *(const uint16_t *)(wr[r] + (int64_t)nb32 * 32 + 2 * uu);
-        }
-    };
-    auto compute = [&](int it, const Sweep &sw) {
-        const int u = slot + it * LPR;
-        const bool ok = u < nb32;
-        const int uu = ok ? u : nb32 - 1;
-        const uint8_t *ab = sx + (uu >> 3) * 320;
-        const uint4 a0 = *(const uint4 *)(ab + 32 * (uu & 7)), a1 = *(const uint4 *)(ab + 32 * (uu & 7) + 16);
-        const float xs = *(const float *)(ab + 288 + 4 * (uu & 7));
-        const int left = nb32 - (u & ~7);          // real blocks in this group of 8
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-            int s = 0;
-            s = sdot4(sw.w0[r].x, a0.x, s); s = sdot4(sw.w0[r].y, a0.y, s);
-            s = sdot4(sw.w0[r].z, a0.z, s); s = sdot4(sw.w0[r].w, a0.w, s);
-            s = sdot4(sw.w1[r].x, a1.x, s); s = sdot4(sw.w1[r].y, a1.y, s);
-            s = sdot4(sw.w1[r].z, a1.z, s); s = sdot4(sw.w1[r].w, a1.w, s);
-            const float t = __fmul_rn(__fmul_rn(h2f(sw.dh[r]), xs), (float)s);
-            // lane base + k's term reaches lane base by row_shl:k (base is a
-            // multiple of 8, so the eight stay inside one 16-lane row)
-            const float o[7] = {dpp_shl<1>(t), dpp_shl<2>(t), dpp_shl<3>(t), dpp_shl<4>(t),
-                                dpp_shl<5>(t), dpp_shl<6>(t), dpp_shl<7>(t)};
-            float fs = t;
-#pragma unroll
-            for (int k = 1; k < 8; k++)
-                if (k < left) fs = __fadd_rn(fs, o[k - 1]);
-            if (ok && (u & 7) == 0) tr[r][u >> 3] = fs;
-        }
-    };
     if (iters == 2) {
         // rows of two sweeps: both sweeps' weights requested before either's
         // arithmetic (one memory round trip, not two)
-        Sweep s0, s1;
-        load(0, s0);
-        load(1, s1);
-        compute(0, s0);
-        compute(1, s1);
+        Q80Sweep<NR> s0, s1;
+        q80_load<NR, LPR>(wr, nb32, slot, 0, s0);
+        q80_load<NR, LPR>(wr, nb32, slot, 1, s1);
+        q80_compute<NR, LPR>(tr, sx, nb32, slot, 0, s0);
+        q80_compute<NR, LPR>(tr, sx, nb32, slot, 1, s1);
         return;
     }
     for (int it = 0; it < iters; it++) {
-        Sweep sw;
-        load(it, sw);
-        compute(it, sw);
+        Q80Sweep<NR> sw;
+        q80_load<NR, LPR>(wr, nb32, slot, it, sw);
+        q80_compute<NR, LPR>(tr, sx, nb32, slot, it, sw);
     }
 }
 
@@ -876,6 +880,54 @@ DEV void gemv_body(const cj_gemv_args &a) {
     // block of x, so each reads its block from global memory beside its
     // weights rather than after x is staged in LDS (one round trip fewer)
     const bool xdirect = f32act && LPR == 1 && a.pro == CJ_PRO_F32 && ((uintptr_t)sl.X & 15) == 0;
+    if constexpr (FMT == CJ_Q8_0 && !MULTI) {
+        // Q8_0 over a packed activation, the workgroup's rows one pass of at
+        // most two sweeps: the activation's words are requested first, then
+        // both sweeps' weights, then the epilogue's operands, and only then
+        // are the words written to LDS — loads retire in issue order, so the
+        // staging waits for the activation alone and the weight stream's
+        // latency overlaps it (a round trip, not two)
+        constexpr int G = 64 / LPR, XW = 2;
+        const int nb32 = (int)(cols / 32), nwords = nblk * 20;
+        if (a.pro == CJ_PRO_PACKED && R <= NR * 4 * G && nb32 <= 2 * LPR && nwords <= 256 * XW) {
+            const uint8_t *xsrc = a.xp + sl.xidx * a.xp_stride;
+            u32x4 xw[XW];
+#pragma unroll
+            for (int k = 0; k < XW; k++) xw[k] = *(const u32x4 *)(xsrc + 16 * min(t + 256 * k, nwords - 1));
+            const int group = lane / LPR, slot = lane % LPR;
+            const int rl0 = NR * (wave * G + group);   // rows past R: loaded (clamped), never stored
+            const uint8_t *wr[NR];
+            float *tr[NR];
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                const int64_t rk = row0 + rl0 + k;
+                wr[k] = sl.W + (rk < a.rows ? rk : a.rows - 1) * a.row_bytes;
+                tr[k] = terms + (rl0 + k) * TB;
+            }
+            Q80Sweep<NR> s0, s1;
+            q80_load<NR, LPR>(wr, nb32, slot, 0, s0);
+            q80_load<NR, LPR>(wr, nb32, slot, 1, s1);
+            const EpiPre pre = epi_prefetch(a, sl);
+#pragma unroll
+            for (int k = 0; k < XW; k++) {
+                const int idx = t + 256 * k;
+                if (idx < nwords) *(u32x4 *)(sx + (idx / 20) * 320 + 16 * (idx % 20)) = xw[k];
+            }
+            lds_barrier();
+            if (rl0 < R) {
+                q80_compute<NR, LPR>(tr, sx, nb32, slot, 0, s0);
+                if (nb32 > LPR) q80_compute<NR, LPR>(tr, sx, nb32, slot, 1, s1);
+            }
+            __syncthreads();
+            float v = 0.0f;
+            if (t < R) {
+                const float *tp = terms + t * TB;
+                for (int b = 0; b < TB; b++) v = __fadd_rn(v, tp[b]);
+            }
+            gemv_epilogue(a, sl, v, bmax, pre);
+            return;
+        }
+    }
     // (the f32-activation formats stage x inside seq_body, after a one-row
     // workgroup's weights are requested)
     if (!f32act && !xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
