@@ -147,6 +147,10 @@ typedef struct {
     int32_t kv_f32;          // the K/V planes hold f32
 } cj_qkprep_args;
 
+// Output dimensions a workgroup of the fp16-K/V two-pass combine (HD/CJ_COMBINE_DH
+// workgroups a query head): the kernels' tiling and the launches' grids.
+#define CJ_COMBINE_DH 16
+
 typedef struct {
     float *part;             // split-K: [n_q][64][hd + 2] partials; two-pass: scores [n_q][splits]
     float *out;              // merged f32 output (null: partials only)

@@ -631,7 +631,7 @@ DEV void combine_store(float *pb, const CombineItem &it, int I, int count, int t
 
 template <int HD>
 struct CombineDims {
-    static constexpr int DH = 32;                   // output dimensions a workgroup (HD/DH workgroups a head)
+    static constexpr int DH = CJ_COMBINE_DH;        // output dimensions a workgroup (HD/DH workgroups a head)
     static constexpr int NSPLIT = HD / DH;
     static constexpr int A = 1;                     // adder wave (DH lanes)
     static constexpr int P = 256 - 64 * A;          // producer lanes
@@ -679,18 +679,23 @@ DEV float combine_pv(const cj_attn_args &a, const int *pgs, const float *ev, flo
             const float *pt = pr + (i & 1) * D::PB;
             const int n = i < ntiles ? min(T, count - i * T) : 0;
             if (n == T) {
-                // every read issued before the first add (the scheduler would
-                // otherwise keep two in flight and wait out each one's latency)
-                float4 p[T / 4];
+                // every read of a half tile issued before its first add (the
+                // scheduler would otherwise keep two in flight and wait out
+                // each one's latency)
+                constexpr int HQ = T / 8;
 #pragma unroll
-                for (int q = 0; q < T / 4; q++) p[q] = *(const float4 *)(pt + 4 * q);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int hh = 0; hh < 2; hh++) {
+                    float4 p[HQ];
 #pragma unroll
-                for (int q = 0; q < T / 4; q++) {
-                    acc = __fadd_rn(acc, p[q].x);
-                    acc = __fadd_rn(acc, p[q].y);
-                    acc = __fadd_rn(acc, p[q].z);
-                    acc = __fadd_rn(acc, p[q].w);
+                    for (int q = 0; q < HQ; q++) p[q] = *(const float4 *)(pt + 4 * (hh * HQ + q));
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int q = 0; q < HQ; q++) {
+                        acc = __fadd_rn(acc, p[q].x);
+                        acc = __fadd_rn(acc, p[q].y);
+                        acc = __fadd_rn(acc, p[q].z);
+                        acc = __fadd_rn(acc, p[q].w);
+                    }
                 }
             } else {
                 for (int q = 0; q < n; q += 4) {
@@ -870,12 +875,12 @@ DEV void combine_body(const cj_attn_args &a, int bx) {
         }
         return;
     }
-    // short spans (the sliding windows, early positions) take a two-tile
-    // ring, so few rounds are padded
-    const int ntiles = (count + D::T - 1) / D::T;
+    // two tiles of V rows in flight where the weights sit in LDS (a tile is
+    // ~3,000 cycles of the adder's chain, so two cover the rows' latency; a
+    // deeper ring's first burst from every workgroup at once only delays the
+    // softmax), six where the producers form the exps themselves
     const float acc = !elds ? combine_pv<HD, 6, true>(a, pgs, sc, m, prod, count, from, kvh, d0, etab, exps, sums)
-                      : ntiles <= 4 ? combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab, exps, sums)
-                                    : combine_pv<HD, 6, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab, exps, sums);
+                            : combine_pv<HD, 2, false>(a, pgs, es, m, prod, count, from, kvh, d0, etab, exps, sums);
     if (l < D::DH) a.out[(int64_t)h * HD + d0 + l] = __fmul_rn(acc, rs);
 }
 

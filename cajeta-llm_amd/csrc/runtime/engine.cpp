@@ -718,7 +718,7 @@ int Engine::enqueue_step(int s) {
                     // the grid covers the longest window; the kernel idles past count
                     if ((rc = launch2(attn_kernel, (uint32_t)((span + 255) / 256), (uint32_t)n_heads, 256, 0, a)))
                         return rc;
-                    if ((rc = launch(combine_kernel, (uint32_t)(n_heads * (head_dim / 32)), 256, 0, a))) return rc;
+                    if ((rc = launch(combine_kernel, (uint32_t)(n_heads * (head_dim / (kv_f32 ? 32 : CJ_COMBINE_DH))), 256, 0, a))) return rc;
                 }
             }
         }
@@ -1090,7 +1090,7 @@ int Engine::rows_forward(const int32_t *tab, int n, bool prefill) {
                     if ((rc = launch2(kname, (uint32_t)(n_heads / hpw), (uint32_t)n, 256, 0, a))) return rc;
                 } else {
                     snprintf(kname, sizeof kname, "cj_attn_combine_rows_%sh%d", kvs, head_dim);
-                    if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / 32)), (uint32_t)n, 256, 0, a))) return rc;
+                    if ((rc = launch2(kname, (uint32_t)(n_heads * (head_dim / (kv_f32 ? 32 : CJ_COMBINE_DH))), (uint32_t)n, 256, 0, a))) return rc;
                 }
             }
             if ((rc = rows_pack(r_attn, qd, L.o.type == CJ_Q8_0, n))) return rc;

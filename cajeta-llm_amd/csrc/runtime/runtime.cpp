@@ -819,7 +819,7 @@ int32_t cj_attend(int64_t part, int64_t out, int64_t q, int64_t kcache, int64_t 
     snprintf(name, sizeof name, "cj_attn_scores_h%d", head_dim);
     if (int32_t rc = launch2(name, (uint32_t)((count + 255) / 256), (uint32_t)n_q, 256, 0, a)) return rc;
     snprintf(name, sizeof name, "cj_attn_combine_h%d", head_dim);
-    return launch(name, (uint32_t)(n_q * (head_dim / 32)), 256, 0, a);
+    return launch(name, (uint32_t)(n_q * (head_dim / CJ_COMBINE_DH)), 256, 0, a);
 }
 
 int32_t cj_decode_splits(int32_t count, int32_t n_kv, int32_t workers) {
