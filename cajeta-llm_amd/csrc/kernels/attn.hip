@@ -75,7 +75,10 @@ DEV void split_body(const cj_attn_args &a) {
     __shared__ uint64_t etab[32];
     cj_exp_table(etab);   // visible after the tile loop's first barrier
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int kvh = blockIdx.x / ATTN_MAX_SPLITS, sp = blockIdx.x % ATTN_MAX_SPLITS;
+    // id mod n_kv = kv head: a kv head's splits run on one XCD (workgroups are
+    // dealt to the eight round-robin by id), whose L2 then holds the
+    // partials its query heads' merges read
+    const int kvh = blockIdx.x % a.n_kv, sp = blockIdx.x / a.n_kv;
     // q, the page table and the step state load together
     for (int e = 4 * t; e < G * HD; e += 1024) *(float4 *)&qs[0][e] = *(const float4 *)(a.q + (int64_t)kvh * G * HD + e);
     if (t < PGMAX) pgs[t] = t < a.pg_n ? a.pgtab[a.pg_base + t] : 0;
@@ -1471,8 +1474,11 @@ extern "C" __global__ void __launch_bounds__(128) cj_attn_merge_q(cj_merge_args 
     __shared__ uint64_t etab[32];
     cj_exp_table(etab);
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, hd = a.head_dim, per = hd / 32;
-    const int h = blockIdx.x / per, j = lane >> 4, i = lane & 15;
-    const int d = (blockIdx.x % per) * 32 + 16 * wave + i;
+    // id mod n_kv = kv head, as the split kernel numbers its workgroups: the
+    // merges of a kv head's query heads read its partials on the same XCD
+    const int kv = (int)(blockIdx.x % a.n_kv), rest = (int)(blockIdx.x / a.n_kv);
+    const int h = kv * (a.n_q / a.n_kv) + rest / per, j = lane >> 4, i = lane & 15;
+    const int d = (rest % per) * 32 + 16 * wave + i;
     const float *pb0 = a.part + (int64_t)h * ATTN_MAX_SPLITS * (hd + 2);
     float pv[16];
 #pragma unroll
