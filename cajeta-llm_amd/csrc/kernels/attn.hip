@@ -1378,14 +1378,21 @@ DEV void fused_body(const cj_attn_args &a, int h) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) { fused_body<64>(a, blockIdx.x); }
-extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) { fused_body<128>(a, blockIdx.x); }
+// a query head a workgroup, numbered kv head = id mod n_kv so the heads that
+// read one kv head's K and V rows share an XCD's L2
+DEV int fused_head(const cj_attn_args &a, int id) { return (id % a.n_kv) * (a.n_q / a.n_kv) + id / a.n_kv; }
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h64(cj_attn_args a) {
+    fused_body<64>(a, fused_head(a, blockIdx.x));
+}
+extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_h128(cj_attn_args a) {
+    fused_body<128>(a, fused_head(a, blockIdx.x));
+}
 // many rows: grid (n_q, rows)
 extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h64(cj_attn_args a) {
-    fused_body<64>(attn_row_args(a, blockIdx.y), blockIdx.x);
+    fused_body<64>(attn_row_args(a, blockIdx.y), fused_head(a, blockIdx.x));
 }
 extern "C" __global__ void __launch_bounds__(256) cj_attn_fused_rows_h128(cj_attn_args a) {
-    fused_body<128>(attn_row_args(a, blockIdx.y), blockIdx.x);
+    fused_body<128>(attn_row_args(a, blockIdx.y), fused_head(a, blockIdx.x));
 }
 
 // Merge split partials into f32 (+ the pack of the result): one workgroup of
