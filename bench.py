@@ -327,8 +327,8 @@ def run_c2(args, native):
     pool of >= 512 MB of distinct prepared copies so the 256 MB last-level
     cache cannot serve them; one captured graph of launches, timed whole.
     Batch 1 is the decode GEMV; batch > 1 the int8 matrix-core product where
-    the format has one (Q8_0, Q4_K), else the many-column GEMV (Q6_K over
-    packs, Q4_0 over the f32 columns)."""
+    the format has one (Q8_0, Q4_K; Q6_K above 8 columns), else the
+    many-column GEMV (Q6_K over packs, Q4_0 over the f32 columns)."""
     lib = native.lib()
     rng = np.random.default_rng(args.seed)
     table = []
@@ -375,7 +375,7 @@ def run_c2(args, native):
                 gbs = nbytes / (us * 1e-6) / 1e9
                 table.append({"format": fname, "rows": rows, "cols": cols, "batch": B, "us": round(us, 2),
                               "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
-                              "kernel": "gemv" if B == 1 else ("many-column gemv" if ty in (2, 14) else "int8 mfma"),
+                              "kernel": "gemv" if B == 1 else ("many-column gemv" if ty == 2 or (ty == 14 and B <= 8) else "int8 mfma"),
                               "pool_copies": ncopy})
                 log("  %-5s %6d x %5d B %2d: %9.2f us  %7.1f GB/s  (%s, %d copies)" % (
                     fname, rows, cols, B, us, gbs, table[-1]["kernel"], ncopy))

@@ -731,91 +731,275 @@ extern "C" __global__ void __launch_bounds__(512) cj_gemm_sk_q4k_n1(cj_gemv_args
 // ------------------------------------------------------------------- Q6_K
 
 // Many columns of Q6_K × q8_K (no matrix-core form: the 16-element
-// sub-block scales sit inside the 32-element dot an MFMA forms). A wave
-// takes a row at a time (4 rows a workgroup pass, 16 a workgroup), its lanes
-// the row's units (block b, quarter j: 64 elements); each unit's weights are
-// loaded and decoded once and then dotted with the NC columns' packs, which
-// every wave reads from the cache (the codes decoded once to signed q − 32,
-// so a column costs only its dots). Per (row, column) the block terms are
-// the one-column GEMV's — sumi = Σ_sb sc_sb·dot_sb over q − 32, an exact
-// integer, then (d·xs)·sumi — kept in the wave's LDS rows, and lane c folds column c's
-// terms in block order (Quant.q6kMatVecIntoQ8, io/Quant.cajeta:3448-3486):
-// each column is bit for bit what cj_matvec gives it.
+// sub-block scales sit inside the 32-element dot an MFMA forms). A
+// workgroup takes 16 rows (4 a wave) and NC columns, and walks the rows in
+// sweeps of 16 blocks: a sweep's activation blocks of the NC columns are
+// staged in LDS once for the four waves (16-byte pieces swizzled so that
+// every 8 lanes of a read touch 8 distinct bank groups), and each lane — a
+// unit (block, quarter: 64 elements) of the sweep — decodes its unit of the
+// wave's 4 rows once to signed q − 32, then reads each column's 64 values
+// once for the 4 rows. The next sweep's activation and weights are requested
+// before the current sweep's arithmetic. Per (row, column) the block terms
+// are the one-column GEMV's — sumi = Σ_sb sc_sb·dot_sb over q − 32, an exact
+// integer, then (d·xs)·sumi — and lane (row, column) of the wave folds them
+// in block order, sweep after sweep (Quant.q6kMatVecIntoQ8,
+// io/Quant.cajeta:3448-3486): each column is bit for bit what cj_matvec
+// gives it.
 // Four 6-bit codes q (0..63, one a byte) as the int8 values q − 32: bit 5
 // set, clearing it subtracts 32; clear, q − 32 = q + 224 is q + 32 with bits
-// 6 and 7 set. (0x20·6 = 0xC0, so the multiply cannot carry between bytes.)
-DEV uint32_t q6_signed(uint32_t q) { return (q ^ 0x20202020u) | ((~q & 0x20202020u) * 6u); }
+// 6 and 7 set: bit 5 of the clear set shifted up by one and by two, the
+// last shift in its own instruction (written as C, the two shifts become a
+// multiply by 6, which issues at a quarter of the rate).
+DEV uint32_t q6_signed(uint32_t q) {
+    const uint32_t m = ~q & 0x20202020u;
+    uint32_t r;
+    asm("v_lshl_or_b32 %0, %1, 1, %2" : "=v"(r) : "v"(m), "v"((q ^ 0x20202020u) | (m << 2)));
+    return r;
+}
+
+// One unit of a Q6_K row as loaded: low and high code nibbles, the high bit
+// pairs, the unit's eight sub-block scales and the block's f16 scale.
+struct Q6Unit {
+    uint4 qa, qb, qh;
+    uint2 sc;
+    uint32_t dh;
+};
+
+DEV Q6Unit q6_load(const uint8_t *w, int64_t nb, int b, int g, int hl) {
+    Q6Unit u;
+    u.qa = ld_stream16(w + (int64_t)b * 128 + 64 * g + 16 * hl);
+    u.qb = ld_stream16(w + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
+    u.qh = ld_stream16(w + nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
+    u.sc = *(const uint2 *)(w + nb * 192 + (int64_t)b * 16 + 8 * g);
+    u.dh = *(const uint16_t *)(w + nb * 208 + 2 * b);
+    return u;
+}
 
 template <int NC>
 DEV void gemm_q6k_cols(const cj_gemv_args &a) {
-    extern __shared__ __align__(16) float tsm[];
+    constexpr int SB = 16;                             // blocks a sweep
+    __shared__ __align__(16) uint8_t xq[NC * SB * 256];
+    __shared__ float xsl[NC * SB];
+    __shared__ float terms[4][4][NC][SB + 1];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int nb = (int)(a.cols / 256), units = nb * 4, ts = nb + 1;
-    float *terms = tsm + wave * NC * ts;               // [NC][nb + 1] a wave
-    const int64_t c0 = (int64_t)blockIdx.y * NC;
+    const int nb = (int)(a.cols / 256);
+    const int64_t c0 = (int64_t)blockIdx.y * NC, rbase = (int64_t)blockIdx.x * 16 + 4 * wave;
     const uint8_t *xcol[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) xcol[c] = a.xp + min(c0 + c, (int64_t)a.batch - 1) * a.xp_stride;
-    for (int rr = 0; rr < 4; rr++) {
-        const int64_t row_i = (int64_t)blockIdx.x * 16 + 4 * wave + rr;
-        const bool live = row_i < a.rows;              // every wave passes the barriers below
-        const int64_t row = live ? row_i : a.rows - 1;
-        const uint8_t *w = a.w + row * a.row_bytes;
-        for (int u0 = 0; u0 < units; u0 += 64) {
-            const int u = min(u0 + lane, units - 1);
-            const int b = u >> 2, j = u & 3, g = j >> 1, hl = j & 1;
-            const uint4 qa = ld_stream16(w + (int64_t)b * 128 + 64 * g + 16 * hl);
-            const uint4 qb = ld_stream16(w + (int64_t)b * 128 + 64 * g + 32 + 16 * hl);
-            const uint4 qh = ld_stream16(w + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 16 * hl);
-            const uint2 sc = *(const uint2 *)(w + (int64_t)nb * 192 + (int64_t)b * 16 + 8 * g);
-            const uint32_t dh = *(const uint16_t *)(w + (int64_t)nb * 208 + 2 * b);
-            uint32_t v[4][4];
-            int scv[4];
+    const uint8_t *wrow[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) wrow[rr] = a.w + min(rbase + rr, a.rows - 1) * a.row_bytes;
+    // this lane's unit of a sweep: block bl, quarter j (g: 128-element half)
+    const int bl = lane >> 2, j = lane & 3, g = j >> 1, hl = j & 1;
+    const int sw = ((bl & 1) << 2) | (g << 1);
+    // staging: thread t carries 16-byte piece ci of sweep block sbl, every column
+    const int sbl = t >> 4, ci = t & 15;
+    const int sp = (ci & 8) | ((ci & 7) ^ (((sbl & 1) << 2) | ((ci >> 3) << 1)));
+    const uint8_t *xsp = a.xp + min(c0 + (t >> 4), (int64_t)a.batch - 1) * a.xp_stride + 288;
+    u32x4 xv[NC];                                      // a native vector: a uint4 array copies through memory
+    float xsv = 0.0f;
+    Q6Unit wu[4];
+    auto fetch = [&](int s0) __attribute__((always_inline)) {
+        const int sb = min(SB, nb - s0);
+        const int64_t xo = (int64_t)(s0 + min(sbl, sb - 1)) * 320 + 16 * ci;   // past the row: its last block again
+#pragma unroll
+        for (int c = 0; c < NC; c++) xv[c] = *(const u32x4 *)(xcol[c] + xo);
+        xsv = *(const float *)(xsp + (int64_t)(s0 + min(ci, sb - 1)) * 320);
+        const int b = s0 + min(bl, sb - 1);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) wu[rr] = q6_load(wrow[rr], nb, b, g, hl);
+    };
+    const int frr = lane / NC, fc = lane % NC;         // the folding lane's (row, column)
+    float acc = 0.0f;
+    fetch(0);
+    for (int s0 = 0; s0 < nb; s0 += SB) {
+        const int sb = min(SB, nb - s0);
+        if (sbl < sb) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) *(u32x4 *)(xq + (c * SB + sbl) * 256 + 16 * sp) = xv[c];
+        }
+        if (t < NC * SB) xsl[t] = xsv;
+        lds_barrier();                                 // the sweep's activation is staged
+        uint32_t v[4][4][4];
+        int scv[4][4];
+        float d[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const Q6Unit &u = wu[rr];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const uint4 ql = (k & 1) ? qb : qa;
+                const uint4 ql = (k & 1) ? u.qb : u.qa;
                 const int sh = (k >> 1) * 4;
                 const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
-                v[k][0] = q6_signed(((ql.x >> sh) & M) | (((qh.x >> (2 * k)) & H) << 4));
-                v[k][1] = q6_signed(((ql.y >> sh) & M) | (((qh.y >> (2 * k)) & H) << 4));
-                v[k][2] = q6_signed(((ql.z >> sh) & M) | (((qh.z >> (2 * k)) & H) << 4));
-                v[k][3] = q6_signed(((ql.w >> sh) & M) | (((qh.w >> (2 * k)) & H) << 4));
+                v[rr][k][0] = q6_signed(((ql.x >> sh) & M) | (((u.qh.x >> (2 * k)) & H) << 4));
+                v[rr][k][1] = q6_signed(((ql.y >> sh) & M) | (((u.qh.y >> (2 * k)) & H) << 4));
+                v[rr][k][2] = q6_signed(((ql.z >> sh) & M) | (((u.qh.z >> (2 * k)) & H) << 4));
+                v[rr][k][3] = q6_signed(((ql.w >> sh) & M) | (((u.qh.w >> (2 * k)) & H) << 4));
                 const int byte_i = 2 * k + hl;
-                const uint32_t word = byte_i < 4 ? sc.x : sc.y;
-                scv[k] = (int)(int8_t)((word >> (8 * (byte_i & 3))) & 255);
+                const uint32_t word = byte_i < 4 ? u.sc.x : u.sc.y;
+                scv[rr][k] = (int)(int8_t)((word >> (8 * (byte_i & 3))) & 255);
             }
-            const float d = h2f(dh);
+            d[rr] = h2f(u.dh);
+        }
+        if (s0 + SB < nb) fetch(s0 + SB);              // the next sweep's operands, in flight meanwhile
+        __builtin_amdgcn_sched_barrier(0);
+        const bool own = j == 0 && bl < sb;
+        const uint8_t *xb = xq + bl * 256 + 128 * g;
+        // at 8 columns a column's 64 values and scale are read a column ahead
+        // (one wave a SIMD there: nothing else hides the LDS latency); at 4
+        // the registers that takes would halve the waves a SIMD
+        constexpr bool AHEAD = NC >= 8;
+        u32x4 an[4];
+        float xn;
+        auto xread = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const uint8_t *ab = xcol[c] + b * 320 + 128 * g + 16 * hl;
-                const float xs = *(const float *)(xcol[c] + b * 320 + 288);
+            for (int k = 0; k < 4; k++) an[k] = *(const u32x4 *)(xb + c * SB * 256 + 16 * ((hl + 2 * k) ^ sw));
+            xn = xsl[c * SB + bl];
+        };
+        if (AHEAD) xread(0);
+#pragma unroll(AHEAD ? NC : 2)
+        for (int c = 0; c < NC; c++) {
+            if (!AHEAD) xread(c);
+            u32x4 av[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) av[k] = an[k];
+            const float xs = xn;
+            if (AHEAD && c + 1 < NC) xread(c + 1);
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
                 int sumi = 0;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint4 av = *(const uint4 *)(ab + 32 * k);
                     int dt = 0;
-                    dt = sdot4(v[k][0], av.x, dt); dt = sdot4(v[k][1], av.y, dt);
-                    dt = sdot4(v[k][2], av.z, dt); dt = sdot4(v[k][3], av.w, dt);
-                    sumi += scv[k] * dt;
+                    dt = sdot4(v[rr][k][0], av[k].x, dt); dt = sdot4(v[rr][k][1], av[k].y, dt);
+                    dt = sdot4(v[rr][k][2], av[k].z, dt); dt = sdot4(v[rr][k][3], av[k].w, dt);
+                    // |dt| <= 16·32·128 and |sc| <= 128: a 24-bit multiply is exact
+                    sumi += __mul24(scv[rr][k], dt);
                 }
-                sumi += quad_xor1(sumi);
-                sumi += quad_xor2(sumi);
-                if (u0 + lane < units && j == 0) terms[c * ts + b] = __fmul_rn(__fmul_rn(d, xs), (float)sumi);
+                sumi += dpp_i<DPP_XOR1>(sumi);
+                sumi += dpp_i<DPP_XOR2>(sumi);
+                const float term = __fmul_rn(__fmul_rn(d[rr], xs), (float)sumi);
+                if (own) terms[wave][rr][c][bl] = term;
             }
         }
-        __syncthreads();                               // the terms are written
-        if (live && lane < NC && c0 + lane < a.batch) {
-            float acc = 0.0f;
-            for (int b = 0; b < nb; b++) acc = __fadd_rn(acc, terms[lane * ts + b]);
-            float *y = a.y + (c0 + lane) * a.y_stride + a.y_off + row;
-            *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
-        }
-        __syncthreads();                               // and read before the next row writes them
+        lds_barrier();                                 // the sweep's terms are written
+        if (lane < 4 * NC)
+            for (int q = 0; q < sb; q++) acc = __fadd_rn(acc, terms[wave][frr][fc][q]);
+        lds_barrier();                                 // and read, with the activation, before the next sweep
+    }
+    const int64_t row = rbase + frr, col = c0 + fc;
+    if (lane < 4 * NC && row < a.rows && col < a.batch) {
+        float *y = a.y + col * a.y_stride + a.y_off + row;
+        *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
     }
 }
 extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c4(cj_gemv_args a) { gemm_q6k_cols<4>(a); }
 extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c8(cj_gemv_args a) { gemm_q6k_cols<8>(a); }
-extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_c16(cj_gemv_args a) { gemm_q6k_cols<16>(a); }
+
+// Q6_K × 16 columns on the int8 matrix cores. A 32-element run of a block
+// holds two 16-element sub-blocks with scales of their own, so each run takes
+// two v_mfma_i32_16x16x32_i8 over the same activation operand: one with the
+// weights of lanes 32-63 (elements 16-31 of the run) zeroed, one with lanes
+// 0-31 zeroed — each product an exact int32 dot of one sub-block. The
+// activation is the A operand (its rows the 16 columns) and the weights the
+// B operand (its columns the 16 rows), so lane l receives columns
+// 4·(l / 16) + i of weight row l % 16 and applies that row's sub-block scales
+// to them: sumi = Σ_sb sc_sb·dot_sb, an exact integer, then (d·xs)·sumi per
+// (row, column) and block, as the one-column GEMV forms it. A workgroup owns
+// 16 rows × 16 columns; its four waves take a round's 16 blocks four apiece
+// (wave w blocks w, w + 4, …), hand the terms through LDS, and thread
+// (row, column) folds them in block order, round after round
+// (Quant.q6kMatVecIntoQ8, io/Quant.cajeta:3448-3486): each column is bit for
+// bit what cj_matvec gives it.
+// One block's operands for cj_gemm_q6k_m16, as one lane loads them.
+struct Q6M {
+    long q[2][2], h[2], xv[2][4];
+    u32x4 sc;
+    uint32_t dh;
+    float xs[4];
+};
+
+extern "C" __global__ void __launch_bounds__(256) cj_gemm_q6k_m16(cj_gemv_args a) {
+    constexpr int RB = 16;                             // blocks a round
+    __shared__ __align__(16) float terms[RB][16][20];  // [block][row][column], rows padded against bank conflicts
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int n = lane & 15, kg = lane >> 4;
+    const int nb = (int)(a.cols / 256);
+    const int64_t r0 = (int64_t)blockIdx.x * 16, c0 = (int64_t)blockIdx.y * 16;
+    const int64_t last = (int64_t)a.batch - 1;
+    const uint8_t *w = a.w + min(r0 + n, a.rows - 1) * a.row_bytes;               // B: weight row r0 + n
+    const uint8_t *xa = a.xp + min(c0 + n, last) * a.xp_stride + 8 * kg;          // A: column c0 + n
+    const uint8_t *xsp[4];                                                        // the received columns' scales
+#pragma unroll
+    for (int i = 0; i < 4; i++) xsp[i] = a.xp + min(c0 + 4 * kg + i, last) * a.xp_stride + 288;
+    const bool lo = kg < 2;
+    // the wave's blocks: j-th is block 16·(j / 4) + wave + 4·(j % 4) of the row;
+    // past the row the last block is read again and its terms left unfolded
+    const int rounds = (nb + RB - 1) / RB, J = 4 * rounds;
+    auto load = [&](Q6M &o, int jj) __attribute__((always_inline)) {
+        const int b = min(RB * (jj >> 2) + wave + 4 * (jj & 3), nb - 1);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) o.xv[g][kk] = ld8(xa + (int64_t)b * 320 + 128 * g + 32 * kk);
+#pragma unroll
+            for (int p = 0; p < 2; p++) o.q[g][p] = ld8(w + (int64_t)b * 128 + 64 * g + 32 * p + 8 * kg);
+            o.h[g] = ld8(w + (int64_t)nb * 128 + (int64_t)b * 64 + 32 * g + 8 * kg);
+        }
+        o.sc = *(const u32x4 *)(w + (int64_t)nb * 192 + (int64_t)b * 16);
+        o.dh = *(const uint16_t *)(w + (int64_t)nb * 208 + 2 * b);
+#pragma unroll
+        for (int c = 0; c < 4; c++) o.xs[c] = *(const float *)(xsp[c] + (int64_t)b * 320);
+    };
+    const int frow = t >> 4, fcol = t & 15;
+    float acc = 0.0f;
+    Q6M cur, nxt;
+    load(cur, 0);
+    for (int jj = 0; jj < J; jj++) {
+        load(nxt, min(jj + 1, J - 1));                 // the next block in flight meanwhile
+        int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                // the run's 8 codes of this lane as int8 q − 32
+                const long ql = cur.q[g][kk & 1], qh = cur.h[g];
+                const int sh = 4 * (kk >> 1);
+                const uint32_t M = 0x0F0F0F0Fu, H = 0x03030303u;
+                const uint32_t lo32 = q6_signed((((uint32_t)ql >> sh) & M) | ((((uint32_t)qh >> (2 * kk)) & H) << 4));
+                const uint32_t hi32 = q6_signed((((uint32_t)(ql >> 32) >> sh) & M) |
+                                                ((((uint32_t)(qh >> 32) >> (2 * kk)) & H) << 4));
+                const long wv = (long)(((uint64_t)hi32 << 32) | lo32);
+                const v4i d0 = mfma_i8(cur.xv[g][kk], lo ? wv : 0);   // sub-block 8g + 2kk
+                const v4i d1 = mfma_i8(cur.xv[g][kk], lo ? 0 : wv);   // sub-block 8g + 2kk + 1
+                const int sb = 8 * g + 2 * kk;
+                const uint32_t word = cur.sc[sb >> 2];
+                const int s0 = (int)(int8_t)(word >> (8 * (sb & 3))), s1 = (int)(int8_t)(word >> (8 * ((sb & 3) + 1)));
+                // |dot| <= 16·32·127 and |sc| <= 128: 24-bit multiplies are exact
+#pragma unroll
+                for (int c = 0; c < 4; c++) sumi[c] += __mul24(s0, d0[c]) + __mul24(s1, d1[c]);
+            }
+        }
+        const float d = h2f(cur.dh);
+        f32x4 tv;
+#pragma unroll
+        for (int c = 0; c < 4; c++) tv[c] = __fmul_rn(__fmul_rn(d, cur.xs[c]), (float)sumi[c]);
+        *(f32x4 *)&terms[wave + 4 * (jj & 3)][n][4 * kg] = tv;
+        cur = nxt;
+        if ((jj & 3) == 3) {
+            lds_barrier();                             // the round's terms are written
+            const int nbr = min(RB, nb - RB * (jj >> 2));
+            for (int k = 0; k < nbr; k++) acc = __fadd_rn(acc, terms[k][frow][fcol]);
+            lds_barrier();                             // and read before the next round writes them
+        }
+    }
+    const int64_t row = r0 + frow, col = c0 + fcol;
+    if (row < a.rows && col < a.batch) {
+        float *y = a.y + col * a.y_stride + a.y_off + row;
+        *y = a.epi == CJ_EPI_ACCUM ? __fadd_rn(*y, acc) : acc;
+    }
+}
 
 // Q4_0 many-column GEMV (cj_matmul over f32 activation columns): the
 // one-column kernel's sweeps for NC columns a workgroup, RW rows a wave

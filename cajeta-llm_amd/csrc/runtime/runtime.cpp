@@ -344,14 +344,15 @@ int run_gemm(const cj_gemv_args &a) {
         return launch2(name, (uint32_t)((a.rows + 4 * rw - 1) / (4 * rw)), (uint32_t)cgroups, 256, 0, a);
     }
     if (a.type == CJ_Q6_K) {
-        // many-column GEMV: 16 rows a workgroup, NC columns a grid row
+        // many-column GEMV (4 or 8 columns a grid row; its LDS fixed: a
+        // 16-block sweep of the columns and the waves' terms), or above 8
+        // columns the matrix-core form, 16 a grid row; 16 rows a workgroup
         const int nc = a.batch <= 4 ? 4 : a.batch <= 8 ? 8 : 16;
-        const int64_t nb = a.cols / 256;
         if (a.cols % 256) return fail(CJ_ERR_ARG, "gemm: Q6_K rows are whole 256-element blocks");
         if ((a.batch + nc - 1) / nc > 65535) return fail(CJ_ERR_ARG, "gemm: %d columns exceed the grid", a.batch);
-        snprintf(name, sizeof name, "cj_gemm_q6k_c%d", nc);
-        return launch2(name, (uint32_t)((a.rows + 15) / 16), (uint32_t)((a.batch + nc - 1) / nc), 256,
-                       (uint32_t)(4 * nc * (nb + 1) * 4), a);
+        if (nc == 16) snprintf(name, sizeof name, "cj_gemm_q6k_m16");
+        else snprintf(name, sizeof name, "cj_gemm_q6k_c%d", nc);
+        return launch2(name, (uint32_t)((a.rows + 15) / 16), (uint32_t)((a.batch + nc - 1) / nc), 256, 0, a);
     }
     const char *fmt = a.type == CJ_Q8_0 ? "q80" : "q4k";
     // Q4_K's 64-column tile needs more registers than two waves a SIMD leave
@@ -415,7 +416,7 @@ int32_t cj_init(int32_t device) {
         "cj_attn_split_h128_g4", "cj_attn_split_h128_g8", "cj_attn_scores_h64", "cj_attn_scores_h128",
         "cj_attn_combine_h64", "cj_attn_combine_h128", "cj_attn_fused_h64", "cj_attn_fused_h128",
         "cj_attn_merge", "cj_attn_merge_q", "cj_moe_group", "cj_argmax_pick", "cj_qkprep", "cj_zero", "cj_moe_route", "cj_router_topk",
-        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_c16",
+        "cj_gemm_q80_n2", "cj_gemm_q4k_n2", "cj_gemm_q80_n4", "cj_gemm_q6k_c4", "cj_gemm_q6k_c8", "cj_gemm_q6k_m16",
         "cj_gemm_sk_q80_n1", "cj_gemm_sk_q80_n2", "cj_gemm_sk_q4k_n1",
         "cj_rows_embed", "cj_rows_qkv", "cj_rows_glu", "cj_rows_argmax", "cj_rows_pick",
         "cj_attn_split_rows_h128_g4", "cj_attn_split_rows_h128_g8", "cj_attn_merge_rows",
