@@ -702,6 +702,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
     constexpr int D = ROWS == 1 ? 2 : SEQ_D;
     static_assert(D % 2 == 0, "the ring depth must be even");
     static_assert(ROWS == 64 || ROWS == 32 || ROWS == 1, "64, 32 or 1 rows a workgroup");
+    static_assert(ROWS != 1 || 96 * 64 <= 32 * (192 / ROWS) + 4, "a one-row tile's products fit 96 a lane");
     constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
     constexpr int S = 32 * TB + 4;            // product row stride (floats): 16-byte reads by 16 lanes, distinct banks
     __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
@@ -717,7 +718,38 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
     const int nit = (ntiles + D - 1) / D * D;
     float acc = 0.0f;
     pro();
-    if (w == 0) {
+    if (w == 0 && ROWS == 1) {
+        // one row: the chain walks the wave's lanes. Lane L holds products
+        // 96·L .. 96·L + 95 of the tile in registers (one batch of LDS reads a
+        // tile); the lanes add their own in lockstep, and after lane L's 96
+        // its sum is broadcast to every lane (readlane), so each of the
+        // chain's adds reads its operand from a register
+        __syncthreads();
+        for (int i = 0; i < nit; i++) {
+            const float *pr = prod[0] + (i & 1) * PBUF + 96 * lane;   // within the row: 96·64 ≤ S
+            const int n = (i < ntiles ? min(TB, nb32 - i * TB) : 0) * 32;
+            f32x4 p[24];
+#pragma unroll
+            for (int q = 0; q < 24; q++) p[q] = *(const f32x4 *)(pr + 4 * q);
+            for (int L = 0; 96 * L < n; L++) {
+                const int cnt = n - 96 * L;                            // a multiple of 32
+#pragma unroll
+                for (int c = 0; c < 3; c++) {
+                    if (c == 0 || cnt > 32 * c) {
+#pragma unroll
+                        for (int q = 8 * c; q < 8 * c + 8; q++) {
+                            acc = __fadd_rn(acc, p[q].x);
+                            acc = __fadd_rn(acc, p[q].y);
+                            acc = __fadd_rn(acc, p[q].z);
+                            acc = __fadd_rn(acc, p[q].w);
+                        }
+                    }
+                }
+                acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), L));
+            }
+            __syncthreads();
+        }
+    } else if (w == 0) {
         __syncthreads();
         const float *pr0 = prod[0] + min(lane, ROWS - 1) * S;
         auto add3 = [&](const float *pr, int b0) {
