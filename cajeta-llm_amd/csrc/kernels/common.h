@@ -384,20 +384,39 @@ DEV float wave_shr1(float v, float first) {
 // Prim.rmsnormDevice (:1440-1450), as the resident layer does for them
 // (CausalLM.cajeta:3643, :3819). Then 1/sqrt(ss/n + eps). `red` is 256 floats
 // of LDS.
-DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red) {
-    const int t = threadIdx.x;
-    // the row's values loaded at once (up to 64 a thread), then summed in
-    // order: kn whole rounds (a uniform bound), then the ragged one
-    float xv[64];
-    const int kn = (int)min(n >> 8, (int64_t)64);
+// A callable run where a prologue's loads are in flight and not yet used.
+struct NoMid {
+    DEV void operator()() const {}
+};
+
+// mid() runs after the row's loads are requested and before any is used:
+// loads it requests stay in flight while the sum is formed (loads complete
+// in the order requested, so waiting for the row's values does not wait
+// for them).
+// Thread t's values t + 256·k, k < K, of a row of n (past the row: its last
+// value again, never summed), every load unconditional.
+template <int K>
+DEV void norm_load(const float *x, int64_t n, float (&xv)[64]) {
 #pragma unroll
-    for (int k = 0; k < 64; k++) xv[k] = k < kn ? x[t + 256 * k] : 0.0f;
-    const int64_t er = t + 256 * (int64_t)kn;
-    const float xr = kn < 64 && er < n ? x[er] : 0.0f;
+    for (int k = 0; k < 64; k++) xv[k] = k < K ? x[min((int64_t)threadIdx.x + 256 * k, n - 1)] : 0.0f;
+}
+
+template <class Mid = NoMid>
+DEV float stage_norm_scale(const float *x, int64_t n, float eps, float *red, Mid &&mid = Mid{}) {
+    const int t = threadIdx.x;
+    // the row's values loaded at once (up to 64 a thread: 16, 32 or 64 loads,
+    // each form with no load under a branch of its own — one branch a load
+    // made the compiler wait at the joins, a memory round trip every few
+    // loads), then summed in order: thread t's values t, t + 256, … < n
+    float xv[64];
+    const int64_t rounds = (n + 255) >> 8;
+    if (rounds <= 16) norm_load<16>(x, n, xv);
+    else if (rounds <= 32) norm_load<32>(x, n, xv);
+    else norm_load<64>(x, n, xv);
+    mid();
     float p = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 64; k++) if (k < kn) p = __fadd_rn(p, __fmul_rn(xv[k], xv[k]));
-    if (kn < 64 && er < n) p = __fadd_rn(p, __fmul_rn(xr, xr));
+    for (int k = 0; k < 64; k++) p = t + 256 * (int64_t)k < n ? __fadd_rn(p, __fmul_rn(xv[k], xv[k])) : p;
     for (int64_t e = t + 256 * 64; e < n; e += 256) p = __fadd_rn(p, __fmul_rn(x[e], x[e]));
     red[t] = p;
     lds_barrier();

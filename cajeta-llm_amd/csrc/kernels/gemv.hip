@@ -400,15 +400,19 @@ DEV GemvSlice gemv_slice(const cj_gemv_args &a) {
 // The activation into LDS: a copied pack, the pack of an f32 vector, RMSNorm
 // + pack, or (f32-activation formats) the f32 values, normed or not. Ends on
 // a barrier.
+template <class Mid = NoMid>
 DEV void gemv_prologue(const cj_gemv_args &a, const GemvSlice &sl, bool f32act, uint8_t *sx, float *red, int bstride,
-                       bool swz = false) {
+                       bool swz = false, Mid &&mid = Mid{}) {
     const int64_t cols = a.cols;
     const int nblk = (int)((cols + 255) / 256);
     if (a.pro == CJ_PRO_PACKED) {
+        mid();
         stage_copy(a.xp + sl.xidx * a.xp_stride, nblk, sx, bstride);
     } else {
         const bool norm = a.pro == CJ_PRO_NORM_PACK || a.pro == CJ_PRO_NORM_F32;
-        const float scale = norm ? stage_norm_scale(sl.X, cols, a.eps, red) : 1.0f;
+        float scale = 1.0f;
+        if (norm) scale = stage_norm_scale(sl.X, cols, a.eps, red, mid);
+        else mid();
         if (f32act) {
             stage_f32(sl.X, cols, nblk, norm, scale, a.nw, a.norm_form, (float *)sx, swz);
             if (a.xout && norm && !swz && blockIdx.x == 0) {   // the staged values (stage_f32 ends on a barrier)
@@ -708,16 +712,26 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
     __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int nb32 = (int)(a.cols / 32), ntiles = (nb32 + TB - 1) / TB;
-    const int pl = t - 64, prow = pl % ROWS, pb = pl / ROWS;
+    const int pl = max(t - 64, 0), prow = pl % ROWS, pb = pl / ROWS;   // (the adder wave as producer 0)
     const uint8_t *wr = sl.W + min(sl.row0 + prow, a.rows - 1) * a.row_bytes;
     float *pdst = prod[0] + prow * S + 32 * pb;
     constexpr int PBUF = 64 * SEQ_S;
     // both loops run a whole number of D-tile rounds: the producer's body
     // is then free of branches (tiles past the end are formed into the idle
     // buffer and never read)
-    const int nit = (ntiles + D - 1) / D * D;
+    // (a one-row workgroup whose row is one tile — the router — runs that
+    // tile alone: one barrier each side, no idle tile formed or read)
+    const bool one = ROWS == 1 && ntiles == 1;
+    const int nit = one ? 0 : (ntiles + D - 1) / D * D;
     float acc = 0.0f;
-    pro();
+    // the first D tiles' weights are requested inside the prologue, after its
+    // own loads (every wave, so no load sits under a branch; the adder wave's
+    // are never used)
+    SeqItem<FMT> ring[D];
+    pro([&] {
+#pragma unroll
+        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * TB + pb);
+    });
     if (w == 0 && ROWS == 1) {
         // one row: the chain walks the wave's lanes. Lane L holds products
         // 96·L .. 96·L + 95 of the tile in registers (one batch of LDS reads a
@@ -725,7 +739,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
         // its sum is broadcast to every lane (readlane), so each of the
         // chain's adds reads its operand from a register
         __syncthreads();
-        for (int i = 0; i < nit; i++) {
+        for (int i = 0; i < max(nit, (int)one); i++) {
             const float *pr = prod[0] + (i & 1) * PBUF + 96 * lane;   // within the row: 96·64 ≤ S
             const int n = (i < ntiles ? min(TB, nb32 - i * TB) : 0) * 32;
             f32x4 p[24];
@@ -747,7 +761,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
                 }
                 acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), L));
             }
-            __syncthreads();
+            if (!one) __syncthreads();
         }
     } else if (w == 0) {
         __syncthreads();
@@ -789,10 +803,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
             __syncthreads();
         }
     } else {
-        SeqItem<FMT> ring[D];
         float4 xr[2][8];
-#pragma unroll
-        for (int j = 0; j < D; j++) ring[j] = seq_fetch<FMT>(wr, nb32, j * TB + pb);
         seq_xload(xs, min(pb, nb32 - 1), xr[0]);
         seq_xload(xs, min(TB + pb, nb32 - 1), xr[1]);
         seq_products<FMT>(ring[0], xr[0], pdst);
@@ -972,8 +983,9 @@ DEV void gemv_body(const cj_gemv_args &a) {
         // ---- one adder lane a row, in element order (64 rows a workgroup)
         // (for these formats LPR is the rows a workgroup: 64, or 32 / 1
         // where the matrix is short and more workgroups fill the chip)
-        const float sv = seq_body<FMT, LPR>(a, sl, xdirect ? sl.X : (const float *)sx, [&] {
-            if (!xdirect) gemv_prologue(a, sl, f32act, sx, red, 320);
+        const float sv = seq_body<FMT, LPR>(a, sl, xdirect ? sl.X : (const float *)sx, [&](auto &&mid) {
+            if (!xdirect) gemv_prologue(a, sl, f32act, sx, red, 320, false, mid);
+            else mid();
         });
         if (live) v = sv;
     } else {
