@@ -93,22 +93,23 @@ extern "C" __global__ void __launch_bounds__(256) cj_norm_pack_rows(cj_pack_args
 // row exactly as cj_norm_pack does from global memory. Dynamic LDS: n floats.
 // Thread t takes the 4-value groups t, t+256, t+512, t+768 (n ≤ 4096, n a
 // multiple of 4, up to 8 experts a row: the host checks), every load of
-// the row issued before the first sum.
-extern "C" __global__ void __launch_bounds__(256) cj_moe_combine_norm(cj_combine_norm_args a) {
-    extern __shared__ __align__(16) float xs[];
+// the row issued before the first sum and none under a branch of its own
+// (NU, 4 or 8, bounds the experts read; past n_used the last expert's row
+// is read again and never added).
+template <int NU>
+DEV void combine_norm_body(const cj_combine_norm_args &a, float *xs) {
     const int t = threadIdx.x, nu = a.n_used;
     const int64_t n4 = a.n / 4;
-    float wk[8];
+    float wk[NU];
 #pragma unroll
-    for (int k = 0; k < 8; k++) wk[k] = k < nu ? a.w[k] : 0.0f;
-    float4 hv[4], yv[4][8];
+    for (int k = 0; k < NU; k++) wk[k] = a.w[min(k, nu - 1)];
+    float4 hv[4], yv[4][NU];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int64_t g = min((int64_t)t + 256 * j, n4 - 1);
         hv[j] = ((const float4 *)a.hs_in)[g];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            if (k < nu) yv[j][k] = ((const float4 *)(a.y + k * a.n))[g];
+        for (int k = 0; k < NU; k++) yv[j][k] = ((const float4 *)(a.y + min(k, nu - 1) * a.n))[g];
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -116,18 +117,24 @@ extern "C" __global__ void __launch_bounds__(256) cj_moe_combine_norm(cj_combine
         if (g >= n4) continue;
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            if (k >= nu) break;
-            acc.x = __fadd_rn(acc.x, __fmul_rn(wk[k], yv[j][k].x));
-            acc.y = __fadd_rn(acc.y, __fmul_rn(wk[k], yv[j][k].y));
-            acc.z = __fadd_rn(acc.z, __fmul_rn(wk[k], yv[j][k].z));
-            acc.w = __fadd_rn(acc.w, __fmul_rn(wk[k], yv[j][k].w));
+        for (int k = 0; k < NU; k++) {
+            const bool on = k < nu;
+            acc.x = on ? __fadd_rn(acc.x, __fmul_rn(wk[k], yv[j][k].x)) : acc.x;
+            acc.y = on ? __fadd_rn(acc.y, __fmul_rn(wk[k], yv[j][k].y)) : acc.y;
+            acc.z = on ? __fadd_rn(acc.z, __fmul_rn(wk[k], yv[j][k].z)) : acc.z;
+            acc.w = on ? __fadd_rn(acc.w, __fmul_rn(wk[k], yv[j][k].w)) : acc.w;
         }
         const float4 h = make_float4(__fadd_rn(hv[j].x, acc.x), __fadd_rn(hv[j].y, acc.y),
                                      __fadd_rn(hv[j].z, acc.z), __fadd_rn(hv[j].w, acc.w));
         ((float4 *)xs)[g] = h;
         if (((4 * g) >> 8) == (int64_t)blockIdx.x) ((float4 *)a.hs_out)[g] = h;
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256) cj_moe_combine_norm(cj_combine_norm_args a) {
+    extern __shared__ __align__(16) float xs[];
+    if (a.n_used <= 4) combine_norm_body<4>(a, xs);
+    else combine_norm_body<8>(a, xs);
     __syncthreads();
     norm_pack_block(a.p, xs);
 }
