@@ -451,13 +451,29 @@ DEV void stage_pack(const float *x, int64_t n, int nblk, bool norm, float scale,
                     int per32, uint8_t *sx, float *xout, int bstride = 320) {
     const int t = threadIdx.x;
     const int64_t total = (int64_t)nblk * 256;
+    // 16-byte reads where the row (and the norm weights) are 16-byte aligned
+    // (the per-value form below loads each value under a branch of its own,
+    // and the compiler waits at every join)
+    const bool al = ((reinterpret_cast<uintptr_t>(x) | (norm ? reinterpret_cast<uintptr_t>(w) : 0)) & 15) == 0;
     for (int64_t e0 = 16 * t; e0 < total; e0 += 4096) {
         float v[16];
-        if (e0 + 16 <= n && !norm) {
+        if (e0 + 16 <= n && al) {
+            f32x4 xv[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float4 f = *(const float4 *)(x + e0 + 4 * k);
-                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+            for (int k = 0; k < 4; k++) xv[k] = *(const f32x4 *)(x + e0 + 4 * k);
+            if (norm) {
+                f32x4 wv[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) wv[k] = *(const f32x4 *)(w + e0 + 4 * k);
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    const float wk = wv[k >> 2][k & 3];
+                    const float wi = form == 1 ? __fadd_rn(1.0f, wk) : wk;
+                    v[k] = __fmul_rn(__fmul_rn(xv[k >> 2][k & 3], scale), wi);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = xv[k >> 2][k & 3];
             }
         } else {
 #pragma unroll
