@@ -1410,6 +1410,14 @@ DEV void mxq8_body(const cj_gemv_args &a) {
     const int t = threadIdx.x, hw = t >> 5, hl = t & 31;
     const int R = a.rows_per_wg;
     GemvSlice sl = gemv_slice(a);
+    // the activation's first round of blocks (below) requested before the
+    // route: it does not depend on the expert, so its latency overlaps the
+    // route's own load and arithmetic
+    constexpr int PR = 3;    // rounds of 32 blocks whose loads are issued together
+    float4 f0[PR];
+#pragma unroll
+    for (int k = 0; k < PR; k++)
+        f0[k] = *(const float4 *)(sl.X + 32 * (int64_t)min(32 * k + (t >> 3), nb - 1) + 4 * (t & 7));
     if (a.route_logits) {
         // the route of this copy's row, then its expert (the row's first
         // workgroup publishes the row's selections and weights)
@@ -1443,14 +1451,7 @@ DEV void mxq8_body(const cj_gemv_args &a) {
     // the activation's codes: eight lanes a 32-block, four values a lane;
     // the block maximum by an xor exchange over the eight (max is exact)
     {
-        constexpr int PR = 3;    // rounds of 32 blocks whose loads are issued together
-        for (int b0 = 0; b0 < nb; b0 += 32 * PR) {
-            float4 f[PR];
-#pragma unroll
-            for (int k = 0; k < PR; k++) {
-                const int b = min(b0 + 32 * k + (t >> 3), nb - 1);
-                f[k] = *(const float4 *)(sl.X + 32 * (int64_t)b + 4 * (t & 7));
-            }
+        auto quant = [&](int b0, const float4 (&f)[PR]) {
 #pragma unroll
             for (int k = 0; k < PR; k++) {
                 const int b = b0 + 32 * k + (t >> 3);
@@ -1465,6 +1466,16 @@ DEV void mxq8_body(const cj_gemv_args &a) {
                     if ((t & 7) == 0) xd[b] = __fdiv_rn(bm, 127.0f);
                 }
             }
+        };
+        quant(0, f0);
+        for (int b0 = 32 * PR; b0 < nb; b0 += 32 * PR) {
+            float4 f[PR];
+#pragma unroll
+            for (int k = 0; k < PR; k++) {
+                const int b = min(b0 + 32 * k + (t >> 3), nb - 1);
+                f[k] = *(const float4 *)(sl.X + 32 * (int64_t)b + 4 * (t & 7));
+            }
+            quant(b0, f);
         }
     }
     __syncthreads();
