@@ -850,6 +850,7 @@ DEV void gemm_q6k_cols(const cj_gemv_args &a) {
         // (one wave a SIMD there: nothing else hides the LDS latency); at 4
         // the registers that takes would halve the waves a SIMD
         constexpr bool AHEAD = NC >= 8;
+        constexpr int CU = AHEAD ? NC : 2;            // the column loop's unroll
         u32x4 an[4];
         float xn;
         auto xread = [&](int c) __attribute__((always_inline)) {
@@ -858,7 +859,7 @@ DEV void gemm_q6k_cols(const cj_gemv_args &a) {
             xn = xsl[c * SB + bl];
         };
         if (AHEAD) xread(0);
-#pragma unroll(AHEAD ? NC : 2)
+#pragma unroll CU
         for (int c = 0; c < NC; c++) {
             if (!AHEAD) xread(c);
             u32x4 av[4];

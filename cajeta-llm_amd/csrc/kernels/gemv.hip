@@ -708,6 +708,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
     static_assert(ROWS == 64 || ROWS == 32 || ROWS == 1, "64, 32 or 1 rows a workgroup");
     static_assert(ROWS != 1 || 96 * 64 <= 32 * (192 / ROWS) + 4, "a one-row tile's products fit 96 a lane");
     constexpr int TB = 192 / ROWS;            // blocks a tile: the 192 producer lanes, one (row, block) each
+    constexpr int TU = TB <= 6 ? TB / 3 : 2;  // the adder's unroll over a whole tile's triples
     constexpr int S = 32 * TB + 4;            // product row stride (floats): 16-byte reads by 16 lanes, distinct banks
     __shared__ __align__(16) float prod[2][64 * SEQ_S];   // ROWS·S ≤ 64·SEQ_S floats a buffer
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
@@ -793,7 +794,7 @@ DEV float seq_body(const cj_gemv_args &a, const GemvSlice &sl, const float *xs, 
             const float *pr = pr0 + (i & 1) * PBUF;
             const int nb = i < ntiles ? min(TB, nb32 - i * TB) : 0;
             if (nb == TB) {
-#pragma unroll(TB <= 6 ? TB / 3 : 2)
+#pragma unroll TU
                 for (int b0 = 0; b0 < TB; b0 += 3) add3(pr, b0);
             } else {
                 int b0 = 0;
