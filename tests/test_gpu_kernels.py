@@ -166,6 +166,26 @@ def test_matvec_matches_oracle(gpu, O, name, ty, rows, cols):
         "%s %dx%d: %d rows differ" % (name, rows, cols, int((got != ref).sum()))
 
 
+@pytest.mark.parametrize("rows,cols", [(32, 2880), (64, 6144), (3, 6176), (40, 14336), (7, 96)])
+def test_matvec_f32_rows_match_oracle(gpu, O, rows, cols):
+    """The f32 GEMV (the MoE router's product) at up to 64 rows: a workgroup a
+    row, whose adder wave walks the row's element-order chain across its
+    lanes — rows of one tile (up to 6144 columns, the tile run alone) and of
+    several (2, 3 tiles) — bit for bit the oracle's column-order dot."""
+    say("matvec f32", rows, cols)
+    rng = np.random.default_rng(rows * 31 + cols)
+    w = (rng.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    lib = gpu.native.lib()
+    wb, xb = gpu.Buffer.of(w), gpu.Buffer.of(x)
+    yb = gpu.Buffer.of(np.zeros(rows, np.float32))
+    gpu.native.check(lib.cj_matvec(O.F32, yb.h, wb.h, xb.h, rows, cols, 0, 0), "matvec f32")
+    got = yb.download(np.float32, rows)
+    ref = O.matvec(O.F32, w.view(np.uint8), rows, cols, x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+        "f32 %dx%d: %d rows differ" % (rows, cols, int((got != ref).sum()))
+
+
 @pytest.mark.parametrize("name,ty", [("q4_k", 12), ("q8_0", 8)])
 def test_matvec_accumulate_store(gpu, O, name, ty):
     got, ref, _, _ = matvec_case(gpu, O, ty, 512, 4096, 7, accum=True)
