@@ -207,8 +207,10 @@ int64_t prepared_row_bytes(int type, int64_t cols) {
 }
 
 bool gemv_supported(int type, int64_t cols) {
-    // the staged activation and the per-row terms stay within 64 KB of LDS
-    return prepared_row_bytes(type, cols) > 0 && cols <= (is_f32_act(type) ? 15360 : 16384);
+    // the staged activation and the per-row terms stay within 64 KB of LDS;
+    // the f32 rows are walked in whole 32-element blocks
+    return prepared_row_bytes(type, cols) > 0 && cols <= (is_f32_act(type) ? 15360 : 16384) &&
+           (type != CJ_F32 || cols % 32 == 0);
 }
 
 // Q4_K: LPR lanes a row (one lane a block), rows a workgroup in whole passes

@@ -184,6 +184,8 @@ def test_matvec_f32_rows_match_oracle(gpu, O, rows, cols):
     ref = O.matvec(O.F32, w.view(np.uint8), rows, cols, x)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
         "f32 %dx%d: %d rows differ" % (rows, cols, int((got != ref).sum()))
+    # a row that is not whole 32-element blocks is refused, not truncated
+    assert lib.cj_matvec(O.F32, yb.h, wb.h, xb.h, 1, cols - 4, 0, 0) == gpu.native.CJ_ERR_ARG
 
 
 @pytest.mark.parametrize("name,ty", [("q4_k", 12), ("q8_0", 8)])
