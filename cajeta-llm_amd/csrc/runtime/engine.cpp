@@ -231,7 +231,10 @@ struct Engine {
     int norm_pack(const float *w, int per32, bool f32_out, const float *x = nullptr);
     // rows a workgroup the head's GEMV aims at: 64 where 128 would leave a
     // workgroup a CU or fewer
-    int head_target() const { return (int64_t)vocab <= 128LL * 2 * std::max(1, device_cus()) ? 64 : 128; }
+    // the head's rows a workgroup: 64 at every vocabulary (128 for large
+    // ones measured slower: C5's 201,088-row head 115.6 -> 108.6 us at 64,
+    // C3's 128,256 rows 75.2 -> 74.1)
+    int head_target() const { return 64; }
     // the many-row path
     int rows_alloc(int cap);
     int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
