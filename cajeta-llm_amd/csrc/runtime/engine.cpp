@@ -231,10 +231,11 @@ struct Engine {
     int norm_pack(const float *w, int per32, bool f32_out, const float *x = nullptr);
     // rows a workgroup the head's GEMV aims at: 64 where 128 would leave a
     // workgroup a CU or fewer
-    // the head's rows a workgroup: 64 at every vocabulary (128 for large
-    // ones measured slower: C5's 201,088-row head 115.6 -> 108.6 us at 64,
-    // C3's 128,256 rows 75.2 -> 74.1)
-    int head_target() const { return 64; }
+    // the head's rows a workgroup, by its format: Q8_0 32, others 64 (128
+    // for large vocabularies measured slower: C5's 201,088-row Q8_0 head
+    // 115.6 -> 108.6 us at 64 -> 106.0 at 32; C3's 128,256-row Q6_K head
+    // 75.2 -> 74.1 at 64, 75.5 at 32)
+    int head_target(int type) const { return type == CJ_Q8_0 ? 32 : 64; }
     // the many-row path
     int rows_alloc(int cap);
     int rows_linear(const DevW &W, const uint8_t *xp, int64_t xp_stride, float *y, int64_t y_stride, bool accum, int n);
@@ -840,7 +841,7 @@ int Engine::enqueue_step(int s) {
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(), a.pro, a.epi);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(a.type), a.pro, a.epi);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
         if (only < 0) {
@@ -1180,7 +1181,7 @@ int Engine::prefill_rows(int s, const int32_t *toks, int n) {
         a.rows = vocab; a.cols = hidden; a.row_bytes = head.row_bytes; a.type = head.type;
         a.pro = is_f32_act(head.type) ? CJ_PRO_F32 : CJ_PRO_PACKED; a.epi = CJ_EPI_ARGMAX;
         a.per32 = head.type == CJ_Q8_0; a.eps = eps; a.batch = 1;
-        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(), a.pro, a.epi);
+        GemvPlan p = plan_gemv(a.type, a.rows, a.cols, head_target(a.type), a.pro, a.epi);
         if ((int64_t)p.grid > (vocab + 3) / 4 + 64) return fail(CJ_ERR_STATE, "head grid exceeds the partial buffers");
         if ((rc = run_gemv(a, p))) return rc;
         cj_pick_args k{};
